@@ -1,0 +1,191 @@
+/*
+ * soso_hip.h -- C ABI of the MI355X (gfx950) decode hot path for soso.
+ *
+ * Drop-in boundary for soso-llm-core's `GpuDispatch` trait
+ * (crates/soso-llm-core/src/gpu.rs:338-737).  A thin Rust `impl GpuDispatch`
+ * wraps these calls 1:1 (the binding is shown in INTEGRATION.md).  No torch or
+ * HIP types cross this boundary: plain pointers, sizes and integer codes.
+ *
+ * Conventions, all taken from the trait and its CUDA implementor:
+ *  - Return codes of the compute entry points mirror Result<bool, ()>:
+ *      1  = computed (outputs valid on return)        -> Ok(true)
+ *      0  = declined, the caller computes on the CPU  -> Ok(false)
+ *     <0  = error; callers treat it like 0            -> Err(())
+ *    (gpu.rs:432-440; try_gpu_matvec turns Err into CPU, gpu.rs:784-787).
+ *  - Weights are resident and keyed by a stable tensor name: the first call
+ *    for a key uploads `w` (and repacks it for the device); later calls read
+ *    only the key.  A key that was declined once (dtype, shape, memory) stays
+ *    declined (crates/soso-llm-api/src/cuda.rs:289-290, 2365-2380).
+ *  - Host-pointer entry points are synchronous: outputs are valid on return
+ *    (cuda.rs:2395-2408).  One caller at a time (the trait takes &mut self);
+ *    a handle may be used from a thread other than its creator: the device is
+ *    made current on every call (cuda.rs:2362-2364).
+ *  - Nothing here aborts or throws.
+ *
+ * dtype codes are soso's (crates/sosomodel/src/layout.rs:8-12):
+ *   1 = F32, 2 = Q8_0 (f32 scale + 32 x i8 = 36 B), 3 = Q4_K (GGML, 144 B),
+ * plus 13 = Q6_K (GGML, 210 B), an extension of this library: soso itself
+ * re-quantizes Q6_K to Q8_0 at import (crates/gguf2som/src/lib.rs:1592-1609).
+ */
+#ifndef SOSO_HIP_H
+#define SOSO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SOSO_HIP_DTYPE_F32 1
+#define SOSO_HIP_DTYPE_Q8_0 2
+#define SOSO_HIP_DTYPE_Q4_K 3
+#define SOSO_HIP_DTYPE_Q6_K 13
+
+#define SOSO_HIP_OK 1
+#define SOSO_HIP_DECLINED 0
+#define SOSO_HIP_ERR (-1)
+#define SOSO_HIP_ERR_ARG (-2)
+#define SOSO_HIP_ERR_DEVICE (-3)
+#define SOSO_HIP_ERR_NOMEM (-4)
+
+typedef struct soso_hip soso_hip; /* opaque; one per device */
+
+/* GpuStats (gpu.rs:18-36): the counters this library maintains. */
+typedef struct soso_hip_stats {
+    uint64_t launches;   /* entry-point calls that ran on the device */
+    uint64_t total_ns;   /* wall time spent inside those calls */
+    uint64_t bytes_up;   /* host -> device (activations, not weights) */
+    uint64_t bytes_down; /* device -> host */
+    uint64_t weight_bytes_resident;
+    uint64_t weights_resident;
+    uint64_t weights_declined;
+} soso_hip_stats_t;
+
+/* MatvecOp (gpu.rs:189-196) for soso_hip_matvec_batch. */
+typedef struct soso_hip_op {
+    const char *key;
+    size_t key_len;
+    const uint8_t *w; /* raw tensor bytes (read only on the key's first use) */
+    size_t w_len;
+    uint8_t dtype;
+    size_t rows, cols;
+    const float *x; /* cols */
+    float *y;       /* rows */
+} soso_hip_op;
+
+/* ExpertoBloque (gpu.rs:176-186) for soso_hip_experts_block. */
+typedef struct soso_hip_expert {
+    const char *keys[3]; /* ffn_gate, ffn_up, ffn_down */
+    size_t key_lens[3];
+    const uint8_t *w[3]; /* raw bytes, or NULL when the caller believes them resident */
+    size_t w_len[3];
+    uint8_t dtype[3]; /* 0 when w is NULL */
+    const uint32_t *tokens;  /* block-local token indices choosing this expert */
+    const uint32_t *targets; /* token * top_k + rank, one per token */
+    size_t n_tokens;
+    int shared; /* 1 = shared expert */
+} soso_hip_expert;
+
+/* ---- lifetime ------------------------------------------------------------ */
+/* Creates a handle on HIP device `device`.  vram_budget = bytes of weights the
+ * handle may keep resident (0 = 90% of the device's free memory).
+ * Returns 0 or a negative error. */
+int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out);
+void soso_hip_destroy(soso_hip *h);
+
+/* GpuDispatch::available (gpu.rs:339). */
+int soso_hip_available(const soso_hip *h);
+/* GpuDispatch::dtype_soportado (gpu.rs:343-345): 1 for F32, Q8_0, Q4_K, Q6_K. */
+int soso_hip_dtype_supported(const soso_hip *h, uint8_t dtype);
+/* GpuDispatch::stats (gpu.rs:352-354). */
+void soso_hip_stats(const soso_hip *h, soso_hip_stats_t *out);
+/* Last error message of this handle ("" if none); valid until the next call. */
+const char *soso_hip_last_error(const soso_hip *h);
+
+/* ---- matvec family (host pointers, synchronous) ---------------------------- */
+/* GpuDispatch::matvec (gpu.rs:432-440): y[rows] = W[rows x cols] . x[cols].
+ * Overwrites y.  w/w_len are read only on the first call for `key`. */
+int soso_hip_matvec(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len,
+                    uint8_t dtype, size_t rows, size_t cols, const float *x, float *y);
+/* GpuDispatch::matmul (gpu.rs:443-455): Y[n x rows] = X[n x cols] . W^T. */
+int soso_hip_matmul(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len,
+                    uint8_t dtype, size_t rows, size_t cols, size_t n, const float *x, float *y);
+/* GpuDispatch::matvec_lote (gpu.rs:694-701): every op with one wait at the
+ * end; done[i] = 1 for the ops computed here.  Returns 1 if all were done,
+ * 0 if some were declined, <0 on error (done[] still tells which finished). */
+int soso_hip_matvec_batch(soso_hip *h, const soso_hip_op *ops, size_t n_ops, uint8_t *done);
+
+/* ---- MoE ---------------------------------------------------------------------- */
+/* GpuDispatch::router_topk (gpu.rs:480-494): logits = W[n_exp x h] . x (f32),
+ * softmax, top-k per token in ranking order (ties: lowest index), weights
+ * renormalised.  idx/wgt: n x top_k. */
+int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const float *w, const float *xs,
+                         size_t n, size_t hdim, size_t n_exp, size_t top_k, int32_t *idx, float *wgt);
+/* GpuDispatch::expertos_bloque (gpu.rs:461-475): per expert, gate/up, SwiGLU
+ * and down for the tokens choosing it; sum[n x h] receives, per token, the
+ * weighted sum (weights wgt[n x top_k]) of the experts resolved here in
+ * ranking order.  done[i] = 1 for the experts resolved.  Returns 1 if all were
+ * resolved, 0 if some were declined (their contribution is not in sum). */
+int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, size_t ffn, size_t top_k,
+                           const float *wgt, const soso_hip_expert *exps, size_t n_exps, float *sum,
+                           uint8_t *done);
+
+/* ---- device-resident API (no host copies; for the decode step, benchmarks
+ * and tests that keep inputs in HBM).  Launches are asynchronous on the
+ * handle's stream; soso_hip_sync waits. -------------------------------------- */
+int soso_hip_dev_alloc(soso_hip *h, size_t bytes, void **dptr);
+int soso_hip_dev_free(soso_hip *h, void *dptr);
+int soso_hip_h2d(soso_hip *h, void *dst, const void *src, size_t bytes);
+int soso_hip_d2h(soso_hip *h, void *dst, const void *src, size_t bytes);
+int soso_hip_sync(soso_hip *h);
+/* Registers a resident weight whose raw (soso/GGML layout) bytes are already
+ * on the device at `raw_dev`; the library repacks them into its own copy. */
+int soso_hip_weight_from_dev(soso_hip *h, const char *key, size_t key_len, const void *raw_dev,
+                             size_t w_len, uint8_t dtype, size_t rows, size_t cols);
+/* Fills a new resident weight with seeded synthetic blocks (bench/test input
+ * generator; same bytes as the documented counter-based generator). */
+int soso_hip_weight_synth(soso_hip *h, const char *key, size_t key_len, uint8_t dtype, size_t rows,
+                          size_t cols, uint64_t seed, uint64_t stream);
+/* Writes the synthetic raw (soso/GGML layout) bytes of a tensor to device memory. */
+int soso_hip_synth_raw(soso_hip *h, void *dst_dev, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
+                       uint64_t stream);
+/* n f32 values ~ N(0,1)*sigma (Irwin-Hall(12) normals of the same generator). */
+int soso_hip_synth_normal(soso_hip *h, float *dst_dev, size_t n, float sigma, uint64_t seed,
+                          uint64_t stream);
+int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len);
+/* y_dev[rows] = W(key) . x_dev; asynchronous on the handle's stream. */
+int soso_hip_matvec_dev(soso_hip *h, const char *key, size_t key_len, const float *x_dev, float *y_dev);
+/* Y[n x rows] = X[n x cols] . W(key)^T, device pointers, asynchronous. */
+int soso_hip_matmul_dev(soso_hip *h, const char *key, size_t key_len, size_t n, const float *x_dev,
+                        float *y_dev);
+/* Exact dequantization of a resident weight into out_dev (rows*cols f32),
+ * with the reference's arithmetic (no FMA): the bit-exactness witness. */
+int soso_hip_dequant_dev(soso_hip *h, const char *key, size_t key_len, float *out_dev);
+/* argmax over n values (last maximum wins, as Runtime::argmax,
+ * crates/soso-llm-core/src/runtime.rs:2021-2028); result in *idx_dev. */
+int soso_hip_argmax_dev(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
+
+/* ---- timing on the handle's stream ------------------------------------------- */
+int soso_hip_timer_start(soso_hip *h);
+/* Milliseconds since the matching start, measured with HIP events. */
+int soso_hip_timer_stop(soso_hip *h, float *ms);
+/* Per-launch timing: records HIP event `slot` (0..65535) on the handle's
+ * stream; elapsed waits for slot_b and returns ms between the two events. */
+int soso_hip_event_record(soso_hip *h, int slot);
+int soso_hip_event_elapsed(soso_hip *h, int slot_a, int slot_b, float *ms);
+
+/* ---- HIP graphs of device-resident work ------------------------------------------
+ * begin/end capture every launch (and event record) the handle issues between
+ * them into one graph; launch replays it on the handle's stream.  Only the
+ * *_dev entry points, event records and the decode step may be captured
+ * (they neither allocate nor synchronize). */
+int soso_hip_graph_begin(soso_hip *h);
+int soso_hip_graph_end(soso_hip *h, int *graph_id);
+int soso_hip_graph_launch(soso_hip *h, int graph_id);
+int soso_hip_graph_destroy(soso_hip *h, int graph_id);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

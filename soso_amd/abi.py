@@ -1,0 +1,107 @@
+"""ctypes binding of include/soso_hip.h (libsoso_hip.so, built in-tree).
+
+The library is the product: if it is missing this module raises at import
+time; there is no CPU fallback behind these calls.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsoso_hip.so")
+
+DTYPE_F32 = 1
+DTYPE_Q8_0 = 2
+DTYPE_Q4_K = 3
+DTYPE_Q6_K = 13
+
+OK = 1
+DECLINED = 0
+
+
+class HipError(RuntimeError):
+    pass
+
+
+class Stats(C.Structure):
+    _fields_ = [(n, C.c_uint64) for n in (
+        "launches", "total_ns", "bytes_up", "bytes_down",
+        "weight_bytes_resident", "weights_resident", "weights_declined")]
+
+
+class Op(C.Structure):
+    _fields_ = [
+        ("key", C.c_char_p), ("key_len", C.c_size_t),
+        ("w", C.c_void_p), ("w_len", C.c_size_t), ("dtype", C.c_uint8),
+        ("rows", C.c_size_t), ("cols", C.c_size_t),
+        ("x", C.c_void_p), ("y", C.c_void_p),
+    ]
+
+
+class Expert(C.Structure):
+    _fields_ = [
+        ("keys", C.c_char_p * 3), ("key_lens", C.c_size_t * 3),
+        ("w", C.c_void_p * 3), ("w_len", C.c_size_t * 3), ("dtype", C.c_uint8 * 3),
+        ("tokens", C.c_void_p), ("targets", C.c_void_p), ("n_tokens", C.c_size_t),
+        ("shared", C.c_int),
+    ]
+
+
+_P = C.c_void_p
+_S = C.c_size_t
+_I = C.c_int
+_U8 = C.c_uint8
+_U64 = C.c_uint64
+
+PROTOTYPES = {
+    "soso_hip_create": (_I, [_I, _U64, C.POINTER(_P)]),
+    "soso_hip_destroy": (None, [_P]),
+    "soso_hip_available": (_I, [_P]),
+    "soso_hip_dtype_supported": (_I, [_P, _U8]),
+    "soso_hip_stats": (None, [_P, C.POINTER(Stats)]),
+    "soso_hip_last_error": (C.c_char_p, [_P]),
+    "soso_hip_matvec": (_I, [_P, C.c_char_p, _S, _P, _S, _U8, _S, _S, _P, _P]),
+    "soso_hip_matmul": (_I, [_P, C.c_char_p, _S, _P, _S, _U8, _S, _S, _S, _P, _P]),
+    "soso_hip_matvec_batch": (_I, [_P, _P, _S, _P]),
+    "soso_hip_router_topk": (_I, [_P, C.c_char_p, _S, _P, _P, _S, _S, _S, _S, _P, _P]),
+    "soso_hip_experts_block": (_I, [_P, _P, _S, _S, _S, _S, _P, _P, _S, _P, _P]),
+    "soso_hip_dev_alloc": (_I, [_P, _S, C.POINTER(_P)]),
+    "soso_hip_dev_free": (_I, [_P, _P]),
+    "soso_hip_h2d": (_I, [_P, _P, _P, _S]),
+    "soso_hip_d2h": (_I, [_P, _P, _P, _S]),
+    "soso_hip_sync": (_I, [_P]),
+    "soso_hip_weight_from_dev": (_I, [_P, C.c_char_p, _S, _P, _S, _U8, _S, _S]),
+    "soso_hip_weight_synth": (_I, [_P, C.c_char_p, _S, _U8, _S, _S, _U64, _U64]),
+    "soso_hip_synth_raw": (_I, [_P, _P, _U8, _S, _S, _U64, _U64]),
+    "soso_hip_synth_normal": (_I, [_P, _P, _S, C.c_float, _U64, _U64]),
+    "soso_hip_weight_drop": (_I, [_P, C.c_char_p, _S]),
+    "soso_hip_matvec_dev": (_I, [_P, C.c_char_p, _S, _P, _P]),
+    "soso_hip_matmul_dev": (_I, [_P, C.c_char_p, _S, _S, _P, _P]),
+    "soso_hip_dequant_dev": (_I, [_P, C.c_char_p, _S, _P]),
+    "soso_hip_argmax_dev": (_I, [_P, _P, _S, _P]),
+    "soso_hip_timer_start": (_I, [_P]),
+    "soso_hip_timer_stop": (_I, [_P, C.POINTER(C.c_float)]),
+    "soso_hip_event_record": (_I, [_P, _I]),
+    "soso_hip_event_elapsed": (_I, [_P, _I, _I, C.POINTER(C.c_float)]),
+    "soso_hip_graph_begin": (_I, [_P]),
+    "soso_hip_graph_end": (_I, [_P, C.POINTER(_I)]),
+    "soso_hip_graph_launch": (_I, [_P, _I]),
+    "soso_hip_graph_destroy": (_I, [_P, _I]),
+}
+
+_lib = None
+
+
+def load(path=LIB_PATH):
+    """Loads libsoso_hip.so and declares every entry point of soso_hip.h."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise HipError(f"{path} is missing: run __graft_entry__.build() (no CPU fallback exists)")
+    lib = C.CDLL(path)
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib

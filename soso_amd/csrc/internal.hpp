@@ -1,0 +1,134 @@
+// internal.hpp -- shared host structures and device helpers of libsoso_hip.
+//
+// Device code targets gfx950 (CDNA4, wave64) only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/soso_hip.h"
+
+// ---------------------------------------------------------------------------
+// Formats (crates/sosomodel/src/layout.rs:57-64; Q6_K from GGML via
+// crates/gguf2som/src/lib.rs:1639-1661)
+// ---------------------------------------------------------------------------
+constexpr int Q8_0_ELEMS = 32, Q8_0_BYTES = 36;
+constexpr int Q4_K_ELEMS = 256, Q4_K_BYTES = 144;
+constexpr int Q6_K_ELEMS = 256, Q6_K_BYTES = 210;
+
+// Every quantized kernel works on "units" of 64 consecutive-in-layout
+// elements owned by one lane; a row of `cols` elements has cols/64 units.
+constexpr int UNIT = 64;
+
+// Bytes per row in soso's layout, or 0 when the shape is not representable
+// (crates/sosomodel/src/dequant.rs:53-68).
+inline size_t fmt_row_bytes(uint8_t dtype, size_t cols)
+{
+    switch (dtype) {
+    case SOSO_HIP_DTYPE_F32: return cols * 4;
+    case SOSO_HIP_DTYPE_Q8_0: return cols % 32 ? 0 : cols / 32 * Q8_0_BYTES;
+    case SOSO_HIP_DTYPE_Q4_K: return cols % 256 ? 0 : cols / 256 * Q4_K_BYTES;
+    case SOSO_HIP_DTYPE_Q6_K: return cols % 256 ? 0 : cols / 256 * Q6_K_BYTES;
+    default: return 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side state
+// ---------------------------------------------------------------------------
+struct Weight {
+    void *dev = nullptr; // device copy in this library's layout
+    size_t bytes = 0;
+    uint8_t dtype = 0;
+    size_t rows = 0, cols = 0;
+    bool declined = false;
+};
+
+struct soso_hip {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    uint64_t budget = 0, used = 0;
+    int num_cu = 256;
+    size_t max_lds = 65536;
+    std::unordered_map<std::string, Weight> weights;
+    std::unordered_map<std::string, void *> f32_tensors; // router weights etc.
+    soso_hip_stats_t stats{};
+    std::string err;
+    // reusable device scratch (grown on demand)
+    void *scratch[8] = {};
+    size_t scratch_cap[8] = {};
+    std::vector<hipEvent_t> events; // per-launch timing slots
+    std::vector<hipGraphExec_t> graphs;
+    bool capturing = false;
+};
+
+// error helpers (defined in runtime.hip)
+int set_err(soso_hip *h, int code, const std::string &msg);
+int hip_check(soso_hip *h, hipError_t e, const char *what);
+void *scratch_get(soso_hip *h, int slot, size_t bytes);
+
+// launchers (k_matvec.hip)
+int repack_weight(soso_hip *h, uint8_t dtype, const void *raw_dev, void *packed_dev, size_t rows, size_t cols);
+int launch_matvec(soso_hip *h, const Weight &w, const float *x_dev, float *y_dev, size_t n);
+int launch_dequant(soso_hip *h, const Weight &w, float *out_dev);
+int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
+// (k_synth.hip)
+int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
+                     uint64_t stream);
+int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream);
+// (k_moe.hip)
+int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim,
+                       size_t n_exp, size_t top_k, int32_t *idx_dev, float *wgt_dev, float *logits_dev);
+
+// ---------------------------------------------------------------------------
+// Device helpers
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// v_dot2c_f32_f16: a.lo*b.lo + a.hi*b.hi + c, products exact, f32 accumulate.
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c)
+{
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+}
+
+// v_perm_b32 with src1 = w: selector bytes 0..3 pick bytes of w, 0x0c gives 0.
+__device__ __forceinline__ uint32_t byte_perm(uint32_t w, uint32_t sel) { return __builtin_amdgcn_perm(0u, w, sel); }
+constexpr uint32_t SEL_B02 = 0x0c020c00u; // [b0, 0, b2, 0] -> two 16-bit halves
+constexpr uint32_t SEL_B13 = 0x0c030c01u; // [b1, 0, b3, 0]
+
+__device__ __forceinline__ float half_bits_to_f32(uint32_t b16)
+{
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)b16);
+}
+
+// f16 -> f32 exactly as crates/sosomodel/src/dequant.rs:26-45: the hardware
+// conversion is exact for every finite half and infinity; NaN is made the
+// canonical f32::NAN (0x7fc00000), as Rust's f32::NAN.
+__device__ __forceinline__ float f16_to_f32_ref(uint32_t b16)
+{
+    b16 &= 0xffffu;
+    if ((b16 & 0x7c00u) == 0x7c00u && (b16 & 0x3ffu)) return __builtin_bit_cast(float, 0x7fc00000u);
+    return half_bits_to_f32(b16);
+}
+
+template <int W>
+__device__ __forceinline__ float seg_sum(float v)
+{
+    // butterfly sum inside aligned groups of W lanes (W power of two <= 64)
+#pragma unroll
+    for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}

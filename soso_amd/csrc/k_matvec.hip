@@ -1,0 +1,748 @@
+// k_matvec.hip -- block-quantized matrix-vector products for gfx950.
+//
+// Reference path: soso-llm-core's fused dequant+dot matvecs
+//   Q8_0  crates/soso-llm-core/src/gemm.rs:295-332, 806-836
+//   Q4_K  crates/soso-llm-core/src/gemm.rs:402-461, 842-894
+//   Q6_K  dequant of crates/gguf2som/src/lib.rs:1639-1661 + f32 dot
+//   F32   crates/soso-llm-core/src/gemm.rs:34-56 (MoE router)
+// and the exact dequantizers of crates/sosomodel/src/dequant.rs.
+//
+// Design (one GPU, HBM-bound):
+//  * Weights are repacked once at upload into a per-row "planar" layout: every
+//    lane of a wavefront owns one 64-element unit of a row, and the 16-byte
+//    pieces of all units are stored plane by plane, so each 128-bit load
+//    instruction of a wavefront reads 1 KiB of contiguous HBM.  Same bytes as
+//    soso's layout (no inflation; Q8_0/Q6_K rows are padded to 16 B only when
+//    their byte count is not a multiple of 16).
+//  * x is staged once per workgroup in LDS as an exact f16 hi/lo split of a
+//    power-of-two-scaled copy (x*2^-k = hi + lo, 22 significant bits), with the
+//    pairs ordered for the byte permutes below, plus f32 sums of every 16
+//    elements for the min / offset terms.
+//  * Quant codes are turned into f16 *subnormals* (bits = q, value q*2^-24)
+//    with one AND or one v_perm per two codes, and multiplied with
+//    v_dot2_f32_f16 (exact products, f32 accumulate).  The 2^-24 and 2^k
+//    factors are folded into the per-block scales.  The reduction across the
+//    lanes of a row is a butterfly of cross-lane shuffles.
+#include "internal.hpp"
+
+#include <algorithm>
+
+// ---------------------------------------------------------------------------
+// Packed layouts (per row; see the repack kernels for the exact byte moves)
+//   Q4_K : H[sb] 16 B (d, dmin, scales) | QA[u] 16 B | QB[u] 16 B
+//          unit u = pair p of superblock sb = 4*sb + p (64 elements);
+//          QA/QB = first/second 16 qs bytes of the pair.
+//   Q8_0 : S[b] f32 (region padded to 16 B) | 4 planes of 16 B per unit
+//          unit u = blocks 2u, 2u+1 (64 elements, 64 qs bytes)
+//   Q6_K : SC[sb] 16 B | QH[u] | QLa[u] | QLb[u] (16 B each) | D[sb] 2 B,
+//          unit u = 4*sb + 2*h + kk covers, in half h, l in [16kk, 16kk+16)
+//          for the four quarter-runs l, l+32, l+64, l+96.
+// ---------------------------------------------------------------------------
+static inline size_t rup16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+size_t packed_row_stride(uint8_t dtype, size_t cols)
+{
+    size_t nb;
+    switch (dtype) {
+    case SOSO_HIP_DTYPE_F32: return cols * 4;
+    case SOSO_HIP_DTYPE_Q4_K: return cols / 256 * Q4_K_BYTES;
+    case SOSO_HIP_DTYPE_Q8_0: nb = cols / 32; return rup16(4 * nb) + 32 * nb;
+    case SOSO_HIP_DTYPE_Q6_K: nb = cols / 256; return rup16(210 * nb);
+    default: return 0;
+    }
+}
+
+// Shapes the quantized kernels accept: the 64-element unit must tile a row.
+bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols)
+{
+    if (rows == 0 || cols == 0) return false;
+    switch (dtype) {
+    case SOSO_HIP_DTYPE_F32: return cols % 4 == 0;
+    case SOSO_HIP_DTYPE_Q4_K:
+    case SOSO_HIP_DTYPE_Q6_K: return cols % 256 == 0;
+    case SOSO_HIP_DTYPE_Q8_0: return cols % 64 == 0;
+    default: return false;
+    }
+}
+
+__global__ void repack_q4k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ out, int rows, int nb)
+{
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (long)rows * nb) return;
+    int r = (int)(t / nb), sb = (int)(t % nb);
+    const uint4 *src = (const uint4 *)(raw + (size_t)r * nb * 144 + (size_t)sb * 144);
+    uint8_t *row = out + (size_t)r * nb * 144;
+    uint4 *H = (uint4 *)row, *QA = (uint4 *)(row + 16 * nb), *QB = QA + 4 * nb;
+    H[sb] = src[0];
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        QA[4 * sb + p] = src[1 + 2 * p];
+        QB[4 * sb + p] = src[2 + 2 * p];
+    }
+}
+
+__global__ void repack_q80(const uint8_t *__restrict__ raw, uint8_t *__restrict__ out, int rows, int nb,
+                           int stride)
+{
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (long)rows * nb) return;
+    int r = (int)(t / nb), b = (int)(t % nb);
+    const uint32_t *src = (const uint32_t *)(raw + (size_t)r * nb * 36 + (size_t)b * 36); // 4-byte aligned
+    uint8_t *row = out + (size_t)r * stride;
+    int sreg = (4 * nb + 15) & ~15, U = nb / 2;
+    ((uint32_t *)row)[b] = src[0];
+    int u = b >> 1, half = b & 1;
+    uint32_t *pl0 = (uint32_t *)(row + sreg + (size_t)(2 * half) * 16 * U + 16 * u);
+    uint32_t *pl1 = (uint32_t *)(row + sreg + (size_t)(2 * half + 1) * 16 * U + 16 * u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        pl0[i] = src[1 + i];
+        pl1[i] = src[5 + i];
+    }
+}
+
+__global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ out, int rows, int nb,
+                           int stride)
+{
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (long)rows * nb) return;
+    int r = (int)(t / nb), sb = (int)(t % nb);
+    const uint8_t *blk = raw + (size_t)r * nb * 210 + (size_t)sb * 210;
+    uint8_t *row = out + (size_t)r * stride;
+    int U = 4 * nb;
+    uint8_t *SC = row, *QH = row + 16 * nb, *QLa = QH + 16 * U, *QLb = QLa + 16 * U, *D = QLb + 16 * U;
+    for (int i = 0; i < 16; i++) SC[16 * sb + i] = blk[192 + i];
+    for (int h = 0; h < 2; h++)
+        for (int kk = 0; kk < 2; kk++) {
+            int u = 4 * sb + 2 * h + kk;
+            for (int i = 0; i < 16; i++) {
+                QH[16 * u + i] = blk[128 + h * 32 + kk * 16 + i];
+                QLa[16 * u + i] = blk[h * 64 + kk * 16 + i];
+                QLb[16 * u + i] = blk[h * 64 + 32 + kk * 16 + i];
+            }
+        }
+    D[2 * sb] = blk[208];
+    D[2 * sb + 1] = blk[209];
+}
+
+int repack_weight(soso_hip *h, uint8_t dtype, const void *raw, void *packed, size_t rows, size_t cols)
+{
+    const int T = 256;
+    size_t nb;
+    switch (dtype) {
+    case SOSO_HIP_DTYPE_F32:
+        return hip_check(h, hipMemcpyAsync(packed, raw, rows * cols * 4, hipMemcpyDeviceToDevice, h->stream),
+                         "copy f32 weight");
+    case SOSO_HIP_DTYPE_Q4_K:
+        nb = cols / 256;
+        repack_q4k<<<(unsigned)((rows * nb + T - 1) / T), T, 0, h->stream>>>((const uint8_t *)raw, (uint8_t *)packed,
+                                                                              (int)rows, (int)nb);
+        break;
+    case SOSO_HIP_DTYPE_Q8_0:
+        nb = cols / 32;
+        repack_q80<<<(unsigned)((rows * nb + T - 1) / T), T, 0, h->stream>>>(
+            (const uint8_t *)raw, (uint8_t *)packed, (int)rows, (int)nb, (int)packed_row_stride(dtype, cols));
+        break;
+    case SOSO_HIP_DTYPE_Q6_K:
+        nb = cols / 256;
+        repack_q6k<<<(unsigned)((rows * nb + T - 1) / T), T, 0, h->stream>>>(
+            (const uint8_t *)raw, (uint8_t *)packed, (int)rows, (int)nb, (int)packed_row_stride(dtype, cols));
+        break;
+    default: return set_err(h, SOSO_HIP_ERR_ARG, "repack: dtype");
+    }
+    return hip_check(h, hipGetLastError(), "repack launch");
+}
+
+// ---------------------------------------------------------------------------
+// x staging
+// LDS: xp[g] = {hi(e0,e2), hi(e1,e3), lo(e0,e2), lo(e1,e3)} for the 4-element
+// group g (elements 4g..4g+3 of x*2^-k); s16[i] = sum of x[16i..16i+16) (f32,
+// unscaled); kexp = k with max|x|*2^-k < 2^14.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t pack_h2(float a, float b)
+{
+    f16x2_t v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ void stage_x(const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kexp_s, float *red)
+{
+    const int G = cols >> 2, nthr = blockDim.x, tid = threadIdx.x;
+    const float4 *x4 = (const float4 *)x;
+    float m = 0.0f;
+    for (int g = tid; g < G; g += nthr) {
+        float4 v = x4[g];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+    m = wave_max(m);
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        float mm = 0.0f;
+        for (int w = 0; w < (nthr >> 6); w++) mm = fmaxf(mm, red[w]);
+        int k = 0;
+        if (mm > 0.0f && mm < INFINITY) k = __builtin_amdgcn_frexp_expf(mm) - 14;
+        *kexp_s = k;
+    }
+    __syncthreads();
+    const int k = *kexp_s;
+    for (int g = tid; g < G; g += nthr) {
+        float4 v = x4[g];
+        float a0 = ldexpf(v.x, -k), a1 = ldexpf(v.y, -k), a2 = ldexpf(v.z, -k), a3 = ldexpf(v.w, -k);
+        _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1, h2 = (_Float16)a2, h3 = (_Float16)a3;
+        float l0 = a0 - (float)h0, l1 = a1 - (float)h1, l2 = a2 - (float)h2, l3 = a3 - (float)h3;
+        uint4 o;
+        o.x = __builtin_bit_cast(uint32_t, (f16x2_t){h0, h2});
+        o.y = __builtin_bit_cast(uint32_t, (f16x2_t){h1, h3});
+        o.z = pack_h2(l0, l2);
+        o.w = pack_h2(l1, l3);
+        xp[g] = o;
+        // cols % 64 == 0 and nthr % 64 == 0: aligned groups of 4 lanes are
+        // active together, so the shuffles below stay inside active lanes.
+        float s = (v.x + v.y) + (v.z + v.w);
+        s += __shfl_xor(s, 1, 64);
+        s += __shfl_xor(s, 2, 64);
+        if ((g & 3) == 0) s16[g >> 2] = s;
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// Per-format unit math
+// ---------------------------------------------------------------------------
+enum { FMT_Q4K = 0, FMT_Q80 = 1, FMT_Q6K = 2 };
+
+template <int FMT> struct WRow;
+template <> struct WRow<FMT_Q4K> {
+    uint4 h, a, b;
+};
+template <> struct WRow<FMT_Q80> {
+    uint2 s;
+    uint4 q[4];
+};
+template <> struct WRow<FMT_Q6K> {
+    uint4 qh, la, lb;
+    uint2 sc;
+    uint32_t d;
+};
+
+// lane constants for one unit
+struct UConst {
+    float c[4];
+    uint32_t k1, k2, s, bsh; // Q4_K scale-decode selectors; Q6_K uses bsh = 8*kk
+    int sb;
+};
+
+template <int FMT>
+__device__ __forceinline__ void unit_setup(const uint4 *xp, const float *s16, int u, uint4 (&xv)[16], UConst &c)
+{
+    if (FMT == FMT_Q4K || FMT == FMT_Q80) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) xv[j] = xp[16 * u + j];
+        float s0 = s16[4 * u] + s16[4 * u + 1], s1 = s16[4 * u + 2] + s16[4 * u + 3];
+        if (FMT == FMT_Q4K) {
+            c.c[0] = s0;
+            c.c[1] = s1;
+            int p = u & 3;
+            bool hi = p >= 2;
+            c.k1 = hi ? 0x0F0F0F0Fu : 0u;
+            c.k2 = hi ? 0x30303030u : 0x3F3F3F3Fu;
+            c.s = hi ? 2u : 0u;
+            c.bsh = (uint32_t)(p & 1) * 16u;
+            c.sb = u >> 2;
+        } else {
+            c.c[0] = 128.0f * s0;
+            c.c[1] = 128.0f * s1;
+        }
+    } else {
+        int sb = u >> 2, h = (u >> 1) & 1, kk = u & 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) xv[4 * i + t] = xp[sb * 64 + h * 32 + 8 * i + 4 * kk + t];
+            c.c[i] = 32.0f * s16[sb * 16 + h * 8 + 2 * i + kk];
+        }
+        c.sb = sb;
+        c.bsh = 8u * (uint32_t)kk;
+        c.s = (uint32_t)h;
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void load_row(const uint8_t *__restrict__ Wr, int cols, int u, const UConst &c, WRow<FMT> &w)
+{
+    if constexpr (FMT == FMT_Q4K) {
+        const int nb = cols >> 8, U = cols >> 6;
+        w.h = *(const uint4 *)(Wr + 16 * c.sb);
+        w.a = *(const uint4 *)(Wr + 16 * nb + 16 * u);
+        w.b = *(const uint4 *)(Wr + 16 * nb + 16 * U + 16 * u);
+    } else if constexpr (FMT == FMT_Q80) {
+        const int nb = cols >> 5, U = cols >> 6, sreg = (4 * nb + 15) & ~15;
+        w.s = *(const uint2 *)(Wr + 8 * u);
+#pragma unroll
+        for (int i = 0; i < 4; i++) w.q[i] = *(const uint4 *)(Wr + sreg + 16 * U * i + 16 * u);
+    } else {
+        const int nb = cols >> 8, U = cols >> 6;
+        const uint8_t *QH = Wr + 16 * nb;
+        w.qh = *(const uint4 *)(QH + 16 * u);
+        w.la = *(const uint4 *)(QH + 16 * U + 16 * u);
+        w.lb = *(const uint4 *)(QH + 32 * U + 16 * u);
+        w.sc = *(const uint2 *)(Wr + 16 * c.sb + 8 * c.s);
+        w.d = *(const unsigned short *)(QH + 48 * U + 2 * c.sb);
+    }
+}
+
+// Partial dot of one unit of one row, in units of x (the 2^k scale is in P).
+template <int FMT>
+__device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[16], const UConst &c, float P)
+{
+    if constexpr (FMT == FMT_Q4K) {
+        // Low nibbles of the pair are sub-block 2p (elements 0..31 of the
+        // unit), high nibbles sub-block 2p+1 (elements 32..63), read as 16*q.
+        const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
+        float l0 = 0.f, l1 = 0.f, h0 = 0.f, h1 = 0.f;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const uint32_t v = q[t], v8 = v >> 8;
+            const uint32_t A = v & 0x000F000Fu, C = v & 0x00F000F0u;
+            const uint32_t B = v8 & 0x000F000Fu, D = v8 & 0x00F000F0u;
+            const uint4 xl = xv[t], xh = xv[8 + t];
+            l0 = dot2(A, xl.x, l0);
+            l1 = dot2(A, xl.z, l1);
+            l0 = dot2(B, xl.y, l0);
+            l1 = dot2(B, xl.w, l1);
+            h0 = dot2(C, xh.x, h0);
+            h1 = dot2(C, xh.z, h1);
+            h0 = dot2(D, xh.y, h0);
+            h1 = dot2(D, xh.w, h1);
+        }
+        // 6-bit scale/min of sub-blocks 2p, 2p+1 (get_scale_min_k4,
+        // crates/sosomodel/src/dequant.rs:150-159), four at a time per byte lane.
+        const uint32_t SC4 = ((w.h.w & c.k1) | ((w.h.y >> c.s) & c.k2)) >> c.bsh;
+        const uint32_t M4 = (((w.h.w >> 4) & c.k1) | ((w.h.z >> c.s) & c.k2)) >> c.bsh;
+        const float sca = (float)(SC4 & 0xffu), scb = (float)((SC4 >> 8) & 0xffu);
+        const float ma = (float)(M4 & 0xffu), mb = (float)((M4 >> 8) & 0xffu);
+        const float d = half_bits_to_f32(w.h.x & 0xffffu), dmin = half_bits_to_f32(w.h.x >> 16);
+        const float uu = fmaf(sca * 16.0f, l0 + l1, scb * (h0 + h1));
+        const float vv = fmaf(mb, c.c[1], ma * c.c[0]);
+        return fmaf(d * P, uu, -(dmin * vv)); // P = 2^(20+k)
+    } else if constexpr (FMT == FMT_Q80) {
+        float s[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll
+        for (int blk = 0; blk < 2; blk++) {
+            const uint32_t q[8] = {w.q[2 * blk].x, w.q[2 * blk].y, w.q[2 * blk].z, w.q[2 * blk].w,
+                                   w.q[2 * blk + 1].x, w.q[2 * blk + 1].y, w.q[2 * blk + 1].z, w.q[2 * blk + 1].w};
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const uint32_t v = q[t] ^ 0x80808080u; // offset binary: q + 128
+                const uint32_t A = byte_perm(v, SEL_B02), B = byte_perm(v, SEL_B13);
+                const uint4 xx = xv[8 * blk + t];
+                s[blk][0] = dot2(A, xx.x, s[blk][0]);
+                s[blk][1] = dot2(A, xx.z, s[blk][1]);
+                s[blk][0] = dot2(B, xx.y, s[blk][0]);
+                s[blk][1] = dot2(B, xx.w, s[blk][1]);
+            }
+        }
+        const float t0 = fmaf(s[0][0] + s[0][1], P, -c.c[0]); // P = 2^(24+k)
+        const float t1 = fmaf(s[1][0] + s[1][1], P, -c.c[1]);
+        return fmaf(__builtin_bit_cast(float, w.s.x), t0, __builtin_bit_cast(float, w.s.y) * t1);
+    } else {
+        float s[4][2];
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[i][0] = s[i][1] = 0.f;
+        const uint32_t la[4] = {w.la.x, w.la.y, w.la.z, w.la.w}, lb[4] = {w.lb.x, w.lb.y, w.lb.z, w.lb.w};
+        const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            // q = ql nibble | 2 bits of qh << 4 (dequantize_row_q6_K,
+            // crates/gguf2som/src/lib.rs:1650-1658), four codes per dword.
+            uint32_t q[4];
+            q[0] = (la[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x03030303u) << 4);
+            q[1] = (lb[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x0C0C0C0Cu) << 2);
+            q[2] = ((la[t] >> 4) & 0x0F0F0F0Fu) | (qh[t] & 0x30303030u);
+            q[3] = ((lb[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> 2) & 0x30303030u);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t A = byte_perm(q[i], SEL_B02), B = byte_perm(q[i], SEL_B13);
+                const uint4 xx = xv[4 * i + t];
+                s[i][0] = dot2(A, xx.x, s[i][0]);
+                s[i][1] = dot2(A, xx.z, s[i][1]);
+                s[i][0] = dot2(B, xx.y, s[i][0]);
+                s[i][1] = dot2(B, xx.w, s[i][1]);
+            }
+        }
+        // sub-scales sc[h*8 + kk + 2i] (int8), the -32 offset through c[i] = 32*sum(x)
+        const float sc0 = (float)(int8_t)(w.sc.x >> c.bsh), sc1 = (float)(int8_t)(w.sc.x >> (c.bsh + 16));
+        const float sc2 = (float)(int8_t)(w.sc.y >> c.bsh), sc3 = (float)(int8_t)(w.sc.y >> (c.bsh + 16));
+        float acc = sc0 * fmaf(s[0][0] + s[0][1], P, -c.c[0]); // P = 2^(24+k)
+        acc = fmaf(sc1, fmaf(s[1][0] + s[1][1], P, -c.c[1]), acc);
+        acc = fmaf(sc2, fmaf(s[2][0] + s[2][1], P, -c.c[2]), acc);
+        acc = fmaf(sc3, fmaf(s[3][0] + s[3][1], P, -c.c[3]), acc);
+        return half_bits_to_f32(w.d) * acc;
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ float fmt_pscale(int k)
+{
+    return ldexpf(1.0f, (FMT == FMT_Q4K ? 20 : 24) + k);
+}
+
+// ---------------------------------------------------------------------------
+// Kernel A: every row has U = cols/64 <= LPR units; each lane keeps its x
+// unit in VGPRs for the whole launch and walks a contiguous strip of row
+// passes with DEPTH rows of loads in flight.
+// ---------------------------------------------------------------------------
+template <int FMT, int LPR, int DEPTH>
+__global__ void __launch_bounds__(512) mv_xreg(const uint8_t *__restrict__ W, size_t stride,
+                                               const float *__restrict__ x, float *__restrict__ y, int rows, int cols)
+{
+    extern __shared__ uint4 smem[];
+    __shared__ float red[16];
+    __shared__ int kexp_s;
+    uint4 *xp = smem;
+    float *s16 = (float *)(xp + (cols >> 2));
+    stage_x(x, cols, xp, s16, &kexp_s, red);
+
+    constexpr int RW = 64 / LPR;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int U = cols >> 6;
+    const int ul = lane & (LPR - 1), slot = lane / LPR;
+    const bool uact = ul < U;
+    const int u = uact ? ul : 0;
+    uint4 xv[16];
+    UConst c;
+    unit_setup<FMT>(xp, s16, u, xv, c);
+    const float P = fmt_pscale<FMT>(kexp_s);
+
+    const int passes = (rows + RW - 1) / RW;
+    const int gw = blockIdx.x * nw + wave, tw = gridDim.x * nw;
+    const int p0 = (int)((long)passes * gw / tw), p1 = (int)((long)passes * (gw + 1) / tw);
+    auto rowp = [&](int pp) {
+        int r = pp * RW + slot;
+        r = r < rows ? r : rows - 1;
+        return W + (size_t)r * stride;
+    };
+    WRow<FMT> buf[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH; i++)
+        if (p0 + i < p1) load_row<FMT>(rowp(p0 + i), cols, u, c, buf[i]);
+    for (int pb = p0; pb < p1; pb += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; i++) {
+            const int pp = pb + i;
+            if (pp < p1) {
+                const WRow<FMT> cur = buf[i];
+                if (pp + DEPTH < p1) load_row<FMT>(rowp(pp + DEPTH), cols, u, c, buf[i]);
+                float part = unit_dot<FMT>(cur, xv, c, P);
+                part = uact ? part : 0.0f;
+                part = seg_sum<LPR>(part);
+                const int r = pp * RW + slot;
+                if (ul == 0 && r < rows) y[r] = part;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel B: rows wider than 64 units.  Each wavefront takes blocks of R rows;
+// the lanes walk the units of the row 64 at a time, reading each x unit once
+// from LDS for the R rows.
+// ---------------------------------------------------------------------------
+template <int FMT, int R>
+__global__ void __launch_bounds__(512) mv_loop(const uint8_t *__restrict__ W, size_t stride,
+                                               const float *__restrict__ x, float *__restrict__ y, int rows, int cols)
+{
+    extern __shared__ uint4 smem[];
+    __shared__ float red[16];
+    __shared__ int kexp_s;
+    uint4 *xp = smem;
+    float *s16 = (float *)(xp + (cols >> 2));
+    stage_x(x, cols, xp, s16, &kexp_s, red);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int U = cols >> 6, iters = (U + 63) >> 6;
+    const float P = fmt_pscale<FMT>(kexp_s);
+    const int nblk = (rows + R - 1) / R;
+    const int gw = blockIdx.x * nw + wave, tw = gridDim.x * nw;
+    const int b0 = (int)((long)nblk * gw / tw), b1 = (int)((long)nblk * (gw + 1) / tw);
+    for (int blk = b0; blk < b1; blk++) {
+        float part[R];
+#pragma unroll
+        for (int rr = 0; rr < R; rr++) part[rr] = 0.0f;
+        for (int it = 0; it < iters; it++) {
+            const int ul = lane + 64 * it;
+            const bool act = ul < U;
+            const int u = act ? ul : U - 1;
+            uint4 xv[16];
+            UConst c;
+            unit_setup<FMT>(xp, s16, u, xv, c);
+            WRow<FMT> w[R];
+#pragma unroll
+            for (int rr = 0; rr < R; rr++) {
+                int r = blk * R + rr;
+                r = r < rows ? r : rows - 1;
+                load_row<FMT>(W + (size_t)r * stride, cols, u, c, w[rr]);
+            }
+#pragma unroll
+            for (int rr = 0; rr < R; rr++) {
+                const float v = unit_dot<FMT>(w[rr], xv, c, P);
+                part[rr] += act ? v : 0.0f;
+            }
+        }
+#pragma unroll
+        for (int rr = 0; rr < R; rr++) {
+            const float v = seg_sum<64>(part[rr]);
+            const int r = blk * R + rr;
+            if (lane == 0 && r < rows) y[r] = v;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// F32 matvec (MoE router and other small f32 tensors): one wavefront per row,
+// float4 loads, butterfly reduction.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) mv_f32(const float *__restrict__ W, const float *__restrict__ x,
+                                              float *__restrict__ y, int rows, int cols)
+{
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (r >= rows) return; // wave-uniform
+    const float4 *w4 = (const float4 *)(W + (size_t)r * cols);
+    const float4 *x4 = (const float4 *)x;
+    float a0 = 0.f, a1 = 0.f;
+    for (int i = lane; i < (cols >> 2); i += 64) {
+        float4 w = w4[i], v = x4[i];
+        a0 = fmaf(w.x, v.x, a0);
+        a1 = fmaf(w.y, v.y, a1);
+        a0 = fmaf(w.z, v.z, a0);
+        a1 = fmaf(w.w, v.w, a1);
+    }
+    float s = seg_sum<64>(a0 + a1);
+    if (lane == 0) y[r] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Launch selection
+// ---------------------------------------------------------------------------
+static int env_int(const char *name, int dflt)
+{
+    const char *v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+template <int FMT>
+static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
+{
+    const int rows = (int)w.rows, cols = (int)w.cols, U = cols / 64;
+    const size_t stride = packed_row_stride(w.dtype, w.cols);
+    const size_t lds = (size_t)cols * 4 + (size_t)cols / 16 * 4;
+    if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec: x does not fit in LDS");
+    const int threads = env_int("SOSO_HIP_WG", 512);
+    const int per_cu = env_int("SOSO_HIP_WG_PER_CU", 1);
+    const uint8_t *W = (const uint8_t *)w.dev;
+    if (U <= 64) {
+        const int LPR = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
+        const int passes = (rows + 64 / LPR - 1) / (64 / LPR);
+        int grid = std::min(h->num_cu * per_cu, (passes + threads / 64 - 1) / (threads / 64));
+        grid = std::max(grid, 1);
+        constexpr int DEP = 4;
+#define MV_CASE(L)                                                                                                  \
+    case L: mv_xreg<FMT, L, DEP><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols); break;
+        switch (LPR) {
+            MV_CASE(1) MV_CASE(2) MV_CASE(4) MV_CASE(8) MV_CASE(16) MV_CASE(32) MV_CASE(64)
+        }
+#undef MV_CASE
+    } else {
+        constexpr int R = 2;
+        const int nblk = (rows + R - 1) / R;
+        int grid = std::min(h->num_cu * per_cu, (nblk + threads / 64 - 1) / (threads / 64));
+        grid = std::max(grid, 1);
+        mv_loop<FMT, R><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
+    }
+    return hip_check(h, hipGetLastError(), "matvec launch");
+}
+
+int launch_matvec(soso_hip *h, const Weight &w, const float *x, float *y, size_t n)
+{
+    for (size_t t = 0; t < n; t++) {
+        const float *xt = x + t * w.cols;
+        float *yt = y + t * w.rows;
+        int rc;
+        switch (w.dtype) {
+        case SOSO_HIP_DTYPE_Q4_K: rc = launch_fmt<FMT_Q4K>(h, w, xt, yt); break;
+        case SOSO_HIP_DTYPE_Q8_0: rc = launch_fmt<FMT_Q80>(h, w, xt, yt); break;
+        case SOSO_HIP_DTYPE_Q6_K: rc = launch_fmt<FMT_Q6K>(h, w, xt, yt); break;
+        case SOSO_HIP_DTYPE_F32: {
+            const int rows = (int)w.rows;
+            mv_f32<<<(rows + 3) / 4, 256, 0, h->stream>>>((const float *)w.dev, xt, yt, rows, (int)w.cols);
+            rc = hip_check(h, hipGetLastError(), "matvec f32 launch");
+            break;
+        }
+        default: rc = set_err(h, SOSO_HIP_ERR_ARG, "matvec: dtype");
+        }
+        if (rc < 0 || rc == 0) return rc;
+    }
+    return SOSO_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Exact dequantization from the packed layout (bit-exactness witness).
+// Arithmetic as crates/sosomodel/src/dequant.rs (Q8_0 :74-97, Q4_K :204-241)
+// and crates/gguf2som/src/lib.rs:1639-1661 (Q6_K), never contracted to FMA.
+// ---------------------------------------------------------------------------
+__global__ void dq_q4k(const uint8_t *__restrict__ W, float *__restrict__ out, int rows, int cols)
+{
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int U = cols >> 6, nb = cols >> 8;
+    if (t >= (long)rows * U) return;
+    const int r = (int)(t / U), u = (int)(t % U), sb = u >> 2, p = u & 3;
+    const uint8_t *Wr = W + (size_t)r * nb * 144;
+    const uint8_t *H = Wr + 16 * sb;
+    const uint8_t *qa = Wr + 16 * nb + 16 * u, *qb = Wr + 16 * nb + 16 * U + 16 * u;
+    const float d = f16_to_f32_ref(H[0] | (H[1] << 8)), dmin = f16_to_f32_ref(H[2] | (H[3] << 8));
+    const uint8_t *s = H + 4;
+    uint8_t sc[2], m[2];
+    for (int k = 0; k < 2; k++) {
+        int j = 2 * p + k;
+        if (j < 4) {
+            sc[k] = s[j] & 63;
+            m[k] = s[j + 4] & 63;
+        } else {
+            sc[k] = (uint8_t)((s[j + 4] & 0x0F) | ((s[j - 4] >> 6) << 4));
+            m[k] = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+        }
+    }
+    const float d1 = __fmul_rn(d, (float)sc[0]), min1 = __fmul_rn(dmin, (float)m[0]);
+    const float d2 = __fmul_rn(d, (float)sc[1]), min2 = __fmul_rn(dmin, (float)m[1]);
+    float *o = out + (size_t)r * cols + 64 * u;
+    for (int l = 0; l < 32; l++) {
+        const uint8_t q = l < 16 ? qa[l] : qb[l - 16];
+        o[l] = __fsub_rn(__fmul_rn(d1, (float)(q & 0x0F)), min1);
+        o[32 + l] = __fsub_rn(__fmul_rn(d2, (float)(q >> 4)), min2);
+    }
+}
+
+__global__ void dq_q80(const uint8_t *__restrict__ W, float *__restrict__ out, int rows, int cols, int stride)
+{
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int nb = cols >> 5, U = cols >> 6, sreg = (4 * nb + 15) & ~15;
+    if (t >= (long)rows * nb) return;
+    const int r = (int)(t / nb), b = (int)(t % nb), u = b >> 1, half = b & 1;
+    const uint8_t *Wr = W + (size_t)r * stride;
+    const float scale = ((const float *)Wr)[b];
+    float *o = out + (size_t)r * cols + 32 * b;
+    for (int i = 0; i < 32; i++) {
+        const int plane = 2 * half + (i >> 4);
+        const int8_t q = (int8_t)Wr[sreg + 16 * U * plane + 16 * u + (i & 15)];
+        o[i] = __fmul_rn((float)q, scale);
+    }
+}
+
+__global__ void dq_q6k(const uint8_t *__restrict__ W, float *__restrict__ out, int rows, int cols, int stride)
+{
+    long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int U = cols >> 6, nb = cols >> 8;
+    if (t >= (long)rows * U) return;
+    const int r = (int)(t / U), u = (int)(t % U), sb = u >> 2, h = (u >> 1) & 1, kk = u & 1;
+    const uint8_t *Wr = W + (size_t)r * stride;
+    const uint8_t *QH = Wr + 16 * nb + 16 * u, *QLa = Wr + 16 * nb + 16 * U + 16 * u;
+    const uint8_t *QLb = Wr + 16 * nb + 32 * U + 16 * u, *Dp = Wr + 16 * nb + 48 * U + 2 * sb;
+    const int8_t *sc = (const int8_t *)(Wr + 16 * sb + 8 * h);
+    const float d = f16_to_f32_ref(Dp[0] | (Dp[1] << 8));
+    float *o = out + (size_t)r * cols + 256 * sb + 128 * h;
+    for (int i = 0; i < 16; i++) {
+        const int l = 16 * kk + i;
+        const int q1 = (int)((QLa[i] & 0x0F) | ((QH[i] & 3) << 4)) - 32;
+        const int q2 = (int)((QLb[i] & 0x0F) | (((QH[i] >> 2) & 3) << 4)) - 32;
+        const int q3 = (int)((QLa[i] >> 4) | (((QH[i] >> 4) & 3) << 4)) - 32;
+        const int q4 = (int)((QLb[i] >> 4) | (((QH[i] >> 6) & 3) << 4)) - 32;
+        o[l] = __fmul_rn(__fmul_rn(d, (float)sc[kk]), (float)q1);
+        o[l + 32] = __fmul_rn(__fmul_rn(d, (float)sc[kk + 2]), (float)q2);
+        o[l + 64] = __fmul_rn(__fmul_rn(d, (float)sc[kk + 4]), (float)q3);
+        o[l + 96] = __fmul_rn(__fmul_rn(d, (float)sc[kk + 6]), (float)q4);
+    }
+}
+
+int launch_dequant(soso_hip *h, const Weight &w, float *out)
+{
+    const int T = 256, rows = (int)w.rows, cols = (int)w.cols;
+    const int stride = (int)packed_row_stride(w.dtype, w.cols);
+    long n;
+    switch (w.dtype) {
+    case SOSO_HIP_DTYPE_Q4_K:
+        n = (long)rows * (cols / 64);
+        dq_q4k<<<(unsigned)((n + T - 1) / T), T, 0, h->stream>>>((const uint8_t *)w.dev, out, rows, cols);
+        break;
+    case SOSO_HIP_DTYPE_Q8_0:
+        n = (long)rows * (cols / 32);
+        dq_q80<<<(unsigned)((n + T - 1) / T), T, 0, h->stream>>>((const uint8_t *)w.dev, out, rows, cols, stride);
+        break;
+    case SOSO_HIP_DTYPE_Q6_K:
+        n = (long)rows * (cols / 64);
+        dq_q6k<<<(unsigned)((n + T - 1) / T), T, 0, h->stream>>>((const uint8_t *)w.dev, out, rows, cols, stride);
+        break;
+    case SOSO_HIP_DTYPE_F32:
+        return hip_check(h, hipMemcpyAsync(out, w.dev, w.rows * w.cols * 4, hipMemcpyDeviceToDevice, h->stream),
+                         "dequant f32");
+    default: return set_err(h, SOSO_HIP_ERR_ARG, "dequant: dtype");
+    }
+    return hip_check(h, hipGetLastError(), "dequant launch");
+}
+
+// ---------------------------------------------------------------------------
+// argmax (crates/soso-llm-core/src/runtime.rs:2021-2028): the LAST maximum
+// wins.  Combining ordered segments as "earlier wins only if strictly
+// greater" reproduces the sequential fold for finite inputs.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, int n, uint32_t *__restrict__ out)
+{
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int tid = threadIdx.x, nt = blockDim.x;
+    // contiguous chunk per thread keeps the combine order simple
+    const int c0 = (int)((long)n * tid / nt), c1 = (int)((long)n * (tid + 1) / nt);
+    float bv = -INFINITY;
+    int bi = -1;
+    for (int i = c0; i < c1; i++) {
+        const float v = x[i];
+        if (bi < 0 || !(bv > v)) {
+            bv = v;
+            bi = i;
+        }
+    }
+    // reduce over lanes (ordered: lower lane = earlier segment)
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_down(bv, o, 64);
+        const int oi = __shfl_down(bi, o, 64);
+        const int lane = tid & 63;
+        if (lane + o < 64 && (lane & (2 * o - 1)) == 0 && oi >= 0) {
+            if (bi < 0 || !(bv > ov)) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float v = sv[0];
+        int i = si[0];
+        for (int w = 1; w < (nt >> 6); w++)
+            if (si[w] >= 0 && (i < 0 || !(v > sv[w]))) {
+                v = sv[w];
+                i = si[w];
+            }
+        *out = (uint32_t)(i < 0 ? 0 : i);
+    }
+}
+
+int launch_argmax(soso_hip *h, const float *x, size_t n, uint32_t *idx)
+{
+    k_argmax<<<1, 1024, 0, h->stream>>>(x, (int)n, idx);
+    return hip_check(h, hipGetLastError(), "argmax launch");
+}

@@ -1,0 +1,164 @@
+// k_synth.hip -- seeded synthetic tensors on the device (bench / test inputs).
+//
+// Counter-based SplitMix64 keyed by (seed, stream, index) and integer-only
+// derived values, so the host generator used by the tests produces the very
+// same bytes.  Normals are Irwin-Hall(12) sums of 16-bit uniforms, computed
+// exactly: N = (S - 393210) / 65536 (mean 0, variance 1).  Half-precision
+// scales use soso's f32->f16 rounding (ties up,
+// crates/soso-llm-core/src/f16.rs:10-37).
+#include "internal.hpp"
+
+__device__ __forceinline__ uint64_t fin64(uint64_t z)
+{
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ uint64_t rng(uint64_t seed, uint64_t stream, uint64_t i)
+{
+    const uint64_t key = fin64(seed ^ fin64(stream + 0x9E3779B97F4A7C15ull));
+    return fin64(key + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+
+__device__ __forceinline__ float normal(uint64_t seed, uint64_t stream, uint64_t i)
+{
+    int32_t s = 0;
+    for (int h = 0; h < 3; h++) {
+        const uint64_t r = rng(seed, stream, 3 * i + (uint64_t)h);
+        s += (int32_t)(r & 0xffff) + (int32_t)((r >> 16) & 0xffff) + (int32_t)((r >> 32) & 0xffff) + (int32_t)(r >> 48);
+    }
+    return __fmul_rn((float)(s - 393210), 1.0f / 65536.0f);
+}
+
+// crates/soso-llm-core/src/f16.rs:10-37
+__device__ __forceinline__ uint16_t f32_to_f16_soso(float v)
+{
+    const uint32_t bits = __builtin_bit_cast(uint32_t, v);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const int32_t exp = (int32_t)((bits >> 23) & 0xffu);
+    const uint32_t frac = bits & 0x7fffffu;
+    if (exp == 255) return (uint16_t)(sign | 0x7c00u | (frac != 0 ? 0x200u : 0u));
+    const int32_t e = exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return sign;
+        const uint32_t f = frac | 0x800000u;
+        const uint32_t shift = (uint32_t)(14 - e);
+        const uint16_t sub = (uint16_t)(f >> shift);
+        const uint16_t round = (uint16_t)((f >> (shift - 1)) & 1u);
+        return (uint16_t)(sign | (uint16_t)(sub + round));
+    }
+    const uint32_t half = ((uint32_t)e << 10) | (frac >> 13);
+    const uint16_t round = (uint16_t)((frac >> 12) & 1u);
+    return (uint16_t)((uint16_t)(sign | (uint16_t)half) + round);
+}
+
+#define SUB(s, f) (((s) << 4) | (uint64_t)(f))
+
+__global__ void synth_q4k(uint8_t *out, long nblk, uint64_t seed, uint64_t st)
+{
+    const long b = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    uint8_t *blk = out + b * Q4_K_BYTES;
+    const uint16_t d = f32_to_f16_soso(__fmul_rn(fabsf(normal(seed, SUB(st, 0), b)), 0.01f));
+    const uint16_t dm = f32_to_f16_soso(__fmul_rn(fabsf(normal(seed, SUB(st, 1), b)), 0.01f));
+    uint32_t *w = (uint32_t *)blk; // 144-byte blocks: 4-byte aligned
+    w[0] = (uint32_t)d | ((uint32_t)dm << 16);
+    const uint64_t a = rng(seed, SUB(st, 2), 2 * b), c = rng(seed, SUB(st, 2), 2 * b + 1);
+    uint8_t sc[8], m[8], s[12];
+    for (int j = 0; j < 8; j++) {
+        sc[j] = (uint8_t)((a >> (8 * j)) & 63);
+        m[j] = (uint8_t)((c >> (8 * j)) & 63);
+    }
+    // crates/soso-llm-core/src/quant.rs:46-54 (q4k_pack_scales)
+    for (int j = 0; j < 4; j++) {
+        s[j] = (uint8_t)((sc[j] & 63) | ((sc[j + 4] >> 4) << 6));
+        s[j + 4] = (uint8_t)((m[j] & 63) | ((m[j + 4] >> 4) << 6));
+        s[j + 8] = (uint8_t)((sc[j + 4] & 0x0F) | ((m[j + 4] & 0x0F) << 4));
+    }
+    for (int j = 0; j < 3; j++) w[1 + j] = s[4 * j] | (s[4 * j + 1] << 8) | (s[4 * j + 2] << 16) | ((uint32_t)s[4 * j + 3] << 24);
+    for (int k = 0; k < 16; k++) {
+        const uint64_t r = rng(seed, SUB(st, 3), 16 * b + k);
+        w[4 + 2 * k] = (uint32_t)r;
+        w[5 + 2 * k] = (uint32_t)(r >> 32);
+    }
+}
+
+__global__ void synth_q80(uint8_t *out, long nblk, uint64_t seed, uint64_t st)
+{
+    const long b = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    uint32_t *w = (uint32_t *)(out + b * Q8_0_BYTES);
+    const uint16_t hb = f32_to_f16_soso(__fmul_rn(fabsf(normal(seed, SUB(st, 0), b)), 0.02f));
+    w[0] = __builtin_bit_cast(uint32_t, half_bits_to_f32(hb)); // finite by construction
+    for (int k = 0; k < 8; k++) {
+        const uint64_t r = rng(seed, SUB(st, 1), 8 * b + k);
+        uint32_t v = 0;
+        for (int j = 0; j < 4; j++) {
+            const uint32_t u = (uint32_t)((r >> (16 * j)) & 0xffff);
+            v |= (uint32_t)(uint8_t)(int8_t)((int)(u % 255u) - 127) << (8 * j);
+        }
+        w[1 + k] = v;
+    }
+}
+
+__global__ void synth_q6k(uint8_t *out, long nblk, uint64_t seed, uint64_t st)
+{
+    const long b = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    uint16_t *w = (uint16_t *)(out + b * Q6_K_BYTES); // 210-byte blocks: 2-byte aligned
+    for (int k = 0; k < 16; k++) {
+        const uint64_t r = rng(seed, SUB(st, 0), 16 * b + k);
+        for (int j = 0; j < 4; j++) w[4 * k + j] = (uint16_t)(r >> (16 * j));
+    }
+    for (int k = 0; k < 8; k++) {
+        const uint64_t r = rng(seed, SUB(st, 1), 8 * b + k);
+        for (int j = 0; j < 4; j++) w[64 + 4 * k + j] = (uint16_t)(r >> (16 * j));
+    }
+    for (int k = 0; k < 2; k++) {
+        const uint64_t r = rng(seed, SUB(st, 2), 2 * b + k);
+        for (int j = 0; j < 4; j++) w[96 + 4 * k + j] = (uint16_t)(r >> (16 * j));
+    }
+    w[104] = f32_to_f16_soso(__fmul_rn(fabsf(normal(seed, SUB(st, 3), b)), 0.01f));
+}
+
+__global__ void synth_normal_k(float *out, long n, float sigma, uint64_t seed, uint64_t st)
+{
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = __fmul_rn(normal(seed, st, i), sigma);
+}
+
+int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed, uint64_t stream)
+{
+    const int T = 256;
+    long nblk;
+    switch (dtype) {
+    case SOSO_HIP_DTYPE_Q4_K:
+        if (cols % 256) return set_err(h, SOSO_HIP_ERR_ARG, "synth: cols");
+        nblk = (long)(rows * (cols / 256));
+        synth_q4k<<<(unsigned)((nblk + T - 1) / T), T, 0, h->stream>>>((uint8_t *)dst, nblk, seed, stream);
+        break;
+    case SOSO_HIP_DTYPE_Q8_0:
+        if (cols % 32) return set_err(h, SOSO_HIP_ERR_ARG, "synth: cols");
+        nblk = (long)(rows * (cols / 32));
+        synth_q80<<<(unsigned)((nblk + T - 1) / T), T, 0, h->stream>>>((uint8_t *)dst, nblk, seed, stream);
+        break;
+    case SOSO_HIP_DTYPE_Q6_K:
+        if (cols % 256) return set_err(h, SOSO_HIP_ERR_ARG, "synth: cols");
+        nblk = (long)(rows * (cols / 256));
+        synth_q6k<<<(unsigned)((nblk + T - 1) / T), T, 0, h->stream>>>((uint8_t *)dst, nblk, seed, stream);
+        break;
+    case SOSO_HIP_DTYPE_F32:
+        return launch_synth_normal(h, (float *)dst, rows * cols, 1.0f, seed, stream);
+    default: return set_err(h, SOSO_HIP_ERR_ARG, "synth: dtype");
+    }
+    return hip_check(h, hipGetLastError(), "synth launch");
+}
+
+int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream)
+{
+    const int T = 256;
+    synth_normal_k<<<(unsigned)((n + T - 1) / T), T, 0, h->stream>>>(dst, (long)n, sigma, seed, stream);
+    return hip_check(h, hipGetLastError(), "synth normal launch");
+}

@@ -1,0 +1,630 @@
+// runtime.hip -- the C ABI of include/soso_hip.h: handle, resident-weight
+// registry keyed by tensor name, host<->device staging, stats and errors.
+//
+// Mirrors the contract of soso-llm-core's GpuDispatch
+// (crates/soso-llm-core/src/gpu.rs:338-737) as its CUDA implementor keeps it
+// (crates/soso-llm-api/src/cuda.rs): upload on a key's first use, remember a
+// declined key forever, synchronous results, never abort.
+#include "internal.hpp"
+
+#include <chrono>
+#include <cstring>
+#include <new>
+
+size_t packed_row_stride(uint8_t dtype, size_t cols);
+bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols);
+int launch_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
+                   const float *wgt_dev, const Weight *const *wts, const soso_hip_expert *exps, const uint8_t *ok,
+                   size_t n_exps, float *sum_dev);
+
+int set_err(soso_hip *h, int code, const std::string &msg)
+{
+    if (h) h->err = msg;
+    return code;
+}
+
+int hip_check(soso_hip *h, hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return SOSO_HIP_OK;
+    return set_err(h, SOSO_HIP_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+void *scratch_get(soso_hip *h, int slot, size_t bytes)
+{
+    if (bytes == 0) bytes = 16;
+    if (h->scratch_cap[slot] >= bytes) return h->scratch[slot];
+    if (h->scratch[slot]) {
+        hipStreamSynchronize(h->stream);
+        hipFree(h->scratch[slot]);
+        h->scratch[slot] = nullptr;
+        h->scratch_cap[slot] = 0;
+    }
+    size_t cap = bytes + bytes / 4 + 4096;
+    void *p = nullptr;
+    if (hipMalloc(&p, cap) != hipSuccess) return nullptr;
+    h->scratch[slot] = p;
+    h->scratch_cap[slot] = cap;
+    return p;
+}
+
+namespace {
+
+struct CallClock {
+    soso_hip *h;
+    std::chrono::steady_clock::time_point t0;
+    explicit CallClock(soso_hip *hh) : h(hh), t0(std::chrono::steady_clock::now()) {}
+    void done()
+    {
+        h->stats.launches++;
+        h->stats.total_ns +=
+            (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(std::chrono::steady_clock::now() - t0)
+                .count();
+    }
+};
+
+bool dtype_ok(uint8_t d)
+{
+    return d == SOSO_HIP_DTYPE_F32 || d == SOSO_HIP_DTYPE_Q8_0 || d == SOSO_HIP_DTYPE_Q4_K || d == SOSO_HIP_DTYPE_Q6_K;
+}
+
+int make_current(soso_hip *h) { return hip_check(h, hipSetDevice(h->device), "hipSetDevice"); }
+
+// Registers a weight from raw bytes already on the device (or uploads host
+// bytes first).  Returns 1 and sets *out, 0 when declined, <0 on error.
+int register_weight(soso_hip *h, const std::string &key, const void *raw, bool raw_on_device, size_t w_len,
+                    uint8_t dtype, size_t rows, size_t cols, Weight **out)
+{
+    Weight w;
+    w.dtype = dtype;
+    w.rows = rows;
+    w.cols = cols;
+    const size_t rb = fmt_row_bytes(dtype, cols);
+    if (!dtype_ok(dtype) || !packed_shape_ok(dtype, rows, cols) || rb == 0 || w_len != rows * rb || !raw) {
+        w.declined = true;
+        h->weights[key] = w;
+        h->stats.weights_declined++;
+        return set_err(h, SOSO_HIP_DECLINED, "weight " + key + ": dtype/shape not handled here");
+    }
+    const size_t bytes = rows * packed_row_stride(dtype, cols);
+    if (h->used + bytes > h->budget) {
+        w.declined = true;
+        h->weights[key] = w;
+        h->stats.weights_declined++;
+        return set_err(h, SOSO_HIP_DECLINED, "weight " + key + ": over the memory budget");
+    }
+    void *dev = nullptr;
+    if (hipMalloc(&dev, bytes) != hipSuccess) {
+        w.declined = true;
+        h->weights[key] = w;
+        h->stats.weights_declined++;
+        return set_err(h, SOSO_HIP_DECLINED, "weight " + key + ": device allocation failed");
+    }
+    const void *raw_dev = raw;
+    void *tmp = nullptr;
+    int rc = SOSO_HIP_OK;
+    if (!raw_on_device) {
+        if (hipMalloc(&tmp, w_len) != hipSuccess) {
+            hipFree(dev);
+            return set_err(h, SOSO_HIP_ERR_NOMEM, "weight " + key + ": staging allocation failed");
+        }
+        rc = hip_check(h, hipMemcpyAsync(tmp, raw, w_len, hipMemcpyHostToDevice, h->stream), "upload weight");
+        raw_dev = tmp;
+    }
+    if (rc == SOSO_HIP_OK) rc = repack_weight(h, dtype, raw_dev, dev, rows, cols);
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "repack sync");
+    if (tmp) hipFree(tmp);
+    if (rc != SOSO_HIP_OK) {
+        hipFree(dev);
+        return rc;
+    }
+    w.dev = dev;
+    w.bytes = bytes;
+    h->used += bytes;
+    h->stats.weight_bytes_resident += bytes;
+    h->stats.weights_resident++;
+    auto it = h->weights.emplace(key, w).first;
+    *out = &it->second;
+    return SOSO_HIP_OK;
+}
+
+// Finds or uploads the weight for `key`; same declines as cuda.rs:2365-2384.
+int get_weight(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len, uint8_t dtype,
+               size_t rows, size_t cols, Weight **out)
+{
+    std::string k(key, key_len);
+    auto it = h->weights.find(k);
+    if (it != h->weights.end()) {
+        Weight &e = it->second;
+        if (e.declined) return SOSO_HIP_DECLINED;
+        if (e.rows != rows || e.cols != cols || (dtype != 0 && e.dtype != dtype))
+            return set_err(h, SOSO_HIP_DECLINED, "weight " + k + ": shape/dtype differs from the resident copy");
+        *out = &e;
+        return SOSO_HIP_OK;
+    }
+    if (!w || dtype == 0) return set_err(h, SOSO_HIP_DECLINED, "weight " + k + ": not resident and no bytes given");
+    return register_weight(h, k, w, false, w_len, dtype, rows, cols, out);
+}
+
+Weight *find_weight(soso_hip *h, const char *key, size_t key_len)
+{
+    auto it = h->weights.find(std::string(key, key_len));
+    if (it == h->weights.end() || it->second.declined) return nullptr;
+    return &it->second;
+}
+
+} // namespace
+
+extern "C" {
+
+int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out)
+{
+    if (!out) return SOSO_HIP_ERR_ARG;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return SOSO_HIP_ERR_DEVICE;
+    if (device < 0 || device >= count) return SOSO_HIP_ERR_ARG;
+    soso_hip *h = new (std::nothrow) soso_hip();
+    if (!h) return SOSO_HIP_ERR_NOMEM;
+    h->device = device;
+    hipDeviceProp_t prop;
+    if (hipSetDevice(device) != hipSuccess || hipGetDeviceProperties(&prop, device) != hipSuccess ||
+        hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreate(&h->ev0) != hipSuccess || hipEventCreate(&h->ev1) != hipSuccess) {
+        delete h;
+        return SOSO_HIP_ERR_DEVICE;
+    }
+    h->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+    h->max_lds = prop.sharedMemPerBlock > 0 ? prop.sharedMemPerBlock : 65536;
+    size_t free_b = 0, total_b = 0;
+    hipMemGetInfo(&free_b, &total_b);
+    h->budget = vram_budget ? vram_budget : (uint64_t)(free_b * 0.9);
+    *out = h;
+    return 0;
+}
+
+void soso_hip_destroy(soso_hip *h)
+{
+    if (!h) return;
+    hipSetDevice(h->device);
+    hipStreamSynchronize(h->stream);
+    for (auto &kv : h->weights)
+        if (kv.second.dev) hipFree(kv.second.dev);
+    for (auto &kv : h->f32_tensors) hipFree(kv.second);
+    for (int i = 0; i < 8; i++)
+        if (h->scratch[i]) hipFree(h->scratch[i]);
+    for (hipEvent_t e : h->events)
+        if (e) hipEventDestroy(e);
+    for (hipGraphExec_t g : h->graphs)
+        if (g) hipGraphExecDestroy(g);
+    hipEventDestroy(h->ev0);
+    hipEventDestroy(h->ev1);
+    hipStreamDestroy(h->stream);
+    delete h;
+}
+
+int soso_hip_available(const soso_hip *h) { return h ? 1 : 0; }
+
+int soso_hip_dtype_supported(const soso_hip *h, uint8_t dtype) { return h && dtype_ok(dtype) ? 1 : 0; }
+
+void soso_hip_stats(const soso_hip *h, soso_hip_stats_t *out)
+{
+    if (h && out) *out = h->stats;
+}
+
+const char *soso_hip_last_error(const soso_hip *h) { return h ? h->err.c_str() : "null handle"; }
+
+int soso_hip_matmul(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len, uint8_t dtype,
+                    size_t rows, size_t cols, size_t n, const float *x, float *y)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!key || !x || !y || rows == 0 || cols == 0 || n == 0) return set_err(h, SOSO_HIP_ERR_ARG, "matmul: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    Weight *wt = nullptr;
+    rc = get_weight(h, key, key_len, w, w_len, dtype, rows, cols, &wt);
+    if (rc != SOSO_HIP_OK) return rc;
+    float *xd = (float *)scratch_get(h, 0, n * cols * 4);
+    float *yd = (float *)scratch_get(h, 1, n * rows * 4);
+    if (!xd || !yd) return set_err(h, SOSO_HIP_ERR_NOMEM, "matmul: scratch");
+    rc = hip_check(h, hipMemcpyAsync(xd, x, n * cols * 4, hipMemcpyHostToDevice, h->stream), "x upload");
+    if (rc == SOSO_HIP_OK) rc = launch_matvec(h, *wt, xd, yd, n);
+    if (rc != SOSO_HIP_OK) {
+        hipStreamSynchronize(h->stream);
+        return rc;
+    }
+    rc = hip_check(h, hipMemcpyAsync(y, yd, n * rows * 4, hipMemcpyDeviceToHost, h->stream), "y download");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "matmul sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    h->stats.bytes_up += n * cols * 4;
+    h->stats.bytes_down += n * rows * 4;
+    clk.done();
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_matvec(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len, uint8_t dtype,
+                    size_t rows, size_t cols, const float *x, float *y)
+{
+    return soso_hip_matmul(h, key, key_len, w, w_len, dtype, rows, cols, 1, x, y);
+}
+
+int soso_hip_matvec_batch(soso_hip *h, const soso_hip_op *ops, size_t n_ops, uint8_t *done)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if ((!ops || !done) && n_ops) return set_err(h, SOSO_HIP_ERR_ARG, "matvec_batch: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    size_t xs = 0, ys = 0;
+    for (size_t i = 0; i < n_ops; i++) {
+        done[i] = 0;
+        xs += ops[i].cols;
+        ys += ops[i].rows;
+    }
+    float *xd = (float *)scratch_get(h, 0, xs * 4);
+    float *yd = (float *)scratch_get(h, 1, ys * 4);
+    if (!xd || !yd) return set_err(h, SOSO_HIP_ERR_NOMEM, "matvec_batch: scratch");
+    std::vector<uint8_t> launched(n_ops, 0);
+    size_t xo = 0, yo = 0;
+    int worst = SOSO_HIP_OK;
+    for (size_t i = 0; i < n_ops; i++) {
+        const soso_hip_op &op = ops[i];
+        Weight *wt = nullptr;
+        int r = (op.key && op.x && op.y && op.rows && op.cols)
+                    ? get_weight(h, op.key, op.key_len, op.w, op.w_len, op.dtype, op.rows, op.cols, &wt)
+                    : SOSO_HIP_DECLINED;
+        if (r == SOSO_HIP_OK) r = hip_check(h, hipMemcpyAsync(xd + xo, op.x, op.cols * 4, hipMemcpyHostToDevice, h->stream),
+                                           "x upload");
+        if (r == SOSO_HIP_OK) r = launch_matvec(h, *wt, xd + xo, yd + yo, 1);
+        if (r == SOSO_HIP_OK) launched[i] = 1;
+        else if (r < worst) worst = r;
+        else if (r == SOSO_HIP_DECLINED && worst == SOSO_HIP_OK) worst = SOSO_HIP_DECLINED;
+        xo += op.cols;
+        yo += op.rows;
+    }
+    rc = hip_check(h, hipStreamSynchronize(h->stream), "matvec_batch sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    yo = 0;
+    for (size_t i = 0; i < n_ops; i++) {
+        if (launched[i]) {
+            if (hip_check(h, hipMemcpy(ops[i].y, yd + yo, ops[i].rows * 4, hipMemcpyDeviceToHost), "y download") ==
+                SOSO_HIP_OK) {
+                done[i] = 1;
+                h->stats.bytes_up += ops[i].cols * 4;
+                h->stats.bytes_down += ops[i].rows * 4;
+            } else {
+                worst = SOSO_HIP_ERR_DEVICE;
+            }
+        }
+        yo += ops[i].rows;
+    }
+    clk.done();
+    return worst;
+}
+
+int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const float *w, const float *xs, size_t n,
+                         size_t hdim, size_t n_exp, size_t top_k, int32_t *idx, float *wgt)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    // cuda.rs:1668-1670: shapes it cannot do are declined, not errors
+    if (!key || !xs || !idx || !wgt || n == 0 || hdim == 0 || hdim % 4 || n_exp == 0 || n_exp > 1024 || top_k == 0 ||
+        top_k > n_exp || top_k > 64)
+        return set_err(h, SOSO_HIP_DECLINED, "router_topk: shape not handled here");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    std::string k(key, key_len);
+    void *wd = nullptr;
+    auto it = h->f32_tensors.find(k);
+    if (it != h->f32_tensors.end()) {
+        wd = it->second;
+    } else {
+        if (!w) return set_err(h, SOSO_HIP_DECLINED, "router_topk: weights not resident and not given");
+        if (hipMalloc(&wd, n_exp * hdim * 4) != hipSuccess) return set_err(h, SOSO_HIP_DECLINED, "router: alloc");
+        rc = hip_check(h, hipMemcpy(wd, w, n_exp * hdim * 4, hipMemcpyHostToDevice), "router upload");
+        if (rc != SOSO_HIP_OK) {
+            hipFree(wd);
+            return rc;
+        }
+        h->f32_tensors[k] = wd;
+    }
+    float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
+    float *ld = (float *)scratch_get(h, 2, n * n_exp * 4);
+    int32_t *id = (int32_t *)scratch_get(h, 3, n * top_k * 4);
+    float *pd = (float *)scratch_get(h, 4, n * top_k * 4);
+    if (!xd || !ld || !id || !pd) return set_err(h, SOSO_HIP_ERR_NOMEM, "router: scratch");
+    rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
+    if (rc == SOSO_HIP_OK) rc = launch_router_topk(h, (const float *)wd, xd, n, hdim, n_exp, top_k, id, pd, ld);
+    if (rc == SOSO_HIP_OK)
+        rc = hip_check(h, hipMemcpyAsync(idx, id, n * top_k * 4, hipMemcpyDeviceToHost, h->stream), "idx");
+    if (rc == SOSO_HIP_OK)
+        rc = hip_check(h, hipMemcpyAsync(wgt, pd, n * top_k * 4, hipMemcpyDeviceToHost, h->stream), "wgt");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "router sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    h->stats.bytes_up += n * hdim * 4;
+    h->stats.bytes_down += n * top_k * 8;
+    clk.done();
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, size_t ffn, size_t top_k,
+                           const float *wgt, const soso_hip_expert *exps, size_t n_exps, float *sum, uint8_t *done)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!xs || !wgt || !sum || !done || (!exps && n_exps) || n == 0 || hdim == 0 || ffn == 0 || top_k == 0)
+        return set_err(h, SOSO_HIP_ERR_ARG, "experts_block: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    const size_t dims[3][2] = {{ffn, hdim}, {ffn, hdim}, {hdim, ffn}};
+    std::vector<const Weight *> wts(n_exps * 3, nullptr);
+    std::vector<uint8_t> ok(n_exps, 0);
+    bool all = true;
+    for (size_t e = 0; e < n_exps; e++) {
+        done[e] = 0;
+        bool good = exps[e].n_tokens > 0;
+        for (int k = 0; k < 3 && good; k++) {
+            Weight *wt = nullptr;
+            if (!exps[e].keys[k]) {
+                good = false;
+                break;
+            }
+            int r = get_weight(h, exps[e].keys[k], exps[e].key_lens[k], exps[e].w[k], exps[e].w_len[k],
+                               exps[e].dtype[k], dims[k][0], dims[k][1], &wt);
+            if (r < 0) return r;
+            if (r != SOSO_HIP_OK || wt->dtype == SOSO_HIP_DTYPE_F32) good = false;
+            else wts[3 * e + k] = wt;
+        }
+        for (size_t t = 0; good && t < exps[e].n_tokens; t++)
+            if (exps[e].tokens[t] >= n || exps[e].targets[t] >= n * top_k) good = false;
+        ok[e] = good ? 1 : 0;
+        if (!good && exps[e].n_tokens > 0) all = false;
+    }
+    float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
+    float *wd = (float *)scratch_get(h, 4, n * top_k * 4);
+    float *sd = (float *)scratch_get(h, 5, n * hdim * 4);
+    if (!xd || !wd || !sd) return set_err(h, SOSO_HIP_ERR_NOMEM, "experts_block: scratch");
+    rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
+    if (rc == SOSO_HIP_OK)
+        rc = hip_check(h, hipMemcpyAsync(wd, wgt, n * top_k * 4, hipMemcpyHostToDevice, h->stream), "wgt upload");
+    if (rc == SOSO_HIP_OK)
+        rc = launch_experts(h, xd, n, hdim, ffn, top_k, wd, wts.data(), exps, ok.data(), n_exps, sd);
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(sum, sd, n * hdim * 4, hipMemcpyDeviceToHost, h->stream), "sum");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "experts sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    for (size_t e = 0; e < n_exps; e++) done[e] = ok[e];
+    h->stats.bytes_up += n * hdim * 4;
+    h->stats.bytes_down += n * hdim * 4;
+    clk.done();
+    return all ? SOSO_HIP_OK : SOSO_HIP_DECLINED;
+}
+
+// ---- device-resident API ----------------------------------------------------
+int soso_hip_dev_alloc(soso_hip *h, size_t bytes, void **dptr)
+{
+    if (!h || !dptr) return SOSO_HIP_ERR_ARG;
+    *dptr = nullptr;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    return hip_check(h, hipMalloc(dptr, bytes ? bytes : 16), "hipMalloc");
+}
+
+int soso_hip_dev_free(soso_hip *h, void *dptr)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    hipStreamSynchronize(h->stream);
+    return hip_check(h, hipFree(dptr), "hipFree");
+}
+
+int soso_hip_h2d(soso_hip *h, void *dst, const void *src, size_t bytes)
+{
+    if (!h || !dst || !src) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    rc = hip_check(h, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, h->stream), "h2d");
+    return rc == SOSO_HIP_OK ? hip_check(h, hipStreamSynchronize(h->stream), "h2d sync") : rc;
+}
+
+int soso_hip_d2h(soso_hip *h, void *dst, const void *src, size_t bytes)
+{
+    if (!h || !dst || !src) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    rc = hip_check(h, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, h->stream), "d2h");
+    return rc == SOSO_HIP_OK ? hip_check(h, hipStreamSynchronize(h->stream), "d2h sync") : rc;
+}
+
+int soso_hip_sync(soso_hip *h)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    return rc == SOSO_HIP_OK ? hip_check(h, hipStreamSynchronize(h->stream), "sync") : rc;
+}
+
+int soso_hip_weight_from_dev(soso_hip *h, const char *key, size_t key_len, const void *raw_dev, size_t w_len,
+                             uint8_t dtype, size_t rows, size_t cols)
+{
+    if (!h || !key || !raw_dev) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    std::string k(key, key_len);
+    if (h->weights.count(k)) return set_err(h, SOSO_HIP_ERR_ARG, "weight " + k + " already registered");
+    Weight *w = nullptr;
+    return register_weight(h, k, raw_dev, true, w_len, dtype, rows, cols, &w);
+}
+
+int soso_hip_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
+                       uint64_t stream)
+{
+    if (!h || !dst) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    return launch_synth_raw(h, dst, dtype, rows, cols, seed, stream);
+}
+
+int soso_hip_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream)
+{
+    if (!h || !dst) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    return launch_synth_normal(h, dst, n, sigma, seed, stream);
+}
+
+int soso_hip_weight_synth(soso_hip *h, const char *key, size_t key_len, uint8_t dtype, size_t rows, size_t cols,
+                          uint64_t seed, uint64_t stream)
+{
+    if (!h || !key) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    const size_t rb = fmt_row_bytes(dtype, cols);
+    if (rb == 0 || dtype == SOSO_HIP_DTYPE_F32) return set_err(h, SOSO_HIP_ERR_ARG, "weight_synth: dtype/shape");
+    void *raw = nullptr;
+    if (hipMalloc(&raw, rows * rb) != hipSuccess) return set_err(h, SOSO_HIP_ERR_NOMEM, "weight_synth: alloc");
+    rc = launch_synth_raw(h, raw, dtype, rows, cols, seed, stream);
+    if (rc == SOSO_HIP_OK) rc = soso_hip_weight_from_dev(h, key, key_len, raw, rows * rb, dtype, rows, cols);
+    hipStreamSynchronize(h->stream);
+    hipFree(raw);
+    return rc;
+}
+
+int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
+{
+    if (!h || !key) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    auto it = h->weights.find(std::string(key, key_len));
+    if (it == h->weights.end()) return SOSO_HIP_DECLINED;
+    hipStreamSynchronize(h->stream);
+    if (it->second.dev) {
+        hipFree(it->second.dev);
+        h->used -= it->second.bytes;
+        h->stats.weight_bytes_resident -= it->second.bytes;
+        h->stats.weights_resident--;
+    }
+    h->weights.erase(it);
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_matvec_dev(soso_hip *h, const char *key, size_t key_len, const float *x_dev, float *y_dev)
+{
+    return soso_hip_matmul_dev(h, key, key_len, 1, x_dev, y_dev);
+}
+
+int soso_hip_matmul_dev(soso_hip *h, const char *key, size_t key_len, size_t n, const float *x_dev, float *y_dev)
+{
+    if (!h || !key || !x_dev || !y_dev || n == 0) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    Weight *w = find_weight(h, key, key_len);
+    if (!w) return set_err(h, SOSO_HIP_DECLINED, "matvec_dev: key not resident");
+    return launch_matvec(h, *w, x_dev, y_dev, n);
+}
+
+int soso_hip_dequant_dev(soso_hip *h, const char *key, size_t key_len, float *out_dev)
+{
+    if (!h || !key || !out_dev) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    Weight *w = find_weight(h, key, key_len);
+    if (!w) return set_err(h, SOSO_HIP_DECLINED, "dequant_dev: key not resident");
+    return launch_dequant(h, *w, out_dev);
+}
+
+int soso_hip_argmax_dev(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev)
+{
+    if (!h || !x_dev || !idx_dev || n == 0) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    return launch_argmax(h, x_dev, n, idx_dev);
+}
+
+int soso_hip_timer_start(soso_hip *h)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    return rc == SOSO_HIP_OK ? hip_check(h, hipEventRecord(h->ev0, h->stream), "event record") : rc;
+}
+
+int soso_hip_timer_stop(soso_hip *h, float *ms)
+{
+    if (!h || !ms) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipEventRecord(h->ev1, h->stream), "event record");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipEventSynchronize(h->ev1), "event sync");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipEventElapsedTime(ms, h->ev0, h->ev1), "event elapsed");
+    return rc;
+}
+
+int soso_hip_event_record(soso_hip *h, int slot)
+{
+    if (!h || slot < 0 || slot > 65535) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    if ((size_t)slot >= h->events.size()) h->events.resize((size_t)slot + 1, nullptr);
+    if (!h->events[slot] && hipEventCreate(&h->events[slot]) != hipSuccess) {
+        h->events[slot] = nullptr;
+        return set_err(h, SOSO_HIP_ERR_DEVICE, "hipEventCreate");
+    }
+    return hip_check(h, hipEventRecord(h->events[slot], h->stream), "event record");
+}
+
+int soso_hip_event_elapsed(soso_hip *h, int a, int b, float *ms)
+{
+    if (!h || !ms || a < 0 || b < 0 || (size_t)a >= h->events.size() || (size_t)b >= h->events.size() ||
+        !h->events[a] || !h->events[b])
+        return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipEventSynchronize(h->events[b]), "event sync");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipEventElapsedTime(ms, h->events[a], h->events[b]), "event elapsed");
+    return rc;
+}
+
+int soso_hip_graph_begin(soso_hip *h)
+{
+    if (!h || h->capturing) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc == SOSO_HIP_OK)
+        rc = hip_check(h, hipStreamBeginCapture(h->stream, hipStreamCaptureModeThreadLocal), "begin capture");
+    if (rc == SOSO_HIP_OK) h->capturing = true;
+    return rc;
+}
+
+int soso_hip_graph_end(soso_hip *h, int *graph_id)
+{
+    if (!h || !graph_id || !h->capturing) return SOSO_HIP_ERR_ARG;
+    h->capturing = false;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    hipGraph_t g = nullptr;
+    rc = hip_check(h, hipStreamEndCapture(h->stream, &g), "end capture");
+    if (rc != SOSO_HIP_OK) return rc;
+    hipGraphExec_t ex = nullptr;
+    rc = hip_check(h, hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "graph instantiate");
+    hipGraphDestroy(g);
+    if (rc != SOSO_HIP_OK) return rc;
+    h->graphs.push_back(ex);
+    *graph_id = (int)h->graphs.size() - 1;
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_graph_launch(soso_hip *h, int id)
+{
+    if (!h || id < 0 || (size_t)id >= h->graphs.size() || !h->graphs[id]) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    return rc == SOSO_HIP_OK ? hip_check(h, hipGraphLaunch(h->graphs[id], h->stream), "graph launch") : rc;
+}
+
+int soso_hip_graph_destroy(soso_hip *h, int id)
+{
+    if (!h || id < 0 || (size_t)id >= h->graphs.size() || !h->graphs[id]) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    hipStreamSynchronize(h->stream);
+    hipGraphExecDestroy(h->graphs[id]);
+    h->graphs[id] = nullptr;
+    return SOSO_HIP_OK;
+}
+
+} // extern "C"

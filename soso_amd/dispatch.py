@@ -1,0 +1,244 @@
+"""HipGpu -- soso's GpuDispatch (crates/soso-llm-core/src/gpu.rs:338-737) over
+the C ABI of libsoso_hip.so, with numpy arrays in place of Rust slices.
+
+Method names and return values follow the trait:
+  matvec / matmul / router_topk -> True (computed), False (declined: the
+  caller computes on the CPU); errors raise HipError.
+  matvec_lote / expertos_bloque fill `hecho` like the trait does.
+The decline-forever residency cache, the key-based uploads and the
+synchronous semantics live in the native library.
+"""
+import ctypes as C
+
+import numpy as np
+
+from . import abi
+
+
+def _key(k):
+    b = k.encode() if isinstance(k, str) else bytes(k)
+    return b, len(b)
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a
+
+
+class HipGpu:
+    def __init__(self, device=0, vram_budget=0):
+        self.lib = abi.load()
+        h = C.c_void_p()
+        rc = self.lib.soso_hip_create(device, vram_budget, C.byref(h))
+        if rc != 0:
+            raise abi.HipError(f"soso_hip_create({device}) failed: {rc}")
+        self.h = h
+
+    # -- lifetime ------------------------------------------------------------
+    def close(self):
+        if self.h:
+            self.lib.soso_hip_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    # -- helpers ---------------------------------------------------------------
+    def last_error(self):
+        return self.lib.soso_hip_last_error(self.h).decode(errors="replace")
+
+    def _rc(self, rc, what):
+        if rc < 0:
+            raise abi.HipError(f"{what}: rc={rc}: {self.last_error()}")
+        return rc == abi.OK
+
+    # -- GpuDispatch -----------------------------------------------------------
+    def available(self):
+        return bool(self.lib.soso_hip_available(self.h))
+
+    def dtype_soportado(self, dtype):
+        return bool(self.lib.soso_hip_dtype_supported(self.h, dtype))
+
+    def stats(self):
+        s = abi.Stats()
+        self.lib.soso_hip_stats(self.h, C.byref(s))
+        return {f: getattr(s, f) for f, _ in abi.Stats._fields_}
+
+    def matvec(self, key, w, dtype, rows, cols, x, out):
+        """gpu.rs:432-440; overwrites `out` (float32, rows) on success."""
+        k, kl = _key(key)
+        wb = None if w is None else np.ascontiguousarray(w, dtype=np.uint8)
+        x = _f32(x)
+        assert out.dtype == np.float32 and out.flags.c_contiguous and out.size == rows
+        rc = self.lib.soso_hip_matvec(self.h, k, kl, None if wb is None else wb.ctypes.data,
+                                      0 if wb is None else wb.size, dtype, rows, cols,
+                                      x.ctypes.data, out.ctypes.data)
+        return self._rc(rc, f"matvec {key}")
+
+    def matmul(self, key, w, dtype, rows, cols, n, x, out):
+        """gpu.rs:443-455: out[n x rows] = x[n x cols] . W^T."""
+        k, kl = _key(key)
+        wb = None if w is None else np.ascontiguousarray(w, dtype=np.uint8)
+        x = _f32(x)
+        assert out.dtype == np.float32 and out.flags.c_contiguous and out.size == n * rows
+        rc = self.lib.soso_hip_matmul(self.h, k, kl, None if wb is None else wb.ctypes.data,
+                                      0 if wb is None else wb.size, dtype, rows, cols, n,
+                                      x.ctypes.data, out.ctypes.data)
+        return self._rc(rc, f"matmul {key}")
+
+    def matvec_lote(self, ops, hecho):
+        """gpu.rs:694-701.  ops: list of dicts key/w/dtype/rows/cols/x/out."""
+        keep = []
+        arr = (abi.Op * len(ops))()
+        for i, op in enumerate(ops):
+            k, kl = _key(op["key"])
+            wb = None if op.get("w") is None else np.ascontiguousarray(op["w"], dtype=np.uint8)
+            x = _f32(op["x"])
+            keep += [k, wb, x]
+            arr[i] = abi.Op(k, kl, None if wb is None else wb.ctypes.data, 0 if wb is None else wb.size,
+                            op["dtype"], op["rows"], op["cols"], x.ctypes.data, op["out"].ctypes.data)
+        done = np.zeros(len(ops), dtype=np.uint8)
+        rc = self.lib.soso_hip_matvec_batch(self.h, arr, len(ops), done.ctypes.data)
+        for i in range(len(ops)):
+            hecho[i] = hecho[i] or bool(done[i])
+        return self._rc(rc, "matvec_lote") if rc < 0 else rc
+
+    def router_topk(self, key, w, xs, n, h, n_exp, top_k, idx, pesos):
+        """gpu.rs:480-494; idx int32 (n*top_k), pesos float32 (n*top_k)."""
+        k, kl = _key(key)
+        w = None if w is None else _f32(w)
+        xs = _f32(xs)
+        rc = self.lib.soso_hip_router_topk(self.h, k, kl, None if w is None else w.ctypes.data, xs.ctypes.data,
+                                           n, h, n_exp, top_k, idx.ctypes.data, pesos.ctypes.data)
+        return self._rc(rc, "router_topk")
+
+    def expertos_bloque(self, xs, n, h, ffn, top_k, pesos, exps, suma, hecho):
+        """gpu.rs:461-475.  exps: list of dicts with keys (3 names), w (3 byte
+        arrays or None), dtype (3 codes), tokens, destinos."""
+        xs = _f32(xs)
+        pesos = _f32(pesos)
+        keep = []
+        arr = (abi.Expert * len(exps))()
+        for i, e in enumerate(exps):
+            ex = abi.Expert()
+            for j in range(3):
+                k, kl = _key(e["claves"][j])
+                wb = None
+                if e.get("w") is not None and e["w"][j] is not None:
+                    wb = np.ascontiguousarray(e["w"][j], dtype=np.uint8)
+                keep += [k, wb]
+                ex.keys[j] = k
+                ex.key_lens[j] = kl
+                ex.w[j] = None if wb is None else wb.ctypes.data
+                ex.w_len[j] = 0 if wb is None else wb.size
+                ex.dtype[j] = 0 if wb is None else e["dtype"][j]
+            tok = np.ascontiguousarray(e["tokens"], dtype=np.uint32)
+            dst = np.ascontiguousarray(e["destinos"], dtype=np.uint32)
+            keep += [tok, dst]
+            ex.tokens = tok.ctypes.data
+            ex.targets = dst.ctypes.data
+            ex.n_tokens = tok.size
+            ex.shared = int(e.get("compartido", False))
+            arr[i] = ex
+        done = np.zeros(len(exps), dtype=np.uint8)
+        assert suma.dtype == np.float32 and suma.size == n * h
+        rc = self.lib.soso_hip_experts_block(self.h, xs.ctypes.data, n, h, ffn, top_k, pesos.ctypes.data, arr,
+                                             len(exps), suma.ctypes.data, done.ctypes.data)
+        for i in range(len(exps)):
+            hecho[i] = hecho[i] or bool(done[i])
+        return self._rc(rc, "expertos_bloque") if rc < 0 else rc
+
+    # -- device-resident helpers (benchmarks, decode step, tests) ----------------
+    def dev_alloc(self, nbytes):
+        p = C.c_void_p()
+        self._rc(self.lib.soso_hip_dev_alloc(self.h, nbytes, C.byref(p)), "dev_alloc")
+        return p.value
+
+    def dev_free(self, p):
+        self._rc(self.lib.soso_hip_dev_free(self.h, p), "dev_free")
+
+    def h2d(self, dst, arr):
+        arr = np.ascontiguousarray(arr)
+        self._rc(self.lib.soso_hip_h2d(self.h, dst, arr.ctypes.data, arr.nbytes), "h2d")
+
+    def d2h(self, src, shape, dtype):
+        out = np.empty(shape, dtype=dtype)
+        self._rc(self.lib.soso_hip_d2h(self.h, out.ctypes.data, src, out.nbytes), "d2h")
+        return out
+
+    def sync(self):
+        self._rc(self.lib.soso_hip_sync(self.h), "sync")
+
+    def weight_from_dev(self, key, raw_dev, w_len, dtype, rows, cols):
+        k, kl = _key(key)
+        return self._rc(self.lib.soso_hip_weight_from_dev(self.h, k, kl, raw_dev, w_len, dtype, rows, cols),
+                        f"weight_from_dev {key}")
+
+    def weight_synth(self, key, dtype, rows, cols, seed, stream):
+        k, kl = _key(key)
+        return self._rc(self.lib.soso_hip_weight_synth(self.h, k, kl, dtype, rows, cols, seed, stream),
+                        f"weight_synth {key}")
+
+    def synth_raw(self, dst, dtype, rows, cols, seed, stream):
+        return self._rc(self.lib.soso_hip_synth_raw(self.h, dst, dtype, rows, cols, seed, stream), "synth_raw")
+
+    def synth_normal(self, dst, n, sigma, seed, stream):
+        return self._rc(self.lib.soso_hip_synth_normal(self.h, dst, n, sigma, seed, stream), "synth_normal")
+
+    def weight_drop(self, key):
+        k, kl = _key(key)
+        return self._rc(self.lib.soso_hip_weight_drop(self.h, k, kl), "weight_drop")
+
+    def matvec_dev(self, key, x_dev, y_dev):
+        k, kl = _key(key)
+        return self._rc(self.lib.soso_hip_matvec_dev(self.h, k, kl, x_dev, y_dev), f"matvec_dev {key}")
+
+    def matmul_dev(self, key, n, x_dev, y_dev):
+        k, kl = _key(key)
+        return self._rc(self.lib.soso_hip_matmul_dev(self.h, k, kl, n, x_dev, y_dev), f"matmul_dev {key}")
+
+    def dequant_dev(self, key, out_dev):
+        k, kl = _key(key)
+        return self._rc(self.lib.soso_hip_dequant_dev(self.h, k, kl, out_dev), f"dequant_dev {key}")
+
+    def argmax_dev(self, x_dev, n, idx_dev):
+        return self._rc(self.lib.soso_hip_argmax_dev(self.h, x_dev, n, idx_dev), "argmax_dev")
+
+    def timer_start(self):
+        self._rc(self.lib.soso_hip_timer_start(self.h), "timer_start")
+
+    def timer_stop(self):
+        ms = C.c_float()
+        self._rc(self.lib.soso_hip_timer_stop(self.h, C.byref(ms)), "timer_stop")
+        return ms.value
+
+    def event_record(self, slot):
+        self._rc(self.lib.soso_hip_event_record(self.h, slot), "event_record")
+
+    def event_elapsed(self, a, b):
+        ms = C.c_float()
+        self._rc(self.lib.soso_hip_event_elapsed(self.h, a, b, C.byref(ms)), "event_elapsed")
+        return ms.value
+
+    def graph_begin(self):
+        self._rc(self.lib.soso_hip_graph_begin(self.h), "graph_begin")
+
+    def graph_end(self):
+        gid = C.c_int()
+        self._rc(self.lib.soso_hip_graph_end(self.h, C.byref(gid)), "graph_end")
+        return gid.value
+
+    def graph_launch(self, gid):
+        self._rc(self.lib.soso_hip_graph_launch(self.h, gid), "graph_launch")
+
+    def graph_destroy(self, gid):
+        self._rc(self.lib.soso_hip_graph_destroy(self.h, gid), "graph_destroy")

@@ -1,0 +1,182 @@
+"""GPU parity of the quantized matvecs through the C ABI (libsoso_hip.so).
+
+Bar (north star): dequantized weights bit-exact; matvec outputs within a
+relative L2 error of 1e-5 against the CPU oracle on the same seeded inputs
+(f32 accumulate).  Inputs come from the oracle's host generator and enter the
+library through the boundary exactly as soso would pass them (raw soso/GGML
+bytes on a key's first use).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5  # relative L2, north star
+Q8, Q4K, Q6K, F32 = 2, 3, 13, 1
+
+
+def dev_dequant(gpu, key, rows, cols):
+    d = gpu.dev_alloc(rows * cols * 4)
+    try:
+        assert gpu.dequant_dev(key, d)
+        return gpu.d2h(d, (rows, cols), np.float32)
+    finally:
+        gpu.dev_free(d)
+
+
+def run_matvec(gpu, key, dtype, w, rows, cols, x):
+    y = np.full(rows, np.nan, np.float32)
+    assert gpu.matvec(key, w, dtype, rows, cols, x, y), gpu.last_error()
+    return y
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [
+    (Q8, 64, 4096), (Q8, 5, 128), (Q4K, 64, 4096), (Q4K, 7, 256), (Q4K, 9, 14336), (Q6K, 33, 4096), (Q6K, 3, 256),
+])
+def test_synth_device_equals_host(gpu, orc, dtype, rows, cols):
+    host = orc.synth(dtype, rows, cols, 1234, 77)
+    d = gpu.dev_alloc(host.size)
+    try:
+        gpu.synth_raw(d, dtype, rows, cols, 1234, 77)
+        dev = gpu.d2h(d, host.shape, np.uint8)
+    finally:
+        gpu.dev_free(d)
+    assert np.array_equal(dev, host)
+    xs = orc.normal(5000, 0.02, 9, 3)
+    d = gpu.dev_alloc(xs.nbytes)
+    try:
+        gpu.synth_normal(d, xs.size, 0.02, 9, 3)
+        assert np.array_equal(gpu.d2h(d, xs.shape, np.float32).view(np.uint32), xs.view(np.uint32))
+    finally:
+        gpu.dev_free(d)
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [
+    (Q8, 4096, 4096), (Q4K, 14336, 4096), (Q6K, 2048, 4096), (Q4K, 13, 768), (Q8, 3, 64), (Q6K, 5, 14336),
+])
+def test_dequant_bit_exact(gpu, orc, dtype, rows, cols):
+    w = orc.synth(dtype, rows, cols, 5, 1)
+    key = f"dq.{dtype}.{rows}x{cols}"
+    x = orc.normal(cols, 1.0, 5, 2)
+    run_matvec(gpu, key, dtype, w, rows, cols, x)  # uploads + repacks
+    dev = dev_dequant(gpu, key, rows, cols)
+    ref = orc.dequant(dtype, w, rows, cols)
+    assert np.array_equal(dev.view(np.uint32), ref.view(np.uint32))
+    gpu.weight_drop(key)
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [
+    (Q8, 4096, 4096),      # config 1
+    (Q4K, 14336, 4096),    # config 2 (headline)
+    (Q4K, 4096, 14336),    # FFN down of the 8B step (rows wider than 64 units)
+    (Q4K, 768, 2048),      # MoE gate/up
+    (Q4K, 2048, 768),      # MoE down (12 units per row)
+    (Q6K, 4096, 4096),
+    (Q4K, 1, 256), (Q4K, 3, 512), (Q8, 1, 64), (Q8, 257, 192), (Q6K, 1, 256), (Q6K, 129, 512),
+    (F32, 128, 2048), (F32, 3, 44),
+])
+def test_matvec_parity(gpu, orc, dtype, rows, cols):
+    w = orc.synth(dtype, rows, cols, 21, 4)
+    x = orc.normal(cols, 1.0, 21, 5)
+    key = f"mv.{dtype}.{rows}x{cols}"
+    y = run_matvec(gpu, key, dtype, w, rows, cols, x)
+    y64 = orc.matvec_f64(dtype, w, rows, cols, x)
+    ycpu = orc.matvec(dtype, w, rows, cols, x, threads=8, avx2=dtype != Q6K)
+    assert np.all(np.isfinite(y))
+    assert orc.rel_l2(y, y64) < TOL, orc.rel_l2(y, y64)
+    assert orc.rel_l2(y, ycpu) < TOL, orc.rel_l2(y, ycpu)
+    gpu.weight_drop(key)
+
+
+def test_q6k_head_argmax(gpu, orc):
+    """Config 3 (rows reduced for the CPU oracle): argmax equal to the CPU's, gap reported."""
+    rows, cols = 32768, 4096
+    w = orc.synth(Q6K, rows, cols, 31, 1)
+    x = orc.normal(cols, 1.0, 31, 2)
+    y = run_matvec(gpu, "head.q6k", Q6K, w, rows, cols, x)
+    ycpu = orc.matvec(Q6K, w, rows, cols, x, threads=8)
+    assert orc.rel_l2(y, ycpu) < TOL
+    L = orc.lib()
+    a_cpu = L.or_argmax(ycpu.ctypes.data, rows)
+    yd = gpu.dev_alloc(rows * 4)
+    idx = gpu.dev_alloc(4)
+    try:
+        gpu.h2d(yd, y)
+        gpu.argmax_dev(yd, rows, idx)
+        a_gpu = int(gpu.d2h(idx, (1,), np.uint32)[0])
+    finally:
+        gpu.dev_free(yd)
+        gpu.dev_free(idx)
+    s = np.sort(ycpu)
+    gap = float(s[-1] - s[-2])
+    print(f"argmax cpu={a_cpu} gpu={a_gpu} top-2 gap={gap:.3e}")
+    assert a_gpu == a_cpu == int(np.argmax(y[::-1]) * -1 + rows - 1)
+    gpu.weight_drop("head.q6k")
+
+
+@pytest.mark.parametrize("scale", [1e-30, 1e-3, 1e6])
+def test_matvec_extreme_x(gpu, orc, scale):
+    rows, cols = 300, 4096
+    w = orc.synth(Q4K, rows, cols, 2, 2)
+    x = (orc.normal(cols, 1.0, 2, 3) * np.float32(scale)).astype(np.float32)
+    y = run_matvec(gpu, f"ext.{scale}", Q4K, w, rows, cols, x)
+    y64 = orc.matvec_f64(Q4K, w, rows, cols, x)
+    assert orc.rel_l2(y, y64) < TOL
+    gpu.weight_drop(f"ext.{scale}")
+
+
+def test_matvec_zero_x_gives_zero(gpu, orc):
+    rows, cols = 64, 4096
+    w = orc.synth(Q4K, rows, cols, 2, 9)
+    y = run_matvec(gpu, "zero", Q4K, w, rows, cols, np.zeros(cols, np.float32))
+    assert np.all(y == 0.0)
+    gpu.weight_drop("zero")
+
+
+def test_matmul_equals_single_matvecs(gpu, orc):
+    rows, cols, n = 512, 2048, 5
+    w = orc.synth(Q4K, rows, cols, 3, 3)
+    xs = orc.normal(n * cols, 1.0, 3, 4).reshape(n, cols)
+    out = np.empty(n * rows, np.float32)
+    assert gpu.matmul("mm", w, Q4K, rows, cols, n, xs, out)
+    out = out.reshape(n, rows)
+    ref = orc.matmul(Q4K, w, rows, cols, xs, threads=8, avx2=True)
+    for j in range(n):
+        assert orc.rel_l2(out[j], ref[j]) < TOL
+        y = run_matvec(gpu, "mm", Q4K, None, rows, cols, xs[j])  # resident: no bytes needed
+        assert np.array_equal(y, out[j])
+    gpu.weight_drop("mm")
+
+
+def test_declines_follow_the_trait(gpu, orc):
+    x = orc.normal(256, 1.0, 1, 1)
+    y = np.zeros(4, np.float32)
+    # cols not a whole number of blocks: declined (Ok(false)), and remembered
+    assert not gpu.matvec("bad.cols", np.zeros(4 * 144, np.uint8), Q4K, 4, 255, x[:255], y)
+    assert not gpu.matvec("bad.cols", np.zeros(4 * 144, np.uint8), Q4K, 4, 255, x[:255], y)
+    # an unknown dtype is declined
+    assert not gpu.dtype_soportado(7)
+    assert not gpu.matvec("bad.dtype", np.zeros(4 * 144, np.uint8), 7, 4, 256, x, y)
+    # a resident key asked with another shape is declined, not recomputed
+    w = orc.synth(Q4K, 4, 256, 1, 1)
+    assert gpu.matvec("shape", w, Q4K, 4, 256, x, y)
+    assert not gpu.matvec("shape", w, Q4K, 2, 512, orc.normal(512, 1.0, 1, 2), np.zeros(2, np.float32))
+    # a key never uploaded and given no bytes is declined
+    assert not gpu.matvec("absent", None, Q4K, 4, 256, x, y)
+    st = gpu.stats()
+    assert st["weights_declined"] >= 2 and st["launches"] >= 1
+
+
+def test_matvec_lote(gpu, orc):
+    ops, refs = [], []
+    for i, (dt, r, c) in enumerate([(Q4K, 300, 1024), (Q8, 100, 512), (7, 10, 256), (Q6K, 40, 512)]):
+        w = orc.synth(dt, r, c, 40 + i, 1) if dt != 7 else np.zeros(10 * 144, np.uint8)
+        x = orc.normal(c, 1.0, 40 + i, 2)
+        ops.append(dict(key=f"lote{i}", w=w, dtype=dt, rows=r, cols=c, x=x, out=np.zeros(r, np.float32)))
+        refs.append(None if dt == 7 else orc.matvec_f64(dt, w, r, c, x))
+    hecho = [False] * len(ops)
+    rc = gpu.matvec_lote(ops, hecho)
+    assert hecho == [True, True, False, True] and rc == 0
+    for op, ref in zip(ops, refs):
+        if ref is not None:
+            assert orc.rel_l2(op["out"], ref) < TOL
