@@ -28,8 +28,23 @@ ROW_BYTES = {Q4K: lambda c: c // 256 * 144, Q8: lambda c: c // 32 * 36, Q6K: lam
 
 
 def algo_bytes(dtype, rows, cols):
-    """weights + x + y, each moved once."""
+    """Algorithmic bytes of one matvec: weights + x + y, each moved once."""
     return rows * ROW_BYTES[dtype](cols) + 4 * cols + 4 * rows
+
+
+def _capture(g, body):
+    """Captures body() into a graph; the capture is always closed."""
+    g.graph_begin()
+    err = None
+    try:
+        body()
+    except Exception as e:  # noqa: BLE001
+        err = e
+    gid = g.graph_end()
+    if err is not None:
+        g.graph_destroy(gid)
+        raise err
+    return gid
 
 
 def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
@@ -45,11 +60,8 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
             g.matvec_dev(keys[i % copies], x, y)
         g.sync()
         # graph of the timed steps: back-to-back launches with no host in between
-        g.graph_begin()
-        for i in range(steps):
-            g.matvec_dev(keys[i % copies], x, y)
-        gid = g.graph_end()
-        g.graph_launch(gid)  # first replay: warm the graph itself
+        gid = _capture(g, lambda: [g.matvec_dev(keys[i % copies], x, y) for i in range(steps)])
+        g.graph_launch(gid)  # first replay warms the graph itself
         g.sync()
         t0 = time.perf_counter()
         g.event_record(0)
@@ -60,28 +72,42 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
         ms_wall = (t1 - t0) * 1e3 / steps
         ms_ev = g.event_elapsed(0, 1) / steps
         g.graph_destroy(gid)
-        # per-launch kernel duration: events around every launch, replayed as a graph
+        # per-launch kernel duration: HIP events around every launch, issued
+        # while the GPU works through a queued backlog so it never waits for
+        # the host; gaps between consecutive launches are reported too.
         n = min(steps, 2000)
-        try:
-            g.graph_begin()
-            for i in range(n):
-                g.event_record(2 + 2 * i)
-                g.matvec_dev(keys[i % copies], x, y)
-                g.event_record(3 + 2 * i)
-            gid = g.graph_end()
-            g.graph_launch(gid)
-            g.sync()
-            durs = sorted(g.event_elapsed(2 + 2 * i, 3 + 2 * i) for i in range(n))
-            g.graph_destroy(gid)
-            ms_kernel = sum(durs) / n
-        except Exception:
-            ms_kernel = ms_ev
+        for i in range(min(400, 4 * n)):
+            g.matvec_dev(keys[i % copies], x, y)
+        for i in range(n):
+            g.event_record(2 + 2 * i)
+            g.matvec_dev(keys[i % copies], x, y)
+            g.event_record(3 + 2 * i)
+        g.sync()
+        durs = [g.event_elapsed(2 + 2 * i, 3 + 2 * i) for i in range(n)]
+        gaps = [g.event_elapsed(3 + 2 * i, 4 + 2 * i) for i in range(n - 1)]
+        ms_kernel = sum(durs) / n
+        time_matvec.last_gap_us = 1e3 * sum(gaps) / max(1, len(gaps))
         return ms_wall, ms_ev, ms_kernel
     finally:
+        g.sync()
         g.dev_free(x)
         g.dev_free(y)
         for k in keys:
             g.weight_drop(k)
+
+
+def copy_calibration(g, nbytes=512 << 20, reps=20):
+    """A plain device-to-device copy of known size, for scaling rocprofv3's
+    FETCH_SIZE / WRITE_SIZE counters (run under --pmc)."""
+    a, b = g.dev_alloc(nbytes), g.dev_alloc(nbytes)
+    try:
+        for _ in range(reps):
+            g.d2d(b, a, nbytes)
+        g.sync()
+    finally:
+        g.dev_free(a)
+        g.dev_free(b)
+    print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}), flush=True)
 
 
 def cpu_baseline(dtype, rows, cols, seconds, threads):
@@ -118,6 +144,7 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
+    ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -127,6 +154,10 @@ def main():
 
     from soso_amd.dispatch import HipGpu
     g = HipGpu(0)
+    if args.copy_calibration:
+        copy_calibration(g)
+        g.close()
+        return
     rows, cols = 14336, 4096
     nbytes = algo_bytes(Q4K, rows, cols)
     ms_wall, ms_ev, ms_k = time_matvec(g, Q4K, rows, cols, 16, args.steps, args.warmup)
@@ -149,7 +180,8 @@ def main():
                    "rows": rows, "cols": cols, "bytes_per_step": nbytes, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic("q4k_14336x4096"),
-                     "kernel_us": round(ms_k * 1e3, 3), "step_us_events": round(ms_ev * 1e3, 3)},
+                     "kernel_us": round(ms_k * 1e3, 3), "step_us_events": round(ms_ev * 1e3, 3),
+                     "inter_launch_gap_us": round(getattr(time_matvec, "last_gap_us", 0.0), 3)},
     }
     if not args.no_extra:
         extra = {}

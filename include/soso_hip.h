@@ -139,6 +139,8 @@ int soso_hip_dev_free(soso_hip *h, void *dptr);
 int soso_hip_h2d(soso_hip *h, void *dst, const void *src, size_t bytes);
 int soso_hip_d2h(soso_hip *h, void *dst, const void *src, size_t bytes);
 int soso_hip_sync(soso_hip *h);
+/* Device-to-device copy on the handle's stream (asynchronous). */
+int soso_hip_d2d(soso_hip *h, void *dst, const void *src, size_t bytes);
 /* Registers a resident weight whose raw (soso/GGML layout) bytes are already
  * on the device at `raw_dev`; the library repacks them into its own copy. */
 int soso_hip_weight_from_dev(soso_hip *h, const char *key, size_t key_len, const void *raw_dev,

@@ -69,6 +69,7 @@ PROTOTYPES = {
     "soso_hip_h2d": (_I, [_P, _P, _P, _S]),
     "soso_hip_d2h": (_I, [_P, _P, _P, _S]),
     "soso_hip_sync": (_I, [_P]),
+    "soso_hip_d2d": (_I, [_P, _P, _P, _S]),
     "soso_hip_weight_from_dev": (_I, [_P, C.c_char_p, _S, _P, _S, _U8, _S, _S]),
     "soso_hip_weight_synth": (_I, [_P, C.c_char_p, _S, _U8, _S, _S, _U64, _U64]),
     "soso_hip_synth_raw": (_I, [_P, _P, _U8, _S, _S, _U64, _U64]),

@@ -132,3 +132,37 @@ __device__ __forceinline__ float wave_max(float v)
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
     return v;
 }
+
+// DPP lane moves (gfx9 encodings): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] =
+// 0x4E, row_half_mirror 0x141, row_mirror 0x140, row_bcast:15 0x142,
+// row_bcast:31 0x143.  Lanes of rows outside `ROWS` keep `old` (= 0 here).
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ float dpp_f(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROWS, 0xf, false));
+}
+
+// Sum over aligned segments of W lanes (W power of two <= 64) with DPP adds.
+// For W <= 16 every lane of the segment holds the sum; for W = 32 and 64 the
+// LAST lane of the segment does (lane 31/63, resp. 63).
+template <int W>
+__device__ __forceinline__ float seg_sum_dpp(float v)
+{
+    if (W >= 2) v += dpp_f<0xB1>(v);
+    if (W >= 4) v += dpp_f<0x4E>(v);
+    if (W >= 8) v += dpp_f<0x141>(v);
+    if (W >= 16) v += dpp_f<0x140>(v);
+    if (W >= 32) v += dpp_f<0x142, 0xA>(v);
+    if (W >= 64) v += dpp_f<0x143, 0xC>(v);
+    return v;
+}
+
+// Max over aligned 16-lane rows (every lane gets it).
+__device__ __forceinline__ float row16_max(float v)
+{
+    v = fmaxf(v, dpp_f<0xB1>(v));
+    v = fmaxf(v, dpp_f<0x4E>(v));
+    v = fmaxf(v, dpp_f<0x141>(v));
+    v = fmaxf(v, dpp_f<0x140>(v));
+    return v;
+}

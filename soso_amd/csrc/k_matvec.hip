@@ -154,10 +154,13 @@ int repack_weight(soso_hip *h, uint8_t dtype, const void *raw, void *packed, siz
 }
 
 // ---------------------------------------------------------------------------
-// x staging
-// LDS: xp[g] = {hi(e0,e2), hi(e1,e3), lo(e0,e2), lo(e1,e3)} for the 4-element
-// group g (elements 4g..4g+3 of x*2^-k); s16[i] = sum of x[16i..16i+16) (f32,
-// unscaled); kexp = k with max|x|*2^-k < 2^14.
+// x staging (one barrier)
+// Each thread converts chunks of 8 elements; the 16 chunks of a 128-element
+// block sit in one 16-lane DPP row, which agrees on the block's scale
+// exponent k (max|x| * 2^-k < 2^14).  LDS receives
+//   xp[g]  = {hi(e0,e2), hi(e1,e3), lo(e0,e2), lo(e1,e3)} for the 4-element
+//            group g of x*2^-k (hi + lo = 22 significant bits, exact f16s),
+//   s16[i] = f32 sum of x[16i .. 16i+16) (unscaled), kx[b] = k of block b.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint32_t pack_h2(float a, float b)
 {
@@ -165,47 +168,52 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b)
     return __builtin_bit_cast(uint32_t, v);
 }
 
-__device__ void stage_x(const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kexp_s, float *red)
+__device__ __forceinline__ void split4(float4 v, int k, uint4 &o)
 {
-    const int G = cols >> 2, nthr = blockDim.x, tid = threadIdx.x;
+    const float a0 = ldexpf(v.x, -k), a1 = ldexpf(v.y, -k), a2 = ldexpf(v.z, -k), a3 = ldexpf(v.w, -k);
+    const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1, h2 = (_Float16)a2, h3 = (_Float16)a3;
+    o.x = __builtin_bit_cast(uint32_t, (f16x2_t){h0, h2});
+    o.y = __builtin_bit_cast(uint32_t, (f16x2_t){h1, h3});
+    o.z = pack_h2(a0 - (float)h0, a2 - (float)h2);
+    o.w = pack_h2(a1 - (float)h1, a3 - (float)h3);
+}
+
+__device__ void stage_x(const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kx)
+{
+    // blockDim % 64 == 0: chunk c sits in lane c % 64, so the 16 chunks of a
+    // block form one DPP row.  The loop bound is uniform over the workgroup
+    // and lanes past the end take part in the DPP steps with zeros (cols is a
+    // multiple of 64, so a trailing block may be half full).
+    const int nch = cols >> 3;
     const float4 *x4 = (const float4 *)x;
-    float m = 0.0f;
-    for (int g = tid; g < G; g += nthr) {
-        float4 v = x4[g];
-        m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-    }
-    m = wave_max(m);
-    if ((tid & 63) == 0) red[tid >> 6] = m;
-    __syncthreads();
-    if (tid == 0) {
-        float mm = 0.0f;
-        for (int w = 0; w < (nthr >> 6); w++) mm = fmaxf(mm, red[w]);
-        int k = 0;
-        if (mm > 0.0f && mm < INFINITY) k = __builtin_amdgcn_frexp_expf(mm) - 14;
-        *kexp_s = k;
-    }
-    __syncthreads();
-    const int k = *kexp_s;
-    for (int g = tid; g < G; g += nthr) {
-        float4 v = x4[g];
-        float a0 = ldexpf(v.x, -k), a1 = ldexpf(v.y, -k), a2 = ldexpf(v.z, -k), a3 = ldexpf(v.w, -k);
-        _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1, h2 = (_Float16)a2, h3 = (_Float16)a3;
-        float l0 = a0 - (float)h0, l1 = a1 - (float)h1, l2 = a2 - (float)h2, l3 = a3 - (float)h3;
-        uint4 o;
-        o.x = __builtin_bit_cast(uint32_t, (f16x2_t){h0, h2});
-        o.y = __builtin_bit_cast(uint32_t, (f16x2_t){h1, h3});
-        o.z = pack_h2(l0, l2);
-        o.w = pack_h2(l1, l3);
-        xp[g] = o;
-        // cols % 64 == 0 and nthr % 64 == 0: aligned groups of 4 lanes are
-        // active together, so the shuffles below stay inside active lanes.
-        float s = (v.x + v.y) + (v.z + v.w);
-        s += __shfl_xor(s, 1, 64);
-        s += __shfl_xor(s, 2, 64);
-        if ((g & 3) == 0) s16[g >> 2] = s;
+    for (int base = 0; base < nch; base += blockDim.x) {
+        const int c = base + threadIdx.x;
+        const bool valid = c < nch;
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+        if (valid) {
+            v0 = x4[2 * c];
+            v1 = x4[2 * c + 1];
+        }
+        float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                        fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+        m = row16_max(m);
+        const int k = (m > 0.0f && m < INFINITY) ? __builtin_amdgcn_frexp_expf(m) - 14 : 0;
+        float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+        sm += dpp_f<0xB1>(sm);
+        if (valid) {
+            uint4 o0, o1;
+            split4(v0, k, o0);
+            split4(v1, k, o1);
+            xp[2 * c] = o0;
+            xp[2 * c + 1] = o1;
+            if ((c & 1) == 0) s16[c >> 1] = sm;
+            if ((c & 15) == 0) kx[c >> 4] = k;
+        }
     }
     __syncthreads();
 }
+
+static inline size_t stage_lds_bytes(size_t cols) { return cols * 4 + cols / 16 * 4 + (cols + 127) / 128 * 4; }
 
 // ---------------------------------------------------------------------------
 // Per-format unit math
@@ -229,42 +237,50 @@ template <> struct WRow<FMT_Q6K> {
 // lane constants for one unit
 struct UConst {
     float c[4];
-    uint32_t k1, k2, s, bsh; // Q4_K scale-decode selectors; Q6_K uses bsh = 8*kk
+    float P;                 // 2^(20+k) (Q4_K) or 2^(24+k): undoes the subnormal codes and the x scale
+    uint32_t k1, k2, s, bsh; // Q4_K scale-decode selectors; Q6_K: s = half, bsh = 8*kk
     int sb;
 };
 
+// weight-side constants (needed before x is staged)
 template <int FMT>
-__device__ __forceinline__ void unit_setup(const uint4 *xp, const float *s16, int u, uint4 (&xv)[16], UConst &c)
+__device__ __forceinline__ void unit_setup_w(int u, UConst &c)
 {
+    if (FMT == FMT_Q4K) {
+        const int p = u & 3;
+        const bool hi = p >= 2;
+        c.k1 = hi ? 0x0F0F0F0Fu : 0u;
+        c.k2 = hi ? 0x30303030u : 0x3F3F3F3Fu;
+        c.s = hi ? 2u : 0u;
+        c.bsh = (uint32_t)(p & 1) * 16u;
+        c.sb = u >> 2;
+    } else if (FMT == FMT_Q6K) {
+        c.sb = u >> 2;
+        c.s = (uint32_t)((u >> 1) & 1);
+        c.bsh = 8u * (uint32_t)(u & 1);
+    }
+}
+
+// x-side constants and the unit's x in registers (after stage_x)
+template <int FMT>
+__device__ __forceinline__ void unit_setup_x(const uint4 *xp, const float *s16, const int *kx, int u, uint4 (&xv)[16],
+                                             UConst &c)
+{
+    c.P = ldexpf(1.0f, (FMT == FMT_Q4K ? 20 : 24) + kx[u >> 1]);
     if (FMT == FMT_Q4K || FMT == FMT_Q80) {
 #pragma unroll
         for (int j = 0; j < 16; j++) xv[j] = xp[16 * u + j];
-        float s0 = s16[4 * u] + s16[4 * u + 1], s1 = s16[4 * u + 2] + s16[4 * u + 3];
-        if (FMT == FMT_Q4K) {
-            c.c[0] = s0;
-            c.c[1] = s1;
-            int p = u & 3;
-            bool hi = p >= 2;
-            c.k1 = hi ? 0x0F0F0F0Fu : 0u;
-            c.k2 = hi ? 0x30303030u : 0x3F3F3F3Fu;
-            c.s = hi ? 2u : 0u;
-            c.bsh = (uint32_t)(p & 1) * 16u;
-            c.sb = u >> 2;
-        } else {
-            c.c[0] = 128.0f * s0;
-            c.c[1] = 128.0f * s1;
-        }
+        const float s0 = s16[4 * u] + s16[4 * u + 1], s1 = s16[4 * u + 2] + s16[4 * u + 3];
+        c.c[0] = FMT == FMT_Q4K ? s0 : 128.0f * s0;
+        c.c[1] = FMT == FMT_Q4K ? s1 : 128.0f * s1;
     } else {
-        int sb = u >> 2, h = (u >> 1) & 1, kk = u & 1;
+        const int sb = u >> 2, h = (u >> 1) & 1, kk = u & 1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
 #pragma unroll
             for (int t = 0; t < 4; t++) xv[4 * i + t] = xp[sb * 64 + h * 32 + 8 * i + 4 * kk + t];
             c.c[i] = 32.0f * s16[sb * 16 + h * 8 + 2 * i + kk];
         }
-        c.sb = sb;
-        c.bsh = 8u * (uint32_t)kk;
-        c.s = (uint32_t)h;
     }
 }
 
@@ -292,10 +308,11 @@ __device__ __forceinline__ void load_row(const uint8_t *__restrict__ Wr, int col
     }
 }
 
-// Partial dot of one unit of one row, in units of x (the 2^k scale is in P).
+// Partial dot of one unit of one row (in units of x).
 template <int FMT>
-__device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[16], const UConst &c, float P)
+__device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[16], const UConst &c)
 {
+    const float P = c.P;
     if constexpr (FMT == FMT_Q4K) {
         // Low nibbles of the pair are sub-block 2p (elements 0..31 of the
         // unit), high nibbles sub-block 2p+1 (elements 32..63), read as 16*q.
@@ -325,7 +342,7 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[
         const float d = half_bits_to_f32(w.h.x & 0xffffu), dmin = half_bits_to_f32(w.h.x >> 16);
         const float uu = fmaf(sca * 16.0f, l0 + l1, scb * (h0 + h1));
         const float vv = fmaf(mb, c.c[1], ma * c.c[0]);
-        return fmaf(d * P, uu, -(dmin * vv)); // P = 2^(20+k)
+        return fmaf(d * P, uu, -(dmin * vv));
     } else if constexpr (FMT == FMT_Q80) {
         float s[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
 #pragma unroll
@@ -343,7 +360,7 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[
                 s[blk][1] = dot2(B, xx.w, s[blk][1]);
             }
         }
-        const float t0 = fmaf(s[0][0] + s[0][1], P, -c.c[0]); // P = 2^(24+k)
+        const float t0 = fmaf(s[0][0] + s[0][1], P, -c.c[0]);
         const float t1 = fmaf(s[1][0] + s[1][1], P, -c.c[1]);
         return fmaf(__builtin_bit_cast(float, w.s.x), t0, __builtin_bit_cast(float, w.s.y) * t1);
     } else {
@@ -374,7 +391,7 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[
         // sub-scales sc[h*8 + kk + 2i] (int8), the -32 offset through c[i] = 32*sum(x)
         const float sc0 = (float)(int8_t)(w.sc.x >> c.bsh), sc1 = (float)(int8_t)(w.sc.x >> (c.bsh + 16));
         const float sc2 = (float)(int8_t)(w.sc.y >> c.bsh), sc3 = (float)(int8_t)(w.sc.y >> (c.bsh + 16));
-        float acc = sc0 * fmaf(s[0][0] + s[0][1], P, -c.c[0]); // P = 2^(24+k)
+        float acc = sc0 * fmaf(s[0][0] + s[0][1], P, -c.c[0]);
         acc = fmaf(sc1, fmaf(s[1][0] + s[1][1], P, -c.c[1]), acc);
         acc = fmaf(sc2, fmaf(s[2][0] + s[2][1], P, -c.c[2]), acc);
         acc = fmaf(sc3, fmaf(s[3][0] + s[3][1], P, -c.c[3]), acc);
@@ -382,42 +399,49 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[
     }
 }
 
-template <int FMT>
-__device__ __forceinline__ float fmt_pscale(int k)
-{
-    return ldexpf(1.0f, (FMT == FMT_Q4K ? 20 : 24) + k);
-}
+// ---------------------------------------------------------------------------
+// The matvec kernel.  A "group" of S wavefronts shares a contiguous strip of
+// row passes; wavefront s of the group owns units [64s, 64s+64) of every row
+// (S = ceil(U/64), U = cols/64 units per row; for U <= 64, S = 1 and a pass
+// covers 64/LPR rows, LPR = lanes per row).  Each lane keeps its x unit in
+// VGPRs for the whole launch.  The loads of the first DEPTH passes are issued
+// before x is staged, then roll DEPTH passes ahead of the math.  With S > 1
+// the per-wavefront sums meet in LDS and are added in wavefront order.
+// ---------------------------------------------------------------------------
+constexpr int COMBINE_CH = 64; // passes per LDS combine round (S > 1)
 
-// ---------------------------------------------------------------------------
-// Kernel A: every row has U = cols/64 <= LPR units; each lane keeps its x
-// unit in VGPRs for the whole launch and walks a contiguous strip of row
-// passes with DEPTH rows of loads in flight.
-// ---------------------------------------------------------------------------
-template <int FMT, int LPR, int DEPTH>
-__global__ void __launch_bounds__(512) mv_xreg(const uint8_t *__restrict__ W, size_t stride,
+template <int FMT, int LPR, int S, int DEPTH>
+__global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, size_t stride,
                                                const float *__restrict__ x, float *__restrict__ y, int rows, int cols)
 {
+    static_assert(S == 1 || LPR == 64, "split rows use whole wavefronts");
+    static_assert(COMBINE_CH % DEPTH == 0, "combine rounds keep the load ring aligned");
     extern __shared__ uint4 smem[];
-    __shared__ float red[16];
-    __shared__ int kexp_s;
     uint4 *xp = smem;
     float *s16 = (float *)(xp + (cols >> 2));
-    stage_x(x, cols, xp, s16, &kexp_s, red);
+    int *kx = (int *)(s16 + (cols >> 4));
+    float *red = (float *)(kx + ((cols + 127) >> 7)); // [groups][COMBINE_CH][S] when S > 1
 
     constexpr int RW = 64 / LPR;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int gpw = (blockDim.x >> 6) / S; // groups per workgroup
+    const int grp = wave / S, sw = wave % S;
     const int U = cols >> 6;
     const int ul = lane & (LPR - 1), slot = lane / LPR;
-    const bool uact = ul < U;
-    const int u = uact ? ul : 0;
-    uint4 xv[16];
+    const int ug = sw * 64 + ul;
+    const bool uact = ug < U && grp < gpw;
+    const int u = uact ? ug : 0;
     UConst c;
-    unit_setup<FMT>(xp, s16, u, xv, c);
-    const float P = fmt_pscale<FMT>(kexp_s);
+    unit_setup_w<FMT>(u, c);
 
     const int passes = (rows + RW - 1) / RW;
-    const int gw = blockIdx.x * nw + wave, tw = gridDim.x * nw;
-    const int p0 = (int)((long)passes * gw / tw), p1 = (int)((long)passes * (gw + 1) / tw);
+    const int tg = gridDim.x * gpw;
+    auto strip = [&](int g, int &q0, int &q1) {
+        q0 = (int)((long)passes * g / tg);
+        q1 = (int)((long)passes * (g + 1) / tg);
+    };
+    int p0 = 0, p1 = 0;
+    if (grp < gpw) strip(blockIdx.x * gpw + grp, p0, p1);
     auto rowp = [&](int pp) {
         int r = pp * RW + slot;
         r = r < rows ? r : rows - 1;
@@ -427,74 +451,61 @@ __global__ void __launch_bounds__(512) mv_xreg(const uint8_t *__restrict__ W, si
 #pragma unroll
     for (int i = 0; i < DEPTH; i++)
         if (p0 + i < p1) load_row<FMT>(rowp(p0 + i), cols, u, c, buf[i]);
-    for (int pb = p0; pb < p1; pb += DEPTH) {
+
+    stage_x(x, cols, xp, s16, kx);
+    uint4 xv[16];
+    unit_setup_x<FMT>(xp, s16, kx, u, xv, c);
+
+    if constexpr (S == 1) {
+        for (int pb = p0; pb < p1; pb += DEPTH) {
 #pragma unroll
-        for (int i = 0; i < DEPTH; i++) {
-            const int pp = pb + i;
-            if (pp < p1) {
-                const WRow<FMT> cur = buf[i];
-                if (pp + DEPTH < p1) load_row<FMT>(rowp(pp + DEPTH), cols, u, c, buf[i]);
-                float part = unit_dot<FMT>(cur, xv, c, P);
-                part = uact ? part : 0.0f;
-                part = seg_sum<LPR>(part);
-                const int r = pp * RW + slot;
-                if (ul == 0 && r < rows) y[r] = part;
+            for (int i = 0; i < DEPTH; i++) {
+                const int pp = pb + i;
+                if (pp < p1) {
+                    float part = unit_dot<FMT>(buf[i], xv, c);
+                    if (pp + DEPTH < p1) load_row<FMT>(rowp(pp + DEPTH), cols, u, c, buf[i]);
+                    part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
+                    const int r = pp * RW + slot;
+                    if (ul == LPR - 1 && r < rows) y[r] = part;
+                }
             }
         }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// Kernel B: rows wider than 64 units.  Each wavefront takes blocks of R rows;
-// the lanes walk the units of the row 64 at a time, reading each x unit once
-// from LDS for the R rows.
-// ---------------------------------------------------------------------------
-template <int FMT, int R>
-__global__ void __launch_bounds__(512) mv_loop(const uint8_t *__restrict__ W, size_t stride,
-                                               const float *__restrict__ x, float *__restrict__ y, int rows, int cols)
-{
-    extern __shared__ uint4 smem[];
-    __shared__ float red[16];
-    __shared__ int kexp_s;
-    uint4 *xp = smem;
-    float *s16 = (float *)(xp + (cols >> 2));
-    stage_x(x, cols, xp, s16, &kexp_s, red);
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int U = cols >> 6, iters = (U + 63) >> 6;
-    const float P = fmt_pscale<FMT>(kexp_s);
-    const int nblk = (rows + R - 1) / R;
-    const int gw = blockIdx.x * nw + wave, tw = gridDim.x * nw;
-    const int b0 = (int)((long)nblk * gw / tw), b1 = (int)((long)nblk * (gw + 1) / tw);
-    for (int blk = b0; blk < b1; blk++) {
-        float part[R];
-#pragma unroll
-        for (int rr = 0; rr < R; rr++) part[rr] = 0.0f;
-        for (int it = 0; it < iters; it++) {
-            const int ul = lane + 64 * it;
-            const bool act = ul < U;
-            const int u = act ? ul : U - 1;
-            uint4 xv[16];
-            UConst c;
-            unit_setup<FMT>(xp, s16, u, xv, c);
-            WRow<FMT> w[R];
-#pragma unroll
-            for (int rr = 0; rr < R; rr++) {
-                int r = blk * R + rr;
-                r = r < rows ? r : rows - 1;
-                load_row<FMT>(W + (size_t)r * stride, cols, u, c, w[rr]);
-            }
-#pragma unroll
-            for (int rr = 0; rr < R; rr++) {
-                const float v = unit_dot<FMT>(w[rr], xv, c, P);
-                part[rr] += act ? v : 0.0f;
-            }
+    } else {
+        // the same number of combine rounds for every wavefront of the workgroup
+        int nmax = 0;
+        for (int q = 0; q < gpw; q++) {
+            int a0, a1;
+            strip(blockIdx.x * gpw + q, a0, a1);
+            nmax = a1 - a0 > nmax ? a1 - a0 : nmax;
         }
+        for (int c0 = 0; c0 < nmax; c0 += COMBINE_CH) {
+            const int e1 = p0 + c0 + COMBINE_CH < p1 ? p0 + c0 + COMBINE_CH : p1;
+            for (int pb = p0 + c0; pb < e1; pb += DEPTH) {
 #pragma unroll
-        for (int rr = 0; rr < R; rr++) {
-            const float v = seg_sum<64>(part[rr]);
-            const int r = blk * R + rr;
-            if (lane == 0 && r < rows) y[r] = v;
+                for (int i = 0; i < DEPTH; i++) {
+                    const int pp = pb + i;
+                    if (pp < e1) {
+                        float part = unit_dot<FMT>(buf[i], xv, c);
+                        if (pp + DEPTH < p1) load_row<FMT>(rowp(pp + DEPTH), cols, u, c, buf[i]);
+                        part = seg_sum_dpp<64>(uact ? part : 0.0f);
+                        if (lane == 63) red[(grp * COMBINE_CH + (pp - p0 - c0)) * S + sw] = part;
+                    }
+                }
+            }
+            __syncthreads();
+            for (int e = threadIdx.x; e < gpw * COMBINE_CH; e += blockDim.x) {
+                const int q = e / COMBINE_CH, i = e % COMBINE_CH;
+                int a0, a1;
+                strip(blockIdx.x * gpw + q, a0, a1);
+                const int pp = a0 + c0 + i;
+                if (pp < a1) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < S; k++) acc += red[(q * COMBINE_CH + i) * S + k];
+                    y[pp] = acc;
+                }
+            }
+            __syncthreads();
         }
     }
 }
@@ -532,34 +543,49 @@ static int env_int(const char *name, int dflt)
     return v && *v ? atoi(v) : dflt;
 }
 
+template <int FMT, int S>
+static void launch_split(soso_hip *h, int grid, int threads, size_t lds, const uint8_t *W, size_t stride,
+                         const float *x, float *y, int rows, int cols)
+{
+    mv_rows<FMT, 64, S, 8><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
+}
+
 template <int FMT>
 static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
 {
     const int rows = (int)w.rows, cols = (int)w.cols, U = cols / 64;
     const size_t stride = packed_row_stride(w.dtype, w.cols);
-    const size_t lds = (size_t)cols * 4 + (size_t)cols / 16 * 4;
+    const int S = (U + 63) / 64;
+    if (S > 8) return set_err(h, SOSO_HIP_DECLINED, "matvec: rows wider than 512 units");
+    const int gpw = 8 / S;                 // groups of S wavefronts per workgroup (<= 512 threads)
+    const int threads = 64 * S * gpw;
+    const size_t lds = stage_lds_bytes(w.cols) + (S > 1 ? (size_t)gpw * COMBINE_CH * S * 4 : 0);
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec: x does not fit in LDS");
-    const int threads = env_int("SOSO_HIP_WG", 512);
     const int per_cu = env_int("SOSO_HIP_WG_PER_CU", 1);
     const uint8_t *W = (const uint8_t *)w.dev;
-    if (U <= 64) {
+    if (S == 1) {
         const int LPR = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
         const int passes = (rows + 64 / LPR - 1) / (64 / LPR);
-        int grid = std::min(h->num_cu * per_cu, (passes + threads / 64 - 1) / (threads / 64));
+        int grid = std::min(h->num_cu * per_cu, (passes + gpw - 1) / gpw);
         grid = std::max(grid, 1);
-        constexpr int DEP = 4;
 #define MV_CASE(L)                                                                                                  \
-    case L: mv_xreg<FMT, L, DEP><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols); break;
+    case L: mv_rows<FMT, L, 1, 8><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols); break;
         switch (LPR) {
             MV_CASE(1) MV_CASE(2) MV_CASE(4) MV_CASE(8) MV_CASE(16) MV_CASE(32) MV_CASE(64)
         }
 #undef MV_CASE
     } else {
-        constexpr int R = 2;
-        const int nblk = (rows + R - 1) / R;
-        int grid = std::min(h->num_cu * per_cu, (nblk + threads / 64 - 1) / (threads / 64));
+        int grid = std::min(h->num_cu * per_cu, (rows + gpw - 1) / gpw);
         grid = std::max(grid, 1);
-        mv_loop<FMT, R><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
+        switch (S) {
+        case 2: launch_split<FMT, 2>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
+        case 3: launch_split<FMT, 3>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
+        case 4: launch_split<FMT, 4>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
+        case 5: launch_split<FMT, 5>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
+        case 6: launch_split<FMT, 6>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
+        case 7: launch_split<FMT, 7>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
+        case 8: launch_split<FMT, 8>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
+        }
     }
     return hip_check(h, hipGetLastError(), "matvec launch");
 }

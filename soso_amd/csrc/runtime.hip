@@ -26,6 +26,9 @@ int set_err(soso_hip *h, int code, const std::string &msg)
 int hip_check(soso_hip *h, hipError_t e, const char *what)
 {
     if (e == hipSuccess) return SOSO_HIP_OK;
+    // hipGetLastError() reports the last failing runtime call of this thread,
+    // not only launches: clear it so a later launch check sees its own status.
+    (void)hipGetLastError();
     return set_err(h, SOSO_HIP_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
@@ -441,6 +444,14 @@ int soso_hip_sync(soso_hip *h)
     if (!h) return SOSO_HIP_ERR_ARG;
     int rc = make_current(h);
     return rc == SOSO_HIP_OK ? hip_check(h, hipStreamSynchronize(h->stream), "sync") : rc;
+}
+
+int soso_hip_d2d(soso_hip *h, void *dst, const void *src, size_t bytes)
+{
+    if (!h || !dst || !src) return SOSO_HIP_ERR_ARG;
+    int rc = make_current(h);
+    return rc == SOSO_HIP_OK ? hip_check(h, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, h->stream), "d2d")
+                             : rc;
 }
 
 int soso_hip_weight_from_dev(soso_hip *h, const char *key, size_t key_len, const void *raw_dev, size_t w_len,

@@ -25,6 +25,12 @@ def _f32(a):
     return a
 
 
+def _raw(w):
+    """The tensor's bytes as soso holds them (TensorView.bytes): F32 weights are
+    viewed, not converted."""
+    return None if w is None else np.ascontiguousarray(w).reshape(-1).view(np.uint8)
+
+
 class HipGpu:
     def __init__(self, device=0, vram_budget=0):
         self.lib = abi.load()
@@ -76,7 +82,7 @@ class HipGpu:
     def matvec(self, key, w, dtype, rows, cols, x, out):
         """gpu.rs:432-440; overwrites `out` (float32, rows) on success."""
         k, kl = _key(key)
-        wb = None if w is None else np.ascontiguousarray(w, dtype=np.uint8)
+        wb = _raw(w)
         x = _f32(x)
         assert out.dtype == np.float32 and out.flags.c_contiguous and out.size == rows
         rc = self.lib.soso_hip_matvec(self.h, k, kl, None if wb is None else wb.ctypes.data,
@@ -87,7 +93,7 @@ class HipGpu:
     def matmul(self, key, w, dtype, rows, cols, n, x, out):
         """gpu.rs:443-455: out[n x rows] = x[n x cols] . W^T."""
         k, kl = _key(key)
-        wb = None if w is None else np.ascontiguousarray(w, dtype=np.uint8)
+        wb = _raw(w)
         x = _f32(x)
         assert out.dtype == np.float32 and out.flags.c_contiguous and out.size == n * rows
         rc = self.lib.soso_hip_matmul(self.h, k, kl, None if wb is None else wb.ctypes.data,
@@ -101,7 +107,7 @@ class HipGpu:
         arr = (abi.Op * len(ops))()
         for i, op in enumerate(ops):
             k, kl = _key(op["key"])
-            wb = None if op.get("w") is None else np.ascontiguousarray(op["w"], dtype=np.uint8)
+            wb = _raw(op.get("w"))
             x = _f32(op["x"])
             keep += [k, wb, x]
             arr[i] = abi.Op(k, kl, None if wb is None else wb.ctypes.data, 0 if wb is None else wb.size,
@@ -134,7 +140,7 @@ class HipGpu:
                 k, kl = _key(e["claves"][j])
                 wb = None
                 if e.get("w") is not None and e["w"][j] is not None:
-                    wb = np.ascontiguousarray(e["w"][j], dtype=np.uint8)
+                    wb = _raw(e["w"][j])
                 keep += [k, wb]
                 ex.keys[j] = k
                 ex.key_lens[j] = kl
@@ -242,3 +248,6 @@ class HipGpu:
 
     def graph_destroy(self, gid):
         self._rc(self.lib.soso_hip_graph_destroy(self.h, gid), "graph_destroy")
+
+    def d2d(self, dst, src, nbytes):
+        self._rc(self.lib.soso_hip_d2d(self.h, dst, src, nbytes), "d2d")

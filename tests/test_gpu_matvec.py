@@ -74,6 +74,10 @@ def test_dequant_bit_exact(gpu, orc, dtype, rows, cols):
     (Q6K, 4096, 4096),
     (Q4K, 1, 256), (Q4K, 3, 512), (Q8, 1, 64), (Q8, 257, 192), (Q6K, 1, 256), (Q6K, 129, 512),
     (F32, 128, 2048), (F32, 3, 44),
+    # rows split across wavefronts (U > 64 units): S = 2, 3, 4 and a ragged last slice
+    (Q4K, 700, 8192), (Q8, 333, 12288), (Q6K, 257, 16384), (Q4K, 65, 12544),
+    # more row passes per group than one LDS combine round holds
+    (Q4K, 33000, 16384),
 ])
 def test_matvec_parity(gpu, orc, dtype, rows, cols):
     w = orc.synth(dtype, rows, cols, 21, 4)
