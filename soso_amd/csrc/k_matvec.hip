@@ -178,15 +178,87 @@ __device__ __forceinline__ void split4(float4 v, int k, uint4 &o)
     o.w = pack_h2(a1 - (float)h1, a3 - (float)h3);
 }
 
-__device__ void stage_x(const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kx)
+enum { FMT_Q4K = 0, FMT_Q80 = 1, FMT_Q6K = 2 };
+
+// LDS slot of 4-element group g: the 16 groups a lane keeps in registers
+// (unit u, register j) sit at j*U + u, so the 64 lanes of a wavefront read 64
+// consecutive 16-byte slots (no bank conflicts).  Q4_K and Q8_0 units are 16
+// consecutive groups; a Q6_K unit (u = 4 sb + 2 h + kk) takes, for i, t < 4,
+// group sb*64 + h*32 + 8i + 4kk + t as register 4i + t.
+template <int FMT>
+__device__ __forceinline__ int xslot(int g, int U)
 {
-    // blockDim % 64 == 0: chunk c sits in lane c % 64, so the 16 chunks of a
-    // block form one DPP row.  The loop bound is uniform over the workgroup
-    // and lanes past the end take part in the DPP steps with zeros (cols is a
-    // multiple of 64, so a trailing block may be half full).
+    if constexpr (FMT == FMT_Q6K) {
+        const int sb = g >> 6, h = (g >> 5) & 1, i = (g >> 3) & 3, kk = (g >> 2) & 1, t = g & 3;
+        return (4 * i + t) * U + 4 * sb + 2 * h + kk;
+    } else {
+        return (g & 15) * U + (g >> 4);
+    }
+}
+
+// One 8-element chunk c (thread lane == c % 64).  Every lane of the 16-lane
+// DPP row takes part (invalid chunks carry zeros); only valid ones store.
+template <int FMT>
+__device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool valid, int U, uint4 *xp, float *s16,
+                                            int *kx)
+{
+    float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                    fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+    m = row16_max(m);
+    const int k = (m > 0.0f && m < INFINITY) ? __builtin_amdgcn_frexp_expf(m) - 14 : 0;
+    float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+    sm += dpp_f<0xB1>(sm);
+    if (valid) {
+        uint4 o0, o1;
+        split4(v0, k, o0);
+        split4(v1, k, o1);
+        xp[xslot<FMT>(2 * c, U)] = o0;
+        xp[xslot<FMT>(2 * c + 1, U)] = o1;
+        if ((c & 1) == 0) s16[c >> 1] = sm;
+        if ((c & 15) == 0) kx[c >> 4] = k;
+    }
+}
+
+// x is read in two steps so that its loads can be issued ahead of the weight
+// loads: vector-memory results return in issue order, so x loads issued after
+// a ring of weight loads would wait for all of those weights.
+constexpr int XPRE = 4; // chunks per thread loaded ahead (cols <= 32 * blockDim)
+struct XPre {
+    float4 v[2 * XPRE];
+};
+
+__device__ __forceinline__ void stage_x_issue(const float *__restrict__ x, int cols, XPre &p)
+{
     const int nch = cols >> 3;
     const float4 *x4 = (const float4 *)x;
-    for (int base = 0; base < nch; base += blockDim.x) {
+#pragma unroll
+    for (int j = 0; j < XPRE; j++) {
+        const int c = j * blockDim.x + threadIdx.x;
+        p.v[2 * j] = p.v[2 * j + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < nch) {
+            p.v[2 * j] = x4[2 * c];
+            p.v[2 * j + 1] = x4[2 * c + 1];
+        }
+    }
+}
+
+// blockDim % 64 == 0: chunk c sits in lane c % 64, so the 16 chunks of a
+// block form one DPP row.  Loop bounds are uniform over the workgroup (cols
+// is a multiple of 64, so a trailing block may be half full).
+template <int FMT>
+__device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kx)
+{
+    const int nch = cols >> 3, U = cols >> 6;
+#pragma unroll
+    for (int j = 0; j < XPRE; j++) {
+        const int base = j * blockDim.x;
+        if (base < nch) {
+            const int c = base + threadIdx.x;
+            stage_chunk<FMT>(p.v[2 * j], p.v[2 * j + 1], c, c < nch, U, xp, s16, kx);
+        }
+    }
+    const float4 *x4 = (const float4 *)x;
+    for (int base = XPRE * blockDim.x; base < nch; base += blockDim.x) {
         const int c = base + threadIdx.x;
         const bool valid = c < nch;
         float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
@@ -194,23 +266,17 @@ __device__ void stage_x(const float *__restrict__ x, int cols, uint4 *xp, float 
             v0 = x4[2 * c];
             v1 = x4[2 * c + 1];
         }
-        float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
-                        fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
-        m = row16_max(m);
-        const int k = (m > 0.0f && m < INFINITY) ? __builtin_amdgcn_frexp_expf(m) - 14 : 0;
-        float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
-        sm += dpp_f<0xB1>(sm);
-        if (valid) {
-            uint4 o0, o1;
-            split4(v0, k, o0);
-            split4(v1, k, o1);
-            xp[2 * c] = o0;
-            xp[2 * c + 1] = o1;
-            if ((c & 1) == 0) s16[c >> 1] = sm;
-            if ((c & 15) == 0) kx[c >> 4] = k;
-        }
+        stage_chunk<FMT>(v0, v1, c, valid, U, xp, s16, kx);
     }
     __syncthreads();
+}
+
+template <int FMT>
+__device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kx)
+{
+    XPre p;
+    stage_x_issue(x, cols, p);
+    stage_x_finish<FMT>(p, x, cols, xp, s16, kx);
 }
 
 static inline size_t stage_lds_bytes(size_t cols) { return cols * 4 + cols / 16 * 4 + (cols + 127) / 128 * 4; }
@@ -218,7 +284,6 @@ static inline size_t stage_lds_bytes(size_t cols) { return cols * 4 + cols / 16 
 // ---------------------------------------------------------------------------
 // Per-format unit math
 // ---------------------------------------------------------------------------
-enum { FMT_Q4K = 0, FMT_Q80 = 1, FMT_Q6K = 2 };
 
 template <int FMT> struct WRow;
 template <> struct WRow<FMT_Q4K> {
@@ -263,13 +328,13 @@ __device__ __forceinline__ void unit_setup_w(int u, UConst &c)
 
 // x-side constants and the unit's x in registers (after stage_x)
 template <int FMT>
-__device__ __forceinline__ void unit_setup_x(const uint4 *xp, const float *s16, const int *kx, int u, uint4 (&xv)[16],
-                                             UConst &c)
+__device__ __forceinline__ void unit_setup_x(const uint4 *xp, const float *s16, const int *kx, int u, int U,
+                                             uint4 (&xv)[16], UConst &c)
 {
     c.P = ldexpf(1.0f, (FMT == FMT_Q4K ? 20 : 24) + kx[u >> 1]);
     if (FMT == FMT_Q4K || FMT == FMT_Q80) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) xv[j] = xp[16 * u + j];
+        for (int j = 0; j < 16; j++) xv[j] = xp[j * U + u];
         const float s0 = s16[4 * u] + s16[4 * u + 1], s1 = s16[4 * u + 2] + s16[4 * u + 3];
         c.c[0] = FMT == FMT_Q4K ? s0 : 128.0f * s0;
         c.c[1] = FMT == FMT_Q4K ? s1 : 128.0f * s1;
@@ -278,33 +343,85 @@ __device__ __forceinline__ void unit_setup_x(const uint4 *xp, const float *s16, 
 #pragma unroll
         for (int i = 0; i < 4; i++) {
 #pragma unroll
-            for (int t = 0; t < 4; t++) xv[4 * i + t] = xp[sb * 64 + h * 32 + 8 * i + 4 * kk + t];
+            for (int t = 0; t < 4; t++) xv[4 * i + t] = xp[(4 * i + t) * U + u];
             c.c[i] = 32.0f * s16[sb * 16 + h * 8 + 2 * i + kk];
         }
     }
 }
 
-template <int FMT>
-__device__ __forceinline__ void load_row(const uint8_t *__restrict__ Wr, int cols, int u, const UConst &c, WRow<FMT> &w)
+// Raw buffer loads over one wavefront's strip of rows.  A pass whose offset
+// lies past the strip's byte count reads zeros without touching memory, so
+// every load of the ring is issued unconditionally and the compiler can wait
+// on exact vmcnt values.  (Raw-buffer range checks use the VGPR offset, so
+// pass offsets are kept there, not in the scalar offset.)
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000; // gfx9 raw buffer: 32-bit dwords, no swizzle
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes)
 {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, RSRC_WORD3);
+}
+__device__ __forceinline__ uint4 bld16(rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint2 bld8(rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bld2(rsrc_t r, uint32_t off)
+{
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// Byte offsets, inside one packed row, of what lane unit u loads.
+struct LaneOff {
+    uint32_t o[3];
+};
+
+template <int FMT>
+__device__ __forceinline__ LaneOff lane_offsets(int cols, int u, const UConst &c)
+{
+    LaneOff L;
     if constexpr (FMT == FMT_Q4K) {
         const int nb = cols >> 8, U = cols >> 6;
-        w.h = *(const uint4 *)(Wr + 16 * c.sb);
-        w.a = *(const uint4 *)(Wr + 16 * nb + 16 * u);
-        w.b = *(const uint4 *)(Wr + 16 * nb + 16 * U + 16 * u);
+        L.o[0] = 16 * c.sb;          // H[sb]
+        L.o[1] = 16 * nb + 16 * u;   // QA[u]
+        L.o[2] = L.o[1] + 16 * U;    // QB[u]
     } else if constexpr (FMT == FMT_Q80) {
-        const int nb = cols >> 5, U = cols >> 6, sreg = (4 * nb + 15) & ~15;
-        w.s = *(const uint2 *)(Wr + 8 * u);
-#pragma unroll
-        for (int i = 0; i < 4; i++) w.q[i] = *(const uint4 *)(Wr + sreg + 16 * U * i + 16 * u);
+        const int nb = cols >> 5, sreg = (4 * nb + 15) & ~15;
+        L.o[0] = 8 * u;              // S[2u], S[2u+1]
+        L.o[1] = sreg + 16 * u;      // plane 0 (planes i at + 16*U*i)
+        L.o[2] = 0;
     } else {
         const int nb = cols >> 8, U = cols >> 6;
-        const uint8_t *QH = Wr + 16 * nb;
-        w.qh = *(const uint4 *)(QH + 16 * u);
-        w.la = *(const uint4 *)(QH + 16 * U + 16 * u);
-        w.lb = *(const uint4 *)(QH + 32 * U + 16 * u);
-        w.sc = *(const uint2 *)(Wr + 16 * c.sb + 8 * c.s);
-        w.d = *(const unsigned short *)(QH + 48 * U + 2 * c.sb);
+        L.o[0] = 16 * nb + 16 * u;                 // QH[u] (QLa at +16U, QLb at +32U)
+        L.o[1] = 16 * c.sb + 8 * c.s;              // SC[sb] half s
+        L.o[2] = 16 * nb + 48 * U + 2 * c.sb;      // D[sb]
+    }
+    return L;
+}
+
+// Loads unit u of the row at byte offset `base` of the strip.
+template <int FMT>
+__device__ __forceinline__ void load_row(rsrc_t r, uint32_t base, int cols, const LaneOff &L, WRow<FMT> &w)
+{
+    if constexpr (FMT == FMT_Q4K) {
+        w.h = bld16(r, base + L.o[0]);
+        w.a = bld16(r, base + L.o[1]);
+        w.b = bld16(r, base + L.o[2]);
+    } else if constexpr (FMT == FMT_Q80) {
+        const uint32_t U16 = (uint32_t)(cols >> 6) * 16u;
+        w.s = bld8(r, base + L.o[0]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) w.q[i] = bld16(r, base + L.o[1] + U16 * i);
+    } else {
+        const uint32_t U16 = (uint32_t)(cols >> 6) * 16u;
+        w.qh = bld16(r, base + L.o[0]);
+        w.la = bld16(r, base + L.o[0] + U16);
+        w.lb = bld16(r, base + L.o[0] + 2 * U16);
+        w.sc = bld8(r, base + L.o[1]);
+        w.d = bld2(r, base + L.o[2]);
     }
 }
 
@@ -404,18 +521,39 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[
 // row passes; wavefront s of the group owns units [64s, 64s+64) of every row
 // (S = ceil(U/64), U = cols/64 units per row; for U <= 64, S = 1 and a pass
 // covers 64/LPR rows, LPR = lanes per row).  Each lane keeps its x unit in
-// VGPRs for the whole launch.  The loads of the first DEPTH passes are issued
-// before x is staged, then roll DEPTH passes ahead of the math.  With S > 1
-// the per-wavefront sums meet in LDS and are added in wavefront order.
+// VGPRs for the whole launch.  x is staged first, then the loads of the
+// first DEPTH passes are issued and the ring rolls DEPTH passes ahead of the
+// math.  Row sums are gathered into one
+// VGPR (lane i = i-th row of the strip, at most 64 rows) and stored once.
+// With S > 1 the per-wavefront sums meet in LDS and are added in wavefront
+// order.
 // ---------------------------------------------------------------------------
 constexpr int COMBINE_CH = 64; // passes per LDS combine round (S > 1)
+
+// Moves the row sums of pass jw (last lane of each LPR-lane segment) into
+// lanes jw*RW .. jw*RW+RW-1 of yacc.
+template <int LPR>
+__device__ __forceinline__ float gather_rows(float part, int jw, float yacc, int lane)
+{
+    constexpr int RW = 64 / LPR;
+    if constexpr (LPR == 64) {
+        const float s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, part), 63));
+        return lane == jw ? s : yacc;
+    } else {
+        const int d = lane - jw * RW;
+        const bool in = d >= 0 && d < RW;
+        const int src = in ? d * LPR + LPR - 1 : lane;
+        const float v = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src * 4, __builtin_bit_cast(int, part)));
+        return in ? v : yacc;
+    }
+}
 
 template <int FMT, int LPR, int S, int DEPTH>
 __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, size_t stride,
                                                const float *__restrict__ x, float *__restrict__ y, int rows, int cols)
 {
     static_assert(S == 1 || LPR == 64, "split rows use whole wavefronts");
-    static_assert(COMBINE_CH % DEPTH == 0, "combine rounds keep the load ring aligned");
+    static_assert(S == 1 || COMBINE_CH % DEPTH == 0, "combine rounds keep the load ring aligned");
     extern __shared__ uint4 smem[];
     uint4 *xp = smem;
     float *s16 = (float *)(xp + (cols >> 2));
@@ -423,16 +561,18 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     float *red = (float *)(kx + ((cols + 127) >> 7)); // [groups][COMBINE_CH][S] when S > 1
 
     constexpr int RW = 64 / LPR;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int gpw = (blockDim.x >> 6) / S; // groups per workgroup
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int gpw = (blockDim.x >> 6) / S; // groups per workgroup (blockDim = 64 * S * gpw)
     const int grp = wave / S, sw = wave % S;
     const int U = cols >> 6;
     const int ul = lane & (LPR - 1), slot = lane / LPR;
     const int ug = sw * 64 + ul;
-    const bool uact = ug < U && grp < gpw;
+    const bool uact = ug < U;
     const int u = uact ? ug : 0;
     UConst c;
     unit_setup_w<FMT>(u, c);
+    const LaneOff L = lane_offsets<FMT>(cols, u, c);
 
     const int passes = (rows + RW - 1) / RW;
     const int tg = gridDim.x * gpw;
@@ -440,36 +580,47 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         q0 = (int)((long)passes * g / tg);
         q1 = (int)((long)passes * (g + 1) / tg);
     };
-    int p0 = 0, p1 = 0;
-    if (grp < gpw) strip(blockIdx.x * gpw + grp, p0, p1);
-    auto rowp = [&](int pp) {
-        int r = pp * RW + slot;
-        r = r < rows ? r : rows - 1;
-        return W + (size_t)r * stride;
-    };
+    int p0, p1;
+    strip(blockIdx.x * gpw + grp, p0, p1);
+    const int n = p1 - p0;
+    const int r0 = p0 * RW, rend = min(p1 * RW, rows);
+    // The strip is the buffer; the host keeps it (plus DEPTH passes) under 2^31 bytes.
+    const uint32_t pass_bytes = (uint32_t)(RW * stride);
+    const rsrc_t rs = make_rsrc(W + (size_t)r0 * stride, (uint32_t)((size_t)(rend - r0) * stride));
+    // inactive lanes (unit past the row end) read nothing
+    const uint32_t lane_base = uact ? (uint32_t)(slot * stride) : 0x80000000u;
+
+    // x first: once the weight stream is requested, x's reads would queue
+    // behind it in the shared L2 channels.
+    stage_x<FMT>(x, cols, xp, s16, kx);
     WRow<FMT> buf[DEPTH];
 #pragma unroll
-    for (int i = 0; i < DEPTH; i++)
-        if (p0 + i < p1) load_row<FMT>(rowp(p0 + i), cols, u, c, buf[i]);
-
-    stage_x(x, cols, xp, s16, kx);
+    for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
     uint4 xv[16];
-    unit_setup_x<FMT>(xp, s16, kx, u, xv, c);
+    unit_setup_x<FMT>(xp, s16, kx, u, U, xv, c);
 
     if constexpr (S == 1) {
-        for (int pb = p0; pb < p1; pb += DEPTH) {
+        // The host sizes the grid so that a strip holds at most 64 rows: the
+        // loop then stores nothing and the strip's rows leave in one store at
+        // the end.  Loads are issued on every step (past the strip they read
+        // zeros for free) and only the math is skipped there, with no early
+        // exit; steps are fenced from the scheduler.  The compiler can then
+        // wait on exact vmcnt values.
+        float yacc = 0.0f;
+        for (int pb = 0; pb < n; pb += DEPTH) {
 #pragma unroll
             for (int i = 0; i < DEPTH; i++) {
-                const int pp = pb + i;
-                if (pp < p1) {
+                const int j = pb + i;
+                if (j < n) {
                     float part = unit_dot<FMT>(buf[i], xv, c);
-                    if (pp + DEPTH < p1) load_row<FMT>(rowp(pp + DEPTH), cols, u, c, buf[i]);
                     part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
-                    const int r = pp * RW + slot;
-                    if (ul == LPR - 1 && r < rows) y[r] = part;
+                    yacc = gather_rows<LPR>(part, j, yacc, lane);
                 }
+                load_row<FMT>(rs, lane_base + (uint32_t)(j + DEPTH) * pass_bytes, cols, L, buf[i]);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
+        if (lane < n * RW && r0 + lane < rows) y[r0 + lane] = yacc;
     } else {
         // the same number of combine rounds for every wavefront of the workgroup
         int nmax = 0;
@@ -479,17 +630,19 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
             nmax = a1 - a0 > nmax ? a1 - a0 : nmax;
         }
         for (int c0 = 0; c0 < nmax; c0 += COMBINE_CH) {
-            const int e1 = p0 + c0 + COMBINE_CH < p1 ? p0 + c0 + COMBINE_CH : p1;
-            for (int pb = p0 + c0; pb < e1; pb += DEPTH) {
+            const int e1 = c0 + COMBINE_CH < n ? c0 + COMBINE_CH : n;
+            for (int pb = c0; pb < e1; pb += DEPTH) {
 #pragma unroll
                 for (int i = 0; i < DEPTH; i++) {
-                    const int pp = pb + i;
-                    if (pp < e1) {
+                    // j - c0 < COMBINE_CH (a multiple of DEPTH) for every step
+                    const int j = pb + i;
+                    if (j < e1) {
                         float part = unit_dot<FMT>(buf[i], xv, c);
-                        if (pp + DEPTH < p1) load_row<FMT>(rowp(pp + DEPTH), cols, u, c, buf[i]);
                         part = seg_sum_dpp<64>(uact ? part : 0.0f);
-                        if (lane == 63) red[(grp * COMBINE_CH + (pp - p0 - c0)) * S + sw] = part;
+                        if (lane == 63) red[(grp * COMBINE_CH + (j - c0)) * S + sw] = part;
                     }
+                    load_row<FMT>(rs, lane_base + (uint32_t)(j + DEPTH) * pass_bytes, cols, L, buf[i]);
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
             __syncthreads();
@@ -543,11 +696,29 @@ static int env_int(const char *name, int dflt)
     return v && *v ? atoi(v) : dflt;
 }
 
+// A group's strip (plus the DEPTH passes the ring reads past it, which come
+// back as zeros) is addressed with 32-bit buffer offsets.
+static bool strip_fits(int passes, int groups, size_t pass_bytes)
+{
+    const size_t per = ((size_t)passes + groups - 1) / groups + 16;
+    return per * pass_bytes < ((size_t)1 << 31);
+}
+
+// Ring depth (passes in flight per wavefront).  Measured on MI355X for the
+// Q4_K 14336 x 4096 matvec: depth 3 beats 2, 4, 6 and 8 (with all of a
+// wavefront's rows in flight at once, every wavefront's first row arrives
+// late and the math cannot overlap the stream).  Split rows (S > 1) need a
+// depth that divides the combine round.
+template <int FMT, int S> constexpr int ring_depth()
+{
+    return S == 1 ? (FMT == FMT_Q4K ? 3 : 4) : 4;
+}
+
 template <int FMT, int S>
 static void launch_split(soso_hip *h, int grid, int threads, size_t lds, const uint8_t *W, size_t stride,
                          const float *x, float *y, int rows, int cols)
 {
-    mv_rows<FMT, 64, S, 8><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
+    mv_rows<FMT, 64, S, ring_depth<FMT, S>()><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
 }
 
 template <int FMT>
@@ -567,9 +738,14 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
         const int LPR = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
         const int passes = (rows + 64 / LPR - 1) / (64 / LPR);
         int grid = std::min(h->num_cu * per_cu, (passes + gpw - 1) / gpw);
+        // every group's strip holds at most 64 rows (the kernel's output register)
+        const int ppw = LPR; // passes per 64 rows = 64 / (64 / LPR)
+        grid = std::max(grid, ((passes + ppw - 1) / ppw + gpw - 1) / gpw);
         grid = std::max(grid, 1);
+        if (!strip_fits(passes, grid * gpw, (size_t)(64 / LPR) * stride))
+            return set_err(h, SOSO_HIP_DECLINED, "matvec: row strip exceeds 2 GiB");
 #define MV_CASE(L)                                                                                                  \
-    case L: mv_rows<FMT, L, 1, 8><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols); break;
+    case L: mv_rows<FMT, L, 1, ring_depth<FMT, 1>()><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols); break;
         switch (LPR) {
             MV_CASE(1) MV_CASE(2) MV_CASE(4) MV_CASE(8) MV_CASE(16) MV_CASE(32) MV_CASE(64)
         }
@@ -577,6 +753,7 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
     } else {
         int grid = std::min(h->num_cu * per_cu, (rows + gpw - 1) / gpw);
         grid = std::max(grid, 1);
+        if (!strip_fits(rows, grid * gpw, stride)) return set_err(h, SOSO_HIP_DECLINED, "matvec: row strip exceeds 2 GiB");
         switch (S) {
         case 2: launch_split<FMT, 2>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
         case 3: launch_split<FMT, 3>(h, grid, threads, lds, W, stride, x, y, rows, cols); break;
