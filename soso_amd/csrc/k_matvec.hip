@@ -156,66 +156,85 @@ int repack_weight(soso_hip *h, uint8_t dtype, const void *raw, void *packed, siz
 // ---------------------------------------------------------------------------
 // x staging (one barrier)
 // Each thread converts chunks of 8 elements; the 16 chunks of a 128-element
-// block sit in one 16-lane DPP row, which agrees on the block's scale
-// exponent k (max|x| * 2^-k < 2^14).  LDS receives
-//   xp[g]  = {hi(e0,e2), hi(e1,e3), lo(e0,e2), lo(e1,e3)} for the 4-element
-//            group g of x*2^-k (hi + lo = 22 significant bits, exact f16s),
-//   s16[i] = f32 sum of x[16i .. 16i+16) (unscaled), kx[b] = k of block b.
+// block sit in one 16-lane DPP row, which agrees on the block's exponent e
+// (max|x| * 2^e <= 2^22).  Every element becomes the integer X = rint(x*2^e)
+// (|X| <= 2^22, 22 significant bits), written as three balanced signed
+// digits X = d2*2^16 + d1*2^8 + d0 (d0, d1 in [-128, 127], |d2| <= 64).  LDS
+// receives, per 4-element group, one dword of bytes per digit, plus
+//   s16[i] = f32 sum of x[16i .. 16i+16) (unscaled), kx[b] = e of block b.
+// The weights' integer codes then meet x in v_dot4_i32_i8 (exact int32 sums
+// per digit), and only the three digit sums of a sub-block are rounded.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t pack_h2(float a, float b)
-{
-    f16x2_t v = {(_Float16)a, (_Float16)b};
-    return __builtin_bit_cast(uint32_t, v);
-}
-
-__device__ __forceinline__ void split4(float4 v, int k, uint4 &o)
-{
-    const float a0 = ldexpf(v.x, -k), a1 = ldexpf(v.y, -k), a2 = ldexpf(v.z, -k), a3 = ldexpf(v.w, -k);
-    const _Float16 h0 = (_Float16)a0, h1 = (_Float16)a1, h2 = (_Float16)a2, h3 = (_Float16)a3;
-    o.x = __builtin_bit_cast(uint32_t, (f16x2_t){h0, h2});
-    o.y = __builtin_bit_cast(uint32_t, (f16x2_t){h1, h3});
-    o.z = pack_h2(a0 - (float)h0, a2 - (float)h2);
-    o.w = pack_h2(a1 - (float)h1, a3 - (float)h3);
-}
-
 enum { FMT_Q4K = 0, FMT_Q80 = 1, FMT_Q6K = 2 };
 
-// LDS slot of 4-element group g: the 16 groups a lane keeps in registers
-// (unit u, register j) sit at j*U + u, so the 64 lanes of a wavefront read 64
-// consecutive 16-byte slots (no bank conflicts).  Q4_K and Q8_0 units are 16
-// consecutive groups; a Q6_K unit (u = 4 sb + 2 h + kk) takes, for i, t < 4,
-// group sb*64 + h*32 + 8i + 4kk + t as register 4i + t.
+constexpr int XDIG = 3;        // digits per element
+constexpr int XD = 16 * XDIG;  // dwords of x per lane unit (16 groups)
+
+// Unit u and register group gi (0..15) of 4-element group g.  Q4_K and Q8_0
+// units are 16 consecutive groups; a Q6_K unit (u = 4 sb + 2 h + kk) takes,
+// for i, t < 4, group sb*64 + h*32 + 8i + 4kk + t as register group 4i + t.
 template <int FMT>
-__device__ __forceinline__ int xslot(int g, int U)
+__device__ __forceinline__ void xunit(int g, int &u, int &gi)
 {
     if constexpr (FMT == FMT_Q6K) {
         const int sb = g >> 6, h = (g >> 5) & 1, i = (g >> 3) & 3, kk = (g >> 2) & 1, t = g & 3;
-        return (4 * i + t) * U + 4 * sb + 2 * h + kk;
+        u = 4 * sb + 2 * h + kk;
+        gi = 4 * i + t;
     } else {
-        return (g & 15) * U + (g >> 4);
+        u = g >> 4;
+        gi = g & 15;
+    }
+}
+
+// LDS dword of register dword w (= 3 gi + digit) of unit u: dwords 4r..4r+3
+// of every unit sit in one 16-byte slot r*U + u, so the 64 lanes of a
+// wavefront read 64 consecutive slots (no bank conflicts).
+__device__ __forceinline__ int xdw(int u, int w, int U) { return ((w >> 2) * U + u) * 4 + (w & 3); }
+
+// Three balanced base-256 digits of the four elements of v (scaled by 2^e),
+// packed one byte per element per digit.
+__device__ __forceinline__ void digits4(float4 v, int e, uint32_t (&d)[XDIG])
+{
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    d[0] = d[1] = d[2] = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int X = (int)rintf(ldexpf(f[i], e));
+        const int d0 = (int)(int8_t)(X & 0xff);
+        const int X1 = (X - d0) >> 8;
+        const int d1 = (int)(int8_t)(X1 & 0xff);
+        const int d2 = (X1 - d1) >> 8;
+        d[0] |= (uint32_t)(d0 & 0xff) << (8 * i);
+        d[1] |= (uint32_t)(d1 & 0xff) << (8 * i);
+        d[2] |= (uint32_t)(d2 & 0xff) << (8 * i);
     }
 }
 
 // One 8-element chunk c (thread lane == c % 64).  Every lane of the 16-lane
 // DPP row takes part (invalid chunks carry zeros); only valid ones store.
 template <int FMT>
-__device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool valid, int U, uint4 *xp, float *s16,
+__device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool valid, int U, uint32_t *xd, float *s16,
                                             int *kx)
 {
     float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
                     fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
     m = row16_max(m);
-    const int k = (m > 0.0f && m < INFINITY) ? __builtin_amdgcn_frexp_expf(m) - 14 : 0;
+    const int e = (m > 0.0f && m < INFINITY) ? 22 - __builtin_amdgcn_frexp_expf(m) : 0;
     float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
     sm += dpp_f<0xB1>(sm);
     if (valid) {
-        uint4 o0, o1;
-        split4(v0, k, o0);
-        split4(v1, k, o1);
-        xp[xslot<FMT>(2 * c, U)] = o0;
-        xp[xslot<FMT>(2 * c + 1, U)] = o1;
+        uint32_t d0[XDIG], d1[XDIG];
+        digits4(v0, e, d0);
+        digits4(v1, e, d1);
+        int u, gi;
+        xunit<FMT>(2 * c, u, gi);
+#pragma unroll
+        for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d0[k];
+        xunit<FMT>(2 * c + 1, u, gi);
+#pragma unroll
+        for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d1[k];
         if ((c & 1) == 0) s16[c >> 1] = sm;
-        if ((c & 15) == 0) kx[c >> 4] = k;
+        if ((c & 15) == 0) kx[c >> 4] = e;
     }
 }
 
@@ -246,7 +265,7 @@ __device__ __forceinline__ void stage_x_issue(const float *__restrict__ x, int c
 // block form one DPP row.  Loop bounds are uniform over the workgroup (cols
 // is a multiple of 64, so a trailing block may be half full).
 template <int FMT>
-__device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kx)
+__device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx)
 {
     const int nch = cols >> 3, U = cols >> 6;
 #pragma unroll
@@ -272,14 +291,14 @@ __device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int c
 }
 
 template <int FMT>
-__device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint4 *xp, float *s16, int *kx)
+__device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx)
 {
     XPre p;
     stage_x_issue(x, cols, p);
     stage_x_finish<FMT>(p, x, cols, xp, s16, kx);
 }
 
-static inline size_t stage_lds_bytes(size_t cols) { return cols * 4 + cols / 16 * 4 + (cols + 127) / 128 * 4; }
+static inline size_t stage_lds_bytes(size_t cols) { return cols * XDIG + cols / 16 * 4 + (cols + 127) / 128 * 4; }
 
 // ---------------------------------------------------------------------------
 // Per-format unit math
@@ -302,7 +321,7 @@ template <> struct WRow<FMT_Q6K> {
 // lane constants for one unit
 struct UConst {
     float c[4];
-    float P;                 // 2^(20+k) (Q4_K) or 2^(24+k): undoes the subnormal codes and the x scale
+    float P;                 // 2^-e of the unit's 128-element block: undoes the x scale
     uint32_t k1, k2, s, bsh; // Q4_K scale-decode selectors; Q6_K: s = half, bsh = 8*kk
     int sb;
 };
@@ -326,27 +345,54 @@ __device__ __forceinline__ void unit_setup_w(int u, UConst &c)
     }
 }
 
+// The unit's x digits in registers: XD dwords, dword 3 gi + k = digit k of
+// register group gi.
+struct XReg {
+    uint32_t d[XD];
+};
+
 // x-side constants and the unit's x in registers (after stage_x)
 template <int FMT>
-__device__ __forceinline__ void unit_setup_x(const uint4 *xp, const float *s16, const int *kx, int u, int U,
-                                             uint4 (&xv)[16], UConst &c)
+__device__ __forceinline__ void unit_setup_x(const uint32_t *xd, const float *s16, const int *kx, int u, int U, XReg &xv,
+                                             UConst &c)
 {
-    c.P = ldexpf(1.0f, (FMT == FMT_Q4K ? 20 : 24) + kx[u >> 1]);
-    if (FMT == FMT_Q4K || FMT == FMT_Q80) {
+    c.P = ldexpf(1.0f, -kx[u >> 1]);
+    const uint4 *x4 = (const uint4 *)xd;
 #pragma unroll
-        for (int j = 0; j < 16; j++) xv[j] = xp[j * U + u];
-        const float s0 = s16[4 * u] + s16[4 * u + 1], s1 = s16[4 * u + 2] + s16[4 * u + 3];
-        c.c[0] = FMT == FMT_Q4K ? s0 : 128.0f * s0;
-        c.c[1] = FMT == FMT_Q4K ? s1 : 128.0f * s1;
-    } else {
+    for (int r = 0; r < XD / 4; r++) {
+        const uint4 v = x4[r * U + u];
+        xv.d[4 * r] = v.x;
+        xv.d[4 * r + 1] = v.y;
+        xv.d[4 * r + 2] = v.z;
+        xv.d[4 * r + 3] = v.w;
+    }
+    if (FMT == FMT_Q4K) {
+        c.c[0] = s16[4 * u] + s16[4 * u + 1];
+        c.c[1] = s16[4 * u + 2] + s16[4 * u + 3];
+    } else if (FMT == FMT_Q6K) {
         const int sb = u >> 2, h = (u >> 1) & 1, kk = u & 1;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-#pragma unroll
-            for (int t = 0; t < 4; t++) xv[4 * i + t] = xp[(4 * i + t) * U + u];
-            c.c[i] = 32.0f * s16[sb * 16 + h * 8 + 2 * i + kk];
-        }
+        for (int i = 0; i < 4; i++) c.c[i] = 32.0f * s16[sb * 16 + h * 8 + 2 * i + kk];
     }
+}
+
+// v_dot4_i32_i8: four signed byte products added to an int32 (exact).
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// One code dword (four signed byte codes) against register group gi.
+__device__ __forceinline__ void dot_group(uint32_t q, const XReg &xv, int gi, int (&s)[XDIG])
+{
+#pragma unroll
+    for (int k = 0; k < XDIG; k++) s[k] = sdot4(q, xv.d[XDIG * gi + k], s[k]);
+}
+
+// Sum over the digits: (s2 * 2^16 + s1 * 2^8 + s0), rounded once or twice.
+__device__ __forceinline__ float digits_value(const int (&s)[XDIG])
+{
+    return fmaf((float)s[2], 65536.0f, (float)(s[1] * 256 + s[0]));
 }
 
 // Raw buffer loads over one wavefront's strip of rows.  A pass whose offset
@@ -427,28 +473,19 @@ __device__ __forceinline__ void load_row(rsrc_t r, uint32_t base, int cols, cons
 
 // Partial dot of one unit of one row (in units of x).
 template <int FMT>
-__device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[16], const UConst &c)
+__device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const XReg &xv, const UConst &c)
 {
     const float P = c.P;
     if constexpr (FMT == FMT_Q4K) {
-        // Low nibbles of the pair are sub-block 2p (elements 0..31 of the
-        // unit), high nibbles sub-block 2p+1 (elements 32..63), read as 16*q.
+        // qs byte l of the pair: low nibble = element l of sub-block 2p (unit
+        // elements 0..31, register groups 0..7), high nibble = element l of
+        // sub-block 2p+1 (register groups 8..15).
         const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
-        float l0 = 0.f, l1 = 0.f, h0 = 0.f, h1 = 0.f;
+        int sa[XDIG] = {0, 0, 0}, sb[XDIG] = {0, 0, 0};
 #pragma unroll
         for (int t = 0; t < 8; t++) {
-            const uint32_t v = q[t], v8 = v >> 8;
-            const uint32_t A = v & 0x000F000Fu, C = v & 0x00F000F0u;
-            const uint32_t B = v8 & 0x000F000Fu, D = v8 & 0x00F000F0u;
-            const uint4 xl = xv[t], xh = xv[8 + t];
-            l0 = dot2(A, xl.x, l0);
-            l1 = dot2(A, xl.z, l1);
-            l0 = dot2(B, xl.y, l0);
-            l1 = dot2(B, xl.w, l1);
-            h0 = dot2(C, xh.x, h0);
-            h1 = dot2(C, xh.z, h1);
-            h0 = dot2(D, xh.y, h0);
-            h1 = dot2(D, xh.w, h1);
+            dot_group(q[t] & 0x0F0F0F0Fu, xv, t, sa);
+            dot_group((q[t] >> 4) & 0x0F0F0F0Fu, xv, 8 + t, sb);
         }
         // 6-bit scale/min of sub-blocks 2p, 2p+1 (get_scale_min_k4,
         // crates/sosomodel/src/dequant.rs:150-159), four at a time per byte lane.
@@ -457,33 +494,27 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[
         const float sca = (float)(SC4 & 0xffu), scb = (float)((SC4 >> 8) & 0xffu);
         const float ma = (float)(M4 & 0xffu), mb = (float)((M4 >> 8) & 0xffu);
         const float d = half_bits_to_f32(w.h.x & 0xffffu), dmin = half_bits_to_f32(w.h.x >> 16);
-        const float uu = fmaf(sca * 16.0f, l0 + l1, scb * (h0 + h1));
+        const float uu = fmaf(sca, digits_value(sa), scb * digits_value(sb));
         const float vv = fmaf(mb, c.c[1], ma * c.c[0]);
         return fmaf(d * P, uu, -(dmin * vv));
     } else if constexpr (FMT == FMT_Q80) {
-        float s[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+        // plane p holds bytes 16(p&1) .. +15 of block p>>1: register groups 4p .. 4p+3
+        int s0[XDIG] = {0, 0, 0}, s1[XDIG] = {0, 0, 0};
 #pragma unroll
-        for (int blk = 0; blk < 2; blk++) {
-            const uint32_t q[8] = {w.q[2 * blk].x, w.q[2 * blk].y, w.q[2 * blk].z, w.q[2 * blk].w,
-                                   w.q[2 * blk + 1].x, w.q[2 * blk + 1].y, w.q[2 * blk + 1].z, w.q[2 * blk + 1].w};
+        for (int p = 0; p < 4; p++) {
+            const uint32_t q[4] = {w.q[p].x, w.q[p].y, w.q[p].z, w.q[p].w};
 #pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const uint32_t v = q[t] ^ 0x80808080u; // offset binary: q + 128
-                const uint32_t A = byte_perm(v, SEL_B02), B = byte_perm(v, SEL_B13);
-                const uint4 xx = xv[8 * blk + t];
-                s[blk][0] = dot2(A, xx.x, s[blk][0]);
-                s[blk][1] = dot2(A, xx.z, s[blk][1]);
-                s[blk][0] = dot2(B, xx.y, s[blk][0]);
-                s[blk][1] = dot2(B, xx.w, s[blk][1]);
+            for (int t = 0; t < 4; t++) {
+                if (p < 2) dot_group(q[t], xv, 4 * p + t, s0);
+                else dot_group(q[t], xv, 4 * p + t, s1);
             }
         }
-        const float t0 = fmaf(s[0][0] + s[0][1], P, -c.c[0]);
-        const float t1 = fmaf(s[1][0] + s[1][1], P, -c.c[1]);
-        return fmaf(__builtin_bit_cast(float, w.s.x), t0, __builtin_bit_cast(float, w.s.y) * t1);
+        return P * fmaf(__builtin_bit_cast(float, w.s.x), digits_value(s0),
+                        __builtin_bit_cast(float, w.s.y) * digits_value(s1));
     } else {
-        float s[4][2];
+        int s[4][XDIG];
 #pragma unroll
-        for (int i = 0; i < 4; i++) s[i][0] = s[i][1] = 0.f;
+        for (int i = 0; i < 4; i++) s[i][0] = s[i][1] = s[i][2] = 0;
         const uint32_t la[4] = {w.la.x, w.la.y, w.la.z, w.la.w}, lb[4] = {w.lb.x, w.lb.y, w.lb.z, w.lb.w};
         const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
 #pragma unroll
@@ -496,22 +527,15 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const uint4 (&xv)[
             q[2] = ((la[t] >> 4) & 0x0F0F0F0Fu) | (qh[t] & 0x30303030u);
             q[3] = ((lb[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> 2) & 0x30303030u);
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t A = byte_perm(q[i], SEL_B02), B = byte_perm(q[i], SEL_B13);
-                const uint4 xx = xv[4 * i + t];
-                s[i][0] = dot2(A, xx.x, s[i][0]);
-                s[i][1] = dot2(A, xx.z, s[i][1]);
-                s[i][0] = dot2(B, xx.y, s[i][0]);
-                s[i][1] = dot2(B, xx.w, s[i][1]);
-            }
+            for (int i = 0; i < 4; i++) dot_group(q[i], xv, 4 * i + t, s[i]);
         }
         // sub-scales sc[h*8 + kk + 2i] (int8), the -32 offset through c[i] = 32*sum(x)
         const float sc0 = (float)(int8_t)(w.sc.x >> c.bsh), sc1 = (float)(int8_t)(w.sc.x >> (c.bsh + 16));
         const float sc2 = (float)(int8_t)(w.sc.y >> c.bsh), sc3 = (float)(int8_t)(w.sc.y >> (c.bsh + 16));
-        float acc = sc0 * fmaf(s[0][0] + s[0][1], P, -c.c[0]);
-        acc = fmaf(sc1, fmaf(s[1][0] + s[1][1], P, -c.c[1]), acc);
-        acc = fmaf(sc2, fmaf(s[2][0] + s[2][1], P, -c.c[2]), acc);
-        acc = fmaf(sc3, fmaf(s[3][0] + s[3][1], P, -c.c[3]), acc);
+        float acc = sc0 * fmaf(digits_value(s[0]), P, -c.c[0]);
+        acc = fmaf(sc1, fmaf(digits_value(s[1]), P, -c.c[1]), acc);
+        acc = fmaf(sc2, fmaf(digits_value(s[2]), P, -c.c[2]), acc);
+        acc = fmaf(sc3, fmaf(digits_value(s[3]), P, -c.c[3]), acc);
         return half_bits_to_f32(w.d) * acc;
     }
 }
@@ -548,15 +572,15 @@ __device__ __forceinline__ float gather_rows(float part, int jw, float yacc, int
     }
 }
 
-template <int FMT, int LPR, int S, int DEPTH>
+template <int FMT, int LPR, int S, int DEPTH, bool XFIRST>
 __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, size_t stride,
                                                const float *__restrict__ x, float *__restrict__ y, int rows, int cols)
 {
     static_assert(S == 1 || LPR == 64, "split rows use whole wavefronts");
     static_assert(S == 1 || COMBINE_CH % DEPTH == 0, "combine rounds keep the load ring aligned");
     extern __shared__ uint4 smem[];
-    uint4 *xp = smem;
-    float *s16 = (float *)(xp + (cols >> 2));
+    uint32_t *xp = (uint32_t *)smem;                 // cols/4 groups x XDIG digit dwords
+    float *s16 = (float *)(xp + (cols >> 2) * XDIG);
     int *kx = (int *)(s16 + (cols >> 4));
     float *red = (float *)(kx + ((cols + 127) >> 7)); // [groups][COMBINE_CH][S] when S > 1
 
@@ -590,34 +614,53 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     // inactive lanes (unit past the row end) read nothing
     const uint32_t lane_base = uact ? (uint32_t)(slot * stride) : 0x80000000u;
 
-    // x first: once the weight stream is requested, x's reads would queue
-    // behind it in the shared L2 channels.
-    stage_x<FMT>(x, cols, xp, s16, kx);
     WRow<FMT> buf[DEPTH];
+    if constexpr (XFIRST) {
+        // x first: once the weight stream is requested, x's reads would queue
+        // behind it in the shared L2 channels.
+        stage_x<FMT>(x, cols, xp, s16, kx);
 #pragma unroll
-    for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
-    uint4 xv[16];
+        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
+    } else {
+        // x's loads, then the ring's, then x's conversion while the ring is
+        // in flight (loads return in issue order)
+        XPre xpre;
+        stage_x_issue(x, cols, xpre);
+#pragma unroll
+        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
+        stage_x_finish<FMT>(xpre, x, cols, xp, s16, kx);
+    }
+    XReg xv;
     unit_setup_x<FMT>(xp, s16, kx, u, U, xv, c);
 
     if constexpr (S == 1) {
         // The host sizes the grid so that a strip holds at most 64 rows: the
         // loop then stores nothing and the strip's rows leave in one store at
-        // the end.  Loads are issued on every step (past the strip they read
-        // zeros for free) and only the math is skipped there, with no early
-        // exit; steps are fenced from the scheduler.  The compiler can then
-        // wait on exact vmcnt values.
+        // the end.  The main loop is a counted loop of whole ring turns with
+        // no branches inside (refills past the strip read zeros for free) and
+        // its steps fenced from the scheduler, so the compiler waits on exact
+        // vmcnt values; the last n % DEPTH passes are already in the ring.
         float yacc = 0.0f;
-        for (int pb = 0; pb < n; pb += DEPTH) {
+        const int turns = n / DEPTH;
+        int j0 = 0;
+        for (int it = 0; it < turns; it++, j0 += DEPTH) {
 #pragma unroll
             for (int i = 0; i < DEPTH; i++) {
-                const int j = pb + i;
-                if (j < n) {
-                    float part = unit_dot<FMT>(buf[i], xv, c);
-                    part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
-                    yacc = gather_rows<LPR>(part, j, yacc, lane);
-                }
+                const int j = j0 + i;
+                float part = unit_dot<FMT>(buf[i], xv, c);
                 load_row<FMT>(rs, lane_base + (uint32_t)(j + DEPTH) * pass_bytes, cols, L, buf[i]);
+                part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
+                yacc = gather_rows<LPR>(part, j, yacc, lane);
                 __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        const int rem = n - j0;
+#pragma unroll
+        for (int i = 0; i < DEPTH - 1; i++) {
+            if (i < rem) {
+                float part = unit_dot<FMT>(buf[i], xv, c);
+                part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
+                yacc = gather_rows<LPR>(part, j0 + i, yacc, lane);
             }
         }
         if (lane < n * RW && r0 + lane < rows) y[r0 + lane] = yacc;
@@ -630,19 +673,29 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
             nmax = a1 - a0 > nmax ? a1 - a0 : nmax;
         }
         for (int c0 = 0; c0 < nmax; c0 += COMBINE_CH) {
+            // passes c0 .. e1-1 of this group; only a group's last round can
+            // end off a ring turn (COMBINE_CH is a multiple of DEPTH)
             const int e1 = c0 + COMBINE_CH < n ? c0 + COMBINE_CH : n;
-            for (int pb = c0; pb < e1; pb += DEPTH) {
+            const int turns = e1 > c0 ? (e1 - c0) / DEPTH : 0;
+            int j0 = c0;
+            for (int it = 0; it < turns; it++, j0 += DEPTH) {
 #pragma unroll
                 for (int i = 0; i < DEPTH; i++) {
-                    // j - c0 < COMBINE_CH (a multiple of DEPTH) for every step
-                    const int j = pb + i;
-                    if (j < e1) {
-                        float part = unit_dot<FMT>(buf[i], xv, c);
-                        part = seg_sum_dpp<64>(uact ? part : 0.0f);
-                        if (lane == 63) red[(grp * COMBINE_CH + (j - c0)) * S + sw] = part;
-                    }
+                    const int j = j0 + i;
+                    float part = unit_dot<FMT>(buf[i], xv, c);
                     load_row<FMT>(rs, lane_base + (uint32_t)(j + DEPTH) * pass_bytes, cols, L, buf[i]);
+                    part = seg_sum_dpp<64>(uact ? part : 0.0f);
+                    if (lane == 63) red[(grp * COMBINE_CH + (j - c0)) * S + sw] = part;
                     __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            const int rem = e1 > j0 ? e1 - j0 : 0;
+#pragma unroll
+            for (int i = 0; i < DEPTH - 1; i++) {
+                if (i < rem) {
+                    float part = unit_dot<FMT>(buf[i], xv, c);
+                    part = seg_sum_dpp<64>(uact ? part : 0.0f);
+                    if (lane == 63) red[(grp * COMBINE_CH + (j0 + i - c0)) * S + sw] = part;
                 }
             }
             __syncthreads();
@@ -704,21 +757,26 @@ static bool strip_fits(int passes, int groups, size_t pass_bytes)
     return per * pass_bytes < ((size_t)1 << 31);
 }
 
-// Ring depth (passes in flight per wavefront).  Measured on MI355X for the
-// Q4_K 14336 x 4096 matvec: depth 3 beats 2, 4, 6 and 8 (with all of a
-// wavefront's rows in flight at once, every wavefront's first row arrives
-// late and the math cannot overlap the stream).  Split rows (S > 1) need a
-// depth that divides the combine round.
+// Ring depth (passes in flight per wavefront) and issue order, measured on
+// MI355X (back-to-back launches over rotating weights above the MALL size):
+//   Q4_K 14336 x 4096: depth 2, ring loads before x's conversion (8.4 us;
+//     depth 8 x-first 11.0 us -- with all of a wavefront's rows in flight at
+//     once every wavefront's first row arrives late and the math cannot
+//     overlap the stream);  Q8_0 4096 x 4096: depth 3 (5.8 us);
+//   Q6_K 128256 x 4096: depth 4 (74.4 us);  split rows 4096 x 14336: depth 2;
+//   narrow rows (LPR < 64, e.g. 768 x 2048): depth 2 with x staged first.
+// Split rows (S > 1) need a depth that divides the combine round.
 template <int FMT, int S> constexpr int ring_depth()
 {
-    return S == 1 ? (FMT == FMT_Q4K ? 3 : 4) : 4;
+    return S > 1 ? 2 : FMT == FMT_Q4K ? 2 : FMT == FMT_Q80 ? 3 : 4;
 }
+template <int LPR> constexpr bool x_first() { return LPR < 64; }
 
 template <int FMT, int S>
 static void launch_split(soso_hip *h, int grid, int threads, size_t lds, const uint8_t *W, size_t stride,
                          const float *x, float *y, int rows, int cols)
 {
-    mv_rows<FMT, 64, S, ring_depth<FMT, S>()><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
+    mv_rows<FMT, 64, S, ring_depth<FMT, S>(), false><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
 }
 
 template <int FMT>
@@ -745,7 +803,10 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
         if (!strip_fits(passes, grid * gpw, (size_t)(64 / LPR) * stride))
             return set_err(h, SOSO_HIP_DECLINED, "matvec: row strip exceeds 2 GiB");
 #define MV_CASE(L)                                                                                                  \
-    case L: mv_rows<FMT, L, 1, ring_depth<FMT, 1>()><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols); break;
+    case L:                                                                                                         \
+        mv_rows<FMT, L, 1, ring_depth<FMT, 1>(), x_first<L>()><<<grid, threads, lds, h->stream>>>(W, stride, x, y,   \
+                                                                                                  rows, cols);      \
+        break;
         switch (LPR) {
             MV_CASE(1) MV_CASE(2) MV_CASE(4) MV_CASE(8) MV_CASE(16) MV_CASE(32) MV_CASE(64)
         }
