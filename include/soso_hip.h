@@ -131,6 +131,25 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
                            const float *wgt, const soso_hip_expert *exps, size_t n_exps, float *sum,
                            uint8_t *done);
 
+/* ---- MoE FFN resident on the device --------------------------------------------
+ * The FFN half of GpuDispatch::moe_capa (gpu.rs; CudaGpu::moe_ejecutar,
+ * crates/soso-llm-api/src/cuda/capa/moe.rs:316): router logits, softmax and
+ * top-k, the chosen experts' gate/up + SwiGLU and down, and the weighted sum
+ * in ranking order, all on the device with no host round trip.
+ * register: router_key names a resident F32 weight [n_exp x hdim];
+ * expert_keys holds 3*n_exp resident keys (gate_e, up_e, down_e for e = 0..):
+ * gate/up [ffn x hdim], down [hdim x ffn], one quantized dtype per role.
+ * Limits: n_exp <= 256, top_k <= 64.  Registering a key again replaces it. */
+int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_len, const char *router_key,
+                          size_t router_key_len, const char *const *expert_keys, const size_t *expert_key_lens,
+                          size_t n_exp, size_t hdim, size_t ffn, size_t top_k);
+/* out_dev[n x hdim] = sum_j wgt[t,j] * down_e(silu(gate_e . x_t) * (up_e . x_t)),
+ * e = idx[t,j], j in ranking order (residual not added, layer.rs:1389 adds it).
+ * idx_dev / wgt_dev (n x top_k) receive the routing when non-null.
+ * Asynchronous on the handle's stream. */
+int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev, size_t n,
+                         float *out_dev, int32_t *idx_dev, float *wgt_dev);
+
 /* ---- device-resident API (no host copies; for the decode step, benchmarks
  * and tests that keep inputs in HBM).  Launches are asynchronous on the
  * handle's stream; soso_hip_sync waits. -------------------------------------- */

@@ -49,6 +49,15 @@ struct Weight {
     bool declined = false;
 };
 
+// A MoE FFN registered for the device-resident path (soso_hip_moe_register).
+struct MoeLayer {
+    const Weight *router = nullptr; // f32 [n_exp x hdim]
+    size_t n_exp = 0, hdim = 0, ffn = 0, top_k = 0;
+    uint8_t dt_gu = 0, dt_down = 0;
+    const uint8_t **tab = nullptr; // device: gate[n_exp], up[n_exp], down[n_exp]
+    std::vector<const void *> host_tab; // the same pointers, for unregistering on weight_drop
+};
+
 struct soso_hip {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -60,9 +69,12 @@ struct soso_hip {
     std::unordered_map<std::string, void *> f32_tensors; // router weights etc.
     soso_hip_stats_t stats{};
     std::string err;
-    // reusable device scratch (grown on demand)
-    void *scratch[8] = {};
-    size_t scratch_cap[8] = {};
+    // reusable device scratch (grown on demand; never inside graph capture)
+    static constexpr int N_SCRATCH = 12;
+    void *scratch[N_SCRATCH] = {};
+    size_t scratch_cap[N_SCRATCH] = {};
+    unsigned *ticket = nullptr; // zero between launches of the "last workgroup" kernels
+    std::unordered_map<std::string, MoeLayer> moe_layers;
     std::vector<hipEvent_t> events; // per-launch timing slots
     std::vector<hipGraphExec_t> graphs;
     bool capturing = false;
@@ -73,6 +85,10 @@ int set_err(soso_hip *h, int code, const std::string &msg);
 int hip_check(soso_hip *h, hipError_t e, const char *what);
 void *scratch_get(soso_hip *h, int slot, size_t bytes);
 
+// packed layouts (k_matvec.hip)
+size_t packed_row_stride(uint8_t dtype, size_t cols);
+bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols);
+
 // launchers (k_matvec.hip)
 int repack_weight(soso_hip *h, uint8_t dtype, const void *raw_dev, void *packed_dev, size_t rows, size_t cols);
 int launch_matvec(soso_hip *h, const Weight &w, const float *x_dev, float *y_dev, size_t n);
@@ -82,9 +98,23 @@ int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
 int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
                      uint64_t stream);
 int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream);
-// (k_moe.hip)
+// (k_moe.hip) -- device scratch of one MoE FFN call
+struct MoeScratch {
+    float *logits = nullptr; // n x n_exp
+    int32_t *idx = nullptr;  // n x top_k
+    float *wgt = nullptr;    // n x top_k
+    int *cnt = nullptr, *offs = nullptr, *list = nullptr; // n_groups, n_groups + 1, n x top_k
+    float *act = nullptr;    // n x top_k x ffn
+    float *ydown = nullptr;  // n x top_k x hdim
+};
+bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s);
 int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim,
                        size_t n_exp, size_t top_k, int32_t *idx_dev, float *wgt_dev, float *logits_dev);
+int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim, size_t n_exp,
+                     size_t top_k, const MoeScratch &s);
+int launch_moe_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
+                       uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab_dev, size_t n_groups,
+                       const float *wgt_dev, const uint8_t *use_dev, const MoeScratch &s, float *out_dev);
 
 // ---------------------------------------------------------------------------
 // Device helpers

@@ -1,0 +1,416 @@
+// mv_core.hpp -- device building blocks of the block-quantized matvecs:
+// x staging into integer digits, per-format lane units (loads and the
+// fused dequant-dot), and the cross-lane row gather.  Shared by the matvec
+// kernels (k_matvec.hip) and the MoE expert kernels (k_moe.hip).
+//
+// Formats and arithmetic follow crates/sosomodel/src/dequant.rs (Q8_0, Q4_K)
+// and crates/gguf2som/src/lib.rs:1639-1661 (Q6_K).
+#pragma once
+
+#include "internal.hpp"
+
+// ---------------------------------------------------------------------------
+// x staging (one barrier)
+// Each thread converts chunks of 8 elements; the 16 chunks of a 128-element
+// block sit in one 16-lane DPP row, which agrees on the block's exponent e
+// (max|x| * 2^e <= 2^22).  Every element becomes the integer X = rint(x*2^e)
+// (|X| <= 2^22, 22 significant bits), written as three balanced signed
+// digits X = d2*2^16 + d1*2^8 + d0 (d0, d1 in [-128, 127], |d2| <= 64).  LDS
+// receives, per 4-element group, one dword of bytes per digit, plus
+//   s16[i] = f32 sum of x[16i .. 16i+16) (unscaled), kx[b] = e of block b.
+// The weights' integer codes then meet x in v_dot4_i32_i8 (exact int32 sums
+// per digit), and only the three digit sums of a sub-block are rounded.
+// ---------------------------------------------------------------------------
+enum { FMT_Q4K = 0, FMT_Q80 = 1, FMT_Q6K = 2 };
+
+constexpr int XDIG = 3;        // digits per element
+constexpr int XD = 16 * XDIG;  // dwords of x per lane unit (16 groups)
+
+// Unit u and register group gi (0..15) of 4-element group g.  Q4_K and Q8_0
+// units are 16 consecutive groups; a Q6_K unit (u = 4 sb + 2 h + kk) takes,
+// for i, t < 4, group sb*64 + h*32 + 8i + 4kk + t as register group 4i + t.
+template <int FMT>
+__device__ __forceinline__ void xunit(int g, int &u, int &gi)
+{
+    if constexpr (FMT == FMT_Q6K) {
+        const int sb = g >> 6, h = (g >> 5) & 1, i = (g >> 3) & 3, kk = (g >> 2) & 1, t = g & 3;
+        u = 4 * sb + 2 * h + kk;
+        gi = 4 * i + t;
+    } else {
+        u = g >> 4;
+        gi = g & 15;
+    }
+}
+
+// LDS dword of register dword w (= 3 gi + digit) of unit u: dwords 4r..4r+3
+// of every unit sit in one 16-byte slot r*U + u, so the 64 lanes of a
+// wavefront read 64 consecutive slots (no bank conflicts).
+__device__ __forceinline__ int xdw(int u, int w, int U) { return ((w >> 2) * U + u) * 4 + (w & 3); }
+
+// Three balanced base-256 digits of the four elements of v (scaled by 2^e),
+// packed one byte per element per digit.
+__device__ __forceinline__ void digits4(float4 v, int e, uint32_t (&d)[XDIG])
+{
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    d[0] = d[1] = d[2] = 0u;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int X = (int)rintf(ldexpf(f[i], e));
+        const int d0 = (int)(int8_t)(X & 0xff);
+        const int X1 = (X - d0) >> 8;
+        const int d1 = (int)(int8_t)(X1 & 0xff);
+        const int d2 = (X1 - d1) >> 8;
+        d[0] |= (uint32_t)(d0 & 0xff) << (8 * i);
+        d[1] |= (uint32_t)(d1 & 0xff) << (8 * i);
+        d[2] |= (uint32_t)(d2 & 0xff) << (8 * i);
+    }
+}
+
+// One 8-element chunk c (thread lane == c % 64).  Every lane of the 16-lane
+// DPP row takes part (invalid chunks carry zeros); only valid ones store.
+template <int FMT>
+__device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool valid, int U, uint32_t *xd, float *s16,
+                                            int *kx)
+{
+    float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                    fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+    m = row16_max(m);
+    const int e = (m > 0.0f && m < INFINITY) ? 22 - __builtin_amdgcn_frexp_expf(m) : 0;
+    float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+    sm += dpp_f<0xB1>(sm);
+    if (valid) {
+        uint32_t d0[XDIG], d1[XDIG];
+        digits4(v0, e, d0);
+        digits4(v1, e, d1);
+        int u, gi;
+        xunit<FMT>(2 * c, u, gi);
+#pragma unroll
+        for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d0[k];
+        xunit<FMT>(2 * c + 1, u, gi);
+#pragma unroll
+        for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d1[k];
+        if ((c & 1) == 0) s16[c >> 1] = sm;
+        if ((c & 15) == 0) kx[c >> 4] = e;
+    }
+}
+
+// x is read in two steps so that its loads can be issued ahead of the weight
+// loads: vector-memory results return in issue order, so x loads issued after
+// a ring of weight loads would wait for all of those weights.
+constexpr int XPRE = 4; // chunks per thread loaded ahead (cols <= 32 * blockDim)
+struct XPre {
+    float4 v[2 * XPRE];
+};
+
+__device__ __forceinline__ void stage_x_issue(const float *__restrict__ x, int cols, XPre &p)
+{
+    const int nch = cols >> 3;
+    const float4 *x4 = (const float4 *)x;
+#pragma unroll
+    for (int j = 0; j < XPRE; j++) {
+        const int c = j * blockDim.x + threadIdx.x;
+        p.v[2 * j] = p.v[2 * j + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < nch) {
+            p.v[2 * j] = x4[2 * c];
+            p.v[2 * j + 1] = x4[2 * c + 1];
+        }
+    }
+}
+
+// blockDim % 64 == 0: chunk c sits in lane c % 64, so the 16 chunks of a
+// block form one DPP row.  Loop bounds are uniform over the workgroup (cols
+// is a multiple of 64, so a trailing block may be half full).
+template <int FMT>
+__device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx)
+{
+    const int nch = cols >> 3, U = cols >> 6;
+#pragma unroll
+    for (int j = 0; j < XPRE; j++) {
+        const int base = j * blockDim.x;
+        if (base < nch) {
+            const int c = base + threadIdx.x;
+            stage_chunk<FMT>(p.v[2 * j], p.v[2 * j + 1], c, c < nch, U, xp, s16, kx);
+        }
+    }
+    const float4 *x4 = (const float4 *)x;
+    for (int base = XPRE * blockDim.x; base < nch; base += blockDim.x) {
+        const int c = base + threadIdx.x;
+        const bool valid = c < nch;
+        float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+        if (valid) {
+            v0 = x4[2 * c];
+            v1 = x4[2 * c + 1];
+        }
+        stage_chunk<FMT>(v0, v1, c, valid, U, xp, s16, kx);
+    }
+    __syncthreads();
+}
+
+template <int FMT>
+__device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx)
+{
+    XPre p;
+    stage_x_issue(x, cols, p);
+    stage_x_finish<FMT>(p, x, cols, xp, s16, kx);
+}
+
+__host__ __device__ inline size_t stage_lds_bytes(size_t cols) { return cols * XDIG + cols / 16 * 4 + (cols + 127) / 128 * 4; }
+
+// ---------------------------------------------------------------------------
+// Per-format unit math
+// ---------------------------------------------------------------------------
+
+template <int FMT> struct WRow;
+template <> struct WRow<FMT_Q4K> {
+    uint4 h, a, b;
+};
+template <> struct WRow<FMT_Q80> {
+    uint2 s;
+    uint4 q[4];
+};
+template <> struct WRow<FMT_Q6K> {
+    uint4 qh, la, lb;
+    uint2 sc;
+    uint32_t d;
+};
+
+// lane constants for one unit
+struct UConst {
+    float c[4];
+    float P;                 // 2^-e of the unit's 128-element block: undoes the x scale
+    uint32_t k1, k2, s, bsh; // Q4_K scale-decode selectors; Q6_K: s = half, bsh = 8*kk
+    int sb;
+};
+
+// weight-side constants (needed before x is staged)
+template <int FMT>
+__device__ __forceinline__ void unit_setup_w(int u, UConst &c)
+{
+    if (FMT == FMT_Q4K) {
+        const int p = u & 3;
+        const bool hi = p >= 2;
+        c.k1 = hi ? 0x0F0F0F0Fu : 0u;
+        c.k2 = hi ? 0x30303030u : 0x3F3F3F3Fu;
+        c.s = hi ? 2u : 0u;
+        c.bsh = (uint32_t)(p & 1) * 16u;
+        c.sb = u >> 2;
+    } else if (FMT == FMT_Q6K) {
+        c.sb = u >> 2;
+        c.s = (uint32_t)((u >> 1) & 1);
+        c.bsh = 8u * (uint32_t)(u & 1);
+    }
+}
+
+// The unit's x digits in registers: XD dwords, dword 3 gi + k = digit k of
+// register group gi.
+struct XReg {
+    uint32_t d[XD];
+};
+
+// x-side constants and the unit's x in registers (after stage_x)
+template <int FMT>
+__device__ __forceinline__ void unit_setup_x(const uint32_t *xd, const float *s16, const int *kx, int u, int U, XReg &xv,
+                                             UConst &c)
+{
+    c.P = ldexpf(1.0f, -kx[u >> 1]);
+    const uint4 *x4 = (const uint4 *)xd;
+#pragma unroll
+    for (int r = 0; r < XD / 4; r++) {
+        const uint4 v = x4[r * U + u];
+        xv.d[4 * r] = v.x;
+        xv.d[4 * r + 1] = v.y;
+        xv.d[4 * r + 2] = v.z;
+        xv.d[4 * r + 3] = v.w;
+    }
+    if (FMT == FMT_Q4K) {
+        c.c[0] = s16[4 * u] + s16[4 * u + 1];
+        c.c[1] = s16[4 * u + 2] + s16[4 * u + 3];
+    } else if (FMT == FMT_Q6K) {
+        const int sb = u >> 2, h = (u >> 1) & 1, kk = u & 1;
+#pragma unroll
+        for (int i = 0; i < 4; i++) c.c[i] = 32.0f * s16[sb * 16 + h * 8 + 2 * i + kk];
+    }
+}
+
+// v_dot4_i32_i8: four signed byte products added to an int32 (exact).
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
+{
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// One code dword (four signed byte codes) against register group gi.
+__device__ __forceinline__ void dot_group(uint32_t q, const XReg &xv, int gi, int (&s)[XDIG])
+{
+#pragma unroll
+    for (int k = 0; k < XDIG; k++) s[k] = sdot4(q, xv.d[XDIG * gi + k], s[k]);
+}
+
+// Sum over the digits: (s2 * 2^16 + s1 * 2^8 + s0), rounded once or twice.
+__device__ __forceinline__ float digits_value(const int (&s)[XDIG])
+{
+    return fmaf((float)s[2], 65536.0f, (float)(s[1] * 256 + s[0]));
+}
+
+// Raw buffer loads over one wavefront's strip of rows.  A pass whose offset
+// lies past the strip's byte count reads zeros without touching memory, so
+// every load of the ring is issued unconditionally and the compiler can wait
+// on exact vmcnt values.  (Raw-buffer range checks use the VGPR offset, so
+// pass offsets are kept there, not in the scalar offset.)
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int RSRC_WORD3 = 0x00020000; // gfx9 raw buffer: 32-bit dwords, no swizzle
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, RSRC_WORD3);
+}
+__device__ __forceinline__ uint4 bld16(rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint2 bld8(rsrc_t r, uint32_t off)
+{
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ uint32_t bld2(rsrc_t r, uint32_t off)
+{
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+}
+
+// Byte offsets, inside one packed row, of what lane unit u loads.
+struct LaneOff {
+    uint32_t o[3];
+};
+
+template <int FMT>
+__device__ __forceinline__ LaneOff lane_offsets(int cols, int u, const UConst &c)
+{
+    LaneOff L;
+    if constexpr (FMT == FMT_Q4K) {
+        const int nb = cols >> 8, U = cols >> 6;
+        L.o[0] = 16 * c.sb;          // H[sb]
+        L.o[1] = 16 * nb + 16 * u;   // QA[u]
+        L.o[2] = L.o[1] + 16 * U;    // QB[u]
+    } else if constexpr (FMT == FMT_Q80) {
+        const int nb = cols >> 5, sreg = (4 * nb + 15) & ~15;
+        L.o[0] = 8 * u;              // S[2u], S[2u+1]
+        L.o[1] = sreg + 16 * u;      // plane 0 (planes i at + 16*U*i)
+        L.o[2] = 0;
+    } else {
+        const int nb = cols >> 8, U = cols >> 6;
+        L.o[0] = 16 * nb + 16 * u;                 // QH[u] (QLa at +16U, QLb at +32U)
+        L.o[1] = 16 * c.sb + 8 * c.s;              // SC[sb] half s
+        L.o[2] = 16 * nb + 48 * U + 2 * c.sb;      // D[sb]
+    }
+    return L;
+}
+
+// Loads unit u of the row at byte offset `base` of the strip.
+template <int FMT>
+__device__ __forceinline__ void load_row(rsrc_t r, uint32_t base, int cols, const LaneOff &L, WRow<FMT> &w)
+{
+    if constexpr (FMT == FMT_Q4K) {
+        w.h = bld16(r, base + L.o[0]);
+        w.a = bld16(r, base + L.o[1]);
+        w.b = bld16(r, base + L.o[2]);
+    } else if constexpr (FMT == FMT_Q80) {
+        const uint32_t U16 = (uint32_t)(cols >> 6) * 16u;
+        w.s = bld8(r, base + L.o[0]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) w.q[i] = bld16(r, base + L.o[1] + U16 * i);
+    } else {
+        const uint32_t U16 = (uint32_t)(cols >> 6) * 16u;
+        w.qh = bld16(r, base + L.o[0]);
+        w.la = bld16(r, base + L.o[0] + U16);
+        w.lb = bld16(r, base + L.o[0] + 2 * U16);
+        w.sc = bld8(r, base + L.o[1]);
+        w.d = bld2(r, base + L.o[2]);
+    }
+}
+
+// Partial dot of one unit of one row (in units of x).
+template <int FMT>
+__device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const XReg &xv, const UConst &c)
+{
+    const float P = c.P;
+    if constexpr (FMT == FMT_Q4K) {
+        // qs byte l of the pair: low nibble = element l of sub-block 2p (unit
+        // elements 0..31, register groups 0..7), high nibble = element l of
+        // sub-block 2p+1 (register groups 8..15).
+        const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
+        int sa[XDIG] = {0, 0, 0}, sb[XDIG] = {0, 0, 0};
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            dot_group(q[t] & 0x0F0F0F0Fu, xv, t, sa);
+            dot_group((q[t] >> 4) & 0x0F0F0F0Fu, xv, 8 + t, sb);
+        }
+        // 6-bit scale/min of sub-blocks 2p, 2p+1 (get_scale_min_k4,
+        // crates/sosomodel/src/dequant.rs:150-159), four at a time per byte lane.
+        const uint32_t SC4 = ((w.h.w & c.k1) | ((w.h.y >> c.s) & c.k2)) >> c.bsh;
+        const uint32_t M4 = (((w.h.w >> 4) & c.k1) | ((w.h.z >> c.s) & c.k2)) >> c.bsh;
+        const float sca = (float)(SC4 & 0xffu), scb = (float)((SC4 >> 8) & 0xffu);
+        const float ma = (float)(M4 & 0xffu), mb = (float)((M4 >> 8) & 0xffu);
+        const float d = half_bits_to_f32(w.h.x & 0xffffu), dmin = half_bits_to_f32(w.h.x >> 16);
+        const float uu = fmaf(sca, digits_value(sa), scb * digits_value(sb));
+        const float vv = fmaf(mb, c.c[1], ma * c.c[0]);
+        return fmaf(d * P, uu, -(dmin * vv));
+    } else if constexpr (FMT == FMT_Q80) {
+        // plane p holds bytes 16(p&1) .. +15 of block p>>1: register groups 4p .. 4p+3
+        int s0[XDIG] = {0, 0, 0}, s1[XDIG] = {0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t q[4] = {w.q[p].x, w.q[p].y, w.q[p].z, w.q[p].w};
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                if (p < 2) dot_group(q[t], xv, 4 * p + t, s0);
+                else dot_group(q[t], xv, 4 * p + t, s1);
+            }
+        }
+        return P * fmaf(__builtin_bit_cast(float, w.s.x), digits_value(s0),
+                        __builtin_bit_cast(float, w.s.y) * digits_value(s1));
+    } else {
+        int s[4][XDIG];
+#pragma unroll
+        for (int i = 0; i < 4; i++) s[i][0] = s[i][1] = s[i][2] = 0;
+        const uint32_t la[4] = {w.la.x, w.la.y, w.la.z, w.la.w}, lb[4] = {w.lb.x, w.lb.y, w.lb.z, w.lb.w};
+        const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            // q = ql nibble | 2 bits of qh << 4 (dequantize_row_q6_K,
+            // crates/gguf2som/src/lib.rs:1650-1658), four codes per dword.
+            uint32_t q[4];
+            q[0] = (la[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x03030303u) << 4);
+            q[1] = (lb[t] & 0x0F0F0F0Fu) | ((qh[t] & 0x0C0C0C0Cu) << 2);
+            q[2] = ((la[t] >> 4) & 0x0F0F0F0Fu) | (qh[t] & 0x30303030u);
+            q[3] = ((lb[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> 2) & 0x30303030u);
+#pragma unroll
+            for (int i = 0; i < 4; i++) dot_group(q[i], xv, 4 * i + t, s[i]);
+        }
+        // sub-scales sc[h*8 + kk + 2i] (int8), the -32 offset through c[i] = 32*sum(x)
+        const float sc0 = (float)(int8_t)(w.sc.x >> c.bsh), sc1 = (float)(int8_t)(w.sc.x >> (c.bsh + 16));
+        const float sc2 = (float)(int8_t)(w.sc.y >> c.bsh), sc3 = (float)(int8_t)(w.sc.y >> (c.bsh + 16));
+        float acc = sc0 * fmaf(digits_value(s[0]), P, -c.c[0]);
+        acc = fmaf(sc1, fmaf(digits_value(s[1]), P, -c.c[1]), acc);
+        acc = fmaf(sc2, fmaf(digits_value(s[2]), P, -c.c[2]), acc);
+        acc = fmaf(sc3, fmaf(digits_value(s[3]), P, -c.c[3]), acc);
+        return half_bits_to_f32(w.d) * acc;
+    }
+}
+
+// Moves the row sums of pass jw (last lane of each LPR-lane segment) into
+// lanes jw*RW .. jw*RW+RW-1 of yacc.
+template <int LPR>
+__device__ __forceinline__ float gather_rows(float part, int jw, float yacc, int lane)
+{
+    constexpr int RW = 64 / LPR;
+    if constexpr (LPR == 64) {
+        const float s = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, part), 63));
+        return lane == jw ? s : yacc;
+    } else {
+        const int d = lane - jw * RW;
+        const bool in = d >= 0 && d < RW;
+        const int src = in ? d * LPR + LPR - 1 : lane;
+        const float v = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src * 4, __builtin_bit_cast(int, part)));
+        return in ? v : yacc;
+    }
+}
+

@@ -11,11 +11,6 @@
 #include <cstring>
 #include <new>
 
-size_t packed_row_stride(uint8_t dtype, size_t cols);
-bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols);
-int launch_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
-                   const float *wgt_dev, const Weight *const *wts, const soso_hip_expert *exps, const uint8_t *ok,
-                   size_t n_exps, float *sum_dev);
 
 int set_err(soso_hip *h, int code, const std::string &msg)
 {
@@ -176,6 +171,11 @@ int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out)
         delete h;
         return SOSO_HIP_ERR_DEVICE;
     }
+    if (hipMalloc((void **)&h->ticket, 256) != hipSuccess || hipMemset(h->ticket, 0, 256) != hipSuccess) {
+        hipStreamDestroy(h->stream);
+        delete h;
+        return SOSO_HIP_ERR_DEVICE;
+    }
     h->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     h->max_lds = prop.sharedMemPerBlock > 0 ? prop.sharedMemPerBlock : 65536;
     size_t free_b = 0, total_b = 0;
@@ -193,8 +193,10 @@ void soso_hip_destroy(soso_hip *h)
     for (auto &kv : h->weights)
         if (kv.second.dev) hipFree(kv.second.dev);
     for (auto &kv : h->f32_tensors) hipFree(kv.second);
-    for (int i = 0; i < 8; i++)
+    for (int i = 0; i < soso_hip::N_SCRATCH; i++)
         if (h->scratch[i]) hipFree(h->scratch[i]);
+    for (auto &kv : h->moe_layers) hipFree(kv.second.tab);
+    if (h->ticket) hipFree(h->ticket);
     for (hipEvent_t e : h->events)
         if (e) hipEventDestroy(e);
     for (hipGraphExec_t g : h->graphs)
@@ -310,7 +312,7 @@ int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const flo
 {
     if (!h) return SOSO_HIP_ERR_ARG;
     // cuda.rs:1668-1670: shapes it cannot do are declined, not errors
-    if (!key || !xs || !idx || !wgt || n == 0 || hdim == 0 || hdim % 4 || n_exp == 0 || n_exp > 1024 || top_k == 0 ||
+    if (!key || !xs || !idx || !wgt || n == 0 || hdim == 0 || hdim % 4 || n_exp == 0 || n_exp > 256 || top_k == 0 ||
         top_k > n_exp || top_k > 64)
         return set_err(h, SOSO_HIP_DECLINED, "router_topk: shape not handled here");
     int rc = make_current(h);
@@ -332,12 +334,12 @@ int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const flo
         h->f32_tensors[k] = wd;
     }
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
-    float *ld = (float *)scratch_get(h, 2, n * n_exp * 4);
-    int32_t *id = (int32_t *)scratch_get(h, 3, n * top_k * 4);
-    float *pd = (float *)scratch_get(h, 4, n * top_k * 4);
-    if (!xd || !ld || !id || !pd) return set_err(h, SOSO_HIP_ERR_NOMEM, "router: scratch");
+    MoeScratch ms;
+    if (!xd || !moe_scratch(h, n, n_exp, top_k, 0, 0, ms)) return set_err(h, SOSO_HIP_ERR_NOMEM, "router: scratch");
+    int32_t *id = ms.idx;
+    float *pd = ms.wgt;
     rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
-    if (rc == SOSO_HIP_OK) rc = launch_router_topk(h, (const float *)wd, xd, n, hdim, n_exp, top_k, id, pd, ld);
+    if (rc == SOSO_HIP_OK) rc = launch_moe_route(h, (const float *)wd, xd, n, hdim, n_exp, top_k, ms);
     if (rc == SOSO_HIP_OK)
         rc = hip_check(h, hipMemcpyAsync(idx, id, n * top_k * 4, hipMemcpyDeviceToHost, h->stream), "idx");
     if (rc == SOSO_HIP_OK)
@@ -360,46 +362,171 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
     if (rc != SOSO_HIP_OK) return rc;
     CallClock clk(h);
     const size_t dims[3][2] = {{ffn, hdim}, {ffn, hdim}, {hdim, ffn}};
+    const size_t slots = n * top_k;
+    // Resolvable experts: the three matrices resident (or uploadable), one
+    // dtype for all gate/up and one for all down (the first resolvable expert
+    // fixes them), valid token/slot indices.  Shared experts are left to the
+    // caller (they are summed through moe_compartido in the reference).
     std::vector<const Weight *> wts(n_exps * 3, nullptr);
-    std::vector<uint8_t> ok(n_exps, 0);
+    std::vector<uint8_t> ok(n_exps, 0), use(slots, 0);
+    uint8_t dt_gu = 0, dt_dn = 0;
     bool all = true;
     for (size_t e = 0; e < n_exps; e++) {
         done[e] = 0;
-        bool good = exps[e].n_tokens > 0;
+        const soso_hip_expert &x = exps[e];
+        bool good = x.n_tokens > 0 && !x.shared && x.tokens && x.targets;
         for (int k = 0; k < 3 && good; k++) {
             Weight *wt = nullptr;
-            if (!exps[e].keys[k]) {
+            if (!x.keys[k]) {
                 good = false;
                 break;
             }
-            int r = get_weight(h, exps[e].keys[k], exps[e].key_lens[k], exps[e].w[k], exps[e].w_len[k],
-                               exps[e].dtype[k], dims[k][0], dims[k][1], &wt);
+            int r = get_weight(h, x.keys[k], x.key_lens[k], x.w[k], x.w_len[k], x.dtype[k], dims[k][0], dims[k][1], &wt);
             if (r < 0) return r;
             if (r != SOSO_HIP_OK || wt->dtype == SOSO_HIP_DTYPE_F32) good = false;
             else wts[3 * e + k] = wt;
         }
-        for (size_t t = 0; good && t < exps[e].n_tokens; t++)
-            if (exps[e].tokens[t] >= n || exps[e].targets[t] >= n * top_k) good = false;
+        if (good) {
+            if (!dt_gu) {
+                dt_gu = wts[3 * e]->dtype;
+                dt_dn = wts[3 * e + 2]->dtype;
+            }
+            good = wts[3 * e]->dtype == dt_gu && wts[3 * e + 1]->dtype == dt_gu && wts[3 * e + 2]->dtype == dt_dn;
+        }
+        for (size_t t = 0; good && t < x.n_tokens; t++)
+            if (x.tokens[t] >= n || x.targets[t] >= slots || x.targets[t] / top_k != x.tokens[t]) good = false;
         ok[e] = good ? 1 : 0;
-        if (!good && exps[e].n_tokens > 0) all = false;
+        if (!good && x.n_tokens > 0) all = false;
     }
+    // groups = resolvable experts; their slots sorted by group
+    std::vector<size_t> gid;
+    for (size_t e = 0; e < n_exps; e++)
+        if (ok[e]) gid.push_back(e);
+    const size_t G = gid.size();
+    std::vector<int> ints(2 * G + 1 + slots, 0);
+    std::vector<const uint8_t *> tab(3 * G);
+    int o = 0;
+    for (size_t g = 0; g < G; g++) {
+        const soso_hip_expert &x = exps[gid[g]];
+        ints[g] = (int)x.n_tokens;
+        ints[G + g] = o;
+        for (size_t t = 0; t < x.n_tokens; t++) {
+            ints[2 * G + 1 + o++] = (int)x.targets[t];
+            use[x.targets[t]] = 1;
+        }
+        for (int k = 0; k < 3; k++) tab[k * G + g] = (const uint8_t *)wts[3 * gid[g] + k]->dev;
+    }
+    ints[2 * G] = o;
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
-    float *wd = (float *)scratch_get(h, 4, n * top_k * 4);
     float *sd = (float *)scratch_get(h, 5, n * hdim * 4);
-    if (!xd || !wd || !sd) return set_err(h, SOSO_HIP_ERR_NOMEM, "experts_block: scratch");
+    char *aux = (char *)scratch_get(h, 11, slots * 4 + slots + 3 * G * sizeof(void *) + 64);
+    MoeScratch ms;
+    if (!xd || !sd || !aux || !moe_scratch(h, n, G, top_k, hdim, ffn, ms))
+        return set_err(h, SOSO_HIP_ERR_NOMEM, "experts_block: scratch");
+    float *wd = (float *)aux;
+    const uint8_t **tabd = (const uint8_t **)(aux + ((slots * 4 + 15) & ~(size_t)15));
+    uint8_t *used = (uint8_t *)(tabd + 3 * G);
     rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
     if (rc == SOSO_HIP_OK)
-        rc = hip_check(h, hipMemcpyAsync(wd, wgt, n * top_k * 4, hipMemcpyHostToDevice, h->stream), "wgt upload");
+        rc = hip_check(h, hipMemcpyAsync(wd, wgt, slots * 4, hipMemcpyHostToDevice, h->stream), "wgt upload");
+    if (rc == SOSO_HIP_OK && G)
+        rc = hip_check(h, hipMemcpyAsync(ms.cnt, ints.data(), ints.size() * 4, hipMemcpyHostToDevice, h->stream),
+                       "groups upload");
+    if (rc == SOSO_HIP_OK && G)
+        rc = hip_check(h, hipMemcpyAsync(tabd, tab.data(), tab.size() * sizeof(void *), hipMemcpyHostToDevice, h->stream),
+                       "tables upload");
     if (rc == SOSO_HIP_OK)
-        rc = launch_experts(h, xd, n, hdim, ffn, top_k, wd, wts.data(), exps, ok.data(), n_exps, sd);
+        rc = hip_check(h, hipMemcpyAsync(used, use.data(), slots, hipMemcpyHostToDevice, h->stream), "slots upload");
+    if (rc == SOSO_HIP_OK) {
+        if (G)
+            rc = launch_moe_experts(h, xd, n, hdim, ffn, top_k, dt_gu, dt_dn, tabd, G, wd, used, ms, sd);
+        else
+            rc = hip_check(h, hipMemsetAsync(sd, 0, n * hdim * 4, h->stream), "zero sum");
+    }
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(sum, sd, n * hdim * 4, hipMemcpyDeviceToHost, h->stream), "sum");
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "experts sync");
-    if (rc != SOSO_HIP_OK) return rc;
+    if (rc != SOSO_HIP_OK) {
+        hipStreamSynchronize(h->stream);
+        return rc;
+    }
     for (size_t e = 0; e < n_exps; e++) done[e] = ok[e];
-    h->stats.bytes_up += n * hdim * 4;
+    h->stats.bytes_up += n * hdim * 4 + slots * 4;
     h->stats.bytes_down += n * hdim * 4;
     clk.done();
     return all ? SOSO_HIP_OK : SOSO_HIP_DECLINED;
+}
+
+// ---- MoE FFN resident on the device ----------------------------------------
+int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_len, const char *router_key,
+                          size_t router_key_len, const char *const *expert_keys, const size_t *expert_key_lens,
+                          size_t n_exp, size_t hdim, size_t ffn, size_t top_k)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!layer_key || !router_key || !expert_keys || !expert_key_lens || n_exp == 0 || n_exp > 256 || top_k == 0 ||
+        top_k > n_exp || top_k > 64 || hdim == 0 || hdim % 4 || ffn == 0)
+        return set_err(h, SOSO_HIP_ERR_ARG, "moe_register: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    MoeLayer m;
+    m.router = find_weight(h, router_key, router_key_len);
+    if (!m.router || m.router->dtype != SOSO_HIP_DTYPE_F32 || m.router->rows != n_exp || m.router->cols != hdim)
+        return set_err(h, SOSO_HIP_DECLINED, "moe_register: router not resident as f32 [n_exp x hdim]");
+    m.n_exp = n_exp;
+    m.hdim = hdim;
+    m.ffn = ffn;
+    m.top_k = top_k;
+    std::vector<const uint8_t *> tab(3 * n_exp);
+    const size_t dims[3][2] = {{ffn, hdim}, {ffn, hdim}, {hdim, ffn}};
+    for (size_t e = 0; e < n_exp; e++)
+        for (int k = 0; k < 3; k++) {
+            const Weight *w = find_weight(h, expert_keys[3 * e + k], expert_key_lens[3 * e + k]);
+            if (!w || w->rows != dims[k][0] || w->cols != dims[k][1] || w->dtype == SOSO_HIP_DTYPE_F32)
+                return set_err(h, SOSO_HIP_DECLINED, "moe_register: expert matrix missing or of the wrong shape");
+            const uint8_t want = k < 2 ? m.dt_gu : m.dt_down;
+            if (want && w->dtype != want) return set_err(h, SOSO_HIP_DECLINED, "moe_register: mixed expert dtypes");
+            if (k < 2) m.dt_gu = w->dtype;
+            else m.dt_down = w->dtype;
+            tab[k * n_exp + e] = (const uint8_t *)w->dev;
+        }
+    m.host_tab.assign(tab.begin(), tab.end());
+    if (hipMalloc((void **)&m.tab, tab.size() * sizeof(void *)) != hipSuccess)
+        return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_register: table");
+    rc = hip_check(h, hipMemcpy(m.tab, tab.data(), tab.size() * sizeof(void *), hipMemcpyHostToDevice), "table upload");
+    if (rc != SOSO_HIP_OK) {
+        hipFree(m.tab);
+        return rc;
+    }
+    std::string k(layer_key, layer_key_len);
+    auto it = h->moe_layers.find(k);
+    if (it != h->moe_layers.end()) {
+        hipDeviceSynchronize();
+        hipFree(it->second.tab);
+        h->moe_layers.erase(it);
+    }
+    h->moe_layers.emplace(k, m);
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev, size_t n,
+                         float *out_dev, int32_t *idx_dev, float *wgt_dev)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!layer_key || !x_dev || !out_dev || n == 0) return set_err(h, SOSO_HIP_ERR_ARG, "moe_ffn_dev: args");
+    auto it = h->moe_layers.find(std::string(layer_key, layer_key_len));
+    if (it == h->moe_layers.end()) return set_err(h, SOSO_HIP_DECLINED, "moe_ffn_dev: layer not registered");
+    const MoeLayer &m = it->second;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    MoeScratch ms;
+    if (!moe_scratch(h, n, m.n_exp, m.top_k, m.hdim, m.ffn, ms))
+        return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_ffn_dev: scratch");
+    if (idx_dev) ms.idx = idx_dev;
+    if (wgt_dev) ms.wgt = wgt_dev;
+    rc = launch_moe_route(h, (const float *)m.router->dev, x_dev, n, m.hdim, m.n_exp, m.top_k, ms);
+    if (rc == SOSO_HIP_OK)
+        rc = launch_moe_experts(h, x_dev, n, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, ms.wgt,
+                                nullptr, ms, out_dev);
+    return rc;
 }
 
 // ---- device-resident API ----------------------------------------------------
@@ -508,6 +635,17 @@ int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
     auto it = h->weights.find(std::string(key, key_len));
     if (it == h->weights.end()) return SOSO_HIP_DECLINED;
     hipStreamSynchronize(h->stream);
+    // a registered MoE layer that reads this weight is unregistered with it
+    for (auto m = h->moe_layers.begin(); m != h->moe_layers.end();) {
+        bool uses = m->second.router == &it->second;
+        for (const void *p : m->second.host_tab) uses = uses || (p && p == it->second.dev);
+        if (uses) {
+            hipFree(m->second.tab);
+            m = h->moe_layers.erase(m);
+        } else {
+            ++m;
+        }
+    }
     if (it->second.dev) {
         hipFree(it->second.dev);
         h->used -= it->second.bytes;

@@ -251,3 +251,20 @@ class HipGpu:
 
     def d2d(self, dst, src, nbytes):
         self._rc(self.lib.soso_hip_d2d(self.h, dst, src, nbytes), "d2d")
+
+    # -- MoE FFN resident on the device (the FFN half of GpuDispatch::moe_capa) --
+    def moe_register(self, layer_key, router_key, expert_keys, n_exp, hdim, ffn, top_k):
+        """expert_keys: 3*n_exp names (gate_e, up_e, down_e for e = 0..n_exp-1)."""
+        lk, ll = _key(layer_key)
+        rk, rl = _key(router_key)
+        enc = [k.encode() for k in expert_keys]
+        arr = (C.c_char_p * len(enc))(*enc)
+        lens = (C.c_size_t * len(enc))(*[len(k) for k in enc])
+        return self._rc(self.lib.soso_hip_moe_register(self.h, lk, ll, rk, rl, C.cast(arr, C.c_void_p),
+                                                       C.cast(lens, C.c_void_p), n_exp, hdim, ffn, top_k),
+                        f"moe_register {layer_key}")
+
+    def moe_ffn_dev(self, layer_key, x_dev, n, out_dev, idx_dev=None, wgt_dev=None):
+        k, kl = _key(layer_key)
+        return self._rc(self.lib.soso_hip_moe_ffn_dev(self.h, k, kl, x_dev, n, out_dev, idx_dev, wgt_dev),
+                        f"moe_ffn_dev {layer_key}")

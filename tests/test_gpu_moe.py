@@ -1,0 +1,196 @@
+"""GPU parity of the MoE decode path through the C ABI.
+
+Reference behaviour: topk_softmax (crates/soso-llm-core/src/gemm.rs:62-91)
+with ties to the lowest index, experts combined in ranking order
+(crates/soso-llm-core/src/layer.rs:1869-1934), GpuDispatch::router_topk and
+expertos_bloque (crates/soso-llm-core/src/gpu.rs:461-494).  The oracle's
+or_moe_ffn composes the same steps on the CPU.
+
+Bar: the chosen expert indices identical, in the same ranking order; routing
+weights and FFN outputs within relative L2 1e-5 (f32 accumulate).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-5
+Q4K, Q8, F32 = 3, 2, 1
+
+
+class Layer:
+    """A seeded MoE FFN (router f32 ~ N(0, 0.02), experts Q4_K like configs[3])."""
+
+    def __init__(self, orc, n_exp, h, ffn, top_k, seed, dt_down=Q4K):
+        self.n_exp, self.h, self.ffn, self.top_k, self.dt_down = n_exp, h, ffn, top_k, dt_down
+        self.router = orc.normal(n_exp * h, 0.02, seed, 1)
+        self.gate = [orc.synth(Q4K, ffn, h, seed, 100 + e) for e in range(n_exp)]
+        self.up = [orc.synth(Q4K, ffn, h, seed, 1000 + e) for e in range(n_exp)]
+        self.down = [orc.synth(dt_down, h, ffn, seed, 2000 + e) for e in range(n_exp)]
+        self.name = f"moe{seed}.{n_exp}.{h}.{ffn}.{top_k}.{dt_down}"
+
+    def keys(self, e):
+        return [f"{self.name}.E{e}.gate", f"{self.name}.E{e}.up", f"{self.name}.E{e}.down"]
+
+    def cpu(self, orc, x):
+        return orc.moe_ffn(self.router, self.n_exp, self.h, self.ffn, self.top_k, self.gate, self.up, self.down,
+                           Q4K, self.dt_down, x)
+
+    def upload(self, gpu):
+        """Every matrix resident under its key, the router as an F32 weight."""
+        for e in range(self.n_exp):
+            for k, (w, dt, r, c) in zip(self.keys(e), ((self.gate[e], Q4K, self.ffn, self.h),
+                                                       (self.up[e], Q4K, self.ffn, self.h),
+                                                       (self.down[e], self.dt_down, self.h, self.ffn))):
+                d = gpu.dev_alloc(w.size)
+                try:
+                    gpu.h2d(d, w)
+                    gpu.weight_from_dev(k, d, w.size, dt, r, c)
+                finally:
+                    gpu.dev_free(d)
+        d = gpu.dev_alloc(self.router.nbytes)
+        try:
+            gpu.h2d(d, self.router)
+            gpu.weight_from_dev(self.name + ".router", d, self.router.nbytes, F32, self.n_exp, self.h)
+        finally:
+            gpu.dev_free(d)
+        keys = [k for e in range(self.n_exp) for k in self.keys(e)]
+        gpu.moe_register(self.name, self.name + ".router", keys, self.n_exp, self.h, self.ffn, self.top_k)
+
+    def drop(self, gpu):
+        for e in range(self.n_exp):
+            for k in self.keys(e):
+                gpu.weight_drop(k)
+        gpu.weight_drop(self.name + ".router")
+
+
+def moe_dev(gpu, layer, xs):
+    n = xs.size // layer.h
+    xd = gpu.dev_alloc(xs.nbytes)
+    od = gpu.dev_alloc(n * layer.h * 4)
+    idd = gpu.dev_alloc(n * layer.top_k * 4)
+    wd = gpu.dev_alloc(n * layer.top_k * 4)
+    try:
+        gpu.h2d(xd, xs)
+        gpu.moe_ffn_dev(layer.name, xd, n, od, idd, wd)
+        gpu.sync()
+        return (gpu.d2h(od, (n, layer.h), np.float32), gpu.d2h(idd, (n, layer.top_k), np.int32),
+                gpu.d2h(wd, (n, layer.top_k), np.float32))
+    finally:
+        for p in (xd, od, idd, wd):
+            gpu.dev_free(p)
+
+
+@pytest.mark.parametrize("n_exp,h,top_k,n", [(128, 2048, 8, 1), (128, 2048, 8, 32), (16, 512, 4, 5), (40, 256, 1, 3)])
+def test_router_topk_matches_cpu(gpu, orc, n_exp, h, top_k, n):
+    w = orc.normal(n_exp * h, 0.02, 71, n_exp)
+    xs = orc.normal(n * h, 1.0, 72, n)
+    idx = np.full(n * top_k, -1, np.int32)
+    wgt = np.zeros(n * top_k, np.float32)
+    assert gpu.router_topk(f"router.{n_exp}.{h}", w, xs, n, h, n_exp, top_k, idx, wgt), gpu.last_error()
+    for t in range(n):
+        logits = orc.matvec(F32, w, n_exp, h, xs[t * h:(t + 1) * h])
+        ci, cw = orc.topk_softmax(logits, top_k)
+        assert np.array_equal(idx[t * top_k:(t + 1) * top_k], ci), (t, idx[t * top_k:(t + 1) * top_k], ci)
+        assert orc.rel_l2(wgt[t * top_k:(t + 1) * top_k], cw) < TOL
+        assert abs(float(np.sum(wgt[t * top_k:(t + 1) * top_k], dtype=np.float64)) - 1.0) < 1e-5
+
+
+def test_router_ties_lowest_index_first(gpu, orc):
+    """Equal logits: the stable descending sort keeps the lower index first."""
+    n_exp, h, top_k = 64, 64, 6
+    w = np.zeros((n_exp, h), np.float32)
+    for e in (3, 10, 17, 40, 41, 63):  # six experts with the same (largest) logit
+        w[e, 0] = 1.0
+    w[20, 0] = 0.5
+    xs = np.zeros(h, np.float32)
+    xs[0] = 2.0
+    idx = np.zeros(top_k, np.int32)
+    wgt = np.zeros(top_k, np.float32)
+    assert gpu.router_topk("router.ties", w.ravel(), xs, 1, h, n_exp, top_k, idx, wgt)
+    assert list(idx) == [3, 10, 17, 40, 41, 63]
+    assert np.allclose(wgt, 1.0 / 6.0, rtol=1e-6)
+
+
+@pytest.mark.parametrize("n_exp,h,ffn,top_k,n,dt_down", [
+    (16, 2048, 768, 8, 1, Q4K),    # configs[3] expert shapes, fewer experts
+    (16, 2048, 768, 8, 32, Q4K),   # batch 32: several tokens per expert
+    (12, 512, 256, 3, 7, Q8),      # Q8_0 down projections (soso's converted Q6_K experts)
+])
+def test_moe_ffn_dev_matches_cpu(gpu, orc, n_exp, h, ffn, top_k, n, dt_down):
+    layer = Layer(orc, n_exp, h, ffn, top_k, 40 + n, dt_down)
+    layer.upload(gpu)
+    try:
+        xs = orc.normal(n * h, 1.0, 73, n)
+        out, idx, wgt = moe_dev(gpu, layer, xs)
+        for t in range(n):
+            ref, ri, rw = layer.cpu(orc, xs[t * h:(t + 1) * h])
+            assert np.array_equal(idx[t], ri), (t, idx[t], ri)
+            assert orc.rel_l2(wgt[t], rw) < TOL
+            assert orc.rel_l2(out[t], ref) < TOL, (t, orc.rel_l2(out[t], ref))
+        # a second call with the same inputs gives the same bits (no state left behind)
+        out2, idx2, _ = moe_dev(gpu, layer, xs)
+        assert np.array_equal(out2.view(np.uint32), out.view(np.uint32)) and np.array_equal(idx2, idx)
+    finally:
+        layer.drop(gpu)
+
+
+def test_experts_block_host_path(gpu, orc):
+    """expertos_bloque: the caller groups tokens by expert (here from the CPU
+    routing); suma = weighted sum over the resolved experts in ranking order."""
+    n_exp, h, ffn, top_k, n = 10, 512, 256, 3, 6
+    layer = Layer(orc, n_exp, h, ffn, top_k, 91)
+    xs = orc.normal(n * h, 1.0, 92, n)
+    refs, idxs, ws = zip(*[layer.cpu(orc, xs[t * h:(t + 1) * h]) for t in range(n)])
+    pesos = np.concatenate(ws).astype(np.float32)
+    exps = []
+    for e in range(n_exp):
+        tok = [t for t in range(n) for j in range(top_k) if idxs[t][j] == e]
+        dst = [t * top_k + j for t in range(n) for j in range(top_k) if idxs[t][j] == e]
+        if tok:
+            exps.append({"claves": layer.keys(e), "w": [layer.gate[e], layer.up[e], layer.down[e]],
+                         "dtype": [Q4K, Q4K, Q4K], "tokens": tok, "destinos": dst})
+    suma = np.zeros(n * h, np.float32)
+    hecho = [False] * len(exps)
+    try:
+        assert gpu.expertos_bloque(xs, n, h, ffn, top_k, pesos, exps, suma, hecho) == 1, gpu.last_error()
+        assert all(hecho)
+        for t in range(n):
+            assert orc.rel_l2(suma[t * h:(t + 1) * h], refs[t]) < TOL
+    finally:
+        layer.drop(gpu)
+
+
+def test_experts_block_declines_shared_and_sums_the_rest(gpu, orc):
+    """A shared expert is left to the caller (hecho false); the sum holds the
+    other experts only."""
+    n_exp, h, ffn, top_k, n = 4, 256, 256, 2, 2
+    layer = Layer(orc, n_exp, h, ffn, top_k, 93)
+    xs = orc.normal(n * h, 1.0, 94, n)
+    refs, idxs, ws = zip(*[layer.cpu(orc, xs[t * h:(t + 1) * h]) for t in range(n)])
+    pesos = np.concatenate(ws).astype(np.float32)
+    exps = []
+    for e in range(n_exp):
+        tok = [t for t in range(n) for j in range(top_k) if idxs[t][j] == e]
+        dst = [t * top_k + j for t in range(n) for j in range(top_k) if idxs[t][j] == e]
+        if tok:
+            exps.append({"claves": layer.keys(e), "w": [layer.gate[e], layer.up[e], layer.down[e]],
+                         "dtype": [Q4K, Q4K, Q4K], "tokens": tok, "destinos": dst, "compartido": False})
+    exps[0]["compartido"] = True
+    suma = np.zeros(n * h, np.float32)
+    hecho = [False] * len(exps)
+    try:
+        assert gpu.expertos_bloque(xs, n, h, ffn, top_k, pesos, exps, suma, hecho) == 0
+        assert hecho[0] is False and all(hecho[1:])
+        # add the shared-flagged expert's part on the CPU and compare with the full sum
+        e0 = [e for e in range(n_exp) if layer.keys(e) == exps[0]["claves"]][0]
+        full = suma.copy()
+        for t, s in zip(exps[0]["tokens"], exps[0]["destinos"]):
+            g = orc.matvec(Q4K, layer.gate[e0], ffn, h, xs[t * h:(t + 1) * h])
+            u = orc.matvec(Q4K, layer.up[e0], ffn, h, xs[t * h:(t + 1) * h])
+            act = (g / (1.0 + np.exp(-g.astype(np.float64))) * u).astype(np.float32)
+            full[t * h:(t + 1) * h] += pesos[s] * orc.matvec(Q4K, layer.down[e0], h, ffn, act)
+        for t in range(n):
+            assert orc.rel_l2(full[t * h:(t + 1) * h], refs[t]) < 1e-5
+    finally:
+        layer.drop(gpu)
