@@ -21,6 +21,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -87,6 +89,75 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
         g.dev_free(y)
         for k in keys:
             g.weight_drop(k)
+
+
+def time_moe(g, n, steps, layers=4, n_x=8, seed=11):
+    """Qwen3-30B-A3B-like MoE FFN (hidden 2048, 128 experts of
+    intermediate 768, top-8, Q4_K experts, f32 router ~ N(0, 0.02)), `n`
+    tokens ~ N(0, 1) per call, routing from the seeded inputs.  `layers`
+    independent layers and `n_x` input batches are rotated so that successive
+    calls touch different experts (HBM, not the MALL).  Returns (ms per call,
+    algorithmic bytes per call averaged over the rotation, distinct experts
+    per call)."""
+    E, H, F, K = 128, 2048, 768, 8
+    names = []
+    try:
+        for L in range(layers):
+            name = f"bm{n}.{L}"
+            keys = []
+            for e in range(E):
+                for j, (r, c) in enumerate(((F, H), (F, H), (H, F))):
+                    k = f"{name}.E{e}.{('gate', 'up', 'down')[j]}"
+                    g.weight_synth(k, Q4K, r, c, seed, L * 1000 + 3 * e + j)
+                    keys.append(k)
+            d = g.dev_alloc(E * H * 4)
+            try:
+                g.synth_normal(d, E * H, 0.02, seed + 1, L)
+                g.weight_from_dev(name + ".router", d, E * H * 4, F32, E, H)
+            finally:
+                g.dev_free(d)
+            g.moe_register(name, name + ".router", keys, E, H, F, K)
+            names.append((name, keys))
+        xs = g.dev_alloc(n_x * n * H * 4)
+        out = g.dev_alloc(n * H * 4)
+        idx = g.dev_alloc(n * K * 4)
+        try:
+            g.synth_normal(xs, n_x * n * H, 1.0, seed + 2, n)
+            per_expert = 3 * F * (H // 256) * 144
+            nbytes = []
+            for L in range(layers):
+                for i in range(n_x):
+                    g.moe_ffn_dev(names[L][0], xs + i * n * H * 4, n, out, idx, None)
+                    ids = g.d2h(idx, (n * K,), np.int32)
+                    u = len(set(ids.tolist()))
+                    nbytes.append((E * H * 4 + u * per_expert + 2 * n * H * 4, u))
+            g.sync()
+            combos = layers * n_x
+            gid = _capture(g, lambda: [g.moe_ffn_dev(names[i % layers][0], xs + ((i // layers) % n_x) * n * H * 4,
+                                                     n, out, None, None) for i in range(steps)])
+            try:
+                g.graph_launch(gid)
+                g.sync()
+                g.event_record(0)
+                g.graph_launch(gid)
+                g.event_record(1)
+                g.sync()
+            finally:
+                g.graph_destroy(gid)
+            ms = g.event_elapsed(0, 1) / steps
+            order = [(i % layers) * n_x + (i // layers) % n_x for i in range(steps)]
+            b = sum(nbytes[o][0] for o in order) / steps
+            u = sum(nbytes[o][1] for o in order) / steps
+            return ms, b, u, combos
+        finally:
+            g.dev_free(xs)
+            g.dev_free(out)
+            g.dev_free(idx)
+    finally:
+        for name, keys in names:
+            for k in keys:
+                g.weight_drop(k)
+            g.weight_drop(name + ".router")
 
 
 def copy_calibration(g, nbytes=512 << 20, reps=20):
@@ -184,6 +255,12 @@ def main():
             b = algo_bytes(dt, r, c)
             extra[name] = {"us_kernel": round(k_ * 1e3, 3), "GB_s": round(b / (k_ * 1e-3) / 1e9, 1),
                            "frac_hbm": round(b / (k_ * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b}
+        for n in (1, 32):
+            ms_m, b_m, u_m, _ = time_moe(g, n, max(40, args.steps // 10))
+            extra[f"moe_qwen3_30b_a3b_batch{n}"] = {
+                "us_per_layer": round(ms_m * 1e3, 3), "tokens_per_s_layer": round(n / (ms_m * 1e-3), 1),
+                "GB_s": round(b_m / (ms_m * 1e-3) / 1e9, 1), "frac_hbm": round(b_m / (ms_m * 1e-3) / 1e9 / PEAK_GBS, 4),
+                "bytes": int(b_m), "distinct_experts": round(u_m, 2)}
         line["configs"] = extra
     if not args.no_cpu:
         gbs, n, ms = cpu_baseline(Q4K, rows, cols, args.cpu_seconds, args.cpu_threads)

@@ -104,6 +104,7 @@ struct MoeScratch {
     int32_t *idx = nullptr;  // n x top_k
     float *wgt = nullptr;    // n x top_k
     int *cnt = nullptr, *offs = nullptr, *list = nullptr; // n_groups, n_groups + 1, n x top_k
+    int *act_list = nullptr, *act_n = nullptr;              // active groups (ascending), their count
     float *act = nullptr;    // n x top_k x ffn
     float *ydown = nullptr;  // n x top_k x hdim
 };

@@ -10,11 +10,11 @@
 //   k_moe_route   logits = W_router . x (f32) for every (token, expert); the
 //                 last workgroup to finish runs softmax + top-k per token and
 //                 counting-sorts the n*top_k slots by expert (cnt, offs, list).
-//   k_moe_mv      grid (expert, row chunk): every weight row of an expert is
-//                 read once from HBM and applied to all the tokens routed to
-//                 it (their x staged in LDS).  Gate and up rows are read side
-//                 by side and leave as silu(gate.x) * up.x; down rows leave as
-//                 y[slot].  Experts nobody chose exit at once.
+//   k_moe_mv      a persistent grid over (active expert, row chunk) items:
+//                 every weight row of an expert is read once from HBM and
+//                 applied to all the tokens routed to it (their x staged in
+//                 LDS).  Gate and up rows are read side by side and leave as
+//                 silu(gate.x) * up.x; down rows leave as y[slot].
 //   k_moe_combine out[t] = sum_j wgt[t,j] * y[t*top_k + j], j in ranking order.
 // Slot s = t * top_k + j is token t's j-th ranked expert ("destinos" in
 // ExpertoBloque, gpu.rs:176-186).
@@ -88,31 +88,48 @@ __device__ void topk_wave(const float *__restrict__ lg, int n_exp, int top_k, in
 }
 
 // grid: ceil(n_exp / waves) workgroups; wave w of workgroup b owns expert
-// b*waves + w.  `ticket` is zero between launches (the last workgroup resets it).
+// b*waves + w.  `ticket` is zero between launches (the last workgroup resets
+// it).  The last workgroup also writes the active-expert list act[0..*act_n)
+// (experts chosen by at least one slot, ascending) for the grouped kernels.
+constexpr int ROUTE_MAX_SLOTS = 4096; // n * top_k handled by the LDS sort
+
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
                                                     int32_t *__restrict__ idx, float *__restrict__ wgt,
                                                     int *__restrict__ cnt, int *__restrict__ offs,
-                                                    int *__restrict__ list, unsigned *__restrict__ ticket)
+                                                    int *__restrict__ list, int *__restrict__ act,
+                                                    int *__restrict__ act_n, unsigned *__restrict__ ticket)
 {
     __shared__ int last;
-    __shared__ float sel[16][64];
+    __shared__ float sel[8][64];
+    __shared__ int c_s[256], o_s[257], f_s[256];
+    __shared__ int16_t e_s[ROUTE_MAX_SLOTS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int e = blockIdx.x * nw + wave;
     if (e < n_exp) {
         const float4 *w4 = (const float4 *)(W + (size_t)e * hdim);
+        const int nv = hdim >> 2;
         for (int t = 0; t < n; t++) {
             const float4 *x4 = (const float4 *)(xs + (size_t)t * hdim);
             float a0 = 0.f, a1 = 0.f;
-            for (int i = lane; i < (hdim >> 2); i += 64) {
-                const float4 w = w4[i], v = x4[i];
-                a0 = fmaf(w.x, v.x, a0);
-                a1 = fmaf(w.y, v.y, a1);
-                a0 = fmaf(w.z, v.z, a0);
-                a1 = fmaf(w.w, v.w, a1);
+            for (int i0 = 0; i0 < nv; i0 += 64 * 4) {
+                float4 w[4], v[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int i = i0 + 64 * q + lane;
+                    w[q] = i < nv ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    v[q] = i < nv ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    a0 = fmaf(w[q].x, v[q].x, a0);
+                    a1 = fmaf(w[q].y, v[q].y, a1);
+                    a0 = fmaf(w[q].z, v[q].z, a0);
+                    a1 = fmaf(w[q].w, v[q].w, a1);
+                }
             }
-            const float s = seg_sum<64>(a0 + a1);
-            if (lane == 0) logits[(size_t)t * n_exp + e] = s;
+            const float sum = seg_sum<64>(a0 + a1);
+            if (lane == 0) logits[(size_t)t * n_exp + e] = sum;
         }
     }
     // the last workgroup to finish ranks the experts of every token
@@ -126,55 +143,95 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
         topk_wave(logits + (size_t)t * n_exp, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k,
                   sel[wave]);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        // counting sort of the slots by expert, slot order kept inside an expert
-        for (int x = 0; x < n_exp; x++) cnt[x] = 0;
-        for (int s = 0; s < n * top_k; s++) cnt[min(max(idx[s], 0), n_exp - 1)]++;
-        int o = 0;
-        for (int x = 0; x < n_exp; x++) {
-            offs[x] = o;
-            o += cnt[x];
+    // counting sort of the slots by expert in LDS (a slot's position inside
+    // its expert's list does not change any result)
+    const int slots = n * top_k;
+    for (int x = threadIdx.x; x < n_exp; x += blockDim.x) c_s[x] = f_s[x] = 0;
+    __syncthreads();
+    for (int sl = threadIdx.x; sl < slots; sl += blockDim.x) {
+        const int x = min(max((int)idx[sl], 0), n_exp - 1);
+        e_s[sl] = (int16_t)x;
+        atomicAdd(&c_s[x], 1);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        // exclusive scan over n_exp <= 256 counts, 4 per lane
+        int v[4], tot = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int x = 4 * lane + q;
+            v[q] = x < n_exp ? c_s[x] : 0;
+            tot += v[q];
         }
-        offs[n_exp] = o;
-        for (int x = 0; x < n_exp; x++) cnt[x] = 0;
-        for (int s = 0; s < n * top_k; s++) {
-            const int x = min(max(idx[s], 0), n_exp - 1);
-            list[offs[x] + cnt[x]++] = s;
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
         }
-        *ticket = 0u;
+        int run = incl - tot;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int x = 4 * lane + q;
+            if (x < n_exp) o_s[x] = run;
+            run += v[q];
+        }
+        if (lane == 63) o_s[n_exp] = incl;
+    }
+    __syncthreads();
+    for (int sl = threadIdx.x; sl < slots; sl += blockDim.x) {
+        const int x = e_s[sl];
+        list[o_s[x] + atomicAdd(&f_s[x], 1)] = sl;
+    }
+    for (int x = threadIdx.x; x < n_exp; x += blockDim.x) {
+        cnt[x] = c_s[x];
+        offs[x] = o_s[x];
+    }
+    if (threadIdx.x == 0) offs[n_exp] = o_s[n_exp];
+    if (wave == 0) {
+        // active experts in ascending order: compaction by ballot over 64 at a time
+        int base = 0;
+        for (int x0 = 0; x0 < n_exp; x0 += 64) {
+            const int x = x0 + lane;
+            const bool on = x < n_exp && c_s[x] > 0;
+            const unsigned long long m = __ballot(on);
+            if (on) act[base + __popcll(m & ((1ull << lane) - 1ull))] = x;
+            base += __popcll(m);
+        }
+        if (lane == 0) {
+            *act_n = base;
+            *ticket = 0u;
+        }
     }
 }
 
 // ---------------------------------------------------------------------------
 // Grouped expert matvecs
 // ---------------------------------------------------------------------------
-constexpr int MOE_TCH = 8; // tokens staged per round
-
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// grid (experts, row chunks), 512 threads.  Expert e's slots are
-// list[offs[e] .. offs[e] + cnt[e]); slot s reads x = xs + (s / xdiv) * cols
+// Persistent grid of workgroups (512 threads) over the work items (active
+// expert a, row chunk c), item w = a * chunks + c, w = blockIdx.x, +gridDim.x.
+// A chunk is 2 passes per wavefront (rpw = 2 * 8 * RW rows): both passes'
+// weights are requested before the tokens' x is staged, so the HBM reads of
+// an item overlap its staging.  Expert e's slots are list[offs[e] ..
+// offs[e] + cnt[e]), `tch` at a time; slot s reads x = xs + (s / xdiv) * cols
 // and writes out[s * rows + r].  NMAT == 2: tabA = gate, tabB = up, output
 // silu(gate.x) * up.x (swiglu, gemm.rs:210-226); NMAT == 1: tabA = down.
 template <int FMT, int LPR, int NMAT>
 __global__ void __launch_bounds__(512) k_moe_mv(const uint8_t *const *__restrict__ tabA,
                                                 const uint8_t *const *__restrict__ tabB, size_t stride, int rows,
-                                                int cols, int rows_per_wg, const float *__restrict__ xs, int xdiv,
+                                                int cols, int chunks, const float *__restrict__ xs, int xdiv,
                                                 const int *__restrict__ cnt, const int *__restrict__ offs,
-                                                const int *__restrict__ list, float *__restrict__ out)
+                                                const int *__restrict__ list, const int *__restrict__ act,
+                                                const int *__restrict__ act_n, int tch, float *__restrict__ out)
 {
-    constexpr int RW = 64 / LPR;
-    const int e = blockIdx.x;
-    const int ne = cnt[e];
-    const int r0 = blockIdx.y * rows_per_wg, r1 = min(rows, r0 + rows_per_wg);
-    if (ne == 0 || r0 >= r1) return; // uniform over the workgroup
+    constexpr int RW = 64 / LPR, NW = 8, RPW = 2 * NW * RW;
     extern __shared__ uint4 smem[];
-    __shared__ int slot_s[MOE_TCH];
+    __shared__ int slot_s[64];
     const size_t tok_bytes = (stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15;
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int nw = blockDim.x >> 6;
     const int U = cols >> 6;
     const int ul = lane & (LPR - 1), slot = lane / LPR;
     const bool uact = ul < U;
@@ -182,48 +239,61 @@ __global__ void __launch_bounds__(512) k_moe_mv(const uint8_t *const *__restrict
     UConst c;
     unit_setup_w<FMT>(u, c);
     const LaneOff L = lane_offsets<FMT>(cols, u, c);
-    const rsrc_t rA = make_rsrc(tabA[e], (uint32_t)((size_t)rows * stride));
-    const rsrc_t rB = make_rsrc(NMAT == 2 ? tabB[e] : tabA[e], (uint32_t)((size_t)rows * stride));
-    const int np = (r1 - r0 + RW - 1) / RW;
-    const int base = offs[e];
-
-    for (int t0 = 0; t0 < ne; t0 += MOE_TCH) {
-        const int nt = min(MOE_TCH, ne - t0);
-        if (threadIdx.x < nt) slot_s[threadIdx.x] = list[base + t0 + threadIdx.x];
-        __syncthreads();
-        for (int j = 0; j < nt; j++) {
-            uint8_t *reg = (uint8_t *)smem + j * tok_bytes;
-            uint32_t *xd = (uint32_t *)reg;
-            float *s16 = (float *)(xd + (cols >> 2) * XDIG);
-            int *kx = (int *)(s16 + (cols >> 4));
-            stage_x<FMT>(xs + (size_t)(slot_s[j] / xdiv) * cols, cols, xd, s16, kx);
+    const int items = *act_n * chunks;
+    for (int w = blockIdx.x; w < items; w += gridDim.x) {
+        const int e = act[w / chunks];
+        const int r0 = (w % chunks) * RPW, r1 = min(rows, r0 + RPW);
+        const int ne = cnt[e], base = offs[e];
+        const rsrc_t rA = make_rsrc(tabA[e], (uint32_t)((size_t)rows * stride));
+        const rsrc_t rB = make_rsrc(NMAT == 2 ? tabB[e] : tabA[e], (uint32_t)((size_t)rows * stride));
+        // this wavefront's two passes: rows r0 + (wave + 8q) * RW + slot
+        int rq[2];
+        uint32_t bq[2];
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            rq[q] = r0 + (wave + NW * q) * RW + slot;
+            bq[q] = (uact && rq[q] < r1) ? (uint32_t)((size_t)rq[q] * stride) : 0x80000000u;
         }
-        for (int p = wave; p < np; p += nw) {
-            const int r = r0 + p * RW + slot;
-            const uint32_t rb = (uact && r < r1) ? (uint32_t)((size_t)r * stride) : 0x80000000u;
-            WRow<FMT> wa, wb;
-            load_row<FMT>(rA, rb, cols, L, wa);
-            if constexpr (NMAT == 2) load_row<FMT>(rB, rb, cols, L, wb);
+        for (int t0 = 0; t0 < ne; t0 += tch) {
+            const int nt = min(tch, ne - t0);
+            WRow<FMT> wa[2], wb[2];
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                load_row<FMT>(rA, bq[q], cols, L, wa[q]);
+                if constexpr (NMAT == 2) load_row<FMT>(rB, bq[q], cols, L, wb[q]);
+            }
+            __syncthreads(); // the previous round's readers of LDS are done
+            if (threadIdx.x < nt) slot_s[threadIdx.x] = list[base + t0 + threadIdx.x];
+            __syncthreads();
             for (int j = 0; j < nt; j++) {
-                const uint8_t *reg = (const uint8_t *)smem + j * tok_bytes;
-                const uint32_t *xd = (const uint32_t *)reg;
+                uint32_t *xd = (uint32_t *)((uint8_t *)smem + j * tok_bytes);
+                float *s16 = (float *)(xd + (cols >> 2) * XDIG);
+                int *kx = (int *)(s16 + (cols >> 4));
+                stage_x<FMT>(xs + (size_t)(slot_s[j] / xdiv) * cols, cols, xd, s16, kx);
+            }
+            for (int j = 0; j < nt; j++) {
+                const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + j * tok_bytes);
                 const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
                 const int *kx = (const int *)(s16 + (cols >> 4));
                 XReg xv;
                 UConst cj = c;
                 unit_setup_x<FMT>(xd, s16, kx, u, U, xv, cj);
-                float pa = unit_dot<FMT>(wa, xv, cj);
-                pa = seg_sum_dpp<LPR>(uact ? pa : 0.0f);
-                float v = pa;
-                if constexpr (NMAT == 2) {
-                    float pb = unit_dot<FMT>(wb, xv, cj);
-                    pb = seg_sum_dpp<LPR>(uact ? pb : 0.0f);
-                    v = silu(pa) * pb;
+                const size_t ob = (size_t)slot_s[j] * rows;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    float pa = unit_dot<FMT>(wa[q], xv, cj);
+                    pa = seg_sum_dpp<LPR>(uact ? pa : 0.0f);
+                    float v = pa;
+                    if constexpr (NMAT == 2) {
+                        float pb = unit_dot<FMT>(wb[q], xv, cj);
+                        pb = seg_sum_dpp<LPR>(uact ? pb : 0.0f);
+                        v = silu(pa) * pb;
+                    }
+                    if (ul == LPR - 1 && rq[q] < r1) out[ob + rq[q]] = v;
                 }
-                if (ul == LPR - 1 && r < r1) out[(size_t)slot_s[j] * rows + r] = v;
             }
         }
-        __syncthreads(); // the next round restages LDS
+        __syncthreads(); // LDS is restaged by the next item
     }
 }
 
@@ -250,7 +320,7 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
 {
     const size_t slots = n * top_k;
     char *f = (char *)scratch_get(h, 8, (n * (n_groups > 0 ? n_groups : 1) + 2 * slots) * 4);
-    int *ints = (int *)scratch_get(h, 9, (2 * n_groups + 1 + slots) * 4);
+    int *ints = (int *)scratch_get(h, 9, (3 * n_groups + 2 + slots) * 4);
     float *big = (float *)scratch_get(h, 10, slots * (ffn + hdim) * 4);
     if (!f || !ints || !big) return false;
     s.logits = (float *)f;
@@ -259,6 +329,8 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
     s.cnt = ints;
     s.offs = ints + n_groups;
     s.list = ints + 2 * n_groups + 1;
+    s.act_list = s.list + slots;
+    s.act_n = s.act_list + n_groups;
     s.act = big;
     s.ydown = big + slots * ffn;
     return true;
@@ -268,8 +340,9 @@ int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size
                      const MoeScratch &s)
 {
     const unsigned grid = (unsigned)((n_exp + 7) / 8);
+    if (n * top_k > ROUTE_MAX_SLOTS || n_exp > 256) return set_err(h, SOSO_HIP_DECLINED, "moe route: too many slots");
     k_moe_route<<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt,
-                                              s.cnt, s.offs, s.list, h->ticket);
+                                              s.cnt, s.offs, s.list, s.act_list, s.act_n, h->ticket);
     return hip_check(h, hipGetLastError(), "moe route launch");
 }
 
@@ -285,14 +358,14 @@ int launch_router_topk(soso_hip *h, const float *w, const float *x, size_t n, si
 }
 
 template <int FMT, int NMAT>
-static void moe_mv_fmt(soso_hip *h, dim3 grid, size_t lds, int lpr, const uint8_t *const *A, const uint8_t *const *B,
-                       size_t stride, int rows, int cols, int rpw, const float *xs, int xdiv, const MoeScratch &s,
-                       float *out)
+static void moe_mv_fmt(soso_hip *h, unsigned grid, size_t lds, int lpr, const uint8_t *const *A,
+                       const uint8_t *const *B, size_t stride, int rows, int cols, int chunks, const float *xs,
+                       int xdiv, int tch, const MoeScratch &s, float *out)
 {
 #define MOE_CASE(LP)                                                                                                   \
     case LP:                                                                                                           \
-        k_moe_mv<FMT, LP, NMAT><<<grid, 512, lds, h->stream>>>(A, B, stride, rows, cols, rpw, xs, xdiv, s.cnt, s.offs, \
-                                                                s.list, out);                                          \
+        k_moe_mv<FMT, LP, NMAT><<<grid, 512, lds, h->stream>>>(A, B, stride, rows, cols, chunks, xs, xdiv, s.cnt,     \
+                                                                s.offs, s.list, s.act_list, s.act_n, tch, out);        \
         break;
     switch (lpr) {
         MOE_CASE(1) MOE_CASE(2) MOE_CASE(4) MOE_CASE(8) MOE_CASE(16) MOE_CASE(32) MOE_CASE(64)
@@ -300,40 +373,40 @@ static void moe_mv_fmt(soso_hip *h, dim3 grid, size_t lds, int lpr, const uint8_
 #undef MOE_CASE
 }
 
-// One grouped matvec over `n_groups` experts (pointer tables on the device).
+// One grouped matvec over the active experts (pointer tables on the device).
+// active_max bounds the number of active experts, tch the tokens per expert
+// staged at a time (at most the tokens of the call).
 static int launch_moe_mv(soso_hip *h, uint8_t dtype, int nmat, const uint8_t *const *A, const uint8_t *const *B,
-                         size_t rows, size_t cols, size_t n_groups, size_t active_hint, const float *xs, int xdiv,
+                         size_t rows, size_t cols, size_t active_max, size_t tch, const float *xs, int xdiv,
                          const MoeScratch &s, float *out)
 {
     const int U = (int)(cols / 64);
     if (U < 1 || U > 64 || !packed_shape_ok(dtype, rows, cols))
         return set_err(h, SOSO_HIP_DECLINED, "moe: expert shape not handled here");
     const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
-    const int rw = 64 / lpr;
+    const size_t rpw = 2 * 8 * (64 / lpr);
+    const size_t chunks = (rows + rpw - 1) / rpw;
+    tch = std::max<size_t>(1, std::min<size_t>(tch, 64));
     const size_t tok_bytes = (stage_lds_bytes(cols) + 15) & ~(size_t)15;
-    const size_t lds = tok_bytes * MOE_TCH;
+    while (tch > 1 && tok_bytes * tch > h->max_lds) tch--;
+    const size_t lds = tok_bytes * tch;
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "moe: x does not fit in LDS");
-    // about two workgroups per CU over the experts expected to be active
-    const size_t act = std::max<size_t>(1, std::min(active_hint, n_groups));
-    size_t chunks = (2 * (size_t)h->num_cu + act - 1) / act;
-    int rpw = (int)((rows + chunks - 1) / chunks);
-    rpw = std::max(rpw, rw * 8);
-    rpw = (rpw + rw - 1) / rw * rw;
-    chunks = (rows + rpw - 1) / rpw;
-    const dim3 grid((unsigned)n_groups, (unsigned)chunks);
+    const size_t items = active_max * chunks;
+    const unsigned grid = (unsigned)std::max<size_t>(1, std::min<size_t>(items, 2 * (size_t)h->num_cu));
     const size_t stride = packed_row_stride(dtype, cols);
+    const int ri = (int)rows, ci = (int)cols, ch = (int)chunks, ti = (int)tch;
     switch (dtype) {
     case SOSO_HIP_DTYPE_Q4_K:
-        if (nmat == 2) moe_mv_fmt<FMT_Q4K, 2>(h, grid, lds, lpr, A, B, stride, (int)rows, (int)cols, rpw, xs, xdiv, s, out);
-        else moe_mv_fmt<FMT_Q4K, 1>(h, grid, lds, lpr, A, B, stride, (int)rows, (int)cols, rpw, xs, xdiv, s, out);
+        if (nmat == 2) moe_mv_fmt<FMT_Q4K, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
+        else moe_mv_fmt<FMT_Q4K, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
         break;
     case SOSO_HIP_DTYPE_Q8_0:
-        if (nmat == 2) moe_mv_fmt<FMT_Q80, 2>(h, grid, lds, lpr, A, B, stride, (int)rows, (int)cols, rpw, xs, xdiv, s, out);
-        else moe_mv_fmt<FMT_Q80, 1>(h, grid, lds, lpr, A, B, stride, (int)rows, (int)cols, rpw, xs, xdiv, s, out);
+        if (nmat == 2) moe_mv_fmt<FMT_Q80, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
+        else moe_mv_fmt<FMT_Q80, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
         break;
     case SOSO_HIP_DTYPE_Q6_K:
-        if (nmat == 2) moe_mv_fmt<FMT_Q6K, 2>(h, grid, lds, lpr, A, B, stride, (int)rows, (int)cols, rpw, xs, xdiv, s, out);
-        else moe_mv_fmt<FMT_Q6K, 1>(h, grid, lds, lpr, A, B, stride, (int)rows, (int)cols, rpw, xs, xdiv, s, out);
+        if (nmat == 2) moe_mv_fmt<FMT_Q6K, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
+        else moe_mv_fmt<FMT_Q6K, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
         break;
     default: return set_err(h, SOSO_HIP_DECLINED, "moe: expert dtype not handled here");
     }
@@ -347,9 +420,9 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
                        const uint8_t *use, const MoeScratch &s, float *out)
 {
     const size_t active = std::min(n_groups, n * top_k);
-    int rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, n_groups, active, xs, (int)top_k, s, s.act);
+    int rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, active, n, xs, (int)top_k, s, s.act);
     if (rc == SOSO_HIP_OK)
-        rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, n_groups, active, s.act, 1, s, s.ydown);
+        rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, active, n, s.act, 1, s, s.ydown);
     if (rc != SOSO_HIP_OK) return rc;
     const dim3 grid((unsigned)((hdim + 255) / 256), (unsigned)n);
     k_moe_combine<<<grid, 256, 0, h->stream>>>(s.ydown, wgt, use, (int)n, (int)hdim, (int)top_k, out);

@@ -403,7 +403,8 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
     for (size_t e = 0; e < n_exps; e++)
         if (ok[e]) gid.push_back(e);
     const size_t G = gid.size();
-    std::vector<int> ints(2 * G + 1 + slots, 0);
+    // [cnt G | offs G+1 | list slots | active groups G | their count], as moe_scratch lays it out
+    std::vector<int> ints(3 * G + 2 + slots, 0);
     std::vector<const uint8_t *> tab(3 * G);
     int o = 0;
     for (size_t g = 0; g < G; g++) {
@@ -417,6 +418,8 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
         for (int k = 0; k < 3; k++) tab[k * G + g] = (const uint8_t *)wts[3 * gid[g] + k]->dev;
     }
     ints[2 * G] = o;
+    for (size_t g = 0; g < G; g++) ints[2 * G + 1 + slots + g] = (int)g;
+    ints[3 * G + 1 + slots] = (int)G;
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
     float *sd = (float *)scratch_get(h, 5, n * hdim * 4);
     char *aux = (char *)scratch_get(h, 11, slots * 4 + slots + 3 * G * sizeof(void *) + 64);
