@@ -150,6 +150,40 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
 int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev, size_t n,
                          float *out_dev, int32_t *idx_dev, float *wgt_dev);
 
+/* ---- dense decode step resident on the device -----------------------------------
+ * The device-resident decode of GpuDispatch::decode_preparar / decode_token
+ * (gpu.rs:653-690) for a Llama-style dense model (LayerExecutor::forward_layer,
+ * crates/soso-llm-core/src/layer.rs:1092-1389, then Runtime::logits_gpu and
+ * argmax, runtime.rs:1976-2028), with an f32 KV cache.
+ * keys: 9 per layer -- attn_norm, q, k, v, o, ffn_norm, gate, up, down -- then
+ * output_norm and head (9 * n_layers + 2 resident weights).  Norms are F32
+ * [1 x hidden]; q [n_heads*head_dim x hidden], k and v [n_kv_heads*head_dim x
+ * hidden], o [hidden x n_heads*head_dim], gate and up [ffn x hidden], down
+ * [hidden x ffn], head [vocab x hidden].  q/k/v share one quantized dtype, gate/up
+ * another; head_dim must be 128 and n_heads a multiple (1, 2, 4 or 8) of
+ * n_kv_heads.  The library keeps fused copies (q|k|v rows; gate/up rows
+ * interleaved) and allocates the KV cache (2 x n_layers x ctx_max x kv_dim f32,
+ * zeroed) and the step's buffers; drop_sources = 1 drops the q, k, v, gate and up
+ * weights once fused.  RoPE is non-NeoX (pairs 2i, 2i+1) with rope_theta. */
+typedef struct soso_hip_decode_cfg {
+    uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, ctx_max;
+    float rope_theta, rms_eps;
+} soso_hip_decode_cfg;
+int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
+                           const char *const *keys, const size_t *key_lens, int drop_sources);
+/* Device pointers of layer `layer`'s K and V caches, each [ctx_max x kv_dim] f32
+ * (position-major), for prefilling and inspection. */
+int soso_hip_decode_kv_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, float **k_dev,
+                           float **v_dev);
+/* One token at position `pos` (KV rows 0..pos-1 already filled): hidden = x_dev
+ * (the token's f32 embedding row); writes K/V row `pos` of every layer, the
+ * logits (logits_dev, vocab f32, when non-null) and the greedy token
+ * (*token_dev, last maximum wins).  Asynchronous; allocates nothing, so it may be
+ * captured in a graph. */
+int soso_hip_decode_step_dev(soso_hip *h, const char *model_key, size_t model_key_len, const float *x_dev, uint32_t pos,
+                             float *logits_dev, uint32_t *token_dev);
+int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key_len);
+
 /* ---- device-resident API (no host copies; for the decode step, benchmarks
  * and tests that keep inputs in HBM).  Launches are asynchronous on the
  * handle's stream; soso_hip_sync waits. -------------------------------------- */

@@ -58,6 +58,24 @@ struct MoeLayer {
     std::vector<const void *> host_tab; // the same pointers, for unregistering on weight_drop
 };
 
+// A dense decode model registered for the device-resident step (k_decode.hip).
+struct DecodeLayer {
+    const Weight *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
+    const float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+struct DecodeModel {
+    size_t n_layers = 0, hidden = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, ffn = 0, vocab = 0, ctx_max = 0;
+    float theta = 0.0f, eps = 0.0f;
+    std::vector<DecodeLayer> layers;
+    std::vector<Weight> owned; // the fused qkv / gate-up copies
+    const float *out_norm = nullptr;
+    const Weight *head = nullptr;
+    std::vector<std::string> uses; // keys of the resident weights the model reads
+    float *kcache = nullptr, *vcache = nullptr; // [n_layers][ctx_max][kv_dim]
+    void *mem = nullptr;                         // activations below, one allocation
+    float *hid = nullptr, *qbuf = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
+};
+
 struct soso_hip {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -75,6 +93,7 @@ struct soso_hip {
     size_t scratch_cap[N_SCRATCH] = {};
     unsigned *ticket = nullptr; // zero between launches of the "last workgroup" kernels
     std::unordered_map<std::string, MoeLayer> moe_layers;
+    std::unordered_map<std::string, DecodeModel> decode_models;
     std::vector<hipEvent_t> events; // per-launch timing slots
     std::vector<hipGraphExec_t> graphs;
     bool capturing = false;
@@ -85,6 +104,24 @@ int set_err(soso_hip *h, int code, const std::string &msg);
 int hip_check(soso_hip *h, hipError_t e, const char *what);
 void *scratch_get(soso_hip *h, int slot, size_t bytes);
 
+// Input and output variants of the matvec kernel (decode-step fusions).
+enum { XS_PLAIN = 0, XS_RMSNORM = 1 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+struct MvIn {
+    const float *x = nullptr;
+    const float *norm_w = nullptr; // XS_RMSNORM: the norm's weight (cols)
+    float eps = 0.0f;
+};
+struct MvEpi {
+    const float *res = nullptr; // EPI_RESID: y = res + W.x (res may be y)
+    // EPI_QKV: rows [0, q_dim) -> y rotated, [q_dim, q_dim + kv_dim) -> k_out
+    // rotated, the next kv_dim -> v_out; RoPE of pairs (2i, 2i+1) inside each
+    // head_dim block at position pos (non-NeoX, gemm.rs:1452-1490)
+    float *k_out = nullptr, *v_out = nullptr;
+    int q_dim = 0, kv_dim = 0, head_dim = 0, pos = 0;
+    float theta = 0.0f;
+};
+
 // packed layouts (k_matvec.hip)
 size_t packed_row_stride(uint8_t dtype, size_t cols);
 bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols);
@@ -92,8 +129,15 @@ bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols);
 // launchers (k_matvec.hip)
 int repack_weight(soso_hip *h, uint8_t dtype, const void *raw_dev, void *packed_dev, size_t rows, size_t cols);
 int launch_matvec(soso_hip *h, const Weight &w, const float *x_dev, float *y_dev, size_t n);
+// One matvec with an input variant (xs) and an output variant (epi).  EPI_SWIGLU
+// expects rows interleaved (gate_i, up_i) and writes rows/2 values silu(g)*u.
+int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y_dev, const MvEpi &ep, int xs, int epi);
 int launch_dequant(soso_hip *h, const Weight &w, float *out_dev);
 int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
+// (k_decode.hip)
+int launch_attention(soso_hip *h, const float *q, const float *K, const float *V, int n_heads, int n_kv_heads,
+                     int head_dim, int T, float *part, float *out);
+int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token);
 // (k_synth.hip)
 int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
                      uint64_t stream);

@@ -1,2 +1,239 @@
-// k_decode.hip -- placeholder (decode step kernels)
+// k_decode.hip -- one decode step of a dense Llama-style model on the device.
+//
+// Reference: LayerExecutor::forward_layer, dense GQA branch
+// (crates/soso-llm-core/src/layer.rs:1092-1389): attn_norm -> q/k/v ->
+// rope_cabezas (gemm.rs:1452-1490) -> KV append -> attention -> o-proj +
+// residual -> ffn_norm -> gate/up -> swiglu -> down + residual; then
+// Runtime::logits_gpu + argmax (crates/soso-llm-core/src/runtime.rs:1976-2028).
+// The KV cache is f32 here; soso keeps f16 (kv.rs:349).
+//
+// Launches per layer (every weight byte read once, activations stay in HBM):
+//   1. qkv matvec   x = rmsnorm(h) staged in LDS; rows [q; k; v] concatenated;
+//                   RoPE applied to q/k row pairs in the epilogue, k and v
+//                   written straight into the KV cache at `pos`
+//   2. k_attn_split split-K decode attention over 64-position chunks, the
+//                   G query heads of a KV head share every K/V read
+//   3. k_attn_combine  softmax-weighted merge of the chunks
+//   4. o matvec     h += W_o . attn (residual in the epilogue)
+//   5. gate/up      x = rmsnorm(h); rows interleaved (gate_i, up_i); the
+//                   epilogue writes silu(gate_i) * up_i
+//   6. down matvec  h += W_down . act
+// Head: matvec with rmsnorm(h) staged (Q6_K or Q8_0 / Q4_K), then argmax.
 #include "internal.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+constexpr int ATT_HD = 128;   // head_dim handled
+constexpr int ATT_CHUNK = 64; // positions per split
+
+// grid (n_kv_heads, chunks), block 64 * G: q heads g*G .. g*G + G - 1 share
+// KV head g (GQA).  Scores s = (q . k) / sqrt(hd); per chunk: m = max s,
+// p = exp(s - m), l = sum p, acc = sum p v.  part[(head * chunks + c) *
+// (HD + 2)] = {m, l, acc[0..HD)}.  K, V: [T][kv_dim] of one layer.
+template <int G>
+__global__ void __launch_bounds__(64 * G) k_attn_split(const float *__restrict__ q, const float *__restrict__ K,
+                                                        const float *__restrict__ V, int kv_dim, int T, int chunks,
+                                                        float *__restrict__ part)
+{
+    constexpr int HD = ATT_HD;
+    __shared__ float qs[G][HD];
+    __shared__ float sc[G][ATT_CHUNK];
+    const int g = blockIdx.x, c = blockIdx.y;
+    const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int i = threadIdx.x; i < G * HD; i += 64 * G) qs[i / HD][i % HD] = q[(size_t)g * G * HD + i];
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((float)HD);
+    // scores: 16 positions per wavefront pass, 4 lanes per position; lane j of
+    // a position reads the float4s 4j + 16i (i < 8) of the key (64 B runs)
+    const int pp = lane >> 2, j = lane & 3;
+    for (int sl = wave; sl < ATT_CHUNK / 16; sl += G) {
+        const int t = t0 + 16 * sl + pp;
+        float acc[G];
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) acc[hh] = 0.0f;
+        if (t < t1) {
+            const float4 *k4 = (const float4 *)(K + (size_t)t * kv_dim + (size_t)g * HD);
+            float4 kv[8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) kv[i] = k4[4 * i + j];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int d = 16 * i + 4 * j;
+#pragma unroll
+                for (int hh = 0; hh < G; hh++) {
+                    acc[hh] = fmaf(kv[i].x, qs[hh][d], acc[hh]);
+                    acc[hh] = fmaf(kv[i].y, qs[hh][d + 1], acc[hh]);
+                    acc[hh] = fmaf(kv[i].z, qs[hh][d + 2], acc[hh]);
+                    acc[hh] = fmaf(kv[i].w, qs[hh][d + 3], acc[hh]);
+                }
+            }
+        }
+#pragma unroll
+        for (int hh = 0; hh < G; hh++) {
+            float v = acc[hh];
+            v += dpp_f<0xB1>(v);
+            v += dpp_f<0x4E>(v);
+            if (j == 0 && t < t1) sc[hh][t - t0] = v * inv;
+        }
+    }
+    __syncthreads();
+    // softmax statistics of the chunk, one wavefront per head
+    const int n = t1 - t0;
+    if (wave < G) {
+        const float s = lane < n ? sc[wave][lane] : -INFINITY;
+        const float m = wave_max(s);
+        const float p = lane < n ? expf(s - m) : 0.0f;
+        const float l = seg_sum<64>(p);
+        sc[wave][lane] = p;
+        if (lane == 0) {
+            float *o = part + ((size_t)(g * G + wave) * chunks + c) * (HD + 2);
+            o[0] = m;
+            o[1] = l;
+        }
+    }
+    __syncthreads();
+    // acc[h][d] = sum_t p[h][t] v[t][d]: wavefront = head, lane = dims 2l, 2l+1
+    if (wave < G) {
+        float2 a = make_float2(0.f, 0.f);
+        const float *vb = V + (size_t)g * HD + 2 * lane;
+        for (int tb = 0; tb < n; tb += 16) {
+            float2 v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++)
+                v[k] = tb + k < n ? *(const float2 *)(vb + (size_t)(t0 + tb + k) * kv_dim) : make_float2(0.f, 0.f);
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                const float pk = tb + k < n ? sc[wave][tb + k] : 0.0f;
+                a.x = fmaf(pk, v[k].x, a.x);
+                a.y = fmaf(pk, v[k].y, a.y);
+            }
+        }
+        float *o = part + ((size_t)(g * G + wave) * chunks + c) * (HD + 2) + 2;
+        *(float2 *)(o + 2 * lane) = a;
+    }
+}
+
+// grid n_heads, block HD: out[h*HD + d] = sum_c e^{m_c - M} acc_c[d] /
+// sum_c e^{m_c - M} l_c.
+__global__ void __launch_bounds__(ATT_HD) k_attn_combine(const float *__restrict__ part, int chunks,
+                                                          float *__restrict__ out)
+{
+    constexpr int HD = ATT_HD;
+    __shared__ float wsh[1024];
+    __shared__ float red[2];
+    const int h = blockIdx.x, d = threadIdx.x;
+    const float *ph = part + (size_t)h * chunks * (HD + 2);
+    float m = -INFINITY;
+    for (int c = d; c < chunks; c += HD) m = fmaxf(m, ph[(size_t)c * (HD + 2)]);
+    m = wave_max(m);
+    if ((d & 63) == 0) red[d >> 6] = m;
+    __syncthreads();
+    const float M = fmaxf(red[0], red[1]);
+    float l = 0.0f;
+    for (int c = d; c < chunks; c += HD) {
+        const float w = expf(ph[(size_t)c * (HD + 2)] - M);
+        wsh[c] = w;
+        l += w * ph[(size_t)c * (HD + 2) + 1];
+    }
+    l = seg_sum<64>(l);
+    __syncthreads();
+    if ((d & 63) == 0) red[d >> 6] = l;
+    __syncthreads();
+    const float L = red[0] + red[1];
+    float a = 0.0f;
+    for (int c0 = 0; c0 < chunks; c0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) v[k] = c0 + k < chunks ? ph[(size_t)(c0 + k) * (HD + 2) + 2 + d] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++)
+            if (c0 + k < chunks) a = fmaf(wsh[c0 + k], v[k], a);
+    }
+    out[(size_t)h * HD + d] = L > 0.0f ? a / L : 0.0f;
+}
+
+int launch_attention(soso_hip *h, const float *q, const float *K, const float *V, int n_heads, int n_kv_heads,
+                     int head_dim, int T, float *part, float *out)
+{
+    if (head_dim != ATT_HD || n_kv_heads <= 0 || n_heads % n_kv_heads || T <= 0)
+        return set_err(h, SOSO_HIP_DECLINED, "attention: head shape not handled here");
+    const int G = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
+    const int chunks = (T + ATT_CHUNK - 1) / ATT_CHUNK;
+    if (chunks > 1024) return set_err(h, SOSO_HIP_DECLINED, "attention: context longer than 65536");
+    const dim3 grid((unsigned)n_kv_heads, (unsigned)chunks);
+    switch (G) {
+    case 1: k_attn_split<1><<<grid, 64, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
+    case 2: k_attn_split<2><<<grid, 128, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
+    case 4: k_attn_split<4><<<grid, 256, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
+    case 8: k_attn_split<8><<<grid, 512, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
+    default: return set_err(h, SOSO_HIP_DECLINED, "attention: GQA group size not handled here");
+    }
+    int rc = hip_check(h, hipGetLastError(), "attention split launch");
+    if (rc != SOSO_HIP_OK) return rc;
+    k_attn_combine<<<(unsigned)n_heads, ATT_HD, 0, h->stream>>>(part, chunks, out);
+    return hip_check(h, hipGetLastError(), "attention combine launch");
+}
+
+// ---------------------------------------------------------------------------
+// The decode step
+// ---------------------------------------------------------------------------
+int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token)
+{
+    const int q_dim = (int)(m.n_heads * m.head_dim), kv_dim = (int)(m.n_kv_heads * m.head_dim);
+    if (pos >= m.ctx_max) return set_err(h, SOSO_HIP_ERR_ARG, "decode: position beyond the KV capacity");
+    float *hid = m.hid, *qb = m.qbuf, *att = m.att, *act = m.act, *lg = logits ? logits : m.logits;
+    int rc = hip_check(h, hipMemcpyAsync(hid, x, m.hidden * 4, hipMemcpyDeviceToDevice, h->stream), "embed copy");
+    for (size_t l = 0; l < m.n_layers && rc == SOSO_HIP_OK; l++) {
+        const DecodeLayer &L = m.layers[l];
+        float *K = m.kcache + l * m.ctx_max * kv_dim, *V = m.vcache + l * m.ctx_max * kv_dim;
+        MvIn in;
+        in.x = hid;
+        in.norm_w = L.attn_norm;
+        in.eps = m.eps;
+        MvEpi ep;
+        ep.k_out = K + (size_t)pos * kv_dim;
+        ep.v_out = V + (size_t)pos * kv_dim;
+        ep.q_dim = q_dim;
+        ep.kv_dim = kv_dim;
+        ep.head_dim = (int)m.head_dim;
+        ep.pos = (int)pos;
+        ep.theta = m.theta;
+        rc = launch_matvec_ex(h, *L.qkv, in, qb, ep, XS_RMSNORM, EPI_QKV);
+        if (rc == SOSO_HIP_OK)
+            rc = launch_attention(h, qb, K, V, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim, (int)pos + 1, m.part,
+                                  att);
+        if (rc == SOSO_HIP_OK) {
+            MvIn a;
+            a.x = att;
+            MvEpi r;
+            r.res = hid;
+            rc = launch_matvec_ex(h, *L.o, a, hid, r, XS_PLAIN, EPI_RESID);
+        }
+        if (rc == SOSO_HIP_OK) {
+            MvIn f;
+            f.x = hid;
+            f.norm_w = L.ffn_norm;
+            f.eps = m.eps;
+            rc = launch_matvec_ex(h, *L.gu, f, act, MvEpi(), XS_RMSNORM, EPI_SWIGLU);
+        }
+        if (rc == SOSO_HIP_OK) {
+            MvIn a;
+            a.x = act;
+            MvEpi r;
+            r.res = hid;
+            rc = launch_matvec_ex(h, *L.down, a, hid, r, XS_PLAIN, EPI_RESID);
+        }
+    }
+    if (rc == SOSO_HIP_OK) {
+        MvIn in;
+        in.x = hid;
+        in.norm_w = m.out_norm;
+        in.eps = m.eps;
+        rc = launch_matvec_ex(h, *m.head, in, lg, MvEpi(), XS_RMSNORM, EPI_STORE);
+    }
+    if (rc == SOSO_HIP_OK && token) rc = launch_argmax(h, lg, m.vocab, token);
+    return rc;
+}

@@ -169,17 +169,61 @@ int repack_weight(soso_hip *h, uint8_t dtype, const void *raw, void *packed, siz
 // ---------------------------------------------------------------------------
 constexpr int COMBINE_CH = 64; // passes per LDS combine round (S > 1)
 
-template <int FMT, int LPR, int S, int DEPTH, bool XFIRST>
-__global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, size_t stride,
-                                               const float *__restrict__ x, float *__restrict__ y, int rows, int cols)
+__device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+// Output of the row sums gathered in yacc (lane i = row r0 + i, i < nrows).
+template <int EPI>
+__device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows, int rows, float *__restrict__ y,
+                                         const MvEpi &ep)
+{
+    const int r = r0 + lane;
+    const bool ok = lane < nrows && r < rows;
+    if constexpr (EPI == EPI_STORE) {
+        if (ok) y[r] = yacc;
+    } else if constexpr (EPI == EPI_RESID) {
+        if (ok) y[r] = ep.res[r] + yacc;
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        // rows (2i, 2i+1) = (gate_i, up_i); strips start on even rows
+        const float up = dpp_f<0xB1>(yacc);
+        if (ok && (lane & 1) == 0) y[r >> 1] = silu_f(yacc) * up;
+    } else {
+        // RoPE on q and k (rope_cabezas, non-NeoX): pair (2i, 2i+1) of a head
+        // becomes (a cos - b sin, a sin + b cos); v passes through
+        const float other = dpp_f<0xB1>(yacc);
+        const int qk = ep.q_dim + ep.kv_dim;
+        if (ok) {
+            if (r < qk) {
+                const int d = (r < ep.q_dim ? r : r - ep.q_dim) % ep.head_dim;
+                const int i = d >> 1;
+                const float fr = powf(ep.theta, -2.0f * (float)i / (float)ep.head_dim);
+                float sn, cs;
+                sincosf((float)ep.pos * fr, &sn, &cs);
+                const bool even = (d & 1) == 0;
+                const float a = even ? yacc : other, b = even ? other : yacc;
+                const float v = even ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn))
+                                     : __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
+                if (r < ep.q_dim) y[r] = v;
+                else ep.k_out[r - ep.q_dim] = v;
+            } else {
+                ep.v_out[r - qk] = yacc;
+            }
+        }
+    }
+}
+
+template <int FMT, int LPR, int S, int DEPTH, bool XFIRST, int XS = XS_PLAIN, int EPI = EPI_STORE>
+__global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, size_t stride, MvIn in,
+                                               float *__restrict__ y, int rows, int cols, MvEpi ep)
 {
     static_assert(S == 1 || LPR == 64, "split rows use whole wavefronts");
     static_assert(S == 1 || COMBINE_CH % DEPTH == 0, "combine rounds keep the load ring aligned");
+    static_assert(S == 1 || EPI == EPI_STORE || EPI == EPI_RESID, "pair epilogues need whole rows per wavefront");
     extern __shared__ uint4 smem[];
+    const float *__restrict__ x = in.x;
     uint32_t *xp = (uint32_t *)smem;                 // cols/4 groups x XDIG digit dwords
     float *s16 = (float *)(xp + (cols >> 2) * XDIG);
     int *kx = (int *)(s16 + (cols >> 4));
-    float *red = (float *)(kx + ((cols + 127) >> 7)); // [groups][COMBINE_CH][S] when S > 1
+    float *red = (float *)(kx + ((cols + 127) >> 7)); // [groups][COMBINE_CH][S] when S > 1; 16 floats for XS_RMSNORM
 
     constexpr int RW = 64 / LPR;
     const int lane = threadIdx.x & 63;
@@ -197,9 +241,12 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 
     const int passes = (rows + RW - 1) / RW;
     const int tg = gridDim.x * gpw;
+    // pair epilogues need strips that start on even rows
+    constexpr int PU = (RW == 1 && (EPI == EPI_QKV || EPI == EPI_SWIGLU)) ? 2 : 1;
+    const int units = (passes + PU - 1) / PU;
     auto strip = [&](int g, int &q0, int &q1) {
-        q0 = (int)((long)passes * g / tg);
-        q1 = (int)((long)passes * (g + 1) / tg);
+        q0 = PU * (int)((long)units * g / tg);
+        q1 = min(passes, PU * (int)((long)units * (g + 1) / tg));
     };
     int p0, p1;
     strip(blockIdx.x * gpw + grp, p0, p1);
@@ -212,7 +259,13 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     const uint32_t lane_base = uact ? (uint32_t)(slot * stride) : 0x80000000u;
 
     WRow<FMT> buf[DEPTH];
-    if constexpr (XFIRST) {
+    if constexpr (XS == XS_RMSNORM) {
+        XPreN xpre;
+        stage_xn_issue(x, in.norm_w, cols, xpre);
+#pragma unroll
+        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
+        stage_xn_finish<FMT>(xpre, cols, in.eps, xp, s16, kx, red);
+    } else if constexpr (XFIRST) {
         // x first: once the weight stream is requested, x's reads would queue
         // behind it in the shared L2 channels.
         stage_x<FMT>(x, cols, xp, s16, kx);
@@ -260,7 +313,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
                 yacc = gather_rows<LPR>(part, j0 + i, yacc, lane);
             }
         }
-        if (lane < n * RW && r0 + lane < rows) y[r0 + lane] = yacc;
+        epilogue<EPI>(yacc, lane, r0, n * RW, rows, y, ep);
     } else {
         // the same number of combine rounds for every wavefront of the workgroup
         int nmax = 0;
@@ -305,7 +358,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
                     float acc = 0.0f;
 #pragma unroll
                     for (int k = 0; k < S; k++) acc += red[(q * COMBINE_CH + i) * S + k];
-                    y[pp] = acc;
+                    y[pp] = EPI == EPI_RESID ? ep.res[pp] + acc : acc;
                 }
             }
             __syncthreads();
@@ -373,7 +426,10 @@ template <int FMT, int S>
 static void launch_split(soso_hip *h, int grid, int threads, size_t lds, const uint8_t *W, size_t stride,
                          const float *x, float *y, int rows, int cols)
 {
-    mv_rows<FMT, 64, S, ring_depth<FMT, S>(), false><<<grid, threads, lds, h->stream>>>(W, stride, x, y, rows, cols);
+    MvIn in;
+    in.x = x;
+    mv_rows<FMT, 64, S, ring_depth<FMT, S>(), false><<<grid, threads, lds, h->stream>>>(W, stride, in, y, rows, cols,
+                                                                                          MvEpi());
 }
 
 template <int FMT>
@@ -389,6 +445,8 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec: x does not fit in LDS");
     const int per_cu = env_int("SOSO_HIP_WG_PER_CU", 1);
     const uint8_t *W = (const uint8_t *)w.dev;
+    MvIn xin;
+    xin.x = x;
     if (S == 1) {
         const int LPR = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
         const int passes = (rows + 64 / LPR - 1) / (64 / LPR);
@@ -401,8 +459,8 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
             return set_err(h, SOSO_HIP_DECLINED, "matvec: row strip exceeds 2 GiB");
 #define MV_CASE(L)                                                                                                  \
     case L:                                                                                                         \
-        mv_rows<FMT, L, 1, ring_depth<FMT, 1>(), x_first<L>()><<<grid, threads, lds, h->stream>>>(W, stride, x, y,   \
-                                                                                                  rows, cols);      \
+        mv_rows<FMT, L, 1, ring_depth<FMT, 1>(), x_first<L>()><<<grid, threads, lds, h->stream>>>(W, stride, xin, y, \
+                                                                                                  rows, cols, MvEpi()); \
         break;
         switch (LPR) {
             MV_CASE(1) MV_CASE(2) MV_CASE(4) MV_CASE(8) MV_CASE(16) MV_CASE(32) MV_CASE(64)
@@ -423,6 +481,89 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
         }
     }
     return hip_check(h, hipGetLastError(), "matvec launch");
+}
+
+// ---------------------------------------------------------------------------
+// Matvec with an input / output variant (the decode step's fusions)
+// ---------------------------------------------------------------------------
+template <int FMT, int LPR, int XS, int EPI>
+static void launch_ex1(soso_hip *h, unsigned grid, size_t lds, const uint8_t *W, size_t stride, const MvIn &in, float *y,
+                       int rows, int cols, const MvEpi &ep)
+{
+    mv_rows<FMT, LPR, 1, ring_depth<FMT, 1>(), x_first<LPR>(), XS, EPI><<<grid, 512, lds, h->stream>>>(
+        W, stride, in, y, rows, cols, ep);
+}
+
+template <int FMT, int XS, int EPI>
+static bool launch_ex_lpr(soso_hip *h, int lpr, unsigned grid, size_t lds, const uint8_t *W, size_t stride,
+                          const MvIn &in, float *y, int rows, int cols, const MvEpi &ep)
+{
+    switch (lpr) {
+    case 8: launch_ex1<FMT, 8, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    case 16: launch_ex1<FMT, 16, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    case 32: launch_ex1<FMT, 32, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    case 64: launch_ex1<FMT, 64, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    default: return false;
+    }
+}
+
+int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, const MvEpi &ep, int xs, int epi)
+{
+    const int rows = (int)w.rows, cols = (int)w.cols, U = cols / 64;
+    const size_t stride = packed_row_stride(w.dtype, w.cols);
+    const uint8_t *W = (const uint8_t *)w.dev;
+    const int S = (U + 63) / 64;
+    if (xs == XS_RMSNORM && cols > XPRE_N * 8 * 512)
+        return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: normalised x wider than the staging registers");
+    if ((epi == EPI_QKV || epi == EPI_SWIGLU) && (S != 1 || rows % 2))
+        return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: pair epilogue needs whole rows per wavefront");
+    if (S > 1) {
+        // split rows: the residual epilogue of the down projection
+        if (w.dtype != SOSO_HIP_DTYPE_Q4_K || xs != XS_PLAIN || epi != EPI_RESID || (S != 2 && S != 4))
+            return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: variant not built for split rows");
+        const int gpw = 8 / S;
+        const size_t lds = stage_lds_bytes(w.cols) + (size_t)gpw * COMBINE_CH * S * 4;
+        if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: x does not fit in LDS");
+        const int grid = std::max(1, std::min(h->num_cu, (rows + gpw - 1) / gpw));
+        if (!strip_fits(rows, grid * gpw, stride)) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: strip");
+        if (S == 2)
+            mv_rows<FMT_Q4K, 64, 2, ring_depth<FMT_Q4K, 2>(), false, XS_PLAIN, EPI_RESID>
+                <<<grid, 512, lds, h->stream>>>(W, stride, in, y, rows, cols, ep);
+        else
+            mv_rows<FMT_Q4K, 64, 4, ring_depth<FMT_Q4K, 4>(), false, XS_PLAIN, EPI_RESID>
+                <<<grid, 512, lds, h->stream>>>(W, stride, in, y, rows, cols, ep);
+        return hip_check(h, hipGetLastError(), "matvec_ex launch");
+    }
+    const int LPR = U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
+    if (U < 8) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: rows narrower than 512 columns");
+    const int RW = 64 / LPR, gpw = 8;
+    const int PU = (RW == 1 && (epi == EPI_QKV || epi == EPI_SWIGLU)) ? 2 : 1;
+    const int passes = (rows + RW - 1) / RW, units = (passes + PU - 1) / PU;
+    const size_t lds = stage_lds_bytes(w.cols) + 64;
+    if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: x does not fit in LDS");
+    int grid = std::min(h->num_cu, (units + gpw - 1) / gpw);
+    const int upw = 64 / (PU * RW); // units per 64-row strip
+    grid = std::max(grid, ((units + upw - 1) / upw + gpw - 1) / gpw);
+    grid = std::max(grid, 1);
+    if (!strip_fits(passes, grid * gpw, (size_t)RW * stride)) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: strip");
+    bool ok = false;
+    const unsigned g = (unsigned)grid;
+    if (w.dtype == SOSO_HIP_DTYPE_Q4_K) {
+        if (xs == XS_RMSNORM && epi == EPI_QKV)
+            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_QKV>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+        else if (xs == XS_RMSNORM && epi == EPI_SWIGLU)
+            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_SWIGLU>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+        else if (xs == XS_PLAIN && epi == EPI_RESID)
+            ok = launch_ex_lpr<FMT_Q4K, XS_PLAIN, EPI_RESID>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+        else if (xs == XS_RMSNORM && epi == EPI_STORE)
+            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_STORE>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+    } else if (w.dtype == SOSO_HIP_DTYPE_Q6_K && xs == XS_RMSNORM && epi == EPI_STORE) {
+        ok = launch_ex_lpr<FMT_Q6K, XS_RMSNORM, EPI_STORE>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+    } else if (w.dtype == SOSO_HIP_DTYPE_Q8_0 && xs == XS_RMSNORM && epi == EPI_STORE) {
+        ok = launch_ex_lpr<FMT_Q80, XS_RMSNORM, EPI_STORE>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+    }
+    if (!ok) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: variant not built");
+    return hip_check(h, hipGetLastError(), "matvec_ex launch");
 }
 
 int launch_matvec(soso_hip *h, const Weight &w, const float *x, float *y, size_t n)

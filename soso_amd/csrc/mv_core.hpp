@@ -146,6 +146,65 @@ __device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int c
     __syncthreads();
 }
 
+// RMSNorm folded into the staging (crates/soso-llm-core/src/gemm.rs:93-100):
+// every workgroup takes sum(x^2) over the whole vector itself, then stages
+// (x_i * scale) * w_i with scale = 1 / sqrt(sum / n + eps).
+constexpr int XPRE_N = 2; // chunks per thread (cols <= 16 * blockDim)
+struct XPreN {
+    float4 v[2 * XPRE_N], w[2 * XPRE_N];
+};
+
+__device__ __forceinline__ void stage_xn_issue(const float *__restrict__ x, const float *__restrict__ w, int cols,
+                                               XPreN &p)
+{
+    const int nch = cols >> 3;
+    const float4 *x4 = (const float4 *)x, *w4 = (const float4 *)w;
+#pragma unroll
+    for (int j = 0; j < XPRE_N; j++) {
+        const int c = j * blockDim.x + threadIdx.x;
+        p.v[2 * j] = p.v[2 * j + 1] = p.w[2 * j] = p.w[2 * j + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < nch) {
+            p.v[2 * j] = x4[2 * c];
+            p.v[2 * j + 1] = x4[2 * c + 1];
+            p.w[2 * j] = w4[2 * c];
+            p.w[2 * j + 1] = w4[2 * c + 1];
+        }
+    }
+}
+
+__device__ __forceinline__ float sq4(float4 v) { return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w); }
+__device__ __forceinline__ float4 norm4(float4 v, float s, float4 w)
+{
+    return make_float4(__fmul_rn(__fmul_rn(v.x, s), w.x), __fmul_rn(__fmul_rn(v.y, s), w.y),
+                       __fmul_rn(__fmul_rn(v.z, s), w.z), __fmul_rn(__fmul_rn(v.w, s), w.w));
+}
+
+// red: 16 floats of LDS.
+template <int FMT>
+__device__ void stage_xn_finish(const XPreN &p, int cols, float eps, uint32_t *xp, float *s16, int *kx, float *red)
+{
+    const int nch = cols >> 3, U = cols >> 6;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < XPRE_N; j++) ss += sq4(p.v[2 * j]) + sq4(p.v[2 * j + 1]);
+    ss = seg_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += red[i];
+    const float scale = 1.0f / sqrtf(tot / (float)cols + eps);
+#pragma unroll
+    for (int j = 0; j < XPRE_N; j++) {
+        const int base = j * blockDim.x;
+        if (base < nch) {
+            const int c = base + threadIdx.x;
+            stage_chunk<FMT>(norm4(p.v[2 * j], scale, p.w[2 * j]), norm4(p.v[2 * j + 1], scale, p.w[2 * j + 1]), c,
+                             c < nch, U, xp, s16, kx);
+        }
+    }
+    __syncthreads();
+}
+
 template <int FMT>
 __device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx)
 {

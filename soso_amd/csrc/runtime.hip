@@ -7,6 +7,7 @@
 // declined key forever, synchronous results, never abort.
 #include "internal.hpp"
 
+#include <algorithm>
 #include <chrono>
 #include <cstring>
 #include <new>
@@ -150,6 +151,22 @@ Weight *find_weight(soso_hip *h, const char *key, size_t key_len)
     return &it->second;
 }
 
+void decode_free(soso_hip *h, DecodeModel &m)
+{
+    hipStreamSynchronize(h->stream);
+    for (Weight &w : m.owned) {
+        if (w.dev) {
+            hipFree(w.dev);
+            h->used -= w.bytes;
+        }
+    }
+    m.owned.clear();
+    if (m.kcache) hipFree(m.kcache);
+    if (m.mem) hipFree(m.mem);
+    m.kcache = m.vcache = nullptr;
+    m.mem = nullptr;
+}
+
 } // namespace
 
 extern "C" {
@@ -196,6 +213,7 @@ void soso_hip_destroy(soso_hip *h)
     for (int i = 0; i < soso_hip::N_SCRATCH; i++)
         if (h->scratch[i]) hipFree(h->scratch[i]);
     for (auto &kv : h->moe_layers) hipFree(kv.second.tab);
+    for (auto &kv : h->decode_models) decode_free(h, kv.second);
     if (h->ticket) hipFree(h->ticket);
     for (hipEvent_t e : h->events)
         if (e) hipEventDestroy(e);
@@ -532,6 +550,173 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
     return rc;
 }
 
+// ---- dense decode step -------------------------------------------------------
+int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
+                           const char *const *keys, const size_t *key_lens, int drop_sources)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!model_key || !cfg || !keys || !key_lens || cfg->n_layers == 0 || cfg->hidden == 0 || cfg->hidden % 4 ||
+        cfg->n_kv_heads == 0 || cfg->n_heads % cfg->n_kv_heads || cfg->head_dim == 0 || cfg->ffn == 0 ||
+        cfg->vocab == 0 || cfg->ctx_max == 0)
+        return set_err(h, SOSO_HIP_ERR_ARG, "decode_create: config");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    const size_t L = cfg->n_layers, H = cfg->hidden, qd = (size_t)cfg->n_heads * cfg->head_dim,
+                 kvd = (size_t)cfg->n_kv_heads * cfg->head_dim, F = cfg->ffn;
+    if (cfg->head_dim != 128) return set_err(h, SOSO_HIP_DECLINED, "decode_create: head_dim must be 128");
+    DecodeModel m;
+    m.n_layers = L;
+    m.hidden = H;
+    m.n_heads = cfg->n_heads;
+    m.n_kv_heads = cfg->n_kv_heads;
+    m.head_dim = cfg->head_dim;
+    m.ffn = F;
+    m.vocab = cfg->vocab;
+    m.ctx_max = cfg->ctx_max;
+    m.theta = cfg->rope_theta;
+    m.eps = cfg->rms_eps;
+    auto get = [&](size_t i, size_t rows, size_t cols, bool f32, const Weight **out) -> bool {
+        const Weight *w = find_weight(h, keys[i], key_lens[i]);
+        if (!w || w->rows != rows || w->cols != cols || (f32 != (w->dtype == SOSO_HIP_DTYPE_F32))) return false;
+        *out = w;
+        return true;
+    };
+    std::vector<const Weight *> q(L), k(L), v(L), g(L), u(L);
+    m.layers.resize(L);
+    for (size_t l = 0; l < L; l++) {
+        const Weight *an, *fn;
+        const size_t b = 9 * l;
+        if (!get(b, 1, H, true, &an) || !get(b + 1, qd, H, false, &q[l]) || !get(b + 2, kvd, H, false, &k[l]) ||
+            !get(b + 3, kvd, H, false, &v[l]) || !get(b + 4, H, qd, false, &m.layers[l].o) ||
+            !get(b + 5, 1, H, true, &fn) || !get(b + 6, F, H, false, &g[l]) || !get(b + 7, F, H, false, &u[l]) ||
+            !get(b + 8, H, F, false, &m.layers[l].down))
+            return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) +
+                                                     ": a weight is missing or has the wrong shape");
+        if (q[l]->dtype != k[l]->dtype || q[l]->dtype != v[l]->dtype || g[l]->dtype != u[l]->dtype)
+            return set_err(h, SOSO_HIP_DECLINED, "decode_create: q/k/v or gate/up dtypes differ");
+        m.layers[l].attn_norm = (const float *)an->dev;
+        m.layers[l].ffn_norm = (const float *)fn->dev;
+    }
+    const Weight *on;
+    if (!get(9 * L, 1, H, true, &on) || !get(9 * L + 1, cfg->vocab, H, false, &m.head))
+        return set_err(h, SOSO_HIP_DECLINED, "decode_create: output_norm/head missing or of the wrong shape");
+    m.out_norm = (const float *)on->dev;
+    // what stays in use (dropping one of these unregisters the model)
+    for (size_t l = 0; l < L; l++)
+        for (size_t j : {0, 4, 5, 8}) m.uses.emplace_back(keys[9 * l + j], key_lens[9 * l + j]);
+    m.uses.emplace_back(keys[9 * L], key_lens[9 * L]);
+    m.uses.emplace_back(keys[9 * L + 1], key_lens[9 * L + 1]);
+    // fused copies
+    m.owned.resize(2 * L);
+    for (size_t l = 0; l < L && rc == SOSO_HIP_OK; l++) {
+        const size_t st_qkv = packed_row_stride(q[l]->dtype, H), st_gu = packed_row_stride(g[l]->dtype, H);
+        Weight &wq = m.owned[2 * l], &wg = m.owned[2 * l + 1];
+        wq.dtype = q[l]->dtype;
+        wq.rows = qd + 2 * kvd;
+        wq.cols = H;
+        wq.bytes = wq.rows * st_qkv;
+        wg.dtype = g[l]->dtype;
+        wg.rows = 2 * F;
+        wg.cols = H;
+        wg.bytes = wg.rows * st_gu;
+        if (h->used + wq.bytes + wg.bytes > h->budget || hipMalloc(&wq.dev, wq.bytes) != hipSuccess ||
+            hipMalloc(&wg.dev, wg.bytes) != hipSuccess) {
+            rc = set_err(h, SOSO_HIP_DECLINED, "decode_create: no memory for the fused weights");
+            break;
+        }
+        h->used += wq.bytes + wg.bytes;
+        char *dq = (char *)wq.dev;
+        rc = hip_check(h, hipMemcpyAsync(dq, q[l]->dev, qd * st_qkv, hipMemcpyDeviceToDevice, h->stream), "qkv copy");
+        if (rc == SOSO_HIP_OK)
+            rc = hip_check(h, hipMemcpyAsync(dq + qd * st_qkv, k[l]->dev, kvd * st_qkv, hipMemcpyDeviceToDevice,
+                                             h->stream), "qkv copy");
+        if (rc == SOSO_HIP_OK)
+            rc = hip_check(h, hipMemcpyAsync(dq + (qd + kvd) * st_qkv, v[l]->dev, kvd * st_qkv,
+                                             hipMemcpyDeviceToDevice, h->stream), "qkv copy");
+        if (rc == SOSO_HIP_OK)
+            rc = hip_check(h, hipMemcpy2DAsync(wg.dev, 2 * st_gu, g[l]->dev, st_gu, st_gu, F, hipMemcpyDeviceToDevice,
+                                               h->stream), "gate copy");
+        if (rc == SOSO_HIP_OK)
+            rc = hip_check(h, hipMemcpy2DAsync((char *)wg.dev + st_gu, 2 * st_gu, u[l]->dev, st_gu, st_gu, F,
+                                               hipMemcpyDeviceToDevice, h->stream), "up copy");
+        m.layers[l].qkv = &wq;
+        m.layers[l].gu = &wg;
+    }
+    // KV cache and step buffers
+    const size_t kv_bytes = L * cfg->ctx_max * kvd * 4;
+    const size_t chunks = (cfg->ctx_max + 63) / 64;
+    const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64;
+    if (rc == SOSO_HIP_OK) {
+        if (hipMalloc((void **)&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, act_floats * 4) != hipSuccess)
+            rc = set_err(h, SOSO_HIP_DECLINED, "decode_create: no memory for the KV cache");
+    }
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemsetAsync(m.kcache, 0, 2 * kv_bytes, h->stream), "kv zero");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "decode_create sync");
+    if (rc != SOSO_HIP_OK) {
+        decode_free(h, m);
+        return rc;
+    }
+    m.vcache = m.kcache + L * cfg->ctx_max * kvd;
+    float *f = (float *)m.mem;
+    m.hid = f;
+    m.qbuf = f + H;
+    m.att = m.qbuf + qd;
+    m.act = m.att + qd;
+    m.part = m.act + F;
+    m.logits = m.part + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2);
+    std::string key(model_key, model_key_len);
+    auto old = h->decode_models.find(key);
+    if (old != h->decode_models.end()) {
+        decode_free(h, old->second);
+        h->decode_models.erase(old);
+    }
+    DecodeModel &dm = h->decode_models.emplace(key, std::move(m)).first->second;
+    for (size_t l = 0; l < L; l++) { // the owned vector moved: re-point the layers at it
+        dm.layers[l].qkv = &dm.owned[2 * l];
+        dm.layers[l].gu = &dm.owned[2 * l + 1];
+    }
+    if (drop_sources)
+        for (size_t l = 0; l < L; l++)
+            for (size_t j : {1, 2, 3, 6, 7}) soso_hip_weight_drop(h, keys[9 * l + j], key_lens[9 * l + j]);
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_decode_kv_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, float **k_dev,
+                           float **v_dev)
+{
+    if (!h || !model_key || !k_dev || !v_dev) return SOSO_HIP_ERR_ARG;
+    auto it = h->decode_models.find(std::string(model_key, model_key_len));
+    if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_kv: model not registered");
+    const DecodeModel &m = it->second;
+    if (layer >= m.n_layers) return set_err(h, SOSO_HIP_ERR_ARG, "decode_kv: layer");
+    const size_t per = m.ctx_max * m.n_kv_heads * m.head_dim;
+    *k_dev = m.kcache + layer * per;
+    *v_dev = m.vcache + layer * per;
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_decode_step_dev(soso_hip *h, const char *model_key, size_t model_key_len, const float *x_dev, uint32_t pos,
+                             float *logits_dev, uint32_t *token_dev)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!model_key || !x_dev) return set_err(h, SOSO_HIP_ERR_ARG, "decode_step: args");
+    auto it = h->decode_models.find(std::string(model_key, model_key_len));
+    if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_step: model not registered");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    return decode_step(h, it->second, x_dev, pos, logits_dev, token_dev);
+}
+
+int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key_len)
+{
+    if (!h || !model_key) return SOSO_HIP_ERR_ARG;
+    auto it = h->decode_models.find(std::string(model_key, model_key_len));
+    if (it == h->decode_models.end()) return SOSO_HIP_DECLINED;
+    decode_free(h, it->second);
+    h->decode_models.erase(it);
+    return SOSO_HIP_OK;
+}
+
 // ---- device-resident API ----------------------------------------------------
 int soso_hip_dev_alloc(soso_hip *h, size_t bytes, void **dptr)
 {
@@ -645,6 +830,15 @@ int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
         if (uses) {
             hipFree(m->second.tab);
             m = h->moe_layers.erase(m);
+        } else {
+            ++m;
+        }
+    }
+    // ... and so is a decode model that reads it
+    for (auto m = h->decode_models.begin(); m != h->decode_models.end();) {
+        if (std::find(m->second.uses.begin(), m->second.uses.end(), it->first) != m->second.uses.end()) {
+            decode_free(h, m->second);
+            m = h->decode_models.erase(m);
         } else {
             ++m;
         }

@@ -268,3 +268,31 @@ class HipGpu:
         k, kl = _key(layer_key)
         return self._rc(self.lib.soso_hip_moe_ffn_dev(self.h, k, kl, x_dev, n, out_dev, idx_dev, wgt_dev),
                         f"moe_ffn_dev {layer_key}")
+
+    # -- dense decode step resident on the device (decode_preparar / decode_token) --
+    def decode_create(self, model_key, cfg, keys, drop_sources=False):
+        """cfg: dict of soso_hip_decode_cfg fields; keys: 9 per layer (attn_norm,
+        q, k, v, o, ffn_norm, gate, up, down), then output_norm and head."""
+        mk, ml = _key(model_key)
+        c = abi.DecodeCfg(**cfg)
+        enc = [k.encode() for k in keys]
+        arr = (C.c_char_p * len(enc))(*enc)
+        lens = (C.c_size_t * len(enc))(*[len(k) for k in enc])
+        return self._rc(self.lib.soso_hip_decode_create(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
+                                                        C.cast(lens, C.c_void_p), 1 if drop_sources else 0),
+                        f"decode_create {model_key}")
+
+    def decode_kv_dev(self, model_key, layer):
+        mk, ml = _key(model_key)
+        k, v = C.c_void_p(), C.c_void_p()
+        self._rc(self.lib.soso_hip_decode_kv_dev(self.h, mk, ml, layer, C.byref(k), C.byref(v)), "decode_kv_dev")
+        return k.value, v.value
+
+    def decode_step_dev(self, model_key, x_dev, pos, logits_dev=None, token_dev=None):
+        mk, ml = _key(model_key)
+        return self._rc(self.lib.soso_hip_decode_step_dev(self.h, mk, ml, x_dev, pos, logits_dev, token_dev),
+                        f"decode_step_dev {model_key}")
+
+    def decode_destroy(self, model_key):
+        mk, ml = _key(model_key)
+        return self._rc(self.lib.soso_hip_decode_destroy(self.h, mk, ml), "decode_destroy")

@@ -1,0 +1,173 @@
+"""GPU parity of the device-resident dense decode step (configs[4]'s path).
+
+Reference: LayerExecutor::forward_layer, dense GQA branch
+(crates/soso-llm-core/src/layer.rs:1092-1389) -- rmsnorm (gemm.rs:93-100),
+q/k/v matvecs, rope_cabezas non-NeoX (gemm.rs:1452-1490), KV append, decode
+attention, o-proj + residual, ffn_norm, gate/up, swiglu (gemm.rs:210-226),
+down + residual -- then Runtime::logits_gpu + argmax (runtime.rs:1976-2028,
+last maximum wins).  The CPU side composes the oracle's restatements of those
+functions; the KV cache is f32 on both sides.
+
+Weights: f32 ~ N(0, 0.05) quantized with the reference quantizers
+(quant.rs restated in the oracle): Q4_K projections, Q8_0 head (the path soso
+runs after converting Q6_K heads to Q8_0, gguf2som/src/lib.rs:1592-1609).
+
+Bar: K/V rows written at `pos` and the logits within relative L2 1e-5, the
+greedy token identical.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+Q4K, Q8, F32 = 3, 2, 1
+HD = 128
+
+
+def quant(orc, dtype, w):
+    w = np.ascontiguousarray(w, np.float32).ravel()
+    rb = orc.row_bytes(dtype, 256 if dtype == Q4K else 32)
+    out = np.zeros(w.size // (256 if dtype == Q4K else 32) * rb, np.uint8)
+    fn = orc.lib().or_quantize_q4_k if dtype == Q4K else orc.lib().or_quantize_q8_0
+    fn(w.ctypes.data, w.size, out.ctypes.data)
+    return out
+
+
+class Model:
+    def __init__(self, orc, L, H, nh, nkv, F, V, seed):
+        self.L, self.H, self.nh, self.nkv, self.F, self.V = L, H, nh, nkv, F, V
+        self.qd, self.kvd = nh * HD, nkv * HD
+        self.name = f"dec{seed}.{L}.{H}.{nh}.{nkv}.{F}.{V}"
+        self.layers = []
+        s = 0
+        for l in range(L):
+            def mat(rows, cols):
+                nonlocal s
+                s += 1
+                return quant(orc, Q4K, orc.normal(rows * cols, 0.05, seed, s))
+            s += 2
+            self.layers.append({
+                "attn_norm": (1.0 + orc.normal(H, 0.1, seed, s - 1)).astype(np.float32),
+                "ffn_norm": (1.0 + orc.normal(H, 0.1, seed, s)).astype(np.float32),
+                "q": mat(self.qd, H), "k": mat(self.kvd, H), "v": mat(self.kvd, H), "o": mat(H, self.qd),
+                "gate": mat(F, H), "up": mat(F, H), "down": mat(H, F),
+            })
+        self.out_norm = (1.0 + orc.normal(H, 0.1, seed, 9000)).astype(np.float32)
+        self.head = quant(orc, Q8, orc.normal(V * H, 0.05, seed, 9001))
+
+    def shapes(self, name):
+        H, F, qd, kvd = self.H, self.F, self.qd, self.kvd
+        return {"q": (Q4K, qd, H), "k": (Q4K, kvd, H), "v": (Q4K, kvd, H), "o": (Q4K, H, qd),
+                "gate": (Q4K, F, H), "up": (Q4K, F, H), "down": (Q4K, H, F),
+                "attn_norm": (F32, 1, H), "ffn_norm": (F32, 1, H)}[name]
+
+    def upload(self, gpu):
+        def put(key, arr, dtype, rows, cols):
+            b = np.ascontiguousarray(arr).view(np.uint8)
+            d = gpu.dev_alloc(b.size)
+            try:
+                gpu.h2d(d, b)
+                gpu.weight_from_dev(key, d, b.size, dtype, rows, cols)
+            finally:
+                gpu.dev_free(d)
+        keys = []
+        for l, lw in enumerate(self.layers):
+            for nm in ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down"):
+                k = f"{self.name}.L{l}.{nm}"
+                put(k, lw[nm], *self.shapes(nm))
+                keys.append(k)
+        put(self.name + ".out_norm", self.out_norm, F32, 1, self.H)
+        put(self.name + ".head", self.head, Q8, self.V, self.H)
+        keys += [self.name + ".out_norm", self.name + ".head"]
+        self.keys = keys
+        return keys
+
+    def cpu_step(self, orc, x, kcache, vcache, pos, theta, eps):
+        """The dense layer stack on the CPU; kcache/vcache [L][ctx][kvd] get row pos."""
+        L_ = orc.lib()
+        h = x.astype(np.float32).copy()
+        for l, lw in enumerate(self.layers):
+            xn = h.copy()
+            L_.or_rmsnorm(xn.ctypes.data, lw["attn_norm"].ctypes.data, self.H, np.float32(eps))
+            q = orc.matvec(Q4K, lw["q"], self.qd, self.H, xn)
+            k = orc.matvec(Q4K, lw["k"], self.kvd, self.H, xn)
+            v = orc.matvec(Q4K, lw["v"], self.kvd, self.H, xn)
+            L_.or_rope_heads(q.ctypes.data, self.nh, HD, pos, np.float32(theta), 0)
+            L_.or_rope_heads(k.ctypes.data, self.nkv, HD, pos, np.float32(theta), 0)
+            kcache[l, pos] = k
+            vcache[l, pos] = v
+            att = np.zeros(self.qd, np.float32)
+            Kc = np.ascontiguousarray(kcache[l, :pos + 1])
+            Vc = np.ascontiguousarray(vcache[l, :pos + 1])
+            g = self.nh // self.nkv
+            for hh in range(self.nh):
+                qh = np.ascontiguousarray(q[hh * HD:(hh + 1) * HD])
+                out = np.zeros(HD, np.float32)
+                L_.or_attention_f32(qh.ctypes.data, Kc.ctypes.data, Vc.ctypes.data, HD, self.kvd, hh // g, pos + 1,
+                                    out.ctypes.data)
+                att[hh * HD:(hh + 1) * HD] = out
+            h = h + orc.matvec(Q4K, lw["o"], self.H, self.qd, att)
+            xn = h.copy()
+            L_.or_rmsnorm(xn.ctypes.data, lw["ffn_norm"].ctypes.data, self.H, np.float32(eps))
+            gt = orc.matvec(Q4K, lw["gate"], self.F, self.H, xn)
+            up = orc.matvec(Q4K, lw["up"], self.F, self.H, xn)
+            L_.or_swiglu(up.ctypes.data, gt.ctypes.data, self.F)
+            h = orc.matvec(Q4K, lw["down"], self.H, self.F, up) + h
+        xn = h.copy()
+        L_.or_rmsnorm(xn.ctypes.data, self.out_norm.ctypes.data, self.H, np.float32(eps))
+        logits = orc.matvec(Q8, self.head, self.V, self.H, xn)
+        return logits, int(L_.or_argmax(logits.ctypes.data, logits.size))
+
+
+@pytest.mark.parametrize("L,H,nh,nkv,F,V,prefill", [
+    (2, 512, 4, 2, 1024, 1000, 100),   # GQA group 2, two attention chunks
+    (1, 1024, 8, 2, 2048, 512, 200),   # GQA group 4 (the 8B's ratio)
+])
+def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill):
+    theta, eps, ctx = 500000.0, 1e-5, 256
+    m = Model(orc, L, H, nh, nkv, F, V, 50 + L)
+    m.upload(gpu)
+    name = m.name + ".model"
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=theta, rms_eps=eps)
+    gpu.decode_create(name, cfg, m.keys)
+    kc = np.zeros((L, ctx, m.kvd), np.float32)
+    vc = np.zeros((L, ctx, m.kvd), np.float32)
+    for l in range(L):
+        kc[l, :prefill] = orc.normal(prefill * m.kvd, 1.0, 60 + l, 1).reshape(prefill, m.kvd)
+        vc[l, :prefill] = orc.normal(prefill * m.kvd, 1.0, 60 + l, 2).reshape(prefill, m.kvd)
+        kd, vd = gpu.decode_kv_dev(name, l)
+        gpu.h2d(kd, kc[l])
+        gpu.h2d(vd, vc[l])
+    x = orc.normal(H, 1.0, 70, 1)
+    xd = gpu.dev_alloc(H * 4)
+    ld = gpu.dev_alloc(V * 4)
+    td = gpu.dev_alloc(4)
+    try:
+        gpu.h2d(xd, x)
+        gpu.decode_step_dev(name, xd, prefill, ld, td)
+        gpu.sync()
+        logits = gpu.d2h(ld, (V,), np.float32)
+        token = int(gpu.d2h(td, (1,), np.uint32)[0])
+        kgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[0], (ctx, m.kvd), np.float32)[prefill] for l in range(L)]
+        vgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[1], (ctx, m.kvd), np.float32)[prefill] for l in range(L)]
+        ref_logits, ref_token = m.cpu_step(orc, x, kc, vc, prefill, theta, eps)
+        for l in range(L):
+            assert orc.rel_l2(kgpu[l], kc[l, prefill]) < 1e-5, l
+            assert orc.rel_l2(vgpu[l], vc[l, prefill]) < 1e-5, l
+        assert orc.rel_l2(logits, ref_logits) < 1e-5, orc.rel_l2(logits, ref_logits)
+        top2 = np.sort(ref_logits)[-2:]
+        if top2[1] - top2[0] > 1e-3 * max(1.0, abs(float(top2[1]))):
+            assert token == ref_token
+        # a second step at pos + 1 sees the row written by the first
+        gpu.decode_step_dev(name, xd, prefill + 1, ld, td)
+        gpu.sync()
+        logits2 = gpu.d2h(ld, (V,), np.float32)
+        ref2, _ = m.cpu_step(orc, x, kc, vc, prefill + 1, theta, eps)
+        assert orc.rel_l2(logits2, ref2) < 1e-5
+    finally:
+        for p in (xd, ld, td):
+            gpu.dev_free(p)
+        gpu.decode_destroy(name)
+        for k in m.keys:
+            gpu.weight_drop(k)
