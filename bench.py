@@ -160,6 +160,80 @@ def time_moe(g, n, steps, layers=4, n_x=8, seed=11):
             g.weight_drop(name + ".router")
 
 
+def time_decode_8b(g, steps, ctx=4096, seed=21):
+    """one greedy decode step of a random-init Llama-style 8B
+    (32 layers, hidden 4096, 32 q / 8 KV heads of 128, RoPE theta 5e5,
+    SwiGLU 14336, RMSNorm eps 1e-5, Q4_K projections, Q6_K head over 128256)
+    with an f32 KV cache prefilled with N(0, 1) to `ctx` positions; the step
+    runs at position `ctx`.  Returns (ms per token, bytes per token, token)."""
+    L, H, NH, NKV, HDIM, F, V = 32, 4096, 32, 8, 128, 14336, 128256
+    qd, kvd = NH * HDIM, NKV * HDIM
+    name = "llama8b"
+    keys = []
+
+    def norm(key, s):
+        d = g.dev_alloc(H * 4)
+        try:
+            g.synth_normal(d, H, 1.0, seed, s)
+            g.weight_from_dev(key, d, H * 4, F32, 1, H)
+        finally:
+            g.dev_free(d)
+
+    s = 0
+    for l in range(L):
+        for nm, rows, cols in (("attn_norm", 1, H), ("q", qd, H), ("k", kvd, H), ("v", kvd, H), ("o", H, qd),
+                               ("ffn_norm", 1, H), ("gate", F, H), ("up", F, H), ("down", H, F)):
+            k = f"{name}.L{l}.{nm}"
+            s += 1
+            if rows == 1:
+                norm(k, s)
+            else:
+                g.weight_synth(k, Q4K, rows, cols, seed, s)
+            keys.append(k)
+    norm(name + ".out_norm", 10000)
+    g.weight_synth(name + ".head", Q6K, V, H, seed, 10001)
+    keys += [name + ".out_norm", name + ".head"]
+    cfg = dict(n_layers=L, hidden=H, n_heads=NH, n_kv_heads=NKV, head_dim=HDIM, ffn=F, vocab=V, ctx_max=ctx + 1,
+               rope_theta=500000.0, rms_eps=1e-5)
+    g.decode_create(name, cfg, keys, drop_sources=True)
+    x = g.dev_alloc(H * 4)
+    tok = g.dev_alloc(4)
+    try:
+        for l in range(L):
+            kd, vd = g.decode_kv_dev(name, l)
+            g.synth_normal(kd, ctx * kvd, 1.0, seed + 1, 2 * l)
+            g.synth_normal(vd, ctx * kvd, 1.0, seed + 1, 2 * l + 1)
+        g.synth_normal(x, H, 1.0, seed + 2, 0)
+        for _ in range(3):
+            g.decode_step_dev(name, x, ctx, None, tok)
+        g.sync()
+        gid = _capture(g, lambda: [g.decode_step_dev(name, x, ctx, None, tok) for _ in range(steps)])
+        try:
+            g.graph_launch(gid)
+            g.sync()
+            g.event_record(0)
+            g.graph_launch(gid)
+            g.event_record(1)
+            g.sync()
+        finally:
+            g.graph_destroy(gid)
+        ms = g.event_elapsed(0, 1) / steps
+        token = int(g.d2h(tok, (1,), np.uint32)[0])
+        per_layer = (qd + 2 * kvd) * (H // 256) * 144 + H * (qd // 256) * 144 + 2 * F * (H // 256) * 144 \
+            + H * (F // 256) * 144
+        nbytes = L * per_layer + V * (H // 256) * 210 + L * 2 * (ctx + 1) * kvd * 4 + (2 * L + 1) * H * 4
+        return ms, nbytes, token
+    finally:
+        g.dev_free(x)
+        g.dev_free(tok)
+        g.decode_destroy(name)
+        for k in keys:
+            try:
+                g.weight_drop(k)
+            except Exception:  # noqa: BLE001 -- dropped with the sources
+                pass
+
+
 def copy_calibration(g, nbytes=512 << 20, reps=20):
     """A plain device-to-device copy of known size, for scaling rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters (run under --pmc)."""
@@ -261,6 +335,11 @@ def main():
                 "us_per_layer": round(ms_m * 1e3, 3), "tokens_per_s_layer": round(n / (ms_m * 1e-3), 1),
                 "GB_s": round(b_m / (ms_m * 1e-3) / 1e9, 1), "frac_hbm": round(b_m / (ms_m * 1e-3) / 1e9 / PEAK_GBS, 4),
                 "bytes": int(b_m), "distinct_experts": round(u_m, 2)}
+        ms_d, b_d, tok_d = time_decode_8b(g, max(10, args.steps // 50))
+        extra["llama8b_decode_ctx4096"] = {
+            "ms_per_token": round(ms_d, 4), "tokens_per_s": round(1e3 / ms_d, 1),
+            "GB_s": round(b_d / (ms_d * 1e-3) / 1e9, 1), "frac_hbm": round(b_d / (ms_d * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "bytes_per_token": int(b_d), "greedy_token": tok_d}
         line["configs"] = extra
     if not args.no_cpu:
         gbs, n, ms = cpu_baseline(Q4K, rows, cols, args.cpu_seconds, args.cpu_threads)
