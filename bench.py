@@ -201,8 +201,8 @@ def time_decode_8b(g, steps, ctx=4096, seed=21):
     try:
         for l in range(L):
             kd, vd = g.decode_kv_dev(name, l)
-            g.synth_normal(kd, ctx * kvd, 1.0, seed + 1, 2 * l)
-            g.synth_normal(vd, ctx * kvd, 1.0, seed + 1, 2 * l + 1)
+            g.synth_normal(kd, (ctx + 1) * kvd, 1.0, seed + 1, 2 * l)
+            g.synth_normal(vd, (ctx + 1) * kvd, 1.0, seed + 1, 2 * l + 1)
         g.synth_normal(x, H, 1.0, seed + 2, 0)
         for _ in range(3):
             g.decode_step_dev(name, x, ctx, None, tok)

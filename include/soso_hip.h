@@ -171,8 +171,9 @@ typedef struct soso_hip_decode_cfg {
 } soso_hip_decode_cfg;
 int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
                            const char *const *keys, const size_t *key_lens, int drop_sources);
-/* Device pointers of layer `layer`'s K and V caches, each [ctx_max x kv_dim] f32
- * (position-major), for prefilling and inspection. */
+/* Device pointers of layer `layer`'s K and V caches, each f32 and head-major:
+ * [n_kv_heads][ctx_max][head_dim] (a head's positions are contiguous), for
+ * prefilling and inspection. */
 int soso_hip_decode_kv_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, float **k_dev,
                            float **v_dev);
 /* One token at position `pos` (KV rows 0..pos-1 already filled): hidden = x_dev

@@ -71,7 +71,7 @@ struct DecodeModel {
     const float *out_norm = nullptr;
     const Weight *head = nullptr;
     std::vector<std::string> uses; // keys of the resident weights the model reads
-    float *kcache = nullptr, *vcache = nullptr; // [n_layers][ctx_max][kv_dim]
+    float *kcache = nullptr, *vcache = nullptr; // [n_layers][n_kv_heads][ctx_max][head_dim]
     void *mem = nullptr;                         // activations below, one allocation
     float *hid = nullptr, *qbuf = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
 };
@@ -91,7 +91,9 @@ struct soso_hip {
     static constexpr int N_SCRATCH = 12;
     void *scratch[N_SCRATCH] = {};
     size_t scratch_cap[N_SCRATCH] = {};
-    unsigned *ticket = nullptr; // zero between launches of the "last workgroup" kernels
+    // 4 KiB: a counter at offset 0 that is zero between launches of the "last
+    // workgroup" kernels (each resets it), then 2 KiB of per-workgroup partials
+    unsigned *ticket = nullptr;
     std::unordered_map<std::string, MoeLayer> moe_layers;
     std::unordered_map<std::string, DecodeModel> decode_models;
     std::vector<hipEvent_t> events; // per-launch timing slots
@@ -117,8 +119,11 @@ struct MvEpi {
     // EPI_QKV: rows [0, q_dim) -> y rotated, [q_dim, q_dim + kv_dim) -> k_out
     // rotated, the next kv_dim -> v_out; RoPE of pairs (2i, 2i+1) inside each
     // head_dim block at position pos (non-NeoX, gemm.rs:1452-1490)
+    // (K/V caches head-major: element d of KV head j at position pos is at
+    // j * kv_stride + pos * head_dim + d)
     float *k_out = nullptr, *v_out = nullptr;
     int q_dim = 0, kv_dim = 0, head_dim = 0, pos = 0;
+    size_t kv_stride = 0;
     float theta = 0.0f;
 };
 
@@ -136,7 +141,7 @@ int launch_dequant(soso_hip *h, const Weight &w, float *out_dev);
 int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
 // (k_decode.hip)
 int launch_attention(soso_hip *h, const float *q, const float *K, const float *V, int n_heads, int n_kv_heads,
-                     int head_dim, int T, float *part, float *out);
+                     int head_dim, int ctx, int T, float *part, float *out);
 int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token);
 // (k_synth.hip)
 int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,

@@ -28,47 +28,57 @@
 constexpr int ATT_HD = 128;   // head_dim handled
 constexpr int ATT_CHUNK = 64; // positions per split
 
-// grid (n_kv_heads, chunks), block 64 * G: q heads g*G .. g*G + G - 1 share
-// KV head g (GQA).  Scores s = (q . k) / sqrt(hd); per chunk: m = max s,
+// grid (n_kv_heads, chunks), block 256: q heads g*G .. g*G + G - 1 share KV
+// head g (GQA).  Scores s = (q . k) / sqrt(hd); per chunk: m = max s,
 // p = exp(s - m), l = sum p, acc = sum p v.  part[(head * chunks + c) *
-// (HD + 2)] = {m, l, acc[0..HD)}.  K, V: [T][kv_dim] of one layer.
+// (HD + 2)] = {m, l, acc[0..HD)}.  K, V of one layer are head-major:
+// [n_kv_heads][ctx][HD], so a chunk of one head is 32 KB of contiguous HBM.
+// Wavefront w owns positions t0 + 16w .. t0 + 16w + 15 of the chunk for all G
+// heads: its V rows are requested first, then its K rows, so both streams are
+// in flight together; every K and V byte is read once.
 template <int G>
-__global__ void __launch_bounds__(64 * G) k_attn_split(const float *__restrict__ q, const float *__restrict__ K,
-                                                        const float *__restrict__ V, int kv_dim, int T, int chunks,
-                                                        float *__restrict__ part)
+__global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q, const float *__restrict__ K,
+                                                     const float *__restrict__ V, int ctx, int T, int chunks,
+                                                     float *__restrict__ part)
 {
-    constexpr int HD = ATT_HD;
+    constexpr int HD = ATT_HD, NW = 4;
     __shared__ float qs[G][HD];
     __shared__ float sc[G][ATT_CHUNK];
+    __shared__ float2 accs[NW][G][HD / 2];
     const int g = blockIdx.x, c = blockIdx.y;
-    const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK);
+    const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK), n = t1 - t0;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    for (int i = threadIdx.x; i < G * HD; i += 64 * G) qs[i / HD][i % HD] = q[(size_t)g * G * HD + i];
+    const int tw = t0 + 16 * wave; // this wavefront's 16 positions
+    // V rows: lane holds dims 2l, 2l+1 of each of the 16 positions
+    float2 vr[16];
+    const float *vb = V + (size_t)g * ctx * HD + 2 * lane;
+#pragma unroll
+    for (int k = 0; k < 16; k++)
+        vr[k] = tw + k < t1 ? *(const float2 *)(vb + (size_t)(tw + k) * HD) : make_float2(0.f, 0.f);
+    // K rows: 4 lanes per position; lane j reads the float4s 4j + 16i (i < 8)
+    const int pp = lane >> 2, j = lane & 3, t = tw + pp;
+    float4 kv[8];
+    {
+        const float4 *k4 = (const float4 *)(K + ((size_t)g * ctx + (t < t1 ? t : t0)) * HD);
+#pragma unroll
+        for (int i = 0; i < 8; i++) kv[i] = k4[4 * i + j];
+    }
+    for (int i = threadIdx.x; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)g * G * HD + i];
     __syncthreads();
     const float inv = 1.0f / sqrtf((float)HD);
-    // scores: 16 positions per wavefront pass, 4 lanes per position; lane j of
-    // a position reads the float4s 4j + 16i (i < 8) of the key (64 B runs)
-    const int pp = lane >> 2, j = lane & 3;
-    for (int sl = wave; sl < ATT_CHUNK / 16; sl += G) {
-        const int t = t0 + 16 * sl + pp;
+    {
         float acc[G];
 #pragma unroll
         for (int hh = 0; hh < G; hh++) acc[hh] = 0.0f;
-        if (t < t1) {
-            const float4 *k4 = (const float4 *)(K + (size_t)t * kv_dim + (size_t)g * HD);
-            float4 kv[8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) kv[i] = k4[4 * i + j];
+        for (int i = 0; i < 8; i++) {
+            const int d = 16 * i + 4 * j;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int d = 16 * i + 4 * j;
-#pragma unroll
-                for (int hh = 0; hh < G; hh++) {
-                    acc[hh] = fmaf(kv[i].x, qs[hh][d], acc[hh]);
-                    acc[hh] = fmaf(kv[i].y, qs[hh][d + 1], acc[hh]);
-                    acc[hh] = fmaf(kv[i].z, qs[hh][d + 2], acc[hh]);
-                    acc[hh] = fmaf(kv[i].w, qs[hh][d + 3], acc[hh]);
-                }
+            for (int hh = 0; hh < G; hh++) {
+                acc[hh] = fmaf(kv[i].x, qs[hh][d], acc[hh]);
+                acc[hh] = fmaf(kv[i].y, qs[hh][d + 1], acc[hh]);
+                acc[hh] = fmaf(kv[i].z, qs[hh][d + 2], acc[hh]);
+                acc[hh] = fmaf(kv[i].w, qs[hh][d + 3], acc[hh]);
             }
         }
 #pragma unroll
@@ -81,99 +91,121 @@ __global__ void __launch_bounds__(64 * G) k_attn_split(const float *__restrict__
     }
     __syncthreads();
     // softmax statistics of the chunk, one wavefront per head
-    const int n = t1 - t0;
-    if (wave < G) {
-        const float s = lane < n ? sc[wave][lane] : -INFINITY;
+    for (int hh = wave; hh < G; hh += NW) {
+        const float s = lane < n ? sc[hh][lane] : -INFINITY;
         const float m = wave_max(s);
         const float p = lane < n ? expf(s - m) : 0.0f;
         const float l = seg_sum<64>(p);
-        sc[wave][lane] = p;
+        sc[hh][lane] = p;
         if (lane == 0) {
-            float *o = part + ((size_t)(g * G + wave) * chunks + c) * (HD + 2);
+            float *o = part + ((size_t)(g * G + hh) * chunks + c) * (HD + 2);
             o[0] = m;
             o[1] = l;
         }
     }
     __syncthreads();
-    // acc[h][d] = sum_t p[h][t] v[t][d]: wavefront = head, lane = dims 2l, 2l+1
-    if (wave < G) {
+    // acc[h] over this wavefront's positions, then across the wavefronts
+#pragma unroll
+    for (int hh = 0; hh < G; hh++) {
         float2 a = make_float2(0.f, 0.f);
-        const float *vb = V + (size_t)g * HD + 2 * lane;
-        for (int tb = 0; tb < n; tb += 16) {
-            float2 v[16];
 #pragma unroll
-            for (int k = 0; k < 16; k++)
-                v[k] = tb + k < n ? *(const float2 *)(vb + (size_t)(t0 + tb + k) * kv_dim) : make_float2(0.f, 0.f);
-#pragma unroll
-            for (int k = 0; k < 16; k++) {
-                const float pk = tb + k < n ? sc[wave][tb + k] : 0.0f;
-                a.x = fmaf(pk, v[k].x, a.x);
-                a.y = fmaf(pk, v[k].y, a.y);
-            }
+        for (int k = 0; k < 16; k++) {
+            const float pk = tw + k < t1 ? sc[hh][16 * wave + k] : 0.0f;
+            a.x = fmaf(pk, vr[k].x, a.x);
+            a.y = fmaf(pk, vr[k].y, a.y);
         }
-        float *o = part + ((size_t)(g * G + wave) * chunks + c) * (HD + 2) + 2;
-        *(float2 *)(o + 2 * lane) = a;
+        accs[wave][hh][lane] = a;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < G * HD / 2; e += 256) {
+        const int hh = e / (HD / 2), dl = e % (HD / 2);
+        float2 a = accs[0][hh][dl];
+#pragma unroll
+        for (int w = 1; w < NW; w++) {
+            a.x += accs[w][hh][dl].x;
+            a.y += accs[w][hh][dl].y;
+        }
+        float *o = part + ((size_t)(g * G + hh) * chunks + c) * (HD + 2) + 2;
+        *(float2 *)(o + 2 * dl) = a;
     }
 }
 
-// grid n_heads, block HD: out[h*HD + d] = sum_c e^{m_c - M} acc_c[d] /
-// sum_c e^{m_c - M} l_c.
-__global__ void __launch_bounds__(ATT_HD) k_attn_combine(const float *__restrict__ part, int chunks,
-                                                          float *__restrict__ out)
+// grid n_heads, block 8 * HD: out[h*HD + d] = sum_c e^{m_c - M} acc_c[d] /
+// sum_c e^{m_c - M} l_c.  The 8 thread groups split the chunks (c = g mod 8)
+// so a head's partials are read with up to 16 loads in flight per thread.
+constexpr int CMB_G = 8;
+
+__global__ void __launch_bounds__(CMB_G * ATT_HD) k_attn_combine(const float *__restrict__ part, int chunks,
+                                                                  float *__restrict__ out)
 {
-    constexpr int HD = ATT_HD;
+    constexpr int HD = ATT_HD, NT = CMB_G * HD;
     __shared__ float wsh[1024];
-    __shared__ float red[2];
-    const int h = blockIdx.x, d = threadIdx.x;
+    __shared__ float red[NT / 64];
+    __shared__ float accs[CMB_G][HD];
+    const int h = blockIdx.x, tid = threadIdx.x, grp = tid / HD, d = tid % HD, lane = tid & 63, wave = tid >> 6;
     const float *ph = part + (size_t)h * chunks * (HD + 2);
     float m = -INFINITY;
-    for (int c = d; c < chunks; c += HD) m = fmaxf(m, ph[(size_t)c * (HD + 2)]);
+    for (int c = tid; c < chunks; c += NT) m = fmaxf(m, ph[(size_t)c * (HD + 2)]);
     m = wave_max(m);
-    if ((d & 63) == 0) red[d >> 6] = m;
+    if (lane == 0) red[wave] = m;
     __syncthreads();
-    const float M = fmaxf(red[0], red[1]);
+    float M = red[0];
+    for (int w = 1; w < NT / 64; w++) M = fmaxf(M, red[w]);
+    __syncthreads();
     float l = 0.0f;
-    for (int c = d; c < chunks; c += HD) {
+    for (int c = tid; c < chunks; c += NT) {
         const float w = expf(ph[(size_t)c * (HD + 2)] - M);
         wsh[c] = w;
         l += w * ph[(size_t)c * (HD + 2) + 1];
     }
     l = seg_sum<64>(l);
+    if (lane == 0) red[wave] = l;
     __syncthreads();
-    if ((d & 63) == 0) red[d >> 6] = l;
-    __syncthreads();
-    const float L = red[0] + red[1];
+    float L = 0.0f;
+    for (int w = 0; w < NT / 64; w++) L += red[w];
     float a = 0.0f;
-    for (int c0 = 0; c0 < chunks; c0 += 8) {
-        float v[8];
+    for (int c0 = grp; c0 < chunks; c0 += CMB_G * 16) {
+        float v[16];
 #pragma unroll
-        for (int k = 0; k < 8; k++) v[k] = c0 + k < chunks ? ph[(size_t)(c0 + k) * (HD + 2) + 2 + d] : 0.0f;
+        for (int k = 0; k < 16; k++) {
+            const int c = c0 + CMB_G * k;
+            v[k] = c < chunks ? ph[(size_t)c * (HD + 2) + 2 + d] : 0.0f;
+        }
 #pragma unroll
-        for (int k = 0; k < 8; k++)
-            if (c0 + k < chunks) a = fmaf(wsh[c0 + k], v[k], a);
+        for (int k = 0; k < 16; k++) {
+            const int c = c0 + CMB_G * k;
+            if (c < chunks) a = fmaf(wsh[c], v[k], a);
+        }
     }
-    out[(size_t)h * HD + d] = L > 0.0f ? a / L : 0.0f;
+    accs[grp][d] = a;
+    __syncthreads();
+    if (grp == 0) {
+        float t = 0.0f;
+#pragma unroll
+        for (int g = 0; g < CMB_G; g++) t += accs[g][d];
+        out[(size_t)h * HD + d] = L > 0.0f ? t / L : 0.0f;
+    }
 }
 
 int launch_attention(soso_hip *h, const float *q, const float *K, const float *V, int n_heads, int n_kv_heads,
-                     int head_dim, int T, float *part, float *out)
+                     int head_dim, int ctx, int T, float *part, float *out)
 {
     if (head_dim != ATT_HD || n_kv_heads <= 0 || n_heads % n_kv_heads || T <= 0)
         return set_err(h, SOSO_HIP_DECLINED, "attention: head shape not handled here");
-    const int G = n_heads / n_kv_heads, kv_dim = n_kv_heads * head_dim;
+    const int G = n_heads / n_kv_heads;
     const int chunks = (T + ATT_CHUNK - 1) / ATT_CHUNK;
     if (chunks > 1024) return set_err(h, SOSO_HIP_DECLINED, "attention: context longer than 65536");
     const dim3 grid((unsigned)n_kv_heads, (unsigned)chunks);
     switch (G) {
-    case 1: k_attn_split<1><<<grid, 64, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
-    case 2: k_attn_split<2><<<grid, 128, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
-    case 4: k_attn_split<4><<<grid, 256, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
-    case 8: k_attn_split<8><<<grid, 512, 0, h->stream>>>(q, K, V, kv_dim, T, chunks, part); break;
+    case 1: k_attn_split<1><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
+    case 2: k_attn_split<2><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
+    case 4: k_attn_split<4><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
+    case 8: k_attn_split<8><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
     default: return set_err(h, SOSO_HIP_DECLINED, "attention: GQA group size not handled here");
     }
     int rc = hip_check(h, hipGetLastError(), "attention split launch");
     if (rc != SOSO_HIP_OK) return rc;
-    k_attn_combine<<<(unsigned)n_heads, ATT_HD, 0, h->stream>>>(part, chunks, out);
+    k_attn_combine<<<(unsigned)n_heads, CMB_G * ATT_HD, 0, h->stream>>>(part, chunks, out);
     return hip_check(h, hipGetLastError(), "attention combine launch");
 }
 
@@ -194,8 +226,9 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         in.norm_w = L.attn_norm;
         in.eps = m.eps;
         MvEpi ep;
-        ep.k_out = K + (size_t)pos * kv_dim;
-        ep.v_out = V + (size_t)pos * kv_dim;
+        ep.k_out = K;
+        ep.v_out = V;
+        ep.kv_stride = m.ctx_max * m.head_dim;
         ep.q_dim = q_dim;
         ep.kv_dim = kv_dim;
         ep.head_dim = (int)m.head_dim;
@@ -203,8 +236,8 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         ep.theta = m.theta;
         rc = launch_matvec_ex(h, *L.qkv, in, qb, ep, XS_RMSNORM, EPI_QKV);
         if (rc == SOSO_HIP_OK)
-            rc = launch_attention(h, qb, K, V, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim, (int)pos + 1, m.part,
-                                  att);
+            rc = launch_attention(h, qb, K, V, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim, (int)m.ctx_max,
+                                  (int)pos + 1, m.part, att);
         if (rc == SOSO_HIP_OK) {
             MvIn a;
             a.x = att;

@@ -202,10 +202,16 @@ __device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows
                 const float a = even ? yacc : other, b = even ? other : yacc;
                 const float v = even ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn))
                                      : __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
-                if (r < ep.q_dim) y[r] = v;
-                else ep.k_out[r - ep.q_dim] = v;
+                if (r < ep.q_dim) {
+                    y[r] = v;
+                } else {
+                    const int e = r - ep.q_dim;
+                    ep.k_out[(size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + d] = v;
+                }
             } else {
-                ep.v_out[r - qk] = yacc;
+                const int e = r - qk;
+                ep.v_out[(size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + e % ep.head_dim] =
+                    yacc;
             }
         }
     }
@@ -696,37 +702,43 @@ int launch_dequant(soso_hip *h, const Weight &w, float *out)
 // ---------------------------------------------------------------------------
 // argmax (crates/soso-llm-core/src/runtime.rs:2021-2028): the LAST maximum
 // wins.  Combining ordered segments as "earlier wins only if strictly
-// greater" reproduces the sequential fold for finite inputs.
+// greater" reproduces the sequential fold for finite inputs.  Every
+// workgroup reduces one contiguous segment; the last one to finish (ticket)
+// combines the segments' winners in order.
 // ---------------------------------------------------------------------------
-__global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, int n, uint32_t *__restrict__ out)
+constexpr int ARGMAX_WG = 256; // workgroups (<= the block size; partials: 2 KiB after the ticket)
+
+__device__ __forceinline__ void keep_later(float &bv, int &bi, float ov, int oi)
 {
-    __shared__ float sv[16];
-    __shared__ int si[16];
-    const int tid = threadIdx.x, nt = blockDim.x;
-    // contiguous chunk per thread keeps the combine order simple
-    const int c0 = (int)((long)n * tid / nt), c1 = (int)((long)n * (tid + 1) / nt);
+    // (bv, bi) is the earlier segment's winner; the later one replaces it
+    // unless the earlier is strictly greater
+    if (oi >= 0 && (bi < 0 || !(bv > ov))) {
+        bv = ov;
+        bi = oi;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_argmax(const float *__restrict__ x, int n, uint32_t *__restrict__ out,
+                                                unsigned *__restrict__ ticket)
+{
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    __shared__ int last;
+    float *pv = (float *)(ticket + 64);
+    int *pi = (int *)(ticket + 64 + ARGMAX_WG);
+    const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
+    const int s0 = (int)((long)n * blockIdx.x / gridDim.x), s1 = (int)((long)n * (blockIdx.x + 1) / gridDim.x);
+    const int c0 = s0 + (int)((long)(s1 - s0) * tid / nt), c1 = s0 + (int)((long)(s1 - s0) * (tid + 1) / nt);
     float bv = -INFINITY;
     int bi = -1;
-    for (int i = c0; i < c1; i++) {
-        const float v = x[i];
-        if (bi < 0 || !(bv > v)) {
-            bv = v;
-            bi = i;
-        }
-    }
-    // reduce over lanes (ordered: lower lane = earlier segment)
+    for (int i = c0; i < c1; i++) keep_later(bv, bi, x[i], i);
+    // lanes hold ordered segments: fold pairs (lower lane = earlier)
     for (int o = 1; o < 64; o <<= 1) {
         const float ov = __shfl_down(bv, o, 64);
         const int oi = __shfl_down(bi, o, 64);
-        const int lane = tid & 63;
-        if (lane + o < 64 && (lane & (2 * o - 1)) == 0 && oi >= 0) {
-            if (bi < 0 || !(bv > ov)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
+        if (lane + o < 64 && (lane & (2 * o - 1)) == 0) keep_later(bv, bi, ov, oi);
     }
-    if ((tid & 63) == 0) {
+    if (lane == 0) {
         sv[tid >> 6] = bv;
         si[tid >> 6] = bi;
     }
@@ -734,17 +746,44 @@ __global__ void __launch_bounds__(1024) k_argmax(const float *__restrict__ x, in
     if (tid == 0) {
         float v = sv[0];
         int i = si[0];
-        for (int w = 1; w < (nt >> 6); w++)
-            if (si[w] >= 0 && (i < 0 || !(v > sv[w]))) {
-                v = sv[w];
-                i = si[w];
-            }
+        for (int w = 1; w < (nt >> 6); w++) keep_later(v, i, sv[w], si[w]);
+        pv[blockIdx.x] = v;
+        pi[blockIdx.x] = i;
+        __threadfence();
+        last = atomicAdd(ticket, 1u) == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    // the segments' winners, in segment order, reduced by the same ordered tree
+    bv = -INFINITY;
+    bi = -1;
+    for (int b = tid; b < (int)gridDim.x; b += nt) keep_later(bv, bi, pv[b], pi[b]);
+    // thread t now holds segments t, t + nt, ...: with gridDim <= blockDim
+    // that is one segment per thread, in order
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_down(bv, o, 64);
+        const int oi = __shfl_down(bi, o, 64);
+        if (lane + o < 64 && (lane & (2 * o - 1)) == 0) keep_later(bv, bi, ov, oi);
+    }
+    __syncthreads();
+    if (lane == 0) {
+        sv[tid >> 6] = bv;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float v = sv[0];
+        int i = si[0];
+        for (int w = 1; w < (nt >> 6); w++) keep_later(v, i, sv[w], si[w]);
         *out = (uint32_t)(i < 0 ? 0 : i);
+        *ticket = 0u;
     }
 }
 
 int launch_argmax(soso_hip *h, const float *x, size_t n, uint32_t *idx)
 {
-    k_argmax<<<1, 1024, 0, h->stream>>>(x, (int)n, idx);
+    const unsigned grid = (unsigned)std::max<size_t>(1, std::min<size_t>(ARGMAX_WG, (n + 1023) / 1024));
+    k_argmax<<<grid, 256, 0, h->stream>>>(x, (int)n, idx, h->ticket);
     return hip_check(h, hipGetLastError(), "argmax launch");
 }

@@ -24,6 +24,12 @@ Q4K, Q8, F32 = 3, 2, 1
 HD = 128
 
 
+def head_major(kv, nkv):
+    """[ctx][nkv*HD] (position-major, as the CPU side keeps it) -> [nkv][ctx][HD]."""
+    ctx = kv.shape[0]
+    return np.ascontiguousarray(kv.reshape(ctx, nkv, HD).transpose(1, 0, 2))
+
+
 def quant(orc, dtype, w):
     w = np.ascontiguousarray(w, np.float32).ravel()
     rb = orc.row_bytes(dtype, 256 if dtype == Q4K else 32)
@@ -137,8 +143,8 @@ def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill):
         kc[l, :prefill] = orc.normal(prefill * m.kvd, 1.0, 60 + l, 1).reshape(prefill, m.kvd)
         vc[l, :prefill] = orc.normal(prefill * m.kvd, 1.0, 60 + l, 2).reshape(prefill, m.kvd)
         kd, vd = gpu.decode_kv_dev(name, l)
-        gpu.h2d(kd, kc[l])
-        gpu.h2d(vd, vc[l])
+        gpu.h2d(kd, head_major(kc[l], nkv))
+        gpu.h2d(vd, head_major(vc[l], nkv))
     x = orc.normal(H, 1.0, 70, 1)
     xd = gpu.dev_alloc(H * 4)
     ld = gpu.dev_alloc(V * 4)
@@ -149,8 +155,10 @@ def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill):
         gpu.sync()
         logits = gpu.d2h(ld, (V,), np.float32)
         token = int(gpu.d2h(td, (1,), np.uint32)[0])
-        kgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[0], (ctx, m.kvd), np.float32)[prefill] for l in range(L)]
-        vgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[1], (ctx, m.kvd), np.float32)[prefill] for l in range(L)]
+        kgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[0], (nkv, ctx, HD), np.float32)[:, prefill].ravel()
+                for l in range(L)]
+        vgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[1], (nkv, ctx, HD), np.float32)[:, prefill].ravel()
+                for l in range(L)]
         ref_logits, ref_token = m.cpu_step(orc, x, kc, vc, prefill, theta, eps)
         for l in range(L):
             assert orc.rel_l2(kgpu[l], kc[l, prefill]) < 1e-5, l
