@@ -13,7 +13,7 @@
 //                   written straight into the KV cache at `pos`
 //   2. k_attn_split split-K decode attention over 64-position chunks, the
 //                   G query heads of a KV head share every K/V read
-//   3. k_attn_combine  softmax-weighted merge of the chunks
+//   3. k_attn_merge softmax-weighted merge of the chunks
 //   4. o matvec     h += W_o . attn (residual in the epilogue)
 //   5. gate/up      x = rmsnorm(h); rows interleaved (gate_i, up_i); the
 //                   epilogue writes silu(gate_i) * up_i
@@ -28,173 +28,195 @@
 constexpr int ATT_HD = 128;   // head_dim handled
 constexpr int ATT_CHUNK = 64; // positions per split
 
-// grid (n_kv_heads, chunks), block 256: q heads g*G .. g*G + G - 1 share KV
-// head g (GQA).  Scores s = (q . k) / sqrt(hd); per chunk: m = max s,
-// p = exp(s - m), l = sum p, acc = sum p v.  part[(head * chunks + c) *
-// (HD + 2)] = {m, l, acc[0..HD)}.  K, V of one layer are head-major:
-// [n_kv_heads][ctx][HD], so a chunk of one head is 32 KB of contiguous HBM.
-// Wavefront w owns positions t0 + 16w .. t0 + 16w + 15 of the chunk for all G
-// heads: its V rows are requested first, then its K rows, so both streams are
-// in flight together; every K and V byte is read once.
+// Split-K decode attention: k_attn_split writes one (m, l, acc) per chunk of
+// 64 positions and query head, k_attn_merge combines the chunks.  (The merge
+// runs as its own launch: a merge by the last workgroup of each head in the
+// same launch needs a device-scope fence per wavefront, which writes back the
+// XCD's L2 each time and cost more than the launch it saves.)
+//
+// k_attn_split: grid (n_kv_heads, chunks), block 256.  Query heads g*G ..
+// g*G + G - 1 share KV head g (GQA), so every K/V byte is read once for all G
+// heads.  K, V of one layer are head-major, [n_kv_heads][ctx][HD]: a chunk of
+// one head is 32 KB of contiguous HBM.  Wavefront w owns positions t0 + 16w ..
+// t0 + 16w + 15.
+//
+// Load order per lane: its K rows, then q, then its V rows.  Loads complete in
+// issue order, so the scores start once K and q are in while V is still on
+// the way.  K: 8 lanes per position (128 B per lane group, whole cache lines),
+// two groups of 8 positions; V: lane holds dims 2l, 2l+1 of the 16 positions.
+// Positions past T are clamped onto the last valid row and get weight 0.
+//
+// Scores s = (q . k) / sqrt(HD).  Each wavefront keeps its own softmax
+// statistics (m_w = max s, p = e^{s - m_w}, l_w = sum p, acc_w = sum p v);
+// the four are merged in LDS into the chunk's (m, l, acc), stored at
+// part[(head * chunks + c) * (HD + 2)].
 template <int G>
 __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q, const float *__restrict__ K,
                                                      const float *__restrict__ V, int ctx, int T, int chunks,
                                                      float *__restrict__ part)
 {
     constexpr int HD = ATT_HD, NW = 4;
-    __shared__ float qs[G][HD];
-    __shared__ float sc[G][ATT_CHUNK];
+    __shared__ float qs[G * HD];
+    __shared__ float wm[NW][G], wl[NW][G];
     __shared__ float2 accs[NW][G][HD / 2];
-    const int g = blockIdx.x, c = blockIdx.y;
-    const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK), n = t1 - t0;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int tw = t0 + 16 * wave; // this wavefront's 16 positions
-    // V rows: lane holds dims 2l, 2l+1 of each of the 16 positions
-    float2 vr[16];
-    const float *vb = V + (size_t)g * ctx * HD + 2 * lane;
+    const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+    const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int tw = t0 + 16 * wave;
+    const float *Kh = K + (size_t)g * ctx * HD, *Vh = V + (size_t)g * ctx * HD;
+    const int pp = lane >> 3, j = lane & 7;
+    float4 kv[2][4];
 #pragma unroll
-    for (int k = 0; k < 16; k++)
-        vr[k] = tw + k < t1 ? *(const float2 *)(vb + (size_t)(tw + k) * HD) : make_float2(0.f, 0.f);
-    // K rows: 4 lanes per position; lane j reads the float4s 4j + 16i (i < 8)
-    const int pp = lane >> 2, j = lane & 3, t = tw + pp;
-    float4 kv[8];
-    {
-        const float4 *k4 = (const float4 *)(K + ((size_t)g * ctx + (t < t1 ? t : t0)) * HD);
+    for (int a = 0; a < 2; a++) {
+        const float4 *k4 = (const float4 *)(Kh + (size_t)min(tw + 8 * a + pp, t1 - 1) * HD);
 #pragma unroll
-        for (int i = 0; i < 8; i++) kv[i] = k4[4 * i + j];
+        for (int i = 0; i < 4; i++) kv[a][i] = k4[8 * i + j];
     }
-    for (int i = threadIdx.x; i < G * HD; i += 256) qs[i / HD][i % HD] = q[(size_t)g * G * HD + i];
+    __builtin_amdgcn_sched_barrier(0);
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < G * HD / 4) qv = ((const float4 *)(q + (size_t)g * G * HD))[tid];
+    __builtin_amdgcn_sched_barrier(0);
+    float2 vr[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) vr[k] = *(const float2 *)(Vh + (size_t)min(tw + k, t1 - 1) * HD + 2 * lane);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < G * HD / 4) *(float4 *)&qs[4 * tid] = qv;
     __syncthreads();
     const float inv = 1.0f / sqrtf((float)HD);
-    {
-        float acc[G];
-#pragma unroll
-        for (int hh = 0; hh < G; hh++) acc[hh] = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const int d = 16 * i + 4 * j;
-#pragma unroll
-            for (int hh = 0; hh < G; hh++) {
-                acc[hh] = fmaf(kv[i].x, qs[hh][d], acc[hh]);
-                acc[hh] = fmaf(kv[i].y, qs[hh][d + 1], acc[hh]);
-                acc[hh] = fmaf(kv[i].z, qs[hh][d + 2], acc[hh]);
-                acc[hh] = fmaf(kv[i].w, qs[hh][d + 3], acc[hh]);
-            }
-        }
-#pragma unroll
-        for (int hh = 0; hh < G; hh++) {
-            float v = acc[hh];
-            v += dpp_f<0xB1>(v);
-            v += dpp_f<0x4E>(v);
-            if (j == 0 && t < t1) sc[hh][t - t0] = v * inv;
-        }
-    }
-    __syncthreads();
-    // softmax statistics of the chunk, one wavefront per head
-    for (int hh = wave; hh < G; hh += NW) {
-        const float s = lane < n ? sc[hh][lane] : -INFINITY;
-        const float m = wave_max(s);
-        const float p = lane < n ? expf(s - m) : 0.0f;
-        const float l = seg_sum<64>(p);
-        sc[hh][lane] = p;
-        if (lane == 0) {
-            float *o = part + ((size_t)(g * G + hh) * chunks + c) * (HD + 2);
-            o[0] = m;
-            o[1] = l;
-        }
-    }
-    __syncthreads();
-    // acc[h] over this wavefront's positions, then across the wavefronts
 #pragma unroll
     for (int hh = 0; hh < G; hh++) {
-        float2 a = make_float2(0.f, 0.f);
+        float s[2];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 qq = *(const float4 *)&qs[hh * HD + 32 * i + 4 * j];
+                acc = fmaf(kv[a][i].x, qq.x, acc);
+                acc = fmaf(kv[a][i].y, qq.y, acc);
+                acc = fmaf(kv[a][i].z, qq.z, acc);
+                acc = fmaf(kv[a][i].w, qq.w, acc);
+            }
+            acc = seg_sum_dpp<8>(acc); // all 8 lanes of the position hold the sum
+            s[a] = tw + 8 * a + pp < t1 ? acc * inv : -INFINITY;
+        }
+        const float m = wave_max(fmaxf(s[0], s[1]));
+        float p[2];
+#pragma unroll
+        for (int a = 0; a < 2; a++) p[a] = s[a] == -INFINITY ? 0.0f : expf(s[a] - m);
+        float2 acc = make_float2(0.f, 0.f);
+        float l = 0.0f;
 #pragma unroll
         for (int k = 0; k < 16; k++) {
-            const float pk = tw + k < t1 ? sc[hh][16 * wave + k] : 0.0f;
-            a.x = fmaf(pk, vr[k].x, a.x);
-            a.y = fmaf(pk, vr[k].y, a.y);
+            const float pk = __builtin_bit_cast(
+                float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[k >> 3]), 8 * (k & 7)));
+            l += pk;
+            acc.x = fmaf(pk, vr[k].x, acc.x);
+            acc.y = fmaf(pk, vr[k].y, acc.y);
         }
-        accs[wave][hh][lane] = a;
+        accs[wave][hh][lane] = acc;
+        if (lane == 0) {
+            wm[wave][hh] = m;
+            wl[wave][hh] = l;
+        }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < G * HD / 2; e += 256) {
+    for (int e = tid; e < G * HD / 2; e += 256) {
         const int hh = e / (HD / 2), dl = e % (HD / 2);
-        float2 a = accs[0][hh][dl];
+        float M = wm[0][hh];
 #pragma unroll
-        for (int w = 1; w < NW; w++) {
-            a.x += accs[w][hh][dl].x;
-            a.y += accs[w][hh][dl].y;
+        for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w][hh]);
+        float L = 0.0f;
+        float2 a = make_float2(0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = wm[w][hh] == -INFINITY ? 0.0f : expf(wm[w][hh] - M);
+            L = fmaf(f, wl[w][hh], L);
+            a.x = fmaf(f, accs[w][hh][dl].x, a.x);
+            a.y = fmaf(f, accs[w][hh][dl].y, a.y);
         }
-        float *o = part + ((size_t)(g * G + hh) * chunks + c) * (HD + 2) + 2;
-        *(float2 *)(o + 2 * dl) = a;
+        float *o = part + ((size_t)(g * G + hh) * chunks + c) * (HD + 2);
+        if (dl == 0) {
+            o[0] = M;
+            o[1] = L;
+        }
+        *(float2 *)(o + 2 + 2 * dl) = a;
     }
 }
 
-// grid n_heads, block 8 * HD: out[h*HD + d] = sum_c e^{m_c - M} acc_c[d] /
-// sum_c e^{m_c - M} l_c.  The 8 thread groups split the chunks (c = g mod 8)
-// so a head's partials are read with up to 16 loads in flight per thread.
-constexpr int CMB_G = 8;
+// k_attn_merge: grid n_heads, block 256.  Wavefront w takes chunks w, w + 4,
+// ... in batches of MERGE_B, all loads of a batch in flight together, and
+// folds them into running (m, l, acc) (lane: dims 2l, 2l + 1); the four
+// wavefronts are then merged in LDS:
+//   out[h*HD + d] = sum_c e^{m_c - M} acc_c[d] / sum_c e^{m_c - M} l_c.
+constexpr int MERGE_B = 20;
 
-__global__ void __launch_bounds__(CMB_G * ATT_HD) k_attn_combine(const float *__restrict__ part, int chunks,
-                                                                  float *__restrict__ out)
+__global__ void __launch_bounds__(256) k_attn_merge(const float *__restrict__ part, int chunks,
+                                                     float *__restrict__ out)
 {
-    constexpr int HD = ATT_HD, NT = CMB_G * HD;
-    __shared__ float wsh[1024];
-    __shared__ float red[NT / 64];
-    __shared__ float accs[CMB_G][HD];
-    const int h = blockIdx.x, tid = threadIdx.x, grp = tid / HD, d = tid % HD, lane = tid & 63, wave = tid >> 6;
+    constexpr int HD = ATT_HD, NW = 4;
+    __shared__ float wm[NW], wl[NW];
+    __shared__ float2 accs[NW][HD / 2];
+    const int h = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const float *ph = part + (size_t)h * chunks * (HD + 2);
-    float m = -INFINITY;
-    for (int c = tid; c < chunks; c += NT) m = fmaxf(m, ph[(size_t)c * (HD + 2)]);
-    m = wave_max(m);
-    if (lane == 0) red[wave] = m;
-    __syncthreads();
-    float M = red[0];
-    for (int w = 1; w < NT / 64; w++) M = fmaxf(M, red[w]);
-    __syncthreads();
-    float l = 0.0f;
-    for (int c = tid; c < chunks; c += NT) {
-        const float w = expf(ph[(size_t)c * (HD + 2)] - M);
-        wsh[c] = w;
-        l += w * ph[(size_t)c * (HD + 2) + 1];
-    }
-    l = seg_sum<64>(l);
-    if (lane == 0) red[wave] = l;
-    __syncthreads();
-    float L = 0.0f;
-    for (int w = 0; w < NT / 64; w++) L += red[w];
-    float a = 0.0f;
-    for (int c0 = grp; c0 < chunks; c0 += CMB_G * 16) {
-        float v[16];
+    float m = -INFINITY, l = 0.0f;
+    float2 acc = make_float2(0.f, 0.f);
+    for (int c0 = wave; c0 < chunks; c0 += NW * MERGE_B) {
+        const int n = min(MERGE_B, (chunks - c0 + NW - 1) / NW); // chunks c0 + NW*k, k < n
+        float2 ml[MERGE_B], v[MERGE_B];
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int c = c0 + CMB_G * k;
-            v[k] = c < chunks ? ph[(size_t)c * (HD + 2) + 2 + d] : 0.0f;
+        for (int k = 0; k < MERGE_B; k++) {
+            const float *pc = ph + (size_t)(c0 + NW * min(k, n - 1)) * (HD + 2);
+            ml[k] = *(const float2 *)pc;
+            v[k] = *(const float2 *)(pc + 2 + 2 * lane);
         }
+        float bm = m;
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            const int c = c0 + CMB_G * k;
-            if (c < chunks) a = fmaf(wsh[c], v[k], a);
+        for (int k = 0; k < MERGE_B; k++) bm = fmaxf(bm, ml[k].x);
+        const float r = m == -INFINITY ? 0.0f : expf(m - bm);
+        l *= r;
+        acc.x *= r;
+        acc.y *= r;
+#pragma unroll
+        for (int k = 0; k < MERGE_B; k++) {
+            const float w = k < n ? expf(ml[k].x - bm) : 0.0f;
+            l = fmaf(w, ml[k].y, l);
+            acc.x = fmaf(w, v[k].x, acc.x);
+            acc.y = fmaf(w, v[k].y, acc.y);
         }
+        m = bm;
     }
-    accs[grp][d] = a;
+    accs[wave][lane] = acc;
+    if (lane == 0) {
+        wm[wave] = m;
+        wl[wave] = l;
+    }
     __syncthreads();
-    if (grp == 0) {
-        float t = 0.0f;
+    if (wave == 0) {
+        float M = wm[0];
 #pragma unroll
-        for (int g = 0; g < CMB_G; g++) t += accs[g][d];
-        out[(size_t)h * HD + d] = L > 0.0f ? t / L : 0.0f;
+        for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w]);
+        float L = 0.0f;
+        float2 a = make_float2(0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float f = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - M);
+            L = fmaf(f, wl[w], L);
+            a.x = fmaf(f, accs[w][lane].x, a.x);
+            a.y = fmaf(f, accs[w][lane].y, a.y);
+        }
+        const float r = L > 0.0f ? 1.0f / L : 0.0f;
+        *(float2 *)(out + (size_t)h * HD + 2 * lane) = make_float2(a.x * r, a.y * r);
     }
 }
 
 int launch_attention(soso_hip *h, const float *q, const float *K, const float *V, int n_heads, int n_kv_heads,
                      int head_dim, int ctx, int T, float *part, float *out)
 {
-    if (head_dim != ATT_HD || n_kv_heads <= 0 || n_heads % n_kv_heads || T <= 0)
+    if (head_dim != ATT_HD || n_kv_heads <= 0 || n_heads % n_kv_heads || T <= 0 || T > ctx)
         return set_err(h, SOSO_HIP_DECLINED, "attention: head shape not handled here");
     const int G = n_heads / n_kv_heads;
     const int chunks = (T + ATT_CHUNK - 1) / ATT_CHUNK;
-    if (chunks > 1024) return set_err(h, SOSO_HIP_DECLINED, "attention: context longer than 65536");
     const dim3 grid((unsigned)n_kv_heads, (unsigned)chunks);
     switch (G) {
     case 1: k_attn_split<1><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
@@ -205,8 +227,8 @@ int launch_attention(soso_hip *h, const float *q, const float *K, const float *V
     }
     int rc = hip_check(h, hipGetLastError(), "attention split launch");
     if (rc != SOSO_HIP_OK) return rc;
-    k_attn_combine<<<(unsigned)n_heads, CMB_G * ATT_HD, 0, h->stream>>>(part, chunks, out);
-    return hip_check(h, hipGetLastError(), "attention combine launch");
+    k_attn_merge<<<(unsigned)n_heads, 256, 0, h->stream>>>(part, chunks, out);
+    return hip_check(h, hipGetLastError(), "attention merge launch");
 }
 
 // ---------------------------------------------------------------------------

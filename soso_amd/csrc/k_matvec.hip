@@ -172,9 +172,25 @@ constexpr int COMBINE_CH = 64; // passes per LDS combine round (S > 1)
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
 // Output of the row sums gathered in yacc (lane i = row r0 + i, i < nrows).
+// RoPE angle of row r (rope_cabezas, non-NeoX: pair i = (r mod head_dim) / 2
+// turns by pos * theta^(-2i / head_dim)).  Depends on the row only, so the
+// kernel evaluates it before its main loop, while the weight loads are in
+// flight.
+__device__ __forceinline__ void rope_angle(const MvEpi &ep, int r, float &cs, float &sn)
+{
+    const int qk = ep.q_dim + ep.kv_dim;
+    cs = 1.0f;
+    sn = 0.0f;
+    if (r < qk) {
+        const int d = (r < ep.q_dim ? r : r - ep.q_dim) % ep.head_dim;
+        const float fr = powf(ep.theta, -2.0f * (float)(d >> 1) / (float)ep.head_dim);
+        sincosf((float)ep.pos * fr, &sn, &cs);
+    }
+}
+
 template <int EPI>
 __device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows, int rows, float *__restrict__ y,
-                                         const MvEpi &ep)
+                                         const MvEpi &ep, float cs = 1.0f, float sn = 0.0f)
 {
     const int r = r0 + lane;
     const bool ok = lane < nrows && r < rows;
@@ -194,10 +210,6 @@ __device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows
         if (ok) {
             if (r < qk) {
                 const int d = (r < ep.q_dim ? r : r - ep.q_dim) % ep.head_dim;
-                const int i = d >> 1;
-                const float fr = powf(ep.theta, -2.0f * (float)i / (float)ep.head_dim);
-                float sn, cs;
-                sincosf((float)ep.pos * fr, &sn, &cs);
                 const bool even = (d & 1) == 0;
                 const float a = even ? yacc : other, b = even ? other : yacc;
                 const float v = even ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn))
@@ -286,6 +298,13 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
         stage_x_finish<FMT>(xpre, x, cols, xp, s16, kx);
     }
+    // the RoPE angle of this lane's output row, computed while the ring is in
+    // flight (the empty asm keeps it from being sunk to the epilogue)
+    float rope_c = 1.0f, rope_s = 0.0f;
+    if constexpr (EPI == EPI_QKV) {
+        rope_angle(ep, r0 + lane, rope_c, rope_s);
+        asm volatile("" ::"v"(rope_c), "v"(rope_s));
+    }
     XReg xv;
     unit_setup_x<FMT>(xp, s16, kx, u, U, xv, c);
 
@@ -319,7 +338,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
                 yacc = gather_rows<LPR>(part, j0 + i, yacc, lane);
             }
         }
-        epilogue<EPI>(yacc, lane, r0, n * RW, rows, y, ep);
+        epilogue<EPI>(yacc, lane, r0, n * RW, rows, y, ep, rope_c, rope_s);
     } else {
         // the same number of combine rounds for every wavefront of the workgroup
         int nmax = 0;
@@ -547,7 +566,11 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, con
     const int passes = (rows + RW - 1) / RW, units = (passes + PU - 1) / PU;
     const size_t lds = stage_lds_bytes(w.cols) + 64;
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: x does not fit in LDS");
-    int grid = std::min(h->num_cu, (units + gpw - 1) / gpw);
+    // two workgroups per CU for the gate/up pair (2 x 14336 x 4096 on MI355X:
+    // 15.2 us, 15.9 us at one per CU); one for the others (qkv, o and the head
+    // were slower at two)
+    const int wg_per_cu = epi == EPI_SWIGLU ? 2 : 1;
+    int grid = std::min(h->num_cu * wg_per_cu, (units + gpw - 1) / gpw);
     const int upw = 64 / (PU * RW); // units per 64-row strip
     grid = std::max(grid, ((units + upw - 1) / upw + gpw - 1) / gpw);
     grid = std::max(grid, 1);

@@ -48,22 +48,31 @@ __device__ __forceinline__ void xunit(int g, int &u, int &gi)
 __device__ __forceinline__ int xdw(int u, int w, int U) { return ((w >> 2) * U + u) * 4 + (w & 3); }
 
 // Three balanced base-256 digits of the four elements of v (scaled by 2^e),
-// packed one byte per element per digit.
+// packed one byte per element per digit: X = rint(v 2^e) = d0 + 256 d1 +
+// 65536 d2 with every d in [-128, 127].
+//
+// |X| <= 2^22 (the block exponent guarantees it), so adding 1.5 * 2^23 rounds
+// v 2^e to an integer with ties to even (as rintf) and leaves X + 2^22 in the
+// low mantissa bits.  Y = X + 0x808080 is then in [0, 2^24) and byte k of Y
+// is digit k plus 128, so d_k = byte_k(Y) ^ 0x80: the same digits as the
+// repeated "d = int8(X); X = (X - d) / 256" (checked for every |X| <= 2^22).
+// Seven byte permutes gather the bytes of the four elements digit by digit.
 __device__ __forceinline__ void digits4(float4 v, int e, uint32_t (&d)[XDIG])
 {
-    const float f[4] = {v.x, v.y, v.z, v.w};
-    d[0] = d[1] = d[2] = 0u;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int X = (int)rintf(ldexpf(f[i], e));
-        const int d0 = (int)(int8_t)(X & 0xff);
-        const int X1 = (X - d0) >> 8;
-        const int d1 = (int)(int8_t)(X1 & 0xff);
-        const int d2 = (X1 - d1) >> 8;
-        d[0] |= (uint32_t)(d0 & 0xff) << (8 * i);
-        d[1] |= (uint32_t)(d1 & 0xff) << (8 * i);
-        d[2] |= (uint32_t)(d2 & 0xff) << (8 * i);
-    }
+    constexpr float MAGIC = 12582912.0f; // 1.5 * 2^23
+    constexpr uint32_t OFF = 0x4B400000u - 0x808080u;
+    const uint32_t y0 = __float_as_uint(__fadd_rn(ldexpf(v.x, e), MAGIC)) - OFF;
+    const uint32_t y1 = __float_as_uint(__fadd_rn(ldexpf(v.y, e), MAGIC)) - OFF;
+    const uint32_t y2 = __float_as_uint(__fadd_rn(ldexpf(v.z, e), MAGIC)) - OFF;
+    const uint32_t y3 = __float_as_uint(__fadd_rn(ldexpf(v.w, e), MAGIC)) - OFF;
+    // v_perm_b32 (s0, s1, sel): selector byte 0-3 picks byte of s1, 4-7 of s0
+    const uint32_t A = __builtin_amdgcn_perm(y1, y0, 0x05010400u); // y0b0 y1b0 y0b1 y1b1
+    const uint32_t B = __builtin_amdgcn_perm(y3, y2, 0x05010400u); // y2b0 y3b0 y2b1 y3b1
+    const uint32_t C = __builtin_amdgcn_perm(y1, y0, 0x0c0c0602u); // y0b2 y1b2
+    const uint32_t D = __builtin_amdgcn_perm(y3, y2, 0x0c0c0602u); // y2b2 y3b2
+    d[0] = __builtin_amdgcn_perm(B, A, 0x05040100u) ^ 0x80808080u;
+    d[1] = __builtin_amdgcn_perm(B, A, 0x07060302u) ^ 0x80808080u;
+    d[2] = __builtin_amdgcn_perm(D, C, 0x05040100u) ^ 0x80808080u;
 }
 
 // One 8-element chunk c (thread lane == c % 64).  Every lane of the 16-lane

@@ -646,11 +646,13 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     const size_t kv_bytes = L * cfg->ctx_max * kvd * 4;
     const size_t chunks = (cfg->ctx_max + 63) / 64;
     const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64;
+    const size_t mem_bytes = act_floats * 4;
     if (rc == SOSO_HIP_OK) {
-        if (hipMalloc((void **)&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, act_floats * 4) != hipSuccess)
+        if (hipMalloc((void **)&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, mem_bytes) != hipSuccess)
             rc = set_err(h, SOSO_HIP_DECLINED, "decode_create: no memory for the KV cache");
     }
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemsetAsync(m.kcache, 0, 2 * kv_bytes, h->stream), "kv zero");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemsetAsync(m.mem, 0, mem_bytes, h->stream), "step buffers zero");
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "decode_create sync");
     if (rc != SOSO_HIP_OK) {
         decode_free(h, m);
