@@ -264,6 +264,119 @@ def cpu_baseline(dtype, rows, cols, seconds, threads):
     return algo_bytes(dtype, rows, cols) / dt / 1e9, n, dt * 1e3
 
 
+def time_single_launch(g, dtype, rows, cols, reps=50, seed=1):
+    """A graph holding ONE matvec launch, replayed `reps` times with a host
+    synchronisation between replays; median event interval per replay in ms
+    (the latency of an isolated call, launch included)."""
+    key = f"bench.single.{dtype}.{rows}x{cols}"
+    g.weight_synth(key, dtype, rows, cols, seed, 1000)
+    x = g.dev_alloc(cols * 4)
+    y = g.dev_alloc(rows * 4)
+    try:
+        g.synth_normal(x, cols, 1.0, seed, 7)
+        gid = _capture(g, lambda: g.matvec_dev(key, x, y))
+        try:
+            ts = []
+            for i in range(reps + 3):
+                g.event_record(0)
+                g.graph_launch(gid)
+                g.event_record(1)
+                g.sync()
+                if i >= 3:
+                    ts.append(g.event_elapsed(0, 1))
+        finally:
+            g.graph_destroy(gid)
+        return float(np.median(ts))
+    finally:
+        g.sync()
+        g.dev_free(x)
+        g.dev_free(y)
+        g.weight_drop(key)
+
+
+def head_parity(g, threads, seed=1):
+    """configs[2] checked in the bench run: the Q6_K head 128256 x 4096 on the
+    GPU (matvec + argmax on the device) against the CPU restatement on the
+    same seeded bytes (oracle/, `threads` host threads).  Returns the GPU and
+    CPU argmax, the CPU logits' top-2 gap and the relative L2 of the logits."""
+    from oracle import oracle as orc
+    rows, cols = 128256, 4096
+    key = "bench.head.parity"
+    g.weight_synth(key, Q6K, rows, cols, seed, 1000)
+    x = g.dev_alloc(cols * 4)
+    y = g.dev_alloc(rows * 4)
+    t = g.dev_alloc(4)
+    try:
+        g.synth_normal(x, cols, 1.0, seed, 7)
+        g.matvec_dev(key, x, y)
+        g.argmax_dev(y, rows, t)
+        g.sync()
+        logits = g.d2h(y, (rows,), np.float32)
+        tok = int(g.d2h(t, (1,), np.uint32)[0])
+    finally:
+        g.dev_free(x)
+        g.dev_free(y)
+        g.dev_free(t)
+        g.weight_drop(key)
+    w = orc.synth(Q6K, rows, cols, seed, 1000)
+    xc = orc.normal(cols, 1.0, seed, 7)
+    ref = orc.matvec(Q6K, w, rows, cols, xc, threads=threads)
+    ref_tok = int(orc.lib().or_argmax(ref.ctypes.data, rows))
+    top2 = np.sort(ref)[-2:]
+    return {"argmax_gpu": tok, "argmax_cpu": ref_tok, "argmax_equal": tok == ref_tok,
+            "cpu_top2_gap": float(top2[1] - top2[0]), "logits_rel_l2": float(orc.rel_l2(logits, ref))}
+
+
+def cpu_extra(seconds, threads):
+    """The rest of the CPU baseline (oracle/ restatements, bounded samples):
+    host DRAM read bandwidth (STREAM-like sum, the CPU roofline), the
+    headline Q4_K at 1 thread, configs[0] Q8_0, and configs[2]'s head both
+    ways soso could run it -- the restated Q6_K dequant+dot, and Q6_K
+    requantized to Q8_0 (gguf2som/src/lib.rs:1592-1609) then AVX2
+    matvec_q8_0 -- on a row sample.  GB/s are algorithmic bytes of the
+    format the kernel reads."""
+    from oracle import oracle as orc
+    out = {}
+
+    def rate(fn, nbytes, budget):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < budget:
+            fn()
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        return round(nbytes / dt / 1e9, 2), n
+
+    a = np.ones(1 << 28, np.float32)  # 1 GiB
+    out["host_read_GB_s"], _ = rate(lambda: orc.lib().or_stream_read(a.ctypes.data, a.size, threads), a.nbytes,
+                                    seconds / 4)
+    del a
+    rows, cols = 14336, 4096
+    w = orc.synth(Q4K, rows, cols, 1, 1000)
+    x = orc.normal(cols, 1.0, 1, 7)
+    out["q4_k_14336x4096_1thread_GB_s"], _ = rate(lambda: orc.matvec(Q4K, w, rows, cols, x, threads=1, avx2=True),
+                                                  algo_bytes(Q4K, rows, cols), seconds / 4)
+    ws = [orc.synth(Q8, 4096, 4096, 1, 1000 + i) for i in range(8)]
+    x8 = orc.normal(4096, 1.0, 1, 7)
+    it = iter(range(1 << 30))
+    out["q8_0_4096x4096_GB_s"], _ = rate(
+        lambda: orc.matvec(Q8, ws[next(it) % 8], 4096, 4096, x8, threads=threads, avx2=True),
+        algo_bytes(Q8, 4096, 4096), seconds / 4)
+    hr = 16384  # head row sample: 55 MB of Q6_K, 75 MB of Q8_0 per call
+    wq6 = orc.synth(Q6K, hr, cols, 1, 1000)
+    out["q6_k_head_restated_GB_s"], _ = rate(lambda: orc.matvec(Q6K, wq6, hr, cols, x, threads=threads),
+                                             algo_bytes(Q6K, hr, cols), seconds / 8)
+    deq = np.empty(hr * cols, np.float32)
+    orc.lib().or_dequant_q6_k(wq6.ctypes.data, wq6.nbytes, deq.ctypes.data, deq.size)
+    wq8 = np.empty(hr * (cols // 32) * 36, np.uint8)
+    orc.lib().or_quantize_q8_0(deq.ctypes.data, deq.size, wq8.ctypes.data)
+    out["q6_k_head_as_q8_0_GB_s"], _ = rate(lambda: orc.matvec(Q8, wq8, hr, cols, x, threads=threads, avx2=True),
+                                            algo_bytes(Q8, hr, cols), seconds / 8)
+    out["sample"] = (f"~{seconds:.0f} s in all: 1 GiB host read; Q4_K 14336x4096 at 1 thread; 8 rotating Q8_0 "
+                     f"4096x4096; head row sample {hr}x{cols} (Q6_K restated, and requantized to Q8_0)")
+    return out
+
+
 def load_traffic(name):
     """HBM bytes per launch measured with rocprofv3 --pmc (profiles/), if recorded."""
     p = os.path.join(ROOT, "profiles", "traffic.json")
@@ -283,6 +396,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
+    ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head"],
+                    help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -295,6 +410,23 @@ def main():
     if args.copy_calibration:
         copy_calibration(g)
         g.close()
+        return
+    if args.only:
+        if args.only == "matvec":
+            ms, _ = time_matvec(g, Q4K, 14336, 4096, 16, args.steps, args.warmup)
+            res = {"q4_k_14336x4096_us": round(ms * 1e3, 3)}
+        elif args.only == "head":
+            ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10))
+            res = {"q6_k_head_128256x4096_us": round(ms * 1e3, 3)}
+        elif args.only == "decode":
+            ms, _, tok = time_decode_8b(g, max(10, args.steps // 50))
+            res = {"llama8b_decode_ms_per_token": round(ms, 4), "greedy_token": tok}
+        else:
+            n = 1 if args.only == "moe1" else 32
+            ms, _, _, _ = time_moe(g, n, max(40, args.steps // 10))
+            res = {f"moe_batch{n}_us_per_layer": round(ms * 1e3, 3)}
+        g.close()
+        print(json.dumps(res), flush=True)
         return
     rows, cols = 14336, 4096
     nbytes = algo_bytes(Q4K, rows, cols)
@@ -317,7 +449,8 @@ def main():
                    "rows": rows, "cols": cols, "bytes_per_step": nbytes, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic("q4k_14336x4096"),
-                     "kernel_us": round(ms * 1e3, 3), "host_wall_us_per_step": round(ms_wall * 1e3, 3)},
+                     "kernel_us": round(ms * 1e3, 3), "host_wall_us_per_step": round(ms_wall * 1e3, 3),
+                     "graph_single_launch_us": round(time_single_launch(g, Q4K, rows, cols) * 1e3, 3)},
     }
     if not args.no_extra:
         extra = {}
@@ -329,6 +462,8 @@ def main():
             b = algo_bytes(dt, r, c)
             extra[name] = {"us_kernel": round(k_ * 1e3, 3), "GB_s": round(b / (k_ * 1e-3) / 1e9, 1),
                            "frac_hbm": round(b / (k_ * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b}
+        if not args.no_cpu:
+            extra["q6_k_head_128256x4096"]["parity_vs_cpu"] = head_parity(g, args.cpu_threads)
         for n in (1, 32):
             ms_m, b_m, u_m, _ = time_moe(g, n, max(40, args.steps // 10))
             extra[f"moe_qwen3_30b_a3b_batch{n}"] = {
@@ -347,6 +482,7 @@ def main():
                                 "sample": f"{n} AVX2 Q4_K matvecs 14336x4096 over 4 rotating copies "
                                           f"({ms:.2f} ms each) in ~{args.cpu_seconds:.0f} s",
                                 "host_nproc": os.cpu_count()}
+        line["cpu_baseline"]["more"] = cpu_extra(args.cpu_seconds, args.cpu_threads)
     g.close()
     print(json.dumps(line), flush=True)
 

@@ -869,3 +869,50 @@ double or_now_seconds(void)
     clock_gettime(CLOCK_MONOTONIC, &ts);
     return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
 }
+
+/* ---------------------------------------------------------------------------
+ * Host DRAM read bandwidth (STREAM-like "sum" kernel), the CPU roofline the
+ * baseline is read against: `threads` contiguous strips of `a`, each summed
+ * with four independent accumulators.  Returns the sum so nothing is elided.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const float *a;
+    size_t s, e;
+    double sum;
+} read_job;
+
+static void *read_thread(void *p)
+{
+    read_job *j = (read_job *)p;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    size_t i = j->s;
+    for (; i + 4 <= j->e; i += 4)
+        for (int k = 0; k < 4; k++) acc[k] += j->a[i + (size_t)k];
+    for (; i < j->e; i++) acc[0] += j->a[i];
+    j->sum = (double)acc[0] + acc[1] + acc[2] + acc[3];
+    return NULL;
+}
+
+double or_stream_read(const float *a, size_t n, int threads)
+{
+    if (threads < 1) threads = 1;
+    read_job *jobs = (read_job *)calloc((size_t)threads, sizeof(read_job));
+    pthread_t *tid = (pthread_t *)calloc((size_t)threads, sizeof(pthread_t));
+    double sum = 0.0;
+    if (!jobs || !tid) {
+        free(jobs);
+        free(tid);
+        return 0.0;
+    }
+    for (int i = 0; i < threads; i++) {
+        jobs[i].a = a;
+        row_strip(n, (size_t)i, (size_t)threads, &jobs[i].s, &jobs[i].e);
+    }
+    for (int i = 1; i < threads; i++) pthread_create(&tid[i], NULL, read_thread, &jobs[i]);
+    read_thread(&jobs[0]);
+    for (int i = 1; i < threads; i++) pthread_join(tid[i], NULL);
+    for (int i = 0; i < threads; i++) sum += jobs[i].sum;
+    free(jobs);
+    free(tid);
+    return sum;
+}

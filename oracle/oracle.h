@@ -136,6 +136,8 @@ void or_synth_normal(float *out, size_t n, float sigma, uint64_t seed, uint64_t 
 
 /* ---- timing helper for the CPU baseline ---------------------------------- */
 double or_now_seconds(void);
+/* STREAM-like threaded read of n floats (host DRAM roofline); returns the sum. */
+double or_stream_read(const float *a, size_t n, int threads);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,7 @@ _PROTO = {
     "or_synth_q6_k": (None, [_P, _S, _S, _U64, _U64]),
     "or_synth_normal": (None, [_P, _S, _F, _U64, _U64]),
     "or_now_seconds": (C.c_double, []),
+    "or_stream_read": (C.c_double, [_P, _S, _I]),
 }
 
 _lib = None

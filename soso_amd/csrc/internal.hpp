@@ -153,11 +153,13 @@ struct MoeScratch {
     int32_t *idx = nullptr;  // n x top_k
     float *wgt = nullptr;    // n x top_k
     int *cnt = nullptr, *offs = nullptr, *list = nullptr; // n_groups, n_groups + 1, n x top_k
-    int *act_list = nullptr, *act_n = nullptr;              // active groups (ascending), their count
+    int *items = nullptr, *n_items = nullptr; // work items {group, count, first slot, chunk | chunks << 16}, count
     float *act = nullptr;    // n x top_k x ffn
     float *ydown = nullptr;  // n x top_k x hdim
 };
 bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s);
+int moe_item_target(const soso_hip *h);
+size_t moe_max_items(const soso_hip *h, size_t slots, size_t n_groups);
 int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim,
                        size_t n_exp, size_t top_k, int32_t *idx_dev, float *wgt_dev, float *logits_dev);
 int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim, size_t n_exp,
@@ -235,6 +237,49 @@ __device__ __forceinline__ float seg_sum_dpp(float v)
     if (W >= 32) v += dpp_f<0x142, 0xA>(v);
     if (W >= 64) v += dpp_f<0x143, 0xC>(v);
     return v;
+}
+
+// DPP move where lanes without a source (and rows outside `ROWS`) keep their
+// own value -- the form max-reductions need.
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ uint32_t dpp_keep(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xf, false);
+}
+
+// Wavefront-wide max / sum by DPP (row butterflies, then the row broadcasts
+// 15 and 31); the result is read from lane 63, uniform over the wavefront.
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    auto st = [](float a, uint32_t b) { return fmaxf(a, __uint_as_float(b)); };
+    v = st(v, dpp_keep<0xB1>(__float_as_uint(v)));
+    v = st(v, dpp_keep<0x4E>(__float_as_uint(v)));
+    v = st(v, dpp_keep<0x141>(__float_as_uint(v)));
+    v = st(v, dpp_keep<0x140>(__float_as_uint(v)));
+    v = st(v, dpp_keep<0x142, 0xA>(__float_as_uint(v)));
+    v = st(v, dpp_keep<0x143, 0xC>(__float_as_uint(v)));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Max of a 64-bit key over the wavefront (uniform result).
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t k)
+{
+#define SOSO_U64_STEP(CTRL, ROWS)                                                                                 \
+    {                                                                                                             \
+        const uint64_t o = ((uint64_t)dpp_keep<CTRL, ROWS>((uint32_t)(k >> 32)) << 32) |                          \
+                           dpp_keep<CTRL, ROWS>((uint32_t)k);                                                     \
+        k = o > k ? o : k;                                                                                        \
+    }
+    SOSO_U64_STEP(0xB1, 0xf)
+    SOSO_U64_STEP(0x4E, 0xf)
+    SOSO_U64_STEP(0x141, 0xf)
+    SOSO_U64_STEP(0x140, 0xf)
+    SOSO_U64_STEP(0x142, 0xA)
+    SOSO_U64_STEP(0x143, 0xC)
+#undef SOSO_U64_STEP
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(k >> 32), 63);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)k, 63);
+    return ((uint64_t)hi << 32) | lo;
 }
 
 // Max over aligned 16-lane rows (every lane gets it).

@@ -100,7 +100,7 @@ __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q,
             acc = seg_sum_dpp<8>(acc); // all 8 lanes of the position hold the sum
             s[a] = tw + 8 * a + pp < t1 ? acc * inv : -INFINITY;
         }
-        const float m = wave_max(fmaxf(s[0], s[1]));
+        const float m = wave_max_dpp(fmaxf(s[0], s[1]));
         float p[2];
 #pragma unroll
         for (int a = 0; a < 2; a++) p[a] = s[a] == -INFINITY ? 0.0f : expf(s[a] - m);

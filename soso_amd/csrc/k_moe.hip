@@ -10,7 +10,7 @@
 //   k_moe_route   logits = W_router . x (f32) for every (token, expert); the
 //                 last workgroup to finish runs softmax + top-k per token and
 //                 counting-sorts the n*top_k slots by expert (cnt, offs, list).
-//   k_moe_mv      a persistent grid over (active expert, row chunk) items:
+//   k_moe_rows    workgroups over (expert, row chunk) items of equal work:
 //                 every weight row of an expert is read once from HBM and
 //                 applied to all the tokens routed to it (their x staged in
 //                 LDS).  Gate and up rows are read side by side and leave as
@@ -28,53 +28,43 @@
 // Softmax and ranking of one token's logits by one wavefront (gemm.rs:62-91):
 // max-shifted expf, normalised, then the top_k largest probabilities with
 // ties to the lowest index (a stable descending sort), renormalised by their
-// sum taken in rank order.
-__device__ void topk_wave(const float *__restrict__ lg, int n_exp, int top_k, int32_t *__restrict__ idx,
+// sum taken in rank order.  lg[q] holds the logit of expert lane + 64 q
+// (n_exp <= 256).  Each round takes the wavefront max of a 64-bit key
+// (probability bits + 1, then 0xFFFF - expert: larger probability first,
+// then lower index); NaN probabilities and removed experts carry key 0 and
+// are never chosen -- should fewer than top_k experts remain, the slot points
+// at expert 0 with weight 0 (indices stay valid).  `sel`: top_k floats of LDS.
+__device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *__restrict__ idx,
                           float *__restrict__ wgt, float *sel)
 {
     const int lane = threadIdx.x & 63;
-    float m = -INFINITY;
-    for (int e = lane; e < n_exp; e += 64) m = fmaxf(m, lg[e]);
-    m = wave_max(m);
-    float s = 0.0f;
-    for (int e = lane; e < n_exp; e += 64) s += expf(lg[e] - m);
-    s = seg_sum<64>(s);
-    // each lane keeps the probabilities of experts lane, lane+64, ... (n_exp <= 256)
-    float p[4];
+    const float m = wave_max_dpp(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])));
+    float ex[4], s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        ex[q] = lane + 64 * q < n_exp ? expf(lg[q] - m) : 0.0f;
+        s += ex[q];
+    }
+    s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(seg_sum_dpp<64>(s)), 63));
+    uint64_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int e = lane + 64 * q;
-        p[q] = e < n_exp ? expf(lg[e] - m) / s : -INFINITY;
+        const float p = ex[q] / s;
+        const uint32_t k32 = e < n_exp && p >= 0.0f ? __float_as_uint(p) + 1u : 0u;
+        key[q] = ((uint64_t)k32 << 32) | (uint32_t)(0xFFFF - e);
     }
     for (int j = 0; j < top_k; j++) {
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
+        uint64_t best = key[0];
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const int e = lane + 64 * q;
-            if (p[q] > bv || (p[q] == bv && e < bi)) {
-                bv = p[q];
-                bi = e;
-            }
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, 64);
-            const int oi = __shfl_xor(bi, o, 64);
-            if (ov > bv || (ov == bv && oi < bi)) {
-                bv = ov;
-                bi = oi;
-            }
-        }
-        // NaN probabilities are never chosen; should fewer than top_k experts
-        // remain, the slot points at expert 0 with weight 0 (indices stay valid)
-        if (bi >= n_exp) {
-            bi = 0;
-            bv = 0.0f;
-        }
+        for (int q = 1; q < 4; q++) best = key[q] > best ? key[q] : best;
+        best = wave_max_u64_dpp(best);
+        const uint32_t k32 = (uint32_t)(best >> 32);
+        const int bi = k32 ? 0xFFFF - (int)(best & 0xFFFFu) : 0;
+        const float bv = k32 ? __uint_as_float(k32 - 1u) : 0.0f;
 #pragma unroll
         for (int q = 0; q < 4; q++)
-            if (lane + 64 * q == bi) p[q] = -INFINITY;
+            if (k32 && lane + 64 * q == bi) key[q] = 0;
         if (lane == 0) {
             idx[j] = bi;
             sel[j] = bv;
@@ -87,61 +77,96 @@ __device__ void topk_wave(const float *__restrict__ lg, int n_exp, int top_k, in
     }
 }
 
-// grid: ceil(n_exp / waves) workgroups; wave w of workgroup b owns expert
-// b*waves + w.  `ticket` is zero between launches (the last workgroup resets
-// it).  The last workgroup also writes the active-expert list act[0..*act_n)
-// (experts chosen by at least one slot, ascending) for the grouped kernels.
+// grid (ceil(n_exp / waves), ceil(n / ROUTE_TT)); wave w of workgroup
+// (bx, by) owns expert bx*waves + w for tokens by*ROUTE_TT .. + ROUTE_TT - 1.
+// `ticket` is zero between launches (the last workgroup resets it).  The last
+// workgroup also writes the work items of the grouped kernels (about `target`
+// of them, each an equal share of tokens x rows): items[4i .. 4i+3] =
+// {expert, its slot count, its first slot in `list`, chunk j | chunks << 16}
+// for i < *n_items, experts ascending.
 constexpr int ROUTE_MAX_SLOTS = 4096; // n * top_k handled by the LDS sort
+constexpr int ROUTE_TT = 4;           // tokens per wavefront
 
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
                                                     int32_t *__restrict__ idx, float *__restrict__ wgt,
                                                     int *__restrict__ cnt, int *__restrict__ offs,
-                                                    int *__restrict__ list, int *__restrict__ act,
-                                                    int *__restrict__ act_n, unsigned *__restrict__ ticket)
+                                                    int *__restrict__ list, int *__restrict__ items,
+                                                    int *__restrict__ n_items, int target,
+                                                    unsigned *__restrict__ ticket)
 {
     __shared__ int last;
+    __shared__ int pre_s[257];
     __shared__ float sel[8][64];
     __shared__ int c_s[256], o_s[257], f_s[256];
     __shared__ int16_t e_s[ROUTE_MAX_SLOTS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int e = blockIdx.x * nw + wave;
+    const int t0 = blockIdx.y * ROUTE_TT, tn = min(ROUTE_TT, n - t0);
     if (e < n_exp) {
+        // this wavefront's expert row against ROUTE_TT tokens: every load of
+        // a 256-float4 step is issued before its products
         const float4 *w4 = (const float4 *)(W + (size_t)e * hdim);
+        const float4 *x4 = (const float4 *)(xs + (size_t)t0 * hdim);
         const int nv = hdim >> 2;
-        for (int t = 0; t < n; t++) {
-            const float4 *x4 = (const float4 *)(xs + (size_t)t * hdim);
-            float a0 = 0.f, a1 = 0.f;
-            for (int i0 = 0; i0 < nv; i0 += 64 * 4) {
-                float4 w[4], v[4];
+        float acc[ROUTE_TT];
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const int i = i0 + 64 * q + lane;
-                    w[q] = i < nv ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                    v[q] = i < nv ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
+        for (int tt = 0; tt < ROUTE_TT; tt++) acc[tt] = 0.0f;
+        for (int i0 = 0; i0 < nv; i0 += 64 * 4) {
+            float4 w[4], v[ROUTE_TT][4];
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    a0 = fmaf(w[q].x, v[q].x, a0);
-                    a1 = fmaf(w[q].y, v[q].y, a1);
-                    a0 = fmaf(w[q].z, v[q].z, a0);
-                    a1 = fmaf(w[q].w, v[q].w, a1);
-                }
+            for (int q = 0; q < 4; q++) {
+                const int i = i0 + 64 * q + lane;
+                w[q] = i < nv ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int tt = 0; tt < ROUTE_TT; tt++)
+                    v[tt][q] = i < nv && tt < tn ? x4[(size_t)tt * nv + i] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            const float sum = seg_sum<64>(a0 + a1);
-            if (lane == 0) logits[(size_t)t * n_exp + e] = sum;
+#pragma unroll
+            for (int tt = 0; tt < ROUTE_TT; tt++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    acc[tt] = fmaf(w[q].x, v[tt][q].x, acc[tt]);
+                    acc[tt] = fmaf(w[q].y, v[tt][q].y, acc[tt]);
+                    acc[tt] = fmaf(w[q].z, v[tt][q].z, acc[tt]);
+                    acc[tt] = fmaf(w[q].w, v[tt][q].w, acc[tt]);
+                }
+        }
+#pragma unroll
+        for (int tt = 0; tt < ROUTE_TT; tt++) {
+            const float sum = seg_sum_dpp<64>(acc[tt]); // lane 63 holds it
+            if (lane == 63 && tt < tn) logits[(size_t)(t0 + tt) * n_exp + e] = sum;
         }
     }
-    // the last workgroup to finish ranks the experts of every token
-    __threadfence();
+    // The last workgroup to finish ranks the experts of every token.  One
+    // thread per workgroup fences: a device-scope fence writes back the L2 of
+    // its XCD, and the workgroup barrier before it orders every wavefront's
+    // stores ahead of it (fences are cumulative).
     __syncthreads();
-    if (threadIdx.x == 0) last = atomicAdd(ticket, 1u) == gridDim.x - 1;
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const bool l = atomicAdd(ticket, 1u) == gridDim.x * gridDim.y - 1;
+        if (l) __threadfence();
+        last = l;
+    }
     __syncthreads();
     if (!last) return;
-    __threadfence();
-    for (int t = wave; t < n; t += nw)
-        topk_wave(logits + (size_t)t * n_exp, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k,
-                  sel[wave]);
+    // four tokens per wavefront at a time, their logits loaded together
+    for (int tb = 4 * wave; tb < n; tb += 4 * nw) {
+        float lg[4][4];
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int x = lane + 64 * q;
+                lg[tt][q] = tb + tt < n && x < n_exp ? logits[(size_t)(tb + tt) * n_exp + x] : -INFINITY;
+            }
+#pragma unroll
+        for (int tt = 0; tt < 4; tt++)
+            if (tb + tt < n)
+                topk_regs(lg[tt], n_exp, top_k, idx + (size_t)(tb + tt) * top_k, wgt + (size_t)(tb + tt) * top_k,
+                          sel[wave]);
+    }
     __syncthreads();
     // counting sort of the slots by expert in LDS (a slot's position inside
     // its expert's list does not change any result)
@@ -189,19 +214,58 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
     }
     if (threadIdx.x == 0) offs[n_exp] = o_s[n_exp];
     if (wave == 0) {
-        // active experts in ascending order: compaction by ballot over 64 at a time
-        int base = 0;
-        for (int x0 = 0; x0 < n_exp; x0 += 64) {
-            const int x = x0 + lane;
-            const bool on = x < n_exp && c_s[x] > 0;
-            const unsigned long long m = __ballot(on);
-            if (on) act[base + __popcll(m & ((1ull << lane) - 1ull))] = x;
-            base += __popcll(m);
+        // work items: expert x with c tokens gets max(1, round(c * target /
+        // slots)) row chunks, so every item carries about the same tokens x
+        // rows; exclusive scan of the chunk counts over the experts
+        int v[4], tot = 0;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int x = 4 * lane + q;
+            const int cx = x < n_exp ? c_s[x] : 0;
+            v[q] = cx > 0 ? min(0xFFFF, max(1, (cx * target + slots / 2) / slots)) : 0;
+            tot += v[q];
         }
-        if (lane == 0) {
-            *act_n = base;
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+        }
+        int run = incl - tot;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int x = 4 * lane + q;
+            if (x < n_exp) pre_s[x] = run;
+            run += v[q];
+        }
+        if (lane == 63) {
+            pre_s[n_exp] = incl;
+            *n_items = incl;
             *ticket = 0u;
         }
+    }
+    __syncthreads();
+    // items[4i .. 4i+3] = {expert, its slot count, its first slot, chunk | chunks << 16};
+    // item i belongs to the expert x with pre_s[x] <= i < pre_s[x + 1]
+    const int total = pre_s[n_exp];
+    for (int i = threadIdx.x; i < total; i += blockDim.x) {
+        int lo = 0, hi = n_exp - 1; // last x with pre_s[x] <= i
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (pre_s[mid] <= i) lo = mid;
+            else hi = mid - 1;
+        }
+        const int nx = pre_s[lo + 1] - pre_s[lo];
+        int4 r;
+        r.x = lo;
+        r.y = c_s[lo];
+        r.z = o_s[lo];
+        r.w = (i - pre_s[lo]) | (nx << 16);
+        int *d = items + 4 * i;
+        d[0] = r.x;
+        d[1] = r.y;
+        d[2] = r.z;
+        d[3] = r.w;
     }
 }
 
@@ -210,90 +274,248 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Persistent grid of workgroups (512 threads) over the work items (active
-// expert a, row chunk c), item w = a * chunks + c, w = blockIdx.x, +gridDim.x.
-// A chunk is 2 passes per wavefront (rpw = 2 * 8 * RW rows): both passes'
-// weights are requested before the tokens' x is staged, so the HBM reads of
-// an item overlap its staging.  Expert e's slots are list[offs[e] ..
-// offs[e] + cnt[e]), `tch` at a time; slot s reads x = xs + (s / xdiv) * cols
-// and writes out[s * rows + r].  NMAT == 2: tabA = gate, tabB = up, output
-// silu(gate.x) * up.x (swiglu, gemm.rs:210-226); NMAT == 1: tabA = down.
-template <int FMT, int LPR, int NMAT>
-__global__ void __launch_bounds__(512) k_moe_mv(const uint8_t *const *__restrict__ tabA,
-                                                const uint8_t *const *__restrict__ tabB, size_t stride, int rows,
-                                                int cols, int chunks, const float *__restrict__ xs, int xdiv,
-                                                const int *__restrict__ cnt, const int *__restrict__ offs,
-                                                const int *__restrict__ list, const int *__restrict__ act,
-                                                const int *__restrict__ act_n, int tch, float *__restrict__ out)
+// Grouped expert matvecs: workgroups (512 threads, 8 wavefronts) over the
+// work items written by k_moe_route, item it = blockIdx.x, + gridDim.x (the
+// host launches about one workgroup per item and the dispatcher balances
+// them).  Item (expert e, chunk j of nx) covers passes [j * passes / nx,
+// (j + 1) * passes / nx) of every wavefront: rows r0 + (p * 8 + wave) * RW +
+// slot, so one item streams a contiguous block of an expert's rows.  Per item:
+//   1. the x of the expert's tokens (up to `tch` at a time) is requested in
+//      one batch -- slot s reads x = xs + (s / xdiv) * cols --,
+//   2. then the weight ring (DEPTH passes, every load unconditional: rows
+//      past the chunk read zeros through the buffer range check),
+//   3. x is converted into LDS (digit planes, one region per token) while
+//      the ring is in flight,
+//   4. the passes stream through the ring; each pass applies its rows to
+//      every staged token (x from LDS) and writes out[s * rows + r].
+// NMAT == 2: tabA = gate, tabB = up, output silu(gate.x) * up.x (swiglu,
+// gemm.rs:210-226); NMAT == 1: tabA = down.
+constexpr int MOE_XK = 4; // x chunks (8 floats) per thread per staging round
+
+// Q4_K unit of one row decoded once per pass and shared by the tokens: the
+// codes of sub-blocks 2p (low nibbles) and 2p+1 (high nibbles), and the
+// factors d*sc and dmin*m of both (get_scale_min_k4, crates/sosomodel/src/
+// dequant.rs:150-159, four at a time per byte lane as in unit_dot).
+struct Q4Prep {
+    uint32_t lo[8], hi[8];
+    float ka, kb, kma, kmb;
+};
+
+__device__ __forceinline__ void q4k_prep(const WRow<FMT_Q4K> &w, const UConst &c, Q4Prep &p)
 {
-    constexpr int RW = 64 / LPR, NW = 8, RPW = 2 * NW * RW;
+    const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        p.lo[t] = q[t] & 0x0F0F0F0Fu;
+        p.hi[t] = (q[t] >> 4) & 0x0F0F0F0Fu;
+    }
+    const uint32_t SC4 = ((w.h.w & c.k1) | ((w.h.y >> c.s) & c.k2)) >> c.bsh;
+    const uint32_t M4 = (((w.h.w >> 4) & c.k1) | ((w.h.z >> c.s) & c.k2)) >> c.bsh;
+    const float d = half_bits_to_f32(w.h.x & 0xffffu), dmin = half_bits_to_f32(w.h.x >> 16);
+    p.ka = d * (float)(SC4 & 0xffu);
+    p.kb = d * (float)((SC4 >> 8) & 0xffu);
+    p.kma = dmin * (float)(M4 & 0xffu);
+    p.kmb = dmin * (float)((M4 >> 8) & 0xffu);
+}
+
+// sum over one sub-block (register groups g0 .. g0+7) of codes x digits
+__device__ __forceinline__ void q4k_half(const uint32_t (&codes)[8], const uint32_t (&xh)[24], int (&s)[XDIG])
+{
+#pragma unroll
+    for (int t = 0; t < 8; t++)
+#pragma unroll
+        for (int k = 0; k < XDIG; k++) s[k] = sdot4(codes[t], xh[XDIG * t + k], s[k]);
+}
+
+template <int FMT, int LPR, int NMAT, int DEPTH>
+__global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restrict__ tabA,
+                                                  const uint8_t *const *__restrict__ tabB, size_t stride, int rows,
+                                                  int cols, const float *__restrict__ xs, int xdiv,
+                                                  const int *__restrict__ list, const int *__restrict__ items,
+                                                  const int *__restrict__ n_items, int tch, float *__restrict__ out)
+{
+    constexpr int RW = 64 / LPR, NW = 8;
     extern __shared__ uint4 smem[];
     __shared__ int slot_s[64];
-    const size_t tok_bytes = (stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15;
+    const int tok_bytes = (int)((stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int U = cols >> 6;
+    const int U = cols >> 6, nch = cols >> 3;
     const int ul = lane & (LPR - 1), slot = lane / LPR;
     const bool uact = ul < U;
     const int u = uact ? ul : 0;
     UConst c;
     unit_setup_w<FMT>(u, c);
     const LaneOff L = lane_offsets<FMT>(cols, u, c);
-    const int items = *act_n * chunks;
-    for (int w = blockIdx.x; w < items; w += gridDim.x) {
-        const int e = act[w / chunks];
-        const int r0 = (w % chunks) * RPW, r1 = min(rows, r0 + RPW);
-        const int ne = cnt[e], base = offs[e];
-        const rsrc_t rA = make_rsrc(tabA[e], (uint32_t)((size_t)rows * stride));
-        const rsrc_t rB = make_rsrc(NMAT == 2 ? tabB[e] : tabA[e], (uint32_t)((size_t)rows * stride));
-        // this wavefront's two passes: rows r0 + (wave + 8q) * RW + slot
-        int rq[2];
-        uint32_t bq[2];
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            rq[q] = r0 + (wave + NW * q) * RW + slot;
-            bq[q] = (uact && rq[q] < r1) ? (uint32_t)((size_t)rq[q] * stride) : 0x80000000u;
-        }
+    const uint32_t pass_bytes = (uint32_t)(NW * RW * stride);
+    const uint32_t lane_base = uact ? (uint32_t)((wave * RW + slot) * stride) : 0x80000000u;
+    const int passes = (rows + NW * RW - 1) / (NW * RW);
+    const int nit = *n_items;
+    for (int it = blockIdx.x; it < nit; it += gridDim.x) {
+        const int *rec = items + 4 * it;
+        const int e = rec[0], ne = rec[1], base = rec[2], j = rec[3] & 0xFFFF, nx = rec[3] >> 16;
+        const int p0 = (int)((long)j * passes / nx), p1 = (int)((long)(j + 1) * passes / nx), P = p1 - p0;
+        if (P <= 0) continue; // more chunks than passes: an empty share
+        const int r0 = p0 * NW * RW, rend = min(rows, p1 * NW * RW);
+        const uint32_t strip = (uint32_t)((size_t)(rend - r0) * stride);
+        const rsrc_t rA = make_rsrc(tabA[e] + (size_t)r0 * stride, strip);
+        const rsrc_t rB = make_rsrc((NMAT == 2 ? tabB[e] : tabA[e]) + (size_t)r0 * stride, strip);
         for (int t0 = 0; t0 < ne; t0 += tch) {
-            const int nt = min(tch, ne - t0);
-            WRow<FMT> wa[2], wb[2];
+            const int nt = min(tch, ne - t0), tot = nt * nch;
+            // 1. x of the tokens: chunk f = token (f / nch), piece (f % nch)
+            float4 xv0[MOE_XK], xv1[MOE_XK];
 #pragma unroll
-            for (int q = 0; q < 2; q++) {
-                load_row<FMT>(rA, bq[q], cols, L, wa[q]);
-                if constexpr (NMAT == 2) load_row<FMT>(rB, bq[q], cols, L, wb[q]);
-            }
-            __syncthreads(); // the previous round's readers of LDS are done
-            if (threadIdx.x < nt) slot_s[threadIdx.x] = list[base + t0 + threadIdx.x];
-            __syncthreads();
-            for (int j = 0; j < nt; j++) {
-                uint32_t *xd = (uint32_t *)((uint8_t *)smem + j * tok_bytes);
-                float *s16 = (float *)(xd + (cols >> 2) * XDIG);
-                int *kx = (int *)(s16 + (cols >> 4));
-                stage_x<FMT>(xs + (size_t)(slot_s[j] / xdiv) * cols, cols, xd, s16, kx);
-            }
-            for (int j = 0; j < nt; j++) {
-                const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + j * tok_bytes);
-                const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
-                const int *kx = (const int *)(s16 + (cols >> 4));
-                XReg xv;
-                UConst cj = c;
-                unit_setup_x<FMT>(xd, s16, kx, u, U, xv, cj);
-                const size_t ob = (size_t)slot_s[j] * rows;
-#pragma unroll
-                for (int q = 0; q < 2; q++) {
-                    float pa = unit_dot<FMT>(wa[q], xv, cj);
-                    pa = seg_sum_dpp<LPR>(uact ? pa : 0.0f);
-                    float v = pa;
-                    if constexpr (NMAT == 2) {
-                        float pb = unit_dot<FMT>(wb[q], xv, cj);
-                        pb = seg_sum_dpp<LPR>(uact ? pb : 0.0f);
-                        v = silu(pa) * pb;
-                    }
-                    if (ul == LPR - 1 && rq[q] < r1) out[ob + rq[q]] = v;
+            for (int k = 0; k < MOE_XK; k++) {
+                const int f = k * 512 + (int)threadIdx.x;
+                xv0[k] = xv1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (f < tot) {
+                    const int sl = list[base + t0 + f / nch];
+                    const float4 *x4 = (const float4 *)(xs + (size_t)(sl / xdiv) * cols) + 2 * (f % nch);
+                    xv0[k] = x4[0];
+                    xv1[k] = x4[1];
                 }
             }
+            if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = list[base + t0 + threadIdx.x];
+            __builtin_amdgcn_sched_barrier(0);
+            // 2. the ring
+            WRow<FMT> wa[DEPTH], wb[DEPTH];
+#pragma unroll
+            for (int i = 0; i < DEPTH; i++) {
+                load_row<FMT>(rA, lane_base + (uint32_t)i * pass_bytes, cols, L, wa[i]);
+                if constexpr (NMAT == 2) load_row<FMT>(rB, lane_base + (uint32_t)i * pass_bytes, cols, L, wb[i]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // 3. x into LDS (16-chunk blocks never straddle tokens: nch % 16 == 0)
+#pragma unroll
+            for (int k = 0; k < MOE_XK; k++) {
+                const int fb = k * 512;
+                if (fb < tot) {
+                    const int f = fb + (int)threadIdx.x, tk = f / nch;
+                    uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)(f < tot ? tk : 0) * tok_bytes);
+                    float *s16 = (float *)(xd + (cols >> 2) * XDIG);
+                    int *kx = (int *)(s16 + (cols >> 4));
+                    stage_chunk<FMT>(xv0[k], xv1[k], f % nch, f < tot, U, xd, s16, kx);
+                }
+            }
+            for (int fb = MOE_XK * 512; fb < tot; fb += 512) { // more tokens than one round holds
+                const int f = fb + (int)threadIdx.x, tk = f / nch;
+                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+                if (f < tot) {
+                    const float4 *x4 = (const float4 *)(xs + (size_t)(list[base + t0 + tk] / xdiv) * cols) + 2 * (f % nch);
+                    v0 = x4[0];
+                    v1 = x4[1];
+                }
+                uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)(f < tot ? tk : 0) * tok_bytes);
+                float *s16 = (float *)(xd + (cols >> 2) * XDIG);
+                int *kx = (int *)(s16 + (cols >> 4));
+                stage_chunk<FMT>(v0, v1, f % nch, f < tot, U, xd, s16, kx);
+            }
+            __syncthreads();
+            // 4. passes through the ring: counted whole turns, then the rest.
+            // Q4_K: each pass's rows are decoded once (q4k_prep) and the ring
+            // slot is refilled before the tokens are applied; a token's x is
+            // read from LDS one sub-block (24 dwords) at a time.
+            auto pass_q4k = [&](int j, const Q4Prep (&pr)[NMAT]) {
+                const int row = r0 + (j * NW + wave) * RW + slot;
+                for (int tk = 0; tk < nt; tk++) {
+                    const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)tk * tok_bytes);
+                    const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
+                    const int *kx = (const int *)(s16 + (cols >> 4));
+                    const uint4 *x4 = (const uint4 *)xd;
+                    int sa[NMAT][XDIG], sb[NMAT][XDIG];
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                        for (int k = 0; k < XDIG; k++) sa[m][k] = sb[m][k] = 0;
+                    uint32_t xh[24];
+#pragma unroll
+                    for (int r = 0; r < 6; r++) {
+                        const uint4 v = x4[r * U + u];
+                        xh[4 * r] = v.x;
+                        xh[4 * r + 1] = v.y;
+                        xh[4 * r + 2] = v.z;
+                        xh[4 * r + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) q4k_half(pr[m].lo, xh, sa[m]);
+#pragma unroll
+                    for (int r = 0; r < 6; r++) {
+                        const uint4 v = x4[(r + 6) * U + u];
+                        xh[4 * r] = v.x;
+                        xh[4 * r + 1] = v.y;
+                        xh[4 * r + 2] = v.z;
+                        xh[4 * r + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) q4k_half(pr[m].hi, xh, sb[m]);
+                    const float P = ldexpf(1.0f, -kx[u >> 1]);
+                    const float c0 = s16[4 * u] + s16[4 * u + 1], c1 = s16[4 * u + 2] + s16[4 * u + 3];
+                    float val[NMAT];
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        const float uu = fmaf(pr[m].ka, digits_value(sa[m]), pr[m].kb * digits_value(sb[m]));
+                        const float vv = fmaf(pr[m].kmb, c1, pr[m].kma * c0);
+                        val[m] = seg_sum_dpp<LPR>(uact ? fmaf(P, uu, -vv) : 0.0f);
+                    }
+                    float v = val[0];
+                    if constexpr (NMAT == 2) v = silu(val[0]) * val[1];
+                    if (ul == LPR - 1 && row < rend) out[(size_t)slot_s[tk] * rows + row] = v;
+                }
+            };
+            auto pass = [&](int j, const WRow<FMT> &pa_w, const WRow<FMT> &pb_w) {
+                const int row = r0 + (j * NW + wave) * RW + slot;
+                for (int tk = 0; tk < nt; tk++) {
+                    const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)tk * tok_bytes);
+                    const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
+                    const int *kx = (const int *)(s16 + (cols >> 4));
+                    XReg xv;
+                    UConst cj = c;
+                    unit_setup_x<FMT>(xd, s16, kx, u, U, xv, cj);
+                    float v = seg_sum_dpp<LPR>(uact ? unit_dot<FMT>(pa_w, xv, cj) : 0.0f);
+                    if constexpr (NMAT == 2) {
+                        const float pb = seg_sum_dpp<LPR>(uact ? unit_dot<FMT>(pb_w, xv, cj) : 0.0f);
+                        v = silu(v) * pb;
+                    }
+                    if (ul == LPR - 1 && row < rend) out[(size_t)slot_s[tk] * rows + row] = v;
+                }
+            };
+            const int turns = P / DEPTH;
+            int j0 = 0;
+            for (int tr = 0; tr < turns; tr++, j0 += DEPTH) {
+#pragma unroll
+                for (int i = 0; i < DEPTH; i++) {
+                    if constexpr (FMT == FMT_Q4K) {
+                        Q4Prep pr[NMAT];
+                        q4k_prep(wa[i], c, pr[0]);
+                        if constexpr (NMAT == 2) q4k_prep(wb[i], c, pr[NMAT - 1]);
+                        load_row<FMT>(rA, lane_base + (uint32_t)(j0 + i + DEPTH) * pass_bytes, cols, L, wa[i]);
+                        if constexpr (NMAT == 2)
+                            load_row<FMT>(rB, lane_base + (uint32_t)(j0 + i + DEPTH) * pass_bytes, cols, L, wb[i]);
+                        __builtin_amdgcn_sched_barrier(0);
+                        pass_q4k(j0 + i, pr);
+                    } else {
+                        pass(j0 + i, wa[i], wb[i]);
+                        load_row<FMT>(rA, lane_base + (uint32_t)(j0 + i + DEPTH) * pass_bytes, cols, L, wa[i]);
+                        if constexpr (NMAT == 2)
+                            load_row<FMT>(rB, lane_base + (uint32_t)(j0 + i + DEPTH) * pass_bytes, cols, L, wb[i]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < DEPTH - 1; i++)
+                if (i < P - j0) {
+                    if constexpr (FMT == FMT_Q4K) {
+                        Q4Prep pr[NMAT];
+                        q4k_prep(wa[i], c, pr[0]);
+                        if constexpr (NMAT == 2) q4k_prep(wb[i], c, pr[NMAT - 1]);
+                        pass_q4k(j0 + i, pr);
+                    } else {
+                        pass(j0 + i, wa[i], wb[i]);
+                    }
+                }
+            __syncthreads(); // LDS and slot_s are restaged next
         }
-        __syncthreads(); // LDS is restaged by the next item
     }
 }
 
@@ -315,12 +537,21 @@ __global__ void k_moe_combine(const float *__restrict__ y, const float *__restri
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
+// Work items of the grouped kernels: about one per CU (the grouped kernel
+// holds one workgroup per CU), plus at most one per group from rounding.
+int moe_item_target(const soso_hip *h) { return h->num_cu; }
+size_t moe_max_items(const soso_hip *h, size_t slots, size_t n_groups)
+{
+    return (size_t)moe_item_target(h) + std::min(slots, n_groups) + 1;
+}
+
 // Scratch slots 8..11 belong to the MoE path.
 bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s)
 {
     const size_t slots = n * top_k;
     char *f = (char *)scratch_get(h, 8, (n * (n_groups > 0 ? n_groups : 1) + 2 * slots) * 4);
-    int *ints = (int *)scratch_get(h, 9, (3 * n_groups + 2 + slots) * 4);
+    const size_t n_g = n_groups > 0 ? n_groups : 1;
+    int *ints = (int *)scratch_get(h, 9, (2 * n_g + 2 + slots + 4 * moe_max_items(h, slots, n_g)) * 4);
     float *big = (float *)scratch_get(h, 10, slots * (ffn + hdim) * 4);
     if (!f || !ints || !big) return false;
     s.logits = (float *)f;
@@ -329,8 +560,8 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
     s.cnt = ints;
     s.offs = ints + n_groups;
     s.list = ints + 2 * n_groups + 1;
-    s.act_list = s.list + slots;
-    s.act_n = s.act_list + n_groups;
+    s.items = s.list + slots;
+    s.n_items = s.items + 4 * moe_max_items(h, slots, n_g);
     s.act = big;
     s.ydown = big + slots * ffn;
     return true;
@@ -339,10 +570,11 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
 int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size_t hdim, size_t n_exp, size_t top_k,
                      const MoeScratch &s)
 {
-    const unsigned grid = (unsigned)((n_exp + 7) / 8);
     if (n * top_k > ROUTE_MAX_SLOTS || n_exp > 256) return set_err(h, SOSO_HIP_DECLINED, "moe route: too many slots");
+    const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
     k_moe_route<<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt,
-                                              s.cnt, s.offs, s.list, s.act_list, s.act_n, h->ticket);
+                                              s.cnt, s.offs, s.list, s.items, s.n_items, moe_item_target(h),
+                                              h->ticket);
     return hip_check(h, hipGetLastError(), "moe route launch");
 }
 
@@ -357,15 +589,21 @@ int launch_router_topk(soso_hip *h, const float *w, const float *x, size_t n, si
     return launch_moe_route(h, w, x, n, hdim, n_exp, top_k, s);
 }
 
+// Weight ring depth of the grouped kernel: the deepest ring that fits the
+// register file without spills at one workgroup (8 wavefronts) per CU
+// (gate/up Q4_K: 239 VGPRs at depth 3; down Q4_K: 192 at depth 4; Q6_K gate/up
+// spills beyond depth 2).
+template <int FMT, int NMAT> constexpr int moe_depth() { return NMAT == 2 ? (FMT == FMT_Q6K ? 2 : 3) : 4; }
+
 template <int FMT, int NMAT>
-static void moe_mv_fmt(soso_hip *h, unsigned grid, size_t lds, int lpr, const uint8_t *const *A,
-                       const uint8_t *const *B, size_t stride, int rows, int cols, int chunks, const float *xs,
-                       int xdiv, int tch, const MoeScratch &s, float *out)
+static void moe_rows_fmt(soso_hip *h, unsigned grid, size_t lds, int lpr, const uint8_t *const *A,
+                         const uint8_t *const *B, size_t stride, int rows, int cols, const float *xs, int xdiv,
+                         int tch, const MoeScratch &s, float *out)
 {
 #define MOE_CASE(LP)                                                                                                   \
     case LP:                                                                                                           \
-        k_moe_mv<FMT, LP, NMAT><<<grid, 512, lds, h->stream>>>(A, B, stride, rows, cols, chunks, xs, xdiv, s.cnt,     \
-                                                                s.offs, s.list, s.act_list, s.act_n, tch, out);        \
+        k_moe_rows<FMT, LP, NMAT, moe_depth<FMT, NMAT>()><<<grid, 512, lds, h->stream>>>(A, B, stride, rows, cols, xs, xdiv, s.list,        \
+                                                                     s.items, s.n_items, tch, out);                   \
         break;
     switch (lpr) {
         MOE_CASE(1) MOE_CASE(2) MOE_CASE(4) MOE_CASE(8) MOE_CASE(16) MOE_CASE(32) MOE_CASE(64)
@@ -373,40 +611,41 @@ static void moe_mv_fmt(soso_hip *h, unsigned grid, size_t lds, int lpr, const ui
 #undef MOE_CASE
 }
 
-// One grouped matvec over the active experts (pointer tables on the device).
-// active_max bounds the number of active experts, tch the tokens per expert
+// One grouped matvec over the work items (pointer tables on the device).
+// max_items bounds the items k_moe_route wrote; tch is the tokens per expert
 // staged at a time (at most the tokens of the call).
 static int launch_moe_mv(soso_hip *h, uint8_t dtype, int nmat, const uint8_t *const *A, const uint8_t *const *B,
-                         size_t rows, size_t cols, size_t active_max, size_t tch, const float *xs, int xdiv,
+                         size_t rows, size_t cols, size_t max_items, size_t tch, const float *xs, int xdiv,
                          const MoeScratch &s, float *out)
 {
     const int U = (int)(cols / 64);
-    if (U < 1 || U > 64 || !packed_shape_ok(dtype, rows, cols))
+    if (U < 1 || U > 64 || cols % 128 || !packed_shape_ok(dtype, rows, cols))
         return set_err(h, SOSO_HIP_DECLINED, "moe: expert shape not handled here");
     const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
-    const size_t rpw = 2 * 8 * (64 / lpr);
-    const size_t chunks = (rows + rpw - 1) / rpw;
+    const size_t rows_per_pass = 8 * (64 / lpr);
+    const size_t passes = (rows + rows_per_pass - 1) / rows_per_pass;
     tch = std::max<size_t>(1, std::min<size_t>(tch, 64));
     const size_t tok_bytes = (stage_lds_bytes(cols) + 15) & ~(size_t)15;
     while (tch > 1 && tok_bytes * tch > h->max_lds) tch--;
     const size_t lds = tok_bytes * tch;
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "moe: x does not fit in LDS");
-    const size_t items = active_max * chunks;
-    const unsigned grid = (unsigned)std::max<size_t>(1, std::min<size_t>(items, 2 * (size_t)h->num_cu));
+    const unsigned grid = (unsigned)std::max<size_t>(1, max_items);
     const size_t stride = packed_row_stride(dtype, cols);
-    const int ri = (int)rows, ci = (int)cols, ch = (int)chunks, ti = (int)tch;
+    if ((passes + 2) * rows_per_pass * stride >= ((size_t)1 << 31))
+        return set_err(h, SOSO_HIP_DECLINED, "moe: expert matrix exceeds 2 GiB");
+    const int ri = (int)rows, ci = (int)cols, ti = (int)tch;
     switch (dtype) {
     case SOSO_HIP_DTYPE_Q4_K:
-        if (nmat == 2) moe_mv_fmt<FMT_Q4K, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
-        else moe_mv_fmt<FMT_Q4K, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
+        if (nmat == 2) moe_rows_fmt<FMT_Q4K, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, xs, xdiv, ti, s, out);
+        else moe_rows_fmt<FMT_Q4K, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, xs, xdiv, ti, s, out);
         break;
     case SOSO_HIP_DTYPE_Q8_0:
-        if (nmat == 2) moe_mv_fmt<FMT_Q80, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
-        else moe_mv_fmt<FMT_Q80, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
+        if (nmat == 2) moe_rows_fmt<FMT_Q80, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, xs, xdiv, ti, s, out);
+        else moe_rows_fmt<FMT_Q80, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, xs, xdiv, ti, s, out);
         break;
     case SOSO_HIP_DTYPE_Q6_K:
-        if (nmat == 2) moe_mv_fmt<FMT_Q6K, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
-        else moe_mv_fmt<FMT_Q6K, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, ch, xs, xdiv, ti, s, out);
+        if (nmat == 2) moe_rows_fmt<FMT_Q6K, 2>(h, grid, lds, lpr, A, B, stride, ri, ci, xs, xdiv, ti, s, out);
+        else moe_rows_fmt<FMT_Q6K, 1>(h, grid, lds, lpr, A, B, stride, ri, ci, xs, xdiv, ti, s, out);
         break;
     default: return set_err(h, SOSO_HIP_DECLINED, "moe: expert dtype not handled here");
     }
@@ -419,10 +658,10 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab, size_t n_groups, const float *wgt,
                        const uint8_t *use, const MoeScratch &s, float *out)
 {
-    const size_t active = std::min(n_groups, n * top_k);
-    int rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, active, n, xs, (int)top_k, s, s.act);
+    const size_t max_items = moe_max_items(h, n * top_k, n_groups);
+    int rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, max_items, n, xs, (int)top_k, s, s.act);
     if (rc == SOSO_HIP_OK)
-        rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, active, n, s.act, 1, s, s.ydown);
+        rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_items, n, s.act, 1, s, s.ydown);
     if (rc != SOSO_HIP_OK) return rc;
     const dim3 grid((unsigned)((hdim + 255) / 256), (unsigned)n);
     k_moe_combine<<<grid, 256, 0, h->stream>>>(s.ydown, wgt, use, (int)n, (int)hdim, (int)top_k, out);

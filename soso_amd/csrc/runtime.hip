@@ -422,7 +422,9 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
         if (ok[e]) gid.push_back(e);
     const size_t G = gid.size();
     // [cnt G | offs G+1 | list slots | active groups G | their count], as moe_scratch lays it out
-    std::vector<int> ints(3 * G + 2 + slots, 0);
+    // [cnt G | offs G + 1 | list slots | work items 4 x max_items | item count]
+    const size_t max_items = moe_max_items(h, slots, G ? G : 1);
+    std::vector<int> ints(2 * G + 2 + slots + 4 * max_items, 0);
     std::vector<const uint8_t *> tab(3 * G);
     int o = 0;
     for (size_t g = 0; g < G; g++) {
@@ -436,8 +438,24 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
         for (int k = 0; k < 3; k++) tab[k * G + g] = (const uint8_t *)wts[3 * gid[g] + k]->dev;
     }
     ints[2 * G] = o;
-    for (size_t g = 0; g < G; g++) ints[2 * G + 1 + slots + g] = (int)g;
-    ints[3 * G + 1 + slots] = (int)G;
+    // work items as k_moe_route writes them: group g with c slots gets
+    // max(1, round(c * target / slots)) row chunks
+    {
+        const int target = moe_item_target(h);
+        size_t ni = 0;
+        for (size_t g = 0; g < G; g++) {
+            const int c = ints[g];
+            const int nx = c > 0 ? std::min(0xFFFF, std::max(1, (int)((c * (long)target + (long)slots / 2) / (long)slots))) : 0;
+            for (int j = 0; j < nx && ni < max_items; j++, ni++) {
+                int *r = &ints[2 * G + 1 + slots + 4 * ni];
+                r[0] = (int)g;
+                r[1] = c;
+                r[2] = ints[G + g];
+                r[3] = j | (nx << 16);
+            }
+        }
+        ints[2 * G + 1 + slots + 4 * max_items] = (int)ni;
+    }
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
     float *sd = (float *)scratch_get(h, 5, n * hdim * 4);
     char *aux = (char *)scratch_get(h, 11, slots * 4 + slots + 3 * G * sizeof(void *) + 64);
