@@ -248,20 +248,40 @@ def copy_calibration(g, nbytes=512 << 20, reps=20):
     print(json.dumps({"copy_calibration_bytes": nbytes, "reps": reps}), flush=True)
 
 
-def cpu_baseline(dtype, rows, cols, seconds, threads):
-    """The AVX2+FMA restatement of soso's CPU matvec, contiguous row strips
-    over `threads` host threads (HostPool), on a bounded sample."""
-    from oracle import oracle as orc
-    copies = 4  # 132 MB of Q4_K: above the host's last-level cache
-    ws = [orc.synth(dtype, rows, cols, 1, 1000 + i) for i in range(copies)]
-    x = orc.normal(cols, 1.0, 1, 7)
-    orc.matvec(dtype, ws[0], rows, cols, x, threads=threads, avx2=True)
+CPU_ROTATE_BYTES = 512 << 20  # every CPU sample rotates this much: above any host last-level cache
+
+
+def _cpu_copies(nbytes):
+    return max(2, -(-CPU_ROTATE_BYTES // nbytes))
+
+
+def _cpu_rate(fn, nbytes, budget):
+    """Calls fn(i) for i = 0, 1, ... for `budget` seconds after one warm call;
+    returns (GB/s of nbytes per call, calls)."""
+    fn(0)
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        orc.matvec(dtype, ws[n % copies], rows, cols, x, threads=threads, avx2=True)
+    while time.perf_counter() - t0 < budget:
+        fn(n)
         n += 1
     dt = (time.perf_counter() - t0) / n
-    return algo_bytes(dtype, rows, cols) / dt / 1e9, n, dt * 1e3
+    return round(nbytes / dt / 1e9, 2), n
+
+
+def cpu_baseline(dtype, rows, cols, seconds, threads):
+    """The AVX2+FMA restatement of soso's CPU matvec, contiguous row strips
+    over `threads` host threads (HostPool), on a bounded sample over rotating
+    copies (>= 512 MB).  Returns (GB/s, calls, ms per call, copies, the
+    1-thread GB/s over the same copies)."""
+    from oracle import oracle as orc
+    nb = algo_bytes(dtype, rows, cols)
+    copies = _cpu_copies(nb)
+    ws = [orc.synth(dtype, rows, cols, 1, 1000 + i) for i in range(copies)]
+    x = orc.normal(cols, 1.0, 1, 7)
+    gbs, n = _cpu_rate(lambda i: orc.matvec(dtype, ws[i % copies], rows, cols, x, threads=threads, avx2=True), nb,
+                       seconds)
+    one, _ = _cpu_rate(lambda i: orc.matvec(dtype, ws[i % copies], rows, cols, x, threads=1, avx2=True), nb,
+                       seconds / 4)
+    return gbs, n, nb / gbs / 1e6, copies, one
 
 
 def time_single_launch(g, dtype, rows, cols, reps=50, seed=1):
@@ -328,52 +348,43 @@ def head_parity(g, threads, seed=1):
 
 
 def cpu_extra(seconds, threads):
-    """The rest of the CPU baseline (oracle/ restatements, bounded samples):
-    host DRAM read bandwidth (STREAM-like sum, the CPU roofline), the
-    headline Q4_K at 1 thread, configs[0] Q8_0, and configs[2]'s head both
-    ways soso could run it -- the restated Q6_K dequant+dot, and Q6_K
-    requantized to Q8_0 (gguf2som/src/lib.rs:1592-1609) then AVX2
-    matvec_q8_0 -- on a row sample.  GB/s are algorithmic bytes of the
-    format the kernel reads."""
+    """The rest of the CPU baseline (oracle/ restatements, bounded samples,
+    every one rotating >= 512 MB): host DRAM read bandwidth (STREAM-like sum,
+    the CPU roofline), configs[0] Q8_0, and configs[2]'s head both ways soso
+    could run it -- the restated Q6_K dequant+dot, and Q6_K requantized to
+    Q8_0 (gguf2som/src/lib.rs:1592-1609) then AVX2 matvec_q8_0 -- on row
+    samples.  GB/s are algorithmic bytes of the format the kernel reads."""
     from oracle import oracle as orc
     out = {}
-
-    def rate(fn, nbytes, budget):
-        fn()
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < budget:
-            fn()
-            n += 1
-        dt = (time.perf_counter() - t0) / n
-        return round(nbytes / dt / 1e9, 2), n
-
     a = np.ones(1 << 28, np.float32)  # 1 GiB
-    out["host_read_GB_s"], _ = rate(lambda: orc.lib().or_stream_read(a.ctypes.data, a.size, threads), a.nbytes,
-                                    seconds / 4)
+    out["host_read_GB_s"], _ = _cpu_rate(lambda i: orc.lib().or_stream_read(a.ctypes.data, a.size, threads),
+                                         a.nbytes, seconds / 4)
     del a
-    rows, cols = 14336, 4096
-    w = orc.synth(Q4K, rows, cols, 1, 1000)
-    x = orc.normal(cols, 1.0, 1, 7)
-    out["q4_k_14336x4096_1thread_GB_s"], _ = rate(lambda: orc.matvec(Q4K, w, rows, cols, x, threads=1, avx2=True),
-                                                  algo_bytes(Q4K, rows, cols), seconds / 4)
-    ws = [orc.synth(Q8, 4096, 4096, 1, 1000 + i) for i in range(8)]
-    x8 = orc.normal(4096, 1.0, 1, 7)
-    it = iter(range(1 << 30))
-    out["q8_0_4096x4096_GB_s"], _ = rate(
-        lambda: orc.matvec(Q8, ws[next(it) % 8], 4096, 4096, x8, threads=threads, avx2=True),
-        algo_bytes(Q8, 4096, 4096), seconds / 4)
-    hr = 16384  # head row sample: 55 MB of Q6_K, 75 MB of Q8_0 per call
-    wq6 = orc.synth(Q6K, hr, cols, 1, 1000)
-    out["q6_k_head_restated_GB_s"], _ = rate(lambda: orc.matvec(Q6K, wq6, hr, cols, x, threads=threads),
-                                             algo_bytes(Q6K, hr, cols), seconds / 8)
+    nb8 = algo_bytes(Q8, 4096, 4096)
+    c8 = _cpu_copies(nb8)
+    ws = [orc.synth(Q8, 4096, 4096, 1, 1000 + i) for i in range(c8)]
+    x = orc.normal(4096, 1.0, 1, 7)
+    out["q8_0_4096x4096_GB_s"], _ = _cpu_rate(
+        lambda i: orc.matvec(Q8, ws[i % c8], 4096, 4096, x, threads=threads, avx2=True), nb8, seconds / 4)
+    del ws
+    hr, cols = 16384, 4096  # head row samples: 55 MB of Q6_K, 75 MB of Q8_0 each
+    ch = _cpu_copies(algo_bytes(Q6K, hr, cols))
+    q6 = [orc.synth(Q6K, hr, cols, 1, 2000 + i) for i in range(ch)]
+    out["q6_k_head_restated_GB_s"], _ = _cpu_rate(
+        lambda i: orc.matvec(Q6K, q6[i % ch], hr, cols, x, threads=threads), algo_bytes(Q6K, hr, cols), seconds / 4)
     deq = np.empty(hr * cols, np.float32)
-    orc.lib().or_dequant_q6_k(wq6.ctypes.data, wq6.nbytes, deq.ctypes.data, deq.size)
-    wq8 = np.empty(hr * (cols // 32) * 36, np.uint8)
-    orc.lib().or_quantize_q8_0(deq.ctypes.data, deq.size, wq8.ctypes.data)
-    out["q6_k_head_as_q8_0_GB_s"], _ = rate(lambda: orc.matvec(Q8, wq8, hr, cols, x, threads=threads, avx2=True),
-                                            algo_bytes(Q8, hr, cols), seconds / 8)
-    out["sample"] = (f"~{seconds:.0f} s in all: 1 GiB host read; Q4_K 14336x4096 at 1 thread; 8 rotating Q8_0 "
-                     f"4096x4096; head row sample {hr}x{cols} (Q6_K restated, and requantized to Q8_0)")
+    q8 = []
+    for w6 in q6:
+        orc.lib().or_dequant_q6_k(w6.ctypes.data, w6.nbytes, deq.ctypes.data, deq.size)
+        w8 = np.empty(hr * (cols // 32) * 36, np.uint8)
+        orc.lib().or_quantize_q8_0(deq.ctypes.data, deq.size, w8.ctypes.data)
+        q8.append(w8)
+    del deq, q6
+    out["q6_k_head_as_q8_0_GB_s"], _ = _cpu_rate(
+        lambda i: orc.matvec(Q8, q8[i % ch], hr, cols, x, threads=threads, avx2=True), algo_bytes(Q8, hr, cols),
+        seconds / 4)
+    out["sample"] = (f"~{seconds:.0f} s in all, each sample rotating >= 512 MB: 1 GiB host read; {c8} Q8_0 "
+                     f"4096x4096 copies; {ch} head row samples {hr}x{cols} (Q6_K restated, and requantized to Q8_0)")
     return out
 
 
@@ -477,11 +488,11 @@ def main():
             "bytes_per_token": int(b_d), "greedy_token": tok_d}
         line["configs"] = extra
     if not args.no_cpu:
-        gbs, n, ms = cpu_baseline(Q4K, rows, cols, args.cpu_seconds, args.cpu_threads)
-        line["cpu_baseline"] = {"value": round(gbs, 2), "unit": "GB/s", "cores": args.cpu_threads, "kind": "port",
-                                "sample": f"{n} AVX2 Q4_K matvecs 14336x4096 over 4 rotating copies "
+        gbs, n, ms, copies, one = cpu_baseline(Q4K, rows, cols, args.cpu_seconds, args.cpu_threads)
+        line["cpu_baseline"] = {"value": gbs, "unit": "GB/s", "cores": args.cpu_threads, "kind": "port",
+                                "sample": f"{n} AVX2 Q4_K matvecs 14336x4096 over {copies} rotating copies "
                                           f"({ms:.2f} ms each) in ~{args.cpu_seconds:.0f} s",
-                                "host_nproc": os.cpu_count()}
+                                "host_nproc": os.cpu_count(), "one_thread_GB_s": one}
         line["cpu_baseline"]["more"] = cpu_extra(args.cpu_seconds, args.cpu_threads)
     g.close()
     print(json.dumps(line), flush=True)

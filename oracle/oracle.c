@@ -884,12 +884,7 @@ typedef struct {
 static void *read_thread(void *p)
 {
     read_job *j = (read_job *)p;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    size_t i = j->s;
-    for (; i + 4 <= j->e; i += 4)
-        for (int k = 0; k < 4; k++) acc[k] += j->a[i + (size_t)k];
-    for (; i < j->e; i++) acc[0] += j->a[i];
-    j->sum = (double)acc[0] + acc[1] + acc[2] + acc[3];
+    j->sum = or_sum_f32_avx2(j->a + j->s, j->e - j->s);
     return NULL;
 }
 

@@ -136,6 +136,8 @@ void or_synth_normal(float *out, size_t n, float sigma, uint64_t seed, uint64_t 
 
 /* ---- timing helper for the CPU baseline ---------------------------------- */
 double or_now_seconds(void);
+/* Sum of n floats with four 8-wide AVX2 accumulators (scalar without AVX2). */
+double or_sum_f32_avx2(const float *a, size_t n);
 /* STREAM-like threaded read of n floats (host DRAM roofline); returns the sum. */
 double or_stream_read(const float *a, size_t n, int threads);
 

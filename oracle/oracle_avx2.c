@@ -160,3 +160,24 @@ void or_swiglu_avx2(float *up, const float *gate, size_t n)
         memcpy(up + i, t, r * 4);
     }
 }
+
+/* The read kernel of the host-bandwidth measurement (not part of soso's path):
+ * four independent 8-wide accumulators so the loop is bound by memory, not by
+ * the add latency. */
+double or_sum_f32_avx2(const float *a, size_t n)
+{
+    __m256 s0 = _mm256_setzero_ps(), s1 = s0, s2 = s0, s3 = s0;
+    size_t i = 0;
+    for (; i + 32 <= n; i += 32) {
+        s0 = _mm256_add_ps(s0, _mm256_loadu_ps(a + i));
+        s1 = _mm256_add_ps(s1, _mm256_loadu_ps(a + i + 8));
+        s2 = _mm256_add_ps(s2, _mm256_loadu_ps(a + i + 16));
+        s3 = _mm256_add_ps(s3, _mm256_loadu_ps(a + i + 24));
+    }
+    float t[8];
+    _mm256_storeu_ps(t, _mm256_add_ps(_mm256_add_ps(s0, s1), _mm256_add_ps(s2, s3)));
+    double sum = 0.0;
+    for (int k = 0; k < 8; k++) sum += t[k];
+    for (; i < n; i++) sum += a[i];
+    return sum;
+}
