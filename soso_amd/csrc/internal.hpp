@@ -154,11 +154,18 @@ struct MoeScratch {
     float *wgt = nullptr;    // n x top_k
     int *cnt = nullptr, *offs = nullptr, *list = nullptr; // n_groups, n_groups + 1, n x top_k
     int *items = nullptr, *n_items = nullptr; // work items {group, count, first slot, chunk | chunks << 16}, count
+    int *recs = nullptr, *n_recs = nullptr;   // active groups {group, count, first slot, 0} (ascending), count
     float *act = nullptr;    // n x top_k x ffn
     float *ydown = nullptr;  // n x top_k x hdim
 };
 bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s);
 int moe_item_target(const soso_hip *h);
+// (k_mfma.hip) -- Q4_K on the matrix cores for several tokens per row
+bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols);
+int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_t *const *B, size_t rows, size_t cols,
+                    size_t max_recs, const float *xs, int xdiv, const int *list, const int *recs, const int *n_recs,
+                    float *out);
+int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y);
 size_t moe_max_items(const soso_hip *h, size_t slots, size_t n_groups);
 int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim,
                        size_t n_exp, size_t top_k, int32_t *idx_dev, float *wgt_dev, float *logits_dev);

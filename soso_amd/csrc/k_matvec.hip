@@ -595,8 +595,15 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, con
     return hip_check(h, hipGetLastError(), "matvec_ex launch");
 }
 
+// n vectors: from MATMUL_MFMA_MIN tokens up, Q4_K goes to the matrix cores
+// (k_mfma.hip: within the same 1e-5 of the exact product, not bit-identical to
+// the single-vector kernel); fewer vectors run the single-vector kernel once
+// per vector, so each is bit-identical to its own matvec.
+constexpr size_t MATMUL_MFMA_MIN = 16;
+
 int launch_matvec(soso_hip *h, const Weight &w, const float *x, float *y, size_t n)
 {
+    if (n >= MATMUL_MFMA_MIN && mfma_shape_ok(w.dtype, w.rows, w.cols)) return launch_mfma_matmul(h, w, x, n, y);
     for (size_t t = 0; t < n; t++) {
         const float *xt = x + t * w.cols;
         float *yt = y + t * w.rows;

@@ -1,0 +1,360 @@
+// k_mfma.hip -- Q4_K products of several tokens per weight row on the matrix
+// cores: the MoE experts when a call routes two or more tokens to each active
+// expert on average, and `matmul` (GpuDispatch::matmul, crates/soso-llm-core/
+// src/gpu.rs:443-455) from 16 tokens up.
+//
+// Exact integer arithmetic, as in the single-token kernels: x is staged as
+// three balanced signed base-256 digits of X = rint(x 2^e), one exponent e per
+// 256-element super-block (|X| <= 2^22), and the Q4_K codes q (0..15) are
+// int8 already, so v_mfma_i32_16x16x32_i8 returns exact int32 sums
+//   S[digit][row] = sum_{k in sub-block} digit_k * q_k
+// for one 32-element sub-block.  Per sub-block the 6-bit scale is applied in
+// integers (acc += sc * S, |acc| < 2^25 over a super-block), per super-block
+// in f32: y += d * 2^-e * (acc0 + 256 acc1 + 65536 acc2) - dmin * sum_sb m_sb
+// * sum(x over sb) -- the factorised Q4_K dot of crates/sosomodel/src/
+// dequant.rs:172-201.
+//
+// MFMA operands (16 x 16 x 32, int8; lane l, g = l / 16):
+//   A (16 x 32): row m = l % 16 = (token m / 4 of the tile, digit m % 4; digit
+//                3 is a zero pad), k = 8g .. 8g + 7  <- LDS
+//   B (32 x 16): column n = l % 16 = weight row, k = 8g .. 8g + 7  <- the 8
+//                codes of row n, elements 8g .. 8g + 7 of the sub-block
+//   D (16 x 16): column n = l % 16, rows 4g .. 4g + 3 = token g of the tile,
+//                digits 0..3
+// so every lane ends up with one (weight row, token) pair per tile: the
+// row's scales apply lane by lane, and the min term is one FMA.
+//
+// Work: a workgroup of MF_NW wavefronts owns 16 rows per wavefront of one
+// expert (or of the dense weight) and loops over its tokens in rounds of
+// 4 * MT, and over the columns in chunks of `kcmax` (as many as LDS holds for
+// the round's tokens: one chunk for the MoE expert shapes).
+#include "mv_core.hpp"
+
+typedef int mf_v4i __attribute__((ext_vector_type(4)));
+
+constexpr int MF_NW = 4;            // wavefronts per workgroup
+constexpr int MF_ROWS = 16 * MF_NW; // rows per workgroup (16 per wavefront)
+
+// LDS per token for kc staged columns: digits [sub-block][3][32 B], then the
+// f32 sums of x per sub-block, then 2^-e per super-block.
+__host__ __device__ inline int mf_tok_bytes(int kc) { return kc / 32 * 96 + kc / 32 * 4 + kc / 256 * 4; }
+
+// One super-block of one weight row as a lane loads it: the 16-byte header
+// (d, dmin, 12 scale bytes) and, for each of the 4 units, the 8 code bytes of
+// elements 8g .. 8g + 7 (low nibbles: sub-block 2p, high: 2p + 1).
+struct MfSb {
+    uint4 h;
+    uint2 q[4];
+};
+
+// `in` false: the super-block lies past the chunk -- the offset is moved past
+// the strip so the loads read zeros without touching memory.
+__device__ __forceinline__ void mf_load_sb(rsrc_t r, uint32_t rowoff, uint32_t qoff, int sb, bool in, MfSb &s)
+{
+    rowoff = in ? rowoff : 0x80000000u;
+    s.h = bld16(r, rowoff + 16u * (uint32_t)sb);
+#pragma unroll
+    for (int p = 0; p < 4; p++) s.q[p] = bld8(r, rowoff + qoff + 16u * (uint32_t)(4 * sb + p));
+}
+
+// The scales of a super-block's 8 sub-blocks (get_scale_min_k4,
+// dequant.rs:150-159), four per dword: sc[j] = byte j of sc4[j / 4], same for m.
+struct MfScale {
+    float d, dmin;
+    uint32_t sc4[2], m4[2];
+};
+
+__device__ __forceinline__ void mf_scales(const uint4 &h, MfScale &s)
+{
+    s.d = half_bits_to_f32(h.x & 0xffffu);
+    s.dmin = half_bits_to_f32(h.x >> 16);
+    s.sc4[0] = h.y & 0x3F3F3F3Fu;
+    s.m4[0] = h.z & 0x3F3F3F3Fu;
+    s.sc4[1] = (h.w & 0x0F0F0F0Fu) | ((h.y >> 2) & 0x30303030u);
+    s.m4[1] = ((h.w >> 4) & 0x0F0F0F0Fu) | ((h.z >> 2) & 0x30303030u);
+}
+
+__device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (8 * j)) & 0xffu); }
+
+// tabA/tabB: per-expert weight pointer tables (MoE), or null with W0 the dense
+// weight.  recs[4a ..] = {expert, tokens, first slot, 0} for a < *n_recs
+// (MoE), or dense_n > 0 tokens of one dense product (slot = token).  Item:
+// blockIdx.x = a * nblk + row block (MoE), or row block + nblk * token round
+// (dense).  Slot s reads x = xs + (s / xdiv) * cols and writes out[s * rows + r].
+template <int NMAT, int MT>
+__global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
+                                                  const uint8_t *const *__restrict__ tabB,
+                                                  const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
+                                                  const float *__restrict__ xs, int xdiv, const int *__restrict__ list,
+                                                  const int *__restrict__ recs, const int *__restrict__ n_recs,
+                                                  int dense_n, int kcmax, float *__restrict__ out)
+{
+    constexpr int TR = 4 * MT; // tokens per round
+    extern __shared__ uint4 mf_smem[];
+    uint8_t *lds = (uint8_t *)mf_smem;
+    __shared__ int slot_s[TR];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nblk = (rows + MF_ROWS - 1) / MF_ROWS;
+    int e = 0, ne, base = 0, b, t_first, t_step;
+    if (dense_n > 0) {
+        b = blockIdx.x % nblk;
+        ne = dense_n;
+        t_first = (blockIdx.x / nblk) * TR; // one round per workgroup
+        t_step = (int)(gridDim.x / nblk) * TR;
+    } else {
+        const int a = blockIdx.x / nblk;
+        b = blockIdx.x % nblk;
+        if (a >= *n_recs) return; // fewer active experts than the grid allows
+        const int *rec = recs + 4 * a;
+        e = rec[0];
+        ne = rec[1];
+        base = rec[2];
+        t_first = 0;
+        t_step = TR;
+    }
+    const uint8_t *WA = dense_n > 0 ? W0 : tabA[e];
+    const uint8_t *WB = NMAT == 2 ? tabB[e] : WA;
+    const int nl = lane & 15, g = lane >> 4;
+    const uint32_t rowoff = (uint32_t)((16 * wave + nl) * stride); // past the strip: zeros
+    const int nb = cols >> 8, U = cols >> 6;
+    const uint32_t qoff = (uint32_t)(16 * nb + (g < 2 ? 0 : 16 * U) + 8 * (g & 1));
+    // A operand of this lane: token (nl / 4) of a tile, digit nl % 4, bytes 8g .. 8g + 7
+    const int a_tok = nl >> 2, a_dig = nl & 3;
+
+    for (int t0 = t_first; t0 < ne; t0 += t_step) {
+        const int nt = min(TR, ne - t0);
+        __syncthreads(); // the previous round's readers of slot_s and LDS are done
+        if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = list ? list[base + t0 + threadIdx.x] : base + t0 + threadIdx.x;
+        __syncthreads();
+        const int r0 = b * MF_ROWS, rend = min(rows, r0 + MF_ROWS);
+        const uint32_t strip = (uint32_t)((size_t)(rend - r0) * stride);
+        const rsrc_t rA = make_rsrc(WA + (size_t)r0 * stride, strip);
+        const rsrc_t rB = make_rsrc(WB + (size_t)r0 * stride, strip);
+        const int row = r0 + 16 * wave + nl; // this lane's weight row
+        float accf[NMAT][MT];
+#pragma unroll
+        for (int m = 0; m < NMAT; m++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) accf[m][mt] = 0.0f;
+        for (int k0 = 0; k0 < cols; k0 += kcmax) {
+            const int kc = min(kcmax, cols - k0), tb = mf_tok_bytes(kc), nsb = kc >> 8;
+            const int sb0 = k0 >> 8;
+            // the chunk's first weights are requested before x is staged, so
+            // their latency overlaps the staging (loads return in issue order)
+            MfSb ca, cb;
+            mf_load_sb(rA, rowoff, qoff, sb0, true, ca);
+            if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0, true, cb);
+            __builtin_amdgcn_sched_barrier(0);
+            // ---- stage x (columns k0 .. k0 + kc of the round's tokens) ----
+            const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
+            for (int fb = 0; fb < tot; fb += 64 * MF_NW) {
+                const int f = fb + (int)threadIdx.x;
+                const bool valid = f < tot;
+                const int tt = valid ? f / cpt : 0, c = f % cpt;
+                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+                if (valid) {
+                    const float4 *x4 =
+                        (const float4 *)(xs + (size_t)(slot_s[tt] / xdiv) * cols + k0) + 2 * c;
+                    v0 = x4[0];
+                    v1 = x4[1];
+                }
+                // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
+                float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                                 fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+                mx = row16_max(mx);
+                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                const int ex = (mx > 0.0f && mx < INFINITY) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+                // f32 sum of x over the 32-element sub-block: 4 aligned lanes
+                float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+                sm += dpp_f<0xB1>(sm);
+                sm += dpp_f<0x4E>(sm);
+                if (valid) {
+                    uint32_t d0[XDIG], d1[XDIG];
+                    digits4(v0, ex, d0);
+                    digits4(v1, ex, d1);
+                    uint8_t *tp = lds + (size_t)tt * tb;
+                    const int sbl = c >> 2, q = c & 3;
+#pragma unroll
+                    for (int k = 0; k < XDIG; k++)
+                        *(uint2 *)(tp + (sbl * 3 + k) * 32 + 8 * q) = make_uint2(d0[k], d1[k]);
+                    if (q == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
+                    if ((c & 31) == 0) *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = ldexpf(1.0f, -ex);
+                }
+            }
+            __syncthreads();
+            // ---- stream this chunk's super-blocks of the wavefront's 16 rows ----
+            auto superblock = [&](int sbl8, const MfSb &A_, const MfSb &B_) {
+                // sbl8: first local sub-block of this super-block
+                MfScale sA, sB;
+                mf_scales(A_.h, sA);
+                if constexpr (NMAT == 2) mf_scales(B_.h, sB);
+                int acc[NMAT][MT][3];
+                float mins[NMAT][MT];
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        acc[m][mt][0] = acc[m][mt][1] = acc[m][mt][2] = 0;
+                        mins[m][mt] = 0.0f;
+                    }
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int j0 = 2 * p, j1 = 2 * p + 1; // sub-blocks of the unit
+                    long lo[NMAT], hi[NMAT];
+                    {
+                        const uint2 q = A_.q[p];
+                        lo[0] = (long)(((uint64_t)(q.y & 0x0F0F0F0Fu) << 32) | (q.x & 0x0F0F0F0Fu));
+                        hi[0] = (long)(((uint64_t)((q.y >> 4) & 0x0F0F0F0Fu) << 32) | ((q.x >> 4) & 0x0F0F0F0Fu));
+                    }
+                    if constexpr (NMAT == 2) {
+                        const uint2 q = B_.q[p];
+                        lo[NMAT - 1] = (long)(((uint64_t)(q.y & 0x0F0F0F0Fu) << 32) | (q.x & 0x0F0F0F0Fu));
+                        hi[NMAT - 1] =
+                            (long)(((uint64_t)((q.y >> 4) & 0x0F0F0F0Fu) << 32) | ((q.x >> 4) & 0x0F0F0F0Fu));
+                    }
+                    int scA0 = mf_byte(sA.sc4[j0 >> 2], j0 & 3), scA1 = mf_byte(sA.sc4[j1 >> 2], j1 & 3);
+                    float mA0 = (float)mf_byte(sA.m4[j0 >> 2], j0 & 3), mA1 = (float)mf_byte(sA.m4[j1 >> 2], j1 & 3);
+                    int scB0 = 0, scB1 = 0;
+                    float mB0 = 0.f, mB1 = 0.f;
+                    if constexpr (NMAT == 2) {
+                        scB0 = mf_byte(sB.sc4[j0 >> 2], j0 & 3);
+                        scB1 = mf_byte(sB.sc4[j1 >> 2], j1 & 3);
+                        mB0 = (float)mf_byte(sB.m4[j0 >> 2], j0 & 3);
+                        mB1 = (float)mf_byte(sB.m4[j1 >> 2], j1 & 3);
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        if (mt * 4 >= nt) break; // uniform
+                        // A: token mt*4 + a_tok, digit a_dig (3: zero), elements 8g..8g+7
+                        const int ta = mt * 4 + a_tok;
+                        long x0 = 0, x1 = 0;
+                        if (a_dig < 3 && ta < nt) {
+                            const uint8_t *tp = lds + (size_t)ta * tb;
+                            const uint2 u0 = *(const uint2 *)(tp + ((sbl8 + j0) * 3 + a_dig) * 32 + 8 * g);
+                            const uint2 u1 = *(const uint2 *)(tp + ((sbl8 + j1) * 3 + a_dig) * 32 + 8 * g);
+                            x0 = (long)(((uint64_t)u0.y << 32) | u0.x);
+                            x1 = (long)(((uint64_t)u1.y << 32) | u1.x);
+                        }
+                        // the x sums of this lane's output token (mt*4 + g)
+                        const int to = mt * 4 + g;
+                        const float *xsum = (const float *)(lds + (size_t)(to < nt ? to : 0) * tb + (kc >> 5) * 96);
+                        const float xs0 = xsum[sbl8 + j0], xs1 = xsum[sbl8 + j1];
+                        const mf_v4i zero = {0, 0, 0, 0};
+                        mf_v4i D0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, lo[0], zero, 0, 0, 0);
+                        mf_v4i D1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, hi[0], zero, 0, 0, 0);
+#pragma unroll
+                        for (int i = 0; i < 3; i++)
+                            acc[0][mt][i] += __mul24(D0[i], scA0) + __mul24(D1[i], scA1);
+                        mins[0][mt] = fmaf(mA0, xs0, fmaf(mA1, xs1, mins[0][mt]));
+                        if constexpr (NMAT == 2) {
+                            mf_v4i E0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, lo[NMAT - 1], zero, 0, 0, 0);
+                            mf_v4i E1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, hi[NMAT - 1], zero, 0, 0, 0);
+#pragma unroll
+                            for (int i = 0; i < 3; i++)
+                                acc[NMAT - 1][mt][i] += __mul24(E0[i], scB0) + __mul24(E1[i], scB1);
+                            mins[NMAT - 1][mt] = fmaf(mB0, xs0, fmaf(mB1, xs1, mins[NMAT - 1][mt]));
+                        }
+                    }
+                    // one unit at a time: keeps each unit's LDS reads and MFMA
+                    // results from being hoisted into the next (register pressure)
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // f32 per super-block: y += d 2^-e (acc0 + 256 acc1 + 65536 acc2) - dmin * mins
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    if (mt * 4 >= nt) break;
+                    const int to = mt * 4 + g;
+                    const float P = *(const float *)(lds + (size_t)(to < nt ? to : 0) * tb + (kc >> 5) * 100 +
+                                                     4 * (sbl8 >> 3));
+                    const float tA = fmaf((float)acc[0][mt][2], 65536.0f,
+                                          fmaf((float)acc[0][mt][1], 256.0f, (float)acc[0][mt][0]));
+                    accf[0][mt] = fmaf(-sA.dmin, mins[0][mt], fmaf(sA.d * P, tA, accf[0][mt]));
+                    if constexpr (NMAT == 2) {
+                        const float tB = fmaf((float)acc[NMAT - 1][mt][2], 65536.0f,
+                                              fmaf((float)acc[NMAT - 1][mt][1], 256.0f, (float)acc[NMAT - 1][mt][0]));
+                        accf[NMAT - 1][mt] =
+                            fmaf(-sB.dmin, mins[NMAT - 1][mt], fmaf(sB.d * P, tB, accf[NMAT - 1][mt]));
+                    }
+                }
+            };
+            // double buffer: super-block i + 1 is requested before i is applied
+            for (int i = 0; i < nsb; i++) {
+                MfSb na, nbx;
+                mf_load_sb(rA, rowoff, qoff, sb0 + i + 1, i + 1 < nsb, na);
+                if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0 + i + 1, i + 1 < nsb, nbx);
+                __builtin_amdgcn_sched_barrier(0);
+                superblock(8 * i, ca, cb);
+                ca = na;
+                if constexpr (NMAT == 2) cb = nbx;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __syncthreads(); // LDS is restaged for the next chunk or round
+        }
+        // ---- outputs: lane (row, token mt*4 + g) ----
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int to = mt * 4 + g;
+            if (mt * 4 < nt && to < nt && row < rows) {
+                float v = accf[0][mt];
+                if constexpr (NMAT == 2) v = v / (1.0f + expf(-v)) * accf[NMAT - 1][mt];
+                out[(size_t)slot_s[to] * rows + row] = v;
+            }
+        }
+    }
+}
+
+// Columns staged per chunk: the largest multiple of 256 whose x for `tokens`
+// tokens fits the workgroup's LDS.
+static int mf_kc(const soso_hip *h, size_t cols, int tokens)
+{
+    int kc = (int)cols;
+    while (kc > 256 && (size_t)tokens * mf_tok_bytes(kc) > h->max_lds) kc = ((kc / 2) + 255) / 256 * 256;
+    return kc;
+}
+
+// Shapes the matrix-core path handles: Q4_K rows, strips addressable with
+// 32-bit offsets.
+bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols)
+{
+    return dtype == SOSO_HIP_DTYPE_Q4_K && cols % 256 == 0 && cols >= 256 && rows > 0 &&
+           (size_t)MF_ROWS * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
+}
+
+// MoE: one grouped product over the active-expert records (device).
+int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_t *const *B, size_t rows, size_t cols,
+                    size_t max_recs, const float *xs, int xdiv, const int *list, const int *recs, const int *n_recs,
+                    float *out)
+{
+    if (!mfma_shape_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols)) return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
+    constexpr int MT = 2;
+    const int kc = mf_kc(h, cols, 4 * MT);
+    const size_t nblk = (rows + MF_ROWS - 1) / MF_ROWS;
+    const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
+    const unsigned grid = (unsigned)(max_recs * nblk);
+    const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
+    if (nmat == 2)
+        k_mfma_q4k<2, MT><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, (int)rows, (int)cols, xs, xdiv,
+                                                                list, recs, n_recs, 0, kc, out);
+    else
+        k_mfma_q4k<1, MT><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, (int)rows, (int)cols, xs,
+                                                                xdiv, list, recs, n_recs, 0, kc, out);
+    return hip_check(h, hipGetLastError(), "mfma moe launch");
+}
+
+// Dense: Y[n x rows] = X[n x cols] . W^T, one workgroup per (128-row block,
+// round of 16 tokens).
+int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
+{
+    if (!mfma_shape_ok(w.dtype, w.rows, w.cols) || n == 0 || n > (1u << 20))
+        return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
+    constexpr int MT = 4;
+    const size_t nblk = (w.rows + MF_ROWS - 1) / MF_ROWS, rounds = (n + 4 * MT - 1) / (4 * MT);
+    const int kc = mf_kc(h, w.cols, 4 * MT);
+    const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
+    const unsigned grid = (unsigned)(nblk * rounds);
+    k_mfma_q4k<1, MT><<<grid, 64 * MF_NW, lds, h->stream>>>(nullptr, nullptr, (const uint8_t *)w.dev,
+                                                            packed_row_stride(w.dtype, w.cols), (int)w.rows,
+                                                            (int)w.cols, x, 1, nullptr, nullptr, nullptr, (int)n, kc, y);
+    return hip_check(h, hipGetLastError(), "mfma matmul launch");
+}

@@ -92,8 +92,8 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
                                                     int32_t *__restrict__ idx, float *__restrict__ wgt,
                                                     int *__restrict__ cnt, int *__restrict__ offs,
                                                     int *__restrict__ list, int *__restrict__ items,
-                                                    int *__restrict__ n_items, int target,
-                                                    unsigned *__restrict__ ticket)
+                                                    int *__restrict__ n_items, int target, int *__restrict__ recs,
+                                                    int *__restrict__ n_recs, unsigned *__restrict__ ticket)
 {
     __shared__ int last;
     __shared__ int pre_s[257];
@@ -243,6 +243,24 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
             *n_items = incl;
             *ticket = 0u;
         }
+    }
+    if (wave == 1) {
+        // active-expert records, ascending: recs[4a ..] = {expert, slots, first slot, 0}
+        int nact = 0;
+        for (int x0 = 0; x0 < n_exp; x0 += 64) {
+            const int x = x0 + lane;
+            const bool on = x < n_exp && c_s[x] > 0;
+            const unsigned long long m = __ballot(on);
+            if (on) {
+                int *r = recs + 4 * (nact + __popcll(m & ((1ull << lane) - 1ull)));
+                r[0] = x;
+                r[1] = c_s[x];
+                r[2] = o_s[x];
+                r[3] = 0;
+            }
+            nact += __popcll(m);
+        }
+        if (lane == 0) *n_recs = nact;
     }
     __syncthreads();
     // items[4i .. 4i+3] = {expert, its slot count, its first slot, chunk | chunks << 16};
@@ -551,7 +569,7 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
     const size_t slots = n * top_k;
     char *f = (char *)scratch_get(h, 8, (n * (n_groups > 0 ? n_groups : 1) + 2 * slots) * 4);
     const size_t n_g = n_groups > 0 ? n_groups : 1;
-    int *ints = (int *)scratch_get(h, 9, (2 * n_g + 2 + slots + 4 * moe_max_items(h, slots, n_g)) * 4);
+    int *ints = (int *)scratch_get(h, 9, (2 * n_g + 2 + slots + 4 * moe_max_items(h, slots, n_g) + 4 * n_g + 1) * 4);
     float *big = (float *)scratch_get(h, 10, slots * (ffn + hdim) * 4);
     if (!f || !ints || !big) return false;
     s.logits = (float *)f;
@@ -562,6 +580,8 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
     s.list = ints + 2 * n_groups + 1;
     s.items = s.list + slots;
     s.n_items = s.items + 4 * moe_max_items(h, slots, n_g);
+    s.recs = s.n_items + 1;
+    s.n_recs = s.recs + 4 * n_g;
     s.act = big;
     s.ydown = big + slots * ffn;
     return true;
@@ -573,8 +593,8 @@ int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size
     if (n * top_k > ROUTE_MAX_SLOTS || n_exp > 256) return set_err(h, SOSO_HIP_DECLINED, "moe route: too many slots");
     const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
     k_moe_route<<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt,
-                                              s.cnt, s.offs, s.list, s.items, s.n_items, moe_item_target(h),
-                                              h->ticket);
+                                              s.cnt, s.offs, s.list, s.items, s.n_items, moe_item_target(h), s.recs,
+                                              s.n_recs, h->ticket);
     return hip_check(h, hipGetLastError(), "moe route launch");
 }
 
@@ -659,9 +679,24 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
                        const uint8_t *use, const MoeScratch &s, float *out)
 {
     const size_t max_items = moe_max_items(h, n * top_k, n_groups);
-    int rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, max_items, n, xs, (int)top_k, s, s.act);
-    if (rc == SOSO_HIP_OK)
-        rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_items, n, s.act, 1, s, s.ydown);
+    // two or more slots per active expert on average: the matrix-core path
+    // (its cost per weight row is flat up to 8 tokens); fewer: the dot4 path
+    const size_t slots = n * top_k, max_recs = std::min(n_groups, slots);
+    const bool many = slots >= 2 * max_recs;
+    int rc;
+    if (many && dt_gu == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_gu, ffn, hdim))
+        rc = launch_mfma_moe(h, 2, tab, tab + n_groups, ffn, hdim, max_recs, xs, (int)top_k, s.list, s.recs, s.n_recs,
+                             s.act);
+    else
+        rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, max_items, n, xs, (int)top_k, s, s.act);
+    if (rc == SOSO_HIP_OK) {
+        if (many && dt_down == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_down, hdim, ffn))
+            rc = launch_mfma_moe(h, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_recs, s.act, 1, s.list, s.recs,
+                                 s.n_recs, s.ydown);
+        else
+            rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_items, n, s.act, 1, s,
+                               s.ydown);
+    }
     if (rc != SOSO_HIP_OK) return rc;
     const dim3 grid((unsigned)((hdim + 255) / 256), (unsigned)n);
     k_moe_combine<<<grid, 256, 0, h->stream>>>(s.ydown, wgt, use, (int)n, (int)hdim, (int)top_k, out);

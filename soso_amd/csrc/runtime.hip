@@ -422,9 +422,9 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
         if (ok[e]) gid.push_back(e);
     const size_t G = gid.size();
     // [cnt G | offs G+1 | list slots | active groups G | their count], as moe_scratch lays it out
-    // [cnt G | offs G + 1 | list slots | work items 4 x max_items | item count]
+    // [cnt G | offs G + 1 | list slots | work items 4 x max_items | item count | records 4G | record count]
     const size_t max_items = moe_max_items(h, slots, G ? G : 1);
-    std::vector<int> ints(2 * G + 2 + slots + 4 * max_items, 0);
+    std::vector<int> ints(2 * G + 2 + slots + 4 * max_items + 4 * G + 1, 0);
     std::vector<const uint8_t *> tab(3 * G);
     int o = 0;
     for (size_t g = 0; g < G; g++) {
@@ -455,6 +455,13 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
             }
         }
         ints[2 * G + 1 + slots + 4 * max_items] = (int)ni;
+        int *rec = &ints[2 * G + 2 + slots + 4 * max_items];
+        for (size_t g = 0; g < G; g++) {
+            rec[4 * g] = (int)g;
+            rec[4 * g + 1] = ints[g];
+            rec[4 * g + 2] = ints[G + g];
+        }
+        rec[4 * G] = (int)G;
     }
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
     float *sd = (float *)scratch_get(h, 5, n * hdim * 4);

@@ -152,6 +152,27 @@ def test_matmul_equals_single_matvecs(gpu, orc):
     gpu.weight_drop("mm")
 
 
+@pytest.mark.parametrize("rows,cols,n", [(1000, 4096, 16), (384, 1536, 37), (136, 768, 20)])
+def test_matmul_matrix_cores_match_cpu(gpu, orc, rows, cols, n):
+    """From 16 vectors up, Q4_K matmul runs on the matrix cores (exact int8
+    products of codes and x digits, scales in f32): every output row within
+    relative L2 1e-5 of the CPU restatement.  Shapes cover a partial 128-row
+    block, column counts that end in a partial 1024-column chunk, and token
+    counts that leave a partial round of 16."""
+    w = orc.synth(Q4K, rows, cols, 7, n)
+    xs = orc.normal(n * cols, 1.0, 8, n).reshape(n, cols)
+    out = np.empty(n * rows, np.float32)
+    key = f"mm.mfma.{rows}.{cols}.{n}"
+    try:
+        assert gpu.matmul(key, w, Q4K, rows, cols, n, xs, out), gpu.last_error()
+        out = out.reshape(n, rows)
+        ref = orc.matmul(Q4K, w, rows, cols, xs, threads=8, avx2=True)
+        for j in range(n):
+            assert orc.rel_l2(out[j], ref[j]) < TOL, (j, orc.rel_l2(out[j], ref[j]))
+    finally:
+        gpu.weight_drop(key)
+
+
 def test_declines_follow_the_trait(gpu, orc):
     x = orc.normal(256, 1.0, 1, 1)
     y = np.zeros(4, np.float32)

@@ -114,8 +114,10 @@ def test_router_ties_lowest_index_first(gpu, orc):
 
 @pytest.mark.parametrize("n_exp,h,ffn,top_k,n,dt_down", [
     (16, 2048, 768, 8, 1, Q4K),    # configs[3] expert shapes, fewer experts
-    (16, 2048, 768, 8, 32, Q4K),   # batch 32: several tokens per expert
+    (16, 2048, 768, 8, 32, Q4K),   # batch 32: 16 tokens per expert, the matrix-core path
     (12, 512, 256, 3, 7, Q8),      # Q8_0 down projections (soso's converted Q6_K experts)
+    (8, 512, 256, 4, 48, Q4K),     # 24 tokens per expert: three token rounds on the matrix cores
+    (6, 512, 256, 3, 16, Q8),      # matrix-core gate/up, dot4 Q8_0 down
 ])
 def test_moe_ffn_dev_matches_cpu(gpu, orc, n_exp, h, ffn, top_k, n, dt_down):
     layer = Layer(orc, n_exp, h, ffn, top_k, 40 + n, dt_down)
