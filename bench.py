@@ -91,6 +91,39 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
             g.weight_drop(k)
 
 
+def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3):
+    """Q4_K matmul Y[n x rows] = X[n x cols] . W^T (GpuDispatch::matmul) with
+    n tokens on the matrix cores; `copies` rotating weights.  Returns ms per
+    call (HIP events around a graph of back-to-back calls)."""
+    keys = [f"bench.mm.{rows}x{cols}.{i}" for i in range(copies)]
+    for i, k in enumerate(keys):
+        g.weight_synth(k, Q4K, rows, cols, seed, 3000 + i)
+    x = g.dev_alloc(n * cols * 4)
+    y = g.dev_alloc(n * rows * 4)
+    try:
+        g.synth_normal(x, n * cols, 1.0, seed, 9)
+        for i in range(warmup):
+            g.matmul_dev(keys[i % copies], n, x, y)
+        g.sync()
+        gid = _capture(g, lambda: [g.matmul_dev(keys[i % copies], n, x, y) for i in range(steps)])
+        try:
+            g.graph_launch(gid)
+            g.sync()
+            g.event_record(0)
+            g.graph_launch(gid)
+            g.event_record(1)
+            g.sync()
+        finally:
+            g.graph_destroy(gid)
+        return g.event_elapsed(0, 1) / steps
+    finally:
+        g.sync()
+        g.dev_free(x)
+        g.dev_free(y)
+        for k in keys:
+            g.weight_drop(k)
+
+
 def time_moe(g, n, steps, layers=4, n_x=8, seed=11):
     """Qwen3-30B-A3B-like MoE FFN (hidden 2048, 128 experts of
     intermediate 768, top-8, Q4_K experts, f32 router ~ N(0, 0.02)), `n`
@@ -407,7 +440,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
-    ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head"],
+    ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head", "matmul"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -429,6 +462,9 @@ def main():
         elif args.only == "head":
             ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10))
             res = {"q6_k_head_128256x4096_us": round(ms * 1e3, 3)}
+        elif args.only == "matmul":
+            ms = time_matmul(g, 14336, 4096, 64, 16, max(20, args.steps // 10), min(args.warmup, 10))
+            res = {"q4_k_matmul_14336x4096_n64_us": round(ms * 1e3, 3)}
         elif args.only == "decode":
             ms, _, tok = time_decode_8b(g, max(10, args.steps // 50))
             res = {"llama8b_decode_ms_per_token": round(ms, 4), "greedy_token": tok}
@@ -475,6 +511,14 @@ def main():
                            "frac_hbm": round(b / (k_ * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b}
         if not args.no_cpu:
             extra["q6_k_head_128256x4096"]["parity_vs_cpu"] = head_parity(g, args.cpu_threads)
+        mm_n = 64
+        ms_mm = time_matmul(g, 14336, 4096, mm_n, 16, max(20, args.steps // 10), min(args.warmup, 10))
+        b_mm = 14336 * (4096 // 256) * 144 + mm_n * 4096 * 4 + mm_n * 14336 * 4
+        extra["q4_k_matmul_14336x4096_n64"] = {
+            "us_kernel": round(ms_mm * 1e3, 3), "GB_s": round(b_mm / (ms_mm * 1e-3) / 1e9, 1),
+            "frac_hbm": round(b_mm / (ms_mm * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "gemm_TFLOP_s": round(2 * mm_n * 14336 * 4096 / (ms_mm * 1e-3) / 1e12, 2), "tokens": mm_n,
+            "path": "int8 MFMA 16x16x32 (exact codes x 3 digit planes of x)"}
         for n in (1, 32):
             ms_m, b_m, u_m, _ = time_moe(g, n, max(40, args.steps // 10))
             extra[f"moe_qwen3_30b_a3b_batch{n}"] = {

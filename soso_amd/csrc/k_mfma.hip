@@ -8,11 +8,12 @@
 // 256-element super-block (|X| <= 2^22), and the Q4_K codes q (0..15) are
 // int8 already, so v_mfma_i32_16x16x32_i8 returns exact int32 sums
 //   S[digit][row] = sum_{k in sub-block} digit_k * q_k
-// for one 32-element sub-block.  Per sub-block the 6-bit scale is applied in
-// integers (acc += sc * S, |acc| < 2^25 over a super-block), per super-block
-// in f32: y += d * 2^-e * (acc0 + 256 acc1 + 65536 acc2) - dmin * sum_sb m_sb
-// * sum(x over sb) -- the factorised Q4_K dot of crates/sosomodel/src/
-// dequant.rs:172-201.
+// for one 32-element sub-block.  The 6-bit scale of each sub-block enters the
+// B operand (sc = 8 hi + lo, codes times hi and times lo are still int8), so
+// two MFMA chains sum a whole super-block exactly (|S| < 2^25); per
+// super-block in f32: y += d * 2^-e * (S0 + 256 S1 + 65536 S2) - dmin *
+// sum_sb m_sb * sum(x over sb) -- the factorised Q4_K dot of
+// crates/sosomodel/src/dequant.rs:172-201.
 //
 // MFMA operands (16 x 16 x 32, int8; lane l, g = l / 16):
 //   A (16 x 32): row m = l % 16 = (token m / 4 of the tile, digit m % 4; digit
@@ -31,8 +32,13 @@
 #include "mv_core.hpp"
 
 typedef int mf_v4i __attribute__((ext_vector_type(4)));
+typedef unsigned short mf_u16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int MF_NW = 4;            // wavefronts per workgroup
+// Super-blocks of weights in flight per wavefront while one is applied
+// (gate+up, single matrix).  Measured on MI355X at batch 32: one
+// is fastest -- 136 us per layer; 2 / 3 ahead gave 144 us.
+constexpr int MF_LA2 = 1, MF_LA1 = 1;
 constexpr int MF_ROWS = 16 * MF_NW; // rows per workgroup (16 per wavefront)
 
 // LDS per token for kc staged columns: digits [sub-block][3][32 B], then the
@@ -81,7 +87,7 @@ __device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (
 // (MoE), or dense_n > 0 tokens of one dense product (slot = token).  Item:
 // blockIdx.x = a * nblk + row block (MoE), or row block + nblk * token round
 // (dense).  Slot s reads x = xs + (s / xdiv) * cols and writes out[s * rows + r].
-template <int NMAT, int MT>
+template <int NMAT, int MT, int LA>
 __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB,
                                                   const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
@@ -148,80 +154,99 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
             __builtin_amdgcn_sched_barrier(0);
             // ---- stage x (columns k0 .. k0 + kc of the round's tokens) ----
             const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
-            for (int fb = 0; fb < tot; fb += 64 * MF_NW) {
-                const int f = fb + (int)threadIdx.x;
-                const bool valid = f < tot;
-                const int tt = valid ? f / cpt : 0, c = f % cpt;
-                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-                if (valid) {
-                    const float4 *x4 =
-                        (const float4 *)(xs + (size_t)(slot_s[tt] / xdiv) * cols + k0) + 2 * c;
-                    v0 = x4[0];
-                    v1 = x4[1];
-                }
-                // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
-                float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
-                                 fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
-                mx = row16_max(mx);
-                mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                const int ex = (mx > 0.0f && mx < INFINITY) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
-                // f32 sum of x over the 32-element sub-block: 4 aligned lanes
-                float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
-                sm += dpp_f<0xB1>(sm);
-                sm += dpp_f<0x4E>(sm);
-                if (valid) {
-                    uint32_t d0[XDIG], d1[XDIG];
-                    digits4(v0, ex, d0);
-                    digits4(v1, ex, d1);
-                    uint8_t *tp = lds + (size_t)tt * tb;
-                    const int sbl = c >> 2, q = c & 3;
+            // four chunks per thread are requested together, then converted
+            // (one L2 round trip per 4 * 64 * MF_NW chunks)
+            constexpr int NT = 64 * MF_NW, XB = 4;
+            for (int fb = 0; fb < tot; fb += XB * NT) {
+                float4 v0[XB], v1[XB];
 #pragma unroll
-                    for (int k = 0; k < XDIG; k++)
-                        *(uint2 *)(tp + (sbl * 3 + k) * 32 + 8 * q) = make_uint2(d0[k], d1[k]);
-                    if (q == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
-                    if ((c & 31) == 0) *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = ldexpf(1.0f, -ex);
+                for (int k = 0; k < XB; k++) {
+                    const int f = fb + k * NT + (int)threadIdx.x;
+                    v0[k] = v1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (f < tot) {
+                        const float4 *x4 =
+                            (const float4 *)(xs + (size_t)(slot_s[f / cpt] / xdiv) * cols + k0) + 2 * (f % cpt);
+                        v0[k] = x4[0];
+                        v1[k] = x4[1];
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < XB; k++) {
+                    if (fb + k * NT >= tot) break; // uniform
+                    const int f = fb + k * NT + (int)threadIdx.x;
+                    const bool valid = f < tot;
+                    const int tt = valid ? f / cpt : 0, c = f % cpt;
+                    // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
+                    float mx = fmaxf(fmaxf(fmaxf(fabsf(v0[k].x), fabsf(v0[k].y)), fmaxf(fabsf(v0[k].z), fabsf(v0[k].w))),
+                                     fmaxf(fmaxf(fabsf(v1[k].x), fabsf(v1[k].y)), fmaxf(fabsf(v1[k].z), fabsf(v1[k].w))));
+                    mx = row16_max(mx);
+                    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                    const int ex = (mx > 0.0f && mx < INFINITY) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+                    // f32 sum of x over the 32-element sub-block: 4 aligned lanes
+                    float sm = ((v0[k].x + v0[k].y) + (v0[k].z + v0[k].w)) + ((v1[k].x + v1[k].y) + (v1[k].z + v1[k].w));
+                    sm += dpp_f<0xB1>(sm);
+                    sm += dpp_f<0x4E>(sm);
+                    if (valid) {
+                        uint32_t d0[XDIG], d1[XDIG];
+                        digits4(v0[k], ex, d0);
+                        digits4(v1[k], ex, d1);
+                        uint8_t *tp = lds + (size_t)tt * tb;
+                        const int sbl = c >> 2, q = c & 3;
+#pragma unroll
+                        for (int kk = 0; kk < XDIG; kk++)
+                            *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * q) = make_uint2(d0[kk], d1[kk]);
+                        if (q == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
+                        if ((c & 31) == 0) *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = ldexpf(1.0f, -ex);
+                    }
                 }
             }
             __syncthreads();
             // ---- stream this chunk's super-blocks of the wavefront's 16 rows ----
+            // The 6-bit scale of each sub-block goes into the B operand: sc =
+            // 8 hi + lo with hi, lo < 8, so q*lo and q*hi (<= 105) are int8 and
+            // one packed 16-bit multiply scales four packed codes (each 16-bit
+            // half holds two codes; the low one's product never carries into
+            // the high byte).  Two MFMA chains (lo, hi) then sum a whole
+            // super-block in the accumulators: S = Clo + 8 Chi = sum_sb sc_sb *
+            // sum_k digit * q.
+            auto scaled = [](uint32_t codes, int f) {
+                const mf_u16x2 c = __builtin_bit_cast(mf_u16x2, codes);
+                const mf_u16x2 k = {(unsigned short)f, (unsigned short)f};
+                return __builtin_bit_cast(uint32_t, c * k);
+            };
             auto superblock = [&](int sbl8, const MfSb &A_, const MfSb &B_) {
                 // sbl8: first local sub-block of this super-block
-                MfScale sA, sB;
-                mf_scales(A_.h, sA);
-                if constexpr (NMAT == 2) mf_scales(B_.h, sB);
-                int acc[NMAT][MT][3];
+                MfScale sc_[NMAT];
+                mf_scales(A_.h, sc_[0]);
+                if constexpr (NMAT == 2) mf_scales(B_.h, sc_[NMAT - 1]);
+                mf_v4i clo[NMAT][MT], chi[NMAT][MT];
                 float mins[NMAT][MT];
 #pragma unroll
                 for (int m = 0; m < NMAT; m++)
 #pragma unroll
                     for (int mt = 0; mt < MT; mt++) {
-                        acc[m][mt][0] = acc[m][mt][1] = acc[m][mt][2] = 0;
+                        clo[m][mt] = chi[m][mt] = mf_v4i{0, 0, 0, 0};
                         mins[m][mt] = 0.0f;
                     }
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
                     const int j0 = 2 * p, j1 = 2 * p + 1; // sub-blocks of the unit
-                    long lo[NMAT], hi[NMAT];
-                    {
-                        const uint2 q = A_.q[p];
-                        lo[0] = (long)(((uint64_t)(q.y & 0x0F0F0F0Fu) << 32) | (q.x & 0x0F0F0F0Fu));
-                        hi[0] = (long)(((uint64_t)((q.y >> 4) & 0x0F0F0F0Fu) << 32) | ((q.x >> 4) & 0x0F0F0F0Fu));
-                    }
-                    if constexpr (NMAT == 2) {
-                        const uint2 q = B_.q[p];
-                        lo[NMAT - 1] = (long)(((uint64_t)(q.y & 0x0F0F0F0Fu) << 32) | (q.x & 0x0F0F0F0Fu));
-                        hi[NMAT - 1] =
-                            (long)(((uint64_t)((q.y >> 4) & 0x0F0F0F0Fu) << 32) | ((q.x >> 4) & 0x0F0F0F0Fu));
-                    }
-                    int scA0 = mf_byte(sA.sc4[j0 >> 2], j0 & 3), scA1 = mf_byte(sA.sc4[j1 >> 2], j1 & 3);
-                    float mA0 = (float)mf_byte(sA.m4[j0 >> 2], j0 & 3), mA1 = (float)mf_byte(sA.m4[j1 >> 2], j1 & 3);
-                    int scB0 = 0, scB1 = 0;
-                    float mB0 = 0.f, mB1 = 0.f;
-                    if constexpr (NMAT == 2) {
-                        scB0 = mf_byte(sB.sc4[j0 >> 2], j0 & 3);
-                        scB1 = mf_byte(sB.sc4[j1 >> 2], j1 & 3);
-                        mB0 = (float)mf_byte(sB.m4[j0 >> 2], j0 & 3);
-                        mB1 = (float)mf_byte(sB.m4[j1 >> 2], j1 & 3);
+                    // B operands: codes x (sc lo, sc hi) of sub-blocks j0 (low
+                    // nibbles) and j1 (high nibbles); the min factors
+                    long b0l[NMAT], b0h[NMAT], b1l[NMAT], b1h[NMAT];
+                    float m0[NMAT], m1[NMAT];
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        const uint2 q = m == 0 ? A_.q[p] : B_.q[p];
+                        const uint32_t lx = q.x & 0x0F0F0F0Fu, ly = q.y & 0x0F0F0F0Fu;
+                        const uint32_t hx = (q.x >> 4) & 0x0F0F0F0Fu, hy = (q.y >> 4) & 0x0F0F0F0Fu;
+                        const int s0 = mf_byte(sc_[m].sc4[j0 >> 2], j0 & 3), s1 = mf_byte(sc_[m].sc4[j1 >> 2], j1 & 3);
+                        b0l[m] = (long)(((uint64_t)scaled(ly, s0 & 7) << 32) | scaled(lx, s0 & 7));
+                        b0h[m] = (long)(((uint64_t)scaled(ly, s0 >> 3) << 32) | scaled(lx, s0 >> 3));
+                        b1l[m] = (long)(((uint64_t)scaled(hy, s1 & 7) << 32) | scaled(hx, s1 & 7));
+                        b1h[m] = (long)(((uint64_t)scaled(hy, s1 >> 3) << 32) | scaled(hx, s1 >> 3));
+                        m0[m] = (float)mf_byte(sc_[m].m4[j0 >> 2], j0 & 3);
+                        m1[m] = (float)mf_byte(sc_[m].m4[j1 >> 2], j1 & 3);
                     }
 #pragma unroll
                     for (int mt = 0; mt < MT; mt++) {
@@ -240,53 +265,55 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
                         const int to = mt * 4 + g;
                         const float *xsum = (const float *)(lds + (size_t)(to < nt ? to : 0) * tb + (kc >> 5) * 96);
                         const float xs0 = xsum[sbl8 + j0], xs1 = xsum[sbl8 + j1];
-                        const mf_v4i zero = {0, 0, 0, 0};
-                        mf_v4i D0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, lo[0], zero, 0, 0, 0);
-                        mf_v4i D1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, hi[0], zero, 0, 0, 0);
 #pragma unroll
-                        for (int i = 0; i < 3; i++)
-                            acc[0][mt][i] += __mul24(D0[i], scA0) + __mul24(D1[i], scA1);
-                        mins[0][mt] = fmaf(mA0, xs0, fmaf(mA1, xs1, mins[0][mt]));
-                        if constexpr (NMAT == 2) {
-                            mf_v4i E0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, lo[NMAT - 1], zero, 0, 0, 0);
-                            mf_v4i E1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, hi[NMAT - 1], zero, 0, 0, 0);
-#pragma unroll
-                            for (int i = 0; i < 3; i++)
-                                acc[NMAT - 1][mt][i] += __mul24(E0[i], scB0) + __mul24(E1[i], scB1);
-                            mins[NMAT - 1][mt] = fmaf(mB0, xs0, fmaf(mB1, xs1, mins[NMAT - 1][mt]));
+                        for (int m = 0; m < NMAT; m++) {
+                            clo[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, b0l[m], clo[m][mt], 0, 0, 0);
+                            chi[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, b0h[m], chi[m][mt], 0, 0, 0);
+                            clo[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, b1l[m], clo[m][mt], 0, 0, 0);
+                            chi[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, b1h[m], chi[m][mt], 0, 0, 0);
+                            mins[m][mt] = fmaf(m0[m], xs0, fmaf(m1[m], xs1, mins[m][mt]));
                         }
                     }
-                    // one unit at a time: keeps each unit's LDS reads and MFMA
-                    // results from being hoisted into the next (register pressure)
+                    // one unit at a time: keeps each unit's LDS reads from being
+                    // hoisted into the next (register pressure)
                     __builtin_amdgcn_sched_barrier(0);
                 }
-                // f32 per super-block: y += d 2^-e (acc0 + 256 acc1 + 65536 acc2) - dmin * mins
+                // f32 per super-block: y += d 2^-e (S0 + 256 S1 + 65536 S2) - dmin * mins,
+                // S_i = clo_i + 8 chi_i (|S_i| < 2^25)
 #pragma unroll
                 for (int mt = 0; mt < MT; mt++) {
                     if (mt * 4 >= nt) break;
                     const int to = mt * 4 + g;
                     const float P = *(const float *)(lds + (size_t)(to < nt ? to : 0) * tb + (kc >> 5) * 100 +
                                                      4 * (sbl8 >> 3));
-                    const float tA = fmaf((float)acc[0][mt][2], 65536.0f,
-                                          fmaf((float)acc[0][mt][1], 256.0f, (float)acc[0][mt][0]));
-                    accf[0][mt] = fmaf(-sA.dmin, mins[0][mt], fmaf(sA.d * P, tA, accf[0][mt]));
-                    if constexpr (NMAT == 2) {
-                        const float tB = fmaf((float)acc[NMAT - 1][mt][2], 65536.0f,
-                                              fmaf((float)acc[NMAT - 1][mt][1], 256.0f, (float)acc[NMAT - 1][mt][0]));
-                        accf[NMAT - 1][mt] =
-                            fmaf(-sB.dmin, mins[NMAT - 1][mt], fmaf(sB.d * P, tB, accf[NMAT - 1][mt]));
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        const int S0 = clo[m][mt][0] + 8 * chi[m][mt][0], S1 = clo[m][mt][1] + 8 * chi[m][mt][1];
+                        const int S2 = clo[m][mt][2] + 8 * chi[m][mt][2];
+                        const float t = fmaf((float)S2, 65536.0f, fmaf((float)S1, 256.0f, (float)S0));
+                        accf[m][mt] = fmaf(-sc_[m].dmin, mins[m][mt], fmaf(sc_[m].d * P, t, accf[m][mt]));
                     }
                 }
             };
-            // double buffer: super-block i + 1 is requested before i is applied
+            // super-blocks i + 1 .. i + LA are in flight while i is applied
+            MfSb pa[LA], pb[LA];
+#pragma unroll
+            for (int k = 0; k < LA - 1; k++) {
+                mf_load_sb(rA, rowoff, qoff, sb0 + 1 + k, 1 + k < nsb, pa[k]);
+                if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0 + 1 + k, 1 + k < nsb, pb[k]);
+            }
             for (int i = 0; i < nsb; i++) {
-                MfSb na, nbx;
-                mf_load_sb(rA, rowoff, qoff, sb0 + i + 1, i + 1 < nsb, na);
-                if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0 + i + 1, i + 1 < nsb, nbx);
+                mf_load_sb(rA, rowoff, qoff, sb0 + i + LA, i + LA < nsb, pa[LA - 1]);
+                if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0 + i + LA, i + LA < nsb, pb[LA - 1]);
                 __builtin_amdgcn_sched_barrier(0);
                 superblock(8 * i, ca, cb);
-                ca = na;
-                if constexpr (NMAT == 2) cb = nbx;
+                ca = pa[0];
+                if constexpr (NMAT == 2) cb = pb[0];
+#pragma unroll
+                for (int k = 0; k < LA - 1; k++) {
+                    pa[k] = pa[k + 1];
+                    if constexpr (NMAT == 2) pb[k] = pb[k + 1];
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
             __syncthreads(); // LDS is restaged for the next chunk or round
@@ -334,10 +361,10 @@ int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_
     const unsigned grid = (unsigned)(max_recs * nblk);
     const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
     if (nmat == 2)
-        k_mfma_q4k<2, MT><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, (int)rows, (int)cols, xs, xdiv,
+        k_mfma_q4k<2, MT, MF_LA2><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, (int)rows, (int)cols, xs, xdiv,
                                                                 list, recs, n_recs, 0, kc, out);
     else
-        k_mfma_q4k<1, MT><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, (int)rows, (int)cols, xs,
+        k_mfma_q4k<1, MT, MF_LA1><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, (int)rows, (int)cols, xs,
                                                                 xdiv, list, recs, n_recs, 0, kc, out);
     return hip_check(h, hipGetLastError(), "mfma moe launch");
 }
@@ -353,7 +380,7 @@ int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, f
     const int kc = mf_kc(h, w.cols, 4 * MT);
     const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
     const unsigned grid = (unsigned)(nblk * rounds);
-    k_mfma_q4k<1, MT><<<grid, 64 * MF_NW, lds, h->stream>>>(nullptr, nullptr, (const uint8_t *)w.dev,
+    k_mfma_q4k<1, MT, MF_LA1><<<grid, 64 * MF_NW, lds, h->stream>>>(nullptr, nullptr, (const uint8_t *)w.dev,
                                                             packed_row_stride(w.dtype, w.cols), (int)w.rows,
                                                             (int)w.cols, x, 1, nullptr, nullptr, nullptr, (int)n, kc, y);
     return hip_check(h, hipGetLastError(), "mfma matmul launch");
