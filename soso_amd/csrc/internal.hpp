@@ -76,6 +76,8 @@ struct DecodeModel {
     float *hid = nullptr, *qbuf = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
 };
 
+constexpr size_t SOSO_TICKET_BYTES = 16384;
+
 struct soso_hip {
     int device = 0;
     hipStream_t stream = nullptr;
@@ -91,8 +93,10 @@ struct soso_hip {
     static constexpr int N_SCRATCH = 12;
     void *scratch[N_SCRATCH] = {};
     size_t scratch_cap[N_SCRATCH] = {};
-    // 4 KiB: a counter at offset 0 that is zero between launches of the "last
-    // workgroup" kernels (each resets it), then 2 KiB of per-workgroup partials
+    // SOSO_TICKET_BYTES of "last workgroup" state, zero between launches (each
+    // kernel resets what it used): uint 0 the final counter (argmax, MoE
+    // route), uints 64 .. 575 argmax partials, uints 2048 .. 3071 the MoE
+    // route's per-token-block counters
     unsigned *ticket = nullptr;
     std::unordered_map<std::string, MoeLayer> moe_layers;
     std::unordered_map<std::string, DecodeModel> decode_models;

@@ -85,7 +85,8 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
 // {expert, its slot count, its first slot in `list`, chunk j | chunks << 16}
 // for i < *n_items, experts ascending.
 constexpr int ROUTE_MAX_SLOTS = 4096; // n * top_k handled by the LDS sort
-constexpr int ROUTE_TT = 4;           // tokens per wavefront
+constexpr int ROUTE_TT = 4;           // tokens per wavefront (and per ranking workgroup)
+constexpr int ROUTE_T1 = 2048;        // first per-token-block counter in the ticket buffer
 
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
@@ -138,36 +139,41 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
             if (lane == 63 && tt < tn) logits[(size_t)(t0 + tt) * n_exp + e] = sum;
         }
     }
-    // The last workgroup to finish ranks the experts of every token.  One
-    // thread per workgroup fences: a device-scope fence writes back the L2 of
-    // its XCD, and the workgroup barrier before it orders every wavefront's
-    // stores ahead of it (fences are cumulative).
+    // Two-level tickets.  The last workgroup of token block by (counter
+    // ticket[ROUTE_T1 + by]) ranks that block's tokens, one per wavefront;
+    // the last token block to be ranked (counter ticket[0]) sorts the slots.
+    // One thread per workgroup fences: a device-scope fence writes back the
+    // L2 of its XCD, and the workgroup barrier before it orders every
+    // wavefront's stores ahead of it (fences are cumulative).
     __syncthreads();
     if (threadIdx.x == 0) {
         __threadfence();
-        const bool l = atomicAdd(ticket, 1u) == gridDim.x * gridDim.y - 1;
+        const bool l = atomicAdd(ticket + ROUTE_T1 + blockIdx.y, 1u) == gridDim.x - 1;
         if (l) __threadfence();
         last = l;
     }
     __syncthreads();
     if (!last) return;
-    // four tokens per wavefront at a time, their logits loaded together
-    for (int tb = 4 * wave; tb < n; tb += 4 * nw) {
-        float lg[4][4];
+    if (wave < tn) {
+        const int t = t0 + wave;
+        float lg[4];
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int x = lane + 64 * q;
-                lg[tt][q] = tb + tt < n && x < n_exp ? logits[(size_t)(tb + tt) * n_exp + x] : -INFINITY;
-            }
-#pragma unroll
-        for (int tt = 0; tt < 4; tt++)
-            if (tb + tt < n)
-                topk_regs(lg[tt], n_exp, top_k, idx + (size_t)(tb + tt) * top_k, wgt + (size_t)(tb + tt) * top_k,
-                          sel[wave]);
+        for (int q = 0; q < 4; q++) {
+            const int x = lane + 64 * q;
+            lg[q] = x < n_exp ? logits[(size_t)t * n_exp + x] : -INFINITY;
+        }
+        topk_regs(lg, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k, sel[wave]);
     }
     __syncthreads();
+    if (threadIdx.x == 0) {
+        ticket[ROUTE_T1 + blockIdx.y] = 0u;
+        __threadfence();
+        const bool l = atomicAdd(ticket, 1u) == gridDim.y - 1;
+        if (l) __threadfence();
+        last = l;
+    }
+    __syncthreads();
+    if (!last) return;
     // counting sort of the slots by expert in LDS (a slot's position inside
     // its expert's list does not change any result)
     const int slots = n * top_k;
@@ -590,7 +596,8 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
 int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size_t hdim, size_t n_exp, size_t top_k,
                      const MoeScratch &s)
 {
-    if (n * top_k > ROUTE_MAX_SLOTS || n_exp > 256) return set_err(h, SOSO_HIP_DECLINED, "moe route: too many slots");
+    if (n * top_k > ROUTE_MAX_SLOTS || n_exp > 256 || (n + ROUTE_TT - 1) / ROUTE_TT > 1024)
+        return set_err(h, SOSO_HIP_DECLINED, "moe route: too many slots");
     const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
     k_moe_route<<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt,
                                               s.cnt, s.offs, s.list, s.items, s.n_items, moe_item_target(h), s.recs,

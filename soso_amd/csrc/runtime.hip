@@ -188,7 +188,8 @@ int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out)
         delete h;
         return SOSO_HIP_ERR_DEVICE;
     }
-    if (hipMalloc((void **)&h->ticket, 4096) != hipSuccess || hipMemset(h->ticket, 0, 4096) != hipSuccess) {
+    if (hipMalloc((void **)&h->ticket, SOSO_TICKET_BYTES) != hipSuccess ||
+        hipMemset(h->ticket, 0, SOSO_TICKET_BYTES) != hipSuccess) {
         hipStreamDestroy(h->stream);
         delete h;
         return SOSO_HIP_ERR_DEVICE;
