@@ -193,12 +193,15 @@ def time_moe(g, n, steps, layers=4, n_x=8, seed=11):
             g.weight_drop(name + ".router")
 
 
-def time_decode_8b(g, steps, ctx=4096, seed=21):
+def time_decode_8b(g, steps, ctx=4096, seed=21, kv_f16=False, eager=False):
     """one greedy decode step of a random-init Llama-style 8B
     (32 layers, hidden 4096, 32 q / 8 KV heads of 128, RoPE theta 5e5,
     SwiGLU 14336, RMSNorm eps 1e-5, Q4_K projections, Q6_K head over 128256)
-    with an f32 KV cache prefilled with N(0, 1) to `ctx` positions; the step
-    runs at position `ctx`.  Returns (ms per token, bytes per token, token)."""
+    with an f32 KV cache prefilled with N(0, 1) to `ctx` positions (kv_f16:
+    soso's f16 KV instead, the same values rounded on upload); the step runs
+    at position `ctx`.  The timed steps replay one HIP graph; eager=True launches
+    them directly instead (for kernel tracers).  Returns (ms per token, bytes per
+    token, token)."""
     L, H, NH, NKV, HDIM, F, V = 32, 4096, 32, 8, 128, 14336, 128256
     qd, kvd = NH * HDIM, NKV * HDIM
     name = "llama8b"
@@ -227,34 +230,53 @@ def time_decode_8b(g, steps, ctx=4096, seed=21):
     g.weight_synth(name + ".head", Q6K, V, H, seed, 10001)
     keys += [name + ".out_norm", name + ".head"]
     cfg = dict(n_layers=L, hidden=H, n_heads=NH, n_kv_heads=NKV, head_dim=HDIM, ffn=F, vocab=V, ctx_max=ctx + 1,
-               rope_theta=500000.0, rms_eps=1e-5)
+               rope_theta=500000.0, rms_eps=1e-5, kv_f16=1 if kv_f16 else 0)
     g.decode_create(name, cfg, keys, drop_sources=True)
     x = g.dev_alloc(H * 4)
     tok = g.dev_alloc(4)
     try:
-        for l in range(L):
-            kd, vd = g.decode_kv_dev(name, l)
-            g.synth_normal(kd, (ctx + 1) * kvd, 1.0, seed + 1, 2 * l)
-            g.synth_normal(vd, (ctx + 1) * kvd, 1.0, seed + 1, 2 * l + 1)
+        if kv_f16:
+            st = [g.dev_alloc((ctx + 1) * kvd * 4) for _ in range(2)]
+            try:
+                for l in range(L):
+                    g.synth_normal(st[0], (ctx + 1) * kvd, 1.0, seed + 1, 2 * l)
+                    g.synth_normal(st[1], (ctx + 1) * kvd, 1.0, seed + 1, 2 * l + 1)
+                    g.decode_kv_upload(name, l, 0, (st[0], ctx + 1), (st[1], ctx + 1), rows_f32=True)
+            finally:
+                for p in st:
+                    g.dev_free(p)
+        else:
+            for l in range(L):
+                kd, vd = g.decode_kv_dev(name, l)
+                g.synth_normal(kd, (ctx + 1) * kvd, 1.0, seed + 1, 2 * l)
+                g.synth_normal(vd, (ctx + 1) * kvd, 1.0, seed + 1, 2 * l + 1)
         g.synth_normal(x, H, 1.0, seed + 2, 0)
         for _ in range(3):
             g.decode_step_dev(name, x, ctx, None, tok)
         g.sync()
-        gid = _capture(g, lambda: [g.decode_step_dev(name, x, ctx, None, tok) for _ in range(steps)])
-        try:
-            g.graph_launch(gid)
-            g.sync()
+        if eager:
             g.event_record(0)
-            g.graph_launch(gid)
+            for _ in range(steps):
+                g.decode_step_dev(name, x, ctx, None, tok)
             g.event_record(1)
             g.sync()
-        finally:
-            g.graph_destroy(gid)
+        else:
+            gid = _capture(g, lambda: [g.decode_step_dev(name, x, ctx, None, tok) for _ in range(steps)])
+            try:
+                g.graph_launch(gid)
+                g.sync()
+                g.event_record(0)
+                g.graph_launch(gid)
+                g.event_record(1)
+                g.sync()
+            finally:
+                g.graph_destroy(gid)
         ms = g.event_elapsed(0, 1) / steps
         token = int(g.d2h(tok, (1,), np.uint32)[0])
         per_layer = (qd + 2 * kvd) * (H // 256) * 144 + H * (qd // 256) * 144 + 2 * F * (H // 256) * 144 \
             + H * (F // 256) * 144
-        nbytes = L * per_layer + V * (H // 256) * 210 + L * 2 * (ctx + 1) * kvd * 4 + (2 * L + 1) * H * 4
+        nbytes = L * per_layer + V * (H // 256) * 210 + L * 2 * (ctx + 1) * kvd * (2 if kv_f16 else 4) \
+            + (2 * L + 1) * H * 4
         return ms, nbytes, token
     finally:
         g.dev_free(x)
@@ -440,6 +462,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
+    ap.add_argument("--eager", action="store_true",
+                    help="with --only decode: launch the timed steps directly instead of replaying a graph")
     ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head", "matmul"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
@@ -466,8 +490,12 @@ def main():
             ms = time_matmul(g, 14336, 4096, 64, 16, max(20, args.steps // 10), min(args.warmup, 10))
             res = {"q4_k_matmul_14336x4096_n64_us": round(ms * 1e3, 3)}
         elif args.only == "decode":
-            ms, _, tok = time_decode_8b(g, max(10, args.steps // 50))
-            res = {"llama8b_decode_ms_per_token": round(ms, 4), "greedy_token": tok}
+            print("decode: f32 KV", file=sys.stderr, flush=True)
+            ms, _, tok = time_decode_8b(g, max(10, args.steps // 50), eager=args.eager)
+            print("decode: f16 KV", file=sys.stderr, flush=True)
+            ms_h, _, tok_h = time_decode_8b(g, max(10, args.steps // 50), kv_f16=True, eager=args.eager)
+            res = {"llama8b_decode_ms_per_token": round(ms, 4), "greedy_token": tok,
+                   "llama8b_decode_kv_f16_ms_per_token": round(ms_h, 4), "greedy_token_kv_f16": tok_h}
         else:
             n = 1 if args.only == "moe1" else 32
             ms, _, _, _ = time_moe(g, n, max(40, args.steps // 10))
@@ -530,6 +558,12 @@ def main():
             "ms_per_token": round(ms_d, 4), "tokens_per_s": round(1e3 / ms_d, 1),
             "GB_s": round(b_d / (ms_d * 1e-3) / 1e9, 1), "frac_hbm": round(b_d / (ms_d * 1e-3) / 1e9 / PEAK_GBS, 4),
             "bytes_per_token": int(b_d), "greedy_token": tok_d}
+        ms_h, b_h, tok_h = time_decode_8b(g, max(10, args.steps // 50), kv_f16=True)
+        extra["llama8b_decode_ctx4096_kv_f16"] = {
+            "ms_per_token": round(ms_h, 4), "tokens_per_s": round(1e3 / ms_h, 1),
+            "GB_s": round(b_h / (ms_h * 1e-3) / 1e9, 1), "frac_hbm": round(b_h / (ms_h * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "bytes_per_token": int(b_h), "greedy_token": tok_h,
+            "kv": "f16 (soso's KvDtype::F16), same N(0,1) prefill rounded on upload"}
         line["configs"] = extra
     if not args.no_cpu:
         gbs, n, ms, copies, one = cpu_baseline(Q4K, rows, cols, args.cpu_seconds, args.cpu_threads)

@@ -154,7 +154,7 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
  * The device-resident decode of GpuDispatch::decode_preparar / decode_token
  * (gpu.rs:653-690) for a Llama-style dense model (LayerExecutor::forward_layer,
  * crates/soso-llm-core/src/layer.rs:1092-1389, then Runtime::logits_gpu and
- * argmax, runtime.rs:1976-2028), with an f32 KV cache.
+ * argmax, runtime.rs:1976-2028).
  * keys: 9 per layer -- attn_norm, q, k, v, o, ffn_norm, gate, up, down -- then
  * output_norm and head (9 * n_layers + 2 resident weights).  Norms are F32
  * [1 x hidden]; q [n_heads*head_dim x hidden], k and v [n_kv_heads*head_dim x
@@ -162,27 +162,45 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
  * [hidden x ffn], head [vocab x hidden].  q/k/v share one quantized dtype, gate/up
  * another; head_dim must be 128 and n_heads a multiple (1, 2, 4 or 8) of
  * n_kv_heads.  The library keeps fused copies (q|k|v rows; gate/up rows
- * interleaved) and allocates the KV cache (2 x n_layers x ctx_max x kv_dim f32,
- * zeroed) and the step's buffers; drop_sources = 1 drops the q, k, v, gate and up
- * weights once fused.  RoPE is non-NeoX (pairs 2i, 2i+1) with rope_theta. */
+ * interleaved) and allocates the KV cache (2 x n_layers x ctx_max x kv_dim
+ * elements, zeroed) and the step's buffers; drop_sources = 1 drops the q, k, v,
+ * gate and up weights once fused.  RoPE is non-NeoX (pairs 2i, 2i+1) with
+ * rope_theta.
+ * kv_f16 = 0: the KV cache holds f32.  kv_f16 = 1: it holds
+ * IEEE half bits, as soso's KvCache does (KvDtype::F16, kv.rs:258-266, the only
+ * KV type soso's device decode accepts, runtime/decode_gpu.rs:63): new rows are
+ * rounded with soso's f32_to_f16 (f16.rs:10-36: nearest, ties away from zero,
+ * NaN -> 0x7e00 | sign) and attention widens them to f32 exactly. */
 typedef struct soso_hip_decode_cfg {
     uint32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, ctx_max;
     float rope_theta, rms_eps;
+    uint32_t kv_f16;
 } soso_hip_decode_cfg;
 int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
                            const char *const *keys, const size_t *key_lens, int drop_sources);
-/* Device pointers of layer `layer`'s K and V caches, each f32 and head-major:
- * [n_kv_heads][ctx_max][head_dim] (a head's positions are contiguous), for
- * prefilling and inspection. */
-int soso_hip_decode_kv_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, float **k_dev,
-                           float **v_dev);
+/* Device pointers of layer `layer`'s K and V caches, head-major:
+ * [n_kv_heads][ctx_max][head_dim] (a head's positions are contiguous), each
+ * element f32 or f16 bits as kv_f16 says, for prefilling and inspection. */
+int soso_hip_decode_kv_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, void **k_dev,
+                           void **v_dev);
+/* decode_subir_estado (gpu.rs:665, EstadoCapaDec.k / .v, gpu.rs:167-173): writes
+ * n_rows position-major rows [n_rows][kv_dim] of K and V into layer `layer`'s
+ * cache at positions row0 .. row0 + n_rows - 1 (scattered to the head-major
+ * layout).  rows_f32 = 1: the rows are f32 and an f16 cache receives them rounded
+ * as KvCache::append does (kv.rs:264-266); rows_f32 = 0: they already hold the
+ * cache's element type (f16 bits for soso's host KV).  k_rows / v_rows may be host
+ * or device pointers.  Synchronous. */
+int soso_hip_decode_kv_upload(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, uint32_t row0,
+                              uint32_t n_rows, const void *k_rows, const void *v_rows, int rows_f32);
 /* One token at position `pos` (KV rows 0..pos-1 already filled): hidden = x_dev
  * (the token's f32 embedding row); writes K/V row `pos` of every layer, the
  * logits (logits_dev, vocab f32, when non-null) and the greedy token
- * (*token_dev, last maximum wins).  Asynchronous; allocates nothing, so it may be
- * captured in a graph. */
+ * (*token_dev, last maximum wins).  kv_rows_dev, when non-null, also receives
+ * the new rows in decode_token's `kv_rows` layout (gpu.rs:670-672): per layer,
+ * k (kv_dim) then v (kv_dim), in the cache's element type.  Asynchronous;
+ * allocates nothing, so it may be captured in a graph. */
 int soso_hip_decode_step_dev(soso_hip *h, const char *model_key, size_t model_key_len, const float *x_dev, uint32_t pos,
-                             float *logits_dev, uint32_t *token_dev);
+                             float *logits_dev, uint32_t *token_dev, void *kv_rows_dev);
 int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key_len);
 
 /* ---- device-resident API (no host copies; for the decode step, benchmarks

@@ -80,6 +80,13 @@ uint16_t or_f32_to_f16(float v)
     return (uint16_t)((uint16_t)(sign | (uint16_t)half) + round); /* wrapping_add */
 }
 
+/* or_f32_to_f16 over n values (KvCache::append's conversion of a row,
+ * kv.rs:264-266). */
+void or_f32_to_f16_n(const float *v, size_t n, uint16_t *out)
+{
+    for (size_t i = 0; i < n; i++) out[i] = or_f32_to_f16(v[i]);
+}
+
 /* ---------------------------------------------------------------------------
  * layout
  * ------------------------------------------------------------------------- */

@@ -64,6 +64,7 @@ extern "C" {
 /* ---- f16 ---------------------------------------------------------------- */
 float or_f16_to_f32(uint16_t bits);
 uint16_t or_f32_to_f16(float v);
+void or_f32_to_f16_n(const float *v, size_t n, uint16_t *out);
 
 /* ---- layout ------------------------------------------------------------- */
 int64_t or_row_bytes(uint8_t dtype, size_t cols); /* -1 = None */

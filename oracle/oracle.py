@@ -22,6 +22,7 @@ _P, _S, _I, _U8, _U64, _F = C.c_void_p, C.c_size_t, C.c_int, C.c_uint8, C.c_uint
 _PROTO = {
     "or_f16_to_f32": (_F, [C.c_uint16]),
     "or_f32_to_f16": (C.c_uint16, [_F]),
+    "or_f32_to_f16_n": (None, [_P, _S, _P]),
     "or_row_bytes": (C.c_int64, [_U8, _S]),
     "or_dequant_q8_0_range": (_I, [_P, _S, _S, _P, _S]),
     "or_dequant_q4_k_range": (_I, [_P, _S, _S, _P, _S]),
@@ -172,6 +173,25 @@ def synth(dtype, rows, cols, seed, stream):
     out = np.empty(rows * rb, dtype=np.uint8)
     fn = {DTYPE_Q4_K: lib().or_synth_q4_k, DTYPE_Q8_0: lib().or_synth_q8_0, DTYPE_Q6_K: lib().or_synth_q6_k}[dtype]
     fn(_p(out), rows, cols, seed, stream)
+    return out
+
+
+def f32_to_f16(v):
+    """soso's f32 -> f16 bits (f16.rs:10-36) over an array, as uint16."""
+    v = f32(v).ravel()
+    out = np.empty(v.size, dtype=np.uint16)
+    lib().or_f32_to_f16_n(_p(v), v.size, _p(out))
+    return out
+
+
+def f16_to_f32(bits):
+    """soso's f16 -> f32 (dequant.rs:26-45) over an array of uint16 bits.  For
+    every non-NaN pattern it equals IEEE widening (all 65536 patterns are
+    compared in tests/test_oracle_golden.py), so numpy's conversion is used,
+    with NaN made canonical as or_f16_to_f32 does."""
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = b.view(np.float16).astype(np.float32)
+    out[np.isnan(out)] = np.float32(np.nan)
     return out
 
 

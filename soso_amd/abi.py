@@ -41,7 +41,7 @@ class DecodeCfg(C.Structure):
     _fields_ = [
         ("n_layers", C.c_uint32), ("hidden", C.c_uint32), ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32),
         ("head_dim", C.c_uint32), ("ffn", C.c_uint32), ("vocab", C.c_uint32), ("ctx_max", C.c_uint32),
-        ("rope_theta", C.c_float), ("rms_eps", C.c_float),
+        ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("kv_f16", C.c_uint32),
     ]
 
 
@@ -76,7 +76,8 @@ PROTOTYPES = {
     "soso_hip_moe_ffn_dev": (_I, [_P, C.c_char_p, _S, _P, _S, _P, _P, _P]),
     "soso_hip_decode_create": (_I, [_P, C.c_char_p, _S, C.POINTER(DecodeCfg), _P, _P, _I]),
     "soso_hip_decode_kv_dev": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),
-    "soso_hip_decode_step_dev": (_I, [_P, C.c_char_p, _S, _P, C.c_uint32, _P, _P]),
+    "soso_hip_decode_kv_upload": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P, _I]),
+    "soso_hip_decode_step_dev": (_I, [_P, C.c_char_p, _S, _P, C.c_uint32, _P, _P, _P]),
     "soso_hip_decode_destroy": (_I, [_P, C.c_char_p, _S]),
     "soso_hip_dev_alloc": (_I, [_P, _S, C.POINTER(_P)]),
     "soso_hip_dev_free": (_I, [_P, _P]),

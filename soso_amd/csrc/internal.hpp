@@ -71,7 +71,8 @@ struct DecodeModel {
     const float *out_norm = nullptr;
     const Weight *head = nullptr;
     std::vector<std::string> uses; // keys of the resident weights the model reads
-    float *kcache = nullptr, *vcache = nullptr; // [n_layers][n_kv_heads][ctx_max][head_dim]
+    bool kv_f16 = false;                        // KV elements: f16 bits (soso's KvDtype::F16) or f32
+    void *kcache = nullptr, *vcache = nullptr;  // [n_layers][n_kv_heads][ctx_max][head_dim]
     void *mem = nullptr;                         // activations below, one allocation
     float *hid = nullptr, *qbuf = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
 };
@@ -124,8 +125,11 @@ struct MvEpi {
     // rotated, the next kv_dim -> v_out; RoPE of pairs (2i, 2i+1) inside each
     // head_dim block at position pos (non-NeoX, gemm.rs:1452-1490)
     // (K/V caches head-major: element d of KV head j at position pos is at
-    // j * kv_stride + pos * head_dim + d)
-    float *k_out = nullptr, *v_out = nullptr;
+    // j * kv_stride + pos * head_dim + d; f32, or f16 bits when kv_f16)
+    void *k_out = nullptr, *v_out = nullptr;
+    // when non-null, also k at rows_out[e] and v at rows_out[kv_dim + e]
+    void *rows_out = nullptr;
+    int kv_f16 = 0;
     int q_dim = 0, kv_dim = 0, head_dim = 0, pos = 0;
     size_t kv_stride = 0;
     float theta = 0.0f;
@@ -144,9 +148,14 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y_dev,
 int launch_dequant(soso_hip *h, const Weight &w, float *out_dev);
 int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
 // (k_decode.hip)
-int launch_attention(soso_hip *h, const float *q, const float *K, const float *V, int n_heads, int n_kv_heads,
-                     int head_dim, int ctx, int T, float *part, float *out);
-int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token);
+int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, bool kv_f16, int n_heads,
+                     int n_kv_heads, int head_dim, int ctx, int T, float *part, float *out);
+int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token,
+                void *kv_rows);
+// Scatter n_rows position-major rows [n_rows][kv_dim] (f32 when src_f32, else
+// the cache's element type) into a head-major cache at positions row0...
+int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, bool cache_f16, int kv_dim,
+                      int head_dim, int ctx, int row0, int n_rows);
 // (k_synth.hip)
 int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
                      uint64_t stream);
@@ -208,6 +217,27 @@ __device__ __forceinline__ float f16_to_f32_ref(uint32_t b16)
     b16 &= 0xffffu;
     if ((b16 & 0x7c00u) == 0x7c00u && (b16 & 0x3ffu)) return __builtin_bit_cast(float, 0x7fc00000u);
     return half_bits_to_f32(b16);
+}
+
+// f32 -> f16 bits with the rounding of crates/soso-llm-core/src/f16.rs:10-36,
+// which the KV rows must reproduce bit for bit: nearest, a tie goes away from
+// zero (the first dropped bit is added to the magnitude, so a carry may step
+// into the exponent or up to infinity), magnitudes below 2^-25 flush to a
+// signed zero, and every NaN becomes 0x7e00 with its sign.  The hardware
+// conversion rounds ties to even, hence the integer form.
+__device__ __forceinline__ uint32_t f32_to_f16_soso(float v)
+{
+    const uint32_t b = __builtin_bit_cast(uint32_t, v);
+    const uint32_t sign = (b >> 16) & 0x8000u, mag = b & 0x7fffffffu, frac = b & 0x7fffffu;
+    const int e = (int)(mag >> 23) - 112; // biased f16 exponent
+    if (mag >= 0x7f800000u) return sign | 0x7c00u | (mag > 0x7f800000u ? 0x200u : 0u);
+    if (e >= 31) return sign | 0x7c00u;
+    if (e <= 0) {
+        if (e < -10) return sign;
+        const uint32_t m = frac | 0x800000u, sh = (uint32_t)(14 - e);
+        return sign | ((m >> sh) + ((m >> (sh - 1)) & 1u));
+    }
+    return (sign | ((uint32_t)e << 10) | (frac >> 13)) + ((frac >> 12) & 1u);
 }
 
 template <int W>

@@ -5,7 +5,8 @@
 // rope_cabezas (gemm.rs:1452-1490) -> KV append -> attention -> o-proj +
 // residual -> ffn_norm -> gate/up -> swiglu -> down + residual; then
 // Runtime::logits_gpu + argmax (crates/soso-llm-core/src/runtime.rs:1976-2028).
-// The KV cache is f32 here; soso keeps f16 (kv.rs:349).
+// The KV cache holds f32 or, as soso's KvCache (kv.rs:258-266),
+// f16 bits rounded with soso's f32_to_f16 (f16.rs:10-36).
 //
 // Launches per layer (every weight byte read once, activations stay in HBM):
 //   1. qkv matvec   x = rmsnorm(h) staged in LDS; rows [q; k; v] concatenated;
@@ -50,9 +51,9 @@ constexpr int ATT_CHUNK = 64; // positions per split
 // statistics (m_w = max s, p = e^{s - m_w}, l_w = sum p, acc_w = sum p v);
 // the four are merged in LDS into the chunk's (m, l, acc), stored at
 // part[(head * chunks + c) * (HD + 2)].
-template <int G>
-__global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q, const float *__restrict__ K,
-                                                     const float *__restrict__ V, int ctx, int T, int chunks,
+template <int G, bool F16>
+__global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q, const void *__restrict__ Kc,
+                                                     const void *__restrict__ Vc, int ctx, int T, int chunks,
                                                      float *__restrict__ part)
 {
     constexpr int HD = ATT_HD, NW = 4;
@@ -63,24 +64,56 @@ __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q,
     const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK);
     const int lane = tid & 63, wave = tid >> 6;
     const int tw = t0 + 16 * wave;
-    const float *Kh = K + (size_t)g * ctx * HD, *Vh = V + (size_t)g * ctx * HD;
+    const size_t head_off = (size_t)g * ctx * HD;
     const int pp = lane >> 3, j = lane & 7;
+    // K: f32 rows are 512 B, lane j of a position takes float4 units j, j+8,
+    // j+16, j+24 (dims 32i + 4j ..); f16 rows are 256 B, lane j takes 16-byte
+    // units j, j+8 (dims 64i + 8j .. 64i + 8j + 7)
     float4 kv[2][4];
+    uint4 kh[2][2];
 #pragma unroll
     for (int a = 0; a < 2; a++) {
-        const float4 *k4 = (const float4 *)(Kh + (size_t)min(tw + 8 * a + pp, t1 - 1) * HD);
+        const size_t row = head_off + (size_t)min(tw + 8 * a + pp, t1 - 1) * HD;
+        if constexpr (F16) {
+            const uint4 *k4 = (const uint4 *)((const uint16_t *)Kc + row);
 #pragma unroll
-        for (int i = 0; i < 4; i++) kv[a][i] = k4[8 * i + j];
+            for (int i = 0; i < 2; i++) kh[a][i] = k4[8 * i + j];
+        } else {
+            const float4 *k4 = (const float4 *)((const float *)Kc + row);
+#pragma unroll
+            for (int i = 0; i < 4; i++) kv[a][i] = k4[8 * i + j];
+        }
     }
     __builtin_amdgcn_sched_barrier(0);
     float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
     if (tid < G * HD / 4) qv = ((const float4 *)(q + (size_t)g * G * HD))[tid];
     __builtin_amdgcn_sched_barrier(0);
+    // V: lane l holds dims 2l, 2l + 1 of the wavefront's 16 positions
     float2 vr[16];
+    uint32_t vh[16];
 #pragma unroll
-    for (int k = 0; k < 16; k++) vr[k] = *(const float2 *)(Vh + (size_t)min(tw + k, t1 - 1) * HD + 2 * lane);
+    for (int k = 0; k < 16; k++) {
+        const size_t row = head_off + (size_t)min(tw + k, t1 - 1) * HD + 2 * lane;
+        if constexpr (F16)
+            vh[k] = *(const uint32_t *)((const uint16_t *)Vc + row);
+        else
+            vr[k] = *(const float2 *)((const float *)Vc + row);
+    }
     __builtin_amdgcn_sched_barrier(0);
     if (tid < G * HD / 4) *(float4 *)&qs[4 * tid] = qv;
+    if constexpr (F16) {
+        // f16 -> f32 is exact; from here on the math is the f32 kernel's
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const uint32_t w[4] = {kh[a][i].x, kh[a][i].y, kh[a][i].z, kh[a][i].w};
+                kv[a][2 * i] = make_float4(half_bits_to_f32(w[0] & 0xffffu), half_bits_to_f32(w[0] >> 16),
+                                           half_bits_to_f32(w[1] & 0xffffu), half_bits_to_f32(w[1] >> 16));
+                kv[a][2 * i + 1] = make_float4(half_bits_to_f32(w[2] & 0xffffu), half_bits_to_f32(w[2] >> 16),
+                                               half_bits_to_f32(w[3] & 0xffffu), half_bits_to_f32(w[3] >> 16));
+            }
+    }
     __syncthreads();
     const float inv = 1.0f / sqrtf((float)HD);
 #pragma unroll
@@ -91,7 +124,9 @@ __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q,
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const float4 qq = *(const float4 *)&qs[hh * HD + 32 * i + 4 * j];
+                // kv[a][i] holds dims 32i + 4j .. (f32) or 64(i/2) + 8j + 4(i%2) .. (f16)
+                const int d0 = F16 ? 64 * (i >> 1) + 8 * j + 4 * (i & 1) : 32 * i + 4 * j;
+                const float4 qq = *(const float4 *)&qs[hh * HD + d0];
                 acc = fmaf(kv[a][i].x, qq.x, acc);
                 acc = fmaf(kv[a][i].y, qq.y, acc);
                 acc = fmaf(kv[a][i].z, qq.z, acc);
@@ -111,8 +146,10 @@ __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q,
             const float pk = __builtin_bit_cast(
                 float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[k >> 3]), 8 * (k & 7)));
             l += pk;
-            acc.x = fmaf(pk, vr[k].x, acc.x);
-            acc.y = fmaf(pk, vr[k].y, acc.y);
+            const float2 vk = F16 ? make_float2(half_bits_to_f32(vh[k] & 0xffffu), half_bits_to_f32(vh[k] >> 16))
+                                  : vr[k];
+            acc.x = fmaf(pk, vk.x, acc.x);
+            acc.y = fmaf(pk, vk.y, acc.y);
         }
         accs[wave][hh][lane] = acc;
         if (lane == 0) {
@@ -210,31 +247,71 @@ __global__ void __launch_bounds__(256) k_attn_merge(const float *__restrict__ pa
     }
 }
 
-int launch_attention(soso_hip *h, const float *q, const float *K, const float *V, int n_heads, int n_kv_heads,
-                     int head_dim, int ctx, int T, float *part, float *out)
+int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, bool kv_f16, int n_heads,
+                     int n_kv_heads, int head_dim, int ctx, int T, float *part, float *out)
 {
     if (head_dim != ATT_HD || n_kv_heads <= 0 || n_heads % n_kv_heads || T <= 0 || T > ctx)
         return set_err(h, SOSO_HIP_DECLINED, "attention: head shape not handled here");
     const int G = n_heads / n_kv_heads;
     const int chunks = (T + ATT_CHUNK - 1) / ATT_CHUNK;
     const dim3 grid((unsigned)n_kv_heads, (unsigned)chunks);
+#define ATT_CASE(GG)                                                                                                \
+    case GG:                                                                                                        \
+        if (kv_f16)                                                                                                 \
+            k_attn_split<GG, true><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);                     \
+        else                                                                                                        \
+            k_attn_split<GG, false><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);                    \
+        break;
     switch (G) {
-    case 1: k_attn_split<1><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
-    case 2: k_attn_split<2><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
-    case 4: k_attn_split<4><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
-    case 8: k_attn_split<8><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part); break;
+        ATT_CASE(1) ATT_CASE(2) ATT_CASE(4) ATT_CASE(8)
     default: return set_err(h, SOSO_HIP_DECLINED, "attention: GQA group size not handled here");
     }
+#undef ATT_CASE
     int rc = hip_check(h, hipGetLastError(), "attention split launch");
     if (rc != SOSO_HIP_OK) return rc;
     k_attn_merge<<<(unsigned)n_heads, 256, 0, h->stream>>>(part, chunks, out);
     return hip_check(h, hipGetLastError(), "attention merge launch");
 }
 
+// KV upload (decode_subir_estado): element e of the position-major rows
+// [n_rows][kv_dim] goes to head e / head_dim, position row0 + e / kv_dim of
+// the head-major cache; f32 rows entering an f16 cache take soso's rounding.
+template <bool SRC_F32, bool DST_F16>
+__global__ void __launch_bounds__(256) k_kv_scatter(const void *__restrict__ src, void *__restrict__ cache,
+                                                     int kv_dim, int head_dim, int ctx, int row0, size_t n)
+{
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= n) return;
+    const int r = (int)(e / kv_dim), c = (int)(e % kv_dim);
+    const size_t at = ((size_t)(c / head_dim) * ctx + row0 + r) * head_dim + c % head_dim;
+    if constexpr (!DST_F16)
+        ((float *)cache)[at] = ((const float *)src)[e];
+    else if constexpr (SRC_F32)
+        ((uint16_t *)cache)[at] = (uint16_t)f32_to_f16_soso(((const float *)src)[e]);
+    else
+        ((uint16_t *)cache)[at] = ((const uint16_t *)src)[e];
+}
+
+int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, bool cache_f16, int kv_dim,
+                      int head_dim, int ctx, int row0, int n_rows)
+{
+    const size_t n = (size_t)n_rows * kv_dim;
+    if (n == 0) return SOSO_HIP_OK;
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (!cache_f16)
+        k_kv_scatter<true, false><<<grid, 256, 0, h->stream>>>(src, cache, kv_dim, head_dim, ctx, row0, n);
+    else if (src_f32)
+        k_kv_scatter<true, true><<<grid, 256, 0, h->stream>>>(src, cache, kv_dim, head_dim, ctx, row0, n);
+    else
+        k_kv_scatter<false, true><<<grid, 256, 0, h->stream>>>(src, cache, kv_dim, head_dim, ctx, row0, n);
+    return hip_check(h, hipGetLastError(), "kv scatter launch");
+}
+
 // ---------------------------------------------------------------------------
 // The decode step
 // ---------------------------------------------------------------------------
-int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token)
+int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token,
+                void *kv_rows)
 {
     const int q_dim = (int)(m.n_heads * m.head_dim), kv_dim = (int)(m.n_kv_heads * m.head_dim);
     if (pos >= m.ctx_max) return set_err(h, SOSO_HIP_ERR_ARG, "decode: position beyond the KV capacity");
@@ -242,7 +319,8 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
     int rc = hip_check(h, hipMemcpyAsync(hid, x, m.hidden * 4, hipMemcpyDeviceToDevice, h->stream), "embed copy");
     for (size_t l = 0; l < m.n_layers && rc == SOSO_HIP_OK; l++) {
         const DecodeLayer &L = m.layers[l];
-        float *K = m.kcache + l * m.ctx_max * kv_dim, *V = m.vcache + l * m.ctx_max * kv_dim;
+        const size_t esz = m.kv_f16 ? 2 : 4, layer_bytes = m.ctx_max * kv_dim * esz;
+        void *K = (char *)m.kcache + l * layer_bytes, *V = (char *)m.vcache + l * layer_bytes;
         MvIn in;
         in.x = hid;
         in.norm_w = L.attn_norm;
@@ -250,6 +328,8 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         MvEpi ep;
         ep.k_out = K;
         ep.v_out = V;
+        ep.kv_f16 = m.kv_f16 ? 1 : 0;
+        ep.rows_out = kv_rows ? (char *)kv_rows + l * 2 * kv_dim * esz : nullptr;
         ep.kv_stride = m.ctx_max * m.head_dim;
         ep.q_dim = q_dim;
         ep.kv_dim = kv_dim;
@@ -258,8 +338,8 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         ep.theta = m.theta;
         rc = launch_matvec_ex(h, *L.qkv, in, qb, ep, XS_RMSNORM, EPI_QKV);
         if (rc == SOSO_HIP_OK)
-            rc = launch_attention(h, qb, K, V, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim, (int)m.ctx_max,
-                                  (int)pos + 1, m.part, att);
+            rc = launch_attention(h, qb, K, V, m.kv_f16, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim,
+                                  (int)m.ctx_max, (int)pos + 1, m.part, att);
         if (rc == SOSO_HIP_OK) {
             MvIn a;
             a.x = att;

@@ -188,6 +188,20 @@ __device__ __forceinline__ void rope_angle(const MvEpi &ep, int r, float &cs, fl
     }
 }
 
+// One new K or V element: into the cache at `at` and, when asked, into the
+// step's row copy at `row_at` (f16 with soso's rounding, or f32).
+__device__ __forceinline__ void kv_put(const MvEpi &ep, void *cache, size_t at, int row_at, float v)
+{
+    if (ep.kv_f16) {
+        const uint16_t b = (uint16_t)f32_to_f16_soso(v);
+        ((uint16_t *)cache)[at] = b;
+        if (ep.rows_out) ((uint16_t *)ep.rows_out)[row_at] = b;
+    } else {
+        ((float *)cache)[at] = v;
+        if (ep.rows_out) ((float *)ep.rows_out)[row_at] = v;
+    }
+}
+
 template <int EPI>
 __device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows, int rows, float *__restrict__ y,
                                          const MvEpi &ep, float cs = 1.0f, float sn = 0.0f)
@@ -218,12 +232,14 @@ __device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows
                     y[r] = v;
                 } else {
                     const int e = r - ep.q_dim;
-                    ep.k_out[(size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + d] = v;
+                    kv_put(ep, ep.k_out, (size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + d,
+                           e, v);
                 }
             } else {
                 const int e = r - qk;
-                ep.v_out[(size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + e % ep.head_dim] =
-                    yacc;
+                kv_put(ep, ep.v_out,
+                       (size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + e % ep.head_dim,
+                       ep.kv_dim + e, yacc);
             }
         }
     }

@@ -31,28 +31,7 @@ __device__ __forceinline__ float normal(uint64_t seed, uint64_t stream, uint64_t
     return __fmul_rn((float)(s - 393210), 1.0f / 65536.0f);
 }
 
-// crates/soso-llm-core/src/f16.rs:10-37
-__device__ __forceinline__ uint16_t f32_to_f16_soso(float v)
-{
-    const uint32_t bits = __builtin_bit_cast(uint32_t, v);
-    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
-    const int32_t exp = (int32_t)((bits >> 23) & 0xffu);
-    const uint32_t frac = bits & 0x7fffffu;
-    if (exp == 255) return (uint16_t)(sign | 0x7c00u | (frac != 0 ? 0x200u : 0u));
-    const int32_t e = exp - 127 + 15;
-    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
-    if (e <= 0) {
-        if (e < -10) return sign;
-        const uint32_t f = frac | 0x800000u;
-        const uint32_t shift = (uint32_t)(14 - e);
-        const uint16_t sub = (uint16_t)(f >> shift);
-        const uint16_t round = (uint16_t)((f >> (shift - 1)) & 1u);
-        return (uint16_t)(sign | (uint16_t)(sub + round));
-    }
-    const uint32_t half = ((uint32_t)e << 10) | (frac >> 13);
-    const uint16_t round = (uint16_t)((frac >> 12) & 1u);
-    return (uint16_t)((uint16_t)(sign | (uint16_t)half) + round);
-}
+// f32_to_f16_soso (internal.hpp) rounds the f16 scales as soso's quantizers do.
 
 #define SUB(s, f) (((s) << 4) | (uint64_t)(f))
 

@@ -601,6 +601,7 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     m.ctx_max = cfg->ctx_max;
     m.theta = cfg->rope_theta;
     m.eps = cfg->rms_eps;
+    m.kv_f16 = cfg->kv_f16 != 0;
     auto get = [&](size_t i, size_t rows, size_t cols, bool f32, const Weight **out) -> bool {
         const Weight *w = find_weight(h, keys[i], key_lens[i]);
         if (!w || w->rows != rows || w->cols != cols || (f32 != (w->dtype == SOSO_HIP_DTYPE_F32))) return false;
@@ -669,12 +670,12 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
         m.layers[l].gu = &wg;
     }
     // KV cache and step buffers
-    const size_t kv_bytes = L * cfg->ctx_max * kvd * 4;
+    const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
     const size_t chunks = (cfg->ctx_max + 63) / 64;
     const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64;
     const size_t mem_bytes = act_floats * 4;
     if (rc == SOSO_HIP_OK) {
-        if (hipMalloc((void **)&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, mem_bytes) != hipSuccess)
+        if (hipMalloc(&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, mem_bytes) != hipSuccess)
             rc = set_err(h, SOSO_HIP_DECLINED, "decode_create: no memory for the KV cache");
     }
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemsetAsync(m.kcache, 0, 2 * kv_bytes, h->stream), "kv zero");
@@ -684,7 +685,7 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
         decode_free(h, m);
         return rc;
     }
-    m.vcache = m.kcache + L * cfg->ctx_max * kvd;
+    m.vcache = (char *)m.kcache + kv_bytes;
     float *f = (float *)m.mem;
     m.hid = f;
     m.qbuf = f + H;
@@ -709,22 +710,57 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     return SOSO_HIP_OK;
 }
 
-int soso_hip_decode_kv_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, float **k_dev,
-                           float **v_dev)
+int soso_hip_decode_kv_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, void **k_dev,
+                           void **v_dev)
 {
     if (!h || !model_key || !k_dev || !v_dev) return SOSO_HIP_ERR_ARG;
     auto it = h->decode_models.find(std::string(model_key, model_key_len));
     if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_kv: model not registered");
     const DecodeModel &m = it->second;
     if (layer >= m.n_layers) return set_err(h, SOSO_HIP_ERR_ARG, "decode_kv: layer");
-    const size_t per = m.ctx_max * m.n_kv_heads * m.head_dim;
-    *k_dev = m.kcache + layer * per;
-    *v_dev = m.vcache + layer * per;
+    const size_t per = m.ctx_max * m.n_kv_heads * m.head_dim * (m.kv_f16 ? 2 : 4);
+    *k_dev = (char *)m.kcache + layer * per;
+    *v_dev = (char *)m.vcache + layer * per;
     return SOSO_HIP_OK;
 }
 
+int soso_hip_decode_kv_upload(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer, uint32_t row0,
+                              uint32_t n_rows, const void *k_rows, const void *v_rows, int rows_f32)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!model_key || (n_rows && (!k_rows || !v_rows))) return set_err(h, SOSO_HIP_ERR_ARG, "decode_kv_upload: args");
+    if (h->capturing) return set_err(h, SOSO_HIP_ERR_ARG, "decode_kv_upload: not inside graph capture");
+    auto it = h->decode_models.find(std::string(model_key, model_key_len));
+    if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_kv_upload: model not registered");
+    const DecodeModel &m = it->second;
+    if (layer >= m.n_layers) return set_err(h, SOSO_HIP_ERR_ARG, "decode_kv_upload: layer");
+    if ((size_t)row0 + n_rows > m.ctx_max) return set_err(h, SOSO_HIP_ERR_ARG, "decode_kv_upload: rows beyond ctx_max");
+    if (n_rows == 0) return SOSO_HIP_OK;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    const size_t kvd = m.n_kv_heads * m.head_dim;
+    const bool src_f32 = rows_f32 != 0 || !m.kv_f16;
+    const size_t bytes = (size_t)n_rows * kvd * (src_f32 ? 4 : 2);
+    void *stage = scratch_get(h, 11, bytes);
+    if (!stage) return set_err(h, SOSO_HIP_DECLINED, "decode_kv_upload: no memory for staging");
+    const size_t per = m.ctx_max * kvd * (m.kv_f16 ? 2 : 4);
+    for (int which = 0; which < 2 && rc == SOSO_HIP_OK; which++) {
+        const void *src = which ? v_rows : k_rows;
+        void *cache = (char *)(which ? m.vcache : m.kcache) + layer * per;
+        // host or device source: the runtime tells them apart (unified addressing)
+        rc = hip_check(h, hipMemcpyAsync(stage, src, bytes, hipMemcpyDefault, h->stream), "kv rows copy");
+        if (rc == SOSO_HIP_OK)
+            rc = launch_kv_scatter(h, stage, src_f32, cache, m.kv_f16, (int)kvd, (int)m.head_dim, (int)m.ctx_max,
+                                   (int)row0, (int)n_rows);
+        // the staging buffer is reused for V: K's scatter must have read it
+        if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "kv upload sync");
+    }
+    if (rc == SOSO_HIP_OK) h->stats.bytes_up += 2 * bytes;
+    return rc;
+}
+
 int soso_hip_decode_step_dev(soso_hip *h, const char *model_key, size_t model_key_len, const float *x_dev, uint32_t pos,
-                             float *logits_dev, uint32_t *token_dev)
+                             float *logits_dev, uint32_t *token_dev, void *kv_rows_dev)
 {
     if (!h) return SOSO_HIP_ERR_ARG;
     if (!model_key || !x_dev) return set_err(h, SOSO_HIP_ERR_ARG, "decode_step: args");
@@ -732,7 +768,7 @@ int soso_hip_decode_step_dev(soso_hip *h, const char *model_key, size_t model_ke
     if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_step: model not registered");
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
-    return decode_step(h, it->second, x_dev, pos, logits_dev, token_dev);
+    return decode_step(h, it->second, x_dev, pos, logits_dev, token_dev, kv_rows_dev);
 }
 
 int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key_len)

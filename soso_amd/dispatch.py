@@ -288,10 +288,27 @@ class HipGpu:
         self._rc(self.lib.soso_hip_decode_kv_dev(self.h, mk, ml, layer, C.byref(k), C.byref(v)), "decode_kv_dev")
         return k.value, v.value
 
-    def decode_step_dev(self, model_key, x_dev, pos, logits_dev=None, token_dev=None):
+    def decode_kv_upload(self, model_key, layer, row0, k_rows, v_rows, rows_f32=True):
+        """decode_subir_estado: position-major rows [n][kv_dim] of K and V (numpy
+        arrays, f32 or uint16 f16 bits; or device pointers with n given as
+        k_rows = (ptr, n)) into the cache at positions row0 .."""
         mk, ml = _key(model_key)
-        return self._rc(self.lib.soso_hip_decode_step_dev(self.h, mk, ml, x_dev, pos, logits_dev, token_dev),
-                        f"decode_step_dev {model_key}")
+        if isinstance(k_rows, tuple):
+            (kp, n), (vp, _) = k_rows, v_rows
+        else:
+            want = np.float32 if rows_f32 else np.uint16
+            k_rows = np.ascontiguousarray(k_rows, dtype=want)
+            v_rows = np.ascontiguousarray(v_rows, dtype=want)
+            if k_rows.shape != v_rows.shape:
+                raise ValueError("decode_kv_upload: K and V rows differ in shape")
+            kp, vp, n = k_rows.ctypes.data, v_rows.ctypes.data, k_rows.shape[0]
+        return self._rc(self.lib.soso_hip_decode_kv_upload(self.h, mk, ml, layer, row0, n, kp, vp,
+                                                           1 if rows_f32 else 0), "decode_kv_upload")
+
+    def decode_step_dev(self, model_key, x_dev, pos, logits_dev=None, token_dev=None, kv_rows_dev=None):
+        mk, ml = _key(model_key)
+        return self._rc(self.lib.soso_hip_decode_step_dev(self.h, mk, ml, x_dev, pos, logits_dev, token_dev,
+                                                          kv_rows_dev), f"decode_step_dev {model_key}")
 
     def decode_destroy(self, model_key):
         mk, ml = _key(model_key)

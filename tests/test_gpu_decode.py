@@ -12,8 +12,14 @@ Weights: f32 ~ N(0, 0.05) quantized with the reference quantizers
 (quant.rs restated in the oracle): Q4_K projections, Q8_0 head (the path soso
 runs after converting Q6_K heads to Q8_0, gguf2som/src/lib.rs:1592-1609).
 
-Bar: K/V rows written at `pos` and the logits within relative L2 1e-5, the
-greedy token identical.
+Bar: logits within relative L2 1e-5, the greedy token identical; K/V rows
+written at `pos` within relative L2 1e-5 (f32).  In f16 the GPU's row, widened,
+must be as close to the CPU's f32 row as the oracle's rounding of that row is,
+within the same 1e-5 (the f32 values feeding the rounding differ slightly
+between CPU and GPU, so an element next to a rounding midpoint, or a small one
+whose f16 step is finer than that difference, may land on a neighbour); most
+elements must match bit for bit.  The rounding itself is checked bit for bit
+on crafted inputs by test_kv_upload_rounds_like_soso.
 """
 import numpy as np
 import pytest
@@ -88,10 +94,13 @@ class Model:
         self.keys = keys
         return keys
 
-    def cpu_step(self, orc, x, kcache, vcache, pos, theta, eps):
-        """The dense layer stack on the CPU; kcache/vcache [L][ctx][kvd] get row pos."""
+    def cpu_step(self, orc, x, kcache, vcache, pos, theta, eps, kv_f16=False):
+        """The dense layer stack on the CPU; kcache/vcache [L][ctx][kvd] get row pos
+        (rounded through soso's f16 when kv_f16, as KvCache::append stores it)."""
         L_ = orc.lib()
         h = x.astype(np.float32).copy()
+        new_k, new_v = [], []
+        self.last_kv = (new_k, new_v)  # the f32 rows appended at pos, per layer
         for l, lw in enumerate(self.layers):
             xn = h.copy()
             L_.or_rmsnorm(xn.ctypes.data, lw["attn_norm"].ctypes.data, self.H, np.float32(eps))
@@ -100,8 +109,10 @@ class Model:
             v = orc.matvec(Q4K, lw["v"], self.kvd, self.H, xn)
             L_.or_rope_heads(q.ctypes.data, self.nh, HD, pos, np.float32(theta), 0)
             L_.or_rope_heads(k.ctypes.data, self.nkv, HD, pos, np.float32(theta), 0)
-            kcache[l, pos] = k
-            vcache[l, pos] = v
+            kcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(k)) if kv_f16 else k
+            vcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(v)) if kv_f16 else v
+            new_k.append(k)
+            new_v.append(v)
             att = np.zeros(self.qd, np.float32)
             Kc = np.ascontiguousarray(kcache[l, :pos + 1])
             Vc = np.ascontiguousarray(vcache[l, :pos + 1])
@@ -125,44 +136,71 @@ class Model:
         return logits, int(L_.or_argmax(logits.ctypes.data, logits.size))
 
 
+@pytest.mark.parametrize("kv_f16", [0, 1])
 @pytest.mark.parametrize("L,H,nh,nkv,F,V,prefill", [
     (2, 512, 4, 2, 1024, 1000, 100),   # GQA group 2, two attention chunks
     (1, 1024, 8, 2, 2048, 512, 200),   # GQA group 4 (the 8B's ratio)
 ])
-def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill):
+def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill, kv_f16):
     theta, eps, ctx = 500000.0, 1e-5, 256
     m = Model(orc, L, H, nh, nkv, F, V, 50 + L)
     m.upload(gpu)
     name = m.name + ".model"
     cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
-               rope_theta=theta, rms_eps=eps)
+               rope_theta=theta, rms_eps=eps, kv_f16=kv_f16)
+    print(f"decode step L={L} H={H} heads={nh}/{nkv} prefill={prefill} kv_f16={kv_f16}", flush=True)
     gpu.decode_create(name, cfg, m.keys)
     kc = np.zeros((L, ctx, m.kvd), np.float32)
     vc = np.zeros((L, ctx, m.kvd), np.float32)
+    kvt, esz = (np.uint16, 2) if kv_f16 else (np.float32, 4)
     for l in range(L):
-        kc[l, :prefill] = orc.normal(prefill * m.kvd, 1.0, 60 + l, 1).reshape(prefill, m.kvd)
-        vc[l, :prefill] = orc.normal(prefill * m.kvd, 1.0, 60 + l, 2).reshape(prefill, m.kvd)
-        kd, vd = gpu.decode_kv_dev(name, l)
-        gpu.h2d(kd, head_major(kc[l], nkv))
-        gpu.h2d(vd, head_major(vc[l], nkv))
+        kr = orc.normal(prefill * m.kvd, 1.0, 60 + l, 1).reshape(prefill, m.kvd)
+        vr = orc.normal(prefill * m.kvd, 1.0, 60 + l, 2).reshape(prefill, m.kvd)
+        # decode_subir_estado: position-major f32 rows, rounded by the library
+        gpu.decode_kv_upload(name, l, 0, kr, vr, rows_f32=True)
+        if kv_f16:
+            kb, vb = orc.f32_to_f16(kr).reshape(kr.shape), orc.f32_to_f16(vr).reshape(vr.shape)
+            kd, vd = gpu.decode_kv_dev(name, l)
+            gk = gpu.d2h(kd, (nkv, ctx, HD), np.uint16)[:, :prefill].transpose(1, 0, 2).reshape(prefill, m.kvd)
+            gv = gpu.d2h(vd, (nkv, ctx, HD), np.uint16)[:, :prefill].transpose(1, 0, 2).reshape(prefill, m.kvd)
+            assert np.array_equal(gk, kb) and np.array_equal(gv, vb), "uploaded f16 rows differ from soso's rounding"
+            kr, vr = orc.f16_to_f32(kb), orc.f16_to_f32(vb)
+        else:
+            kd, vd = gpu.decode_kv_dev(name, l)
+            assert np.array_equal(gpu.d2h(kd, (nkv, ctx, HD), np.float32)[:, :prefill], head_major(kr, nkv)[:, :prefill])
+        kc[l, :prefill] = kr
+        vc[l, :prefill] = vr
     x = orc.normal(H, 1.0, 70, 1)
     xd = gpu.dev_alloc(H * 4)
     ld = gpu.dev_alloc(V * 4)
     td = gpu.dev_alloc(4)
+    rd = gpu.dev_alloc(L * 2 * m.kvd * esz)
     try:
         gpu.h2d(xd, x)
-        gpu.decode_step_dev(name, xd, prefill, ld, td)
+        gpu.decode_step_dev(name, xd, prefill, ld, td, rd)
         gpu.sync()
         logits = gpu.d2h(ld, (V,), np.float32)
         token = int(gpu.d2h(td, (1,), np.uint32)[0])
-        kgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[0], (nkv, ctx, HD), np.float32)[:, prefill].ravel()
-                for l in range(L)]
-        vgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[1], (nkv, ctx, HD), np.float32)[:, prefill].ravel()
-                for l in range(L)]
-        ref_logits, ref_token = m.cpu_step(orc, x, kc, vc, prefill, theta, eps)
+        rows = gpu.d2h(rd, (L, 2, m.kvd), kvt)
+        kgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[0], (nkv, ctx, HD), kvt)[:, prefill].ravel() for l in range(L)]
+        vgpu = [gpu.d2h(gpu.decode_kv_dev(name, l)[1], (nkv, ctx, HD), kvt)[:, prefill].ravel() for l in range(L)]
+        # the kv_rows copy (decode_token's layout) equals what went into the cache
         for l in range(L):
-            assert orc.rel_l2(kgpu[l], kc[l, prefill]) < 1e-5, l
-            assert orc.rel_l2(vgpu[l], vc[l, prefill]) < 1e-5, l
+            assert np.array_equal(rows[l, 0], kgpu[l]) and np.array_equal(rows[l, 1], vgpu[l]), l
+        ref_logits, ref_token = m.cpu_step(orc, x, kc, vc, prefill, theta, eps, kv_f16=bool(kv_f16))
+        k32, v32 = m.last_kv
+        for l in range(L):
+            if kv_f16:
+                # ref32: the CPU's f32 row before rounding (kc holds it rounded)
+                for got, ref32 in ((kgpu[l], k32[l]), (vgpu[l], v32[l])):
+                    want = orc.f32_to_f16(ref32)
+                    e_gpu = orc.rel_l2(orc.f16_to_f32(got), ref32)
+                    e_orc = orc.rel_l2(orc.f16_to_f32(want), ref32)
+                    assert e_gpu <= e_orc + 1e-5, (l, e_gpu, e_orc)
+                    assert (got == want).mean() > 0.95, (l, float((got == want).mean()))
+            else:
+                assert orc.rel_l2(kgpu[l], kc[l, prefill]) < 1e-5, l
+                assert orc.rel_l2(vgpu[l], vc[l, prefill]) < 1e-5, l
         assert orc.rel_l2(logits, ref_logits) < 1e-5, orc.rel_l2(logits, ref_logits)
         top2 = np.sort(ref_logits)[-2:]
         if top2[1] - top2[0] > 1e-3 * max(1.0, abs(float(top2[1]))):
@@ -171,11 +209,57 @@ def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill):
         gpu.decode_step_dev(name, xd, prefill + 1, ld, td)
         gpu.sync()
         logits2 = gpu.d2h(ld, (V,), np.float32)
-        ref2, _ = m.cpu_step(orc, x, kc, vc, prefill + 1, theta, eps)
+        ref2, _ = m.cpu_step(orc, x, kc, vc, prefill + 1, theta, eps, kv_f16=bool(kv_f16))
         assert orc.rel_l2(logits2, ref2) < 1e-5
     finally:
-        for p in (xd, ld, td):
+        for p in (xd, ld, td, rd):
             gpu.dev_free(p)
+        gpu.decode_destroy(name)
+        for k in m.keys:
+            gpu.weight_drop(k)
+
+
+def test_kv_upload_rounds_like_soso(gpu, orc):
+    """f32 rows entering an f16 cache take soso's f32_to_f16 bit for bit:
+    ties away from zero, subnormal rounding and flushing, overflow, NaN."""
+    L, H, nh, nkv, F, V, ctx = 1, 256, 2, 1, 256, 64, 64
+    m = Model(orc, L, H, nh, nkv, F, V, 91)
+    m.upload(gpu)
+    name = m.name + ".round"
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=1e4, rms_eps=1e-5, kv_f16=1)
+    gpu.decode_create(name, cfg, m.keys)
+    try:
+        rng = np.random.default_rng(9)
+        special = []
+        for e in range(-26, 17):  # ties and near-ties at every f16 binade, subnormals included
+            step = 2.0 ** max(e - 10, -24)
+            base = 2.0 ** e
+            for k in (0, 1, 3, 511):
+                special += [base + (k + 0.5) * step, base + (k + 0.5) * step * (1 + 2 ** -20),
+                            base + (k + 0.5) * step * (1 - 2 ** -20)]
+        special += [2.0 ** -25, 2.0 ** -26, 3 * 2.0 ** -26, 65504.0, 65519.0, 65520.0, 1e6, np.inf, np.nan, 0.0]
+        vals = np.array(special, np.float64)
+        vals = np.concatenate([vals, -vals]).astype(np.float32)
+        n_rows = -(-vals.size // m.kvd)
+        rows = np.concatenate([vals, rng.standard_normal(n_rows * m.kvd - vals.size).astype(np.float32) * 100])
+        rows = rows.reshape(n_rows, m.kvd)
+        gpu.decode_kv_upload(name, 0, 3, rows, rows[::-1].copy(), rows_f32=True)
+        kd, vd = gpu.decode_kv_dev(name, 0)
+        gk = gpu.d2h(kd, (nkv, ctx, HD), np.uint16)[:, 3:3 + n_rows].transpose(1, 0, 2).reshape(n_rows, m.kvd)
+        gv = gpu.d2h(vd, (nkv, ctx, HD), np.uint16)[:, 3:3 + n_rows].transpose(1, 0, 2).reshape(n_rows, m.kvd)
+        want_k = orc.f32_to_f16(rows).reshape(rows.shape)
+        want_v = orc.f32_to_f16(rows[::-1].copy()).reshape(rows.shape)
+        bad = np.flatnonzero(gk.ravel() != want_k.ravel())
+        assert bad.size == 0, [(float(rows.ravel()[i]), hex(int(gk.ravel()[i])), hex(int(want_k.ravel()[i])))
+                               for i in bad[:6]]
+        assert np.array_equal(gv, want_v)
+        # rows already in f16 go in untouched
+        bits = rng.integers(0, 0x7C00, size=(2, m.kvd), dtype=np.uint16)
+        gpu.decode_kv_upload(name, 0, ctx - 2, bits, bits, rows_f32=False)
+        gk = gpu.d2h(kd, (nkv, ctx, HD), np.uint16)[:, ctx - 2:].transpose(1, 0, 2).reshape(2, m.kvd)
+        assert np.array_equal(gk, bits)
+    finally:
         gpu.decode_destroy(name)
         for k in m.keys:
             gpu.weight_drop(k)

@@ -75,6 +75,60 @@ def test_f32_to_f16_rules(orc):
         assert abs(v - rt) <= abs(v) * 1e-3 + 1e-4
 
 
+def test_f32_to_f16_against_ieee(orc):
+    """soso's rounding differs from IEEE round-to-nearest-even only on exact
+    ties, which it sends away from zero.  numpy's float16 conversion is the
+    IEEE one: every non-tie input must agree with it, every tie must land one
+    step further from zero than the even neighbour when that neighbour is the
+    smaller magnitude.  Inputs cover every f32 exponent that reaches f16
+    (subnormal flushes, the subnormal range, normals, overflow) with random
+    and tie-shaped mantissas."""
+    rng = np.random.default_rng(5)
+    exps = np.arange(90, 150, dtype=np.uint32)  # 2^-37 .. 2^22
+    mant = rng.integers(0, 1 << 23, size=(exps.size, 4000), dtype=np.uint32)
+    # tie-shaped mantissas: the first dropped bit set, the rest zero, at every
+    # shift a normal or subnormal half can have
+    ties = []
+    for sh in range(13, 25):
+        m = rng.integers(0, 1 << 23, size=(exps.size, 50), dtype=np.uint32)
+        keep = ~np.uint32((1 << sh) - 1) & np.uint32(0x7FFFFF)
+        ties.append((m & keep) | np.uint32(1 << (sh - 1)) if sh <= 23 else m * 0)
+    mant = np.concatenate([mant] + ties, axis=1)
+    bits = (exps[:, None] << np.uint32(23)) | mant
+    bits = np.concatenate([bits.ravel(), bits.ravel() | np.uint32(0x80000000)])
+    v = bits.view(np.float32)
+    ours = orc.f32_to_f16(v)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return _check_ties(orc, bits, v, ours)
+
+
+def _check_ties(orc, bits, v, ours):
+    ieee = v.astype(np.float16).view(np.uint16)
+    # exact ties: the input sits halfway between two adjacent halves
+    lo = ieee.view(np.float16).astype(np.float64)
+    nxt = (ieee.astype(np.int32) + 1).astype(np.uint16)
+    prv = (ieee.astype(np.int32) - 1).astype(np.uint16)
+    up = np.abs(nxt.view(np.float16).astype(np.float64))
+    dn = np.abs(prv.view(np.float16).astype(np.float64))
+    a = np.abs(v.astype(np.float64))
+    finite = np.isfinite(ieee.view(np.float16))
+    tie_up = finite & (np.abs(lo) < a) & (2 * a == np.abs(lo) + up)      # even neighbour below: soso goes up
+    tie_dn = finite & (np.abs(lo) > a) & (2 * a == np.abs(lo) + dn)      # even neighbour above: both go up
+    assert tie_up.sum() > 1000  # the tie-shaped inputs are there
+    want = ieee.copy()
+    want[tie_up] = nxt[tie_up]
+    # ties between 0 and the smallest subnormal: numpy gives 0, soso 2^-24
+    zero_tie = (ieee & 0x7FFF) == 0
+    zero_tie &= a == 2.0 ** -25
+    want[zero_tie] = ieee[zero_tie] | 1
+    bad = np.flatnonzero(ours != want)
+    assert bad.size == 0, [(hex(int(bits[i])), hex(int(ours[i])), hex(int(want[i]))) for i in bad[:8]]
+    assert not tie_dn.any() or np.array_equal(ours[tie_dn], ieee[tie_dn])
+    # NaN keeps its sign and becomes 0x7e00; overflow is infinity
+    assert orc.f32_to_f16(np.array([np.nan], np.float32))[0] & 0x7FFF == 0x7E00
+    assert list(orc.f32_to_f16(np.array([65520.0, -1e6], np.float32))) == [0x7C00, 0xFC00]
+
+
 # ---------------------------------------------------------------- layout
 def test_row_bytes_reference_cases(orc):
     for dtype, cols, want in GOLD["row_bytes"]["cases"]:
