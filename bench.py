@@ -124,14 +124,15 @@ def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3):
             g.weight_drop(k)
 
 
-def time_moe(g, n, steps, layers=4, n_x=8, seed=11):
+def time_moe(g, n, steps, layers=4, n_x=8, seed=11, eager=False):
     """Qwen3-30B-A3B-like MoE FFN (hidden 2048, 128 experts of
     intermediate 768, top-8, Q4_K experts, f32 router ~ N(0, 0.02)), `n`
     tokens ~ N(0, 1) per call, routing from the seeded inputs.  `layers`
     independent layers and `n_x` input batches are rotated so that successive
-    calls touch different experts (HBM, not the MALL).  Returns (ms per call,
-    algorithmic bytes per call averaged over the rotation, distinct experts
-    per call)."""
+    calls touch different experts (HBM, not the MALL).  The timed calls replay
+    one HIP graph; eager=True launches them directly (for kernel tracers).
+    Returns (ms per call, algorithmic bytes per call averaged over the
+    rotation, distinct experts per call)."""
     E, H, F, K = 128, 2048, 768, 8
     names = []
     try:
@@ -166,17 +167,26 @@ def time_moe(g, n, steps, layers=4, n_x=8, seed=11):
                     nbytes.append((E * H * 4 + u * per_expert + 2 * n * H * 4, u))
             g.sync()
             combos = layers * n_x
-            gid = _capture(g, lambda: [g.moe_ffn_dev(names[i % layers][0], xs + ((i // layers) % n_x) * n * H * 4,
-                                                     n, out, None, None) for i in range(steps)])
-            try:
-                g.graph_launch(gid)
+            calls = lambda: [g.moe_ffn_dev(names[i % layers][0], xs + ((i // layers) % n_x) * n * H * 4,
+                                           n, out, None, None) for i in range(steps)]
+            if eager:
+                calls()
                 g.sync()
                 g.event_record(0)
-                g.graph_launch(gid)
+                calls()
                 g.event_record(1)
                 g.sync()
-            finally:
-                g.graph_destroy(gid)
+            else:
+                gid = _capture(g, calls)
+                try:
+                    g.graph_launch(gid)
+                    g.sync()
+                    g.event_record(0)
+                    g.graph_launch(gid)
+                    g.event_record(1)
+                    g.sync()
+                finally:
+                    g.graph_destroy(gid)
             ms = g.event_elapsed(0, 1) / steps
             order = [(i % layers) * n_x + (i // layers) % n_x for i in range(steps)]
             b = sum(nbytes[o][0] for o in order) / steps
@@ -463,7 +473,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
     ap.add_argument("--eager", action="store_true",
-                    help="with --only decode: launch the timed steps directly instead of replaying a graph")
+                    help="with --only decode/moe1/moe32: launch the timed steps directly instead of replaying a graph")
     ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head", "matmul"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
@@ -498,7 +508,7 @@ def main():
                    "llama8b_decode_kv_f16_ms_per_token": round(ms_h, 4), "greedy_token_kv_f16": tok_h}
         else:
             n = 1 if args.only == "moe1" else 32
-            ms, _, _, _ = time_moe(g, n, max(40, args.steps // 10))
+            ms, _, _, _ = time_moe(g, n, max(40, args.steps // 10), eager=args.eager)
             res = {f"moe_batch{n}_us_per_layer": round(ms * 1e3, 3)}
         g.close()
         print(json.dumps(res), flush=True)

@@ -186,7 +186,8 @@ int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t
                      size_t top_k, const MoeScratch &s);
 int launch_moe_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab_dev, size_t n_groups,
-                       const float *wgt_dev, const uint8_t *use_dev, const MoeScratch &s, float *out_dev);
+                       const float *wgt_dev, const uint8_t *use_dev, const int32_t *route_idx_dev,
+                       const MoeScratch &s, float *out_dev);
 
 // ---------------------------------------------------------------------------
 // Device helpers

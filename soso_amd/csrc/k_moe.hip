@@ -35,7 +35,7 @@
 // are never chosen -- should fewer than top_k experts remain, the slot points
 // at expert 0 with weight 0 (indices stay valid).  `sel`: top_k floats of LDS.
 __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *__restrict__ idx,
-                          float *__restrict__ wgt, float *sel)
+                          float *__restrict__ wgt, float *sel, int16_t *rank_lds)
 {
     const int lane = threadIdx.x & 63;
     const float m = wave_max_dpp(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])));
@@ -68,6 +68,7 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
         if (lane == 0) {
             idx[j] = bi;
             sel[j] = bv;
+            rank_lds[j] = (int16_t)bi;
         }
     }
     if (lane == 0) {
@@ -77,17 +78,21 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
     }
 }
 
-// grid (ceil(n_exp / waves), ceil(n / ROUTE_TT)); wave w of workgroup
-// (bx, by) owns expert bx*waves + w for tokens by*ROUTE_TT .. + ROUTE_TT - 1.
-// `ticket` is zero between launches (the last workgroup resets it).  The last
-// workgroup also writes the work items of the grouped kernels (about `target`
-// of them, each an equal share of tokens x rows): items[4i .. 4i+3] =
-// {expert, its slot count, its first slot in `list`, chunk j | chunks << 16}
-// for i < *n_items, experts ascending.
+// grid (ceil(n_exp / waves), ceil(n / TT)); wave w of workgroup (bx, by)
+// owns expert bx*waves + w for tokens by*TT .. + TT - 1.  `ticket` is zero
+// between launches (the last workgroup resets it).  The last workgroup also
+// writes the work items of the grouped kernels (about `target` of them, each
+// an equal share of tokens x rows): items[4i .. 4i+3] = {expert, its slot
+// count, its first slot in `list`, chunk j | chunks << 16} for i < *n_items,
+// experts ascending.
 constexpr int ROUTE_MAX_SLOTS = 4096; // n * top_k handled by the LDS sort
-constexpr int ROUTE_TT = 4;           // tokens per wavefront (and per ranking workgroup)
+constexpr int ROUTE_TT = 4;           // tokens per wavefront (and per ranking workgroup) from 2 tokens
 constexpr int ROUTE_T1 = 2048;        // first per-token-block counter in the ticket buffer
 
+// TT tokens per wavefront; each lane requests Q float4 of the expert row (and
+// of every token's x) per step: TT = 1 (one token, the decode case) takes a
+// 2048-wide row in a single round trip.
+template <int TT, int Q>
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
                                                     int32_t *__restrict__ idx, float *__restrict__ wgt,
@@ -101,32 +106,33 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
     __shared__ float sel[8][64];
     __shared__ int c_s[256], o_s[257], f_s[256];
     __shared__ int16_t e_s[ROUTE_MAX_SLOTS];
+    __shared__ int16_t rank_s[ROUTE_TT * 64]; // the ranking of a single token block, for its sort
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int e = blockIdx.x * nw + wave;
-    const int t0 = blockIdx.y * ROUTE_TT, tn = min(ROUTE_TT, n - t0);
+    const int t0 = blockIdx.y * TT, tn = min(TT, n - t0);
     if (e < n_exp) {
-        // this wavefront's expert row against ROUTE_TT tokens: every load of
-        // a 256-float4 step is issued before its products
+        // this wavefront's expert row against TT tokens: every load of a
+        // 64*Q-float4 step is issued before its products
         const float4 *w4 = (const float4 *)(W + (size_t)e * hdim);
         const float4 *x4 = (const float4 *)(xs + (size_t)t0 * hdim);
         const int nv = hdim >> 2;
-        float acc[ROUTE_TT];
+        float acc[TT];
 #pragma unroll
-        for (int tt = 0; tt < ROUTE_TT; tt++) acc[tt] = 0.0f;
-        for (int i0 = 0; i0 < nv; i0 += 64 * 4) {
-            float4 w[4], v[ROUTE_TT][4];
+        for (int tt = 0; tt < TT; tt++) acc[tt] = 0.0f;
+        for (int i0 = 0; i0 < nv; i0 += 64 * Q) {
+            float4 w[Q], v[TT][Q];
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
+            for (int q = 0; q < Q; q++) {
                 const int i = i0 + 64 * q + lane;
                 w[q] = i < nv ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-                for (int tt = 0; tt < ROUTE_TT; tt++)
+                for (int tt = 0; tt < TT; tt++)
                     v[tt][q] = i < nv && tt < tn ? x4[(size_t)tt * nv + i] : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
-            for (int tt = 0; tt < ROUTE_TT; tt++)
+            for (int tt = 0; tt < TT; tt++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
+                for (int q = 0; q < Q; q++) {
                     acc[tt] = fmaf(w[q].x, v[tt][q].x, acc[tt]);
                     acc[tt] = fmaf(w[q].y, v[tt][q].y, acc[tt]);
                     acc[tt] = fmaf(w[q].z, v[tt][q].z, acc[tt]);
@@ -134,7 +140,7 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
                 }
         }
 #pragma unroll
-        for (int tt = 0; tt < ROUTE_TT; tt++) {
+        for (int tt = 0; tt < TT; tt++) {
             const float sum = seg_sum_dpp<64>(acc[tt]); // lane 63 holds it
             if (lane == 63 && tt < tn) logits[(size_t)(t0 + tt) * n_exp + e] = sum;
         }
@@ -142,6 +148,8 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
     // Two-level tickets.  The last workgroup of token block by (counter
     // ticket[ROUTE_T1 + by]) ranks that block's tokens, one per wavefront;
     // the last token block to be ranked (counter ticket[0]) sorts the slots.
+    // With a single token block the ranking workgroup sorts straight away,
+    // from the ranking it kept in LDS.
     // One thread per workgroup fences: a device-scope fence writes back the
     // L2 of its XCD, and the workgroup barrier before it orders every
     // wavefront's stores ahead of it (fences are cumulative).
@@ -162,15 +170,19 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
             const int x = lane + 64 * q;
             lg[q] = x < n_exp ? logits[(size_t)t * n_exp + x] : -INFINITY;
         }
-        topk_regs(lg, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k, sel[wave]);
+        topk_regs(lg, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k, sel[wave],
+                  rank_s + wave * top_k);
     }
+    const bool single = gridDim.y == 1;
     __syncthreads();
     if (threadIdx.x == 0) {
         ticket[ROUTE_T1 + blockIdx.y] = 0u;
-        __threadfence();
-        const bool l = atomicAdd(ticket, 1u) == gridDim.y - 1;
-        if (l) __threadfence();
-        last = l;
+        if (!single) {
+            __threadfence();
+            const bool l = atomicAdd(ticket, 1u) == gridDim.y - 1;
+            if (l) __threadfence();
+            last = l;
+        }
     }
     __syncthreads();
     if (!last) return;
@@ -180,7 +192,7 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
     for (int x = threadIdx.x; x < n_exp; x += blockDim.x) c_s[x] = f_s[x] = 0;
     __syncthreads();
     for (int sl = threadIdx.x; sl < slots; sl += blockDim.x) {
-        const int x = min(max((int)idx[sl], 0), n_exp - 1);
+        const int x = min(max((int)(single ? rank_s[sl] : idx[sl]), 0), n_exp - 1);
         e_s[sl] = (int16_t)x;
         atomicAdd(&c_s[x], 1);
     }
@@ -247,7 +259,7 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
         if (lane == 63) {
             pre_s[n_exp] = incl;
             *n_items = incl;
-            *ticket = 0u;
+            if (!single) *ticket = 0u;
         }
     }
     if (wave == 1) {
@@ -351,6 +363,52 @@ __device__ __forceinline__ void q4k_half(const uint32_t (&codes)[8], const uint3
         for (int k = 0; k < XDIG; k++) s[k] = sdot4(codes[t], xh[XDIG * t + k], s[k]);
 }
 
+// One decoded row unit (pr[m], m < NMAT) against the x staged in LDS at xd
+// (digit planes, then the 16-element sums s16, then the 128-block exponents
+// kx): returns the row's dot in the last lane of each LPR-lane group.
+template <int LPR, int NMAT>
+__device__ __forceinline__ void q4k_token_dot(const Q4Prep (&pr)[NMAT], const uint32_t *xd, int cols, int U, int u,
+                                              bool uact, float (&val)[NMAT])
+{
+    const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
+    const int *kx = (const int *)(s16 + (cols >> 4));
+    const uint4 *x4 = (const uint4 *)xd;
+    int sa[NMAT][XDIG], sb[NMAT][XDIG];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++)
+#pragma unroll
+        for (int k = 0; k < XDIG; k++) sa[m][k] = sb[m][k] = 0;
+    uint32_t xh[24];
+#pragma unroll
+    for (int r = 0; r < 6; r++) {
+        const uint4 v = x4[r * U + u];
+        xh[4 * r] = v.x;
+        xh[4 * r + 1] = v.y;
+        xh[4 * r + 2] = v.z;
+        xh[4 * r + 3] = v.w;
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) q4k_half(pr[m].lo, xh, sa[m]);
+#pragma unroll
+    for (int r = 0; r < 6; r++) {
+        const uint4 v = x4[(r + 6) * U + u];
+        xh[4 * r] = v.x;
+        xh[4 * r + 1] = v.y;
+        xh[4 * r + 2] = v.z;
+        xh[4 * r + 3] = v.w;
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) q4k_half(pr[m].hi, xh, sb[m]);
+    const float P = ldexpf(1.0f, -kx[u >> 1]);
+    const float c0 = s16[4 * u] + s16[4 * u + 1], c1 = s16[4 * u + 2] + s16[4 * u + 3];
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) {
+        const float uu = fmaf(pr[m].ka, digits_value(sa[m]), pr[m].kb * digits_value(sb[m]));
+        const float vv = fmaf(pr[m].kmb, c1, pr[m].kma * c0);
+        val[m] = seg_sum_dpp<LPR>(uact ? fmaf(P, uu, -vv) : 0.0f);
+    }
+}
+
 template <int FMT, int LPR, int NMAT, int DEPTH>
 __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB, size_t stride, int rows,
@@ -443,44 +501,8 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                 const int row = r0 + (j * NW + wave) * RW + slot;
                 for (int tk = 0; tk < nt; tk++) {
                     const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)tk * tok_bytes);
-                    const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
-                    const int *kx = (const int *)(s16 + (cols >> 4));
-                    const uint4 *x4 = (const uint4 *)xd;
-                    int sa[NMAT][XDIG], sb[NMAT][XDIG];
-#pragma unroll
-                    for (int m = 0; m < NMAT; m++)
-#pragma unroll
-                        for (int k = 0; k < XDIG; k++) sa[m][k] = sb[m][k] = 0;
-                    uint32_t xh[24];
-#pragma unroll
-                    for (int r = 0; r < 6; r++) {
-                        const uint4 v = x4[r * U + u];
-                        xh[4 * r] = v.x;
-                        xh[4 * r + 1] = v.y;
-                        xh[4 * r + 2] = v.z;
-                        xh[4 * r + 3] = v.w;
-                    }
-#pragma unroll
-                    for (int m = 0; m < NMAT; m++) q4k_half(pr[m].lo, xh, sa[m]);
-#pragma unroll
-                    for (int r = 0; r < 6; r++) {
-                        const uint4 v = x4[(r + 6) * U + u];
-                        xh[4 * r] = v.x;
-                        xh[4 * r + 1] = v.y;
-                        xh[4 * r + 2] = v.z;
-                        xh[4 * r + 3] = v.w;
-                    }
-#pragma unroll
-                    for (int m = 0; m < NMAT; m++) q4k_half(pr[m].hi, xh, sb[m]);
-                    const float P = ldexpf(1.0f, -kx[u >> 1]);
-                    const float c0 = s16[4 * u] + s16[4 * u + 1], c1 = s16[4 * u + 2] + s16[4 * u + 3];
                     float val[NMAT];
-#pragma unroll
-                    for (int m = 0; m < NMAT; m++) {
-                        const float uu = fmaf(pr[m].ka, digits_value(sa[m]), pr[m].kb * digits_value(sb[m]));
-                        const float vv = fmaf(pr[m].kmb, c1, pr[m].kma * c0);
-                        val[m] = seg_sum_dpp<LPR>(uact ? fmaf(P, uu, -vv) : 0.0f);
-                    }
+                    q4k_token_dot<LPR, NMAT>(pr, xd, cols, U, u, uact, val);
                     float v = val[0];
                     if constexpr (NMAT == 2) v = silu(val[0]) * val[1];
                     if (ul == LPR - 1 && row < rend) out[(size_t)slot_s[tk] * rows + row] = v;
@@ -543,6 +565,94 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
     }
 }
 
+// Down projection and weighted sum in one launch, for calls with a few
+// tokens (about one token per routed expert, where grouping tokens by expert
+// saves no weight reads).  Work item = (token t, block of RW*P rows);
+// wavefront j of the workgroup takes the token's j-th ranked expert: it stages
+// its own act row (slot t*top_k + j) in LDS, streams the block's rows of that
+// expert (all P passes requested at once) and leaves its dots in LDS; then one
+// lane per row forms
+//   out[t*rows + r] = sum_j wgt[t,j] * (down_{e_j} . act[t*top_k + j])[r]
+// with the fmaf of k_moe_combine, j = 0, 1, ... in ranking order (the
+// ranking-order sum of layer.rs:1914-1924).  Q4_K, top_k <= MDC_K.
+constexpr int MDC_K = 8;  // ranked experts per token (one wavefront each)
+constexpr int MDC_XR = 4; // act chunks (8 floats) per lane: cols <= 64 * 8 * MDC_XR
+
+template <int LPR, int P>
+__global__ void __launch_bounds__(512) k_moe_down_comb(const uint8_t *const *__restrict__ tab, size_t stride, int rows,
+                                                       int cols, int n_exp, const float *__restrict__ act,
+                                                       const int32_t *__restrict__ idx, const float *__restrict__ wgt,
+                                                       int n, int top_k, float *__restrict__ out)
+{
+    constexpr int RW = 64 / LPR, RB = RW * P; // rows per item
+    extern __shared__ uint4 smem[];
+    __shared__ float dots[MDC_K][RB];
+    const int tok_bytes = (int)((stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15);
+    const int lane = threadIdx.x & 63;
+    const int j = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); // ranked slot of this wavefront
+    const int U = cols >> 6, nch = cols >> 3;
+    const int ul = lane & (LPR - 1), slot = lane / LPR;
+    const bool uact = ul < U;
+    const int u = uact ? ul : 0;
+    UConst c;
+    unit_setup_w<FMT_Q4K>(u, c);
+    const LaneOff L = lane_offsets<FMT_Q4K>(cols, u, c);
+    uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)j * tok_bytes);
+    float *s16 = (float *)(xd + (cols >> 2) * XDIG);
+    int *kx = (int *)(s16 + (cols >> 4));
+    const bool on = j < top_k;
+    const int blocks = (rows + RB - 1) / RB, items = n * blocks;
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {
+        const int t = it / blocks, r0 = (it % blocks) * RB;
+        const int sl = t * top_k + j;
+        // 1. this wavefront's act row
+        float4 xv0[MDC_XR], xv1[MDC_XR];
+#pragma unroll
+        for (int k = 0; k < MDC_XR; k++) {
+            const int f = 64 * k + lane;
+            xv0[k] = xv1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (on && f < nch) {
+                const float4 *x4 = (const float4 *)(act + (size_t)sl * cols) + 2 * f;
+                xv0[k] = x4[0];
+                xv1[k] = x4[1];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // 2. the block's rows of expert e_j, all passes in flight (rows past
+        // the matrix and idle wavefronts read zeros through the range check)
+        const int e = on ? min(max((int)idx[sl], 0), n_exp - 1) : 0;
+        const rsrc_t rs = make_rsrc(tab[e] + (size_t)r0 * stride, (uint32_t)((size_t)(min(rows, r0 + RB) - r0) * stride));
+        const uint32_t base = on && uact ? (uint32_t)(slot * stride) : 0x80000000u;
+        WRow<FMT_Q4K> w[P];
+#pragma unroll
+        for (int p = 0; p < P; p++) load_row<FMT_Q4K>(rs, base + (uint32_t)(p * RW) * (uint32_t)stride, cols, L, w[p]);
+        __builtin_amdgcn_sched_barrier(0);
+        // 3. act into this wavefront's LDS region (16-chunk blocks: nch % 16 == 0)
+#pragma unroll
+        for (int k = 0; k < MDC_XR; k++)
+            if (64 * k < nch) stage_chunk<FMT_Q4K>(xv0[k], xv1[k], 64 * k + lane, 64 * k + lane < nch, U, xd, s16, kx);
+        __syncthreads();
+        // 4. the dots of this wavefront's rows
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            Q4Prep pr[1];
+            q4k_prep(w[p], c, pr[0]);
+            float val[1];
+            q4k_token_dot<LPR, 1>(pr, xd, cols, U, u, uact, val);
+            if (ul == LPR - 1) dots[j][p * RW + slot] = val[0];
+        }
+        __syncthreads();
+        // 5. the weighted sum in ranking order, one lane per row
+        if ((int)threadIdx.x < RB) {
+            const int r = r0 + (int)threadIdx.x;
+            float acc = 0.0f;
+            for (int q = 0; q < top_k; q++) acc = fmaf(dots[q][threadIdx.x], wgt[(size_t)t * top_k + q], acc);
+            if (r < rows) out[(size_t)t * rows + r] = acc;
+        }
+        __syncthreads(); // dots and the act regions are rewritten by the next item
+    }
+}
+
 // out[t * hdim + i] = sum_j wgt[t*k + j] * y[(t*k + j) * hdim + i] over the
 // slots marked in `use` (all when null), j in ranking order (layer.rs:1914-1924).
 __global__ void k_moe_combine(const float *__restrict__ y, const float *__restrict__ wgt,
@@ -598,10 +708,18 @@ int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size
 {
     if (n * top_k > ROUTE_MAX_SLOTS || n_exp > 256 || (n + ROUTE_TT - 1) / ROUTE_TT > 1024)
         return set_err(h, SOSO_HIP_DECLINED, "moe route: too many slots");
-    const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
-    k_moe_route<<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt,
-                                              s.cnt, s.offs, s.list, s.items, s.n_items, moe_item_target(h), s.recs,
-                                              s.n_recs, h->ticket);
+    if (n == 1) {
+        const dim3 grid((unsigned)((n_exp + 7) / 8), 1u);
+        k_moe_route<1, 8><<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits,
+                                                        s.idx, s.wgt, s.cnt, s.offs, s.list, s.items, s.n_items,
+                                                        moe_item_target(h), s.recs, s.n_recs, h->ticket);
+    } else {
+        const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
+        k_moe_route<ROUTE_TT, 4><<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k,
+                                                               s.logits, s.idx, s.wgt, s.cnt, s.offs, s.list, s.items,
+                                                               s.n_items, moe_item_target(h), s.recs, s.n_recs,
+                                                               h->ticket);
+    }
     return hip_check(h, hipGetLastError(), "moe route launch");
 }
 
@@ -681,9 +799,44 @@ static int launch_moe_mv(soso_hip *h, uint8_t dtype, int nmat, const uint8_t *co
 
 // gate/up + swiglu, down, combine for the slots grouped in s.cnt/offs/list.
 // tab: 3 * n_groups device pointers (gate[], up[], down[]).
+// Down + combine in one launch for few tokens (k_moe_down_comb): at most
+// this many tokens, where the ranked experts of different tokens rarely
+// coincide and reading an expert once per token costs about what grouping saves.
+constexpr size_t MDC_MAX_TOKENS = 4;
+
+static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp, size_t rows, size_t cols,
+                            const float *act, const int32_t *idx, const float *wgt, size_t n, size_t top_k, float *out)
+{
+    const int U = (int)(cols / 64);
+    const int lpr = U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
+    const size_t rw = 64 / lpr;
+    // rows per item: the most passes that still give every CU a workgroup
+    int P = 4;
+    while (P > 1 && n * ((rows + rw * P - 1) / (rw * P)) < (size_t)h->num_cu) P >>= 1;
+    const size_t items = n * ((rows + rw * P - 1) / (rw * P));
+    const size_t lds = ((stage_lds_bytes(cols) + 15) & ~(size_t)15) * MDC_K;
+    const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
+    const unsigned grid = (unsigned)std::min<size_t>(items, 4 * (size_t)h->num_cu);
+    const int ri = (int)rows, ci = (int)cols, ne = (int)n_exp, ni = (int)n, ki = (int)top_k;
+#define MDC_CASE(LP)                                                                                                   \
+    case LP:                                                                                                           \
+        if (P == 4)                                                                                                    \
+            k_moe_down_comb<LP, 4><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, out); \
+        else if (P == 2)                                                                                               \
+            k_moe_down_comb<LP, 2><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, out); \
+        else                                                                                                           \
+            k_moe_down_comb<LP, 1><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, out); \
+        break;
+    switch (lpr) {
+        MDC_CASE(8) MDC_CASE(16) MDC_CASE(32) MDC_CASE(64)
+    }
+#undef MDC_CASE
+    return hip_check(h, hipGetLastError(), "moe down+combine launch");
+}
+
 int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab, size_t n_groups, const float *wgt,
-                       const uint8_t *use, const MoeScratch &s, float *out)
+                       const uint8_t *use, const int32_t *route_idx, const MoeScratch &s, float *out)
 {
     const size_t max_items = moe_max_items(h, n * top_k, n_groups);
     // two or more slots per active expert on average: the matrix-core path
@@ -696,6 +849,12 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
                              s.act);
     else
         rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, max_items, n, xs, (int)top_k, s, s.act);
+    // few tokens with the device's own routing: down and the weighted sum in one launch
+    const size_t Uf = ffn / 64;
+    if (rc == SOSO_HIP_OK && route_idx && !use && n <= MDC_MAX_TOKENS && top_k <= (size_t)MDC_K &&
+        dt_down == SOSO_HIP_DTYPE_Q4_K && ffn % 256 == 0 && Uf >= 4 && Uf <= 8 * MDC_XR &&
+        ((stage_lds_bytes(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds && packed_shape_ok(dt_down, hdim, ffn))
+        return launch_down_comb(h, tab + 2 * n_groups, n_groups, hdim, ffn, s.act, route_idx, wgt, n, top_k, out);
     if (rc == SOSO_HIP_OK) {
         if (many && dt_down == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_down, hdim, ffn))
             rc = launch_mfma_moe(h, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_recs, s.act, 1, s.list, s.recs,

@@ -486,7 +486,7 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
         rc = hip_check(h, hipMemcpyAsync(used, use.data(), slots, hipMemcpyHostToDevice, h->stream), "slots upload");
     if (rc == SOSO_HIP_OK) {
         if (G)
-            rc = launch_moe_experts(h, xd, n, hdim, ffn, top_k, dt_gu, dt_dn, tabd, G, wd, used, ms, sd);
+            rc = launch_moe_experts(h, xd, n, hdim, ffn, top_k, dt_gu, dt_dn, tabd, G, wd, used, nullptr, ms, sd);
         else
             rc = hip_check(h, hipMemsetAsync(sd, 0, n * hdim * 4, h->stream), "zero sum");
     }
@@ -572,7 +572,7 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
     rc = launch_moe_route(h, (const float *)m.router->dev, x_dev, n, m.hdim, m.n_exp, m.top_k, ms);
     if (rc == SOSO_HIP_OK)
         rc = launch_moe_experts(h, x_dev, n, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, ms.wgt,
-                                nullptr, ms, out_dev);
+                                nullptr, ms.idx, ms, out_dev);
     return rc;
 }
 

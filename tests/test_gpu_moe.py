@@ -118,6 +118,9 @@ def test_router_ties_lowest_index_first(gpu, orc):
     (12, 512, 256, 3, 7, Q8),      # Q8_0 down projections (soso's converted Q6_K experts)
     (8, 512, 256, 4, 48, Q4K),     # 24 tokens per expert: three token rounds on the matrix cores
     (6, 512, 256, 3, 16, Q8),      # matrix-core gate/up, dot4 Q8_0 down
+    (20, 512, 512, 6, 4, Q4K),     # 4 tokens, top-6: down and the weighted sum in one launch
+    (10, 256, 1024, 2, 3, Q4K),    # 3 tokens, top-2, wide ffn: down + sum in one launch
+    (24, 512, 256, 8, 5, Q4K),     # 5 tokens: one past the fused launch, grouped down + combine
 ])
 def test_moe_ffn_dev_matches_cpu(gpu, orc, n_exp, h, ffn, top_k, n, dt_down):
     layer = Layer(orc, n_exp, h, ffn, top_k, 40 + n, dt_down)
