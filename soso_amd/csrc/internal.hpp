@@ -56,6 +56,12 @@ struct MoeLayer {
     uint8_t dt_gu = 0, dt_down = 0;
     const uint8_t **tab = nullptr; // device: gate[n_exp], up[n_exp], down[n_exp]
     std::vector<const void *> host_tab; // the same pointers, for unregistering on weight_drop
+    // tile-major copies of the Q4_K experts for the matrix-core path (k_mfma.hip),
+    // laid out like `tab`; tiled_gu / tiled_down say which roles have them
+    const uint8_t **tiled = nullptr;
+    void *tiled_mem = nullptr;
+    size_t tiled_bytes = 0;
+    bool tiled_gu = false, tiled_down = false;
 };
 
 // A dense decode model registered for the device-resident step (k_decode.hip).
@@ -177,7 +183,10 @@ int moe_item_target(const soso_hip *h);
 bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols);
 int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_t *const *B, size_t rows, size_t cols,
                     size_t max_recs, const float *xs, int xdiv, const int *list, const int *recs, const int *n_recs,
-                    float *out);
+                    float *out, bool tiled);
+// tile-major Q4_K copies (same size as the row-major packing) for launch_mfma_moe
+bool tiled_q4k_ok(uint8_t dtype, size_t rows, size_t cols);
+int launch_tile_q4k(soso_hip *h, const void *src_dev, void *dst_dev, size_t rows, size_t cols);
 int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y);
 size_t moe_max_items(const soso_hip *h, size_t slots, size_t n_groups);
 int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim,
@@ -187,7 +196,7 @@ int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t
 int launch_moe_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab_dev, size_t n_groups,
                        const float *wgt_dev, const uint8_t *use_dev, const int32_t *route_idx_dev,
-                       const MoeScratch &s, float *out_dev);
+                       const MoeScratch &s, float *out_dev, const MoeLayer *layer = nullptr);
 
 // ---------------------------------------------------------------------------
 // Device helpers

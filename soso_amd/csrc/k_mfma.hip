@@ -63,6 +63,67 @@ __device__ __forceinline__ void mf_load_sb(rsrc_t r, uint32_t rowoff, uint32_t q
     for (int p = 0; p < 4; p++) s.q[p] = bld8(r, rowoff + qoff + 16u * (uint32_t)(4 * sb + p));
 }
 
+// Tile-major Q4_K (the registered MoE experts' copy for this kernel).  In the
+// row-major packing a wavefront's 16 rows x one super-block are 48 pieces of
+// 16-64 bytes spread over 16 rows (measured on MI355X: ~2.7 TB/s for that
+// pattern, 5.7 TB/s for the same bytes read contiguously).  Here the rows of a
+// 16-row tile are stored super-block by super-block, each block of 2304 bytes
+// already in the order the lanes consume it:
+//   [0, 256)     the 16 rows' 16-byte headers, row n at 16 n
+//   [256, 1280)  lane l = 16 g + n: its pieces of units 0 and 1
+//   [1280, 2304) lane l: its pieces of units 2 and 3
+// where lane (n, g)'s piece of unit p is bytes 8g .. 8g + 7 of the unit's 32
+// code bytes in row n (what mf_load_sb reads into q[p]).  A tile takes as many
+// bytes as its 16 rows (nb * 2304 = 16 * row stride), so tile t starts where
+// row 16 t would.  Every load below is contiguous across the wavefront.
+constexpr int MF_TBLK = 2304; // bytes per (tile, super-block)
+__device__ __forceinline__ void mf_load_sb_tiled(rsrc_t r, uint32_t tileoff, int nl, int lane, int sb, bool in,
+                                                 MfSb &s)
+{
+    const uint32_t b = (in ? tileoff : 0x80000000u) + (uint32_t)MF_TBLK * (uint32_t)sb;
+    s.h = bld16(r, b + 16u * (uint32_t)nl);
+    const uint4 a = bld16(r, b + 256u + 16u * (uint32_t)lane);
+    const uint4 c = bld16(r, b + 1280u + 16u * (uint32_t)lane);
+    s.q[0] = make_uint2(a.x, a.y);
+    s.q[1] = make_uint2(a.z, a.w);
+    s.q[2] = make_uint2(c.x, c.y);
+    s.q[3] = make_uint2(c.z, c.w);
+}
+
+// Row-major packed Q4_K -> tile-major (rows % 16 == 0): thread (tile,
+// super-block, lane).
+__global__ void tile_q4k(const uint8_t *__restrict__ src, uint8_t *__restrict__ dst, int tiles, int nb)
+{
+    const long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (long)tiles * nb * 64) return;
+    const int lane = (int)(t & 63), sb = (int)((t >> 6) % nb), tile = (int)((t >> 6) / nb);
+    const int n = lane & 15, g = lane >> 4, U = 4 * nb;
+    const size_t stride = (size_t)nb * 144;
+    const uint8_t *row = src + ((size_t)tile * 16 + n) * stride;
+    uint8_t *blk = dst + ((size_t)tile * nb + sb) * MF_TBLK;
+    if (g == 0) *(uint4 *)(blk + 16 * n) = *(const uint4 *)(row + 16 * sb);
+    // piece of unit p: bytes 8g .. 8g+7 of its 32 code bytes (QA: 0..15, QB: 16..31)
+    uint2 pc[4];
+#pragma unroll
+    for (int p = 0; p < 4; p++)
+        pc[p] = *(const uint2 *)(row + 16 * nb + (g < 2 ? 0 : 16 * U) + 16 * (4 * sb + p) + 8 * (g & 1));
+    *(uint4 *)(blk + 256 + 16 * lane) = make_uint4(pc[0].x, pc[0].y, pc[1].x, pc[1].y);
+    *(uint4 *)(blk + 1280 + 16 * lane) = make_uint4(pc[2].x, pc[2].y, pc[3].x, pc[3].y);
+}
+
+bool tiled_q4k_ok(uint8_t dtype, size_t rows, size_t cols)
+{
+    return dtype == SOSO_HIP_DTYPE_Q4_K && rows % 16 == 0 && cols % 256 == 0 && cols >= 256;
+}
+
+int launch_tile_q4k(soso_hip *h, const void *src, void *dst, size_t rows, size_t cols)
+{
+    const size_t tiles = rows / 16, nb = cols / 256, n = tiles * nb * 64;
+    tile_q4k<<<(unsigned)((n + 255) / 256), 256, 0, h->stream>>>((const uint8_t *)src, (uint8_t *)dst, (int)tiles,
+                                                                   (int)nb);
+    return hip_check(h, hipGetLastError(), "tile q4k launch");
+}
+
 // The scales of a super-block's 8 sub-blocks (get_scale_min_k4,
 // dequant.rs:150-159), four per dword: sc[j] = byte j of sc4[j / 4], same for m.
 struct MfScale {
@@ -87,7 +148,7 @@ __device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (
 // (MoE), or dense_n > 0 tokens of one dense product (slot = token).  Item:
 // blockIdx.x = a * nblk + row block (MoE), or row block + nblk * token round
 // (dense).  Slot s reads x = xs + (s / xdiv) * cols and writes out[s * rows + r].
-template <int NMAT, int MT, int LA>
+template <int NMAT, int MT, int LA, bool TILED = false>
 __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB,
                                                   const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
@@ -122,7 +183,8 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
     const uint8_t *WA = dense_n > 0 ? W0 : tabA[e];
     const uint8_t *WB = NMAT == 2 ? tabB[e] : WA;
     const int nl = lane & 15, g = lane >> 4;
-    const uint32_t rowoff = (uint32_t)((16 * wave + nl) * stride); // past the strip: zeros
+    // row-major: this lane's row; tiled: the wavefront's tile (past the strip: zeros)
+    const uint32_t rowoff = (uint32_t)((16 * wave + (TILED ? 0 : nl)) * stride);
     const int nb = cols >> 8, U = cols >> 6;
     const uint32_t qoff = (uint32_t)(16 * nb + (g < 2 ? 0 : 16 * U) + 8 * (g & 1));
     // A operand of this lane: token (nl / 4) of a tile, digit nl % 4, bytes 8g .. 8g + 7
@@ -148,9 +210,13 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
             const int sb0 = k0 >> 8;
             // the chunk's first weights are requested before x is staged, so
             // their latency overlaps the staging (loads return in issue order)
+            auto load_sb = [&](rsrc_t r, int sb, bool in, MfSb &out) {
+                if constexpr (TILED) mf_load_sb_tiled(r, rowoff, nl, lane, sb, in, out);
+                else mf_load_sb(r, rowoff, qoff, sb, in, out);
+            };
             MfSb ca, cb;
-            mf_load_sb(rA, rowoff, qoff, sb0, true, ca);
-            if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0, true, cb);
+            load_sb(rA, sb0, true, ca);
+            if constexpr (NMAT == 2) load_sb(rB, sb0, true, cb);
             __builtin_amdgcn_sched_barrier(0);
             // ---- stage x (columns k0 .. k0 + kc of the round's tokens) ----
             const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
@@ -299,12 +365,12 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
             MfSb pa[LA], pb[LA];
 #pragma unroll
             for (int k = 0; k < LA - 1; k++) {
-                mf_load_sb(rA, rowoff, qoff, sb0 + 1 + k, 1 + k < nsb, pa[k]);
-                if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0 + 1 + k, 1 + k < nsb, pb[k]);
+                load_sb(rA, sb0 + 1 + k, 1 + k < nsb, pa[k]);
+                if constexpr (NMAT == 2) load_sb(rB, sb0 + 1 + k, 1 + k < nsb, pb[k]);
             }
             for (int i = 0; i < nsb; i++) {
-                mf_load_sb(rA, rowoff, qoff, sb0 + i + LA, i + LA < nsb, pa[LA - 1]);
-                if constexpr (NMAT == 2) mf_load_sb(rB, rowoff, qoff, sb0 + i + LA, i + LA < nsb, pb[LA - 1]);
+                load_sb(rA, sb0 + i + LA, i + LA < nsb, pa[LA - 1]);
+                if constexpr (NMAT == 2) load_sb(rB, sb0 + i + LA, i + LA < nsb, pb[LA - 1]);
                 __builtin_amdgcn_sched_barrier(0);
                 superblock(8 * i, ca, cb);
                 ca = pa[0];
@@ -351,21 +417,29 @@ bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols)
 // MoE: one grouped product over the active-expert records (device).
 int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_t *const *B, size_t rows, size_t cols,
                     size_t max_recs, const float *xs, int xdiv, const int *list, const int *recs, const int *n_recs,
-                    float *out)
+                    float *out, bool tiled)
 {
-    if (!mfma_shape_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols)) return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
+    if (!mfma_shape_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols) || (tiled && !tiled_q4k_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols)))
+        return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
     constexpr int MT = 2;
     const int kc = mf_kc(h, cols, 4 * MT);
     const size_t nblk = (rows + MF_ROWS - 1) / MF_ROWS;
     const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
     const unsigned grid = (unsigned)(max_recs * nblk);
     const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
-    if (nmat == 2)
-        k_mfma_q4k<2, MT, MF_LA2><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, (int)rows, (int)cols, xs, xdiv,
-                                                                list, recs, n_recs, 0, kc, out);
+    const int ri = (int)rows, ci = (int)cols;
+    if (nmat == 2 && tiled)
+        k_mfma_q4k<2, MT, MF_LA2, true><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, ri, ci, xs, xdiv,
+                                                                              list, recs, n_recs, 0, kc, out);
+    else if (nmat == 2)
+        k_mfma_q4k<2, MT, MF_LA2><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, ri, ci, xs, xdiv, list,
+                                                                        recs, n_recs, 0, kc, out);
+    else if (tiled)
+        k_mfma_q4k<1, MT, MF_LA1, true><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, ri, ci, xs,
+                                                                              xdiv, list, recs, n_recs, 0, kc, out);
     else
-        k_mfma_q4k<1, MT, MF_LA1><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, (int)rows, (int)cols, xs,
-                                                                xdiv, list, recs, n_recs, 0, kc, out);
+        k_mfma_q4k<1, MT, MF_LA1><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, ri, ci, xs, xdiv,
+                                                                        list, recs, n_recs, 0, kc, out);
     return hip_check(h, hipGetLastError(), "mfma moe launch");
 }
 

@@ -836,7 +836,8 @@ static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp
 
 int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab, size_t n_groups, const float *wgt,
-                       const uint8_t *use, const int32_t *route_idx, const MoeScratch &s, float *out)
+                       const uint8_t *use, const int32_t *route_idx, const MoeScratch &s, float *out,
+                       const MoeLayer *layer)
 {
     const size_t max_items = moe_max_items(h, n * top_k, n_groups);
     // two or more slots per active expert on average: the matrix-core path
@@ -844,9 +845,12 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
     const size_t slots = n * top_k, max_recs = std::min(n_groups, slots);
     const bool many = slots >= 2 * max_recs;
     int rc;
+    // a registered layer's tile-major copies, where it has them
+    const bool tgu = layer && layer->tiled && layer->tiled_gu, tdn = layer && layer->tiled && layer->tiled_down;
+    const uint8_t *const *ttab = layer ? layer->tiled : nullptr;
     if (many && dt_gu == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_gu, ffn, hdim))
-        rc = launch_mfma_moe(h, 2, tab, tab + n_groups, ffn, hdim, max_recs, xs, (int)top_k, s.list, s.recs, s.n_recs,
-                             s.act);
+        rc = launch_mfma_moe(h, 2, tgu ? ttab : tab, (tgu ? ttab : tab) + n_groups, ffn, hdim, max_recs, xs, (int)top_k,
+                             s.list, s.recs, s.n_recs, s.act, tgu);
     else
         rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, max_items, n, xs, (int)top_k, s, s.act);
     // few tokens with the device's own routing: down and the weighted sum in one launch
@@ -857,8 +861,8 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
         return launch_down_comb(h, tab + 2 * n_groups, n_groups, hdim, ffn, s.act, route_idx, wgt, n, top_k, out);
     if (rc == SOSO_HIP_OK) {
         if (many && dt_down == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_down, hdim, ffn))
-            rc = launch_mfma_moe(h, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_recs, s.act, 1, s.list, s.recs,
-                                 s.n_recs, s.ydown);
+            rc = launch_mfma_moe(h, 1, (tdn ? ttab : tab) + 2 * n_groups, nullptr, hdim, ffn, max_recs, s.act, 1, s.list,
+                                 s.recs, s.n_recs, s.ydown, tdn);
         else
             rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_items, n, s.act, 1, s,
                                s.ydown);

@@ -151,6 +151,20 @@ Weight *find_weight(soso_hip *h, const char *key, size_t key_len)
     return &it->second;
 }
 
+void moe_free(soso_hip *h, MoeLayer &m)
+{
+    hipStreamSynchronize(h->stream);
+    if (m.tab) hipFree(m.tab);
+    if (m.tiled) hipFree(m.tiled);
+    if (m.tiled_mem) {
+        hipFree(m.tiled_mem);
+        h->used -= m.tiled_bytes;
+    }
+    m.tab = m.tiled = nullptr;
+    m.tiled_mem = nullptr;
+    m.tiled_bytes = 0;
+}
+
 void decode_free(soso_hip *h, DecodeModel &m)
 {
     hipStreamSynchronize(h->stream);
@@ -213,7 +227,7 @@ void soso_hip_destroy(soso_hip *h)
     for (auto &kv : h->f32_tensors) hipFree(kv.second);
     for (int i = 0; i < soso_hip::N_SCRATCH; i++)
         if (h->scratch[i]) hipFree(h->scratch[i]);
-    for (auto &kv : h->moe_layers) hipFree(kv.second.tab);
+    for (auto &kv : h->moe_layers) moe_free(h, kv.second);
     for (auto &kv : h->decode_models) decode_free(h, kv.second);
     if (h->ticket) hipFree(h->ticket);
     for (hipEvent_t e : h->events)
@@ -539,15 +553,44 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
     if (hipMalloc((void **)&m.tab, tab.size() * sizeof(void *)) != hipSuccess)
         return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_register: table");
     rc = hip_check(h, hipMemcpy(m.tab, tab.data(), tab.size() * sizeof(void *), hipMemcpyHostToDevice), "table upload");
+    // Tile-major copies of the Q4_K experts for the matrix-core path (the
+    // row-major ones stay for the single-token kernels); skipped, with the
+    // row-major matrix-core path as fallback, when the budget has no room.
+    const bool tgu = m.dt_gu == SOSO_HIP_DTYPE_Q4_K && tiled_q4k_ok(m.dt_gu, ffn, hdim);
+    const bool tdn = m.dt_down == SOSO_HIP_DTYPE_Q4_K && tiled_q4k_ok(m.dt_down, hdim, ffn);
+    const size_t b_gu = ffn * packed_row_stride(SOSO_HIP_DTYPE_Q4_K, hdim);
+    const size_t b_dn = hdim * packed_row_stride(SOSO_HIP_DTYPE_Q4_K, ffn);
+    const size_t tbytes = n_exp * ((tgu ? 2 * b_gu : 0) + (tdn ? b_dn : 0));
+    if (rc == SOSO_HIP_OK && tbytes > 0 && h->used + tbytes <= h->budget &&
+        hipMalloc(&m.tiled_mem, tbytes) == hipSuccess) {
+        h->used += tbytes;
+        m.tiled_bytes = tbytes;
+        std::vector<const uint8_t *> tt(3 * n_exp, nullptr);
+        uint8_t *p = (uint8_t *)m.tiled_mem;
+        for (size_t e = 0; e < n_exp && rc == SOSO_HIP_OK; e++)
+            for (int k = 0; k < 3 && rc == SOSO_HIP_OK; k++) {
+                if (k < 2 ? !tgu : !tdn) continue;
+                rc = launch_tile_q4k(h, tab[k * n_exp + e], p, dims[k][0], dims[k][1]);
+                tt[k * n_exp + e] = p;
+                p += k < 2 ? b_gu : b_dn;
+            }
+        if (rc == SOSO_HIP_OK && hipMalloc((void **)&m.tiled, tt.size() * sizeof(void *)) != hipSuccess)
+            rc = set_err(h, SOSO_HIP_ERR_NOMEM, "moe_register: tiled table");
+        if (rc == SOSO_HIP_OK)
+            rc = hip_check(h, hipMemcpyAsync(m.tiled, tt.data(), tt.size() * sizeof(void *), hipMemcpyHostToDevice,
+                                             h->stream), "tiled table upload");
+        if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "tiled copies");
+        m.tiled_gu = tgu;
+        m.tiled_down = tdn;
+    }
     if (rc != SOSO_HIP_OK) {
-        hipFree(m.tab);
+        moe_free(h, m);
         return rc;
     }
     std::string k(layer_key, layer_key_len);
     auto it = h->moe_layers.find(k);
     if (it != h->moe_layers.end()) {
-        hipDeviceSynchronize();
-        hipFree(it->second.tab);
+        moe_free(h, it->second);
         h->moe_layers.erase(it);
     }
     h->moe_layers.emplace(k, m);
@@ -572,7 +615,7 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
     rc = launch_moe_route(h, (const float *)m.router->dev, x_dev, n, m.hdim, m.n_exp, m.top_k, ms);
     if (rc == SOSO_HIP_OK)
         rc = launch_moe_experts(h, x_dev, n, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, ms.wgt,
-                                nullptr, ms.idx, ms, out_dev);
+                                nullptr, ms.idx, ms, out_dev, &m);
     return rc;
 }
 
@@ -892,7 +935,7 @@ int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
         bool uses = m->second.router == &it->second;
         for (const void *p : m->second.host_tab) uses = uses || (p && p == it->second.dev);
         if (uses) {
-            hipFree(m->second.tab);
+            moe_free(h, m->second);
             m = h->moe_layers.erase(m);
         } else {
             ++m;
