@@ -172,11 +172,14 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
     } else {
         const int a = blockIdx.x / nblk;
         b = blockIdx.x % nblk;
-        if (a >= *n_recs) return; // fewer active experts than the grid allows
+        // the record and the count are requested together (the grid holds at
+        // most as many records as `recs` has room for, so the read is in
+        // bounds; `recs` is only int-aligned)
         const int *rec = recs + 4 * a;
         e = rec[0];
         ne = rec[1];
         base = rec[2];
+        if (a >= *n_recs) return; // fewer active experts than the grid allows
         t_first = 0;
         t_step = TR;
     }
