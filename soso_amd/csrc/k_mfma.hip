@@ -39,7 +39,10 @@ constexpr int MF_NW = 4;            // wavefronts per workgroup
 // (gate+up, single matrix).  Measured on MI355X at batch 32: one
 // is fastest -- 136 us per layer; 2 / 3 ahead gave 144 us.
 constexpr int MF_LA2 = 1, MF_LA1 = 1;
-constexpr int MF_ROWS = 16 * MF_NW; // rows per workgroup (16 per wavefront)
+constexpr int MF_ROWS = 16 * MF_NW; // rows per MoE workgroup (16 per wavefront)
+// Dense matmul workgroups: more rows per workgroup share each staging of x
+// (the round's tokens converted into LDS), which is what bounds that kernel.
+constexpr int MF_NW_DENSE = 8;
 
 // LDS per token for kc staged columns: digits [sub-block][3][32 B], then the
 // f32 sums of x per sub-block, then 2^-e per super-block.
@@ -148,8 +151,8 @@ __device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (
 // (MoE), or dense_n > 0 tokens of one dense product (slot = token).  Item:
 // blockIdx.x = a * nblk + row block (MoE), or row block + nblk * token round
 // (dense).  Slot s reads x = xs + (s / xdiv) * cols and writes out[s * rows + r].
-template <int NMAT, int MT, int LA, bool TILED = false>
-__global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
+template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW>
+__global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB,
                                                   const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
                                                   const float *__restrict__ xs, int xdiv, const int *__restrict__ list,
@@ -162,7 +165,8 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
     __shared__ int slot_s[TR];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int nblk = (rows + MF_ROWS - 1) / MF_ROWS;
+    constexpr int ROWS = 16 * NW; // rows per workgroup
+    const int nblk = (rows + ROWS - 1) / ROWS;
     int e = 0, ne, base = 0, b, t_first, t_step;
     if (dense_n > 0) {
         b = blockIdx.x % nblk;
@@ -198,7 +202,7 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
         __syncthreads(); // the previous round's readers of slot_s and LDS are done
         if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = list ? list[base + t0 + threadIdx.x] : base + t0 + threadIdx.x;
         __syncthreads();
-        const int r0 = b * MF_ROWS, rend = min(rows, r0 + MF_ROWS);
+        const int r0 = b * ROWS, rend = min(rows, r0 + ROWS);
         const uint32_t strip = (uint32_t)((size_t)(rend - r0) * stride);
         const rsrc_t rA = make_rsrc(WA + (size_t)r0 * stride, strip);
         const rsrc_t rB = make_rsrc(WB + (size_t)r0 * stride, strip);
@@ -224,8 +228,8 @@ __global__ void __launch_bounds__(64 * MF_NW) k_mfma_q4k(const uint8_t *const *_
             // ---- stage x (columns k0 .. k0 + kc of the round's tokens) ----
             const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
             // four chunks per thread are requested together, then converted
-            // (one L2 round trip per 4 * 64 * MF_NW chunks)
-            constexpr int NT = 64 * MF_NW, XB = 4;
+            // (one L2 round trip per 4 * 64 * NW chunks)
+            constexpr int NT = 64 * NW, XB = 4;
             for (int fb = 0; fb < tot; fb += XB * NT) {
                 float4 v0[XB], v1[XB];
 #pragma unroll
@@ -414,7 +418,7 @@ static int mf_kc(const soso_hip *h, size_t cols, int tokens)
 bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols)
 {
     return dtype == SOSO_HIP_DTYPE_Q4_K && cols % 256 == 0 && cols >= 256 && rows > 0 &&
-           (size_t)MF_ROWS * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
+           (size_t)16 * MF_NW_DENSE * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
 }
 
 // MoE: one grouped product over the active-expert records (device).
@@ -453,11 +457,11 @@ int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, f
     if (!mfma_shape_ok(w.dtype, w.rows, w.cols) || n == 0 || n > (1u << 20))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
     constexpr int MT = 4;
-    const size_t nblk = (w.rows + MF_ROWS - 1) / MF_ROWS, rounds = (n + 4 * MT - 1) / (4 * MT);
+    const size_t nblk = (w.rows + 16 * MF_NW_DENSE - 1) / (16 * MF_NW_DENSE), rounds = (n + 4 * MT - 1) / (4 * MT);
     const int kc = mf_kc(h, w.cols, 4 * MT);
     const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
     const unsigned grid = (unsigned)(nblk * rounds);
-    k_mfma_q4k<1, MT, MF_LA1><<<grid, 64 * MF_NW, lds, h->stream>>>(nullptr, nullptr, (const uint8_t *)w.dev,
+    k_mfma_q4k<1, MT, MF_LA1, false, MF_NW_DENSE><<<grid, 64 * MF_NW_DENSE, lds, h->stream>>>(nullptr, nullptr, (const uint8_t *)w.dev,
                                                             packed_row_stride(w.dtype, w.cols), (int)w.rows,
                                                             (int)w.cols, x, 1, nullptr, nullptr, nullptr, (int)n, kc, y);
     return hip_check(h, hipGetLastError(), "mfma matmul launch");
