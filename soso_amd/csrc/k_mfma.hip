@@ -40,9 +40,16 @@ constexpr int MF_NW = 4;            // wavefronts per workgroup
 // is fastest -- 136 us per layer; 2 / 3 ahead gave 144 us.
 constexpr int MF_LA2 = 1, MF_LA1 = 1;
 constexpr int MF_ROWS = 16 * MF_NW; // rows per MoE workgroup (16 per wavefront)
-// Dense matmul workgroups: more rows per workgroup share each staging of x
-// (the round's tokens converted into LDS), which is what bounds that kernel.
-constexpr int MF_NW_DENSE = 8;
+// Dense matmul workgroups of 4, 8 or 16 wavefronts: more rows per workgroup
+// share each staging of x (the round's tokens converted into LDS), which
+// bounds that kernel, but a workgroup's own chain (staging, then its rows'
+// super-blocks) sets the time once the grid is a single round.  Measured on
+// MI355X (us, 14336x4096 / 4096x4096 at 16, 32, 64 tokens):
+//   4 wavefronts: 48.9 93.6 183.3 / 46.8 47.1 47.9
+//   8 wavefronts: 50.1 52.4  98.0 / 47.9 48.4 49.9
+//  16 wavefronts: 70.3 71.4  74.4 / 68.9 69.1 68.9
+// so the widest workgroup that still gives the grid about one per CU wins.
+constexpr int MF_NW_MAX = 16;
 
 // LDS per token for kc staged columns: digits [sub-block][3][32 B], then the
 // f32 sums of x per sub-block, then 2^-e per super-block.
@@ -418,7 +425,7 @@ static int mf_kc(const soso_hip *h, size_t cols, int tokens)
 bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols)
 {
     return dtype == SOSO_HIP_DTYPE_Q4_K && cols % 256 == 0 && cols >= 256 && rows > 0 &&
-           (size_t)16 * MF_NW_DENSE * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
+           (size_t)16 * MF_NW_MAX * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
 }
 
 // MoE: one grouped product over the active-expert records (device).
@@ -457,12 +464,24 @@ int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, f
     if (!mfma_shape_ok(w.dtype, w.rows, w.cols) || n == 0 || n > (1u << 20))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
     constexpr int MT = 4;
-    const size_t nblk = (w.rows + 16 * MF_NW_DENSE - 1) / (16 * MF_NW_DENSE), rounds = (n + 4 * MT - 1) / (4 * MT);
+    const size_t rounds = (n + 4 * MT - 1) / (4 * MT);
+    auto groups = [&](int nw) { return (w.rows + 16 * nw - 1) / (16 * nw) * rounds; };
+    const size_t want = (size_t)h->num_cu * 7 / 8;
+    const int nw = groups(16) >= want ? 16 : groups(8) >= want ? 8 : 4;
     const int kc = mf_kc(h, w.cols, 4 * MT);
     const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
-    const unsigned grid = (unsigned)(nblk * rounds);
-    k_mfma_q4k<1, MT, MF_LA1, false, MF_NW_DENSE><<<grid, 64 * MF_NW_DENSE, lds, h->stream>>>(nullptr, nullptr, (const uint8_t *)w.dev,
-                                                            packed_row_stride(w.dtype, w.cols), (int)w.rows,
-                                                            (int)w.cols, x, 1, nullptr, nullptr, nullptr, (int)n, kc, y);
+    const unsigned grid = (unsigned)groups(nw);
+    const size_t stride = packed_row_stride(w.dtype, w.cols);
+    const uint8_t *W = (const uint8_t *)w.dev;
+    const int ri = (int)w.rows, ci = (int)w.cols, ni = (int)n;
+    if (nw == 16)
+        k_mfma_q4k<1, MT, MF_LA1, false, 16><<<grid, 1024, lds, h->stream>>>(nullptr, nullptr, W, stride, ri, ci, x, 1,
+                                                                            nullptr, nullptr, nullptr, ni, kc, y);
+    else if (nw == 8)
+        k_mfma_q4k<1, MT, MF_LA1, false, 8><<<grid, 512, lds, h->stream>>>(nullptr, nullptr, W, stride, ri, ci, x, 1,
+                                                                          nullptr, nullptr, nullptr, ni, kc, y);
+    else
+        k_mfma_q4k<1, MT, MF_LA1, false, 4><<<grid, 256, lds, h->stream>>>(nullptr, nullptr, W, stride, ri, ci, x, 1,
+                                                                          nullptr, nullptr, nullptr, ni, kc, y);
     return hip_check(h, hipGetLastError(), "mfma matmul launch");
 }
