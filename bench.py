@@ -91,10 +91,11 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
             g.weight_drop(k)
 
 
-def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3):
+def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False):
     """Q4_K matmul Y[n x rows] = X[n x cols] . W^T (GpuDispatch::matmul) with
     n tokens on the matrix cores; `copies` rotating weights.  Returns ms per
-    call (HIP events around a graph of back-to-back calls)."""
+    call (HIP events around a graph of back-to-back calls; eager=True launches
+    them directly, for kernel tracers)."""
     keys = [f"bench.mm.{rows}x{cols}.{i}" for i in range(copies)]
     for i, k in enumerate(keys):
         g.weight_synth(k, Q4K, rows, cols, seed, 3000 + i)
@@ -105,16 +106,23 @@ def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3):
         for i in range(warmup):
             g.matmul_dev(keys[i % copies], n, x, y)
         g.sync()
-        gid = _capture(g, lambda: [g.matmul_dev(keys[i % copies], n, x, y) for i in range(steps)])
-        try:
-            g.graph_launch(gid)
-            g.sync()
+        calls = lambda: [g.matmul_dev(keys[i % copies], n, x, y) for i in range(steps)]
+        if eager:
             g.event_record(0)
-            g.graph_launch(gid)
+            calls()
             g.event_record(1)
             g.sync()
-        finally:
-            g.graph_destroy(gid)
+        else:
+            gid = _capture(g, calls)
+            try:
+                g.graph_launch(gid)
+                g.sync()
+                g.event_record(0)
+                g.graph_launch(gid)
+                g.event_record(1)
+                g.sync()
+            finally:
+                g.graph_destroy(gid)
         return g.event_elapsed(0, 1) / steps
     finally:
         g.sync()
@@ -473,7 +481,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
     ap.add_argument("--eager", action="store_true",
-                    help="with --only decode/moe1/moe32: launch the timed steps directly instead of replaying a graph")
+                    help="with --only decode/moe1/moe32/matmul: launch the timed steps directly instead of replaying a graph")
     ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head", "matmul"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
@@ -497,7 +505,7 @@ def main():
             ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10))
             res = {"q6_k_head_128256x4096_us": round(ms * 1e3, 3)}
         elif args.only == "matmul":
-            ms = time_matmul(g, 14336, 4096, 64, 16, max(20, args.steps // 10), min(args.warmup, 10))
+            ms = time_matmul(g, 14336, 4096, 64, 16, max(20, args.steps // 10), min(args.warmup, 10), eager=args.eager)
             res = {"q4_k_matmul_14336x4096_n64_us": round(ms * 1e3, 3)}
         elif args.only == "decode":
             print("decode: f32 KV", file=sys.stderr, flush=True)

@@ -457,31 +457,40 @@ int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_
     return hip_check(h, hipGetLastError(), "mfma moe launch");
 }
 
-// Dense: Y[n x rows] = X[n x cols] . W^T, one workgroup per (128-row block,
-// round of 16 tokens).
+template <int NW, int MT>
+static void mfma_dense(soso_hip *h, const Weight &w, const float *x, size_t n, float *y, int kc, unsigned grid)
+{
+    k_mfma_q4k<1, MT, MF_LA1, false, NW><<<grid, 64 * NW, (size_t)4 * MT * mf_tok_bytes(kc), h->stream>>>(
+        nullptr, nullptr, (const uint8_t *)w.dev, packed_row_stride(w.dtype, w.cols), (int)w.rows, (int)w.cols, x, 1,
+        nullptr, nullptr, nullptr, (int)n, kc, y);
+}
+
+// Dense: Y[n x rows] = X[n x cols] . W^T.  The grid is (row block of 16 NW
+// rows) x (round of 4 MT tokens).  Widest workgroups first (16 or 8
+// wavefronts, 4-tile rounds) when they still give about one per CU; else
+// 4 wavefronts with the largest token round that gives as many workgroups and
+// stages each round's x in at most 4 column chunks, or 1-tile rounds.
+// Measured on MI355X (us; 4 wavefronts, tiles per round 4 / 2 / 1):
+//   4096 x 4096,  16 tokens: 46.9 / 27.5 / 16.1;   64 tokens: 48.3 / 55.0 / 46.9
+//   4096 x 14336, 16 tokens: 242.7 / 86.9 / 52.1;  64 tokens: 243.0 / 172.3 / 189.6
 int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
 {
     if (!mfma_shape_ok(w.dtype, w.rows, w.cols) || n == 0 || n > (1u << 20))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
-    constexpr int MT = 4;
-    const size_t rounds = (n + 4 * MT - 1) / (4 * MT);
-    auto groups = [&](int nw) { return (w.rows + 16 * nw - 1) / (16 * nw) * rounds; };
     const size_t want = (size_t)h->num_cu * 7 / 8;
-    const int nw = groups(16) >= want ? 16 : groups(8) >= want ? 8 : 4;
-    const int kc = mf_kc(h, w.cols, 4 * MT);
-    const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
-    const unsigned grid = (unsigned)groups(nw);
-    const size_t stride = packed_row_stride(w.dtype, w.cols);
-    const uint8_t *W = (const uint8_t *)w.dev;
-    const int ri = (int)w.rows, ci = (int)w.cols, ni = (int)n;
-    if (nw == 16)
-        k_mfma_q4k<1, MT, MF_LA1, false, 16><<<grid, 1024, lds, h->stream>>>(nullptr, nullptr, W, stride, ri, ci, x, 1,
-                                                                            nullptr, nullptr, nullptr, ni, kc, y);
-    else if (nw == 8)
-        k_mfma_q4k<1, MT, MF_LA1, false, 8><<<grid, 512, lds, h->stream>>>(nullptr, nullptr, W, stride, ri, ci, x, 1,
-                                                                          nullptr, nullptr, nullptr, ni, kc, y);
-    else
-        k_mfma_q4k<1, MT, MF_LA1, false, 4><<<grid, 256, lds, h->stream>>>(nullptr, nullptr, W, stride, ri, ci, x, 1,
-                                                                          nullptr, nullptr, nullptr, ni, kc, y);
+    auto groups = [&](int nw, int mt) { return (w.rows + 16 * nw - 1) / (16 * nw) * ((n + 4 * mt - 1) / (4 * mt)); };
+    auto chunks = [&](int mt) { return (w.cols + mf_kc(h, w.cols, 4 * mt) - 1) / mf_kc(h, w.cols, 4 * mt); };
+    if (groups(16, 4) >= want) {
+        mfma_dense<16, 4>(h, w, x, n, y, mf_kc(h, w.cols, 16), (unsigned)groups(16, 4));
+    } else if (groups(8, 4) >= want) {
+        mfma_dense<8, 4>(h, w, x, n, y, mf_kc(h, w.cols, 16), (unsigned)groups(8, 4));
+    } else {
+        const int mt = groups(4, 4) >= want && chunks(4) <= 4 ? 4 : groups(4, 2) >= want && chunks(2) <= 4 ? 2 : 1;
+        const int kc = mf_kc(h, w.cols, 4 * mt);
+        const unsigned grid = (unsigned)groups(4, mt);
+        if (mt == 4) mfma_dense<4, 4>(h, w, x, n, y, kc, grid);
+        else if (mt == 2) mfma_dense<4, 2>(h, w, x, n, y, kc, grid);
+        else mfma_dense<4, 1>(h, w, x, n, y, kc, grid);
+    }
     return hip_check(h, hipGetLastError(), "mfma matmul launch");
 }
