@@ -139,7 +139,13 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
  * register: router_key names a resident F32 weight [n_exp x hdim];
  * expert_keys holds 3*n_exp resident keys (gate_e, up_e, down_e for e = 0..):
  * gate/up [ffn x hdim], down [hdim x ffn], one quantized dtype per role.
- * Limits: n_exp <= 256, top_k <= 64.  Registering a key again replaces it. */
+ * Limits: n_exp <= 256, top_k <= 64.  Registering a key again replaces it.
+ * For Q4_K experts the layer also keeps a tile-major copy of every expert
+ * matrix (the same bytes again, counted in the handle's budget) that the
+ * matrix-core path reads when a call routes two or more tokens per active
+ * expert; it is skipped, and that path reads the resident weights, when the
+ * budget has no room.  Dropping any of the layer's weights unregisters it and
+ * frees the copy. */
 int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_len, const char *router_key,
                           size_t router_key_len, const char *const *expert_keys, const size_t *expert_key_lens,
                           size_t n_exp, size_t hdim, size_t ffn, size_t top_k);
