@@ -456,8 +456,93 @@ def cpu_extra(seconds, threads):
     out["q6_k_head_as_q8_0_GB_s"], _ = _cpu_rate(
         lambda i: orc.matvec(Q8, q8[i % ch], hr, cols, x, threads=threads, avx2=True), algo_bytes(Q8, hr, cols),
         seconds / 4)
-    out["sample"] = (f"~{seconds:.0f} s in all, each sample rotating >= 512 MB: 1 GiB host read; {c8} Q8_0 "
-                     f"4096x4096 copies; {ch} head row samples {hr}x{cols} (Q6_K restated, and requantized to Q8_0)")
+    head_q8_ms = algo_bytes(Q8, 128256, 4096) / (out["q6_k_head_as_q8_0_GB_s"] * 1e9) * 1e3
+    del q8
+    out.update(cpu_more_configs(seconds, threads, head_q8_ms))
+    out["sample"] = (f"~{1.75 * seconds:.0f} s in all, each sample rotating >= 512 MB: 1 GiB host read; {c8} Q8_0 "
+                     f"4096x4096 copies; {ch} head row samples {hr}x{cols} (Q6_K restated, and requantized to Q8_0); "
+                     f"MoE, decode layer and matmul samples as stated in their entries")
+    return out
+
+
+def cpu_more_configs(seconds, threads, head_q8_ms):
+    """CPU baselines of configs[3] and configs[4] and of the 64-token matmul,
+    the oracle's restatements on the same host threads: the MoE FFN of one
+    token (forward_moe_ffn's CPU branch, layer.rs:1938-2105) over 2 rotated
+    layers of 128 Q4_K experts; one dense 8B decode layer at position 4096 of
+    an f32 KV cache (forward_layer, layer.rs:1092-1389) over 4 rotated layers,
+    scaled to a token as 32 layers + the head as soso runs it (Q8_0, timed
+    above); Q4_K 14336x4096 against 64 vectors (matvec_view_batch_par) over 4
+    rotated copies."""
+    import ctypes as C
+    from oracle import oracle as orc
+    out = {}
+    E, H, F, K = 128, 2048, 768, 8
+    layers = []
+    for L in range(2):
+        mats = [[orc.synth(Q4K, r, c, 11, L * 1000 + 3 * e + j) for j, (r, c) in enumerate(((F, H), (F, H), (H, F)))]
+                for e in range(E)]
+        tabs = [(C.c_void_p * E)(*[mats[e][j].ctypes.data for e in range(E)]) for j in range(3)]
+        layers.append((orc.normal(E * H, 0.02, 12, L), mats, tabs))
+    xs = orc.normal(8 * H, 1.0, 13, 1).reshape(8, H)
+    y = np.empty(H, np.float32)
+    idx = np.empty(K, np.int32)
+    wgt = np.empty(K, np.float32)
+
+    def moe(i):
+        router, _, tabs = layers[i % 2]
+        x = xs[(i // 2) % 8]
+        orc.lib().or_moe_ffn(router.ctypes.data, E, H, F, K, C.cast(tabs[0], C.c_void_p), C.cast(tabs[1], C.c_void_p),
+                             C.cast(tabs[2], C.c_void_p), Q4K, Q4K, x.ctypes.data, y.ctypes.data, idx.ctypes.data,
+                             wgt.ctypes.data, threads, 1)
+    moe_bytes = E * H * 4 + K * 3 * F * (H // 256) * 144
+    gbs, n = _cpu_rate(moe, moe_bytes, seconds / 4)
+    out["moe_qwen3_30b_a3b_batch1"] = {"us_per_layer": round(moe_bytes / (gbs * 1e9) * 1e6, 1), "GB_s": gbs,
+                                       "sample": f"{n} tokens over 2 rotated layers of 128 Q4_K experts"}
+    del layers
+    Hd, NH, NKV, HDIM, Fd, ctx = 4096, 32, 8, 128, 14336, 4096
+    qd, kvd = NH * HDIM, NKV * HDIM
+    dec = []
+    for L in range(4):
+        w = [(1.0 + orc.normal(Hd, 0.1, 21, 100 * L)).astype(np.float32)]
+        for j, (r, c) in enumerate(((qd, Hd), (kvd, Hd), (kvd, Hd), (Hd, qd))):
+            w.append(orc.synth(Q4K, r, c, 21, 100 * L + 1 + j))
+        w.append((1.0 + orc.normal(Hd, 0.1, 21, 100 * L + 5)).astype(np.float32))
+        for j, (r, c) in enumerate(((Fd, Hd), (Fd, Hd), (Hd, Fd))):
+            w.append(orc.synth(Q4K, r, c, 21, 100 * L + 6 + j))
+        kc = orc.normal((ctx + 1) * kvd, 1.0, 22, 2 * L).reshape(ctx + 1, kvd)
+        vc = orc.normal((ctx + 1) * kvd, 1.0, 22, 2 * L + 1).reshape(ctx + 1, kvd)
+        dec.append((w, (C.c_void_p * 9)(*[a.ctypes.data for a in w]), kc, vc))
+    hid = orc.normal(Hd, 1.0, 23, 0)
+
+    def layer(i):
+        _, ptrs, kc, vc = dec[i % 4]
+        h = hid.copy()
+        orc.lib().or_decode_layer(h.ctypes.data, C.cast(ptrs, C.c_void_p), Q4K, Hd, NH, NKV, HDIM, Fd, kc.ctypes.data,
+                                  vc.ctypes.data, ctx, np.float32(500000.0), np.float32(1e-5), threads, 1)
+    layer_bytes = ((qd + 2 * kvd) * Hd + Hd * qd + 3 * Fd * Hd) // 256 * 144 + 2 * (ctx + 1) * kvd * 4
+    gbs, n = _cpu_rate(layer, layer_bytes, seconds / 4)
+    layer_ms = layer_bytes / (gbs * 1e9) * 1e3
+    tok_ms = 32 * layer_ms + head_q8_ms
+    out["llama8b_decode_ctx4096"] = {
+        "ms_per_layer": round(layer_ms, 3), "tokens_per_s_est": round(1e3 / tok_ms, 2), "GB_s": gbs,
+        "sample": f"{n} layers over 4 rotated 8B layers (f32 KV at 4096 positions, attention as the oracle's "
+                  f"scalar restatement over the head tasks); a token = 32 layers + the Q8_0 head ({head_q8_ms:.1f} ms)"}
+    del dec
+    rows, cols, nt = 14336, 4096, 64
+    ws = [orc.synth(Q4K, rows, cols, 3, 3000 + i) for i in range(4)]
+    xm = orc.normal(nt * cols, 1.0, 3, 9).reshape(nt, cols)
+    ym = np.empty(nt * rows, np.float32)
+
+    def mm(i):
+        orc.lib().or_matmul_par(Q4K, ws[i % 4].ctypes.data, rows, cols, nt, xm.ctypes.data, ym.ctypes.data, threads, 1)
+    mm_bytes = algo_bytes(Q4K, rows, cols)
+    gbs, n = _cpu_rate(mm, mm_bytes, seconds / 4)
+    mm_s = mm_bytes / (gbs * 1e9)
+    out["q4_k_matmul_14336x4096_n64"] = {"us": round(mm_s * 1e6, 1),
+                                         "gemm_TFLOP_s": round(2 * nt * rows * cols / mm_s / 1e12, 3),
+                                         "sample": f"{n} calls over 4 rotated copies, as 64 per-vector AVX2 "
+                                                   f"matvecs (soso's batched q4_k_nb kernel is not restated)"}
     return out
 
 

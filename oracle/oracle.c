@@ -473,9 +473,128 @@ int or_matvec_f64(uint8_t dtype, const uint8_t *w, size_t rows, size_t cols, con
 }
 
 /* ---------------------------------------------------------------------------
+ * Host thread pool: HostPool (crates/soso-llm-api/src/host_pool.rs:37-137).
+ * n threads in all, the caller being thread 0; workers spin on an epoch
+ * counter for OR_SPINS rounds and then sleep on a condition variable; a call
+ * cuts `rows` into strips [rows*i/n, rows*(i+1)/n) (`franja`, :31-33), runs
+ * strip 0 itself and spins until the n - 1 workers have counted themselves
+ * done.  One caller at a time (the oracle is driven from one thread).
+ * ------------------------------------------------------------------------- */
+#include <stdatomic.h>
+
+#define OR_SPINS 20000 /* GIROS_ANTES_DE_DORMIR, host_pool.rs:13 */
+
+typedef void (*or_rows_fn)(void *ctx, size_t r0, size_t r1);
+
+static struct {
+    int n;
+    pthread_t *tid;
+    atomic_uint epoch;
+    atomic_size_t done;
+    atomic_int stop;
+    size_t rows;
+    or_rows_fn fn;
+    void *ctx;
+    pthread_mutex_t mu;
+    pthread_cond_t cv;
+} or_pool = {1, NULL, 0, 0, 0, 0, NULL, NULL, PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER};
+
+static void pool_strip(size_t rows, int i, int n, size_t *r0, size_t *r1)
+{
+    *r0 = rows * (size_t)i / (size_t)n;
+    *r1 = rows * (size_t)(i + 1) / (size_t)n;
+}
+
+static unsigned or_pool_start; /* the epoch when the workers were made */
+
+static void *pool_worker(void *arg)
+{
+    const int i = (int)(intptr_t)arg;
+    /* the epoch as it was before any call could bump it (a worker that read
+     * the live value after the first call's bump would wait for the next) */
+    unsigned last = or_pool_start;
+    for (;;) {
+        unsigned spins = 0;
+        while (atomic_load_explicit(&or_pool.epoch, memory_order_acquire) == last) {
+            if (atomic_load_explicit(&or_pool.stop, memory_order_acquire)) return NULL;
+            if (++spins < OR_SPINS) continue;
+            pthread_mutex_lock(&or_pool.mu);
+            if (atomic_load_explicit(&or_pool.epoch, memory_order_acquire) == last &&
+                !atomic_load_explicit(&or_pool.stop, memory_order_acquire))
+                pthread_cond_wait(&or_pool.cv, &or_pool.mu);
+            pthread_mutex_unlock(&or_pool.mu);
+            spins = 0;
+        }
+        last = atomic_load_explicit(&or_pool.epoch, memory_order_acquire);
+        size_t r0, r1;
+        pool_strip(or_pool.rows, i, or_pool.n, &r0, &r1);
+        if (r0 < r1) or_pool.fn(or_pool.ctx, r0, r1);
+        atomic_fetch_add_explicit(&or_pool.done, 1, memory_order_acq_rel);
+    }
+}
+
+static void pool_stop(void)
+{
+    if (!or_pool.tid) return;
+    atomic_store_explicit(&or_pool.stop, 1, memory_order_release);
+    pthread_mutex_lock(&or_pool.mu);
+    pthread_cond_broadcast(&or_pool.cv);
+    pthread_mutex_unlock(&or_pool.mu);
+    for (int i = 1; i < or_pool.n; i++) pthread_join(or_pool.tid[i], NULL);
+    free(or_pool.tid);
+    or_pool.tid = NULL;
+    or_pool.n = 1;
+    atomic_store_explicit(&or_pool.stop, 0, memory_order_release);
+}
+
+/* A pool of `threads` threads (made once, remade when the count changes). */
+static int pool_size(int threads)
+{
+    if (threads < 1) threads = 1;
+    if (threads == or_pool.n) return 0;
+    pool_stop();
+    if (threads == 1) return 0;
+    or_pool.tid = (pthread_t *)calloc((size_t)threads, sizeof(pthread_t));
+    if (!or_pool.tid) return -1;
+    or_pool.n = threads;
+    or_pool_start = atomic_load_explicit(&or_pool.epoch, memory_order_acquire);
+    for (int i = 1; i < threads; i++)
+        if (pthread_create(&or_pool.tid[i], NULL, pool_worker, (void *)(intptr_t)i)) {
+            or_pool.n = i;
+            pool_stop();
+            return -1;
+        }
+    return 0;
+}
+
+/* for_rows (host_pool.rs:102-124). */
+static int pool_for_rows(int threads, size_t rows, or_rows_fn fn, void *ctx)
+{
+    if (pool_size(threads)) return -1;
+    if (or_pool.n <= 1 || rows == 0) {
+        fn(ctx, 0, rows);
+        return 0;
+    }
+    or_pool.rows = rows;
+    or_pool.fn = fn;
+    or_pool.ctx = ctx;
+    atomic_store_explicit(&or_pool.done, 0, memory_order_release);
+    atomic_fetch_add_explicit(&or_pool.epoch, 1, memory_order_acq_rel);
+    pthread_mutex_lock(&or_pool.mu);
+    pthread_cond_broadcast(&or_pool.cv);
+    pthread_mutex_unlock(&or_pool.mu);
+    size_t r0, r1;
+    pool_strip(rows, 0, or_pool.n, &r0, &r1);
+    if (r0 < r1) fn(ctx, r0, r1);
+    while (atomic_load_explicit(&or_pool.done, memory_order_acquire) < (size_t)(or_pool.n - 1)) {
+    }
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------
  * matvec_view_par: dtype dispatch + contiguous row strips
- * crates/soso-llm-core/src/layer.rs:124-240, strips from parallel.rs:22-31
- * (`row_strip`) as the host pool cuts them (soso-llm-api/src/host_pool.rs:32-34).
+ * crates/soso-llm-core/src/layer.rs:124-240, run on the host pool above
+ * (its strips, host_pool.rs:31-33).
  * ------------------------------------------------------------------------- */
 
 typedef struct {
@@ -516,17 +635,21 @@ static void run_strip(const strip_job *j)
     }
 }
 
-static void *strip_thread(void *p)
-{
-    run_strip((const strip_job *)p);
-    return NULL;
-}
-
+/* parallel.rs:22-31 (`row_strip`): the even split with the remainder spread
+ * over the first strips (the read-bandwidth probe below uses it). */
 static void row_strip(size_t rows, size_t i, size_t n, size_t *s, size_t *e)
 {
     size_t base = rows / n, rem = rows % n;
     *s = i * base + (i < rem ? i : rem);
     *e = *s + base + (i < rem ? 1 : 0);
+}
+
+static void strip_rows(void *ctx, size_t r0, size_t r1)
+{
+    strip_job j = *(const strip_job *)ctx;
+    j.r0 = r0;
+    j.r1 = r1;
+    run_strip(&j);
 }
 
 int or_matmul_par(uint8_t dtype, const uint8_t *w, size_t rows, size_t cols, size_t n, const float *xs,
@@ -535,26 +658,8 @@ int or_matmul_par(uint8_t dtype, const uint8_t *w, size_t rows, size_t cols, siz
     if (dtype != OR_DTYPE_F32 && or_row_bytes(dtype, cols) < 0) return -1;
     if (rows == 0 || n == 0) return 0;
     if (avx2 && !or_have_avx2()) avx2 = 0;
-    if (threads < 1) threads = 1;
-    if ((size_t)threads > rows) threads = (int)rows;
-    strip_job *jobs = (strip_job *)calloc((size_t)threads, sizeof(strip_job));
-    pthread_t *tid = (pthread_t *)calloc((size_t)threads, sizeof(pthread_t));
-    if (!jobs || !tid) {
-        free(jobs);
-        free(tid);
-        return -1;
-    }
-    for (int i = 0; i < threads; i++) {
-        strip_job j = {dtype, w, rows, cols, n, xs, outs, 0, 0, avx2};
-        row_strip(rows, (size_t)i, (size_t)threads, &j.r0, &j.r1);
-        jobs[i] = j;
-    }
-    for (int i = 1; i < threads; i++) pthread_create(&tid[i], NULL, strip_thread, &jobs[i]);
-    run_strip(&jobs[0]);
-    for (int i = 1; i < threads; i++) pthread_join(tid[i], NULL);
-    free(jobs);
-    free(tid);
-    return 0;
+    strip_job j = {dtype, w, rows, cols, n, xs, outs, 0, 0, avx2};
+    return pool_for_rows(threads, rows, strip_rows, &j);
 }
 
 int or_matvec_par(uint8_t dtype, const uint8_t *w, size_t rows, size_t cols, const float *x, float *out,
@@ -718,6 +823,78 @@ void or_attention_f32(const float *q, const float *k, const float *v, size_t hd,
         float il = 1.0f / l;
         for (size_t d = 0; d < hd; d++) out[d] *= il;
     }
+}
+
+/* Decode attention of every query head, heads spread over `threads` threads
+ * (atencion_f16_grupos splits (KV head, chunk) tasks over the host pool,
+ * layer.rs:804-896; here one task per query head).  q [n_heads * hd], caches
+ * position-major [T][n_kv_heads * hd], out [n_heads * hd]. */
+typedef struct {
+    const float *q, *k, *v;
+    size_t hd, kv_dim, group, T;
+    float *out;
+} attn_job;
+
+static void attn_rows(void *ctx, size_t h0, size_t h1)
+{
+    const attn_job *j = (const attn_job *)ctx;
+    for (size_t h = h0; h < h1; h++)
+        or_attention_f32(j->q + h * j->hd, j->k, j->v, j->hd, j->kv_dim, h / j->group, j->T, j->out + h * j->hd);
+}
+
+int or_attention_heads_par(const float *q, const float *k, const float *v, size_t hd, size_t n_heads,
+                           size_t n_kv_heads, size_t T, float *out, int threads)
+{
+    if (n_kv_heads == 0 || n_heads % n_kv_heads) return -1;
+    attn_job j = {q, k, v, hd, n_kv_heads * hd, n_heads / n_kv_heads, T, out};
+    return pool_for_rows(threads, n_heads, attn_rows, &j);
+}
+
+/* One dense decode layer on the CPU (the CPU baseline of the device decode
+ * step): LayerExecutor::forward_layer's GQA branch (layer.rs:1092-1389) with
+ * the pieces restated above -- rmsnorm, q/k/v, rope_cabezas (non-NeoX), K/V
+ * rows appended at `pos` of position-major f32 caches [ctx][n_kv*hd],
+ * attention over pos + 1 positions, o + residual, rmsnorm, gate/up, swiglu,
+ * down + residual.  h is updated in place.  w[0..8] = attn_norm (f32), q, k,
+ * v, o, ffn_norm (f32), gate, up, down (dtype). */
+int or_decode_layer(float *h, const void *const *w, uint8_t dtype, size_t hidden, size_t n_heads, size_t n_kv_heads,
+                    size_t hd, size_t ffn, float *kcache, float *vcache, size_t pos, float theta, float eps,
+                    int threads, int avx2)
+{
+    const size_t qd = n_heads * hd, kvd = n_kv_heads * hd;
+    float *xn = (float *)malloc(hidden * 4), *q = (float *)malloc(qd * 4), *att = (float *)malloc(qd * 4);
+    float *o = (float *)malloc(hidden * 4), *g = (float *)malloc(ffn * 4), *u = (float *)malloc(ffn * 4);
+    int rc = -1;
+    if (!xn || !q || !att || !o || !g || !u) goto done;
+    memcpy(xn, h, hidden * 4);
+    or_rmsnorm(xn, (const float *)w[0], hidden, eps);
+    if (or_matvec_par(dtype, (const uint8_t *)w[1], qd, hidden, xn, q, threads, avx2) ||
+        or_matvec_par(dtype, (const uint8_t *)w[2], kvd, hidden, xn, kcache + pos * kvd, threads, avx2) ||
+        or_matvec_par(dtype, (const uint8_t *)w[3], kvd, hidden, xn, vcache + pos * kvd, threads, avx2))
+        goto done;
+    or_rope_heads(q, n_heads, hd, pos, theta, 0);
+    or_rope_heads(kcache + pos * kvd, n_kv_heads, hd, pos, theta, 0);
+    if (or_attention_heads_par(q, kcache, vcache, hd, n_heads, n_kv_heads, pos + 1, att, threads)) goto done;
+    if (or_matvec_par(dtype, (const uint8_t *)w[4], hidden, qd, att, o, threads, avx2)) goto done;
+    for (size_t i = 0; i < hidden; i++) h[i] += o[i];
+    memcpy(xn, h, hidden * 4);
+    or_rmsnorm(xn, (const float *)w[5], hidden, eps);
+    if (or_matvec_par(dtype, (const uint8_t *)w[6], ffn, hidden, xn, g, threads, avx2) ||
+        or_matvec_par(dtype, (const uint8_t *)w[7], ffn, hidden, xn, u, threads, avx2))
+        goto done;
+    if (avx2 && or_have_avx2()) or_swiglu_avx2(u, g, ffn);
+    else or_swiglu(u, g, ffn);
+    if (or_matvec_par(dtype, (const uint8_t *)w[8], hidden, ffn, u, o, threads, avx2)) goto done;
+    for (size_t i = 0; i < hidden; i++) h[i] += o[i];
+    rc = 0;
+done:
+    free(xn);
+    free(q);
+    free(att);
+    free(o);
+    free(g);
+    free(u);
+    return rc;
 }
 
 /* ---------------------------------------------------------------------------

@@ -122,6 +122,11 @@ void or_attention_f32(const float *q, const float *k_cache, const float *v_cache
  * router (n_exp x h f32) -> topk_softmax -> per expert gate/up (ffn x h),
  * swiglu, down (h x ffn) -> out = sum_j w_j * down_j in ranking order.
  * Expert weights are given as arrays of pointers (dtype Q4_K or Q8_0). */
+int or_attention_heads_par(const float *q, const float *k, const float *v, size_t hd, size_t n_heads,
+                           size_t n_kv_heads, size_t T, float *out, int threads);
+int or_decode_layer(float *h, const void *const *w, uint8_t dtype, size_t hidden, size_t n_heads, size_t n_kv_heads,
+                    size_t hd, size_t ffn, float *kcache, float *vcache, size_t pos, float theta, float eps,
+                    int threads, int avx2);
 int or_moe_ffn(const float *router, size_t n_exp, size_t h, size_t ffn, size_t top_k,
                const uint8_t *const *gate, const uint8_t *const *up, const uint8_t *const *down,
                uint8_t dtype_gu, uint8_t dtype_down, const float *x, float *out, int32_t *idx_out,

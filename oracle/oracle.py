@@ -23,6 +23,8 @@ _PROTO = {
     "or_f16_to_f32": (_F, [C.c_uint16]),
     "or_f32_to_f16": (C.c_uint16, [_F]),
     "or_f32_to_f16_n": (None, [_P, _S, _P]),
+    "or_attention_heads_par": (_I, [_P, _P, _P, _S, _S, _S, _S, _P, _I]),
+    "or_decode_layer": (_I, [_P, _P, _U8, _S, _S, _S, _S, _S, _P, _P, _S, _F, _F, _I, _I]),
     "or_row_bytes": (C.c_int64, [_U8, _S]),
     "or_dequant_q8_0_range": (_I, [_P, _S, _S, _P, _S]),
     "or_dequant_q4_k_range": (_I, [_P, _S, _S, _P, _S]),
