@@ -434,12 +434,6 @@ __global__ void __launch_bounds__(256) mv_f32(const float *__restrict__ W, const
 // ---------------------------------------------------------------------------
 // Launch selection
 // ---------------------------------------------------------------------------
-static int env_int(const char *name, int dflt)
-{
-    const char *v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 // A group's strip (plus the DEPTH passes the ring reads past it, which come
 // back as zeros) is addressed with 32-bit buffer offsets.
 static bool strip_fits(int passes, int groups, size_t pass_bytes)
@@ -484,7 +478,7 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
     const int threads = 64 * S * gpw;
     const size_t lds = stage_lds_bytes(w.cols) + (S > 1 ? (size_t)gpw * COMBINE_CH * S * 4 : 0);
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec: x does not fit in LDS");
-    const int per_cu = env_int("SOSO_HIP_WG_PER_CU", 1);
+    const int per_cu = 1; // one 512-thread workgroup per CU (two measured slower for these shapes)
     const uint8_t *W = (const uint8_t *)w.dev;
     MvIn xin;
     xin.x = x;
