@@ -201,19 +201,6 @@ int launch_moe_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, 
 // ---------------------------------------------------------------------------
 // Device helpers
 // ---------------------------------------------------------------------------
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
-
-// v_dot2c_f32_f16: a.lo*b.lo + a.hi*b.hi + c, products exact, f32 accumulate.
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c)
-{
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
-}
-
-// v_perm_b32 with src1 = w: selector bytes 0..3 pick bytes of w, 0x0c gives 0.
-__device__ __forceinline__ uint32_t byte_perm(uint32_t w, uint32_t sel) { return __builtin_amdgcn_perm(0u, w, sel); }
-constexpr uint32_t SEL_B02 = 0x0c020c00u; // [b0, 0, b2, 0] -> two 16-bit halves
-constexpr uint32_t SEL_B13 = 0x0c030c01u; // [b1, 0, b3, 0]
-
 __device__ __forceinline__ float half_bits_to_f32(uint32_t b16)
 {
     return (float)__builtin_bit_cast(_Float16, (unsigned short)b16);
@@ -259,12 +246,6 @@ __device__ __forceinline__ float seg_sum(float v)
     return v;
 }
 
-__device__ __forceinline__ float wave_max(float v)
-{
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
 
 // DPP lane moves (gfx9 encodings): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] =
 // 0x4E, row_half_mirror 0x141, row_mirror 0x140, row_bcast:15 0x142,

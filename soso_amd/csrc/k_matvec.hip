@@ -14,15 +14,16 @@
 //    instruction of a wavefront reads 1 KiB of contiguous HBM.  Same bytes as
 //    soso's layout (no inflation; Q8_0/Q6_K rows are padded to 16 B only when
 //    their byte count is not a multiple of 16).
-//  * x is staged once per workgroup in LDS as an exact f16 hi/lo split of a
-//    power-of-two-scaled copy (x*2^-k = hi + lo, 22 significant bits), with the
-//    pairs ordered for the byte permutes below, plus f32 sums of every 16
-//    elements for the min / offset terms.
-//  * Quant codes are turned into f16 *subnormals* (bits = q, value q*2^-24)
-//    with one AND or one v_perm per two codes, and multiplied with
-//    v_dot2_f32_f16 (exact products, f32 accumulate).  The 2^-24 and 2^k
-//    factors are folded into the per-block scales.  The reduction across the
-//    lanes of a row is a butterfly of cross-lane shuffles.
+//  * x is staged once per workgroup in LDS as integers X = rint(x * 2^e), one
+//    exponent e per 128-element block (|X| <= 2^22), written as three balanced
+//    signed base-256 digit planes (one byte per element per digit), plus f32
+//    sums of every 16 elements for the min / offset terms; each lane then keeps
+//    its unit's digits in VGPRs for the whole launch.
+//  * Quant codes are unpacked in registers (an AND or a shift per four codes)
+//    and meet the digits in v_dot4_i32_i8: exact int32 sums per digit and
+//    sub-block, rounded to f32 once per sub-block before the block scales are
+//    applied.  The reduction across the lanes of a row uses DPP adds, and a
+//    strip's row sums leave in one store.
 #include "internal.hpp"
 
 #include <algorithm>
