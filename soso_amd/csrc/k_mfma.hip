@@ -25,10 +25,12 @@
 // so every lane ends up with one (weight row, token) pair per tile: the
 // row's scales apply lane by lane, and the min term is one FMA.
 //
-// Work: a workgroup of MF_NW wavefronts owns 16 rows per wavefront of one
+// Work: a workgroup of NW wavefronts (4 for the MoE experts; 4, 8 or 16 for
+// a dense matmul, chosen from the grid size) owns 16 rows per wavefront of one
 // expert (or of the dense weight) and loops over its tokens in rounds of
 // 4 * MT, and over the columns in chunks of `kcmax` (as many as LDS holds for
-// the round's tokens: one chunk for the MoE expert shapes).
+// the round's tokens: one chunk for the MoE expert shapes).  Registered MoE
+// layers are read from tile-major copies (below).
 #include "mv_core.hpp"
 
 typedef int mf_v4i __attribute__((ext_vector_type(4)));

@@ -14,7 +14,11 @@
 //                 every weight row of an expert is read once from HBM and
 //                 applied to all the tokens routed to it (their x staged in
 //                 LDS).  Gate and up rows are read side by side and leave as
-//                 silu(gate.x) * up.x; down rows leave as y[slot].
+//                 silu(gate.x) * up.x; down rows leave as y[slot].  (Two or
+//                 more tokens per active expert: the matrix-core kernel of
+//                 k_mfma.hip instead.)
+//   k_moe_down_comb  up to 4 tokens: down and the weighted sum in one launch,
+//                 one wavefront per ranked expert.
 //   k_moe_combine out[t] = sum_j wgt[t,j] * y[t*top_k + j], j in ranking order.
 // Slot s = t * top_k + j is token t's j-th ranked expert ("destinos" in
 // ExpertoBloque, gpu.rs:176-186).
