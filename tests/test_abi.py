@@ -1,5 +1,6 @@
-"""The C-ABI library builds, loads and exports every symbol include/soso_hip.h
-declares; without a device it refuses cleanly (no compute calls here)."""
+"""The C-ABI libraries build, load and export every symbol include/soso_hip.h
+and include/soso_som.h declare; without a device libsoso_hip refuses cleanly
+(no compute calls here)."""
 import ctypes as C
 import os
 import re
@@ -30,6 +31,18 @@ def test_library_exports_every_declared_symbol():
     assert not missing, missing
     # and the ctypes prototypes cover exactly that list
     assert sorted(abi.PROTOTYPES) == declared_symbols()
+
+
+def test_som_library_exports_every_declared_symbol():
+    """libsoso_som.so against include/soso_som.h, and the Python binding's
+    prototypes cover exactly that list."""
+    from soso_amd import som
+    text = re.sub(r"/\*.*?\*/", "", open(os.path.join(ROOT, "include", "soso_som.h")).read(), flags=re.S)
+    syms = sorted(set(re.findall(r"\b(soso_som_[a-z0-9_]+)\s*\(", text)))
+    lib = som.lib()
+    assert syms and not [s for s in syms if not hasattr(lib, s)]
+    src = open(som.__file__).read()
+    assert sorted(set(re.findall(r'"(soso_som_[a-z0-9_]+)"', src))) == syms
 
 
 def test_null_and_bad_arguments_are_errors_not_crashes():

@@ -66,6 +66,7 @@ class Model:
             })
         self.out_norm = (1.0 + orc.normal(H, 0.1, seed, 9000)).astype(np.float32)
         self.head = quant(orc, Q8, orc.normal(V * H, 0.05, seed, 9001))
+        self.head_dtype = Q8
 
     def shapes(self, name):
         H, F, qd, kvd = self.H, self.F, self.qd, self.kvd
@@ -89,7 +90,7 @@ class Model:
                 put(k, lw[nm], *self.shapes(nm))
                 keys.append(k)
         put(self.name + ".out_norm", self.out_norm, F32, 1, self.H)
-        put(self.name + ".head", self.head, Q8, self.V, self.H)
+        put(self.name + ".head", self.head, self.head_dtype, self.V, self.H)
         keys += [self.name + ".out_norm", self.name + ".head"]
         self.keys = keys
         return keys
@@ -132,7 +133,7 @@ class Model:
             h = orc.matvec(Q4K, lw["down"], self.H, self.F, up) + h
         xn = h.copy()
         L_.or_rmsnorm(xn.ctypes.data, self.out_norm.ctypes.data, self.H, np.float32(eps))
-        logits = orc.matvec(Q8, self.head, self.V, self.H, xn)
+        logits = orc.matvec(self.head_dtype, self.head, self.V, self.H, xn)
         return logits, int(L_.or_argmax(logits.ctypes.data, logits.size))
 
 

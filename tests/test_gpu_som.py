@@ -1,0 +1,89 @@
+"""A converted model directory (.som) through the GPU path: the device decode
+step built from the mapped tensors, and an MoE layer registered from them.
+
+Reference: MmapTensorSource::tensor_view / load_f32_range
+(crates/soso-llm-core/src/source.rs:308-352) feeding GpuDispatch under the
+tensors' own names, the tensor names and shapes Runtime checks
+(runtime.rs:330-475), the dense decode step (layer.rs:1092-1389,
+runtime.rs:1976-2028) and the MoE FFN (layer.rs:1732-2105).  The CPU side is
+the oracle's composition used by the direct decode and MoE tests; the head is
+stored as Q6_K, this build's dtype 13.
+
+Bar: logits within relative L2 1e-5 and the greedy token identical at every
+step; MoE indices identical, outputs within relative L2 1e-5.
+"""
+import numpy as np
+import pytest
+
+from soso_amd import som
+from test_gpu_decode import Model
+from test_gpu_moe import Layer, moe_dev
+
+pytestmark = pytest.mark.gpu
+
+NAMES = {"attn_norm": "attn_norm", "q": "attn_q", "k": "attn_k", "v": "attn_v", "o": "attn_output",
+         "ffn_norm": "ffn_norm", "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down"}
+
+
+def test_decode_from_som_matches_cpu(gpu, orc, tmp_path):
+    L, H, nh, nkv, F, V, ctx, theta, eps = 2, 512, 4, 2, 1024, 1000, 16, 500000.0, 1e-5
+    m = Model(orc, L, H, nh, nkv, F, V, 77)
+    m.head, m.head_dtype = orc.synth(som.DTYPE_Q6_K, V, H, 77, 9001), som.DTYPE_Q6_K
+    embed = orc.normal(V * H, 1.0, 77, 9002).reshape(V, H)
+    man = som.Manifest(name="gpu-dense", vocab_size=V, hidden_dim=H, num_layers=L, num_heads=nh, num_kv_heads=nkv,
+                       ffn_dim=F, max_seq=ctx, rope_theta=theta, rms_eps=eps)
+    man.fill_layers_from_globals()
+    ts = []
+    for l, lw in enumerate(m.layers):
+        for k, nm in NAMES.items():
+            dt, r, c = m.shapes(k)
+            ts.append((f"L{l:02}.{nm}", dt, (c,) if r == 1 else (r, c), lw[k]))
+    ts += [("output_norm", som.DTYPE_F32, (H,), m.out_norm), ("embed", som.DTYPE_F32, (V, H), embed),
+           ("lm_head", som.DTYPE_Q6_K, (V, H), m.head)]
+    som.write_model(str(tmp_path), man, ts)
+    print(f"som decode L={L} H={H} heads={nh}/{nkv} V={V}", flush=True)
+    with som.SomModel.open(str(tmp_path)) as s:
+        dec = som.prepare_decode(gpu, s, "som.dense", ctx_max=ctx)
+        try:
+            kc = np.zeros((L, ctx, m.kvd), np.float32)
+            vc = np.zeros((L, ctx, m.kvd), np.float32)
+            tok = 5
+            for pos in range(5):
+                got, logits = dec.step(tok, pos, logits=True)
+                ref, ref_tok = m.cpu_step(orc, embed[tok], kc, vc, pos, theta, eps)
+                assert orc.rel_l2(logits, ref) < 1e-5, (pos, orc.rel_l2(logits, ref))
+                top2 = np.sort(ref)[-2:]
+                if top2[1] - top2[0] > 1e-3 * max(1.0, abs(float(top2[1]))):
+                    assert got == ref_tok, pos
+                tok = ref_tok
+        finally:
+            dec.close()
+
+
+def test_moe_layer_from_som_matches_cpu(gpu, orc, tmp_path):
+    E, H, FF, K, n = 8, 256, 512, 2, 3
+    layer = Layer(orc, E, H, FF, K, 81)
+    man = som.Manifest(name="gpu-moe", vocab_size=64, hidden_dim=H, num_layers=1, num_heads=2, num_kv_heads=1,
+                       ffn_dim=FF, max_seq=16, num_experts=E, num_experts_per_tok=K, moe_ffn_dim=FF)
+    man.fill_layers_from_globals()
+    ts = [("L00.ffn_gate_inp", som.DTYPE_F32, (E, H), layer.router)]
+    for e in range(E):
+        ts += [(f"L00.E{e:02}.ffn_gate", som.DTYPE_Q4_K, (FF, H), layer.gate[e]),
+               (f"L00.E{e:02}.ffn_up", som.DTYPE_Q4_K, (FF, H), layer.up[e]),
+               (f"L00.E{e:02}.ffn_down", som.DTYPE_Q4_K, (H, FF), layer.down[e])]
+    som.write_model(str(tmp_path), man, ts)
+    print(f"som moe E={E} H={H} ffn={FF} top{K} n={n}", flush=True)
+    with som.SomModel.open(str(tmp_path)) as s:
+        key = som.prepare_moe_layer(gpu, s, 0)
+        try:
+            layer.name = key
+            xs = orc.normal(n * H, 1.0, 82, 1)
+            out, idx, wgt = moe_dev(gpu, layer, xs)
+            for t in range(n):
+                ref, ri, rw = layer.cpu(orc, xs[t * H:(t + 1) * H])
+                assert np.array_equal(idx[t], ri), (t, idx[t], ri)
+                assert orc.rel_l2(wgt[t], rw) < 1e-5
+                assert orc.rel_l2(out[t], ref) < 1e-5, (t, orc.rel_l2(out[t], ref))
+        finally:
+            for name, *_ in ts:
+                gpu.weight_drop(name)
