@@ -316,13 +316,18 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
     const int q_dim = (int)(m.n_heads * m.head_dim), kv_dim = (int)(m.n_kv_heads * m.head_dim);
     if (pos >= m.ctx_max) return set_err(h, SOSO_HIP_ERR_ARG, "decode: position beyond the KV capacity");
     float *hid = m.hid, *qb = m.qbuf, *att = m.att, *act = m.act, *lg = logits ? logits : m.logits;
-    int rc = hip_check(h, hipMemcpyAsync(hid, x, m.hidden * 4, hipMemcpyDeviceToDevice, h->stream), "embed copy");
+    // layer 0 reads the caller's x in place (its o projection writes the first
+    // hid) when x is 16-byte aligned for the staging's vector loads; else a copy
+    const bool direct = ((uintptr_t)x & 15) == 0;
+    int rc = direct ? SOSO_HIP_OK
+                    : hip_check(h, hipMemcpyAsync(hid, x, m.hidden * 4, hipMemcpyDeviceToDevice, h->stream), "x copy");
     for (size_t l = 0; l < m.n_layers && rc == SOSO_HIP_OK; l++) {
+        const float *hin = l == 0 && direct ? x : hid;
         const DecodeLayer &L = m.layers[l];
         const size_t esz = m.kv_f16 ? 2 : 4, layer_bytes = m.ctx_max * kv_dim * esz;
         void *K = (char *)m.kcache + l * layer_bytes, *V = (char *)m.vcache + l * layer_bytes;
         MvIn in;
-        in.x = hid;
+        in.x = hin;
         in.norm_w = L.attn_norm;
         in.eps = m.eps;
         MvEpi ep;
@@ -344,7 +349,7 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
             MvIn a;
             a.x = att;
             MvEpi r;
-            r.res = hid;
+            r.res = hin;
             rc = launch_matvec_ex(h, *L.o, a, hid, r, XS_PLAIN, EPI_RESID);
         }
         if (rc == SOSO_HIP_OK) {

@@ -220,6 +220,35 @@ def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill, kv_f16)
             gpu.weight_drop(k)
 
 
+def test_decode_step_input_alignment(gpu, orc):
+    """The step reads an aligned x in place and copies an unaligned one first:
+    the same bits either way."""
+    L, H, nh, nkv, F, V, ctx = 1, 512, 4, 2, 1024, 256, 16
+    m = Model(orc, L, H, nh, nkv, F, V, 93)
+    m.upload(gpu)
+    name = m.name + ".align"
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=1e4, rms_eps=1e-5)
+    gpu.decode_create(name, cfg, m.keys)
+    x = orc.normal(H, 1.0, 94, 1)
+    xd = gpu.dev_alloc((H + 4) * 4)
+    ld = gpu.dev_alloc(V * 4)
+    try:
+        out = []
+        for off in (0, 4):  # bytes
+            gpu.h2d(xd + off, x)
+            gpu.decode_step_dev(name, xd + off, 3, ld, None)
+            gpu.sync()
+            out.append(gpu.d2h(ld, (V,), np.float32))
+        assert np.array_equal(out[0].view(np.uint32), out[1].view(np.uint32))
+    finally:
+        gpu.dev_free(xd)
+        gpu.dev_free(ld)
+        gpu.decode_destroy(name)
+        for k in m.keys:
+            gpu.weight_drop(k)
+
+
 def test_kv_upload_rounds_like_soso(gpu, orc):
     """f32 rows entering an f16 cache take soso's f32_to_f16 bit for bit:
     ties away from zero, subnormal rounding and flushing, overflow, NaN."""
