@@ -91,13 +91,29 @@ __device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool va
         uint32_t d0[XDIG], d1[XDIG];
         digits4(v0, e, d0);
         digits4(v1, e, d1);
-        int u, gi;
-        xunit<FMT>(2 * c, u, gi);
+        if constexpr (FMT == FMT_Q6K) {
+            int u, gi;
+            xunit<FMT>(2 * c, u, gi);
 #pragma unroll
-        for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d0[k];
-        xunit<FMT>(2 * c + 1, u, gi);
+            for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d0[k];
+            xunit<FMT>(2 * c + 1, u, gi);
 #pragma unroll
-        for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d1[k];
+            for (int k = 0; k < XDIG; k++) xd[xdw(u, XDIG * gi + k, U)] = d1[k];
+        } else {
+            // groups 2m, 2m + 1 (m = c mod 8) of unit c / 8 are register dwords
+            // 6m .. 6m + 5 (xdw): one aligned 16-byte and one 8-byte store
+            // instead of six 4-byte ones (on MI355X a 4096 x 4096 Q4_K matvec
+            // went from 5.07 to 4.30 us with this alone)
+            const int u = c >> 3, m = c & 7, s0 = (3 * m) >> 1;
+            uint4 *slot = (uint4 *)xd + s0 * U + u;
+            if ((m & 1) == 0) {
+                *slot = make_uint4(d0[0], d0[1], d0[2], d1[0]);
+                *(uint2 *)(slot + U) = make_uint2(d1[1], d1[2]);
+            } else {
+                *((uint2 *)slot + 1) = make_uint2(d0[0], d0[1]);
+                slot[U] = make_uint4(d0[2], d1[0], d1[1], d1[2]);
+            }
+        }
         if ((c & 1) == 0) s16[c >> 1] = sm;
         if ((c & 15) == 0) kx[c >> 4] = e;
     }
