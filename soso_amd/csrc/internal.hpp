@@ -193,6 +193,9 @@ int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size
                        size_t n_exp, size_t top_k, int32_t *idx_dev, float *wgt_dev, float *logits_dev);
 int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim, size_t n_exp,
                      size_t top_k, const MoeScratch &s);
+// One token through a registered MoE layer, the ranking done by the expert
+// kernel (DECLINED when the layer's shapes need the general path).
+int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x_dev, const MoeScratch &s, float *out_dev);
 int launch_moe_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab_dev, size_t n_groups,
                        const float *wgt_dev, const uint8_t *use_dev, const int32_t *route_idx_dev,

@@ -92,11 +92,12 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
 constexpr int ROUTE_MAX_SLOTS = 4096; // n * top_k handled by the LDS sort
 constexpr int ROUTE_TT = 4;           // tokens per wavefront (and per ranking workgroup) from 2 tokens
 constexpr int ROUTE_T1 = 2048;        // first per-token-block counter in the ticket buffer
+constexpr int MOE_SELF_K = 8;         // top_k of the self-ranked single-token path
 
 // TT tokens per wavefront; each lane requests Q float4 of the expert row (and
 // of every token's x) per step: TT = 1 (one token, the decode case) takes a
 // 2048-wide row in a single round trip.
-template <int TT, int Q>
+template <int TT, int Q, bool LOGITS_ONLY = false>
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
                                                     int32_t *__restrict__ idx, float *__restrict__ wgt,
@@ -149,6 +150,7 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
             if (lane == 63 && tt < tn) logits[(size_t)(t0 + tt) * n_exp + e] = sum;
         }
     }
+    if constexpr (LOGITS_ONLY) return; // the expert kernels rank the token themselves
     // Two-level tickets.  The last workgroup of token block by (counter
     // ticket[ROUTE_T1 + by]) ranks that block's tokens, one per wavefront;
     // the last token block to be ranked (counter ticket[0]) sorts the slots.
@@ -413,12 +415,25 @@ __device__ __forceinline__ void q4k_token_dot(const Q4Prep (&pr)[NMAT], const ui
     }
 }
 
-template <int FMT, int LPR, int NMAT, int DEPTH>
+// One token ranked by the expert kernel itself (SELF): every workgroup takes
+// the softmax top-k of the token's logits (topk_regs, the same ranking as the
+// route kernel's) and runs `chunks` row chunks of each ranked expert j on
+// slot j; workgroup 0 also writes the ranking to idx / wgt for the kernels
+// that follow.  No work items or slot lists are read.
+struct MoeSelf {
+    const float *logits = nullptr;
+    int n_exp = 0, top_k = 0, chunks = 0;
+    int32_t *idx = nullptr;
+    float *wgt = nullptr;
+};
+
+template <int FMT, int LPR, int NMAT, int DEPTH, bool SELF = false>
 __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB, size_t stride, int rows,
                                                   int cols, const float *__restrict__ xs, int xdiv,
                                                   const int *__restrict__ list, const int *__restrict__ items,
-                                                  const int *__restrict__ n_items, int tch, float *__restrict__ out)
+                                                  const int *__restrict__ n_items, int tch, float *__restrict__ out,
+                                                  MoeSelf sr = MoeSelf())
 {
     constexpr int RW = 64 / LPR, NW = 8;
     extern __shared__ uint4 smem[];
@@ -436,10 +451,46 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
     const uint32_t pass_bytes = (uint32_t)(NW * RW * stride);
     const uint32_t lane_base = uact ? (uint32_t)((wave * RW + slot) * stride) : 0x80000000u;
     const int passes = (rows + NW * RW - 1) / (NW * RW);
-    const int nit = *n_items;
+    __shared__ int32_t self_idx[MOE_SELF_K];
+    __shared__ float self_wgt[MOE_SELF_K], self_sel[MOE_SELF_K];
+    __shared__ int16_t self_rank[MOE_SELF_K];
+    int nit;
+    if constexpr (SELF) {
+        if (wave == 0) {
+            float lg[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int x = lane + 64 * q;
+                lg[q] = x < sr.n_exp ? sr.logits[x] : -INFINITY;
+            }
+            topk_regs(lg, sr.n_exp, sr.top_k, self_idx, self_wgt, self_sel, self_rank);
+        }
+        __syncthreads();
+        if (blockIdx.x == 0 && (int)threadIdx.x < sr.top_k) {
+            sr.idx[threadIdx.x] = self_idx[threadIdx.x];
+            sr.wgt[threadIdx.x] = self_wgt[threadIdx.x];
+        }
+        nit = sr.top_k * sr.chunks;
+    } else {
+        nit = *n_items;
+    }
     for (int it = blockIdx.x; it < nit; it += gridDim.x) {
-        const int *rec = items + 4 * it;
-        const int e = rec[0], ne = rec[1], base = rec[2], j = rec[3] & 0xFFFF, nx = rec[3] >> 16;
+        int e, ne, base, j, nx, self_slot = 0;
+        if constexpr (SELF) {
+            self_slot = it / sr.chunks; // rank = slot of the single token
+            e = min(max((int)self_idx[self_slot], 0), sr.n_exp - 1);
+            ne = 1;
+            base = 0;
+            j = it % sr.chunks;
+            nx = sr.chunks;
+        } else {
+            const int *rec = items + 4 * it;
+            e = rec[0];
+            ne = rec[1];
+            base = rec[2];
+            j = rec[3] & 0xFFFF;
+            nx = rec[3] >> 16;
+        }
         const int p0 = (int)((long)j * passes / nx), p1 = (int)((long)(j + 1) * passes / nx), P = p1 - p0;
         if (P <= 0) continue; // more chunks than passes: an empty share
         const int r0 = p0 * NW * RW, rend = min(rows, p1 * NW * RW);
@@ -455,13 +506,13 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                 const int f = k * 512 + (int)threadIdx.x;
                 xv0[k] = xv1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (f < tot) {
-                    const int sl = list[base + t0 + f / nch];
+                    const int sl = SELF ? self_slot : list[base + t0 + f / nch];
                     const float4 *x4 = (const float4 *)(xs + (size_t)(sl / xdiv) * cols) + 2 * (f % nch);
                     xv0[k] = x4[0];
                     xv1[k] = x4[1];
                 }
             }
-            if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = list[base + t0 + threadIdx.x];
+            if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = SELF ? self_slot : list[base + t0 + threadIdx.x];
             __builtin_amdgcn_sched_barrier(0);
             // 2. the ring
             WRow<FMT> wa[DEPTH], wb[DEPTH];
@@ -487,7 +538,8 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                 const int f = fb + (int)threadIdx.x, tk = f / nch;
                 float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
                 if (f < tot) {
-                    const float4 *x4 = (const float4 *)(xs + (size_t)(list[base + t0 + tk] / xdiv) * cols) + 2 * (f % nch);
+                    const int sl = SELF ? self_slot : list[base + t0 + tk];
+                    const float4 *x4 = (const float4 *)(xs + (size_t)(sl / xdiv) * cols) + 2 * (f % nch);
                     v0 = x4[0];
                     v1 = x4[1];
                 }
@@ -799,6 +851,80 @@ static int launch_moe_mv(soso_hip *h, uint8_t dtype, int nmat, const uint8_t *co
     default: return set_err(h, SOSO_HIP_DECLINED, "moe: expert dtype not handled here");
     }
     return hip_check(h, hipGetLastError(), "moe mv launch");
+}
+
+// ---------------------------------------------------------------------------
+// One token through a registered layer, ranked by the expert kernel itself:
+// logits (k_moe_route<1, 8, true>: no ticket, no sort), gate/up + swiglu of
+// the ranked experts (k_moe_rows<..., SELF>), down and the ranking-order sum
+// (k_moe_down_comb).  The route kernel's last-workgroup ranking and sort are
+// chains of dependent round trips; here every expert workgroup ranks the
+// token's logits itself, which costs less than those chains.
+// ---------------------------------------------------------------------------
+template <int FMT>
+static void moe_rows_self(soso_hip *h, unsigned grid, size_t lds, int lpr, const uint8_t *const *A,
+                          const uint8_t *const *B, size_t stride, int rows, int cols, const float *x, int top_k,
+                          const MoeSelf &sr, float *out)
+{
+#define MOE_SELF_CASE(LP)                                                                                          \
+    case LP:                                                                                                       \
+        k_moe_rows<FMT, LP, 2, moe_depth<FMT, 2>(), true><<<grid, 512, lds, h->stream>>>(                          \
+            A, B, stride, rows, cols, x, top_k, nullptr, nullptr, nullptr, 1, out, sr);                            \
+        break;
+    switch (lpr) {
+        MOE_SELF_CASE(1) MOE_SELF_CASE(2) MOE_SELF_CASE(4) MOE_SELF_CASE(8) MOE_SELF_CASE(16) MOE_SELF_CASE(32)
+        MOE_SELF_CASE(64)
+    }
+#undef MOE_SELF_CASE
+}
+
+static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp, size_t rows, size_t cols,
+                            const float *act, const int32_t *idx, const float *wgt, size_t n, size_t top_k, float *out);
+
+int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScratch &s, float *out)
+{
+    const size_t hdim = m.hdim, ffn = m.ffn, top_k = m.top_k, n_exp = m.n_exp;
+    const int U = (int)(hdim / 64);
+    const size_t Uf = ffn / 64;
+    const bool gu_ok = (m.dt_gu == SOSO_HIP_DTYPE_Q4_K || m.dt_gu == SOSO_HIP_DTYPE_Q8_0 ||
+                        m.dt_gu == SOSO_HIP_DTYPE_Q6_K) &&
+                       U >= 1 && U <= 64 && hdim % 128 == 0 && packed_shape_ok(m.dt_gu, ffn, hdim);
+    const bool down_ok = m.dt_down == SOSO_HIP_DTYPE_Q4_K && ffn % 256 == 0 && Uf >= 4 && Uf <= 8 * (size_t)MDC_XR &&
+                         ((stage_lds_bytes(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds &&
+                         packed_shape_ok(m.dt_down, hdim, ffn);
+    if (top_k == 0 || top_k > (size_t)MOE_SELF_K || n_exp > 256 || !gu_ok || !down_ok)
+        return set_err(h, SOSO_HIP_DECLINED, "moe ffn1: shape for the general path");
+    const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
+    const size_t rows_per_pass = 8 * (64 / lpr), passes = (ffn + rows_per_pass - 1) / rows_per_pass;
+    const size_t stride = packed_row_stride(m.dt_gu, hdim);
+    const size_t lds = (stage_lds_bytes(hdim) + 15) & ~(size_t)15;
+    if (lds > h->max_lds || (passes + 2) * rows_per_pass * stride >= ((size_t)1 << 31))
+        return set_err(h, SOSO_HIP_DECLINED, "moe ffn1: shape for the general path");
+    // the route kernel's item count for one token: about moe_item_target
+    // chunks in all, the same share for every ranked expert
+    const int chunks = std::max(1, (moe_item_target(h) + (int)top_k / 2) / (int)top_k);
+    k_moe_route<1, 8, true><<<dim3((unsigned)((n_exp + 7) / 8), 1u), 512, 0, h->stream>>>(
+        (const float *)m.router->dev, x, 1, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt, s.cnt, s.offs,
+        s.list, s.items, s.n_items, moe_item_target(h), s.recs, s.n_recs, h->ticket);
+    int rc = hip_check(h, hipGetLastError(), "moe ffn1 route launch");
+    if (rc != SOSO_HIP_OK) return rc;
+    MoeSelf sr;
+    sr.logits = s.logits;
+    sr.n_exp = (int)n_exp;
+    sr.top_k = (int)top_k;
+    sr.chunks = chunks;
+    sr.idx = s.idx;
+    sr.wgt = s.wgt;
+    const unsigned grid = (unsigned)(top_k * chunks);
+    const uint8_t *const *A = m.tab, *const *B = m.tab + n_exp;
+    switch (m.dt_gu) {
+    case SOSO_HIP_DTYPE_Q4_K: moe_rows_self<FMT_Q4K>(h, grid, lds, lpr, A, B, stride, (int)ffn, (int)hdim, x, (int)top_k, sr, s.act); break;
+    case SOSO_HIP_DTYPE_Q8_0: moe_rows_self<FMT_Q80>(h, grid, lds, lpr, A, B, stride, (int)ffn, (int)hdim, x, (int)top_k, sr, s.act); break;
+    default: moe_rows_self<FMT_Q6K>(h, grid, lds, lpr, A, B, stride, (int)ffn, (int)hdim, x, (int)top_k, sr, s.act); break;
+    }
+    rc = hip_check(h, hipGetLastError(), "moe ffn1 gate/up launch");
+    if (rc != SOSO_HIP_OK) return rc;
+    return launch_down_comb(h, m.tab + 2 * n_exp, n_exp, hdim, ffn, s.act, s.idx, s.wgt, 1, top_k, out);
 }
 
 // gate/up + swiglu, down, combine for the slots grouped in s.cnt/offs/list.

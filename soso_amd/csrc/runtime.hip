@@ -612,6 +612,10 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
         return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_ffn_dev: scratch");
     if (idx_dev) ms.idx = idx_dev;
     if (wgt_dev) ms.wgt = wgt_dev;
+    if (n == 1) {
+        rc = launch_moe_ffn1(h, m, x_dev, ms, out_dev);
+        if (rc != SOSO_HIP_DECLINED) return rc;
+    }
     rc = launch_moe_route(h, (const float *)m.router->dev, x_dev, n, m.hdim, m.n_exp, m.top_k, ms);
     if (rc == SOSO_HIP_OK)
         rc = launch_moe_experts(h, x_dev, n, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, ms.wgt,
