@@ -132,6 +132,46 @@ def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False):
             g.weight_drop(k)
 
 
+READ_SHAPES = ((1, 256), (2, 256), (4, 256), (8, 256), (1, 512), (2, 512), (4, 512), (1, 1024), (2, 1024))
+
+
+def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES):
+    """A plain streaming read (soso_hip_read_probe) of `nbytes` over `copies`
+    rotating buffers, per launch shape (workgroups per CU, threads): the
+    bandwidth ceiling the matvec is held against, timed like time_matvec
+    (one graph of back-to-back launches between two HIP events).  Returns
+    {(wg_per_cu, threads): ms per launch}."""
+    bufs = [g.dev_alloc(nbytes) for _ in range(copies)]
+    out_len = 32 * 1024 * 1024
+    out = g.dev_alloc(out_len * 4)
+    res = {}
+    try:
+        for i, b in enumerate(bufs):
+            g.synth_normal(b, nbytes // 4, 1.0, 5, 900 + i)
+        for wpc, thr in shapes:
+            for i in range(warmup):
+                g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len)
+            g.sync()
+            gid = _capture(g, lambda: [g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len)
+                                       for i in range(steps)])
+            try:
+                g.graph_launch(gid)
+                g.sync()
+                g.event_record(0)
+                g.graph_launch(gid)
+                g.event_record(1)
+                g.sync()
+            finally:
+                g.graph_destroy(gid)
+            res[(wpc, thr)] = g.event_elapsed(0, 1) / steps
+    finally:
+        g.sync()
+        for b in bufs:
+            g.dev_free(b)
+        g.dev_free(out)
+    return res
+
+
 def time_moe(g, n, steps, layers=4, n_x=8, seed=11, eager=False):
     """Qwen3-30B-A3B-like MoE FFN (hidden 2048, 128 experts of
     intermediate 768, top-8, Q4_K experts, f32 router ~ N(0, 0.02)), `n`
@@ -567,7 +607,7 @@ def main():
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
     ap.add_argument("--eager", action="store_true",
                     help="with --only decode/moe1/moe32/matmul: launch the timed steps directly instead of replaying a graph")
-    ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head", "matmul"],
+    ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head", "matmul", "readprobe"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -599,6 +639,13 @@ def main():
             ms_h, _, tok_h = time_decode_8b(g, max(10, args.steps // 50), kv_f16=True, eager=args.eager)
             res = {"llama8b_decode_ms_per_token": round(ms, 4), "greedy_token": tok,
                    "llama8b_decode_kv_f16_ms_per_token": round(ms_h, 4), "greedy_token_kv_f16": tok_h}
+        elif args.only == "readprobe":
+            nb = 14336 * ROW_BYTES[Q4K](4096)  # the headline's weight bytes
+            small = time_read_probe(g, nb, 16, max(100, args.steps // 2), 20)
+            big = time_read_probe(g, 512 << 20, 2, 20, 4)
+            res = {"read_33MB_us": {f"{w}x{t}": round(v * 1e3, 3) for (w, t), v in small.items()},
+                   "read_512MB_us": {f"{w}x{t}": round(v * 1e3, 3) for (w, t), v in big.items()},
+                   "bytes": [nb, 512 << 20], "shape": "workgroups per CU x threads"}
         else:
             n = 1 if args.only == "moe1" else 32
             ms, _, _, _ = time_moe(g, n, max(40, args.steps // 10), eager=args.eager)
@@ -640,6 +687,15 @@ def main():
             b = algo_bytes(dt, r, c)
             extra[name] = {"us_kernel": round(k_ * 1e3, 3), "GB_s": round(b / (k_ * 1e-3) / 1e9, 1),
                            "frac_hbm": round(b / (k_ * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": b}
+        # the same weight bytes read by a plain streaming kernel, best of its launch shapes:
+        # the ceiling a dependent 33 MB launch can reach on this GPU
+        nb = 14336 * ROW_BYTES[Q4K](4096)
+        rd = time_read_probe(g, nb, 16, max(100, args.steps // 5), 20)
+        (bw, bt), best = min(rd.items(), key=lambda kv: kv[1])
+        extra["plain_read_33MB"] = {"us_kernel": round(best * 1e3, 3), "GB_s": round(nb / (best * 1e-3) / 1e9, 1),
+                                    "frac_hbm": round(nb / (best * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": nb,
+                                    "shape": f"{bw} workgroups per CU x {bt} threads (best of {len(rd)})",
+                                    "headline_vs_read": round(best / ms, 4)}
         if not args.no_cpu:
             extra["q6_k_head_128256x4096"]["parity_vs_cpu"] = head_parity(g, args.cpu_threads)
         mm_n = 64

@@ -166,6 +166,8 @@ int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, b
 int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
                      uint64_t stream);
 int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream);
+int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads, uint32_t *out,
+                      size_t out_len);
 // (k_moe.hip) -- device scratch of one MoE FFN call
 struct MoeScratch {
     float *logits = nullptr; // n x n_exp

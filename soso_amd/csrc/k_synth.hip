@@ -141,3 +141,29 @@ int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t
     synth_normal_k<<<(unsigned)((n + T - 1) / T), T, 0, h->stream>>>(dst, (long)n, sigma, seed, stream);
     return hip_check(h, hipGetLastError(), "synth normal launch");
 }
+
+// ---------------------------------------------------------------------------
+// Plain streaming read: the bandwidth reference the matvec kernels are held
+// against (bench.py --only readprobe).  Grid-stride over n16 16-byte words,
+// one load per thread per step; the xor of everything a thread read goes to
+// out[thread] (threads past out_len keep theirs: the store is conditional at
+// run time, so no load is dead either way).
+// ---------------------------------------------------------------------------
+__global__ void read_probe_k(const uint4 *__restrict__ p, size_t n16, uint32_t *__restrict__ out, size_t out_len)
+{
+    const size_t T = (size_t)gridDim.x * blockDim.x, t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    uint32_t acc = 0;
+    for (size_t i = t; i < n16; i += T) {
+        const uint4 v = p[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (t < out_len) out[t] = acc;
+}
+
+int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads, uint32_t *out,
+                      size_t out_len)
+{
+    const unsigned grid = wg_per_cu * (unsigned)h->num_cu;
+    read_probe_k<<<grid, threads, 0, h->stream>>>((const uint4 *)src, bytes / 16, out, out_len);
+    return hip_check(h, hipGetLastError(), "read probe launch");
+}

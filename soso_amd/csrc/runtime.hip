@@ -909,6 +909,18 @@ int soso_hip_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64
     return launch_synth_normal(h, dst, n, sigma, seed, stream);
 }
 
+int soso_hip_read_probe(soso_hip *h, const void *src_dev, size_t bytes, uint32_t wg_per_cu, uint32_t threads,
+                        uint32_t *out_dev, size_t out_len)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!src_dev || !out_dev || bytes < 16 || wg_per_cu == 0 || wg_per_cu > 32 || threads == 0 || threads > 1024 ||
+        threads % 64)
+        return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    return launch_read_probe(h, src_dev, bytes, wg_per_cu, threads, out_dev, out_len);
+}
+
 int soso_hip_weight_synth(soso_hip *h, const char *key, size_t key_len, uint8_t dtype, size_t rows, size_t cols,
                           uint64_t seed, uint64_t stream)
 {
