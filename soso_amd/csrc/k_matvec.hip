@@ -445,16 +445,17 @@ static bool strip_fits(int passes, int groups, size_t pass_bytes)
 
 // Ring depth (passes in flight per wavefront) and issue order, measured on
 // MI355X (back-to-back launches over rotating weights above the MALL size):
-//   Q4_K 14336 x 4096: depth 2, ring loads before x's conversion (8.4 us;
+//   Q4_K 14336 x 4096: depth 2, ring loads before x's conversion (7.7 us;
 //     depth 8 x-first 11.0 us -- with all of a wavefront's rows in flight at
 //     once every wavefront's first row arrives late and the math cannot
-//     overlap the stream);  Q8_0 4096 x 4096: depth 3 (5.8 us);
-//   Q6_K 128256 x 4096: depth 4 (74.4 us);  split rows 4096 x 14336: depth 2;
+//     overlap the stream);  Q8_0 4096 x 4096: depth 2 (5.6 us; 5.9 at depth 3,
+//     6.3 at 4: a wavefront has two rows, so deeper rings only read past them);
+//   Q6_K 128256 x 4096: depth 4 (79 us; 3 and 6 the same);  split rows 4096 x 14336: depth 2;
 //   narrow rows (LPR < 64, e.g. 768 x 2048): depth 2 with x staged first.
 // Split rows (S > 1) need a depth that divides the combine round.
 template <int FMT, int S> constexpr int ring_depth()
 {
-    return S > 1 ? 2 : FMT == FMT_Q4K ? 2 : FMT == FMT_Q80 ? 3 : 4;
+    return S > 1 ? 2 : FMT == FMT_Q6K ? 4 : 2;
 }
 template <int LPR> constexpr bool x_first() { return LPR < 64; }
 
