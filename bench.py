@@ -259,7 +259,8 @@ def time_decode_8b(g, steps, ctx=4096, seed=21, kv_f16=False, eager=False):
     soso's f16 KV instead, the same values rounded on upload); the step runs
     at position `ctx`.  The timed steps replay one HIP graph; eager=True launches
     them directly instead (for kernel tracers).  Returns (ms per token, bytes per
-    token, token)."""
+    token, token, ms per token of a host loop that launches a one-step graph and
+    reads the token back each step -- None when eager)."""
     L, H, NH, NKV, HDIM, F, V = 32, 4096, 32, 8, 128, 14336, 128256
     qd, kvd = NH * HDIM, NKV * HDIM
     name = "llama8b"
@@ -331,11 +332,27 @@ def time_decode_8b(g, steps, ctx=4096, seed=21, kv_f16=False, eager=False):
                 g.graph_destroy(gid)
         ms = g.event_elapsed(0, 1) / steps
         token = int(g.d2h(tok, (1,), np.uint32)[0])
+        # a serving loop's view: one step per graph launch, the host waiting
+        # for each token (launch, sync and the 4-byte token read per step)
+        host_ms = None
+        if not eager:
+            gid1 = _capture(g, lambda: g.decode_step_dev(name, x, ctx, None, tok))
+            try:
+                g.graph_launch(gid1)
+                g.sync()
+                n1 = max(10, steps // 2)
+                t0 = time.perf_counter()
+                for _ in range(n1):
+                    g.graph_launch(gid1)
+                    g.d2h(tok, (1,), np.uint32)
+                host_ms = (time.perf_counter() - t0) * 1e3 / n1
+            finally:
+                g.graph_destroy(gid1)
         per_layer = (qd + 2 * kvd) * (H // 256) * 144 + H * (qd // 256) * 144 + 2 * F * (H // 256) * 144 \
             + H * (F // 256) * 144
         nbytes = L * per_layer + V * (H // 256) * 210 + L * 2 * (ctx + 1) * kvd * (2 if kv_f16 else 4) \
             + (2 * L + 1) * H * 4
-        return ms, nbytes, token
+        return ms, nbytes, token, host_ms
     finally:
         g.dev_free(x)
         g.dev_free(tok)
@@ -634,9 +651,9 @@ def main():
             res = {"q4_k_matmul_14336x4096_n64_us": round(ms * 1e3, 3)}
         elif args.only == "decode":
             print("decode: f32 KV", file=sys.stderr, flush=True)
-            ms, _, tok = time_decode_8b(g, max(10, args.steps // 50), eager=args.eager)
+            ms, _, tok, _ = time_decode_8b(g, max(10, args.steps // 50), eager=args.eager)
             print("decode: f16 KV", file=sys.stderr, flush=True)
-            ms_h, _, tok_h = time_decode_8b(g, max(10, args.steps // 50), kv_f16=True, eager=args.eager)
+            ms_h, _, tok_h, _ = time_decode_8b(g, max(10, args.steps // 50), kv_f16=True, eager=args.eager)
             res = {"llama8b_decode_ms_per_token": round(ms, 4), "greedy_token": tok,
                    "llama8b_decode_kv_f16_ms_per_token": round(ms_h, 4), "greedy_token_kv_f16": tok_h}
         elif args.only == "readprobe":
@@ -712,12 +729,13 @@ def main():
                 "us_per_layer": round(ms_m * 1e3, 3), "tokens_per_s_layer": round(n / (ms_m * 1e-3), 1),
                 "GB_s": round(b_m / (ms_m * 1e-3) / 1e9, 1), "frac_hbm": round(b_m / (ms_m * 1e-3) / 1e9 / PEAK_GBS, 4),
                 "bytes": int(b_m), "distinct_experts": round(u_m, 2)}
-        ms_d, b_d, tok_d = time_decode_8b(g, max(10, args.steps // 50))
+        ms_d, b_d, tok_d, host_d = time_decode_8b(g, max(10, args.steps // 10))
         extra["llama8b_decode_ctx4096"] = {
             "ms_per_token": round(ms_d, 4), "tokens_per_s": round(1e3 / ms_d, 1),
             "GB_s": round(b_d / (ms_d * 1e-3) / 1e9, 1), "frac_hbm": round(b_d / (ms_d * 1e-3) / 1e9 / PEAK_GBS, 4),
-            "bytes_per_token": int(b_d), "greedy_token": tok_d}
-        ms_h, b_h, tok_h = time_decode_8b(g, max(10, args.steps // 50), kv_f16=True)
+            "bytes_per_token": int(b_d), "greedy_token": tok_d,
+            "host_loop_ms_per_token": round(host_d, 4)}
+        ms_h, b_h, tok_h, _ = time_decode_8b(g, max(10, args.steps // 10), kv_f16=True)
         extra["llama8b_decode_ctx4096_kv_f16"] = {
             "ms_per_token": round(ms_h, 4), "tokens_per_s": round(1e3 / ms_h, 1),
             "GB_s": round(b_h / (ms_h * 1e-3) / 1e9, 1), "frac_hbm": round(b_h / (ms_h * 1e-3) / 1e9 / PEAK_GBS, 4),
