@@ -81,6 +81,7 @@ struct DecodeModel {
     void *kcache = nullptr, *vcache = nullptr;  // [n_layers][n_kv_heads][ctx_max][head_dim]
     void *mem = nullptr;                         // activations below, one allocation
     float *hid = nullptr, *qbuf = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
+    float *rope_freq = nullptr; // head_dim / 2 floats
 };
 
 constexpr size_t SOSO_TICKET_BYTES = 16384;
@@ -139,6 +140,10 @@ struct MvEpi {
     int q_dim = 0, kv_dim = 0, head_dim = 0, pos = 0;
     size_t kv_stride = 0;
     float theta = 0.0f;
+    // head_dim / 2 RoPE frequencies theta^(-2i / head_dim), computed on the
+    // host with the C library's powf as the reference does on its CPU; the
+    // angle pos * freq is then the same f32 product (null: powf on the device)
+    const float *rope_freq = nullptr;
 };
 
 // packed layouts (k_matvec.hip)

@@ -341,6 +341,7 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         ep.head_dim = (int)m.head_dim;
         ep.pos = (int)pos;
         ep.theta = m.theta;
+        ep.rope_freq = m.rope_freq;
         rc = launch_matvec_ex(h, *L.qkv, in, qb, ep, XS_RMSNORM, EPI_QKV);
         if (rc == SOSO_HIP_OK)
             rc = launch_attention(h, qb, K, V, m.kv_f16, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim,

@@ -184,7 +184,8 @@ __device__ __forceinline__ void rope_angle(const MvEpi &ep, int r, float &cs, fl
     sn = 0.0f;
     if (r < qk) {
         const int d = (r < ep.q_dim ? r : r - ep.q_dim) % ep.head_dim;
-        const float fr = powf(ep.theta, -2.0f * (float)(d >> 1) / (float)ep.head_dim);
+        const float fr = ep.rope_freq ? ep.rope_freq[d >> 1]
+                                      : powf(ep.theta, -2.0f * (float)(d >> 1) / (float)ep.head_dim);
         sincosf((float)ep.pos * fr, &sn, &cs);
     }
 }

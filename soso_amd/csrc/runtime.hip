@@ -719,7 +719,8 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     // KV cache and step buffers
     const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
     const size_t chunks = (cfg->ctx_max + 63) / 64;
-    const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64;
+    const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64 +
+                              cfg->head_dim / 2;
     const size_t mem_bytes = act_floats * 4;
     if (rc == SOSO_HIP_OK) {
         if (hipMalloc(&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, mem_bytes) != hipSuccess)
@@ -740,6 +741,18 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     m.act = m.att + qd;
     m.part = m.act + F;
     m.logits = m.part + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2);
+    m.rope_freq = m.logits + cfg->vocab + 64;
+    {
+        // rope_cabezas (gemm.rs:1468-1470): freq_i = powf(theta, -2 i / head_dim) in f32
+        std::vector<float> fr(cfg->head_dim / 2);
+        const float n_f = (float)cfg->head_dim;
+        for (size_t i = 0; i < fr.size(); i++) fr[i] = powf(cfg->rope_theta, -2.0f * (float)i / n_f);
+        rc = hip_check(h, hipMemcpy(m.rope_freq, fr.data(), fr.size() * 4, hipMemcpyHostToDevice), "rope table");
+        if (rc != SOSO_HIP_OK) {
+            decode_free(h, m);
+            return rc;
+        }
+    }
     std::string key(model_key, model_key_len);
     auto old = h->decode_models.find(key);
     if (old != h->decode_models.end()) {

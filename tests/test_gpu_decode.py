@@ -220,6 +220,55 @@ def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill, kv_f16)
             gpu.weight_drop(k)
 
 
+def test_decode_8b_layer_shape_matches_cpu(gpu, orc):
+    """configs[4] at its real layer shape and context: one layer of hidden 4096,
+    32 / 8 heads of 128 and FFN 14336 (synthetic Q4_K blocks like the bench's),
+    at position 4096 of an f32 KV cache, then a 512-row Q8_0 head.  Same bar as
+    above: logits within relative L2 1e-5 of the oracle's composition, the
+    K / V rows of the step within 1e-5."""
+    H, nh, nkv, F, V, ctx, theta, eps = 4096, 32, 8, 14336, 512, 4097, 500000.0, 1e-5
+    m = Model.__new__(Model)
+    m.L, m.H, m.nh, m.nkv, m.F, m.V = 1, H, nh, nkv, F, V
+    m.qd, m.kvd = nh * HD, nkv * HD
+    m.name = "dec8b.layer"
+    sy = lambda r, c, st: orc.synth(Q4K, r, c, 61, st)
+    m.layers = [{"attn_norm": (1.0 + orc.normal(H, 0.1, 61, 1)).astype(np.float32),
+                 "ffn_norm": (1.0 + orc.normal(H, 0.1, 61, 2)).astype(np.float32),
+                 "q": sy(m.qd, H, 3), "k": sy(m.kvd, H, 4), "v": sy(m.kvd, H, 5), "o": sy(H, m.qd, 6),
+                 "gate": sy(F, H, 7), "up": sy(F, H, 8), "down": sy(H, F, 9)}]
+    m.out_norm = (1.0 + orc.normal(H, 0.1, 61, 10)).astype(np.float32)
+    m.head, m.head_dtype = quant(orc, Q8, orc.normal(V * H, 0.05, 61, 11)), Q8
+    m.upload(gpu)
+    name = m.name + ".model"
+    cfg = dict(n_layers=1, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=theta, rms_eps=eps)
+    print("decode 8B layer shape at position 4096", flush=True)
+    gpu.decode_create(name, cfg, m.keys)
+    pos = ctx - 1
+    kc = np.zeros((1, ctx, m.kvd), np.float32)
+    vc = np.zeros((1, ctx, m.kvd), np.float32)
+    kc[0, :pos] = orc.normal(pos * m.kvd, 1.0, 62, 1).reshape(pos, m.kvd)
+    vc[0, :pos] = orc.normal(pos * m.kvd, 1.0, 62, 2).reshape(pos, m.kvd)
+    gpu.decode_kv_upload(name, 0, 0, kc[0, :pos], vc[0, :pos], rows_f32=True)
+    x = orc.normal(H, 1.0, 63, 1)
+    xd, ld, rd = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(2 * m.kvd * 4)
+    try:
+        gpu.h2d(xd, x)
+        gpu.decode_step_dev(name, xd, pos, ld, None, rd)
+        gpu.sync()
+        logits = gpu.d2h(ld, (V,), np.float32)
+        rows = gpu.d2h(rd, (2, m.kvd), np.float32)
+        ref, _ = m.cpu_step(orc, x, kc, vc, pos, theta, eps)
+        assert orc.rel_l2(rows[0], kc[0, pos]) < 1e-5 and orc.rel_l2(rows[1], vc[0, pos]) < 1e-5
+        assert orc.rel_l2(logits, ref) < 1e-5, orc.rel_l2(logits, ref)
+    finally:
+        for p in (xd, ld, rd):
+            gpu.dev_free(p)
+        gpu.decode_destroy(name)
+        for k in m.keys:
+            gpu.weight_drop(k)
+
+
 def test_decode_step_input_alignment(gpu, orc):
     """The step reads an aligned x in place and copies an unaligned one first:
     the same bits either way."""
