@@ -220,7 +220,8 @@ def test_decode_step_matches_cpu(gpu, orc, L, H, nh, nkv, F, V, prefill, kv_f16)
             gpu.weight_drop(k)
 
 
-def test_decode_8b_layer_shape_matches_cpu(gpu, orc):
+@pytest.mark.parametrize("kv_f16", [0, 1])
+def test_decode_8b_layer_shape_matches_cpu(gpu, orc, kv_f16):
     """configs[4] at its real layer shape and context: one layer of hidden 4096,
     32 / 8 heads of 128 and FFN 14336 (synthetic Q4_K blocks like the bench's),
     at position 4096 of an f32 KV cache, then a 512-row Q8_0 head.  Same bar as
@@ -241,15 +242,19 @@ def test_decode_8b_layer_shape_matches_cpu(gpu, orc):
     m.upload(gpu)
     name = m.name + ".model"
     cfg = dict(n_layers=1, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
-               rope_theta=theta, rms_eps=eps)
-    print("decode 8B layer shape at position 4096", flush=True)
+               rope_theta=theta, rms_eps=eps, kv_f16=kv_f16)
+    print(f"decode 8B layer shape at position 4096, kv_f16={kv_f16}", flush=True)
     gpu.decode_create(name, cfg, m.keys)
     pos = ctx - 1
     kc = np.zeros((1, ctx, m.kvd), np.float32)
     vc = np.zeros((1, ctx, m.kvd), np.float32)
-    kc[0, :pos] = orc.normal(pos * m.kvd, 1.0, 62, 1).reshape(pos, m.kvd)
-    vc[0, :pos] = orc.normal(pos * m.kvd, 1.0, 62, 2).reshape(pos, m.kvd)
-    gpu.decode_kv_upload(name, 0, 0, kc[0, :pos], vc[0, :pos], rows_f32=True)
+    kr = orc.normal(pos * m.kvd, 1.0, 62, 1).reshape(pos, m.kvd)
+    vr = orc.normal(pos * m.kvd, 1.0, 62, 2).reshape(pos, m.kvd)
+    gpu.decode_kv_upload(name, 0, 0, kr, vr, rows_f32=True)  # the library rounds to f16 when kv_f16
+    if kv_f16:
+        kr = orc.f16_to_f32(orc.f32_to_f16(kr)).reshape(kr.shape)
+        vr = orc.f16_to_f32(orc.f32_to_f16(vr)).reshape(vr.shape)
+    kc[0, :pos], vc[0, :pos] = kr, vr
     x = orc.normal(H, 1.0, 63, 1)
     xd, ld, rd = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(2 * m.kvd * 4)
     try:
@@ -257,9 +262,17 @@ def test_decode_8b_layer_shape_matches_cpu(gpu, orc):
         gpu.decode_step_dev(name, xd, pos, ld, None, rd)
         gpu.sync()
         logits = gpu.d2h(ld, (V,), np.float32)
-        rows = gpu.d2h(rd, (2, m.kvd), np.float32)
-        ref, _ = m.cpu_step(orc, x, kc, vc, pos, theta, eps)
-        assert orc.rel_l2(rows[0], kc[0, pos]) < 1e-5 and orc.rel_l2(rows[1], vc[0, pos]) < 1e-5
+        ref, _ = m.cpu_step(orc, x, kc, vc, pos, theta, eps, kv_f16=bool(kv_f16))
+        k32, v32 = m.last_kv
+        if kv_f16:
+            rows = gpu.d2h(rd, (2, m.kvd), np.uint16)
+            for got, ref32 in ((rows[0], k32[0]), (rows[1], v32[0])):
+                e_gpu = orc.rel_l2(orc.f16_to_f32(got), ref32)
+                e_orc = orc.rel_l2(orc.f16_to_f32(orc.f32_to_f16(ref32)), ref32)
+                assert e_gpu <= e_orc + 1e-5, (e_gpu, e_orc)
+        else:
+            rows = gpu.d2h(rd, (2, m.kvd), np.float32)
+            assert orc.rel_l2(rows[0], k32[0]) < 1e-5 and orc.rel_l2(rows[1], v32[0]) < 1e-5
         assert orc.rel_l2(logits, ref) < 1e-5, orc.rel_l2(logits, ref)
     finally:
         for p in (xd, ld, rd):
