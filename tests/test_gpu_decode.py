@@ -26,7 +26,7 @@ import pytest
 
 pytestmark = pytest.mark.gpu
 
-Q4K, Q8, F32 = 3, 2, 1
+Q4K, Q8, F32, Q6K = 3, 2, 1, 13
 HD = 128
 
 
@@ -280,6 +280,82 @@ def test_decode_8b_layer_shape_matches_cpu(gpu, orc, kv_f16):
         gpu.decode_destroy(name)
         for k in m.keys:
             gpu.weight_drop(k)
+
+
+def test_decode_8b_full_step_matches_cpu(gpu, orc):
+    """configs[4] end to end: the bench's 8B step (32 layers at the 8B shape,
+    Q6_K head over 128256, f32 KV prefilled with N(0, 1) to position 4096) on
+    the same seeded bytes as the CPU's composition.  The weights are made by
+    the device generator and read back, so both sides hold the same bytes (the
+    generators agree byte for byte: test_synth_device_equals_host).  Bar:
+    logits within relative L2 1e-5, the greedy token equal."""
+    L, H, nh, nkv, F, V, ctx, theta, eps = 32, 4096, 32, 8, 14336, 128256, 4097, 500000.0, 1e-5
+    m = Model.__new__(Model)
+    m.L, m.H, m.nh, m.nkv, m.F, m.V = L, H, nh, nkv, F, V
+    m.qd, m.kvd = nh * HD, nkv * HD
+    m.name = "dec8b.full"
+
+    def raw(dtype, rows, cols, stream):
+        nb = rows * (cols // 256) * (144 if dtype == Q4K else 210)
+        d = gpu.dev_alloc(nb)
+        try:
+            gpu.synth_raw(d, dtype, rows, cols, 71, stream)
+            return gpu.d2h(d, (nb,), np.uint8)
+        finally:
+            gpu.dev_free(d)
+
+    print("decode 8B full step: generating weights", flush=True)
+    m.layers = []
+    st = 0
+    for l in range(L):
+        lw = {"attn_norm": (1.0 + orc.normal(H, 0.1, 72, 2 * l)).astype(np.float32),
+              "ffn_norm": (1.0 + orc.normal(H, 0.1, 72, 2 * l + 1)).astype(np.float32)}
+        for nm in ("q", "k", "v", "o", "gate", "up", "down"):
+            _, r, c = m.shapes(nm)
+            st += 1
+            lw[nm] = raw(Q4K, r, c, st)
+        m.layers.append(lw)
+    m.out_norm = (1.0 + orc.normal(H, 0.1, 72, 999)).astype(np.float32)
+    m.head, m.head_dtype = raw(Q6K, V, H, 10001), Q6K
+    m.upload(gpu)
+    name = m.name + ".model"
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=theta, rms_eps=eps)
+    gpu.decode_create(name, cfg, m.keys, drop_sources=True)
+    pos = ctx - 1
+    kc = np.zeros((L, ctx, m.kvd), np.float32)
+    vc = np.zeros((L, ctx, m.kvd), np.float32)
+    xd, ld, td = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(4)
+    try:
+        for l in range(L):
+            kd, vd = gpu.decode_kv_dev(name, l)
+            gpu.synth_normal(kd, ctx * m.kvd, 1.0, 73, 2 * l)
+            gpu.synth_normal(vd, ctx * m.kvd, 1.0, 73, 2 * l + 1)
+            # head-major on the device, position-major on the CPU side
+            kc[l] = gpu.d2h(kd, (nkv, ctx, HD), np.float32).transpose(1, 0, 2).reshape(ctx, m.kvd)
+            vc[l] = gpu.d2h(vd, (nkv, ctx, HD), np.float32).transpose(1, 0, 2).reshape(ctx, m.kvd)
+        x = orc.normal(H, 1.0, 74, 1)
+        gpu.h2d(xd, x)
+        print("decode 8B full step: GPU step", flush=True)
+        gpu.decode_step_dev(name, xd, pos, ld, td)
+        gpu.sync()
+        logits = gpu.d2h(ld, (V,), np.float32)
+        token = int(gpu.d2h(td, (1,), np.uint32)[0])
+        print("decode 8B full step: CPU step", flush=True)
+        ref, ref_token = m.cpu_step(orc, x, kc, vc, pos, theta, eps)
+        assert orc.rel_l2(logits, ref) < 1e-5, orc.rel_l2(logits, ref)
+        top2 = np.sort(ref)[-2:]
+        if top2[1] - top2[0] > 1e-3 * max(1.0, abs(float(top2[1]))):
+            assert token == ref_token, (token, ref_token)
+    finally:
+        for p in (xd, ld, td):
+            gpu.dev_free(p)
+        gpu.decode_destroy(name)
+        for k in m.keys:
+            try:
+                gpu.weight_drop(k)
+            except Exception:  # noqa: BLE001 -- the q/k/v/gate/up sources were dropped with drop_sources
+                pass
 
 
 def test_decode_step_input_alignment(gpu, orc):
