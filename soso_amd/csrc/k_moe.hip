@@ -38,8 +38,8 @@
 // then lower index); NaN probabilities and removed experts carry key 0 and
 // are never chosen -- should fewer than top_k experts remain, the slot points
 // at expert 0 with weight 0 (indices stay valid).  `sel`: top_k floats of LDS.
-__device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *__restrict__ idx,
-                          float *__restrict__ wgt, float *sel, int16_t *rank_lds)
+// The softmax and the ranking keys of one token's logits, by one wavefront.
+__device__ __forceinline__ void topk_keys(const float (&lg)[4], int n_exp, uint64_t (&key)[4])
 {
     const int lane = threadIdx.x & 63;
     const float m = wave_max_dpp(fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3])));
@@ -50,7 +50,6 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
         s += ex[q];
     }
     s = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(seg_sum_dpp<64>(s)), 63));
-    uint64_t key[4];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int e = lane + 64 * q;
@@ -58,6 +57,14 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
         const uint32_t k32 = e < n_exp && p >= 0.0f ? __float_as_uint(p) + 1u : 0u;
         key[q] = ((uint64_t)k32 << 32) | (uint32_t)(0xFFFF - e);
     }
+}
+
+__device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *__restrict__ idx,
+                          float *__restrict__ wgt, float *sel, int16_t *rank_lds)
+{
+    const int lane = threadIdx.x & 63;
+    uint64_t key[4];
+    topk_keys(lg, n_exp, key);
     for (int j = 0; j < top_k; j++) {
         uint64_t best = key[0];
 #pragma unroll
@@ -453,9 +460,30 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
     const int passes = (rows + NW * RW - 1) / (NW * RW);
     __shared__ int32_t self_idx[MOE_SELF_K];
     __shared__ float self_wgt[MOE_SELF_K], self_sel[MOE_SELF_K];
-    __shared__ int16_t self_rank[MOE_SELF_K];
+    __shared__ __align__(16) uint32_t self_keys[256];
     int nit;
     if constexpr (SELF) {
+        // The ranking of topk_regs, by the whole workgroup: wavefront 0 makes
+        // the keys (topk_keys; the upper word is the order, 0 for experts
+        // that cannot be chosen, the lower word breaks ties to the lower
+        // index).  Expert e's rank is then the number of experts i with
+        // k[i] > k[e], or k[i] == k[e] and i < e, counted by tpe adjacent
+        // threads over one share each of the 256 zero-padded upper words.
+        // Ranks below top_k fill the slots; slots no valid expert reaches
+        // keep expert 0 with weight 0, as in topk_regs.
+        // The one token's x row (every slot's row is row 0: xdiv = top_k) is
+        // staged into LDS here, once; its loads are in flight with the logits'.
+        float4 xv0[MOE_XK], xv1[MOE_XK];
+#pragma unroll
+        for (int k = 0; k < MOE_XK; k++) {
+            const int f = k * 512 + (int)threadIdx.x;
+            xv0[k] = xv1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (f < nch) {
+                const float4 *x4 = (const float4 *)xs + 2 * f;
+                xv0[k] = x4[0];
+                xv1[k] = x4[1];
+            }
+        }
         if (wave == 0) {
             float lg[4];
 #pragma unroll
@@ -463,7 +491,71 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                 const int x = lane + 64 * q;
                 lg[q] = x < sr.n_exp ? sr.logits[x] : -INFINITY;
             }
-            topk_regs(lg, sr.n_exp, sr.top_k, self_idx, self_wgt, self_sel, self_rank);
+            uint64_t key[4];
+            topk_keys(lg, sr.n_exp, key);
+#pragma unroll
+            for (int q = 0; q < 4; q++) self_keys[lane + 64 * q] = (uint32_t)(key[q] >> 32);
+            if (lane < sr.top_k) {
+                self_idx[lane] = 0;
+                self_sel[lane] = 0.0f;
+            }
+        }
+        {
+            uint32_t *xd = (uint32_t *)smem;
+            float *s16 = (float *)(xd + (cols >> 2) * XDIG);
+            int *kx = (int *)(s16 + (cols >> 4));
+#pragma unroll
+            for (int k = 0; k < MOE_XK; k++) {
+                const int f = k * 512 + (int)threadIdx.x;
+                if (k * 512 < nch) stage_chunk<FMT>(xv0[k], xv1[k], f % nch, f < nch, U, xd, s16, kx);
+            }
+            for (int fb = MOE_XK * 512; fb < nch; fb += 512) { // rows longer than one round holds
+                const int f = fb + (int)threadIdx.x;
+                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+                if (f < nch) {
+                    const float4 *x4 = (const float4 *)xs + 2 * f;
+                    v0 = x4[0];
+                    v1 = x4[1];
+                }
+                stage_chunk<FMT>(v0, v1, f % nch, f < nch, U, xd, s16, kx);
+            }
+        }
+        __syncthreads();
+        {
+            const int tpe = sr.n_exp <= 64 ? 8 : sr.n_exp <= 128 ? 4 : 2; // threads per expert
+            const int ex = (int)threadIdx.x / tpe, part = (int)threadIdx.x % tpe;
+            const uint32_t mine = self_keys[ex];
+            // share: n4 groups of 4 keys; tpe * 4 * n4 <= 256 for n_exp <= 256
+            const int n4 = (sr.n_exp + 4 * tpe - 1) / (4 * tpe);
+            const uint4 *kv = (const uint4 *)self_keys + part * n4;
+            int above = 0, i = 4 * part * n4;
+#pragma unroll 8
+            for (int g = 0; g < n4; g++, i += 4) {
+                const uint4 k = kv[g];
+                above += (k.x > mine || (k.x == mine && i < ex)) ? 1 : 0;
+                above += (k.y > mine || (k.y == mine && i + 1 < ex)) ? 1 : 0;
+                above += (k.z > mine || (k.z == mine && i + 2 < ex)) ? 1 : 0;
+                above += (k.w > mine || (k.w == mine && i + 3 < ex)) ? 1 : 0;
+            }
+            // the tpe counts of an expert sit in adjacent lanes
+            float fa = (float)above;
+            if (tpe >= 2) fa += dpp_f<0xB1>(fa);
+            if (tpe >= 4) fa += dpp_f<0x4E>(fa);
+            if (tpe >= 8) fa += dpp_f<0x141>(fa);
+            const int rank = (int)fa;
+            if (part == 0 && ex < sr.n_exp && mine != 0u && rank < sr.top_k) {
+                self_idx[rank] = ex;
+                self_sel[rank] = __uint_as_float(mine - 1u);
+            }
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < sr.top_k) {
+            float tot = 0.0f;
+#pragma unroll
+            for (int j = 0; j < MOE_SELF_K; j++)
+                if (j < sr.top_k) tot += self_sel[j];
+            const float sj = self_sel[threadIdx.x];
+            self_wgt[threadIdx.x] = tot > 0.0f ? sj / tot : sj;
         }
         __syncthreads();
         if (blockIdx.x == 0 && (int)threadIdx.x < sr.top_k) {
@@ -500,19 +592,22 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
         for (int t0 = 0; t0 < ne; t0 += tch) {
             const int nt = min(tch, ne - t0), tot = nt * nch;
             // 1. x of the tokens: chunk f = token (f / nch), piece (f % nch)
+            // (the self-ranked path staged its one row before the ranking)
             float4 xv0[MOE_XK], xv1[MOE_XK];
+            if constexpr (!SELF) {
 #pragma unroll
-            for (int k = 0; k < MOE_XK; k++) {
-                const int f = k * 512 + (int)threadIdx.x;
-                xv0[k] = xv1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (f < tot) {
-                    const int sl = SELF ? self_slot : list[base + t0 + f / nch];
-                    const float4 *x4 = (const float4 *)(xs + (size_t)(sl / xdiv) * cols) + 2 * (f % nch);
-                    xv0[k] = x4[0];
-                    xv1[k] = x4[1];
+                for (int k = 0; k < MOE_XK; k++) {
+                    const int f = k * 512 + (int)threadIdx.x;
+                    xv0[k] = xv1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (f < tot) {
+                        const int sl = list[base + t0 + f / nch];
+                        const float4 *x4 = (const float4 *)(xs + (size_t)(sl / xdiv) * cols) + 2 * (f % nch);
+                        xv0[k] = x4[0];
+                        xv1[k] = x4[1];
+                    }
                 }
+                if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = list[base + t0 + threadIdx.x];
             }
-            if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = SELF ? self_slot : list[base + t0 + threadIdx.x];
             __builtin_amdgcn_sched_barrier(0);
             // 2. the ring
             WRow<FMT> wa[DEPTH], wb[DEPTH];
@@ -523,32 +618,34 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
             }
             __builtin_amdgcn_sched_barrier(0);
             // 3. x into LDS (16-chunk blocks never straddle tokens: nch % 16 == 0)
+            if constexpr (!SELF) {
 #pragma unroll
-            for (int k = 0; k < MOE_XK; k++) {
-                const int fb = k * 512;
-                if (fb < tot) {
+                for (int k = 0; k < MOE_XK; k++) {
+                    const int fb = k * 512;
+                    if (fb < tot) {
+                        const int f = fb + (int)threadIdx.x, tk = f / nch;
+                        uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)(f < tot ? tk : 0) * tok_bytes);
+                        float *s16 = (float *)(xd + (cols >> 2) * XDIG);
+                        int *kx = (int *)(s16 + (cols >> 4));
+                        stage_chunk<FMT>(xv0[k], xv1[k], f % nch, f < tot, U, xd, s16, kx);
+                    }
+                }
+                for (int fb = MOE_XK * 512; fb < tot; fb += 512) { // more tokens than one round holds
                     const int f = fb + (int)threadIdx.x, tk = f / nch;
+                    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+                    if (f < tot) {
+                        const int sl = list[base + t0 + tk];
+                        const float4 *x4 = (const float4 *)(xs + (size_t)(sl / xdiv) * cols) + 2 * (f % nch);
+                        v0 = x4[0];
+                        v1 = x4[1];
+                    }
                     uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)(f < tot ? tk : 0) * tok_bytes);
                     float *s16 = (float *)(xd + (cols >> 2) * XDIG);
                     int *kx = (int *)(s16 + (cols >> 4));
-                    stage_chunk<FMT>(xv0[k], xv1[k], f % nch, f < tot, U, xd, s16, kx);
+                    stage_chunk<FMT>(v0, v1, f % nch, f < tot, U, xd, s16, kx);
                 }
+                __syncthreads();
             }
-            for (int fb = MOE_XK * 512; fb < tot; fb += 512) { // more tokens than one round holds
-                const int f = fb + (int)threadIdx.x, tk = f / nch;
-                float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
-                if (f < tot) {
-                    const int sl = SELF ? self_slot : list[base + t0 + tk];
-                    const float4 *x4 = (const float4 *)(xs + (size_t)(sl / xdiv) * cols) + 2 * (f % nch);
-                    v0 = x4[0];
-                    v1 = x4[1];
-                }
-                uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)(f < tot ? tk : 0) * tok_bytes);
-                float *s16 = (float *)(xd + (cols >> 2) * XDIG);
-                int *kx = (int *)(s16 + (cols >> 4));
-                stage_chunk<FMT>(v0, v1, f % nch, f < tot, U, xd, s16, kx);
-            }
-            __syncthreads();
             // 4. passes through the ring: counted whole turns, then the rest.
             // Q4_K: each pass's rows are decoded once (q4k_prep) and the ring
             // slot is refilled before the tokens are applied; a token's x is
@@ -561,7 +658,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                     q4k_token_dot<LPR, NMAT>(pr, xd, cols, U, u, uact, val);
                     float v = val[0];
                     if constexpr (NMAT == 2) v = silu(val[0]) * val[1];
-                    if (ul == LPR - 1 && row < rend) out[(size_t)slot_s[tk] * rows + row] = v;
+                    if (ul == LPR - 1 && row < rend) out[(size_t)(SELF ? self_slot : slot_s[tk]) * rows + row] = v;
                 }
             };
             auto pass = [&](int j, const WRow<FMT> &pa_w, const WRow<FMT> &pb_w) {
@@ -578,7 +675,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                         const float pb = seg_sum_dpp<LPR>(uact ? unit_dot<FMT>(pb_w, xv, cj) : 0.0f);
                         v = silu(v) * pb;
                     }
-                    if (ul == LPR - 1 && row < rend) out[(size_t)slot_s[tk] * rows + row] = v;
+                    if (ul == LPR - 1 && row < rend) out[(size_t)(SELF ? self_slot : slot_s[tk]) * rows + row] = v;
                 }
             };
             const int turns = P / DEPTH;
@@ -616,7 +713,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                         pass(j0 + i, wa[i], wb[i]);
                     }
                 }
-            __syncthreads(); // LDS and slot_s are restaged next
+            if constexpr (!SELF) __syncthreads(); // LDS and slot_s are restaged next
         }
     }
 }
