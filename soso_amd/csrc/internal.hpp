@@ -159,6 +159,7 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y_dev,
 int launch_dequant(soso_hip *h, const Weight &w, float *out_dev);
 int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
 // (k_decode.hip)
+constexpr int ATT_CHUNK = 64; // positions per split of the decode attention (a multiple of 16)
 int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, bool kv_f16, int n_heads,
                      int n_kv_heads, int head_dim, int ctx, int T, float *part, float *out);
 int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token,

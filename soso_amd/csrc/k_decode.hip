@@ -26,16 +26,16 @@
 #include <cmath>
 #include <vector>
 
-constexpr int ATT_HD = 128;   // head_dim handled
-constexpr int ATT_CHUNK = 64; // positions per split
+constexpr int ATT_HD = 128;                // head_dim handled
+constexpr int ATT_NW = ATT_CHUNK / 16;     // wavefronts per split workgroup, 16 positions each
 
 // Split-K decode attention: k_attn_split writes one (m, l, acc) per chunk of
-// 64 positions and query head, k_attn_merge combines the chunks.  (The merge
+// ATT_CHUNK positions and query head, k_attn_merge combines the chunks.  (The merge
 // runs as its own launch: a merge by the last workgroup of each head in the
 // same launch needs a device-scope fence per wavefront, which writes back the
 // XCD's L2 each time and cost more than the launch it saves.)
 //
-// k_attn_split: grid (n_kv_heads, chunks), block 256.  Query heads g*G ..
+// k_attn_split: grid (n_kv_heads, chunks), block 64 * ATT_NW.  Query heads g*G ..
 // g*G + G - 1 share KV head g (GQA), so every K/V byte is read once for all G
 // heads.  K, V of one layer are head-major, [n_kv_heads][ctx][HD]: a chunk of
 // one head is 32 KB of contiguous HBM.  Wavefront w owns positions t0 + 16w ..
@@ -52,11 +52,11 @@ constexpr int ATT_CHUNK = 64; // positions per split
 // the four are merged in LDS into the chunk's (m, l, acc), stored at
 // part[(head * chunks + c) * (HD + 2)].
 template <int G, bool F16>
-__global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q, const void *__restrict__ Kc,
-                                                     const void *__restrict__ Vc, int ctx, int T, int chunks,
-                                                     float *__restrict__ part)
+__global__ void __launch_bounds__(64 * ATT_NW) k_attn_split(const float *__restrict__ q, const void *__restrict__ Kc,
+                                                             const void *__restrict__ Vc, int ctx, int T, int chunks,
+                                                             float *__restrict__ part)
 {
-    constexpr int HD = ATT_HD, NW = 4;
+    constexpr int HD = ATT_HD, NW = ATT_NW, NT = 64 * NW;
     __shared__ float qs[G * HD];
     __shared__ float wm[NW][G], wl[NW][G];
     __shared__ float2 accs[NW][G][HD / 2];
@@ -85,8 +85,13 @@ __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q,
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < G * HD / 4) qv = ((const float4 *)(q + (size_t)g * G * HD))[tid];
+    constexpr int QR = (G * HD / 4 + NT - 1) / NT; // float4 of the group's q per thread
+    float4 qv[QR];
+#pragma unroll
+    for (int r = 0; r < QR; r++) {
+        qv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tid + r * NT < G * HD / 4) qv[r] = ((const float4 *)(q + (size_t)g * G * HD))[tid + r * NT];
+    }
     __builtin_amdgcn_sched_barrier(0);
     // V: lane l holds dims 2l, 2l + 1 of the wavefront's 16 positions
     float2 vr[16];
@@ -100,7 +105,9 @@ __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q,
             vr[k] = *(const float2 *)((const float *)Vc + row);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (tid < G * HD / 4) *(float4 *)&qs[4 * tid] = qv;
+#pragma unroll
+    for (int r = 0; r < QR; r++)
+        if (tid + r * NT < G * HD / 4) *(float4 *)&qs[4 * (tid + r * NT)] = qv[r];
     if constexpr (F16) {
         // f16 -> f32 is exact; from here on the math is the f32 kernel's
 #pragma unroll
@@ -158,7 +165,7 @@ __global__ void __launch_bounds__(256) k_attn_split(const float *__restrict__ q,
         }
     }
     __syncthreads();
-    for (int e = tid; e < G * HD / 2; e += 256) {
+    for (int e = tid; e < G * HD / 2; e += NT) {
         const int hh = e / (HD / 2), dl = e % (HD / 2);
         float M = wm[0][hh];
 #pragma unroll
@@ -258,9 +265,9 @@ int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, 
 #define ATT_CASE(GG)                                                                                                \
     case GG:                                                                                                        \
         if (kv_f16)                                                                                                 \
-            k_attn_split<GG, true><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);                     \
+            k_attn_split<GG, true><<<grid, 64 * ATT_NW, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);             \
         else                                                                                                        \
-            k_attn_split<GG, false><<<grid, 256, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);                    \
+            k_attn_split<GG, false><<<grid, 64 * ATT_NW, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);            \
         break;
     switch (G) {
         ATT_CASE(1) ATT_CASE(2) ATT_CASE(4) ATT_CASE(8)

@@ -718,7 +718,7 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     }
     // KV cache and step buffers
     const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
-    const size_t chunks = (cfg->ctx_max + 63) / 64;
+    const size_t chunks = (cfg->ctx_max + ATT_CHUNK - 1) / ATT_CHUNK;
     const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64 +
                               cfg->head_dim / 2;
     const size_t mem_bytes = act_floats * 4;

@@ -145,6 +145,34 @@ def test_moe_ffn_dev_matches_cpu(gpu, orc, n_exp, h, ffn, top_k, n, dt_down):
         layer.drop(gpu)
 
 
+@pytest.mark.parametrize("n_exp", [64, 128, 200])
+def test_moe_ffn_dev_single_token_ties(gpu, orc, n_exp):
+    """One token whose router gives two groups of equal logits, the second
+    straddling the top-k cut: the expert kernels rank the token themselves
+    (8, 4 and 2 counting threads per expert at these widths) and must keep
+    the stable order of topk_softmax, lower index first, and the oracle's
+    weights and output."""
+    h, ffn, top_k = 512, 256, 6
+    layer = Layer(orc, n_exp, h, ffn, top_k, 77 + n_exp)
+    x = orc.normal(h, 1.0, 5, n_exp)
+    r = layer.router.reshape(n_exp, h)
+    first, second = [5, 33, n_exp - 1], [2, 9, 20, 47, n_exp - 2]
+    for e in first:
+        r[e] = np.float32(0.012) * x
+    for e in second:
+        r[e] = np.float32(0.008) * x
+    layer.upload(gpu)
+    try:
+        out, idx, wgt = moe_dev(gpu, layer, x)
+        ref, ri, rw = layer.cpu(orc, x)
+        assert list(ri) == first + second[:3]
+        assert np.array_equal(idx[0], ri), (idx[0], ri)
+        assert orc.rel_l2(wgt[0], rw) < TOL
+        assert orc.rel_l2(out[0], ref) < TOL
+    finally:
+        layer.drop(gpu)
+
+
 def test_experts_block_host_path(gpu, orc):
     """expertos_bloque: the caller groups tokens by expert (here from the CPU
     routing); suma = weighted sum over the resolved experts in ranking order."""
