@@ -6,24 +6,28 @@
 // Exact integer arithmetic, as in the single-token kernels: x is staged as
 // three balanced signed base-256 digits of X = rint(x 2^e), one exponent e per
 // 256-element super-block (|X| <= 2^22), and the Q4_K codes q (0..15) are
-// int8 already, so v_mfma_i32_16x16x32_i8 returns exact int32 sums
-//   S[digit][row] = sum_{k in sub-block} digit_k * q_k
-// for one 32-element sub-block.  The 6-bit scale of each sub-block enters the
-// B operand (sc = 8 hi + lo, codes times hi and times lo are still int8), so
-// two MFMA chains sum a whole super-block exactly (|S| < 2^25); per
-// super-block in f32: y += d * 2^-e * (S0 + 256 S1 + 65536 S2) - dmin *
-// sum_sb m_sb * sum(x over sb) -- the factorised Q4_K dot of
-// crates/sosomodel/src/dequant.rs:172-201.
+// int8 already, so v_mfma_i32_16x16x64_i8 returns exact int32 sums
+//   S[digit][row] = sum_{k in unit} digit_k * q_k * s_k
+// over one 64-element unit (two 32-element sub-blocks).  The 6-bit scale
+// s_k of each sub-block enters the B operand (sc = 8 hi + lo, codes times hi
+// and times lo are still int8), so two MFMA chains sum a whole super-block
+// exactly (|S| < 2^25); per super-block in f32: y += d * 2^-e * (S0 + 256 S1 +
+// 65536 S2) - dmin * sum_sb m_sb * sum(x over sb) -- the factorised Q4_K dot
+// of crates/sosomodel/src/dequant.rs:172-201.
 //
-// MFMA operands (16 x 16 x 32, int8; lane l, g = l / 16):
-//   A (16 x 32): row m = l % 16 = (token m / 4 of the tile, digit m % 4; digit
-//                3 is a zero pad), k = 8g .. 8g + 7  <- LDS
-//   B (32 x 16): column n = l % 16 = weight row, k = 8g .. 8g + 7  <- the 8
-//                codes of row n, elements 8g .. 8g + 7 of the sub-block
+// MFMA operands (16 x 16 x 64, int8; lane l, g = l / 16):
+//   A (16 x 64): row m = l % 16 = (token m / 4 of the tile, digit m % 4; digit
+//                3 is a zero pad); bytes 0..7 elements 8g .. 8g + 7 of the
+//                unit's first sub-block, bytes 8..15 the same of its second
+//                <- LDS
+//   B (64 x 16): column n = l % 16 = weight row, the same bytes of row n's
+//                codes (low nibbles, then high nibbles), times a scale part
 //   D (16 x 16): column n = l % 16, rows 4g .. 4g + 3 = token g of the tile,
 //                digits 0..3
-// so every lane ends up with one (weight row, token) pair per tile: the
-// row's scales apply lane by lane, and the min term is one FMA.
+// A and B share the map from (lane group, byte) to k, so which k a byte is
+// does not matter, only that both operands put the same element there.
+// Every lane ends up with one (weight row, token) pair per tile: the row's
+// scales apply lane by lane, and the min term is one FMA.
 //
 // Work: a workgroup of NW wavefronts (4 for the MoE experts; 4, 8 or 16 for
 // a dense matmul, chosen from the grid size) owns 16 rows per wavefront of one
@@ -313,9 +317,13 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
 #pragma unroll
                 for (int p = 0; p < 4; p++) {
                     const int j0 = 2 * p, j1 = 2 * p + 1; // sub-blocks of the unit
-                    // B operands: codes x (sc lo, sc hi) of sub-blocks j0 (low
-                    // nibbles) and j1 (high nibbles); the min factors
-                    long b0l[NMAT], b0h[NMAT], b1l[NMAT], b1h[NMAT];
+                    // B operands of the unit's 64 elements: bytes 0..7 the
+                    // codes of sub-block j0 (low nibbles), bytes 8..15 those
+                    // of j1 (high nibbles), times sc lo (bl) or sc hi (bh); A
+                    // holds the x digits in the same byte order, so one K=64
+                    // product sums both sub-blocks (A and B share the lane /
+                    // byte -> k map).  The min factors.
+                    mf_v4i bl[NMAT], bh[NMAT];
                     float m0[NMAT], m1[NMAT];
 #pragma unroll
                     for (int m = 0; m < NMAT; m++) {
@@ -323,10 +331,10 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
                         const uint32_t lx = q.x & 0x0F0F0F0Fu, ly = q.y & 0x0F0F0F0Fu;
                         const uint32_t hx = (q.x >> 4) & 0x0F0F0F0Fu, hy = (q.y >> 4) & 0x0F0F0F0Fu;
                         const int s0 = mf_byte(sc_[m].sc4[j0 >> 2], j0 & 3), s1 = mf_byte(sc_[m].sc4[j1 >> 2], j1 & 3);
-                        b0l[m] = (long)(((uint64_t)scaled(ly, s0 & 7) << 32) | scaled(lx, s0 & 7));
-                        b0h[m] = (long)(((uint64_t)scaled(ly, s0 >> 3) << 32) | scaled(lx, s0 >> 3));
-                        b1l[m] = (long)(((uint64_t)scaled(hy, s1 & 7) << 32) | scaled(hx, s1 & 7));
-                        b1h[m] = (long)(((uint64_t)scaled(hy, s1 >> 3) << 32) | scaled(hx, s1 >> 3));
+                        bl[m] = mf_v4i{(int)scaled(lx, s0 & 7), (int)scaled(ly, s0 & 7), (int)scaled(hx, s1 & 7),
+                                       (int)scaled(hy, s1 & 7)};
+                        bh[m] = mf_v4i{(int)scaled(lx, s0 >> 3), (int)scaled(ly, s0 >> 3), (int)scaled(hx, s1 >> 3),
+                                       (int)scaled(hy, s1 >> 3)};
                         m0[m] = (float)mf_byte(sc_[m].m4[j0 >> 2], j0 & 3);
                         m1[m] = (float)mf_byte(sc_[m].m4[j1 >> 2], j1 & 3);
                     }
@@ -335,13 +343,12 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
                         if (mt * 4 >= nt) break; // uniform
                         // A: token mt*4 + a_tok, digit a_dig (3: zero), elements 8g..8g+7
                         const int ta = mt * 4 + a_tok;
-                        long x0 = 0, x1 = 0;
+                        mf_v4i xa = mf_v4i{0, 0, 0, 0};
                         if (a_dig < 3 && ta < nt) {
                             const uint8_t *tp = lds + (size_t)ta * tb;
                             const uint2 u0 = *(const uint2 *)(tp + ((sbl8 + j0) * 3 + a_dig) * 32 + 8 * g);
                             const uint2 u1 = *(const uint2 *)(tp + ((sbl8 + j1) * 3 + a_dig) * 32 + 8 * g);
-                            x0 = (long)(((uint64_t)u0.y << 32) | u0.x);
-                            x1 = (long)(((uint64_t)u1.y << 32) | u1.x);
+                            xa = mf_v4i{(int)u0.x, (int)u0.y, (int)u1.x, (int)u1.y};
                         }
                         // the x sums of this lane's output token (mt*4 + g)
                         const int to = mt * 4 + g;
@@ -349,10 +356,8 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
                         const float xs0 = xsum[sbl8 + j0], xs1 = xsum[sbl8 + j1];
 #pragma unroll
                         for (int m = 0; m < NMAT; m++) {
-                            clo[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, b0l[m], clo[m][mt], 0, 0, 0);
-                            chi[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x0, b0h[m], chi[m][mt], 0, 0, 0);
-                            clo[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, b1l[m], clo[m][mt], 0, 0, 0);
-                            chi[m][mt] = __builtin_amdgcn_mfma_i32_16x16x32_i8(x1, b1h[m], chi[m][mt], 0, 0, 0);
+                            clo[m][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bl[m], clo[m][mt], 0, 0, 0);
+                            chi[m][mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bh[m], chi[m][mt], 0, 0, 0);
                             mins[m][mt] = fmaf(m0[m], xs0, fmaf(m1[m], xs1, mins[m][mt]));
                         }
                     }
