@@ -46,20 +46,18 @@ constexpr int MF_NW = 4;            // wavefronts per workgroup
 // is fastest -- 136 us per layer; 2 / 3 ahead gave 144 us.
 constexpr int MF_LA2 = 1, MF_LA1 = 1;
 constexpr int MF_ROWS = 16 * MF_NW; // rows per MoE workgroup (16 per wavefront)
-// Dense matmul workgroups of 4, 8 or 16 wavefronts: more rows per workgroup
-// share each staging of x (the round's tokens converted into LDS), which
-// bounds that kernel, but a workgroup's own chain (staging, then its rows'
-// super-blocks) sets the time once the grid is a single round.  Measured on
-// MI355X (us, 14336x4096 / 4096x4096 at 16, 32, 64 tokens):
-//   4 wavefronts: 48.9 93.6 183.3 / 46.8 47.1 47.9
-//   8 wavefronts: 50.1 52.4  98.0 / 47.9 48.4 49.9
-//  16 wavefronts: 70.3 71.4  74.4 / 68.9 69.1 68.9
-// so the widest workgroup that still gives the grid about one per CU wins.
+// Dense matmul workgroups have 4, 8 or 16 wavefronts (launch_mfma_matmul).
 constexpr int MF_NW_MAX = 16;
 
 // LDS per token for kc staged columns: digits [sub-block][3][32 B], then the
-// f32 sums of x per sub-block, then 2^-e per super-block.
-__host__ __device__ inline int mf_tok_bytes(int kc) { return kc / 32 * 96 + kc / 32 * 4 + kc / 256 * 4; }
+// f32 sums of x per sub-block, then 2^-e per super-block; the token stride is
+// rounded up to 16 bytes (804 bytes per super-block would leave the 8-byte
+// digit accesses of every other token misaligned when kc / 256 is odd, e.g. the
+// 768 columns of the MoE down projection: measured twice as slow).
+__host__ __device__ inline int mf_tok_bytes(int kc)
+{
+    return (kc / 32 * 96 + kc / 32 * 4 + kc / 256 * 4 + 15) & ~15;
+}
 
 // One super-block of one weight row as a lane loads it: the 16-byte header
 // (d, dmin, 12 scale bytes) and, for each of the 4 units, the 8 code bytes of
@@ -419,11 +417,12 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
 }
 
 // Columns staged per chunk: the largest multiple of 256 whose x for `tokens`
-// tokens fits the workgroup's LDS.
-static int mf_kc(const soso_hip *h, size_t cols, int tokens)
+// tokens fits `budget` bytes of LDS (the workgroup's whole LDS by default).
+static int mf_kc(const soso_hip *h, size_t cols, int tokens, size_t budget = 0)
 {
+    if (budget == 0) budget = h->max_lds;
     int kc = (int)cols;
-    while (kc > 256 && (size_t)tokens * mf_tok_bytes(kc) > h->max_lds) kc = ((kc / 2) + 255) / 256 * 256;
+    while (kc > 256 && (size_t)tokens * mf_tok_bytes(kc) > budget) kc = ((kc / 2) + 255) / 256 * 256;
     return kc;
 }
 
@@ -473,31 +472,52 @@ static void mfma_dense(soso_hip *h, const Weight &w, const float *x, size_t n, f
 }
 
 // Dense: Y[n x rows] = X[n x cols] . W^T.  The grid is (row block of 16 NW
-// rows) x (round of 4 MT tokens).  Widest workgroups first (16 or 8
-// wavefronts, 4-tile rounds) when they still give about one per CU; else
-// 4 wavefronts with the largest token round that gives as many workgroups and
-// stages each round's x in at most 4 column chunks, or 1-tile rounds.
-// Measured on MI355X (us; 4 wavefronts, tiles per round 4 / 2 / 1):
-//   4096 x 4096,  16 tokens: 46.9 / 27.5 / 16.1;   64 tokens: 48.3 / 55.0 / 46.9
-//   4096 x 14336, 16 tokens: 242.7 / 86.9 / 52.1;  64 tokens: 243.0 / 172.3 / 189.6
+// rows) x (round of 4 MT tokens), one round per workgroup.  A workgroup's own
+// chain (staging x, then its rows' super-blocks with one wavefront per SIMD
+// or two) sets the time, so the launch takes the (NW, MT) that gives the most
+// workgroups still fitting one per CU -- ties to the cheaper workgroup, in
+// the order below -- and, when even the largest tiles need more workgroups
+// than CUs, the fewest workgroups with half the LDS each (two per CU).  Every
+// choice computes the same bits: the integer sums are exact and each lane adds
+// its super-blocks in column order whatever the chunking.
+// Measured on MI355X, us for one round of workgroups at 4096 columns (any
+// row count): (4,1) 17, (8,1) 24, (4,2) 28, (8,2) 28, (16,1) 41, (4,4) 45,
+// (16,2) 46, (8,4) 47, (16,4) 66.  Chosen against the best of all 27 (NW, MT,
+// LDS share) settings, us: 4096x4096 at 16/32/64/128 tokens 17/24/28/47 (best
+// 17/24/28/47); 14336x4096 28/46/70/129 (28/46/66/129); 4096x14336 49/75/88/150
+// (49/75/88/150); the rule it replaces gave 14336x4096 46/49/72/136 and
+// 4096x14336 51/87/171/362.
+static const int MF_DENSE[9][2] = {{4, 1}, {8, 1}, {4, 2}, {8, 2}, {16, 1}, {4, 4}, {16, 2}, {8, 4}, {16, 4}};
+
 int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
 {
     if (!mfma_shape_ok(w.dtype, w.rows, w.cols) || n == 0 || n > (1u << 20))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
-    const size_t want = (size_t)h->num_cu * 7 / 8;
+    const size_t cu = (size_t)h->num_cu;
     auto groups = [&](int nw, int mt) { return (w.rows + 16 * nw - 1) / (16 * nw) * ((n + 4 * mt - 1) / (4 * mt)); };
-    auto chunks = [&](int mt) { return (w.cols + mf_kc(h, w.cols, 4 * mt) - 1) / mf_kc(h, w.cols, 4 * mt); };
-    if (groups(16, 4) >= want) {
-        mfma_dense<16, 4>(h, w, x, n, y, mf_kc(h, w.cols, 16), (unsigned)groups(16, 4));
-    } else if (groups(8, 4) >= want) {
-        mfma_dense<8, 4>(h, w, x, n, y, mf_kc(h, w.cols, 16), (unsigned)groups(8, 4));
-    } else {
-        const int mt = groups(4, 4) >= want && chunks(4) <= 4 ? 4 : groups(4, 2) >= want && chunks(2) <= 4 ? 2 : 1;
-        const int kc = mf_kc(h, w.cols, 4 * mt);
-        const unsigned grid = (unsigned)groups(4, mt);
-        if (mt == 4) mfma_dense<4, 4>(h, w, x, n, y, kc, grid);
-        else if (mt == 2) mfma_dense<4, 2>(h, w, x, n, y, kc, grid);
-        else mfma_dense<4, 1>(h, w, x, n, y, kc, grid);
+    int pick = -1;
+    for (int i = 0; i < 9; i++) { // the most workgroups within one per CU
+        const size_t gi = groups(MF_DENSE[i][0], MF_DENSE[i][1]);
+        if (gi <= cu && (pick < 0 || gi > groups(MF_DENSE[pick][0], MF_DENSE[pick][1]))) pick = i;
+    }
+    if (pick < 0) // else the fewest
+        for (int i = 0; i < 9; i++)
+            if (pick < 0 || groups(MF_DENSE[i][0], MF_DENSE[i][1]) < groups(MF_DENSE[pick][0], MF_DENSE[pick][1]))
+                pick = i;
+    const int nw = MF_DENSE[pick][0], mt = MF_DENSE[pick][1];
+    const size_t grid = groups(nw, mt);
+    const int kc = mf_kc(h, w.cols, 4 * mt, grid > cu ? h->max_lds / 2 : h->max_lds);
+    const unsigned gu = (unsigned)grid;
+    switch (nw * 8 + mt) {
+    case 4 * 8 + 1: mfma_dense<4, 1>(h, w, x, n, y, kc, gu); break;
+    case 4 * 8 + 2: mfma_dense<4, 2>(h, w, x, n, y, kc, gu); break;
+    case 4 * 8 + 4: mfma_dense<4, 4>(h, w, x, n, y, kc, gu); break;
+    case 8 * 8 + 1: mfma_dense<8, 1>(h, w, x, n, y, kc, gu); break;
+    case 8 * 8 + 2: mfma_dense<8, 2>(h, w, x, n, y, kc, gu); break;
+    case 8 * 8 + 4: mfma_dense<8, 4>(h, w, x, n, y, kc, gu); break;
+    case 16 * 8 + 1: mfma_dense<16, 1>(h, w, x, n, y, kc, gu); break;
+    case 16 * 8 + 2: mfma_dense<16, 2>(h, w, x, n, y, kc, gu); break;
+    default: mfma_dense<16, 4>(h, w, x, n, y, kc, gu); break;
     }
     return hip_check(h, hipGetLastError(), "mfma matmul launch");
 }
