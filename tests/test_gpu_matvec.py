@@ -154,17 +154,20 @@ def test_matmul_equals_single_matvecs(gpu, orc):
 
 @pytest.mark.parametrize("rows,cols,n", [(1000, 4096, 16), (384, 1536, 37), (136, 768, 20),
                                          (14336, 4096, 32), (14336, 4096, 64), (4096, 4096, 64),
-                                         (4096, 14336, 32)])
+                                         (4096, 14336, 32), (528, 1024, 256), (720, 1024, 200),
+                                         (1296, 1024, 96), (1424, 1024, 200), (14336, 4096, 128)])
 def test_matmul_matrix_cores_match_cpu(gpu, orc, rows, cols, n):
     """From 16 vectors up, Q4_K matmul runs on the matrix cores (exact int8
     products of codes and x digits, scales in f32): every output row within
-    relative L2 1e-5 of the CPU restatement.  Shapes cover a partial 128-row
-    block, column counts that end in a partial 1024-column chunk, and token
-    counts that leave a partial round of tokens.  The launcher picks the
-    workgroup shape by grid size: the small shapes run 4-wavefront workgroups
-    on rounds of 4 tokens, 14336 x 4096 fills the GPU with 8- (32 tokens) and
-    16-wavefront workgroups (64 tokens), 4096 x 4096 at 64 tokens takes rounds
-    of 16 and 4096 x 14336 at 32 tokens rounds of 8 in four column chunks."""
+    relative L2 1e-5 of the CPU restatement.  Shapes cover a partial row
+    block, column counts that end in a partial chunk, and token counts that
+    leave a partial round of tokens.  The launcher takes the (wavefronts,
+    tokens per round) pair giving the most workgroups within one per CU; the
+    cases reach all nine: (4, 1) the three small shapes, (16, 2) 14336 x 4096
+    at 32 tokens, (16, 4) at 64 (two column chunks) and at 128 (more
+    workgroups than CUs: half the LDS each, four chunks), (8, 2) 4096 x 4096
+    at 64, (8, 1) 4096 x 14336 at 32 (two chunks), and (16, 1), (4, 4),
+    (4, 2), (8, 4) the four 1024-column shapes."""
     w = orc.synth(Q4K, rows, cols, 7, n)
     xs = orc.normal(n * cols, 1.0, 8, n).reshape(n, cols)
     out = np.empty(n * rows, np.float32)
