@@ -30,7 +30,7 @@
 // scales apply lane by lane, and the min term is one FMA.
 //
 // Work: a workgroup of NW wavefronts (4 for the MoE experts; 4, 8 or 16 for
-// a dense matmul, chosen from the grid size) owns 16 rows per wavefront of one
+// a dense matmul, chosen by launch_mfma_matmul) owns 16 rows per wavefront of one
 // expert (or of the dense weight) and loops over its tokens in rounds of
 // 4 * MT, and over the columns in chunks of `kcmax` (as many as LDS holds for
 // the round's tokens: one chunk for the MoE expert shapes).  Registered MoE
