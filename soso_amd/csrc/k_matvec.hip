@@ -204,12 +204,12 @@ __device__ __forceinline__ void kv_put(const MvEpi &ep, void *cache, size_t at, 
     }
 }
 
+// Lane `lane` holds row r (valid when ok); pair epilogues find the other row
+// of a pair (2i, 2i + 1) in the neighbouring lane.
 template <int EPI>
-__device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows, int rows, float *__restrict__ y,
-                                         const MvEpi &ep, float cs = 1.0f, float sn = 0.0f)
+__device__ __forceinline__ void epilogue(float yacc, int lane, int r, bool ok, float *__restrict__ y, const MvEpi &ep,
+                                         float cs = 1.0f, float sn = 0.0f)
 {
-    const int r = r0 + lane;
-    const bool ok = lane < nrows && r < rows;
     if constexpr (EPI == EPI_STORE) {
         if (ok) y[r] = yacc;
     } else if constexpr (EPI == EPI_RESID) {
@@ -247,10 +247,11 @@ __device__ __forceinline__ void epilogue(float yacc, int lane, int r0, int nrows
     }
 }
 
-template <int FMT, int LPR, int S, int DEPTH, bool XFIRST, int XS = XS_PLAIN, int EPI = EPI_STORE>
+template <int FMT, int LPR, int S, int DEPTH, bool XFIRST, int XS = XS_PLAIN, int EPI = EPI_STORE, bool IL = false>
 __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, size_t stride, MvIn in,
                                                float *__restrict__ y, int rows, int cols, MvEpi ep)
 {
+    static_assert(S == 1 || !IL, "split rows walk contiguous strips");
     static_assert(S == 1 || LPR == 64, "split rows use whole wavefronts");
     static_assert(S == 1 || COMBINE_CH % DEPTH == 0, "combine rounds keep the load ring aligned");
     static_assert(S == 1 || EPI == EPI_STORE || EPI == EPI_RESID, "pair epilogues need whole rows per wavefront");
@@ -277,20 +278,45 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 
     const int passes = (rows + RW - 1) / RW;
     const int tg = gridDim.x * gpw;
-    // pair epilogues need strips that start on even rows
+    // pair epilogues need whole pairs of rows (2i, 2i + 1) in neighbouring lanes
     constexpr int PU = (RW == 1 && (EPI == EPI_QKV || EPI == EPI_SWIGLU)) ? 2 : 1;
+    static_assert(DEPTH % PU == 0, "a ring turn holds whole units");
     const int units = (passes + PU - 1) / PU;
     auto strip = [&](int g, int &q0, int &q1) {
         q0 = PU * (int)((long)units * g / tg);
         q1 = min(passes, PU * (int)((long)units * (g + 1) / tg));
     };
-    int p0, p1;
-    strip(blockIdx.x * gpw + grp, p0, p1);
-    const int n = p1 - p0;
-    const int r0 = p0 * RW, rend = min(p1 * RW, rows);
-    // The strip is the buffer; the host keeps it (plus DEPTH passes) under 2^31 bytes.
+    const int g = blockIdx.x * gpw + grp;
+    // Rows reach the group in units of PU passes.  IL: group g takes units g,
+    // g + tg, g + 2 tg, ..., so at every step of the ring the groups of the
+    // whole grid read one contiguous stretch of the matrix (on MI355X the
+    // 14336 x 4096 Q4_K matvec: 7.3 us against 7.7 us for contiguous strips,
+    // whose concurrent reads sit a strip apart).  Otherwise group g takes the
+    // contiguous strip of units [units g / tg, units (g + 1) / tg).
+    int p0, n;
+    if constexpr (IL) {
+        p0 = PU * g;
+        n = g < units ? PU * ((units - g + tg - 1) / tg) : 0; // the last unit may run past `passes`: zeros
+    } else {
+        int p1;
+        strip(g, p0, p1);
+        n = p1 - p0;
+    }
+    const int r0 = p0 * RW, rend = IL ? rows : min((p0 + n) * RW, rows);
+    // From the group's first pass to the end of its rows is the buffer; the
+    // host keeps it (plus DEPTH passes) under 2^31 bytes.
     const uint32_t pass_bytes = (uint32_t)(RW * stride);
-    const rsrc_t rs = make_rsrc(W + (size_t)r0 * stride, (uint32_t)((size_t)(rend - r0) * stride));
+    const rsrc_t rs = make_rsrc(W + (size_t)r0 * stride, (uint32_t)((size_t)(rend > r0 ? rend - r0 : 0) * stride));
+    // byte offset of the group's pass k from its first pass
+    auto pass_off = [&](int k) -> uint32_t {
+        if constexpr (IL) return (uint32_t)((k / PU) * PU * tg + k % PU) * pass_bytes;
+        else return (uint32_t)k * pass_bytes;
+    };
+    // row of the sum in lane i, once gathered (lane i holds pass i / RW)
+    auto lane_row = [&](int i) -> int {
+        const int k = i / RW;
+        return RW * (IL ? PU * (g + (k / PU) * tg) + k % PU : p0 + k) + i % RW;
+    };
     // inactive lanes (unit past the row end) read nothing
     const uint32_t lane_base = uact ? (uint32_t)(slot * stride) : 0x80000000u;
 
@@ -299,28 +325,28 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         XPreN xpre;
         stage_xn_issue(x, in.norm_w, cols, xpre);
 #pragma unroll
-        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
+        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
         stage_xn_finish<FMT>(xpre, cols, in.eps, xp, s16, kx, red);
     } else if constexpr (XFIRST) {
         // x first: once the weight stream is requested, x's reads would queue
         // behind it in the shared L2 channels.
         stage_x<FMT>(x, cols, xp, s16, kx);
 #pragma unroll
-        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
+        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
     } else {
         // x's loads, then the ring's, then x's conversion while the ring is
         // in flight (loads return in issue order)
         XPre xpre;
         stage_x_issue(x, cols, xpre);
 #pragma unroll
-        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + (uint32_t)i * pass_bytes, cols, L, buf[i]);
+        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
         stage_x_finish<FMT>(xpre, x, cols, xp, s16, kx);
     }
     // the RoPE angle of this lane's output row, computed while the ring is in
     // flight (the empty asm keeps it from being sunk to the epilogue)
     float rope_c = 1.0f, rope_s = 0.0f;
     if constexpr (EPI == EPI_QKV) {
-        rope_angle(ep, r0 + lane, rope_c, rope_s);
+        rope_angle(ep, lane_row(lane), rope_c, rope_s);
         asm volatile("" ::"v"(rope_c), "v"(rope_s));
     }
     XReg xv;
@@ -341,7 +367,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
             for (int i = 0; i < DEPTH; i++) {
                 const int j = j0 + i;
                 float part = unit_dot<FMT>(buf[i], xv, c);
-                load_row<FMT>(rs, lane_base + (uint32_t)(j + DEPTH) * pass_bytes, cols, L, buf[i]);
+                load_row<FMT>(rs, lane_base + pass_off(j + DEPTH), cols, L, buf[i]);
                 part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
                 yacc = gather_rows<LPR>(part, j, yacc, lane);
                 __builtin_amdgcn_sched_barrier(0);
@@ -356,7 +382,8 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
                 yacc = gather_rows<LPR>(part, j0 + i, yacc, lane);
             }
         }
-        epilogue<EPI>(yacc, lane, r0, n * RW, rows, y, ep, rope_c, rope_s);
+        const int r = lane_row(lane);
+        epilogue<EPI>(yacc, lane, r, lane < n * RW && r < rows, y, ep, rope_c, rope_s);
     } else {
         // the same number of combine rounds for every wavefront of the workgroup
         int nmax = 0;
@@ -376,7 +403,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
                 for (int i = 0; i < DEPTH; i++) {
                     const int j = j0 + i;
                     float part = unit_dot<FMT>(buf[i], xv, c);
-                    load_row<FMT>(rs, lane_base + (uint32_t)(j + DEPTH) * pass_bytes, cols, L, buf[i]);
+                    load_row<FMT>(rs, lane_base + pass_off(j + DEPTH), cols, L, buf[i]);
                     part = seg_sum_dpp<64>(uact ? part : 0.0f);
                     if (lane == 63) red[(grp * COMBINE_CH + (j - c0)) * S + sw] = part;
                     __builtin_amdgcn_sched_barrier(0);
@@ -444,6 +471,16 @@ static bool strip_fits(int passes, int groups, size_t pass_bytes)
     return per * pass_bytes < ((size_t)1 << 31);
 }
 
+// The interleaved mapping addresses every pass of a group from its first one:
+// the last ring offset (a whole grid of passes per unit step) must stay below
+// 2^31 bytes.
+static bool interleave_fits(int passes, int pu, int groups, size_t pass_bytes)
+{
+    const size_t units = ((size_t)passes + pu - 1) / pu;
+    const size_t steps = (units + groups - 1) / groups + 16;
+    return steps * (size_t)pu * groups * pass_bytes < ((size_t)1 << 31);
+}
+
 // Ring depth (passes in flight per wavefront) and issue order, measured on
 // MI355X (back-to-back launches over rotating weights above the MALL size):
 //   Q4_K 14336 x 4096: depth 2, ring loads before x's conversion (7.7 us;
@@ -495,10 +532,15 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
         grid = std::max(grid, 1);
         if (!strip_fits(passes, grid * gpw, (size_t)(64 / LPR) * stride))
             return set_err(h, SOSO_HIP_DECLINED, "matvec: row strip exceeds 2 GiB");
+        const bool il = interleave_fits(passes, 1, grid * gpw, (size_t)(64 / LPR) * stride);
 #define MV_CASE(L)                                                                                                  \
     case L:                                                                                                         \
-        mv_rows<FMT, L, 1, ring_depth<FMT, 1>(), x_first<L>()><<<grid, threads, lds, h->stream>>>(W, stride, xin, y, \
-                                                                                                  rows, cols, MvEpi()); \
+        if (il)                                                                                                     \
+            mv_rows<FMT, L, 1, ring_depth<FMT, 1>(), x_first<L>(), XS_PLAIN, EPI_STORE, true>                        \
+                <<<grid, threads, lds, h->stream>>>(W, stride, xin, y, rows, cols, MvEpi());                        \
+        else                                                                                                        \
+            mv_rows<FMT, L, 1, ring_depth<FMT, 1>(), x_first<L>()><<<grid, threads, lds, h->stream>>>(               \
+                W, stride, xin, y, rows, cols, MvEpi());                                                            \
         break;
         switch (LPR) {
             MV_CASE(1) MV_CASE(2) MV_CASE(4) MV_CASE(8) MV_CASE(16) MV_CASE(32) MV_CASE(64)
@@ -525,22 +567,26 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
 // Matvec with an input / output variant (the decode step's fusions)
 // ---------------------------------------------------------------------------
 template <int FMT, int LPR, int XS, int EPI>
-static void launch_ex1(soso_hip *h, unsigned grid, size_t lds, const uint8_t *W, size_t stride, const MvIn &in, float *y,
-                       int rows, int cols, const MvEpi &ep)
+static void launch_ex1(soso_hip *h, bool il, unsigned grid, size_t lds, const uint8_t *W, size_t stride, const MvIn &in,
+                       float *y, int rows, int cols, const MvEpi &ep)
 {
-    mv_rows<FMT, LPR, 1, ring_depth<FMT, 1>(), x_first<LPR>(), XS, EPI><<<grid, 512, lds, h->stream>>>(
-        W, stride, in, y, rows, cols, ep);
+    if (il)
+        mv_rows<FMT, LPR, 1, ring_depth<FMT, 1>(), x_first<LPR>(), XS, EPI, true><<<grid, 512, lds, h->stream>>>(
+            W, stride, in, y, rows, cols, ep);
+    else
+        mv_rows<FMT, LPR, 1, ring_depth<FMT, 1>(), x_first<LPR>(), XS, EPI><<<grid, 512, lds, h->stream>>>(
+            W, stride, in, y, rows, cols, ep);
 }
 
 template <int FMT, int XS, int EPI>
-static bool launch_ex_lpr(soso_hip *h, int lpr, unsigned grid, size_t lds, const uint8_t *W, size_t stride,
+static bool launch_ex_lpr(soso_hip *h, int lpr, bool il, unsigned grid, size_t lds, const uint8_t *W, size_t stride,
                           const MvIn &in, float *y, int rows, int cols, const MvEpi &ep)
 {
     switch (lpr) {
-    case 8: launch_ex1<FMT, 8, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
-    case 16: launch_ex1<FMT, 16, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
-    case 32: launch_ex1<FMT, 32, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
-    case 64: launch_ex1<FMT, 64, XS, EPI>(h, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    case 8: launch_ex1<FMT, 8, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    case 16: launch_ex1<FMT, 16, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    case 32: launch_ex1<FMT, 32, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
+    case 64: launch_ex1<FMT, 64, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
     default: return false;
     }
 }
@@ -588,21 +634,22 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, con
     grid = std::max(grid, ((units + upw - 1) / upw + gpw - 1) / gpw);
     grid = std::max(grid, 1);
     if (!strip_fits(passes, grid * gpw, (size_t)RW * stride)) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: strip");
+    const bool il = interleave_fits(passes, PU, grid * gpw, (size_t)RW * stride);
     bool ok = false;
     const unsigned g = (unsigned)grid;
     if (w.dtype == SOSO_HIP_DTYPE_Q4_K) {
         if (xs == XS_RMSNORM && epi == EPI_QKV)
-            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_QKV>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_QKV>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
         else if (xs == XS_RMSNORM && epi == EPI_SWIGLU)
-            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_SWIGLU>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_SWIGLU>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
         else if (xs == XS_PLAIN && epi == EPI_RESID)
-            ok = launch_ex_lpr<FMT_Q4K, XS_PLAIN, EPI_RESID>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+            ok = launch_ex_lpr<FMT_Q4K, XS_PLAIN, EPI_RESID>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
         else if (xs == XS_RMSNORM && epi == EPI_STORE)
-            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_STORE>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_STORE>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
     } else if (w.dtype == SOSO_HIP_DTYPE_Q6_K && xs == XS_RMSNORM && epi == EPI_STORE) {
-        ok = launch_ex_lpr<FMT_Q6K, XS_RMSNORM, EPI_STORE>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+        ok = launch_ex_lpr<FMT_Q6K, XS_RMSNORM, EPI_STORE>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
     } else if (w.dtype == SOSO_HIP_DTYPE_Q8_0 && xs == XS_RMSNORM && epi == EPI_STORE) {
-        ok = launch_ex_lpr<FMT_Q80, XS_RMSNORM, EPI_STORE>(h, LPR, g, lds, W, stride, in, y, rows, cols, ep);
+        ok = launch_ex_lpr<FMT_Q80, XS_RMSNORM, EPI_STORE>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
     }
     if (!ok) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: variant not built");
     return hip_check(h, hipGetLastError(), "matvec_ex launch");

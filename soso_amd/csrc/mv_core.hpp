@@ -322,11 +322,23 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c)
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// One code dword (four signed byte codes) against register group gi.
+// v_dot4_i32_i8 onto an inline zero: starts a chain without first moving 0
+// into the accumulator (the compiler otherwise picks the two-operand form,
+// which adds one v_mov per digit and chain)
+__device__ __forceinline__ int sdot4_first(uint32_t a, uint32_t b)
+{
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
+// One code dword (four signed byte codes) against register group gi; FIRST
+// starts the digit sums (their previous values are ignored).
+template <bool FIRST = false>
 __device__ __forceinline__ void dot_group(uint32_t q, const XReg &xv, int gi, int (&s)[XDIG])
 {
 #pragma unroll
-    for (int k = 0; k < XDIG; k++) s[k] = sdot4(q, xv.d[XDIG * gi + k], s[k]);
+    for (int k = 0; k < XDIG; k++) s[k] = FIRST ? sdot4_first(q, xv.d[XDIG * gi + k]) : sdot4(q, xv.d[XDIG * gi + k], s[k]);
 }
 
 // Sum over the digits: (s2 * 2^16 + s1 * 2^8 + s0), rounded once or twice.
@@ -421,9 +433,11 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const XReg &xv, co
         // elements 0..31, register groups 0..7), high nibble = element l of
         // sub-block 2p+1 (register groups 8..15).
         const uint32_t q[8] = {w.a.x, w.a.y, w.a.z, w.a.w, w.b.x, w.b.y, w.b.z, w.b.w};
-        int sa[XDIG] = {0, 0, 0}, sb[XDIG] = {0, 0, 0};
+        int sa[XDIG], sb[XDIG];
+        dot_group<true>(q[0] & 0x0F0F0F0Fu, xv, 0, sa);
+        dot_group<true>((q[0] >> 4) & 0x0F0F0F0Fu, xv, 8, sb);
 #pragma unroll
-        for (int t = 0; t < 8; t++) {
+        for (int t = 1; t < 8; t++) {
             dot_group(q[t] & 0x0F0F0F0Fu, xv, t, sa);
             dot_group((q[t] >> 4) & 0x0F0F0F0Fu, xv, 8 + t, sb);
         }
@@ -439,13 +453,15 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const XReg &xv, co
         return fmaf(d * P, uu, -(dmin * vv));
     } else if constexpr (FMT == FMT_Q80) {
         // plane p holds bytes 16(p&1) .. +15 of block p>>1: register groups 4p .. 4p+3
-        int s0[XDIG] = {0, 0, 0}, s1[XDIG] = {0, 0, 0};
+        int s0[XDIG], s1[XDIG];
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const uint32_t q[4] = {w.q[p].x, w.q[p].y, w.q[p].z, w.q[p].w};
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                if (p < 2) dot_group(q[t], xv, 4 * p + t, s0);
+                if (p == 0 && t == 0) dot_group<true>(q[t], xv, 0, s0);
+                else if (p == 2 && t == 0) dot_group<true>(q[t], xv, 8, s1);
+                else if (p < 2) dot_group(q[t], xv, 4 * p + t, s0);
                 else dot_group(q[t], xv, 4 * p + t, s1);
             }
         }
@@ -453,8 +469,6 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const XReg &xv, co
                         __builtin_bit_cast(float, w.s.y) * digits_value(s1));
     } else {
         int s[4][XDIG];
-#pragma unroll
-        for (int i = 0; i < 4; i++) s[i][0] = s[i][1] = s[i][2] = 0;
         const uint32_t la[4] = {w.la.x, w.la.y, w.la.z, w.la.w}, lb[4] = {w.lb.x, w.lb.y, w.lb.z, w.lb.w};
         const uint32_t qh[4] = {w.qh.x, w.qh.y, w.qh.z, w.qh.w};
 #pragma unroll
@@ -467,7 +481,10 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const XReg &xv, co
             q[2] = ((la[t] >> 4) & 0x0F0F0F0Fu) | (qh[t] & 0x30303030u);
             q[3] = ((lb[t] >> 4) & 0x0F0F0F0Fu) | ((qh[t] >> 2) & 0x30303030u);
 #pragma unroll
-            for (int i = 0; i < 4; i++) dot_group(q[i], xv, 4 * i + t, s[i]);
+            for (int i = 0; i < 4; i++) {
+                if (t == 0) dot_group<true>(q[i], xv, 4 * i, s[i]);
+                else dot_group(q[i], xv, 4 * i + t, s[i]);
+            }
         }
         // sub-scales sc[h*8 + kk + 2i] (int8), the -32 offset through c[i] = 32*sum(x)
         const float sc0 = (float)(int8_t)(w.sc.x >> c.bsh), sc1 = (float)(int8_t)(w.sc.x >> (c.bsh + 16));
