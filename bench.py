@@ -51,15 +51,43 @@ def _capture(g, body):
     return gid
 
 
+def _timed_graph(g, calls, steps):
+    """Captures `calls` (which issues `steps` steps) into one graph, replays it
+    once to warm it, then times one replay: HIP events on the library's
+    stream bracket exactly that replay's `steps` steps.  The timed replay and
+    its events are enqueued while an untimed replay still runs, so the graph
+    starts as soon as the stream reaches it and the host's submission latency
+    (a fixed cost per replay, not per step) stays out of the per-step figure
+    even at small `steps`.  Returns (ms per step between the events, host
+    wall ms per step of one replay on an idle stream)."""
+    gid = _capture(g, calls)
+    try:
+        g.graph_launch(gid)
+        g.sync()
+        t0 = time.perf_counter()
+        g.graph_launch(gid)
+        g.sync()
+        t1 = time.perf_counter()
+        g.graph_launch(gid)  # keeps the stream busy while the timed replay is enqueued
+        g.event_record(0)
+        g.graph_launch(gid)
+        g.event_record(1)
+        g.sync()
+    finally:
+        g.graph_destroy(gid)
+    return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
+
+
 def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
     """Average duration of one matvec launch, in ms.
 
     `copies` resident weights are rotated so HBM, not the MALL, serves them.
     The timed region is one HIP graph of `steps` back-to-back launches on the
-    library's stream, bracketed by HIP events recorded on that stream: the
-    average is (event interval) / steps, the same per-dispatch figure
-    rocprofv3 --kernel-trace reports (profiles/ holds that cross-check).
-    Returns (ms_per_launch_events, ms_per_launch_host_wall)."""
+    library's stream, bracketed by HIP events recorded on that stream (see
+    _timed_graph): the average is (event interval) / steps,
+    the same per-dispatch figure rocprofv3 --kernel-trace reports (profiles/
+    holds that cross-check).  Returns (ms_per_launch_events,
+    ms_per_launch_host_wall)."""
     keys = [f"bench.{dtype}.{rows}x{cols}.{i}" for i in range(copies)]
     for i, k in enumerate(keys):
         g.weight_synth(k, dtype, rows, cols, seed, 1000 + i)
@@ -70,19 +98,7 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
         for i in range(warmup):
             g.matvec_dev(keys[i % copies], x, y)
         g.sync()
-        gid = _capture(g, lambda: [g.matvec_dev(keys[i % copies], x, y) for i in range(steps)])
-        try:
-            g.graph_launch(gid)  # first replay warms the graph itself
-            g.sync()
-            t0 = time.perf_counter()
-            g.event_record(0)
-            g.graph_launch(gid)
-            g.event_record(1)
-            g.sync()
-            t1 = time.perf_counter()
-        finally:
-            g.graph_destroy(gid)
-        return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
+        return _timed_graph(g, lambda: [g.matvec_dev(keys[i % copies], x, y) for i in range(steps)], steps)
     finally:
         g.sync()
         g.dev_free(x)
@@ -113,16 +129,7 @@ def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False):
             g.event_record(1)
             g.sync()
         else:
-            gid = _capture(g, calls)
-            try:
-                g.graph_launch(gid)
-                g.sync()
-                g.event_record(0)
-                g.graph_launch(gid)
-                g.event_record(1)
-                g.sync()
-            finally:
-                g.graph_destroy(gid)
+            return _timed_graph(g, calls, steps)[0]
         return g.event_elapsed(0, 1) / steps
     finally:
         g.sync()
@@ -152,18 +159,8 @@ def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES):
             for i in range(warmup):
                 g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len)
             g.sync()
-            gid = _capture(g, lambda: [g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len)
-                                       for i in range(steps)])
-            try:
-                g.graph_launch(gid)
-                g.sync()
-                g.event_record(0)
-                g.graph_launch(gid)
-                g.event_record(1)
-                g.sync()
-            finally:
-                g.graph_destroy(gid)
-            res[(wpc, thr)] = g.event_elapsed(0, 1) / steps
+            res[(wpc, thr)] = _timed_graph(g, lambda: [g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len)
+                                                       for i in range(steps)], steps)[0]
     finally:
         g.sync()
         for b in bufs:
@@ -224,18 +221,9 @@ def time_moe(g, n, steps, layers=4, n_x=8, seed=11, eager=False):
                 calls()
                 g.event_record(1)
                 g.sync()
+                ms = g.event_elapsed(0, 1) / steps
             else:
-                gid = _capture(g, calls)
-                try:
-                    g.graph_launch(gid)
-                    g.sync()
-                    g.event_record(0)
-                    g.graph_launch(gid)
-                    g.event_record(1)
-                    g.sync()
-                finally:
-                    g.graph_destroy(gid)
-            ms = g.event_elapsed(0, 1) / steps
+                ms = _timed_graph(g, calls, steps)[0]
             order = [(i % layers) * n_x + (i // layers) % n_x for i in range(steps)]
             b = sum(nbytes[o][0] for o in order) / steps
             u = sum(nbytes[o][1] for o in order) / steps
@@ -319,18 +307,9 @@ def time_decode_8b(g, steps, ctx=4096, seed=21, kv_f16=False, eager=False):
                 g.decode_step_dev(name, x, ctx, None, tok)
             g.event_record(1)
             g.sync()
+            ms = g.event_elapsed(0, 1) / steps
         else:
-            gid = _capture(g, lambda: [g.decode_step_dev(name, x, ctx, None, tok) for _ in range(steps)])
-            try:
-                g.graph_launch(gid)
-                g.sync()
-                g.event_record(0)
-                g.graph_launch(gid)
-                g.event_record(1)
-                g.sync()
-            finally:
-                g.graph_destroy(gid)
-        ms = g.event_elapsed(0, 1) / steps
+            ms = _timed_graph(g, lambda: [g.decode_step_dev(name, x, ctx, None, tok) for _ in range(steps)], steps)[0]
         token = int(g.d2h(tok, (1,), np.uint32)[0])
         # a serving loop's view: one step per graph launch, the host waiting
         # for each token (launch, sync and the 4-byte token read per step)
