@@ -97,13 +97,17 @@ struct soso_hip {
     std::unordered_map<std::string, void *> f32_tensors; // router weights etc.
     soso_hip_stats_t stats{};
     std::string err;
-    // reusable device scratch (grown on demand; never inside graph capture)
+    // reusable device scratch, grown on demand (scratch_get).  A graph keeps
+    // the scratch pointers it was captured with, so a slot outgrown while any
+    // graph exists is retired, not freed: retired buffers are freed once no
+    // graph is left (graph_destroy) or with the handle.
     static constexpr int N_SCRATCH = 12;
     void *scratch[N_SCRATCH] = {};
     size_t scratch_cap[N_SCRATCH] = {};
+    std::vector<void *> retired;
     // SOSO_TICKET_BYTES of "last workgroup" state, zero between launches (each
     // kernel resets what it used): uint 0 the final counter (argmax, MoE
-    // route), uints 64 .. 575 argmax partials, uints 2048 .. 3071 the MoE
+    // route), uints 64 .. 831 argmax partials (winner, index, holds-NaN flag per segment), uints 2048 .. 3071 the MoE
     // route's per-token-block counters
     unsigned *ticket = nullptr;
     std::unordered_map<std::string, MoeLayer> moe_layers;
@@ -156,6 +160,8 @@ int launch_matvec(soso_hip *h, const Weight &w, const float *x_dev, float *y_dev
 // One matvec with an input variant (xs) and an output variant (epi).  EPI_SWIGLU
 // expects rows interleaved (gate_i, up_i) and writes rows/2 values silu(g)*u.
 int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y_dev, const MvEpi &ep, int xs, int epi);
+// Null when launch_matvec_ex runs this (dtype, shape, xs, epi), else why not.
+const char *matvec_ex_unsupported(const soso_hip *h, uint8_t dtype, size_t rows, size_t cols, int xs, int epi);
 int launch_dequant(soso_hip *h, const Weight &w, float *out_dev);
 int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
 // (k_decode.hip)

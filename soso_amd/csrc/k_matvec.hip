@@ -573,58 +573,90 @@ static void launch_ex1(soso_hip *h, bool il, unsigned grid, size_t lds, const ui
     if (il)
         mv_rows<FMT, LPR, 1, ring_depth<FMT, 1>(), x_first<LPR>(), XS, EPI, true><<<grid, 512, lds, h->stream>>>(
             W, stride, in, y, rows, cols, ep);
-    else
+    else if constexpr (EPI == EPI_STORE) // the head: contiguous strips past 2^31 bytes of interleaved offsets
         mv_rows<FMT, LPR, 1, ring_depth<FMT, 1>(), x_first<LPR>(), XS, EPI><<<grid, 512, lds, h->stream>>>(
             W, stride, in, y, rows, cols, ep);
 }
 
 template <int FMT, int XS, int EPI>
-static bool launch_ex_lpr(soso_hip *h, int lpr, bool il, unsigned grid, size_t lds, const uint8_t *W, size_t stride,
+static void launch_ex_lpr(soso_hip *h, int lpr, bool il, unsigned grid, size_t lds, const uint8_t *W, size_t stride,
                           const MvIn &in, float *y, int rows, int cols, const MvEpi &ep)
 {
     switch (lpr) {
-    case 8: launch_ex1<FMT, 8, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
-    case 16: launch_ex1<FMT, 16, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
-    case 32: launch_ex1<FMT, 32, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
-    case 64: launch_ex1<FMT, 64, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); return true;
-    default: return false;
+    case 8: launch_ex1<FMT, 8, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+    case 16: launch_ex1<FMT, 16, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+    case 32: launch_ex1<FMT, 32, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+    default: launch_ex1<FMT, 64, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
     }
 }
 
-int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, const MvEpi &ep, int xs, int epi)
+template <int FMT>
+static void launch_ex_fmt(soso_hip *h, int xs, int epi, int lpr, bool il, unsigned grid, size_t lds, const uint8_t *W,
+                          size_t stride, const MvIn &in, float *y, int rows, int cols, const MvEpi &ep)
 {
-    const int rows = (int)w.rows, cols = (int)w.cols, U = cols / 64;
-    const size_t stride = packed_row_stride(w.dtype, w.cols);
-    const uint8_t *W = (const uint8_t *)w.dev;
-    const int S = (U + 63) / 64;
-    if (xs == XS_RMSNORM && cols > XPRE_N * 8 * 512)
-        return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: normalised x wider than the staging registers");
-    if ((epi == EPI_QKV || epi == EPI_SWIGLU) && (S != 1 || rows % 2))
-        return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: pair epilogue needs whole rows per wavefront");
-    if (S > 1) {
-        // split rows: the residual epilogue of the down projection
-        if (w.dtype != SOSO_HIP_DTYPE_Q4_K || xs != XS_PLAIN || epi != EPI_RESID || (S != 2 && S != 4))
-            return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: variant not built for split rows");
-        const int gpw = 8 / S;
-        const size_t lds = stage_lds_bytes(w.cols) + (size_t)gpw * COMBINE_CH * S * 4;
-        if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: x does not fit in LDS");
-        const int grid = std::max(1, std::min(h->num_cu, (rows + gpw - 1) / gpw));
-        if (!strip_fits(rows, grid * gpw, stride)) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: strip");
-        if (S == 2)
-            mv_rows<FMT_Q4K, 64, 2, ring_depth<FMT_Q4K, 2>(), false, XS_PLAIN, EPI_RESID>
-                <<<grid, 512, lds, h->stream>>>(W, stride, in, y, rows, cols, ep);
-        else
-            mv_rows<FMT_Q4K, 64, 4, ring_depth<FMT_Q4K, 4>(), false, XS_PLAIN, EPI_RESID>
-                <<<grid, 512, lds, h->stream>>>(W, stride, in, y, rows, cols, ep);
-        return hip_check(h, hipGetLastError(), "matvec_ex launch");
+    if (xs == XS_RMSNORM && epi == EPI_QKV)
+        launch_ex_lpr<FMT, XS_RMSNORM, EPI_QKV>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
+    else if (xs == XS_RMSNORM && epi == EPI_SWIGLU)
+        launch_ex_lpr<FMT, XS_RMSNORM, EPI_SWIGLU>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
+    else if (xs == XS_PLAIN && epi == EPI_RESID)
+        launch_ex_lpr<FMT, XS_PLAIN, EPI_RESID>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
+    else
+        launch_ex_lpr<FMT, XS_RMSNORM, EPI_STORE>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
+}
+
+template <int FMT, int S>
+static void launch_ex_split(soso_hip *h, unsigned grid, size_t lds, const uint8_t *W, size_t stride, const MvIn &in,
+                            float *y, int rows, int cols, const MvEpi &ep)
+{
+    mv_rows<FMT, 64, S, ring_depth<FMT, S>(), false, XS_PLAIN, EPI_RESID><<<grid, 512, lds, h->stream>>>(
+        W, stride, in, y, rows, cols, ep);
+}
+
+// The launch of one decode-step matvec (input variant xs, output variant
+// epi), or the reason it cannot run here.  The variants built: every
+// quantized format (Q4_K, Q8_0, Q6_K) with (RMSNORM, QKV), (RMSNORM, SWIGLU),
+// (PLAIN, RESID) and (RMSNORM, STORE); rows of up to 64 units (4096 columns)
+// per wavefront, and the residual variant also with rows split over 2 or 4
+// wavefronts (up to 16384 columns).
+struct ExPlan {
+    int S = 1, lpr = 64, grid = 1;
+    size_t lds = 0, stride = 0;
+    bool il = false;
+};
+
+static const char *plan_matvec_ex(const soso_hip *h, uint8_t dtype, size_t rows_, size_t cols_, int xs, int epi,
+                                  ExPlan &p)
+{
+    if (dtype != SOSO_HIP_DTYPE_Q4_K && dtype != SOSO_HIP_DTYPE_Q8_0 && dtype != SOSO_HIP_DTYPE_Q6_K)
+        return "matvec_ex: the decode matvecs take Q4_K, Q8_0 or Q6_K weights";
+    if (!packed_shape_ok(dtype, rows_, cols_) || rows_ > (1u << 30) || cols_ > (1u << 20))
+        return "matvec_ex: shape not handled here";
+    if (!(xs == XS_RMSNORM && (epi == EPI_QKV || epi == EPI_SWIGLU || epi == EPI_STORE)) &&
+        !(xs == XS_PLAIN && epi == EPI_RESID))
+        return "matvec_ex: input/output variant not built";
+    const int rows = (int)rows_, cols = (int)cols_, U = cols / 64;
+    p.stride = packed_row_stride(dtype, cols_);
+    p.S = (U + 63) / 64;
+    if (xs == XS_RMSNORM && cols > XPRE_N * 8 * 512) return "matvec_ex: normalised x wider than the staging registers";
+    if ((epi == EPI_QKV || epi == EPI_SWIGLU) && (p.S != 1 || rows % 2))
+        return "matvec_ex: pair epilogue needs whole rows per wavefront";
+    if (p.S > 1) {
+        if (xs != XS_PLAIN || epi != EPI_RESID || (p.S != 2 && p.S != 4))
+            return "matvec_ex: variant not built for split rows";
+        const int gpw = 8 / p.S;
+        p.lds = stage_lds_bytes(cols_) + (size_t)gpw * COMBINE_CH * p.S * 4;
+        if (p.lds > h->max_lds) return "matvec_ex: x does not fit in LDS";
+        p.grid = std::max(1, std::min(h->num_cu, (rows + gpw - 1) / gpw));
+        if (!strip_fits(rows, p.grid * gpw, p.stride)) return "matvec_ex: row strip exceeds 2 GiB";
+        return nullptr;
     }
-    const int LPR = U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
-    if (U < 8) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: rows narrower than 512 columns");
-    const int RW = 64 / LPR, gpw = 8;
+    if (U < 8) return "matvec_ex: rows narrower than 512 columns";
+    p.lpr = U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
+    const int RW = 64 / p.lpr, gpw = 8;
     const int PU = (RW == 1 && (epi == EPI_QKV || epi == EPI_SWIGLU)) ? 2 : 1;
     const int passes = (rows + RW - 1) / RW, units = (passes + PU - 1) / PU;
-    const size_t lds = stage_lds_bytes(w.cols) + 64;
-    if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: x does not fit in LDS");
+    p.lds = stage_lds_bytes(cols_) + 64;
+    if (p.lds > h->max_lds) return "matvec_ex: x does not fit in LDS";
     // two workgroups per CU for the gate/up pair (2 x 14336 x 4096 on MI355X:
     // 15.2 us, 15.9 us at one per CU); one for the others (qkv, o and the head
     // were slower at two)
@@ -632,26 +664,47 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, con
     int grid = std::min(h->num_cu * wg_per_cu, (units + gpw - 1) / gpw);
     const int upw = 64 / (PU * RW); // units per 64-row strip
     grid = std::max(grid, ((units + upw - 1) / upw + gpw - 1) / gpw);
-    grid = std::max(grid, 1);
-    if (!strip_fits(passes, grid * gpw, (size_t)RW * stride)) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: strip");
-    const bool il = interleave_fits(passes, PU, grid * gpw, (size_t)RW * stride);
-    bool ok = false;
-    const unsigned g = (unsigned)grid;
-    if (w.dtype == SOSO_HIP_DTYPE_Q4_K) {
-        if (xs == XS_RMSNORM && epi == EPI_QKV)
-            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_QKV>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
-        else if (xs == XS_RMSNORM && epi == EPI_SWIGLU)
-            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_SWIGLU>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
-        else if (xs == XS_PLAIN && epi == EPI_RESID)
-            ok = launch_ex_lpr<FMT_Q4K, XS_PLAIN, EPI_RESID>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
-        else if (xs == XS_RMSNORM && epi == EPI_STORE)
-            ok = launch_ex_lpr<FMT_Q4K, XS_RMSNORM, EPI_STORE>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
-    } else if (w.dtype == SOSO_HIP_DTYPE_Q6_K && xs == XS_RMSNORM && epi == EPI_STORE) {
-        ok = launch_ex_lpr<FMT_Q6K, XS_RMSNORM, EPI_STORE>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
-    } else if (w.dtype == SOSO_HIP_DTYPE_Q8_0 && xs == XS_RMSNORM && epi == EPI_STORE) {
-        ok = launch_ex_lpr<FMT_Q80, XS_RMSNORM, EPI_STORE>(h, LPR, il, g, lds, W, stride, in, y, rows, cols, ep);
+    p.grid = std::max(grid, 1);
+    if (!strip_fits(passes, p.grid * gpw, (size_t)RW * p.stride)) return "matvec_ex: row strip exceeds 2 GiB";
+    p.il = interleave_fits(passes, PU, p.grid * gpw, (size_t)RW * p.stride);
+    if (!p.il && epi != EPI_STORE) return "matvec_ex: matrix too large for the interleaved rows of this variant";
+    return nullptr;
+}
+
+const char *matvec_ex_unsupported(const soso_hip *h, uint8_t dtype, size_t rows, size_t cols, int xs, int epi)
+{
+    ExPlan p;
+    return plan_matvec_ex(h, dtype, rows, cols, xs, epi, p);
+}
+
+int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, const MvEpi &ep, int xs, int epi)
+{
+    ExPlan p;
+    if (const char *why = plan_matvec_ex(h, w.dtype, w.rows, w.cols, xs, epi, p)) return set_err(h, SOSO_HIP_DECLINED, why);
+    const int rows = (int)w.rows, cols = (int)w.cols;
+    const uint8_t *W = (const uint8_t *)w.dev;
+    const unsigned g = (unsigned)p.grid;
+    if (p.S > 1) {
+#define EX_SPLIT(F)                                                                                                    \
+    if (p.S == 2) launch_ex_split<F, 2>(h, g, p.lds, W, p.stride, in, y, rows, cols, ep);                              \
+    else launch_ex_split<F, 4>(h, g, p.lds, W, p.stride, in, y, rows, cols, ep);
+        switch (w.dtype) {
+        case SOSO_HIP_DTYPE_Q4_K: EX_SPLIT(FMT_Q4K) break;
+        case SOSO_HIP_DTYPE_Q8_0: EX_SPLIT(FMT_Q80) break;
+        default: EX_SPLIT(FMT_Q6K) break;
+        }
+#undef EX_SPLIT
+        return hip_check(h, hipGetLastError(), "matvec_ex launch");
     }
-    if (!ok) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: variant not built");
+    switch (w.dtype) {
+    case SOSO_HIP_DTYPE_Q4_K:
+        launch_ex_fmt<FMT_Q4K>(h, xs, epi, p.lpr, p.il, g, p.lds, W, p.stride, in, y, rows, cols, ep);
+        break;
+    case SOSO_HIP_DTYPE_Q8_0:
+        launch_ex_fmt<FMT_Q80>(h, xs, epi, p.lpr, p.il, g, p.lds, W, p.stride, in, y, rows, cols, ep);
+        break;
+    default: launch_ex_fmt<FMT_Q6K>(h, xs, epi, p.lpr, p.il, g, p.lds, W, p.stride, in, y, rows, cols, ep); break;
+    }
     return hip_check(h, hipGetLastError(), "matvec_ex launch");
 }
 
@@ -790,55 +843,67 @@ int launch_dequant(soso_hip *h, const Weight &w, float *out)
 }
 
 // ---------------------------------------------------------------------------
-// argmax (crates/soso-llm-core/src/runtime.rs:2021-2028): the LAST maximum
-// wins.  Combining ordered segments as "earlier wins only if strictly
-// greater" reproduces the sequential fold for finite inputs.  Every
+// argmax (crates/soso-llm-core/src/runtime.rs:2021-2028): Iterator::max_by
+// with partial_cmp(..).unwrap_or(Equal), i.e. the fold "keep the running
+// maximum only if it is strictly greater than the next element, else take the
+// next": the LAST maximum wins, and a NaN compares Equal both ways, so it
+// takes over the running maximum and hands it to the next element.  Every
+// thread folds a contiguous stretch exactly so; stretches combine in order:
+// the later stretch's winner replaces the earlier one unless the earlier is
+// strictly greater -- or always, when the later stretch holds a NaN (the
+// sequential fold restarts at that NaN whatever came before).  Every
 // workgroup reduces one contiguous segment; the last one to finish (ticket)
 // combines the segments' winners in order.
 // ---------------------------------------------------------------------------
-constexpr int ARGMAX_WG = 256; // workgroups (<= the block size; partials: 2 KiB after the ticket)
+constexpr int ARGMAX_WG = 256; // workgroups (<= the block size; partials: 3 KiB after the ticket)
 
-__device__ __forceinline__ void keep_later(float &bv, int &bi, float ov, int oi)
+__device__ __forceinline__ void keep_later(float &bv, int &bi, int &bn, float ov, int oi, int on)
 {
-    // (bv, bi) is the earlier segment's winner; the later one replaces it
-    // unless the earlier is strictly greater
-    if (oi >= 0 && (bi < 0 || !(bv > ov))) {
+    // (bv, bi, bn) is the earlier stretch's (winner, index, holds a NaN)
+    if (oi >= 0 && (bi < 0 || on || !(bv > ov))) {
         bv = ov;
         bi = oi;
     }
+    bn |= on;
 }
 
 __global__ void __launch_bounds__(256) k_argmax(const float *__restrict__ x, int n, uint32_t *__restrict__ out,
                                                 unsigned *__restrict__ ticket)
 {
     __shared__ float sv[4];
-    __shared__ int si[4];
+    __shared__ int si[4], sn[4];
     __shared__ int last;
     float *pv = (float *)(ticket + 64);
     int *pi = (int *)(ticket + 64 + ARGMAX_WG);
+    int *pn = (int *)(ticket + 64 + 2 * ARGMAX_WG);
     const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63;
     const int s0 = (int)((long)n * blockIdx.x / gridDim.x), s1 = (int)((long)n * (blockIdx.x + 1) / gridDim.x);
     const int c0 = s0 + (int)((long)(s1 - s0) * tid / nt), c1 = s0 + (int)((long)(s1 - s0) * (tid + 1) / nt);
     float bv = -INFINITY;
-    int bi = -1;
-    for (int i = c0; i < c1; i++) keep_later(bv, bi, x[i], i);
-    // lanes hold ordered segments: fold pairs (lower lane = earlier)
+    int bi = -1, bn = 0;
+    for (int i = c0; i < c1; i++) {
+        const float v = x[i];
+        keep_later(bv, bi, bn, v, i, v != v);
+    }
+    // lanes hold ordered stretches: fold pairs (lower lane = earlier)
     for (int o = 1; o < 64; o <<= 1) {
         const float ov = __shfl_down(bv, o, 64);
-        const int oi = __shfl_down(bi, o, 64);
-        if (lane + o < 64 && (lane & (2 * o - 1)) == 0) keep_later(bv, bi, ov, oi);
+        const int oi = __shfl_down(bi, o, 64), on = __shfl_down(bn, o, 64);
+        if (lane + o < 64 && (lane & (2 * o - 1)) == 0) keep_later(bv, bi, bn, ov, oi, on);
     }
     if (lane == 0) {
         sv[tid >> 6] = bv;
         si[tid >> 6] = bi;
+        sn[tid >> 6] = bn;
     }
     __syncthreads();
     if (tid == 0) {
         float v = sv[0];
-        int i = si[0];
-        for (int w = 1; w < (nt >> 6); w++) keep_later(v, i, sv[w], si[w]);
+        int i = si[0], q = sn[0];
+        for (int w = 1; w < (nt >> 6); w++) keep_later(v, i, q, sv[w], si[w], sn[w]);
         pv[blockIdx.x] = v;
         pi[blockIdx.x] = i;
+        pn[blockIdx.x] = q;
         __threadfence();
         last = atomicAdd(ticket, 1u) == gridDim.x - 1;
     }
@@ -848,24 +913,26 @@ __global__ void __launch_bounds__(256) k_argmax(const float *__restrict__ x, int
     // the segments' winners, in segment order, reduced by the same ordered tree
     bv = -INFINITY;
     bi = -1;
-    for (int b = tid; b < (int)gridDim.x; b += nt) keep_later(bv, bi, pv[b], pi[b]);
+    bn = 0;
+    for (int b = tid; b < (int)gridDim.x; b += nt) keep_later(bv, bi, bn, pv[b], pi[b], pn[b]);
     // thread t now holds segments t, t + nt, ...: with gridDim <= blockDim
     // that is one segment per thread, in order
     for (int o = 1; o < 64; o <<= 1) {
         const float ov = __shfl_down(bv, o, 64);
-        const int oi = __shfl_down(bi, o, 64);
-        if (lane + o < 64 && (lane & (2 * o - 1)) == 0) keep_later(bv, bi, ov, oi);
+        const int oi = __shfl_down(bi, o, 64), on = __shfl_down(bn, o, 64);
+        if (lane + o < 64 && (lane & (2 * o - 1)) == 0) keep_later(bv, bi, bn, ov, oi, on);
     }
     __syncthreads();
     if (lane == 0) {
         sv[tid >> 6] = bv;
         si[tid >> 6] = bi;
+        sn[tid >> 6] = bn;
     }
     __syncthreads();
     if (tid == 0) {
         float v = sv[0];
-        int i = si[0];
-        for (int w = 1; w < (nt >> 6); w++) keep_later(v, i, sv[w], si[w]);
+        int i = si[0], q = sn[0];
+        for (int w = 1; w < (nt >> 6); w++) keep_later(v, i, q, sv[w], si[w], sn[w]);
         *out = (uint32_t)(i < 0 ? 0 : i);
         *ticket = 0u;
     }

@@ -263,11 +263,13 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
                     // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
                     float mx = fmaxf(fmaxf(fmaxf(fabsf(v0[k].x), fabsf(v0[k].y)), fmaxf(fabsf(v0[k].z), fabsf(v0[k].w))),
                                      fmaxf(fmaxf(fabsf(v1[k].x), fabsf(v1[k].y)), fmaxf(fabsf(v1[k].z), fabsf(v1[k].w))));
-                    mx = row16_max(mx);
-                    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                    const int ex = (mx > 0.0f && mx < INFINITY) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
                     // f32 sum of x over the 32-element sub-block: 4 aligned lanes
                     float sm = ((v0[k].x + v0[k].y) + (v0[k].z + v0[k].w)) + ((v1[k].x + v1[k].y) + (v1[k].z + v1[k].w));
+                    if (sm != sm) mx = INFINITY; // a NaN element: the super-block is non-finite
+                    mx = row16_max(mx);
+                    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+                    const bool finite = mx < INFINITY;
+                    const int ex = (mx > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
                     sm += dpp_f<0xB1>(sm);
                     sm += dpp_f<0x4E>(sm);
                     if (valid) {
@@ -280,7 +282,9 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
                         for (int kk = 0; kk < XDIG; kk++)
                             *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * q) = make_uint2(d0[kk], d1[kk]);
                         if (q == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
-                        if ((c & 31) == 0) *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = ldexpf(1.0f, -ex);
+                        // a non-finite super-block: NaN products, as the CPU's dot gives Inf or NaN
+                        if ((c & 31) == 0)
+                            *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
                     }
                 }
             }

@@ -412,7 +412,7 @@ __device__ __forceinline__ void q4k_token_dot(const Q4Prep (&pr)[NMAT], const ui
     }
 #pragma unroll
     for (int m = 0; m < NMAT; m++) q4k_half(pr[m].hi, xh, sb[m]);
-    const float P = ldexpf(1.0f, -kx[u >> 1]);
+    const float P = block_unscale(kx[u >> 1]);
     const float c0 = s16[4 * u] + s16[4 * u + 1], c1 = s16[4 * u + 2] + s16[4 * u + 3];
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {

@@ -75,6 +75,16 @@ __device__ __forceinline__ void digits4(float4 v, int e, uint32_t (&d)[XDIG])
     d[2] = __builtin_amdgcn_perm(D, C, 0x05040100u) ^ 0x80808080u;
 }
 
+// A block of x holding an Inf or a NaN gets this exponent.  Its unscale
+// factor is NaN, so every dot product that meets the block is NaN, as the
+// CPU's f32 dot of such a row is Inf or NaN; the block's digits (of a
+// non-finite value) are never used for a finite result.
+constexpr int KX_NONFINITE = 0x40000000;
+__device__ __forceinline__ float block_unscale(int k)
+{
+    return k == KX_NONFINITE ? __builtin_nanf("") : ldexpf(1.0f, -k);
+}
+
 // One 8-element chunk c (thread lane == c % 64).  Every lane of the 16-lane
 // DPP row takes part (invalid chunks carry zeros); only valid ones store.
 template <int FMT>
@@ -83,9 +93,13 @@ __device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool va
 {
     float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
                     fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
-    m = row16_max(m);
-    const int e = (m > 0.0f && m < INFINITY) ? 22 - __builtin_amdgcn_frexp_expf(m) : 0;
     float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+    // fmaxf passes over a NaN, which the sum keeps: a NaN element marks the
+    // block as an infinite maximum would
+    if (sm != sm) m = INFINITY;
+    m = row16_max(m);
+    const bool finite = m < INFINITY;
+    const int e = (m > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(m) : 0;
     sm += dpp_f<0xB1>(sm);
     if (valid) {
         uint32_t d0[XDIG], d1[XDIG];
@@ -115,7 +129,7 @@ __device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool va
             }
         }
         if ((c & 1) == 0) s16[c >> 1] = sm;
-        if ((c & 15) == 0) kx[c >> 4] = e;
+        if ((c & 15) == 0) kx[c >> 4] = finite ? e : KX_NONFINITE;
     }
 }
 
@@ -296,7 +310,7 @@ template <int FMT>
 __device__ __forceinline__ void unit_setup_x(const uint32_t *xd, const float *s16, const int *kx, int u, int U, XReg &xv,
                                              UConst &c)
 {
-    c.P = ldexpf(1.0f, -kx[u >> 1]);
+    c.P = block_unscale(kx[u >> 1]);
     const uint4 *x4 = (const uint4 *)xd;
 #pragma unroll
     for (int r = 0; r < XD / 4; r++) {

@@ -28,13 +28,29 @@ int hip_check(soso_hip *h, hipError_t e, const char *what)
     return set_err(h, SOSO_HIP_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+static bool any_graph(const soso_hip *h)
+{
+    for (hipGraphExec_t g : h->graphs)
+        if (g) return true;
+    return false;
+}
+
+// Scratch slot `slot` of at least `bytes`, or null.  Growing it inside graph
+// capture is refused (null): it would synchronise and allocate within the
+// capture.  While any graph exists the outgrown buffer is retired instead of
+// freed, since a graph may hold it as a kernel argument.
 void *scratch_get(soso_hip *h, int slot, size_t bytes)
 {
     if (bytes == 0) bytes = 16;
     if (h->scratch_cap[slot] >= bytes) return h->scratch[slot];
+    if (h->capturing) return nullptr;
     if (h->scratch[slot]) {
-        hipStreamSynchronize(h->stream);
-        hipFree(h->scratch[slot]);
+        if (any_graph(h)) {
+            h->retired.push_back(h->scratch[slot]);
+        } else {
+            (void)hipStreamSynchronize(h->stream);
+            (void)hipFree(h->scratch[slot]);
+        }
         h->scratch[slot] = nullptr;
         h->scratch_cap[slot] = 0;
     }
@@ -44,6 +60,14 @@ void *scratch_get(soso_hip *h, int slot, size_t bytes)
     h->scratch[slot] = p;
     h->scratch_cap[slot] = cap;
     return p;
+}
+
+static void free_retired(soso_hip *h)
+{
+    if (h->retired.empty()) return;
+    (void)hipStreamSynchronize(h->stream);
+    for (void *p : h->retired) (void)hipFree(p);
+    h->retired.clear();
 }
 
 namespace {
@@ -226,7 +250,8 @@ void soso_hip_destroy(soso_hip *h)
         if (kv.second.dev) hipFree(kv.second.dev);
     for (auto &kv : h->f32_tensors) hipFree(kv.second);
     for (int i = 0; i < soso_hip::N_SCRATCH; i++)
-        if (h->scratch[i]) hipFree(h->scratch[i]);
+        if (h->scratch[i]) (void)hipFree(h->scratch[i]);
+    for (void *p : h->retired) (void)hipFree(p);
     for (auto &kv : h->moe_layers) moe_free(h, kv.second);
     for (auto &kv : h->decode_models) decode_free(h, kv.second);
     if (h->ticket) hipFree(h->ticket);
@@ -609,7 +634,10 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
     if (rc != SOSO_HIP_OK) return rc;
     MoeScratch ms;
     if (!moe_scratch(h, n, m.n_exp, m.top_k, m.hdim, m.ffn, ms))
-        return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_ffn_dev: scratch");
+        return h->capturing ? set_err(h, SOSO_HIP_DECLINED,
+                                      "moe_ffn_dev: its scratch would have to grow inside graph capture (make one call "
+                                      "with this token count outside capture first)")
+                            : set_err(h, SOSO_HIP_ERR_NOMEM, "moe_ffn_dev: scratch");
     if (idx_dev) ms.idx = idx_dev;
     if (wgt_dev) ms.wgt = wgt_dev;
     if (n == 1) {
@@ -637,6 +665,11 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     const size_t L = cfg->n_layers, H = cfg->hidden, qd = (size_t)cfg->n_heads * cfg->head_dim,
                  kvd = (size_t)cfg->n_kv_heads * cfg->head_dim, F = cfg->ffn;
     if (cfg->head_dim != 128) return set_err(h, SOSO_HIP_DECLINED, "decode_create: head_dim must be 128");
+    {
+        const uint32_t G = cfg->n_heads / cfg->n_kv_heads;
+        if (G != 1 && G != 2 && G != 4 && G != 8)
+            return set_err(h, SOSO_HIP_DECLINED, "decode_create: query heads per KV head must be 1, 2, 4 or 8");
+    }
     DecodeModel m;
     m.n_layers = L;
     m.hidden = H;
@@ -668,12 +701,29 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
                                                      ": a weight is missing or has the wrong shape");
         if (q[l]->dtype != k[l]->dtype || q[l]->dtype != v[l]->dtype || g[l]->dtype != u[l]->dtype)
             return set_err(h, SOSO_HIP_DECLINED, "decode_create: q/k/v or gate/up dtypes differ");
+        // every launch of the step, checked here so that a step never declines
+        // halfway through a token
+        const struct {
+            const Weight *w;
+            size_t rows, cols;
+            int xs, epi;
+            const char *role;
+        } roles[] = {{q[l], qd + 2 * kvd, H, XS_RMSNORM, EPI_QKV, "q/k/v"},
+                     {m.layers[l].o, H, qd, XS_PLAIN, EPI_RESID, "o"},
+                     {g[l], 2 * F, H, XS_RMSNORM, EPI_SWIGLU, "gate/up"},
+                     {m.layers[l].down, H, F, XS_PLAIN, EPI_RESID, "down"}};
+        for (const auto &r : roles)
+            if (const char *why = matvec_ex_unsupported(h, r.w->dtype, r.rows, r.cols, r.xs, r.epi))
+                return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + " " + r.role + ": " +
+                                                         why);
         m.layers[l].attn_norm = (const float *)an->dev;
         m.layers[l].ffn_norm = (const float *)fn->dev;
     }
     const Weight *on;
     if (!get(9 * L, 1, H, true, &on) || !get(9 * L + 1, cfg->vocab, H, false, &m.head))
         return set_err(h, SOSO_HIP_DECLINED, "decode_create: output_norm/head missing or of the wrong shape");
+    if (const char *why = matvec_ex_unsupported(h, m.head->dtype, cfg->vocab, H, XS_RMSNORM, EPI_STORE))
+        return set_err(h, SOSO_HIP_DECLINED, std::string("decode_create: head: ") + why);
     m.out_norm = (const float *)on->dev;
     // what stays in use (dropping one of these unregisters the model)
     for (size_t l = 0; l < L; l++)
@@ -693,12 +743,18 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
         wg.rows = 2 * F;
         wg.cols = H;
         wg.bytes = wg.rows * st_gu;
-        if (h->used + wq.bytes + wg.bytes > h->budget || hipMalloc(&wq.dev, wq.bytes) != hipSuccess ||
-            hipMalloc(&wg.dev, wg.bytes) != hipSuccess) {
+        // each allocation is counted as it succeeds, so decode_free's release
+        // of whatever was allocated keeps h->used exact on a failure
+        bool got = h->used + wq.bytes + wg.bytes <= h->budget && hipMalloc(&wq.dev, wq.bytes) == hipSuccess;
+        if (got) h->used += wq.bytes;
+        else wq.dev = nullptr;
+        got = got && hipMalloc(&wg.dev, wg.bytes) == hipSuccess;
+        if (got) h->used += wg.bytes;
+        else wg.dev = nullptr;
+        if (!got) {
             rc = set_err(h, SOSO_HIP_DECLINED, "decode_create: no memory for the fused weights");
             break;
         }
-        h->used += wq.bytes + wg.bytes;
         char *dq = (char *)wq.dev;
         rc = hip_check(h, hipMemcpyAsync(dq, q[l]->dev, qd * st_qkv, hipMemcpyDeviceToDevice, h->stream), "qkv copy");
         if (rc == SOSO_HIP_OK)
@@ -1103,9 +1159,10 @@ int soso_hip_graph_destroy(soso_hip *h, int id)
     if (!h || id < 0 || (size_t)id >= h->graphs.size() || !h->graphs[id]) return SOSO_HIP_ERR_ARG;
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
-    hipStreamSynchronize(h->stream);
-    hipGraphExecDestroy(h->graphs[id]);
+    (void)hipStreamSynchronize(h->stream);
+    (void)hipGraphExecDestroy(h->graphs[id]);
     h->graphs[id] = nullptr;
+    if (!any_graph(h)) free_retired(h); // no graph can hold them any more
     return SOSO_HIP_OK;
 }
 

@@ -742,7 +742,8 @@ def prepare_decode(gpu, som, model_key, ctx_max=None, kv_f16=False):
             rows, cols = (1, shape[0]) if len(shape) == 1 else shape
             _upload(gpu, name, v, rows, cols)
         keys.append(name)
-    gpu.decode_create(model_key, cfg, keys)
+    if not gpu.decode_create(model_key, cfg, keys):
+        raise SomError(f"prepare_decode: the device step declined the model: {gpu.last_error()}", ERR_ARG)
     return SomDecoder(gpu, som, model_key, cfg, keys, m.embed_scale())
 
 

@@ -214,3 +214,76 @@ def test_matvec_lote(gpu, orc):
     for op, ref in zip(ops, refs):
         if ref is not None:
             assert orc.rel_l2(op["out"], ref) < TOL
+
+
+@pytest.mark.parametrize("dtype", [Q4K, Q8, Q6K])
+def test_matvec_nonfinite_x_gives_nan(gpu, orc, dtype):
+    """An Inf or a NaN in x makes every output non-finite, as the CPU's f32
+    dot does (Inf or NaN); the staging marks the block instead of turning the
+    value into finite digits.  Rows are unchanged once x is finite again (the
+    marked block leaves no state behind)."""
+    rows, cols = 200, 4096
+    w = orc.synth(dtype, rows, cols, 81, dtype)
+    key = f"nonfinite.{dtype}"
+    x = orc.normal(cols, 1.0, 82, 1).copy()
+    try:
+        for bad in ((300, np.inf), (2000, np.nan), (4095, -np.inf)):
+            xb = x.copy()
+            xb[bad[0]] = bad[1]
+            y = run_matvec(gpu, key, dtype, w, rows, cols, xb)
+            ycpu = orc.matvec(dtype, w, rows, cols, xb)
+            assert not np.any(np.isfinite(ycpu))
+            assert np.all(np.isnan(y)), (bad, y[:4])
+        y = run_matvec(gpu, key, dtype, w, rows, cols, x)
+        assert orc.rel_l2(y, orc.matvec_f64(dtype, w, rows, cols, x)) < TOL
+    finally:
+        gpu.weight_drop(key)
+
+
+def test_matmul_nonfinite_token_stays_its_own(gpu, orc):
+    """On the matrix cores (16 tokens) a token with an Inf in x gets NaN rows;
+    the other tokens' rows match the CPU."""
+    rows, cols, n = 384, 2048, 16
+    w = orc.synth(Q4K, rows, cols, 83, 1)
+    xs = orc.normal(n * cols, 1.0, 84, 1).reshape(n, cols).copy()
+    xs[5, 1000] = np.inf
+    out = np.empty(n * rows, np.float32)
+    key = "nonfinite.mm"
+    try:
+        assert gpu.matmul(key, w, Q4K, rows, cols, n, xs, out), gpu.last_error()
+        out = out.reshape(n, rows)
+        ref = orc.matmul(Q4K, w, rows, cols, np.where(np.isfinite(xs), xs, 0).astype(np.float32), threads=8)
+        assert np.all(np.isnan(out[5]))
+        for j in range(n):
+            if j != 5:
+                assert orc.rel_l2(out[j], ref[j]) < TOL, j
+    finally:
+        gpu.weight_drop(key)
+
+
+@pytest.mark.parametrize("n,nans", [
+    (300000, [5, 100000]),            # NaNs in early segments; the maximum lies after them
+    (300000, [299999]),               # a NaN last: it wins
+    (300000, [150000, 150001]),       # two NaNs in a row inside one segment
+    (1000, [0]), (7, [3]), (257, [256, 1]),
+])
+def test_argmax_nan_follows_max_by(gpu, orc, n, nans):
+    """Runtime::argmax is max_by over partial_cmp, a NaN comparing Equal both
+    ways: the running maximum restarts after every NaN.  The device argmax
+    must give the oracle's index (the same fold) across segment boundaries."""
+    x = orc.normal(n, 1.0, 85, len(nans)).copy()
+    x[n // 3] = 50.0
+    x[n // 7] = 60.0  # the largest, before or after the NaNs
+    for p in nans:
+        x[p] = np.nan
+    want = int(orc.lib().or_argmax(x.ctypes.data, n))
+    xd = gpu.dev_alloc(n * 4)
+    idx = gpu.dev_alloc(4)
+    try:
+        gpu.h2d(xd, x)
+        gpu.argmax_dev(xd, n, idx)
+        got = int(gpu.d2h(idx, (1,), np.uint32)[0])
+    finally:
+        gpu.dev_free(xd)
+        gpu.dev_free(idx)
+    assert got == want, (got, want)

@@ -232,3 +232,66 @@ def test_experts_block_declines_shared_and_sums_the_rest(gpu, orc):
             assert orc.rel_l2(full[t * h:(t + 1) * h], refs[t]) < 1e-5
     finally:
         layer.drop(gpu)
+
+
+def test_moe_graph_survives_scratch_growth(gpu, orc):
+    """A graph holding a single-token moe_ffn_dev keeps the scratch it was
+    captured with: a later call that outgrows the MoE scratch slots (a
+    256-token router call) must leave that memory alive, so replaying the
+    graph gives the eager call's bits.  A call whose scratch would have to
+    grow inside the capture is declined instead of allocating there."""
+    n_exp, h, ffn, top_k = 128, 2048, 768, 8
+    layer = Layer(orc, n_exp, h, ffn, top_k, 61)
+    layer.upload(gpu)
+    x = orc.normal(h, 1.0, 62, 1)
+    xd = gpu.dev_alloc(x.nbytes)
+    od = gpu.dev_alloc(h * 4)
+    gid = None
+    try:
+        gpu.h2d(xd, x)
+        assert gpu.moe_ffn_dev(layer.name, xd, 1, od), gpu.last_error()
+        gpu.sync()
+        eager = gpu.d2h(od, (h,), np.float32)
+        gpu.graph_begin()
+        try:
+            ok = gpu.moe_ffn_dev(layer.name, xd, 1, od)
+        finally:
+            gid = gpu.graph_end()
+        assert ok, gpu.last_error()
+        # outgrow the MoE scratch slots while the graph exists
+        n = 256
+        w = orc.normal(n_exp * h, 0.02, 63, 1)
+        xs = orc.normal(n * h, 1.0, 64, 1)
+        idx = np.zeros(n * top_k, np.int32)
+        wgt = np.zeros(n * top_k, np.float32)
+        assert gpu.router_topk("router.growth", w, xs, n, h, n_exp, top_k, idx, wgt), gpu.last_error()
+        for rep in range(3):
+            gpu.h2d(od, np.zeros(h, np.float32))
+            gpu.graph_launch(gid)
+            gpu.sync()
+            got = gpu.d2h(od, (h,), np.float32)
+            assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), rep
+        gpu.graph_destroy(gid)
+        gid = None
+        # a capture whose call would need more scratch than the slots hold is declined
+        big = 500
+        xb = gpu.dev_alloc(big * h * 4)
+        ob = gpu.dev_alloc(big * h * 4)
+        try:
+            gpu.graph_begin()
+            try:
+                ok = gpu.moe_ffn_dev(layer.name, xb, big, ob)
+            finally:
+                g2 = gpu.graph_end()
+                gpu.graph_destroy(g2)
+            assert ok is False
+            assert "inside graph capture" in gpu.last_error()
+        finally:
+            gpu.dev_free(xb)
+            gpu.dev_free(ob)
+    finally:
+        if gid is not None:
+            gpu.graph_destroy(gid)
+        gpu.dev_free(xd)
+        gpu.dev_free(od)
+        layer.drop(gpu)

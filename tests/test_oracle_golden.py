@@ -406,6 +406,24 @@ def test_argmax_last_maximum_wins(orc):
         assert L.or_argmax(a.ctypes.data, a.size) == want
 
 
+def test_argmax_nan_known_answers(orc):
+    """Runtime::argmax (runtime.rs:2021-2028) is Iterator::max_by with
+    partial_cmp(..).unwrap_or(Equal): max_by reduces with cmp::max_by, which
+    keeps the running value only when it compares Greater and otherwise takes
+    the next element; a NaN compares Equal both ways.  Indices worked out by
+    hand from that rule."""
+    L = orc.lib()
+    nan = float("nan")
+    for arr, want in (([1, nan, 0.5], 2),      # NaN takes over, then hands over to 0.5
+                      ([5, 1, nan], 2),        # a NaN last wins
+                      ([nan, 3, 2], 1),        # a NaN first is replaced by the next element
+                      ([3, nan, 1, 2], 3),     # after the NaN the fold restarts at 1
+                      ([9, nan, 1, 9], 3),
+                      ([nan], 0), ([2, nan, nan], 2)):
+        a = np.array(arr, np.float32)
+        assert L.or_argmax(a.ctypes.data, a.size) == want, (arr, want)
+
+
 def test_swiglu_avx2_close_to_libm(orc):
     L = orc.lib()
     if not L.or_have_avx2():
