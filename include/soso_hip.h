@@ -156,6 +156,23 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
 int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev, size_t n,
                          float *out_dev, int32_t *idx_dev, float *wgt_dev);
 
+/* No counterpart in the reference: soso_hip_moe_ffn_dev for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as soso_hip_moe_ffn_dev (the
+ * same kernels), but its scratch (router logits, routing, slot lists, work
+ * items, activations) is a fixed array of SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES
+ * that the library holds on every GPU it runs on until the process ends; the
+ * call allocates and frees nothing.  A call whose scratch (about
+ * n * top_k * (ffn + hdim) * 4 bytes plus the routing lists) exceeds the
+ * array returns SOSO_HIP_ERR_ARG.  Every call on a GPU shares that GPU's
+ * array, so calls that overlap on one GPU (two streams, two handles) race;
+ * calls in order on one stream do not.  Nothing in the array needs to start
+ * at zero: each call writes every region before it reads it.  Asynchronous
+ * on the handle's stream. */
+#define SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES (8u << 20)
+int soso_hip_moe_ffn_dev_noalloc(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev,
+                                 size_t n, float *out_dev, int32_t *idx_dev, float *wgt_dev);
+
 /* ---- dense decode step resident on the device -----------------------------------
  * The device-resident decode of GpuDispatch::decode_preparar / decode_token
  * (gpu.rs:653-690) for a Llama-style dense model (LayerExecutor::forward_layer,

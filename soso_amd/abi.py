@@ -74,6 +74,7 @@ PROTOTYPES = {
     "soso_hip_experts_block": (_I, [_P, _P, _S, _S, _S, _S, _P, _P, _S, _P, _P]),
     "soso_hip_moe_register": (_I, [_P, C.c_char_p, _S, C.c_char_p, _S, _P, _P, _S, _S, _S, _S]),
     "soso_hip_moe_ffn_dev": (_I, [_P, C.c_char_p, _S, _P, _S, _P, _P, _P]),
+    "soso_hip_moe_ffn_dev_noalloc": (_I, [_P, C.c_char_p, _S, _P, _S, _P, _P, _P]),
     "soso_hip_decode_create": (_I, [_P, C.c_char_p, _S, C.POINTER(DecodeCfg), _P, _P, _I]),
     "soso_hip_decode_kv_dev": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),
     "soso_hip_decode_kv_upload": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P, _I]),
@@ -104,6 +105,8 @@ PROTOTYPES = {
     "soso_hip_graph_launch": (_I, [_P, _I]),
     "soso_hip_graph_destroy": (_I, [_P, _I]),
 }
+
+MOE_NOALLOC_SCRATCH_BYTES = 8 << 20  # SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 

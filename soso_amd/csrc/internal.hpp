@@ -110,6 +110,9 @@ struct soso_hip {
     // route), uints 64 .. 831 argmax partials (winner, index, holds-NaN flag per segment), uints 2048 .. 3071 the MoE
     // route's per-token-block counters
     unsigned *ticket = nullptr;
+    // device address of this GPU's fixed scratch array (runtime.hip), the
+    // scratch of soso_hip_moe_ffn_dev_noalloc; looked up once, at create
+    void *fixed_scratch = nullptr;
     std::unordered_map<std::string, MoeLayer> moe_layers;
     std::unordered_map<std::string, DecodeModel> decode_models;
     std::vector<hipEvent_t> events; // per-launch timing slots
@@ -192,6 +195,10 @@ struct MoeScratch {
     float *ydown = nullptr;  // n x top_k x hdim
 };
 bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s);
+// The same regions in one buffer of `cap` bytes at `base` (256-byte aligned
+// pieces); returns the bytes needed, and sets s only when they fit.
+size_t moe_scratch_fixed(const soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn,
+                         void *base, size_t cap, MoeScratch &s);
 int moe_item_target(const soso_hip *h);
 // (k_mfma.hip) -- Q4_K on the matrix cores for several tokens per row
 bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols);

@@ -832,15 +832,22 @@ size_t moe_max_items(const soso_hip *h, size_t slots, size_t n_groups)
     return (size_t)moe_item_target(h) + std::min(slots, n_groups) + 1;
 }
 
-// Scratch slots 8..11 belong to the MoE path.
-bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s)
+// Bytes of the three scratch regions of one MoE FFN call: f32 logits and the
+// routing, the integer lists (counts, offsets, slots, work items, records),
+// and the activations (gate/up results and down outputs per slot).
+static void moe_scratch_sizes(const soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn,
+                              size_t (&sz)[3])
 {
-    const size_t slots = n * top_k;
-    char *f = (char *)scratch_get(h, 8, (n * (n_groups > 0 ? n_groups : 1) + 2 * slots) * 4);
-    const size_t n_g = n_groups > 0 ? n_groups : 1;
-    int *ints = (int *)scratch_get(h, 9, (2 * n_g + 2 + slots + 4 * moe_max_items(h, slots, n_g) + 4 * n_g + 1) * 4);
-    float *big = (float *)scratch_get(h, 10, slots * (ffn + hdim) * 4);
-    if (!f || !ints || !big) return false;
+    const size_t slots = n * top_k, n_g = n_groups > 0 ? n_groups : 1;
+    sz[0] = (n * n_g + 2 * slots) * 4;
+    sz[1] = (2 * n_g + 2 + slots + 4 * moe_max_items(h, slots, n_g) + 4 * n_g + 1) * 4;
+    sz[2] = slots * (ffn + hdim) * 4;
+}
+
+static void moe_scratch_carve(const soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t ffn, char *f,
+                              int *ints, float *big, MoeScratch &s)
+{
+    const size_t slots = n * top_k, n_g = n_groups > 0 ? n_groups : 1;
     s.logits = (float *)f;
     s.idx = (int32_t *)(s.logits + n * n_groups);
     s.wgt = (float *)(s.idx + slots);
@@ -853,7 +860,35 @@ bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hd
     s.n_recs = s.recs + 4 * n_g;
     s.act = big;
     s.ydown = big + slots * ffn;
+}
+
+// Scratch slots 8..11 belong to the MoE path.
+bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s)
+{
+    size_t sz[3];
+    moe_scratch_sizes(h, n, n_groups, top_k, hdim, ffn, sz);
+    char *f = (char *)scratch_get(h, 8, sz[0]);
+    int *ints = (int *)scratch_get(h, 9, sz[1]);
+    float *big = (float *)scratch_get(h, 10, sz[2]);
+    if (!f || !ints || !big) return false;
+    moe_scratch_carve(h, n, n_groups, top_k, ffn, f, ints, big, s);
     return true;
+}
+
+// The same regions carved out of one buffer of `cap` bytes at `base`, each on
+// a 256-byte boundary.  Returns the bytes the call needs; s is set only when
+// they fit.
+size_t moe_scratch_fixed(const soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn,
+                         void *base, size_t cap, MoeScratch &s)
+{
+    size_t sz[3];
+    moe_scratch_sizes(h, n, n_groups, top_k, hdim, ffn, sz);
+    auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    const size_t o1 = up(sz[0]), o2 = o1 + up(sz[1]), need = o2 + up(sz[2]);
+    if (need > cap || !base) return need;
+    char *b = (char *)base;
+    moe_scratch_carve(h, n, n_groups, top_k, ffn, b, (int *)(b + o1), (float *)(b + o2), s);
+    return need;
 }
 
 int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size_t hdim, size_t n_exp, size_t top_k,

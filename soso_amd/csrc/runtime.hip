@@ -13,6 +13,11 @@
 #include <new>
 
 
+// The scratch of soso_hip_moe_ffn_dev_noalloc: one array per GPU for the
+// life of the process.  Host code uses only the device address that
+// soso_hip_create looks up for its GPU (h->fixed_scratch), never this name.
+static __device__ __align__(256) unsigned char scratch[SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES];
+
 int set_err(soso_hip *h, int code, const std::string &msg)
 {
     if (h) h->err = msg;
@@ -229,6 +234,14 @@ int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out)
     if (hipMalloc((void **)&h->ticket, SOSO_TICKET_BYTES) != hipSuccess ||
         hipMemset(h->ticket, 0, SOSO_TICKET_BYTES) != hipSuccess) {
         hipStreamDestroy(h->stream);
+        delete h;
+        return SOSO_HIP_ERR_DEVICE;
+    }
+    // this GPU's copy of the fixed scratch array (with the device current)
+    if (hipGetSymbolAddress(&h->fixed_scratch, HIP_SYMBOL(scratch)) != hipSuccess || !h->fixed_scratch) {
+        (void)hipGetLastError();
+        (void)hipFree(h->ticket);
+        (void)hipStreamDestroy(h->stream);
         delete h;
         return SOSO_HIP_ERR_DEVICE;
     }
@@ -638,6 +651,38 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
                                       "moe_ffn_dev: its scratch would have to grow inside graph capture (make one call "
                                       "with this token count outside capture first)")
                             : set_err(h, SOSO_HIP_ERR_NOMEM, "moe_ffn_dev: scratch");
+    if (idx_dev) ms.idx = idx_dev;
+    if (wgt_dev) ms.wgt = wgt_dev;
+    if (n == 1) {
+        rc = launch_moe_ffn1(h, m, x_dev, ms, out_dev);
+        if (rc != SOSO_HIP_DECLINED) return rc;
+    }
+    rc = launch_moe_route(h, (const float *)m.router->dev, x_dev, n, m.hdim, m.n_exp, m.top_k, ms);
+    if (rc == SOSO_HIP_OK)
+        rc = launch_moe_experts(h, x_dev, n, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, ms.wgt,
+                                nullptr, ms.idx, ms, out_dev, &m);
+    return rc;
+}
+
+// The allocation-free form of soso_hip_moe_ffn_dev: the same kernels, with
+// the scratch carved out of this GPU's fixed array.
+int soso_hip_moe_ffn_dev_noalloc(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev, size_t n,
+                                 float *out_dev, int32_t *idx_dev, float *wgt_dev)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!layer_key || !x_dev || !out_dev || n == 0) return set_err(h, SOSO_HIP_ERR_ARG, "moe_ffn_dev_noalloc: args");
+    auto it = h->moe_layers.find(std::string(layer_key, layer_key_len));
+    if (it == h->moe_layers.end()) return set_err(h, SOSO_HIP_DECLINED, "moe_ffn_dev_noalloc: layer not registered");
+    const MoeLayer &m = it->second;
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    MoeScratch ms;
+    const size_t need = moe_scratch_fixed(h, n, m.n_exp, m.top_k, m.hdim, m.ffn, h->fixed_scratch,
+                                          SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES, ms);
+    if (need > SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES)
+        return set_err(h, SOSO_HIP_ERR_ARG, "moe_ffn_dev_noalloc: " + std::to_string(n) + " tokens need " +
+                                                std::to_string(need) + " bytes of scratch; the fixed array holds " +
+                                                std::to_string((size_t)SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES));
     if (idx_dev) ms.idx = idx_dev;
     if (wgt_dev) ms.wgt = wgt_dev;
     if (n == 1) {

@@ -273,6 +273,12 @@ class HipGpu:
         return self._rc(self.lib.soso_hip_moe_ffn_dev(self.h, k, kl, x_dev, n, out_dev, idx_dev, wgt_dev),
                         f"moe_ffn_dev {layer_key}")
 
+    def moe_ffn_dev_noalloc(self, layer_key, x_dev, n, out_dev, idx_dev=None, wgt_dev=None):
+        """moe_ffn_dev with the library's fixed scratch array: allocates nothing."""
+        k, kl = _key(layer_key)
+        return self._rc(self.lib.soso_hip_moe_ffn_dev_noalloc(self.h, k, kl, x_dev, n, out_dev, idx_dev, wgt_dev),
+                        f"moe_ffn_dev_noalloc {layer_key}")
+
     # -- dense decode step resident on the device (decode_preparar / decode_token) --
     def decode_create(self, model_key, cfg, keys, drop_sources=False):
         """cfg: dict of soso_hip_decode_cfg fields; keys: 9 per layer (attn_norm,
