@@ -437,6 +437,113 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 }
 
 // ---------------------------------------------------------------------------
+// Several tokens per launch: GpuDispatch::matmul (gpu.rs:443-455) with n > 1
+// vectors, as soso's batched q4_k_nb / q8_0_nb kernels do on the CPU
+// (crates/soso-llm-core/src/gemm.rs:902-1076): every weight row is read once
+// for a group of tokens.  Rows of up to 64 units (4096 columns).
+//
+// A workgroup's 8 wavefronts form 8 / G "row groups" of G wavefronts; the G
+// wavefronts of a row group walk the same rows (interleaved over the grid as
+// in mv_rows), each for NT tokens of its own (tokens NT*q .. NT*q + NT - 1 for
+// wavefront q of the group).  Each loaded unit meets the NT tokens' digit
+// registers, and the G wavefronts of a row group request a row at about the
+// same time, so it leaves HBM once and the other requests hit the cache.
+// Every token of the launch is staged in LDS (one staging region each).  Per
+// token the integer sums, the f32 steps and the lane reduction are exactly
+// mv_rows', so each output is bit-identical to the token's own matvec.
+// ---------------------------------------------------------------------------
+template <int FMT, int LPR, int NT, int DEPTH>
+__global__ void __launch_bounds__(512) mv_tok(const uint8_t *__restrict__ W, size_t stride, const float *__restrict__ x,
+                                              float *__restrict__ y, int rows, int cols, int ntok, int G)
+{
+    constexpr int RW = 64 / LPR;
+    extern __shared__ uint4 smem[];
+    const size_t sl = (stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15; // bytes of one token's staging
+    auto region = [&](int t, uint32_t *&xp, float *&s16, int *&kx) {
+        xp = (uint32_t *)((char *)smem + (size_t)t * sl);
+        s16 = (float *)(xp + (cols >> 2) * XDIG);
+        kx = (int *)(s16 + (cols >> 4));
+    };
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int rgw = (int)(blockDim.x >> 6) / G; // row groups per workgroup
+    const int tq = wave % G, rgi = wave / G;
+    const int t0 = tq * NT; // this wavefront's first token
+    const int U = cols >> 6;
+    const int ul = lane & (LPR - 1), slot = lane / LPR;
+    const bool uact = ul < U;
+    const int u = uact ? ul : 0;
+    UConst c;
+    unit_setup_w<FMT>(u, c);
+    const LaneOff L = lane_offsets<FMT>(cols, u, c);
+    const int passes = (rows + RW - 1) / RW;
+    const int tg = gridDim.x * rgw;
+    const int g = blockIdx.x * rgw + rgi;
+    const int n = g < passes ? (passes - g + tg - 1) / tg : 0;
+    const int r0 = g * RW;
+    const uint32_t pass_bytes = (uint32_t)(RW * stride);
+    const rsrc_t rs = make_rsrc(W + (size_t)r0 * stride, (uint32_t)((size_t)(rows > r0 ? rows - r0 : 0) * stride));
+    auto pass_off = [&](int k) -> uint32_t { return (uint32_t)(k * tg) * pass_bytes; };
+    const uint32_t lane_base = uact ? (uint32_t)(slot * stride) : 0x80000000u;
+
+    WRow<FMT> buf[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
+    for (int t = 0; t < ntok; t++) {
+        uint32_t *xp;
+        float *s16;
+        int *kx;
+        region(t, xp, s16, kx);
+        stage_x<FMT>(x + (size_t)t * cols, cols, xp, s16, kx);
+    }
+    XReg xv[NT];
+    UConst ct[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        ct[t] = c;
+        uint32_t *xp;
+        float *s16;
+        int *kx;
+        region(t0 + t < ntok ? t0 + t : 0, xp, s16, kx);
+        unit_setup_x<FMT>(xp, s16, kx, u, U, xv[t], ct[t]);
+    }
+    const int nt = max(0, min(NT, ntok - t0)); // tokens this wavefront computes (uniform)
+    float yacc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) yacc[t] = 0.0f;
+    auto row = [&](int i, int j) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            if (t < nt) {
+                const float part = seg_sum_dpp<LPR>(uact ? unit_dot<FMT>(buf[i], xv[t], ct[t]) : 0.0f);
+                yacc[t] = gather_rows<LPR>(part, j, yacc[t], lane);
+            }
+        }
+    };
+    const int turns = n / DEPTH;
+    int j0 = 0;
+    for (int it = 0; it < turns; it++, j0 += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; i++) {
+            row(i, j0 + i);
+            load_row<FMT>(rs, lane_base + pass_off(j0 + i + DEPTH), cols, L, buf[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    const int rem = n - j0;
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; i++)
+        if (i < rem) row(i, j0 + i);
+    const int k = lane / RW;
+    const int r = RW * (g + k * tg) + lane % RW;
+    if (lane < n * RW && r < rows) {
+#pragma unroll
+        for (int t = 0; t < NT; t++)
+            if (t < nt) y[(size_t)(t0 + t) * rows + r] = yacc[t];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // F32 matvec (MoE router and other small f32 tensors): one wavefront per row,
 // float4 loads, butterfly reduction.
 // ---------------------------------------------------------------------------
@@ -710,13 +817,69 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, con
 
 // n vectors: from MATMUL_MFMA_MIN tokens up, Q4_K goes to the matrix cores
 // (k_mfma.hip: within the same 1e-5 of the exact product, not bit-identical to
-// the single-vector kernel); fewer vectors run the single-vector kernel once
-// per vector, so each is bit-identical to its own matvec.
+// the single-vector kernel); fewer Q4_K vectors, and Q8_0 / Q6_K at any count,
+// run mv_tok (each row read once per launch of up to 16 tokens, every output
+// bit-identical to its own matvec); rows wider than 4096 columns run the
+// single-vector kernel once per vector.
 constexpr size_t MATMUL_MFMA_MIN = 16;
+
+// Tokens per wavefront of mv_tok: each loaded unit meets two tokens' digits
+// (two tokens' digit registers, 96 VGPRs, leave two wavefronts per SIMD).
+constexpr int TOK_NT = 2;
+
+template <int FMT>
+static int launch_tok_fmt(soso_hip *h, const Weight &w, const float *x, float *y, size_t n)
+{
+    const int rows = (int)w.rows, cols = (int)w.cols, U = cols / 64;
+    const size_t stride = packed_row_stride(w.dtype, w.cols);
+    const int LPR = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
+    const int RW = 64 / LPR, passes = (rows + RW - 1) / RW;
+    const size_t sl = (stage_lds_bytes(w.cols) + 15) & ~(size_t)15;
+    // tokens per launch: as many as LDS stages, at most 8 row-group wavefronts x TOK_NT
+    const size_t per = std::min<size_t>(std::min<size_t>(h->max_lds / sl, 8 * TOK_NT), n);
+    for (size_t t0 = 0; t0 < n; t0 += per) {
+        const int m = (int)std::min(per, n - t0);
+        int G = (m + TOK_NT - 1) / TOK_NT;
+        G = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+        const int rgw = 8 / G;
+        // every row group holds at most 64 rows (one output register); one
+        // workgroup per CU at least
+        int grid = std::max(h->num_cu, ((passes + LPR - 1) / LPR + rgw - 1) / rgw);
+        grid = std::min(grid, std::max(1, (passes + rgw - 1) / rgw));
+        grid = std::max(grid, ((passes + LPR - 1) / LPR + rgw - 1) / rgw);
+        if (!interleave_fits(passes, 1, grid * rgw, (size_t)RW * stride))
+            return set_err(h, SOSO_HIP_DECLINED, "matmul: matrix too large for the batched kernel");
+        const size_t lds = sl * (size_t)m;
+        const float *xt = x + t0 * w.cols;
+        float *yt = y + t0 * w.rows;
+#define TOK_CASE(LP)                                                                                                   \
+    case LP:                                                                                                          \
+        mv_tok<FMT, LP, TOK_NT, ring_depth<FMT, 1>()><<<grid, 512, lds, h->stream>>>((const uint8_t *)w.dev, stride, xt, \
+                                                                                     yt, rows, cols, m, G);          \
+        break;
+        switch (LPR) {
+            TOK_CASE(1) TOK_CASE(2) TOK_CASE(4) TOK_CASE(8) TOK_CASE(16) TOK_CASE(32) TOK_CASE(64)
+        }
+#undef TOK_CASE
+        const int rc = hip_check(h, hipGetLastError(), "matmul launch");
+        if (rc != SOSO_HIP_OK) return rc;
+    }
+    return SOSO_HIP_OK;
+}
 
 int launch_matvec(soso_hip *h, const Weight &w, const float *x, float *y, size_t n)
 {
     if (n >= MATMUL_MFMA_MIN && mfma_shape_ok(w.dtype, w.rows, w.cols)) return launch_mfma_matmul(h, w, x, n, y);
+    // several tokens, rows of at most 64 units: each row read once per launch
+    if (n > 1 && w.cols <= 4096 && w.dtype != SOSO_HIP_DTYPE_F32 &&
+        (stage_lds_bytes(w.cols) + 15) / 16 * 16 * 2 <= h->max_lds) {
+        switch (w.dtype) {
+        case SOSO_HIP_DTYPE_Q4_K: return launch_tok_fmt<FMT_Q4K>(h, w, x, y, n);
+        case SOSO_HIP_DTYPE_Q8_0: return launch_tok_fmt<FMT_Q80>(h, w, x, y, n);
+        case SOSO_HIP_DTYPE_Q6_K: return launch_tok_fmt<FMT_Q6K>(h, w, x, y, n);
+        default: break;
+        }
+    }
     for (size_t t = 0; t < n; t++) {
         const float *xt = x + t * w.cols;
         float *yt = y + t * w.rows;
