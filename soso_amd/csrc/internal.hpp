@@ -347,3 +347,11 @@ __device__ __forceinline__ float row16_max(float v)
     v = fmaxf(v, dpp_f<0x140>(v));
     return v;
 }
+__device__ __forceinline__ float row16_min(float v)
+{
+    v = fminf(v, dpp_f<0xB1>(v));
+    v = fminf(v, dpp_f<0x4E>(v));
+    v = fminf(v, dpp_f<0x141>(v));
+    v = fminf(v, dpp_f<0x140>(v));
+    return v;
+}

@@ -260,12 +260,20 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     uint32_t *xp = (uint32_t *)smem;                 // cols/4 groups x XDIG digit dwords
     float *s16 = (float *)(xp + (cols >> 2) * XDIG);
     int *kx = (int *)(s16 + (cols >> 4));
-    float *red = (float *)(kx + ((cols + 127) >> 7)); // [groups][COMBINE_CH][S] when S > 1; 16 floats for XS_RMSNORM
+    // after the outlier lists: [groups][COMBINE_CH][S] when S > 1; 16 floats for XS_RMSNORM
+    float *red = (float *)(out_lists(kx, cols) + ((cols + 127) >> 7) * OUT_DW);
 
     constexpr int RW = 64 / LPR;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int gpw = (blockDim.x >> 6) / S; // groups per workgroup (blockDim = 64 * S * gpw)
+    constexpr int gpw = 8 / S;          // groups of S wavefronts per workgroup
+    constexpr int NTHR = 64 * S * gpw;  // the launch's thread count (launch_fmt, launch_ex_*)
+    // x chunks per thread loaded ahead (rounds of NTHR chunks; rows of up to
+    // 64 S units have at most 512 S chunks, so S = 1 needs one round).  The
+    // rounds past the row end cost a skipped branch each, yet on MI355X the
+    // 14336 x 4096 Q4_K matvec took 7.93 / 7.51 / 7.32 / 7.34 us with one to
+    // four rounds built, and the 8B decode step 1.705 / - / 1.688 / 1.728 ms.
+    constexpr int XP = S == 1 ? 3 : 4;
     const int grp = wave / S, sw = wave % S;
     const int U = cols >> 6;
     const int ul = lane & (LPR - 1), slot = lane / LPR;
@@ -322,25 +330,25 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 
     WRow<FMT> buf[DEPTH];
     if constexpr (XS == XS_RMSNORM) {
-        XPreN xpre;
-        stage_xn_issue(x, in.norm_w, cols, xpre);
+        XPreN<XP> xpre;
+        stage_xn_issue<XP>(x, in.norm_w, cols, xpre, NTHR);
 #pragma unroll
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
-        stage_xn_finish<FMT>(xpre, cols, in.eps, xp, s16, kx, red);
+        stage_xn_finish<FMT, true, XP>(xpre, cols, in.eps, xp, s16, kx, red, NTHR);
     } else if constexpr (XFIRST) {
         // x first: once the weight stream is requested, x's reads would queue
         // behind it in the shared L2 channels.
-        stage_x<FMT>(x, cols, xp, s16, kx);
+        stage_x<FMT, true, XP>(x, cols, xp, s16, kx, NTHR);
 #pragma unroll
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
     } else {
         // x's loads, then the ring's, then x's conversion while the ring is
         // in flight (loads return in issue order)
-        XPre xpre;
-        stage_x_issue(x, cols, xpre);
+        XPre<XP> xpre;
+        stage_x_issue<XP>(x, cols, xpre, NTHR);
 #pragma unroll
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
-        stage_x_finish<FMT>(xpre, x, cols, xp, s16, kx);
+        stage_x_finish<FMT, true, XP>(xpre, x, cols, xp, s16, kx, NTHR);
     }
     // the RoPE angle of this lane's output row, computed while the ring is in
     // flight (the empty asm keeps it from being sunk to the epilogue)
@@ -350,7 +358,8 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         asm volatile("" ::"v"(rope_c), "v"(rope_s));
     }
     XReg xv;
-    unit_setup_x<FMT>(xp, s16, kx, u, U, xv, c);
+    unit_setup_x<FMT, true>(xp, s16, kx, u, U, xv, c);
+    auto dot = [&](const WRow<FMT> &w) -> float { return unit_dot<FMT>(w, xv, c); };
 
     if constexpr (S == 1) {
         // The host sizes the grid so that a strip holds at most 64 rows: the
@@ -366,7 +375,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 #pragma unroll
             for (int i = 0; i < DEPTH; i++) {
                 const int j = j0 + i;
-                float part = unit_dot<FMT>(buf[i], xv, c);
+                float part = dot(buf[i]);
                 load_row<FMT>(rs, lane_base + pass_off(j + DEPTH), cols, L, buf[i]);
                 part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
                 yacc = gather_rows<LPR>(part, j, yacc, lane);
@@ -377,11 +386,13 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 #pragma unroll
         for (int i = 0; i < DEPTH - 1; i++) {
             if (i < rem) {
-                float part = unit_dot<FMT>(buf[i], xv, c);
+                float part = dot(buf[i]);
                 part = seg_sum_dpp<LPR>(uact ? part : 0.0f);
                 yacc = gather_rows<LPR>(part, j0 + i, yacc, lane);
             }
         }
+        if (__builtin_expect(c.onum != 0, 0))
+            yacc += outlier_rows<FMT, LPR>(rs, lane_base, pass_off, 0, n, cols, L, c, u, uact, lane);
         const int r = lane_row(lane);
         epilogue<EPI>(yacc, lane, r, lane < n * RW && r < rows, y, ep, rope_c, rope_s);
     } else {
@@ -402,7 +413,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 #pragma unroll
                 for (int i = 0; i < DEPTH; i++) {
                     const int j = j0 + i;
-                    float part = unit_dot<FMT>(buf[i], xv, c);
+                    float part = dot(buf[i]);
                     load_row<FMT>(rs, lane_base + pass_off(j + DEPTH), cols, L, buf[i]);
                     part = seg_sum_dpp<64>(uact ? part : 0.0f);
                     if (lane == 63) red[(grp * COMBINE_CH + (j - c0)) * S + sw] = part;
@@ -413,13 +424,24 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 #pragma unroll
             for (int i = 0; i < DEPTH - 1; i++) {
                 if (i < rem) {
-                    float part = unit_dot<FMT>(buf[i], xv, c);
+                    float part = dot(buf[i]);
                     part = seg_sum_dpp<64>(uact ? part : 0.0f);
                     if (lane == 63) red[(grp * COMBINE_CH + (j0 + i - c0)) * S + sw] = part;
                 }
             }
+            if (__builtin_expect(c.onum != 0, 0)) {
+                // the outliers' share of this round's passes, added to the
+                // wavefront's own partial sums
+                const float corr = outlier_rows<FMT, 64>(rs, lane_base, pass_off, c0, e1 > c0 ? e1 : c0, cols, L, c,
+                                                         u, uact, lane);
+                for (int i = 0; i < e1 - c0; i++) {
+                    const float ci =
+                        __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, corr), i));
+                    if (lane == 63) red[(grp * COMBINE_CH + i) * S + sw] += ci;
+                }
+            }
             __syncthreads();
-            for (int e = threadIdx.x; e < gpw * COMBINE_CH; e += blockDim.x) {
+            for (int e = threadIdx.x; e < gpw * COMBINE_CH; e += NTHR) {
                 const int q = e / COMBINE_CH, i = e % COMBINE_CH;
                 int a0, a1;
                 strip(blockIdx.x * gpw + q, a0, a1);
@@ -452,13 +474,14 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
 // token the integer sums, the f32 steps and the lane reduction are exactly
 // mv_rows', so each output is bit-identical to the token's own matvec.
 // ---------------------------------------------------------------------------
+constexpr int TOK_THREADS = 512; // mv_tok's launch size
 template <int FMT, int LPR, int NT, int DEPTH>
 __global__ void __launch_bounds__(512) mv_tok(const uint8_t *__restrict__ W, size_t stride, const float *__restrict__ x,
                                               float *__restrict__ y, int rows, int cols, int ntok, int G)
 {
     constexpr int RW = 64 / LPR;
     extern __shared__ uint4 smem[];
-    const size_t sl = (stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15; // bytes of one token's staging
+    const size_t sl = (stage_lds_bytes_o((size_t)cols) + 15) & ~(size_t)15; // bytes of one token's staging
     auto region = [&](int t, uint32_t *&xp, float *&s16, int *&kx) {
         xp = (uint32_t *)((char *)smem + (size_t)t * sl);
         s16 = (float *)(xp + (cols >> 2) * XDIG);
@@ -466,7 +489,7 @@ __global__ void __launch_bounds__(512) mv_tok(const uint8_t *__restrict__ W, siz
     };
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int rgw = (int)(blockDim.x >> 6) / G; // row groups per workgroup
+    const int rgw = (TOK_THREADS >> 6) / G; // row groups per workgroup
     const int tq = wave % G, rgi = wave / G;
     const int t0 = tq * NT; // this wavefront's first token
     const int U = cols >> 6;
@@ -494,7 +517,7 @@ __global__ void __launch_bounds__(512) mv_tok(const uint8_t *__restrict__ W, siz
         float *s16;
         int *kx;
         region(t, xp, s16, kx);
-        stage_x<FMT>(x + (size_t)t * cols, cols, xp, s16, kx);
+        stage_x<FMT, true, 1>(x + (size_t)t * cols, cols, xp, s16, kx, TOK_THREADS); // cols <= 4096
     }
     XReg xv[NT];
     UConst ct[NT];
@@ -505,7 +528,7 @@ __global__ void __launch_bounds__(512) mv_tok(const uint8_t *__restrict__ W, siz
         float *s16;
         int *kx;
         region(t0 + t < ntok ? t0 + t : 0, xp, s16, kx);
-        unit_setup_x<FMT>(xp, s16, kx, u, U, xv[t], ct[t]);
+        unit_setup_x<FMT, true>(xp, s16, kx, u, U, xv[t], ct[t]);
     }
     const int nt = max(0, min(NT, ntok - t0)); // tokens this wavefront computes (uniform)
     float yacc[NT];
@@ -534,6 +557,10 @@ __global__ void __launch_bounds__(512) mv_tok(const uint8_t *__restrict__ W, siz
 #pragma unroll
     for (int i = 0; i < DEPTH - 1; i++)
         if (i < rem) row(i, j0 + i);
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+        if (__builtin_expect(t < nt && ct[t].onum != 0, 0))
+            yacc[t] += outlier_rows<FMT, LPR>(rs, lane_base, pass_off, 0, n, cols, L, ct[t], u, uact, lane);
     const int k = lane / RW;
     const int r = RW * (g + k * tg) + lane % RW;
     if (lane < n * RW && r < rows) {
@@ -623,7 +650,7 @@ static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
     if (S > 8) return set_err(h, SOSO_HIP_DECLINED, "matvec: rows wider than 512 units");
     const int gpw = 8 / S;                 // groups of S wavefronts per workgroup (<= 512 threads)
     const int threads = 64 * S * gpw;
-    const size_t lds = stage_lds_bytes(w.cols) + (S > 1 ? (size_t)gpw * COMBINE_CH * S * 4 : 0);
+    const size_t lds = stage_lds_bytes_o(w.cols) + (S > 1 ? (size_t)gpw * COMBINE_CH * S * 4 : 0);
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec: x does not fit in LDS");
     const int per_cu = 1; // one 512-thread workgroup per CU (two measured slower for these shapes)
     const uint8_t *W = (const uint8_t *)w.dev;
@@ -744,14 +771,14 @@ static const char *plan_matvec_ex(const soso_hip *h, uint8_t dtype, size_t rows_
     const int rows = (int)rows_, cols = (int)cols_, U = cols / 64;
     p.stride = packed_row_stride(dtype, cols_);
     p.S = (U + 63) / 64;
-    if (xs == XS_RMSNORM && cols > XPRE_N * 8 * 512) return "matvec_ex: normalised x wider than the staging registers";
+    if (xs == XS_RMSNORM && cols > 8 * 512) return "matvec_ex: normalised x wider than the staging registers";
     if ((epi == EPI_QKV || epi == EPI_SWIGLU) && (p.S != 1 || rows % 2))
         return "matvec_ex: pair epilogue needs whole rows per wavefront";
     if (p.S > 1) {
         if (xs != XS_PLAIN || epi != EPI_RESID || (p.S != 2 && p.S != 4))
             return "matvec_ex: variant not built for split rows";
         const int gpw = 8 / p.S;
-        p.lds = stage_lds_bytes(cols_) + (size_t)gpw * COMBINE_CH * p.S * 4;
+        p.lds = stage_lds_bytes_o(cols_) + (size_t)gpw * COMBINE_CH * p.S * 4;
         if (p.lds > h->max_lds) return "matvec_ex: x does not fit in LDS";
         p.grid = std::max(1, std::min(h->num_cu, (rows + gpw - 1) / gpw));
         if (!strip_fits(rows, p.grid * gpw, p.stride)) return "matvec_ex: row strip exceeds 2 GiB";
@@ -762,7 +789,7 @@ static const char *plan_matvec_ex(const soso_hip *h, uint8_t dtype, size_t rows_
     const int RW = 64 / p.lpr, gpw = 8;
     const int PU = (RW == 1 && (epi == EPI_QKV || epi == EPI_SWIGLU)) ? 2 : 1;
     const int passes = (rows + RW - 1) / RW, units = (passes + PU - 1) / PU;
-    p.lds = stage_lds_bytes(cols_) + 64;
+    p.lds = stage_lds_bytes_o(cols_) + 64;
     if (p.lds > h->max_lds) return "matvec_ex: x does not fit in LDS";
     // two workgroups per CU for the gate/up pair (2 x 14336 x 4096 on MI355X:
     // 15.2 us, 15.9 us at one per CU); one for the others (qkv, o and the head
@@ -834,7 +861,7 @@ static int launch_tok_fmt(soso_hip *h, const Weight &w, const float *x, float *y
     const size_t stride = packed_row_stride(w.dtype, w.cols);
     const int LPR = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
     const int RW = 64 / LPR, passes = (rows + RW - 1) / RW;
-    const size_t sl = (stage_lds_bytes(w.cols) + 15) & ~(size_t)15;
+    const size_t sl = (stage_lds_bytes_o(w.cols) + 15) & ~(size_t)15;
     // tokens per launch: as many as LDS stages, at most 8 row-group wavefronts x TOK_NT
     const size_t per = std::min<size_t>(std::min<size_t>(h->max_lds / sl, 8 * TOK_NT), n);
     for (size_t t0 = 0; t0 < n; t0 += per) {
@@ -854,8 +881,8 @@ static int launch_tok_fmt(soso_hip *h, const Weight &w, const float *x, float *y
         float *yt = y + t0 * w.rows;
 #define TOK_CASE(LP)                                                                                                   \
     case LP:                                                                                                          \
-        mv_tok<FMT, LP, TOK_NT, ring_depth<FMT, 1>()><<<grid, 512, lds, h->stream>>>((const uint8_t *)w.dev, stride, xt, \
-                                                                                     yt, rows, cols, m, G);          \
+        mv_tok<FMT, LP, TOK_NT, ring_depth<FMT, 1>()><<<grid, TOK_THREADS, lds, h->stream>>>(                        \
+            (const uint8_t *)w.dev, stride, xt, yt, rows, cols, m, G);                                                \
         break;
         switch (LPR) {
             TOK_CASE(1) TOK_CASE(2) TOK_CASE(4) TOK_CASE(8) TOK_CASE(16) TOK_CASE(32) TOK_CASE(64)
@@ -872,7 +899,7 @@ int launch_matvec(soso_hip *h, const Weight &w, const float *x, float *y, size_t
     if (n >= MATMUL_MFMA_MIN && mfma_shape_ok(w.dtype, w.rows, w.cols)) return launch_mfma_matmul(h, w, x, n, y);
     // several tokens, rows of at most 64 units: each row read once per launch
     if (n > 1 && w.cols <= 4096 && w.dtype != SOSO_HIP_DTYPE_F32 &&
-        (stage_lds_bytes(w.cols) + 15) / 16 * 16 * 2 <= h->max_lds) {
+        (stage_lds_bytes_o(w.cols) + 15) / 16 * 16 * 2 <= h->max_lds) {
         switch (w.dtype) {
         case SOSO_HIP_DTYPE_Q4_K: return launch_tok_fmt<FMT_Q4K>(h, w, x, y, n);
         case SOSO_HIP_DTYPE_Q8_0: return launch_tok_fmt<FMT_Q80>(h, w, x, y, n);

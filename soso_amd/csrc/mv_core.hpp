@@ -85,10 +85,53 @@ __device__ __forceinline__ float block_unscale(int k)
     return k == KX_NONFINITE ? __builtin_nanf("") : ldexpf(1.0f, -k);
 }
 
+// ---------------------------------------------------------------------------
+// Outliers.  An element of x far above the rest of its 128-element block
+// would set the block's exponent alone and leave the other elements few
+// significant bits: where those elements carry the product (a large element
+// meeting a small or zero weight), the error would be relative to the large
+// element, not to the result.  Kernels that stage with OUTL therefore take
+// such elements out of the digits.  An element is an outlier when it exceeds
+// 16 times the third largest of the block's sixteen 8-element chunk maxima
+// (ties counted): at most two chunks can hold outliers (so at most 16 per
+// block), and a block without a few dominant elements (an N(0,1) block, for
+// one) has none.  Outliers get zero digits and stay out of the block's
+// exponent and f32 sums; their (position, value) pairs go to the block's
+// list in LDS, in a fixed order, and the matvec adds w * x for each, with w
+// dequantized exactly as the reference dequantizes (unit_outliers).
+// List of block b: dword 0 the count, dwords 1-4 the positions (bytes, 0..127
+// inside the block), dwords 8-23 the values.
+// ---------------------------------------------------------------------------
+constexpr int OUT_MAX = 16;
+constexpr int OUT_DW = 24;
+__host__ __device__ inline size_t out_lds_bytes(size_t cols) { return (cols + 127) / 128 * OUT_DW * 4; }
+// the lists follow the exponents kx (one int per 128-element block)
+__device__ __forceinline__ uint32_t *out_lists(int *kx, int cols) { return (uint32_t *)(kx + ((cols + 127) >> 7)); }
+__device__ __forceinline__ const uint32_t *out_lists(const int *kx, int cols)
+{
+    return (const uint32_t *)(kx + ((cols + 127) >> 7));
+}
+
+// lanes of this lane's 16-lane row for which pred holds
+__device__ __forceinline__ int row16_count(bool pred)
+{
+    const uint64_t b = __ballot(pred);
+    return __popcll((b >> (threadIdx.x & 48u)) & 0xFFFFull);
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v)
+{
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
 // One 8-element chunk c (thread lane == c % 64).  Every lane of the 16-lane
 // DPP row takes part (invalid chunks carry zeros); only valid ones store.
-template <int FMT>
-__device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool valid, int U, uint32_t *xd, float *s16,
+// FAST (with OUTL): a wavefront that would have to search for outliers
+// stages nothing and returns false (uniform), for the caller to stage the
+// chunk again through the full path; otherwise returns true.
+template <int FMT, bool OUTL = false, bool FAST = false>
+__device__ __forceinline__ bool stage_chunk(float4 v0, float4 v1, int c, bool valid, int U, uint32_t *xd, float *s16,
                                             int *kx)
 {
     float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
@@ -97,14 +140,88 @@ __device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool va
     // fmaxf passes over a NaN, which the sum keeps: a NaN element marks the
     // block as an infinite maximum would
     if (sm != sm) m = INFINITY;
-    m = row16_max(m);
+    uint32_t om = 0; // OUTL: bit i = element i of the chunk is an outlier
+    const float vo[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    bool none = !OUTL; // OUTL: no block of the wavefront has an outlier, m is the block maximum
+    if constexpr (OUTL) {
+        // maxima of the four 4-chunk quads, then of the block; the third
+        // largest chunk maximum is at least the smallest quad maximum (the
+        // two largest chunks sit in at most two quads), so blocks whose
+        // maximum is within 16x of their smallest quad maximum have no
+        // outlier, and a wavefront of such blocks (N(0,1), Laplace or
+        // silu(g) * u blocks, all but a few percent of Student-t(3) ones)
+        // skips the search
+        float q = fmaxf(m, dpp_f<0xB1>(m));
+        q = fmaxf(q, dpp_f<0x4E>(q));
+        const float h = fmaxf(q, dpp_f<0x141>(q));
+        const float m1 = fmaxf(h, dpp_f<0x140>(h));
+        float qn = fminf(q, dpp_f<0x141>(q));
+        qn = fminf(qn, dpp_f<0x140>(qn));
+        none = __ballot(m1 > 16.0f * qn) == 0;
+        if (FAST && !none) return false;
+        if (__builtin_expect(!none, 0)) {
+            // the third largest chunk maximum of the block, ties counted (a
+            // non-finite block has no outliers: its result is NaN anyway)
+            const int n1 = row16_count(m == m1);
+            const float m2 = row16_max(m < m1 ? m : -1.0f);
+            const int n2 = row16_count(m == m2);
+            const float m3b = row16_max(m < m2 ? m : -1.0f);
+            const float thr = m1 < INFINITY ? 16.0f * (n1 >= 3 ? m1 : n1 + n2 >= 3 ? m2 : m3b) : INFINITY;
+            none = __ballot(m1 > thr) == 0;
+            if (__builtin_expect(!none, 0)) {
+                float km = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if (fabsf(vv[i]) > thr) {
+                        om |= 1u << i;
+                        vv[i] = 0.0f;
+                    }
+                    km = fmaxf(km, fabsf(vv[i]));
+                }
+                m = km;
+                sm = ((vv[0] + vv[1]) + (vv[2] + vv[3])) + ((vv[4] + vv[5]) + (vv[6] + vv[7]));
+            }
+        }
+        if (none) m = m1;
+    }
+    if (!none || !OUTL) m = row16_max(m);
     const bool finite = m < INFINITY;
     const int e = (m > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(m) : 0;
     sm += dpp_f<0xB1>(sm);
+    if constexpr (OUTL) {
+        uint32_t *ol = out_lists(kx, 64 * U) + (c >> 4) * OUT_DW;
+        if (__builtin_expect(none, 1)) {
+            if (valid && (c & 15) == 0) ol[0] = 0u;
+        } else {
+            // the block's list, in chunk order then element order: an
+            // inclusive scan of the chunks' counts over the 16-lane row gives
+            // each chunk its first slot
+            const int cnt = __popc(om);
+            int incl = cnt;
+            incl += dpp_i<0x111>(incl); // row_shr:1 (lanes with no source add 0)
+            incl += dpp_i<0x112>(incl);
+            incl += dpp_i<0x114>(incl);
+            incl += dpp_i<0x118>(incl);
+            const int tot = (int)row16_max((float)incl);
+            if (valid) {
+                if ((c & 15) == 0) ol[0] = (uint32_t)tot;
+                int slot = incl - cnt;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    if (((om >> i) & 1u) && slot < OUT_MAX) {
+                        ((uint8_t *)(ol + 1))[slot] = (uint8_t)(8 * (c & 15) + i);
+                        ol[8 + slot] = __float_as_uint(vo[i]);
+                        slot++;
+                    }
+                }
+            }
+        }
+    }
     if (valid) {
         uint32_t d0[XDIG], d1[XDIG];
-        digits4(v0, e, d0);
-        digits4(v1, e, d1);
+        digits4(make_float4(vv[0], vv[1], vv[2], vv[3]), e, d0);
+        digits4(make_float4(vv[4], vv[5], vv[6], vv[7]), e, d1);
         if constexpr (FMT == FMT_Q6K) {
             int u, gi;
             xunit<FMT>(2 * c, u, gi);
@@ -118,9 +235,9 @@ __device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool va
             // 6m .. 6m + 5 (xdw): one aligned 16-byte and one 8-byte store
             // instead of six 4-byte ones (on MI355X a 4096 x 4096 Q4_K matvec
             // went from 5.07 to 4.30 us with this alone)
-            const int u = c >> 3, m = c & 7, s0 = (3 * m) >> 1;
+            const int u = c >> 3, mm = c & 7, s0 = (3 * mm) >> 1;
             uint4 *slot = (uint4 *)xd + s0 * U + u;
-            if ((m & 1) == 0) {
+            if ((mm & 1) == 0) {
                 *slot = make_uint4(d0[0], d0[1], d0[2], d1[0]);
                 *(uint2 *)(slot + U) = make_uint2(d1[1], d1[2]);
             } else {
@@ -131,23 +248,32 @@ __device__ __forceinline__ void stage_chunk(float4 v0, float4 v1, int c, bool va
         if ((c & 1) == 0) s16[c >> 1] = sm;
         if ((c & 15) == 0) kx[c >> 4] = finite ? e : KX_NONFINITE;
     }
+    return true;
 }
 
 // x is read in two steps so that its loads can be issued ahead of the weight
 // loads: vector-memory results return in issue order, so x loads issued after
 // a ring of weight loads would wait for all of those weights.
-constexpr int XPRE = 4; // chunks per thread loaded ahead (cols <= 32 * blockDim)
+// The staging functions take the workgroup's thread count as an argument:
+// kernels launched at one fixed size pass it as a constant, so that it is
+// not re-read from the dispatch arguments (a vector load, whose wait would
+// also wait for every weight load issued before it).
+// XP chunks per thread are loaded ahead (the rest, past 8 * XP * nthr
+// columns, are loaded as they are staged); kernels pick the smallest XP that
+// covers their rows, as every unrolled round is code the wavefronts fetch.
+template <int XP>
 struct XPre {
-    float4 v[2 * XPRE];
+    float4 v[2 * XP];
 };
 
-__device__ __forceinline__ void stage_x_issue(const float *__restrict__ x, int cols, XPre &p)
+template <int XP>
+__device__ __forceinline__ void stage_x_issue(const float *__restrict__ x, int cols, XPre<XP> &p, int nthr)
 {
     const int nch = cols >> 3;
     const float4 *x4 = (const float4 *)x;
 #pragma unroll
-    for (int j = 0; j < XPRE; j++) {
-        const int c = j * blockDim.x + threadIdx.x;
+    for (int j = 0; j < XP; j++) {
+        const int c = j * nthr + threadIdx.x;
         p.v[2 * j] = p.v[2 * j + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (c < nch) {
             p.v[2 * j] = x4[2 * c];
@@ -156,23 +282,29 @@ __device__ __forceinline__ void stage_x_issue(const float *__restrict__ x, int c
     }
 }
 
-// blockDim % 64 == 0: chunk c sits in lane c % 64, so the 16 chunks of a
+// nthr % 64 == 0: chunk c sits in lane c % 64, so the 16 chunks of a
 // block form one DPP row.  Loop bounds are uniform over the workgroup (cols
 // is a multiple of 64, so a trailing block may be half full).
-template <int FMT>
-__device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx)
+template <int FMT, bool OUTL, int XP>
+__device__ void stage_x_finish(const XPre<XP> &p, const float *__restrict__ x, int cols, uint32_t *xp, float *s16,
+                               int *kx, int nthr)
 {
     const int nch = cols >> 3, U = cols >> 6;
+    // with several rounds, the rounds held in registers take the fast path
+    // only, and the (rare) rounds that need the outlier search are staged
+    // again below from x, through one copy of the full path
+    constexpr bool FAST = OUTL && XP > 1;
+    uint32_t redo = 0; // rounds to stage again (uniform)
 #pragma unroll
-    for (int j = 0; j < XPRE; j++) {
-        const int base = j * blockDim.x;
+    for (int j = 0; j < XP; j++) {
+        const int base = j * nthr;
         if (base < nch) {
             const int c = base + threadIdx.x;
-            stage_chunk<FMT>(p.v[2 * j], p.v[2 * j + 1], c, c < nch, U, xp, s16, kx);
+            if (!stage_chunk<FMT, OUTL, FAST>(p.v[2 * j], p.v[2 * j + 1], c, c < nch, U, xp, s16, kx)) redo |= 1u << j;
         }
     }
     const float4 *x4 = (const float4 *)x;
-    for (int base = XPRE * blockDim.x; base < nch; base += blockDim.x) {
+    auto full = [&](int base) {
         const int c = base + threadIdx.x;
         const bool valid = c < nch;
         float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
@@ -180,27 +312,34 @@ __device__ void stage_x_finish(const XPre &p, const float *__restrict__ x, int c
             v0 = x4[2 * c];
             v1 = x4[2 * c + 1];
         }
-        stage_chunk<FMT>(v0, v1, c, valid, U, xp, s16, kx);
-    }
+        stage_chunk<FMT, OUTL>(v0, v1, c, valid, U, xp, s16, kx);
+    };
+    // the rounds past the registers, and the rounds to stage again
+    const int j0 = redo ? __builtin_ctz(redo) : XP;
+#pragma unroll 1
+    for (int j = j0, base = j0 * nthr; base < nch; j++, base += nthr)
+        if (j >= XP || ((redo >> j) & 1u)) full(base);
     __syncthreads();
 }
 
 // RMSNorm folded into the staging (crates/soso-llm-core/src/gemm.rs:93-100):
 // every workgroup takes sum(x^2) over the whole vector itself, then stages
 // (x_i * scale) * w_i with scale = 1 / sqrt(sum / n + eps).
-constexpr int XPRE_N = 2; // chunks per thread (cols <= 16 * blockDim)
+// XP chunks per thread, all loaded ahead (cols <= 8 * XP * nthr)
+template <int XP>
 struct XPreN {
-    float4 v[2 * XPRE_N], w[2 * XPRE_N];
+    float4 v[2 * XP], w[2 * XP];
 };
 
+template <int XP>
 __device__ __forceinline__ void stage_xn_issue(const float *__restrict__ x, const float *__restrict__ w, int cols,
-                                               XPreN &p)
+                                               XPreN<XP> &p, int nthr)
 {
     const int nch = cols >> 3;
     const float4 *x4 = (const float4 *)x, *w4 = (const float4 *)w;
 #pragma unroll
-    for (int j = 0; j < XPRE_N; j++) {
-        const int c = j * blockDim.x + threadIdx.x;
+    for (int j = 0; j < XP; j++) {
+        const int c = j * nthr + threadIdx.x;
         p.v[2 * j] = p.v[2 * j + 1] = p.w[2 * j] = p.w[2 * j + 1] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (c < nch) {
             p.v[2 * j] = x4[2 * c];
@@ -219,40 +358,44 @@ __device__ __forceinline__ float4 norm4(float4 v, float s, float4 w)
 }
 
 // red: 16 floats of LDS.
-template <int FMT>
-__device__ void stage_xn_finish(const XPreN &p, int cols, float eps, uint32_t *xp, float *s16, int *kx, float *red)
+template <int FMT, bool OUTL, int XP>
+__device__ void stage_xn_finish(const XPreN<XP> &p, int cols, float eps, uint32_t *xp, float *s16, int *kx, float *red,
+                                int nthr)
 {
     const int nch = cols >> 3, U = cols >> 6;
     float ss = 0.0f;
 #pragma unroll
-    for (int j = 0; j < XPRE_N; j++) ss += sq4(p.v[2 * j]) + sq4(p.v[2 * j + 1]);
+    for (int j = 0; j < XP; j++) ss += sq4(p.v[2 * j]) + sq4(p.v[2 * j + 1]);
     ss = seg_sum<64>(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     float tot = 0.0f;
-    for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += red[i];
+    for (int i = 0; i < (nthr >> 6); i++) tot += red[i];
     const float scale = 1.0f / sqrtf(tot / (float)cols + eps);
 #pragma unroll
-    for (int j = 0; j < XPRE_N; j++) {
-        const int base = j * blockDim.x;
+    for (int j = 0; j < XP; j++) {
+        const int base = j * nthr;
         if (base < nch) {
             const int c = base + threadIdx.x;
-            stage_chunk<FMT>(norm4(p.v[2 * j], scale, p.w[2 * j]), norm4(p.v[2 * j + 1], scale, p.w[2 * j + 1]), c,
-                             c < nch, U, xp, s16, kx);
+            stage_chunk<FMT, OUTL>(norm4(p.v[2 * j], scale, p.w[2 * j]), norm4(p.v[2 * j + 1], scale, p.w[2 * j + 1]),
+                                   c, c < nch, U, xp, s16, kx);
         }
     }
     __syncthreads();
 }
 
-template <int FMT>
-__device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx)
+template <int FMT, bool OUTL, int XP>
+__device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx,
+                                        int nthr)
 {
-    XPre p;
-    stage_x_issue(x, cols, p);
-    stage_x_finish<FMT>(p, x, cols, xp, s16, kx);
+    XPre<XP> p;
+    stage_x_issue(x, cols, p, nthr);
+    stage_x_finish<FMT, OUTL>(p, x, cols, xp, s16, kx, nthr);
 }
 
 __host__ __device__ inline size_t stage_lds_bytes(size_t cols) { return cols * XDIG + cols / 16 * 4 + (cols + 127) / 128 * 4; }
+// ... with the outlier lists of OUTL staging
+__host__ __device__ inline size_t stage_lds_bytes_o(size_t cols) { return stage_lds_bytes(cols) + out_lds_bytes(cols); }
 
 // ---------------------------------------------------------------------------
 // Per-format unit math
@@ -278,6 +421,11 @@ struct UConst {
     float P;                 // 2^-e of the unit's 128-element block: undoes the x scale
     uint32_t k1, k2, s, bsh; // Q4_K scale-decode selectors; Q6_K: s = half, bsh = 8*kk
     int sb;
+    // OUTL staging: the list of the unit's block, its length, and whether any
+    // lane of the wavefront has outliers (uniform; 0 = nothing to add; in
+    // outlier_rows, the longest list over the wavefront)
+    const uint32_t *ol = nullptr;
+    int ocnt = 0, onum = 0;
 };
 
 // weight-side constants (needed before x is staged)
@@ -306,10 +454,15 @@ struct XReg {
 };
 
 // x-side constants and the unit's x in registers (after stage_x)
-template <int FMT>
+template <int FMT, bool OUTL = false>
 __device__ __forceinline__ void unit_setup_x(const uint32_t *xd, const float *s16, const int *kx, int u, int U, XReg &xv,
                                              UConst &c)
 {
+    if constexpr (OUTL) {
+        c.ol = out_lists(kx, 64 * U) + (u >> 1) * OUT_DW;
+        c.ocnt = min((int)c.ol[0], OUT_MAX);
+        c.onum = __ballot(c.ocnt > 0) != 0;
+    }
     c.P = block_unscale(kx[u >> 1]);
     const uint4 *x4 = (const uint4 *)xd;
 #pragma unroll
@@ -511,6 +664,88 @@ __device__ __forceinline__ float unit_dot(const WRow<FMT> &w, const XReg &xv, co
     }
 }
 
+// The exactly dequantized weight of element e (0..63) of the unit, as the
+// reference dequantizes it (crates/sosomodel/src/dequant.rs:74-97, 204-241;
+// crates/gguf2som/src/lib.rs:1639-1661), with no FMA.
+// A value the compiler cannot trace back to memory: a chain of selects over
+// fields of a struct could otherwise be folded into one load at a computed
+// address, which would move the whole struct (the row ring) into scratch.
+__device__ __forceinline__ uint32_t opaque(uint32_t v)
+{
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
+template <int FMT>
+__device__ __forceinline__ float unit_weight(const WRow<FMT> &wr, const UConst &c, int e)
+{
+    WRow<FMT> w = wr;
+    if constexpr (FMT == FMT_Q4K) {
+        w.a = make_uint4(opaque(w.a.x), opaque(w.a.y), opaque(w.a.z), opaque(w.a.w));
+        w.b = make_uint4(opaque(w.b.x), opaque(w.b.y), opaque(w.b.z), opaque(w.b.w));
+    } else if constexpr (FMT == FMT_Q80) {
+        for (int i = 0; i < 4; i++)
+            w.q[i] = make_uint4(opaque(w.q[i].x), opaque(w.q[i].y), opaque(w.q[i].z), opaque(w.q[i].w));
+        w.s = make_uint2(opaque(w.s.x), opaque(w.s.y));
+    } else {
+        w.la = make_uint4(opaque(w.la.x), opaque(w.la.y), opaque(w.la.z), opaque(w.la.w));
+        w.lb = make_uint4(opaque(w.lb.x), opaque(w.lb.y), opaque(w.lb.z), opaque(w.lb.w));
+        w.qh = make_uint4(opaque(w.qh.x), opaque(w.qh.y), opaque(w.qh.z), opaque(w.qh.w));
+        w.sc = make_uint2(opaque(w.sc.x), opaque(w.sc.y));
+    }
+    if constexpr (FMT == FMT_Q4K) {
+        // element e: sub-block 2p + (e >> 5), qs byte e & 31 of the pair, low
+        // nibble for the first sub-block, high for the second
+        const int sub = e >> 5, l = e & 31, k = l >> 2;
+        const uint32_t A = k == 0 ? w.a.x : k == 1 ? w.a.y : k == 2 ? w.a.z : w.a.w;
+        const uint32_t B = k == 4 ? w.b.x : k == 5 ? w.b.y : k == 6 ? w.b.z : w.b.w;
+        const uint32_t q = ((k < 4 ? A : B) >> (8 * (l & 3) + 4 * sub)) & 15u;
+        const uint32_t SC4 = ((w.h.w & c.k1) | ((w.h.y >> c.s) & c.k2)) >> c.bsh;
+        const uint32_t M4 = (((w.h.w >> 4) & c.k1) | ((w.h.z >> c.s) & c.k2)) >> c.bsh;
+        const float sc = (float)((SC4 >> (8 * sub)) & 0xffu), m = (float)((M4 >> (8 * sub)) & 0xffu);
+        const float d = half_bits_to_f32(w.h.x & 0xffffu), dmin = half_bits_to_f32(w.h.x >> 16);
+        return __fsub_rn(__fmul_rn(__fmul_rn(d, sc), (float)q), __fmul_rn(dmin, m));
+    } else if constexpr (FMT == FMT_Q80) {
+        // plane e >> 4 holds bytes 16 (e >> 4 & 1) .. of block e >> 5
+        const int pl = e >> 4, k = (e >> 2) & 3;
+        const uint4 P = pl == 0 ? w.q[0] : pl == 1 ? w.q[1] : pl == 2 ? w.q[2] : w.q[3];
+        const uint32_t dw = k == 0 ? P.x : k == 1 ? P.y : k == 2 ? P.z : P.w;
+        const int q = (int)(int8_t)(dw >> (8 * (e & 3)));
+        return __fmul_rn((float)q, __builtin_bit_cast(float, (e >> 5) ? w.s.y : w.s.x));
+    } else {
+        // element e = 16 i + j: quarter-run i, position 16 kk + j of the half
+        const int i = e >> 4, j = e & 15, t = j >> 2, sh = 8 * (j & 3);
+        const uint32_t la = t == 0 ? w.la.x : t == 1 ? w.la.y : t == 2 ? w.la.z : w.la.w;
+        const uint32_t lb = t == 0 ? w.lb.x : t == 1 ? w.lb.y : t == 2 ? w.lb.z : w.lb.w;
+        const uint32_t qh = t == 0 ? w.qh.x : t == 1 ? w.qh.y : t == 2 ? w.qh.z : w.qh.w;
+        const uint32_t lo = (((i & 1) ? lb : la) >> (sh + ((i & 2) ? 4 : 0))) & 15u;
+        const uint32_t hi = (qh >> (sh + 2 * i)) & 3u;
+        const int q = (int)(lo | (hi << 4)) - 32;
+        const uint32_t sw = (i & 2) ? w.sc.y : w.sc.x;
+        const float sc = (float)(int8_t)(sw >> (c.bsh + ((i & 1) ? 16u : 0u)));
+        return __fmul_rn(__fmul_rn(half_bits_to_f32(w.d), sc), (float)q);
+    }
+}
+
+// Sum of w * x over the outliers of unit u's block that fall in the unit (OUTL
+// staging), in list order; c.onum > 0.
+template <int FMT>
+__device__ __forceinline__ float unit_outliers(const WRow<FMT> &w, const UConst &c, int u)
+{
+    float corr = 0.0f;
+    for (int k = 0; k < c.onum; k++) {
+        if (k < c.ocnt) {
+            const uint32_t p = (c.ol[1 + (k >> 2)] >> (8 * (k & 3))) & 0xffu;
+            const uint32_t half = FMT == FMT_Q6K ? (p >> 4) & 1u : p >> 6;
+            if (half == ((uint32_t)u & 1u)) {
+                const int e = FMT == FMT_Q6K ? (int)((p >> 5) * 16 + (p & 15)) : (int)(p & 63);
+                corr = fmaf(unit_weight<FMT>(w, c, e), __uint_as_float(c.ol[8 + k]), corr);
+            }
+        }
+    }
+    return corr;
+}
+
 // Moves the row sums of pass jw (last lane of each LPR-lane segment) into
 // lanes jw*RW .. jw*RW+RW-1 of yacc.
 template <int LPR>
@@ -527,5 +762,29 @@ __device__ __forceinline__ float gather_rows(float part, int jw, float yacc, int
         const float v = __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(src * 4, __builtin_bit_cast(int, part)));
         return in ? v : yacc;
     }
+}
+
+// The outliers' share of a group's n passes, gathered as the row sums are
+// (lane i: pass i / RW): a second walk over the passes, after the main one,
+// in which only lanes whose unit's block has outliers load their unit again
+// (the others address past the buffer and read zeros for free).  Taken only
+// when some lane of the wavefront has outliers (c.onum > 0); the main loop
+// stays free of the branch.  Every kernel that stages with OUTL adds this
+// to the same row sums, so their results stay bit-identical.
+template <int FMT, int LPR, class PassOff>
+__device__ float outlier_rows(rsrc_t rs, uint32_t lane_base, PassOff pass_off, int j0, int j1, int cols,
+                              const LaneOff &L, const UConst &c, int u, bool uact, int lane)
+{
+    float corr = 0.0f;
+    UConst co = c;
+    co.onum = (int)wave_max_dpp((float)c.ocnt);
+    const uint32_t base = (uact && c.ocnt > 0) ? lane_base : 0x80000000u;
+    for (int j = j0; j < j1; j++) {
+        WRow<FMT> w;
+        load_row<FMT>(rs, base + pass_off(j), cols, L, w);
+        const float part = seg_sum_dpp<LPR>(uact ? unit_outliers<FMT>(w, co, u) : 0.0f);
+        corr = gather_rows<LPR>(part, j - j0, corr, lane);
+    }
+    return corr;
 }
 

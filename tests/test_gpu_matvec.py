@@ -332,3 +332,144 @@ def test_argmax_nan_follows_max_by(gpu, orc, n, nans):
         gpu.dev_free(xd)
         gpu.dev_free(idx)
     assert got == want, (got, want)
+
+
+def outlier_x(orc, cols, seed, scales=(1e3, 1e4), at=(5, 77)):
+    """N(0, 1) with, in every 128-element block, the elements at `at` scaled by
+    `scales` (the activation outliers of real models, 1e3-1e4 x the rest)."""
+    x = orc.normal(cols, 1.0, seed, 1).copy()
+    cols_o = []
+    for b in range(cols // 128):
+        for s, a in zip(scales, at):
+            x[b * 128 + a] = np.float32(s) * np.float32(1.0 if x[b * 128 + a] >= 0 else -1.0)
+            cols_o.append(b * 128 + a)
+    return x, np.array(cols_o)
+
+
+def zero_columns(dtype, w, rows, cols, zc):
+    """The raw soso/GGML bytes with every weight of columns `zc` exactly zero
+    (Q8_0: code 0; Q4_K: code 0 and the super-block's dmin 0; Q6_K: code 32)."""
+    w = w.copy()
+    if dtype == Q8:
+        blk = w.reshape(rows, cols // 32, 36)
+        for c in zc:
+            blk[:, c // 32, 4 + c % 32] = 0
+    elif dtype == Q4K:
+        blk = w.reshape(rows, cols // 256, 144)
+        for c in zc:
+            sb, pos = c // 256, c % 256
+            pr, e = pos // 64, pos % 64
+            byte = 16 + 32 * pr + (e & 31)
+            blk[:, sb, 2:4] = 0  # dmin = 0: the element's weight is d * sc * q
+            blk[:, sb, byte] &= np.uint8(0xF0 if e < 32 else 0x0F)
+    else:
+        blk = w.reshape(rows, cols // 256, 210)
+        for c in zc:
+            sb, pos = c // 256, c % 256
+            h, lp = pos // 128, pos % 128
+            i, l = lp // 32, lp % 32
+            qlb = 64 * h + (32 if i & 1 else 0) + l
+            blk[:, sb, qlb] &= np.uint8(0xF0 if i < 2 else 0x0F)  # the 4 low bits of the code: 0
+            qhb = 128 + 32 * h + l
+            keep = np.uint8(~(3 << (2 * i)) & 0xFF)
+            blk[:, sb, qhb] = (blk[:, sb, qhb] & keep) | np.uint8(2 << (2 * i))  # high bits 2
+    return w
+
+
+@pytest.mark.parametrize("dtype,rows,cols,zero", [
+    (Q4K, 14336, 4096, False),   # configs[1]
+    (Q4K, 2048, 4096, True),
+    (Q8, 4096, 4096, True),      # the outlier columns hold zero codes
+    (Q8, 1024, 4096, False),
+    (Q6K, 1024, 4096, True),
+    (Q4K, 1024, 14336, True),    # rows split over wavefronts
+])
+def test_matvec_activation_outliers(gpu, orc, dtype, rows, cols, zero):
+    """Elements 1e3 and 1e4 times the rest in every 128-element block.  With
+    one exponent per block the other elements would keep ~10 significant
+    bits, and where the large elements meet zero weights the result would be
+    off by ~1e-3; the staging takes such elements out (exactly weighted
+    w * x), so the matvec stays within 1e-5 of the f64 oracle either way."""
+    w = orc.synth(dtype, rows, cols, 91, dtype)
+    x, oc = outlier_x(orc, cols, 92)
+    if zero:
+        w = zero_columns(dtype, w, rows, cols, oc)
+        deq = orc.dequant(dtype, w, rows, cols)
+        assert np.all(deq[:, oc] == 0)
+    key = f"outl.{dtype}.{rows}.{cols}.{zero}"
+    try:
+        y = run_matvec(gpu, key, dtype, w, rows, cols, x)
+        y64 = orc.matvec_f64(dtype, w, rows, cols, x)
+        err = orc.rel_l2(y, y64)
+        print(f"outliers dtype {dtype} {rows}x{cols} zero-weight={zero}: rel_l2 {err:.3e}", flush=True)
+        assert err < TOL, err
+    finally:
+        gpu.weight_drop(key)
+
+
+@pytest.mark.parametrize("cols", [4096, 14336])
+@pytest.mark.parametrize("case", ["constant", "two_full_chunks", "mostly_zero", "ties_at_top", "some_rounds"])
+def test_matvec_outlier_edge_patterns(gpu, orc, case, cols):
+    """Patterns at the edges of the outlier rule: a constant x (ties for every
+    chunk maximum: no outliers), two whole chunks of a block far above the
+    rest (16 outliers, the list's capacity), a block that is zero but for a
+    few elements (all of them exact), three tied dominant chunks (no
+    outliers), outliers in the blocks of a single stretch of x (with 14336
+    columns: one of the rounds of chunks staged per thread).  Zero-weight
+    columns under the large elements."""
+    rows = 512
+    x = orc.normal(cols, 1.0, 93, 1).copy()
+    zc = []
+    if case == "constant":
+        x[:] = 0.75
+    elif case == "two_full_chunks":
+        for b in range(cols // 128):
+            x[b * 128 + 16:b * 128 + 24] = 5e4
+            x[b * 128 + 96:b * 128 + 104] = -3e3
+            zc += list(range(b * 128 + 16, b * 128 + 24)) + list(range(b * 128 + 96, b * 128 + 104))
+    elif case == "mostly_zero":
+        x[:] = 0.0
+        x[3::128] = 7.0
+        x[64::512] = -1e5
+        zc = list(range(64, cols, 512))
+    elif case == "ties_at_top":
+        for b in range(cols // 128):
+            for k in (1, 40, 90):
+                x[b * 128 + k] = 2e4
+    else:
+        lo = 40 if cols > 4096 else 8  # 14336 columns: blocks of the second round
+        for b in range(lo, lo + 16):
+            x[b * 128 + 33] = -4e4
+            zc.append(b * 128 + 33)
+    for dtype in (Q4K, Q8, Q6K):
+        w = orc.synth(dtype, rows, cols, 94, dtype)
+        if zc:
+            w = zero_columns(dtype, w, rows, cols, np.array(zc))
+        key = f"outl.edge.{case}.{cols}.{dtype}"
+        try:
+            y = run_matvec(gpu, key, dtype, w, rows, cols, x)
+            y64 = orc.matvec_f64(dtype, w, rows, cols, x)
+            assert orc.rel_l2(y, y64) < TOL, (case, dtype, orc.rel_l2(y, y64))
+        finally:
+            gpu.weight_drop(key)
+
+
+def test_matmul_matrix_cores_outliers(gpu, orc):
+    """The 64-token Q4_K matmul on the matrix cores (one exponent per
+    256-element super-block) with 1e3 / 1e4 outliers in every 128 elements
+    of every token: within 1e-5 of the CPU per row (its staging keeps the
+    outliers in the digits; the weights here are the generator's, nonzero)."""
+    rows, cols, n = 4096, 4096, 64
+    w = orc.synth(Q4K, rows, cols, 95, 1)
+    xs = np.stack([outlier_x(orc, cols, 96 + t)[0] for t in range(n)])
+    out = np.empty(n * rows, np.float32)
+    key = "outl.mfma"
+    try:
+        assert gpu.matmul(key, w, Q4K, rows, cols, n, xs, out), gpu.last_error()
+        out = out.reshape(n, rows)
+        ref = orc.matmul(Q4K, w, rows, cols, xs, threads=8, avx2=True)
+        worst = max(orc.rel_l2(out[j], ref[j]) for j in range(n))
+        print(f"matrix-core outliers: worst rel_l2 {worst:.3e}", flush=True)
+        assert worst < TOL
+    finally:
+        gpu.weight_drop(key)
