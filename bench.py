@@ -78,7 +78,7 @@ def _timed_graph(g, calls, steps):
     return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
 
 
-def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
+def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1, eager=False):
     """Average duration of one matvec launch, in ms.
 
     `copies` resident weights are rotated so HBM, not the MALL, serves them.
@@ -86,8 +86,9 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
     library's stream, bracketed by HIP events recorded on that stream (see
     _timed_graph): the average is (event interval) / steps,
     the same per-dispatch figure rocprofv3 --kernel-trace reports (profiles/
-    holds that cross-check).  Returns (ms_per_launch_events,
-    ms_per_launch_host_wall)."""
+    holds that cross-check).  eager=True launches the steps directly instead
+    (for counter and tracer runs).  Returns (ms_per_launch_events,
+    ms_per_launch_host_wall; None when eager)."""
     keys = [f"bench.{dtype}.{rows}x{cols}.{i}" for i in range(copies)]
     for i, k in enumerate(keys):
         g.weight_synth(k, dtype, rows, cols, seed, 1000 + i)
@@ -98,7 +99,14 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1):
         for i in range(warmup):
             g.matvec_dev(keys[i % copies], x, y)
         g.sync()
-        return _timed_graph(g, lambda: [g.matvec_dev(keys[i % copies], x, y) for i in range(steps)], steps)
+        calls = lambda: [g.matvec_dev(keys[i % copies], x, y) for i in range(steps)]
+        if eager:
+            g.event_record(0)
+            calls()
+            g.event_record(1)
+            g.sync()
+            return g.event_elapsed(0, 1) / steps, None
+        return _timed_graph(g, calls, steps)
     finally:
         g.sync()
         g.dev_free(x)
@@ -140,14 +148,18 @@ def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False):
 
 
 READ_SHAPES = ((1, 256), (2, 256), (4, 256), (8, 256), (1, 512), (2, 512), (4, 512), (1, 1024), (2, 1024))
+# read-probe variants: grid-stride with K independent 16-byte loads per thread,
+# or per-wavefront contiguous stretches with K 1-KiB buffer loads in flight
+READ_VARIANTS = (("gs", 1), ("gs", 2), ("gs", 4), ("gs", 8), ("chunk", 2), ("chunk", 4), ("chunk", 8), ("chunk", 16))
 
 
-def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES):
-    """A plain streaming read (soso_hip_read_probe) of `nbytes` over `copies`
-    rotating buffers, per launch shape (workgroups per CU, threads): the
-    bandwidth ceiling the matvec is held against, timed like time_matvec
-    (one graph of back-to-back launches between two HIP events).  Returns
-    {(wg_per_cu, threads): ms per launch}."""
+def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES, variants=READ_VARIANTS):
+    """Plain streaming reads (soso_hip_read_probe) of `nbytes` over `copies`
+    rotating buffers, per variant (grid-stride with K independent loads per
+    thread, or per-wavefront KiB stretches with K loads in flight) and launch
+    shape (workgroups per CU, threads): the bandwidth ceiling the matvec is
+    held against, timed like time_matvec (back-to-back graph replays between
+    two HIP events).  Returns {(variant, K, wg_per_cu, threads): ms per launch}."""
     bufs = [g.dev_alloc(nbytes) for _ in range(copies)]
     out_len = 32 * 1024 * 1024
     out = g.dev_alloc(out_len * 4)
@@ -155,18 +167,25 @@ def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES):
     try:
         for i, b in enumerate(bufs):
             g.synth_normal(b, nbytes // 4, 1.0, 5, 900 + i)
-        for wpc, thr in shapes:
-            for i in range(warmup):
-                g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len)
-            g.sync()
-            res[(wpc, thr)] = _timed_graph(g, lambda: [g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len)
-                                                       for i in range(steps)], steps)[0]
+        for var, k in variants:
+            for wpc, thr in shapes:
+                def call(i):
+                    g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len, loads=k, chunked=var == "chunk")
+                for i in range(warmup):
+                    call(i)
+                g.sync()
+                res[(var, k, wpc, thr)] = _timed_graph(g, lambda: [call(i) for i in range(steps)], steps)[0]
     finally:
         g.sync()
         for b in bufs:
             g.dev_free(b)
         g.dev_free(out)
     return res
+
+
+def read_probe_bytes(var, nbytes):
+    """Bytes a read-probe variant reads: whole 16-byte words, or whole KiB."""
+    return nbytes // 1024 * 1024 if var == "chunk" else nbytes // 16 * 16
 
 
 def time_moe(g, n, steps, layers=4, n_x=8, seed=11, eager=False):
@@ -602,8 +621,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="only the headline config")
     ap.add_argument("--copy-calibration", action="store_true", help="only run a 512 MiB D2D copy (PMC scaling)")
     ap.add_argument("--eager", action="store_true",
-                    help="with --only decode/moe1/moe32/matmul: launch the timed steps directly instead of replaying a graph")
-    ap.add_argument("--only", choices=["matvec", "decode", "moe1", "moe32", "head", "matmul", "readprobe"],
+                    help="with --only: launch the timed steps directly instead of replaying a graph")
+    ap.add_argument("--only", choices=["matvec", "q8_0", "down", "decode", "moe1", "moe32", "head", "matmul",
+                                       "readprobe"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -620,10 +640,17 @@ def main():
         return
     if args.only:
         if args.only == "matvec":
-            ms, _ = time_matvec(g, Q4K, 14336, 4096, 16, args.steps, args.warmup)
+            ms, _ = time_matvec(g, Q4K, 14336, 4096, 16, args.steps, args.warmup, eager=args.eager)
             res = {"q4_k_14336x4096_us": round(ms * 1e3, 3)}
+        elif args.only == "q8_0":
+            ms, _ = time_matvec(g, Q8, 4096, 4096, 28, args.steps, args.warmup, eager=args.eager)
+            res = {"q8_0_4096x4096_us": round(ms * 1e3, 3)}
+        elif args.only == "down":
+            ms, _ = time_matvec(g, Q4K, 4096, 14336, 16, args.steps, args.warmup, eager=args.eager)
+            res = {"q4_k_down_4096x14336_us": round(ms * 1e3, 3)}
         elif args.only == "head":
-            ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10))
+            ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10),
+                                eager=args.eager)
             res = {"q6_k_head_128256x4096_us": round(ms * 1e3, 3)}
         elif args.only == "matmul":
             ms = time_matmul(g, 14336, 4096, 64, 16, max(20, args.steps // 10), min(args.warmup, 10), eager=args.eager)
@@ -639,9 +666,11 @@ def main():
             nb = 14336 * ROW_BYTES[Q4K](4096)  # the headline's weight bytes
             small = time_read_probe(g, nb, 16, max(100, args.steps // 2), 20)
             big = time_read_probe(g, 512 << 20, 2, 20, 4)
-            res = {"read_33MB_us": {f"{w}x{t}": round(v * 1e3, 3) for (w, t), v in small.items()},
-                   "read_512MB_us": {f"{w}x{t}": round(v * 1e3, 3) for (w, t), v in big.items()},
-                   "bytes": [nb, 512 << 20], "shape": "workgroups per CU x threads"}
+            res = {"read_33MB_us": {f"{v}{k} {w}x{t}": round(ms * 1e3, 3) for (v, k, w, t), ms in small.items()},
+                   "read_512MB_us": {f"{v}{k} {w}x{t}": round(ms * 1e3, 3) for (v, k, w, t), ms in big.items()},
+                   "bytes": [nb, 512 << 20],
+                   "key": "variant (gs: grid-stride, chunk: per-wavefront KiB stretches) and loads in flight, "
+                          "workgroups per CU x threads"}
         else:
             n = 1 if args.only == "moe1" else 32
             ms, _, _, _ = time_moe(g, n, max(40, args.steps // 10), eager=args.eager)
@@ -687,10 +716,13 @@ def main():
         # the ceiling a dependent 33 MB launch can reach on this GPU
         nb = 14336 * ROW_BYTES[Q4K](4096)
         rd = time_read_probe(g, nb, 16, max(100, args.steps // 5), 20)
-        (bw, bt), best = min(rd.items(), key=lambda kv: kv[1])
-        extra["plain_read_33MB"] = {"us_kernel": round(best * 1e3, 3), "GB_s": round(nb / (best * 1e-3) / 1e9, 1),
-                                    "frac_hbm": round(nb / (best * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": nb,
-                                    "shape": f"{bw} workgroups per CU x {bt} threads (best of {len(rd)})",
+        (bv, bk, bw, bt), best = min(rd.items(), key=lambda kv: kv[1])
+        rb = read_probe_bytes(bv, nb)
+        extra["plain_read_33MB"] = {"us_kernel": round(best * 1e3, 3), "GB_s": round(rb / (best * 1e-3) / 1e9, 1),
+                                    "frac_hbm": round(rb / (best * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": rb,
+                                    "shape": f"{'grid-stride' if bv == 'gs' else 'per-wavefront KiB stretches'}, "
+                                             f"{bk} loads in flight, {bw} workgroups per CU x {bt} threads "
+                                             f"(best of {len(rd)} variants and shapes)",
                                     "headline_vs_read": round(best / ms, 4)}
         if not args.no_cpu:
             extra["q6_k_head_128256x4096"]["parity_vs_cpu"] = head_parity(g, args.cpu_threads)
@@ -720,6 +752,11 @@ def main():
             "GB_s": round(b_h / (ms_h * 1e-3) / 1e9, 1), "frac_hbm": round(b_h / (ms_h * 1e-3) / 1e9 / PEAK_GBS, 4),
             "bytes_per_token": int(b_h), "greedy_token": tok_h,
             "kv": "f16 (soso's KvDtype::F16), same N(0,1) prefill rounded on upload"}
+        # measured HBM traffic over algorithmic bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, profiles/)
+        for name, entry in extra.items():
+            detail = load_traffic(name + "_detail")
+            if isinstance(detail, dict) and "ratio" in detail:
+                entry["traffic_ratio"] = detail["ratio"]
         line["configs"] = extra
     if not args.no_cpu:
         gbs, n, ms, copies, one = cpu_baseline(Q4K, rows, cols, args.cpu_seconds, args.cpu_threads)

@@ -240,23 +240,6 @@ int soso_hip_d2d(soso_hip *h, void *dst, const void *src, size_t bytes);
  * on the device at `raw_dev`; the library repacks them into its own copy. */
 int soso_hip_weight_from_dev(soso_hip *h, const char *key, size_t key_len, const void *raw_dev,
                              size_t w_len, uint8_t dtype, size_t rows, size_t cols);
-/* Fills a new resident weight with seeded synthetic blocks (bench/test input
- * generator; same bytes as the documented counter-based generator). */
-int soso_hip_weight_synth(soso_hip *h, const char *key, size_t key_len, uint8_t dtype, size_t rows,
-                          size_t cols, uint64_t seed, uint64_t stream);
-/* Writes the synthetic raw (soso/GGML layout) bytes of a tensor to device memory. */
-int soso_hip_synth_raw(soso_hip *h, void *dst_dev, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
-                       uint64_t stream);
-/* n f32 values ~ N(0,1)*sigma (Irwin-Hall(12) normals of the same generator). */
-int soso_hip_synth_normal(soso_hip *h, float *dst_dev, size_t n, float sigma, uint64_t seed,
-                          uint64_t stream);
-/* Bench support, no counterpart in the reference: a plain streaming read of
- * bytes (rounded down to 16) from src_dev, the bandwidth the matvec kernels are
- * held against.  wg_per_cu (1..32) workgroups per CU of `threads` (a multiple
- * of 64, <= 1024) grid-stride over the buffer; thread t < out_len writes the
- * xor of what it read to out_dev[t].  Asynchronous on the handle's stream. */
-int soso_hip_read_probe(soso_hip *h, const void *src_dev, size_t bytes, uint32_t wg_per_cu, uint32_t threads,
-                        uint32_t *out_dev, size_t out_len);
 int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len);
 /* y_dev[rows] = W(key) . x_dev; asynchronous on the handle's stream. */
 int soso_hip_matvec_dev(soso_hip *h, const char *key, size_t key_len, const float *x_dev, float *y_dev);

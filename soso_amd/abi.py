@@ -1,4 +1,5 @@
-"""ctypes binding of include/soso_hip.h (libsoso_hip.so, built in-tree).
+"""ctypes binding of include/soso_hip.h and include/soso_hip_bench.h
+(libsoso_hip.so, built in-tree).
 
 The library is the product: if it is missing this module raises at import
 time; there is no CPU fallback behind these calls.
@@ -90,7 +91,7 @@ PROTOTYPES = {
     "soso_hip_weight_synth": (_I, [_P, C.c_char_p, _S, _U8, _S, _S, _U64, _U64]),
     "soso_hip_synth_raw": (_I, [_P, _P, _U8, _S, _S, _U64, _U64]),
     "soso_hip_synth_normal": (_I, [_P, _P, _S, C.c_float, _U64, _U64]),
-    "soso_hip_read_probe": (_I, [_P, _P, _S, C.c_uint32, C.c_uint32, _P, _S]),
+    "soso_hip_read_probe": (_I, [_P, _P, _S, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, _P, _S]),
     "soso_hip_weight_drop": (_I, [_P, C.c_char_p, _S]),
     "soso_hip_matvec_dev": (_I, [_P, C.c_char_p, _S, _P, _P]),
     "soso_hip_matmul_dev": (_I, [_P, C.c_char_p, _S, _S, _P, _P]),

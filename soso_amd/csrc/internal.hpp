@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "../../include/soso_hip.h"
+#include "../../include/soso_hip_bench.h"
 
 // ---------------------------------------------------------------------------
 // Formats (crates/sosomodel/src/layout.rs:57-64; Q6_K from GGML via
@@ -105,6 +106,9 @@ struct soso_hip {
     void *scratch[N_SCRATCH] = {};
     size_t scratch_cap[N_SCRATCH] = {};
     std::vector<void *> retired;
+    // pinned host staging (pinned_get)
+    void *pinned = nullptr;
+    size_t pinned_cap = 0;
     // SOSO_TICKET_BYTES of "last workgroup" state, zero between launches (each
     // kernel resets what it used): uint 0 the final counter (argmax, MoE
     // route), uints 64 .. 831 argmax partials (winner, index, holds-NaN flag per segment), uints 2048 .. 3071 the MoE
@@ -123,7 +127,13 @@ struct soso_hip {
 // error helpers (defined in runtime.hip)
 int set_err(soso_hip *h, int code, const std::string &msg);
 int hip_check(soso_hip *h, hipError_t e, const char *what);
+// Release-path calls (frees, destroys and the waits before them): a failure
+// leaves nothing to undo, so the release goes on; the failure is appended to
+// the handle's last error (keeping the error that led to the release) and
+// SOSO_HIP_ERR_DEVICE returned for the caller to pass on.
+int hip_release(soso_hip *h, hipError_t e, const char *what);
 void *scratch_get(soso_hip *h, int slot, size_t bytes);
+void *pinned_get(soso_hip *h, size_t bytes);
 
 // Input and output variants of the matvec kernel (decode-step fusions).
 enum { XS_PLAIN = 0, XS_RMSNORM = 1 };
@@ -181,8 +191,8 @@ int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, b
 int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
                      uint64_t stream);
 int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream);
-int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads, uint32_t *out,
-                      size_t out_len);
+int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads,
+                      unsigned loads, bool chunked, uint32_t *out, size_t out_len);
 // (k_moe.hip) -- device scratch of one MoE FFN call
 struct MoeScratch {
     float *logits = nullptr; // n x n_exp

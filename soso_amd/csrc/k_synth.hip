@@ -143,27 +143,87 @@ int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t
 }
 
 // ---------------------------------------------------------------------------
-// Plain streaming read: the bandwidth reference the matvec kernels are held
-// against (bench.py --only readprobe).  Grid-stride over n16 16-byte words,
-// one load per thread per step; the xor of everything a thread read goes to
-// out[thread] (threads past out_len keep theirs: the store is conditional at
-// run time, so no load is dead either way).
+// Plain streaming reads: the bandwidth reference the matvec kernels are held
+// against (bench.py --only readprobe sweeps every variant and launch shape).
+// Each thread xors what it read into out[thread] (threads past out_len keep
+// theirs: the store is conditional at run time, so no load is dead).
+//  - read_probe_gs<K>: grid-stride over 16-byte words, K independent loads
+//    issued per thread before any is used;
+//  - read_probe_chunk<K>: each wavefront streams its own contiguous stretch
+//    of whole KiB, K 1-KiB wavefront loads in flight (raw buffer loads, as
+//    the matvec kernels use; a load past the stretch returns zeros without
+//    touching memory).
 // ---------------------------------------------------------------------------
-__global__ void read_probe_k(const uint4 *__restrict__ p, size_t n16, uint32_t *__restrict__ out, size_t out_len)
+template <int K>
+__global__ void read_probe_gs(const uint4 *__restrict__ p, size_t n16, uint32_t *__restrict__ out, size_t out_len)
 {
     const size_t T = (size_t)gridDim.x * blockDim.x, t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     uint32_t acc = 0;
-    for (size_t i = t; i < n16; i += T) {
+    size_t i = t;
+    for (; i + (size_t)(K - 1) * T < n16; i += (size_t)K * T) {
+        uint4 v[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) v[k] = p[i + (size_t)k * T];
+#pragma unroll
+        for (int k = 0; k < K; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    for (; i < n16; i += T) {
         const uint4 v = p[i];
         acc ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     if (t < out_len) out[t] = acc;
 }
 
-int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads, uint32_t *out,
-                      size_t out_len)
+template <int K>
+__global__ void read_probe_chunk(const uint8_t *__restrict__ p, uint32_t kib, uint32_t *__restrict__ out,
+                                 size_t out_len)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t nw = gridDim.x * (blockDim.x >> 6);
+    const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t c0 = (uint32_t)((uint64_t)kib * w / nw), c1 = (uint32_t)((uint64_t)kib * (w + 1) / nw);
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(p) + (size_t)c0 * 1024,
+                                                                       (short)0, (int)((c1 - c0) * 1024), 0x00020000);
+    uint32_t acc = 0;
+    for (uint32_t j = 0; j < c1 - c0; j += K) {
+        uint4 v[K];
+#pragma unroll
+        for (int k = 0; k < K; k++)
+            v[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((j + k) * 1024u + 16u * lane),
+                                                                                   0, 0));
+#pragma unroll
+        for (int k = 0; k < K; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
+    }
+    const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < out_len) out[t] = acc;
+}
+
+int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads,
+                      unsigned loads, bool chunked, uint32_t *out, size_t out_len)
 {
     const unsigned grid = wg_per_cu * (unsigned)h->num_cu;
-    read_probe_k<<<grid, threads, 0, h->stream>>>((const uint4 *)src, bytes / 16, out, out_len);
+    if (chunked) {
+        const uint32_t kib = (uint32_t)(bytes >> 10);
+        const uint8_t *b = (const uint8_t *)src;
+        switch (loads) {
+        case 1: read_probe_chunk<1><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+        case 2: read_probe_chunk<2><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+        case 4: read_probe_chunk<4><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+        case 8: read_probe_chunk<8><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+        case 16: read_probe_chunk<16><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+        default: return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: loads");
+        }
+    } else {
+        const uint4 *q = (const uint4 *)src;
+        const size_t n16 = bytes / 16;
+        switch (loads) {
+        case 1: read_probe_gs<1><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+        case 2: read_probe_gs<2><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+        case 4: read_probe_gs<4><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+        case 8: read_probe_gs<8><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+        case 16: read_probe_gs<16><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+        default: return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: loads");
+        }
+    }
     return hip_check(h, hipGetLastError(), "read probe launch");
 }

@@ -33,6 +33,17 @@ int hip_check(soso_hip *h, hipError_t e, const char *what)
     return set_err(h, SOSO_HIP_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
+int hip_release(soso_hip *h, hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return SOSO_HIP_OK;
+    (void)hipGetLastError();
+    if (h) h->err += (h->err.empty() ? "" : "; ") + std::string(what) + ": " + hipGetErrorString(e);
+    return SOSO_HIP_ERR_DEVICE;
+}
+
+// the first failure of a sequence of release calls
+static int first_fail(int a, int b) { return a != SOSO_HIP_OK ? a : b; }
+
 static bool any_graph(const soso_hip *h)
 {
     for (hipGraphExec_t g : h->graphs)
@@ -44,6 +55,28 @@ static bool any_graph(const soso_hip *h)
 // capture is refused (null): it would synchronise and allocate within the
 // capture.  While any graph exists the outgrown buffer is retired instead of
 // freed, since a graph may hold it as a kernel argument.
+// Pinned host staging, grown on demand (hipHostMalloc: new pinned memory,
+// never registration of existing memory); freed with the handle.
+void *pinned_get(soso_hip *h, size_t bytes)
+{
+    if (bytes <= h->pinned_cap) return h->pinned;
+    if (h->pinned && hip_release(h, hipHostFree(h->pinned), "free pinned staging") != SOSO_HIP_OK) {
+        h->pinned = nullptr;
+        h->pinned_cap = 0;
+        return nullptr;
+    }
+    h->pinned = nullptr;
+    h->pinned_cap = 0;
+    const size_t cap = std::max<size_t>(bytes, 1u << 20);
+    if (hipHostMalloc(&h->pinned, cap, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        h->pinned = nullptr;
+        return nullptr;
+    }
+    h->pinned_cap = cap;
+    return h->pinned;
+}
+
 void *scratch_get(soso_hip *h, int slot, size_t bytes)
 {
     if (bytes == 0) bytes = 16;
@@ -132,17 +165,18 @@ int register_weight(soso_hip *h, const std::string &key, const void *raw, bool r
     int rc = SOSO_HIP_OK;
     if (!raw_on_device) {
         if (hipMalloc(&tmp, w_len) != hipSuccess) {
-            hipFree(dev);
-            return set_err(h, SOSO_HIP_ERR_NOMEM, "weight " + key + ": staging allocation failed");
+            set_err(h, SOSO_HIP_ERR_NOMEM, "weight " + key + ": staging allocation failed");
+            (void)hip_release(h, hipFree(dev), "free weight");
+            return SOSO_HIP_ERR_NOMEM;
         }
         rc = hip_check(h, hipMemcpyAsync(tmp, raw, w_len, hipMemcpyHostToDevice, h->stream), "upload weight");
         raw_dev = tmp;
     }
     if (rc == SOSO_HIP_OK) rc = repack_weight(h, dtype, raw_dev, dev, rows, cols);
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "repack sync");
-    if (tmp) hipFree(tmp);
+    if (tmp) rc = first_fail(rc, hip_release(h, hipFree(tmp), "free staging"));
     if (rc != SOSO_HIP_OK) {
-        hipFree(dev);
+        (void)hip_release(h, hipFree(dev), "free weight");
         return rc;
     }
     w.dev = dev;
@@ -180,34 +214,36 @@ Weight *find_weight(soso_hip *h, const char *key, size_t key_len)
     return &it->second;
 }
 
-void moe_free(soso_hip *h, MoeLayer &m)
+int moe_free(soso_hip *h, MoeLayer &m)
 {
-    hipStreamSynchronize(h->stream);
-    if (m.tab) hipFree(m.tab);
-    if (m.tiled) hipFree(m.tiled);
+    int rc = hip_release(h, hipStreamSynchronize(h->stream), "moe free sync");
+    if (m.tab) rc = first_fail(rc, hip_release(h, hipFree(m.tab), "free expert table"));
+    if (m.tiled) rc = first_fail(rc, hip_release(h, hipFree(m.tiled), "free tiled table"));
     if (m.tiled_mem) {
-        hipFree(m.tiled_mem);
+        rc = first_fail(rc, hip_release(h, hipFree(m.tiled_mem), "free tiled experts"));
         h->used -= m.tiled_bytes;
     }
     m.tab = m.tiled = nullptr;
     m.tiled_mem = nullptr;
     m.tiled_bytes = 0;
+    return rc;
 }
 
-void decode_free(soso_hip *h, DecodeModel &m)
+int decode_free(soso_hip *h, DecodeModel &m)
 {
-    hipStreamSynchronize(h->stream);
+    int rc = hip_release(h, hipStreamSynchronize(h->stream), "decode free sync");
     for (Weight &w : m.owned) {
         if (w.dev) {
-            hipFree(w.dev);
+            rc = first_fail(rc, hip_release(h, hipFree(w.dev), "free fused weight"));
             h->used -= w.bytes;
         }
     }
     m.owned.clear();
-    if (m.kcache) hipFree(m.kcache);
-    if (m.mem) hipFree(m.mem);
+    if (m.kcache) rc = first_fail(rc, hip_release(h, hipFree(m.kcache), "free KV cache"));
+    if (m.mem) rc = first_fail(rc, hip_release(h, hipFree(m.mem), "free step buffers"));
     m.kcache = m.vcache = nullptr;
     m.mem = nullptr;
+    return rc;
 }
 
 } // namespace
@@ -233,7 +269,10 @@ int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out)
     }
     if (hipMalloc((void **)&h->ticket, SOSO_TICKET_BYTES) != hipSuccess ||
         hipMemset(h->ticket, 0, SOSO_TICKET_BYTES) != hipSuccess) {
-        hipStreamDestroy(h->stream);
+        // a failed create has no handle to report through: teardown results are moot
+        (void)hipGetLastError();
+        if (h->ticket) (void)hipFree(h->ticket);
+        (void)hipStreamDestroy(h->stream);
         delete h;
         return SOSO_HIP_ERR_DEVICE;
     }
@@ -248,7 +287,11 @@ int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out)
     h->num_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     h->max_lds = prop.sharedMemPerBlock > 0 ? prop.sharedMemPerBlock : 65536;
     size_t free_b = 0, total_b = 0;
-    hipMemGetInfo(&free_b, &total_b);
+    if (!vram_budget && hipMemGetInfo(&free_b, &total_b) != hipSuccess) {
+        (void)hipGetLastError();
+        soso_hip_destroy(h);
+        return SOSO_HIP_ERR_DEVICE;
+    }
     h->budget = vram_budget ? vram_budget : (uint64_t)(free_b * 0.9);
     *out = h;
     return 0;
@@ -257,24 +300,28 @@ int soso_hip_create(int device, uint64_t vram_budget, soso_hip **out)
 void soso_hip_destroy(soso_hip *h)
 {
     if (!h) return;
-    hipSetDevice(h->device);
-    hipStreamSynchronize(h->stream);
+    // the handle is gone when this returns, and with it any channel to report
+    // a failed release: every result here is deliberately dropped
+    (void)hipSetDevice(h->device);
+    (void)hipStreamSynchronize(h->stream);
     for (auto &kv : h->weights)
-        if (kv.second.dev) hipFree(kv.second.dev);
-    for (auto &kv : h->f32_tensors) hipFree(kv.second);
+        if (kv.second.dev) (void)hipFree(kv.second.dev);
+    for (auto &kv : h->f32_tensors) (void)hipFree(kv.second);
     for (int i = 0; i < soso_hip::N_SCRATCH; i++)
         if (h->scratch[i]) (void)hipFree(h->scratch[i]);
     for (void *p : h->retired) (void)hipFree(p);
-    for (auto &kv : h->moe_layers) moe_free(h, kv.second);
-    for (auto &kv : h->decode_models) decode_free(h, kv.second);
-    if (h->ticket) hipFree(h->ticket);
+    if (h->pinned) (void)hipHostFree(h->pinned);
+    for (auto &kv : h->moe_layers) (void)moe_free(h, kv.second);
+    for (auto &kv : h->decode_models) (void)decode_free(h, kv.second);
+    if (h->ticket) (void)hipFree(h->ticket);
     for (hipEvent_t e : h->events)
-        if (e) hipEventDestroy(e);
+        if (e) (void)hipEventDestroy(e);
     for (hipGraphExec_t g : h->graphs)
-        if (g) hipGraphExecDestroy(g);
-    hipEventDestroy(h->ev0);
-    hipEventDestroy(h->ev1);
-    hipStreamDestroy(h->stream);
+        if (g) (void)hipGraphExecDestroy(g);
+    (void)hipEventDestroy(h->ev0);
+    (void)hipEventDestroy(h->ev1);
+    (void)hipStreamDestroy(h->stream);
+    (void)hipGetLastError();
     delete h;
 }
 
@@ -306,7 +353,7 @@ int soso_hip_matmul(soso_hip *h, const char *key, size_t key_len, const uint8_t 
     rc = hip_check(h, hipMemcpyAsync(xd, x, n * cols * 4, hipMemcpyHostToDevice, h->stream), "x upload");
     if (rc == SOSO_HIP_OK) rc = launch_matvec(h, *wt, xd, yd, n);
     if (rc != SOSO_HIP_OK) {
-        hipStreamSynchronize(h->stream);
+        (void)hip_release(h, hipStreamSynchronize(h->stream), "matmul drain");
         return rc;
     }
     rc = hip_check(h, hipMemcpyAsync(y, yd, n * rows * 4, hipMemcpyDeviceToHost, h->stream), "y download");
@@ -337,20 +384,31 @@ int soso_hip_matvec_batch(soso_hip *h, const soso_hip_op *ops, size_t n_ops, uin
         xs += ops[i].cols;
         ys += ops[i].rows;
     }
+    if (n_ops == 0) return SOSO_HIP_OK;
+    // every x and every y pass through one pinned staging buffer: one upload,
+    // the launches, one download, one wait (Lote's single synchronisation)
     float *xd = (float *)scratch_get(h, 0, xs * 4);
     float *yd = (float *)scratch_get(h, 1, ys * 4);
-    if (!xd || !yd) return set_err(h, SOSO_HIP_ERR_NOMEM, "matvec_batch: scratch");
+    float *hx = (float *)pinned_get(h, (xs + ys) * 4);
+    if (!xd || !yd || !hx) return set_err(h, SOSO_HIP_ERR_NOMEM, "matvec_batch: staging");
+    float *hy = hx + xs;
+    size_t xo = 0;
+    for (size_t i = 0; i < n_ops; i++) {
+        if (ops[i].x) memcpy(hx + xo, ops[i].x, ops[i].cols * 4);
+        xo += ops[i].cols;
+    }
+    rc = hip_check(h, hipMemcpyAsync(xd, hx, xs * 4, hipMemcpyHostToDevice, h->stream), "x upload");
+    if (rc != SOSO_HIP_OK) return rc;
     std::vector<uint8_t> launched(n_ops, 0);
-    size_t xo = 0, yo = 0;
+    size_t yo = 0;
     int worst = SOSO_HIP_OK;
+    xo = 0;
     for (size_t i = 0; i < n_ops; i++) {
         const soso_hip_op &op = ops[i];
         Weight *wt = nullptr;
         int r = (op.key && op.x && op.y && op.rows && op.cols)
                     ? get_weight(h, op.key, op.key_len, op.w, op.w_len, op.dtype, op.rows, op.cols, &wt)
                     : SOSO_HIP_DECLINED;
-        if (r == SOSO_HIP_OK) r = hip_check(h, hipMemcpyAsync(xd + xo, op.x, op.cols * 4, hipMemcpyHostToDevice, h->stream),
-                                           "x upload");
         if (r == SOSO_HIP_OK) r = launch_matvec(h, *wt, xd + xo, yd + yo, 1);
         if (r == SOSO_HIP_OK) launched[i] = 1;
         else if (r < worst) worst = r;
@@ -358,19 +416,19 @@ int soso_hip_matvec_batch(soso_hip *h, const soso_hip_op *ops, size_t n_ops, uin
         xo += op.cols;
         yo += op.rows;
     }
-    rc = hip_check(h, hipStreamSynchronize(h->stream), "matvec_batch sync");
-    if (rc != SOSO_HIP_OK) return rc;
+    rc = hip_check(h, hipMemcpyAsync(hy, yd, ys * 4, hipMemcpyDeviceToHost, h->stream), "y download");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "matvec_batch sync");
+    if (rc != SOSO_HIP_OK) {
+        (void)hip_release(h, hipStreamSynchronize(h->stream), "matvec_batch drain");
+        return rc;
+    }
     yo = 0;
     for (size_t i = 0; i < n_ops; i++) {
         if (launched[i]) {
-            if (hip_check(h, hipMemcpy(ops[i].y, yd + yo, ops[i].rows * 4, hipMemcpyDeviceToHost), "y download") ==
-                SOSO_HIP_OK) {
-                done[i] = 1;
-                h->stats.bytes_up += ops[i].cols * 4;
-                h->stats.bytes_down += ops[i].rows * 4;
-            } else {
-                worst = SOSO_HIP_ERR_DEVICE;
-            }
+            memcpy(ops[i].y, hy + yo, ops[i].rows * 4);
+            done[i] = 1;
+            h->stats.bytes_up += ops[i].cols * 4;
+            h->stats.bytes_down += ops[i].rows * 4;
         }
         yo += ops[i].rows;
     }
@@ -399,7 +457,7 @@ int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const flo
         if (hipMalloc(&wd, n_exp * hdim * 4) != hipSuccess) return set_err(h, SOSO_HIP_DECLINED, "router: alloc");
         rc = hip_check(h, hipMemcpy(wd, w, n_exp * hdim * 4, hipMemcpyHostToDevice), "router upload");
         if (rc != SOSO_HIP_OK) {
-            hipFree(wd);
+            (void)hip_release(h, hipFree(wd), "free router weights");
             return rc;
         }
         h->f32_tensors[k] = wd;
@@ -545,7 +603,7 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(sum, sd, n * hdim * 4, hipMemcpyDeviceToHost, h->stream), "sum");
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "experts sync");
     if (rc != SOSO_HIP_OK) {
-        hipStreamSynchronize(h->stream);
+        (void)hip_release(h, hipStreamSynchronize(h->stream), "experts drain");
         return rc;
     }
     for (size_t e = 0; e < n_exps; e++) done[e] = ok[e];
@@ -622,17 +680,17 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
         m.tiled_down = tdn;
     }
     if (rc != SOSO_HIP_OK) {
-        moe_free(h, m);
+        (void)moe_free(h, m);
         return rc;
     }
     std::string k(layer_key, layer_key_len);
     auto it = h->moe_layers.find(k);
     if (it != h->moe_layers.end()) {
-        moe_free(h, it->second);
+        rc = moe_free(h, it->second);
         h->moe_layers.erase(it);
     }
     h->moe_layers.emplace(k, m);
-    return SOSO_HIP_OK;
+    return rc;
 }
 
 int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev, size_t n,
@@ -831,7 +889,7 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemsetAsync(m.mem, 0, mem_bytes, h->stream), "step buffers zero");
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "decode_create sync");
     if (rc != SOSO_HIP_OK) {
-        decode_free(h, m);
+        (void)decode_free(h, m);
         return rc;
     }
     m.vcache = (char *)m.kcache + kv_bytes;
@@ -850,14 +908,14 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
         for (size_t i = 0; i < fr.size(); i++) fr[i] = powf(cfg->rope_theta, -2.0f * (float)i / n_f);
         rc = hip_check(h, hipMemcpy(m.rope_freq, fr.data(), fr.size() * 4, hipMemcpyHostToDevice), "rope table");
         if (rc != SOSO_HIP_OK) {
-            decode_free(h, m);
+            (void)decode_free(h, m);
             return rc;
         }
     }
     std::string key(model_key, model_key_len);
     auto old = h->decode_models.find(key);
     if (old != h->decode_models.end()) {
-        decode_free(h, old->second);
+        rc = decode_free(h, old->second);
         h->decode_models.erase(old);
     }
     DecodeModel &dm = h->decode_models.emplace(key, std::move(m)).first->second;
@@ -937,9 +995,9 @@ int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key
     if (!h || !model_key) return SOSO_HIP_ERR_ARG;
     auto it = h->decode_models.find(std::string(model_key, model_key_len));
     if (it == h->decode_models.end()) return SOSO_HIP_DECLINED;
-    decode_free(h, it->second);
+    const int rc = decode_free(h, it->second);
     h->decode_models.erase(it);
-    return SOSO_HIP_OK;
+    return rc;
 }
 
 // ---- device-resident API ----------------------------------------------------
@@ -957,8 +1015,8 @@ int soso_hip_dev_free(soso_hip *h, void *dptr)
     if (!h) return SOSO_HIP_ERR_ARG;
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
-    hipStreamSynchronize(h->stream);
-    return hip_check(h, hipFree(dptr), "hipFree");
+    rc = hip_check(h, hipStreamSynchronize(h->stream), "dev_free sync");
+    return first_fail(rc, hip_check(h, hipFree(dptr), "hipFree"));
 }
 
 int soso_hip_h2d(soso_hip *h, void *dst, const void *src, size_t bytes)
@@ -1024,15 +1082,16 @@ int soso_hip_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64
 }
 
 int soso_hip_read_probe(soso_hip *h, const void *src_dev, size_t bytes, uint32_t wg_per_cu, uint32_t threads,
-                        uint32_t *out_dev, size_t out_len)
+                        uint32_t loads, uint32_t chunked, uint32_t *out_dev, size_t out_len)
 {
     if (!h) return SOSO_HIP_ERR_ARG;
     if (!src_dev || !out_dev || bytes < 16 || wg_per_cu == 0 || wg_per_cu > 32 || threads == 0 || threads > 1024 ||
-        threads % 64)
+        threads % 64 || !(loads == 1 || loads == 2 || loads == 4 || loads == 8 || loads == 16) ||
+        (chunked && (bytes < 1024 || bytes >= (1ull << 31))))
         return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: args");
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
-    return launch_read_probe(h, src_dev, bytes, wg_per_cu, threads, out_dev, out_len);
+    return launch_read_probe(h, src_dev, bytes, wg_per_cu, threads, loads, chunked != 0, out_dev, out_len);
 }
 
 int soso_hip_weight_synth(soso_hip *h, const char *key, size_t key_len, uint8_t dtype, size_t rows, size_t cols,
@@ -1047,9 +1106,8 @@ int soso_hip_weight_synth(soso_hip *h, const char *key, size_t key_len, uint8_t 
     if (hipMalloc(&raw, rows * rb) != hipSuccess) return set_err(h, SOSO_HIP_ERR_NOMEM, "weight_synth: alloc");
     rc = launch_synth_raw(h, raw, dtype, rows, cols, seed, stream);
     if (rc == SOSO_HIP_OK) rc = soso_hip_weight_from_dev(h, key, key_len, raw, rows * rb, dtype, rows, cols);
-    hipStreamSynchronize(h->stream);
-    hipFree(raw);
-    return rc;
+    rc = first_fail(rc, hip_release(h, hipStreamSynchronize(h->stream), "weight_synth sync"));
+    return first_fail(rc, hip_release(h, hipFree(raw), "free synth staging"));
 }
 
 int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
@@ -1059,13 +1117,13 @@ int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
     if (rc != SOSO_HIP_OK) return rc;
     auto it = h->weights.find(std::string(key, key_len));
     if (it == h->weights.end()) return SOSO_HIP_DECLINED;
-    hipStreamSynchronize(h->stream);
+    rc = hip_release(h, hipStreamSynchronize(h->stream), "weight_drop sync");
     // a registered MoE layer that reads this weight is unregistered with it
     for (auto m = h->moe_layers.begin(); m != h->moe_layers.end();) {
         bool uses = m->second.router == &it->second;
         for (const void *p : m->second.host_tab) uses = uses || (p && p == it->second.dev);
         if (uses) {
-            moe_free(h, m->second);
+            rc = first_fail(rc, moe_free(h, m->second));
             m = h->moe_layers.erase(m);
         } else {
             ++m;
@@ -1074,20 +1132,20 @@ int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
     // ... and so is a decode model that reads it
     for (auto m = h->decode_models.begin(); m != h->decode_models.end();) {
         if (std::find(m->second.uses.begin(), m->second.uses.end(), it->first) != m->second.uses.end()) {
-            decode_free(h, m->second);
+            rc = first_fail(rc, decode_free(h, m->second));
             m = h->decode_models.erase(m);
         } else {
             ++m;
         }
     }
     if (it->second.dev) {
-        hipFree(it->second.dev);
+        rc = first_fail(rc, hip_release(h, hipFree(it->second.dev), "free weight"));
         h->used -= it->second.bytes;
         h->stats.weight_bytes_resident -= it->second.bytes;
         h->stats.weights_resident--;
     }
     h->weights.erase(it);
-    return SOSO_HIP_OK;
+    return rc;
 }
 
 int soso_hip_matvec_dev(soso_hip *h, const char *key, size_t key_len, const float *x_dev, float *y_dev)
@@ -1185,7 +1243,8 @@ int soso_hip_graph_end(soso_hip *h, int *graph_id)
     if (rc != SOSO_HIP_OK) return rc;
     hipGraphExec_t ex = nullptr;
     rc = hip_check(h, hipGraphInstantiate(&ex, g, nullptr, nullptr, 0), "graph instantiate");
-    hipGraphDestroy(g);
+    // the captured template is not needed once instantiated (nor after a failure)
+    (void)hip_release(h, hipGraphDestroy(g), "graph destroy");
     if (rc != SOSO_HIP_OK) return rc;
     h->graphs.push_back(ex);
     *graph_id = (int)h->graphs.size() - 1;

@@ -1,5 +1,5 @@
-"""The C-ABI libraries build, load and export every symbol include/soso_hip.h
-and include/soso_som.h declare; without a device libsoso_hip refuses cleanly
+"""The C-ABI libraries build, load and export every symbol include/soso_hip.h,
+include/soso_hip_bench.h and include/soso_som.h declare; without a device libsoso_hip refuses cleanly
 (no compute calls here)."""
 import ctypes as C
 import os
@@ -8,11 +8,11 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "soso_hip.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("soso_hip.h", "soso_hip_bench.h")]
 
 
 def declared_symbols():
-    text = open(HEADER).read()
+    text = "".join(open(h).read() for h in HEADERS)
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(soso_hip_[a-z0-9_]+)\s*\(", text)))
 
