@@ -115,14 +115,14 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1, eager=False
             g.weight_drop(k)
 
 
-def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False):
-    """Q4_K matmul Y[n x rows] = X[n x cols] . W^T (GpuDispatch::matmul) with
-    n tokens on the matrix cores; `copies` rotating weights.  Returns ms per
-    call (HIP events around a graph of back-to-back calls; eager=True launches
-    them directly, for kernel tracers)."""
-    keys = [f"bench.mm.{rows}x{cols}.{i}" for i in range(copies)]
+def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False, dtype=Q4K):
+    """matmul Y[n x rows] = X[n x cols] . W^T (GpuDispatch::matmul) with n
+    tokens (Q4_K or Q8_0: on the matrix cores from 16 tokens); `copies`
+    rotating weights.  Returns ms per call (HIP events around a graph of
+    back-to-back calls; eager=True launches them directly, for tracers)."""
+    keys = [f"bench.mm.{dtype}.{rows}x{cols}.{i}" for i in range(copies)]
     for i, k in enumerate(keys):
-        g.weight_synth(k, Q4K, rows, cols, seed, 3000 + i)
+        g.weight_synth(k, dtype, rows, cols, seed, 3000 + i)
     x = g.dev_alloc(n * cols * 4)
     y = g.dev_alloc(n * rows * 4)
     try:
@@ -623,7 +623,7 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="with --only: launch the timed steps directly instead of replaying a graph")
     ap.add_argument("--only", choices=["matvec", "q8_0", "down", "decode", "moe1", "moe32", "head", "matmul",
-                                       "readprobe"],
+                                       "matmul_q8", "batch8", "readprobe"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -652,6 +652,13 @@ def main():
             ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10),
                                 eager=args.eager)
             res = {"q6_k_head_128256x4096_us": round(ms * 1e3, 3)}
+        elif args.only == "batch8":
+            ms = time_matmul(g, 14336, 4096, 8, 16, max(20, args.steps // 10), min(args.warmup, 10), eager=args.eager)
+            res = {"q4_k_matmul_14336x4096_n8_us": round(ms * 1e3, 3)}
+        elif args.only == "matmul_q8":
+            ms = time_matmul(g, 4096, 4096, 64, 28, max(20, args.steps // 10), min(args.warmup, 10), eager=args.eager,
+                             dtype=Q8)
+            res = {"q8_0_matmul_4096x4096_n64_us": round(ms * 1e3, 3)}
         elif args.only == "matmul":
             ms = time_matmul(g, 14336, 4096, 64, 16, max(20, args.steps // 10), min(args.warmup, 10), eager=args.eager)
             res = {"q4_k_matmul_14336x4096_n64_us": round(ms * 1e3, 3)}
@@ -733,7 +740,14 @@ def main():
             "us_kernel": round(ms_mm * 1e3, 3), "GB_s": round(b_mm / (ms_mm * 1e-3) / 1e9, 1),
             "frac_hbm": round(b_mm / (ms_mm * 1e-3) / 1e9 / PEAK_GBS, 4),
             "gemm_TFLOP_s": round(2 * mm_n * 14336 * 4096 / (ms_mm * 1e-3) / 1e12, 2), "tokens": mm_n,
-            "path": "int8 MFMA 16x16x32 (exact codes x 3 digit planes of x)"}
+            "path": "int8 MFMA 16x16x64 (exact codes x 3 digit planes of x)"}
+        ms_q8 = time_matmul(g, 4096, 4096, mm_n, 28, max(20, args.steps // 10), min(args.warmup, 10), dtype=Q8)
+        b_q8 = algo_bytes(Q8, 4096, 4096) + (mm_n - 1) * 4096 * 8
+        extra["q8_0_matmul_4096x4096_n64"] = {
+            "us_kernel": round(ms_q8 * 1e3, 3), "GB_s": round(b_q8 / (ms_q8 * 1e-3) / 1e9, 1),
+            "frac_hbm": round(b_q8 / (ms_q8 * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "gemm_TFLOP_s": round(2 * mm_n * 4096 * 4096 / (ms_q8 * 1e-3) / 1e12, 2), "tokens": mm_n,
+            "path": "int8 MFMA 16x16x32, one per 32-element block and 4-token tile"}
         for n in (1, 32):
             ms_m, b_m, u_m, _ = time_moe(g, n, max(40, args.steps // 10))
             extra[f"moe_qwen3_30b_a3b_batch{n}"] = {

@@ -842,12 +842,13 @@ int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, con
     return hip_check(h, hipGetLastError(), "matvec_ex launch");
 }
 
-// n vectors: from MATMUL_MFMA_MIN tokens up, Q4_K goes to the matrix cores
-// (k_mfma.hip: within the same 1e-5 of the exact product, not bit-identical to
-// the single-vector kernel); fewer Q4_K vectors, and Q8_0 / Q6_K at any count,
-// run mv_tok (each row read once per launch of up to 16 tokens, every output
-// bit-identical to its own matvec); rows wider than 4096 columns run the
-// single-vector kernel once per vector.
+// n vectors: from MATMUL_MFMA_MIN tokens up, Q4_K and Q8_0 rows of whole
+// 256-column super-blocks go to the matrix cores (k_mfma.hip: within the same
+// 1e-5 of the exact product, not bit-identical to the single-vector kernel);
+// fewer vectors, Q6_K at any count and other Q8_0 widths run mv_tok (each row
+// read once per launch of up to 16 tokens, every output bit-identical to its
+// own matvec); rows wider than 4096 columns run the single-vector kernel once
+// per vector.
 constexpr size_t MATMUL_MFMA_MIN = 16;
 
 // Tokens per wavefront of mv_tok: each loaded unit meets two tokens' digits

@@ -1,7 +1,7 @@
-// k_mfma.hip -- Q4_K products of several tokens per weight row on the matrix
-// cores: the MoE experts when a call routes two or more tokens to each active
-// expert on average, and `matmul` (GpuDispatch::matmul, crates/soso-llm-core/
-// src/gpu.rs:443-455) from 16 tokens up.
+// k_mfma.hip -- products of several tokens per weight row on the matrix
+// cores: the Q4_K MoE experts when a call routes two or more tokens to each
+// active expert on average, and Q4_K or Q8_0 `matmul` (GpuDispatch::matmul,
+// crates/soso-llm-core/src/gpu.rs:443-455) from 16 tokens up.
 //
 // Exact integer arithmetic, as in the single-token kernels: x is staged as
 // three balanced signed base-256 digits of X = rint(x 2^e), one exponent e per
@@ -157,6 +157,68 @@ __device__ __forceinline__ void mf_scales(const uint4 &h, MfScale &s)
 
 __device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (8 * j)) & 0xffu); }
 
+// Stages columns k0 .. k0 + kc of the round's nt tokens (x rows slot_s[t] / xdiv)
+// into LDS, token t at t * mf_tok_bytes(kc): per 32-element sub-block the
+// three digit planes (32 bytes each), then the f32 sums of x per sub-block,
+// then 2^-e per 256-element super-block (NaN for a non-finite one).
+template <int NW>
+__device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__ xs, const int *slot_s, int xdiv, int cols,
+                                         int k0, int kc, int nt)
+{
+    const int tb = mf_tok_bytes(kc);
+    const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
+    // four chunks per thread are requested together, then converted
+    // (one L2 round trip per 4 * 64 * NW chunks)
+    constexpr int NT = 64 * NW, XB = 4;
+    for (int fb = 0; fb < tot; fb += XB * NT) {
+        float4 v0[XB], v1[XB];
+#pragma unroll
+        for (int k = 0; k < XB; k++) {
+            const int f = fb + k * NT + (int)threadIdx.x;
+            v0[k] = v1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (f < tot) {
+                const float4 *x4 =
+                    (const float4 *)(xs + (size_t)(slot_s[f / cpt] / xdiv) * cols + k0) + 2 * (f % cpt);
+                v0[k] = x4[0];
+                v1[k] = x4[1];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < XB; k++) {
+            if (fb + k * NT >= tot) break; // uniform
+            const int f = fb + k * NT + (int)threadIdx.x;
+            const bool valid = f < tot;
+            const int tt = valid ? f / cpt : 0, c = f % cpt;
+            // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
+            float mx = fmaxf(fmaxf(fmaxf(fabsf(v0[k].x), fabsf(v0[k].y)), fmaxf(fabsf(v0[k].z), fabsf(v0[k].w))),
+                             fmaxf(fmaxf(fabsf(v1[k].x), fabsf(v1[k].y)), fmaxf(fabsf(v1[k].z), fabsf(v1[k].w))));
+            // f32 sum of x over the 32-element sub-block: 4 aligned lanes
+            float sm = ((v0[k].x + v0[k].y) + (v0[k].z + v0[k].w)) + ((v1[k].x + v1[k].y) + (v1[k].z + v1[k].w));
+            if (sm != sm) mx = INFINITY; // a NaN element: the super-block is non-finite
+            mx = row16_max(mx);
+            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+            const bool finite = mx < INFINITY;
+            const int ex = (mx > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+            sm += dpp_f<0xB1>(sm);
+            sm += dpp_f<0x4E>(sm);
+            if (valid) {
+                uint32_t d0[XDIG], d1[XDIG];
+                digits4(v0[k], ex, d0);
+                digits4(v1[k], ex, d1);
+                uint8_t *tp = lds + (size_t)tt * tb;
+                const int sbl = c >> 2, q = c & 3;
+#pragma unroll
+                for (int kk = 0; kk < XDIG; kk++)
+                    *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * q) = make_uint2(d0[kk], d1[kk]);
+                if (q == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
+                // a non-finite super-block: NaN products, as the CPU's dot gives Inf or NaN
+                if ((c & 31) == 0)
+                    *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
+            }
+        }
+    }
+}
+
 // tabA/tabB: per-expert weight pointer tables (MoE), or null with W0 the dense
 // weight.  recs[4a ..] = {expert, tokens, first slot, 0} for a < *n_recs
 // (MoE), or dense_n > 0 tokens of one dense product (slot = token).  Item:
@@ -237,57 +299,7 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
             if constexpr (NMAT == 2) load_sb(rB, sb0, true, cb);
             __builtin_amdgcn_sched_barrier(0);
             // ---- stage x (columns k0 .. k0 + kc of the round's tokens) ----
-            const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
-            // four chunks per thread are requested together, then converted
-            // (one L2 round trip per 4 * 64 * NW chunks)
-            constexpr int NT = 64 * NW, XB = 4;
-            for (int fb = 0; fb < tot; fb += XB * NT) {
-                float4 v0[XB], v1[XB];
-#pragma unroll
-                for (int k = 0; k < XB; k++) {
-                    const int f = fb + k * NT + (int)threadIdx.x;
-                    v0[k] = v1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (f < tot) {
-                        const float4 *x4 =
-                            (const float4 *)(xs + (size_t)(slot_s[f / cpt] / xdiv) * cols + k0) + 2 * (f % cpt);
-                        v0[k] = x4[0];
-                        v1[k] = x4[1];
-                    }
-                }
-#pragma unroll
-                for (int k = 0; k < XB; k++) {
-                    if (fb + k * NT >= tot) break; // uniform
-                    const int f = fb + k * NT + (int)threadIdx.x;
-                    const bool valid = f < tot;
-                    const int tt = valid ? f / cpt : 0, c = f % cpt;
-                    // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
-                    float mx = fmaxf(fmaxf(fmaxf(fabsf(v0[k].x), fabsf(v0[k].y)), fmaxf(fabsf(v0[k].z), fabsf(v0[k].w))),
-                                     fmaxf(fmaxf(fabsf(v1[k].x), fabsf(v1[k].y)), fmaxf(fabsf(v1[k].z), fabsf(v1[k].w))));
-                    // f32 sum of x over the 32-element sub-block: 4 aligned lanes
-                    float sm = ((v0[k].x + v0[k].y) + (v0[k].z + v0[k].w)) + ((v1[k].x + v1[k].y) + (v1[k].z + v1[k].w));
-                    if (sm != sm) mx = INFINITY; // a NaN element: the super-block is non-finite
-                    mx = row16_max(mx);
-                    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-                    const bool finite = mx < INFINITY;
-                    const int ex = (mx > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
-                    sm += dpp_f<0xB1>(sm);
-                    sm += dpp_f<0x4E>(sm);
-                    if (valid) {
-                        uint32_t d0[XDIG], d1[XDIG];
-                        digits4(v0[k], ex, d0);
-                        digits4(v1[k], ex, d1);
-                        uint8_t *tp = lds + (size_t)tt * tb;
-                        const int sbl = c >> 2, q = c & 3;
-#pragma unroll
-                        for (int kk = 0; kk < XDIG; kk++)
-                            *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * q) = make_uint2(d0[kk], d1[kk]);
-                        if (q == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
-                        // a non-finite super-block: NaN products, as the CPU's dot gives Inf or NaN
-                        if ((c & 31) == 0)
-                            *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
-                    }
-                }
-            }
+            mf_stage<NW>(lds, xs, slot_s, xdiv, cols, k0, kc, nt);
             __syncthreads();
             // ---- stream this chunk's super-blocks of the wavefront's 16 rows ----
             // The 6-bit scale of each sub-block goes into the B operand: sc =
@@ -420,6 +432,127 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q8_0 products of several tokens per weight row (dense matmul from 16
+// tokens).  The codes are int8 already and every 32-element block has its
+// own f32 scale, so each block is one v_mfma_i32_16x16x32_i8 per 4-token
+// tile: exact int32 sums S[digit] = sum_k digit_k * q_k (|S| < 2^20), then in
+// f32 y += scale * 2^-e * (S0 + 256 S1 + 65536 S2), block by block in column
+// order (the Q8_0 dot of crates/sosomodel/src/dequant.rs:292-315 with x in
+// exact digits).  x is staged as for Q4_K (mf_stage: one exponent per 256
+// columns).  Operands (16 x 16 x 32, int8; lane l, n = l % 16, g = l / 16):
+//   A: row m = n = (token n / 4 of the tile, digit n % 4; 3 a zero pad),
+//      bytes 0..7 = elements 8g .. 8g + 7 of the block      <- LDS
+//   B: column n = weight row n, the same 8 code bytes of the block
+//      (bytes 16 (g / 2) .. of the block are plane 2b + g / 2 of the packed
+//      row, so the lane's 8 bytes are one aligned load)
+//   D: column n, rows 4g .. 4g + 3 = token g of the tile, digits 0..3.
+// A workgroup of NW wavefronts owns 16 rows per wavefront and one round of
+// 4 MT tokens; it walks the columns 256 at a time (8 blocks), the next 256
+// columns' loads in flight while one stretch is applied.  Measured on MI355X,
+// 4096 x 4096 at 64 tokens: 45 us (one 64-column unit at a time: 54 us;
+// three 256-column stretches in flight: 48 us).
+// ---------------------------------------------------------------------------
+struct MfQ80 {
+    uint4 s[2]; // f32 scales of the 8 blocks of 256 columns (this lane's row)
+    uint2 q[8]; // bytes 8g .. 8g + 7 of each block's codes
+};
+
+template <int MT, int NW>
+__global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
+                                                      const float *__restrict__ xs, int dense_n, int kcmax,
+                                                      float *__restrict__ out)
+{
+    typedef long mf_i64;
+    constexpr int TR = 4 * MT;
+    extern __shared__ uint4 mf_smem[];
+    uint8_t *lds = (uint8_t *)mf_smem;
+    __shared__ int slot_s[TR];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    constexpr int ROWS = 16 * NW;
+    const int nblk = (rows + ROWS - 1) / ROWS;
+    const int b = blockIdx.x % nblk;
+    const int t_step = (int)(gridDim.x / nblk) * TR;
+    const int nl = lane & 15, g = lane >> 4;
+    const int U = cols >> 6, nbk = cols >> 5;
+    // packed row: the f32 scales (8 bytes per unit, padded to 16), then 4
+    // planes of 16 bytes per unit (plane i at + 16 U i)
+    const uint32_t sreg = (uint32_t)((4 * nbk + 15) & ~15);
+    const uint32_t rowoff = (uint32_t)((16 * wave + nl) * stride);
+    const uint32_t qoff = sreg + (uint32_t)(16 * U * (g >> 1) + 8 * (g & 1));
+    const int a_tok = nl >> 2, a_dig = nl & 3;
+    for (int t0 = (blockIdx.x / nblk) * TR; t0 < dense_n; t0 += t_step) {
+        const int nt = min(TR, dense_n - t0);
+        __syncthreads();
+        if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = t0 + threadIdx.x;
+        __syncthreads();
+        const int r0 = b * ROWS, rend = min(rows, r0 + ROWS);
+        const rsrc_t rA = make_rsrc(W0 + (size_t)r0 * stride, (uint32_t)((size_t)(rend - r0) * stride));
+        const int row = r0 + 16 * wave + nl;
+        float accf[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) accf[mt] = 0.0f;
+        for (int k0 = 0; k0 < cols; k0 += kcmax) {
+            const int kc = min(kcmax, cols - k0), tb = mf_tok_bytes(kc), nsb = kc >> 8, sb0 = k0 >> 8;
+            auto load_sb = [&](int sb, bool in, MfQ80 &o) {
+                const uint32_t off = in ? rowoff : 0x80000000u;
+                o.s[0] = bld16(rA, off + 32u * (uint32_t)sb);
+                o.s[1] = bld16(rA, off + 32u * (uint32_t)sb + 16u);
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const uint32_t u = 4u * (uint32_t)sb + (uint32_t)p;
+                    o.q[2 * p] = bld8(rA, off + qoff + 16u * u);
+                    o.q[2 * p + 1] = bld8(rA, off + qoff + 32u * (uint32_t)U + 16u * u);
+                }
+            };
+            MfQ80 cur, nxt;
+            load_sb(sb0, true, cur); // requested before x is staged: its latency overlaps the staging
+            __builtin_amdgcn_sched_barrier(0);
+            mf_stage<NW>(lds, xs, slot_s, 1, cols, k0, kc, nt);
+            __syncthreads();
+            for (int i = 0; i < nsb; i++) {
+                load_sb(sb0 + i + 1, i + 1 < nsb, nxt);
+                __builtin_amdgcn_sched_barrier(0);
+                const uint32_t scs[8] = {cur.s[0].x, cur.s[0].y, cur.s[0].z, cur.s[0].w,
+                                         cur.s[1].x, cur.s[1].y, cur.s[1].z, cur.s[1].w};
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    const int sbl = 8 * i + k; // the block's 32-element sub-block in the chunk
+                    const float scale = __builtin_bit_cast(float, scs[k]);
+                    // block k: unit k / 2, half k % 2 (q[2 p + half])
+                    const uint2 qq = cur.q[2 * (k >> 1) + (k & 1)];
+                    const mf_i64 bq = (mf_i64)(((uint64_t)qq.y << 32) | qq.x);
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        if (mt * 4 >= nt) break; // uniform
+                        const int ta = mt * 4 + a_tok;
+                        mf_i64 xa = 0;
+                        if (a_dig < 3 && ta < nt) {
+                            const uint2 u = *(const uint2 *)(lds + (size_t)ta * tb + (sbl * 3 + a_dig) * 32 + 8 * g);
+                            xa = (mf_i64)(((uint64_t)u.y << 32) | u.x);
+                        }
+                        const mf_v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, bq, mf_v4i{0, 0, 0, 0}, 0, 0, 0);
+                        const int to = mt * 4 + g;
+                        const float P = *(const float *)(lds + (size_t)(to < nt ? to : 0) * tb + (kc >> 5) * 100 +
+                                                         4 * i);
+                        const float t = fmaf((float)d[2], 65536.0f, fmaf((float)d[1], 256.0f, (float)d[0]));
+                        accf[mt] = fmaf(scale * P, t, accf[mt]);
+                    }
+                }
+                cur = nxt;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            __syncthreads(); // LDS is restaged for the next chunk or round
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int to = mt * 4 + g;
+            if (mt * 4 < nt && to < nt && row < rows) out[(size_t)slot_s[to] * rows + row] = accf[mt];
+        }
+    }
+}
+
 // Columns staged per chunk: the largest multiple of 256 whose x for `tokens`
 // tokens fits `budget` bytes of LDS (the workgroup's whole LDS by default).
 static int mf_kc(const soso_hip *h, size_t cols, int tokens, size_t budget = 0)
@@ -430,12 +563,12 @@ static int mf_kc(const soso_hip *h, size_t cols, int tokens, size_t budget = 0)
     return kc;
 }
 
-// Shapes the matrix-core path handles: Q4_K rows, strips addressable with
-// 32-bit offsets.
+// Shapes the matrix-core path handles: Q4_K or Q8_0 rows of whole 256-column
+// super-blocks (x's exponents), strips addressable with 32-bit offsets.
 bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols)
 {
-    return dtype == SOSO_HIP_DTYPE_Q4_K && cols % 256 == 0 && cols >= 256 && rows > 0 &&
-           (size_t)16 * MF_NW_MAX * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
+    return (dtype == SOSO_HIP_DTYPE_Q4_K || dtype == SOSO_HIP_DTYPE_Q8_0) && cols % 256 == 0 && cols >= 256 &&
+           rows > 0 && (size_t)16 * MF_NW_MAX * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
 }
 
 // MoE: one grouped product over the active-expert records (device).
@@ -470,9 +603,14 @@ int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_
 template <int NW, int MT>
 static void mfma_dense(soso_hip *h, const Weight &w, const float *x, size_t n, float *y, int kc, unsigned grid)
 {
-    k_mfma_q4k<1, MT, MF_LA1, false, NW><<<grid, 64 * NW, (size_t)4 * MT * mf_tok_bytes(kc), h->stream>>>(
-        nullptr, nullptr, (const uint8_t *)w.dev, packed_row_stride(w.dtype, w.cols), (int)w.rows, (int)w.cols, x, 1,
-        nullptr, nullptr, nullptr, (int)n, kc, y);
+    const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc), stride = packed_row_stride(w.dtype, w.cols);
+    if (w.dtype == SOSO_HIP_DTYPE_Q8_0)
+        k_mfma_q80<MT, NW><<<grid, 64 * NW, lds, h->stream>>>((const uint8_t *)w.dev, stride, (int)w.rows,
+                                                              (int)w.cols, x, (int)n, kc, y);
+    else
+        k_mfma_q4k<1, MT, MF_LA1, false, NW><<<grid, 64 * NW, lds, h->stream>>>(
+            nullptr, nullptr, (const uint8_t *)w.dev, stride, (int)w.rows, (int)w.cols, x, 1, nullptr, nullptr,
+            nullptr, (int)n, kc, y);
 }
 
 // Dense: Y[n x rows] = X[n x cols] . W^T.  The grid is (row block of 16 NW

@@ -177,8 +177,8 @@ def test_matmul_equals_single_matvecs(gpu, orc, dtype, rows, cols, n):
     tokens goes to the matrix cores instead), and each output row is the very
     same bits as that vector's own matvec, as soso's batched q4_k_nb is to its
     single kernel (gemm.rs:902-1076); all within 1e-5 of the CPU."""
-    if dtype == Q4K and n >= 16:
-        pytest.skip("Q4_K from 16 tokens runs on the matrix cores (test_matmul_matrix_cores_match_cpu)")
+    if dtype in (Q4K, Q8) and n >= 16 and cols % 256 == 0:
+        pytest.skip("Q4_K / Q8_0 from 16 tokens run on the matrix cores (test_matmul_matrix_cores_match_cpu)")
     if dtype == Q6K and cols % 256:
         pytest.skip("Q6_K rows are whole super-blocks")
     w = orc.synth(dtype, rows, cols, 3, 3 + n)
@@ -201,10 +201,11 @@ def test_matmul_equals_single_matvecs(gpu, orc, dtype, rows, cols, n):
                                          (14336, 4096, 32), (14336, 4096, 64), (4096, 4096, 64),
                                          (4096, 14336, 32), (528, 1024, 256), (720, 1024, 200),
                                          (1296, 1024, 96), (1424, 1024, 200), (14336, 4096, 128)])
-def test_matmul_matrix_cores_match_cpu(gpu, orc, rows, cols, n):
-    """From 16 vectors up, Q4_K matmul runs on the matrix cores (exact int8
-    products of codes and x digits, scales in f32): every output row within
-    relative L2 1e-5 of the CPU restatement.  Shapes cover a partial row
+@pytest.mark.parametrize("dtype", [Q4K, Q8])
+def test_matmul_matrix_cores_match_cpu(gpu, orc, dtype, rows, cols, n):
+    """From 16 vectors up, Q4_K and Q8_0 matmul run on the matrix cores
+    (exact int8 products of codes and x digits, scales in f32): every output
+    row within relative L2 1e-5 of the CPU restatement.  Shapes cover a partial row
     block, column counts that end in a partial chunk, and token counts that
     leave a partial round of tokens.  The launcher takes the (wavefronts,
     tokens per round) pair giving the most workgroups within one per CU; the
@@ -213,14 +214,14 @@ def test_matmul_matrix_cores_match_cpu(gpu, orc, rows, cols, n):
     workgroups than CUs: half the LDS each, four chunks), (8, 2) 4096 x 4096
     at 64, (8, 1) 4096 x 14336 at 32 (two chunks), and (16, 1), (4, 4),
     (4, 2), (8, 4) the four 1024-column shapes."""
-    w = orc.synth(Q4K, rows, cols, 7, n)
+    w = orc.synth(dtype, rows, cols, 7, n)
     xs = orc.normal(n * cols, 1.0, 8, n).reshape(n, cols)
     out = np.empty(n * rows, np.float32)
-    key = f"mm.mfma.{rows}.{cols}.{n}"
+    key = f"mm.mfma.{dtype}.{rows}.{cols}.{n}"
     try:
-        assert gpu.matmul(key, w, Q4K, rows, cols, n, xs, out), gpu.last_error()
+        assert gpu.matmul(key, w, dtype, rows, cols, n, xs, out), gpu.last_error()
         out = out.reshape(n, rows)
-        ref = orc.matmul(Q4K, w, rows, cols, xs, threads=8, avx2=True)
+        ref = orc.matmul(dtype, w, rows, cols, xs, threads=8, avx2=True)
         for j in range(n):
             assert orc.rel_l2(out[j], ref[j]) < TOL, (j, orc.rel_l2(out[j], ref[j]))
     finally:
