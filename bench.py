@@ -362,6 +362,105 @@ def time_decode_8b(g, steps, ctx=4096, seed=21, kv_f16=False, eager=False):
                 pass
 
 
+def time_decode_moe(g, steps, ctx=4096, seed=31, eager=False):
+    """A Qwen3-30B-A3B-like decode step on the device (soso_hip_decode_create_moe;
+    GpuDispatch::moe_capa): 48 layers of GQA attention (hidden 2048, 32 query /
+    4 KV heads of 128, Q4_K q/k/v/o; the dense step's attention: non-NeoX RoPE,
+    no QK norm) and an MoE FFN (f32 router ~ N(0, 0.02), 128 Q4_K experts of
+    width 768, top-8), a Q6_K head over 151936, soso's f16 KV cache (the only KV
+    type soso's device MoE layer takes) prefilled with N(0, 1) to `ctx`
+    positions; the step runs at position `ctx`.  Timed like time_decode_8b.
+    Returns (ms per token, bytes per token, token)."""
+    L, H, NH, NKV, HDIM, E, F, K, V = 48, 2048, 32, 4, 128, 128, 768, 8, 151936
+    qd, kvd = NH * HDIM, NKV * HDIM
+    name = "qwen3moe"
+    keys, moe_names, exp_keys = [], [], []
+    s_ = 0
+
+    def norm(key, st):
+        d = g.dev_alloc(H * 4)
+        try:
+            g.synth_normal(d, H, 1.0, seed, st)
+            g.weight_from_dev(key, d, H * 4, F32, 1, H)
+        finally:
+            g.dev_free(d)
+    try:
+        for l in range(L):
+            for nm, rows, cols in (("attn_norm", 1, H), ("q", qd, H), ("k", kvd, H), ("v", kvd, H), ("o", H, qd),
+                                   ("ffn_norm", 1, H)):
+                k = f"{name}.L{l}.{nm}"
+                s_ += 1
+                if rows == 1:
+                    norm(k, s_)
+                else:
+                    g.weight_synth(k, Q4K, rows, cols, seed, s_)
+                keys.append(k)
+            keys += [None, None, None]
+            mk = f"{name}.L{l}.moe"
+            ek = []
+            for e in range(E):
+                for j, (nm, r, c) in enumerate((("gate", F, H), ("up", F, H), ("down", H, F))):
+                    k = f"{mk}.E{e}.{nm}"
+                    g.weight_synth(k, Q4K, r, c, seed, 100000 + l * 1000 + 3 * e + j)
+                    ek.append(k)
+            d = g.dev_alloc(E * H * 4)
+            try:
+                g.synth_normal(d, E * H, 0.02, seed + 1, l)
+                g.weight_from_dev(mk + ".router", d, E * H * 4, F32, E, H)
+            finally:
+                g.dev_free(d)
+            g.moe_register(mk, mk + ".router", ek, E, H, F, K)
+            moe_names.append(mk)
+            exp_keys += ek + [mk + ".router"]
+        norm(name + ".out_norm", 10000)
+        g.weight_synth(name + ".head", Q6K, V, H, seed, 10001)
+        keys += [name + ".out_norm", name + ".head"]
+        cfg = dict(n_layers=L, hidden=H, n_heads=NH, n_kv_heads=NKV, head_dim=HDIM, ffn=F, vocab=V, ctx_max=ctx + 1,
+                   rope_theta=1000000.0, rms_eps=1e-6, kv_f16=1)
+        assert g.decode_create(name, cfg, keys, drop_sources=True, moe_layers=moe_names), g.last_error()
+        x = g.dev_alloc(H * 4)
+        tok = g.dev_alloc(4)
+        st = [g.dev_alloc((ctx + 1) * kvd * 4) for _ in range(2)]
+        try:
+            for l in range(L):
+                g.synth_normal(st[0], (ctx + 1) * kvd, 1.0, seed + 2, 2 * l)
+                g.synth_normal(st[1], (ctx + 1) * kvd, 1.0, seed + 2, 2 * l + 1)
+                g.decode_kv_upload(name, l, 0, (st[0], ctx + 1), (st[1], ctx + 1), rows_f32=True)
+            g.synth_normal(x, H, 1.0, seed + 3, 0)
+            for _ in range(3):
+                g.decode_step_dev(name, x, ctx, None, tok)
+            g.sync()
+            if eager:
+                g.event_record(0)
+                for _ in range(steps):
+                    g.decode_step_dev(name, x, ctx, None, tok)
+                g.event_record(1)
+                g.sync()
+                ms = g.event_elapsed(0, 1) / steps
+            else:
+                ms = _timed_graph(g, lambda: [g.decode_step_dev(name, x, ctx, None, tok) for _ in range(steps)],
+                                  steps)[0]
+            token = int(g.d2h(tok, (1,), np.uint32)[0])
+        finally:
+            for p in st + [x, tok]:
+                g.dev_free(p)
+        attn = (qd + 2 * kvd) * (H // 256) * 144 + H * (qd // 256) * 144
+        expert = 3 * F * (H // 256) * 144  # gate + up + down of one expert (F % 256 == 0 for down's rows)
+        per_layer = attn + K * expert + E * H * 4 + 2 * H * 4
+        nbytes = L * per_layer + V * (H // 256) * 210 + L * 2 * (ctx + 1) * kvd * 2 + H * 4
+        return ms, nbytes, token
+    finally:
+        try:
+            g.decode_destroy(name)
+        except Exception:  # noqa: BLE001
+            pass
+        for k in [k for k in keys if k] + exp_keys:
+            try:
+                g.weight_drop(k)
+            except Exception:  # noqa: BLE001 -- dropped with the sources
+                pass
+
+
 def copy_calibration(g, nbytes=512 << 20, reps=20):
     """A plain device-to-device copy of known size, for scaling rocprofv3's
     FETCH_SIZE / WRITE_SIZE counters (run under --pmc)."""
@@ -623,7 +722,7 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="with --only: launch the timed steps directly instead of replaying a graph")
     ap.add_argument("--only", choices=["matvec", "q8_0", "down", "decode", "moe1", "moe32", "head", "matmul",
-                                       "matmul_q8", "batch8", "readprobe"],
+                                       "matmul_q8", "batch8", "decode_moe", "readprobe"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -652,6 +751,10 @@ def main():
             ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10),
                                 eager=args.eager)
             res = {"q6_k_head_128256x4096_us": round(ms * 1e3, 3)}
+        elif args.only == "decode_moe":
+            ms, nb, tok = time_decode_moe(g, max(10, args.steps // 50), eager=args.eager)
+            res = {"qwen3_30b_a3b_like_decode_ms_per_token": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+                   "bytes_per_token": int(nb), "greedy_token": tok}
         elif args.only == "batch8":
             ms = time_matmul(g, 14336, 4096, 8, 16, max(20, args.steps // 10), min(args.warmup, 10), eager=args.eager)
             res = {"q4_k_matmul_14336x4096_n8_us": round(ms * 1e3, 3)}
@@ -766,6 +869,13 @@ def main():
             "GB_s": round(b_h / (ms_h * 1e-3) / 1e9, 1), "frac_hbm": round(b_h / (ms_h * 1e-3) / 1e9 / PEAK_GBS, 4),
             "bytes_per_token": int(b_h), "greedy_token": tok_h,
             "kv": "f16 (soso's KvDtype::F16), same N(0,1) prefill rounded on upload"}
+        ms_q, b_q, tok_q = time_decode_moe(g, max(10, args.steps // 10))
+        extra["qwen3_30b_a3b_like_decode_ctx4096_kv_f16"] = {
+            "ms_per_token": round(ms_q, 4), "tokens_per_s": round(1e3 / ms_q, 1),
+            "GB_s": round(b_q / (ms_q * 1e-3) / 1e9, 1), "frac_hbm": round(b_q / (ms_q * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "bytes_per_token": int(b_q), "greedy_token": tok_q,
+            "model": "48 layers: GQA attention (32/4 heads of 128, hidden 2048, Q4_K) + MoE FFN (128 Q4_K experts "
+                     "of 768, top-8, f32 router), Q6_K head over 151936, f16 KV"}
         # measured HBM traffic over algorithmic bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, profiles/)
         for name, entry in extra.items():
             detail = load_traffic(name + "_detail")

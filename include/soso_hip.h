@@ -201,6 +201,28 @@ typedef struct soso_hip_decode_cfg {
 } soso_hip_decode_cfg;
 int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
                            const char *const *keys, const size_t *key_lens, int drop_sources);
+/* The same step with MoE layers (GpuDispatch::moe_capa for one token,
+ * crates/soso-llm-core/src/gpu.rs; the GQA-MoE layer that capa_moe_en_gpu,
+ * crates/soso-llm-core/src/moe_gpu.rs:37, runs on the device): layer l's FFN
+ * is the registered MoE layer moe_layer_keys[l] (soso_hip_moe_register, width
+ * hidden) when that entry is non-null -- forward_moe_ffn, layer.rs:1938-1975:
+ * x = rmsnorm(h) * ffn_norm, router + top-k, the chosen experts' gate/up +
+ * SwiGLU and down, h += their ranking-order sum -- and the dense FFN of
+ * soso_hip_decode_create otherwise.  The keys array keeps its 9 entries per
+ * layer; an MoE layer's gate, up and down entries are ignored (may be null
+ * with length 0).  Attention is the dense step's (non-NeoX RoPE, no QK norm).
+ * MoE layers take the single-token expert path: gate/up Q4_K, Q8_0 or Q6_K
+ * with hidden a multiple of 128 up to 4096, down Q4_K with an expert width of
+ * 256 to 2048 (a multiple of 256), top_k <= 8; others are declined here.
+ * Re-registering or unregistering an MoE layer the model reads destroys the
+ * model. */
+int soso_hip_decode_create_moe(soso_hip *h, const char *model_key, size_t model_key_len,
+                               const soso_hip_decode_cfg *cfg, const char *const *keys, const size_t *key_lens,
+                               const char *const *moe_layer_keys, const size_t *moe_layer_key_lens, int drop_sources);
+/* Device pointers of MoE layer `layer`'s routing in the last step: top_k
+ * expert indices (int32) and weights (f32), in ranking order. */
+int soso_hip_decode_moe_routing_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer,
+                                    int32_t **idx_dev, float **wgt_dev);
 /* Device pointers of layer `layer`'s K and V caches, head-major:
  * [n_kv_heads][ctx_max][head_dim] (a head's positions are contiguous), each
  * element f32 or f16 bits as kv_f16 says, for prefilling and inspection. */

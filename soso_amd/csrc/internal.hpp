@@ -66,9 +66,25 @@ struct MoeLayer {
 };
 
 // A dense decode model registered for the device-resident step (k_decode.hip).
+// (k_moe.hip) -- device scratch of one MoE FFN call
+struct MoeScratch {
+    float *logits = nullptr; // n x n_exp
+    int32_t *idx = nullptr;  // n x top_k
+    float *wgt = nullptr;    // n x top_k
+    int *cnt = nullptr, *offs = nullptr, *list = nullptr; // n_groups, n_groups + 1, n x top_k
+    int *items = nullptr, *n_items = nullptr; // work items {group, count, first slot, chunk | chunks << 16}, count
+    int *recs = nullptr, *n_recs = nullptr;   // active groups {group, count, first slot, 0} (ascending), count
+    float *act = nullptr;    // n x top_k x ffn
+    float *ydown = nullptr;  // n x top_k x hdim
+};
+
 struct DecodeLayer {
     const Weight *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
     const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    // a registered MoE layer as the FFN (instead of gu / down), its scratch
+    // (carved from the model's buffer; idx / wgt per layer: the last step's routing)
+    const MoeLayer *moe = nullptr;
+    MoeScratch moe_s;
 };
 struct DecodeModel {
     size_t n_layers = 0, hidden = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, ffn = 0, vocab = 0, ctx_max = 0;
@@ -77,12 +93,15 @@ struct DecodeModel {
     std::vector<Weight> owned; // the fused qkv / gate-up copies
     const float *out_norm = nullptr;
     const Weight *head = nullptr;
-    std::vector<std::string> uses; // keys of the resident weights the model reads
+    std::vector<std::string> uses;     // keys of the resident weights the model reads
+    std::vector<std::string> moe_uses; // keys of the registered MoE layers it reads
     bool kv_f16 = false;                        // KV elements: f16 bits (soso's KvDtype::F16) or f32
     void *kcache = nullptr, *vcache = nullptr;  // [n_layers][n_kv_heads][ctx_max][head_dim]
     void *mem = nullptr;                         // activations below, one allocation
     float *hid = nullptr, *qbuf = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
     float *rope_freq = nullptr; // head_dim / 2 floats
+    float *xn = nullptr;        // the MoE layers' normalized x (hidden floats)
+    void *moe_mem = nullptr;    // the MoE layers' scratch and routing
 };
 
 constexpr size_t SOSO_TICKET_BYTES = 16384;
@@ -193,17 +212,6 @@ int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t 
 int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream);
 int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads,
                       unsigned loads, bool chunked, uint32_t *out, size_t out_len);
-// (k_moe.hip) -- device scratch of one MoE FFN call
-struct MoeScratch {
-    float *logits = nullptr; // n x n_exp
-    int32_t *idx = nullptr;  // n x top_k
-    float *wgt = nullptr;    // n x top_k
-    int *cnt = nullptr, *offs = nullptr, *list = nullptr; // n_groups, n_groups + 1, n x top_k
-    int *items = nullptr, *n_items = nullptr; // work items {group, count, first slot, chunk | chunks << 16}, count
-    int *recs = nullptr, *n_recs = nullptr;   // active groups {group, count, first slot, 0} (ascending), count
-    float *act = nullptr;    // n x top_k x ffn
-    float *ydown = nullptr;  // n x top_k x hdim
-};
 bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s);
 // The same regions in one buffer of `cap` bytes at `base` (256-byte aligned
 // pieces); returns the bytes needed, and sets s only when they fit.
@@ -226,7 +234,13 @@ int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t
                      size_t top_k, const MoeScratch &s);
 // One token through a registered MoE layer, the ranking done by the expert
 // kernel (DECLINED when the layer's shapes need the general path).
-int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x_dev, const MoeScratch &s, float *out_dev);
+// One token through a registered layer (route, gate/up + SwiGLU, down +
+// weighted sum), three launches; res: added to the output (may be out_dev).
+int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x_dev, const MoeScratch &s, float *out_dev,
+                    const float *res = nullptr);
+const char *moe_ffn1_unsupported(const soso_hip *h, const MoeLayer &m);
+// (k_decode.hip) out[n] = rmsnorm(x) * w (one workgroup)
+int launch_rmsnorm(soso_hip *h, const float *x, const float *w, size_t n, float eps, float *out);
 int launch_moe_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab_dev, size_t n_groups,
                        const float *wgt_dev, const uint8_t *use_dev, const int32_t *route_idx_dev,

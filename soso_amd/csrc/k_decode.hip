@@ -1,4 +1,5 @@
-// k_decode.hip -- one decode step of a dense Llama-style model on the device.
+// k_decode.hip -- one decode step of a Llama-style model on the device (dense
+// FFN layers, or registered MoE layers as the FFN).
 //
 // Reference: LayerExecutor::forward_layer, dense GQA branch
 // (crates/soso-llm-core/src/layer.rs:1092-1389): attn_norm -> q/k/v ->
@@ -19,6 +20,9 @@
 //   5. gate/up      x = rmsnorm(h); rows interleaved (gate_i, up_i); the
 //                   epilogue writes silu(gate_i) * up_i
 //   6. down matvec  h += W_down . act
+// or, for a layer whose FFN is a registered MoE layer (4-6): x = rmsnorm(h),
+// then the single-token MoE path (route; gate/up + SwiGLU; down, weighted sum
+// and residual).
 // Head: matvec with rmsnorm(h) staged (Q6_K or Q8_0 / Q4_K), then argmax.
 #include "internal.hpp"
 
@@ -280,6 +284,44 @@ int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, 
     return hip_check(h, hipGetLastError(), "attention merge launch");
 }
 
+// rmsnorm (crates/soso-llm-core/src/gemm.rs:93-100) into a new vector: one
+// workgroup of 1024 threads, x loaded once into registers (n <= 8192),
+// out_i = (x_i * scale) * w_i with scale = 1 / sqrt(sum(x^2) / n + eps) --
+// the arithmetic the matvec staging's RMSNorm uses.  The MoE FFN of a decode
+// layer reads it (its experts stage x as given).
+constexpr int RMS_T = 1024, RMS_PER = 8; // threads, elements per thread
+__global__ void __launch_bounds__(RMS_T) k_rmsnorm(const float *__restrict__ x, const float *__restrict__ w, int n,
+                                                   float eps, float *__restrict__ out)
+{
+    __shared__ float red[RMS_T / 64];
+    float v[RMS_PER];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < RMS_PER; k++) {
+        const int i = k * RMS_T + (int)threadIdx.x;
+        v[k] = i < n ? x[i] : 0.0f;
+        ss = fmaf(v[k], v[k], ss);
+    }
+    ss = seg_sum<64>(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int i = 0; i < RMS_T / 64; i++) tot += red[i];
+    const float scale = 1.0f / sqrtf(tot / (float)n + eps);
+#pragma unroll
+    for (int k = 0; k < RMS_PER; k++) {
+        const int i = k * RMS_T + (int)threadIdx.x;
+        if (i < n) out[i] = __fmul_rn(__fmul_rn(v[k], scale), w[i]);
+    }
+}
+
+int launch_rmsnorm(soso_hip *h, const float *x, const float *w, size_t n, float eps, float *out)
+{
+    if (n == 0 || n > (size_t)RMS_T * RMS_PER) return set_err(h, SOSO_HIP_DECLINED, "rmsnorm: width");
+    k_rmsnorm<<<1, RMS_T, 0, h->stream>>>(x, w, (int)n, eps, out);
+    return hip_check(h, hipGetLastError(), "rmsnorm launch");
+}
+
 // KV upload (decode_subir_estado): element e of the position-major rows
 // [n_rows][kv_dim] goes to head e / head_dim, position row0 + e / kv_dim of
 // the head-major cache; f32 rows entering an f16 cache take soso's rounding.
@@ -360,19 +402,26 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
             r.res = hin;
             rc = launch_matvec_ex(h, *L.o, a, hid, r, XS_PLAIN, EPI_RESID);
         }
-        if (rc == SOSO_HIP_OK) {
-            MvIn f;
-            f.x = hid;
-            f.norm_w = L.ffn_norm;
-            f.eps = m.eps;
-            rc = launch_matvec_ex(h, *L.gu, f, act, MvEpi(), XS_RMSNORM, EPI_SWIGLU);
-        }
-        if (rc == SOSO_HIP_OK) {
-            MvIn a;
-            a.x = act;
-            MvEpi r;
-            r.res = hid;
-            rc = launch_matvec_ex(h, *L.down, a, hid, r, XS_PLAIN, EPI_RESID);
+        if (L.moe) {
+            // MoE FFN (forward_moe_ffn, layer.rs:1938-1975): x = rmsnorm(h) * ffn_norm,
+            // router + top-k, the chosen experts, h += their ranking-order sum
+            if (rc == SOSO_HIP_OK) rc = launch_rmsnorm(h, hid, L.ffn_norm, m.hidden, m.eps, m.xn);
+            if (rc == SOSO_HIP_OK) rc = launch_moe_ffn1(h, *L.moe, m.xn, L.moe_s, hid, hid);
+        } else {
+            if (rc == SOSO_HIP_OK) {
+                MvIn f;
+                f.x = hid;
+                f.norm_w = L.ffn_norm;
+                f.eps = m.eps;
+                rc = launch_matvec_ex(h, *L.gu, f, act, MvEpi(), XS_RMSNORM, EPI_SWIGLU);
+            }
+            if (rc == SOSO_HIP_OK) {
+                MvIn a;
+                a.x = act;
+                MvEpi r;
+                r.res = hid;
+                rc = launch_matvec_ex(h, *L.down, a, hid, r, XS_PLAIN, EPI_RESID);
+            }
         }
     }
     if (rc == SOSO_HIP_OK) {

@@ -735,7 +735,8 @@ template <int LPR, int P>
 __global__ void __launch_bounds__(512) k_moe_down_comb(const uint8_t *const *__restrict__ tab, size_t stride, int rows,
                                                        int cols, int n_exp, const float *__restrict__ act,
                                                        const int32_t *__restrict__ idx, const float *__restrict__ wgt,
-                                                       int n, int top_k, float *__restrict__ out)
+                                                       int n, int top_k, const float *__restrict__ res,
+                                                       float *__restrict__ out)
 {
     constexpr int RW = 64 / LPR, RB = RW * P; // rows per item
     extern __shared__ uint4 smem[];
@@ -800,7 +801,8 @@ __global__ void __launch_bounds__(512) k_moe_down_comb(const uint8_t *const *__r
             const int r = r0 + (int)threadIdx.x;
             float acc = 0.0f;
             for (int q = 0; q < top_k; q++) acc = fmaf(dots[q][threadIdx.x], wgt[(size_t)t * top_k + q], acc);
-            if (r < rows) out[(size_t)t * rows + r] = acc;
+            // res (may be out itself): the residual added after the sum, as layer.rs:1389 adds it
+            if (r < rows) out[(size_t)t * rows + r] = res ? res[(size_t)t * rows + r] + acc : acc;
         }
         __syncthreads(); // dots and the act regions are rewritten by the next item
     }
@@ -1011,9 +1013,12 @@ static void moe_rows_self(soso_hip *h, unsigned grid, size_t lds, int lpr, const
 }
 
 static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp, size_t rows, size_t cols,
-                            const float *act, const int32_t *idx, const float *wgt, size_t n, size_t top_k, float *out);
+                            const float *act, const int32_t *idx, const float *wgt, size_t n, size_t top_k,
+                            const float *res, float *out);
 
-int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScratch &s, float *out)
+// The single-token path's limits (launch_moe_ffn1): why a layer cannot take
+// it, or null.
+const char *moe_ffn1_unsupported(const soso_hip *h, const MoeLayer &m)
 {
     const size_t hdim = m.hdim, ffn = m.ffn, top_k = m.top_k, n_exp = m.n_exp;
     const int U = (int)(hdim / 64);
@@ -1021,17 +1026,29 @@ int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScr
     const bool gu_ok = (m.dt_gu == SOSO_HIP_DTYPE_Q4_K || m.dt_gu == SOSO_HIP_DTYPE_Q8_0 ||
                         m.dt_gu == SOSO_HIP_DTYPE_Q6_K) &&
                        U >= 1 && U <= 64 && hdim % 128 == 0 && packed_shape_ok(m.dt_gu, ffn, hdim);
+    if (!gu_ok) return "gate/up: Q4_K, Q8_0 or Q6_K rows of 128 to 4096 columns (a multiple of 128)";
     const bool down_ok = m.dt_down == SOSO_HIP_DTYPE_Q4_K && ffn % 256 == 0 && Uf >= 4 && Uf <= 8 * (size_t)MDC_XR &&
                          ((stage_lds_bytes(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds &&
                          packed_shape_ok(m.dt_down, hdim, ffn);
-    if (top_k == 0 || top_k > (size_t)MOE_SELF_K || n_exp > 256 || !gu_ok || !down_ok)
-        return set_err(h, SOSO_HIP_DECLINED, "moe ffn1: shape for the general path");
+    if (!down_ok) return "down: Q4_K, expert width 256 to 2048 (a multiple of 256)";
+    if (top_k == 0 || top_k > (size_t)MOE_SELF_K || n_exp > 256) return "top_k above 8 or more than 256 experts";
     const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
     const size_t rows_per_pass = 8 * (64 / lpr), passes = (ffn + rows_per_pass - 1) / rows_per_pass;
     const size_t stride = packed_row_stride(m.dt_gu, hdim);
     const size_t lds = (stage_lds_bytes(hdim) + 15) & ~(size_t)15;
-    if (lds > h->max_lds || (passes + 2) * rows_per_pass * stride >= ((size_t)1 << 31))
-        return set_err(h, SOSO_HIP_DECLINED, "moe ffn1: shape for the general path");
+    if (lds > h->max_lds || (passes + 2) * rows_per_pass * stride >= ((size_t)1 << 31)) return "expert too large";
+    return nullptr;
+}
+
+// res: added to the output after the ranking-order sum (may be out itself), or null.
+int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScratch &s, float *out, const float *res)
+{
+    if (moe_ffn1_unsupported(h, m)) return set_err(h, SOSO_HIP_DECLINED, "moe ffn1: shape for the general path");
+    const size_t hdim = m.hdim, ffn = m.ffn, top_k = m.top_k, n_exp = m.n_exp;
+    const int U = (int)(hdim / 64);
+    const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
+    const size_t stride = packed_row_stride(m.dt_gu, hdim);
+    const size_t lds = (stage_lds_bytes(hdim) + 15) & ~(size_t)15;
     // the route kernel's item count for one token: about moe_item_target
     // chunks in all, the same share for every ranked expert
     const int chunks = std::max(1, (moe_item_target(h) + (int)top_k / 2) / (int)top_k);
@@ -1056,7 +1073,7 @@ int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScr
     }
     rc = hip_check(h, hipGetLastError(), "moe ffn1 gate/up launch");
     if (rc != SOSO_HIP_OK) return rc;
-    return launch_down_comb(h, m.tab + 2 * n_exp, n_exp, hdim, ffn, s.act, s.idx, s.wgt, 1, top_k, out);
+    return launch_down_comb(h, m.tab + 2 * n_exp, n_exp, hdim, ffn, s.act, s.idx, s.wgt, 1, top_k, res, out);
 }
 
 // gate/up + swiglu, down, combine for the slots grouped in s.cnt/offs/list.
@@ -1067,7 +1084,8 @@ int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScr
 constexpr size_t MDC_MAX_TOKENS = 4;
 
 static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp, size_t rows, size_t cols,
-                            const float *act, const int32_t *idx, const float *wgt, size_t n, size_t top_k, float *out)
+                            const float *act, const int32_t *idx, const float *wgt, size_t n, size_t top_k,
+                            const float *res, float *out)
 {
     const int U = (int)(cols / 64);
     const int lpr = U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
@@ -1083,11 +1101,11 @@ static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp
 #define MDC_CASE(LP)                                                                                                   \
     case LP:                                                                                                           \
         if (P == 4)                                                                                                    \
-            k_moe_down_comb<LP, 4><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, out); \
+            k_moe_down_comb<LP, 4><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, res, out); \
         else if (P == 2)                                                                                               \
-            k_moe_down_comb<LP, 2><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, out); \
+            k_moe_down_comb<LP, 2><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, res, out); \
         else                                                                                                           \
-            k_moe_down_comb<LP, 1><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, out); \
+            k_moe_down_comb<LP, 1><<<grid, 512, lds, h->stream>>>(tab, stride, ri, ci, ne, act, idx, wgt, ni, ki, res, out); \
         break;
     switch (lpr) {
         MDC_CASE(8) MDC_CASE(16) MDC_CASE(32) MDC_CASE(64)
@@ -1120,7 +1138,8 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
     if (rc == SOSO_HIP_OK && route_idx && !use && n <= MDC_MAX_TOKENS && top_k <= (size_t)MDC_K &&
         dt_down == SOSO_HIP_DTYPE_Q4_K && ffn % 256 == 0 && Uf >= 4 && Uf <= 8 * MDC_XR &&
         ((stage_lds_bytes(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds && packed_shape_ok(dt_down, hdim, ffn))
-        return launch_down_comb(h, tab + 2 * n_groups, n_groups, hdim, ffn, s.act, route_idx, wgt, n, top_k, out);
+        return launch_down_comb(h, tab + 2 * n_groups, n_groups, hdim, ffn, s.act, route_idx, wgt, n, top_k, nullptr,
+                                out);
     if (rc == SOSO_HIP_OK) {
         if (many && dt_down == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_down, hdim, ffn))
             rc = launch_mfma_moe(h, 1, (tdn ? ttab : tab) + 2 * n_groups, nullptr, hdim, ffn, max_recs, s.act, 1, s.list,

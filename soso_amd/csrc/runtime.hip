@@ -241,8 +241,25 @@ int decode_free(soso_hip *h, DecodeModel &m)
     m.owned.clear();
     if (m.kcache) rc = first_fail(rc, hip_release(h, hipFree(m.kcache), "free KV cache"));
     if (m.mem) rc = first_fail(rc, hip_release(h, hipFree(m.mem), "free step buffers"));
+    if (m.moe_mem) rc = first_fail(rc, hip_release(h, hipFree(m.moe_mem), "free MoE scratch"));
     m.kcache = m.vcache = nullptr;
-    m.mem = nullptr;
+    m.mem = m.moe_mem = nullptr;
+    return rc;
+}
+
+// Unregisters the decode models that read MoE layer `key` (it is being
+// replaced or unregistered).
+int drop_models_using_moe(soso_hip *h, const std::string &key)
+{
+    int rc = SOSO_HIP_OK;
+    for (auto d = h->decode_models.begin(); d != h->decode_models.end();) {
+        if (std::find(d->second.moe_uses.begin(), d->second.moe_uses.end(), key) != d->second.moe_uses.end()) {
+            rc = first_fail(rc, decode_free(h, d->second));
+            d = h->decode_models.erase(d);
+        } else {
+            ++d;
+        }
+    }
     return rc;
 }
 
@@ -686,7 +703,7 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
     std::string k(layer_key, layer_key_len);
     auto it = h->moe_layers.find(k);
     if (it != h->moe_layers.end()) {
-        rc = moe_free(h, it->second);
+        rc = first_fail(drop_models_using_moe(h, k), moe_free(h, it->second));
         h->moe_layers.erase(it);
     }
     h->moe_layers.emplace(k, m);
@@ -755,8 +772,12 @@ int soso_hip_moe_ffn_dev_noalloc(soso_hip *h, const char *layer_key, size_t laye
 }
 
 // ---- dense decode step -------------------------------------------------------
-int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
-                           const char *const *keys, const size_t *key_lens, int drop_sources)
+// decode_create / decode_create_moe: moe_keys (n_layers entries, null for a
+// dense model) names the registered MoE layer that is layer l's FFN, or null
+// for a dense FFN.
+static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
+                              const char *const *keys, const size_t *key_lens, const char *const *moe_keys,
+                              const size_t *moe_key_lens, int drop_sources)
 {
     if (!h) return SOSO_HIP_ERR_ARG;
     if (!model_key || !cfg || !keys || !key_lens || cfg->n_layers == 0 || cfg->hidden == 0 || cfg->hidden % 4 ||
@@ -793,16 +814,39 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     };
     std::vector<const Weight *> q(L), k(L), v(L), g(L), u(L);
     m.layers.resize(L);
+    size_t moe_need = 0, n_moe = 0; // MoE scratch bytes (the largest layer's) and layers
     for (size_t l = 0; l < L; l++) {
         const Weight *an, *fn;
         const size_t b = 9 * l;
+        const bool is_moe = moe_keys && moe_keys[l];
+        if (is_moe) {
+            const std::string mk(moe_keys[l], moe_key_lens[l]);
+            auto mit = h->moe_layers.find(mk);
+            if (mit == h->moe_layers.end())
+                return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + ": MoE layer " +
+                                                         mk + " is not registered");
+            const MoeLayer &ml = mit->second;
+            if (ml.hdim != H)
+                return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) +
+                                                         ": the MoE layer's width is not hidden");
+            if (const char *why = moe_ffn1_unsupported(h, ml))
+                return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + " MoE: " + why);
+            if (H > 8192) return set_err(h, SOSO_HIP_DECLINED, "decode_create: MoE layers take hidden <= 8192");
+            m.layers[l].moe = &ml;
+            MoeScratch probe;
+            moe_need = std::max(moe_need, moe_scratch_fixed(h, 1, ml.n_exp, ml.top_k, ml.hdim, ml.ffn, nullptr, 0,
+                                                            probe));
+            n_moe++;
+            m.moe_uses.push_back(mk);
+        }
         if (!get(b, 1, H, true, &an) || !get(b + 1, qd, H, false, &q[l]) || !get(b + 2, kvd, H, false, &k[l]) ||
             !get(b + 3, kvd, H, false, &v[l]) || !get(b + 4, H, qd, false, &m.layers[l].o) ||
-            !get(b + 5, 1, H, true, &fn) || !get(b + 6, F, H, false, &g[l]) || !get(b + 7, F, H, false, &u[l]) ||
-            !get(b + 8, H, F, false, &m.layers[l].down))
+            !get(b + 5, 1, H, true, &fn) ||
+            (!is_moe && (!get(b + 6, F, H, false, &g[l]) || !get(b + 7, F, H, false, &u[l]) ||
+                         !get(b + 8, H, F, false, &m.layers[l].down))))
             return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) +
                                                      ": a weight is missing or has the wrong shape");
-        if (q[l]->dtype != k[l]->dtype || q[l]->dtype != v[l]->dtype || g[l]->dtype != u[l]->dtype)
+        if (q[l]->dtype != k[l]->dtype || q[l]->dtype != v[l]->dtype || (!is_moe && g[l]->dtype != u[l]->dtype))
             return set_err(h, SOSO_HIP_DECLINED, "decode_create: q/k/v or gate/up dtypes differ");
         // every launch of the step, checked here so that a step never declines
         // halfway through a token
@@ -816,7 +860,8 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
                      {g[l], 2 * F, H, XS_RMSNORM, EPI_SWIGLU, "gate/up"},
                      {m.layers[l].down, H, F, XS_PLAIN, EPI_RESID, "down"}};
         for (const auto &r : roles)
-            if (const char *why = matvec_ex_unsupported(h, r.w->dtype, r.rows, r.cols, r.xs, r.epi))
+            if (r.w && (!is_moe || r.epi == EPI_QKV || r.w == m.layers[l].o))
+                if (const char *why = matvec_ex_unsupported(h, r.w->dtype, r.rows, r.cols, r.xs, r.epi))
                 return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + " " + r.role + ": " +
                                                          why);
         m.layers[l].attn_norm = (const float *)an->dev;
@@ -830,28 +875,32 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     m.out_norm = (const float *)on->dev;
     // what stays in use (dropping one of these unregisters the model)
     for (size_t l = 0; l < L; l++)
-        for (size_t j : {0, 4, 5, 8}) m.uses.emplace_back(keys[9 * l + j], key_lens[9 * l + j]);
+        for (size_t j : {0, 4, 5, 8})
+            if (!(j == 8 && m.layers[l].moe)) m.uses.emplace_back(keys[9 * l + j], key_lens[9 * l + j]);
     m.uses.emplace_back(keys[9 * L], key_lens[9 * L]);
     m.uses.emplace_back(keys[9 * L + 1], key_lens[9 * L + 1]);
     // fused copies
     m.owned.resize(2 * L);
     for (size_t l = 0; l < L && rc == SOSO_HIP_OK; l++) {
-        const size_t st_qkv = packed_row_stride(q[l]->dtype, H), st_gu = packed_row_stride(g[l]->dtype, H);
+        const bool dense = !m.layers[l].moe; // an MoE layer fuses q/k/v only
+        const size_t st_qkv = packed_row_stride(q[l]->dtype, H), st_gu = dense ? packed_row_stride(g[l]->dtype, H) : 0;
         Weight &wq = m.owned[2 * l], &wg = m.owned[2 * l + 1];
         wq.dtype = q[l]->dtype;
         wq.rows = qd + 2 * kvd;
         wq.cols = H;
         wq.bytes = wq.rows * st_qkv;
-        wg.dtype = g[l]->dtype;
-        wg.rows = 2 * F;
-        wg.cols = H;
-        wg.bytes = wg.rows * st_gu;
+        if (dense) {
+            wg.dtype = g[l]->dtype;
+            wg.rows = 2 * F;
+            wg.cols = H;
+            wg.bytes = wg.rows * st_gu;
+        }
         // each allocation is counted as it succeeds, so decode_free's release
         // of whatever was allocated keeps h->used exact on a failure
         bool got = h->used + wq.bytes + wg.bytes <= h->budget && hipMalloc(&wq.dev, wq.bytes) == hipSuccess;
         if (got) h->used += wq.bytes;
         else wq.dev = nullptr;
-        got = got && hipMalloc(&wg.dev, wg.bytes) == hipSuccess;
+        got = got && (!dense || hipMalloc(&wg.dev, wg.bytes) == hipSuccess);
         if (got) h->used += wg.bytes;
         else wg.dev = nullptr;
         if (!got) {
@@ -866,10 +915,10 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
         if (rc == SOSO_HIP_OK)
             rc = hip_check(h, hipMemcpyAsync(dq + (qd + kvd) * st_qkv, v[l]->dev, kvd * st_qkv,
                                              hipMemcpyDeviceToDevice, h->stream), "qkv copy");
-        if (rc == SOSO_HIP_OK)
+        if (rc == SOSO_HIP_OK && dense)
             rc = hip_check(h, hipMemcpy2DAsync(wg.dev, 2 * st_gu, g[l]->dev, st_gu, st_gu, F, hipMemcpyDeviceToDevice,
                                                h->stream), "gate copy");
-        if (rc == SOSO_HIP_OK)
+        if (rc == SOSO_HIP_OK && dense)
             rc = hip_check(h, hipMemcpy2DAsync((char *)wg.dev + st_gu, 2 * st_gu, u[l]->dev, st_gu, st_gu, F,
                                                hipMemcpyDeviceToDevice, h->stream), "up copy");
         m.layers[l].qkv = &wq;
@@ -879,10 +928,15 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
     const size_t chunks = (cfg->ctx_max + ATT_CHUNK - 1) / ATT_CHUNK;
     const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64 +
-                              cfg->head_dim / 2;
+                              cfg->head_dim / 2 + H;
+    // MoE scratch (shared by the MoE layers, which run one after another) and
+    // each layer's routing of the last step (256-byte slots)
+    const size_t moe_route_bytes = 512;
+    const size_t moe_bytes = n_moe ? moe_need + n_moe * moe_route_bytes : 0;
     const size_t mem_bytes = act_floats * 4;
     if (rc == SOSO_HIP_OK) {
-        if (hipMalloc(&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, mem_bytes) != hipSuccess)
+        if (hipMalloc(&m.kcache, 2 * kv_bytes) != hipSuccess || hipMalloc(&m.mem, mem_bytes) != hipSuccess ||
+            (moe_bytes && hipMalloc(&m.moe_mem, moe_bytes) != hipSuccess))
             rc = set_err(h, SOSO_HIP_DECLINED, "decode_create: no memory for the KV cache");
     }
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemsetAsync(m.kcache, 0, 2 * kv_bytes, h->stream), "kv zero");
@@ -901,6 +955,16 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     m.part = m.act + F;
     m.logits = m.part + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2);
     m.rope_freq = m.logits + cfg->vocab + 64;
+    m.xn = m.rope_freq + cfg->head_dim / 2;
+    for (size_t l = 0, j = 0; l < L; l++) {
+        DecodeLayer &dl = m.layers[l];
+        if (!dl.moe) continue;
+        const MoeLayer &ml = *dl.moe;
+        moe_scratch_fixed(h, 1, ml.n_exp, ml.top_k, ml.hdim, ml.ffn, m.moe_mem, moe_need, dl.moe_s);
+        char *r = (char *)m.moe_mem + moe_need + j++ * moe_route_bytes; // top_k <= 8: 32 + 32 bytes
+        dl.moe_s.idx = (int32_t *)r;
+        dl.moe_s.wgt = (float *)(r + 256);
+    }
     {
         // rope_cabezas (gemm.rs:1468-1470): freq_i = powf(theta, -2 i / head_dim) in f32
         std::vector<float> fr(cfg->head_dim / 2);
@@ -925,7 +989,36 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
     }
     if (drop_sources)
         for (size_t l = 0; l < L; l++)
-            for (size_t j : {1, 2, 3, 6, 7}) soso_hip_weight_drop(h, keys[9 * l + j], key_lens[9 * l + j]);
+            for (size_t j : {1, 2, 3, 6, 7})
+                if (!(j >= 6 && dm.layers[l].moe)) soso_hip_weight_drop(h, keys[9 * l + j], key_lens[9 * l + j]);
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
+                           const char *const *keys, const size_t *key_lens, int drop_sources)
+{
+    return decode_create_impl(h, model_key, model_key_len, cfg, keys, key_lens, nullptr, nullptr, drop_sources);
+}
+
+int soso_hip_decode_create_moe(soso_hip *h, const char *model_key, size_t model_key_len,
+                               const soso_hip_decode_cfg *cfg, const char *const *keys, const size_t *key_lens,
+                               const char *const *moe_layer_keys, const size_t *moe_layer_key_lens, int drop_sources)
+{
+    if (h && (!moe_layer_keys || !moe_layer_key_lens)) return set_err(h, SOSO_HIP_ERR_ARG, "decode_create_moe: args");
+    return decode_create_impl(h, model_key, model_key_len, cfg, keys, key_lens, moe_layer_keys, moe_layer_key_lens,
+                              drop_sources);
+}
+
+int soso_hip_decode_moe_routing_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer,
+                                    int32_t **idx_dev, float **wgt_dev)
+{
+    if (!h || !model_key || !idx_dev || !wgt_dev) return SOSO_HIP_ERR_ARG;
+    auto it = h->decode_models.find(std::string(model_key, model_key_len));
+    if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_moe_routing: no such model");
+    if (layer >= it->second.n_layers || !it->second.layers[layer].moe)
+        return set_err(h, SOSO_HIP_ERR_ARG, "decode_moe_routing: not an MoE layer");
+    *idx_dev = it->second.layers[layer].moe_s.idx;
+    *wgt_dev = it->second.layers[layer].moe_s.wgt;
     return SOSO_HIP_OK;
 }
 
@@ -1123,6 +1216,7 @@ int soso_hip_weight_drop(soso_hip *h, const char *key, size_t key_len)
         bool uses = m->second.router == &it->second;
         for (const void *p : m->second.host_tab) uses = uses || (p && p == it->second.dev);
         if (uses) {
+            rc = first_fail(rc, drop_models_using_moe(h, m->first));
             rc = first_fail(rc, moe_free(h, m->second));
             m = h->moe_layers.erase(m);
         } else {

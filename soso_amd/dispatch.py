@@ -280,17 +280,37 @@ class HipGpu:
                         f"moe_ffn_dev_noalloc {layer_key}")
 
     # -- dense decode step resident on the device (decode_preparar / decode_token) --
-    def decode_create(self, model_key, cfg, keys, drop_sources=False):
+    def decode_create(self, model_key, cfg, keys, drop_sources=False, moe_layers=None):
         """cfg: dict of soso_hip_decode_cfg fields; keys: 9 per layer (attn_norm,
-        q, k, v, o, ffn_norm, gate, up, down), then output_norm and head."""
+        q, k, v, o, ffn_norm, gate, up, down), then output_norm and head.
+        moe_layers: per layer, the key of a registered MoE layer that is its
+        FFN, or None (soso_hip_decode_create_moe); an MoE layer's gate, up and
+        down keys may be None."""
         mk, ml = _key(model_key)
         c = abi.DecodeCfg(**cfg)
-        enc = [k.encode() for k in keys]
+        enc = [k.encode() if k is not None else None for k in keys]
         arr = (C.c_char_p * len(enc))(*enc)
-        lens = (C.c_size_t * len(enc))(*[len(k) for k in enc])
-        return self._rc(self.lib.soso_hip_decode_create(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
-                                                        C.cast(lens, C.c_void_p), 1 if drop_sources else 0),
-                        f"decode_create {model_key}")
+        lens = (C.c_size_t * len(enc))(*[len(k) if k is not None else 0 for k in enc])
+        drop = 1 if drop_sources else 0
+        if moe_layers is None:
+            return self._rc(self.lib.soso_hip_decode_create(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
+                                                            C.cast(lens, C.c_void_p), drop),
+                            f"decode_create {model_key}")
+        menc = [k.encode() if k is not None else None for k in moe_layers]
+        marr = (C.c_char_p * len(menc))(*menc)
+        mlens = (C.c_size_t * len(menc))(*[len(k) if k is not None else 0 for k in menc])
+        return self._rc(self.lib.soso_hip_decode_create_moe(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
+                                                            C.cast(lens, C.c_void_p), C.cast(marr, C.c_void_p),
+                                                            C.cast(mlens, C.c_void_p), drop),
+                        f"decode_create_moe {model_key}")
+
+    def decode_moe_routing(self, model_key, layer, top_k):
+        """The routing of MoE layer `layer` in the model's last step: (indices, weights)."""
+        mk, ml = _key(model_key)
+        i, w = C.c_void_p(), C.c_void_p()
+        self._rc(self.lib.soso_hip_decode_moe_routing_dev(self.h, mk, ml, layer, C.byref(i), C.byref(w)),
+                 "decode_moe_routing")
+        return self.d2h(i.value, (top_k,), np.int32), self.d2h(w.value, (top_k,), np.float32)
 
     def decode_kv_dev(self, model_key, layer):
         mk, ml = _key(model_key)

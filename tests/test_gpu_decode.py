@@ -119,13 +119,17 @@ class Model:
         self.keys = keys
         return keys
 
-    def cpu_step(self, orc, x, kcache, vcache, pos, theta, eps, kv_f16=False):
-        """The dense layer stack on the CPU; kcache/vcache [L][ctx][kvd] get row pos
-        (rounded through soso's f16 when kv_f16, as KvCache::append stores it)."""
+    def cpu_step(self, orc, x, kcache, vcache, pos, theta, eps, kv_f16=False, moe=None):
+        """The layer stack on the CPU; kcache/vcache [L][ctx][kvd] get row pos
+        (rounded through soso's f16 when kv_f16, as KvCache::append stores it).
+        moe: {layer: MoeFfn} -- those layers' FFN is the MoE FFN (forward_moe_ffn,
+        layer.rs:1938-1975: rmsnorm, or_moe_ffn, residual); their routing is
+        kept in self.routing[layer]."""
         L_ = orc.lib()
         h = x.astype(np.float32).copy()
         new_k, new_v = [], []
         self.last_kv = (new_k, new_v)  # the f32 rows appended at pos, per layer
+        self.routing = {}
         for l, lw in enumerate(self.layers):
             xn = h.copy()
             L_.or_rmsnorm(xn.ctypes.data, lw["attn_norm"].ctypes.data, self.H, np.float32(eps))
@@ -153,6 +157,11 @@ class Model:
             h = h + orc.matvec(d("o"), lw["o"], self.H, self.qd, att)
             xn = h.copy()
             L_.or_rmsnorm(xn.ctypes.data, lw["ffn_norm"].ctypes.data, self.H, np.float32(eps))
+            if moe and l in moe:
+                out, idx, w = moe[l].cpu(orc, xn)
+                self.routing[l] = (idx, w)
+                h = h + out
+                continue
             gt = orc.matvec(d("gate"), lw["gate"], self.F, self.H, xn)
             up = orc.matvec(d("up"), lw["up"], self.F, self.H, xn)
             L_.or_swiglu(up.ctypes.data, gt.ctypes.data, self.F)
@@ -548,3 +557,118 @@ def test_kv_upload_rounds_like_soso(gpu, orc):
         gpu.decode_destroy(name)
         for k in m.keys:
             gpu.weight_drop(k)
+
+
+class MoeFfn:
+    """A seeded MoE FFN for a decode layer: router f32 ~ N(0, 0.02), experts
+    N(0, 0.05) through the reference quantizers (Q4_K), like the dense model's
+    weights, so a stack of layers keeps its scale."""
+
+    def __init__(self, orc, n_exp, h, ffn, top_k, seed):
+        self.n_exp, self.h, self.ffn, self.top_k = n_exp, h, ffn, top_k
+        self.router = orc.normal(n_exp * h, 0.02, seed, 1)
+        self.gate = [quant(orc, Q4K, orc.normal(ffn * h, 0.05, seed, 100 + e)) for e in range(n_exp)]
+        self.up = [quant(orc, Q4K, orc.normal(ffn * h, 0.05, seed, 1000 + e)) for e in range(n_exp)]
+        self.down = [quant(orc, Q4K, orc.normal(h * ffn, 0.05, seed, 2000 + e)) for e in range(n_exp)]
+        self.name = f"decmoe{seed}.{n_exp}.{h}.{ffn}.{top_k}"
+
+    def cpu(self, orc, x):
+        return orc.moe_ffn(self.router, self.n_exp, self.h, self.ffn, self.top_k, self.gate, self.up, self.down,
+                           Q4K, Q4K, x)
+
+    def upload(self, gpu):
+        def put(key, arr, dtype, rows, cols):
+            b = np.ascontiguousarray(arr).view(np.uint8)
+            d = gpu.dev_alloc(b.size)
+            try:
+                gpu.h2d(d, b)
+                gpu.weight_from_dev(key, d, b.size, dtype, rows, cols)
+            finally:
+                gpu.dev_free(d)
+        keys = []
+        for e in range(self.n_exp):
+            for nm, w, r, c in (("gate", self.gate[e], self.ffn, self.h), ("up", self.up[e], self.ffn, self.h),
+                                ("down", self.down[e], self.h, self.ffn)):
+                k = f"{self.name}.E{e}.{nm}"
+                put(k, w, Q4K, r, c)
+                keys.append(k)
+        put(self.name + ".router", self.router, F32, self.n_exp, self.h)
+        self.keys = keys
+        self.register(gpu)
+
+    def register(self, gpu):
+        gpu.moe_register(self.name, self.name + ".router", self.keys, self.n_exp, self.h, self.ffn, self.top_k)
+
+
+@pytest.mark.parametrize("kv_f16", [0, 1])
+def test_decode_step_with_moe_layers_matches_cpu(gpu, orc, kv_f16):
+    """A GQA model whose layers 1 and 2 take registered MoE layers as their FFN
+    (soso_hip_decode_create_moe; GpuDispatch::moe_capa for one token): one
+    step at position 150 against the oracle's composition (the dense layer,
+    then rmsnorm + or_moe_ffn + residual for the MoE layers): logits within
+    1e-5, the greedy token, and each MoE layer's routing -- indices identical
+    in ranking order, weights within 1e-5.  Layer 1's unused gate/up/down keys
+    are passed as null.  Re-registering an MoE layer the model reads destroys
+    the model."""
+    L, H, nh, nkv, F, V, prefill = 3, 1024, 8, 2, 2048, 1000, 150
+    theta, eps, ctx = 500000.0, 1e-5, 256
+    m = Model(orc, L, H, nh, nkv, F, V, 80 + 10 * kv_f16)
+    m.upload(gpu)
+    moe = {1: MoeFfn(orc, 16, H, 512, 4, 81 + 10 * kv_f16), 2: MoeFfn(orc, 24, H, 256, 8, 82 + 10 * kv_f16)}
+    for f in moe.values():
+        f.upload(gpu)
+    keys = list(m.keys)
+    for j in (6, 7, 8):
+        keys[9 * 1 + j] = None
+    name = m.name + f".moe{kv_f16}"
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=theta, rms_eps=eps, kv_f16=kv_f16)
+    assert gpu.decode_create(name, cfg, keys, moe_layers=[None, moe[1].name, moe[2].name]), gpu.last_error()
+    kc = np.zeros((L, ctx, m.kvd), np.float32)
+    vc = np.zeros((L, ctx, m.kvd), np.float32)
+    for l in range(L):
+        kr = orc.normal(prefill * m.kvd, 1.0, 90 + l, 1).reshape(prefill, m.kvd)
+        vr = orc.normal(prefill * m.kvd, 1.0, 90 + l, 2).reshape(prefill, m.kvd)
+        gpu.decode_kv_upload(name, l, 0, kr, vr, rows_f32=True)
+        if kv_f16:
+            kr, vr = orc.f16_to_f32(orc.f32_to_f16(kr)).reshape(kr.shape), orc.f16_to_f32(orc.f32_to_f16(vr)).reshape(
+                vr.shape)
+        kc[l, :prefill] = kr
+        vc[l, :prefill] = vr
+    x = orc.normal(H, 1.0, 95, 1)
+    xd, ld, td = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(4)
+    try:
+        gpu.h2d(xd, x)
+        gpu.decode_step_dev(name, xd, prefill, ld, td)
+        gpu.sync()
+        logits = gpu.d2h(ld, (V,), np.float32)
+        token = int(gpu.d2h(td, (1,), np.uint32)[0])
+        ref, ref_tok = m.cpu_step(orc, x, kc, vc, prefill, theta, eps, kv_f16=bool(kv_f16), moe=moe)
+        err = orc.rel_l2(logits, ref)
+        print(f"decode with MoE layers kv_f16={kv_f16}: logits rel_l2 {err:.3e}", flush=True)
+        assert err < 1e-5, err
+        check_greedy(orc, token, logits, ref_tok, ref)
+        for l, f in moe.items():
+            idx, w = gpu.decode_moe_routing(name, l, f.top_k)
+            ri, rw = m.routing[l]
+            assert np.array_equal(idx, ri), (l, idx, ri)
+            assert orc.rel_l2(w, rw) < 1e-5, (l, w, rw)
+        # the same step replayed from a graph (after restoring the KV rows it
+        # wrote) gives the same bits
+        gpu.graph_begin()
+        gpu.decode_step_dev(name, xd, prefill, ld, td)
+        gid = gpu.graph_end()
+        try:
+            for _ in range(2):
+                gpu.graph_launch(gid)
+                gpu.sync()
+                again = gpu.d2h(ld, (V,), np.float32)
+                assert np.array_equal(again.view(np.uint32), logits.view(np.uint32))
+        finally:
+            gpu.graph_destroy(gid)
+        # re-registering an MoE layer the model reads unregisters the model
+        moe[2].register(gpu)
+        assert not gpu.decode_step_dev(name, xd, prefill, ld, td)
+    finally:
+        for p in (xd, ld, td):
+            gpu.dev_free(p)
