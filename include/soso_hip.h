@@ -60,6 +60,14 @@ typedef struct soso_hip_stats {
     uint64_t weight_bytes_resident;
     uint64_t weights_resident;
     uint64_t weights_declined;
+    /* the per-token transfers of soso_hip_decode_token (GpuStats::decode_*,
+     * gpu.rs:23-29): embedding rows up, control words up (none: the position
+     * travels as a kernel argument), logits and KV rows down, steps */
+    uint64_t decode_embed_up;
+    uint64_t decode_control_up;
+    uint64_t decode_logits_down;
+    uint64_t decode_kv_down;
+    uint64_t decode_steps;
 } soso_hip_stats_t;
 
 /* MatvecOp (gpu.rs:189-196) for soso_hip_matvec_batch. */
@@ -145,7 +153,12 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
  * matrix-core path reads when a call routes two or more tokens per active
  * expert; it is skipped, and that path reads the resident weights, when the
  * budget has no room.  Dropping any of the layer's weights unregisters it and
- * frees the copy. */
+ * frees the copy.
+ * expert_keys = NULL registers the router alone: a layer whose experts stay
+ * on the host (soso's layers whose experts are not on the card, computed by
+ * decode_token's cpu_moe callback).  Such a layer serves as an FFN of
+ * soso_hip_decode_create_moe models run through soso_hip_decode_token; the
+ * MoE FFN entry points decline it. */
 int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_len, const char *router_key,
                           size_t router_key_len, const char *const *expert_keys, const size_t *expert_key_lens,
                           size_t n_exp, size_t hdim, size_t ffn, size_t top_k);
@@ -246,6 +259,25 @@ int soso_hip_decode_kv_upload(soso_hip *h, const char *model_key, size_t model_k
  * allocates nothing, so it may be captured in a graph. */
 int soso_hip_decode_step_dev(soso_hip *h, const char *model_key, size_t model_key_len, const float *x_dev, uint32_t pos,
                              float *logits_dev, uint32_t *token_dev, void *kv_rows_dev);
+/* cpu_moe of decode_token (gpu.rs:674-679): for MoE layer `layer` whose
+ * experts stay on the host, out[hidden] = the ranking-order weighted sum of
+ * the chosen experts' SwiGLU FFNs of xn[hidden] (= rmsnorm(h) * ffn_norm),
+ * experts idx[top_k] with weights wgt[top_k] as the device routed them.
+ * Returns 0, or nonzero on failure. */
+typedef int (*soso_hip_cpu_moe_fn)(void *ctx, uint32_t layer, const float *xn, const int32_t *idx, const float *wgt,
+                                   size_t top_k, float *out);
+/* GpuDispatch::decode_token (gpu.rs:670-685) on host buffers: embed (hidden
+ * f32) up, one step at `pos`, then logits (vocab f32, when non-null), the new
+ * KV rows (soso_hip_decode_step_dev's kv_rows layout, when non-null) and the
+ * greedy token (when non-null) down; synchronous.  A layer whose FFN was
+ * registered without experts stops the step after its routing: xn and the
+ * routing go down, cpu_moe(cpu_moe_ctx, ...) computes the FFN, its output
+ * comes up and is added to the hidden state, and the step goes on.  Models
+ * with such layers run only here (soso_hip_decode_step_dev declines them), and
+ * need cpu_moe.  Counts the transfers in the decode_* stats. */
+int soso_hip_decode_token(soso_hip *h, const char *model_key, size_t model_key_len, const float *embed, uint32_t pos,
+                          soso_hip_cpu_moe_fn cpu_moe, void *cpu_moe_ctx, float *logits, void *kv_rows,
+                          uint32_t *token);
 int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key_len);
 
 /* ---- device-resident API (no host copies; for the decode step, benchmarks

@@ -26,7 +26,13 @@ class HipError(RuntimeError):
 class Stats(C.Structure):
     _fields_ = [(n, C.c_uint64) for n in (
         "launches", "total_ns", "bytes_up", "bytes_down",
-        "weight_bytes_resident", "weights_resident", "weights_declined")]
+        "weight_bytes_resident", "weights_resident", "weights_declined",
+        "decode_embed_up", "decode_control_up", "decode_logits_down", "decode_kv_down", "decode_steps")]
+
+
+# soso_hip_cpu_moe_fn: (ctx, layer, xn, idx, wgt, top_k, out) -> 0 on success
+CpuMoeFn = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint32, C.POINTER(C.c_float), C.POINTER(C.c_int32),
+                       C.POINTER(C.c_float), C.c_size_t, C.POINTER(C.c_float))
 
 
 class Op(C.Structure):
@@ -82,6 +88,7 @@ PROTOTYPES = {
     "soso_hip_decode_kv_dev": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),
     "soso_hip_decode_kv_upload": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P, _I]),
     "soso_hip_decode_step_dev": (_I, [_P, C.c_char_p, _S, _P, C.c_uint32, _P, _P, _P]),
+    "soso_hip_decode_token": (_I, [_P, C.c_char_p, _S, _P, C.c_uint32, CpuMoeFn, _P, _P, _P, _P]),
     "soso_hip_decode_destroy": (_I, [_P, C.c_char_p, _S]),
     "soso_hip_dev_alloc": (_I, [_P, _S, C.POINTER(_P)]),
     "soso_hip_dev_free": (_I, [_P, _P]),

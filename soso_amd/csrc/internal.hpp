@@ -102,9 +102,22 @@ struct DecodeModel {
     float *rope_freq = nullptr; // head_dim / 2 floats
     float *xn = nullptr;        // the MoE layers' normalized x (hidden floats)
     void *moe_mem = nullptr;    // the MoE layers' scratch and routing
+    size_t n_host_moe = 0;      // MoE layers whose experts stay on the host (router only)
+};
+
+// decode_token's cpu_moe: what the step calls for a layer whose experts stay
+// on the host (soso_hip_decode_token)
+struct HostMoe {
+    soso_hip_cpu_moe_fn fn = nullptr;
+    void *ctx = nullptr;
 };
 
 constexpr size_t SOSO_TICKET_BYTES = 16384;
+// (token, rank) slots one route launch sorts in LDS; larger MoE calls run in
+// blocks of at most MOE_ROUTE_MAX_SLOTS / top_k tokens (a token's routing and
+// expert work do not depend on the other tokens of the call)
+constexpr int MOE_ROUTE_MAX_SLOTS = 4096;
+inline size_t moe_block_tokens(size_t top_k) { return top_k ? (size_t)MOE_ROUTE_MAX_SLOTS / top_k : 1; }
 
 struct soso_hip {
     int device = 0;
@@ -200,8 +213,12 @@ int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
 constexpr int ATT_CHUNK = 64; // positions per split of the decode attention (a multiple of 16)
 int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, bool kv_f16, int n_heads,
                      int n_kv_heads, int head_dim, int ctx, int T, float *part, float *out);
+// host: the callback for layers whose experts stay on the host (those layers
+// decline without one)
 int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token,
-                void *kv_rows);
+                void *kv_rows, const HostMoe *host = nullptr);
+// y[i] += v[i] (i < n)
+int launch_vec_add(soso_hip *h, float *y, const float *v, size_t n);
 // Scatter n_rows position-major rows [n_rows][kv_dim] (f32 when src_f32, else
 // the cache's element type) into a head-major cache at positions row0...
 int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, bool cache_f16, int kv_dim,

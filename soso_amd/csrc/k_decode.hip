@@ -356,11 +356,50 @@ int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, b
     return hip_check(h, hipGetLastError(), "kv scatter launch");
 }
 
+__global__ void __launch_bounds__(256) k_vec_add(float *__restrict__ y, const float *__restrict__ v, int n)
+{
+    const int i = (int)(blockIdx.x * 256 + threadIdx.x);
+    if (i < n) y[i] += v[i];
+}
+
+int launch_vec_add(soso_hip *h, float *y, const float *v, size_t n)
+{
+    if (n == 0) return SOSO_HIP_OK;
+    k_vec_add<<<(unsigned)((n + 255) / 256), 256, 0, h->stream>>>(y, v, (int)n);
+    return hip_check(h, hipGetLastError(), "vec add launch");
+}
+
+// A layer whose experts stay on the host (decode_token's cpu_moe, gpu.rs:674-679):
+// xn and the routing the device computed go down, the callback's weighted sum
+// of the chosen experts comes up into xn's buffer and joins the residual.
+static int host_moe_ffn(soso_hip *h, DecodeModel &m, size_t layer, const MoeLayer &ml, const MoeScratch &s,
+                        const HostMoe &host)
+{
+    const size_t H = m.hidden, k = ml.top_k;
+    char *st = (char *)pinned_get(h, (2 * H + 2 * k) * 4);
+    if (!st) return set_err(h, SOSO_HIP_ERR_NOMEM, "decode_token: pinned staging");
+    float *xn = (float *)st, *out = xn + H;
+    int32_t *idx = (int32_t *)(out + H);
+    float *wgt = (float *)(idx + k);
+    int rc = hip_check(h, hipMemcpyAsync(xn, m.xn, H * 4, hipMemcpyDeviceToHost, h->stream), "xn down");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(idx, s.idx, k * 4, hipMemcpyDeviceToHost, h->stream), "idx");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(wgt, s.wgt, k * 4, hipMemcpyDeviceToHost, h->stream), "wgt");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "host moe sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    if (host.fn(host.ctx, (uint32_t)layer, xn, idx, wgt, k, out) != 0)
+        return set_err(h, SOSO_HIP_ERR_ARG, "decode_token: cpu_moe failed at layer " + std::to_string(layer));
+    h->stats.bytes_down += (H + 2 * k) * 4;
+    h->stats.bytes_up += H * 4;
+    rc = hip_check(h, hipMemcpyAsync(m.xn, out, H * 4, hipMemcpyHostToDevice, h->stream), "moe out up");
+    if (rc == SOSO_HIP_OK) rc = launch_vec_add(h, m.hid, m.xn, H);
+    return rc;
+}
+
 // ---------------------------------------------------------------------------
 // The decode step
 // ---------------------------------------------------------------------------
 int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token,
-                void *kv_rows)
+                void *kv_rows, const HostMoe *host)
 {
     const int q_dim = (int)(m.n_heads * m.head_dim), kv_dim = (int)(m.n_kv_heads * m.head_dim);
     if (pos >= m.ctx_max) return set_err(h, SOSO_HIP_ERR_ARG, "decode: position beyond the KV capacity");
@@ -402,7 +441,16 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
             r.res = hin;
             rc = launch_matvec_ex(h, *L.o, a, hid, r, XS_PLAIN, EPI_RESID);
         }
-        if (L.moe) {
+        if (L.moe && !L.moe->tab) {
+            // experts on the host: routing here, the FFN by the caller's cpu_moe
+            if (!host || !host->fn)
+                return set_err(h, SOSO_HIP_DECLINED, "decode: a layer's experts stay on the host (decode_token)");
+            const MoeLayer &ml = *L.moe;
+            if (rc == SOSO_HIP_OK) rc = launch_rmsnorm(h, hid, L.ffn_norm, m.hidden, m.eps, m.xn);
+            if (rc == SOSO_HIP_OK)
+                rc = launch_moe_route(h, (const float *)ml.router->dev, m.xn, 1, ml.hdim, ml.n_exp, ml.top_k, L.moe_s);
+            if (rc == SOSO_HIP_OK) rc = host_moe_ffn(h, m, l, ml, L.moe_s, *host);
+        } else if (L.moe) {
             // MoE FFN (forward_moe_ffn, layer.rs:1938-1975): x = rmsnorm(h) * ffn_norm,
             // router + top-k, the chosen experts, h += their ranking-order sum
             if (rc == SOSO_HIP_OK) rc = launch_rmsnorm(h, hid, L.ffn_norm, m.hidden, m.eps, m.xn);

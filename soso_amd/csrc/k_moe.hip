@@ -96,7 +96,7 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
 // an equal share of tokens x rows): items[4i .. 4i+3] = {expert, its slot
 // count, its first slot in `list`, chunk j | chunks << 16} for i < *n_items,
 // experts ascending.
-constexpr int ROUTE_MAX_SLOTS = 4096; // n * top_k handled by the LDS sort
+constexpr int ROUTE_MAX_SLOTS = MOE_ROUTE_MAX_SLOTS; // n * top_k handled by the LDS sort
 constexpr int ROUTE_TT = 4;           // tokens per wavefront (and per ranking workgroup) from 2 tokens
 constexpr int ROUTE_T1 = 2048;        // first per-token-block counter in the ticket buffer
 constexpr int MOE_SELF_K = 8;         // top_k of the self-ranked single-token path

@@ -479,17 +479,23 @@ int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const flo
         }
         h->f32_tensors[k] = wd;
     }
+    // blocks of at most moe_block_tokens(top_k) tokens per route launch, each
+    // block's routing copied out before the next overwrites the scratch
+    const size_t nb = std::min(n, moe_block_tokens(top_k));
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
     MoeScratch ms;
-    if (!xd || !moe_scratch(h, n, n_exp, top_k, 0, 0, ms)) return set_err(h, SOSO_HIP_ERR_NOMEM, "router: scratch");
-    int32_t *id = ms.idx;
-    float *pd = ms.wgt;
+    if (!xd || !moe_scratch(h, nb, n_exp, top_k, 0, 0, ms)) return set_err(h, SOSO_HIP_ERR_NOMEM, "router: scratch");
     rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
-    if (rc == SOSO_HIP_OK) rc = launch_moe_route(h, (const float *)wd, xd, n, hdim, n_exp, top_k, ms);
-    if (rc == SOSO_HIP_OK)
-        rc = hip_check(h, hipMemcpyAsync(idx, id, n * top_k * 4, hipMemcpyDeviceToHost, h->stream), "idx");
-    if (rc == SOSO_HIP_OK)
-        rc = hip_check(h, hipMemcpyAsync(wgt, pd, n * top_k * 4, hipMemcpyDeviceToHost, h->stream), "wgt");
+    for (size_t t0 = 0; t0 < n && rc == SOSO_HIP_OK; t0 += nb) {
+        const size_t m = std::min(nb, n - t0);
+        rc = launch_moe_route(h, (const float *)wd, xd + t0 * hdim, m, hdim, n_exp, top_k, ms);
+        if (rc == SOSO_HIP_OK)
+            rc = hip_check(h, hipMemcpyAsync(idx + t0 * top_k, ms.idx, m * top_k * 4, hipMemcpyDeviceToHost, h->stream),
+                           "idx");
+        if (rc == SOSO_HIP_OK)
+            rc = hip_check(h, hipMemcpyAsync(wgt + t0 * top_k, ms.wgt, m * top_k * 4, hipMemcpyDeviceToHost, h->stream),
+                           "wgt");
+    }
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "router sync");
     if (rc != SOSO_HIP_OK) return rc;
     h->stats.bytes_up += n * hdim * 4;
@@ -636,7 +642,7 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
                           size_t n_exp, size_t hdim, size_t ffn, size_t top_k)
 {
     if (!h) return SOSO_HIP_ERR_ARG;
-    if (!layer_key || !router_key || !expert_keys || !expert_key_lens || n_exp == 0 || n_exp > 256 || top_k == 0 ||
+    if (!layer_key || !router_key || (expert_keys && !expert_key_lens) || n_exp == 0 || n_exp > 256 || top_k == 0 ||
         top_k > n_exp || top_k > 64 || hdim == 0 || hdim % 4 || ffn == 0)
         return set_err(h, SOSO_HIP_ERR_ARG, "moe_register: args");
     int rc = make_current(h);
@@ -649,6 +655,16 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
     m.hdim = hdim;
     m.ffn = ffn;
     m.top_k = top_k;
+    if (!expert_keys) { // the router alone: experts stay on the host (decode_token's cpu_moe)
+        std::string k(layer_key, layer_key_len);
+        auto it = h->moe_layers.find(k);
+        if (it != h->moe_layers.end()) {
+            rc = first_fail(drop_models_using_moe(h, k), moe_free(h, it->second));
+            h->moe_layers.erase(it);
+        }
+        h->moe_layers.emplace(k, m);
+        return rc;
+    }
     std::vector<const uint8_t *> tab(3 * n_exp);
     const size_t dims[3][2] = {{ffn, hdim}, {ffn, hdim}, {hdim, ffn}};
     for (size_t e = 0; e < n_exp; e++)
@@ -710,6 +726,35 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
     return rc;
 }
 
+// A registered layer over n tokens with its scratch in ms (sized for
+// min(n, moe_block_tokens(top_k)) tokens): one token takes the single-token
+// path; more run route + experts in blocks of moe_block_tokens(top_k).
+static int moe_ffn_run(soso_hip *h, const MoeLayer &m, const float *x_dev, size_t n, float *out_dev, int32_t *idx_dev,
+                       float *wgt_dev, const MoeScratch &ms)
+{
+    if (n == 1) {
+        MoeScratch s = ms;
+        if (idx_dev) s.idx = idx_dev;
+        if (wgt_dev) s.wgt = wgt_dev;
+        const int rc = launch_moe_ffn1(h, m, x_dev, s, out_dev);
+        if (rc != SOSO_HIP_DECLINED) return rc;
+    }
+    const size_t nb = moe_block_tokens(m.top_k);
+    int rc = SOSO_HIP_OK;
+    for (size_t t0 = 0; t0 < n && rc == SOSO_HIP_OK; t0 += nb) {
+        const size_t c = std::min(nb, n - t0);
+        MoeScratch s = ms;
+        if (idx_dev) s.idx = idx_dev + t0 * m.top_k;
+        if (wgt_dev) s.wgt = wgt_dev + t0 * m.top_k;
+        const float *xc = x_dev + t0 * m.hdim;
+        rc = launch_moe_route(h, (const float *)m.router->dev, xc, c, m.hdim, m.n_exp, m.top_k, s);
+        if (rc == SOSO_HIP_OK)
+            rc = launch_moe_experts(h, xc, c, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, s.wgt,
+                                    nullptr, s.idx, s, out_dev + t0 * m.hdim, &m);
+    }
+    return rc;
+}
+
 int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev, size_t n,
                          float *out_dev, int32_t *idx_dev, float *wgt_dev)
 {
@@ -718,25 +763,16 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
     auto it = h->moe_layers.find(std::string(layer_key, layer_key_len));
     if (it == h->moe_layers.end()) return set_err(h, SOSO_HIP_DECLINED, "moe_ffn_dev: layer not registered");
     const MoeLayer &m = it->second;
+    if (!m.tab) return set_err(h, SOSO_HIP_DECLINED, "moe_ffn_dev: the layer's experts stay on the host");
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
     MoeScratch ms;
-    if (!moe_scratch(h, n, m.n_exp, m.top_k, m.hdim, m.ffn, ms))
+    if (!moe_scratch(h, std::min(n, moe_block_tokens(m.top_k)), m.n_exp, m.top_k, m.hdim, m.ffn, ms))
         return h->capturing ? set_err(h, SOSO_HIP_DECLINED,
                                       "moe_ffn_dev: its scratch would have to grow inside graph capture (make one call "
                                       "with this token count outside capture first)")
                             : set_err(h, SOSO_HIP_ERR_NOMEM, "moe_ffn_dev: scratch");
-    if (idx_dev) ms.idx = idx_dev;
-    if (wgt_dev) ms.wgt = wgt_dev;
-    if (n == 1) {
-        rc = launch_moe_ffn1(h, m, x_dev, ms, out_dev);
-        if (rc != SOSO_HIP_DECLINED) return rc;
-    }
-    rc = launch_moe_route(h, (const float *)m.router->dev, x_dev, n, m.hdim, m.n_exp, m.top_k, ms);
-    if (rc == SOSO_HIP_OK)
-        rc = launch_moe_experts(h, x_dev, n, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, ms.wgt,
-                                nullptr, ms.idx, ms, out_dev, &m);
-    return rc;
+    return moe_ffn_run(h, m, x_dev, n, out_dev, idx_dev, wgt_dev, ms);
 }
 
 // The allocation-free form of soso_hip_moe_ffn_dev: the same kernels, with
@@ -749,26 +785,17 @@ int soso_hip_moe_ffn_dev_noalloc(soso_hip *h, const char *layer_key, size_t laye
     auto it = h->moe_layers.find(std::string(layer_key, layer_key_len));
     if (it == h->moe_layers.end()) return set_err(h, SOSO_HIP_DECLINED, "moe_ffn_dev_noalloc: layer not registered");
     const MoeLayer &m = it->second;
+    if (!m.tab) return set_err(h, SOSO_HIP_DECLINED, "moe_ffn_dev_noalloc: the layer's experts stay on the host");
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
     MoeScratch ms;
-    const size_t need = moe_scratch_fixed(h, n, m.n_exp, m.top_k, m.hdim, m.ffn, h->fixed_scratch,
-                                          SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES, ms);
+    const size_t need = moe_scratch_fixed(h, std::min(n, moe_block_tokens(m.top_k)), m.n_exp, m.top_k, m.hdim, m.ffn,
+                                          h->fixed_scratch, SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES, ms);
     if (need > SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES)
         return set_err(h, SOSO_HIP_ERR_ARG, "moe_ffn_dev_noalloc: " + std::to_string(n) + " tokens need " +
                                                 std::to_string(need) + " bytes of scratch; the fixed array holds " +
                                                 std::to_string((size_t)SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES));
-    if (idx_dev) ms.idx = idx_dev;
-    if (wgt_dev) ms.wgt = wgt_dev;
-    if (n == 1) {
-        rc = launch_moe_ffn1(h, m, x_dev, ms, out_dev);
-        if (rc != SOSO_HIP_DECLINED) return rc;
-    }
-    rc = launch_moe_route(h, (const float *)m.router->dev, x_dev, n, m.hdim, m.n_exp, m.top_k, ms);
-    if (rc == SOSO_HIP_OK)
-        rc = launch_moe_experts(h, x_dev, n, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, ms.wgt,
-                                nullptr, ms.idx, ms, out_dev, &m);
-    return rc;
+    return moe_ffn_run(h, m, x_dev, n, out_dev, idx_dev, wgt_dev, ms);
 }
 
 // ---- dense decode step -------------------------------------------------------
@@ -829,7 +856,9 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
             if (ml.hdim != H)
                 return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) +
                                                          ": the MoE layer's width is not hidden");
-            if (const char *why = moe_ffn1_unsupported(h, ml))
+            // a layer registered without experts runs them on the host (decode_token's cpu_moe)
+            if (!ml.tab) m.n_host_moe++;
+            else if (const char *why = moe_ffn1_unsupported(h, ml))
                 return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + " MoE: " + why);
             if (H > 8192) return set_err(h, SOSO_HIP_DECLINED, "decode_create: MoE layers take hidden <= 8192");
             m.layers[l].moe = &ml;
@@ -1080,7 +1109,53 @@ int soso_hip_decode_step_dev(soso_hip *h, const char *model_key, size_t model_ke
     if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_step: model not registered");
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
+    if (it->second.n_host_moe)
+        return set_err(h, SOSO_HIP_DECLINED,
+                       "decode_step: the model has MoE layers whose experts stay on the host (soso_hip_decode_token)");
     return decode_step(h, it->second, x_dev, pos, logits_dev, token_dev, kv_rows_dev);
+}
+
+int soso_hip_decode_token(soso_hip *h, const char *model_key, size_t model_key_len, const float *embed, uint32_t pos,
+                          soso_hip_cpu_moe_fn cpu_moe, void *cpu_moe_ctx, float *logits, void *kv_rows,
+                          uint32_t *token)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!model_key || !embed) return set_err(h, SOSO_HIP_ERR_ARG, "decode_token: args");
+    if (h->capturing) return set_err(h, SOSO_HIP_DECLINED, "decode_token: synchronous, not inside graph capture");
+    auto it = h->decode_models.find(std::string(model_key, model_key_len));
+    if (it == h->decode_models.end()) return set_err(h, SOSO_HIP_DECLINED, "decode_token: model not registered");
+    DecodeModel &m = it->second;
+    if (m.n_host_moe && !cpu_moe)
+        return set_err(h, SOSO_HIP_DECLINED, "decode_token: the model's host-side experts need cpu_moe");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    const size_t H = m.hidden, esz = m.kv_f16 ? 2 : 4;
+    const size_t kv_bytes = m.n_layers * 2 * m.n_kv_heads * m.head_dim * esz;
+    // device staging: the step's KV rows, then its token
+    char *dev = (char *)scratch_get(h, 6, kv_bytes + 256);
+    if (!dev) return set_err(h, SOSO_HIP_ERR_NOMEM, "decode_token: staging");
+    uint32_t *tok_dev = (uint32_t *)(dev + ((kv_bytes + 255) & ~(size_t)255));
+    // the embedding row becomes the hidden state (layer 0 reads it in place)
+    rc = hip_check(h, hipMemcpyAsync(m.hid, embed, H * 4, hipMemcpyHostToDevice, h->stream), "embed upload");
+    HostMoe hm;
+    hm.fn = cpu_moe;
+    hm.ctx = cpu_moe_ctx;
+    if (rc == SOSO_HIP_OK) rc = decode_step(h, m, m.hid, pos, nullptr, tok_dev, kv_rows ? dev : nullptr, &hm);
+    if (rc == SOSO_HIP_OK && logits)
+        rc = hip_check(h, hipMemcpyAsync(logits, m.logits, m.vocab * 4, hipMemcpyDeviceToHost, h->stream), "logits");
+    if (rc == SOSO_HIP_OK && kv_rows)
+        rc = hip_check(h, hipMemcpyAsync(kv_rows, dev, kv_bytes, hipMemcpyDeviceToHost, h->stream), "kv rows");
+    if (rc == SOSO_HIP_OK && token)
+        rc = hip_check(h, hipMemcpyAsync(token, tok_dev, 4, hipMemcpyDeviceToHost, h->stream), "token");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "decode_token sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    h->stats.decode_embed_up += H * 4;
+    h->stats.decode_logits_down += logits ? m.vocab * 4 : 0;
+    h->stats.decode_kv_down += kv_rows ? kv_bytes : 0;
+    h->stats.decode_steps++;
+    clk.done();
+    return SOSO_HIP_OK;
 }
 
 int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key_len)

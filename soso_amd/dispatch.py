@@ -39,6 +39,7 @@ class HipGpu:
         if rc != 0:
             raise abi.HipError(f"soso_hip_create({device}) failed: {rc}")
         self.h = h
+        self._decode_cfg = {}  # model key -> the cfg it was created with (decode_token's buffer sizes)
 
     # -- lifetime ------------------------------------------------------------
     def close(self):
@@ -258,14 +259,18 @@ class HipGpu:
 
     # -- MoE FFN resident on the device (the FFN half of GpuDispatch::moe_capa) --
     def moe_register(self, layer_key, router_key, expert_keys, n_exp, hdim, ffn, top_k):
-        """expert_keys: 3*n_exp names (gate_e, up_e, down_e for e = 0..n_exp-1)."""
+        """expert_keys: 3*n_exp names (gate_e, up_e, down_e for e = 0..n_exp-1),
+        or None: the router alone, the experts staying on the host (a decode
+        model's cpu_moe layer)."""
         lk, ll = _key(layer_key)
         rk, rl = _key(router_key)
-        enc = [k.encode() for k in expert_keys]
-        arr = (C.c_char_p * len(enc))(*enc)
-        lens = (C.c_size_t * len(enc))(*[len(k) for k in enc])
-        return self._rc(self.lib.soso_hip_moe_register(self.h, lk, ll, rk, rl, C.cast(arr, C.c_void_p),
-                                                       C.cast(lens, C.c_void_p), n_exp, hdim, ffn, top_k),
+        if expert_keys is None:
+            arr = lens = None
+        else:
+            enc = [k.encode() for k in expert_keys]
+            arr = C.cast((C.c_char_p * len(enc))(*enc), C.c_void_p)
+            lens = C.cast((C.c_size_t * len(enc))(*[len(k) for k in enc]), C.c_void_p)
+        return self._rc(self.lib.soso_hip_moe_register(self.h, lk, ll, rk, rl, arr, lens, n_exp, hdim, ffn, top_k),
                         f"moe_register {layer_key}")
 
     def moe_ffn_dev(self, layer_key, x_dev, n, out_dev, idx_dev=None, wgt_dev=None):
@@ -293,16 +298,20 @@ class HipGpu:
         lens = (C.c_size_t * len(enc))(*[len(k) if k is not None else 0 for k in enc])
         drop = 1 if drop_sources else 0
         if moe_layers is None:
-            return self._rc(self.lib.soso_hip_decode_create(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
-                                                            C.cast(lens, C.c_void_p), drop),
-                            f"decode_create {model_key}")
-        menc = [k.encode() if k is not None else None for k in moe_layers]
-        marr = (C.c_char_p * len(menc))(*menc)
-        mlens = (C.c_size_t * len(menc))(*[len(k) if k is not None else 0 for k in menc])
-        return self._rc(self.lib.soso_hip_decode_create_moe(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
-                                                            C.cast(lens, C.c_void_p), C.cast(marr, C.c_void_p),
-                                                            C.cast(mlens, C.c_void_p), drop),
-                        f"decode_create_moe {model_key}")
+            ok = self._rc(self.lib.soso_hip_decode_create(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
+                                                          C.cast(lens, C.c_void_p), drop),
+                          f"decode_create {model_key}")
+        else:
+            menc = [k.encode() if k is not None else None for k in moe_layers]
+            marr = (C.c_char_p * len(menc))(*menc)
+            mlens = (C.c_size_t * len(menc))(*[len(k) if k is not None else 0 for k in menc])
+            ok = self._rc(self.lib.soso_hip_decode_create_moe(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
+                                                              C.cast(lens, C.c_void_p), C.cast(marr, C.c_void_p),
+                                                              C.cast(mlens, C.c_void_p), drop),
+                          f"decode_create_moe {model_key}")
+        if ok:
+            self._decode_cfg[model_key] = dict(cfg)
+        return ok
 
     def decode_moe_routing(self, model_key, layer, top_k):
         """The routing of MoE layer `layer` in the model's last step: (indices, weights)."""
@@ -339,6 +348,42 @@ class HipGpu:
         mk, ml = _key(model_key)
         return self._rc(self.lib.soso_hip_decode_step_dev(self.h, mk, ml, x_dev, pos, logits_dev, token_dev,
                                                           kv_rows_dev), f"decode_step_dev {model_key}")
+
+    def decode_token(self, model_key, embed, pos, cpu_moe=None, logits=True, kv_rows=False):
+        """GpuDispatch::decode_token on host buffers (soso_hip_decode_token):
+        embed (hidden f32) -> (logits or None, greedy token, kv rows or None).
+        cpu_moe(layer, xn, idx, wgt) -> out (numpy f32, hidden) computes the
+        FFN of layers whose experts stay on the host."""
+        mk, ml = _key(model_key)
+        embed = np.ascontiguousarray(embed, np.float32)
+        cfg = self._decode_cfg[model_key]
+        lg = np.zeros(cfg["vocab"], np.float32) if logits else None
+        kv = None
+        if kv_rows:
+            n = cfg["n_layers"] * 2 * cfg["n_kv_heads"] * cfg["head_dim"]
+            kv = np.zeros(n, np.uint16 if cfg.get("kv_f16") else np.float32)
+        tok = np.zeros(1, np.uint32)
+        err = []
+
+        def trampoline(_ctx, layer, xn, idx, wgt, top_k, out):
+            try:
+                h = embed.size
+                res = cpu_moe(int(layer), np.ctypeslib.as_array(xn, (h,)).copy(),
+                              np.ctypeslib.as_array(idx, (top_k,)).copy(), np.ctypeslib.as_array(wgt, (top_k,)).copy())
+                np.ctypeslib.as_array(out, (h,))[:] = np.asarray(res, np.float32)
+                return 0
+            except Exception as e:  # noqa: BLE001 -- reported to the caller after the call
+                err.append(e)
+                return 1
+        cb = abi.CpuMoeFn(trampoline) if cpu_moe else abi.CpuMoeFn()
+        rc = self.lib.soso_hip_decode_token(self.h, mk, ml, embed.ctypes.data, pos, cb, None,
+                                            lg.ctypes.data if lg is not None else None,
+                                            kv.ctypes.data if kv is not None else None, tok.ctypes.data)
+        if err:
+            raise err[0]
+        if not self._rc(rc, f"decode_token {model_key}"):
+            return None
+        return lg, int(tok[0]), kv
 
     def decode_destroy(self, model_key):
         mk, ml = _key(model_key)

@@ -672,3 +672,106 @@ def test_decode_step_with_moe_layers_matches_cpu(gpu, orc, kv_f16):
     finally:
         for p in (xd, ld, td):
             gpu.dev_free(p)
+
+
+def test_decode_token_host_buffers_and_host_experts(gpu, orc):
+    """soso_hip_decode_token (GpuDispatch::decode_token, gpu.rs:670-685) on host
+    buffers.  A dense model: logits, token and KV rows bit-identical to
+    decode_step_dev at the same position, and the decode_* stats count the
+    embedding row up, the logits and the KV rows down and one step.  A model
+    whose layer 1 FFN is registered as its router alone (the experts stay on
+    the host): the device routes, cpu_moe computes the chosen experts on the
+    CPU (oracle matvecs and SwiGLU, summed in ranking order), the step goes
+    on; the routing handed to cpu_moe equals the device-resident MoE model's,
+    and the logits are within 1e-5 of that model's and of the oracle's
+    composition.  decode_step_dev declines the host-expert model, and a
+    failing cpu_moe fails decode_token with the callback's error."""
+    L, H, nh, nkv, F, V, pos = 3, 1024, 8, 2, 2048, 1000, 150
+    theta, eps, ctx = 500000.0, 1e-5, 256
+    m = Model(orc, L, H, nh, nkv, F, V, 160)
+    m.upload(gpu)
+    moe = MoeFfn(orc, 16, H, 512, 4, 161)
+    moe.upload(gpu)
+    host_key = moe.name + ".host"
+    assert gpu.moe_register(host_key, moe.name + ".router", None, moe.n_exp, H, moe.ffn, moe.top_k)
+    keys = list(m.keys)
+    for j in (6, 7, 8):
+        keys[9 * 1 + j] = None
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=theta, rms_eps=eps, kv_f16=0)
+    names = {"dense": m.name + ".tok.dense", "dev": m.name + ".tok.devmoe", "host": m.name + ".tok.hostmoe"}
+    assert gpu.decode_create(names["dense"], cfg, m.keys), gpu.last_error()
+    assert gpu.decode_create(names["dev"], cfg, keys, moe_layers=[None, moe.name, None]), gpu.last_error()
+    assert gpu.decode_create(names["host"], cfg, keys, moe_layers=[None, host_key, None]), gpu.last_error()
+    kc = np.zeros((L, ctx, m.kvd), np.float32)
+    vc = np.zeros((L, ctx, m.kvd), np.float32)
+    for l in range(L):
+        kr = orc.normal(pos * m.kvd, 1.0, 170 + l, 1).reshape(pos, m.kvd)
+        vr = orc.normal(pos * m.kvd, 1.0, 170 + l, 2).reshape(pos, m.kvd)
+        for name in names.values():
+            gpu.decode_kv_upload(name, l, 0, kr, vr, rows_f32=True)
+        kc[l, :pos], vc[l, :pos] = kr, vr
+    x = orc.normal(H, 1.0, 175, 1)
+    xd, ld, td, rd = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(4), gpu.dev_alloc(L * 2 * m.kvd * 4)
+    try:
+        gpu.h2d(xd, x)
+        # dense: the host entry against the device entry
+        gpu.decode_step_dev(names["dense"], xd, pos, ld, td, rd)
+        gpu.sync()
+        l_dev, t_dev = gpu.d2h(ld, (V,), np.float32), int(gpu.d2h(td, (1,), np.uint32)[0])
+        r_dev = gpu.d2h(rd, (L * 2 * m.kvd,), np.float32)
+        s0 = gpu.stats()
+        lg, tok, kv = gpu.decode_token(names["dense"], x, pos, logits=True, kv_rows=True)
+        s1 = gpu.stats()
+        assert np.array_equal(lg.view(np.uint32), l_dev.view(np.uint32)) and tok == t_dev
+        assert np.array_equal(kv.view(np.uint32), r_dev.view(np.uint32))
+        assert s1["decode_steps"] - s0["decode_steps"] == 1
+        assert s1["decode_embed_up"] - s0["decode_embed_up"] == H * 4
+        assert s1["decode_logits_down"] - s0["decode_logits_down"] == V * 4
+        assert s1["decode_kv_down"] - s0["decode_kv_down"] == L * 2 * m.kvd * 4
+        assert s1["decode_control_up"] == s0["decode_control_up"]
+        # MoE layer 1 with resident experts (the device path) ...
+        gpu.decode_step_dev(names["dev"], xd, pos, ld, td)
+        gpu.sync()
+        l_moe = gpu.d2h(ld, (V,), np.float32)
+        dev_idx, dev_w = gpu.decode_moe_routing(names["dev"], 1, moe.top_k)
+        # ... and with its experts on the host
+        calls = []
+
+        def cpu_moe(layer, xn, idx, wgt):
+            calls.append((layer, idx, wgt))
+            out = np.zeros(H, np.float32)
+            for j in range(moe.top_k):
+                e = int(idx[j])
+                g = orc.matvec(Q4K, moe.gate[e], moe.ffn, H, xn)
+                u = orc.matvec(Q4K, moe.up[e], moe.ffn, H, xn)
+                orc.lib().or_swiglu(u.ctypes.data, g.ctypes.data, moe.ffn)
+                out = out + np.float32(wgt[j]) * orc.matvec(Q4K, moe.down[e], H, moe.ffn, u)
+            return out
+        lh, th, _ = gpu.decode_token(names["host"], x, pos, cpu_moe=cpu_moe)
+        assert len(calls) == 1 and calls[0][0] == 1
+        assert np.array_equal(calls[0][1], dev_idx), (calls[0][1], dev_idx)
+        assert orc.rel_l2(calls[0][2], dev_w) < 1e-5
+        err = orc.rel_l2(lh, l_moe)
+        ref, ref_tok = m.cpu_step(orc, x, kc, vc, pos, theta, eps, moe={1: moe})
+        print(f"decode_token host experts: vs device experts {err:.3e}, vs oracle {orc.rel_l2(lh, ref):.3e}",
+              flush=True)
+        assert err < 1e-5 and orc.rel_l2(lh, ref) < 1e-5
+        check_greedy(orc, th, lh, ref_tok, ref)
+        # the device-only entries decline it; a failing callback fails the call
+        assert not gpu.decode_step_dev(names["host"], xd, pos, ld, td)
+        assert not gpu.moe_ffn_dev(host_key, xd, 1, rd)
+
+        def broken(layer, xn, idx, wgt):
+            raise RuntimeError("host experts unavailable")
+        with pytest.raises(RuntimeError, match="host experts unavailable"):
+            gpu.decode_token(names["host"], x, pos, cpu_moe=broken)
+        # ... and so does a host-expert model called without one
+        assert gpu.decode_token(names["host"], x, pos) is None
+    finally:
+        for p in (xd, ld, td, rd):
+            gpu.dev_free(p)
+        for name in names.values():
+            gpu.decode_destroy(name)
+        for k in m.keys + moe.keys + [moe.name + ".router"]:
+            gpu.weight_drop(k)

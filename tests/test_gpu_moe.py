@@ -96,6 +96,23 @@ def test_router_topk_matches_cpu(gpu, orc, n_exp, h, top_k, n):
         assert abs(float(np.sum(wgt[t * top_k:(t + 1) * top_k], dtype=np.float64)) - 1.0) < 1e-5
 
 
+def test_router_topk_beyond_one_route_launch(gpu, orc):
+    """600 tokens at top-8 (4800 slots) run as two route launches of at most
+    4096 slots (the reference's router has no cap): every token's indices and
+    weights match the CPU, the block edge (tokens 511, 512) included."""
+    n_exp, h, top_k, n = 32, 256, 8, 600
+    w = orc.normal(n_exp * h, 0.05, 74, 1)
+    xs = orc.normal(n * h, 1.0, 75, 1)
+    idx = np.full(n * top_k, -1, np.int32)
+    wgt = np.zeros(n * top_k, np.float32)
+    assert gpu.router_topk("router.many", w, xs, n, h, n_exp, top_k, idx, wgt), gpu.last_error()
+    for t in range(n):
+        logits = orc.matvec(F32, w, n_exp, h, xs[t * h:(t + 1) * h])
+        ci, cw = orc.topk_softmax(logits, top_k)
+        assert np.array_equal(idx[t * top_k:(t + 1) * top_k], ci), t
+        assert orc.rel_l2(wgt[t * top_k:(t + 1) * top_k], cw) < TOL, t
+
+
 def test_router_ties_lowest_index_first(gpu, orc):
     """Equal logits: the stable descending sort keeps the lower index first."""
     n_exp, h, top_k = 64, 64, 6
@@ -141,6 +158,26 @@ def test_moe_ffn_dev_matches_cpu(gpu, orc, n_exp, h, ffn, top_k, n, dt_down):
         # a second call with the same inputs gives the same bits (no state left behind)
         out2, idx2, _ = moe_dev(gpu, layer, xs)
         assert np.array_equal(out2.view(np.uint32), out.view(np.uint32)) and np.array_equal(idx2, idx)
+    finally:
+        layer.drop(gpu)
+
+
+def test_moe_ffn_dev_beyond_one_route_launch(gpu, orc):
+    """600 tokens at top-8: the call runs as blocks of 512 tokens (4096 route
+    slots) and one of 88; tokens on both sides of the block edge and a sample
+    of the rest match the CPU (indices identical, weights and outputs within
+    1e-5)."""
+    n_exp, h, ffn, top_k, n = 16, 512, 256, 8, 600
+    layer = Layer(orc, n_exp, h, ffn, top_k, 47)
+    layer.upload(gpu)
+    try:
+        xs = orc.normal(n * h, 1.0, 76, 1)
+        out, idx, wgt = moe_dev(gpu, layer, xs)
+        for t in sorted(set(range(0, n, 23)) | {510, 511, 512, 513, n - 1}):
+            ref, ri, rw = layer.cpu(orc, xs[t * h:(t + 1) * h])
+            assert np.array_equal(idx[t], ri), (t, idx[t], ri)
+            assert orc.rel_l2(wgt[t], rw) < TOL, t
+            assert orc.rel_l2(out[t], ref) < TOL, (t, orc.rel_l2(out[t], ref))
     finally:
         layer.drop(gpu)
 
