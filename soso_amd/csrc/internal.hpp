@@ -249,12 +249,15 @@ int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size
                        size_t n_exp, size_t top_k, int32_t *idx_dev, float *wgt_dev, float *logits_dev);
 int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim, size_t n_exp,
                      size_t top_k, const MoeScratch &s);
-// One token through a registered MoE layer, the ranking done by the expert
-// kernel (DECLINED when the layer's shapes need the general path).
 // One token through a registered layer (route, gate/up + SwiGLU, down +
-// weighted sum), three launches; res: added to the output (may be out_dev).
+// weighted sum), three launches, the ranking done by the expert kernel
+// (DECLINED when the layer's shapes need the general path); res: added to the
+// output (may be out_dev); norm_w: x_dev is h and the FFN's input is
+// rmsnorm(h) * norm_w, folded into the route and gate/up staging (only where
+// moe_ffn1_norm_ok).
 int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x_dev, const MoeScratch &s, float *out_dev,
-                    const float *res = nullptr);
+                    const float *res = nullptr, const float *norm_w = nullptr, float eps = 0.0f);
+bool moe_ffn1_norm_ok(const MoeLayer &m);
 const char *moe_ffn1_unsupported(const soso_hip *h, const MoeLayer &m);
 // (k_decode.hip) out[n] = rmsnorm(x) * w (one workgroup)
 int launch_rmsnorm(soso_hip *h, const float *x, const float *w, size_t n, float eps, float *out);

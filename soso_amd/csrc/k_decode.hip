@@ -452,9 +452,15 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
             if (rc == SOSO_HIP_OK) rc = host_moe_ffn(h, m, l, ml, L.moe_s, *host);
         } else if (L.moe) {
             // MoE FFN (forward_moe_ffn, layer.rs:1938-1975): x = rmsnorm(h) * ffn_norm,
-            // router + top-k, the chosen experts, h += their ranking-order sum
-            if (rc == SOSO_HIP_OK) rc = launch_rmsnorm(h, hid, L.ffn_norm, m.hidden, m.eps, m.xn);
-            if (rc == SOSO_HIP_OK) rc = launch_moe_ffn1(h, *L.moe, m.xn, L.moe_s, hid, hid);
+            // router + top-k, the chosen experts, h += their ranking-order sum;
+            // the norm folded into the route's and the experts' x staging where
+            // the route holds the row in one step, else a launch of its own
+            if (moe_ffn1_norm_ok(*L.moe)) {
+                if (rc == SOSO_HIP_OK) rc = launch_moe_ffn1(h, *L.moe, hid, L.moe_s, hid, hid, L.ffn_norm, m.eps);
+            } else {
+                if (rc == SOSO_HIP_OK) rc = launch_rmsnorm(h, hid, L.ffn_norm, m.hidden, m.eps, m.xn);
+                if (rc == SOSO_HIP_OK) rc = launch_moe_ffn1(h, *L.moe, m.xn, L.moe_s, hid, hid);
+            }
         } else {
             if (rc == SOSO_HIP_OK) {
                 MvIn f;

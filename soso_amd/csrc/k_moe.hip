@@ -104,6 +104,9 @@ constexpr int MOE_SELF_K = 8;         // top_k of the self-ranked single-token p
 // TT tokens per wavefront; each lane requests Q float4 of the expert row (and
 // of every token's x) per step: TT = 1 (one token, the decode case) takes a
 // 2048-wide row in a single round trip.
+// norm_w (TT = 1, hdim <= 256 Q, so the row is one step): xs is h and the
+// row is rmsnorm(h) * norm_w (gemm.rs:93-100), each wavefront taking sum(h^2)
+// over the row it holds.
 template <int TT, int Q, bool LOGITS_ONLY = false>
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
@@ -111,7 +114,8 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
                                                     int *__restrict__ cnt, int *__restrict__ offs,
                                                     int *__restrict__ list, int *__restrict__ items,
                                                     int *__restrict__ n_items, int target, int *__restrict__ recs,
-                                                    int *__restrict__ n_recs, unsigned *__restrict__ ticket)
+                                                    int *__restrict__ n_recs, unsigned *__restrict__ ticket,
+                                                    const float *__restrict__ norm_w = nullptr, float eps = 0.0f)
 {
     __shared__ int last;
     __shared__ int pre_s[257];
@@ -132,7 +136,7 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) acc[tt] = 0.0f;
         for (int i0 = 0; i0 < nv; i0 += 64 * Q) {
-            float4 w[Q], v[TT][Q];
+            float4 w[Q], v[TT][Q], nw[Q];
 #pragma unroll
             for (int q = 0; q < Q; q++) {
                 const int i = i0 + 64 * q + lane;
@@ -140,6 +144,19 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
 #pragma unroll
                 for (int tt = 0; tt < TT; tt++)
                     v[tt][q] = i < nv && tt < tn ? x4[(size_t)tt * nv + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                if (TT == 1 && norm_w)
+                    nw[q] = i < nv ? ((const float4 *)norm_w)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            if constexpr (TT == 1) {
+                if (norm_w) {
+                    float ss = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < Q; q++) ss += sq4(v[0][q]);
+                    ss = seg_sum<64>(ss); // every lane holds the sum
+                    const float scale = 1.0f / sqrtf(ss / (float)hdim + eps);
+#pragma unroll
+                    for (int q = 0; q < Q; q++) v[0][q] = norm4(v[0][q], scale, nw[q]);
+                }
             }
 #pragma unroll
             for (int tt = 0; tt < TT; tt++)
@@ -432,6 +449,10 @@ struct MoeSelf {
     int n_exp = 0, top_k = 0, chunks = 0;
     int32_t *idx = nullptr;
     float *wgt = nullptr;
+    // when set, xs is h and the staged row is rmsnorm(h) * norm_w (the decode
+    // step's MoE layers; cols <= 4096, one staging round)
+    const float *norm_w = nullptr;
+    float eps = 0.0f;
 };
 
 template <int FMT, int LPR, int NMAT, int DEPTH, bool SELF = false>
@@ -461,6 +482,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
     __shared__ int32_t self_idx[MOE_SELF_K];
     __shared__ float self_wgt[MOE_SELF_K], self_sel[MOE_SELF_K];
     __shared__ __align__(16) uint32_t self_keys[256];
+    __shared__ float nrm_s[NW];
     int nit;
     if constexpr (SELF) {
         // The ranking of topk_regs, by the whole workgroup: wavefront 0 makes
@@ -473,15 +495,20 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
         // keep expert 0 with weight 0, as in topk_regs.
         // The one token's x row (every slot's row is row 0: xdiv = top_k) is
         // staged into LDS here, once; its loads are in flight with the logits'.
-        float4 xv0[MOE_XK], xv1[MOE_XK];
+        float4 xv0[MOE_XK], xv1[MOE_XK], nw0[MOE_XK], nw1[MOE_XK];
 #pragma unroll
         for (int k = 0; k < MOE_XK; k++) {
             const int f = k * 512 + (int)threadIdx.x;
-            xv0[k] = xv1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            xv0[k] = xv1[k] = nw0[k] = nw1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (f < nch) {
                 const float4 *x4 = (const float4 *)xs + 2 * f;
                 xv0[k] = x4[0];
                 xv1[k] = x4[1];
+                if (sr.norm_w) {
+                    const float4 *w4 = (const float4 *)sr.norm_w + 2 * f;
+                    nw0[k] = w4[0];
+                    nw1[k] = w4[1];
+                }
             }
         }
         if (wave == 0) {
@@ -498,6 +525,25 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
             if (lane < sr.top_k) {
                 self_idx[lane] = 0;
                 self_sel[lane] = 0.0f;
+            }
+        }
+        if (sr.norm_w) {
+            // RMSNorm of the row (zeros past its end add nothing): every
+            // workgroup takes sum(h^2) itself, as the matvec staging does
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < MOE_XK; k++) ss += sq4(xv0[k]) + sq4(xv1[k]);
+            ss = seg_sum<64>(ss);
+            if (lane == 0) nrm_s[wave] = ss;
+            __syncthreads();
+            float tot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NW; i++) tot += nrm_s[i];
+            const float scale = 1.0f / sqrtf(tot / (float)cols + sr.eps);
+#pragma unroll
+            for (int k = 0; k < MOE_XK; k++) {
+                xv0[k] = norm4(xv0[k], scale, nw0[k]);
+                xv1[k] = norm4(xv1[k], scale, nw1[k]);
             }
         }
         {
@@ -1041,9 +1087,14 @@ const char *moe_ffn1_unsupported(const soso_hip *h, const MoeLayer &m)
 }
 
 // res: added to the output after the ranking-order sum (may be out itself), or null.
-int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScratch &s, float *out, const float *res)
+// norm_w: x is h and the FFN's input is rmsnorm(h) * norm_w (moe_ffn1_norm_ok).
+bool moe_ffn1_norm_ok(const MoeLayer &m) { return m.hdim <= 2048; } // the route's one-step rows (Q = 8)
+
+int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScratch &s, float *out, const float *res,
+                    const float *norm_w, float eps)
 {
     if (moe_ffn1_unsupported(h, m)) return set_err(h, SOSO_HIP_DECLINED, "moe ffn1: shape for the general path");
+    if (norm_w && !moe_ffn1_norm_ok(m)) return set_err(h, SOSO_HIP_DECLINED, "moe ffn1: folded norm width");
     const size_t hdim = m.hdim, ffn = m.ffn, top_k = m.top_k, n_exp = m.n_exp;
     const int U = (int)(hdim / 64);
     const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
@@ -1054,7 +1105,7 @@ int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScr
     const int chunks = std::max(1, (moe_item_target(h) + (int)top_k / 2) / (int)top_k);
     k_moe_route<1, 8, true><<<dim3((unsigned)((n_exp + 7) / 8), 1u), 512, 0, h->stream>>>(
         (const float *)m.router->dev, x, 1, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt, s.cnt, s.offs,
-        s.list, s.items, s.n_items, moe_item_target(h), s.recs, s.n_recs, h->ticket);
+        s.list, s.items, s.n_items, moe_item_target(h), s.recs, s.n_recs, h->ticket, norm_w, eps);
     int rc = hip_check(h, hipGetLastError(), "moe ffn1 route launch");
     if (rc != SOSO_HIP_OK) return rc;
     MoeSelf sr;
@@ -1064,6 +1115,8 @@ int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScr
     sr.chunks = chunks;
     sr.idx = s.idx;
     sr.wgt = s.wgt;
+    sr.norm_w = norm_w;
+    sr.eps = eps;
     const unsigned grid = (unsigned)(top_k * chunks);
     const uint8_t *const *A = m.tab, *const *B = m.tab + n_exp;
     switch (m.dt_gu) {
