@@ -31,7 +31,6 @@
 #include <vector>
 
 constexpr int ATT_HD = 128;                // head_dim handled
-constexpr int ATT_NW = ATT_CHUNK / 16;     // wavefronts per split workgroup, 16 positions each
 
 // Split-K decode attention: k_attn_split writes one (m, l, acc) per chunk of
 // ATT_CHUNK positions and query head, k_attn_merge combines the chunks.  (The merge
@@ -39,44 +38,48 @@ constexpr int ATT_NW = ATT_CHUNK / 16;     // wavefronts per split workgroup, 16
 // same launch needs a device-scope fence per wavefront, which writes back the
 // XCD's L2 each time and cost more than the launch it saves.)
 //
-// k_attn_split: grid (n_kv_heads, chunks), block 64 * ATT_NW.  Query heads g*G ..
-// g*G + G - 1 share KV head g (GQA), so every K/V byte is read once for all G
-// heads.  K, V of one layer are head-major, [n_kv_heads][ctx][HD]: a chunk of
-// one head is 32 KB of contiguous HBM.  Wavefront w owns positions t0 + 16w ..
-// t0 + 16w + 15.
+// k_attn_split<G, F16, PW>: grid (n_kv_heads, chunks), block 64 * ATT_CHUNK /
+// PW.  Query heads g*G .. g*G + G - 1 share KV head g (GQA), so every K/V
+// byte is read once for all G heads.  K, V of one layer are head-major,
+// [n_kv_heads][ctx][HD]: a chunk of one head is 32 KB of contiguous HBM.
+// Wavefront w owns positions t0 + PW w .. t0 + PW w + PW - 1 (PW = 16 or 8:
+// fewer positions per wavefront put more wavefronts on the G heads' scores,
+// which each wavefront computes head after head).
 //
 // Load order per lane: its K rows, then q, then its V rows.  Loads complete in
 // issue order, so the scores start once K and q are in while V is still on
 // the way.  K: 8 lanes per position (128 B per lane group, whole cache lines),
-// two groups of 8 positions; V: lane holds dims 2l, 2l+1 of the 16 positions.
+// PW / 8 groups of 8 positions; V: lane holds dims 2l, 2l+1 of the PW positions.
 // Positions past T are clamped onto the last valid row and get weight 0.
 //
 // Scores s = (q . k) / sqrt(HD).  Each wavefront keeps its own softmax
 // statistics (m_w = max s, p = e^{s - m_w}, l_w = sum p, acc_w = sum p v);
-// the four are merged in LDS into the chunk's (m, l, acc), stored at
+// the wavefronts' are merged in LDS into the chunk's (m, l, acc), stored at
 // part[(head * chunks + c) * (HD + 2)].
-template <int G, bool F16>
-__global__ void __launch_bounds__(64 * ATT_NW) k_attn_split(const float *__restrict__ q, const void *__restrict__ Kc,
-                                                             const void *__restrict__ Vc, int ctx, int T, int chunks,
-                                                             float *__restrict__ part)
+template <int G, bool F16, int PW>
+__global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(const float *__restrict__ q,
+                                                                     const void *__restrict__ Kc,
+                                                                     const void *__restrict__ Vc, int ctx, int T,
+                                                                     int chunks, float *__restrict__ part)
 {
-    constexpr int HD = ATT_HD, NW = ATT_NW, NT = 64 * NW;
+    static_assert(PW == 8 || PW == 16, "8 or 16 positions per wavefront");
+    constexpr int HD = ATT_HD, NW = ATT_CHUNK / PW, NT = 64 * NW, KA = PW / 8;
     __shared__ float qs[G * HD];
     __shared__ float wm[NW][G], wl[NW][G];
     __shared__ float2 accs[NW][G][HD / 2];
     const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
     const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK);
     const int lane = tid & 63, wave = tid >> 6;
-    const int tw = t0 + 16 * wave;
+    const int tw = t0 + PW * wave;
     const size_t head_off = (size_t)g * ctx * HD;
     const int pp = lane >> 3, j = lane & 7;
     // K: f32 rows are 512 B, lane j of a position takes float4 units j, j+8,
     // j+16, j+24 (dims 32i + 4j ..); f16 rows are 256 B, lane j takes 16-byte
     // units j, j+8 (dims 64i + 8j .. 64i + 8j + 7)
-    float4 kv[2][4];
-    uint4 kh[2][2];
+    float4 kv[KA][4];
+    uint4 kh[KA][2];
 #pragma unroll
-    for (int a = 0; a < 2; a++) {
+    for (int a = 0; a < KA; a++) {
         const size_t row = head_off + (size_t)min(tw + 8 * a + pp, t1 - 1) * HD;
         if constexpr (F16) {
             const uint4 *k4 = (const uint4 *)((const uint16_t *)Kc + row);
@@ -97,11 +100,11 @@ __global__ void __launch_bounds__(64 * ATT_NW) k_attn_split(const float *__restr
         if (tid + r * NT < G * HD / 4) qv[r] = ((const float4 *)(q + (size_t)g * G * HD))[tid + r * NT];
     }
     __builtin_amdgcn_sched_barrier(0);
-    // V: lane l holds dims 2l, 2l + 1 of the wavefront's 16 positions
-    float2 vr[16];
-    uint32_t vh[16];
+    // V: lane l holds dims 2l, 2l + 1 of the wavefront's PW positions
+    float2 vr[PW];
+    uint32_t vh[PW];
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
+    for (int k = 0; k < PW; k++) {
         const size_t row = head_off + (size_t)min(tw + k, t1 - 1) * HD + 2 * lane;
         if constexpr (F16)
             vh[k] = *(const uint32_t *)((const uint16_t *)Vc + row);
@@ -115,7 +118,7 @@ __global__ void __launch_bounds__(64 * ATT_NW) k_attn_split(const float *__restr
     if constexpr (F16) {
         // f16 -> f32 is exact; from here on the math is the f32 kernel's
 #pragma unroll
-        for (int a = 0; a < 2; a++)
+        for (int a = 0; a < KA; a++)
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 const uint32_t w[4] = {kh[a][i].x, kh[a][i].y, kh[a][i].z, kh[a][i].w};
@@ -129,9 +132,9 @@ __global__ void __launch_bounds__(64 * ATT_NW) k_attn_split(const float *__restr
     const float inv = 1.0f / sqrtf((float)HD);
 #pragma unroll
     for (int hh = 0; hh < G; hh++) {
-        float s[2];
+        float s[KA];
 #pragma unroll
-        for (int a = 0; a < 2; a++) {
+        for (int a = 0; a < KA; a++) {
             float acc = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -146,14 +149,17 @@ __global__ void __launch_bounds__(64 * ATT_NW) k_attn_split(const float *__restr
             acc = seg_sum_dpp<8>(acc); // all 8 lanes of the position hold the sum
             s[a] = tw + 8 * a + pp < t1 ? acc * inv : -INFINITY;
         }
-        const float m = wave_max_dpp(fmaxf(s[0], s[1]));
-        float p[2];
+        float smax = s[0];
 #pragma unroll
-        for (int a = 0; a < 2; a++) p[a] = s[a] == -INFINITY ? 0.0f : expf(s[a] - m);
+        for (int a = 1; a < KA; a++) smax = fmaxf(smax, s[a]);
+        const float m = wave_max_dpp(smax);
+        float p[KA];
+#pragma unroll
+        for (int a = 0; a < KA; a++) p[a] = s[a] == -INFINITY ? 0.0f : expf(s[a] - m);
         float2 acc = make_float2(0.f, 0.f);
         float l = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
+        for (int k = 0; k < PW; k++) {
             const float pk = __builtin_bit_cast(
                 float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, p[k >> 3]), 8 * (k & 7)));
             l += pk;
@@ -258,6 +264,12 @@ __global__ void __launch_bounds__(256) k_attn_merge(const float *__restrict__ pa
     }
 }
 
+// Positions per wavefront of the split kernel.  Measured on MI355X (graph-
+// replayed steps at position 4096): f32 rows 8 (8B model, groups of 4: 1.686
+// against 1.721 ms per token with 16); f16 rows 16 (8B: 1.701 against 1.709 ms;
+// Qwen3-30B-A3B-like, groups of 8: 2.197 against 2.224 ms).
+template <bool F16> constexpr int att_pw() { return F16 ? 16 : 8; }
+
 int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, bool kv_f16, int n_heads,
                      int n_kv_heads, int head_dim, int ctx, int T, float *part, float *out)
 {
@@ -269,9 +281,11 @@ int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, 
 #define ATT_CASE(GG)                                                                                                \
     case GG:                                                                                                        \
         if (kv_f16)                                                                                                 \
-            k_attn_split<GG, true><<<grid, 64 * ATT_NW, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);             \
+            k_attn_split<GG, true, att_pw<true>()><<<grid, 64 * ATT_CHUNK / att_pw<true>(), 0, h->stream>>>(       \
+                q, K, V, ctx, T, chunks, part);                                                                     \
         else                                                                                                        \
-            k_attn_split<GG, false><<<grid, 64 * ATT_NW, 0, h->stream>>>(q, K, V, ctx, T, chunks, part);            \
+            k_attn_split<GG, false, att_pw<false>()><<<grid, 64 * ATT_CHUNK / att_pw<false>(), 0, h->stream>>>(    \
+                q, K, V, ctx, T, chunks, part);                                                                     \
         break;
     switch (G) {
         ATT_CASE(1) ATT_CASE(2) ATT_CASE(4) ATT_CASE(8)
