@@ -1092,20 +1092,26 @@ __global__ void __launch_bounds__(256) k_argmax(const float *__restrict__ x, int
         float v = sv[0];
         int i = si[0], q = sn[0];
         for (int w = 1; w < (nt >> 6); w++) keep_later(v, i, q, sv[w], si[w], sn[w]);
-        pv[blockIdx.x] = v;
-        pi[blockIdx.x] = i;
-        pn[blockIdx.x] = q;
-        __threadfence();
+        // the segment's winner leaves through agent-scope atomic stores (they
+        // reach the coherence point; no fence, so no write-back of the XCD's
+        // L2), acknowledged before the ticket; the last workgroup reads the
+        // winners with coherent loads
+        __hip_atomic_store(pv + blockIdx.x, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pi + blockIdx.x, i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pn + blockIdx.x, q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
         last = atomicAdd(ticket, 1u) == gridDim.x - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
     // the segments' winners, in segment order, reduced by the same ordered tree
     bv = -INFINITY;
     bi = -1;
     bn = 0;
-    for (int b = tid; b < (int)gridDim.x; b += nt) keep_later(bv, bi, bn, pv[b], pi[b], pn[b]);
+    for (int b = tid; b < (int)gridDim.x; b += nt)
+        keep_later(bv, bi, bn, __hip_atomic_load(pv + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                   __hip_atomic_load(pi + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                   __hip_atomic_load(pn + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     // thread t now holds segments t, t + nt, ...: with gridDim <= blockDim
     // that is one segment per thread, in order
     for (int o = 1; o < 64; o <<= 1) {

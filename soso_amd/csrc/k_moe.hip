@@ -77,7 +77,8 @@ __device__ void topk_regs(const float (&lg)[4], int n_exp, int top_k, int32_t *_
         for (int q = 0; q < 4; q++)
             if (k32 && lane + 64 * q == bi) key[q] = 0;
         if (lane == 0) {
-            idx[j] = bi;
+            // read by the workgroup that sorts the slots: a coherent store
+            __hip_atomic_store(idx + j, (int32_t)bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             sel[j] = bv;
             rank_lds[j] = (int16_t)bi;
         }
@@ -172,7 +173,12 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
 #pragma unroll
         for (int tt = 0; tt < TT; tt++) {
             const float sum = seg_sum_dpp<64>(acc[tt]); // lane 63 holds it
-            if (lane == 63 && tt < tn) logits[(size_t)(t0 + tt) * n_exp + e] = sum;
+            if (lane == 63 && tt < tn) {
+                float *dst = logits + (size_t)(t0 + tt) * n_exp + e;
+                // the ranking workgroup of this launch reads it: a coherent store
+                if constexpr (LOGITS_ONLY) *dst = sum;
+                else __hip_atomic_store(dst, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     if constexpr (LOGITS_ONLY) return; // the expert kernels rank the token themselves
@@ -181,16 +187,15 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
     // the last token block to be ranked (counter ticket[0]) sorts the slots.
     // With a single token block the ranking workgroup sorts straight away,
     // from the ranking it kept in LDS.
-    // One thread per workgroup fences: a device-scope fence writes back the
-    // L2 of its XCD, and the workgroup barrier before it orders every
-    // wavefront's stores ahead of it (fences are cumulative).
+    // What the next level reads (the logits, then the ranked experts) leaves
+    // through agent-scope atomic stores, which reach the device's coherence
+    // point; once every wavefront has them acknowledged (s_waitcnt, then the
+    // barrier), thread 0 takes the ticket, and the next level reads them with
+    // coherent loads.  No fence, so no write-back of the XCD's L2 (a
+    // device-scope fence per workgroup costs microseconds here).
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        __threadfence();
-        const bool l = atomicAdd(ticket + ROUTE_T1 + blockIdx.y, 1u) == gridDim.x - 1;
-        if (l) __threadfence();
-        last = l;
-    }
+    if (threadIdx.x == 0) last = atomicAdd(ticket + ROUTE_T1 + blockIdx.y, 1u) == gridDim.x - 1;
     __syncthreads();
     if (!last) return;
     if (wave < tn) {
@@ -199,21 +204,19 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             const int x = lane + 64 * q;
-            lg[q] = x < n_exp ? logits[(size_t)t * n_exp + x] : -INFINITY;
+            lg[q] = x < n_exp ? __hip_atomic_load(logits + (size_t)t * n_exp + x, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                              : -INFINITY;
         }
         topk_regs(lg, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k, sel[wave],
                   rank_s + wave * top_k);
     }
     const bool single = gridDim.y == 1;
+    __builtin_amdgcn_s_waitcnt(0); // the ranked experts acknowledged
     __syncthreads();
     if (threadIdx.x == 0) {
         ticket[ROUTE_T1 + blockIdx.y] = 0u;
-        if (!single) {
-            __threadfence();
-            const bool l = atomicAdd(ticket, 1u) == gridDim.y - 1;
-            if (l) __threadfence();
-            last = l;
-        }
+        if (!single) last = atomicAdd(ticket, 1u) == gridDim.y - 1;
     }
     __syncthreads();
     if (!last) return;
@@ -223,7 +226,10 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
     for (int x = threadIdx.x; x < n_exp; x += blockDim.x) c_s[x] = f_s[x] = 0;
     __syncthreads();
     for (int sl = threadIdx.x; sl < slots; sl += blockDim.x) {
-        const int x = min(max((int)(single ? rank_s[sl] : idx[sl]), 0), n_exp - 1);
+        const int x = min(max((int)(single ? rank_s[sl]
+                                           : __hip_atomic_load(idx + sl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
+                              0),
+                          n_exp - 1);
         e_s[sl] = (int16_t)x;
         atomicAdd(&c_s[x], 1);
     }
