@@ -223,7 +223,8 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
  * SwiGLU and down, h += their ranking-order sum -- and the dense FFN of
  * soso_hip_decode_create otherwise.  The keys array keeps its 9 entries per
  * layer; an MoE layer's gate, up and down entries are ignored (may be null
- * with length 0).  Attention is the dense step's (non-NeoX RoPE, no QK norm).
+ * with length 0).  Attention is the dense step's (non-NeoX RoPE, no QK norm;
+ * soso_hip_decode_create_ex takes those).
  * MoE layers take the single-token expert path: gate/up Q4_K, Q8_0 or Q6_K
  * with hidden a multiple of 128 up to 4096, down Q4_K with an expert width of
  * 256 to 2048 (a multiple of 256), top_k <= 8; others are declined here.
@@ -232,6 +233,23 @@ int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_
 int soso_hip_decode_create_moe(soso_hip *h, const char *model_key, size_t model_key_len,
                                const soso_hip_decode_cfg *cfg, const char *const *keys, const size_t *key_lens,
                                const char *const *moe_layer_keys, const size_t *moe_layer_key_lens, int drop_sources);
+/* The step for the Qwen-style attention variants soso's forward_layer takes
+ * (layer.rs:1164-1192, its FLAG_QK_NORM and FLAG_ROPE_NEOX): flags
+ * SOSO_HIP_DECODE_QK_NORM -- q and k are RMS-normalised per head before RoPE
+ * with the layer's attn_q_norm / attn_k_norm weights (F32 [head_dim]), given
+ * as two more keys per layer (11 per layer: the 9 of soso_hip_decode_create,
+ * then q_norm, k_norm; then output_norm and head); SOSO_HIP_DECODE_ROPE_NEOX
+ * -- RoPE turns the pairs (i, i + head_dim/2) (rope_cabezas with neox,
+ * gemm.rs:1474-1479) instead of (2i, 2i + 1).  moe_layer_keys as in
+ * soso_hip_decode_create_moe (null for a dense model).  With either flag the
+ * qkv projection stores its rows and one more launch per layer normalises,
+ * rotates and appends them.  flags 0 is soso_hip_decode_create(_moe). */
+#define SOSO_HIP_DECODE_QK_NORM 1u
+#define SOSO_HIP_DECODE_ROPE_NEOX 2u
+int soso_hip_decode_create_ex(soso_hip *h, const char *model_key, size_t model_key_len,
+                              const soso_hip_decode_cfg *cfg, uint32_t flags, const char *const *keys,
+                              const size_t *key_lens, const char *const *moe_layer_keys,
+                              const size_t *moe_layer_key_lens, int drop_sources);
 /* Device pointers of MoE layer `layer`'s routing in the last step: top_k
  * expert indices (int32) and weights (f32), in ranking order. */
 int soso_hip_decode_moe_routing_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer,

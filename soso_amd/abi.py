@@ -18,6 +18,9 @@ DTYPE_Q6_K = 13
 OK = 1
 DECLINED = 0
 
+DECODE_QK_NORM = 1    # SOSO_HIP_DECODE_QK_NORM
+DECODE_ROPE_NEOX = 2  # SOSO_HIP_DECODE_ROPE_NEOX
+
 
 class HipError(RuntimeError):
     pass
@@ -88,6 +91,7 @@ PROTOTYPES = {
     "soso_hip_decode_kv_dev": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),
     "soso_hip_decode_kv_upload": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.c_uint32, C.c_uint32, _P, _P, _I]),
     "soso_hip_decode_step_dev": (_I, [_P, C.c_char_p, _S, _P, C.c_uint32, _P, _P, _P]),
+    "soso_hip_decode_create_ex": (_I, [_P, C.c_char_p, _S, C.POINTER(DecodeCfg), C.c_uint32, _P, _P, _P, _P, C.c_int]),
     "soso_hip_decode_token": (_I, [_P, C.c_char_p, _S, _P, C.c_uint32, CpuMoeFn, _P, _P, _P, _P]),
     "soso_hip_decode_destroy": (_I, [_P, C.c_char_p, _S]),
     "soso_hip_dev_alloc": (_I, [_P, _S, C.POINTER(_P)]),

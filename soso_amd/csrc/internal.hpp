@@ -81,6 +81,7 @@ struct MoeScratch {
 struct DecodeLayer {
     const Weight *qkv = nullptr, *o = nullptr, *gu = nullptr, *down = nullptr;
     const float *attn_norm = nullptr, *ffn_norm = nullptr;
+    const float *q_norm = nullptr, *k_norm = nullptr; // QK norm weights (head_dim), or null
     // a registered MoE layer as the FFN (instead of gu / down), its scratch
     // (carved from the model's buffer; idx / wgt per layer: the last step's routing)
     const MoeLayer *moe = nullptr;
@@ -103,6 +104,10 @@ struct DecodeModel {
     float *xn = nullptr;        // the MoE layers' normalized x (hidden floats)
     void *moe_mem = nullptr;    // the MoE layers' scratch and routing
     size_t n_host_moe = 0;      // MoE layers whose experts stay on the host (router only)
+    // SOSO_HIP_DECODE_QK_NORM / ROPE_NEOX: the qkv rows go to qkv_raw and
+    // k_qkv_post normalises (per head), rotates and appends them
+    bool qk_norm = false, rope_neox = false;
+    float *qkv_raw = nullptr; // q_dim + 2 kv_dim floats
 };
 
 // decode_token's cpu_moe: what the step calls for a layer whose experts stay
@@ -219,6 +224,12 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
                 void *kv_rows, const HostMoe *host = nullptr);
 // y[i] += v[i] (i < n)
 int launch_vec_add(soso_hip *h, float *y, const float *v, size_t n);
+// The qkv rows of a step (raw: q_dim + 2 kv_dim floats) to q, the caches and
+// the rows copy: per head RMSNorm with qn / kn when non-null, RoPE (pairs
+// (i, i + head_dim / 2) when neox, else (2i, 2i + 1)) on q and k, then the
+// element stores of the fused qkv epilogue (ep: caches, pos, kv_f16, rows_out).
+int launch_qkv_post(soso_hip *h, const float *raw, const float *qn, const float *kn, float eps, bool neox,
+                    int n_heads, int n_kv_heads, const MvEpi &ep, float *q);
 // Scatter n_rows position-major rows [n_rows][kv_dim] (f32 when src_f32, else
 // the cache's element type) into a head-major cache at positions row0...
 int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, bool cache_f16, int kv_dim,

@@ -12,7 +12,8 @@
 // Launches per layer (every weight byte read once, activations stay in HBM):
 //   1. qkv matvec   x = rmsnorm(h) staged in LDS; rows [q; k; v] concatenated;
 //                   RoPE applied to q/k row pairs in the epilogue, k and v
-//                   written straight into the KV cache at `pos`
+//                   written straight into the KV cache at `pos` (with QK
+//                   norm or NeoX RoPE: the rows stored, then k_qkv_post)
 //   2. k_attn_split split-K decode attention over 64-position chunks, the
 //                   G query heads of a KV head share every K/V read
 //   3. k_attn_merge softmax-weighted merge of the chunks
@@ -298,6 +299,82 @@ int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, 
     return hip_check(h, hipGetLastError(), "attention merge launch");
 }
 
+// ---------------------------------------------------------------------------
+// QK norm and NeoX RoPE (layer.rs:1164-1192, FLAG_QK_NORM / FLAG_ROPE_NEOX):
+// the qkv projection stores its rows (q heads, then k heads, then v heads,
+// head_dim 128 each) and one wavefront per head finishes them.  Lane l holds
+// the head's elements l and l + 64 with NeoX RoPE (pair l of rope_cabezas'
+// neox branch, gemm.rs:1474-1479), 2l and 2l + 1 otherwise: either way the
+// lane's pair has frequency index l.  q and k heads are first RMS-normalised
+// with the layer's attn_q_norm / attn_k_norm (rmsnorm, gemm.rs:93-100:
+// x * scale * w with scale = 1 / sqrt(sum(x^2) / n + eps)), then rotated with
+// the arithmetic of the fused qkv epilogue; the stores are that epilogue's.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void post_put(const MvEpi &ep, void *cache, size_t at, int row_at, float v)
+{
+    if (ep.kv_f16) {
+        const uint16_t b = (uint16_t)f32_to_f16_soso(v);
+        ((uint16_t *)cache)[at] = b;
+        if (ep.rows_out) ((uint16_t *)ep.rows_out)[row_at] = b;
+    } else {
+        ((float *)cache)[at] = v;
+        if (ep.rows_out) ((float *)ep.rows_out)[row_at] = v;
+    }
+}
+
+__global__ void __launch_bounds__(256) k_qkv_post(const float *__restrict__ raw, const float *__restrict__ qn,
+                                                   const float *__restrict__ kn, float eps, int neox, int n_heads,
+                                                   int n_kv, MvEpi ep, float *__restrict__ q)
+{
+    constexpr int HD = ATT_HD;
+    const int lane = threadIdx.x & 63;
+    const int hd = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (hd >= n_heads + 2 * n_kv) return; // whole wavefronts
+    const int kind = hd < n_heads ? 0 : hd < n_heads + n_kv ? 1 : 2; // q, k, v
+    const int d0 = neox ? lane : 2 * lane, d1 = neox ? lane + 64 : 2 * lane + 1;
+    const float *src = raw + (size_t)hd * HD;
+    float a = src[d0], b = src[d1];
+    if (kind < 2) {
+        const float *w = kind == 0 ? qn : kn;
+        if (w) {
+            float ss = fmaf(a, a, b * b);
+            ss = __builtin_bit_cast(float,
+                                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, seg_sum_dpp<64>(ss)), 63));
+            const float scale = 1.0f / sqrtf(ss / (float)HD + eps);
+            a = __fmul_rn(__fmul_rn(a, scale), w[d0]);
+            b = __fmul_rn(__fmul_rn(b, scale), w[d1]);
+        }
+        const float fr = ep.rope_freq ? ep.rope_freq[lane] : powf(ep.theta, -2.0f * (float)lane / (float)HD);
+        float sn, cs;
+        sincosf((float)ep.pos * fr, &sn, &cs);
+        const float na = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
+        const float nb = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
+        a = na;
+        b = nb;
+    }
+    if (kind == 0) {
+        q[(size_t)hd * HD + d0] = a;
+        q[(size_t)hd * HD + d1] = b;
+    } else {
+        const int j = kind == 1 ? hd - n_heads : hd - n_heads - n_kv; // KV head
+        void *cache = kind == 1 ? ep.k_out : ep.v_out;
+        const size_t at = (size_t)j * ep.kv_stride + (size_t)ep.pos * HD;
+        const int row = (kind == 1 ? 0 : ep.kv_dim) + j * HD;
+        post_put(ep, cache, at + d0, row + d0, a);
+        post_put(ep, cache, at + d1, row + d1, b);
+    }
+}
+
+int launch_qkv_post(soso_hip *h, const float *raw, const float *qn, const float *kn, float eps, bool neox,
+                    int n_heads, int n_kv_heads, const MvEpi &ep, float *q)
+{
+    if (ep.head_dim != ATT_HD) return set_err(h, SOSO_HIP_DECLINED, "qkv post: head_dim");
+    const int heads = n_heads + 2 * n_kv_heads;
+    k_qkv_post<<<(unsigned)((heads + 3) / 4), 256, 0, h->stream>>>(raw, qn, kn, eps, neox ? 1 : 0, n_heads,
+                                                                    n_kv_heads, ep, q);
+    return hip_check(h, hipGetLastError(), "qkv post launch");
+}
+
 // rmsnorm (crates/soso-llm-core/src/gemm.rs:93-100) into a new vector: one
 // workgroup of 1024 threads, x loaded once into registers (n <= 8192),
 // out_i = (x_i * scale) * w_i with scale = 1 / sqrt(sum(x^2) / n + eps) --
@@ -444,7 +521,15 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         ep.pos = (int)pos;
         ep.theta = m.theta;
         ep.rope_freq = m.rope_freq;
-        rc = launch_matvec_ex(h, *L.qkv, in, qb, ep, XS_RMSNORM, EPI_QKV);
+        if (m.qk_norm || m.rope_neox) {
+            // the rows as computed, then per head: QK norm, RoPE, KV append
+            rc = launch_matvec_ex(h, *L.qkv, in, m.qkv_raw, MvEpi(), XS_RMSNORM, EPI_STORE);
+            if (rc == SOSO_HIP_OK)
+                rc = launch_qkv_post(h, m.qkv_raw, L.q_norm, L.k_norm, m.eps, m.rope_neox, (int)m.n_heads,
+                                     (int)m.n_kv_heads, ep, qb);
+        } else {
+            rc = launch_matvec_ex(h, *L.qkv, in, qb, ep, XS_RMSNORM, EPI_QKV);
+        }
         if (rc == SOSO_HIP_OK)
             rc = launch_attention(h, qb, K, V, m.kv_f16, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim,
                                   (int)m.ctx_max, (int)pos + 1, m.part, att);

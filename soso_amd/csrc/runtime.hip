@@ -803,8 +803,8 @@ int soso_hip_moe_ffn_dev_noalloc(soso_hip *h, const char *layer_key, size_t laye
 // dense model) names the registered MoE layer that is layer l's FFN, or null
 // for a dense FFN.
 static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
-                              const char *const *keys, const size_t *key_lens, const char *const *moe_keys,
-                              const size_t *moe_key_lens, int drop_sources)
+                              uint32_t flags, const char *const *keys, const size_t *key_lens,
+                              const char *const *moe_keys, const size_t *moe_key_lens, int drop_sources)
 {
     if (!h) return SOSO_HIP_ERR_ARG;
     if (!model_key || !cfg || !keys || !key_lens || cfg->n_layers == 0 || cfg->hidden == 0 || cfg->hidden % 4 ||
@@ -833,6 +833,12 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     m.theta = cfg->rope_theta;
     m.eps = cfg->rms_eps;
     m.kv_f16 = cfg->kv_f16 != 0;
+    if (flags & ~(SOSO_HIP_DECODE_QK_NORM | SOSO_HIP_DECODE_ROPE_NEOX))
+        return set_err(h, SOSO_HIP_ERR_ARG, "decode_create: unknown flags");
+    m.qk_norm = (flags & SOSO_HIP_DECODE_QK_NORM) != 0;
+    m.rope_neox = (flags & SOSO_HIP_DECODE_ROPE_NEOX) != 0;
+    const bool post = m.qk_norm || m.rope_neox; // the qkv rows finished by k_qkv_post
+    const size_t kpl = m.qk_norm ? 11 : 9;      // keys per layer
     auto get = [&](size_t i, size_t rows, size_t cols, bool f32, const Weight **out) -> bool {
         const Weight *w = find_weight(h, keys[i], key_lens[i]);
         if (!w || w->rows != rows || w->cols != cols || (f32 != (w->dtype == SOSO_HIP_DTYPE_F32))) return false;
@@ -843,8 +849,8 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     m.layers.resize(L);
     size_t moe_need = 0, n_moe = 0; // MoE scratch bytes (the largest layer's) and layers
     for (size_t l = 0; l < L; l++) {
-        const Weight *an, *fn;
-        const size_t b = 9 * l;
+        const Weight *an, *fn, *qn = nullptr, *kn = nullptr;
+        const size_t b = kpl * l;
         const bool is_moe = moe_keys && moe_keys[l];
         if (is_moe) {
             const std::string mk(moe_keys[l], moe_key_lens[l]);
@@ -875,6 +881,9 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
                          !get(b + 8, H, F, false, &m.layers[l].down))))
             return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) +
                                                      ": a weight is missing or has the wrong shape");
+        if (m.qk_norm && (!get(b + 9, 1, cfg->head_dim, true, &qn) || !get(b + 10, 1, cfg->head_dim, true, &kn)))
+            return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) +
+                                                     ": q_norm / k_norm missing or not F32 [head_dim]");
         if (q[l]->dtype != k[l]->dtype || q[l]->dtype != v[l]->dtype || (!is_moe && g[l]->dtype != u[l]->dtype))
             return set_err(h, SOSO_HIP_DECLINED, "decode_create: q/k/v or gate/up dtypes differ");
         // every launch of the step, checked here so that a step never declines
@@ -884,30 +893,35 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
             size_t rows, cols;
             int xs, epi;
             const char *role;
-        } roles[] = {{q[l], qd + 2 * kvd, H, XS_RMSNORM, EPI_QKV, "q/k/v"},
+        } roles[] = {{q[l], qd + 2 * kvd, H, XS_RMSNORM, post ? EPI_STORE : EPI_QKV, "q/k/v"},
                      {m.layers[l].o, H, qd, XS_PLAIN, EPI_RESID, "o"},
                      {g[l], 2 * F, H, XS_RMSNORM, EPI_SWIGLU, "gate/up"},
                      {m.layers[l].down, H, F, XS_PLAIN, EPI_RESID, "down"}};
         for (const auto &r : roles)
-            if (r.w && (!is_moe || r.epi == EPI_QKV || r.w == m.layers[l].o))
+            if (r.w && (!is_moe || r.w == q[l] || r.w == m.layers[l].o))
                 if (const char *why = matvec_ex_unsupported(h, r.w->dtype, r.rows, r.cols, r.xs, r.epi))
                 return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + " " + r.role + ": " +
                                                          why);
         m.layers[l].attn_norm = (const float *)an->dev;
         m.layers[l].ffn_norm = (const float *)fn->dev;
+        m.layers[l].q_norm = qn ? (const float *)qn->dev : nullptr;
+        m.layers[l].k_norm = kn ? (const float *)kn->dev : nullptr;
     }
     const Weight *on;
-    if (!get(9 * L, 1, H, true, &on) || !get(9 * L + 1, cfg->vocab, H, false, &m.head))
+    if (!get(kpl * L, 1, H, true, &on) || !get(kpl * L + 1, cfg->vocab, H, false, &m.head))
         return set_err(h, SOSO_HIP_DECLINED, "decode_create: output_norm/head missing or of the wrong shape");
     if (const char *why = matvec_ex_unsupported(h, m.head->dtype, cfg->vocab, H, XS_RMSNORM, EPI_STORE))
         return set_err(h, SOSO_HIP_DECLINED, std::string("decode_create: head: ") + why);
     m.out_norm = (const float *)on->dev;
     // what stays in use (dropping one of these unregisters the model)
-    for (size_t l = 0; l < L; l++)
+    for (size_t l = 0; l < L; l++) {
         for (size_t j : {0, 4, 5, 8})
-            if (!(j == 8 && m.layers[l].moe)) m.uses.emplace_back(keys[9 * l + j], key_lens[9 * l + j]);
-    m.uses.emplace_back(keys[9 * L], key_lens[9 * L]);
-    m.uses.emplace_back(keys[9 * L + 1], key_lens[9 * L + 1]);
+            if (!(j == 8 && m.layers[l].moe)) m.uses.emplace_back(keys[kpl * l + j], key_lens[kpl * l + j]);
+        if (m.qk_norm)
+            for (size_t j : {9, 10}) m.uses.emplace_back(keys[kpl * l + j], key_lens[kpl * l + j]);
+    }
+    m.uses.emplace_back(keys[kpl * L], key_lens[kpl * L]);
+    m.uses.emplace_back(keys[kpl * L + 1], key_lens[kpl * L + 1]);
     // fused copies
     m.owned.resize(2 * L);
     for (size_t l = 0; l < L && rc == SOSO_HIP_OK; l++) {
@@ -957,7 +971,7 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
     const size_t chunks = (cfg->ctx_max + ATT_CHUNK - 1) / ATT_CHUNK;
     const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64 +
-                              cfg->head_dim / 2 + H;
+                              cfg->head_dim / 2 + H + (post ? qd + 2 * kvd : 0);
     // MoE scratch (shared by the MoE layers, which run one after another) and
     // each layer's routing of the last step (256-byte slots)
     const size_t moe_route_bytes = 512;
@@ -985,6 +999,7 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     m.logits = m.part + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2);
     m.rope_freq = m.logits + cfg->vocab + 64;
     m.xn = m.rope_freq + cfg->head_dim / 2;
+    m.qkv_raw = post ? m.xn + H : nullptr;
     for (size_t l = 0, j = 0; l < L; l++) {
         DecodeLayer &dl = m.layers[l];
         if (!dl.moe) continue;
@@ -1019,14 +1034,14 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     if (drop_sources)
         for (size_t l = 0; l < L; l++)
             for (size_t j : {1, 2, 3, 6, 7})
-                if (!(j >= 6 && dm.layers[l].moe)) soso_hip_weight_drop(h, keys[9 * l + j], key_lens[9 * l + j]);
+                if (!(j >= 6 && dm.layers[l].moe)) soso_hip_weight_drop(h, keys[kpl * l + j], key_lens[kpl * l + j]);
     return SOSO_HIP_OK;
 }
 
 int soso_hip_decode_create(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
                            const char *const *keys, const size_t *key_lens, int drop_sources)
 {
-    return decode_create_impl(h, model_key, model_key_len, cfg, keys, key_lens, nullptr, nullptr, drop_sources);
+    return decode_create_impl(h, model_key, model_key_len, cfg, 0, keys, key_lens, nullptr, nullptr, drop_sources);
 }
 
 int soso_hip_decode_create_moe(soso_hip *h, const char *model_key, size_t model_key_len,
@@ -1034,8 +1049,18 @@ int soso_hip_decode_create_moe(soso_hip *h, const char *model_key, size_t model_
                                const char *const *moe_layer_keys, const size_t *moe_layer_key_lens, int drop_sources)
 {
     if (h && (!moe_layer_keys || !moe_layer_key_lens)) return set_err(h, SOSO_HIP_ERR_ARG, "decode_create_moe: args");
-    return decode_create_impl(h, model_key, model_key_len, cfg, keys, key_lens, moe_layer_keys, moe_layer_key_lens,
+    return decode_create_impl(h, model_key, model_key_len, cfg, 0, keys, key_lens, moe_layer_keys, moe_layer_key_lens,
                               drop_sources);
+}
+
+int soso_hip_decode_create_ex(soso_hip *h, const char *model_key, size_t model_key_len,
+                              const soso_hip_decode_cfg *cfg, uint32_t flags, const char *const *keys,
+                              const size_t *key_lens, const char *const *moe_layer_keys,
+                              const size_t *moe_layer_key_lens, int drop_sources)
+{
+    if (h && moe_layer_keys && !moe_layer_key_lens) return set_err(h, SOSO_HIP_ERR_ARG, "decode_create_ex: args");
+    return decode_create_impl(h, model_key, model_key_len, cfg, flags, keys, key_lens, moe_layer_keys,
+                              moe_layer_key_lens, drop_sources);
 }
 
 int soso_hip_decode_moe_routing_dev(soso_hip *h, const char *model_key, size_t model_key_len, uint32_t layer,

@@ -285,19 +285,32 @@ class HipGpu:
                         f"moe_ffn_dev_noalloc {layer_key}")
 
     # -- dense decode step resident on the device (decode_preparar / decode_token) --
-    def decode_create(self, model_key, cfg, keys, drop_sources=False, moe_layers=None):
+    def decode_create(self, model_key, cfg, keys, drop_sources=False, moe_layers=None, flags=0):
         """cfg: dict of soso_hip_decode_cfg fields; keys: 9 per layer (attn_norm,
         q, k, v, o, ffn_norm, gate, up, down), then output_norm and head.
         moe_layers: per layer, the key of a registered MoE layer that is its
         FFN, or None (soso_hip_decode_create_moe); an MoE layer's gate, up and
-        down keys may be None."""
+        down keys may be None.  flags: DECODE_QK_NORM (then 11 keys per layer,
+        q_norm and k_norm last) and DECODE_ROPE_NEOX (soso_hip_decode_create_ex)."""
         mk, ml = _key(model_key)
         c = abi.DecodeCfg(**cfg)
         enc = [k.encode() if k is not None else None for k in keys]
         arr = (C.c_char_p * len(enc))(*enc)
         lens = (C.c_size_t * len(enc))(*[len(k) if k is not None else 0 for k in enc])
         drop = 1 if drop_sources else 0
-        if moe_layers is None:
+        if flags:
+            marr = mlens = None  # the arrays stay referenced until the call returns
+            if moe_layers is not None:
+                menc = [k.encode() if k is not None else None for k in moe_layers]
+                marr = (C.c_char_p * len(menc))(*menc)
+                mlens = (C.c_size_t * len(menc))(*[len(k) if k is not None else 0 for k in menc])
+            ok = self._rc(self.lib.soso_hip_decode_create_ex(self.h, mk, ml, C.byref(c), flags,
+                                                             C.cast(arr, C.c_void_p), C.cast(lens, C.c_void_p),
+                                                             C.cast(marr, C.c_void_p) if marr is not None else None,
+                                                             C.cast(mlens, C.c_void_p) if mlens is not None else None,
+                                                             drop),
+                          f"decode_create_ex {model_key}")
+        elif moe_layers is None:
             ok = self._rc(self.lib.soso_hip_decode_create(self.h, mk, ml, C.byref(c), C.cast(arr, C.c_void_p),
                                                           C.cast(lens, C.c_void_p), drop),
                           f"decode_create {model_key}")

@@ -61,14 +61,17 @@ class Model:
     generator's blocks at a small scale."""
 
     ROLES = ("q", "k", "v", "o", "gate", "up", "down")
+    qk_norm = neox = False  # also for instances built without __init__
 
-    def __init__(self, orc, L, H, nh, nkv, F, V, seed, dt=None):
+    def __init__(self, orc, L, H, nh, nkv, F, V, seed, dt=None, qk_norm=False, neox=False):
         self.L, self.H, self.nh, self.nkv, self.F, self.V = L, H, nh, nkv, F, V
         self.qd, self.kvd = nh * HD, nkv * HD
+        self.qk_norm, self.neox = qk_norm, neox
         self.dt = {r: Q4K for r in self.ROLES}
         self.dt["head"] = Q8
         self.dt.update(dt or {})
         tag = "" if dt is None else "." + ".".join(f"{k}{v}" for k, v in sorted(dt.items()))
+        tag += (".qkn" if qk_norm else "") + (".neox" if neox else "")
         self.name = f"dec{seed}.{L}.{H}.{nh}.{nkv}.{F}.{V}{tag}"
         self.layers = []
         s = 0
@@ -86,6 +89,10 @@ class Model:
             for r in self.ROLES:
                 _, rows, cols = self.shapes(r)
                 lw[r] = mat(self.dt[r], rows, cols)
+            if qk_norm:
+                # attn_q_norm / attn_k_norm: F32 [head_dim]
+                lw["q_norm"] = (1.0 + orc.normal(HD, 0.1, seed, 5000 + 2 * l)).astype(np.float32)
+                lw["k_norm"] = (1.0 + orc.normal(HD, 0.1, seed, 5001 + 2 * l)).astype(np.float32)
             self.layers.append(lw)
         self.out_norm = (1.0 + orc.normal(H, 0.1, seed, 9000)).astype(np.float32)
         self.head_dtype = self.dt["head"]
@@ -95,7 +102,7 @@ class Model:
         H, F, qd, kvd = self.H, self.F, self.qd, self.kvd
         dt = getattr(self, "dt", None) or {}
         rc = {"q": (qd, H), "k": (kvd, H), "v": (kvd, H), "o": (H, qd), "gate": (F, H), "up": (F, H), "down": (H, F),
-              "attn_norm": (1, H), "ffn_norm": (1, H)}[name]
+              "attn_norm": (1, H), "ffn_norm": (1, H), "q_norm": (1, HD), "k_norm": (1, HD)}[name]
         return (F32 if name.endswith("norm") else dt.get(name, Q4K),) + rc
 
     def upload(self, gpu):
@@ -109,7 +116,8 @@ class Model:
                 gpu.dev_free(d)
         keys = []
         for l, lw in enumerate(self.layers):
-            for nm in ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down"):
+            for nm in ("attn_norm", "q", "k", "v", "o", "ffn_norm", "gate", "up", "down") + (
+                    ("q_norm", "k_norm") if self.qk_norm else ()):
                 k = f"{self.name}.L{l}.{nm}"
                 put(k, lw[nm], *self.shapes(nm))
                 keys.append(k)
@@ -138,8 +146,14 @@ class Model:
             q = orc.matvec(d("q"), lw["q"], self.qd, self.H, xn)
             k = orc.matvec(d("k"), lw["k"], self.kvd, self.H, xn)
             v = orc.matvec(d("v"), lw["v"], self.kvd, self.H, xn)
-            L_.or_rope_heads(q.ctypes.data, self.nh, HD, pos, np.float32(theta), 0)
-            L_.or_rope_heads(k.ctypes.data, self.nkv, HD, pos, np.float32(theta), 0)
+            if self.qk_norm:
+                # per head, before RoPE (layer.rs:1164-1180)
+                for vec, n, w in ((q, self.nh, lw["q_norm"]), (k, self.nkv, lw["k_norm"])):
+                    for hh in range(n):
+                        L_.or_rmsnorm(vec[hh * HD:].ctypes.data, w.ctypes.data, HD, np.float32(eps))
+            neox = 1 if self.neox else 0
+            L_.or_rope_heads(q.ctypes.data, self.nh, HD, pos, np.float32(theta), neox)
+            L_.or_rope_heads(k.ctypes.data, self.nkv, HD, pos, np.float32(theta), neox)
             kcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(k)) if kv_f16 else k
             vcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(v)) if kv_f16 else v
             new_k.append(k)
@@ -672,6 +686,115 @@ def test_decode_step_with_moe_layers_matches_cpu(gpu, orc, kv_f16):
     finally:
         for p in (xd, ld, td):
             gpu.dev_free(p)
+
+
+@pytest.mark.parametrize("qk_norm,neox,kv_f16,with_moe", [
+    (True, True, 0, False),    # Qwen3's attention: QK norm and NeoX RoPE
+    (True, True, 1, True),     # the same over soso's f16 cache, layer 1 an MoE layer
+    (True, False, 1, False),   # QK norm alone
+    (False, True, 0, False),   # NeoX RoPE alone
+])
+def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with_moe):
+    """soso_hip_decode_create_ex with SOSO_HIP_DECODE_QK_NORM (each q and k
+    head RMS-normalised with the layer's attn_q_norm / attn_k_norm before RoPE,
+    layer.rs:1164-1180) and SOSO_HIP_DECODE_ROPE_NEOX (rope_cabezas' NeoX
+    pairs (i, i + head_dim/2), gemm.rs:1474-1479).  Two steps (positions 90
+    and 91, the second reading the row the first wrote) against the oracle's
+    composition: logits within relative L2 1e-5, the greedy token, and the K/V
+    rows written at 90 under the bar of test_decode_step_matches_cpu."""
+    L, H, nh, nkv, F, V, prefill = 2, 1024, 8, 2, 2048, 1000, 90
+    theta, eps, ctx = 1000000.0, 1e-6, 128
+    flags = (1 if qk_norm else 0) | (2 if neox else 0)  # SOSO_HIP_DECODE_QK_NORM | _ROPE_NEOX
+    m = Model(orc, L, H, nh, nkv, F, V, 400 + flags + 4 * kv_f16, qk_norm=qk_norm, neox=neox)
+    m.upload(gpu)
+    kpl = 11 if qk_norm else 9
+    keys, moe, moe_layers = list(m.keys), None, None
+    if with_moe:
+        moe = {1: MoeFfn(orc, 16, H, 512, 4, 410)}
+        moe[1].upload(gpu)
+        for j in (6, 7, 8):
+            keys[kpl * 1 + j] = None
+        moe_layers = [None, moe[1].name]
+    name = m.name + ".model"
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=theta, rms_eps=eps, kv_f16=kv_f16)
+    print(f"decode step qk_norm={qk_norm} neox={neox} kv_f16={kv_f16} moe={with_moe}", flush=True)
+    assert gpu.decode_create(name, cfg, keys, moe_layers=moe_layers, flags=flags), gpu.last_error()
+    kvt, esz = (np.uint16, 2) if kv_f16 else (np.float32, 4)
+    kc = np.zeros((L, ctx, m.kvd), np.float32)
+    vc = np.zeros((L, ctx, m.kvd), np.float32)
+    xd, ld, td, rd = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(4), gpu.dev_alloc(L * 2 * m.kvd * esz)
+    try:
+        for l in range(L):
+            kr = orc.normal(prefill * m.kvd, 1.0, 420 + l, 1).reshape(prefill, m.kvd)
+            vr = orc.normal(prefill * m.kvd, 1.0, 420 + l, 2).reshape(prefill, m.kvd)
+            gpu.decode_kv_upload(name, l, 0, kr, vr, rows_f32=True)
+            if kv_f16:
+                kr = orc.f16_to_f32(orc.f32_to_f16(kr)).reshape(kr.shape)
+                vr = orc.f16_to_f32(orc.f32_to_f16(vr)).reshape(vr.shape)
+            kc[l, :prefill], vc[l, :prefill] = kr, vr
+        x = orc.normal(H, 1.0, 430, 1)
+        gpu.h2d(xd, x)
+        assert gpu.decode_step_dev(name, xd, prefill, ld, td, rd), gpu.last_error()
+        gpu.sync()
+        logits = gpu.d2h(ld, (V,), np.float32)
+        token = int(gpu.d2h(td, (1,), np.uint32)[0])
+        rows = gpu.d2h(rd, (L, 2, m.kvd), kvt)
+        ref, ref_token = m.cpu_step(orc, x, kc, vc, prefill, theta, eps, kv_f16=bool(kv_f16), moe=moe)
+        k32, v32 = m.last_kv
+        for l in range(L):
+            for got, ref32 in ((rows[l, 0], k32[l]), (rows[l, 1], v32[l])):
+                if kv_f16:
+                    want = orc.f32_to_f16(ref32)
+                    e_gpu = orc.rel_l2(orc.f16_to_f32(got), ref32)
+                    e_orc = orc.rel_l2(orc.f16_to_f32(want), ref32)
+                    assert e_gpu <= e_orc + 1e-5, (l, e_gpu, e_orc)
+                    assert (got == want).mean() > 0.95, (l, float((got == want).mean()))
+                else:
+                    assert orc.rel_l2(got, ref32) < 1e-5, l
+        err = orc.rel_l2(logits, ref)
+        print(f"  logits rel_l2 {err:.3e}", flush=True)
+        assert err < 1e-5, err
+        check_greedy(orc, token, logits, ref_token, ref)
+        assert gpu.decode_step_dev(name, xd, prefill + 1, ld, td), gpu.last_error()
+        gpu.sync()
+        logits2 = gpu.d2h(ld, (V,), np.float32)
+        ref2, _ = m.cpu_step(orc, x, kc, vc, prefill + 1, theta, eps, kv_f16=bool(kv_f16), moe=moe)
+        assert orc.rel_l2(logits2, ref2) < 1e-5, orc.rel_l2(logits2, ref2)
+    finally:
+        for p in (xd, ld, td, rd):
+            gpu.dev_free(p)
+        gpu.decode_destroy(name)
+        for k in m.keys:
+            gpu.weight_drop(k)
+
+
+def test_decode_create_ex_declines_bad_flags_and_norms(gpu, orc):
+    """decode_create_ex rejects an unknown flag bit (an argument error) and
+    declines QK norm whose q_norm key is not F32 [head_dim]; neither
+    registers a model."""
+    L, H, nh, nkv, F, V = 1, 512, 4, 2, 512, 64
+    m = Model(orc, L, H, nh, nkv, F, V, 440, qk_norm=True)
+    m.upload(gpu)
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=64,
+               rope_theta=10000.0, rms_eps=1e-6)
+    xd, ld = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4)
+    try:
+        with pytest.raises(RuntimeError, match="unknown flags"):
+            gpu.decode_create("bad.flags", cfg, m.keys, flags=4)
+        bad = list(m.keys)
+        bad[9] = m.keys[0]  # attn_norm: F32 [1 x hidden], not [1 x head_dim]
+        assert not gpu.decode_create("bad.norm", cfg, bad, flags=1)
+        assert "q_norm" in gpu.last_error(), gpu.last_error()
+        for nm in ("bad.flags", "bad.norm"):
+            assert not gpu.decode_step_dev(nm, xd, 0, ld, None)
+        assert gpu.decode_create("good", cfg, m.keys, flags=3), gpu.last_error()
+        gpu.decode_destroy("good")
+    finally:
+        for p in (xd, ld):
+            gpu.dev_free(p)
+        for k in m.keys:
+            gpu.weight_drop(k)
 
 
 def test_decode_token_host_buffers_and_host_experts(gpu, orc):
