@@ -362,14 +362,16 @@ def time_decode_8b(g, steps, ctx=4096, seed=21, kv_f16=False, eager=False):
                 pass
 
 
-def time_decode_moe(g, steps, ctx=4096, seed=31, eager=False):
-    """A Qwen3-30B-A3B-like decode step on the device (soso_hip_decode_create_moe;
-    GpuDispatch::moe_capa): 48 layers of GQA attention (hidden 2048, 32 query /
-    4 KV heads of 128, Q4_K q/k/v/o; the dense step's attention: non-NeoX RoPE,
-    no QK norm) and an MoE FFN (f32 router ~ N(0, 0.02), 128 Q4_K experts of
-    width 768, top-8), a Q6_K head over 151936, soso's f16 KV cache (the only KV
-    type soso's device MoE layer takes) prefilled with N(0, 1) to `ctx`
-    positions; the step runs at position `ctx`.  Timed like time_decode_8b.
+def time_decode_moe(g, steps, ctx=4096, seed=31, eager=False, qwen3_attn=True):
+    """A Qwen3-30B-A3B-like decode step on the device (soso_hip_decode_create_ex
+    with MoE layers; GpuDispatch::moe_capa): 48 layers of GQA attention (hidden
+    2048, 32 query / 4 KV heads of 128, Q4_K q/k/v/o; with qwen3_attn, Qwen3's
+    per-head QK RMSNorm (F32 attn_q_norm / attn_k_norm ~ N(0, 1)) and NeoX RoPE,
+    otherwise the dense step's non-NeoX RoPE without QK norm) and an MoE FFN
+    (f32 router ~ N(0, 0.02), 128 Q4_K experts of width 768, top-8), a Q6_K
+    head over 151936, soso's f16 KV cache (the only KV type soso's device MoE
+    layer takes) prefilled with N(0, 1) to `ctx` positions; the step runs at
+    position `ctx`.  Timed like time_decode_8b.
     Returns (ms per token, bytes per token, token)."""
     L, H, NH, NKV, HDIM, E, F, K, V = 48, 2048, 32, 4, 128, 128, 768, 8, 151936
     qd, kvd = NH * HDIM, NKV * HDIM
@@ -377,11 +379,11 @@ def time_decode_moe(g, steps, ctx=4096, seed=31, eager=False):
     keys, moe_names, exp_keys = [], [], []
     s_ = 0
 
-    def norm(key, st):
-        d = g.dev_alloc(H * 4)
+    def norm(key, st, n=H):
+        d = g.dev_alloc(n * 4)
         try:
-            g.synth_normal(d, H, 1.0, seed, st)
-            g.weight_from_dev(key, d, H * 4, F32, 1, H)
+            g.synth_normal(d, n, 1.0, seed, st)
+            g.weight_from_dev(key, d, n * 4, F32, 1, n)
         finally:
             g.dev_free(d)
     try:
@@ -396,6 +398,11 @@ def time_decode_moe(g, steps, ctx=4096, seed=31, eager=False):
                     g.weight_synth(k, Q4K, rows, cols, seed, s_)
                 keys.append(k)
             keys += [None, None, None]
+            if qwen3_attn:
+                for nm in ("q_norm", "k_norm"):
+                    s_ += 1
+                    norm(f"{name}.L{l}.{nm}", s_, HDIM)
+                    keys.append(f"{name}.L{l}.{nm}")
             mk = f"{name}.L{l}.moe"
             ek = []
             for e in range(E):
@@ -417,7 +424,9 @@ def time_decode_moe(g, steps, ctx=4096, seed=31, eager=False):
         keys += [name + ".out_norm", name + ".head"]
         cfg = dict(n_layers=L, hidden=H, n_heads=NH, n_kv_heads=NKV, head_dim=HDIM, ffn=F, vocab=V, ctx_max=ctx + 1,
                    rope_theta=1000000.0, rms_eps=1e-6, kv_f16=1)
-        assert g.decode_create(name, cfg, keys, drop_sources=True, moe_layers=moe_names), g.last_error()
+        flags = 3 if qwen3_attn else 0  # SOSO_HIP_DECODE_QK_NORM | SOSO_HIP_DECODE_ROPE_NEOX
+        assert g.decode_create(name, cfg, keys, drop_sources=True, moe_layers=moe_names, flags=flags), \
+            g.last_error()
         x = g.dev_alloc(H * 4)
         tok = g.dev_alloc(4)
         st = [g.dev_alloc((ctx + 1) * kvd * 4) for _ in range(2)]
@@ -446,7 +455,7 @@ def time_decode_moe(g, steps, ctx=4096, seed=31, eager=False):
                 g.dev_free(p)
         attn = (qd + 2 * kvd) * (H // 256) * 144 + H * (qd // 256) * 144
         expert = 3 * F * (H // 256) * 144  # gate + up + down of one expert (F % 256 == 0 for down's rows)
-        per_layer = attn + K * expert + E * H * 4 + 2 * H * 4
+        per_layer = attn + K * expert + E * H * 4 + 2 * H * 4 + (2 * HDIM * 4 if qwen3_attn else 0)
         nbytes = L * per_layer + V * (H // 256) * 210 + L * 2 * (ctx + 1) * kvd * 2 + H * 4
         return ms, nbytes, token
     finally:
@@ -874,8 +883,8 @@ def main():
             "ms_per_token": round(ms_q, 4), "tokens_per_s": round(1e3 / ms_q, 1),
             "GB_s": round(b_q / (ms_q * 1e-3) / 1e9, 1), "frac_hbm": round(b_q / (ms_q * 1e-3) / 1e9 / PEAK_GBS, 4),
             "bytes_per_token": int(b_q), "greedy_token": tok_q,
-            "model": "48 layers: GQA attention (32/4 heads of 128, hidden 2048, Q4_K) + MoE FFN (128 Q4_K experts "
-                     "of 768, top-8, f32 router), Q6_K head over 151936, f16 KV"}
+            "model": "48 layers: GQA attention (32/4 heads of 128, hidden 2048, Q4_K, QK RMSNorm, NeoX RoPE) + MoE "
+                     "FFN (128 Q4_K experts of 768, top-8, f32 router), Q6_K head over 151936, f16 KV"}
         # measured HBM traffic over algorithmic bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, profiles/)
         for name, entry in extra.items():
             detail = load_traffic(name + "_detail")

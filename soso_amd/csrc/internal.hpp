@@ -99,13 +99,14 @@ struct DecodeModel {
     bool kv_f16 = false;                        // KV elements: f16 bits (soso's KvDtype::F16) or f32
     void *kcache = nullptr, *vcache = nullptr;  // [n_layers][n_kv_heads][ctx_max][head_dim]
     void *mem = nullptr;                         // activations below, one allocation
-    float *hid = nullptr, *qbuf = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
+    float *hid = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
     float *rope_freq = nullptr; // head_dim / 2 floats
     float *xn = nullptr;        // the MoE layers' normalized x (hidden floats)
     void *moe_mem = nullptr;    // the MoE layers' scratch and routing
     size_t n_host_moe = 0;      // MoE layers whose experts stay on the host (router only)
-    // SOSO_HIP_DECODE_QK_NORM / ROPE_NEOX: the qkv rows go to qkv_raw and
-    // k_qkv_post normalises (per head), rotates and appends them
+    // the step's q/k/v rows as the qkv matvec leaves them; the attention
+    // normalises them per head (SOSO_HIP_DECODE_QK_NORM), rotates them (NeoX
+    // pairs with SOSO_HIP_DECODE_ROPE_NEOX) and appends k and v to the cache
     bool qk_norm = false, rope_neox = false;
     float *qkv_raw = nullptr; // q_dim + 2 kv_dim floats
 };
@@ -174,7 +175,7 @@ void *pinned_get(soso_hip *h, size_t bytes);
 
 // Input and output variants of the matvec kernel (decode-step fusions).
 enum { XS_PLAIN = 0, XS_RMSNORM = 1 };
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 3 };
 struct MvIn {
     const float *x = nullptr;
     const float *norm_w = nullptr; // XS_RMSNORM: the norm's weight (cols)
@@ -182,22 +183,6 @@ struct MvIn {
 };
 struct MvEpi {
     const float *res = nullptr; // EPI_RESID: y = res + W.x (res may be y)
-    // EPI_QKV: rows [0, q_dim) -> y rotated, [q_dim, q_dim + kv_dim) -> k_out
-    // rotated, the next kv_dim -> v_out; RoPE of pairs (2i, 2i+1) inside each
-    // head_dim block at position pos (non-NeoX, gemm.rs:1452-1490)
-    // (K/V caches head-major: element d of KV head j at position pos is at
-    // j * kv_stride + pos * head_dim + d; f32, or f16 bits when kv_f16)
-    void *k_out = nullptr, *v_out = nullptr;
-    // when non-null, also k at rows_out[e] and v at rows_out[kv_dim + e]
-    void *rows_out = nullptr;
-    int kv_f16 = 0;
-    int q_dim = 0, kv_dim = 0, head_dim = 0, pos = 0;
-    size_t kv_stride = 0;
-    float theta = 0.0f;
-    // head_dim / 2 RoPE frequencies theta^(-2i / head_dim), computed on the
-    // host with the C library's powf as the reference does on its CPU; the
-    // angle pos * freq is then the same f32 product (null: powf on the device)
-    const float *rope_freq = nullptr;
 };
 
 // packed layouts (k_matvec.hip)
@@ -216,7 +201,21 @@ int launch_dequant(soso_hip *h, const Weight &w, float *out_dev);
 int launch_argmax(soso_hip *h, const float *x_dev, size_t n, uint32_t *idx_dev);
 // (k_decode.hip)
 constexpr int ATT_CHUNK = 64; // positions per split of the decode attention (a multiple of 16)
-int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, bool kv_f16, int n_heads,
+// The step's q/k/v rows as the qkv matvec stored them (raw: q heads, k heads,
+// v heads, f32), finished per head by the attention (layer.rs:1164-1192):
+// QK norm with qn / kn when non-null, RoPE (NeoX pairs (i, i + head_dim / 2)
+// when neox, else (2i, 2i + 1)) with the frequency table `freq` -- q by
+// every workgroup for its query heads, the new K/V row (stored at position
+// T - 1, and at rows_out when non-null) by the workgroup of the last chunk.
+struct QkvRows {
+    const float *raw = nullptr;
+    const float *qn = nullptr, *kn = nullptr; // attn_q_norm / attn_k_norm [head_dim], or null
+    const float *freq = nullptr;              // RoPE frequencies [head_dim / 2]
+    void *rows_out = nullptr;                 // [k row; v row] of the step, or null
+    float eps = 0.0f;
+    int neox = 0, n_heads = 0, n_kv = 0;
+};
+int launch_attention(soso_hip *h, const QkvRows &rows, const void *K, const void *V, bool kv_f16, int n_heads,
                      int n_kv_heads, int head_dim, int ctx, int T, float *part, float *out);
 // host: the callback for layers whose experts stay on the host (those layers
 // decline without one)
@@ -224,12 +223,6 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
                 void *kv_rows, const HostMoe *host = nullptr);
 // y[i] += v[i] (i < n)
 int launch_vec_add(soso_hip *h, float *y, const float *v, size_t n);
-// The qkv rows of a step (raw: q_dim + 2 kv_dim floats) to q, the caches and
-// the rows copy: per head RMSNorm with qn / kn when non-null, RoPE (pairs
-// (i, i + head_dim / 2) when neox, else (2i, 2i + 1)) on q and k, then the
-// element stores of the fused qkv epilogue (ep: caches, pos, kv_f16, rows_out).
-int launch_qkv_post(soso_hip *h, const float *raw, const float *qn, const float *kn, float eps, bool neox,
-                    int n_heads, int n_kv_heads, const MvEpi &ep, float *q);
 // Scatter n_rows position-major rows [n_rows][kv_dim] (f32 when src_f32, else
 // the cache's element type) into a head-major cache at positions row0...
 int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, bool cache_f16, int kv_dim,

@@ -10,12 +10,12 @@
 // f16 bits rounded with soso's f32_to_f16 (f16.rs:10-36).
 //
 // Launches per layer (every weight byte read once, activations stay in HBM):
-//   1. qkv matvec   x = rmsnorm(h) staged in LDS; rows [q; k; v] concatenated;
-//                   RoPE applied to q/k row pairs in the epilogue, k and v
-//                   written straight into the KV cache at `pos` (with QK
-//                   norm or NeoX RoPE: the rows stored, then k_qkv_post)
-//   2. k_attn_split split-K decode attention over 64-position chunks, the
-//                   G query heads of a KV head share every K/V read
+//   1. qkv matvec   x = rmsnorm(h) staged in LDS; rows [q; k; v] concatenated,
+//                   stored as computed
+//   2. k_attn_split finishes the rows (QK norm when the model has it, RoPE,
+//                   the new K/V row into the cache at `pos`), then split-K
+//                   decode attention over 64-position chunks, the G query
+//                   heads of a KV head sharing every K/V read
 //   3. k_attn_merge softmax-weighted merge of the chunks
 //   4. o matvec     h += W_o . attn (residual in the epilogue)
 //   5. gate/up      x = rmsnorm(h); rows interleaved (gate_i, up_i); the
@@ -57,22 +57,182 @@ constexpr int ATT_HD = 128;                // head_dim handled
 // statistics (m_w = max s, p = e^{s - m_w}, l_w = sum p, acc_w = sum p v);
 // the wavefronts' are merged in LDS into the chunk's (m, l, acc), stored at
 // part[(head * chunks + c) * (HD + 2)].
+//
+// The qkv launch stores its rows as computed and this launch finishes them
+// (QkvRows).  Every workgroup normalises (QK norm) and rotates (RoPE) its G
+// query heads in registers while its V rows are in flight.  The new position
+// T - 1 has a workgroup row of its own (row 0, dispatched first): it
+// normalises, rotates and stores the new K row, copies the new V row into the
+// cache (and the step's row copy), and scores it against the G heads from
+// registers and LDS, as a chunk of one position; the other rows stream the
+// cached positions and never read the new row, so nothing waits for its
+// stores.  Measured on MI355X, ms per token (8B step with f32 / f16 KV;
+// Qwen3-30B-A3B-like step with QK norm and NeoX RoPE):
+//   this arrangement                                  1.664 / 1.627; 2.081
+//   RoPE and KV append in the qkv epilogue            1.711 / 1.654
+//   the last chunk's workgroup appending, then
+//   reading the row back (store, wait, barrier)       1.713 / 1.654; 2.166
+//   a separate finishing launch (QK norm / NeoX)                     2.306
+//
+// (a, b) -> (a cos - b sin, a sin + b cos), rope_cabezas' rotation
+// (gemm.rs:1452-1490) with each product rounded on its own.
+__device__ __forceinline__ void turn_pair(float &a, float &b, float cs, float sn)
+{
+    const float na = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
+    const float nb = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
+    a = na;
+    b = nb;
+}
+
+// QK norm and RoPE (layer.rs:1164-1192, FLAG_QK_NORM / FLAG_ROPE_NEOX) of one
+// head of 128 held as one rotation pair (a, b) per lane.  With `norm`
+// (uniform over the wavefront) the head is first RMS-normalised and scaled by
+// the layer's attn_q_norm / attn_k_norm weights w0, w1 at the pair's elements
+// (rmsnorm, gemm.rs:93-100: x * scale * w, scale = 1 / sqrt(sum(x^2) / n +
+// eps)); then (a, b) turns by the angle whose cosine and sine are cs, sn.
+__device__ __forceinline__ void head_post(float &a, float &b, bool norm, float w0, float w1, float eps, float cs,
+                                          float sn)
+{
+    if (norm) {
+        float ss = fmaf(a, a, b * b);
+        ss = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, seg_sum_dpp<64>(ss)), 63));
+        const float scale = 1.0f / sqrtf(ss / (float)ATT_HD + eps);
+        a = __fmul_rn(__fmul_rn(a, scale), w0);
+        b = __fmul_rn(__fmul_rn(b, scale), w1);
+    }
+    turn_pair(a, b, cs, sn);
+}
+
+// One element of a new K or V row: into the cache at `at` and, when asked,
+// into the step's row copy at `row_at` (f16 with soso's rounding, or f32).
+// Returns the value as the cache holds it.
+template <bool F16>
+__device__ __forceinline__ float kv_row_put(void *cache, void *rows_out, size_t at, int row_at, float v)
+{
+    if constexpr (F16) {
+        const uint16_t bits = (uint16_t)f32_to_f16_soso(v);
+        ((uint16_t *)cache)[at] = bits;
+        if (rows_out) ((uint16_t *)rows_out)[row_at] = bits;
+        return half_bits_to_f32(bits);
+    } else {
+        ((float *)cache)[at] = v;
+        if (rows_out) ((float *)rows_out)[row_at] = v;
+        return v;
+    }
+}
+
+// QK norm and RoPE of the group's q in registers (layer.rs:1164-1192):
+// thread t holds float4 t of the G heads (head t / 32, one half of a
+// wavefront) and qw, the norm weights of its 4 elements; lane l computes the
+// angle of pair l, (T - 1) * fr, and passes it to the lanes holding that pair.
+__device__ __forceinline__ float4 finish_q(float4 qv, float4 qw, float fr, const QkvRows &rows, int T)
+{
+    constexpr int HD = ATT_HD;
+    const int lane = threadIdx.x & 63, tq = lane & 31;
+    if (rows.qn) {
+        // lanes 31 and 63 hold their half's sum (readlane takes a uniform lane)
+        float ss = seg_sum_dpp<32>((qv.x * qv.x + qv.y * qv.y) + (qv.z * qv.z + qv.w * qv.w));
+        const float s_lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 31));
+        const float s_hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 63));
+        ss = lane < 32 ? s_lo : s_hi;
+        const float scale = 1.0f / sqrtf(ss / (float)HD + rows.eps);
+        qv = make_float4(__fmul_rn(__fmul_rn(qv.x, scale), qw.x), __fmul_rn(__fmul_rn(qv.y, scale), qw.y),
+                         __fmul_rn(__fmul_rn(qv.z, scale), qw.z), __fmul_rn(__fmul_rn(qv.w, scale), qw.w));
+    }
+    float cs, sn;
+    sincosf((float)(T - 1) * fr, &sn, &cs);
+    if (!rows.neox) {
+        // pairs (4tq, 4tq + 1) and (4tq + 2, 4tq + 3): 2tq and 2tq + 1
+        turn_pair(qv.x, qv.y, __shfl(cs, 2 * tq, 64), __shfl(sn, 2 * tq, 64));
+        turn_pair(qv.z, qv.w, __shfl(cs, 2 * tq + 1, 64), __shfl(sn, 2 * tq + 1, 64));
+        return qv;
+    }
+    // pairs (i, i + 64): thread tq < 16 holds the first elements of pairs
+    // 4tq .. 4tq + 3, thread tq + 16 the second ones
+    const float ot[4] = {__shfl_xor(qv.x, 16, 64), __shfl_xor(qv.y, 16, 64), __shfl_xor(qv.z, 16, 64),
+                         __shfl_xor(qv.w, 16, 64)};
+    float me[4] = {qv.x, qv.y, qv.z, qv.w};
+    const bool lo = tq < 16;
+    const int i0 = 4 * (tq & 15);
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        float a = lo ? me[k] : ot[k], b = lo ? ot[k] : me[k];
+        turn_pair(a, b, __shfl(cs, i0 + k, 64), __shfl(sn, i0 + k, 64));
+        me[k] = lo ? a : b;
+    }
+    return make_float4(me[0], me[1], me[2], me[3]);
+}
+
+// grid (n_kv_heads, 1 + ceil((T - 1) / ATT_CHUNK)): workgroup row 0 appends
+// the new position T - 1 and takes it as a chunk of its own (partial index
+// chunks - 1); rows 1 .. hold the cached positions 0 .. T - 2 in chunks of
+// ATT_CHUNK (partial index blockIdx.y - 1).
 template <int G, bool F16, int PW>
-__global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(const float *__restrict__ q,
-                                                                     const void *__restrict__ Kc,
+__global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(QkvRows rows, const void *__restrict__ Kc,
                                                                      const void *__restrict__ Vc, int ctx, int T,
                                                                      int chunks, float *__restrict__ part)
 {
     static_assert(PW == 8 || PW == 16, "8 or 16 positions per wavefront");
     constexpr int HD = ATT_HD, NW = ATT_CHUNK / PW, NT = 64 * NW, KA = PW / 8;
+    static_assert(G * HD / 4 <= NT, "one float4 of q per thread");
     __shared__ float qs[G * HD];
     __shared__ float wm[NW][G], wl[NW][G];
     __shared__ float2 accs[NW][G][HD / 2];
-    const int g = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
-    const int t0 = c * ATT_CHUNK, t1 = min(T, t0 + ATT_CHUNK);
+    const int g = blockIdx.x, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int tw = t0 + PW * wave;
     const size_t head_off = (size_t)g * ctx * HD;
+    const float inv = 1.0f / sqrtf((float)HD);
+    const float *qsrc = rows.raw + (size_t)g * G * HD;
+    if (blockIdx.y == 0) {
+        // The new position: its K row (wavefront 0: QK norm, RoPE; lane l
+        // holds the rotation pair l, elements (l, l + 64) with NeoX RoPE,
+        // (2l, 2l + 1) otherwise) and V row (wavefront 1: elements 2l, 2l + 1)
+        // go into the cache at T - 1 and the step's row copy, and into LDS as
+        // the cache holds them; then each query head's score against that one
+        // row: (m, l, acc) = (q.k / sqrt(HD), 1, v).  Nothing in this launch
+        // reads the stores back.
+        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), qw = make_float4(1.f, 1.f, 1.f, 1.f);
+        if (tid < G * HD / 4) qv = ((const float4 *)qsrc)[tid];
+        if (rows.qn) qw = ((const float4 *)rows.qn)[lane & 31];
+        const float fr = rows.freq[lane];
+        float *knew = (float *)accs, *vnew = knew + HD; // LDS reused
+        if (wave < 2) {
+            const int d0 = wave == 0 && rows.neox ? lane : 2 * lane;
+            const int d1 = wave == 0 && rows.neox ? lane + 64 : 2 * lane + 1;
+            const float *src = rows.raw + (size_t)(rows.n_heads + wave * rows.n_kv + g) * HD;
+            float a = src[d0], b = src[d1];
+            if (wave == 0) {
+                float cs, sn;
+                sincosf((float)(T - 1) * fr, &sn, &cs);
+                head_post(a, b, rows.kn != nullptr, rows.kn ? rows.kn[d0] : 1.0f, rows.kn ? rows.kn[d1] : 1.0f,
+                          rows.eps, cs, sn);
+            }
+            void *cache = const_cast<void *>(wave == 0 ? Kc : Vc);
+            const size_t at = head_off + (size_t)(T - 1) * HD;
+            const int row = wave * rows.n_kv * HD + g * HD;
+            float *dst = wave == 0 ? knew : vnew;
+            dst[d0] = kv_row_put<F16>(cache, rows.rows_out, at + d0, row + d0, a);
+            dst[d1] = kv_row_put<F16>(cache, rows.rows_out, at + d1, row + d1, b);
+        }
+        qv = finish_q(qv, qw, fr, rows, T);
+        if (tid < G * HD / 4) *(float4 *)&qs[4 * tid] = qv;
+        __syncthreads();
+        for (int hh = wave; hh < G; hh += NW) {
+            float acc = fmaf(qs[hh * HD + 2 * lane], knew[2 * lane], qs[hh * HD + 2 * lane + 1] * knew[2 * lane + 1]);
+            acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(seg_sum_dpp<64>(acc)), 63));
+            float *o = part + ((size_t)(g * G + hh) * chunks + (chunks - 1)) * (HD + 2);
+            if (lane == 0) {
+                o[0] = acc * inv;
+                o[1] = 1.0f;
+            }
+            *(float2 *)(o + 2 + 2 * lane) = make_float2(vnew[2 * lane], vnew[2 * lane + 1]);
+        }
+        return;
+    }
+    // cached positions 0 .. T - 2
+    const int c = (int)blockIdx.y - 1, Tc = T - 1;
+    const int t0 = c * ATT_CHUNK, t1 = min(Tc, t0 + ATT_CHUNK);
+    const int tw = t0 + PW * wave;
     const int pp = lane >> 3, j = lane & 7;
     // K: f32 rows are 512 B, lane j of a position takes float4 units j, j+8,
     // j+16, j+24 (dims 32i + 4j ..); f16 rows are 256 B, lane j takes 16-byte
@@ -93,13 +253,10 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(const float 
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    constexpr int QR = (G * HD / 4 + NT - 1) / NT; // float4 of the group's q per thread
-    float4 qv[QR];
-#pragma unroll
-    for (int r = 0; r < QR; r++) {
-        qv[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (tid + r * NT < G * HD / 4) qv[r] = ((const float4 *)(q + (size_t)g * G * HD))[tid + r * NT];
-    }
+    float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), qw = make_float4(1.f, 1.f, 1.f, 1.f);
+    if (tid < G * HD / 4) qv = ((const float4 *)qsrc)[tid];
+    if (rows.qn) qw = ((const float4 *)rows.qn)[lane & 31];
+    const float fr = rows.freq[lane];
     __builtin_amdgcn_sched_barrier(0);
     // V: lane l holds dims 2l, 2l + 1 of the wavefront's PW positions
     float2 vr[PW];
@@ -113,9 +270,8 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(const float 
             vr[k] = *(const float2 *)((const float *)Vc + row);
     }
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int r = 0; r < QR; r++)
-        if (tid + r * NT < G * HD / 4) *(float4 *)&qs[4 * (tid + r * NT)] = qv[r];
+    qv = finish_q(qv, qw, fr, rows, T);
+    if (tid < G * HD / 4) *(float4 *)&qs[4 * tid] = qv;
     if constexpr (F16) {
         // f16 -> f32 is exact; from here on the math is the f32 kernel's
 #pragma unroll
@@ -130,7 +286,6 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(const float 
             }
     }
     __syncthreads();
-    const float inv = 1.0f / sqrtf((float)HD);
 #pragma unroll
     for (int hh = 0; hh < G; hh++) {
         float s[KA];
@@ -271,108 +426,34 @@ __global__ void __launch_bounds__(256) k_attn_merge(const float *__restrict__ pa
 // Qwen3-30B-A3B-like, groups of 8: 2.197 against 2.224 ms).
 template <bool F16> constexpr int att_pw() { return F16 ? 16 : 8; }
 
-int launch_attention(soso_hip *h, const float *q, const void *K, const void *V, bool kv_f16, int n_heads,
+int launch_attention(soso_hip *h, const QkvRows &rows, const void *K, const void *V, bool kv_f16, int n_heads,
                      int n_kv_heads, int head_dim, int ctx, int T, float *part, float *out)
 {
     if (head_dim != ATT_HD || n_kv_heads <= 0 || n_heads % n_kv_heads || T <= 0 || T > ctx)
         return set_err(h, SOSO_HIP_DECLINED, "attention: head shape not handled here");
     const int G = n_heads / n_kv_heads;
-    const int chunks = (T + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int chunks = 1 + (T - 1 + ATT_CHUNK - 1) / ATT_CHUNK; // the new position, then the cached ones
     const dim3 grid((unsigned)n_kv_heads, (unsigned)chunks);
+    if (!rows.raw || !rows.freq || rows.n_heads != n_heads || rows.n_kv != n_kv_heads)
+        return set_err(h, SOSO_HIP_ERR_ARG, "attention: q/k/v rows missing");
+#define ATT_LAUNCH(GG, F)                                                                                           \
+    k_attn_split<GG, F, att_pw<F>()><<<grid, 64 * ATT_CHUNK / att_pw<F>(), 0, h->stream>>>(rows, K, V, ctx, T,      \
+                                                                                           chunks, part)
 #define ATT_CASE(GG)                                                                                                \
     case GG:                                                                                                        \
-        if (kv_f16)                                                                                                 \
-            k_attn_split<GG, true, att_pw<true>()><<<grid, 64 * ATT_CHUNK / att_pw<true>(), 0, h->stream>>>(       \
-                q, K, V, ctx, T, chunks, part);                                                                     \
-        else                                                                                                        \
-            k_attn_split<GG, false, att_pw<false>()><<<grid, 64 * ATT_CHUNK / att_pw<false>(), 0, h->stream>>>(    \
-                q, K, V, ctx, T, chunks, part);                                                                     \
+        if (kv_f16) ATT_LAUNCH(GG, true);                                                                           \
+        else ATT_LAUNCH(GG, false);                                                                                 \
         break;
     switch (G) {
         ATT_CASE(1) ATT_CASE(2) ATT_CASE(4) ATT_CASE(8)
     default: return set_err(h, SOSO_HIP_DECLINED, "attention: GQA group size not handled here");
     }
 #undef ATT_CASE
+#undef ATT_LAUNCH
     int rc = hip_check(h, hipGetLastError(), "attention split launch");
     if (rc != SOSO_HIP_OK) return rc;
     k_attn_merge<<<(unsigned)n_heads, 256, 0, h->stream>>>(part, chunks, out);
     return hip_check(h, hipGetLastError(), "attention merge launch");
-}
-
-// ---------------------------------------------------------------------------
-// QK norm and NeoX RoPE (layer.rs:1164-1192, FLAG_QK_NORM / FLAG_ROPE_NEOX):
-// the qkv projection stores its rows (q heads, then k heads, then v heads,
-// head_dim 128 each) and one wavefront per head finishes them.  Lane l holds
-// the head's elements l and l + 64 with NeoX RoPE (pair l of rope_cabezas'
-// neox branch, gemm.rs:1474-1479), 2l and 2l + 1 otherwise: either way the
-// lane's pair has frequency index l.  q and k heads are first RMS-normalised
-// with the layer's attn_q_norm / attn_k_norm (rmsnorm, gemm.rs:93-100:
-// x * scale * w with scale = 1 / sqrt(sum(x^2) / n + eps)), then rotated with
-// the arithmetic of the fused qkv epilogue; the stores are that epilogue's.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void post_put(const MvEpi &ep, void *cache, size_t at, int row_at, float v)
-{
-    if (ep.kv_f16) {
-        const uint16_t b = (uint16_t)f32_to_f16_soso(v);
-        ((uint16_t *)cache)[at] = b;
-        if (ep.rows_out) ((uint16_t *)ep.rows_out)[row_at] = b;
-    } else {
-        ((float *)cache)[at] = v;
-        if (ep.rows_out) ((float *)ep.rows_out)[row_at] = v;
-    }
-}
-
-__global__ void __launch_bounds__(256) k_qkv_post(const float *__restrict__ raw, const float *__restrict__ qn,
-                                                   const float *__restrict__ kn, float eps, int neox, int n_heads,
-                                                   int n_kv, MvEpi ep, float *__restrict__ q)
-{
-    constexpr int HD = ATT_HD;
-    const int lane = threadIdx.x & 63;
-    const int hd = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-    if (hd >= n_heads + 2 * n_kv) return; // whole wavefronts
-    const int kind = hd < n_heads ? 0 : hd < n_heads + n_kv ? 1 : 2; // q, k, v
-    const int d0 = neox ? lane : 2 * lane, d1 = neox ? lane + 64 : 2 * lane + 1;
-    const float *src = raw + (size_t)hd * HD;
-    float a = src[d0], b = src[d1];
-    if (kind < 2) {
-        const float *w = kind == 0 ? qn : kn;
-        if (w) {
-            float ss = fmaf(a, a, b * b);
-            ss = __builtin_bit_cast(float,
-                                    __builtin_amdgcn_readlane(__builtin_bit_cast(int, seg_sum_dpp<64>(ss)), 63));
-            const float scale = 1.0f / sqrtf(ss / (float)HD + eps);
-            a = __fmul_rn(__fmul_rn(a, scale), w[d0]);
-            b = __fmul_rn(__fmul_rn(b, scale), w[d1]);
-        }
-        const float fr = ep.rope_freq ? ep.rope_freq[lane] : powf(ep.theta, -2.0f * (float)lane / (float)HD);
-        float sn, cs;
-        sincosf((float)ep.pos * fr, &sn, &cs);
-        const float na = __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn));
-        const float nb = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
-        a = na;
-        b = nb;
-    }
-    if (kind == 0) {
-        q[(size_t)hd * HD + d0] = a;
-        q[(size_t)hd * HD + d1] = b;
-    } else {
-        const int j = kind == 1 ? hd - n_heads : hd - n_heads - n_kv; // KV head
-        void *cache = kind == 1 ? ep.k_out : ep.v_out;
-        const size_t at = (size_t)j * ep.kv_stride + (size_t)ep.pos * HD;
-        const int row = (kind == 1 ? 0 : ep.kv_dim) + j * HD;
-        post_put(ep, cache, at + d0, row + d0, a);
-        post_put(ep, cache, at + d1, row + d1, b);
-    }
-}
-
-int launch_qkv_post(soso_hip *h, const float *raw, const float *qn, const float *kn, float eps, bool neox,
-                    int n_heads, int n_kv_heads, const MvEpi &ep, float *q)
-{
-    if (ep.head_dim != ATT_HD) return set_err(h, SOSO_HIP_DECLINED, "qkv post: head_dim");
-    const int heads = n_heads + 2 * n_kv_heads;
-    k_qkv_post<<<(unsigned)((heads + 3) / 4), 256, 0, h->stream>>>(raw, qn, kn, eps, neox ? 1 : 0, n_heads,
-                                                                    n_kv_heads, ep, q);
-    return hip_check(h, hipGetLastError(), "qkv post launch");
 }
 
 // rmsnorm (crates/soso-llm-core/src/gemm.rs:93-100) into a new vector: one
@@ -492,9 +573,9 @@ static int host_moe_ffn(soso_hip *h, DecodeModel &m, size_t layer, const MoeLaye
 int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float *logits, uint32_t *token,
                 void *kv_rows, const HostMoe *host)
 {
-    const int q_dim = (int)(m.n_heads * m.head_dim), kv_dim = (int)(m.n_kv_heads * m.head_dim);
+    const int kv_dim = (int)(m.n_kv_heads * m.head_dim);
     if (pos >= m.ctx_max) return set_err(h, SOSO_HIP_ERR_ARG, "decode: position beyond the KV capacity");
-    float *hid = m.hid, *qb = m.qbuf, *att = m.att, *act = m.act, *lg = logits ? logits : m.logits;
+    float *hid = m.hid, *att = m.att, *act = m.act, *lg = logits ? logits : m.logits;
     // layer 0 reads the caller's x in place (its o projection writes the first
     // hid) when x is 16-byte aligned for the staging's vector loads; else a copy
     const bool direct = ((uintptr_t)x & 15) == 0;
@@ -509,29 +590,21 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         in.x = hin;
         in.norm_w = L.attn_norm;
         in.eps = m.eps;
-        MvEpi ep;
-        ep.k_out = K;
-        ep.v_out = V;
-        ep.kv_f16 = m.kv_f16 ? 1 : 0;
-        ep.rows_out = kv_rows ? (char *)kv_rows + l * 2 * kv_dim * esz : nullptr;
-        ep.kv_stride = m.ctx_max * m.head_dim;
-        ep.q_dim = q_dim;
-        ep.kv_dim = kv_dim;
-        ep.head_dim = (int)m.head_dim;
-        ep.pos = (int)pos;
-        ep.theta = m.theta;
-        ep.rope_freq = m.rope_freq;
-        if (m.qk_norm || m.rope_neox) {
-            // the rows as computed, then per head: QK norm, RoPE, KV append
-            rc = launch_matvec_ex(h, *L.qkv, in, m.qkv_raw, MvEpi(), XS_RMSNORM, EPI_STORE);
-            if (rc == SOSO_HIP_OK)
-                rc = launch_qkv_post(h, m.qkv_raw, L.q_norm, L.k_norm, m.eps, m.rope_neox, (int)m.n_heads,
-                                     (int)m.n_kv_heads, ep, qb);
-        } else {
-            rc = launch_matvec_ex(h, *L.qkv, in, qb, ep, XS_RMSNORM, EPI_QKV);
-        }
+        // the q/k/v rows as computed; the attention finishes them per head
+        // (QK norm, RoPE) and appends the new K/V row
+        QkvRows rows;
+        rows.raw = m.qkv_raw;
+        rows.qn = L.q_norm;
+        rows.kn = L.k_norm;
+        rows.freq = m.rope_freq;
+        rows.rows_out = kv_rows ? (char *)kv_rows + l * 2 * kv_dim * esz : nullptr;
+        rows.eps = m.eps;
+        rows.neox = m.rope_neox ? 1 : 0;
+        rows.n_heads = (int)m.n_heads;
+        rows.n_kv = (int)m.n_kv_heads;
+        rc = launch_matvec_ex(h, *L.qkv, in, m.qkv_raw, MvEpi(), XS_RMSNORM, EPI_STORE);
         if (rc == SOSO_HIP_OK)
-            rc = launch_attention(h, qb, K, V, m.kv_f16, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim,
+            rc = launch_attention(h, rows, K, V, m.kv_f16, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim,
                                   (int)m.ctx_max, (int)pos + 1, m.part, att);
         if (rc == SOSO_HIP_OK) {
             MvIn a;

@@ -173,77 +173,20 @@ constexpr int COMBINE_CH = 64; // passes per LDS combine round (S > 1)
 __device__ __forceinline__ float silu_f(float g) { return g / (1.0f + expf(-g)); }
 
 // Output of the row sums gathered in yacc (lane i = row r0 + i, i < nrows).
-// RoPE angle of row r (rope_cabezas, non-NeoX: pair i = (r mod head_dim) / 2
-// turns by pos * theta^(-2i / head_dim)).  Depends on the row only, so the
-// kernel evaluates it before its main loop, while the weight loads are in
-// flight.
-__device__ __forceinline__ void rope_angle(const MvEpi &ep, int r, float &cs, float &sn)
-{
-    const int qk = ep.q_dim + ep.kv_dim;
-    cs = 1.0f;
-    sn = 0.0f;
-    if (r < qk) {
-        const int d = (r < ep.q_dim ? r : r - ep.q_dim) % ep.head_dim;
-        const float fr = ep.rope_freq ? ep.rope_freq[d >> 1]
-                                      : powf(ep.theta, -2.0f * (float)(d >> 1) / (float)ep.head_dim);
-        sincosf((float)ep.pos * fr, &sn, &cs);
-    }
-}
-
-// One new K or V element: into the cache at `at` and, when asked, into the
-// step's row copy at `row_at` (f16 with soso's rounding, or f32).
-__device__ __forceinline__ void kv_put(const MvEpi &ep, void *cache, size_t at, int row_at, float v)
-{
-    if (ep.kv_f16) {
-        const uint16_t b = (uint16_t)f32_to_f16_soso(v);
-        ((uint16_t *)cache)[at] = b;
-        if (ep.rows_out) ((uint16_t *)ep.rows_out)[row_at] = b;
-    } else {
-        ((float *)cache)[at] = v;
-        if (ep.rows_out) ((float *)ep.rows_out)[row_at] = v;
-    }
-}
-
 // Lane `lane` holds row r (valid when ok); pair epilogues find the other row
 // of a pair (2i, 2i + 1) in the neighbouring lane.
 template <int EPI>
-__device__ __forceinline__ void epilogue(float yacc, int lane, int r, bool ok, float *__restrict__ y, const MvEpi &ep,
-                                         float cs = 1.0f, float sn = 0.0f)
+__device__ __forceinline__ void epilogue(float yacc, int lane, int r, bool ok, float *__restrict__ y, const MvEpi &ep)
 {
     if constexpr (EPI == EPI_STORE) {
         if (ok) y[r] = yacc;
     } else if constexpr (EPI == EPI_RESID) {
         if (ok) y[r] = ep.res[r] + yacc;
-    } else if constexpr (EPI == EPI_SWIGLU) {
+    } else {
+        static_assert(EPI == EPI_SWIGLU, "epilogue variant");
         // rows (2i, 2i+1) = (gate_i, up_i); strips start on even rows
         const float up = dpp_f<0xB1>(yacc);
         if (ok && (lane & 1) == 0) y[r >> 1] = silu_f(yacc) * up;
-    } else {
-        // RoPE on q and k (rope_cabezas, non-NeoX): pair (2i, 2i+1) of a head
-        // becomes (a cos - b sin, a sin + b cos); v passes through
-        const float other = dpp_f<0xB1>(yacc);
-        const int qk = ep.q_dim + ep.kv_dim;
-        if (ok) {
-            if (r < qk) {
-                const int d = (r < ep.q_dim ? r : r - ep.q_dim) % ep.head_dim;
-                const bool even = (d & 1) == 0;
-                const float a = even ? yacc : other, b = even ? other : yacc;
-                const float v = even ? __fsub_rn(__fmul_rn(a, cs), __fmul_rn(b, sn))
-                                     : __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, cs));
-                if (r < ep.q_dim) {
-                    y[r] = v;
-                } else {
-                    const int e = r - ep.q_dim;
-                    kv_put(ep, ep.k_out, (size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + d,
-                           e, v);
-                }
-            } else {
-                const int e = r - qk;
-                kv_put(ep, ep.v_out,
-                       (size_t)(e / ep.head_dim) * ep.kv_stride + (size_t)ep.pos * ep.head_dim + e % ep.head_dim,
-                       ep.kv_dim + e, yacc);
-            }
-        }
     }
 }
 
@@ -287,7 +230,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     const int passes = (rows + RW - 1) / RW;
     const int tg = gridDim.x * gpw;
     // pair epilogues need whole pairs of rows (2i, 2i + 1) in neighbouring lanes
-    constexpr int PU = (RW == 1 && (EPI == EPI_QKV || EPI == EPI_SWIGLU)) ? 2 : 1;
+    constexpr int PU = (RW == 1 && EPI == EPI_SWIGLU) ? 2 : 1;
     static_assert(DEPTH % PU == 0, "a ring turn holds whole units");
     const int units = (passes + PU - 1) / PU;
     auto strip = [&](int g, int &q0, int &q1) {
@@ -350,13 +293,6 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
         stage_x_finish<FMT, true, XP>(xpre, x, cols, xp, s16, kx, NTHR);
     }
-    // the RoPE angle of this lane's output row, computed while the ring is in
-    // flight (the empty asm keeps it from being sunk to the epilogue)
-    float rope_c = 1.0f, rope_s = 0.0f;
-    if constexpr (EPI == EPI_QKV) {
-        rope_angle(ep, lane_row(lane), rope_c, rope_s);
-        asm volatile("" ::"v"(rope_c), "v"(rope_s));
-    }
     XReg xv;
     unit_setup_x<FMT, true>(xp, s16, kx, u, U, xv, c);
     auto dot = [&](const WRow<FMT> &w) -> float { return unit_dot<FMT>(w, xv, c); };
@@ -394,7 +330,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         if (__builtin_expect(c.onum != 0, 0))
             yacc += outlier_rows<FMT, LPR>(rs, lane_base, pass_off, 0, n, cols, L, c, u, uact, lane);
         const int r = lane_row(lane);
-        epilogue<EPI>(yacc, lane, r, lane < n * RW && r < rows, y, ep, rope_c, rope_s);
+        epilogue<EPI>(yacc, lane, r, lane < n * RW && r < rows, y, ep);
     } else {
         // the same number of combine rounds for every wavefront of the workgroup
         int nmax = 0;
@@ -728,9 +664,7 @@ template <int FMT>
 static void launch_ex_fmt(soso_hip *h, int xs, int epi, int lpr, bool il, unsigned grid, size_t lds, const uint8_t *W,
                           size_t stride, const MvIn &in, float *y, int rows, int cols, const MvEpi &ep)
 {
-    if (xs == XS_RMSNORM && epi == EPI_QKV)
-        launch_ex_lpr<FMT, XS_RMSNORM, EPI_QKV>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
-    else if (xs == XS_RMSNORM && epi == EPI_SWIGLU)
+    if (xs == XS_RMSNORM && epi == EPI_SWIGLU)
         launch_ex_lpr<FMT, XS_RMSNORM, EPI_SWIGLU>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
     else if (xs == XS_PLAIN && epi == EPI_RESID)
         launch_ex_lpr<FMT, XS_PLAIN, EPI_RESID>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
@@ -765,14 +699,14 @@ static const char *plan_matvec_ex(const soso_hip *h, uint8_t dtype, size_t rows_
         return "matvec_ex: the decode matvecs take Q4_K, Q8_0 or Q6_K weights";
     if (!packed_shape_ok(dtype, rows_, cols_) || rows_ > (1u << 30) || cols_ > (1u << 20))
         return "matvec_ex: shape not handled here";
-    if (!(xs == XS_RMSNORM && (epi == EPI_QKV || epi == EPI_SWIGLU || epi == EPI_STORE)) &&
+    if (!(xs == XS_RMSNORM && (epi == EPI_SWIGLU || epi == EPI_STORE)) &&
         !(xs == XS_PLAIN && epi == EPI_RESID))
         return "matvec_ex: input/output variant not built";
     const int rows = (int)rows_, cols = (int)cols_, U = cols / 64;
     p.stride = packed_row_stride(dtype, cols_);
     p.S = (U + 63) / 64;
     if (xs == XS_RMSNORM && cols > 8 * 512) return "matvec_ex: normalised x wider than the staging registers";
-    if ((epi == EPI_QKV || epi == EPI_SWIGLU) && (p.S != 1 || rows % 2))
+    if (epi == EPI_SWIGLU && (p.S != 1 || rows % 2))
         return "matvec_ex: pair epilogue needs whole rows per wavefront";
     if (p.S > 1) {
         if (xs != XS_PLAIN || epi != EPI_RESID || (p.S != 2 && p.S != 4))
@@ -787,7 +721,7 @@ static const char *plan_matvec_ex(const soso_hip *h, uint8_t dtype, size_t rows_
     if (U < 8) return "matvec_ex: rows narrower than 512 columns";
     p.lpr = U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
     const int RW = 64 / p.lpr, gpw = 8;
-    const int PU = (RW == 1 && (epi == EPI_QKV || epi == EPI_SWIGLU)) ? 2 : 1;
+    const int PU = (RW == 1 && epi == EPI_SWIGLU) ? 2 : 1;
     const int passes = (rows + RW - 1) / RW, units = (passes + PU - 1) / PU;
     p.lds = stage_lds_bytes_o(cols_) + 64;
     if (p.lds > h->max_lds) return "matvec_ex: x does not fit in LDS";

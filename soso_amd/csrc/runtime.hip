@@ -837,7 +837,6 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
         return set_err(h, SOSO_HIP_ERR_ARG, "decode_create: unknown flags");
     m.qk_norm = (flags & SOSO_HIP_DECODE_QK_NORM) != 0;
     m.rope_neox = (flags & SOSO_HIP_DECODE_ROPE_NEOX) != 0;
-    const bool post = m.qk_norm || m.rope_neox; // the qkv rows finished by k_qkv_post
     const size_t kpl = m.qk_norm ? 11 : 9;      // keys per layer
     auto get = [&](size_t i, size_t rows, size_t cols, bool f32, const Weight **out) -> bool {
         const Weight *w = find_weight(h, keys[i], key_lens[i]);
@@ -893,7 +892,7 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
             size_t rows, cols;
             int xs, epi;
             const char *role;
-        } roles[] = {{q[l], qd + 2 * kvd, H, XS_RMSNORM, post ? EPI_STORE : EPI_QKV, "q/k/v"},
+        } roles[] = {{q[l], qd + 2 * kvd, H, XS_RMSNORM, EPI_STORE, "q/k/v"},
                      {m.layers[l].o, H, qd, XS_PLAIN, EPI_RESID, "o"},
                      {g[l], 2 * F, H, XS_RMSNORM, EPI_SWIGLU, "gate/up"},
                      {m.layers[l].down, H, F, XS_PLAIN, EPI_RESID, "down"}};
@@ -969,9 +968,9 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     }
     // KV cache and step buffers
     const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
-    const size_t chunks = (cfg->ctx_max + ATT_CHUNK - 1) / ATT_CHUNK;
-    const size_t act_floats = H + 2 * qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) + cfg->vocab + 64 +
-                              cfg->head_dim / 2 + H + (post ? qd + 2 * kvd : 0);
+    const size_t chunks = 1 + (cfg->ctx_max + ATT_CHUNK - 1) / ATT_CHUNK; // attention partials per head, at most
+    const size_t act_floats = H + (qd + 2 * kvd) + qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) +
+                              cfg->vocab + 64 + cfg->head_dim / 2 + H;
     // MoE scratch (shared by the MoE layers, which run one after another) and
     // each layer's routing of the last step (256-byte slots)
     const size_t moe_route_bytes = 512;
@@ -992,14 +991,13 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     m.vcache = (char *)m.kcache + kv_bytes;
     float *f = (float *)m.mem;
     m.hid = f;
-    m.qbuf = f + H;
-    m.att = m.qbuf + qd;
+    m.qkv_raw = f + H;
+    m.att = m.qkv_raw + qd + 2 * kvd;
     m.act = m.att + qd;
     m.part = m.act + F;
     m.logits = m.part + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2);
     m.rope_freq = m.logits + cfg->vocab + 64;
     m.xn = m.rope_freq + cfg->head_dim / 2;
-    m.qkv_raw = post ? m.xn + H : nullptr;
     for (size_t l = 0, j = 0; l < L; l++) {
         DecodeLayer &dl = m.layers[l];
         if (!dl.moe) continue;

@@ -688,22 +688,25 @@ def test_decode_step_with_moe_layers_matches_cpu(gpu, orc, kv_f16):
             gpu.dev_free(p)
 
 
-@pytest.mark.parametrize("qk_norm,neox,kv_f16,with_moe", [
-    (True, True, 0, False),    # Qwen3's attention: QK norm and NeoX RoPE
-    (True, True, 1, True),     # the same over soso's f16 cache, layer 1 an MoE layer
-    (True, False, 1, False),   # QK norm alone
-    (False, True, 0, False),   # NeoX RoPE alone
+@pytest.mark.parametrize("qk_norm,neox,kv_f16,with_moe,prefill", [
+    (True, True, 0, False, 90),    # Qwen3's attention: QK norm and NeoX RoPE
+    (True, True, 0, False, 63),    # steps at 63 (one chunk) and 64 (a chunk of one new position)
+    (True, True, 1, True, 90),     # the same over soso's f16 cache, layer 1 an MoE layer
+    (True, False, 1, False, 127),  # QK norm alone; steps at 127 and 128
+    (False, True, 0, False, 0),    # NeoX RoPE alone; steps at 0 and 1
 ])
-def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with_moe):
+def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with_moe, prefill):
     """soso_hip_decode_create_ex with SOSO_HIP_DECODE_QK_NORM (each q and k
     head RMS-normalised with the layer's attn_q_norm / attn_k_norm before RoPE,
     layer.rs:1164-1180) and SOSO_HIP_DECODE_ROPE_NEOX (rope_cabezas' NeoX
-    pairs (i, i + head_dim/2), gemm.rs:1474-1479).  Two steps (positions 90
-    and 91, the second reading the row the first wrote) against the oracle's
-    composition: logits within relative L2 1e-5, the greedy token, and the K/V
-    rows written at 90 under the bar of test_decode_step_matches_cpu."""
-    L, H, nh, nkv, F, V, prefill = 2, 1024, 8, 2, 2048, 1000, 90
-    theta, eps, ctx = 1000000.0, 1e-6, 128
+    pairs (i, i + head_dim/2), gemm.rs:1474-1479).  Two steps (positions
+    `prefill` and `prefill` + 1, the second reading the row the first wrote;
+    the attention's last chunk appends the row, so the positions straddle
+    chunk ends) against the oracle's composition: logits within relative L2
+    1e-5, the greedy token, and the K/V rows written at `prefill` under the
+    bar of test_decode_step_matches_cpu."""
+    L, H, nh, nkv, F, V = 2, 1024, 8, 2, 2048, 1000
+    theta, eps, ctx = 1000000.0, 1e-6, 192
     flags = (1 if qk_norm else 0) | (2 if neox else 0)  # SOSO_HIP_DECODE_QK_NORM | _ROPE_NEOX
     m = Model(orc, L, H, nh, nkv, F, V, 400 + flags + 4 * kv_f16, qk_norm=qk_norm, neox=neox)
     m.upload(gpu)
@@ -725,7 +728,7 @@ def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with
     vc = np.zeros((L, ctx, m.kvd), np.float32)
     xd, ld, td, rd = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(4), gpu.dev_alloc(L * 2 * m.kvd * esz)
     try:
-        for l in range(L):
+        for l in range(L if prefill else 0):
             kr = orc.normal(prefill * m.kvd, 1.0, 420 + l, 1).reshape(prefill, m.kvd)
             vr = orc.normal(prefill * m.kvd, 1.0, 420 + l, 2).reshape(prefill, m.kvd)
             gpu.decode_kv_upload(name, l, 0, kr, vr, rows_f32=True)
