@@ -637,9 +637,17 @@ def _upload(gpu, key, view, rows, cols):
         gpu.dev_free(d)
 
 
+DEVICE_LAYER_FLAGS = FLAG_ROPE_NEOX | FLAG_QK_NORM  # what soso_hip_decode_create_ex takes
+
+
 def decode_plan(som):
-    """The tensors a dense GQA decoder needs, in the device decode step's key
-    order, after the checks Runtime makes (runtime.rs:330-475).  Raises
+    """The tensors a GQA decoder needs, in the device decode step's key order,
+    after the checks Runtime makes (runtime.rs:330-475): per layer attn_norm,
+    q, k, v, o, ffn_norm, gate, up, down (None for an MoE layer's FFN, which
+    runs from its registered router and experts), then attn_q_norm /
+    attn_k_norm with FLAG_QK_NORM (layer.rs:1164-1180); then output_norm and
+    the head.  Returns (cfg, want, extra): extra = {"flags": the
+    SOSO_HIP_DECODE_* flags, "moe_layers": the MoE layer indices}.  Raises
     SomError(ERR_ARG) for a model the device step does not run."""
     m = som.manifest
     if m is None:
@@ -652,21 +660,33 @@ def decode_plan(som):
     elif m.ext.tied_lm_head and som.find("lm_head") is not None:
         why = "lm_head present although the manifest ties it to embed (runtime.rs:349-353)"
     H, L = m.hidden_dim, m.num_layers
-    nh, nkv, hd, F = (m.effective_num_heads(0), m.effective_num_kv_heads(0), m.effective_head_dim(0),
-                      m.effective_ffn_dim(0))
+    nh, nkv, hd = m.effective_num_heads(0), m.effective_num_kv_heads(0), m.effective_head_dim(0)
+    dense = [l for l in range(L) if not m.layer_is_moe(l)]
+    F = m.effective_ffn_dim(dense[0]) if dense else 0
+    flags0 = (m.layer(0) or LayerSpec()).flags
+    moe_layers = []
     for l in range(L):
         s = m.layer(l) or LayerSpec()
         if why:
             break
-        if s.attn_kind != ATTN_GQA or m.layer_is_moe(l) or s.ffn_kind != FFN_DENSE:
-            why = f"layer {l}: only GQA attention with a dense FFN"
-        elif s.flags:
-            why = f"layer {l}: flags {s.flags:#x} (NeoX RoPE, QK norm, Gemma norms, ...) are not on the device step"
-        elif (m.effective_num_heads(l), m.effective_num_kv_heads(l), m.effective_head_dim(l),
-              m.effective_ffn_dim(l)) != (nh, nkv, hd, F):
+        if s.attn_kind != ATTN_GQA:
+            why = f"layer {l}: only GQA attention"
+        elif m.layer_is_moe(l) and (s.ffn_kind != FFN_MOE or s.num_shared_experts):
+            why = f"layer {l}: only plain MoE FFNs (no latent or shared experts)"
+        elif not m.layer_is_moe(l) and s.ffn_kind != FFN_DENSE:
+            why = f"layer {l}: FFN kind {s.ffn_kind} is not on the device step"
+        elif s.flags & ~DEVICE_LAYER_FLAGS:
+            why = f"layer {l}: flags {s.flags:#x} (Gemma norms, ...) are not on the device step"
+        elif s.flags != flags0:
+            why = f"layer {l}: layers differ in flags"
+        elif (m.effective_num_heads(l), m.effective_num_kv_heads(l), m.effective_head_dim(l)) != (nh, nkv, hd) or \
+                (not m.layer_is_moe(l) and m.effective_ffn_dim(l) != F):
             why = f"layer {l}: layers differ in shape"
+        if m.layer_is_moe(l):
+            moe_layers.append(l)
     if why:
         raise SomError(f"decode_plan: {why}", ERR_ARG)
+    flags = (1 if flags0 & FLAG_QK_NORM else 0) | (2 if flags0 & FLAG_ROPE_NEOX else 0)  # SOSO_HIP_DECODE_*
     qd, kvd, V = nh * hd, nkv * hd, m.vocab_size
     # with tied embeddings (or no lm_head) the logits come from embed (runtime.rs:1165)
     head = "lm_head" if som.find("lm_head") is not None else "embed"
@@ -674,18 +694,25 @@ def decode_plan(som):
     for l in range(L):
         p = f"L{l:02}"
         want += [(f"{p}.attn_norm", (H,)), (f"{p}.attn_q", (qd, H)), (f"{p}.attn_k", (kvd, H)),
-                 (f"{p}.attn_v", (kvd, H)), (f"{p}.attn_output", (H, qd)), (f"{p}.ffn_norm", (H,)),
-                 (f"{p}.ffn_gate", (F, H)), (f"{p}.ffn_up", (F, H)), (f"{p}.ffn_down", (H, F))]
+                 (f"{p}.attn_v", (kvd, H)), (f"{p}.attn_output", (H, qd)), (f"{p}.ffn_norm", (H,))]
+        if l in moe_layers:
+            want += [(None, None)] * 3
+        else:
+            want += [(f"{p}.ffn_gate", (F, H)), (f"{p}.ffn_up", (F, H)), (f"{p}.ffn_down", (H, F))]
+        if flags & 1:
+            want += [(f"{p}.attn_q_norm", (hd,)), (f"{p}.attn_k_norm", (hd,))]
     want += [("output_norm", (H,)), (head, (V, H))]
     for name, shape in want + [("embed", (V, H))]:
+        if name is None:
+            continue
         e = som.find(name)
         if e is None:
             raise SomError(f"decode_plan: {name}: missing", ERR_ARG)
         if e.shape != shape:
             raise SomError(f"decode_plan: {name}: shape {list(e.shape)} vs {list(shape)}", ERR_ARG)
-    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=F, vocab=V,
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=hd, ffn=F or 1, vocab=V,
                rope_theta=m.rope_theta, rms_eps=m.rms_eps)
-    return cfg, want
+    return cfg, want, {"flags": flags, "moe_layers": moe_layers}
 
 
 class SomDecoder:
@@ -726,23 +753,29 @@ class SomDecoder:
         self._x = None
         g.decode_destroy(self.key)
         for k in dict.fromkeys(self.keys):
-            g.weight_drop(k)
+            if k is not None:
+                g.weight_drop(k)
 
 
 def prepare_decode(gpu, som, model_key, ctx_max=None, kv_f16=False):
-    """Makes a converted dense model resident and builds its device decode
-    step (KV cache of ctx_max positions, manifest max_seq by default)."""
-    cfg, want = decode_plan(som)
+    """Makes a converted model resident and builds its device decode step (KV
+    cache of ctx_max positions, manifest max_seq by default): dense layers
+    from their tensors, MoE layers registered first (prepare_moe_layer)."""
+    cfg, want, extra = decode_plan(som)
     m = som.manifest
     cfg = dict(cfg, ctx_max=ctx_max or m.max_seq, kv_f16=1 if kv_f16 else 0)
-    keys = []
+    keys, moe_keys = [], [None] * cfg["n_layers"]
+    for l in extra["moe_layers"]:
+        moe_keys[l] = prepare_moe_layer(gpu, som, l, f"{model_key}.L{l:02}.moe")
     for name, shape in want:
-        if name not in keys:
+        if name is not None and name not in keys:
             v = som.tensor_view(name)
             rows, cols = (1, shape[0]) if len(shape) == 1 else shape
             _upload(gpu, name, v, rows, cols)
         keys.append(name)
-    if not gpu.decode_create(model_key, cfg, keys):
+    ok = gpu.decode_create(model_key, cfg, keys, moe_layers=moe_keys if extra["moe_layers"] else None,
+                           flags=extra["flags"])
+    if not ok:
         raise SomError(f"prepare_decode: the device step declined the model: {gpu.last_error()}", ERR_ARG)
     return SomDecoder(gpu, som, model_key, cfg, keys, m.embed_scale())
 

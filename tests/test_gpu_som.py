@@ -60,6 +60,65 @@ def test_decode_from_som_matches_cpu(gpu, orc, tmp_path):
             dec.close()
 
 
+def test_qwen3_style_decode_from_som_matches_cpu(gpu, orc, tmp_path):
+    """A converted model with Qwen3's attention (FLAG_QK_NORM | FLAG_ROPE_NEOX
+    on every layer, attn_q_norm / attn_k_norm tensors) whose layer 1 is an MoE
+    layer (router L01.ffn_gate_inp, experts L01.Eee.ffn_*): decode_plan maps it
+    onto soso_hip_decode_create_ex with the MoE layer registered from the
+    mapped tensors; five greedy steps against the oracle's composition."""
+    from test_gpu_decode import MoeFfn
+    L, H, nh, nkv, F, V, ctx, theta, eps = 2, 1024, 8, 2, 2048, 800, 16, 1000000.0, 1e-6
+    m = Model(orc, L, H, nh, nkv, F, V, 78, qk_norm=True, neox=True)
+    moe = MoeFfn(orc, 8, H, 512, 2, 79)
+    embed = orc.normal(V * H, 1.0, 78, 9002).reshape(V, H)
+    man = som.Manifest(name="gpu-qwen3ish", vocab_size=V, hidden_dim=H, num_layers=L, num_heads=nh,
+                       num_kv_heads=nkv, ffn_dim=F, max_seq=ctx, rope_theta=theta, rms_eps=eps)
+    man.fill_layers_from_globals()
+    for ls in man.layers:
+        ls.flags = som.FLAG_QK_NORM | som.FLAG_ROPE_NEOX
+    ls = man.layers[1]
+    ls.ffn_kind, ls.num_experts, ls.num_experts_per_tok, ls.moe_ffn_dim = som.FFN_MOE, moe.n_exp, moe.top_k, moe.ffn
+    ts = []
+    for l, lw in enumerate(m.layers):
+        for k, nm in NAMES.items():
+            if l == 1 and k in ("gate", "up", "down"):
+                continue
+            dt, r, c = m.shapes(k)
+            ts.append((f"L{l:02}.{nm}", dt, (c,) if r == 1 else (r, c), lw[k]))
+        ts += [(f"L{l:02}.attn_q_norm", som.DTYPE_F32, (128,), lw["q_norm"]),
+               (f"L{l:02}.attn_k_norm", som.DTYPE_F32, (128,), lw["k_norm"])]
+    ts.append(("L01.ffn_gate_inp", som.DTYPE_F32, (moe.n_exp, H), moe.router))
+    for e in range(moe.n_exp):
+        ts += [(f"L01.E{e:02}.ffn_gate", som.DTYPE_Q4_K, (moe.ffn, H), moe.gate[e]),
+               (f"L01.E{e:02}.ffn_up", som.DTYPE_Q4_K, (moe.ffn, H), moe.up[e]),
+               (f"L01.E{e:02}.ffn_down", som.DTYPE_Q4_K, (H, moe.ffn), moe.down[e])]
+    ts += [("output_norm", som.DTYPE_F32, (H,), m.out_norm), ("embed", som.DTYPE_F32, (V, H), embed),
+           ("lm_head", m.head_dtype, (V, H), m.head)]
+    som.write_model(str(tmp_path), man, ts)
+    print(f"som qwen3-style decode L={L} H={H} heads={nh}/{nkv} moe layer 1 E={moe.n_exp}", flush=True)
+    with som.SomModel.open(str(tmp_path)) as s:
+        # f32 KV: at position 0 the new row is the whole context, and an f16
+        # rounding that lands on the other neighbour (the GPU's f32 row differs
+        # from the CPU's in the last bits) would move the logits by ~5e-5
+        dec = som.prepare_decode(gpu, s, "som.qwen3ish", ctx_max=ctx)
+        try:
+            kc = np.zeros((L, ctx, m.kvd), np.float32)
+            vc = np.zeros((L, ctx, m.kvd), np.float32)
+            tok = 7
+            for pos in range(5):
+                got, logits = dec.step(tok, pos, logits=True)
+                ref, ref_tok = m.cpu_step(orc, embed[tok], kc, vc, pos, theta, eps, moe={1: moe})
+                assert orc.rel_l2(logits, ref) < 1e-5, (pos, orc.rel_l2(logits, ref))
+                top2 = np.sort(ref)[-2:]
+                if top2[1] - top2[0] > 1e-3 * max(1.0, abs(float(top2[1]))):
+                    assert got == ref_tok, pos
+                tok = ref_tok
+        finally:
+            dec.close()
+            for name, *_ in ts:
+                gpu.weight_drop(name)
+
+
 def test_moe_layer_from_som_matches_cpu(gpu, orc, tmp_path):
     E, H, FF, K, n = 8, 256, 512, 2, 3
     layer = Layer(orc, E, H, FF, K, 81)

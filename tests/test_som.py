@@ -402,7 +402,9 @@ def test_views_bounds_dtypes_and_duplicates(tmp_path):
 
 def test_write_model_and_decode_plan(tmp_path):
     """A dense GQA decoder passes the checks of Runtime (runtime.rs:330-475);
-    what the device step does not run is refused with the reason."""
+    NeoX RoPE and QK norm (with their attn_q_norm / attn_k_norm tensors) and
+    plain MoE layers map onto the device step; what it does not run is
+    refused with the reason."""
     H, nh, nkv, F, V, L = 256, 2, 1, 512, 64, 2
     man = som.Manifest(name="d", vocab_size=V, hidden_dim=H, num_layers=L, num_heads=nh, num_kv_heads=nkv,
                        ffn_dim=F, max_seq=64, rope_theta=5e5, rms_eps=1e-5)
@@ -422,7 +424,8 @@ def test_write_model_and_decode_plan(tmp_path):
     ts += [t("output_norm", 1, (H,)), t("embed", 1, (V, H)), t("lm_head", 13, (V, H))]
     som.write_model(str(tmp_path / "ok"), man, ts)
     with som.SomModel.open(str(tmp_path / "ok")) as s:
-        cfg, want = som.decode_plan(s)
+        cfg, want, extra = som.decode_plan(s)
+        assert extra == {"flags": 0, "moe_layers": []}
         assert cfg["n_layers"] == L and cfg["head_dim"] == 128 and cfg["rope_theta"] == np.float32(5e5)
         assert [n for n, _ in want][:9] == ["L00.attn_norm", "L00.attn_q", "L00.attn_k", "L00.attn_v",
                                             "L00.attn_output", "L00.ffn_norm", "L00.ffn_gate", "L00.ffn_up",
@@ -432,19 +435,46 @@ def test_write_model_and_decode_plan(tmp_path):
     som.write_model(str(tmp_path / "tied"), man, [x for x in ts if x[0] != "lm_head"])
     with som.SomModel.open(str(tmp_path / "tied")) as s:
         assert som.decode_plan(s)[1][-1] == ("embed", (V, H))
+    import copy
+
+    def flagged(fl):
+        m2 = copy.deepcopy(man)
+        for ls in m2.layers:
+            ls.flags = fl
+        return m2
+    # NeoX RoPE on every layer: flags 2, the same tensors
+    som.write_model(str(tmp_path / "neox"), flagged(som.FLAG_ROPE_NEOX), ts)
+    with som.SomModel.open(str(tmp_path / "neox")) as s:
+        _, want2, extra = som.decode_plan(s)
+        assert extra["flags"] == 2 and want2 == want
+    # QK norm: flags 1, attn_q_norm / attn_k_norm [head_dim] after each layer's nine
+    qk = ts + [t(f"L{l:02}.attn_{w}_norm", 1, (128,)) for l in range(L) for w in "qk"]
+    som.write_model(str(tmp_path / "qk"), flagged(som.FLAG_QK_NORM | som.FLAG_ROPE_NEOX), qk)
+    with som.SomModel.open(str(tmp_path / "qk")) as s:
+        _, want2, extra = som.decode_plan(s)
+        assert extra["flags"] == 3
+        assert [n for n, _ in want2][9:11] == ["L00.attn_q_norm", "L00.attn_k_norm"] and len(want2) == 11 * L + 2
+    # an MoE layer: its gate/up/down slots are None, the layer listed
+    m2 = copy.deepcopy(man)
+    m2.layers[1].ffn_kind, m2.layers[1].num_experts, m2.layers[1].num_experts_per_tok = som.FFN_MOE, 4, 2
+    som.write_model(str(tmp_path / "moe"), m2, ts)
+    with som.SomModel.open(str(tmp_path / "moe")) as s:
+        _, want2, extra = som.decode_plan(s)
+        assert extra["moe_layers"] == [1] and want2[15:18] == [(None, None)] * 3
     refusals = {
-        "neox": lambda m: setattr(m.layers[1], "flags", som.FLAG_ROPE_NEOX),
-        "moe": lambda m: setattr(m.layers[0], "ffn_kind", som.FFN_MOE),
-        "softcap": lambda m: setattr(m.ext, "logit_softcap", 30.0),
-        "asr": lambda m: setattr(m, "model_kind", som.MODEL_ASR),
+        "qk_norm_missing": (lambda m: [setattr(x, "flags", som.FLAG_QK_NORM) for x in m.layers], "attn_q_norm"),
+        "flags_differ": (lambda m: setattr(m.layers[1], "flags", som.FLAG_ROPE_NEOX), "differ in flags"),
+        "sandwich": (lambda m: [setattr(x, "flags", som.FLAG_SANDWICH_NORM) for x in m.layers], "flags"),
+        "latent_moe": (lambda m: setattr(m.layers[0], "ffn_kind", som.FFN_LATENT_MOE), "MoE"),
+        "softcap": (lambda m: setattr(m.ext, "logit_softcap", 30.0), "extensions"),
+        "asr": (lambda m: setattr(m, "model_kind", som.MODEL_ASR), "decoders"),
     }
-    for why, f in refusals.items():
-        import copy
+    for why, (f, msg) in refusals.items():
         m2 = copy.deepcopy(man)
         f(m2)
         som.write_model(str(tmp_path / why), m2, ts)
         with som.SomModel.open(str(tmp_path / why)) as s:
-            with pytest.raises(som.SomError):
+            with pytest.raises(som.SomError, match=msg):
                 som.decode_plan(s)
     som.write_model(str(tmp_path / "missing"), man, [x for x in ts if x[0] != "L01.ffn_gate"])
     with som.SomModel.open(str(tmp_path / "missing")) as s:
