@@ -558,12 +558,13 @@ static bool interleave_fits(int passes, int pu, int groups, size_t pass_bytes)
 //     once every wavefront's first row arrives late and the math cannot
 //     overlap the stream);  Q8_0 4096 x 4096: depth 2 (5.6 us; 5.9 at depth 3,
 //     6.3 at 4: a wavefront has two rows, so deeper rings only read past them);
-//   Q6_K 128256 x 4096: depth 4 (79 us; 3 and 6 the same);  split rows 4096 x 14336: depth 2;
+//   Q6_K 128256 x 4096: depth 4 (79 us; 3 and 6 the same);  split rows 4096 x 14336: depth 4
+//     (10.53 us against 10.80 at depth 2 and 12.8 at 8; the 8B step 1.644 against 1.667 ms);
 //   narrow rows (LPR < 64, e.g. 768 x 2048): depth 2 with x staged first.
 // Split rows (S > 1) need a depth that divides the combine round.
 template <int FMT, int S> constexpr int ring_depth()
 {
-    return S > 1 ? 2 : FMT == FMT_Q6K ? 4 : 2;
+    return S > 1 || FMT == FMT_Q6K ? 4 : 2;
 }
 template <int LPR> constexpr bool x_first() { return LPR < 64; }
 
