@@ -241,9 +241,9 @@ int soso_hip_decode_create_moe(soso_hip *h, const char *model_key, size_t model_
  * then q_norm, k_norm; then output_norm and head); SOSO_HIP_DECODE_ROPE_NEOX
  * -- RoPE turns the pairs (i, i + head_dim/2) (rope_cabezas with neox,
  * gemm.rs:1474-1479) instead of (2i, 2i + 1).  moe_layer_keys as in
- * soso_hip_decode_create_moe (null for a dense model).  With either flag the
- * qkv projection stores its rows and one more launch per layer normalises,
- * rotates and appends them.  flags 0 is soso_hip_decode_create(_moe). */
+ * soso_hip_decode_create_moe (null for a dense model).  The attention kernel
+ * finishes the q/k/v rows either way, so the flags add no launch.  flags 0
+ * is soso_hip_decode_create(_moe). */
 #define SOSO_HIP_DECODE_QK_NORM 1u
 #define SOSO_HIP_DECODE_ROPE_NEOX 2u
 int soso_hip_decode_create_ex(soso_hip *h, const char *model_key, size_t model_key_len,
