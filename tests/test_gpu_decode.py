@@ -688,14 +688,16 @@ def test_decode_step_with_moe_layers_matches_cpu(gpu, orc, kv_f16):
             gpu.dev_free(p)
 
 
-@pytest.mark.parametrize("qk_norm,neox,kv_f16,with_moe,prefill", [
-    (True, True, 0, False, 90),    # Qwen3's attention: QK norm and NeoX RoPE
-    (True, True, 0, False, 63),    # steps at 63 (one chunk) and 64 (a chunk of one new position)
-    (True, True, 1, True, 90),     # the same over soso's f16 cache, layer 1 an MoE layer
-    (True, False, 1, False, 127),  # QK norm alone; steps at 127 and 128
-    (False, True, 0, False, 0),    # NeoX RoPE alone; steps at 0 and 1
+@pytest.mark.parametrize("qk_norm,neox,kv_f16,with_moe,prefill,nh,nkv", [
+    (True, True, 0, False, 90, 8, 2),    # Qwen3's attention: QK norm and NeoX RoPE
+    (True, True, 0, False, 63, 8, 2),    # steps at 63 (one chunk) and 64 (a chunk of one new position)
+    (True, True, 1, True, 90, 8, 2),     # the same over soso's f16 cache, layer 1 an MoE layer
+    (True, False, 1, False, 127, 8, 2),  # QK norm alone; steps at 127 and 128
+    (False, True, 0, False, 0, 8, 2),    # NeoX RoPE alone; steps at 0 and 1
+    (True, True, 1, False, 70, 16, 2),   # groups of 8 query heads (Qwen3-30B-A3B's 32 / 4)
+    (True, True, 0, False, 70, 4, 4),    # one query head per KV head
 ])
-def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with_moe, prefill):
+def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with_moe, prefill, nh, nkv):
     """soso_hip_decode_create_ex with SOSO_HIP_DECODE_QK_NORM (each q and k
     head RMS-normalised with the layer's attn_q_norm / attn_k_norm before RoPE,
     layer.rs:1164-1180) and SOSO_HIP_DECODE_ROPE_NEOX (rope_cabezas' NeoX
@@ -705,10 +707,10 @@ def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with
     chunk ends) against the oracle's composition: logits within relative L2
     1e-5, the greedy token, and the K/V rows written at `prefill` under the
     bar of test_decode_step_matches_cpu."""
-    L, H, nh, nkv, F, V = 2, 1024, 8, 2, 2048, 1000
+    L, H, F, V = 2, 1024, 2048, 1000
     theta, eps, ctx = 1000000.0, 1e-6, 192
     flags = (1 if qk_norm else 0) | (2 if neox else 0)  # SOSO_HIP_DECODE_QK_NORM | _ROPE_NEOX
-    m = Model(orc, L, H, nh, nkv, F, V, 400 + flags + 4 * kv_f16, qk_norm=qk_norm, neox=neox)
+    m = Model(orc, L, H, nh, nkv, F, V, 400 + flags + 4 * kv_f16 + nh, qk_norm=qk_norm, neox=neox)
     m.upload(gpu)
     kpl = 11 if qk_norm else 9
     keys, moe, moe_layers = list(m.keys), None, None
@@ -721,7 +723,7 @@ def test_decode_step_qk_norm_and_neox_rope(gpu, orc, qk_norm, neox, kv_f16, with
     name = m.name + ".model"
     cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
                rope_theta=theta, rms_eps=eps, kv_f16=kv_f16)
-    print(f"decode step qk_norm={qk_norm} neox={neox} kv_f16={kv_f16} moe={with_moe}", flush=True)
+    print(f"decode step qk_norm={qk_norm} neox={neox} kv_f16={kv_f16} moe={with_moe} heads={nh}/{nkv}", flush=True)
     assert gpu.decode_create(name, cfg, keys, moe_layers=moe_layers, flags=flags), gpu.last_error()
     kvt, esz = (np.uint16, 2) if kv_f16 else (np.float32, 4)
     kc = np.zeros((L, ctx, m.kvd), np.float32)
