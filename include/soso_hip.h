@@ -186,6 +186,34 @@ int soso_hip_moe_ffn_dev(soso_hip *h, const char *layer_key, size_t layer_key_le
 int soso_hip_moe_ffn_dev_noalloc(soso_hip *h, const char *layer_key, size_t layer_key_len, const float *x_dev,
                                  size_t n, float *out_dev, int32_t *idx_dev, float *wgt_dev);
 
+/* ---- Gated DeltaNet (Qwen3.5's linear-attention layers) -------------------------
+ * GpuDispatch::gdn_bloque (gpu.rs:577-599): the recurrence of a GDN layer for
+ * a block of n tokens, on host buffers, synchronous.  With C = (2 n_k + n_v) d:
+ *   hist  [(kernel - 1 + n) x C]  the conv state (oldest row first), then the
+ *                                 n tokens' qkv projections
+ *   conv  [C x kernel]            ssm_conv1d weights
+ *   z     [n x n_v d]             attn_gate projections
+ *   decay [n x n_v]               exp(softplus(alpha + ssm_dt) * ssm_a)
+ *   beta  [n x n_v]               sigmoid(ssm_beta projection)
+ *   norm  [d]                     ssm_norm
+ *   state [n_v x d x d]           in and out (value head vh: row i, column j)
+ *   out   [n x n_v d]             the gated, normalised heads (ssm_out's input)
+ * Per token: causal conv + SiLU, q and k heads l2-normalised (q also scaled
+ * by 1 / sqrt(d)), per value head vh (q/k head vh mod n_k) delta = beta (v -
+ * decay S^T k), S <- decay S + k delta^T, o = S^T q, rmsnorm(o) * norm * silu(z)
+ * (bloque35.rs:372-465).  The conv state after the block is the last
+ * kernel - 1 rows of hist (the caller's, as in soso).  d must be 128 and
+ * kernel 1..16 (others decline); eps is the model's rms_eps. */
+int soso_hip_gdn_block(soso_hip *h, const float *hist, const float *conv, const float *z, const float *decay,
+                       const float *beta, const float *norm, float *state, float *out, size_t n, size_t n_k,
+                       size_t n_v, size_t d, size_t kernel, float eps);
+/* The same with every buffer in device memory, queued on the library's
+ * stream (no synchronisation; capturable in a HIP graph once its scratch of
+ * n * C floats has been grown by an earlier call). */
+int soso_hip_gdn_block_dev(soso_hip *h, const float *hist, const float *conv, const float *z, const float *decay,
+                           const float *beta, const float *norm, float *state, float *out, size_t n, size_t n_k,
+                           size_t n_v, size_t d, size_t kernel, float eps);
+
 /* ---- dense decode step resident on the device -----------------------------------
  * The device-resident decode of GpuDispatch::decode_preparar / decode_token
  * (gpu.rs:653-690) for a Llama-style dense model (LayerExecutor::forward_layer,

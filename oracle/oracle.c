@@ -945,6 +945,115 @@ done:
 }
 
 /* ---------------------------------------------------------------------------
+ * Gated DeltaNet (Qwen3.5): the recurrence of GpuDispatch::gdn_bloque
+ * (gpu.rs:577-599) as soso's CPU path computes it (bloque35.rs:372-465 from
+ * `hist` on; the decode layer forward_gdn_attn, arch.rs:586-768, is the same
+ * for one token).
+ * ------------------------------------------------------------------------- */
+
+/* arch.rs:358-360 (`sigmoid`). */
+float or_sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* arch.rs:362-368 (`softplus`): x above 20 passes through. */
+float or_softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+/* arch.rs:370-380 (`l2_normalize`): x *= 1 / sqrt(sum(x^2) + eps). */
+void or_l2_normalize(float *x, size_t n, float eps)
+{
+    float ss = 0.0f;
+    for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
+    float inv = 1.0f / sqrtf(ss + eps);
+    for (size_t i = 0; i < n; i++) x[i] *= inv;
+}
+
+/* arch.rs:382-415 (`gdn_step`): with S the d x d state (row i, column j),
+ * delta_j = (v_j - g sum_i S_ij k_i) beta; S_ij <- g S_ij + k_i delta_j;
+ * out_j = sum_i S_ij q_i over the updated state; sums in i order. */
+void or_gdn_step(float *state, const float *q, const float *k, const float *v, size_t d, float g, float beta,
+                 float *out)
+{
+    float delta[256];
+    if (d > 256) return;
+    for (size_t j = 0; j < d; j++) {
+        delta[j] = 0.0f;
+        out[j] = 0.0f;
+    }
+    for (size_t i = 0; i < d; i++)
+        for (size_t j = 0; j < d; j++) delta[j] += state[i * d + j] * k[i];
+    for (size_t j = 0; j < d; j++) delta[j] = (v[j] - g * delta[j]) * beta;
+    for (size_t i = 0; i < d; i++)
+        for (size_t j = 0; j < d; j++) {
+            float ns = g * state[i * d + j] + k[i] * delta[j];
+            state[i * d + j] = ns;
+            out[j] += ns * q[i];
+        }
+}
+
+/* bloque35.rs:391-395 / arch.rs:640-647: per token and value head, decay =
+ * exp(softplus(alpha + dt) * a) and beta = sigmoid(beta_raw), from the
+ * ssm_alpha / ssm_beta projections ([n][n_v]). */
+void or_gdn_gates(const float *alpha, const float *beta_raw, const float *dt, const float *a, size_t n, size_t n_v,
+                  float *decay, float *beta)
+{
+    for (size_t t = 0; t < n; t++)
+        for (size_t i = 0; i < n_v; i++) {
+            decay[t * n_v + i] = expf(or_softplus(alpha[t * n_v + i] + dt[i]) * a[i]);
+            beta[t * n_v + i] = or_sigmoid(beta_raw[t * n_v + i]);
+        }
+}
+
+/* GpuDispatch::gdn_bloque's contract, computed as bloque35.rs:412-465:
+ *   hist  [(kernel - 1 + n) x C]  the conv state (oldest first), then the
+ *                                 block's qkv projections (C = 2 n_k d + n_v d)
+ *   conv  [C x kernel]            causal conv weights
+ *   z [n x n_v d], decay / beta [n x n_v], norm [d]
+ *   state [n_v x d x d]           in and out
+ *   out   [n x n_v d]
+ * Per token: u = silu(conv over hist rows t .. t + kernel - 1); q and k heads
+ * l2-normalised, q scaled by 1 / sqrt(d); per value head vh (q/k head
+ * vh mod n_k): gdn_step, rmsnorm(o, norm, eps), o *= silu(z).  The conv
+ * state after the block (the last kernel - 1 rows of hist) is the caller's. */
+int or_gdn_block(const float *hist, const float *conv, const float *z, const float *decay, const float *beta,
+                 const float *norm, float *state, float *out, size_t n, size_t n_k, size_t n_v, size_t d,
+                 size_t kernel, float eps)
+{
+    if (d == 0 || d > 256 || kernel == 0 || n_k == 0 || n_v == 0) return -1;
+    const size_t qk_dim = n_k * d, v_dim = n_v * d, C = 2 * qk_dim + v_dim, prev = kernel - 1;
+    float *ups = (float *)malloc(n * C * sizeof(float));
+    if (!ups) return -1;
+    const float scale = 1.0f / sqrtf((float)d);
+    for (size_t t = 0; t < n; t++) {
+        float *up = ups + t * C;
+        for (size_t ch = 0; ch < C; ch++) {
+            float acc = 0.0f;
+            for (size_t k = 0; k < prev; k++) acc += conv[ch * kernel + k] * hist[(t + k) * C + ch];
+            acc += conv[ch * kernel + prev] * hist[(t + prev) * C + ch];
+            up[ch] = or_silu(acc);
+        }
+        for (size_t hh = 0; hh < n_k; hh++) {
+            or_l2_normalize(up + hh * d, d, eps);
+            or_l2_normalize(up + qk_dim + hh * d, d, eps);
+        }
+        for (size_t i = 0; i < qk_dim; i++) up[i] *= scale;
+    }
+    for (size_t vh = 0; vh < n_v; vh++) {
+        const size_t kh = vh % n_k;
+        float *st = state + vh * d * d;
+        for (size_t t = 0; t < n; t++) {
+            const float *base = ups + t * C;
+            float *o = out + t * v_dim + vh * d;
+            const float *g = z + t * v_dim + vh * d;
+            or_gdn_step(st, base + kh * d, base + qk_dim + kh * d, base + 2 * qk_dim + vh * d, d,
+                        decay[t * n_v + vh], beta[t * n_v + vh], o);
+            or_rmsnorm(o, norm, d, eps);
+            for (size_t i = 0; i < d; i++) o[i] *= or_silu(g[i]);
+        }
+    }
+    free(ups);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------------
  * Synthetic inputs: counter-based SplitMix64 keyed by (seed, stream, index),
  * integer-only so that the device generator of the HIP library produces the
  * same bytes.  Normals are Irwin-Hall(12) over 16-bit uniforms, computed

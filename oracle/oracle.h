@@ -132,6 +132,18 @@ int or_moe_ffn(const float *router, size_t n_exp, size_t h, size_t ffn, size_t t
                uint8_t dtype_gu, uint8_t dtype_down, const float *x, float *out, int32_t *idx_out,
                float *w_out, int threads, int avx2);
 
+/* ---- Gated DeltaNet (GpuDispatch::gdn_bloque) ------------------------------ */
+float or_sigmoid(float x);
+float or_softplus(float x);
+void or_l2_normalize(float *x, size_t n, float eps);
+void or_gdn_step(float *state, const float *q, const float *k, const float *v, size_t d, float g, float beta,
+                 float *out);
+void or_gdn_gates(const float *alpha, const float *beta_raw, const float *dt, const float *a, size_t n, size_t n_v,
+                  float *decay, float *beta);
+int or_gdn_block(const float *hist, const float *conv, const float *z, const float *decay, const float *beta,
+                 const float *norm, float *state, float *out, size_t n, size_t n_k, size_t n_v, size_t d,
+                 size_t kernel, float eps);
+
 /* ---- synthetic, counter-based generators ---------------------------------- */
 uint64_t or_rng(uint64_t seed, uint64_t stream, uint64_t i);
 float or_normal(uint64_t seed, uint64_t stream, uint64_t i);

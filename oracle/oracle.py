@@ -57,6 +57,12 @@ _PROTO = {
     "or_argmax": (C.c_uint32, [_P, _S]),
     "or_attention_f32": (None, [_P, _P, _P, _S, _S, _S, _S, _P]),
     "or_moe_ffn": (_I, [_P, _S, _S, _S, _S, _P, _P, _P, _U8, _U8, _P, _P, _P, _P, _I, _I]),
+    "or_sigmoid": (_F, [_F]),
+    "or_softplus": (_F, [_F]),
+    "or_l2_normalize": (None, [_P, _S, _F]),
+    "or_gdn_step": (None, [_P, _P, _P, _P, _S, _F, _F, _P]),
+    "or_gdn_gates": (None, [_P, _P, _P, _P, _S, _S, _P, _P]),
+    "or_gdn_block": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _S, _F]),
     "or_rng": (_U64, [_U64, _U64, _U64]),
     "or_normal": (_F, [_U64, _U64, _U64]),
     "or_synth_q4_k": (None, [_P, _S, _S, _U64, _U64]),
@@ -217,6 +223,19 @@ def moe_ffn(router, n_exp, h, ffn, top_k, gate, up, down, dtype_gu, dtype_down, 
     if rc != 0:
         raise ValueError("moe_ffn failed")
     return out, idx, w
+
+
+def gdn_block(hist, conv, z, decay, beta, norm, state, n, n_k, n_v, d, kernel, eps):
+    """GpuDispatch::gdn_bloque on the CPU: returns (out [n x n_v d], state');
+    `state` is not modified."""
+    st = np.array(state, dtype=np.float32, copy=True)
+    out = np.empty(n * n_v * d, dtype=np.float32)
+    hist, conv, z, decay, beta, norm = (f32(a) for a in (hist, conv, z, decay, beta, norm))
+    rc = lib().or_gdn_block(_p(hist), _p(conv), _p(z), _p(decay), _p(beta), _p(norm), _p(st), _p(out), n, n_k, n_v,
+                            d, kernel, np.float32(eps))
+    if rc != 0:
+        raise ValueError("gdn_block failed")
+    return out, st
 
 
 def rel_l2(a, b):

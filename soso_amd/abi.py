@@ -85,6 +85,8 @@ PROTOTYPES = {
     "soso_hip_moe_register": (_I, [_P, C.c_char_p, _S, C.c_char_p, _S, _P, _P, _S, _S, _S, _S]),
     "soso_hip_moe_ffn_dev": (_I, [_P, C.c_char_p, _S, _P, _S, _P, _P, _P]),
     "soso_hip_moe_ffn_dev_noalloc": (_I, [_P, C.c_char_p, _S, _P, _S, _P, _P, _P]),
+    "soso_hip_gdn_block": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _S, C.c_float]),
+    "soso_hip_gdn_block_dev": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S, _S, _S, C.c_float]),
     "soso_hip_decode_create": (_I, [_P, C.c_char_p, _S, C.POINTER(DecodeCfg), _P, _P, _I]),
     "soso_hip_decode_create_moe": (_I, [_P, C.c_char_p, _S, C.POINTER(DecodeCfg), _P, _P, _P, _P, _I]),
     "soso_hip_decode_moe_routing_dev": (_I, [_P, C.c_char_p, _S, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),

@@ -11,7 +11,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libsoso_hip.so")
-SOURCES = ["runtime.hip", "k_matvec.hip", "k_moe.hip", "k_synth.hip", "k_decode.hip", "k_mfma.hip"]
+SOURCES = ["runtime.hip", "k_matvec.hip", "k_moe.hip", "k_synth.hip", "k_decode.hip", "k_mfma.hip", "k_gdn.hip"]
 
 # Packed FP32 VALU ops are disabled for all device code; hipcc's host pass
 # warns that it does not know the feature, which is harmless.

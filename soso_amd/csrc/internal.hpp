@@ -227,6 +227,12 @@ int launch_vec_add(soso_hip *h, float *y, const float *v, size_t n);
 // the cache's element type) into a head-major cache at positions row0...
 int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, bool cache_f16, int kv_dim,
                       int head_dim, int ctx, int row0, int n_rows);
+// (k_gdn.hip) Gated DeltaNet block (GpuDispatch::gdn_bloque): null when the
+// shape runs, else why not; the launch needs u, n x (2 n_k + n_v) d floats.
+const char *gdn_unsupported(size_t n, size_t n_k, size_t n_v, size_t d, size_t kernel);
+int launch_gdn_block(soso_hip *h, const float *hist, const float *conv, const float *z, const float *decay,
+                     const float *beta, const float *norm, float *state, float *out, float *u, int n, int n_k,
+                     int n_v, int kernel, float eps);
 // (k_synth.hip)
 int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t cols, uint64_t seed,
                      uint64_t stream);

@@ -453,6 +453,78 @@ int soso_hip_matvec_batch(soso_hip *h, const soso_hip_op *ops, size_t n_ops, uin
     return worst;
 }
 
+// ---------------------------------------------------------------------------
+// Gated DeltaNet block (GpuDispatch::gdn_bloque, gpu.rs:577-599)
+// ---------------------------------------------------------------------------
+static int gdn_args_ok(soso_hip *h, const void *hist, const void *conv, const void *z, const void *decay,
+                       const void *beta, const void *norm, const void *state, const void *out, size_t n, size_t n_k,
+                       size_t n_v, size_t d, size_t kernel)
+{
+    if (!hist || !conv || !z || !decay || !beta || !norm || !state || !out)
+        return set_err(h, SOSO_HIP_ERR_ARG, "gdn_block: null buffer");
+    if (const char *why = gdn_unsupported(n, n_k, n_v, d, kernel)) return set_err(h, SOSO_HIP_DECLINED, why);
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_gdn_block(soso_hip *h, const float *hist, const float *conv, const float *z, const float *decay,
+                       const float *beta, const float *norm, float *state, float *out, size_t n, size_t n_k,
+                       size_t n_v, size_t d, size_t kernel, float eps)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    int rc = gdn_args_ok(h, hist, conv, z, decay, beta, norm, state, out, n, n_k, n_v, d, kernel);
+    if (rc != SOSO_HIP_OK) return rc;
+    rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    const size_t C = (2 * n_k + n_v) * d, vd = n_v * d;
+    // one device buffer, 256-byte aligned pieces: the inputs, the state, the
+    // output and the conv/normalisation result u
+    const size_t sz[] = {(kernel - 1 + n) * C, C * kernel, n * vd, n * n_v, n * n_v, d, n_v * d * d, n * vd, n * C};
+    size_t off[9], total = 0;
+    for (int i = 0; i < 9; i++) {
+        off[i] = total;
+        total += (sz[i] * 4 + 255) & ~(size_t)255;
+    }
+    char *dev = (char *)scratch_get(h, 7, total);
+    if (!dev) return set_err(h, SOSO_HIP_ERR_NOMEM, "gdn_block: scratch");
+    float *p[9];
+    for (int i = 0; i < 9; i++) p[i] = (float *)(dev + off[i]);
+    const float *src[7] = {hist, conv, z, decay, beta, norm, state};
+    for (int i = 0; i < 7 && rc == SOSO_HIP_OK; i++)
+        rc = hip_check(h, hipMemcpyAsync(p[i], src[i], sz[i] * 4, hipMemcpyHostToDevice, h->stream), "gdn upload");
+    if (rc == SOSO_HIP_OK)
+        rc = launch_gdn_block(h, p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7], p[8], (int)n, (int)n_k, (int)n_v,
+                              (int)kernel, eps);
+    if (rc == SOSO_HIP_OK)
+        rc = hip_check(h, hipMemcpyAsync(out, p[7], sz[7] * 4, hipMemcpyDeviceToHost, h->stream), "gdn out");
+    if (rc == SOSO_HIP_OK)
+        rc = hip_check(h, hipMemcpyAsync(state, p[6], sz[6] * 4, hipMemcpyDeviceToHost, h->stream), "gdn state");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "gdn sync");
+    if (rc != SOSO_HIP_OK) {
+        (void)hip_release(h, hipStreamSynchronize(h->stream), "gdn drain");
+        return rc;
+    }
+    for (int i = 0; i < 7; i++) h->stats.bytes_up += sz[i] * 4;
+    h->stats.bytes_down += (sz[6] + sz[7]) * 4;
+    clk.done();
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_gdn_block_dev(soso_hip *h, const float *hist, const float *conv, const float *z, const float *decay,
+                           const float *beta, const float *norm, float *state, float *out, size_t n, size_t n_k,
+                           size_t n_v, size_t d, size_t kernel, float eps)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    int rc = gdn_args_ok(h, hist, conv, z, decay, beta, norm, state, out, n, n_k, n_v, d, kernel);
+    if (rc != SOSO_HIP_OK) return rc;
+    rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    float *u = (float *)scratch_get(h, 4, n * (2 * n_k + n_v) * d * 4);
+    if (!u) return set_err(h, SOSO_HIP_ERR_NOMEM, "gdn_block_dev: scratch (or growing it during capture)");
+    return launch_gdn_block(h, hist, conv, z, decay, beta, norm, state, out, u, (int)n, (int)n_k, (int)n_v,
+                            (int)kernel, eps);
+}
+
 int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const float *w, const float *xs, size_t n,
                          size_t hdim, size_t n_exp, size_t top_k, int32_t *idx, float *wgt)
 {

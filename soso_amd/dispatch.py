@@ -284,6 +284,24 @@ class HipGpu:
         return self._rc(self.lib.soso_hip_moe_ffn_dev_noalloc(self.h, k, kl, x_dev, n, out_dev, idx_dev, wgt_dev),
                         f"moe_ffn_dev_noalloc {layer_key}")
 
+    # -- Gated DeltaNet (GpuDispatch::gdn_bloque) ---------------------------------
+    def gdn_block(self, hist, conv, z, decay, beta, norm, state, n, n_k, n_v, d, kernel, eps):
+        """gdn_bloque on host arrays: returns out [n * n_v * d]; `state` (f32,
+        contiguous) is updated in place.  False when the shape is declined."""
+        f = [np.ascontiguousarray(a, dtype=np.float32) for a in (hist, conv, z, decay, beta, norm)]
+        if not (isinstance(state, np.ndarray) and state.dtype == np.float32 and state.flags.c_contiguous):
+            raise ValueError("gdn_block: state must be a contiguous float32 array (updated in place)")
+        out = np.zeros(n * n_v * d, np.float32)
+        ok = self._rc(self.lib.soso_hip_gdn_block(self.h, *[a.ctypes.data for a in f], state.ctypes.data,
+                                                  out.ctypes.data, n, n_k, n_v, d, kernel, C.c_float(eps)),
+                      "gdn_block")
+        return out if ok else False
+
+    def gdn_block_dev(self, hist, conv, z, decay, beta, norm, state, out, n, n_k, n_v, d, kernel, eps):
+        """gdn_bloque on device pointers, queued on the library's stream."""
+        return self._rc(self.lib.soso_hip_gdn_block_dev(self.h, hist, conv, z, decay, beta, norm, state, out, n, n_k,
+                                                        n_v, d, kernel, C.c_float(eps)), "gdn_block_dev")
+
     # -- dense decode step resident on the device (decode_preparar / decode_token) --
     def decode_create(self, model_key, cfg, keys, drop_sources=False, moe_layers=None, flags=0):
         """cfg: dict of soso_hip_decode_cfg fields; keys: 9 per layer (attn_norm,
