@@ -188,6 +188,58 @@ def read_probe_bytes(var, nbytes):
     return nbytes // 1024 * 1024 if var == "chunk" else nbytes // 16 * 16
 
 
+def time_gdn(g, n, steps, layers=8, n_k=16, n_v=32, d=128, kernel=4, seed=41, eager=False):
+    """A Qwen3-Next-80B-A3B-like Gated DeltaNet layer's recurrence
+    (soso_hip_gdn_block_dev, GpuDispatch::gdn_bloque) for a block of `n`
+    tokens: 16 q/k heads, 32 value heads of 128, conv kernel 4; seeded inputs
+    and states (N(0, 1) projections, state ~ N(0, 0.05), decay in (0, 1],
+    beta in (0, 1)).  `layers` independent states (32 x 128 x 128 f32 = 2 MiB
+    each) are rotated so each call reads its state from HBM.  Returns (ms per
+    call, algorithmic bytes per call: the state read and written, the conv
+    history and weights, z, the gates and norm, the output, and the conv
+    result u the two launches hand over)."""
+    C, vd = (2 * n_k + n_v) * d, n_v * d
+    sizes = [(kernel - 1 + n) * C, C * kernel, n * vd, n * n_v, n * n_v, d, n_v * d * d, n * vd]
+    bufs = []
+    try:
+        for layer in range(layers):
+            ptrs = []
+            for i, sz in enumerate(sizes):
+                p = g.dev_alloc(sz * 4)
+                ptrs.append(p)
+                sigma = (1.0, 0.5, 1.0, 0.3, 1.0, 0.1, 0.05, 1.0)[i]
+                g.synth_normal(p, sz, sigma, seed + layer, i)
+            # decay = exp(-|N|) in (0, 1] and beta = sigmoid(N) in (0, 1), as the model's gates give them
+            for i, f in ((3, lambda a: np.exp(-np.abs(a))), (4, lambda a: 1.0 / (1.0 + np.exp(-a)))):
+                a = g.d2h(ptrs[i], (sizes[i],), np.float32)
+                g.h2d(ptrs[i], f(a).astype(np.float32))
+            bufs.append(ptrs)
+        call = [0]
+
+        def one():
+            b = bufs[call[0] % layers]
+            call[0] += 1
+            assert g.gdn_block_dev(*b, n, n_k, n_v, d, kernel, 1e-6), g.last_error()
+        for _ in range(3):
+            one()
+        g.sync()
+        if eager:
+            g.event_record(0)
+            for _ in range(steps):
+                one()
+            g.event_record(1)
+            g.sync()
+            ms = g.event_elapsed(0, 1) / steps
+        else:
+            ms = _timed_graph(g, lambda: [one() for _ in range(steps)], steps)[0]
+    finally:
+        for ptrs in bufs:
+            for p in ptrs:
+                g.dev_free(p)
+    nbytes = 4 * (sizes[0] + sizes[1] + sizes[2] + sizes[3] + sizes[4] + sizes[5] + 2 * sizes[6] + sizes[7] + 2 * n * C)
+    return ms, nbytes
+
+
 def time_moe(g, n, steps, layers=4, n_x=8, seed=11, eager=False):
     """Qwen3-30B-A3B-like MoE FFN (hidden 2048, 128 experts of
     intermediate 768, top-8, Q4_K experts, f32 router ~ N(0, 0.02)), `n`
@@ -731,7 +783,7 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="with --only: launch the timed steps directly instead of replaying a graph")
     ap.add_argument("--only", choices=["matvec", "q8_0", "down", "decode", "moe1", "moe32", "head", "matmul",
-                                       "matmul_q8", "batch8", "decode_moe", "readprobe"],
+                                       "matmul_q8", "batch8", "decode_moe", "gdn", "readprobe"],
                     help="run one workload and print its own JSON line (for profiling runs)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -781,6 +833,12 @@ def main():
             ms_h, _, tok_h, _ = time_decode_8b(g, max(10, args.steps // 50), kv_f16=True, eager=args.eager)
             res = {"llama8b_decode_ms_per_token": round(ms, 4), "greedy_token": tok,
                    "llama8b_decode_kv_f16_ms_per_token": round(ms_h, 4), "greedy_token_kv_f16": tok_h}
+        elif args.only == "gdn":
+            res = {}
+            for n in (1, 64):
+                ms, nb = time_gdn(g, n, max(40, args.steps // 10), eager=args.eager)
+                res[f"gdn_block_n{n}_us"] = round(ms * 1e3, 3)
+                res[f"gdn_block_n{n}_GB_s"] = round(nb / (ms * 1e-3) / 1e9, 1)
         elif args.only == "readprobe":
             nb = 14336 * ROW_BYTES[Q4K](4096)  # the headline's weight bytes
             small = time_read_probe(g, nb, 16, max(100, args.steps // 2), 20)
@@ -866,6 +924,12 @@ def main():
                 "us_per_layer": round(ms_m * 1e3, 3), "tokens_per_s_layer": round(n / (ms_m * 1e-3), 1),
                 "GB_s": round(b_m / (ms_m * 1e-3) / 1e9, 1), "frac_hbm": round(b_m / (ms_m * 1e-3) / 1e9 / PEAK_GBS, 4),
                 "bytes": int(b_m), "distinct_experts": round(u_m, 2)}
+        for n in (1, 64):
+            ms_g, b_g = time_gdn(g, n, max(40, args.steps // 10))
+            extra[f"gdn_block_qwen3_next_like_n{n}"] = {
+                "us": round(ms_g * 1e3, 3), "GB_s": round(b_g / (ms_g * 1e-3) / 1e9, 1),
+                "frac_hbm": round(b_g / (ms_g * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": int(b_g), "tokens": n,
+                "shape": "16 q/k heads, 32 value heads of 128, conv kernel 4 (state 2 MiB, 8 rotated layers)"}
         ms_d, b_d, tok_d, host_d = time_decode_8b(g, max(10, args.steps // 10))
         extra["llama8b_decode_ctx4096"] = {
             "ms_per_token": round(ms_d, 4), "tokens_per_s": round(1e3 / ms_d, 1),

@@ -18,6 +18,8 @@
 //               then rmsnorm(o) with the ssm_norm weights and o *= silu(z).
 // The column sums run as 16-row partial sums per thread, combined over the 8
 // row groups through LDS (the CPU sums i in order; the bar is relative L2).
+// The next token's q, k, v and z are requested while the current token's
+// recurrence runs.
 // State traffic per block: 2 * n_v d^2 * 4 bytes (2 MiB each way for 32 heads
 // of 128), independent of n.
 #include "internal.hpp"
@@ -27,6 +29,12 @@ constexpr int GDN_RG = 8;              // row groups of the state per workgroup
 constexpr int GDN_RPT = GDN_D / GDN_RG; // state rows per thread
 
 __device__ __forceinline__ float gdn_silu(float x) { return x / (1.0f + expf(-x)); }
+
+// Workgroup barrier for LDS only: LDS operations complete, then s_barrier,
+// without waiting for outstanding global loads (__syncthreads' fence would
+// wait for the next token's q/k/v/z, requested ahead on purpose).  The memory
+// clobber keeps the compiler from moving memory operations across it.
+__device__ __forceinline__ void gdn_lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // sum over the 128 threads of a two-wavefront workgroup, returned to all
 __device__ __forceinline__ float gdn_sum128(float v, float *red)
@@ -75,29 +83,41 @@ __global__ void __launch_bounds__(GDN_D * GDN_RG) k_gdn_rec(const float *__restr
     float S[GDN_RPT];
 #pragma unroll
     for (int ii = 0; ii < GDN_RPT; ii++) S[ii] = st[(size_t)(r * GDN_RPT + ii) * D + j];
-    for (int t = 0; t < n; t++) {
-        const float *ut = u + (size_t)t * C;
+    // threads 0 .. 127 carry one token's q, k, v, z ahead of the recurrence
+    float nq = 0.0f, nk = 0.0f, nv = 0.0f, nz = 0.0f;
+    auto fetch = [&](int t) {
         if (tid < D) {
-            qs[tid] = ut[kh * D + tid];
-            ks[tid] = ut[qk + kh * D + tid];
-            vs[tid] = ut[2 * qk + vh * D + tid];
-            zs[tid] = z[(size_t)t * vd + vh * D + tid];
+            const float *ut = u + (size_t)t * C;
+            nq = ut[kh * D + tid];
+            nk = ut[qk + kh * D + tid];
+            nv = ut[2 * qk + vh * D + tid];
+            nz = z[(size_t)t * vd + vh * D + tid];
+        }
+    };
+    fetch(0);
+    for (int t = 0; t < n; t++) {
+        if (tid < D) {
+            qs[tid] = nq;
+            ks[tid] = nk;
+            vs[tid] = nv;
+            zs[tid] = nz;
         }
         const float g = decay[(size_t)t * n_v + vh], b = beta[(size_t)t * n_v + vh];
-        __syncthreads();
+        gdn_lds_barrier();
+        if (t + 1 < n) fetch(t + 1); // in flight during this token's recurrence
         // delta_j = (v_j - g sum_i S_ij k_i) beta
         float p = 0.0f;
 #pragma unroll
         for (int ii = 0; ii < GDN_RPT; ii++) p = __fadd_rn(p, __fmul_rn(S[ii], ks[r * GDN_RPT + ii]));
         part[r][j] = p;
-        __syncthreads();
+        gdn_lds_barrier();
         if (tid < D) {
             float s = part[0][j];
 #pragma unroll
             for (int q = 1; q < GDN_RG; q++) s = __fadd_rn(s, part[q][j]);
             dl[j] = __fmul_rn(__fsub_rn(vs[j], __fmul_rn(g, s)), b);
         }
-        __syncthreads();
+        gdn_lds_barrier();
         // S_ij <- g S_ij + k_i delta_j;  o_j = sum_i S_ij q_i (updated state)
         const float dj = dl[j];
         p = 0.0f;
@@ -108,7 +128,7 @@ __global__ void __launch_bounds__(GDN_D * GDN_RG) k_gdn_rec(const float *__restr
             p = __fadd_rn(p, __fmul_rn(S[ii], qs[i]));
         }
         part[r][j] = p;
-        __syncthreads();
+        gdn_lds_barrier();
         // o_j in threads 0 .. 127 (wavefronts 0 and 1); rmsnorm over the head
         // (gemm.rs:93-100), then the SiLU gate
         float o = 0.0f;
@@ -119,13 +139,13 @@ __global__ void __launch_bounds__(GDN_D * GDN_RG) k_gdn_rec(const float *__restr
         }
         const float ws = seg_sum_dpp<64>(tid < D ? o * o : 0.0f);
         if ((tid & 63) == 63 && tid < D) red[tid >> 6] = ws;
-        __syncthreads();
+        gdn_lds_barrier();
         if (tid < D) {
             const float scale = 1.0f / sqrtf((red[0] + red[1]) / (float)D + eps);
             o = __fmul_rn(__fmul_rn(o, scale), norm[j]);
             out[(size_t)t * vd + vh * D + j] = __fmul_rn(o, gdn_silu(zs[j]));
         }
-        __syncthreads(); // qs / ks / vs / zs / part / red reused by the next token
+        gdn_lds_barrier(); // qs / ks / vs / zs / part / red reused by the next token
     }
 #pragma unroll
     for (int ii = 0; ii < GDN_RPT; ii++) st[(size_t)(r * GDN_RPT + ii) * D + j] = S[ii];
