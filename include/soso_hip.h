@@ -134,10 +134,24 @@ int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const flo
  * and down for the tokens choosing it; sum[n x h] receives, per token, the
  * weighted sum (weights wgt[n x top_k]) of the experts resolved here in
  * ranking order.  done[i] = 1 for the experts resolved.  Returns 1 if all were
- * resolved, 0 if some were declined (their contribution is not in sum). */
+ * resolved, 0 if some were declined (their contribution is not in sum).  A
+ * shared expert computed by soso_hip_moe_shared for the same n and hdim is
+ * added to sum after the ranked experts (and consumed); one computed for
+ * another block makes the call fail (< 0). */
 int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, size_t ffn, size_t top_k,
                            const float *wgt, const soso_hip_expert *exps, size_t n_exps, float *sum,
                            uint8_t *done);
+/* GpuDispatch::moe_compartido (gpu.rs:518-534): the shared expert of an MoE
+ * block of n tokens (xs [n x hdim]), c_t = down(silu(gate x_t) * up x_t) *
+ * sigmoid(x_t . pg_w) (soso's CPU path, bloque35.rs:950-1005), computed and
+ * kept on the device for the next soso_hip_experts_block call with the same n
+ * and hdim, which adds it to its sum.  keys / key_lens / w / w_len / dtype:
+ * gate [ffn x hdim], up [ffn x hdim], down [hdim x ffn] (quantized; uploaded
+ * on first use under their keys, as soso_hip_expert's); pg_w: the
+ * ffn_gate_inp_shexp row, hdim f32.  1 = computed, 0 = declined, < 0 error. */
+int soso_hip_moe_shared(soso_hip *h, const char *const *keys, const size_t *key_lens, const uint8_t *const *w,
+                        const size_t *w_len, const uint8_t *dtype, const float *pg_w, const float *xs, size_t n,
+                        size_t hdim, size_t ffn);
 
 /* ---- MoE FFN resident on the device --------------------------------------------
  * The FFN half of GpuDispatch::moe_capa (gpu.rs; CudaGpu::moe_ejecutar,

@@ -945,6 +945,39 @@ done:
 }
 
 /* ---------------------------------------------------------------------------
+ * Shared expert of an MoE block (GpuDispatch::moe_compartido, gpu.rs:518-534)
+ * as soso's CPU path computes it (bloque35.rs:952-985): per token t, puerta =
+ * sigmoid(x_t . pg_w) (the f32 row ffn_gate_inp_shexp), gate and up matvecs,
+ * swiglu_inplace, down; out_t = c_t * puerta (the block sum adds it last,
+ * bloque35.rs:1000-1005).
+ * ------------------------------------------------------------------------- */
+int or_moe_shared(const float *pg_w, size_t h, size_t ffn, const uint8_t *gate, const uint8_t *up,
+                  const uint8_t *down, uint8_t dtype_gu, uint8_t dtype_down, const float *xs, size_t n, float *out)
+{
+    float *g = (float *)malloc(ffn * sizeof(float));
+    float *u = (float *)malloc(ffn * sizeof(float));
+    int rc = -1;
+    if (!g || !u) goto done;
+    for (size_t t = 0; t < n; t++) {
+        const float *x = xs + t * h;
+        float pg;
+        if (or_matvec_par(OR_DTYPE_F32, (const uint8_t *)pg_w, 1, h, x, &pg, 1, 0)) goto done;
+        const float puerta = 1.0f / (1.0f + expf(-pg));
+        if (or_matvec_par(dtype_gu, gate, ffn, h, x, g, 1, 0) || or_matvec_par(dtype_gu, up, ffn, h, x, u, 1, 0))
+            goto done;
+        or_swiglu(u, g, ffn);
+        float *o = out + t * h;
+        if (or_matvec_par(dtype_down, down, h, ffn, u, o, 1, 0)) goto done;
+        for (size_t i = 0; i < h; i++) o[i] = o[i] * puerta;
+    }
+    rc = 0;
+done:
+    free(g);
+    free(u);
+    return rc;
+}
+
+/* ---------------------------------------------------------------------------
  * Gated DeltaNet (Qwen3.5): the recurrence of GpuDispatch::gdn_bloque
  * (gpu.rs:577-599) as soso's CPU path computes it (bloque35.rs:372-465 from
  * `hist` on; the decode layer forward_gdn_attn, arch.rs:586-768, is the same

@@ -132,6 +132,10 @@ int or_moe_ffn(const float *router, size_t n_exp, size_t h, size_t ffn, size_t t
                uint8_t dtype_gu, uint8_t dtype_down, const float *x, float *out, int32_t *idx_out,
                float *w_out, int threads, int avx2);
 
+/* ---- shared expert of an MoE block (GpuDispatch::moe_compartido) ---------- */
+int or_moe_shared(const float *pg_w, size_t h, size_t ffn, const uint8_t *gate, const uint8_t *up,
+                  const uint8_t *down, uint8_t dtype_gu, uint8_t dtype_down, const float *xs, size_t n, float *out);
+
 /* ---- Gated DeltaNet (GpuDispatch::gdn_bloque) ------------------------------ */
 float or_sigmoid(float x);
 float or_softplus(float x);

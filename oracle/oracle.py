@@ -57,6 +57,7 @@ _PROTO = {
     "or_argmax": (C.c_uint32, [_P, _S]),
     "or_attention_f32": (None, [_P, _P, _P, _S, _S, _S, _S, _P]),
     "or_moe_ffn": (_I, [_P, _S, _S, _S, _S, _P, _P, _P, _U8, _U8, _P, _P, _P, _P, _I, _I]),
+    "or_moe_shared": (_I, [_P, _S, _S, _P, _P, _P, _U8, _U8, _P, _S, _P]),
     "or_sigmoid": (_F, [_F]),
     "or_softplus": (_F, [_F]),
     "or_l2_normalize": (None, [_P, _S, _F]),
@@ -223,6 +224,16 @@ def moe_ffn(router, n_exp, h, ffn, top_k, gate, up, down, dtype_gu, dtype_down, 
     if rc != 0:
         raise ValueError("moe_ffn failed")
     return out, idx, w
+
+
+def moe_shared(pg_w, h, ffn, gate, up, down, dtype_gu, dtype_down, xs, n):
+    """The shared expert of an MoE block for n tokens: out [n * h]."""
+    pg_w, xs = f32(pg_w), f32(xs)
+    g, u, d = (np.ascontiguousarray(a, dtype=np.uint8) for a in (gate, up, down))
+    out = np.empty(n * h, dtype=np.float32)
+    if lib().or_moe_shared(_p(pg_w), h, ffn, _p(g), _p(u), _p(d), dtype_gu, dtype_down, _p(xs), n, _p(out)) != 0:
+        raise ValueError("moe_shared failed")
+    return out
 
 
 def gdn_block(hist, conv, z, decay, beta, norm, state, n, n_k, n_v, d, kernel, eps):

@@ -82,6 +82,7 @@ PROTOTYPES = {
     "soso_hip_matvec_batch": (_I, [_P, _P, _S, _P]),
     "soso_hip_router_topk": (_I, [_P, C.c_char_p, _S, _P, _P, _S, _S, _S, _S, _P, _P]),
     "soso_hip_experts_block": (_I, [_P, _P, _S, _S, _S, _S, _P, _P, _S, _P, _P]),
+    "soso_hip_moe_shared": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _S, _S, _S]),
     "soso_hip_moe_register": (_I, [_P, C.c_char_p, _S, C.c_char_p, _S, _P, _P, _S, _S, _S, _S]),
     "soso_hip_moe_ffn_dev": (_I, [_P, C.c_char_p, _S, _P, _S, _P, _P, _P]),
     "soso_hip_moe_ffn_dev_noalloc": (_I, [_P, C.c_char_p, _S, _P, _S, _P, _P, _P]),

@@ -140,7 +140,7 @@ struct soso_hip {
     // the scratch pointers it was captured with, so a slot outgrown while any
     // graph exists is retired, not freed: retired buffers are freed once no
     // graph is left (graph_destroy) or with the handle.
-    static constexpr int N_SCRATCH = 12;
+    static constexpr int N_SCRATCH = 14;
     void *scratch[N_SCRATCH] = {};
     size_t scratch_cap[N_SCRATCH] = {};
     std::vector<void *> retired;
@@ -157,6 +157,10 @@ struct soso_hip {
     void *fixed_scratch = nullptr;
     std::unordered_map<std::string, MoeLayer> moe_layers;
     std::unordered_map<std::string, DecodeModel> decode_models;
+    // soso_hip_moe_shared's output (n x hdim f32 in scratch slot 12), waiting
+    // for the next soso_hip_experts_block call, which adds it to its sum
+    bool shared_pending = false;
+    size_t shared_n = 0, shared_hdim = 0;
     std::vector<hipEvent_t> events; // per-launch timing slots
     std::vector<hipGraphExec_t> graphs;
     bool capturing = false;
@@ -227,6 +231,10 @@ int launch_vec_add(soso_hip *h, float *y, const float *v, size_t n);
 // the cache's element type) into a head-major cache at positions row0...
 int launch_kv_scatter(soso_hip *h, const void *src, bool src_f32, void *cache, bool cache_f16, int kv_dim,
                       int head_dim, int ctx, int row0, int n_rows);
+// (k_moe.hip) shared expert: u[i] = silu(g[i]) * u[i] (i < n); then per
+// token t (rows of hdim) y_t *= sigmoid(x_t . pg_w)
+int launch_shared_swiglu(soso_hip *h, const float *g, float *u, size_t n);
+int launch_shared_gate(soso_hip *h, const float *x, const float *pg_w, float *y, size_t n, size_t hdim);
 // (k_gdn.hip) Gated DeltaNet block (GpuDispatch::gdn_bloque): null when the
 // shape runs, else why not; the launch needs u, n x (2 n_k + n_v) d floats.
 const char *gdn_unsupported(size_t n, size_t n_k, size_t n_v, size_t d, size_t kernel);

@@ -24,6 +24,7 @@
 // ExpertoBloque, gpu.rs:176-186).
 #include "mv_core.hpp"
 
+#include <algorithm>
 #include <vector>
 
 // ---------------------------------------------------------------------------
@@ -1221,4 +1222,47 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
     const dim3 grid((unsigned)((hdim + 255) / 256), (unsigned)n);
     k_moe_combine<<<grid, 256, 0, h->stream>>>(s.ydown, wgt, use, (int)n, (int)hdim, (int)top_k, out);
     return hip_check(h, hipGetLastError(), "moe combine launch");
+}
+
+// ---------------------------------------------------------------------------
+// Shared expert of an MoE block (GpuDispatch::moe_compartido, gpu.rs:518-534;
+// soso's CPU path bloque35.rs:950-985): gate / up / down run as matmuls, then
+// these two finish it -- SwiGLU (gemm.rs:210-226) and the per-token sigmoid
+// gate sigmoid(x_t . ffn_gate_inp_shexp) (bloque35.rs:955-960).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_shared_swiglu(const float *__restrict__ g, float *__restrict__ u, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        u[i] = silu(g[i]) * u[i];
+}
+
+// one workgroup per token: the dot in one 256-thread reduction, then the scale
+__global__ void __launch_bounds__(256) k_shared_gate(const float *__restrict__ x, const float *__restrict__ pg_w,
+                                                      float *__restrict__ y, int hdim)
+{
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float *xt = x + (size_t)t * hdim;
+    float acc = 0.0f;
+    for (int i = tid; i < hdim; i += 256) acc = fmaf(xt[i], pg_w[i], acc);
+    acc = seg_sum_dpp<64>(acc);
+    if ((tid & 63) == 63) red[tid >> 6] = acc;
+    __syncthreads();
+    const float pg = (red[0] + red[1]) + (red[2] + red[3]);
+    const float s = 1.0f / (1.0f + expf(-pg));
+    float *yt = y + (size_t)t * hdim;
+    for (int i = tid; i < hdim; i += 256) yt[i] *= s;
+}
+
+int launch_shared_swiglu(soso_hip *h, const float *g, float *u, size_t n)
+{
+    const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+    k_shared_swiglu<<<grid, 256, 0, h->stream>>>(g, u, n);
+    return hip_check(h, hipGetLastError(), "shared swiglu launch");
+}
+
+int launch_shared_gate(soso_hip *h, const float *x, const float *pg_w, float *y, size_t n, size_t hdim)
+{
+    k_shared_gate<<<(unsigned)n, 256, 0, h->stream>>>(x, pg_w, y, (int)hdim);
+    return hip_check(h, hipGetLastError(), "shared gate launch");
 }

@@ -585,6 +585,10 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
     CallClock clk(h);
+    const bool pending = h->shared_pending;
+    h->shared_pending = false;
+    if (pending && (h->shared_n != n || h->shared_hdim != hdim))
+        return set_err(h, SOSO_HIP_ERR_ARG, "experts_block: the pending shared expert was computed for another block");
     const size_t dims[3][2] = {{ffn, hdim}, {ffn, hdim}, {hdim, ffn}};
     const size_t slots = n * top_k;
     // Resolvable experts: the three matrices resident (or uploadable), one
@@ -695,6 +699,9 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
         else
             rc = hip_check(h, hipMemsetAsync(sd, 0, n * hdim * 4, h->stream), "zero sum");
     }
+    // the shared expert of the same block (moe_shared, gpu.rs:518-521) joins
+    // the sum after the ranked experts, as soso adds it last (bloque35.rs:1000-1005)
+    if (rc == SOSO_HIP_OK && pending) rc = launch_vec_add(h, sd, (const float *)h->scratch[12], n * hdim);
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(sum, sd, n * hdim * 4, hipMemcpyDeviceToHost, h->stream), "sum");
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "experts sync");
     if (rc != SOSO_HIP_OK) {
@@ -706,6 +713,49 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
     h->stats.bytes_down += n * hdim * 4;
     clk.done();
     return all ? SOSO_HIP_OK : SOSO_HIP_DECLINED;
+}
+
+// ---- shared expert of an MoE block (GpuDispatch::moe_compartido) -------------
+int soso_hip_moe_shared(soso_hip *h, const char *const *keys, const size_t *key_lens, const uint8_t *const *w,
+                        const size_t *w_len, const uint8_t *dtype, const float *pg_w, const float *xs, size_t n,
+                        size_t hdim, size_t ffn)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!keys || !key_lens || !w || !w_len || !dtype || !pg_w || !xs || n == 0 || hdim == 0 || ffn == 0)
+        return set_err(h, SOSO_HIP_ERR_ARG, "moe_shared: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    h->shared_pending = false;
+    const size_t dims[3][2] = {{ffn, hdim}, {ffn, hdim}, {hdim, ffn}};
+    Weight *wt[3] = {};
+    for (int k = 0; k < 3; k++) {
+        if (!keys[k]) return set_err(h, SOSO_HIP_ERR_ARG, "moe_shared: key");
+        rc = get_weight(h, keys[k], key_lens[k], w[k], w_len[k], dtype[k], dims[k][0], dims[k][1], &wt[k]);
+        if (rc != SOSO_HIP_OK) return rc;
+        if (wt[k]->dtype == SOSO_HIP_DTYPE_F32) return set_err(h, SOSO_HIP_DECLINED, "moe_shared: f32 expert");
+    }
+    float *xd = (float *)scratch_get(h, 2, (n * hdim + hdim) * 4);
+    float *gu = (float *)scratch_get(h, 3, 2 * n * ffn * 4);
+    float *out = (float *)scratch_get(h, 12, n * hdim * 4);
+    if (!xd || !gu || !out) return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_shared: scratch");
+    float *pgd = xd + n * hdim;
+    rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
+    if (rc == SOSO_HIP_OK)
+        rc = hip_check(h, hipMemcpyAsync(pgd, pg_w, hdim * 4, hipMemcpyHostToDevice, h->stream), "gate upload");
+    // gate, up, SwiGLU, down (each a matmul over the n tokens), then the gate
+    if (rc == SOSO_HIP_OK) rc = launch_matvec(h, *wt[0], xd, gu, n);
+    if (rc == SOSO_HIP_OK) rc = launch_matvec(h, *wt[1], xd, gu + n * ffn, n);
+    if (rc == SOSO_HIP_OK) rc = launch_shared_swiglu(h, gu, gu + n * ffn, n * ffn);
+    if (rc == SOSO_HIP_OK) rc = launch_matvec(h, *wt[2], gu + n * ffn, out, n);
+    if (rc == SOSO_HIP_OK) rc = launch_shared_gate(h, xd, pgd, out, n, hdim);
+    if (rc != SOSO_HIP_OK) return rc;
+    h->shared_pending = true;
+    h->shared_n = n;
+    h->shared_hdim = hdim;
+    h->stats.bytes_up += (n * hdim + hdim) * 4;
+    clk.done();
+    return SOSO_HIP_OK;
 }
 
 // ---- MoE FFN resident on the device ----------------------------------------

@@ -164,6 +164,31 @@ class HipGpu:
             hecho[i] = hecho[i] or bool(done[i])
         return self._rc(rc, "expertos_bloque") if rc < 0 else rc
 
+    def moe_compartido(self, claves, vistas, dtypes, pg_w, xs, n, h, ffn):
+        """gpu.rs:518-534: the shared expert of the block (3 keys, 3 byte arrays
+        or None when resident, 3 dtype codes; pg_w: h f32), kept on the device
+        and added by the next expertos_bloque call for the same block."""
+        keep = []
+        keys = (C.c_char_p * 3)()
+        lens = (C.c_size_t * 3)()
+        ws = (C.c_void_p * 3)()
+        wl = (C.c_size_t * 3)()
+        dt = (C.c_uint8 * 3)()
+        for j in range(3):
+            k, kl = _key(claves[j])
+            keys[j], lens[j] = k, kl
+            wb = None if vistas is None or vistas[j] is None else _raw(vistas[j])
+            keep += [k, wb]
+            ws[j] = None if wb is None else wb.ctypes.data
+            wl[j] = 0 if wb is None else wb.size
+            dt[j] = 0 if wb is None else dtypes[j]
+        pg = _f32(pg_w)
+        xs = _f32(xs)
+        rc = self.lib.soso_hip_moe_shared(self.h, C.cast(keys, C.c_void_p), C.cast(lens, C.c_void_p),
+                                          C.cast(ws, C.c_void_p), C.cast(wl, C.c_void_p), C.cast(dt, C.c_void_p),
+                                          pg.ctypes.data, xs.ctypes.data, n, h, ffn)
+        return self._rc(rc, "moe_compartido")
+
     # -- device-resident helpers (benchmarks, decode step, tests) ----------------
     def dev_alloc(self, nbytes):
         p = C.c_void_p()

@@ -271,6 +271,56 @@ def test_experts_block_declines_shared_and_sums_the_rest(gpu, orc):
         layer.drop(gpu)
 
 
+@pytest.mark.parametrize("n", [5, 20])
+def test_moe_shared_joins_the_experts_block_sum(gpu, orc, n):
+    """moe_compartido (gpu.rs:518-534): the shared expert of the block, c_t =
+    down(silu(gate x_t) * up x_t) * sigmoid(x_t . pg_w), stays on the device
+    and the next expertos_bloque for the same block adds it to its sum: per
+    token the ranked experts (oracle or_moe_ffn) plus the oracle's shared
+    expert (or_moe_shared), within 1e-5.  The shared expert is consumed: a
+    second expertos_bloque sums the ranked experts alone.  One computed for a
+    block of another size makes expertos_bloque fail.  (20 tokens take the
+    shared matrices through the matrix-core matmul.)"""
+    n_exp, h, ffn, top_k = 8, 512, 256, 2
+    layer = Layer(orc, n_exp, h, ffn, top_k, 95 + n)
+    sg = [orc.synth(Q4K, ffn, h, 96 + n, 1), orc.synth(Q4K, ffn, h, 96 + n, 2), orc.synth(Q4K, h, ffn, 96 + n, 3)]
+    skeys = [f"shared{n}.gate", f"shared{n}.up", f"shared{n}.down"]
+    pg = orc.normal(h, 0.05, 97 + n, 1)
+    xs = orc.normal(n * h, 1.0, 98 + n, 1)
+    refs, idxs, ws = zip(*[layer.cpu(orc, xs[t * h:(t + 1) * h]) for t in range(n)])
+    shared = orc.moe_shared(pg, h, ffn, sg[0], sg[1], sg[2], Q4K, Q4K, xs, n)
+    pesos = np.concatenate(ws).astype(np.float32)
+    exps = []
+    for e in range(n_exp):
+        tok = [t for t in range(n) for j in range(top_k) if idxs[t][j] == e]
+        dst = [t * top_k + j for t in range(n) for j in range(top_k) if idxs[t][j] == e]
+        if tok:
+            exps.append({"claves": layer.keys(e), "w": [layer.gate[e], layer.up[e], layer.down[e]],
+                         "dtype": [Q4K, Q4K, Q4K], "tokens": tok, "destinos": dst})
+    print(f"shared expert n={n}", flush=True)
+    try:
+        assert gpu.moe_compartido(skeys, sg, [Q4K] * 3, pg, xs, n, h, ffn), gpu.last_error()
+        suma = np.zeros(n * h, np.float32)
+        hecho = [False] * len(exps)
+        assert gpu.expertos_bloque(xs, n, h, ffn, top_k, pesos, exps, suma, hecho) == 1, gpu.last_error()
+        for t in range(n):
+            want = refs[t] + shared[t * h:(t + 1) * h]
+            assert orc.rel_l2(suma[t * h:(t + 1) * h], want) < TOL, (t, orc.rel_l2(suma[t * h:(t + 1) * h], want))
+        # consumed: the next block sums the ranked experts alone
+        suma2 = np.zeros(n * h, np.float32)
+        assert gpu.expertos_bloque(xs, n, h, ffn, top_k, pesos, exps, suma2, [False] * len(exps)) == 1
+        for t in range(n):
+            assert orc.rel_l2(suma2[t * h:(t + 1) * h], refs[t]) < TOL
+        # computed for a block of another size: the sum cannot hold it
+        assert gpu.moe_compartido(skeys, None, [Q4K] * 3, pg, xs[:h], 1, h, ffn)
+        with pytest.raises(RuntimeError, match="another block"):
+            gpu.expertos_bloque(xs, n, h, ffn, top_k, pesos, exps, suma2, [False] * len(exps))
+    finally:
+        layer.drop(gpu)
+        for k in skeys:
+            gpu.weight_drop(k)
+
+
 def test_moe_graph_survives_scratch_growth(gpu, orc):
     """A graph holding a single-token moe_ffn_dev keeps the scratch it was
     captured with: a later call that outgrows the MoE scratch slots (a
