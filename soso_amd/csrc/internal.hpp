@@ -257,7 +257,9 @@ int moe_item_target(const soso_hip *h);
 bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols);
 int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_t *const *B, size_t rows, size_t cols,
                     size_t max_recs, const float *xs, int xdiv, const int *list, const int *recs, const int *n_recs,
-                    float *out, bool tiled);
+                    float *out, bool tiled, const int32_t *sidx = nullptr, size_t nslots = 0);
+bool mfma_moe_scan_ok(size_t n, size_t top_k, size_t n_groups, uint8_t dt_gu, uint8_t dt_down, size_t hdim,
+                      size_t ffn);
 // tile-major Q4_K copies (same size as the row-major packing) for launch_mfma_moe
 bool tiled_q4k_ok(uint8_t dtype, size_t rows, size_t cols);
 int launch_tile_q4k(soso_hip *h, const void *src_dev, void *dst_dev, size_t rows, size_t cols);
@@ -265,8 +267,11 @@ int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, f
 size_t moe_max_items(const soso_hip *h, size_t slots, size_t n_groups);
 int launch_router_topk(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim,
                        size_t n_exp, size_t top_k, int32_t *idx_dev, float *wgt_dev, float *logits_dev);
+// sort false: the ranking only (idx / wgt), no slot sort, work items or
+// records -- for calls whose experts scan the ranking themselves
+// (mfma_moe_scan_ok)
 int launch_moe_route(soso_hip *h, const float *w_dev, const float *x_dev, size_t n, size_t hdim, size_t n_exp,
-                     size_t top_k, const MoeScratch &s);
+                     size_t top_k, const MoeScratch &s, bool sort = true);
 // One token through a registered layer (route, gate/up + SwiGLU, down +
 // weighted sum), three launches, the ranking done by the expert kernel
 // (DECLINED when the layer's shapes need the general path); res: added to the
@@ -282,7 +287,7 @@ int launch_rmsnorm(soso_hip *h, const float *x, const float *w, size_t n, float 
 int launch_moe_experts(soso_hip *h, const float *xs_dev, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab_dev, size_t n_groups,
                        const float *wgt_dev, const uint8_t *use_dev, const int32_t *route_idx_dev,
-                       const MoeScratch &s, float *out_dev, const MoeLayer *layer = nullptr);
+                       const MoeScratch &s, float *out_dev, const MoeLayer *layer = nullptr, bool scan = false);
 
 // ---------------------------------------------------------------------------
 // Device helpers

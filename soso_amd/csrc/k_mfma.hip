@@ -46,6 +46,7 @@ constexpr int MF_NW = 4;            // wavefronts per workgroup
 // is fastest -- 136 us per layer; 2 / 3 ahead gave 144 us.
 constexpr int MF_LA2 = 1, MF_LA1 = 1;
 constexpr int MF_ROWS = 16 * MF_NW; // rows per MoE workgroup (16 per wavefront)
+constexpr int MF_SCAN_MAX = 512;    // ranked slots an expert workgroup scans itself (n * top_k)
 // Dense matmul workgroups have 4, 8 or 16 wavefronts (launch_mfma_matmul).
 constexpr int MF_NW_MAX = 16;
 
@@ -219,23 +220,54 @@ __device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__
     }
 }
 
+// The slots s < nslots with sidx[s] == e (the token t = s / top_k ranked expert
+// e j = s % top_k-th), ascending, into scan_s; returns their count.  The MoE
+// route then needs no slot sort: each expert's workgroups find their tokens
+// in the n * top_k ranked indices (at most MF_SCAN_MAX of them).
+template <int NW>
+__device__ int mf_scan_slots(const int32_t *__restrict__ sidx, int nslots, int e, int *scan_s, int *wtot_s)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int total = 0;
+    for (int s0 = 0; s0 < nslots; s0 += 64 * NW) {
+        const int sl = s0 + (int)threadIdx.x;
+        const bool hit = sl < nslots && sidx[sl] == e;
+        const uint64_t m = __ballot(hit);
+        if (lane == 0) wtot_s[wave] = __popcll(m);
+        __syncthreads();
+        int before = total, all = total;
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const int c = wtot_s[w];
+            before += w < wave ? c : 0;
+            all += c;
+        }
+        if (hit) scan_s[before + __popcll(m & ((1ull << lane) - 1ull))] = sl;
+        total = all;
+        __syncthreads(); // wtot_s is rewritten by the next stretch
+    }
+    return total;
+}
+
 // tabA/tabB: per-expert weight pointer tables (MoE), or null with W0 the dense
 // weight.  recs[4a ..] = {expert, tokens, first slot, 0} for a < *n_recs
 // (MoE), or dense_n > 0 tokens of one dense product (slot = token).  Item:
 // blockIdx.x = a * nblk + row block (MoE), or row block + nblk * token round
 // (dense).  Slot s reads x = xs + (s / xdiv) * cols and writes out[s * rows + r].
-template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW>
+template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW, bool SCAN = false>
 __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB,
                                                   const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
                                                   const float *__restrict__ xs, int xdiv, const int *__restrict__ list,
                                                   const int *__restrict__ recs, const int *__restrict__ n_recs,
-                                                  int dense_n, int kcmax, float *__restrict__ out)
+                                                  int dense_n, int kcmax, float *__restrict__ out,
+                                                  const int32_t *__restrict__ sidx, int nslots)
 {
     constexpr int TR = 4 * MT; // tokens per round
     extern __shared__ uint4 mf_smem[];
     uint8_t *lds = (uint8_t *)mf_smem;
     __shared__ int slot_s[TR];
+    __shared__ int scan_s[SCAN ? MF_SCAN_MAX : 1], wtot_s[NW];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     constexpr int ROWS = 16 * NW; // rows per workgroup
@@ -246,6 +278,14 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
         ne = dense_n;
         t_first = (blockIdx.x / nblk) * TR; // one round per workgroup
         t_step = (int)(gridDim.x / nblk) * TR;
+    } else if constexpr (SCAN) {
+        // expert a's slots, ascending, read off the ranking itself
+        e = blockIdx.x / nblk;
+        b = blockIdx.x % nblk;
+        ne = mf_scan_slots<NW>(sidx, nslots, e, scan_s, wtot_s);
+        if (ne == 0) return; // uniform: nobody chose this expert
+        t_first = 0;
+        t_step = TR;
     } else {
         const int a = blockIdx.x / nblk;
         b = blockIdx.x % nblk;
@@ -273,7 +313,9 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
     for (int t0 = t_first; t0 < ne; t0 += t_step) {
         const int nt = min(TR, ne - t0);
         __syncthreads(); // the previous round's readers of slot_s and LDS are done
-        if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = list ? list[base + t0 + threadIdx.x] : base + t0 + threadIdx.x;
+        if ((int)threadIdx.x < nt)
+            slot_s[threadIdx.x] = SCAN ? scan_s[t0 + threadIdx.x]
+                                       : list ? list[base + t0 + threadIdx.x] : base + t0 + threadIdx.x;
         __syncthreads();
         const int r0 = b * ROWS, rend = min(rows, r0 + ROWS);
         const uint32_t strip = (uint32_t)((size_t)(rend - r0) * stride);
@@ -571,33 +613,59 @@ bool mfma_shape_ok(uint8_t dtype, size_t rows, size_t cols)
            rows > 0 && (size_t)16 * MF_NW_MAX * packed_row_stride(dtype, cols) < ((size_t)1 << 31);
 }
 
-// MoE: one grouped product over the active-expert records (device).
+// MoE: one grouped product over the active-expert records (device), or, with
+// sidx set, over every expert, each workgroup finding its expert's slots in
+// the nslots ranked indices (the route then skips its slot sort).
+template <int NMAT, bool TILED>
+static void mfma_moe_one(soso_hip *h, unsigned grid, size_t lds, const uint8_t *const *A, const uint8_t *const *B,
+                         size_t stride, int rows, int cols, const float *xs, int xdiv, const int *list, const int *recs,
+                         const int *n_recs, int kc, float *out, const int32_t *sidx, int nslots)
+{
+    constexpr int MT = 2, LA = NMAT == 2 ? MF_LA2 : MF_LA1;
+    if (sidx)
+        k_mfma_q4k<NMAT, MT, LA, TILED, MF_NW, true><<<grid, 64 * MF_NW, lds, h->stream>>>(
+            A, B, nullptr, stride, rows, cols, xs, xdiv, list, recs, n_recs, 0, kc, out, sidx, nslots);
+    else
+        k_mfma_q4k<NMAT, MT, LA, TILED><<<grid, 64 * MF_NW, lds, h->stream>>>(
+            A, B, nullptr, stride, rows, cols, xs, xdiv, list, recs, n_recs, 0, kc, out, nullptr, 0);
+}
+
 int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_t *const *B, size_t rows, size_t cols,
                     size_t max_recs, const float *xs, int xdiv, const int *list, const int *recs, const int *n_recs,
-                    float *out, bool tiled)
+                    float *out, bool tiled, const int32_t *sidx, size_t nslots)
 {
     if (!mfma_shape_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols) || (tiled && !tiled_q4k_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols)))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
+    if (sidx && nslots > (size_t)MF_SCAN_MAX) return set_err(h, SOSO_HIP_ERR_ARG, "mfma: too many slots to scan");
     constexpr int MT = 2;
     const int kc = mf_kc(h, cols, 4 * MT);
     const size_t nblk = (rows + MF_ROWS - 1) / MF_ROWS;
     const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
     const unsigned grid = (unsigned)(max_recs * nblk);
     const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
-    const int ri = (int)rows, ci = (int)cols;
+    const int ri = (int)rows, ci = (int)cols, ns = (int)nslots;
     if (nmat == 2 && tiled)
-        k_mfma_q4k<2, MT, MF_LA2, true><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, ri, ci, xs, xdiv,
-                                                                              list, recs, n_recs, 0, kc, out);
+        mfma_moe_one<2, true>(h, grid, lds, A, B, stride, ri, ci, xs, xdiv, list, recs, n_recs, kc, out, sidx, ns);
     else if (nmat == 2)
-        k_mfma_q4k<2, MT, MF_LA2><<<grid, 64 * MF_NW, lds, h->stream>>>(A, B, nullptr, stride, ri, ci, xs, xdiv, list,
-                                                                        recs, n_recs, 0, kc, out);
+        mfma_moe_one<2, false>(h, grid, lds, A, B, stride, ri, ci, xs, xdiv, list, recs, n_recs, kc, out, sidx, ns);
     else if (tiled)
-        k_mfma_q4k<1, MT, MF_LA1, true><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, ri, ci, xs,
-                                                                              xdiv, list, recs, n_recs, 0, kc, out);
+        mfma_moe_one<1, true>(h, grid, lds, A, nullptr, stride, ri, ci, xs, xdiv, list, recs, n_recs, kc, out, sidx,
+                              ns);
     else
-        k_mfma_q4k<1, MT, MF_LA1><<<grid, 64 * MF_NW, lds, h->stream>>>(A, nullptr, nullptr, stride, ri, ci, xs, xdiv,
-                                                                        list, recs, n_recs, 0, kc, out);
+        mfma_moe_one<1, false>(h, grid, lds, A, nullptr, stride, ri, ci, xs, xdiv, list, recs, n_recs, kc, out, sidx,
+                               ns);
     return hip_check(h, hipGetLastError(), "mfma moe launch");
+}
+
+// The MoE calls whose experts both run on the matrix cores with each expert
+// workgroup scanning the ranked slots itself (launch_moe_experts' choice, at
+// most MF_SCAN_MAX slots): their route can skip the slot sort.
+bool mfma_moe_scan_ok(size_t n, size_t top_k, size_t n_groups, uint8_t dt_gu, uint8_t dt_down, size_t hdim,
+                      size_t ffn)
+{
+    const size_t slots = n * top_k, max_recs = std::min(n_groups, slots);
+    return slots >= 2 * max_recs && slots <= (size_t)MF_SCAN_MAX && dt_gu == SOSO_HIP_DTYPE_Q4_K &&
+           dt_down == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_gu, ffn, hdim) && mfma_shape_ok(dt_down, hdim, ffn);
 }
 
 template <int NW, int MT>
@@ -610,7 +678,7 @@ static void mfma_dense(soso_hip *h, const Weight &w, const float *x, size_t n, f
     else
         k_mfma_q4k<1, MT, MF_LA1, false, NW><<<grid, 64 * NW, lds, h->stream>>>(
             nullptr, nullptr, (const uint8_t *)w.dev, stride, (int)w.rows, (int)w.cols, x, 1, nullptr, nullptr,
-            nullptr, (int)n, kc, y);
+            nullptr, (int)n, kc, y, nullptr, 0);
 }
 
 // Dense: Y[n x rows] = X[n x cols] . W^T.  The grid is (row block of 16 NW

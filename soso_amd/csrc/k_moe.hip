@@ -109,7 +109,7 @@ constexpr int MOE_SELF_K = 8;         // top_k of the self-ranked single-token p
 // norm_w (TT = 1, hdim <= 256 Q, so the row is one step): xs is h and the
 // row is rmsnorm(h) * norm_w (gemm.rs:93-100), each wavefront taking sum(h^2)
 // over the row it holds.
-template <int TT, int Q, bool LOGITS_ONLY = false>
+template <int TT, int Q, bool LOGITS_ONLY = false, bool SORT = true>
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
                                                     int32_t *__restrict__ idx, float *__restrict__ wgt,
@@ -211,6 +211,11 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
         }
         topk_regs(lg, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k, sel[wave],
                   rank_s + wave * top_k);
+    }
+    if constexpr (!SORT) {
+        // the expert kernels read the ranking after this launch ends
+        if (threadIdx.x == 0) ticket[ROUTE_T1 + blockIdx.y] = 0u;
+        return;
     }
     const bool single = gridDim.y == 1;
     __builtin_amdgcn_s_waitcnt(0); // the ranked experts acknowledged
@@ -952,7 +957,7 @@ size_t moe_scratch_fixed(const soso_hip *h, size_t n, size_t n_groups, size_t to
 }
 
 int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size_t hdim, size_t n_exp, size_t top_k,
-                     const MoeScratch &s)
+                     const MoeScratch &s, bool sort)
 {
     if (n * top_k > ROUTE_MAX_SLOTS || n_exp > 256 || (n + ROUTE_TT - 1) / ROUTE_TT > 1024)
         return set_err(h, SOSO_HIP_DECLINED, "moe route: too many slots");
@@ -961,6 +966,11 @@ int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size
         k_moe_route<1, 8><<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits,
                                                         s.idx, s.wgt, s.cnt, s.offs, s.list, s.items, s.n_items,
                                                         moe_item_target(h), s.recs, s.n_recs, h->ticket);
+    } else if (!sort) {
+        const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
+        k_moe_route<ROUTE_TT, 4, false, false><<<grid, 512, 0, h->stream>>>(
+            w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt, s.cnt, s.offs, s.list, s.items,
+            s.n_items, moe_item_target(h), s.recs, s.n_recs, h->ticket);
     } else {
         const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
         k_moe_route<ROUTE_TT, 4><<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k,
@@ -1187,9 +1197,14 @@ static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp
 int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size_t ffn, size_t top_k,
                        uint8_t dt_gu, uint8_t dt_down, const uint8_t *const *tab, size_t n_groups, const float *wgt,
                        const uint8_t *use, const int32_t *route_idx, const MoeScratch &s, float *out,
-                       const MoeLayer *layer)
+                       const MoeLayer *layer, bool scan)
 {
     const size_t max_items = moe_max_items(h, n * top_k, n_groups);
+    // scan: the route wrote only the ranking (route_idx); each expert
+    // workgroup of the matrix-core kernels finds its slots there
+    if (scan && (!route_idx || use || !mfma_moe_scan_ok(n, top_k, n_groups, dt_gu, dt_down, hdim, ffn)))
+        return set_err(h, SOSO_HIP_ERR_ARG, "moe experts: scanning the ranking needs the matrix-core path");
+    const int32_t *sidx = scan ? route_idx : nullptr;
     // two or more slots per active expert on average: the matrix-core path
     // (its cost per weight row is flat up to 8 tokens); fewer: the dot4 path
     const size_t slots = n * top_k, max_recs = std::min(n_groups, slots);
@@ -1200,7 +1215,7 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
     const uint8_t *const *ttab = layer ? layer->tiled : nullptr;
     if (many && dt_gu == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_gu, ffn, hdim))
         rc = launch_mfma_moe(h, 2, tgu ? ttab : tab, (tgu ? ttab : tab) + n_groups, ffn, hdim, max_recs, xs, (int)top_k,
-                             s.list, s.recs, s.n_recs, s.act, tgu);
+                             s.list, s.recs, s.n_recs, s.act, tgu, sidx, n * top_k);
     else
         rc = launch_moe_mv(h, dt_gu, 2, tab, tab + n_groups, ffn, hdim, max_items, n, xs, (int)top_k, s, s.act);
     // few tokens with the device's own routing: down and the weighted sum in one launch
@@ -1213,7 +1228,7 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
     if (rc == SOSO_HIP_OK) {
         if (many && dt_down == SOSO_HIP_DTYPE_Q4_K && mfma_shape_ok(dt_down, hdim, ffn))
             rc = launch_mfma_moe(h, 1, (tdn ? ttab : tab) + 2 * n_groups, nullptr, hdim, ffn, max_recs, s.act, 1, s.list,
-                                 s.recs, s.n_recs, s.ydown, tdn);
+                                 s.recs, s.n_recs, s.ydown, tdn, sidx, n * top_k);
         else
             rc = launch_moe_mv(h, dt_down, 1, tab + 2 * n_groups, nullptr, hdim, ffn, max_items, n, s.act, 1, s,
                                s.ydown);

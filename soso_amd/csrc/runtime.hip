@@ -869,10 +869,12 @@ static int moe_ffn_run(soso_hip *h, const MoeLayer &m, const float *x_dev, size_
         if (idx_dev) s.idx = idx_dev + t0 * m.top_k;
         if (wgt_dev) s.wgt = wgt_dev + t0 * m.top_k;
         const float *xc = x_dev + t0 * m.hdim;
-        rc = launch_moe_route(h, (const float *)m.router->dev, xc, c, m.hdim, m.n_exp, m.top_k, s);
+        // experts that scan the ranking themselves spare the route its slot sort
+        const bool scan = mfma_moe_scan_ok(c, m.top_k, m.n_exp, m.dt_gu, m.dt_down, m.hdim, m.ffn);
+        rc = launch_moe_route(h, (const float *)m.router->dev, xc, c, m.hdim, m.n_exp, m.top_k, s, !scan);
         if (rc == SOSO_HIP_OK)
             rc = launch_moe_experts(h, xc, c, m.hdim, m.ffn, m.top_k, m.dt_gu, m.dt_down, m.tab, m.n_exp, s.wgt,
-                                    nullptr, s.idx, s, out_dev + t0 * m.hdim, &m);
+                                    nullptr, s.idx, s, out_dev + t0 * m.hdim, &m, scan);
     }
     return rc;
 }
