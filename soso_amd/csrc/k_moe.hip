@@ -348,6 +348,28 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
     }
 }
 
+// The ranking of calls whose expert kernels scan it (no slot sort): one
+// wavefront per token ranks its logits with topk_regs, as the route kernel's
+// last workgroup would, in a launch of its own after k_moe_route<TT, Q, true>.
+// On MI355X (configs[3] at batch 32) the layer took 88.7 us with this pair
+// against 89.4 with the route's own ticket and last-workgroup ranking.
+__global__ void __launch_bounds__(256) k_moe_rank(const float *__restrict__ logits, int n, int n_exp, int top_k,
+                                                  int32_t *__restrict__ idx, float *__restrict__ wgt)
+{
+    __shared__ float sel[4][64];
+    __shared__ int16_t rank_s[4 * 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x * 4 + wave;
+    if (t >= n) return; // whole wavefronts
+    float lg[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int x = lane + 64 * q;
+        lg[q] = x < n_exp ? logits[(size_t)t * n_exp + x] : -INFINITY;
+    }
+    topk_regs(lg, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k, sel[wave], rank_s + wave * 64);
+}
+
 // ---------------------------------------------------------------------------
 // Grouped expert matvecs
 // ---------------------------------------------------------------------------
@@ -967,10 +989,15 @@ int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size
                                                         s.idx, s.wgt, s.cnt, s.offs, s.list, s.items, s.n_items,
                                                         moe_item_target(h), s.recs, s.n_recs, h->ticket);
     } else if (!sort) {
-        const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
-        k_moe_route<ROUTE_TT, 4, false, false><<<grid, 512, 0, h->stream>>>(
+        // logits by two-wavefront workgroups, then the ranking in a launch of its own
+        const dim3 grid((unsigned)((n_exp + 1) / 2), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
+        k_moe_route<ROUTE_TT, 4, true><<<grid, 128, 0, h->stream>>>(
             w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt, s.cnt, s.offs, s.list, s.items,
             s.n_items, moe_item_target(h), s.recs, s.n_recs, h->ticket);
+        int rc = hip_check(h, hipGetLastError(), "moe route launch");
+        if (rc != SOSO_HIP_OK) return rc;
+        k_moe_rank<<<(unsigned)((n + 3) / 4), 256, 0, h->stream>>>(s.logits, (int)n, (int)n_exp, (int)top_k, s.idx,
+                                                                  s.wgt);
     } else {
         const dim3 grid((unsigned)((n_exp + 7) / 8), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
         k_moe_route<ROUTE_TT, 4><<<grid, 512, 0, h->stream>>>(w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k,
