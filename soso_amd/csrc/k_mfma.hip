@@ -273,6 +273,7 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
     constexpr int ROWS = 16 * NW; // rows per workgroup
     const int nblk = (rows + ROWS - 1) / ROWS;
     int e = 0, ne, base = 0, b, t_first, t_step;
+    const uint8_t *WA, *WB;
     if (dense_n > 0) {
         b = blockIdx.x % nblk;
         ne = dense_n;
@@ -282,6 +283,9 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
         // expert a's slots, ascending, read off the ranking itself
         e = blockIdx.x / nblk;
         b = blockIdx.x % nblk;
+        // the expert's tables are requested before the scan, which does not need them
+        WA = tabA[e];
+        WB = NMAT == 2 ? tabB[e] : WA;
         ne = mf_scan_slots<NW>(sidx, nslots, e, scan_s, wtot_s);
         if (ne == 0) return; // uniform: nobody chose this expert
         t_first = 0;
@@ -300,8 +304,10 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
         t_first = 0;
         t_step = TR;
     }
-    const uint8_t *WA = dense_n > 0 ? W0 : tabA[e];
-    const uint8_t *WB = NMAT == 2 ? tabB[e] : WA;
+    if (!SCAN) {
+        WA = dense_n > 0 ? W0 : tabA[e];
+        WB = NMAT == 2 ? tabB[e] : WA;
+    }
     const int nl = lane & 15, g = lane >> 4;
     // row-major: this lane's row; tiled: the wavefront's tile (past the strip: zeros)
     const uint32_t rowoff = (uint32_t)((16 * wave + (TILED ? 0 : nl)) * stride);
