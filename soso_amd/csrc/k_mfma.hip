@@ -45,7 +45,7 @@ constexpr int MF_NW = 4;            // wavefronts per workgroup
 // (gate+up, single matrix).  Measured on MI355X at batch 32: one
 // is fastest -- 136 us per layer; 2 / 3 ahead gave 144 us.
 constexpr int MF_LA2 = 1, MF_LA1 = 1;
-constexpr int MF_ROWS = 16 * MF_NW; // rows per MoE workgroup (16 per wavefront)
+constexpr int MF_NW_GU = 4, MF_NW_DN = 4; // wavefronts per MoE workgroup: gate/up, down
 constexpr int MF_SCAN_MAX = 512;    // ranked slots an expert workgroup scans itself (n * top_k)
 // Dense matmul workgroups have 4, 8 or 16 wavefronts (launch_mfma_matmul).
 constexpr int MF_NW_MAX = 16;
@@ -225,7 +225,7 @@ __device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__
 // route then needs no slot sort: each expert's workgroups find their tokens
 // in the n * top_k ranked indices (at most MF_SCAN_MAX of them).
 template <int NW>
-__device__ int mf_scan_slots(const int32_t *__restrict__ sidx, int nslots, int e, int *scan_s, int *wtot_s)
+__device__ int mf_scan_slots(const int32_t *__restrict__ sidx, int nslots, int e, int16_t *scan_s, int *wtot_s)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int total = 0;
@@ -242,7 +242,7 @@ __device__ int mf_scan_slots(const int32_t *__restrict__ sidx, int nslots, int e
             before += w < wave ? c : 0;
             all += c;
         }
-        if (hit) scan_s[before + __popcll(m & ((1ull << lane) - 1ull))] = sl;
+        if (hit) scan_s[before + __popcll(m & ((1ull << lane) - 1ull))] = (int16_t)sl;
         total = all;
         __syncthreads(); // wtot_s is rewritten by the next stretch
     }
@@ -267,7 +267,10 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
     extern __shared__ uint4 mf_smem[];
     uint8_t *lds = (uint8_t *)mf_smem;
     __shared__ int slot_s[TR];
-    __shared__ int scan_s[SCAN ? MF_SCAN_MAX : 1], wtot_s[NW];
+    // 16-bit slot list: with 8 tokens' x staged (51.5 KB for 2048 columns),
+    // three gate/up workgroups still fit a CU's 160 KB of LDS
+    __shared__ int16_t scan_s[SCAN ? MF_SCAN_MAX : 1];
+    __shared__ int wtot_s[NW];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     constexpr int ROWS = 16 * NW; // rows per workgroup
@@ -627,12 +630,12 @@ static void mfma_moe_one(soso_hip *h, unsigned grid, size_t lds, const uint8_t *
                          size_t stride, int rows, int cols, const float *xs, int xdiv, const int *list, const int *recs,
                          const int *n_recs, int kc, float *out, const int32_t *sidx, int nslots)
 {
-    constexpr int MT = 2, LA = NMAT == 2 ? MF_LA2 : MF_LA1;
+    constexpr int MT = 2, LA = NMAT == 2 ? MF_LA2 : MF_LA1, NW = NMAT == 2 ? MF_NW_GU : MF_NW_DN;
     if (sidx)
-        k_mfma_q4k<NMAT, MT, LA, TILED, MF_NW, true><<<grid, 64 * MF_NW, lds, h->stream>>>(
+        k_mfma_q4k<NMAT, MT, LA, TILED, NW, true><<<grid, 64 * NW, lds, h->stream>>>(
             A, B, nullptr, stride, rows, cols, xs, xdiv, list, recs, n_recs, 0, kc, out, sidx, nslots);
     else
-        k_mfma_q4k<NMAT, MT, LA, TILED><<<grid, 64 * MF_NW, lds, h->stream>>>(
+        k_mfma_q4k<NMAT, MT, LA, TILED, NW><<<grid, 64 * NW, lds, h->stream>>>(
             A, B, nullptr, stride, rows, cols, xs, xdiv, list, recs, n_recs, 0, kc, out, nullptr, 0);
 }
 
@@ -645,7 +648,8 @@ int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_
     if (sidx && nslots > (size_t)MF_SCAN_MAX) return set_err(h, SOSO_HIP_ERR_ARG, "mfma: too many slots to scan");
     constexpr int MT = 2;
     const int kc = mf_kc(h, cols, 4 * MT);
-    const size_t nblk = (rows + MF_ROWS - 1) / MF_ROWS;
+    const size_t mrows = (size_t)16 * (nmat == 2 ? MF_NW_GU : MF_NW_DN); // rows per workgroup
+    const size_t nblk = (rows + mrows - 1) / mrows;
     const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
     const unsigned grid = (unsigned)(max_recs * nblk);
     const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
