@@ -474,3 +474,36 @@ def test_matmul_matrix_cores_outliers(gpu, orc):
         assert worst < TOL
     finally:
         gpu.weight_drop(key)
+
+
+@pytest.mark.parametrize("dtype,off,bsz", [(Q4K, 0, 144), (Q4K, 2, 144), (Q6K, 208, 210)])
+def test_nonfinite_f16_scales(gpu, orc, dtype, off, bsz):
+    """f16 scales that are NaN (any payload, either sign) or infinite: the
+    dequant decodes them as dequant.rs:26-45 does -- the same elements NaN,
+    every other element bit for bit (NaN bits are not compared: Inf * 0 gives
+    each machine's own default NaN) -- and the matvec rows holding them are
+    not finite while the others stay within the bar."""
+    rows, cols = 64, 512
+    w = orc.synth(dtype, rows, cols, 31, 1).copy()
+    nb = cols // 256
+    bad = {3: 0x7e00, 10: 0x7c01, 20: 0xfe01, 33: 0x7c00, 47: 0xfc00}  # row -> f16 bits of d (or dmin)
+    for r, bits in bad.items():
+        b = (r * nb + 1) * bsz + off  # the row's second super-block
+        w[b:b + 2] = np.frombuffer(np.uint16(bits).tobytes(), np.uint8)
+    key = f"nf.{dtype}.{off}"
+    x = orc.normal(cols, 1.0, 31, 2)
+    try:
+        y = run_matvec(gpu, key, dtype, w, rows, cols, x)
+        dev = dev_dequant(gpu, key, rows, cols)
+        ref = orc.dequant(dtype, w, rows, cols)
+        nan_dev, nan_ref = np.isnan(dev), np.isnan(ref)
+        assert nan_ref.any() and np.array_equal(nan_dev, nan_ref)
+        assert np.array_equal(dev.view(np.uint32)[~nan_dev], ref.view(np.uint32)[~nan_ref])
+        y64 = orc.matvec_f64(dtype, w, rows, cols, x)
+        for r in range(rows):
+            if r in bad:
+                assert not np.isfinite(y[r]), (r, y[r])
+        good = [r for r in range(rows) if r not in bad]
+        assert orc.rel_l2(y[good], y64[good]) < TOL
+    finally:
+        gpu.weight_drop(key)

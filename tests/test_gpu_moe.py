@@ -384,3 +384,28 @@ def test_moe_graph_survives_scratch_growth(gpu, orc):
         gpu.dev_free(xd)
         gpu.dev_free(od)
         layer.drop(gpu)
+
+
+def test_moe_nan_token_at_batch_32(gpu, orc):
+    """A token whose x holds a NaN has NaN logits: it ranks no expert, its
+    eight slots name expert 0 with weight 0 (the matrix-core kernels then find
+    all of them in expert 0's scan) and its output is NaN, as soso's NaN
+    weights make it.  The other tokens keep the oracle's routing and outputs."""
+    layer = Layer(orc, 16, 512, 256, 8, 91, Q4K)
+    layer.upload(gpu)
+    try:
+        n, h = 32, layer.h
+        xs = orc.normal(n * h, 1.0, 92, n).copy()
+        xs[5 * h + 17] = np.nan
+        out, idx, wgt = moe_dev(gpu, layer, xs)
+        assert np.all(np.isnan(out[5]))
+        assert np.array_equal(idx[5], np.zeros(8, np.int32)) and np.all(wgt[5] == 0.0), (idx[5], wgt[5])
+        for t in range(n):
+            if t == 5:
+                continue
+            ref, ri, rw = layer.cpu(orc, xs[t * h:(t + 1) * h])
+            assert np.array_equal(idx[t], ri), (t, idx[t], ri)
+            assert orc.rel_l2(wgt[t], rw) < TOL
+            assert orc.rel_l2(out[t], ref) < TOL, (t, orc.rel_l2(out[t], ref))
+    finally:
+        layer.drop(gpu)
