@@ -360,16 +360,34 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
             // the high byte).  Two MFMA chains (lo, hi) then sum a whole
             // super-block in the accumulators: S = Clo + 8 Chi = sum_sb sc_sb *
             // sum_k digit * q.
-            auto scaled = [](uint32_t codes, int f) {
-                const mf_u16x2 c = __builtin_bit_cast(mf_u16x2, codes);
-                const mf_u16x2 k = {(unsigned short)f, (unsigned short)f};
-                return __builtin_bit_cast(uint32_t, c * k);
+            // k: the factor in both 16-bit halves
+            auto scaled = [](uint32_t codes, uint32_t k) {
+                return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mf_u16x2, codes) *
+                                                        __builtin_bit_cast(mf_u16x2, k));
+            };
+            // {f, f} for the low / high 3 bits f of each sub-block's scale,
+            // eight sub-blocks from two masked dwords: byte j % 4 of the
+            // dword moved into bytes 0 and 2 by one permute, zeros elsewhere
+            auto scale_parts = [](const MfScale &sc, uint32_t (&klo)[8], uint32_t (&khi)[8]) {
+#pragma unroll
+                for (int t = 0; t < 2; t++) {
+                    const uint32_t lo4 = sc.sc4[t] & 0x07070707u, hi4 = (sc.sc4[t] >> 3) & 0x07070707u;
+#pragma unroll
+                    for (int b = 0; b < 4; b++) {
+                        const uint32_t sel = 0x0c000c00u | (uint32_t)b | ((uint32_t)b << 16);
+                        klo[4 * t + b] = __builtin_amdgcn_perm(0u, lo4, sel);
+                        khi[4 * t + b] = __builtin_amdgcn_perm(0u, hi4, sel);
+                    }
+                }
             };
             auto superblock = [&](int sbl8, const MfSb &A_, const MfSb &B_) {
                 // sbl8: first local sub-block of this super-block
                 MfScale sc_[NMAT];
                 mf_scales(A_.h, sc_[0]);
                 if constexpr (NMAT == 2) mf_scales(B_.h, sc_[NMAT - 1]);
+                uint32_t klo[NMAT][8], khi[NMAT][8];
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) scale_parts(sc_[m], klo[m], khi[m]);
                 mf_v4i clo[NMAT][MT], chi[NMAT][MT];
                 float mins[NMAT][MT];
 #pragma unroll
@@ -395,11 +413,10 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
                         const uint2 q = m == 0 ? A_.q[p] : B_.q[p];
                         const uint32_t lx = q.x & 0x0F0F0F0Fu, ly = q.y & 0x0F0F0F0Fu;
                         const uint32_t hx = (q.x >> 4) & 0x0F0F0F0Fu, hy = (q.y >> 4) & 0x0F0F0F0Fu;
-                        const int s0 = mf_byte(sc_[m].sc4[j0 >> 2], j0 & 3), s1 = mf_byte(sc_[m].sc4[j1 >> 2], j1 & 3);
-                        bl[m] = mf_v4i{(int)scaled(lx, s0 & 7), (int)scaled(ly, s0 & 7), (int)scaled(hx, s1 & 7),
-                                       (int)scaled(hy, s1 & 7)};
-                        bh[m] = mf_v4i{(int)scaled(lx, s0 >> 3), (int)scaled(ly, s0 >> 3), (int)scaled(hx, s1 >> 3),
-                                       (int)scaled(hy, s1 >> 3)};
+                        bl[m] = mf_v4i{(int)scaled(lx, klo[m][j0]), (int)scaled(ly, klo[m][j0]),
+                                       (int)scaled(hx, klo[m][j1]), (int)scaled(hy, klo[m][j1])};
+                        bh[m] = mf_v4i{(int)scaled(lx, khi[m][j0]), (int)scaled(ly, khi[m][j0]),
+                                       (int)scaled(hx, khi[m][j1]), (int)scaled(hy, khi[m][j1])};
                         m0[m] = (float)mf_byte(sc_[m].m4[j0 >> 2], j0 & 3);
                         m1[m] = (float)mf_byte(sc_[m].m4[j1 >> 2], j1 & 3);
                     }
