@@ -989,9 +989,11 @@ int launch_moe_route(soso_hip *h, const float *w, const float *x, size_t n, size
                                                         s.idx, s.wgt, s.cnt, s.offs, s.list, s.items, s.n_items,
                                                         moe_item_target(h), s.recs, s.n_recs, h->ticket);
     } else if (!sort) {
-        // logits by two-wavefront workgroups, then the ranking in a launch of its own
-        const dim3 grid((unsigned)((n_exp + 1) / 2), (unsigned)((n + ROUTE_TT - 1) / ROUTE_TT));
-        k_moe_route<ROUTE_TT, 4, true><<<grid, 128, 0, h->stream>>>(
+        // logits by two-wavefront workgroups, two tokens per wavefront (batch
+        // 32: 87.3 us per layer against 87.6 with four tokens and with one),
+        // then the ranking in a launch of its own
+        const dim3 grid((unsigned)((n_exp + 1) / 2), (unsigned)((n + 1) / 2));
+        k_moe_route<2, 4, true><<<grid, 128, 0, h->stream>>>(
             w, x, (int)n, (int)hdim, (int)n_exp, (int)top_k, s.logits, s.idx, s.wgt, s.cnt, s.offs, s.list, s.items,
             s.n_items, moe_item_target(h), s.recs, s.n_recs, h->ticket);
         int rc = hip_check(h, hipGetLastError(), "moe route launch");
