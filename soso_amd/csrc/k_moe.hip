@@ -10,6 +10,9 @@
 //   k_moe_route   logits = W_router . x (f32) for every (token, expert); the
 //                 last workgroup to finish runs softmax + top-k per token and
 //                 counting-sorts the n*top_k slots by expert (cnt, offs, list).
+//                 Calls whose experts scan the ranking themselves (at most 512
+//                 slots on the matrix cores) take the logits alone, then
+//                 k_moe_rank (softmax + top-k, one wavefront per token).
 //   k_moe_rows    workgroups over (expert, row chunk) items of equal work:
 //                 every weight row of an expert is read once from HBM and
 //                 applied to all the tokens routed to it (their x staged in
@@ -109,7 +112,7 @@ constexpr int MOE_SELF_K = 8;         // top_k of the self-ranked single-token p
 // norm_w (TT = 1, hdim <= 256 Q, so the row is one step): xs is h and the
 // row is rmsnorm(h) * norm_w (gemm.rs:93-100), each wavefront taking sum(h^2)
 // over the row it holds.
-template <int TT, int Q, bool LOGITS_ONLY = false, bool SORT = true>
+template <int TT, int Q, bool LOGITS_ONLY = false>
 __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, const float *__restrict__ xs, int n,
                                                     int hdim, int n_exp, int top_k, float *__restrict__ logits,
                                                     int32_t *__restrict__ idx, float *__restrict__ wgt,
@@ -211,11 +214,6 @@ __global__ void __launch_bounds__(512) k_moe_route(const float *__restrict__ W, 
         }
         topk_regs(lg, n_exp, top_k, idx + (size_t)t * top_k, wgt + (size_t)t * top_k, sel[wave],
                   rank_s + wave * top_k);
-    }
-    if constexpr (!SORT) {
-        // the expert kernels read the ranking after this launch ends
-        if (threadIdx.x == 0) ticket[ROUTE_T1 + blockIdx.y] = 0u;
-        return;
     }
     const bool single = gridDim.y == 1;
     __builtin_amdgcn_s_waitcnt(0); // the ranked experts acknowledged
