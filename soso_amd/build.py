@@ -48,17 +48,32 @@ def build_som(verbose=False):
     return SOM_LIB
 
 
-def build(verbose=False):
-    build_som(verbose)
-    srcs = [os.path.join(CSRC, s) for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc()] + HIPCC_FLAGS + srcs + ["-o", tmp]
+def _run(cmd, verbose, what):
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
-        raise RuntimeError("hipcc failed building libsoso_hip.so")
+        raise RuntimeError(f"hipcc failed: {what}")
+
+
+def build(verbose=False):
+    """Each source compiles to its own object (in parallel: the translation
+    units share no device code, every kernel is launched from its own file),
+    then one link makes the library."""
+    from concurrent.futures import ThreadPoolExecutor
+    build_som(verbose)
+    srcs = [s for s in SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    cflags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in srcs]
+    jobs = min(len(srcs), max(1, int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(jobs) as ex:
+        list(ex.map(lambda so: _run([hipcc()] + cflags + ["-c", os.path.join(CSRC, so[0]), "-o", so[1]], verbose,
+                                    so[0]), zip(srcs, objs)))
+    tmp = LIB + ".tmp"
+    _run([hipcc(), "-shared", "-fPIC", "--offload-arch=gfx950"] + objs + ["-o", tmp], verbose, "link")
     os.replace(tmp, LIB)
     return LIB
 

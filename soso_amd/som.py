@@ -682,6 +682,12 @@ def decode_plan(som):
         elif (m.effective_num_heads(l), m.effective_num_kv_heads(l), m.effective_head_dim(l)) != (nh, nkv, hd) or \
                 (not m.layer_is_moe(l) and m.effective_ffn_dim(l) != F):
             why = f"layer {l}: layers differ in shape"
+        elif any(som.find(f"L{l:02}.attn_{p}.bias") is not None for p in ("q", "k", "v")):
+            # Qwen2 conversions carry q/k/v biases (gguf2som/src/lib.rs:673-680);
+            # the CPU adds them (layer.rs:1146-1163, add_optional_bias), the
+            # device step has no bias term, and soso's own device MoE layer
+            # declines such layers too (moe_gpu.rs:85-90)
+            why = f"layer {l}: attention q/k/v biases are not on the device step"
         if m.layer_is_moe(l):
             moe_layers.append(l)
     if why:
@@ -765,25 +771,42 @@ def prepare_decode(gpu, som, model_key, ctx_max=None, kv_f16=False):
     m = som.manifest
     cfg = dict(cfg, ctx_max=ctx_max or m.max_seq, kv_f16=1 if kv_f16 else 0)
     keys, moe_keys = [], [None] * cfg["n_layers"]
-    for l in extra["moe_layers"]:
-        moe_keys[l] = prepare_moe_layer(gpu, som, l, f"{model_key}.L{l:02}.moe")
-    for name, shape in want:
-        if name is not None and name not in keys:
-            v = som.tensor_view(name)
-            rows, cols = (1, shape[0]) if len(shape) == 1 else shape
-            _upload(gpu, name, v, rows, cols)
-        keys.append(name)
-    ok = gpu.decode_create(model_key, cfg, keys, moe_layers=moe_keys if extra["moe_layers"] else None,
-                           flags=extra["flags"])
+    uploaded = []
+
+    def undo():
+        # a declined or failed model leaves nothing resident, so a caller
+        # that falls back to the CPU gets the device memory back (dropping a
+        # weight also unregisters the MoE layers that read it)
+        for k in dict.fromkeys(uploaded):
+            gpu.weight_drop(k)
+
+    try:
+        for l in extra["moe_layers"]:
+            moe_keys[l] = prepare_moe_layer(gpu, som, l, f"{model_key}.L{l:02}.moe", uploaded=uploaded)
+        for name, shape in want:
+            if name is not None and name not in keys:
+                v = som.tensor_view(name)
+                rows, cols = (1, shape[0]) if len(shape) == 1 else shape
+                _upload(gpu, name, v, rows, cols)
+                uploaded.append(name)
+            keys.append(name)
+        ok = gpu.decode_create(model_key, cfg, keys, moe_layers=moe_keys if extra["moe_layers"] else None,
+                               flags=extra["flags"])
+    except BaseException:
+        undo()
+        raise
     if not ok:
-        raise SomError(f"prepare_decode: the device step declined the model: {gpu.last_error()}", ERR_ARG)
+        err = gpu.last_error()
+        undo()
+        raise SomError(f"prepare_decode: the device step declined the model: {err}", ERR_ARG)
     return SomDecoder(gpu, som, model_key, cfg, keys, m.embed_scale())
 
 
-def prepare_moe_layer(gpu, som, layer, layer_key=None):
+def prepare_moe_layer(gpu, som, layer, layer_key=None, uploaded=None):
     """Registers layer `layer`'s MoE FFN (router L{ll}.ffn_gate_inp, experts
     L{ll}.E{e}.ffn_gate/up/down; runtime.rs:448-469) for moe_ffn_dev; returns
-    the layer key."""
+    the layer key.  The keys it makes resident are appended to `uploaded`
+    (when given) as they go up, so that a caller can drop them on failure."""
     m = som.manifest
     if m is None or not m.layer_is_moe(layer):
         raise SomError(f"prepare_moe_layer: layer {layer} is not MoE", ERR_ARG)
@@ -807,6 +830,8 @@ def prepare_moe_layer(gpu, som, layer, layer_key=None):
             raise SomError(f"prepare_moe_layer: {name}: missing or shape "
                            f"{None if ent is None else list(ent.shape)} vs {list(shape)}", ERR_ARG)
         _upload(gpu, name, som.tensor_view(name), *shape)
+        if uploaded is not None:
+            uploaded.append(name)
     key = layer_key or f"{p}.moe"
     gpu.moe_register(key, router, experts, E, H, F, k)
     return key

@@ -146,3 +146,47 @@ def test_moe_layer_from_som_matches_cpu(gpu, orc, tmp_path):
         finally:
             for name, *_ in ts:
                 gpu.weight_drop(name)
+
+
+def test_prepare_decode_declined_leaves_nothing_resident(gpu, orc, tmp_path):
+    """A model that passes decode_plan but that the device step declines
+    (layer 1's MoE experts have Q8_0 down projections, which the step's
+    single-token MoE path does not run): prepare_decode raises, and every
+    weight it uploaded and the MoE layer it registered are gone again, so a
+    caller that falls back to the CPU keeps no device memory for it."""
+    L, H, nh, nkv, F, V, ctx = 2, 512, 4, 2, 1024, 300, 16
+    m = Model(orc, L, H, nh, nkv, F, V, 83)
+    E, FF, K = 4, 256, 2
+    moe = Layer(orc, E, H, FF, K, 84, dt_down=som.DTYPE_Q8_0)
+    embed = orc.normal(V * H, 1.0, 83, 9002).reshape(V, H)
+    man = som.Manifest(name="gpu-declined", vocab_size=V, hidden_dim=H, num_layers=L, num_heads=nh,
+                       num_kv_heads=nkv, ffn_dim=F, max_seq=ctx, rope_theta=5e5, rms_eps=1e-5)
+    man.fill_layers_from_globals()
+    ls = man.layers[1]
+    ls.ffn_kind, ls.num_experts, ls.num_experts_per_tok, ls.moe_ffn_dim = som.FFN_MOE, E, K, FF
+    ts = []
+    for l, lw in enumerate(m.layers):
+        for k, nm in NAMES.items():
+            if l == 1 and k in ("gate", "up", "down"):
+                continue
+            dt, r, c = m.shapes(k)
+            ts.append((f"L{l:02}.{nm}", dt, (c,) if r == 1 else (r, c), lw[k]))
+    ts.append(("L01.ffn_gate_inp", som.DTYPE_F32, (E, H), moe.router))
+    for e in range(E):
+        ts += [(f"L01.E{e:02}.ffn_gate", som.DTYPE_Q4_K, (FF, H), moe.gate[e]),
+               (f"L01.E{e:02}.ffn_up", som.DTYPE_Q4_K, (FF, H), moe.up[e]),
+               (f"L01.E{e:02}.ffn_down", som.DTYPE_Q8_0, (H, FF), moe.down[e])]
+    ts += [("output_norm", som.DTYPE_F32, (H,), m.out_norm), ("embed", som.DTYPE_F32, (V, H), embed),
+           ("lm_head", m.head_dtype, (V, H), m.head)]
+    som.write_model(str(tmp_path), man, ts)
+    before = gpu.stats()
+    with som.SomModel.open(str(tmp_path)) as s:
+        som.decode_plan(s)  # the plan itself accepts the model
+        with pytest.raises(som.SomError, match="declined"):
+            som.prepare_decode(gpu, s, "som.declined", ctx_max=ctx)
+    after = gpu.stats()
+    assert after["weights_resident"] == before["weights_resident"], (before, after)
+    assert after["weight_bytes_resident"] == before["weight_bytes_resident"]
+    # no key of the model is resident any more: dropping one finds nothing
+    for name, *_ in ts:
+        assert not gpu.weight_drop(name), name

@@ -460,6 +460,41 @@ def test_rmsnorm_and_rope_closed_forms(orc):
     assert np.allclose(z[1:128:2], a * np.sin(ang) + b * np.cos(ang), atol=1e-5)
 
 
+@pytest.mark.parametrize("pos", [0, 1, 7, 4096])
+def test_rope_neox_closed_form(orc, pos):
+    """rope_cabezas' NeoX branch (crates/soso-llm-core/src/gemm.rs:1474-1479):
+    pair i is (i, i + d/2), not (2i, 2i + 1), rotated by pos * theta^(-2i/d).
+    Checked per head against a float64 rotation; pos 0 is the identity, and a
+    mistake such as rotating interleaved pairs, swapping the sine's sign or
+    taking the frequency of the wrong index fails the check."""
+    L = orc.lib()
+    hd, nh, theta = 128, 3, 1000000.0
+    v = orc.normal(nh * hd, 1.0, 8, pos + 1)
+    z = v.copy()
+    L.or_rope_heads(z.ctypes.data, nh, hd, pos, np.float32(theta), 1)
+    if pos == 0:
+        assert np.array_equal(z, v)
+        return
+    half = hd // 2
+    i = np.arange(half)
+    ang = pos * np.float64(theta) ** (-2.0 * i / hd)
+    # f32 angles at large pos: allow the angle's own rounding (|pos * freq| ulp)
+    tol = 1e-5 + 4 * pos * np.finfo(np.float32).eps
+    for h in range(nh):
+        a = v[h * hd:h * hd + half].astype(np.float64)
+        b = v[h * hd + half:(h + 1) * hd].astype(np.float64)
+        assert np.allclose(z[h * hd:h * hd + half], a * np.cos(ang) - b * np.sin(ang), atol=tol), h
+        assert np.allclose(z[h * hd + half:(h + 1) * hd], a * np.sin(ang) + b * np.cos(ang), atol=tol), h
+    # the interleaved branch moves other elements: the two differ
+    w = v.copy()
+    L.or_rope_heads(w.ctypes.data, nh, hd, pos, np.float32(theta), 0)
+    assert not np.allclose(w, z, atol=1e-3)
+    # the rotation keeps each pair's norm
+    za, zb = z[:half].astype(np.float64), z[half:hd].astype(np.float64)
+    va, vb = v[:half].astype(np.float64), v[half:hd].astype(np.float64)
+    assert np.allclose(za ** 2 + zb ** 2, va ** 2 + vb ** 2, rtol=1e-5)
+
+
 def test_attention_matches_f64_softmax(orc):
     L = orc.lib()
     hd, kvd, n = 128, 1024, 300

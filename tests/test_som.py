@@ -485,3 +485,41 @@ def test_write_model_and_decode_plan(tmp_path):
     with som.SomModel.open(str(tmp_path / "shape")) as s:
         with pytest.raises(som.SomError, match="L00.attn_k"):
             som.decode_plan(s)
+
+
+@pytest.mark.parametrize("part", ["q", "k", "v"])
+def test_decode_plan_refuses_attention_biases(tmp_path, part):
+    """A Qwen2 conversion (NeoX RoPE) writes L{ll}.attn_{q,k,v}.bias
+    (gguf2som/src/lib.rs:673-680), which soso's CPU layer adds
+    (layer.rs:1146-1163).  The device step has no bias term, so decode_plan
+    refuses such a model with the reason, as soso's device MoE layer declines
+    it (moe_gpu.rs:85-90), instead of returning wrong logits."""
+    import copy
+    H, nh, nkv, F, V, L = 256, 2, 1, 512, 64, 2
+    man = som.Manifest(name="b", vocab_size=V, hidden_dim=H, num_layers=L, num_heads=nh, num_kv_heads=nkv,
+                       ffn_dim=F, max_seq=64, rope_theta=1e6, rms_eps=1e-6)
+    man.fill_layers_from_globals()
+    for ls in man.layers:
+        ls.flags = som.FLAG_ROPE_NEOX
+    qd, kvd = nh * 128, nkv * 128
+
+    def t(name, dtype, shape):
+        e = som.make_entry(dtype, 0, name, "", 0, shape)
+        return (name, dtype, shape, np.zeros(e.byte_len, np.uint8))
+
+    ts = []
+    for l in range(L):
+        p = f"L{l:02}"
+        ts += [t(f"{p}.attn_norm", 1, (H,)), t(f"{p}.attn_q", 3, (qd, H)), t(f"{p}.attn_k", 3, (kvd, H)),
+               t(f"{p}.attn_v", 3, (kvd, H)), t(f"{p}.attn_output", 3, (H, qd)), t(f"{p}.ffn_norm", 1, (H,)),
+               t(f"{p}.ffn_gate", 3, (F, H)), t(f"{p}.ffn_up", 3, (F, H)), t(f"{p}.ffn_down", 3, (H, F))]
+    ts += [t("output_norm", 1, (H,)), t("embed", 1, (V, H))]
+    som.write_model(str(tmp_path / "nobias"), copy.deepcopy(man), ts)
+    with som.SomModel.open(str(tmp_path / "nobias")) as s:
+        assert som.decode_plan(s)[2]["flags"] == 2
+    dim = qd if part == "q" else kvd
+    som.write_model(str(tmp_path / "bias"), man, ts + [t(f"L01.attn_{part}.bias", 1, (dim,))])
+    with som.SomModel.open(str(tmp_path / "bias")) as s:
+        with pytest.raises(som.SomError, match="bias") as ei:
+            som.decode_plan(s)
+        assert ei.value.rc == som.ERR_ARG
