@@ -51,14 +51,20 @@ constexpr int MF_SCAN_MAX = 512;    // ranked slots an expert workgroup scans it
 constexpr int MF_NW_MAX = 16;
 
 // LDS per token for kc staged columns: digits [sub-block][3][32 B], then the
-// f32 sums of x per sub-block, then 2^-e per super-block; the token stride is
-// rounded up to 16 bytes (804 bytes per super-block would leave the 8-byte
-// digit accesses of every other token misaligned when kc / 256 is odd, e.g. the
-// 768 columns of the MoE down projection: measured twice as slow).
+// f32 sums of x per sub-block, then 2^-e per super-block, then (16-byte
+// aligned) the outlier mask, one bit per element (byte c: chunk c's eight);
+// the token stride is rounded up to 16 bytes (804 bytes per super-block would
+// leave the 8-byte digit accesses of every other token misaligned when kc / 256
+// is odd, e.g. the 768 columns of the MoE down projection: measured twice as
+// slow).
+__host__ __device__ inline int mf_mask_off(int kc) { return (kc / 32 * 100 + kc / 256 * 4 + 15) & ~15; }
 __host__ __device__ inline int mf_tok_bytes(int kc)
 {
-    return (kc / 32 * 96 + kc / 32 * 4 + kc / 256 * 4 + 15) & ~15;
+    return (mf_mask_off(kc) + kc / 8 + 15) & ~15;
 }
+// The MoE experts that scan the ranking keep their slot list (16-bit entries)
+// ahead of the tokens' staging in dynamic LDS.
+__host__ __device__ inline int mf_scan_bytes(int nslots) { return (2 * nslots + 15) & ~15; }
 
 // One super-block of one weight row as a lane loads it: the 16-byte header
 // (d, dmin, 12 scale bytes) and, for each of the 4 units, the 8 code bytes of
@@ -158,19 +164,96 @@ __device__ __forceinline__ void mf_scales(const uint4 &h, MfScale &s)
 
 __device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (8 * j)) & 0xffu); }
 
+// One 8-element chunk c of a token's row (tp: the token's staging) into LDS:
+// the three digit planes, the sub-block's f32 sum, the super-block's 2^-e
+// (NaN for a non-finite one) and the chunk's outlier bits.  The 32 lanes of a
+// super-block and the 16 of a 128-element block run it together (invalid
+// chunks carry zeros and write nothing).  Outliers follow the single-token
+// staging's rule (stage_chunk<OUTL>) per 128-element block: above 16 times
+// the third largest of the block's chunk maxima.  They get zero digits, stay
+// out of the exponent and the sums, and are marked in the mask; the products
+// then add w * x for them with w dequantized exactly (mf_outliers).  FAST:
+// the cheap test only -- a block whose maximum is within 16x of its smallest
+// 4-chunk maximum has none (the two largest chunks sit in at most two
+// quads); when some block of the wavefront fails it, nothing is written and
+// false is returned (uniform), for the caller to stage the chunk again
+// through the full search.
+template <bool FAST>
+__device__ __forceinline__ bool mf_chunk(float4 v0, float4 v1, uint8_t *tp, int c, int kc, bool valid)
+{
+    float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float mx = fmaxf(fmaxf(fmaxf(fabsf(vv[0]), fabsf(vv[1])), fmaxf(fabsf(vv[2]), fabsf(vv[3]))),
+                     fmaxf(fmaxf(fabsf(vv[4]), fabsf(vv[5])), fmaxf(fabsf(vv[6]), fabsf(vv[7]))));
+    // f32 sum of x over the 32-element sub-block: 4 aligned lanes
+    float sm = ((vv[0] + vv[1]) + (vv[2] + vv[3])) + ((vv[4] + vv[5]) + (vv[6] + vv[7]));
+    if (sm != sm) mx = INFINITY; // a NaN element: the super-block is non-finite
+    float q = fmaxf(mx, dpp_f<0xB1>(mx));
+    q = fmaxf(q, dpp_f<0x4E>(q));
+    const float hq = fmaxf(q, dpp_f<0x141>(q));
+    const float m1 = fmaxf(hq, dpp_f<0x140>(hq)); // the 128-element block's maximum
+    float qn = fminf(q, dpp_f<0x141>(q));
+    qn = fminf(qn, dpp_f<0x140>(qn));
+    uint32_t om = 0;
+    bool none = __ballot(m1 > 16.0f * qn) == 0;
+    if constexpr (FAST) {
+        if (!none) return false;
+    } else if (!none) {
+        const float thr = outlier_thr16(mx, m1);
+        none = __ballot(m1 > thr) == 0;
+        if (!none) {
+            float km = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                if (fabsf(vv[i]) > thr) {
+                    om |= 1u << i;
+                    vv[i] = 0.0f;
+                }
+                km = fmaxf(km, fabsf(vv[i]));
+            }
+            mx = row16_max(km);
+            sm = ((vv[0] + vv[1]) + (vv[2] + vv[3])) + ((vv[4] + vv[5]) + (vv[6] + vv[7]));
+        }
+    }
+    if (none) mx = m1;
+    // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    const bool finite = mx < INFINITY;
+    const int ex = (mx > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+    sm += dpp_f<0xB1>(sm);
+    sm += dpp_f<0x4E>(sm);
+    if (valid) {
+        uint32_t d0[XDIG], d1[XDIG];
+        digits4(make_float4(vv[0], vv[1], vv[2], vv[3]), ex, d0);
+        digits4(make_float4(vv[4], vv[5], vv[6], vv[7]), ex, d1);
+        const int sbl = c >> 2, qq = c & 3;
+#pragma unroll
+        for (int kk = 0; kk < XDIG; kk++)
+            *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * qq) = make_uint2(d0[kk], d1[kk]);
+        if (qq == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
+        // a non-finite super-block: NaN products, as the CPU's dot gives Inf or NaN
+        if ((c & 31) == 0)
+            *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
+        tp[mf_mask_off(kc) + c] = (uint8_t)om;
+    }
+    return true;
+}
+
 // Stages columns k0 .. k0 + kc of the round's nt tokens (x rows slot_s[t] / xdiv)
-// into LDS, token t at t * mf_tok_bytes(kc): per 32-element sub-block the
-// three digit planes (32 bytes each), then the f32 sums of x per sub-block,
-// then 2^-e per 256-element super-block (NaN for a non-finite one).
+// into LDS, token t at t * mf_tok_bytes(kc) (mf_chunk).  Four chunks per
+// thread are requested together, then converted (one L2 round trip per
+// 4 * 64 * NW chunks) through the cheap outlier test; rounds that fail it are
+// staged again afterwards through the full search, one at a time, from x
+// (rare: the unrolled loop stays free of that code).
 template <int NW>
 __device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__ xs, const int *slot_s, int xdiv, int cols,
                                          int k0, int kc, int nt)
 {
     const int tb = mf_tok_bytes(kc);
     const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
-    // four chunks per thread are requested together, then converted
-    // (one L2 round trip per 4 * 64 * NW chunks)
     constexpr int NT = 64 * NW, XB = 4;
+    auto xchunk = [&](int f) {
+        return (const float4 *)(xs + (size_t)(slot_s[f / cpt] / xdiv) * cols + k0) + 2 * (f % cpt);
+    };
     for (int fb = 0; fb < tot; fb += XB * NT) {
         float4 v0[XB], v1[XB];
 #pragma unroll
@@ -178,46 +261,121 @@ __device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__
             const int f = fb + k * NT + (int)threadIdx.x;
             v0[k] = v1[k] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (f < tot) {
-                const float4 *x4 =
-                    (const float4 *)(xs + (size_t)(slot_s[f / cpt] / xdiv) * cols + k0) + 2 * (f % cpt);
+                const float4 *x4 = xchunk(f);
                 v0[k] = x4[0];
                 v1[k] = x4[1];
             }
         }
+        uint32_t redo = 0; // uniform
 #pragma unroll
         for (int k = 0; k < XB; k++) {
             if (fb + k * NT >= tot) break; // uniform
             const int f = fb + k * NT + (int)threadIdx.x;
             const bool valid = f < tot;
-            const int tt = valid ? f / cpt : 0, c = f % cpt;
-            // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
-            float mx = fmaxf(fmaxf(fmaxf(fabsf(v0[k].x), fabsf(v0[k].y)), fmaxf(fabsf(v0[k].z), fabsf(v0[k].w))),
-                             fmaxf(fmaxf(fabsf(v1[k].x), fabsf(v1[k].y)), fmaxf(fabsf(v1[k].z), fabsf(v1[k].w))));
-            // f32 sum of x over the 32-element sub-block: 4 aligned lanes
-            float sm = ((v0[k].x + v0[k].y) + (v0[k].z + v0[k].w)) + ((v1[k].x + v1[k].y) + (v1[k].z + v1[k].w));
-            if (sm != sm) mx = INFINITY; // a NaN element: the super-block is non-finite
-            mx = row16_max(mx);
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            const bool finite = mx < INFINITY;
-            const int ex = (mx > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
-            sm += dpp_f<0xB1>(sm);
-            sm += dpp_f<0x4E>(sm);
-            if (valid) {
-                uint32_t d0[XDIG], d1[XDIG];
-                digits4(v0[k], ex, d0);
-                digits4(v1[k], ex, d1);
-                uint8_t *tp = lds + (size_t)tt * tb;
-                const int sbl = c >> 2, q = c & 3;
-#pragma unroll
-                for (int kk = 0; kk < XDIG; kk++)
-                    *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * q) = make_uint2(d0[kk], d1[kk]);
-                if (q == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
-                // a non-finite super-block: NaN products, as the CPU's dot gives Inf or NaN
-                if ((c & 31) == 0)
-                    *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
+            if (!mf_chunk<true>(v0[k], v1[k], lds + (size_t)(valid ? f / cpt : 0) * tb, f % cpt, kc, valid))
+                redo |= 1u << k;
+        }
+        if (__builtin_expect(redo != 0, 0)) {
+#pragma unroll 1
+            for (int k = 0; k < XB; k++) {
+                if (!((redo >> k) & 1u)) continue; // uniform
+                const int f = fb + k * NT + (int)threadIdx.x;
+                const bool valid = f < tot;
+                float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+                if (valid) {
+                    const float4 *x4 = xchunk(f);
+                    a = x4[0];
+                    b = x4[1];
+                }
+                mf_chunk<false>(a, b, lds + (size_t)(valid ? f / cpt : 0) * tb, f % cpt, kc, valid);
             }
         }
     }
+}
+
+// Dword di (0 .. 2N - 1) of lane src's pieces q[0 .. N - 1] (two dwords each),
+// through ds_bpermute (every lane must run it).
+template <int N>
+__device__ __forceinline__ uint32_t mf_fetch(const uint2 (&q)[N], int src, int di)
+{
+    uint32_t r = 0;
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const uint32_t x = (uint32_t)__builtin_amdgcn_ds_bpermute(src * 4, (int)q[i].x);
+        const uint32_t y = (uint32_t)__builtin_amdgcn_ds_bpermute(src * 4, (int)q[i].y);
+        r = di == 2 * i ? x : di == 2 * i + 1 ? y : r;
+    }
+    return r;
+}
+
+// Whether any of the round's nt staged tokens has an outlier (after the
+// staging's barrier; every wavefront reads the masks itself).
+__device__ __forceinline__ bool mf_any_outliers(const uint8_t *lds, int tb, int kc, int nt)
+{
+    const int nb = kc >> 7, tot = nt * nb;
+    bool any = false;
+    for (int i = (int)(threadIdx.x & 63); i < tot; i += 64) {
+        const uint4 m = *(const uint4 *)(lds + (size_t)(i / nb) * tb + mf_mask_off(kc) + 16 * (i % nb));
+        any = any || (m.x | m.y | m.z | m.w) != 0u;
+    }
+    return __ballot(any) != 0;
+}
+
+// Whether any of the round's nt tokens has outliers in super-block sbl of the
+// staged chunk; uniform.
+__device__ __forceinline__ bool mf_sb_has_outliers(const uint8_t *lds, int tb, int kc, int nt, int sbl)
+{
+    const int lane = (int)(threadIdx.x & 63), t = lane >> 1;
+    bool any = false;
+    for (int t0 = 0; t0 < nt; t0 += 32) {
+        if (t0 + t < nt) {
+            const uint4 m =
+                *(const uint4 *)(lds + (size_t)(t0 + t) * tb + mf_mask_off(kc) + 32 * sbl + 16 * (lane & 1));
+            any = any || (m.x | m.y | m.z | m.w) != 0u;
+        }
+    }
+    return __ballot(any) != 0;
+}
+
+// The outliers' share of super-block sbl for this lane's weight row and the
+// token staged at tp, whose x row (from the chunk's first column) is xr
+// (valid: a token of the round): sum of w * x over the elements marked in the
+// super-block's mask, in column order, x read again from the row and w
+// dequantized exactly as the reference dequantizes (get_code(e): element e's
+// code of this lane's row, e in 0..255; wt(code, e): its weight).  Every lane
+// runs the loop (the codes come from other lanes by ds_bpermute); the count is
+// the wavefront's largest.
+template <class Code, class Wt>
+__device__ __forceinline__ float mf_outliers(const uint8_t *tp, const float *xr, int kc, int sbl, bool valid,
+                                             Code get_code, Wt wt)
+{
+    uint4 ma = make_uint4(0u, 0u, 0u, 0u), mb = ma;
+    if (valid) {
+        ma = *(const uint4 *)(tp + mf_mask_off(kc) + 32 * sbl);
+        mb = *(const uint4 *)(tp + mf_mask_off(kc) + 32 * sbl + 16);
+    }
+    uint32_t m[8] = {ma.x, ma.y, ma.z, ma.w, mb.x, mb.y, mb.z, mb.w};
+    int cnt = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) cnt += __popc(m[i]);
+    const int nmax = (int)wave_max_dpp((float)cnt);
+    float corr = 0.0f;
+    for (int k = 0; k < nmax; k++) {
+        // this lane's next marked element: the lowest set bit left
+        int e = 0;
+        bool found = false;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            if (!found && m[i] != 0u) {
+                e = 32 * i + __builtin_ctz(m[i]);
+                m[i] &= m[i] - 1u;
+                found = true;
+            }
+        }
+        const float v = found ? xr[256 * sbl + e] : 0.0f;
+        corr = fmaf(wt(get_code(e), e), v, corr);
+    }
+    return corr;
 }
 
 // The slots s < nslots with sidx[s] == e (the token t = s / top_k ranked expert
@@ -265,11 +423,12 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
 {
     constexpr int TR = 4 * MT; // tokens per round
     extern __shared__ uint4 mf_smem[];
-    uint8_t *lds = (uint8_t *)mf_smem;
+    // SCAN: the expert's slots (16-bit, as many as the call ranked) ahead of
+    // the staging: with 8 tokens' x staged (53.5 KB for 2048 columns), three
+    // gate/up workgroups still fit a CU's 160 KB of LDS
+    int16_t *scan_s = (int16_t *)mf_smem;
+    uint8_t *lds = (uint8_t *)mf_smem + (SCAN ? mf_scan_bytes(nslots) : 0);
     __shared__ int slot_s[TR];
-    // 16-bit slot list: with 8 tokens' x staged (51.5 KB for 2048 columns),
-    // three gate/up workgroups still fit a CU's 160 KB of LDS
-    __shared__ int16_t scan_s[SCAN ? MF_SCAN_MAX : 1];
     __shared__ int wtot_s[NW];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -485,6 +644,44 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            // ---- the outliers of the round's tokens: a second walk over the
+            // super-blocks that hold some (rare; outside the streaming loop,
+            // so that its registers do not add to the loop's), reloading the
+            // codes: w * x with w = fl(fl(d sc) q) - fl(dmin m)
+            // (dequant.rs:204-241).  Element e of a super-block: unit e / 64,
+            // code byte l = e % 32 of the unit (lane group l / 8 of this row
+            // holds it), the high nibble from 32 on.
+            if (__builtin_expect(mf_any_outliers(lds, tb, kc, nt), 0)) {
+                for (int i = 0; i < nsb; i++) {
+                    if (!mf_sb_has_outliers(lds, tb, kc, nt, i)) continue; // uniform
+                    MfSb S_[NMAT];
+                    load_sb(rA, sb0 + i, true, S_[0]);
+                    if constexpr (NMAT == 2) load_sb(rB, sb0 + i, true, S_[NMAT - 1]);
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        MfScale K_;
+                        mf_scales(S_[m].h, K_);
+                        auto code = [&](int e) {
+                            const int eu = e & 63, l = eu & 31;
+                            const uint32_t dw = mf_fetch<4>(S_[m].q, 16 * (l >> 3) + nl, 2 * (e >> 6) + ((l & 7) >> 2));
+                            return (dw >> (8 * (l & 3) + (eu >= 32 ? 4 : 0))) & 15u;
+                        };
+                        auto wt = [&](uint32_t q, int e) {
+                            const int j = 2 * (e >> 6) + ((e & 63) >= 32 ? 1 : 0), sh = 8 * (j & 3);
+                            const float sc = (float)(((j < 4 ? K_.sc4[0] : K_.sc4[1]) >> sh) & 0xffu);
+                            const float mn = (float)(((j < 4 ? K_.m4[0] : K_.m4[1]) >> sh) & 0xffu);
+                            return __fsub_rn(__fmul_rn(__fmul_rn(K_.d, sc), (float)q), __fmul_rn(K_.dmin, mn));
+                        };
+#pragma unroll
+                        for (int mt = 0; mt < MT; mt++) {
+                            if (mt * 4 >= nt) break; // uniform
+                            const int to = mt * 4 + g, tv = to < nt ? to : 0;
+                            const float *xr = xs + (size_t)(slot_s[tv] / xdiv) * cols + k0;
+                            accf[m][mt] += mf_outliers(lds + (size_t)tv * tb, xr, kc, i, to < nt, code, wt);
+                        }
+                    }
+                }
+            }
             __syncthreads(); // LDS is restaged for the next chunk or round
         }
         // ---- outputs: lane (row, token mt*4 + g) ----
@@ -611,6 +808,36 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict_
                 cur = nxt;
                 __builtin_amdgcn_sched_barrier(0);
             }
+            // ---- the outliers of the round's tokens: a second walk over the
+            // 256-column stretches that hold some (rare), reloading the codes:
+            // w * x with w = fl(q * scale) (dequant.rs:74-97).  Element e of a
+            // stretch: block e / 32, code byte l = e % 32 (lane group l / 8 of
+            // this row holds it).
+            if (__builtin_expect(mf_any_outliers(lds, tb, kc, nt), 0)) {
+                for (int i = 0; i < nsb; i++) {
+                    if (!mf_sb_has_outliers(lds, tb, kc, nt, i)) continue; // uniform
+                    MfQ80 o;
+                    load_sb(sb0 + i, true, o);
+                    auto code = [&](int e) {
+                        const int l = e & 31;
+                        const uint32_t dw = mf_fetch<8>(o.q, 16 * (l >> 3) + nl, 2 * (e >> 5) + ((l & 7) >> 2));
+                        return (dw >> (8 * (l & 3))) & 0xffu;
+                    };
+                    auto wt = [&](uint32_t q, int e) {
+                        const int kb = e >> 5, kq = kb & 3;
+                        const uint4 sv = kb < 4 ? o.s[0] : o.s[1];
+                        const uint32_t sbits = kq == 0 ? sv.x : kq == 1 ? sv.y : kq == 2 ? sv.z : sv.w;
+                        return __fmul_rn((float)(int8_t)(uint8_t)q, __builtin_bit_cast(float, opaque(sbits)));
+                    };
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        if (mt * 4 >= nt) break; // uniform
+                        const int to = mt * 4 + g, tv = to < nt ? to : 0;
+                        const float *xr = xs + (size_t)slot_s[tv] * cols + k0;
+                        accf[mt] += mf_outliers(lds + (size_t)tv * tb, xr, kc, i, to < nt, code, wt);
+                    }
+                }
+            }
             __syncthreads(); // LDS is restaged for the next chunk or round
         }
 #pragma unroll
@@ -664,10 +891,11 @@ int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
     if (sidx && nslots > (size_t)MF_SCAN_MAX) return set_err(h, SOSO_HIP_ERR_ARG, "mfma: too many slots to scan");
     constexpr int MT = 2;
-    const int kc = mf_kc(h, cols, 4 * MT);
+    const size_t scan_b = sidx ? (size_t)mf_scan_bytes((int)nslots) : 0;
+    const int kc = mf_kc(h, cols, 4 * MT, h->max_lds - scan_b);
     const size_t mrows = (size_t)16 * (nmat == 2 ? MF_NW_GU : MF_NW_DN); // rows per workgroup
     const size_t nblk = (rows + mrows - 1) / mrows;
-    const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc);
+    const size_t lds = scan_b + (size_t)4 * MT * mf_tok_bytes(kc);
     const unsigned grid = (unsigned)(max_recs * nblk);
     const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
     const int ri = (int)rows, ci = (int)cols, ns = (int)nslots;

@@ -28,6 +28,7 @@
 #include "mv_core.hpp"
 
 #include <algorithm>
+#include <type_traits>
 #include <vector>
 
 // ---------------------------------------------------------------------------
@@ -426,10 +427,58 @@ __device__ __forceinline__ void q4k_half(const uint32_t (&codes)[8], const uint3
         for (int k = 0; k < XDIG; k++) s[k] = sdot4(codes[t], xh[XDIG * t + k], s[k]);
 }
 
+// Code l (0..31) of one sub-block's packed nibbles (four per dword), picked
+// by a select chain: a dynamically indexed register array would go to scratch.
+__device__ __forceinline__ uint32_t q4k_code(const uint32_t (&c)[8], int l)
+{
+    const int k = l >> 2;
+    // opaque: a select chain over the array's elements could be folded into
+    // one load at a computed address, which would move the array to scratch
+    uint32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = opaque(c[i]);
+    const uint32_t a = k == 0 ? v[0] : k == 1 ? v[1] : k == 2 ? v[2] : v[3];
+    const uint32_t b = k == 4 ? v[4] : k == 5 ? v[5] : k == 6 ? v[6] : v[7];
+    return ((k < 4 ? a : b) >> (8 * (l & 3))) & 15u;
+}
+
+// Sum of w * x over the outliers (OUTL staging: the list ol of unit u's
+// 128-element block, ocnt entries, onum the longest list of the wavefront)
+// that fall in the unit, w decoded from the prepared unit exactly as
+// dequant_q4_k_range decodes it (crates/sosomodel/src/dequant.rs:204-241):
+// fl(fl(d sc) q) - fl(dmin m), with pr.ka = fl(d sc) and pr.kma = fl(dmin m).
+template <int NMAT>
+__device__ __forceinline__ void q4k_outliers(const Q4Prep (&pr)[NMAT], const uint32_t *ol, int ocnt, int onum, int u,
+                                             float (&corr)[NMAT])
+{
+    for (int k = 0; k < onum; k++) {
+        if (k < ocnt) {
+            const uint32_t p = (ol[1 + (k >> 2)] >> (8 * (k & 3))) & 0xffu;
+            if ((p >> 6) == ((uint32_t)u & 1u)) {
+                const int e = (int)(p & 63u), sub = e >> 5, l = e & 31;
+                const float v = __uint_as_float(ol[8 + k]);
+#pragma unroll
+                for (int m = 0; m < NMAT; m++) {
+                    const uint32_t q = sub ? q4k_code(pr[m].hi, l) : q4k_code(pr[m].lo, l);
+                    // (opaque for the same reason as in q4k_code)
+                    const float ka = __uint_as_float(opaque(__float_as_uint(pr[m].ka)));
+                    const float kb = __uint_as_float(opaque(__float_as_uint(pr[m].kb)));
+                    const float kma = __uint_as_float(opaque(__float_as_uint(pr[m].kma)));
+                    const float kmb = __uint_as_float(opaque(__float_as_uint(pr[m].kmb)));
+                    const float w = __fsub_rn(__fmul_rn(sub ? kb : ka, (float)q), sub ? kmb : kma);
+                    corr[m] = fmaf(w, v, corr[m]);
+                }
+            }
+        }
+    }
+}
+
 // One decoded row unit (pr[m], m < NMAT) against the x staged in LDS at xd
 // (digit planes, then the 16-element sums s16, then the 128-block exponents
-// kx): returns the row's dot in the last lane of each LPR-lane group.
-template <int LPR, int NMAT>
+// kx, then the outlier lists): returns the row's dot in the last lane of each
+// LPR-lane group.  OUTL: the outliers of the unit's block are added as w * x
+// (the kernels take that variant only for rounds that have outliers).
+template <int LPR, int NMAT, bool OUTL = false>
 __device__ __forceinline__ void q4k_token_dot(const Q4Prep (&pr)[NMAT], const uint32_t *xd, int cols, int U, int u,
                                               bool uact, float (&val)[NMAT])
 {
@@ -464,12 +513,34 @@ __device__ __forceinline__ void q4k_token_dot(const Q4Prep (&pr)[NMAT], const ui
     for (int m = 0; m < NMAT; m++) q4k_half(pr[m].hi, xh, sb[m]);
     const float P = block_unscale(kx[u >> 1]);
     const float c0 = s16[4 * u] + s16[4 * u + 1], c1 = s16[4 * u + 2] + s16[4 * u + 3];
+    float part[NMAT];
 #pragma unroll
     for (int m = 0; m < NMAT; m++) {
         const float uu = fmaf(pr[m].ka, digits_value(sa[m]), pr[m].kb * digits_value(sb[m]));
         const float vv = fmaf(pr[m].kmb, c1, pr[m].kma * c0);
-        val[m] = seg_sum_dpp<LPR>(uact ? fmaf(P, uu, -vv) : 0.0f);
+        part[m] = uact ? fmaf(P, uu, -vv) : 0.0f;
     }
+    if constexpr (OUTL) {
+        const uint32_t *ol = out_lists(kx, cols) + (u >> 1) * OUT_DW;
+        const int ocnt = uact ? min((int)ol[0], OUT_MAX) : 0;
+        if (__ballot(ocnt > 0) != 0) q4k_outliers<NMAT>(pr, ol, ocnt, (int)wave_max_dpp((float)ocnt), u, part);
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; m++) val[m] = seg_sum_dpp<LPR>(part[m]);
+}
+
+// Whether any of the nt tokens staged at smem (tok_bytes apart, cols wide, OUTL
+// staging) has a non-empty outlier list; uniform over the wavefront.
+__device__ __forceinline__ bool moe_any_outliers(const void *smem, int tok_bytes, int cols, int nt)
+{
+    const int nb = (cols + 127) >> 7, tot = nt * nb;
+    bool any = false;
+    for (int i = (int)(threadIdx.x & 63); i < tot; i += 64) {
+        const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)(i / nb) * tok_bytes);
+        const int *kx = (const int *)((const float *)(xd + (cols >> 2) * XDIG) + (cols >> 4));
+        any = any || out_lists(kx, cols)[(i % nb) * OUT_DW] != 0u;
+    }
+    return __ballot(any) != 0;
 }
 
 // One token ranked by the expert kernel itself (SELF): every workgroup takes
@@ -499,7 +570,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
     constexpr int RW = 64 / LPR, NW = 8;
     extern __shared__ uint4 smem[];
     __shared__ int slot_s[64];
-    const int tok_bytes = (int)((stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15);
+    const int tok_bytes = (int)((stage_lds_bytes_o((size_t)cols) + 15) & ~(size_t)15);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int U = cols >> 6, nch = cols >> 3;
@@ -517,6 +588,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
     __shared__ __align__(16) uint32_t self_keys[256];
     __shared__ float nrm_s[NW];
     int nit;
+    bool oany = false; // SELF: the staged token has outliers (its passes take the exact-weight loop)
     if constexpr (SELF) {
         // The ranking of topk_regs, by the whole workgroup: wavefront 0 makes
         // the keys (topk_keys; the upper word is the order, 0 for experts
@@ -590,7 +662,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
 #pragma unroll
             for (int k = 0; k < MOE_XK; k++) {
                 const int f = k * 512 + (int)threadIdx.x;
-                if (k * 512 < nch) stage_chunk<FMT>(xv0[k], xv1[k], f % nch, f < nch, U, xd, s16, kx);
+                if (k * 512 < nch) stage_chunk<FMT, true>(xv0[k], xv1[k], f % nch, f < nch, U, xd, s16, kx);
             }
             for (int fb = MOE_XK * 512; fb < nch; fb += 512) { // rows longer than one round holds
                 const int f = fb + (int)threadIdx.x;
@@ -600,7 +672,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                     v0 = x4[0];
                     v1 = x4[1];
                 }
-                stage_chunk<FMT>(v0, v1, f % nch, f < nch, U, xd, s16, kx);
+                stage_chunk<FMT, true>(v0, v1, f % nch, f < nch, U, xd, s16, kx);
             }
         }
         __syncthreads();
@@ -646,6 +718,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
             sr.wgt[threadIdx.x] = self_wgt[threadIdx.x];
         }
         nit = sr.top_k * sr.chunks;
+        oany = moe_any_outliers(smem, tok_bytes, cols, 1);
     } else {
         nit = *n_items;
     }
@@ -692,6 +765,67 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                 if ((int)threadIdx.x < nt) slot_s[threadIdx.x] = list[base + t0 + threadIdx.x];
             }
             __builtin_amdgcn_sched_barrier(0);
+            // The passes: Q4_K rows are decoded once per pass (q4k_prep) and
+            // applied to every staged token; a token's x is read from LDS one
+            // sub-block (24 dwords) at a time.  OUTL (a constant): the
+            // tokens' outliers are added with their exactly decoded weights
+            // (the grouped path always; the self-ranked path only when its
+            // token has some, through the loop just below).
+            auto pass_q4k = [&](int j, const Q4Prep (&pr)[NMAT], auto outl) {
+                const int row = r0 + (j * NW + wave) * RW + slot;
+                for (int tk = 0; tk < nt; tk++) {
+                    const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)tk * tok_bytes);
+                    float val[NMAT];
+                    q4k_token_dot<LPR, NMAT, decltype(outl)::value>(pr, xd, cols, U, u, uact, val);
+                    float v = val[0];
+                    if constexpr (NMAT == 2) v = silu(val[0]) * val[1];
+                    if (ul == LPR - 1 && row < rend) out[(size_t)(SELF ? self_slot : slot_s[tk]) * rows + row] = v;
+                }
+            };
+            auto pass = [&](int j, const WRow<FMT> &pa_w, const WRow<FMT> &pb_w, auto outl) {
+                constexpr bool OL = decltype(outl)::value;
+                const int row = r0 + (j * NW + wave) * RW + slot;
+                for (int tk = 0; tk < nt; tk++) {
+                    const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)tk * tok_bytes);
+                    const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
+                    const int *kx = (const int *)(s16 + (cols >> 4));
+                    XReg xv;
+                    UConst cj = c;
+                    unit_setup_x<FMT, OL>(xd, s16, kx, u, U, xv, cj);
+                    float pa = uact ? unit_dot<FMT>(pa_w, xv, cj) : 0.0f, pb = 0.0f;
+                    if constexpr (NMAT == 2) pb = uact ? unit_dot<FMT>(pb_w, xv, cj) : 0.0f;
+                    if (OL && cj.onum != 0) {
+                        // the outliers of the unit's block, exactly weighted
+                        cj.ocnt = uact ? cj.ocnt : 0;
+                        cj.onum = (int)wave_max_dpp((float)cj.ocnt);
+                        pa += unit_outliers<FMT>(pa_w, cj, u);
+                        if constexpr (NMAT == 2) pb += unit_outliers<FMT>(pb_w, cj, u);
+                    }
+                    float v = seg_sum_dpp<LPR>(pa);
+                    if constexpr (NMAT == 2) v = silu(v) * seg_sum_dpp<LPR>(pb);
+                    if (ul == LPR - 1 && row < rend) out[(size_t)(SELF ? self_slot : slot_s[tk]) * rows + row] = v;
+                }
+            };
+            if (SELF && __builtin_expect(oany, 0)) {
+                // the self-ranked token has outliers (known before the ring is
+                // issued): every pass loaded on its own and the outliers added
+                // with their exactly decoded weights, so that the streaming
+                // loop below stays free of that code
+                for (int j = 0; j < P; j++) {
+                    WRow<FMT> ra, rb;
+                    load_row<FMT>(rA, lane_base + (uint32_t)j * pass_bytes, cols, L, ra);
+                    if constexpr (NMAT == 2) load_row<FMT>(rB, lane_base + (uint32_t)j * pass_bytes, cols, L, rb);
+                    if constexpr (FMT == FMT_Q4K) {
+                        Q4Prep pr[NMAT];
+                        q4k_prep(ra, c, pr[0]);
+                        if constexpr (NMAT == 2) q4k_prep(rb, c, pr[NMAT - 1]);
+                        pass_q4k(j, pr, std::true_type{});
+                    } else {
+                        pass(j, ra, rb, std::true_type{});
+                    }
+                }
+                continue;
+            }
             // 2. the ring
             WRow<FMT> wa[DEPTH], wb[DEPTH];
 #pragma unroll
@@ -710,7 +844,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                         uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)(f < tot ? tk : 0) * tok_bytes);
                         float *s16 = (float *)(xd + (cols >> 2) * XDIG);
                         int *kx = (int *)(s16 + (cols >> 4));
-                        stage_chunk<FMT>(xv0[k], xv1[k], f % nch, f < tot, U, xd, s16, kx);
+                        stage_chunk<FMT, true>(xv0[k], xv1[k], f % nch, f < tot, U, xd, s16, kx);
                     }
                 }
                 for (int fb = MOE_XK * 512; fb < tot; fb += 512) { // more tokens than one round holds
@@ -725,7 +859,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                     uint32_t *xd = (uint32_t *)((uint8_t *)smem + (size_t)(f < tot ? tk : 0) * tok_bytes);
                     float *s16 = (float *)(xd + (cols >> 2) * XDIG);
                     int *kx = (int *)(s16 + (cols >> 4));
-                    stage_chunk<FMT>(v0, v1, f % nch, f < tot, U, xd, s16, kx);
+                    stage_chunk<FMT, true>(v0, v1, f % nch, f < tot, U, xd, s16, kx);
                 }
                 __syncthreads();
             }
@@ -733,34 +867,6 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
             // Q4_K: each pass's rows are decoded once (q4k_prep) and the ring
             // slot is refilled before the tokens are applied; a token's x is
             // read from LDS one sub-block (24 dwords) at a time.
-            auto pass_q4k = [&](int j, const Q4Prep (&pr)[NMAT]) {
-                const int row = r0 + (j * NW + wave) * RW + slot;
-                for (int tk = 0; tk < nt; tk++) {
-                    const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)tk * tok_bytes);
-                    float val[NMAT];
-                    q4k_token_dot<LPR, NMAT>(pr, xd, cols, U, u, uact, val);
-                    float v = val[0];
-                    if constexpr (NMAT == 2) v = silu(val[0]) * val[1];
-                    if (ul == LPR - 1 && row < rend) out[(size_t)(SELF ? self_slot : slot_s[tk]) * rows + row] = v;
-                }
-            };
-            auto pass = [&](int j, const WRow<FMT> &pa_w, const WRow<FMT> &pb_w) {
-                const int row = r0 + (j * NW + wave) * RW + slot;
-                for (int tk = 0; tk < nt; tk++) {
-                    const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)tk * tok_bytes);
-                    const float *s16 = (const float *)(xd + (cols >> 2) * XDIG);
-                    const int *kx = (const int *)(s16 + (cols >> 4));
-                    XReg xv;
-                    UConst cj = c;
-                    unit_setup_x<FMT>(xd, s16, kx, u, U, xv, cj);
-                    float v = seg_sum_dpp<LPR>(uact ? unit_dot<FMT>(pa_w, xv, cj) : 0.0f);
-                    if constexpr (NMAT == 2) {
-                        const float pb = seg_sum_dpp<LPR>(uact ? unit_dot<FMT>(pb_w, xv, cj) : 0.0f);
-                        v = silu(v) * pb;
-                    }
-                    if (ul == LPR - 1 && row < rend) out[(size_t)(SELF ? self_slot : slot_s[tk]) * rows + row] = v;
-                }
-            };
             const int turns = P / DEPTH;
             int j0 = 0;
             for (int tr = 0; tr < turns; tr++, j0 += DEPTH) {
@@ -774,9 +880,9 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                         if constexpr (NMAT == 2)
                             load_row<FMT>(rB, lane_base + (uint32_t)(j0 + i + DEPTH) * pass_bytes, cols, L, wb[i]);
                         __builtin_amdgcn_sched_barrier(0);
-                        pass_q4k(j0 + i, pr);
+                        pass_q4k(j0 + i, pr, std::integral_constant<bool, !SELF>{});
                     } else {
-                        pass(j0 + i, wa[i], wb[i]);
+                        pass(j0 + i, wa[i], wb[i], std::integral_constant<bool, !SELF>{});
                         load_row<FMT>(rA, lane_base + (uint32_t)(j0 + i + DEPTH) * pass_bytes, cols, L, wa[i]);
                         if constexpr (NMAT == 2)
                             load_row<FMT>(rB, lane_base + (uint32_t)(j0 + i + DEPTH) * pass_bytes, cols, L, wb[i]);
@@ -791,9 +897,9 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                         Q4Prep pr[NMAT];
                         q4k_prep(wa[i], c, pr[0]);
                         if constexpr (NMAT == 2) q4k_prep(wb[i], c, pr[NMAT - 1]);
-                        pass_q4k(j0 + i, pr);
+                        pass_q4k(j0 + i, pr, std::integral_constant<bool, !SELF>{});
                     } else {
-                        pass(j0 + i, wa[i], wb[i]);
+                        pass(j0 + i, wa[i], wb[i], std::integral_constant<bool, !SELF>{});
                     }
                 }
             if constexpr (!SELF) __syncthreads(); // LDS and slot_s are restaged next
@@ -824,7 +930,7 @@ __global__ void __launch_bounds__(512) k_moe_down_comb(const uint8_t *const *__r
     constexpr int RW = 64 / LPR, RB = RW * P; // rows per item
     extern __shared__ uint4 smem[];
     __shared__ float dots[MDC_K][RB];
-    const int tok_bytes = (int)((stage_lds_bytes((size_t)cols) + 15) & ~(size_t)15);
+    const int tok_bytes = (int)((stage_lds_bytes_o((size_t)cols) + 15) & ~(size_t)15);
     const int lane = threadIdx.x & 63;
     const int j = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); // ranked slot of this wavefront
     const int U = cols >> 6, nch = cols >> 3;
@@ -867,16 +973,31 @@ __global__ void __launch_bounds__(512) k_moe_down_comb(const uint8_t *const *__r
         // 3. act into this wavefront's LDS region (16-chunk blocks: nch % 16 == 0)
 #pragma unroll
         for (int k = 0; k < MDC_XR; k++)
-            if (64 * k < nch) stage_chunk<FMT_Q4K>(xv0[k], xv1[k], 64 * k + lane, 64 * k + lane < nch, U, xd, s16, kx);
+            if (64 * k < nch) stage_chunk<FMT_Q4K, true>(xv0[k], xv1[k], 64 * k + lane, 64 * k + lane < nch, U, xd, s16, kx);
         __syncthreads();
-        // 4. the dots of this wavefront's rows
+        // 4. the dots of this wavefront's rows.  When its act row has
+        // outliers (a uniform branch per wavefront), their w * x is taken
+        // first from the raw rows, with w decoded exactly as the reference
+        // decodes it, and joins each row's dot.
+        const bool oany = moe_any_outliers(xd, 0, cols, 1);
+        float corr[P];
+#pragma unroll
+        for (int p = 0; p < P; p++) corr[p] = 0.0f;
+        if (__builtin_expect(oany, 0)) {
+            UConst co = c;
+            co.ol = out_lists(kx, cols) + (u >> 1) * OUT_DW;
+            co.ocnt = uact ? min((int)co.ol[0], OUT_MAX) : 0;
+            co.onum = (int)wave_max_dpp((float)co.ocnt);
+#pragma unroll
+            for (int p = 0; p < P; p++) corr[p] = seg_sum_dpp<LPR>(unit_outliers<FMT_Q4K>(w[p], co, u));
+        }
 #pragma unroll
         for (int p = 0; p < P; p++) {
             Q4Prep pr[1];
             q4k_prep(w[p], c, pr[0]);
             float val[1];
             q4k_token_dot<LPR, 1>(pr, xd, cols, U, u, uact, val);
-            if (ul == LPR - 1) dots[j][p * RW + slot] = val[0];
+            if (ul == LPR - 1) dots[j][p * RW + slot] = val[0] + corr[p];
         }
         __syncthreads();
         // 5. the weighted sum in ranking order, one lane per row
@@ -1055,7 +1176,7 @@ static int launch_moe_mv(soso_hip *h, uint8_t dtype, int nmat, const uint8_t *co
     const size_t rows_per_pass = 8 * (64 / lpr);
     const size_t passes = (rows + rows_per_pass - 1) / rows_per_pass;
     tch = std::max<size_t>(1, std::min<size_t>(tch, 64));
-    const size_t tok_bytes = (stage_lds_bytes(cols) + 15) & ~(size_t)15;
+    const size_t tok_bytes = (stage_lds_bytes_o(cols) + 15) & ~(size_t)15;
     while (tch > 1 && tok_bytes * tch > h->max_lds) tch--;
     const size_t lds = tok_bytes * tch;
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "moe: x does not fit in LDS");
@@ -1123,14 +1244,14 @@ const char *moe_ffn1_unsupported(const soso_hip *h, const MoeLayer &m)
                        U >= 1 && U <= 64 && hdim % 128 == 0 && packed_shape_ok(m.dt_gu, ffn, hdim);
     if (!gu_ok) return "gate/up: Q4_K, Q8_0 or Q6_K rows of 128 to 4096 columns (a multiple of 128)";
     const bool down_ok = m.dt_down == SOSO_HIP_DTYPE_Q4_K && ffn % 256 == 0 && Uf >= 4 && Uf <= 8 * (size_t)MDC_XR &&
-                         ((stage_lds_bytes(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds &&
+                         ((stage_lds_bytes_o(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds &&
                          packed_shape_ok(m.dt_down, hdim, ffn);
     if (!down_ok) return "down: Q4_K, expert width 256 to 2048 (a multiple of 256)";
     if (top_k == 0 || top_k > (size_t)MOE_SELF_K || n_exp > 256) return "top_k above 8 or more than 256 experts";
     const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
     const size_t rows_per_pass = 8 * (64 / lpr), passes = (ffn + rows_per_pass - 1) / rows_per_pass;
     const size_t stride = packed_row_stride(m.dt_gu, hdim);
-    const size_t lds = (stage_lds_bytes(hdim) + 15) & ~(size_t)15;
+    const size_t lds = (stage_lds_bytes_o(hdim) + 15) & ~(size_t)15;
     if (lds > h->max_lds || (passes + 2) * rows_per_pass * stride >= ((size_t)1 << 31)) return "expert too large";
     return nullptr;
 }
@@ -1148,7 +1269,7 @@ int launch_moe_ffn1(soso_hip *h, const MoeLayer &m, const float *x, const MoeScr
     const int U = (int)(hdim / 64);
     const int lpr = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
     const size_t stride = packed_row_stride(m.dt_gu, hdim);
-    const size_t lds = (stage_lds_bytes(hdim) + 15) & ~(size_t)15;
+    const size_t lds = (stage_lds_bytes_o(hdim) + 15) & ~(size_t)15;
     // the route kernel's item count for one token: about moe_item_target
     // chunks in all, the same share for every ranked expert
     const int chunks = std::max(1, (moe_item_target(h) + (int)top_k / 2) / (int)top_k);
@@ -1201,7 +1322,7 @@ static int launch_down_comb(soso_hip *h, const uint8_t *const *tab, size_t n_exp
     int P = 4;
     while (P > 1 && n * ((rows + rw * P - 1) / (rw * P)) < (size_t)h->num_cu) P >>= 1;
     const size_t items = n * ((rows + rw * P - 1) / (rw * P));
-    const size_t lds = ((stage_lds_bytes(cols) + 15) & ~(size_t)15) * MDC_K;
+    const size_t lds = ((stage_lds_bytes_o(cols) + 15) & ~(size_t)15) * MDC_K;
     const size_t stride = packed_row_stride(SOSO_HIP_DTYPE_Q4_K, cols);
     const unsigned grid = (unsigned)std::min<size_t>(items, 4 * (size_t)h->num_cu);
     const int ri = (int)rows, ci = (int)cols, ne = (int)n_exp, ni = (int)n, ki = (int)top_k;
@@ -1249,7 +1370,7 @@ int launch_moe_experts(soso_hip *h, const float *xs, size_t n, size_t hdim, size
     const size_t Uf = ffn / 64;
     if (rc == SOSO_HIP_OK && route_idx && !use && n <= MDC_MAX_TOKENS && top_k <= (size_t)MDC_K &&
         dt_down == SOSO_HIP_DTYPE_Q4_K && ffn % 256 == 0 && Uf >= 4 && Uf <= 8 * MDC_XR &&
-        ((stage_lds_bytes(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds && packed_shape_ok(dt_down, hdim, ffn))
+        ((stage_lds_bytes_o(ffn) + 15) & ~(size_t)15) * MDC_K <= h->max_lds && packed_shape_ok(dt_down, hdim, ffn))
         return launch_down_comb(h, tab + 2 * n_groups, n_groups, hdim, ffn, s.act, route_idx, wgt, n, top_k, nullptr,
                                 out);
     if (rc == SOSO_HIP_OK) {

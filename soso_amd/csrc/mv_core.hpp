@@ -125,6 +125,19 @@ __device__ __forceinline__ int dpp_i(int v)
     return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
 }
 
+// The outlier threshold of a 128-element block from its sixteen 8-element
+// chunk maxima (m: this lane's chunk, one chunk per lane of the 16-lane row;
+// m1: the block maximum): 16 times the third largest chunk maximum, ties
+// counted; infinite for a non-finite block (its result is NaN anyway).
+__device__ __forceinline__ float outlier_thr16(float m, float m1)
+{
+    const int n1 = row16_count(m == m1);
+    const float m2 = row16_max(m < m1 ? m : -1.0f);
+    const int n2 = row16_count(m == m2);
+    const float m3b = row16_max(m < m2 ? m : -1.0f);
+    return m1 < INFINITY ? 16.0f * (n1 >= 3 ? m1 : n1 + n2 >= 3 ? m2 : m3b) : INFINITY;
+}
+
 // One 8-element chunk c (thread lane == c % 64).  Every lane of the 16-lane
 // DPP row takes part (invalid chunks carry zeros); only valid ones store.
 // FAST (with OUTL): a wavefront that would have to search for outliers
@@ -161,13 +174,7 @@ __device__ __forceinline__ bool stage_chunk(float4 v0, float4 v1, int c, bool va
         none = __ballot(m1 > 16.0f * qn) == 0;
         if (FAST && !none) return false;
         if (__builtin_expect(!none, 0)) {
-            // the third largest chunk maximum of the block, ties counted (a
-            // non-finite block has no outliers: its result is NaN anyway)
-            const int n1 = row16_count(m == m1);
-            const float m2 = row16_max(m < m1 ? m : -1.0f);
-            const int n2 = row16_count(m == m2);
-            const float m3b = row16_max(m < m2 ? m : -1.0f);
-            const float thr = m1 < INFINITY ? 16.0f * (n1 >= 3 ? m1 : n1 + n2 >= 3 ? m2 : m3b) : INFINITY;
+            const float thr = outlier_thr16(m, m1);
             none = __ballot(m1 > thr) == 0;
             if (__builtin_expect(!none, 0)) {
                 float km = 0.0f;
