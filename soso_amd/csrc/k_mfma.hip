@@ -177,7 +177,8 @@ __device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (
 // 4-chunk maximum has none (the two largest chunks sit in at most two
 // quads); when some block of the wavefront fails it, nothing is written and
 // false is returned (uniform), for the caller to stage the chunk again
-// through the full search.
+// through the full search.  The full search returns whether some block of
+// the wavefront has outliers (uniform).
 template <bool FAST>
 __device__ __forceinline__ bool mf_chunk(float4 v0, float4 v1, uint8_t *tp, int c, int kc, bool valid)
 {
@@ -214,6 +215,7 @@ __device__ __forceinline__ bool mf_chunk(float4 v0, float4 v1, uint8_t *tp, int 
             sm = ((vv[0] + vv[1]) + (vv[2] + vv[3])) + ((vv[4] + vv[5]) + (vv[6] + vv[7]));
         }
     }
+    const bool found = !none;
     if (none) mx = m1;
     // exponent of the 256-element super-block: 32 chunks = 32 aligned lanes
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
@@ -235,18 +237,48 @@ __device__ __forceinline__ bool mf_chunk(float4 v0, float4 v1, uint8_t *tp, int 
             *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
         tp[mf_mask_off(kc) + c] = (uint8_t)om;
     }
-    return true;
+    return !FAST || found;
+}
+
+// Writes one chunk staged without outliers: m is its 128-element block's
+// maximum (the exponent takes the super-block's, over 32 lanes), sm the
+// chunk's f32 sum (the sub-block's over 4 lanes).
+__device__ __forceinline__ void mf_put(float4 v0, float4 v1, float m, float sm, uint8_t *tp, int c, int kc, bool valid)
+{
+    const float mx = fmaxf(m, __shfl_xor(m, 16, 64));
+    const bool finite = mx < INFINITY;
+    const int ex = (mx > 0.0f && finite) ? 22 - __builtin_amdgcn_frexp_expf(mx) : 0;
+    sm += dpp_f<0xB1>(sm);
+    sm += dpp_f<0x4E>(sm);
+    if (valid) {
+        uint32_t d0[XDIG], d1[XDIG];
+        digits4(v0, ex, d0);
+        digits4(v1, ex, d1);
+        const int sbl = c >> 2, qq = c & 3;
+#pragma unroll
+        for (int kk = 0; kk < XDIG; kk++)
+            *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * qq) = make_uint2(d0[kk], d1[kk]);
+        if (qq == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
+        if ((c & 31) == 0)
+            *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
+        tp[mf_mask_off(kc) + c] = 0;
+    }
 }
 
 // Stages columns k0 .. k0 + kc of the round's nt tokens (x rows slot_s[t] / xdiv)
-// into LDS, token t at t * mf_tok_bytes(kc) (mf_chunk).  Four chunks per
-// thread are requested together, then converted (one L2 round trip per
-// 4 * 64 * NW chunks) through the cheap outlier test; rounds that fail it are
-// staged again afterwards through the full search, one at a time, from x
-// (rare: the unrolled loop stays free of that code).
+// into LDS, token t at t * mf_tok_bytes(kc).  Four chunks per thread are
+// requested together (one L2 round trip per 4 * 64 * NW chunks); all four
+// take the cheap outlier test first (mf_chunk<true>'s), and when no block of
+// the wavefront fails it -- the common case -- they are staged straight away
+// (mf_put), the four chunks' code interleaved.  Otherwise the round is staged
+// again from x through the full search (mf_chunk<false>), one chunk at a
+// time: that rare code stays out of the unrolled loop.
+// A wavefront that finds outliers writes seq into *oflag (LDS): after the
+// staging's barrier, *oflag == seq tells every wavefront that the chunk has
+// some (no flag to clear: each chunk staged has its own seq).
 template <int NW>
 __device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__ xs, const int *slot_s, int xdiv, int cols,
-                                         int k0, int kc, int nt)
+                                         int k0, int kc, int nt, int *oflag, int seq)
 {
     const int tb = mf_tok_bytes(kc);
     const int cpt = kc >> 3, tot = nt * cpt; // 8-element chunks
@@ -266,19 +298,38 @@ __device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__
                 v1[k] = x4[1];
             }
         }
-        uint32_t redo = 0; // uniform
+        float m1[XB], sm[XB];
+        bool suspect = false;
 #pragma unroll
         for (int k = 0; k < XB; k++) {
-            if (fb + k * NT >= tot) break; // uniform
-            const int f = fb + k * NT + (int)threadIdx.x;
-            const bool valid = f < tot;
-            if (!mf_chunk<true>(v0[k], v1[k], lds + (size_t)(valid ? f / cpt : 0) * tb, f % cpt, kc, valid))
-                redo |= 1u << k;
+            m1[k] = sm[k] = 0.0f;
+            if (fb + k * NT < tot) { // uniform
+                const float4 a = v0[k], b = v1[k];
+                float mx = fmaxf(fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))),
+                                 fmaxf(fmaxf(fabsf(b.x), fabsf(b.y)), fmaxf(fabsf(b.z), fabsf(b.w))));
+                sm[k] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+                if (sm[k] != sm[k]) mx = INFINITY; // a NaN element: the super-block is non-finite
+                float q = fmaxf(mx, dpp_f<0xB1>(mx));
+                q = fmaxf(q, dpp_f<0x4E>(q));
+                const float hq = fmaxf(q, dpp_f<0x141>(q));
+                m1[k] = fmaxf(hq, dpp_f<0x140>(hq));
+                float qn = fminf(q, dpp_f<0x141>(q));
+                qn = fminf(qn, dpp_f<0x140>(qn));
+                suspect = suspect || m1[k] > 16.0f * qn;
+            }
         }
-        if (__builtin_expect(redo != 0, 0)) {
+        if (__builtin_expect(__ballot(suspect) == 0, 1)) {
+#pragma unroll
+            for (int k = 0; k < XB; k++) {
+                if (fb + k * NT >= tot) break; // uniform
+                const int f = fb + k * NT + (int)threadIdx.x;
+                const bool valid = f < tot;
+                mf_put(v0[k], v1[k], m1[k], sm[k], lds + (size_t)(valid ? f / cpt : 0) * tb, f % cpt, kc, valid);
+            }
+        } else {
 #pragma unroll 1
             for (int k = 0; k < XB; k++) {
-                if (!((redo >> k) & 1u)) continue; // uniform
+                if (fb + k * NT >= tot) break; // uniform
                 const int f = fb + k * NT + (int)threadIdx.x;
                 const bool valid = f < tot;
                 float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
@@ -287,7 +338,9 @@ __device__ __forceinline__ void mf_stage(uint8_t *lds, const float *__restrict__
                     a = x4[0];
                     b = x4[1];
                 }
-                mf_chunk<false>(a, b, lds + (size_t)(valid ? f / cpt : 0) * tb, f % cpt, kc, valid);
+                if (mf_chunk<false>(a, b, lds + (size_t)(valid ? f / cpt : 0) * tb, f % cpt, kc, valid) &&
+                    (threadIdx.x & 63) == 0)
+                    *oflag = seq;
             }
         }
     }
@@ -306,19 +359,6 @@ __device__ __forceinline__ uint32_t mf_fetch(const uint2 (&q)[N], int src, int d
         r = di == 2 * i ? x : di == 2 * i + 1 ? y : r;
     }
     return r;
-}
-
-// Whether any of the round's nt staged tokens has an outlier (after the
-// staging's barrier; every wavefront reads the masks itself).
-__device__ __forceinline__ bool mf_any_outliers(const uint8_t *lds, int tb, int kc, int nt)
-{
-    const int nb = kc >> 7, tot = nt * nb;
-    bool any = false;
-    for (int i = (int)(threadIdx.x & 63); i < tot; i += 64) {
-        const uint4 m = *(const uint4 *)(lds + (size_t)(i / nb) * tb + mf_mask_off(kc) + 16 * (i % nb));
-        any = any || (m.x | m.y | m.z | m.w) != 0u;
-    }
-    return __ballot(any) != 0;
 }
 
 // Whether any of the round's nt tokens has outliers in super-block sbl of the
@@ -413,7 +453,7 @@ __device__ int mf_scan_slots(const int32_t *__restrict__ sidx, int nslots, int e
 // blockIdx.x = a * nblk + row block (MoE), or row block + nblk * token round
 // (dense).  Slot s reads x = xs + (s / xdiv) * cols and writes out[s * rows + r].
 template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW, bool SCAN = false>
-__global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
+__global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 : 4) : 1) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB,
                                                   const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
                                                   const float *__restrict__ xs, int xdiv, const int *__restrict__ list,
@@ -429,6 +469,9 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
     int16_t *scan_s = (int16_t *)mf_smem;
     uint8_t *lds = (uint8_t *)mf_smem + (SCAN ? mf_scan_bytes(nslots) : 0);
     __shared__ int slot_s[TR];
+    __shared__ int oflag_s; // the seq of the last staged chunk with outliers
+    if (threadIdx.x == 0) oflag_s = -1;
+    int seq = 0;
     __shared__ int wtot_s[NW];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -509,8 +552,9 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
             if constexpr (NMAT == 2) load_sb(rB, sb0, true, cb);
             __builtin_amdgcn_sched_barrier(0);
             // ---- stage x (columns k0 .. k0 + kc of the round's tokens) ----
-            mf_stage<NW>(lds, xs, slot_s, xdiv, cols, k0, kc, nt);
+            mf_stage<NW>(lds, xs, slot_s, xdiv, cols, k0, kc, nt, &oflag_s, ++seq);
             __syncthreads();
+            const bool oany = __builtin_amdgcn_readfirstlane(oflag_s) == seq;
             // ---- stream this chunk's super-blocks of the wavefront's 16 rows ----
             // The 6-bit scale of each sub-block goes into the B operand: sc =
             // 8 hi + lo with hi, lo < 8, so q*lo and q*hi (<= 105) are int8 and
@@ -651,7 +695,7 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q4k(const uint8_t *const *__re
             // (dequant.rs:204-241).  Element e of a super-block: unit e / 64,
             // code byte l = e % 32 of the unit (lane group l / 8 of this row
             // holds it), the high nibble from 32 on.
-            if (__builtin_expect(mf_any_outliers(lds, tb, kc, nt), 0)) {
+            if (__builtin_expect(oany, 0)) {
                 for (int i = 0; i < nsb; i++) {
                     if (!mf_sb_has_outliers(lds, tb, kc, nt, i)) continue; // uniform
                     MfSb S_[NMAT];
@@ -733,6 +777,9 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict_
     extern __shared__ uint4 mf_smem[];
     uint8_t *lds = (uint8_t *)mf_smem;
     __shared__ int slot_s[TR];
+    __shared__ int oflag_s; // the seq of the last staged chunk with outliers
+    if (threadIdx.x == 0) oflag_s = -1;
+    int seq = 0;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     constexpr int ROWS = 16 * NW;
@@ -774,8 +821,9 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict_
             MfQ80 cur, nxt;
             load_sb(sb0, true, cur); // requested before x is staged: its latency overlaps the staging
             __builtin_amdgcn_sched_barrier(0);
-            mf_stage<NW>(lds, xs, slot_s, 1, cols, k0, kc, nt);
+            mf_stage<NW>(lds, xs, slot_s, 1, cols, k0, kc, nt, &oflag_s, ++seq);
             __syncthreads();
+            const bool oany = __builtin_amdgcn_readfirstlane(oflag_s) == seq;
             for (int i = 0; i < nsb; i++) {
                 load_sb(sb0 + i + 1, i + 1 < nsb, nxt);
                 __builtin_amdgcn_sched_barrier(0);
@@ -813,7 +861,7 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict_
             // w * x with w = fl(q * scale) (dequant.rs:74-97).  Element e of a
             // stretch: block e / 32, code byte l = e % 32 (lane group l / 8 of
             // this row holds it).
-            if (__builtin_expect(mf_any_outliers(lds, tb, kc, nt), 0)) {
+            if (__builtin_expect(oany, 0)) {
                 for (int i = 0; i < nsb; i++) {
                     if (!mf_sb_has_outliers(lds, tb, kc, nt, i)) continue; // uniform
                     MfQ80 o;

@@ -529,20 +529,6 @@ __device__ __forceinline__ void q4k_token_dot(const Q4Prep (&pr)[NMAT], const ui
     for (int m = 0; m < NMAT; m++) val[m] = seg_sum_dpp<LPR>(part[m]);
 }
 
-// Whether any of the nt tokens staged at smem (tok_bytes apart, cols wide, OUTL
-// staging) has a non-empty outlier list; uniform over the wavefront.
-__device__ __forceinline__ bool moe_any_outliers(const void *smem, int tok_bytes, int cols, int nt)
-{
-    const int nb = (cols + 127) >> 7, tot = nt * nb;
-    bool any = false;
-    for (int i = (int)(threadIdx.x & 63); i < tot; i += 64) {
-        const uint32_t *xd = (const uint32_t *)((const uint8_t *)smem + (size_t)(i / nb) * tok_bytes);
-        const int *kx = (const int *)((const float *)(xd + (cols >> 2) * XDIG) + (cols >> 4));
-        any = any || out_lists(kx, cols)[(i % nb) * OUT_DW] != 0u;
-    }
-    return __ballot(any) != 0;
-}
-
 // One token ranked by the expert kernel itself (SELF): every workgroup takes
 // the softmax top-k of the token's logits (topk_regs, the same ranking as the
 // route kernel's) and runs `chunks` row chunks of each ranked expert j on
@@ -587,6 +573,7 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
     __shared__ float self_wgt[MOE_SELF_K], self_sel[MOE_SELF_K];
     __shared__ __align__(16) uint32_t self_keys[256];
     __shared__ float nrm_s[NW];
+    __shared__ int found_s[NW]; // SELF: the wavefronts' staging found outliers
     int nit;
     bool oany = false; // SELF: the staged token has outliers (its passes take the exact-weight loop)
     if constexpr (SELF) {
@@ -659,10 +646,22 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
             uint32_t *xd = (uint32_t *)smem;
             float *s16 = (float *)(xd + (cols >> 2) * XDIG);
             int *kx = (int *)(s16 + (cols >> 4));
+            // the cheap outlier test first; rounds whose blocks may hold
+            // outliers are staged again through the full search
+            bool found = false;
+            uint32_t redo = 0;
 #pragma unroll
             for (int k = 0; k < MOE_XK; k++) {
                 const int f = k * 512 + (int)threadIdx.x;
-                if (k * 512 < nch) stage_chunk<FMT, true>(xv0[k], xv1[k], f % nch, f < nch, U, xd, s16, kx);
+                if (k * 512 < nch && !stage_chunk<FMT, true, true>(xv0[k], xv1[k], f % nch, f < nch, U, xd, s16, kx))
+                    redo |= 1u << k;
+            }
+            if (__builtin_expect(redo != 0, 0)) {
+#pragma unroll
+                for (int k = 0; k < MOE_XK; k++) {
+                    const int f = k * 512 + (int)threadIdx.x;
+                    if ((redo >> k) & 1u) stage_chunk<FMT, true>(xv0[k], xv1[k], f % nch, f < nch, U, xd, s16, kx, &found);
+                }
             }
             for (int fb = MOE_XK * 512; fb < nch; fb += 512) { // rows longer than one round holds
                 const int f = fb + (int)threadIdx.x;
@@ -672,8 +671,10 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
                     v0 = x4[0];
                     v1 = x4[1];
                 }
-                stage_chunk<FMT, true>(v0, v1, f % nch, f < nch, U, xd, s16, kx);
+                stage_chunk<FMT, true>(v0, v1, f % nch, f < nch, U, xd, s16, kx, &found);
             }
+            // every wavefront writes its own word: nothing to clear between calls
+            if (lane == 0) found_s[wave] = found ? 1 : 0;
         }
         __syncthreads();
         {
@@ -718,7 +719,8 @@ __global__ void __launch_bounds__(512) k_moe_rows(const uint8_t *const *__restri
             sr.wgt[threadIdx.x] = self_wgt[threadIdx.x];
         }
         nit = sr.top_k * sr.chunks;
-        oany = moe_any_outliers(smem, tok_bytes, cols, 1);
+#pragma unroll
+        for (int i = 0; i < NW; i++) oany = oany || found_s[i] != 0;
     } else {
         nit = *n_items;
     }
@@ -971,33 +973,47 @@ __global__ void __launch_bounds__(512) k_moe_down_comb(const uint8_t *const *__r
         for (int p = 0; p < P; p++) load_row<FMT_Q4K>(rs, base + (uint32_t)(p * RW) * (uint32_t)stride, cols, L, w[p]);
         __builtin_amdgcn_sched_barrier(0);
         // 3. act into this wavefront's LDS region (16-chunk blocks: nch % 16 == 0)
+        // (the cheap outlier test first; a wavefront whose act row may hold
+        // outliers stages it again through the full search)
+        bool oany = false;
+        uint32_t redo = 0;
 #pragma unroll
         for (int k = 0; k < MDC_XR; k++)
-            if (64 * k < nch) stage_chunk<FMT_Q4K, true>(xv0[k], xv1[k], 64 * k + lane, 64 * k + lane < nch, U, xd, s16, kx);
-        __syncthreads();
-        // 4. the dots of this wavefront's rows.  When its act row has
-        // outliers (a uniform branch per wavefront), their w * x is taken
-        // first from the raw rows, with w decoded exactly as the reference
-        // decodes it, and joins each row's dot.
-        const bool oany = moe_any_outliers(xd, 0, cols, 1);
-        float corr[P];
+            if (64 * k < nch &&
+                !stage_chunk<FMT_Q4K, true, true>(xv0[k], xv1[k], 64 * k + lane, 64 * k + lane < nch, U, xd, s16, kx))
+                redo |= 1u << k;
+        if (__builtin_expect(redo != 0, 0)) {
 #pragma unroll
-        for (int p = 0; p < P; p++) corr[p] = 0.0f;
-        if (__builtin_expect(oany, 0)) {
-            UConst co = c;
-            co.ol = out_lists(kx, cols) + (u >> 1) * OUT_DW;
-            co.ocnt = uact ? min((int)co.ol[0], OUT_MAX) : 0;
-            co.onum = (int)wave_max_dpp((float)co.ocnt);
-#pragma unroll
-            for (int p = 0; p < P; p++) corr[p] = seg_sum_dpp<LPR>(unit_outliers<FMT_Q4K>(w[p], co, u));
+            for (int k = 0; k < MDC_XR; k++)
+                if (64 * k < nch)
+                    stage_chunk<FMT_Q4K, true>(xv0[k], xv1[k], 64 * k + lane, 64 * k + lane < nch, U, xd, s16, kx,
+                                               &oany);
         }
+        __syncthreads();
+        // 4. the dots of this wavefront's rows
 #pragma unroll
         for (int p = 0; p < P; p++) {
             Q4Prep pr[1];
             q4k_prep(w[p], c, pr[0]);
             float val[1];
             q4k_token_dot<LPR, 1>(pr, xd, cols, U, u, uact, val);
-            if (ul == LPR - 1) dots[j][p * RW + slot] = val[0] + corr[p];
+            if (ul == LPR - 1) dots[j][p * RW + slot] = val[0];
+        }
+        // ... and, when its act row has outliers (a uniform branch per
+        // wavefront), their w * x, with the rows loaded again (the ring is
+        // gone by now, so this adds no registers to the loop above) and w
+        // decoded exactly as the reference decodes it
+        if (__builtin_expect(oany, 0)) {
+            UConst co = c;
+            co.ol = out_lists(kx, cols) + (u >> 1) * OUT_DW;
+            co.ocnt = uact ? min((int)co.ol[0], OUT_MAX) : 0;
+            co.onum = (int)wave_max_dpp((float)co.ocnt);
+            for (int p = 0; p < P; p++) {
+                WRow<FMT_Q4K> wr;
+                load_row<FMT_Q4K>(rs, base + (uint32_t)(p * RW) * (uint32_t)stride, cols, L, wr);
+                const float corr = seg_sum_dpp<LPR>(unit_outliers<FMT_Q4K>(wr, co, u));
+                if (ul == LPR - 1) dots[j][p * RW + slot] += corr;
+            }
         }
         __syncthreads();
         // 5. the weighted sum in ranking order, one lane per row

@@ -142,10 +142,11 @@ __device__ __forceinline__ float outlier_thr16(float m, float m1)
 // DPP row takes part (invalid chunks carry zeros); only valid ones store.
 // FAST (with OUTL): a wavefront that would have to search for outliers
 // stages nothing and returns false (uniform), for the caller to stage the
-// chunk again through the full path; otherwise returns true.
+// chunk again through the full path; otherwise returns true.  found (OUTL,
+// when given) is set when some block of the wavefront has outliers.
 template <int FMT, bool OUTL = false, bool FAST = false>
 __device__ __forceinline__ bool stage_chunk(float4 v0, float4 v1, int c, bool valid, int U, uint32_t *xd, float *s16,
-                                            int *kx)
+                                            int *kx, bool *found = nullptr)
 {
     float m = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
                     fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
@@ -176,6 +177,7 @@ __device__ __forceinline__ bool stage_chunk(float4 v0, float4 v1, int c, bool va
         if (__builtin_expect(!none, 0)) {
             const float thr = outlier_thr16(m, m1);
             none = __ballot(m1 > thr) == 0;
+            if (found && !none) *found = true; // (uniform) some block of the wavefront has outliers
             if (__builtin_expect(!none, 0)) {
                 float km = 0.0f;
 #pragma unroll
