@@ -78,13 +78,43 @@ def _timed_graph(g, calls, steps):
     return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
 
 
+# Below this many timed steps a graph replay's own start (a few microseconds
+# on the GPU, measured 7.7-7.9 us per headline launch at 20 steps against 7.4 at
+# 1000) would weigh on the per-step figure: short windows launch their steps
+# directly, right behind untimed steps that keep the GPU busy up to the start
+# event (7.3 us per launch at 20 steps; at 1000, 7.5 eager against 7.4 from a
+# graph).  Either way the events bracket exactly the timed steps.
+GRAPH_MIN_STEPS = 200
+
+
+def _timed_steps(g, launch, steps, lead):
+    """Times exactly `steps` steps (launch(i) issues step i): from
+    GRAPH_MIN_STEPS on one graph replay (_timed_graph), below it direct
+    launches enqueued right behind `lead` untimed ones.  Returns (ms per step
+    between the events, host wall ms per step)."""
+    if steps >= GRAPH_MIN_STEPS:
+        return _timed_graph(g, lambda: [launch(i) for i in range(steps)], steps)
+    g.sync()
+    for i in range(lead):
+        launch(i)
+    t0 = time.perf_counter()
+    g.event_record(0)
+    for i in range(steps):
+        launch(i)
+    g.event_record(1)
+    g.sync()
+    t1 = time.perf_counter()
+    return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
+
+
 def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1, eager=False):
     """Average duration of one matvec launch, in ms.
 
     `copies` resident weights are rotated so HBM, not the MALL, serves them.
-    The timed region is one HIP graph of `steps` back-to-back launches on the
-    library's stream, bracketed by HIP events recorded on that stream (see
-    _timed_graph): the average is (event interval) / steps,
+    The timed region is `steps` back-to-back launches on the library's stream
+    (one HIP graph from GRAPH_MIN_STEPS on, direct launches below it),
+    bracketed by HIP events recorded on that stream (_timed_steps): the
+    average is (event interval) / steps,
     the same per-dispatch figure rocprofv3 --kernel-trace reports (profiles/
     holds that cross-check).  eager=True launches the steps directly instead
     (for counter and tracer runs).  Returns (ms_per_launch_events,
@@ -106,13 +136,38 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1, eager=False
             g.event_record(1)
             g.sync()
             return g.event_elapsed(0, 1) / steps, None
-        return _timed_graph(g, calls, steps)
+        return _timed_steps(g, lambda i: g.matvec_dev(keys[i % copies], x, y), steps, max(warmup, 5))
     finally:
         g.sync()
         g.dev_free(x)
         g.dev_free(y)
         for k in keys:
             g.weight_drop(k)
+
+
+def time_host_matvec(g, dtype, rows, cols, calls=300, seed=5):
+    """What one op costs soso through the drop-in boundary: soso_hip_matvec on
+    host buffers (matvec_step calls GpuDispatch::matvec synchronously per op,
+    crates/soso-llm-core/src/layer.rs:644-672): x up, the kernel, y down and
+    the wait, on a resident weight.  Returns (median, 10th, 90th percentile)
+    microseconds per call, host wall clock."""
+    import numpy as np
+    key = f"bench.host.{dtype}.{rows}x{cols}"
+    g.weight_synth(key, dtype, rows, cols, seed, 1)
+    x = np.random.default_rng(seed).standard_normal(cols).astype(np.float32)
+    y = np.empty(rows, np.float32)
+    try:
+        for _ in range(20):
+            g.matvec(key, None, dtype, rows, cols, x, y)
+        ts = []
+        for _ in range(calls):
+            t0 = time.perf_counter()
+            g.matvec(key, None, dtype, rows, cols, x, y)
+            ts.append((time.perf_counter() - t0) * 1e6)
+        ts.sort()
+        return ts[len(ts) // 2], ts[len(ts) // 10], ts[(9 * len(ts)) // 10]
+    finally:
+        g.weight_drop(key)
 
 
 def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False, dtype=Q4K):
@@ -137,6 +192,8 @@ def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False, dt
             g.event_record(1)
             g.sync()
         else:
+            # (always a graph: issued directly, the matmul's host-side launch
+            # selection showed through, 75 against 67 us per call at 100 calls)
             return _timed_graph(g, calls, steps)[0]
         return g.event_elapsed(0, 1) / steps
     finally:
@@ -877,7 +934,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic("q4k_14336x4096"),
                      "kernel_us": round(ms * 1e3, 3), "host_wall_us_per_step": round(ms_wall * 1e3, 3),
-                     "graph_single_launch_us": round(time_single_launch(g, Q4K, rows, cols) * 1e3, 3)},
+                     "graph_single_launch_us": round(time_single_launch(g, Q4K, rows, cols) * 1e3, 3),
+                     "timed_as": (f"{args.steps} launches replayed from one graph" if args.steps >= GRAPH_MIN_STEPS
+                                  else f"{args.steps} launches issued directly behind {max(args.warmup, 5)} "
+                                       "untimed ones")},
     }
     if not args.no_extra:
         extra = {}
@@ -903,6 +963,13 @@ def main():
                                     "headline_vs_read": round(best / ms, 4)}
         if not args.no_cpu:
             extra["q6_k_head_128256x4096"]["parity_vs_cpu"] = head_parity(g, args.cpu_threads)
+        # the drop-in boundary's own cost per op (host buffers, synchronous)
+        for name, dt, r, c in (("q8_0_4096x4096", Q8, 4096, 4096), ("q4_k_14336x4096", Q4K, 14336, 4096)):
+            med, p10, p90 = time_host_matvec(g, dt, r, c)
+            extra[f"host_call_{name}"] = {
+                "us_per_call_median": round(med, 2), "us_p10": round(p10, 2), "us_p90": round(p90, 2),
+                "what": "soso_hip_matvec on host x / y (upload, kernel, download, wait) on a resident weight; "
+                        "the kernel alone is the entry of the same shape above"}
         mm_n = 64
         ms_mm = time_matmul(g, 14336, 4096, mm_n, 16, max(20, args.steps // 10), min(args.warmup, 10))
         b_mm = 14336 * (4096 // 256) * 144 + mm_n * 4096 * 4 + mm_n * 14336 * 4

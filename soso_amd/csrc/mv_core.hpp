@@ -535,17 +535,26 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes)
 {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, RSRC_WORD3);
 }
+// Cache policy of a buffer load (the instruction's cache-policy bits): 0 the
+// default; LD_STREAM sets the nontemporal bit, for weight bytes a launch
+// reads once.  Measured on MI355X (rotating weights): the Q4_K 14336 x 4096
+// matvec 7.47 -> 7.02 us, Q8_0 4096 x 4096 5.58 -> 5.09 us, the 8B decode
+// step 1.646 -> 1.622 ms per token.
+constexpr int LD_STREAM = 2;
+template <int POL = 0>
 __device__ __forceinline__ uint4 bld16(rsrc_t r, uint32_t off)
 {
-    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, POL));
 }
+template <int POL = 0>
 __device__ __forceinline__ uint2 bld8(rsrc_t r, uint32_t off)
 {
-    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+    return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, POL));
 }
+template <int POL = 0>
 __device__ __forceinline__ uint32_t bld2(rsrc_t r, uint32_t off)
 {
-    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, POL);
 }
 
 // Byte offsets, inside one packed row, of what lane unit u loads.
@@ -576,26 +585,27 @@ __device__ __forceinline__ LaneOff lane_offsets(int cols, int u, const UConst &c
     return L;
 }
 
-// Loads unit u of the row at byte offset `base` of the strip.
+// Loads unit u of the row at byte offset `base` of the strip (streaming:
+// each weight byte is read once per launch).
 template <int FMT>
 __device__ __forceinline__ void load_row(rsrc_t r, uint32_t base, int cols, const LaneOff &L, WRow<FMT> &w)
 {
     if constexpr (FMT == FMT_Q4K) {
-        w.h = bld16(r, base + L.o[0]);
-        w.a = bld16(r, base + L.o[1]);
-        w.b = bld16(r, base + L.o[2]);
+        w.h = bld16<LD_STREAM>(r, base + L.o[0]);
+        w.a = bld16<LD_STREAM>(r, base + L.o[1]);
+        w.b = bld16<LD_STREAM>(r, base + L.o[2]);
     } else if constexpr (FMT == FMT_Q80) {
         const uint32_t U16 = (uint32_t)(cols >> 6) * 16u;
-        w.s = bld8(r, base + L.o[0]);
+        w.s = bld8<LD_STREAM>(r, base + L.o[0]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) w.q[i] = bld16(r, base + L.o[1] + U16 * i);
+        for (int i = 0; i < 4; i++) w.q[i] = bld16<LD_STREAM>(r, base + L.o[1] + U16 * i);
     } else {
         const uint32_t U16 = (uint32_t)(cols >> 6) * 16u;
-        w.qh = bld16(r, base + L.o[0]);
-        w.la = bld16(r, base + L.o[0] + U16);
-        w.lb = bld16(r, base + L.o[0] + 2 * U16);
-        w.sc = bld8(r, base + L.o[1]);
-        w.d = bld2(r, base + L.o[2]);
+        w.qh = bld16<LD_STREAM>(r, base + L.o[0]);
+        w.la = bld16<LD_STREAM>(r, base + L.o[0] + U16);
+        w.lb = bld16<LD_STREAM>(r, base + L.o[0] + 2 * U16);
+        w.sc = bld8<LD_STREAM>(r, base + L.o[1]);
+        w.d = bld2<LD_STREAM>(r, base + L.o[2]);
     }
 }
 
