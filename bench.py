@@ -207,7 +207,8 @@ def time_matmul(g, rows, cols, n, copies, steps, warmup, seed=3, eager=False, dt
 READ_SHAPES = ((1, 256), (2, 256), (4, 256), (8, 256), (1, 512), (2, 512), (4, 512), (1, 1024), (2, 1024))
 # read-probe variants: grid-stride with K independent 16-byte loads per thread,
 # or per-wavefront contiguous stretches with K 1-KiB buffer loads in flight
-READ_VARIANTS = (("gs", 1), ("gs", 2), ("gs", 4), ("gs", 8), ("chunk", 2), ("chunk", 4), ("chunk", 8), ("chunk", 16))
+READ_VARIANTS = (("gs", 1), ("gs", 2), ("gs", 4), ("gs", 8), ("chunk", 2), ("chunk", 4), ("chunk", 8), ("chunk", 16),
+                 ("gs_nt", 2), ("gs_nt", 4), ("chunk_nt", 4), ("chunk_nt", 8))  # _nt: nontemporal loads
 
 
 def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES, variants=READ_VARIANTS):
@@ -227,7 +228,8 @@ def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES, varian
         for var, k in variants:
             for wpc, thr in shapes:
                 def call(i):
-                    g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len, loads=k, chunked=var == "chunk")
+                    g.read_probe(bufs[i % copies], nbytes, wpc, thr, out, out_len, loads=k,
+                                 chunked=var.startswith("chunk"), stream=var.endswith("_nt"))
                 for i in range(warmup):
                     call(i)
                 g.sync()
@@ -242,7 +244,7 @@ def time_read_probe(g, nbytes, copies, steps, warmup, shapes=READ_SHAPES, varian
 
 def read_probe_bytes(var, nbytes):
     """Bytes a read-probe variant reads: whole 16-byte words, or whole KiB."""
-    return nbytes // 1024 * 1024 if var == "chunk" else nbytes // 16 * 16
+    return nbytes // 1024 * 1024 if var.startswith("chunk") else nbytes // 16 * 16
 
 
 def time_gdn(g, n, steps, layers=8, n_k=16, n_v=32, d=128, kernel=4, seed=41, eager=False):
@@ -957,7 +959,8 @@ def main():
         rb = read_probe_bytes(bv, nb)
         extra["plain_read_33MB"] = {"us_kernel": round(best * 1e3, 3), "GB_s": round(rb / (best * 1e-3) / 1e9, 1),
                                     "frac_hbm": round(rb / (best * 1e-3) / 1e9 / PEAK_GBS, 4), "bytes": rb,
-                                    "shape": f"{'grid-stride' if bv == 'gs' else 'per-wavefront KiB stretches'}, "
+                                    "shape": f"{'grid-stride' if bv.startswith('gs') else 'per-wavefront KiB stretches'}"
+                                             f"{' (nontemporal loads)' if bv.endswith('_nt') else ''}, "
                                              f"{bk} loads in flight, {bw} workgroups per CU x {bt} threads "
                                              f"(best of {len(rd)} variants and shapes)",
                                     "headline_vs_read": round(best / ms, 4)}

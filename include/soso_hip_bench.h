@@ -32,9 +32,10 @@ int soso_hip_synth_normal(soso_hip *h, float *dst_dev, size_t n, float sigma, ui
  * (1, 2, 4, 8 or 16) independent loads in flight per thread.  chunked = 1:
  * every wavefront streams its own contiguous stretch of whole KiB (bytes
  * rounded down to 1 KiB, < 2 GiB) with `loads` 1-KiB wavefront loads in
- * flight, through raw buffer loads as the matvec kernels issue them.  Thread
- * t < out_len writes the xor of what it read to out_dev[t].  Asynchronous on
- * the handle's stream. */
+ * flight, through raw buffer loads as the matvec kernels issue them.
+ * chunked | 2: the same with the loads' nontemporal (streaming) cache policy,
+ * as the matvec's weight loads use.  Thread t < out_len writes the xor of
+ * what it read to out_dev[t].  Asynchronous on the handle's stream. */
 int soso_hip_read_probe(soso_hip *h, const void *src_dev, size_t bytes, uint32_t wg_per_cu, uint32_t threads,
                         uint32_t loads, uint32_t chunked, uint32_t *out_dev, size_t out_len);
 

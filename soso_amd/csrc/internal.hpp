@@ -246,7 +246,7 @@ int launch_synth_raw(soso_hip *h, void *dst, uint8_t dtype, size_t rows, size_t 
                      uint64_t stream);
 int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t seed, uint64_t stream);
 int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads,
-                      unsigned loads, bool chunked, uint32_t *out, size_t out_len);
+                      unsigned loads, bool chunked, bool stream, uint32_t *out, size_t out_len);
 bool moe_scratch(soso_hip *h, size_t n, size_t n_groups, size_t top_k, size_t hdim, size_t ffn, MoeScratch &s);
 // The same regions in one buffer of `cap` bytes at `base` (256-byte aligned
 // pieces); returns the bytes needed, and sets s only when they fit.

@@ -8,6 +8,8 @@
 // crates/soso-llm-core/src/f16.rs:10-37).
 #include "internal.hpp"
 
+#include <type_traits>
+
 __device__ __forceinline__ uint64_t fin64(uint64_t z)
 {
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
@@ -154,7 +156,7 @@ int launch_synth_normal(soso_hip *h, float *dst, size_t n, float sigma, uint64_t
 //    the matvec kernels use; a load past the stretch returns zeros without
 //    touching memory).
 // ---------------------------------------------------------------------------
-template <int K>
+template <int K, bool NT>
 __global__ void read_probe_gs(const uint4 *__restrict__ p, size_t n16, uint32_t *__restrict__ out, size_t out_len)
 {
     const size_t T = (size_t)gridDim.x * blockDim.x, t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -163,7 +165,15 @@ __global__ void read_probe_gs(const uint4 *__restrict__ p, size_t n16, uint32_t 
     for (; i + (size_t)(K - 1) * T < n16; i += (size_t)K * T) {
         uint4 v[K];
 #pragma unroll
-        for (int k = 0; k < K; k++) v[k] = p[i + (size_t)k * T];
+        for (int k = 0; k < K; k++) {
+            if constexpr (NT) {
+                typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 t4 = __builtin_nontemporal_load((const u32x4 *)(p + i + (size_t)k * T));
+                v[k] = make_uint4(t4.x, t4.y, t4.z, t4.w);
+            } else {
+                v[k] = p[i + (size_t)k * T];
+            }
+        }
 #pragma unroll
         for (int k = 0; k < K; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
     }
@@ -174,7 +184,7 @@ __global__ void read_probe_gs(const uint4 *__restrict__ p, size_t n16, uint32_t 
     if (t < out_len) out[t] = acc;
 }
 
-template <int K>
+template <int K, bool NT>
 __global__ void read_probe_chunk(const uint8_t *__restrict__ p, uint32_t kib, uint32_t *__restrict__ out,
                                  size_t out_len)
 {
@@ -190,7 +200,7 @@ __global__ void read_probe_chunk(const uint8_t *__restrict__ p, uint32_t kib, ui
 #pragma unroll
         for (int k = 0; k < K; k++)
             v[k] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)((j + k) * 1024u + 16u * lane),
-                                                                                   0, 0));
+                                                                                   0, NT ? 2 : 0));
 #pragma unroll
         for (int k = 0; k < K; k++) acc ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
     }
@@ -199,31 +209,36 @@ __global__ void read_probe_chunk(const uint8_t *__restrict__ p, uint32_t kib, ui
 }
 
 int launch_read_probe(soso_hip *h, const void *src, size_t bytes, unsigned wg_per_cu, unsigned threads,
-                      unsigned loads, bool chunked, uint32_t *out, size_t out_len)
+                      unsigned loads, bool chunked, bool stream, uint32_t *out, size_t out_len)
 {
     const unsigned grid = wg_per_cu * (unsigned)h->num_cu;
-    if (chunked) {
-        const uint32_t kib = (uint32_t)(bytes >> 10);
-        const uint8_t *b = (const uint8_t *)src;
-        switch (loads) {
-        case 1: read_probe_chunk<1><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
-        case 2: read_probe_chunk<2><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
-        case 4: read_probe_chunk<4><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
-        case 8: read_probe_chunk<8><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
-        case 16: read_probe_chunk<16><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
-        default: return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: loads");
+    if (loads != 1 && loads != 2 && loads != 4 && loads != 8 && loads != 16)
+        return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: loads");
+    auto go = [&](auto nt) {
+        constexpr bool NT = decltype(nt)::value;
+        if (chunked) {
+            const uint32_t kib = (uint32_t)(bytes >> 10);
+            const uint8_t *b = (const uint8_t *)src;
+            switch (loads) {
+            case 1: read_probe_chunk<1, NT><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+            case 2: read_probe_chunk<2, NT><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+            case 4: read_probe_chunk<4, NT><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+            case 8: read_probe_chunk<8, NT><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+            default: read_probe_chunk<16, NT><<<grid, threads, 0, h->stream>>>(b, kib, out, out_len); break;
+            }
+        } else {
+            const uint4 *q = (const uint4 *)src;
+            const size_t n16 = bytes / 16;
+            switch (loads) {
+            case 1: read_probe_gs<1, NT><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+            case 2: read_probe_gs<2, NT><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+            case 4: read_probe_gs<4, NT><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+            case 8: read_probe_gs<8, NT><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+            default: read_probe_gs<16, NT><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
+            }
         }
-    } else {
-        const uint4 *q = (const uint4 *)src;
-        const size_t n16 = bytes / 16;
-        switch (loads) {
-        case 1: read_probe_gs<1><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
-        case 2: read_probe_gs<2><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
-        case 4: read_probe_gs<4><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
-        case 8: read_probe_gs<8><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
-        case 16: read_probe_gs<16><<<grid, threads, 0, h->stream>>>(q, n16, out, out_len); break;
-        default: return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: loads");
-        }
-    }
+    };
+    if (stream) go(std::true_type{});
+    else go(std::false_type{});
     return hip_check(h, hipGetLastError(), "read probe launch");
 }

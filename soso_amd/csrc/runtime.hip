@@ -1406,7 +1406,8 @@ int soso_hip_read_probe(soso_hip *h, const void *src_dev, size_t bytes, uint32_t
         return set_err(h, SOSO_HIP_ERR_ARG, "read_probe: args");
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
-    return launch_read_probe(h, src_dev, bytes, wg_per_cu, threads, loads, chunked != 0, out_dev, out_len);
+    return launch_read_probe(h, src_dev, bytes, wg_per_cu, threads, loads, chunked & 1u, (chunked & 2u) != 0, out_dev,
+                             out_len);
 }
 
 int soso_hip_weight_synth(soso_hip *h, const char *key, size_t key_len, uint8_t dtype, size_t rows, size_t cols,

@@ -226,9 +226,10 @@ class HipGpu:
     def synth_normal(self, dst, n, sigma, seed, stream):
         return self._rc(self.lib.soso_hip_synth_normal(self.h, dst, n, sigma, seed, stream), "synth_normal")
 
-    def read_probe(self, src_dev, nbytes, wg_per_cu, threads, out_dev, out_len, loads=1, chunked=False):
+    def read_probe(self, src_dev, nbytes, wg_per_cu, threads, out_dev, out_len, loads=1, chunked=False, stream=False):
         return self._rc(self.lib.soso_hip_read_probe(self.h, src_dev, nbytes, wg_per_cu, threads, loads,
-                                                     1 if chunked else 0, out_dev, out_len), "read_probe")
+                                                     (1 if chunked else 0) | (2 if stream else 0), out_dev, out_len),
+                        "read_probe")
 
     def weight_drop(self, key):
         k, kl = _key(key)
