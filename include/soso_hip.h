@@ -340,6 +340,66 @@ int soso_hip_decode_token(soso_hip *h, const char *model_key, size_t model_key_l
                           uint32_t *token);
 int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key_len);
 
+/* ---- one GQA-MoE layer at a time: GpuDispatch::moe_capa -----------------------
+ * The layer that capa_moe_en_gpu (crates/soso-llm-core/src/moe_gpu.rs:37-269)
+ * hands to GpuDispatch::moe_capa (gpu.rs:426; MoeCapa, gpu.rs:294-335):
+ * forward_layer of one Qwen3-MoE-style layer (layer.rs:1092-1389, 1938-1975)
+ * -- attention with attn_norm, q/k/v, QK norm (qk_norm), NeoX RoPE and the f16
+ * KV cache the device keeps for the layer, o with the residual, then ffn_norm,
+ * router + top-k and the chosen experts' SwiGLU FFNs summed in ranking order,
+ * with the residual -- for n tokens at positions pos0 .. pos0 + n - 1, taken
+ * one after another (each sees the positions before it).
+ * Fields follow MoeCapa: hidden_dim is MoeCapa::h; the q/k/v/o keys and
+ * prefix are NUL-terminated; the experts are the resident weights
+ * "{prefix}.E{ee}.ffn_gate" / "_up" / "_down" (ee two or more digits, as
+ * soso names them); attn_norm, q_norm, k_norm (with qk_norm), ffn_norm
+ * (hidden_dim floats, head_dim for the QK norms) and router (n_exp x
+ * hidden_dim f32) are MoeNormas, needed on a layer's first call and ignored
+ * once the layer is ready (soso_hip_moe_capa_ready).  escala must be
+ * 1 / sqrt(head_dim).  Declined (0, the CPU keeps the layer): sliding windows
+ * (ventana > 0), YaRN (rope_factors or rope_mscale != 1), shapes the decode
+ * step does not run (head_dim 128, GQA groups 1/2/4/8, the single-token MoE
+ * path's limits), pos0 beyond the positions this layer's device KV holds
+ * (the earlier ones were computed elsewhere), pos0 + n > ctx_max.
+ * continuar: the input is the pending output of layer - 1 for the same
+ * tokens (soso_hip_moe_capa_pending), not `hidden`.  encadenar: the output
+ * stays pending on the device and `hidden` is left as it is (no download, no
+ * wait); otherwise it is written to `hidden` (n x hidden_dim) on return.
+ * Returns 1 done, 0 declined, < 0 error. */
+typedef struct soso_hip_moe_capa {
+    uint32_t layer;
+    size_t pos0, n;
+    size_t hidden_dim, heads, kv_heads, head_dim, ffn, n_exp, top_k, ventana, ctx_max;
+    float eps, theta, escala, rope_mscale;
+    int qk_norm, continuar, encadenar;
+    const char *key_q, *key_k, *key_v, *key_o, *prefix;
+    const float *attn_norm, *q_norm, *k_norm, *ffn_norm, *router, *rope_factors;
+} soso_hip_moe_capa;
+int soso_hip_moe_capa_run(soso_hip *h, const soso_hip_moe_capa *capa, float *hidden);
+/* moe_puede (gpu.rs:380): 0 once the layer was discarded, else 1. */
+int soso_hip_moe_capa_can(const soso_hip *h, uint32_t layer);
+/* moe_lista (gpu.rs:386): 1 when the layer's norms, router and device step exist. */
+int soso_hip_moe_capa_ready(const soso_hip *h, uint32_t layer);
+/* moe_pendiente (gpu.rs:392): 1 when the output of `layer` for n tokens from
+ * pos0 is pending on the device. */
+int soso_hip_moe_capa_pending(const soso_hip *h, uint32_t layer, size_t pos0, size_t n);
+/* moe_volcar (gpu.rs:398): writes the pending output (n x hidden_dim) to
+ * hidden and clears it; nothing when none is pending.  Synchronous. */
+int soso_hip_moe_capa_flush(soso_hip *h, float *hidden);
+/* moe_descartar (gpu.rs:421): the layer is not tried again; its device step
+ * and KV cache are freed. */
+void soso_hip_moe_capa_discard(soso_hip *h, uint32_t layer);
+/* Device pointers of the layer's K and V caches (head-major
+ * [kv_heads][ctx_max][head_dim] f16 bits), for inspection. */
+int soso_hip_moe_capa_kv_dev(soso_hip *h, uint32_t layer, void **k_dev, void **v_dev);
+/* gemma_subir / gemma_residente (gpu.rs:362-370), which soso uses to make a
+ * moe_capa layer's attention and expert weights resident: upload makes `key`
+ * resident from its raw bytes (1, 0 declined, < 0 error; a resident key is
+ * kept as it is), resident says whether it is. */
+int soso_hip_weight_upload(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len,
+                           uint8_t dtype, size_t rows, size_t cols);
+int soso_hip_weight_resident(const soso_hip *h, const char *key, size_t key_len);
+
 /* ---- device-resident API (no host copies; for the decode step, benchmarks
  * and tests that keep inputs in HBM).  Launches are asynchronous on the
  * handle's stream; soso_hip_sync waits. -------------------------------------- */

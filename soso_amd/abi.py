@@ -64,6 +64,22 @@ class Expert(C.Structure):
     ]
 
 
+class MoeCapa(C.Structure):
+    """soso_hip_moe_capa: GpuDispatch::moe_capa's MoeCapa (gpu.rs:294-335)."""
+    _fields_ = [
+        ("layer", C.c_uint32), ("pos0", C.c_size_t), ("n", C.c_size_t),
+        ("hidden_dim", C.c_size_t), ("heads", C.c_size_t), ("kv_heads", C.c_size_t), ("head_dim", C.c_size_t),
+        ("ffn", C.c_size_t), ("n_exp", C.c_size_t), ("top_k", C.c_size_t), ("ventana", C.c_size_t),
+        ("ctx_max", C.c_size_t),
+        ("eps", C.c_float), ("theta", C.c_float), ("escala", C.c_float), ("rope_mscale", C.c_float),
+        ("qk_norm", C.c_int), ("continuar", C.c_int), ("encadenar", C.c_int),
+        ("key_q", C.c_char_p), ("key_k", C.c_char_p), ("key_v", C.c_char_p), ("key_o", C.c_char_p),
+        ("prefix", C.c_char_p),
+        ("attn_norm", C.c_void_p), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+        ("router", C.c_void_p), ("rope_factors", C.c_void_p),
+    ]
+
+
 _P = C.c_void_p
 _S = C.c_size_t
 _I = C.c_int
@@ -121,6 +137,15 @@ PROTOTYPES = {
     "soso_hip_graph_end": (_I, [_P, C.POINTER(_I)]),
     "soso_hip_graph_launch": (_I, [_P, _I]),
     "soso_hip_graph_destroy": (_I, [_P, _I]),
+    "soso_hip_moe_capa_run": (_I, [_P, C.POINTER(MoeCapa), _P]),
+    "soso_hip_moe_capa_can": (_I, [_P, C.c_uint32]),
+    "soso_hip_moe_capa_ready": (_I, [_P, C.c_uint32]),
+    "soso_hip_moe_capa_pending": (_I, [_P, C.c_uint32, _S, _S]),
+    "soso_hip_moe_capa_flush": (_I, [_P, _P]),
+    "soso_hip_moe_capa_discard": (None, [_P, C.c_uint32]),
+    "soso_hip_moe_capa_kv_dev": (_I, [_P, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),
+    "soso_hip_weight_upload": (_I, [_P, C.c_char_p, _S, _P, _S, _U8, _S, _S]),
+    "soso_hip_weight_resident": (_I, [_P, C.c_char_p, _S]),
 }
 
 MOE_NOALLOC_SCRATCH_BYTES = 8 << 20  # SOSO_HIP_MOE_NOALLOC_SCRATCH_BYTES

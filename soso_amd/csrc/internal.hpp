@@ -140,7 +140,7 @@ struct soso_hip {
     // the scratch pointers it was captured with, so a slot outgrown while any
     // graph exists is retired, not freed: retired buffers are freed once no
     // graph is left (graph_destroy) or with the handle.
-    static constexpr int N_SCRATCH = 14;
+    static constexpr int N_SCRATCH = 16;
     void *scratch[N_SCRATCH] = {};
     size_t scratch_cap[N_SCRATCH] = {};
     std::vector<void *> retired;
@@ -157,6 +157,25 @@ struct soso_hip {
     void *fixed_scratch = nullptr;
     std::unordered_map<std::string, MoeLayer> moe_layers;
     std::unordered_map<std::string, DecodeModel> decode_models;
+    // soso_hip_moe_capa: per layer, its one-layer device step ("moe_capa.L<l>"
+    // in decode_models), the MoE layer it registered and the library's own
+    // keys (norms, router); the positions its KV cache holds; discarded layers;
+    // the pending output of the last chained call (encadenar)
+    struct MoeCapaLayer {
+        std::string model, moe_key;
+        std::vector<std::string> own_keys;
+        size_t kv_pos = 0;
+        float theta = 0.0f, eps = 0.0f;
+        int qk_norm = 0;
+    };
+    std::unordered_map<uint32_t, MoeCapaLayer> moe_capas;
+    std::vector<uint32_t> moe_capa_discarded;
+    struct {
+        bool valid = false;
+        uint32_t layer = 0;
+        size_t pos0 = 0, n = 0, width = 0;
+        const float *dev = nullptr; // n x width floats
+    } moe_pend;
     // soso_hip_moe_shared's output (n x hdim f32 in scratch slot 12), waiting
     // for the next soso_hip_experts_block call, which adds it to its sum
     bool shared_pending = false;

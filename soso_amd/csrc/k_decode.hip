@@ -650,6 +650,7 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
             }
         }
     }
+    if (!m.head) return rc; // a stack of layers without the head (soso_hip_moe_capa)
     if (rc == SOSO_HIP_OK) {
         MvIn in;
         in.x = hid;

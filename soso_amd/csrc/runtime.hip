@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <chrono>
+#include <cstdio>
 #include <cstring>
 #include <new>
 
@@ -759,9 +760,11 @@ int soso_hip_moe_shared(soso_hip *h, const char *const *keys, const size_t *key_
 }
 
 // ---- MoE FFN resident on the device ----------------------------------------
-int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_len, const char *router_key,
-                          size_t router_key_len, const char *const *expert_keys, const size_t *expert_key_lens,
-                          size_t n_exp, size_t hdim, size_t ffn, size_t top_k)
+// want_tiled = false: no tile-major copies (a layer only the single-token
+// kernels read, such as soso_hip_moe_capa's).
+static int moe_register_impl(soso_hip *h, const char *layer_key, size_t layer_key_len, const char *router_key,
+                             size_t router_key_len, const char *const *expert_keys, const size_t *expert_key_lens,
+                             size_t n_exp, size_t hdim, size_t ffn, size_t top_k, bool want_tiled)
 {
     if (!h) return SOSO_HIP_ERR_ARG;
     if (!layer_key || !router_key || (expert_keys && !expert_key_lens) || n_exp == 0 || n_exp > 256 || top_k == 0 ||
@@ -807,8 +810,8 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
     // Tile-major copies of the Q4_K experts for the matrix-core path (the
     // row-major ones stay for the single-token kernels); skipped, with the
     // row-major matrix-core path as fallback, when the budget has no room.
-    const bool tgu = m.dt_gu == SOSO_HIP_DTYPE_Q4_K && tiled_q4k_ok(m.dt_gu, ffn, hdim);
-    const bool tdn = m.dt_down == SOSO_HIP_DTYPE_Q4_K && tiled_q4k_ok(m.dt_down, hdim, ffn);
+    const bool tgu = want_tiled && m.dt_gu == SOSO_HIP_DTYPE_Q4_K && tiled_q4k_ok(m.dt_gu, ffn, hdim);
+    const bool tdn = want_tiled && m.dt_down == SOSO_HIP_DTYPE_Q4_K && tiled_q4k_ok(m.dt_down, hdim, ffn);
     const size_t b_gu = ffn * packed_row_stride(SOSO_HIP_DTYPE_Q4_K, hdim);
     const size_t b_dn = hdim * packed_row_stride(SOSO_HIP_DTYPE_Q4_K, ffn);
     const size_t tbytes = n_exp * ((tgu ? 2 * b_gu : 0) + (tdn ? b_dn : 0));
@@ -846,6 +849,14 @@ int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_l
     }
     h->moe_layers.emplace(k, m);
     return rc;
+}
+
+int soso_hip_moe_register(soso_hip *h, const char *layer_key, size_t layer_key_len, const char *router_key,
+                          size_t router_key_len, const char *const *expert_keys, const size_t *expert_key_lens,
+                          size_t n_exp, size_t hdim, size_t ffn, size_t top_k)
+{
+    return moe_register_impl(h, layer_key, layer_key_len, router_key, router_key_len, expert_keys, expert_key_lens,
+                             n_exp, hdim, ffn, top_k, true);
 }
 
 // A registered layer over n tokens with its scratch in ms (sized for
@@ -926,14 +937,18 @@ int soso_hip_moe_ffn_dev_noalloc(soso_hip *h, const char *layer_key, size_t laye
 // decode_create / decode_create_moe: moe_keys (n_layers entries, null for a
 // dense model) names the registered MoE layer that is layer l's FFN, or null
 // for a dense FFN.
+// layers_only: a stack of layers without the output norm and head (the keys
+// end with the last layer's; cfg->vocab is ignored): soso_hip_moe_capa's
+// per-layer steps, hidden state in and out.
 static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_key_len, const soso_hip_decode_cfg *cfg,
                               uint32_t flags, const char *const *keys, const size_t *key_lens,
-                              const char *const *moe_keys, const size_t *moe_key_lens, int drop_sources)
+                              const char *const *moe_keys, const size_t *moe_key_lens, int drop_sources,
+                              bool layers_only = false)
 {
     if (!h) return SOSO_HIP_ERR_ARG;
     if (!model_key || !cfg || !keys || !key_lens || cfg->n_layers == 0 || cfg->hidden == 0 || cfg->hidden % 4 ||
         cfg->n_kv_heads == 0 || cfg->n_heads % cfg->n_kv_heads || cfg->head_dim == 0 || cfg->ffn == 0 ||
-        cfg->vocab == 0 || cfg->ctx_max == 0)
+        (cfg->vocab == 0 && !layers_only) || cfg->ctx_max == 0)
         return set_err(h, SOSO_HIP_ERR_ARG, "decode_create: config");
     int rc = make_current(h);
     if (rc != SOSO_HIP_OK) return rc;
@@ -952,7 +967,7 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     m.n_kv_heads = cfg->n_kv_heads;
     m.head_dim = cfg->head_dim;
     m.ffn = F;
-    m.vocab = cfg->vocab;
+    m.vocab = layers_only ? 0 : cfg->vocab;
     m.ctx_max = cfg->ctx_max;
     m.theta = cfg->rope_theta;
     m.eps = cfg->rms_eps;
@@ -1030,12 +1045,14 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
         m.layers[l].q_norm = qn ? (const float *)qn->dev : nullptr;
         m.layers[l].k_norm = kn ? (const float *)kn->dev : nullptr;
     }
-    const Weight *on;
-    if (!get(kpl * L, 1, H, true, &on) || !get(kpl * L + 1, cfg->vocab, H, false, &m.head))
-        return set_err(h, SOSO_HIP_DECLINED, "decode_create: output_norm/head missing or of the wrong shape");
-    if (const char *why = matvec_ex_unsupported(h, m.head->dtype, cfg->vocab, H, XS_RMSNORM, EPI_STORE))
-        return set_err(h, SOSO_HIP_DECLINED, std::string("decode_create: head: ") + why);
-    m.out_norm = (const float *)on->dev;
+    if (!layers_only) {
+        const Weight *on;
+        if (!get(kpl * L, 1, H, true, &on) || !get(kpl * L + 1, cfg->vocab, H, false, &m.head))
+            return set_err(h, SOSO_HIP_DECLINED, "decode_create: output_norm/head missing or of the wrong shape");
+        if (const char *why = matvec_ex_unsupported(h, m.head->dtype, cfg->vocab, H, XS_RMSNORM, EPI_STORE))
+            return set_err(h, SOSO_HIP_DECLINED, std::string("decode_create: head: ") + why);
+        m.out_norm = (const float *)on->dev;
+    }
     // what stays in use (dropping one of these unregisters the model)
     for (size_t l = 0; l < L; l++) {
         for (size_t j : {0, 4, 5, 8})
@@ -1043,8 +1060,10 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
         if (m.qk_norm)
             for (size_t j : {9, 10}) m.uses.emplace_back(keys[kpl * l + j], key_lens[kpl * l + j]);
     }
-    m.uses.emplace_back(keys[kpl * L], key_lens[kpl * L]);
-    m.uses.emplace_back(keys[kpl * L + 1], key_lens[kpl * L + 1]);
+    if (!layers_only) {
+        m.uses.emplace_back(keys[kpl * L], key_lens[kpl * L]);
+        m.uses.emplace_back(keys[kpl * L + 1], key_lens[kpl * L + 1]);
+    }
     // fused copies
     m.owned.resize(2 * L);
     for (size_t l = 0; l < L && rc == SOSO_HIP_OK; l++) {
@@ -1094,7 +1113,7 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
     const size_t chunks = 1 + (cfg->ctx_max + ATT_CHUNK - 1) / ATT_CHUNK; // attention partials per head, at most
     const size_t act_floats = H + (qd + 2 * kvd) + qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) +
-                              cfg->vocab + 64 + cfg->head_dim / 2 + H;
+                              m.vocab + 64 + cfg->head_dim / 2 + H;
     // MoE scratch (shared by the MoE layers, which run one after another) and
     // each layer's routing of the last step (256-byte slots)
     const size_t moe_route_bytes = 512;
@@ -1120,7 +1139,7 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     m.act = m.att + qd;
     m.part = m.act + F;
     m.logits = m.part + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2);
-    m.rope_freq = m.logits + cfg->vocab + 64;
+    m.rope_freq = m.logits + m.vocab + 64;
     m.xn = m.rope_freq + cfg->head_dim / 2;
     for (size_t l = 0, j = 0; l < L; l++) {
         DecodeLayer &dl = m.layers[l];
@@ -1313,6 +1332,294 @@ int soso_hip_decode_destroy(soso_hip *h, const char *model_key, size_t model_key
     const int rc = decode_free(h, it->second);
     h->decode_models.erase(it);
     return rc;
+}
+
+// ---- one GQA-MoE layer at a time (GpuDispatch::moe_capa) ---------------------
+// The layer runs as a one-layer device step without a head (decode_step over a
+// layers_only model: the attention with its f16 KV cache, then the MoE FFN of
+// the layer registered from the caller's experts), token by token.  The
+// output of a chained call (encadenar) stays in the step's hidden buffer, or,
+// for several tokens, in scratch slot 15, until the next layer reads it
+// (continuar) or soso_hip_moe_capa_flush brings it down.
+static bool moe_capa_is_discarded(const soso_hip *h, uint32_t layer)
+{
+    return std::find(h->moe_capa_discarded.begin(), h->moe_capa_discarded.end(), layer) !=
+           h->moe_capa_discarded.end();
+}
+
+static int moe_capa_drop(soso_hip *h, uint32_t layer)
+{
+    auto it = h->moe_capas.find(layer);
+    if (it == h->moe_capas.end()) return SOSO_HIP_OK;
+    int rc = SOSO_HIP_OK;
+    auto dm = h->decode_models.find(it->second.model);
+    if (dm != h->decode_models.end()) {
+        rc = decode_free(h, dm->second);
+        h->decode_models.erase(dm);
+    }
+    // the library's own keys (dropping the router also unregisters the MoE layer)
+    for (const std::string &k : it->second.own_keys) {
+        const int r = soso_hip_weight_drop(h, k.data(), k.size());
+        if (r < 0) rc = first_fail(rc, r);
+    }
+    if (h->moe_pend.valid && h->moe_pend.layer == layer) h->moe_pend.valid = false;
+    h->moe_capas.erase(it);
+    return rc;
+}
+
+// First call of a layer: its norms and router become resident under the
+// library's own keys, its MoE FFN is registered and its one-layer step built.
+static int moe_capa_prepare(soso_hip *h, const soso_hip_moe_capa *c)
+{
+    const size_t H = c->hidden_dim, hd = c->head_dim;
+    if (!c->attn_norm || !c->ffn_norm || !c->router || (c->qk_norm && (!c->q_norm || !c->k_norm)))
+        return set_err(h, SOSO_HIP_ERR_ARG, "moe_capa: the layer's first call needs its norms and router (MoeNormas)");
+    soso_hip::MoeCapaLayer st;
+    const std::string base = "moe_capa.L" + std::to_string(c->layer);
+    st.model = base;
+    st.moe_key = base + ".moe";
+    st.theta = c->theta;
+    st.eps = c->eps;
+    st.qk_norm = c->qk_norm ? 1 : 0;
+    int rc = SOSO_HIP_OK;
+    auto put = [&](const std::string &k, const float *v, size_t rows, size_t cols) {
+        if (rc != SOSO_HIP_OK) return;
+        Weight *w = nullptr;
+        (void)soso_hip_weight_drop(h, k.data(), k.size()); // a stale copy from an earlier life of the layer
+        rc = get_weight(h, k.data(), k.size(), (const uint8_t *)v, rows * cols * 4, SOSO_HIP_DTYPE_F32, rows, cols, &w);
+        if (rc == SOSO_HIP_OK) st.own_keys.push_back(k);
+    };
+    put(base + ".attn_norm", c->attn_norm, 1, H);
+    put(base + ".ffn_norm", c->ffn_norm, 1, H);
+    if (c->qk_norm) {
+        put(base + ".q_norm", c->q_norm, 1, hd);
+        put(base + ".k_norm", c->k_norm, 1, hd);
+    }
+    put(base + ".router", c->router, c->n_exp, H);
+    std::vector<std::string> ek;
+    std::vector<const char *> ep;
+    std::vector<size_t> el;
+    if (rc == SOSO_HIP_OK) {
+        static const char *const part[3] = {"ffn_gate", "ffn_up", "ffn_down"};
+        ek.reserve(3 * c->n_exp);
+        for (size_t e = 0; e < c->n_exp; e++)
+            for (int j = 0; j < 3; j++) {
+                char num[24];
+                snprintf(num, sizeof num, "%02zu", e);
+                ek.push_back(std::string(c->prefix) + ".E" + num + "." + part[j]);
+            }
+        for (const std::string &k : ek) {
+            ep.push_back(k.data());
+            el.push_back(k.size());
+        }
+        const std::string rk = base + ".router";
+        rc = moe_register_impl(h, st.moe_key.data(), st.moe_key.size(), rk.data(), rk.size(), ep.data(), el.data(),
+                               c->n_exp, H, c->ffn, c->top_k, false);
+    }
+    if (rc == SOSO_HIP_OK) {
+        soso_hip_decode_cfg cfg{};
+        cfg.n_layers = 1;
+        cfg.hidden = (uint32_t)H;
+        cfg.n_heads = (uint32_t)c->heads;
+        cfg.n_kv_heads = (uint32_t)c->kv_heads;
+        cfg.head_dim = (uint32_t)hd;
+        cfg.ffn = 1; // the layer's FFN is the MoE layer
+        cfg.vocab = 0;
+        cfg.ctx_max = (uint32_t)c->ctx_max;
+        cfg.rope_theta = c->theta;
+        cfg.rms_eps = c->eps;
+        cfg.kv_f16 = 1; // soso's device MoE layers keep an f16 KV (moe_gpu.rs:47)
+        const std::string an = base + ".attn_norm", fn = base + ".ffn_norm", qn = base + ".q_norm",
+                          kn = base + ".k_norm";
+        const char *keys[11] = {an.data(), c->key_q, c->key_k, c->key_v, c->key_o, fn.data(), nullptr, nullptr,
+                                nullptr, qn.data(), kn.data()};
+        size_t lens[11] = {an.size(), strlen(c->key_q), strlen(c->key_k), strlen(c->key_v), strlen(c->key_o),
+                           fn.size(), 0, 0, 0, qn.size(), kn.size()};
+        const char *mk[1] = {st.moe_key.data()};
+        const size_t ml[1] = {st.moe_key.size()};
+        const uint32_t flags = SOSO_HIP_DECODE_ROPE_NEOX | (c->qk_norm ? SOSO_HIP_DECODE_QK_NORM : 0u);
+        rc = decode_create_impl(h, st.model.data(), st.model.size(), &cfg, flags, keys, lens, mk, ml, 0, true);
+    }
+    const std::string err = h->err;
+    h->moe_capas[c->layer] = st;
+    if (rc != SOSO_HIP_OK) {
+        (void)moe_capa_drop(h, c->layer);
+        h->err = err;
+    }
+    return rc;
+}
+
+int soso_hip_moe_capa_run(soso_hip *h, const soso_hip_moe_capa *c, float *hidden)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!c || !c->key_q || !c->key_k || !c->key_v || !c->key_o || !c->prefix || c->n == 0 || c->hidden_dim == 0 ||
+        c->heads == 0 || c->kv_heads == 0 || c->n_exp == 0 || c->top_k == 0 || (!hidden && !c->encadenar) ||
+        (!hidden && !c->continuar))
+        return set_err(h, SOSO_HIP_ERR_ARG, "moe_capa: args");
+    if (h->capturing) return set_err(h, SOSO_HIP_ERR_ARG, "moe_capa: not inside graph capture");
+    if (moe_capa_is_discarded(h, c->layer)) return set_err(h, SOSO_HIP_DECLINED, "moe_capa: layer discarded");
+    // what the device step does not run: the CPU keeps the layer
+    if (c->ventana > 0) return set_err(h, SOSO_HIP_DECLINED, "moe_capa: sliding-window attention");
+    if (c->rope_factors || c->rope_mscale != 1.0f) return set_err(h, SOSO_HIP_DECLINED, "moe_capa: YaRN RoPE");
+    if (c->head_dim == 0 || c->escala != 1.0f / sqrtf((float)c->head_dim))
+        return set_err(h, SOSO_HIP_DECLINED, "moe_capa: attention scale other than 1/sqrt(head_dim)");
+    if (c->pos0 + c->n > c->ctx_max) return set_err(h, SOSO_HIP_DECLINED, "moe_capa: positions beyond ctx_max");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    CallClock clk(h);
+    auto it = h->moe_capas.find(c->layer);
+    if (it != h->moe_capas.end() &&
+        (it->second.theta != c->theta || it->second.eps != c->eps || it->second.qk_norm != (c->qk_norm ? 1 : 0) ||
+         !h->decode_models.count(it->second.model))) {
+        // the layer's configuration changed, or a weight its step read was
+        // dropped: built again (from the norms this call must then carry)
+        rc = moe_capa_drop(h, c->layer);
+        if (rc < 0) return rc;
+        it = h->moe_capas.end();
+    }
+    if (it == h->moe_capas.end()) {
+        rc = moe_capa_prepare(h, c);
+        if (rc != SOSO_HIP_OK) return rc;
+        it = h->moe_capas.find(c->layer);
+    }
+    soso_hip::MoeCapaLayer &st = it->second;
+    auto dmi = h->decode_models.find(st.model);
+    if (dmi == h->decode_models.end()) return set_err(h, SOSO_HIP_ERR, "moe_capa: the layer's step is gone");
+    DecodeModel &m = dmi->second;
+    const size_t H = c->hidden_dim;
+    if (m.hidden != H || m.n_heads != c->heads || m.n_kv_heads != c->kv_heads || m.head_dim != c->head_dim ||
+        !m.layers[0].moe || m.layers[0].moe->n_exp != c->n_exp || m.layers[0].moe->top_k != c->top_k ||
+        m.layers[0].moe->ffn != c->ffn || m.ctx_max < c->ctx_max)
+        return set_err(h, SOSO_HIP_ERR_ARG, "moe_capa: the layer's shape differs from its first call");
+    // the positions before pos0 must be in this layer's device KV (computed here)
+    if (c->pos0 > st.kv_pos)
+        return set_err(h, SOSO_HIP_DECLINED, "moe_capa: earlier positions of the layer were not computed here");
+    // input: the pending output of layer - 1 (continuar), or the caller's hidden
+    const float *xin = nullptr;
+    if (c->continuar) {
+        if (!h->moe_pend.valid || h->moe_pend.layer + 1 != c->layer || h->moe_pend.pos0 != c->pos0 ||
+            h->moe_pend.n != c->n || h->moe_pend.width != H)
+            return set_err(h, SOSO_HIP_ERR_ARG, "moe_capa: continuar without the previous layer's pending output");
+        xin = h->moe_pend.dev;
+    } else {
+        float *xd = (float *)scratch_get(h, 14, c->n * H * 4);
+        if (!xd) return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_capa: input staging");
+        rc = hip_check(h, hipMemcpyAsync(xd, hidden, c->n * H * 4, hipMemcpyHostToDevice, h->stream), "hidden up");
+        if (rc != SOSO_HIP_OK) return rc;
+        h->stats.bytes_up += c->n * H * 4;
+        xin = xd;
+    }
+    // several tokens: their outputs gather in scratch slot 15 (the previous
+    // layer's, when it is the input, is copied aside first)
+    float *outs = nullptr;
+    if (c->n > 1) {
+        if (c->continuar && h->moe_pend.dev != m.hid) {
+            float *tmp = (float *)scratch_get(h, 14, c->n * H * 4);
+            if (!tmp) return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_capa: input staging");
+            rc = hip_check(h, hipMemcpyAsync(tmp, xin, c->n * H * 4, hipMemcpyDeviceToDevice, h->stream), "pending");
+            if (rc != SOSO_HIP_OK) return rc;
+            xin = tmp;
+        }
+        outs = (float *)scratch_get(h, 15, c->n * H * 4);
+        if (!outs) return set_err(h, SOSO_HIP_ERR_NOMEM, "moe_capa: output staging");
+    }
+    h->moe_pend.valid = false;
+    for (size_t t = 0; t < c->n && rc == SOSO_HIP_OK; t++) {
+        rc = decode_step(h, m, xin + t * H, (uint32_t)(c->pos0 + t), nullptr, nullptr, nullptr);
+        if (rc == SOSO_HIP_OK && outs)
+            rc = hip_check(h, hipMemcpyAsync(outs + t * H, m.hid, H * 4, hipMemcpyDeviceToDevice, h->stream),
+                           "token output");
+    }
+    if (rc != SOSO_HIP_OK) {
+        (void)hip_release(h, hipStreamSynchronize(h->stream), "moe_capa drain");
+        return rc;
+    }
+    st.kv_pos = c->pos0 + c->n;
+    const float *res = outs ? outs : m.hid;
+    if (c->encadenar) {
+        h->moe_pend.valid = true;
+        h->moe_pend.layer = c->layer;
+        h->moe_pend.pos0 = c->pos0;
+        h->moe_pend.n = c->n;
+        h->moe_pend.width = H;
+        h->moe_pend.dev = res;
+        clk.done();
+        return SOSO_HIP_OK;
+    }
+    rc = hip_check(h, hipMemcpyAsync(hidden, res, c->n * H * 4, hipMemcpyDeviceToHost, h->stream), "hidden down");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "moe_capa sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    h->stats.bytes_down += c->n * H * 4;
+    clk.done();
+    return SOSO_HIP_OK;
+}
+
+int soso_hip_moe_capa_can(const soso_hip *h, uint32_t layer)
+{
+    return h && !moe_capa_is_discarded(h, layer) ? 1 : 0;
+}
+
+int soso_hip_moe_capa_ready(const soso_hip *h, uint32_t layer)
+{
+    if (!h) return 0;
+    auto it = h->moe_capas.find(layer);
+    return it != h->moe_capas.end() && h->decode_models.count(it->second.model) ? 1 : 0;
+}
+
+int soso_hip_moe_capa_pending(const soso_hip *h, uint32_t layer, size_t pos0, size_t n)
+{
+    return h && h->moe_pend.valid && h->moe_pend.layer == layer && h->moe_pend.pos0 == pos0 && h->moe_pend.n == n
+               ? 1
+               : 0;
+}
+
+int soso_hip_moe_capa_flush(soso_hip *h, float *hidden)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!h->moe_pend.valid) return SOSO_HIP_OK;
+    if (!hidden) return set_err(h, SOSO_HIP_ERR_ARG, "moe_capa_flush: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    const size_t bytes = h->moe_pend.n * h->moe_pend.width * 4;
+    rc = hip_check(h, hipMemcpyAsync(hidden, h->moe_pend.dev, bytes, hipMemcpyDeviceToHost, h->stream), "pending down");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "moe_capa_flush sync");
+    if (rc != SOSO_HIP_OK) return rc;
+    h->stats.bytes_down += bytes;
+    h->moe_pend.valid = false;
+    return SOSO_HIP_OK;
+}
+
+void soso_hip_moe_capa_discard(soso_hip *h, uint32_t layer)
+{
+    if (!h) return;
+    if (make_current(h) == SOSO_HIP_OK) (void)moe_capa_drop(h, layer);
+    if (!moe_capa_is_discarded(h, layer)) h->moe_capa_discarded.push_back(layer);
+}
+
+int soso_hip_moe_capa_kv_dev(soso_hip *h, uint32_t layer, void **k_dev, void **v_dev)
+{
+    if (!h || !k_dev || !v_dev) return SOSO_HIP_ERR_ARG;
+    auto it = h->moe_capas.find(layer);
+    if (it == h->moe_capas.end()) return set_err(h, SOSO_HIP_DECLINED, "moe_capa_kv: layer not prepared");
+    return soso_hip_decode_kv_dev(h, it->second.model.data(), it->second.model.size(), 0, k_dev, v_dev);
+}
+
+int soso_hip_weight_upload(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len,
+                           uint8_t dtype, size_t rows, size_t cols)
+{
+    if (!h) return SOSO_HIP_ERR_ARG;
+    if (!key || !w || rows == 0 || cols == 0) return set_err(h, SOSO_HIP_ERR_ARG, "weight_upload: args");
+    int rc = make_current(h);
+    if (rc != SOSO_HIP_OK) return rc;
+    Weight *wt = nullptr;
+    return get_weight(h, key, key_len, w, w_len, dtype, rows, cols, &wt);
+}
+
+int soso_hip_weight_resident(const soso_hip *h, const char *key, size_t key_len)
+{
+    if (!h || !key) return 0;
+    auto it = h->weights.find(std::string(key, key_len));
+    return it != h->weights.end() && !it->second.declined ? 1 : 0;
 }
 
 // ---- device-resident API ----------------------------------------------------

@@ -378,6 +378,62 @@ class HipGpu:
                  "decode_moe_routing")
         return self.d2h(i.value, (top_k,), np.int32), self.d2h(w.value, (top_k,), np.float32)
 
+    # -- moe_capa: one GQA-MoE layer at a time (gpu.rs:380-426) ----------------
+    def gemma_subir(self, key, w, dtype, rows, cols):
+        """gpu.rs:368: makes `key` resident from its raw bytes."""
+        k, kl = _key(key)
+        wb = _raw(w)
+        return self._rc(self.lib.soso_hip_weight_upload(self.h, k, kl, wb.ctypes.data, wb.size, dtype, rows, cols),
+                        f"weight_upload {key}")
+
+    def gemma_residente(self, key):
+        k, kl = _key(key)
+        return bool(self.lib.soso_hip_weight_resident(self.h, k, kl))
+
+    def moe_capa(self, capa, hidden):
+        """gpu.rs:426.  capa: a dict of MoeCapa's fields (soso_hip_moe_capa;
+        norms/router numpy f32 or None; keys str); hidden: float32 n x h,
+        read unless continuar, written unless encadenar."""
+        c = abi.MoeCapa()
+        keep = []
+        for name, _ in abi.MoeCapa._fields_:
+            if name not in capa or capa[name] is None:
+                continue
+            v = capa[name]
+            if name.startswith("key_") or name == "prefix":
+                v = v.encode()
+            elif name in ("attn_norm", "q_norm", "k_norm", "ffn_norm", "router", "rope_factors"):
+                v = _f32(v)
+                keep.append(v)
+                v = v.ctypes.data
+            elif isinstance(v, np.generic):
+                v = v.item()
+            setattr(c, name, v)
+        assert hidden is None or (hidden.dtype == np.float32 and hidden.flags.c_contiguous)
+        rc = self.lib.soso_hip_moe_capa_run(self.h, C.byref(c), None if hidden is None else hidden.ctypes.data)
+        return self._rc(rc, f"moe_capa layer {capa.get('layer')}")
+
+    def moe_puede(self, layer):
+        return bool(self.lib.soso_hip_moe_capa_can(self.h, layer))
+
+    def moe_lista(self, layer):
+        return bool(self.lib.soso_hip_moe_capa_ready(self.h, layer))
+
+    def moe_pendiente(self, layer, pos0, n):
+        return bool(self.lib.soso_hip_moe_capa_pending(self.h, layer, pos0, n))
+
+    def moe_volcar(self, hidden):
+        assert hidden.dtype == np.float32 and hidden.flags.c_contiguous
+        self._rc(self.lib.soso_hip_moe_capa_flush(self.h, hidden.ctypes.data), "moe_volcar")
+
+    def moe_descartar(self, layer):
+        self.lib.soso_hip_moe_capa_discard(self.h, layer)
+
+    def moe_capa_kv_dev(self, layer):
+        k, v = C.c_void_p(), C.c_void_p()
+        self._rc(self.lib.soso_hip_moe_capa_kv_dev(self.h, layer, C.byref(k), C.byref(v)), "moe_capa_kv_dev")
+        return k.value, v.value
+
     def decode_kv_dev(self, model_key, layer):
         mk, ml = _key(model_key)
         k, v = C.c_void_p(), C.c_void_p()

@@ -127,12 +127,14 @@ class Model:
         self.keys = keys
         return keys
 
-    def cpu_step(self, orc, x, kcache, vcache, pos, theta, eps, kv_f16=False, moe=None):
+    def cpu_step(self, orc, x, kcache, vcache, pos, theta, eps, kv_f16=False, moe=None, kv_rows=None):
         """The layer stack on the CPU; kcache/vcache [L][ctx][kvd] get row pos
         (rounded through soso's f16 when kv_f16, as KvCache::append stores it).
         moe: {layer: MoeFfn} -- those layers' FFN is the MoE FFN (forward_moe_ffn,
         layer.rs:1938-1975: rmsnorm, or_moe_ffn, residual); their routing is
-        kept in self.routing[layer]."""
+        kept in self.routing[layer].  kv_rows: {layer: (k, v)} rows to store at
+        pos instead of the CPU's own (the f32 rows it computed are still kept
+        in self.last_kv)."""
         L_ = orc.lib()
         h = x.astype(np.float32).copy()
         new_k, new_v = [], []
@@ -154,8 +156,11 @@ class Model:
             neox = 1 if self.neox else 0
             L_.or_rope_heads(q.ctypes.data, self.nh, HD, pos, np.float32(theta), neox)
             L_.or_rope_heads(k.ctypes.data, self.nkv, HD, pos, np.float32(theta), neox)
-            kcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(k)) if kv_f16 else k
-            vcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(v)) if kv_f16 else v
+            if kv_rows and l in kv_rows:
+                kcache[l, pos], vcache[l, pos] = kv_rows[l]
+            else:
+                kcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(k)) if kv_f16 else k
+                vcache[l, pos] = orc.f16_to_f32(orc.f32_to_f16(v)) if kv_f16 else v
             new_k.append(k)
             new_v.append(v)
             att = np.zeros(self.qd, np.float32)
@@ -180,6 +185,7 @@ class Model:
             up = orc.matvec(d("up"), lw["up"], self.F, self.H, xn)
             L_.or_swiglu(up.ctypes.data, gt.ctypes.data, self.F)
             h = orc.matvec(d("down"), lw["down"], self.H, self.F, up) + h
+        self.last_hidden = h  # the stack's output, before the output norm
         xn = h.copy()
         L_.or_rmsnorm(xn.ctypes.data, self.out_norm.ctypes.data, self.H, np.float32(eps))
         logits = orc.matvec(self.head_dtype, self.head, self.V, self.H, xn)
