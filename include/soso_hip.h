@@ -392,6 +392,10 @@ void soso_hip_moe_capa_discard(soso_hip *h, uint32_t layer);
 /* Device pointers of the layer's K and V caches (head-major
  * [kv_heads][ctx_max][head_dim] f16 bits), for inspection. */
 int soso_hip_moe_capa_kv_dev(soso_hip *h, uint32_t layer, void **k_dev, void **v_dev);
+/* The layer's routing of the last token it computed: top_k int32 expert
+ * indices in ranking order and their f32 weights (device pointers), for
+ * inspection. */
+int soso_hip_moe_capa_routing_dev(soso_hip *h, uint32_t layer, int32_t **idx_dev, float **wgt_dev);
 /* gemma_subir / gemma_residente (gpu.rs:362-370), which soso uses to make a
  * moe_capa layer's attention and expert weights resident: upload makes `key`
  * resident from its raw bytes (1, 0 declined, < 0 error; a resident key is

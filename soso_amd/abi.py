@@ -144,6 +144,7 @@ PROTOTYPES = {
     "soso_hip_moe_capa_flush": (_I, [_P, _P]),
     "soso_hip_moe_capa_discard": (None, [_P, C.c_uint32]),
     "soso_hip_moe_capa_kv_dev": (_I, [_P, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),
+    "soso_hip_moe_capa_routing_dev": (_I, [_P, C.c_uint32, C.POINTER(_P), C.POINTER(_P)]),
     "soso_hip_weight_upload": (_I, [_P, C.c_char_p, _S, _P, _S, _U8, _S, _S]),
     "soso_hip_weight_resident": (_I, [_P, C.c_char_p, _S]),
 }

@@ -1604,6 +1604,14 @@ int soso_hip_moe_capa_kv_dev(soso_hip *h, uint32_t layer, void **k_dev, void **v
     return soso_hip_decode_kv_dev(h, it->second.model.data(), it->second.model.size(), 0, k_dev, v_dev);
 }
 
+int soso_hip_moe_capa_routing_dev(soso_hip *h, uint32_t layer, int32_t **idx_dev, float **wgt_dev)
+{
+    if (!h || !idx_dev || !wgt_dev) return SOSO_HIP_ERR_ARG;
+    auto it = h->moe_capas.find(layer);
+    if (it == h->moe_capas.end()) return set_err(h, SOSO_HIP_DECLINED, "moe_capa_routing: layer not prepared");
+    return soso_hip_decode_moe_routing_dev(h, it->second.model.data(), it->second.model.size(), 0, idx_dev, wgt_dev);
+}
+
 int soso_hip_weight_upload(soso_hip *h, const char *key, size_t key_len, const uint8_t *w, size_t w_len,
                            uint8_t dtype, size_t rows, size_t cols)
 {

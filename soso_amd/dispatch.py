@@ -434,6 +434,12 @@ class HipGpu:
         self._rc(self.lib.soso_hip_moe_capa_kv_dev(self.h, layer, C.byref(k), C.byref(v)), "moe_capa_kv_dev")
         return k.value, v.value
 
+    def moe_capa_routing(self, layer, top_k):
+        """The routing of the layer's last token: (indices, weights)."""
+        i, w = C.c_void_p(), C.c_void_p()
+        self._rc(self.lib.soso_hip_moe_capa_routing_dev(self.h, layer, C.byref(i), C.byref(w)), "moe_capa_routing")
+        return self.d2h(i.value, (top_k,), np.int32), self.d2h(w.value, (top_k,), np.float32)
+
     def decode_kv_dev(self, model_key, layer):
         mk, ml = _key(model_key)
         k, v = C.c_void_p(), C.c_void_p()

@@ -6,8 +6,9 @@ with continuar / encadenar, as capa_moe_en_gpu drives it
 methods, crates/soso-llm-core/src/gpu.rs:294-335, 380-426).
 
 The CPU side is the oracle's composition of the same layers (the decode
-tests' Model.cpu_step with MoE FFNs).  Bar: each token's hidden state within
-relative L2 1e-5, and the KV rows the device appended as close to the CPU's
+tests' Model.cpu_step with MoE FFNs).  Bar: each layer's routing of each
+token identical (the same experts in the same order, weights within relative
+L2 1e-5), each token's hidden state within relative L2 1e-5, and the KV rows the device appended as close to the CPU's
 f32 rows as soso's f32_to_f16 of those rows is, to 1e-5 relative L2, with
 more than 95 % of the f16 values equal to it (where the two f32 rows, equal
 to ~1e-6, straddle an f16 rounding point, or where a small element of a
@@ -94,7 +95,8 @@ def kv_rows_f16(gpu, layer, nkv, ctx, n):
 def test_moe_capa_chained_layers_match_cpu(gpu, orc):
     """Five tokens, each through layer 0 (output left pending: encadenar) and
     layer 1 (input the pending output: continuar), the norms and router sent
-    on each layer's first call only: hidden within 1e-5 (the CPU attending
+    on each layer's first call only: routing identical (weights within
+    1e-5), hidden within 1e-5 (the CPU attending
     to the device's f16 rows), the KV rows as close to the CPU's as soso's
     f16 rounding of them.  Then the same tokens with
     every layer's output brought down (no chaining) give the same bits, and a
@@ -117,6 +119,7 @@ def test_moe_capa_chained_layers_match_cpu(gpu, orc):
             assert np.array_equal(hid, xs[t])  # encadenar: hidden untouched
             assert gpu.moe_capa(st.capa(1, t, 1, ctx, theta, eps, True, False, t == 0), hid), gpu.last_error()
             assert not gpu.moe_pendiente(0, t, 1) and not gpu.moe_pendiente(1, t, 1)
+            routing = [gpu.moe_capa_routing(l, st.top_k) for l in range(st.L)]
             rows = {}
             for l in range(st.L):
                 kg, vg = kv_rows_f16(gpu, l, st.nkv, ctx, t + 1)
@@ -125,6 +128,10 @@ def test_moe_capa_chained_layers_match_cpu(gpu, orc):
             for l in range(st.L):
                 cpu_k[l].append(m.last_kv[0][l])
                 cpu_v[l].append(m.last_kv[1][l])
+            for l in range(st.L):
+                (gi, gw), (ri, rw) = routing[l], m.routing[l]
+                assert np.array_equal(gi, ri), (t, l, gi, ri)
+                assert orc.rel_l2(gw, rw) < TOL, (t, l, gw, rw)
             err = orc.rel_l2(hid, m.last_hidden)
             print(f"moe_capa token {t}: hidden rel_l2 {err:.3e}", flush=True)
             assert err < TOL, (t, err)
