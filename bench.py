@@ -51,14 +51,31 @@ def _capture(g, body):
     return gid
 
 
+# The GPU's clocks climb over the first milliseconds of load: a timed region
+# that starts on a rested GPU reads slower the shorter it is (measured 5-12 %
+# at 20 steps against 100-1000, headline matvec to 64-token matmul).  Every
+# timed region therefore starts behind at least SPIN_MS of untimed replays of
+# the same launches, still running when the timed ones are enqueued, so the
+# per-step figure is the steady state whatever `steps` is.
+SPIN_MS = 30.0
+
+
+def _spin(g, gid, replay_ms):
+    """Enqueues untimed replays of graph gid (one takes replay_ms) covering
+    SPIN_MS, without waiting for them.  Returns how many."""
+    reps = max(2, int(SPIN_MS / max(replay_ms, 1e-3)) + 1)
+    for _ in range(reps):
+        g.graph_launch(gid)
+    return reps
+
+
 def _timed_graph(g, calls, steps):
     """Captures `calls` (which issues `steps` steps) into one graph, replays it
-    once to warm it, then times one replay: HIP events on the library's
-    stream bracket exactly that replay's `steps` steps.  The timed replay and
-    its events are enqueued while an untimed replay still runs, so the graph
-    starts as soon as the stream reaches it and the host's submission latency
-    (a fixed cost per replay, not per step) stays out of the per-step figure
-    even at small `steps`.  Returns (ms per step between the events, host
+    once to warm it and once on an idle stream (the host wall figure), then
+    enqueues untimed replays covering SPIN_MS (_spin) and, behind them, the
+    timed replay between two HIP events on the library's stream: the events
+    bracket exactly that replay's `steps` steps, started while the GPU is
+    busy and its clocks up.  Returns (ms per step between the events, host
     wall ms per step of one replay on an idle stream)."""
     gid = _capture(g, calls)
     try:
@@ -68,7 +85,7 @@ def _timed_graph(g, calls, steps):
         g.graph_launch(gid)
         g.sync()
         t1 = time.perf_counter()
-        g.graph_launch(gid)  # keeps the stream busy while the timed replay is enqueued
+        _spin(g, gid, (t1 - t0) * 1e3)
         g.event_record(0)
         g.graph_launch(gid)
         g.event_record(1)
@@ -78,32 +95,47 @@ def _timed_graph(g, calls, steps):
     return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
 
 
-# Below this many timed steps a graph replay's own start (a few microseconds
-# on the GPU, measured 7.7-7.9 us per headline launch at 20 steps against 7.4 at
-# 1000) would weigh on the per-step figure: short windows launch their steps
-# directly, right behind untimed steps that keep the GPU busy up to the start
-# event (7.3 us per launch at 20 steps; at 1000, 7.5 eager against 7.4 from a
-# graph).  Either way the events bracket exactly the timed steps.
-GRAPH_MIN_STEPS = 200
+# A timed window carries a fixed cost of its own besides its steps: the two
+# event records and the restart of the stream behind them, measured 2-6 us
+# per window with direct launches and 6-13 us from a graph (Q4_K/Q8_0
+# matvecs, 20 and 50 steps against 1000, behind the spin-up).  At 20 steps of
+# 7 us that is 2-9 % of the per-step figure.  The single-launch matvecs are
+# therefore timed over at least MIN_TIMED launches (`timed_launches` in the
+# JSON line; `steps` stays the count asked for), where it is below 0.2 %.
+MIN_TIMED = 1000
+SPIN_LAUNCHES = 256  # launches in the spin-up graph of a direct-launch window
 
 
-def _timed_steps(g, launch, steps, lead):
-    """Times exactly `steps` steps (launch(i) issues step i): from
-    GRAPH_MIN_STEPS on one graph replay (_timed_graph), below it direct
-    launches enqueued right behind `lead` untimed ones.  Returns (ms per step
-    between the events, host wall ms per step)."""
-    if steps >= GRAPH_MIN_STEPS:
+def _timed_steps(g, launch, steps, eager=False):
+    """Times exactly `steps` steps (launch(i) issues step i), behind SPIN_MS
+    of untimed replays of the same launches: as one graph replay
+    (_timed_graph), or with eager (for tracers) as direct launches enqueued
+    while the spin-up replays still run.  Returns (ms per step between the
+    events, host wall ms per step of one replay or of the direct launches,
+    on an idle stream)."""
+    if not eager:
         return _timed_graph(g, lambda: [launch(i) for i in range(steps)], steps)
     g.sync()
-    for i in range(lead):
-        launch(i)
     t0 = time.perf_counter()
-    g.event_record(0)
     for i in range(steps):
         launch(i)
-    g.event_record(1)
     g.sync()
     t1 = time.perf_counter()
+    gid = _capture(g, lambda: [launch(i) for i in range(SPIN_LAUNCHES)])
+    try:
+        g.graph_launch(gid)
+        g.sync()
+        t2 = time.perf_counter()
+        g.graph_launch(gid)
+        g.sync()
+        _spin(g, gid, (time.perf_counter() - t2) * 1e3)
+        g.event_record(0)
+        for i in range(steps):
+            launch(i)
+        g.event_record(1)
+        g.sync()
+    finally:
+        g.graph_destroy(gid)
     return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
 
 
@@ -112,13 +144,12 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1, eager=False
 
     `copies` resident weights are rotated so HBM, not the MALL, serves them.
     The timed region is `steps` back-to-back launches on the library's stream
-    (one HIP graph from GRAPH_MIN_STEPS on, direct launches below it),
-    bracketed by HIP events recorded on that stream (_timed_steps): the
-    average is (event interval) / steps,
-    the same per-dispatch figure rocprofv3 --kernel-trace reports (profiles/
-    holds that cross-check).  eager=True launches the steps directly instead
-    (for counter and tracer runs).  Returns (ms_per_launch_events,
-    ms_per_launch_host_wall; None when eager)."""
+    (one HIP graph), behind untimed spin-up replays and bracketed by HIP
+    events recorded on that stream (_timed_steps): the average is (event
+    interval) / steps, the same per-dispatch figure rocprofv3 --kernel-trace
+    reports (profiles/ holds that cross-check).  eager=True launches the
+    steps directly (for counter and tracer runs).  Returns (ms_per_launch_events,
+    ms_per_launch_host_wall on an idle stream)."""
     keys = [f"bench.{dtype}.{rows}x{cols}.{i}" for i in range(copies)]
     for i, k in enumerate(keys):
         g.weight_synth(k, dtype, rows, cols, seed, 1000 + i)
@@ -129,14 +160,7 @@ def time_matvec(g, dtype, rows, cols, copies, steps, warmup, seed=1, eager=False
         for i in range(warmup):
             g.matvec_dev(keys[i % copies], x, y)
         g.sync()
-        calls = lambda: [g.matvec_dev(keys[i % copies], x, y) for i in range(steps)]
-        if eager:
-            g.event_record(0)
-            calls()
-            g.event_record(1)
-            g.sync()
-            return g.event_elapsed(0, 1) / steps, None
-        return _timed_steps(g, lambda i: g.matvec_dev(keys[i % copies], x, y), steps, max(warmup, 5))
+        return _timed_steps(g, lambda i: g.matvec_dev(keys[i % copies], x, y), steps, eager)
     finally:
         g.sync()
         g.dev_free(x)
@@ -859,13 +883,13 @@ def main():
         return
     if args.only:
         if args.only == "matvec":
-            ms, _ = time_matvec(g, Q4K, 14336, 4096, 16, args.steps, args.warmup, eager=args.eager)
+            ms, _ = time_matvec(g, Q4K, 14336, 4096, 16, max(args.steps, MIN_TIMED), args.warmup, eager=args.eager)
             res = {"q4_k_14336x4096_us": round(ms * 1e3, 3)}
         elif args.only == "q8_0":
-            ms, _ = time_matvec(g, Q8, 4096, 4096, 28, args.steps, args.warmup, eager=args.eager)
+            ms, _ = time_matvec(g, Q8, 4096, 4096, 28, max(args.steps, MIN_TIMED), args.warmup, eager=args.eager)
             res = {"q8_0_4096x4096_us": round(ms * 1e3, 3)}
         elif args.only == "down":
-            ms, _ = time_matvec(g, Q4K, 4096, 14336, 16, args.steps, args.warmup, eager=args.eager)
+            ms, _ = time_matvec(g, Q4K, 4096, 14336, 16, max(args.steps, MIN_TIMED), args.warmup, eager=args.eager)
             res = {"q4_k_down_4096x14336_us": round(ms * 1e3, 3)}
         elif args.only == "head":
             ms, _ = time_matvec(g, Q6K, 128256, 4096, 2, max(20, args.steps // 10), min(args.warmup, 10),
@@ -900,7 +924,7 @@ def main():
                 res[f"gdn_block_n{n}_GB_s"] = round(nb / (ms * 1e-3) / 1e9, 1)
         elif args.only == "readprobe":
             nb = 14336 * ROW_BYTES[Q4K](4096)  # the headline's weight bytes
-            small = time_read_probe(g, nb, 16, max(100, args.steps // 2), 20)
+            small = time_read_probe(g, nb, 16, MIN_TIMED // 2, 20)
             big = time_read_probe(g, 512 << 20, 2, 20, 4)
             res = {"read_33MB_us": {f"{v}{k} {w}x{t}": round(ms * 1e3, 3) for (v, k, w, t), ms in small.items()},
                    "read_512MB_us": {f"{v}{k} {w}x{t}": round(ms * 1e3, 3) for (v, k, w, t), ms in big.items()},
@@ -916,7 +940,8 @@ def main():
         return
     rows, cols = 14336, 4096
     nbytes = algo_bytes(Q4K, rows, cols)
-    ms, ms_wall = time_matvec(g, Q4K, rows, cols, 16, args.steps, args.warmup)
+    timed = max(args.steps, MIN_TIMED)
+    ms, ms_wall = time_matvec(g, Q4K, rows, cols, 16, timed, args.warmup)
     achieved = nbytes / (ms * 1e-3) / 1e9
     line = {
         "metric": "Q4_K matvec GB/s (% HBM peak) at 14336x4096; decode tok/s on 1 GPU",
@@ -924,6 +949,7 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
+        "timed_launches": timed,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
         "higher_is_better": True,
@@ -937,16 +963,15 @@ def main():
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": load_traffic("q4k_14336x4096"),
                      "kernel_us": round(ms * 1e3, 3), "host_wall_us_per_step": round(ms_wall * 1e3, 3),
                      "graph_single_launch_us": round(time_single_launch(g, Q4K, rows, cols) * 1e3, 3),
-                     "timed_as": (f"{args.steps} launches replayed from one graph" if args.steps >= GRAPH_MIN_STEPS
-                                  else f"{args.steps} launches issued directly behind {max(args.warmup, 5)} "
-                                       "untimed ones")},
+                     "timed_as": (f"{timed} launches ({args.steps} asked for, at least {MIN_TIMED}) replayed "
+                                  f"from one graph, behind {SPIN_MS:g} ms of untimed replays of the same launches")},
     }
     if not args.no_extra:
         extra = {}
         for name, dt, r, c, copies in (("q8_0_4096x4096", Q8, 4096, 4096, 28),
                                        ("q6_k_head_128256x4096", Q6K, 128256, 4096, 2),
                                        ("q4_k_down_4096x14336", Q4K, 4096, 14336, 16)):
-            steps = max(20, args.steps // (10 if dt == Q6K else 1))
+            steps = max(20, args.steps // 10) if dt == Q6K else max(args.steps, MIN_TIMED)
             k_, _ = time_matvec(g, dt, r, c, copies, steps, min(args.warmup, 10))
             b = algo_bytes(dt, r, c)
             extra[name] = {"us_kernel": round(k_ * 1e3, 3), "GB_s": round(b / (k_ * 1e-3) / 1e9, 1),
@@ -954,7 +979,7 @@ def main():
         # the same weight bytes read by a plain streaming kernel, best of its launch shapes:
         # the ceiling a dependent 33 MB launch can reach on this GPU
         nb = 14336 * ROW_BYTES[Q4K](4096)
-        rd = time_read_probe(g, nb, 16, max(100, args.steps // 5), 20)
+        rd = time_read_probe(g, nb, 16, MIN_TIMED // 2, 20)
         (bv, bk, bw, bt), best = min(rd.items(), key=lambda kv: kv[1])
         rb = read_probe_bytes(bv, nb)
         extra["plain_read_33MB"] = {"us_kernel": round(best * 1e3, 3), "GB_s": round(rb / (best * 1e-3) / 1e9, 1),
