@@ -103,14 +103,14 @@ def _timed_graph(g, calls, steps):
 # therefore timed over at least MIN_TIMED launches (`timed_launches` in the
 # JSON line; `steps` stays the count asked for), where it is below 0.2 %.
 MIN_TIMED = 1000
-SPIN_LAUNCHES = 256  # launches in the spin-up graph of a direct-launch window
+SPIN_LAUNCHES = 256  # at least this many direct spin-up launches (eager windows)
 
 
 def _timed_steps(g, launch, steps, eager=False):
     """Times exactly `steps` steps (launch(i) issues step i), behind SPIN_MS
-    of untimed replays of the same launches: as one graph replay
-    (_timed_graph), or with eager (for tracers) as direct launches enqueued
-    while the spin-up replays still run.  Returns (ms per step between the
+    of untimed work: as one graph replay behind replays of it (_timed_graph),
+    or with eager (for tracers and counter collectors) as direct launches
+    behind direct spin-up launches of the same steps.  Returns (ms per step between the
     events, host wall ms per step of one replay or of the direct launches,
     on an idle stream)."""
     if not eager:
@@ -121,21 +121,18 @@ def _timed_steps(g, launch, steps, eager=False):
         launch(i)
     g.sync()
     t1 = time.perf_counter()
-    gid = _capture(g, lambda: [launch(i) for i in range(SPIN_LAUNCHES)])
-    try:
-        g.graph_launch(gid)
-        g.sync()
-        t2 = time.perf_counter()
-        g.graph_launch(gid)
-        g.sync()
-        _spin(g, gid, (time.perf_counter() - t2) * 1e3)
-        g.event_record(0)
-        for i in range(steps):
-            launch(i)
-        g.event_record(1)
-        g.sync()
-    finally:
-        g.graph_destroy(gid)
+    # the spin-up as direct launches too (no graph: counter collectors take
+    # graph replays badly), issued for SPIN_MS of host time and at least
+    # SPIN_LAUNCHES launches; the timed launches queue behind them
+    i, t2 = 0, time.perf_counter()
+    while i < SPIN_LAUNCHES or (time.perf_counter() - t2) * 1e3 < SPIN_MS:
+        launch(i)
+        i += 1
+    g.event_record(0)
+    for i in range(steps):
+        launch(i)
+    g.event_record(1)
+    g.sync()
     return g.event_elapsed(0, 1) / steps, (t1 - t0) * 1e3 / steps
 
 
