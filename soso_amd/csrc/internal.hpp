@@ -47,8 +47,13 @@ struct Weight {
     size_t bytes = 0;
     uint8_t dtype = 0;
     size_t rows = 0, cols = 0;
+    // columns of the packed copy the kernels walk when they differ from cols:
+    // Q8_0 rows of an odd number of 32-element blocks get a zero block (scale
+    // 0, codes 0) so that 64-element units tile them; 0 = cols
+    size_t kcols = 0;
     bool declined = false;
 };
+inline size_t weight_kcols(const Weight &w) { return w.kcols ? w.kcols : w.cols; }
 
 // A MoE FFN registered for the device-resident path (soso_hip_moe_register).
 struct MoeLayer {
@@ -211,6 +216,10 @@ struct MvEpi {
 // packed layouts (k_matvec.hip)
 size_t packed_row_stride(uint8_t dtype, size_t cols);
 bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols);
+// shapes a weight may be uploaded with (packed_shape_ok, or Q8_0 rows of an
+// odd number of blocks, padded to kernel_cols)
+bool upload_shape_ok(uint8_t dtype, size_t rows, size_t cols);
+size_t kernel_cols(uint8_t dtype, size_t cols);
 
 // launchers (k_matvec.hip)
 int repack_weight(soso_hip *h, uint8_t dtype, const void *raw_dev, void *packed_dev, size_t rows, size_t cols);

@@ -53,6 +53,21 @@ size_t packed_row_stride(uint8_t dtype, size_t cols)
     }
 }
 
+// Q8_0 rows of an odd number of blocks (soso accepts any multiple of 32,
+// dequant.rs:53-68) are stored with one zero block appended: its scale and
+// codes are 0, so it adds exactly 0 to every sum, and the 64-element units of
+// the layout tile the row.  The x a kernel reads over such a row is padded
+// with zeros to match (launch_matvec).
+size_t kernel_cols(uint8_t dtype, size_t cols)
+{
+    return dtype == SOSO_HIP_DTYPE_Q8_0 && cols % 64 == 32 ? cols + 32 : cols;
+}
+
+bool upload_shape_ok(uint8_t dtype, size_t rows, size_t cols)
+{
+    return packed_shape_ok(dtype, rows, kernel_cols(dtype, cols)) && (dtype != SOSO_HIP_DTYPE_Q8_0 || cols % 32 == 0);
+}
+
 // Shapes the quantized kernels accept: the 64-element unit must tile a row.
 bool packed_shape_ok(uint8_t dtype, size_t rows, size_t cols)
 {
@@ -82,23 +97,30 @@ __global__ void repack_q4k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
     }
 }
 
-__global__ void repack_q80(const uint8_t *__restrict__ raw, uint8_t *__restrict__ out, int rows, int nb,
+// raw rows of nbs blocks -> packed rows of nb blocks (nb = nbs, or nbs + 1:
+// the appended block is all zeros)
+__global__ void repack_q80(const uint8_t *__restrict__ raw, uint8_t *__restrict__ out, int rows, int nbs, int nb,
                            int stride)
 {
     long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (long)rows * nb) return;
     int r = (int)(t / nb), b = (int)(t % nb);
-    const uint32_t *src = (const uint32_t *)(raw + (size_t)r * nb * 36 + (size_t)b * 36); // 4-byte aligned
+    uint32_t v[9] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    if (b < nbs) {
+        const uint32_t *src = (const uint32_t *)(raw + (size_t)r * nbs * 36 + (size_t)b * 36); // 4-byte aligned
+#pragma unroll
+        for (int i = 0; i < 9; i++) v[i] = src[i];
+    }
     uint8_t *row = out + (size_t)r * stride;
     int sreg = (4 * nb + 15) & ~15, U = nb / 2;
-    ((uint32_t *)row)[b] = src[0];
+    ((uint32_t *)row)[b] = v[0];
     int u = b >> 1, half = b & 1;
     uint32_t *pl0 = (uint32_t *)(row + sreg + (size_t)(2 * half) * 16 * U + 16 * u);
     uint32_t *pl1 = (uint32_t *)(row + sreg + (size_t)(2 * half + 1) * 16 * U + 16 * u);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        pl0[i] = src[1 + i];
-        pl1[i] = src[5 + i];
+        pl0[i] = v[1 + i];
+        pl1[i] = v[5 + i];
     }
 }
 
@@ -139,11 +161,14 @@ int repack_weight(soso_hip *h, uint8_t dtype, const void *raw, void *packed, siz
         repack_q4k<<<(unsigned)((rows * nb + T - 1) / T), T, 0, h->stream>>>((const uint8_t *)raw, (uint8_t *)packed,
                                                                               (int)rows, (int)nb);
         break;
-    case SOSO_HIP_DTYPE_Q8_0:
-        nb = cols / 32;
+    case SOSO_HIP_DTYPE_Q8_0: {
+        const size_t kc = kernel_cols(dtype, cols);
+        nb = kc / 32;
         repack_q80<<<(unsigned)((rows * nb + T - 1) / T), T, 0, h->stream>>>(
-            (const uint8_t *)raw, (uint8_t *)packed, (int)rows, (int)nb, (int)packed_row_stride(dtype, cols));
+            (const uint8_t *)raw, (uint8_t *)packed, (int)rows, (int)(cols / 32), (int)nb,
+            (int)packed_row_stride(dtype, kc));
         break;
+    }
     case SOSO_HIP_DTYPE_Q6_K:
         nb = cols / 256;
         repack_q6k<<<(unsigned)((rows * nb + T - 1) / T), T, 0, h->stream>>>(
@@ -581,13 +606,14 @@ static void launch_split(soso_hip *h, int grid, int threads, size_t lds, const u
 template <int FMT>
 static int launch_fmt(soso_hip *h, const Weight &w, const float *x, float *y)
 {
-    const int rows = (int)w.rows, cols = (int)w.cols, U = cols / 64;
-    const size_t stride = packed_row_stride(w.dtype, w.cols);
+    const size_t kc = weight_kcols(w);
+    const int rows = (int)w.rows, cols = (int)kc, U = cols / 64;
+    const size_t stride = packed_row_stride(w.dtype, kc);
     const int S = (U + 63) / 64;
     if (S > 8) return set_err(h, SOSO_HIP_DECLINED, "matvec: rows wider than 512 units");
     const int gpw = 8 / S;                 // groups of S wavefronts per workgroup (<= 512 threads)
     const int threads = 64 * S * gpw;
-    const size_t lds = stage_lds_bytes_o(w.cols) + (S > 1 ? (size_t)gpw * COMBINE_CH * S * 4 : 0);
+    const size_t lds = stage_lds_bytes_o(kc) + (S > 1 ? (size_t)gpw * COMBINE_CH * S * 4 : 0);
     if (lds > h->max_lds) return set_err(h, SOSO_HIP_DECLINED, "matvec: x does not fit in LDS");
     const int per_cu = 1; // one 512-thread workgroup per CU (two measured slower for these shapes)
     const uint8_t *W = (const uint8_t *)w.dev;
@@ -748,6 +774,7 @@ const char *matvec_ex_unsupported(const soso_hip *h, uint8_t dtype, size_t rows,
 
 int launch_matvec_ex(soso_hip *h, const Weight &w, const MvIn &in, float *y, const MvEpi &ep, int xs, int epi)
 {
+    if (weight_kcols(w) != w.cols) return set_err(h, SOSO_HIP_DECLINED, "matvec_ex: padded Q8_0 rows not built here");
     ExPlan p;
     if (const char *why = plan_matvec_ex(h, w.dtype, w.rows, w.cols, xs, epi, p)) return set_err(h, SOSO_HIP_DECLINED, why);
     const int rows = (int)w.rows, cols = (int)w.cols;
@@ -793,11 +820,12 @@ constexpr int TOK_NT = 2;
 template <int FMT>
 static int launch_tok_fmt(soso_hip *h, const Weight &w, const float *x, float *y, size_t n)
 {
-    const int rows = (int)w.rows, cols = (int)w.cols, U = cols / 64;
-    const size_t stride = packed_row_stride(w.dtype, w.cols);
+    const size_t kc = weight_kcols(w);
+    const int rows = (int)w.rows, cols = (int)kc, U = cols / 64;
+    const size_t stride = packed_row_stride(w.dtype, kc);
     const int LPR = U <= 1 ? 1 : U <= 2 ? 2 : U <= 4 ? 4 : U <= 8 ? 8 : U <= 16 ? 16 : U <= 32 ? 32 : 64;
     const int RW = 64 / LPR, passes = (rows + RW - 1) / RW;
-    const size_t sl = (stage_lds_bytes_o(w.cols) + 15) & ~(size_t)15;
+    const size_t sl = (stage_lds_bytes_o(kc) + 15) & ~(size_t)15;
     // tokens per launch: as many as LDS stages, at most 8 row-group wavefronts x TOK_NT
     const size_t per = std::min<size_t>(std::min<size_t>(h->max_lds / sl, 8 * TOK_NT), n);
     for (size_t t0 = 0; t0 < n; t0 += per) {
@@ -813,7 +841,7 @@ static int launch_tok_fmt(soso_hip *h, const Weight &w, const float *x, float *y
         if (!interleave_fits(passes, 1, grid * rgw, (size_t)RW * stride))
             return set_err(h, SOSO_HIP_DECLINED, "matmul: matrix too large for the batched kernel");
         const size_t lds = sl * (size_t)m;
-        const float *xt = x + t0 * w.cols;
+        const float *xt = x + t0 * kc;
         float *yt = y + t0 * w.rows;
 #define TOK_CASE(LP)                                                                                                   \
     case LP:                                                                                                          \
@@ -830,12 +858,36 @@ static int launch_tok_fmt(soso_hip *h, const Weight &w, const float *x, float *y
     return SOSO_HIP_OK;
 }
 
+// x rows of `cols` floats -> rows of `kcols` with zeros after each (the
+// columns of a weight's appended zero block)
+__global__ void k_pad_rows(const float *__restrict__ x, float *__restrict__ out, int cols, int kcols, long total)
+{
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (long)gridDim.x * blockDim.x) {
+        const long t = i / kcols;
+        const int c = (int)(i % kcols);
+        out[i] = c < cols ? x[t * cols + c] : 0.0f;
+    }
+}
+
 int launch_matvec(soso_hip *h, const Weight &w, const float *x, float *y, size_t n)
 {
-    if (n >= MATMUL_MFMA_MIN && mfma_shape_ok(w.dtype, w.rows, w.cols)) return launch_mfma_matmul(h, w, x, n, y);
+    const size_t kc = weight_kcols(w);
+    if (kc != w.cols) {
+        // a padded weight reads padded x (scratch slot 13; under graph capture
+        // only once an earlier call has grown it)
+        float *xp = (float *)scratch_get(h, 13, n * kc * 4);
+        if (!xp) return set_err(h, SOSO_HIP_ERR_NOMEM, "matvec: padded x");
+        const long total = (long)(n * kc);
+        k_pad_rows<<<(unsigned)std::min<long>((total + 255) / 256, 4096), 256, 0, h->stream>>>(x, xp, (int)w.cols,
+                                                                                              (int)kc, total);
+        const int rc = hip_check(h, hipGetLastError(), "pad x launch");
+        if (rc != SOSO_HIP_OK) return rc;
+        x = xp;
+    }
+    if (n >= MATMUL_MFMA_MIN && mfma_shape_ok(w.dtype, w.rows, kc)) return launch_mfma_matmul(h, w, x, n, y);
     // several tokens, rows of at most 64 units: each row read once per launch
-    if (n > 1 && w.cols <= 4096 && w.dtype != SOSO_HIP_DTYPE_F32 &&
-        (stage_lds_bytes_o(w.cols) + 15) / 16 * 16 * 2 <= h->max_lds) {
+    if (n > 1 && kc <= 4096 && w.dtype != SOSO_HIP_DTYPE_F32 &&
+        (stage_lds_bytes_o(kc) + 15) / 16 * 16 * 2 <= h->max_lds) {
         switch (w.dtype) {
         case SOSO_HIP_DTYPE_Q4_K: return launch_tok_fmt<FMT_Q4K>(h, w, x, y, n);
         case SOSO_HIP_DTYPE_Q8_0: return launch_tok_fmt<FMT_Q80>(h, w, x, y, n);
@@ -844,7 +896,7 @@ int launch_matvec(soso_hip *h, const Weight &w, const float *x, float *y, size_t
         }
     }
     for (size_t t = 0; t < n; t++) {
-        const float *xt = x + t * w.cols;
+        const float *xt = x + t * kc;
         float *yt = y + t * w.rows;
         int rc;
         switch (w.dtype) {
@@ -901,10 +953,13 @@ __global__ void dq_q4k(const uint8_t *__restrict__ W, float *__restrict__ out, i
     }
 }
 
-__global__ void dq_q80(const uint8_t *__restrict__ W, float *__restrict__ out, int rows, int cols, int stride)
+// cols: the caller's columns (the output's row length); kcols: the packed
+// layout's (cols, or cols + 32 with an appended zero block)
+__global__ void dq_q80(const uint8_t *__restrict__ W, float *__restrict__ out, int rows, int cols, int kcols,
+                       int stride)
 {
     long t = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    const int nb = cols >> 5, U = cols >> 6, sreg = (4 * nb + 15) & ~15;
+    const int nb = cols >> 5, U = kcols >> 6, sreg = (4 * (kcols >> 5) + 15) & ~15;
     if (t >= (long)rows * nb) return;
     const int r = (int)(t / nb), b = (int)(t % nb), u = b >> 1, half = b & 1;
     const uint8_t *Wr = W + (size_t)r * stride;
@@ -944,8 +999,8 @@ __global__ void dq_q6k(const uint8_t *__restrict__ W, float *__restrict__ out, i
 
 int launch_dequant(soso_hip *h, const Weight &w, float *out)
 {
-    const int T = 256, rows = (int)w.rows, cols = (int)w.cols;
-    const int stride = (int)packed_row_stride(w.dtype, w.cols);
+    const int T = 256, rows = (int)w.rows, cols = (int)w.cols, kcols = (int)weight_kcols(w);
+    const int stride = (int)packed_row_stride(w.dtype, kcols);
     long n;
     switch (w.dtype) {
     case SOSO_HIP_DTYPE_Q4_K:
@@ -954,7 +1009,8 @@ int launch_dequant(soso_hip *h, const Weight &w, float *out)
         break;
     case SOSO_HIP_DTYPE_Q8_0:
         n = (long)rows * (cols / 32);
-        dq_q80<<<(unsigned)((n + T - 1) / T), T, 0, h->stream>>>((const uint8_t *)w.dev, out, rows, cols, stride);
+        dq_q80<<<(unsigned)((n + T - 1) / T), T, 0, h->stream>>>((const uint8_t *)w.dev, out, rows, cols, kcols,
+                                                                 stride);
         break;
     case SOSO_HIP_DTYPE_Q6_K:
         n = (long)rows * (cols / 64);

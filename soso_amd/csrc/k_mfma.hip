@@ -974,13 +974,14 @@ bool mfma_moe_scan_ok(size_t n, size_t top_k, size_t n_groups, uint8_t dt_gu, ui
 template <int NW, int MT>
 static void mfma_dense(soso_hip *h, const Weight &w, const float *x, size_t n, float *y, int kc, unsigned grid)
 {
-    const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc), stride = packed_row_stride(w.dtype, w.cols);
+    const size_t kcols = weight_kcols(w);
+    const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc), stride = packed_row_stride(w.dtype, kcols);
     if (w.dtype == SOSO_HIP_DTYPE_Q8_0)
         k_mfma_q80<MT, NW><<<grid, 64 * NW, lds, h->stream>>>((const uint8_t *)w.dev, stride, (int)w.rows,
-                                                              (int)w.cols, x, (int)n, kc, y);
+                                                              (int)kcols, x, (int)n, kc, y);
     else
         k_mfma_q4k<1, MT, MF_LA1, false, NW><<<grid, 64 * NW, lds, h->stream>>>(
-            nullptr, nullptr, (const uint8_t *)w.dev, stride, (int)w.rows, (int)w.cols, x, 1, nullptr, nullptr,
+            nullptr, nullptr, (const uint8_t *)w.dev, stride, (int)w.rows, (int)kcols, x, 1, nullptr, nullptr,
             nullptr, (int)n, kc, y, nullptr, 0);
 }
 
@@ -1004,7 +1005,8 @@ static const int MF_DENSE[9][2] = {{4, 1}, {8, 1}, {4, 2}, {8, 2}, {16, 1}, {4, 
 
 int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
 {
-    if (!mfma_shape_ok(w.dtype, w.rows, w.cols) || n == 0 || n > (1u << 20))
+    const size_t kcols = weight_kcols(w);
+    if (!mfma_shape_ok(w.dtype, w.rows, kcols) || n == 0 || n > (1u << 20))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
     const size_t cu = (size_t)h->num_cu;
     auto groups = [&](int nw, int mt) { return (w.rows + 16 * nw - 1) / (16 * nw) * ((n + 4 * mt - 1) / (4 * mt)); };
@@ -1019,7 +1021,7 @@ int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, f
                 pick = i;
     const int nw = MF_DENSE[pick][0], mt = MF_DENSE[pick][1];
     const size_t grid = groups(nw, mt);
-    const int kc = mf_kc(h, w.cols, 4 * mt, grid > cu ? h->max_lds / 2 : h->max_lds);
+    const int kc = mf_kc(h, kcols, 4 * mt, grid > cu ? h->max_lds / 2 : h->max_lds);
     const unsigned gu = (unsigned)grid;
     switch (nw * 8 + mt) {
     case 4 * 8 + 1: mfma_dense<4, 1>(h, w, x, n, y, kc, gu); break;

@@ -140,14 +140,16 @@ int register_weight(soso_hip *h, const std::string &key, const void *raw, bool r
     w.dtype = dtype;
     w.rows = rows;
     w.cols = cols;
+    const size_t kc = kernel_cols(dtype, cols);
+    w.kcols = kc != cols ? kc : 0;
     const size_t rb = fmt_row_bytes(dtype, cols);
-    if (!dtype_ok(dtype) || !packed_shape_ok(dtype, rows, cols) || rb == 0 || w_len != rows * rb || !raw) {
+    if (!dtype_ok(dtype) || !upload_shape_ok(dtype, rows, cols) || rb == 0 || w_len != rows * rb || !raw) {
         w.declined = true;
         h->weights[key] = w;
         h->stats.weights_declined++;
         return set_err(h, SOSO_HIP_DECLINED, "weight " + key + ": dtype/shape not handled here");
     }
-    const size_t bytes = rows * packed_row_stride(dtype, cols);
+    const size_t bytes = rows * packed_row_stride(dtype, kc);
     if (h->used + bytes > h->budget) {
         w.declined = true;
         h->weights[key] = w;
@@ -612,7 +614,7 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
             }
             int r = get_weight(h, x.keys[k], x.key_lens[k], x.w[k], x.w_len[k], x.dtype[k], dims[k][0], dims[k][1], &wt);
             if (r < 0) return r;
-            if (r != SOSO_HIP_OK || wt->dtype == SOSO_HIP_DTYPE_F32) good = false;
+            if (r != SOSO_HIP_OK || wt->dtype == SOSO_HIP_DTYPE_F32 || weight_kcols(*wt) != wt->cols) good = false;
             else wts[3 * e + k] = wt;
         }
         if (good) {
@@ -795,7 +797,8 @@ static int moe_register_impl(soso_hip *h, const char *layer_key, size_t layer_ke
     for (size_t e = 0; e < n_exp; e++)
         for (int k = 0; k < 3; k++) {
             const Weight *w = find_weight(h, expert_keys[3 * e + k], expert_key_lens[3 * e + k]);
-            if (!w || w->rows != dims[k][0] || w->cols != dims[k][1] || w->dtype == SOSO_HIP_DTYPE_F32)
+            if (!w || w->rows != dims[k][0] || w->cols != dims[k][1] || weight_kcols(*w) != w->cols ||
+                w->dtype == SOSO_HIP_DTYPE_F32)
                 return set_err(h, SOSO_HIP_DECLINED, "moe_register: expert matrix missing or of the wrong shape");
             const uint8_t want = k < 2 ? m.dt_gu : m.dt_down;
             if (want && w->dtype != want) return set_err(h, SOSO_HIP_DECLINED, "moe_register: mixed expert dtypes");
@@ -979,7 +982,10 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     const size_t kpl = m.qk_norm ? 11 : 9;      // keys per layer
     auto get = [&](size_t i, size_t rows, size_t cols, bool f32, const Weight **out) -> bool {
         const Weight *w = find_weight(h, keys[i], key_lens[i]);
-        if (!w || w->rows != rows || w->cols != cols || (f32 != (w->dtype == SOSO_HIP_DTYPE_F32))) return false;
+        // (a padded Q8_0 copy is for launch_matvec's callers only)
+        if (!w || w->rows != rows || w->cols != cols || weight_kcols(*w) != cols ||
+            (f32 != (w->dtype == SOSO_HIP_DTYPE_F32)))
+            return false;
         *out = w;
         return true;
     };

@@ -53,6 +53,8 @@ def test_synth_device_equals_host(gpu, orc, dtype, rows, cols):
 
 @pytest.mark.parametrize("dtype,rows,cols", [
     (Q8, 4096, 4096), (Q4K, 14336, 4096), (Q6K, 2048, 4096), (Q4K, 13, 768), (Q8, 3, 64), (Q6K, 5, 14336),
+    # Q8_0 rows of an odd number of blocks (stored with a zero block appended)
+    (Q8, 5, 96), (Q8, 300, 4064),
 ])
 def test_dequant_bit_exact(gpu, orc, dtype, rows, cols):
     w = orc.synth(dtype, rows, cols, 5, 1)
@@ -78,6 +80,9 @@ def test_dequant_bit_exact(gpu, orc, dtype, rows, cols):
     (Q4K, 700, 8192), (Q8, 333, 12288), (Q6K, 257, 16384), (Q4K, 65, 12544),
     # more row passes per group than one LDS combine round holds
     (Q4K, 33000, 16384),
+    # Q8_0 rows of an odd number of 32-element blocks (soso accepts any multiple of 32): a zero block
+    # appended to each row and zeros after x; one wavefront per row, and rows split over 4
+    (Q8, 7, 96), (Q8, 513, 4064), (Q8, 301, 14304),
 ])
 def test_matvec_parity(gpu, orc, dtype, rows, cols):
     w = orc.synth(dtype, rows, cols, 21, 4)
@@ -245,6 +250,51 @@ def test_declines_follow_the_trait(gpu, orc):
     assert not gpu.matvec("absent", None, Q4K, 4, 256, x, y)
     st = gpu.stats()
     assert st["weights_declined"] >= 2 and st["launches"] >= 1
+
+
+@pytest.mark.parametrize("cols", [96, 4064])
+def test_q8_0_odd_block_rows_every_entry(gpu, orc, cols):
+    """Q8_0 rows of an odd number of blocks (dequant.rs:53-68 accepts any
+    multiple of 32) through every entry that takes a host or device x: matmul
+    on the batched vector kernel (3 tokens) and, at 4064 columns, on the
+    matrix cores (20 tokens); matvec_lote beside an even-width op; the device
+    entry matvec_dev.  Each within 1e-5 of the f64 brute force; the device
+    entry gives the host entry's bits."""
+    rows = 257
+    w = orc.synth(Q8, rows, cols, 61, cols)
+    key = f"q8odd.{cols}"
+    try:
+        for n in ((3, 20) if cols == 4064 else (3,)):
+            xs = orc.normal(n * cols, 1.0, 62, n).reshape(n, cols)
+            out = np.full(n * rows, np.nan, np.float32)
+            assert gpu.matmul(key, w, Q8, rows, cols, n, xs, out), gpu.last_error()
+            out = out.reshape(n, rows)
+            for j in range(n):
+                ref = orc.matvec_f64(Q8, w, rows, cols, xs[j])
+                assert orc.rel_l2(out[j], ref) < TOL, (n, j, orc.rel_l2(out[j], ref))
+        x = orc.normal(cols, 1.0, 63, 1)
+        w2 = orc.synth(Q8, 64, 512, 64, 1)
+        x2 = orc.normal(512, 1.0, 64, 2)
+        ops = [dict(key=key, w=w, dtype=Q8, rows=rows, cols=cols, x=x, out=np.zeros(rows, np.float32)),
+               dict(key=key + ".even", w=w2, dtype=Q8, rows=64, cols=512, x=x2, out=np.zeros(64, np.float32))]
+        hecho = [False, False]
+        assert gpu.matvec_lote(ops, hecho) == 1 and hecho == [True, True]  # 1: every op ran
+        assert orc.rel_l2(ops[0]["out"], orc.matvec_f64(Q8, w, rows, cols, x)) < TOL
+        assert orc.rel_l2(ops[1]["out"], orc.matvec_f64(Q8, w2, 64, 512, x2)) < TOL
+        host = run_matvec(gpu, key, Q8, w, rows, cols, x)
+        xd, yd = gpu.dev_alloc(cols * 4), gpu.dev_alloc(rows * 4)
+        try:
+            gpu.h2d(xd, x)
+            gpu.matvec_dev(key, xd, yd)
+            gpu.sync()
+            dev = gpu.d2h(yd, (rows,), np.float32)
+        finally:
+            gpu.dev_free(xd)
+            gpu.dev_free(yd)
+        assert np.array_equal(dev.view(np.uint32), host.view(np.uint32))
+    finally:
+        gpu.weight_drop(key)
+        gpu.weight_drop(key + ".even")
 
 
 def test_matvec_lote(gpu, orc):
