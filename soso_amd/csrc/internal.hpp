@@ -145,7 +145,7 @@ struct soso_hip {
     // the scratch pointers it was captured with, so a slot outgrown while any
     // graph exists is retired, not freed: retired buffers are freed once no
     // graph is left (graph_destroy) or with the handle.
-    static constexpr int N_SCRATCH = 16;
+    static constexpr int N_SCRATCH = 17;
     void *scratch[N_SCRATCH] = {};
     size_t scratch_cap[N_SCRATCH] = {};
     std::vector<void *> retired;

@@ -57,8 +57,8 @@ constexpr int MF_NW_MAX = 16;
 // leave the 8-byte digit accesses of every other token misaligned when kc / 256
 // is odd, e.g. the 768 columns of the MoE down projection: measured twice as
 // slow).
-__host__ __device__ inline int mf_mask_off(int kc) { return (kc / 32 * 100 + kc / 256 * 4 + 15) & ~15; }
-__host__ __device__ inline int mf_tok_bytes(int kc)
+__host__ __device__ constexpr inline int mf_mask_off(int kc) { return (kc / 32 * 100 + kc / 256 * 4 + 15) & ~15; }
+__host__ __device__ constexpr inline int mf_tok_bytes(int kc)
 {
     return (mf_mask_off(kc) + kc / 8 + 15) & ~15;
 }
@@ -452,7 +452,10 @@ __device__ int mf_scan_slots(const int32_t *__restrict__ sidx, int nslots, int e
 // (MoE), or dense_n > 0 tokens of one dense product (slot = token).  Item:
 // blockIdx.x = a * nblk + row block (MoE), or row block + nblk * token round
 // (dense).  Slot s reads x = xs + (s / xdiv) * cols and writes out[s * rows + r].
-template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW, bool SCAN = false>
+// FULL (dense products whose token count is a multiple of 4 MT): every round
+// holds 4 MT tokens, so the per-tile checks compile away and the A operand is
+// loaded by every lane (the zero-pad digit lanes read digit 2 and select 0).
+template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW, bool SCAN = false, bool FULL = false>
 __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 : 4) : 1) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB,
                                                   const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
@@ -521,8 +524,9 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
     // A operand of this lane: token (nl / 4) of a tile, digit nl % 4, bytes 8g .. 8g + 7
     const int a_tok = nl >> 2, a_dig = nl & 3;
 
+    const int a_dg = a_dig < 3 ? a_dig : 2; // FULL: the pad lanes' (discarded) digit
     for (int t0 = t_first; t0 < ne; t0 += t_step) {
-        const int nt = min(TR, ne - t0);
+        const int nt = FULL ? TR : min(TR, ne - t0);
         __syncthreads(); // the previous round's readers of slot_s and LDS are done
         if ((int)threadIdx.x < nt)
             slot_s[threadIdx.x] = SCAN ? scan_s[t0 + threadIdx.x]
@@ -629,7 +633,13 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
                         // A: token mt*4 + a_tok, digit a_dig (3: zero), elements 8g..8g+7
                         const int ta = mt * 4 + a_tok;
                         mf_v4i xa = mf_v4i{0, 0, 0, 0};
-                        if (a_dig < 3 && ta < nt) {
+                        if constexpr (FULL) {
+                            const uint8_t *tp = lds + (size_t)ta * tb;
+                            const uint2 u0 = *(const uint2 *)(tp + ((sbl8 + j0) * 3 + a_dg) * 32 + 8 * g);
+                            const uint2 u1 = *(const uint2 *)(tp + ((sbl8 + j1) * 3 + a_dg) * 32 + 8 * g);
+                            const bool z = a_dig == 3;
+                            xa = mf_v4i{z ? 0 : (int)u0.x, z ? 0 : (int)u0.y, z ? 0 : (int)u1.x, z ? 0 : (int)u1.y};
+                        } else if (a_dig < 3 && ta < nt) {
                             const uint8_t *tp = lds + (size_t)ta * tb;
                             const uint2 u0 = *(const uint2 *)(tp + ((sbl8 + j0) * 3 + a_dig) * 32 + 8 * g);
                             const uint2 u1 = *(const uint2 *)(tp + ((sbl8 + j1) * 3 + a_dig) * 32 + 8 * g);
@@ -739,6 +749,260 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
             }
         }
     }
+}
+
+// ---------------------------------------------------------------------------
+// Dense Q4_K products of many tokens (matmul with a token count that is a
+// multiple of 16): x staged once per call, the workgroups' rounds always full.
+//
+// k_mfma_q4k stages its round's tokens itself, so every row block converts
+// the same x again (14336 x 4096 at 64 tokens: 56 row blocks x 4 rounds, about
+// 1,000 of its 7,100 VALU instructions per wavefront), and its code carries the
+// checks of partial rounds and MoE token lists.  Here k_mm_stage converts the
+// n rows of x once into the layout mf_stage writes (the whole row as one
+// chunk, token t at t * mf_tok_bytes(cols)), and each workgroup of k_mm_q4k
+// copies the stretch of its chunk from there into LDS (four contiguous
+// regions per token: digits, sub-block sums, 2^-e per super-block, outlier
+// mask).  Arithmetic, operands and the order of every sum are k_mfma_q4k's
+// (the outliers' corrections, where a token has some, join after each
+// staged chunk, whose width may differ from k_mfma_q4k's).
+// ---------------------------------------------------------------------------
+
+// One wavefront per 512 columns (64 chunks: two super-blocks, the lanes of each
+// 128-element block together) of one token; the outlier search as mf_stage's.
+__global__ void __launch_bounds__(256) k_mm_stage(const float *__restrict__ x, int n, int cols,
+                                                  uint8_t *__restrict__ xg)
+{
+    const int lane = threadIdx.x & 63;
+    const int gw = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int wpt = (cols + 511) / 512, nch = cols >> 3;
+    const int t = gw / wpt, c = (gw % wpt) * 64 + lane;
+    if (t >= n) return; // uniform per wavefront; no barriers here
+    const bool valid = c < nch;
+    float4 v0 = make_float4(0.f, 0.f, 0.f, 0.f), v1 = v0;
+    if (valid) {
+        const float4 *x4 = (const float4 *)(x + (size_t)t * cols) + 2 * c;
+        v0 = x4[0];
+        v1 = x4[1];
+    }
+    uint8_t *tp = xg + (size_t)t * mf_tok_bytes(cols);
+    float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                     fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+    const float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+    if (sm != sm) mx = INFINITY; // a NaN element: the super-block is non-finite
+    float q = fmaxf(mx, dpp_f<0xB1>(mx));
+    q = fmaxf(q, dpp_f<0x4E>(q));
+    const float hq = fmaxf(q, dpp_f<0x141>(q));
+    const float m1 = fmaxf(hq, dpp_f<0x140>(hq));
+    float qn = fminf(q, dpp_f<0x141>(q));
+    qn = fminf(qn, dpp_f<0x140>(qn));
+    if (__builtin_expect(__ballot(m1 > 16.0f * qn) == 0, 1)) mf_put(v0, v1, m1, sm, tp, c, cols, valid);
+    else (void)mf_chunk<false>(v0, v1, tp, c, cols, valid);
+}
+
+// Copies columns k0 .. k0 + KC of tokens t0 .. t0 + TR - 1 from the staged rows
+// (xg, mf_tok_bytes(cols) bytes per token) into LDS (mf_stage's chunk layout,
+// mf_tok_bytes(KC) per token); a thread that copies a nonzero outlier mask word
+// writes seq into *oflag.  cols, k0 and KC are multiples of 256, so every region
+// but the 2^-e one moves in 16-byte words: MB of them per thread are requested
+// before any is stored, so a batch costs one round trip.
+template <int KC, int TR, int NT>
+__device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict__ xg, int t0, int cols, int k0,
+                                        int *oflag, int seq)
+{
+    constexpr int tb = mf_tok_bytes(KC), DW = 3 * KC / 16, SW = KC / 128, MW = KC / 128, PW = KC / 256;
+    constexpr int PT = DW + SW + MW, TOT = TR * PT, MB = 4;
+    const int tbf = mf_tok_bytes(cols);
+    const int dsrc = (k0 >> 5) * 96, ssrc = (cols >> 5) * 96 + (k0 >> 3), psrc = (cols >> 5) * 100 + (k0 >> 6),
+              msrc = mf_mask_off(cols) + (k0 >> 3);
+    // word w of a token: its source and LDS offsets
+    auto offs = [&](int w, int &src, int &dst) {
+        if (w < DW) {
+            src = dsrc + 16 * w;
+            dst = 16 * w;
+        } else if (w < DW + SW) {
+            src = ssrc + 16 * (w - DW);
+            dst = (KC >> 5) * 96 + 16 * (w - DW);
+        } else {
+            src = msrc + 16 * (w - DW - SW);
+            dst = mf_mask_off(KC) + 16 * (w - DW - SW);
+        }
+    };
+    bool any = false;
+    for (int i0 = 0; i0 < TOT; i0 += MB * NT) {
+        uint4 v[MB];
+#pragma unroll
+        for (int k = 0; k < MB; k++) {
+            const int i = i0 + k * NT + (int)threadIdx.x;
+            v[k] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < TOT) {
+                int src, dst;
+                offs(i % PT, src, dst);
+                v[k] = *(const uint4 *)(xg + (size_t)(t0 + i / PT) * tbf + src);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < MB; k++) {
+            const int i = i0 + k * NT + (int)threadIdx.x;
+            if (i < TOT) {
+                const int t = i / PT, w = i % PT;
+                int src, dst;
+                offs(w, src, dst);
+                *(uint4 *)(lds + (size_t)t * tb + dst) = v[k];
+                if (w >= DW + SW) any = any || (v[k].x | v[k].y | v[k].z | v[k].w) != 0u;
+            }
+        }
+    }
+    for (int i = (int)threadIdx.x; i < TR * PW; i += NT) {
+        const int t = i / PW, w = i % PW;
+        *(float *)(lds + (size_t)t * tb + (KC >> 5) * 100 + 4 * w) =
+            *(const float *)(xg + (size_t)(t0 + t) * tbf + psrc + 4 * w);
+    }
+    if (any) *oflag = seq;
+}
+
+// NW wavefronts of 16 rows, rounds of 4 MT tokens, KC columns per staged
+// chunk, LAH super-blocks of weights in flight per wavefront across chunk edges.
+template <int NW, int MT, int KC, int LAH>
+__global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ W, size_t stride, int rows, int cols,
+                                                    const uint8_t *__restrict__ xg, const float *__restrict__ xs,
+                                                    float *__restrict__ out)
+{
+    constexpr int TR = 4 * MT, ROWS = 16 * NW, NSB = KC / 256, MM_LAH = LAH;
+    constexpr int tb = mf_tok_bytes(KC);
+    extern __shared__ uint4 mm_smem[];
+    uint8_t *lds = (uint8_t *)mm_smem;
+    __shared__ int oflag_s;
+    if (threadIdx.x == 0) oflag_s = -1;
+    int seq = 0;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nblk = (rows + ROWS - 1) / ROWS;
+    const int b = (int)blockIdx.x % nblk, t0 = ((int)blockIdx.x / nblk) * TR;
+    const int r0 = b * ROWS, rend = min(rows, r0 + ROWS);
+    const rsrc_t rA = make_rsrc(W + (size_t)r0 * stride, (uint32_t)((size_t)(rend - r0) * stride));
+    const int nl = lane & 15, g = lane >> 4;
+    const uint32_t rowoff = (uint32_t)((16 * wave + nl) * stride);
+    const int nb = cols >> 8, U = cols >> 6;
+    const uint32_t qoff = (uint32_t)(16 * nb + (g < 2 ? 0 : 16 * U) + 8 * (g & 1));
+    const int a_tok = nl >> 2, a_dig = nl & 3, a_dg = a_dig < 3 ? a_dig : 2;
+    const bool a_pad = a_dig == 3;
+    const int row = r0 + 16 * wave + nl;
+    float accf[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) accf[mt] = 0.0f;
+    auto scaled = [](uint32_t codes, uint32_t k) {
+        return __builtin_bit_cast(uint32_t, __builtin_bit_cast(mf_u16x2, codes) * __builtin_bit_cast(mf_u16x2, k));
+    };
+    // super-block i of the staged chunk with this lane's weights c
+    auto superblock = [&](int i, const MfSb &c) {
+        MfScale sc;
+        mf_scales(c.h, sc);
+        uint32_t klo[8], khi[8];
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const uint32_t lo4 = sc.sc4[t] & 0x07070707u, hi4 = (sc.sc4[t] >> 3) & 0x07070707u;
+#pragma unroll
+            for (int bb = 0; bb < 4; bb++) {
+                const uint32_t sel = 0x0c000c00u | (uint32_t)bb | ((uint32_t)bb << 16);
+                klo[4 * t + bb] = __builtin_amdgcn_perm(0u, lo4, sel);
+                khi[4 * t + bb] = __builtin_amdgcn_perm(0u, hi4, sel);
+            }
+        }
+        mf_v4i clo[MT], chi[MT];
+        float mins[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            clo[mt] = chi[mt] = mf_v4i{0, 0, 0, 0};
+            mins[mt] = 0.0f;
+        }
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int j0 = 2 * p, j1 = 2 * p + 1, s0 = 8 * i + j0, s1 = 8 * i + j1;
+            const uint2 qv = c.q[p];
+            const uint32_t lx = qv.x & 0x0F0F0F0Fu, ly = qv.y & 0x0F0F0F0Fu;
+            const uint32_t hx = (qv.x >> 4) & 0x0F0F0F0Fu, hy = (qv.y >> 4) & 0x0F0F0F0Fu;
+            const mf_v4i bl = mf_v4i{(int)scaled(lx, klo[j0]), (int)scaled(ly, klo[j0]), (int)scaled(hx, klo[j1]),
+                                     (int)scaled(hy, klo[j1])};
+            const mf_v4i bh = mf_v4i{(int)scaled(lx, khi[j0]), (int)scaled(ly, khi[j0]), (int)scaled(hx, khi[j1]),
+                                     (int)scaled(hy, khi[j1])};
+            const float m0 = (float)mf_byte(sc.m4[j0 >> 2], j0 & 3), m1 = (float)mf_byte(sc.m4[j1 >> 2], j1 & 3);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const uint8_t *tp = lds + (size_t)(mt * 4 + a_tok) * tb;
+                const uint2 u0 = *(const uint2 *)(tp + (s0 * 3 + a_dg) * 32 + 8 * g);
+                const uint2 u1 = *(const uint2 *)(tp + (s1 * 3 + a_dg) * 32 + 8 * g);
+                const mf_v4i xa = mf_v4i{a_pad ? 0 : (int)u0.x, a_pad ? 0 : (int)u0.y, a_pad ? 0 : (int)u1.x,
+                                         a_pad ? 0 : (int)u1.y};
+                const float *xsum = (const float *)(lds + (size_t)(mt * 4 + g) * tb + (KC >> 5) * 96);
+                clo[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bl, clo[mt], 0, 0, 0);
+                chi[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bh, chi[mt], 0, 0, 0);
+                mins[mt] = fmaf(m0, xsum[s0], fmaf(m1, xsum[s1], mins[mt]));
+            }
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const float P = *(const float *)(lds + (size_t)(mt * 4 + g) * tb + (KC >> 5) * 100 + 4 * i);
+            const int S0 = clo[mt][0] + 8 * chi[mt][0], S1 = clo[mt][1] + 8 * chi[mt][1];
+            const int S2 = clo[mt][2] + 8 * chi[mt][2];
+            const float t = fmaf((float)S2, 65536.0f, fmaf((float)S1, 256.0f, (float)S0));
+            accf[mt] = fmaf(-sc.dmin, mins[mt], fmaf(sc.d * P, t, accf[mt]));
+        }
+    };
+    // the outliers of the staged chunk (first column k0), as k_mfma_q4k adds them
+    auto correct = [&](int k0) {
+        for (int i = 0; i < NSB; i++) {
+            if (!mf_sb_has_outliers(lds, tb, KC, TR, i)) continue; // uniform
+            MfSb S_;
+            mf_load_sb(rA, rowoff, qoff, (k0 >> 8) + i, true, S_);
+            MfScale K_;
+            mf_scales(S_.h, K_);
+            auto code = [&](int e) {
+                const int eu = e & 63, l = eu & 31;
+                const uint32_t dw = mf_fetch<4>(S_.q, 16 * (l >> 3) + nl, 2 * (e >> 6) + ((l & 7) >> 2));
+                return (dw >> (8 * (l & 3) + (eu >= 32 ? 4 : 0))) & 15u;
+            };
+            auto wt = [&](uint32_t q, int e) {
+                const int j = 2 * (e >> 6) + ((e & 63) >= 32 ? 1 : 0), sh = 8 * (j & 3);
+                const float scv = (float)(((j < 4 ? K_.sc4[0] : K_.sc4[1]) >> sh) & 0xffu);
+                const float mn = (float)(((j < 4 ? K_.m4[0] : K_.m4[1]) >> sh) & 0xffu);
+                return __fsub_rn(__fmul_rn(__fmul_rn(K_.d, scv), (float)q), __fmul_rn(K_.dmin, mn));
+            };
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const int to = mt * 4 + g;
+                const float *xr = xs + (size_t)(t0 + to) * cols + k0;
+                accf[mt] += mf_outliers(lds + (size_t)to * tb, xr, KC, i, true, code, wt);
+            }
+        }
+    };
+    MfSb w[MM_LAH];
+#pragma unroll
+    for (int k = 0; k < MM_LAH; k++) mf_load_sb(rA, rowoff, qoff, k, k < nb, w[k]);
+    bool oany = false;
+    for (int s0 = 0; s0 < nb; s0 += MM_LAH) {
+#pragma unroll
+        for (int j = 0; j < MM_LAH; j++) {
+            const int s = s0 + j;
+            if (s < nb) { // uniform
+                if (s % NSB == 0) {
+                    // a new chunk: the last one's outliers, then its staging
+                    if (__builtin_expect(oany, 0)) correct((s - NSB) * 256); // (oany is false at s = 0)
+                    __syncthreads(); // the previous chunk's readers of LDS are done
+                    mm_copy<KC, TR, 64 * NW>(lds, xg, t0, cols, s * 256, &oflag_s, ++seq);
+                    __syncthreads();
+                    oany = __builtin_amdgcn_readfirstlane(oflag_s) == seq;
+                }
+                superblock(s % NSB, w[j]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            mf_load_sb(rA, rowoff, qoff, s + MM_LAH, s + MM_LAH < nb, w[j]);
+        }
+    }
+    if (__builtin_expect(oany, 0)) correct((nb - NSB) * 256);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+        if (row < rows) out[(size_t)(t0 + mt * 4 + g) * rows + row] = accf[mt];
 }
 
 // ---------------------------------------------------------------------------
@@ -974,11 +1238,16 @@ bool mfma_moe_scan_ok(size_t n, size_t top_k, size_t n_groups, uint8_t dt_gu, ui
 template <int NW, int MT>
 static void mfma_dense(soso_hip *h, const Weight &w, const float *x, size_t n, float *y, int kc, unsigned grid)
 {
+    const bool full = n % (4 * MT) == 0;
     const size_t kcols = weight_kcols(w);
     const size_t lds = (size_t)4 * MT * mf_tok_bytes(kc), stride = packed_row_stride(w.dtype, kcols);
     if (w.dtype == SOSO_HIP_DTYPE_Q8_0)
         k_mfma_q80<MT, NW><<<grid, 64 * NW, lds, h->stream>>>((const uint8_t *)w.dev, stride, (int)w.rows,
                                                               (int)kcols, x, (int)n, kc, y);
+    else if (full)
+        k_mfma_q4k<1, MT, MF_LA1, false, NW, false, true><<<grid, 64 * NW, lds, h->stream>>>(
+            nullptr, nullptr, (const uint8_t *)w.dev, stride, (int)w.rows, (int)kcols, x, 1, nullptr, nullptr,
+            nullptr, (int)n, kc, y, nullptr, 0);
     else
         k_mfma_q4k<1, MT, MF_LA1, false, NW><<<grid, 64 * NW, lds, h->stream>>>(
             nullptr, nullptr, (const uint8_t *)w.dev, stride, (int)w.rows, (int)kcols, x, 1, nullptr, nullptr,
@@ -1003,11 +1272,52 @@ static void mfma_dense(soso_hip *h, const Weight &w, const float *x, size_t n, f
 // 4096x14336 51/87/171/362.
 static const int MF_DENSE[9][2] = {{4, 1}, {8, 1}, {4, 2}, {8, 2}, {16, 1}, {4, 4}, {16, 2}, {8, 4}, {16, 4}};
 
+// Dense Q4_K with a token count that is a multiple of 16, whose grid fills the
+// GPU: x staged once (k_mm_stage into scratch slot 16), then k_mm_q4k with 16
+// wavefronts (256 rows), rounds of 16 tokens, 1024-column chunks and one
+// super-block ahead.  Measured on MI355X, 14336 x 4096 at 64 tokens (us):
+// this shape 56.3-56.7; 2048-column chunks 59.3; 512: 58.9; 256: 76.7;
+// 8 wavefronts x 32 tokens 60.8, x 16 tokens 64.6-69.0; 4 wavefronts x 16
+// tokens 72.1; 4 x 64 (1 wavefront per SIMD) 120.8; 16 x 8 tokens 88.3;
+// k_mfma_q4k staging its own rounds 68.1-68.3.
+constexpr int MM_NW = 16, MM_MT = 4, MM_KC = 1024, MM_LA = 1;
+
+template <int NW, int MT, int KC, int LAH>
+static void mm_launch(soso_hip *h, const Weight &w, size_t stride, const uint8_t *xg, const float *x, float *y,
+                      unsigned grid)
+{
+    const size_t lds = (size_t)4 * MT * mf_tok_bytes(KC);
+    k_mm_q4k<NW, MT, KC, LAH><<<grid, 64 * NW, lds, h->stream>>>((const uint8_t *)w.dev, stride, (int)w.rows,
+                                                                 (int)weight_kcols(w), xg, x, y);
+}
+
+static int launch_mm_q4k(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
+{
+    constexpr int NW = MM_NW, MT = MM_MT, KC = MM_KC, LAH = MM_LA;
+    const size_t cols = weight_kcols(w), nblk = (w.rows + 16 * NW - 1) / (16 * NW);
+    if (n % (size_t)(4 * MT) || cols % KC || (size_t)4 * MT * mf_tok_bytes(KC) > h->max_lds ||
+        nblk * (n / (4 * MT)) * 5 < (size_t)h->num_cu * 4)
+        return SOSO_HIP_DECLINED; // k_mfma_q4k's launch, which picks its shape from the grid, takes it
+    uint8_t *xg = (uint8_t *)scratch_get(h, 16, n * (size_t)mf_tok_bytes((int)cols));
+    if (!xg) return set_err(h, SOSO_HIP_ERR_NOMEM, "mfma: staged x");
+    const size_t waves = n * ((cols + 511) / 512);
+    k_mm_stage<<<(unsigned)((waves + 3) / 4), 256, 0, h->stream>>>(x, (int)n, (int)cols, xg);
+    int rc = hip_check(h, hipGetLastError(), "mm stage launch");
+    if (rc != SOSO_HIP_OK) return rc;
+    const size_t stride = packed_row_stride(w.dtype, cols);
+    mm_launch<NW, MT, KC, LAH>(h, w, stride, xg, x, y, (unsigned)(nblk * (n / (4 * (size_t)MT))));
+    return hip_check(h, hipGetLastError(), "mm launch");
+}
+
 int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
 {
     const size_t kcols = weight_kcols(w);
     if (!mfma_shape_ok(w.dtype, w.rows, kcols) || n == 0 || n > (1u << 20))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
+    if (w.dtype == SOSO_HIP_DTYPE_Q4_K) {
+        const int rc = launch_mm_q4k(h, w, x, n, y);
+        if (rc != SOSO_HIP_DECLINED) return rc;
+    }
     const size_t cu = (size_t)h->num_cu;
     auto groups = [&](int nw, int mt) { return (w.rows + 16 * nw - 1) / (16 * nw) * ((n + 4 * mt - 1) / (4 * mt)); };
     int pick = -1;
