@@ -62,6 +62,16 @@ __host__ __device__ constexpr inline int mf_tok_bytes(int kc)
 {
     return (mf_mask_off(kc) + kc / 8 + 15) & ~15;
 }
+// The dense matmul's layout (k_mm_q4k) per token for kc staged columns: the
+// digits of each pair of sub-blocks as [4 planes: digits 0..2 and a zero
+// plane][4 lane groups][2 sub-blocks][8 bytes] (256 bytes per pair), so that a
+// lane's A operand -- 8 bytes of each sub-block of a unit -- is one aligned
+// 16-byte load and the zero-pad digit lanes load zeros; then the f32 sums per
+// sub-block, 2^-e per super-block and (16-byte aligned) the outlier mask.
+__host__ __device__ constexpr inline int mm_sum_off(int kc) { return 4 * kc; }
+__host__ __device__ constexpr inline int mm_p_off(int kc) { return 4 * kc + kc / 8; }
+__host__ __device__ constexpr inline int mm_mask_off(int kc) { return (4 * kc + kc / 8 + kc / 64 + 15) & ~15; }
+__host__ __device__ constexpr inline int mm_tok_bytes(int kc) { return (mm_mask_off(kc) + kc / 8 + 15) & ~15; }
 // The MoE experts that scan the ranking keep their slot list (16-bit entries)
 // ahead of the tokens' staging in dynamic LDS.
 __host__ __device__ inline int mf_scan_bytes(int nslots) { return (2 * nslots + 15) & ~15; }
@@ -179,7 +189,35 @@ __device__ __forceinline__ int mf_byte(uint32_t w, int j) { return (int)((w >> (
 // false is returned (uniform), for the caller to stage the chunk again
 // through the full search.  The full search returns whether some block of
 // the wavefront has outliers (uniform).
-template <bool FAST>
+// Where chunk c's pieces go in a token's staging (mf_stage's layout, or with
+// MM the dense matmul's: mm_*_off).
+template <bool MM>
+__device__ __forceinline__ void mf_write(uint8_t *tp, int c, int kc, const uint32_t (&d0)[XDIG],
+                                         const uint32_t (&d1)[XDIG], float sm, bool finite, int ex, uint32_t om)
+{
+    const int sbl = c >> 2, qq = c & 3;
+    if constexpr (MM) {
+        uint8_t *dp = tp + (sbl >> 1) * 256 + 16 * qq + 8 * (sbl & 1);
+#pragma unroll
+        for (int kk = 0; kk < XDIG; kk++) *(uint2 *)(dp + 64 * kk) = make_uint2(d0[kk], d1[kk]);
+        *(uint2 *)(dp + 64 * XDIG) = make_uint2(0u, 0u);
+        if (qq == 0) *(float *)(tp + mm_sum_off(kc) + 4 * sbl) = sm;
+        if ((c & 31) == 0)
+            *(float *)(tp + mm_p_off(kc) + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
+        tp[mm_mask_off(kc) + c] = (uint8_t)om;
+    } else {
+#pragma unroll
+        for (int kk = 0; kk < XDIG; kk++)
+            *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * qq) = make_uint2(d0[kk], d1[kk]);
+        if (qq == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
+        // a non-finite super-block: NaN products, as the CPU's dot gives Inf or NaN
+        if ((c & 31) == 0)
+            *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
+        tp[mf_mask_off(kc) + c] = (uint8_t)om;
+    }
+}
+
+template <bool FAST, bool MM = false>
 __device__ __forceinline__ bool mf_chunk(float4 v0, float4 v1, uint8_t *tp, int c, int kc, bool valid)
 {
     float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
@@ -227,15 +265,7 @@ __device__ __forceinline__ bool mf_chunk(float4 v0, float4 v1, uint8_t *tp, int 
         uint32_t d0[XDIG], d1[XDIG];
         digits4(make_float4(vv[0], vv[1], vv[2], vv[3]), ex, d0);
         digits4(make_float4(vv[4], vv[5], vv[6], vv[7]), ex, d1);
-        const int sbl = c >> 2, qq = c & 3;
-#pragma unroll
-        for (int kk = 0; kk < XDIG; kk++)
-            *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * qq) = make_uint2(d0[kk], d1[kk]);
-        if (qq == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
-        // a non-finite super-block: NaN products, as the CPU's dot gives Inf or NaN
-        if ((c & 31) == 0)
-            *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
-        tp[mf_mask_off(kc) + c] = (uint8_t)om;
+        mf_write<MM>(tp, c, kc, d0, d1, sm, finite, ex, om);
     }
     return !FAST || found;
 }
@@ -243,6 +273,7 @@ __device__ __forceinline__ bool mf_chunk(float4 v0, float4 v1, uint8_t *tp, int 
 // Writes one chunk staged without outliers: m is its 128-element block's
 // maximum (the exponent takes the super-block's, over 32 lanes), sm the
 // chunk's f32 sum (the sub-block's over 4 lanes).
+template <bool MM = false>
 __device__ __forceinline__ void mf_put(float4 v0, float4 v1, float m, float sm, uint8_t *tp, int c, int kc, bool valid)
 {
     const float mx = fmaxf(m, __shfl_xor(m, 16, 64));
@@ -254,14 +285,7 @@ __device__ __forceinline__ void mf_put(float4 v0, float4 v1, float m, float sm, 
         uint32_t d0[XDIG], d1[XDIG];
         digits4(v0, ex, d0);
         digits4(v1, ex, d1);
-        const int sbl = c >> 2, qq = c & 3;
-#pragma unroll
-        for (int kk = 0; kk < XDIG; kk++)
-            *(uint2 *)(tp + (sbl * 3 + kk) * 32 + 8 * qq) = make_uint2(d0[kk], d1[kk]);
-        if (qq == 0) *(float *)(tp + (kc >> 5) * 96 + 4 * sbl) = sm;
-        if ((c & 31) == 0)
-            *(float *)(tp + (kc >> 5) * 100 + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
-        tp[mf_mask_off(kc) + c] = 0;
+        mf_write<MM>(tp, c, kc, d0, d1, sm, finite, ex, 0u);
     }
 }
 
@@ -363,14 +387,14 @@ __device__ __forceinline__ uint32_t mf_fetch(const uint2 (&q)[N], int src, int d
 
 // Whether any of the round's nt tokens has outliers in super-block sbl of the
 // staged chunk; uniform.
-__device__ __forceinline__ bool mf_sb_has_outliers(const uint8_t *lds, int tb, int kc, int nt, int sbl)
+__device__ __forceinline__ bool mf_sb_has_outliers(const uint8_t *lds, int tb, int moff, int nt, int sbl)
 {
     const int lane = (int)(threadIdx.x & 63), t = lane >> 1;
     bool any = false;
     for (int t0 = 0; t0 < nt; t0 += 32) {
         if (t0 + t < nt) {
             const uint4 m =
-                *(const uint4 *)(lds + (size_t)(t0 + t) * tb + mf_mask_off(kc) + 32 * sbl + 16 * (lane & 1));
+                *(const uint4 *)(lds + (size_t)(t0 + t) * tb + moff + 32 * sbl + 16 * (lane & 1));
             any = any || (m.x | m.y | m.z | m.w) != 0u;
         }
     }
@@ -386,13 +410,13 @@ __device__ __forceinline__ bool mf_sb_has_outliers(const uint8_t *lds, int tb, i
 // runs the loop (the codes come from other lanes by ds_bpermute); the count is
 // the wavefront's largest.
 template <class Code, class Wt>
-__device__ __forceinline__ float mf_outliers(const uint8_t *tp, const float *xr, int kc, int sbl, bool valid,
+__device__ __forceinline__ float mf_outliers(const uint8_t *tp, const float *xr, int moff, int sbl, bool valid,
                                              Code get_code, Wt wt)
 {
     uint4 ma = make_uint4(0u, 0u, 0u, 0u), mb = ma;
     if (valid) {
-        ma = *(const uint4 *)(tp + mf_mask_off(kc) + 32 * sbl);
-        mb = *(const uint4 *)(tp + mf_mask_off(kc) + 32 * sbl + 16);
+        ma = *(const uint4 *)(tp + moff + 32 * sbl);
+        mb = *(const uint4 *)(tp + moff + 32 * sbl + 16);
     }
     uint32_t m[8] = {ma.x, ma.y, ma.z, ma.w, mb.x, mb.y, mb.z, mb.w};
     int cnt = 0;
@@ -707,7 +731,7 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
             // holds it), the high nibble from 32 on.
             if (__builtin_expect(oany, 0)) {
                 for (int i = 0; i < nsb; i++) {
-                    if (!mf_sb_has_outliers(lds, tb, kc, nt, i)) continue; // uniform
+                    if (!mf_sb_has_outliers(lds, tb, mf_mask_off(kc), nt, i)) continue; // uniform
                     MfSb S_[NMAT];
                     load_sb(rA, sb0 + i, true, S_[0]);
                     if constexpr (NMAT == 2) load_sb(rB, sb0 + i, true, S_[NMAT - 1]);
@@ -731,7 +755,8 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
                             if (mt * 4 >= nt) break; // uniform
                             const int to = mt * 4 + g, tv = to < nt ? to : 0;
                             const float *xr = xs + (size_t)(slot_s[tv] / xdiv) * cols + k0;
-                            accf[m][mt] += mf_outliers(lds + (size_t)tv * tb, xr, kc, i, to < nt, code, wt);
+                            accf[m][mt] +=
+                                mf_outliers(lds + (size_t)tv * tb, xr, mf_mask_off(kc), i, to < nt, code, wt);
                         }
                     }
                 }
@@ -759,17 +784,21 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
 // the same x again (14336 x 4096 at 64 tokens: 56 row blocks x 4 rounds, about
 // 1,000 of its 7,100 VALU instructions per wavefront), and its code carries the
 // checks of partial rounds and MoE token lists.  Here k_mm_stage converts the
-// n rows of x once into the layout mf_stage writes (the whole row as one
-// chunk, token t at t * mf_tok_bytes(cols)), and each workgroup of k_mm_q4k
-// copies the stretch of its chunk from there into LDS (four contiguous
-// regions per token: digits, sub-block sums, 2^-e per super-block, outlier
-// mask).  Arithmetic, operands and the order of every sum are k_mfma_q4k's
-// (the outliers' corrections, where a token has some, join after each
-// staged chunk, whose width may differ from k_mfma_q4k's).
+// n rows of x once (the whole row as one chunk, token t at t *
+// mm_tok_bytes(cols)), in the paired layout of mm_*_off: a lane's A operand is
+// one 16-byte LDS load and the zero-pad digit lanes read a zero plane (against
+// mf_stage's layout: two 8-byte loads and four selects per unit and token
+// tile; 56.3 -> 51.9 us at 14336 x 4096 x 64).  Each workgroup of k_mm_q4k
+// copies the stretch of its chunk from there into LDS (four contiguous regions
+// per token: digits, sub-block sums, 2^-e per super-block, outlier mask).
+// Arithmetic, operands and the order of every sum are k_mfma_q4k's (the
+// outliers' corrections, where a token has some, join after each staged
+// chunk, whose width may differ from k_mfma_q4k's).
 // ---------------------------------------------------------------------------
 
 // One wavefront per 512 columns (64 chunks: two super-blocks, the lanes of each
-// 128-element block together) of one token; the outlier search as mf_stage's.
+// 128-element block together) of one token; the outlier search as mf_stage's,
+// the output in the paired layout (mf_write<true>).
 __global__ void __launch_bounds__(256) k_mm_stage(const float *__restrict__ x, int n, int cols,
                                                   uint8_t *__restrict__ xg)
 {
@@ -785,7 +814,7 @@ __global__ void __launch_bounds__(256) k_mm_stage(const float *__restrict__ x, i
         v0 = x4[0];
         v1 = x4[1];
     }
-    uint8_t *tp = xg + (size_t)t * mf_tok_bytes(cols);
+    uint8_t *tp = xg + (size_t)t * mm_tok_bytes(cols);
     float mx = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
                      fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
     const float sm = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
@@ -796,25 +825,25 @@ __global__ void __launch_bounds__(256) k_mm_stage(const float *__restrict__ x, i
     const float m1 = fmaxf(hq, dpp_f<0x140>(hq));
     float qn = fminf(q, dpp_f<0x141>(q));
     qn = fminf(qn, dpp_f<0x140>(qn));
-    if (__builtin_expect(__ballot(m1 > 16.0f * qn) == 0, 1)) mf_put(v0, v1, m1, sm, tp, c, cols, valid);
-    else (void)mf_chunk<false>(v0, v1, tp, c, cols, valid);
+    if (__builtin_expect(__ballot(m1 > 16.0f * qn) == 0, 1)) mf_put<true>(v0, v1, m1, sm, tp, c, cols, valid);
+    else (void)mf_chunk<false, true>(v0, v1, tp, c, cols, valid);
 }
 
 // Copies columns k0 .. k0 + KC of tokens t0 .. t0 + TR - 1 from the staged rows
-// (xg, mf_tok_bytes(cols) bytes per token) into LDS (mf_stage's chunk layout,
-// mf_tok_bytes(KC) per token); a thread that copies a nonzero outlier mask word
-// writes seq into *oflag.  cols, k0 and KC are multiples of 256, so every region
-// but the 2^-e one moves in 16-byte words: MB of them per thread are requested
-// before any is stored, so a batch costs one round trip.
+// (xg, mm_tok_bytes(cols) bytes per token) into LDS (mm_tok_bytes(KC) per
+// token, the same layout for the chunk); a thread that copies a nonzero
+// outlier mask word writes seq into *oflag.  cols, k0 and KC are multiples of
+// 256, so every region but the 2^-e one moves in 16-byte words: MB of them per
+// thread are requested before any is stored, so a batch costs one round trip.
 template <int KC, int TR, int NT>
 __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict__ xg, int t0, int cols, int k0,
                                         int *oflag, int seq)
 {
-    constexpr int tb = mf_tok_bytes(KC), DW = 3 * KC / 16, SW = KC / 128, MW = KC / 128, PW = KC / 256;
+    constexpr int tb = mm_tok_bytes(KC), DW = KC / 4, SW = KC / 128, MW = KC / 128, PW = KC / 256;
     constexpr int PT = DW + SW + MW, TOT = TR * PT, MB = 4;
-    const int tbf = mf_tok_bytes(cols);
-    const int dsrc = (k0 >> 5) * 96, ssrc = (cols >> 5) * 96 + (k0 >> 3), psrc = (cols >> 5) * 100 + (k0 >> 6),
-              msrc = mf_mask_off(cols) + (k0 >> 3);
+    const int tbf = mm_tok_bytes(cols);
+    const int dsrc = 4 * k0, ssrc = mm_sum_off(cols) + (k0 >> 3), psrc = mm_p_off(cols) + (k0 >> 6),
+              msrc = mm_mask_off(cols) + (k0 >> 3);
     // word w of a token: its source and LDS offsets
     auto offs = [&](int w, int &src, int &dst) {
         if (w < DW) {
@@ -822,10 +851,10 @@ __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict_
             dst = 16 * w;
         } else if (w < DW + SW) {
             src = ssrc + 16 * (w - DW);
-            dst = (KC >> 5) * 96 + 16 * (w - DW);
+            dst = mm_sum_off(KC) + 16 * (w - DW);
         } else {
             src = msrc + 16 * (w - DW - SW);
-            dst = mf_mask_off(KC) + 16 * (w - DW - SW);
+            dst = mm_mask_off(KC) + 16 * (w - DW - SW);
         }
     };
     bool any = false;
@@ -855,7 +884,7 @@ __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict_
     }
     for (int i = (int)threadIdx.x; i < TR * PW; i += NT) {
         const int t = i / PW, w = i % PW;
-        *(float *)(lds + (size_t)t * tb + (KC >> 5) * 100 + 4 * w) =
+        *(float *)(lds + (size_t)t * tb + mm_p_off(KC) + 4 * w) =
             *(const float *)(xg + (size_t)(t0 + t) * tbf + psrc + 4 * w);
     }
     if (any) *oflag = seq;
@@ -869,7 +898,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
                                                     float *__restrict__ out)
 {
     constexpr int TR = 4 * MT, ROWS = 16 * NW, NSB = KC / 256, MM_LAH = LAH;
-    constexpr int tb = mf_tok_bytes(KC);
+    constexpr int tb = mm_tok_bytes(KC);
     extern __shared__ uint4 mm_smem[];
     uint8_t *lds = (uint8_t *)mm_smem;
     __shared__ int oflag_s;
@@ -885,8 +914,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
     const uint32_t rowoff = (uint32_t)((16 * wave + nl) * stride);
     const int nb = cols >> 8, U = cols >> 6;
     const uint32_t qoff = (uint32_t)(16 * nb + (g < 2 ? 0 : 16 * U) + 8 * (g & 1));
-    const int a_tok = nl >> 2, a_dig = nl & 3, a_dg = a_dig < 3 ? a_dig : 2;
-    const bool a_pad = a_dig == 3;
+    const int a_tok = nl >> 2, a_dig = nl & 3; // digit 3: the zero plane
     const int row = r0 + 16 * wave + nl;
     float accf[MT];
 #pragma unroll
@@ -930,11 +958,9 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
 #pragma unroll
             for (int mt = 0; mt < MT; mt++) {
                 const uint8_t *tp = lds + (size_t)(mt * 4 + a_tok) * tb;
-                const uint2 u0 = *(const uint2 *)(tp + (s0 * 3 + a_dg) * 32 + 8 * g);
-                const uint2 u1 = *(const uint2 *)(tp + (s1 * 3 + a_dg) * 32 + 8 * g);
-                const mf_v4i xa = mf_v4i{a_pad ? 0 : (int)u0.x, a_pad ? 0 : (int)u0.y, a_pad ? 0 : (int)u1.x,
-                                         a_pad ? 0 : (int)u1.y};
-                const float *xsum = (const float *)(lds + (size_t)(mt * 4 + g) * tb + (KC >> 5) * 96);
+                const uint4 u = *(const uint4 *)(tp + ((s0 >> 1) * 4 + a_dig) * 64 + 16 * g);
+                const mf_v4i xa = mf_v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+                const float *xsum = (const float *)(lds + (size_t)(mt * 4 + g) * tb + mm_sum_off(KC));
                 clo[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bl, clo[mt], 0, 0, 0);
                 chi[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bh, chi[mt], 0, 0, 0);
                 mins[mt] = fmaf(m0, xsum[s0], fmaf(m1, xsum[s1], mins[mt]));
@@ -942,7 +968,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
         }
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            const float P = *(const float *)(lds + (size_t)(mt * 4 + g) * tb + (KC >> 5) * 100 + 4 * i);
+            const float P = *(const float *)(lds + (size_t)(mt * 4 + g) * tb + mm_p_off(KC) + 4 * i);
             const int S0 = clo[mt][0] + 8 * chi[mt][0], S1 = clo[mt][1] + 8 * chi[mt][1];
             const int S2 = clo[mt][2] + 8 * chi[mt][2];
             const float t = fmaf((float)S2, 65536.0f, fmaf((float)S1, 256.0f, (float)S0));
@@ -952,7 +978,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
     // the outliers of the staged chunk (first column k0), as k_mfma_q4k adds them
     auto correct = [&](int k0) {
         for (int i = 0; i < NSB; i++) {
-            if (!mf_sb_has_outliers(lds, tb, KC, TR, i)) continue; // uniform
+            if (!mf_sb_has_outliers(lds, tb, mm_mask_off(KC), TR, i)) continue; // uniform
             MfSb S_;
             mf_load_sb(rA, rowoff, qoff, (k0 >> 8) + i, true, S_);
             MfScale K_;
@@ -972,7 +998,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
             for (int mt = 0; mt < MT; mt++) {
                 const int to = mt * 4 + g;
                 const float *xr = xs + (size_t)(t0 + to) * cols + k0;
-                accf[mt] += mf_outliers(lds + (size_t)to * tb, xr, KC, i, true, code, wt);
+                accf[mt] += mf_outliers(lds + (size_t)to * tb, xr, mm_mask_off(KC), i, true, code, wt);
             }
         }
     };
@@ -1127,7 +1153,7 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict_
             // this row holds it).
             if (__builtin_expect(oany, 0)) {
                 for (int i = 0; i < nsb; i++) {
-                    if (!mf_sb_has_outliers(lds, tb, kc, nt, i)) continue; // uniform
+                    if (!mf_sb_has_outliers(lds, tb, mf_mask_off(kc), nt, i)) continue; // uniform
                     MfQ80 o;
                     load_sb(sb0 + i, true, o);
                     auto code = [&](int e) {
@@ -1146,7 +1172,7 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict_
                         if (mt * 4 >= nt) break; // uniform
                         const int to = mt * 4 + g, tv = to < nt ? to : 0;
                         const float *xr = xs + (size_t)slot_s[tv] * cols + k0;
-                        accf[mt] += mf_outliers(lds + (size_t)tv * tb, xr, kc, i, to < nt, code, wt);
+                        accf[mt] += mf_outliers(lds + (size_t)tv * tb, xr, mf_mask_off(kc), i, to < nt, code, wt);
                     }
                 }
             }
@@ -1286,7 +1312,7 @@ template <int NW, int MT, int KC, int LAH>
 static void mm_launch(soso_hip *h, const Weight &w, size_t stride, const uint8_t *xg, const float *x, float *y,
                       unsigned grid)
 {
-    const size_t lds = (size_t)4 * MT * mf_tok_bytes(KC);
+    const size_t lds = (size_t)4 * MT * mm_tok_bytes(KC);
     k_mm_q4k<NW, MT, KC, LAH><<<grid, 64 * NW, lds, h->stream>>>((const uint8_t *)w.dev, stride, (int)w.rows,
                                                                  (int)weight_kcols(w), xg, x, y);
 }
@@ -1295,10 +1321,10 @@ static int launch_mm_q4k(soso_hip *h, const Weight &w, const float *x, size_t n,
 {
     constexpr int NW = MM_NW, MT = MM_MT, KC = MM_KC, LAH = MM_LA;
     const size_t cols = weight_kcols(w), nblk = (w.rows + 16 * NW - 1) / (16 * NW);
-    if (n % (size_t)(4 * MT) || cols % KC || (size_t)4 * MT * mf_tok_bytes(KC) > h->max_lds ||
+    if (n % (size_t)(4 * MT) || cols % KC || (size_t)4 * MT * mm_tok_bytes(KC) > h->max_lds ||
         nblk * (n / (4 * MT)) * 5 < (size_t)h->num_cu * 4)
         return SOSO_HIP_DECLINED; // k_mfma_q4k's launch, which picks its shape from the grid, takes it
-    uint8_t *xg = (uint8_t *)scratch_get(h, 16, n * (size_t)mf_tok_bytes((int)cols));
+    uint8_t *xg = (uint8_t *)scratch_get(h, 16, n * (size_t)mm_tok_bytes((int)cols));
     if (!xg) return set_err(h, SOSO_HIP_ERR_NOMEM, "mfma: staged x");
     const size_t waves = n * ((cols + 511) / 512);
     k_mm_stage<<<(unsigned)((waves + 3) / 4), 256, 0, h->stream>>>(x, (int)n, (int)cols, xg);
