@@ -937,42 +937,50 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
                 khi[4 * t + bb] = __builtin_amdgcn_perm(0u, hi4, sel);
             }
         }
-        mf_v4i clo[MT], chi[MT];
-        float mins[MT];
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++) {
-            clo[mt] = chi[mt] = mf_v4i{0, 0, 0, 0};
-            mins[mt] = 0.0f;
-        }
+        // the super-block's B operands (the four units' codes times the scale
+        // parts) and min factors once, then token tile after token tile: its
+        // four units' A operands, the two MFMA chains, the min term and the f32
+        // step (the sums are k_mfma_q4k's, in its order)
+        mf_v4i bl[4], bh[4];
+        float mf[8];
 #pragma unroll
         for (int p = 0; p < 4; p++) {
-            const int j0 = 2 * p, j1 = 2 * p + 1, s0 = 8 * i + j0, s1 = 8 * i + j1;
+            const int j0 = 2 * p, j1 = 2 * p + 1;
             const uint2 qv = c.q[p];
             const uint32_t lx = qv.x & 0x0F0F0F0Fu, ly = qv.y & 0x0F0F0F0Fu;
             const uint32_t hx = (qv.x >> 4) & 0x0F0F0F0Fu, hy = (qv.y >> 4) & 0x0F0F0F0Fu;
-            const mf_v4i bl = mf_v4i{(int)scaled(lx, klo[j0]), (int)scaled(ly, klo[j0]), (int)scaled(hx, klo[j1]),
-                                     (int)scaled(hy, klo[j1])};
-            const mf_v4i bh = mf_v4i{(int)scaled(lx, khi[j0]), (int)scaled(ly, khi[j0]), (int)scaled(hx, khi[j1]),
-                                     (int)scaled(hy, khi[j1])};
-            const float m0 = (float)mf_byte(sc.m4[j0 >> 2], j0 & 3), m1 = (float)mf_byte(sc.m4[j1 >> 2], j1 & 3);
-#pragma unroll
-            for (int mt = 0; mt < MT; mt++) {
-                const uint8_t *tp = lds + (size_t)(mt * 4 + a_tok) * tb;
-                const uint4 u = *(const uint4 *)(tp + ((s0 >> 1) * 4 + a_dig) * 64 + 16 * g);
-                const mf_v4i xa = mf_v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
-                const float *xsum = (const float *)(lds + (size_t)(mt * 4 + g) * tb + mm_sum_off(KC));
-                clo[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bl, clo[mt], 0, 0, 0);
-                chi[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa, bh, chi[mt], 0, 0, 0);
-                mins[mt] = fmaf(m0, xsum[s0], fmaf(m1, xsum[s1], mins[mt]));
-            }
+            bl[p] = mf_v4i{(int)scaled(lx, klo[j0]), (int)scaled(ly, klo[j0]), (int)scaled(hx, klo[j1]),
+                           (int)scaled(hy, klo[j1])};
+            bh[p] = mf_v4i{(int)scaled(lx, khi[j0]), (int)scaled(ly, khi[j0]), (int)scaled(hx, khi[j1]),
+                           (int)scaled(hy, khi[j1])};
+            mf[j0] = (float)mf_byte(sc.m4[j0 >> 2], j0 & 3);
+            mf[j1] = (float)mf_byte(sc.m4[j1 >> 2], j1 & 3);
         }
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
-            const float P = *(const float *)(lds + (size_t)(mt * 4 + g) * tb + mm_p_off(KC) + 4 * i);
-            const int S0 = clo[mt][0] + 8 * chi[mt][0], S1 = clo[mt][1] + 8 * chi[mt][1];
-            const int S2 = clo[mt][2] + 8 * chi[mt][2];
+            const uint8_t *tp = lds + (size_t)(mt * 4 + a_tok) * tb + (4 * i * 4 + a_dig) * 64 + 16 * g;
+            mf_v4i xa[4];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const uint4 u = *(const uint4 *)(tp + 256 * p);
+                xa[p] = mf_v4i{(int)u.x, (int)u.y, (int)u.z, (int)u.w};
+            }
+            const uint8_t *to = lds + (size_t)(mt * 4 + g) * tb;
+            const float4 xs0 = *(const float4 *)(to + mm_sum_off(KC) + 32 * i);
+            const float4 xs1 = *(const float4 *)(to + mm_sum_off(KC) + 32 * i + 16);
+            const float xsm[8] = {xs0.x, xs0.y, xs0.z, xs0.w, xs1.x, xs1.y, xs1.z, xs1.w};
+            const float P = *(const float *)(to + mm_p_off(KC) + 4 * i);
+            mf_v4i clo = mf_v4i{0, 0, 0, 0}, chi = clo;
+            float mins = 0.0f;
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                clo = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[p], bl[p], clo, 0, 0, 0);
+                chi = __builtin_amdgcn_mfma_i32_16x16x64_i8(xa[p], bh[p], chi, 0, 0, 0);
+                mins = fmaf(mf[2 * p], xsm[2 * p], fmaf(mf[2 * p + 1], xsm[2 * p + 1], mins));
+            }
+            const int S0 = clo[0] + 8 * chi[0], S1 = clo[1] + 8 * chi[1], S2 = clo[2] + 8 * chi[2];
             const float t = fmaf((float)S2, 65536.0f, fmaf((float)S1, 256.0f, (float)S0));
-            accf[mt] = fmaf(-sc.dmin, mins[mt], fmaf(sc.d * P, t, accf[mt]));
+            accf[mt] = fmaf(-sc.dmin, mins, fmaf(sc.d * P, t, accf[mt]));
         }
     };
     // the outliers of the staged chunk (first column k0), as k_mfma_q4k adds them
