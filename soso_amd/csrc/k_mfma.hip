@@ -1194,6 +1194,125 @@ __global__ void __launch_bounds__(64 * NW) k_mfma_q80(const uint8_t *__restrict_
     }
 }
 
+// ---------------------------------------------------------------------------
+// Dense Q8_0 products with x staged once (k_mm_stage, the paired layout), as
+// k_mm_q4k is to k_mfma_q4k: k_mfma_q80's arithmetic and order of sums (one
+// v_mfma_i32_16x16x32_i8 per 32-element block and 4-token tile, the block's
+// f32 step at once), the A operand one 8-byte load (the zero plane for the
+// pad lanes), full rounds only, token tile after token tile per 256 columns.
+// ---------------------------------------------------------------------------
+template <int NW, int MT, int KC>
+__global__ void __launch_bounds__(64 * NW) k_mm_q80(const uint8_t *__restrict__ W, size_t stride, int rows, int cols,
+                                                    const uint8_t *__restrict__ xg, const float *__restrict__ xs,
+                                                    float *__restrict__ out)
+{
+    typedef long mf_i64;
+    constexpr int TR = 4 * MT, ROWS = 16 * NW, NSB = KC / 256;
+    constexpr int tb = mm_tok_bytes(KC);
+    extern __shared__ uint4 mm_smem[];
+    uint8_t *lds = (uint8_t *)mm_smem;
+    __shared__ int oflag_s;
+    if (threadIdx.x == 0) oflag_s = -1;
+    int seq = 0;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int nblk = (rows + ROWS - 1) / ROWS;
+    const int b = (int)blockIdx.x % nblk, t0 = ((int)blockIdx.x / nblk) * TR;
+    const int r0 = b * ROWS, rend = min(rows, r0 + ROWS);
+    const rsrc_t rA = make_rsrc(W + (size_t)r0 * stride, (uint32_t)((size_t)(rend - r0) * stride));
+    const int nl = lane & 15, g = lane >> 4;
+    const int U = cols >> 6, nbk = cols >> 5, nb = cols >> 8;
+    // packed row: the f32 scales (padded to 16 bytes), then 4 planes of 16
+    // bytes per unit (plane i at + 16 U i)
+    const uint32_t sreg = (uint32_t)((4 * nbk + 15) & ~15);
+    const uint32_t rowoff = (uint32_t)((16 * wave + nl) * stride);
+    const uint32_t qoff = sreg + (uint32_t)(16 * U * (g >> 1) + 8 * (g & 1));
+    const int a_tok = nl >> 2, a_dig = nl & 3; // digit 3: the zero plane
+    const int row = r0 + 16 * wave + nl;
+    auto load_sb = [&](int sb, bool in, MfQ80 &o) {
+        const uint32_t off = in ? rowoff : 0x80000000u;
+        o.s[0] = bld16(rA, off + 32u * (uint32_t)sb);
+        o.s[1] = bld16(rA, off + 32u * (uint32_t)sb + 16u);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const uint32_t u = 4u * (uint32_t)sb + (uint32_t)p;
+            o.q[2 * p] = bld8(rA, off + qoff + 16u * u);
+            o.q[2 * p + 1] = bld8(rA, off + qoff + 32u * (uint32_t)U + 16u * u);
+        }
+    };
+    float accf[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) accf[mt] = 0.0f;
+    auto superblock = [&](int i, const MfQ80 &c) {
+        const uint32_t scs[8] = {c.s[0].x, c.s[0].y, c.s[0].z, c.s[0].w, c.s[1].x, c.s[1].y, c.s[1].z, c.s[1].w};
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const uint8_t *tp = lds + (size_t)(mt * 4 + a_tok) * tb + (16 * i + a_dig) * 64 + 16 * g;
+            const float P = *(const float *)(lds + (size_t)(mt * 4 + g) * tb + mm_p_off(KC) + 4 * i);
+            uint2 u[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) u[k] = *(const uint2 *)(tp + (k >> 1) * 256 + 8 * (k & 1));
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                const uint2 qq = c.q[2 * (k >> 1) + (k & 1)];
+                const mf_i64 bq = (mf_i64)(((uint64_t)qq.y << 32) | qq.x);
+                const mf_i64 xa = (mf_i64)(((uint64_t)u[k].y << 32) | u[k].x);
+                const mf_v4i d = __builtin_amdgcn_mfma_i32_16x16x32_i8(xa, bq, mf_v4i{0, 0, 0, 0}, 0, 0, 0);
+                const float t = fmaf((float)d[2], 65536.0f, fmaf((float)d[1], 256.0f, (float)d[0]));
+                accf[mt] = fmaf(__builtin_bit_cast(float, scs[k]) * P, t, accf[mt]);
+            }
+        }
+    };
+    // the outliers of the staged chunk (first column k0): w * x with w =
+    // fl(q * scale) (dequant.rs:74-97), as k_mfma_q80 adds them
+    auto correct = [&](int k0) {
+        for (int i = 0; i < NSB; i++) {
+            if (!mf_sb_has_outliers(lds, tb, mm_mask_off(KC), TR, i)) continue; // uniform
+            MfQ80 o;
+            load_sb((k0 >> 8) + i, true, o);
+            auto code = [&](int e) {
+                const int l = e & 31;
+                const uint32_t dw = mf_fetch<8>(o.q, 16 * (l >> 3) + nl, 2 * (e >> 5) + ((l & 7) >> 2));
+                return (dw >> (8 * (l & 3))) & 0xffu;
+            };
+            auto wt = [&](uint32_t q, int e) {
+                const int kb = e >> 5, kq = kb & 3;
+                const uint4 sv = kb < 4 ? o.s[0] : o.s[1];
+                const uint32_t sbits = kq == 0 ? sv.x : kq == 1 ? sv.y : kq == 2 ? sv.z : sv.w;
+                return __fmul_rn((float)(int8_t)(uint8_t)q, __builtin_bit_cast(float, opaque(sbits)));
+            };
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const int to = mt * 4 + g;
+                const float *xr = xs + (size_t)(t0 + to) * cols + k0;
+                accf[mt] += mf_outliers(lds + (size_t)to * tb, xr, mm_mask_off(KC), i, true, code, wt);
+            }
+        }
+    };
+    MfQ80 cur;
+    load_sb(0, true, cur);
+    bool oany = false;
+    for (int s = 0; s < nb; s++) {
+        if (s % NSB == 0) {
+            if (__builtin_expect(oany, 0)) correct((s - NSB) * 256); // (oany is false at s = 0)
+            __syncthreads(); // the previous chunk's readers of LDS are done
+            mm_copy<KC, TR, 64 * NW>(lds, xg, t0, cols, s * 256, &oflag_s, ++seq);
+            __syncthreads();
+            oany = __builtin_amdgcn_readfirstlane(oflag_s) == seq;
+        }
+        MfQ80 nxt;
+        load_sb(s + 1, s + 1 < nb, nxt);
+        __builtin_amdgcn_sched_barrier(0);
+        superblock(s % NSB, cur);
+        cur = nxt;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (__builtin_expect(oany, 0)) correct((nb - NSB) * 256);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+        if (row < rows) out[(size_t)(t0 + mt * 4 + g) * rows + row] = accf[mt];
+}
+
 // Columns staged per chunk: the largest multiple of 256 whose x for `tokens`
 // tokens fits `budget` bytes of LDS (the workgroup's whole LDS by default).
 static int mf_kc(const soso_hip *h, size_t cols, int tokens, size_t budget = 0)
@@ -1343,13 +1462,39 @@ static int launch_mm_q4k(soso_hip *h, const Weight &w, const float *x, size_t n,
     return hip_check(h, hipGetLastError(), "mm launch");
 }
 
+// Dense Q8_0 with x staged once: 4 wavefronts (64 rows), rounds of 16 tokens,
+// 1024-column chunks, where that grid fills the GPU.  Measured on MI355X,
+// 4096 x 4096 at 64 tokens (us): this shape 37.0; 512- / 2048-column chunks
+// 41.3 / 42.2; rounds of 8 tokens with 4 or 8 wavefronts 48.9 / 49.8;
+// k_mfma_q80 staging its own rounds 46.6.
+constexpr int MQ_NW = 4, MQ_MT = 4, MQ_KC = 1024;
+
+static int launch_mm_q80(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
+{
+    constexpr int NW = MQ_NW, MT = MQ_MT, KC = MQ_KC;
+    const size_t cols = weight_kcols(w), nblk = (w.rows + 16 * NW - 1) / (16 * NW);
+    if (n % (size_t)(4 * MT) || cols % KC || (size_t)4 * MT * mm_tok_bytes(KC) > h->max_lds ||
+        nblk * (n / (4 * MT)) * 5 < (size_t)h->num_cu * 4)
+        return SOSO_HIP_DECLINED; // k_mfma_q80's launch takes it
+    uint8_t *xg = (uint8_t *)scratch_get(h, 16, n * (size_t)mm_tok_bytes((int)cols));
+    if (!xg) return set_err(h, SOSO_HIP_ERR_NOMEM, "mfma: staged x");
+    const size_t waves = n * ((cols + 511) / 512);
+    k_mm_stage<<<(unsigned)((waves + 3) / 4), 256, 0, h->stream>>>(x, (int)n, (int)cols, xg);
+    int rc = hip_check(h, hipGetLastError(), "mm stage launch");
+    if (rc != SOSO_HIP_OK) return rc;
+    const size_t stride = packed_row_stride(w.dtype, cols), lds = (size_t)4 * MT * mm_tok_bytes(KC);
+    k_mm_q80<NW, MT, KC><<<(unsigned)(nblk * (n / (4 * (size_t)MT))), 64 * NW, lds, h->stream>>>(
+        (const uint8_t *)w.dev, stride, (int)w.rows, (int)cols, xg, x, y);
+    return hip_check(h, hipGetLastError(), "mm q80 launch");
+}
+
 int launch_mfma_matmul(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
 {
     const size_t kcols = weight_kcols(w);
     if (!mfma_shape_ok(w.dtype, w.rows, kcols) || n == 0 || n > (1u << 20))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
-    if (w.dtype == SOSO_HIP_DTYPE_Q4_K) {
-        const int rc = launch_mm_q4k(h, w, x, n, y);
+    {
+        const int rc = w.dtype == SOSO_HIP_DTYPE_Q4_K ? launch_mm_q4k(h, w, x, n, y) : launch_mm_q80(h, w, x, n, y);
         if (rc != SOSO_HIP_DECLINED) return rc;
     }
     const size_t cu = (size_t)h->num_cu;
