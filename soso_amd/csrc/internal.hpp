@@ -91,6 +91,10 @@ struct DecodeLayer {
     // (carved from the model's buffer; idx / wgt per layer: the last step's routing)
     const MoeLayer *moe = nullptr;
     MoeScratch moe_s;
+    // the down projection runs as MV_SEG column segments (EPI_PARTS) into the
+    // model's dpart, summed into h by the next launch that stages h (the next
+    // layer's q/k/v or the head, XS_RMSNORM_P4)
+    bool down_parts = false;
 };
 struct DecodeModel {
     size_t n_layers = 0, hidden = 0, n_heads = 0, n_kv_heads = 0, head_dim = 0, ffn = 0, vocab = 0, ctx_max = 0;
@@ -105,6 +109,8 @@ struct DecodeModel {
     void *kcache = nullptr, *vcache = nullptr;  // [n_layers][n_kv_heads][ctx_max][head_dim]
     void *mem = nullptr;                         // activations below, one allocation
     float *hid = nullptr, *att = nullptr, *act = nullptr, *part = nullptr, *logits = nullptr;
+    float *hid2 = nullptr;  // h summed from a segmented down projection (hidden floats)
+    float *dpart = nullptr; // the segmented down projection's partials (MV_SEG x hidden floats)
     float *rope_freq = nullptr; // head_dim / 2 floats
     float *xn = nullptr;        // the MoE layers' normalized x (hidden floats)
     void *moe_mem = nullptr;    // the MoE layers' scratch and routing
@@ -202,12 +208,23 @@ void *scratch_get(soso_hip *h, int slot, size_t bytes);
 void *pinned_get(soso_hip *h, size_t bytes);
 
 // Input and output variants of the matvec kernel (decode-step fusions).
-enum { XS_PLAIN = 0, XS_RMSNORM = 1 };
-enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 3 };
+// XS_RMSNORM_P4: x = ((p0 + p1) + p2) + p3, the four column-segment partials
+// of an EPI_PARTS matvec (parts, MV_SEG rows of cols floats; p0 holds the
+// residual), then RMSNorm as XS_RMSNORM; the summed x also goes to hout (each
+// workgroup writes a share; hout must not alias parts).  in.x is not read.
+// EPI_PARTS: the columns split into MV_SEG segments run by different
+// workgroups; y receives MV_SEG rows of partial sums (segment s at y + s*rows,
+// segment 0's plus ep.res when given), which an XS_RMSNORM_P4 consumer adds in
+// segment order.
+enum { XS_PLAIN = 0, XS_RMSNORM = 1, XS_RMSNORM_P4 = 2 };
+enum { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 3, EPI_PARTS = 4 };
+constexpr int MV_SEG = 4;
 struct MvIn {
     const float *x = nullptr;
     const float *norm_w = nullptr; // XS_RMSNORM: the norm's weight (cols)
     float eps = 0.0f;
+    const float *parts = nullptr; // XS_RMSNORM_P4: MV_SEG partial vectors of cols floats
+    float *hout = nullptr;        // XS_RMSNORM_P4: where the summed x goes
 };
 struct MvEpi {
     const float *res = nullptr; // EPI_RESID: y = res + W.x (res may be y)

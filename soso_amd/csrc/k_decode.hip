@@ -74,6 +74,20 @@ constexpr int ATT_HD = 128;                // head_dim handled
 //   reading the row back (store, wait, barrier)       1.713 / 1.654; 2.166
 //   a separate finishing launch (QK norm / NeoX)                     2.306
 //
+// Streaming loads of cached K/V bytes (the nontemporal bit): every cached
+// row is read once per step and layer.
+typedef uint32_t kv_u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t kv_u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 kv_ld16(const void *p)
+{
+    return __builtin_bit_cast(uint4, __builtin_nontemporal_load((const kv_u32x4 *)p));
+}
+__device__ __forceinline__ uint2 kv_ld8(const void *p)
+{
+    return __builtin_bit_cast(uint2, __builtin_nontemporal_load((const kv_u32x2 *)p));
+}
+__device__ __forceinline__ uint32_t kv_ld4(const void *p) { return __builtin_nontemporal_load((const uint32_t *)p); }
+
 // (a, b) -> (a cos - b sin, a sin + b cos), rope_cabezas' rotation
 // (gemm.rs:1452-1490) with each product rounded on its own.
 __device__ __forceinline__ void turn_pair(float &a, float &b, float cs, float sn)
@@ -245,11 +259,11 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(QkvRows rows
         if constexpr (F16) {
             const uint4 *k4 = (const uint4 *)((const uint16_t *)Kc + row);
 #pragma unroll
-            for (int i = 0; i < 2; i++) kh[a][i] = k4[8 * i + j];
+            for (int i = 0; i < 2; i++) kh[a][i] = kv_ld16(k4 + 8 * i + j);
         } else {
             const float4 *k4 = (const float4 *)((const float *)Kc + row);
 #pragma unroll
-            for (int i = 0; i < 4; i++) kv[a][i] = k4[8 * i + j];
+            for (int i = 0; i < 4; i++) kv[a][i] = __builtin_bit_cast(float4, kv_ld16(k4 + 8 * i + j));
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -265,9 +279,9 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(QkvRows rows
     for (int k = 0; k < PW; k++) {
         const size_t row = head_off + (size_t)min(tw + k, t1 - 1) * HD + 2 * lane;
         if constexpr (F16)
-            vh[k] = *(const uint32_t *)((const uint16_t *)Vc + row);
+            vh[k] = kv_ld4((const uint16_t *)Vc + row);
         else
-            vr[k] = *(const float2 *)((const float *)Vc + row);
+            vr[k] = __builtin_bit_cast(float2, kv_ld8((const float *)Vc + row));
     }
     __builtin_amdgcn_sched_barrier(0);
     qv = finish_q(qv, qw, fr, rows, T);
@@ -581,6 +595,10 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
     const bool direct = ((uintptr_t)x & 15) == 0;
     int rc = direct ? SOSO_HIP_OK
                     : hip_check(h, hipMemcpyAsync(hid, x, m.hidden * 4, hipMemcpyDeviceToDevice, h->stream), "x copy");
+    // pending: hid lacks the last down projection, whose MV_SEG column-segment
+    // partials wait in m.dpart; the next launch that stages h adds them (into
+    // m.hid2, which then holds the layer's input h)
+    bool pending = false;
     for (size_t l = 0; l < m.n_layers && rc == SOSO_HIP_OK; l++) {
         const float *hin = l == 0 && direct ? x : hid;
         const DecodeLayer &L = m.layers[l];
@@ -602,7 +620,13 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         rows.neox = m.rope_neox ? 1 : 0;
         rows.n_heads = (int)m.n_heads;
         rows.n_kv = (int)m.n_kv_heads;
-        rc = launch_matvec_ex(h, *L.qkv, in, m.qkv_raw, MvEpi(), XS_RMSNORM, EPI_STORE);
+        if (pending) {
+            in.parts = m.dpart;
+            in.hout = m.hid2;
+            hin = m.hid2;
+        }
+        rc = launch_matvec_ex(h, *L.qkv, in, m.qkv_raw, MvEpi(), pending ? XS_RMSNORM_P4 : XS_RMSNORM, EPI_STORE);
+        pending = false;
         if (rc == SOSO_HIP_OK)
             rc = launch_attention(h, rows, K, V, m.kv_f16, (int)m.n_heads, (int)m.n_kv_heads, (int)m.head_dim,
                                   (int)m.ctx_max, (int)pos + 1, m.part, att);
@@ -646,7 +670,12 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
                 a.x = act;
                 MvEpi r;
                 r.res = hid;
-                rc = launch_matvec_ex(h, *L.down, a, hid, r, XS_PLAIN, EPI_RESID);
+                if (L.down_parts) {
+                    rc = launch_matvec_ex(h, *L.down, a, m.dpart, r, XS_PLAIN, EPI_PARTS);
+                    pending = true;
+                } else {
+                    rc = launch_matvec_ex(h, *L.down, a, hid, r, XS_PLAIN, EPI_RESID);
+                }
             }
         }
     }
@@ -656,7 +685,11 @@ int decode_step(soso_hip *h, DecodeModel &m, const float *x, uint32_t pos, float
         in.x = hid;
         in.norm_w = m.out_norm;
         in.eps = m.eps;
-        rc = launch_matvec_ex(h, *m.head, in, lg, MvEpi(), XS_RMSNORM, EPI_STORE);
+        if (pending) {
+            in.parts = m.dpart;
+            in.hout = m.hid2;
+        }
+        rc = launch_matvec_ex(h, *m.head, in, lg, MvEpi(), pending ? XS_RMSNORM_P4 : XS_RMSNORM, EPI_STORE);
     }
     if (rc == SOSO_HIP_OK && token) rc = launch_argmax(h, lg, m.vocab, token);
     return rc;

@@ -215,21 +215,32 @@ __device__ __forceinline__ void epilogue(float yacc, int lane, int r, bool ok, f
     }
 }
 
+// EPI_PARTS (column segments): workgroup b takes segment b % MV_SEG of every
+// row (cols / MV_SEG columns, whose x alone it stages) and the row units of
+// group b / MV_SEG as the plain kernel; the segment's sums go to row block
+// b % MV_SEG of y, segment 0's plus the residual ep.res when given.  A row's
+// segments are thus summed by the consumer, so no workgroup converts all of x
+// nor meets the others in LDS.
 template <int FMT, int LPR, int S, int DEPTH, bool XFIRST, int XS = XS_PLAIN, int EPI = EPI_STORE, bool IL = false>
 __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, size_t stride, MvIn in,
                                                float *__restrict__ y, int rows, int cols, MvEpi ep)
 {
     static_assert(S == 1 || !IL, "split rows walk contiguous strips");
+    static_assert(EPI != EPI_PARTS || (S == 1 && LPR == 64 && XS == XS_PLAIN), "column segments: whole wavefronts");
+    constexpr int SEG = EPI == EPI_PARTS ? MV_SEG : 1;
     static_assert(S == 1 || LPR == 64, "split rows use whole wavefronts");
     static_assert(S == 1 || COMBINE_CH % DEPTH == 0, "combine rounds keep the load ring aligned");
     static_assert(S == 1 || EPI == EPI_STORE || EPI == EPI_RESID, "pair epilogues need whole rows per wavefront");
     extern __shared__ uint4 smem[];
-    const float *__restrict__ x = in.x;
-    uint32_t *xp = (uint32_t *)smem;                 // cols/4 groups x XDIG digit dwords
-    float *s16 = (float *)(xp + (cols >> 2) * XDIG);
-    int *kx = (int *)(s16 + (cols >> 4));
+    const int seg = SEG > 1 ? (int)blockIdx.x % SEG : 0;
+    const int bx = SEG > 1 ? (int)blockIdx.x / SEG : (int)blockIdx.x, nbx = (int)gridDim.x / SEG;
+    const int xcols = cols / SEG; // columns of x this workgroup stages
+    const float *__restrict__ x = in.x + (size_t)seg * xcols;
+    uint32_t *xp = (uint32_t *)smem;                 // xcols/4 groups x XDIG digit dwords
+    float *s16 = (float *)(xp + (xcols >> 2) * XDIG);
+    int *kx = (int *)(s16 + (xcols >> 4));
     // after the outlier lists: [groups][COMBINE_CH][S] when S > 1; 16 floats for XS_RMSNORM
-    float *red = (float *)(out_lists(kx, cols) + ((cols + 127) >> 7) * OUT_DW);
+    float *red = (float *)(out_lists(kx, xcols) + ((xcols + 127) >> 7) * OUT_DW);
 
     constexpr int RW = 64 / LPR;
     const int lane = threadIdx.x & 63;
@@ -243,17 +254,18 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     // four rounds built, and the 8B decode step 1.705 / - / 1.688 / 1.728 ms.
     constexpr int XP = S == 1 ? 3 : 4;
     const int grp = wave / S, sw = wave % S;
-    const int U = cols >> 6;
+    const int U = xcols >> 6; // units of the staged x
     const int ul = lane & (LPR - 1), slot = lane / LPR;
     const int ug = sw * 64 + ul;
     const bool uact = ug < U;
-    const int u = uact ? ug : 0;
+    const int u = uact ? ug : 0;  // the lane's unit of the staged x
+    const int uw = seg * U + u;   // ... and of the weight rows
     UConst c;
-    unit_setup_w<FMT>(u, c);
-    const LaneOff L = lane_offsets<FMT>(cols, u, c);
+    unit_setup_w<FMT>(uw, c);
+    const LaneOff L = lane_offsets<FMT>(cols, uw, c);
 
     const int passes = (rows + RW - 1) / RW;
-    const int tg = gridDim.x * gpw;
+    const int tg = nbx * gpw;
     // pair epilogues need whole pairs of rows (2i, 2i + 1) in neighbouring lanes
     constexpr int PU = (RW == 1 && EPI == EPI_SWIGLU) ? 2 : 1;
     static_assert(DEPTH % PU == 0, "a ring turn holds whole units");
@@ -262,7 +274,7 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         q0 = PU * (int)((long)units * g / tg);
         q1 = min(passes, PU * (int)((long)units * (g + 1) / tg));
     };
-    const int g = blockIdx.x * gpw + grp;
+    const int g = bx * gpw + grp;
     // Rows reach the group in units of PU passes.  IL: group g takes units g,
     // g + tg, g + 2 tg, ..., so at every step of the ring the groups of the
     // whole grid read one contiguous stretch of the matrix (on MI355X the
@@ -297,26 +309,40 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     const uint32_t lane_base = uact ? (uint32_t)(slot * stride) : 0x80000000u;
 
     WRow<FMT> buf[DEPTH];
+    float resv = 0.0f; // EPI_PARTS: the residual added to segment 0's sums
     if constexpr (XS == XS_RMSNORM) {
         XPreN<XP> xpre;
         stage_xn_issue<XP>(x, in.norm_w, cols, xpre, NTHR);
 #pragma unroll
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
         stage_xn_finish<FMT, true, XP>(xpre, cols, in.eps, xp, s16, kx, red, NTHR);
+    } else if constexpr (XS == XS_RMSNORM_P4) {
+        XPreNP xpre;
+        stage_xnp_issue(in, cols, xpre, NTHR);
+#pragma unroll
+        for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
+        stage_xnp_finish<FMT, true>(xpre, in, cols, xp, s16, kx, red, NTHR);
     } else if constexpr (XFIRST) {
         // x first: once the weight stream is requested, x's reads would queue
         // behind it in the shared L2 channels.
-        stage_x<FMT, true, XP>(x, cols, xp, s16, kx, NTHR);
+        stage_x<FMT, true, XP>(x, xcols, xp, s16, kx, NTHR);
 #pragma unroll
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
     } else {
         // x's loads, then the ring's, then x's conversion while the ring is
         // in flight (loads return in issue order)
-        XPre<XP> xpre;
-        stage_x_issue<XP>(x, cols, xpre, NTHR);
+        constexpr int XPP = SEG > 1 ? 1 : XP; // a segment is at most 64 units: one round
+        XPre<XPP> xpre;
+        stage_x_issue<XPP>(x, xcols, xpre, NTHR);
+        if constexpr (SEG > 1) {
+            // segment 0 carries the residual of its rows (ep.res), loaded
+            // ahead of the ring so that it costs no wait at the end
+            const int rr = lane_row(lane);
+            if (seg == 0 && ep.res && lane < n * RW && rr < rows) resv = ep.res[rr];
+        }
 #pragma unroll
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
-        stage_x_finish<FMT, true, XP>(xpre, x, cols, xp, s16, kx, NTHR);
+        stage_x_finish<FMT, true, XPP>(xpre, x, xcols, xp, s16, kx, NTHR);
     }
     XReg xv;
     unit_setup_x<FMT, true>(xp, s16, kx, u, U, xv, c);
@@ -353,9 +379,10 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
             }
         }
         if (__builtin_expect(c.onum != 0, 0))
-            yacc += outlier_rows<FMT, LPR>(rs, lane_base, pass_off, 0, n, cols, L, c, u, uact, lane);
+            yacc += outlier_rows<FMT, LPR>(rs, lane_base, pass_off, 0, n, cols, L, c, uw, uact, lane);
         const int r = lane_row(lane);
-        epilogue<EPI>(yacc, lane, r, lane < n * RW && r < rows, y, ep);
+        if constexpr (SEG > 1) yacc = resv + yacc;
+        epilogue<(SEG > 1 ? EPI_STORE : EPI)>(yacc, lane, r, lane < n * RW && r < rows, y + (size_t)seg * rows, ep);
     } else {
         // the same number of combine rounds for every wavefront of the workgroup
         int nmax = 0;
@@ -679,11 +706,15 @@ template <int FMT, int XS, int EPI>
 static void launch_ex_lpr(soso_hip *h, int lpr, bool il, unsigned grid, size_t lds, const uint8_t *W, size_t stride,
                           const MvIn &in, float *y, int rows, int cols, const MvEpi &ep)
 {
-    switch (lpr) {
-    case 8: launch_ex1<FMT, 8, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
-    case 16: launch_ex1<FMT, 16, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
-    case 32: launch_ex1<FMT, 32, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
-    default: launch_ex1<FMT, 64, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+    if constexpr (XS == XS_RMSNORM_P4 || EPI == EPI_PARTS) { // built for whole-wavefront rows only
+        launch_ex1<FMT, 64, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep);
+    } else {
+        switch (lpr) {
+        case 8: launch_ex1<FMT, 8, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+        case 16: launch_ex1<FMT, 16, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+        case 32: launch_ex1<FMT, 32, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+        default: launch_ex1<FMT, 64, XS, EPI>(h, il, grid, lds, W, stride, in, y, rows, cols, ep); break;
+        }
     }
 }
 
@@ -695,6 +726,10 @@ static void launch_ex_fmt(soso_hip *h, int xs, int epi, int lpr, bool il, unsign
         launch_ex_lpr<FMT, XS_RMSNORM, EPI_SWIGLU>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
     else if (xs == XS_PLAIN && epi == EPI_RESID)
         launch_ex_lpr<FMT, XS_PLAIN, EPI_RESID>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
+    else if (xs == XS_PLAIN && epi == EPI_PARTS)
+        launch_ex_lpr<FMT, XS_PLAIN, EPI_PARTS>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
+    else if (xs == XS_RMSNORM_P4)
+        launch_ex_lpr<FMT, XS_RMSNORM_P4, EPI_STORE>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
     else
         launch_ex_lpr<FMT, XS_RMSNORM, EPI_STORE>(h, lpr, il, grid, lds, W, stride, in, y, rows, cols, ep);
 }
@@ -727,12 +762,32 @@ static const char *plan_matvec_ex(const soso_hip *h, uint8_t dtype, size_t rows_
     if (!packed_shape_ok(dtype, rows_, cols_) || rows_ > (1u << 30) || cols_ > (1u << 20))
         return "matvec_ex: shape not handled here";
     if (!(xs == XS_RMSNORM && (epi == EPI_SWIGLU || epi == EPI_STORE)) &&
-        !(xs == XS_PLAIN && epi == EPI_RESID))
+        !(xs == XS_PLAIN && (epi == EPI_RESID || epi == EPI_PARTS)) && !(xs == XS_RMSNORM_P4 && epi == EPI_STORE))
         return "matvec_ex: input/output variant not built";
     const int rows = (int)rows_, cols = (int)cols_, U = cols / 64;
     p.stride = packed_row_stride(dtype, cols_);
     p.S = (U + 63) / 64;
-    if (xs == XS_RMSNORM && cols > 8 * 512) return "matvec_ex: normalised x wider than the staging registers";
+    if ((xs == XS_RMSNORM || xs == XS_RMSNORM_P4) && cols > 8 * 512)
+        return "matvec_ex: normalised x wider than the staging registers";
+    if (xs == XS_RMSNORM_P4 && U <= 32) return "matvec_ex: summed partials built for rows of 33-64 units";
+    if (epi == EPI_PARTS) {
+        // MV_SEG column segments of 33-64 units each, whole 256-column groups
+        // (Q6_K's x layout spans super-blocks; the others' exponents span 128)
+        const int us = U / MV_SEG;
+        if (U % (4 * MV_SEG) || us <= 32 || us > 64) return "matvec_ex: column segments not built for this width";
+        const int gpw = 8, per = std::max(1, h->num_cu / MV_SEG);
+        p.lpr = 64;
+        p.lds = stage_lds_bytes_o(cols_ / MV_SEG) + 64;
+        if (p.lds > h->max_lds) return "matvec_ex: x does not fit in LDS";
+        int grid = std::min(per, (rows + gpw - 1) / gpw);
+        grid = std::max(grid, ((rows + 63) / 64 + gpw - 1) / gpw); // at most 64 rows per group
+        p.grid = MV_SEG * std::max(grid, 1);
+        p.S = 1;
+        if (!strip_fits(rows, grid * gpw, p.stride)) return "matvec_ex: row strip exceeds 2 GiB";
+        p.il = interleave_fits(rows, 1, grid * gpw, p.stride);
+        if (!p.il) return "matvec_ex: matrix too large for the interleaved rows of this variant";
+        return nullptr;
+    }
     if (epi == EPI_SWIGLU && (p.S != 1 || rows % 2))
         return "matvec_ex: pair epilogue needs whole rows per wavefront";
     if (p.S > 1) {

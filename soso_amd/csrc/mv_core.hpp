@@ -393,6 +393,62 @@ __device__ void stage_xn_finish(const XPreN<XP> &p, int cols, float eps, uint32_
     __syncthreads();
 }
 
+// XS_RMSNORM_P4: x is the sum of the MV_SEG column-segment partials of the
+// matvec that produced them (segment 0's with the residual in it), added in
+// segment order: ((p0 + p1) + p2) + p3.  One round (cols <= 8 * nthr).
+// Workgroup b writes the sums of the chunks c with c % gridDim.x == b to hout,
+// so every chunk is written once.
+struct XPreNP {
+    float4 w[2], p[MV_SEG][2];
+};
+
+__device__ __forceinline__ void stage_xnp_issue(const MvIn &in, int cols, XPreNP &p, int nthr)
+{
+    const int nch = cols >> 3, c = threadIdx.x;
+    const float4 *w4 = (const float4 *)in.norm_w;
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+    p.w[0] = p.w[1] = z;
+#pragma unroll
+    for (int s = 0; s < MV_SEG; s++) p.p[s][0] = p.p[s][1] = z;
+    if (c < nch) {
+#pragma unroll
+        for (int s = 0; s < MV_SEG; s++) {
+            const float4 *p4 = (const float4 *)(in.parts + (size_t)s * cols);
+            p.p[s][0] = p4[2 * c];
+            p.p[s][1] = p4[2 * c + 1];
+        }
+        p.w[0] = w4[2 * c];
+        p.w[1] = w4[2 * c + 1];
+    }
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b)
+{
+    return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+template <int FMT, bool OUTL>
+__device__ void stage_xnp_finish(const XPreNP &p, const MvIn &in, int cols, uint32_t *xp, float *s16, int *kx,
+                                 float *red, int nthr)
+{
+    XPreN<1> q;
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        float4 acc = p.p[0][k];
+#pragma unroll
+        for (int s = 1; s < MV_SEG; s++) acc = add4(acc, p.p[s][k]);
+        q.v[k] = acc;
+        q.w[k] = p.w[k];
+    }
+    const int c = threadIdx.x;
+    if (c < (cols >> 3) && c % (int)gridDim.x == (int)blockIdx.x) {
+        float4 *h4 = (float4 *)in.hout;
+        h4[2 * c] = q.v[0];
+        h4[2 * c + 1] = q.v[1];
+    }
+    stage_xn_finish<FMT, OUTL, 1>(q, cols, in.eps, xp, s16, kx, red, nthr);
+}
+
 template <int FMT, bool OUTL, int XP>
 __device__ __forceinline__ void stage_x(const float *__restrict__ x, int cols, uint32_t *xp, float *s16, int *kx,
                                         int nthr)

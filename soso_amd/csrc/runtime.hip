@@ -1048,6 +1048,10 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
                                                          why);
         m.layers[l].attn_norm = (const float *)an->dev;
         m.layers[l].ffn_norm = (const float *)fn->dev;
+        // a segmented down projection where it is built; whether its
+        // consumer (the next q/k/v or the head) sums the partials is settled
+        // once the whole stack is known
+        m.layers[l].down_parts = !is_moe && !matvec_ex_unsupported(h, m.layers[l].down->dtype, H, F, XS_PLAIN, EPI_PARTS);
         m.layers[l].q_norm = qn ? (const float *)qn->dev : nullptr;
         m.layers[l].k_norm = kn ? (const float *)kn->dev : nullptr;
     }
@@ -1058,6 +1062,14 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
         if (const char *why = matvec_ex_unsupported(h, m.head->dtype, cfg->vocab, H, XS_RMSNORM, EPI_STORE))
             return set_err(h, SOSO_HIP_DECLINED, std::string("decode_create: head: ") + why);
         m.out_norm = (const float *)on->dev;
+    }
+    // the consumer of each segmented down projection must take the partials
+    for (size_t l = 0; l < L; l++) {
+        DecodeLayer &dl = m.layers[l];
+        if (!dl.down_parts) continue;
+        if (l + 1 < L)
+            dl.down_parts = !matvec_ex_unsupported(h, q[l + 1]->dtype, qd + 2 * kvd, H, XS_RMSNORM_P4, EPI_STORE);
+        else dl.down_parts = m.head && !matvec_ex_unsupported(h, m.head->dtype, cfg->vocab, H, XS_RMSNORM_P4, EPI_STORE);
     }
     // what stays in use (dropping one of these unregisters the model)
     for (size_t l = 0; l < L; l++) {
@@ -1119,7 +1131,7 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     const size_t kv_bytes = L * cfg->ctx_max * kvd * (m.kv_f16 ? 2 : 4);
     const size_t chunks = 1 + (cfg->ctx_max + ATT_CHUNK - 1) / ATT_CHUNK; // attention partials per head, at most
     const size_t act_floats = H + (qd + 2 * kvd) + qd + F + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2) +
-                              m.vocab + 64 + cfg->head_dim / 2 + H;
+                              m.vocab + 64 + cfg->head_dim / 2 + H + H + (size_t)MV_SEG * H;
     // MoE scratch (shared by the MoE layers, which run one after another) and
     // each layer's routing of the last step (256-byte slots)
     const size_t moe_route_bytes = 512;
@@ -1147,6 +1159,8 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
     m.logits = m.part + (size_t)cfg->n_heads * chunks * (cfg->head_dim + 2);
     m.rope_freq = m.logits + m.vocab + 64;
     m.xn = m.rope_freq + cfg->head_dim / 2;
+    m.hid2 = m.xn + H;
+    m.dpart = m.hid2 + H;
     for (size_t l = 0, j = 0; l < L; l++) {
         DecodeLayer &dl = m.layers[l];
         if (!dl.moe) continue;
