@@ -267,10 +267,16 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(QkvRows rows
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+    // only the wavefronts holding q (one float4 per thread) finish it
+    constexpr int QW = (G * HD / 4 + 63) / 64;
+    const bool qwave = wave < QW;
     float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), qw = make_float4(1.f, 1.f, 1.f, 1.f);
-    if (tid < G * HD / 4) qv = ((const float4 *)qsrc)[tid];
-    if (rows.qn) qw = ((const float4 *)rows.qn)[lane & 31];
-    const float fr = rows.freq[lane];
+    float fr = 0.0f;
+    if (qwave) {
+        if (tid < G * HD / 4) qv = ((const float4 *)qsrc)[tid];
+        if (rows.qn) qw = ((const float4 *)rows.qn)[lane & 31];
+        fr = rows.freq[lane];
+    }
     __builtin_amdgcn_sched_barrier(0);
     // V: lane l holds dims 2l, 2l + 1 of the wavefront's PW positions
     float2 vr[PW];
@@ -284,8 +290,10 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(QkvRows rows
             vr[k] = __builtin_bit_cast(float2, kv_ld8((const float *)Vc + row));
     }
     __builtin_amdgcn_sched_barrier(0);
-    qv = finish_q(qv, qw, fr, rows, T);
-    if (tid < G * HD / 4) *(float4 *)&qs[4 * tid] = qv;
+    if (qwave) {
+        qv = finish_q(qv, qw, fr, rows, T);
+        if (tid < G * HD / 4) *(float4 *)&qs[4 * tid] = qv;
+    }
     if constexpr (F16) {
         // f16 -> f32 is exact; from here on the math is the f32 kernel's
 #pragma unroll
@@ -345,16 +353,19 @@ __global__ void __launch_bounds__(64 * ATT_CHUNK / PW) k_attn_split(QkvRows rows
         }
     }
     __syncthreads();
-    for (int e = tid; e < G * HD / 2; e += NT) {
+    for (int e = tid; e < G * HD / 2; e += NT) { // a whole wavefront per head hh
         const int hh = e / (HD / 2), dl = e % (HD / 2);
         float M = wm[0][hh];
 #pragma unroll
         for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w][hh]);
+        // lane w < NW takes wavefront w's factor, read by every lane of the head
+        const float mw = wm[lane < NW ? lane : 0][hh];
+        const float fw = mw == -INFINITY ? 0.0f : expf(mw - M);
         float L = 0.0f;
         float2 a = make_float2(0.f, 0.f);
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float f = wm[w][hh] == -INFINITY ? 0.0f : expf(wm[w][hh] - M);
+            const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fw), w));
             L = fmaf(f, wl[w][hh], L);
             a.x = fmaf(f, accs[w][hh][dl].x, a.x);
             a.y = fmaf(f, accs[w][hh][dl].y, a.y);
@@ -401,9 +412,15 @@ __global__ void __launch_bounds__(256) k_attn_merge(const float *__restrict__ pa
         l *= r;
         acc.x *= r;
         acc.y *= r;
+        // the batch's weights are uniform: lane k computes chunk k's, every
+        // lane reads them (one expf per lane instead of MERGE_B)
+        float mk = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < MERGE_B; k++) mk = lane == k && k < n ? ml[k].x : mk;
+        const float wk = mk == -INFINITY ? 0.0f : expf(mk - bm);
 #pragma unroll
         for (int k = 0; k < MERGE_B; k++) {
-            const float w = k < n ? expf(ml[k].x - bm) : 0.0f;
+            const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wk), k));
             l = fmaf(w, ml[k].y, l);
             acc.x = fmaf(w, v[k].x, acc.x);
             acc.y = fmaf(w, v[k].y, acc.y);
@@ -420,11 +437,13 @@ __global__ void __launch_bounds__(256) k_attn_merge(const float *__restrict__ pa
         float M = wm[0];
 #pragma unroll
         for (int w = 1; w < NW; w++) M = fmaxf(M, wm[w]);
+        const float mw = wm[lane < NW ? lane : 0];
+        const float fw = mw == -INFINITY ? 0.0f : expf(mw - M);
         float L = 0.0f;
         float2 a = make_float2(0.f, 0.f);
 #pragma unroll
         for (int w = 0; w < NW; w++) {
-            const float f = wm[w] == -INFINITY ? 0.0f : expf(wm[w] - M);
+            const float f = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, fw), w));
             L = fmaf(f, wl[w], L);
             a.x = fmaf(f, accs[w][lane].x, a.x);
             a.y = fmaf(f, accs[w][lane].y, a.y);

@@ -336,7 +336,10 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
         stage_x_issue<XPP>(x, xcols, xpre, NTHR);
         if constexpr (SEG > 1) {
             // segment 0 carries the residual of its rows (ep.res), loaded
-            // ahead of the ring so that it costs no wait at the end
+            // behind x and ahead of the ring.  Measured on MI355X (8B decode
+            // step): 1.522 ms per token, 1.529 with the load at the end.  The
+            // EPI_RESID epilogue keeps its load at the end: loaded here or
+            // behind the ring the step took 1.548 / 1.557 ms.
             const int rr = lane_row(lane);
             if (seg == 0 && ep.res && lane < n * RW && rr < rows) resv = ep.res[rr];
         }
