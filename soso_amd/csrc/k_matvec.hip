@@ -311,11 +311,12 @@ __global__ void __launch_bounds__(512) mv_rows(const uint8_t *__restrict__ W, si
     WRow<FMT> buf[DEPTH];
     float resv = 0.0f; // EPI_PARTS: the residual added to segment 0's sums
     if constexpr (XS == XS_RMSNORM) {
-        XPreN<XP> xpre;
-        stage_xn_issue<XP>(x, in.norm_w, cols, xpre, NTHR);
+        // one round: normalised rows are at most 8 * NTHR columns wide
+        XPreN<1> xpre;
+        stage_xn_issue<1>(x, in.norm_w, cols, xpre, NTHR);
 #pragma unroll
         for (int i = 0; i < DEPTH; i++) load_row<FMT>(rs, lane_base + pass_off(i), cols, L, buf[i]);
-        stage_xn_finish<FMT, true, XP>(xpre, cols, in.eps, xp, s16, kx, red, NTHR);
+        stage_xn_finish<FMT, true, 1>(xpre, cols, in.eps, xp, s16, kx, red, NTHR);
     } else if constexpr (XS == XS_RMSNORM_P4) {
         XPreNP xpre;
         stage_xnp_issue(in, cols, xpre, NTHR);
@@ -811,8 +812,9 @@ static const char *plan_matvec_ex(const soso_hip *h, uint8_t dtype, size_t rows_
     p.lds = stage_lds_bytes_o(cols_) + 64;
     if (p.lds > h->max_lds) return "matvec_ex: x does not fit in LDS";
     // two workgroups per CU for the gate/up pair (2 x 14336 x 4096 on MI355X:
-    // 15.2 us, 15.9 us at one per CU); one for the others (qkv, o and the head
-    // were slower at two)
+    // 15.2 us, 15.9 us at one per CU; in the 8B step three or four per CU took
+    // 5 / 8 % longer, and one workgroup of 1024 threads per CU 4 %); one for
+    // the others (qkv, o and the head were slower at two)
     const int wg_per_cu = epi == EPI_SWIGLU ? 2 : 1;
     int grid = std::min(h->num_cu * wg_per_cu, (units + gpw - 1) / gpw);
     const int upw = 64 / (PU * RW); // units per 64-row strip
