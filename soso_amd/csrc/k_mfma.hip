@@ -1432,8 +1432,14 @@ static const int MF_DENSE[9][2] = {{4, 1}, {8, 1}, {4, 2}, {8, 2}, {16, 1}, {4, 
 // this shape 56.3-56.7; 2048-column chunks 59.3; 512: 58.9; 256: 76.7;
 // 8 wavefronts x 32 tokens 60.8, x 16 tokens 64.6-69.0; 4 wavefronts x 16
 // tokens 72.1; 4 x 64 (1 wavefront per SIMD) 120.8; 16 x 8 tokens 88.3;
-// k_mfma_q4k staging its own rounds 68.1-68.3.
-constexpr int MM_NW = 16, MM_MT = 4, MM_KC = 1024, MM_LA = 1;
+// k_mfma_q4k staging its own rounds 68.1-68.3.  The wavefront count is then
+// chosen per shape among MM_NWS so that the workgroups fill the CUs best (one
+// per CU; each CU's work is one workgroup's): 14336 rows at 64 tokens take 14
+// wavefronts (224 rows, 64 row blocks x 4 rounds = 256 workgroups): 48.1 us
+// against 51.1 with 16 (224 workgroups); 12 (300 workgroups, two per CU on
+// some) 76.8 us.
+constexpr int MM_MT = 4, MM_KC = 1024, MM_LA = 1;
+constexpr int MM_NWS[3] = {16, 14, 12};
 
 template <int NW, int MT, int KC, int LAH>
 static void mm_launch(soso_hip *h, const Weight &w, size_t stride, const uint8_t *xg, const float *x, float *y,
@@ -1446,10 +1452,24 @@ static void mm_launch(soso_hip *h, const Weight &w, size_t stride, const uint8_t
 
 static int launch_mm_q4k(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
 {
-    constexpr int NW = MM_NW, MT = MM_MT, KC = MM_KC, LAH = MM_LA;
-    const size_t cols = weight_kcols(w), nblk = (w.rows + 16 * NW - 1) / (16 * NW);
+    constexpr int MT = MM_MT, KC = MM_KC, LAH = MM_LA;
+    const size_t cols = weight_kcols(w), rounds = n / (4 * MT), cu = (size_t)h->num_cu;
+    // the wavefront count whose workgroups keep the CUs busiest: rows over
+    // (passes of one workgroup per CU x CUs x rows per workgroup), the larger
+    // count on ties
+    int NW = MM_NWS[0];
+    double best = -1.0;
+    for (int nw : MM_NWS) {
+        const size_t g = (w.rows + 16 * nw - 1) / (16 * nw) * rounds, passes = (g + cu - 1) / cu;
+        const double eff = (double)w.rows * (double)rounds / ((double)passes * (double)cu * 16.0 * nw);
+        if (eff > best + 1e-9) {
+            best = eff;
+            NW = nw;
+        }
+    }
+    const size_t nblk = (w.rows + 16 * NW - 1) / (16 * NW);
     if (n % (size_t)(4 * MT) || cols % KC || (size_t)4 * MT * mm_tok_bytes(KC) > h->max_lds ||
-        nblk * (n / (4 * MT)) * 5 < (size_t)h->num_cu * 4)
+        nblk * rounds * 5 < cu * 4)
         return SOSO_HIP_DECLINED; // k_mfma_q4k's launch, which picks its shape from the grid, takes it
     uint8_t *xg = (uint8_t *)scratch_get(h, 16, n * (size_t)mm_tok_bytes((int)cols));
     if (!xg) return set_err(h, SOSO_HIP_ERR_NOMEM, "mfma: staged x");
@@ -1458,7 +1478,12 @@ static int launch_mm_q4k(soso_hip *h, const Weight &w, const float *x, size_t n,
     int rc = hip_check(h, hipGetLastError(), "mm stage launch");
     if (rc != SOSO_HIP_OK) return rc;
     const size_t stride = packed_row_stride(w.dtype, cols);
-    mm_launch<NW, MT, KC, LAH>(h, w, stride, xg, x, y, (unsigned)(nblk * (n / (4 * (size_t)MT))));
+    const unsigned grid = (unsigned)(nblk * rounds);
+    switch (NW) {
+    case 16: mm_launch<16, MT, KC, LAH>(h, w, stride, xg, x, y, grid); break;
+    case 14: mm_launch<14, MT, KC, LAH>(h, w, stride, xg, x, y, grid); break;
+    default: mm_launch<12, MT, KC, LAH>(h, w, stride, xg, x, y, grid); break;
+    }
     return hip_check(h, hipGetLastError(), "mm launch");
 }
 
