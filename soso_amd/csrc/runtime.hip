@@ -1042,10 +1042,17 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
                      {g[l], 2 * F, H, XS_RMSNORM, EPI_SWIGLU, "gate/up"},
                      {m.layers[l].down, H, F, XS_PLAIN, EPI_RESID, "down"}};
         for (const auto &r : roles)
-            if (r.w && (!is_moe || r.w == q[l] || r.w == m.layers[l].o))
-                if (const char *why = matvec_ex_unsupported(h, r.w->dtype, r.rows, r.cols, r.xs, r.epi))
-                return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + " " + r.role + ": " +
-                                                         why);
+            if (r.w && (!is_moe || r.w == q[l] || r.w == m.layers[l].o)) {
+                const char *why = matvec_ex_unsupported(h, r.w->dtype, r.rows, r.cols, r.xs, r.epi);
+                // a down projection the split-row form does not take may still
+                // run as column segments (whose consumer is checked below)
+                if (why && r.w == m.layers[l].down &&
+                    !matvec_ex_unsupported(h, r.w->dtype, r.rows, r.cols, XS_PLAIN, EPI_PARTS))
+                    why = nullptr;
+                if (why)
+                    return set_err(h, SOSO_HIP_DECLINED,
+                                   "decode_create: layer " + std::to_string(l) + " " + r.role + ": " + why);
+            }
         m.layers[l].attn_norm = (const float *)an->dev;
         m.layers[l].ffn_norm = (const float *)fn->dev;
         // a segmented down projection where it is built; whether its
@@ -1063,13 +1070,17 @@ static int decode_create_impl(soso_hip *h, const char *model_key, size_t model_k
             return set_err(h, SOSO_HIP_DECLINED, std::string("decode_create: head: ") + why);
         m.out_norm = (const float *)on->dev;
     }
-    // the consumer of each segmented down projection must take the partials
+    // the consumer of each segmented down projection must take the partials;
+    // where it cannot, the split-row form runs the projection, if it can
     for (size_t l = 0; l < L; l++) {
         DecodeLayer &dl = m.layers[l];
         if (!dl.down_parts) continue;
         if (l + 1 < L)
             dl.down_parts = !matvec_ex_unsupported(h, q[l + 1]->dtype, qd + 2 * kvd, H, XS_RMSNORM_P4, EPI_STORE);
         else dl.down_parts = m.head && !matvec_ex_unsupported(h, m.head->dtype, cfg->vocab, H, XS_RMSNORM_P4, EPI_STORE);
+        if (!dl.down_parts)
+            if (const char *why = matvec_ex_unsupported(h, dl.down->dtype, H, F, XS_PLAIN, EPI_RESID))
+                return set_err(h, SOSO_HIP_DECLINED, "decode_create: layer " + std::to_string(l) + " down: " + why);
     }
     // what stays in use (dropping one of these unregisters the model)
     for (size_t l = 0; l < L; l++) {

@@ -368,6 +368,54 @@ def test_decode_create_declines_what_the_step_cannot_run(gpu, orc, case):
             gpu.weight_drop(k)
 
 
+@pytest.mark.parametrize("dt", [
+    {"q": Q8, "k": Q8, "v": Q8, "down": Q8, "head": Q8},
+    {"q": Q6K, "k": Q6K, "v": Q6K, "down": Q6K, "head": Q6K},
+    {"head": Q4K},
+])
+def test_decode_step_segmented_down(gpu, orc, dt):
+    """Hidden 3072, FFN 9216: the width at which the step runs each down
+    projection as four column segments whose partials the next layer's q/k/v
+    staging (and, after the last layer, the head's) sums with the residual.
+    Every format takes both sides of that hand-over here (the 8B tests cover
+    Q4_K at 4096 x 14336).  Same bar: logits within relative L2 1e-5 of the
+    oracle's composition, the greedy token checked."""
+    L, H, nh, nkv, F, V, prefill, ctx, theta, eps = 2, 3072, 24, 6, 9216, 777, 70, 128, 500000.0, 1e-5
+    m = Model(orc, L, H, nh, nkv, F, V, 700, dt=dt)
+    m.upload(gpu)
+    name = m.name + ".model"
+    cfg = dict(n_layers=L, hidden=H, n_heads=nh, n_kv_heads=nkv, head_dim=HD, ffn=F, vocab=V, ctx_max=ctx,
+               rope_theta=theta, rms_eps=eps)
+    print(f"decode step segmented down {dt}", flush=True)
+    assert gpu.decode_create(name, cfg, m.keys), gpu.last_error()
+    kc = np.zeros((L, ctx, m.kvd), np.float32)
+    vc = np.zeros((L, ctx, m.kvd), np.float32)
+    xd, ld, td = gpu.dev_alloc(H * 4), gpu.dev_alloc(V * 4), gpu.dev_alloc(4)
+    try:
+        for l in range(L):
+            kr = orc.normal(prefill * m.kvd, 1.0, 710 + l, 1).reshape(prefill, m.kvd)
+            vr = orc.normal(prefill * m.kvd, 1.0, 710 + l, 2).reshape(prefill, m.kvd)
+            gpu.decode_kv_upload(name, l, 0, kr, vr, rows_f32=True)
+            kc[l, :prefill], vc[l, :prefill] = kr, vr
+        x = orc.normal(H, 1.0, 720, 1)
+        gpu.h2d(xd, x)
+        assert gpu.decode_step_dev(name, xd, prefill, ld, td), gpu.last_error()
+        gpu.sync()
+        logits = gpu.d2h(ld, (V,), np.float32)
+        token = int(gpu.d2h(td, (1,), np.uint32)[0])
+        ref, ref_token = m.cpu_step(orc, x, kc, vc, prefill, theta, eps)
+        err = orc.rel_l2(logits, ref)
+        print(f"  logits rel_l2 {err:.3e}", flush=True)
+        assert err < 1e-5, err
+        check_greedy(orc, token, logits, ref_token, ref)
+    finally:
+        for p in (xd, ld, td):
+            gpu.dev_free(p)
+        gpu.decode_destroy(name)
+        for k in m.keys:
+            gpu.weight_drop(k)
+
+
 @pytest.mark.parametrize("kv_f16", [0, 1])
 def test_decode_8b_layer_shape_matches_cpu(gpu, orc, kv_f16):
     """configs[4] at its real layer shape and context: one layer of hidden 4096,
