@@ -572,21 +572,33 @@ int soso_hip_router_topk(soso_hip *h, const char *key, size_t key_len, const flo
     // block's routing copied out before the next overwrites the scratch
     const size_t nb = std::min(n, moe_block_tokens(top_k));
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
+    // x, idx and wgt pass through the pinned staging buffer (the caller's
+    // buffers are pageable: the runtime's own staging of each copy is slow)
+    float *hx = (float *)pinned_get(h, (n * hdim + 2 * n * top_k) * 4);
     MoeScratch ms;
-    if (!xd || !moe_scratch(h, nb, n_exp, top_k, 0, 0, ms)) return set_err(h, SOSO_HIP_ERR_NOMEM, "router: scratch");
-    rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
+    if (!xd || !hx || !moe_scratch(h, nb, n_exp, top_k, 0, 0, ms))
+        return set_err(h, SOSO_HIP_ERR_NOMEM, "router: scratch");
+    int32_t *hidx = (int32_t *)(hx + n * hdim);
+    float *hwgt = (float *)(hidx + n * top_k);
+    memcpy(hx, xs, n * hdim * 4);
+    rc = hip_check(h, hipMemcpyAsync(xd, hx, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
     for (size_t t0 = 0; t0 < n && rc == SOSO_HIP_OK; t0 += nb) {
         const size_t m = std::min(nb, n - t0);
         rc = launch_moe_route(h, (const float *)wd, xd + t0 * hdim, m, hdim, n_exp, top_k, ms);
         if (rc == SOSO_HIP_OK)
-            rc = hip_check(h, hipMemcpyAsync(idx + t0 * top_k, ms.idx, m * top_k * 4, hipMemcpyDeviceToHost, h->stream),
+            rc = hip_check(h, hipMemcpyAsync(hidx + t0 * top_k, ms.idx, m * top_k * 4, hipMemcpyDeviceToHost, h->stream),
                            "idx");
         if (rc == SOSO_HIP_OK)
-            rc = hip_check(h, hipMemcpyAsync(wgt + t0 * top_k, ms.wgt, m * top_k * 4, hipMemcpyDeviceToHost, h->stream),
+            rc = hip_check(h, hipMemcpyAsync(hwgt + t0 * top_k, ms.wgt, m * top_k * 4, hipMemcpyDeviceToHost, h->stream),
                            "wgt");
     }
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "router sync");
-    if (rc != SOSO_HIP_OK) return rc;
+    if (rc != SOSO_HIP_OK) {
+        (void)hip_release(h, hipStreamSynchronize(h->stream), "router drain");
+        return rc;
+    }
+    memcpy(idx, hidx, n * top_k * 4);
+    memcpy(wgt, hwgt, n * top_k * 4);
     h->stats.bytes_up += n * hdim * 4;
     h->stats.bytes_down += n * top_k * 8;
     clk.done();
@@ -692,24 +704,33 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
     }
     float *xd = (float *)scratch_get(h, 0, n * hdim * 4);
     float *sd = (float *)scratch_get(h, 5, n * hdim * 4);
-    char *aux = (char *)scratch_get(h, 11, slots * 4 + slots + 3 * G * sizeof(void *) + 64);
+    // the weights, tables and slot marks sit together in aux (one upload)
+    const size_t tab_off = (slots * 4 + 15) & ~(size_t)15, aux_bytes = tab_off + 3 * G * sizeof(void *) + slots;
+    char *aux = (char *)scratch_get(h, 11, aux_bytes + 64);
+    // every host-side buffer passes through the pinned staging buffer: x, the
+    // groups, aux's image, then the sum on its way back
+    const size_t x_b = (n * hdim * 4 + 15) & ~(size_t)15, ints_b = (ints.size() * 4 + 15) & ~(size_t)15,
+                 aux_b = (aux_bytes + 15) & ~(size_t)15;
+    char *hs = (char *)pinned_get(h, x_b + ints_b + aux_b + n * hdim * 4);
     MoeScratch ms;
-    if (!xd || !sd || !aux || !moe_scratch(h, n, G, top_k, hdim, ffn, ms))
+    if (!xd || !sd || !aux || !hs || !moe_scratch(h, n, G, top_k, hdim, ffn, ms))
         return set_err(h, SOSO_HIP_ERR_NOMEM, "experts_block: scratch");
     float *wd = (float *)aux;
-    const uint8_t **tabd = (const uint8_t **)(aux + ((slots * 4 + 15) & ~(size_t)15));
+    const uint8_t **tabd = (const uint8_t **)(aux + tab_off);
     uint8_t *used = (uint8_t *)(tabd + 3 * G);
-    rc = hip_check(h, hipMemcpyAsync(xd, xs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
-    if (rc == SOSO_HIP_OK)
-        rc = hip_check(h, hipMemcpyAsync(wd, wgt, slots * 4, hipMemcpyHostToDevice, h->stream), "wgt upload");
+    char *hints = hs + x_b, *haux = hints + ints_b;
+    float *hsum = (float *)(haux + aux_b);
+    memcpy(hs, xs, n * hdim * 4);
+    if (G) memcpy(hints, ints.data(), ints.size() * 4);
+    memcpy(haux, wgt, slots * 4);
+    if (G) memcpy(haux + tab_off, tab.data(), tab.size() * sizeof(void *));
+    memcpy(haux + tab_off + 3 * G * sizeof(void *), use.data(), slots);
+    rc = hip_check(h, hipMemcpyAsync(xd, hs, n * hdim * 4, hipMemcpyHostToDevice, h->stream), "x upload");
     if (rc == SOSO_HIP_OK && G)
-        rc = hip_check(h, hipMemcpyAsync(ms.cnt, ints.data(), ints.size() * 4, hipMemcpyHostToDevice, h->stream),
+        rc = hip_check(h, hipMemcpyAsync(ms.cnt, hints, ints.size() * 4, hipMemcpyHostToDevice, h->stream),
                        "groups upload");
-    if (rc == SOSO_HIP_OK && G)
-        rc = hip_check(h, hipMemcpyAsync(tabd, tab.data(), tab.size() * sizeof(void *), hipMemcpyHostToDevice, h->stream),
-                       "tables upload");
     if (rc == SOSO_HIP_OK)
-        rc = hip_check(h, hipMemcpyAsync(used, use.data(), slots, hipMemcpyHostToDevice, h->stream), "slots upload");
+        rc = hip_check(h, hipMemcpyAsync(aux, haux, aux_bytes, hipMemcpyHostToDevice, h->stream), "aux upload");
     if (rc == SOSO_HIP_OK) {
         if (G)
             rc = launch_moe_experts(h, xd, n, hdim, ffn, top_k, dt_gu, dt_dn, tabd, G, wd, used, nullptr, ms, sd);
@@ -719,12 +740,13 @@ int soso_hip_experts_block(soso_hip *h, const float *xs, size_t n, size_t hdim, 
     // the shared expert of the same block (moe_shared, gpu.rs:518-521) joins
     // the sum after the ranked experts, as soso adds it last (bloque35.rs:1000-1005)
     if (rc == SOSO_HIP_OK && pending) rc = launch_vec_add(h, sd, (const float *)h->scratch[12], n * hdim);
-    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(sum, sd, n * hdim * 4, hipMemcpyDeviceToHost, h->stream), "sum");
+    if (rc == SOSO_HIP_OK) rc = hip_check(h, hipMemcpyAsync(hsum, sd, n * hdim * 4, hipMemcpyDeviceToHost, h->stream), "sum");
     if (rc == SOSO_HIP_OK) rc = hip_check(h, hipStreamSynchronize(h->stream), "experts sync");
     if (rc != SOSO_HIP_OK) {
         (void)hip_release(h, hipStreamSynchronize(h->stream), "experts drain");
         return rc;
     }
+    memcpy(sum, hsum, n * hdim * 4);
     for (size_t e = 0; e < n_exps; e++) done[e] = ok[e];
     h->stats.bytes_up += n * hdim * 4 + slots * 4;
     h->stats.bytes_down += n * hdim * 4;
