@@ -200,7 +200,8 @@ __device__ __forceinline__ void mf_write(uint8_t *tp, int c, int kc, const uint3
         uint8_t *dp = tp + (sbl >> 1) * 256 + 16 * qq + 8 * (sbl & 1);
 #pragma unroll
         for (int kk = 0; kk < XDIG; kk++) *(uint2 *)(dp + 64 * kk) = make_uint2(d0[kk], d1[kk]);
-        *(uint2 *)(dp + 64 * XDIG) = make_uint2(0u, 0u);
+        // (bytes 192 .. 255 of each 256, the A operand's zero pad, are left
+        // unwritten: the matmul kernels clear them in LDS once, mm_zero_pad)
         if (qq == 0) *(float *)(tp + mm_sum_off(kc) + 4 * sbl) = sm;
         if ((c & 31) == 0)
             *(float *)(tp + mm_p_off(kc) + 4 * (c >> 5)) = finite ? ldexpf(1.0f, -ex) : __builtin_nanf("");
@@ -829,17 +830,35 @@ __global__ void __launch_bounds__(256) k_mm_stage(const float *__restrict__ x, i
     else (void)mf_chunk<false, true>(v0, v1, tp, c, cols, valid);
 }
 
+// The zero pad of the A operand (digit plane 3: 64 bytes of every 256 of a
+// token's digits) for tokens 0 .. TR - 1 of a chunk buffer in LDS: cleared
+// once per workgroup, mm_copy never writes it.
+template <int KC, int TR, int NT>
+__device__ __forceinline__ void mm_zero_pad(uint8_t *lds)
+{
+    constexpr int tb = mm_tok_bytes(KC), PADW = KC / 16; // 16-byte pad words per token
+    for (int i = (int)threadIdx.x; i < TR * PADW; i += NT) {
+        const int t = i / PADW, u = i % PADW;
+        *(uint4 *)(lds + (size_t)t * tb + 256 * (u >> 2) + 192 + 16 * (u & 3)) = make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
 // Copies columns k0 .. k0 + KC of tokens t0 .. t0 + TR - 1 from the staged rows
 // (xg, mm_tok_bytes(cols) bytes per token) into LDS (mm_tok_bytes(KC) per
 // token, the same layout for the chunk); a thread that copies a nonzero
 // outlier mask word writes seq into *oflag.  cols, k0 and KC are multiples of
 // 256, so every region but the 2^-e one moves in 16-byte words: MB of them per
 // thread are requested before any is stored, so a batch costs one round trip.
+// The digits' zero pad (mm_zero_pad) is not copied: per 256 bytes, words 0 ..
+// 11 (planes 0 .. 2) move and 12 .. 15 stay.  On MI355X, 64 tokens, per call:
+// Q8_0 4096 x 4096 34.7 -> 32.8 us, Q4_K 14336 x 4096 47.8 -> 47.2 us (the
+// Q8_0 kernel is bound by the bytes each CU pulls through its L1, about 8 per
+// cycle: 64 rows of weights and 16 tokens of staged x per workgroup).
 template <int KC, int TR, int NT>
 __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict__ xg, int t0, int cols, int k0,
                                         int *oflag, int seq)
 {
-    constexpr int tb = mm_tok_bytes(KC), DW = KC / 4, SW = KC / 128, MW = KC / 128, PW = KC / 256;
+    constexpr int tb = mm_tok_bytes(KC), DW = KC * 3 / 16, SW = KC / 128, MW = KC / 128, PW = KC / 256;
     // MB words per thread in flight: on MI355X, 64 tokens, 4 / 8 / 16: Q8_0
     // 4096 x 4096 (256 threads) 37.0 / 34.7 / 43.1 us, Q4_K 14336 x 4096 (896
     // threads) 47.1 / 46.9 / 46.9 us
@@ -850,8 +869,9 @@ __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict_
     // word w of a token: its source and LDS offsets
     auto offs = [&](int w, int &src, int &dst) {
         if (w < DW) {
-            src = dsrc + 16 * w;
-            dst = 16 * w;
+            const int wd = (w / 12) * 16 + w % 12; // the digit word, pad words skipped
+            src = dsrc + 16 * wd;
+            dst = 16 * wd;
         } else if (w < DW + SW) {
             src = ssrc + 16 * (w - DW);
             dst = mm_sum_off(KC) + 16 * (w - DW);
@@ -907,6 +927,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q4k(const uint8_t *__restrict__ 
     __shared__ int oflag_s;
     if (threadIdx.x == 0) oflag_s = -1;
     int seq = 0;
+    mm_zero_pad<KC, TR, 64 * NW>(lds); // (the first chunk's copy follows a barrier)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int nblk = (rows + ROWS - 1) / ROWS;
@@ -1217,6 +1238,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q80(const uint8_t *__restrict__ 
     __shared__ int oflag_s;
     if (threadIdx.x == 0) oflag_s = -1;
     int seq = 0;
+    mm_zero_pad<KC, TR, 64 * NW>(lds); // (the first chunk's copy follows a barrier)
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int nblk = (rows + ROWS - 1) / ROWS;
