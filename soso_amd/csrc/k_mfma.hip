@@ -854,11 +854,12 @@ __device__ __forceinline__ void mm_zero_pad(uint8_t *lds)
 // Q8_0 4096 x 4096 34.7 -> 32.8 us, Q4_K 14336 x 4096 47.8 -> 47.2 us (the
 // Q8_0 kernel is bound by the bytes each CU pulls through its L1, about 8 per
 // cycle: 64 rows of weights and 16 tokens of staged x per workgroup).
-template <int KC, int TR, int NT>
+template <int KC, int TR, int NT, bool SUMS = true>
 __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict__ xg, int t0, int cols, int k0,
                                         int *oflag, int seq)
 {
-    constexpr int tb = mm_tok_bytes(KC), DW = KC * 3 / 16, SW = KC / 128, MW = KC / 128, PW = KC / 256;
+    // (SUMS false: the sub-block sums, which only Q4_K's min term reads, stay behind)
+    constexpr int tb = mm_tok_bytes(KC), DW = KC * 3 / 16, SW = SUMS ? KC / 128 : 0, MW = KC / 128, PW = KC / 256;
     // MB words per thread in flight: on MI355X, 64 tokens, 4 / 8 / 16: Q8_0
     // 4096 x 4096 (256 threads) 37.0 / 34.7 / 43.1 us, Q4_K 14336 x 4096 (896
     // threads) 47.1 / 46.9 / 46.9 us
@@ -911,6 +912,50 @@ __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict_
             *(const float *)(xg + (size_t)(t0 + t) * tbf + psrc + 4 * w);
     }
     if (any) *oflag = seq;
+}
+
+// gfx950 lane swaps: V32 exchanges a of lanes 32 .. 63 with b of lanes 0 ..
+// 31, V16 a of the odd 16-lane rows with b of the even rows.  In the MFMA
+// layouts here (lane = 16 g + n) they pair lanes (n, g) with (n, g ^ 2) and
+// (n, g ^ 1): a row's four lanes can load its bytes contiguously and then
+// regroup them.  (The Q4_K matmul keeps mf_load_sb's loads: with its codes
+// and header loaded this way, 14336 x 4096 at 64 tokens measured 47.0-48.1 ->
+// 48.5-49.3 us, the codes alone 47.3-47.8, the header alone 47.5-48.2.)
+__device__ __forceinline__ void lane_swap32(uint32_t &a, uint32_t &b)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+__device__ __forceinline__ void lane_swap16(uint32_t &a, uint32_t &b)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    a = r[0];
+    b = r[1];
+}
+
+// Two 16-byte pieces per lane of a row's four lanes (n, g), piece P of lane
+// j = piece (plane P, unit j) -> lane (n, g) gets, for each j, the 8 bytes
+// at half g & 1 of lane j's piece of plane g >> 1: q[j].  V32 then V16.
+__device__ __forceinline__ void lane_regroup(uint4 A, uint4 B, uint2 (&q)[4])
+{
+    // lanes with g < 2 keep plane 0 and receive it from g + 2, the others
+    // keep plane 1 and receive it from g - 2: A then holds the pieces of
+    // source lane g & 1, B of (g & 1) + 2
+    lane_swap32(A.x, B.x);
+    lane_swap32(A.y, B.y);
+    lane_swap32(A.z, B.z);
+    lane_swap32(A.w, B.w);
+    // the same across g ^ 1 with the halves: .xy then holds source lane
+    // 2 s + 0, .zw source lane 2 s + 1 (s = 0 for A, 1 for B)
+    lane_swap16(A.x, A.z);
+    lane_swap16(A.y, A.w);
+    lane_swap16(B.x, B.z);
+    lane_swap16(B.y, B.w);
+    q[0] = make_uint2(A.x, A.y);
+    q[1] = make_uint2(A.z, A.w);
+    q[2] = make_uint2(B.x, B.y);
+    q[3] = make_uint2(B.z, B.w);
 }
 
 // NW wavefronts of 16 rows, rounds of 4 MT tokens, KC columns per staged
@@ -1291,16 +1336,8 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q80(const uint8_t *__restrict__ 
         for (int p = 0; p < 4; p++)
             o.v[p] = bld16(rA, off + sreg + 16u * (uint32_t)U * (uint32_t)p + 16u * (4u * (uint32_t)sb + (uint32_t)g));
     };
-    auto swap32 = [](uint32_t &a, uint32_t &b) {
-        const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
-        a = r[0];
-        b = r[1];
-    };
-    auto swap16 = [](uint32_t &a, uint32_t &b) {
-        const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
-        a = r[0];
-        b = r[1];
-    };
+    auto swap32 = lane_swap32;
+    auto swap16 = lane_swap16;
     // MmQ80 -> MfQ80: q[2 j + q'] = bytes 8 g .. 8 g + 7 of block 2 (4 sb + j) + q'
     auto unpack = [&](const MmQ80 &c, MfQ80 &o) {
         {
@@ -1318,25 +1355,11 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q80(const uint8_t *__restrict__ 
             o.s[1] = make_uint4(a1, b1, a1c, b1c);
         }
 #pragma unroll
-        for (int q = 0; q < 2; q++) {
-            // lanes with g < 2 keep plane 2q and receive it from g + 2, lanes
-            // with g >= 2 keep plane 2q + 1 and receive it from g - 2: A then
-            // holds the data of source lanes g & 1, B of (g & 1) + 2
-            uint4 A = c.v[2 * q], B = c.v[2 * q + 1];
-            swap32(A.x, B.x);
-            swap32(A.y, B.y);
-            swap32(A.z, B.z);
-            swap32(A.w, B.w);
-            // the same across g ^ 1 with the halves: .xy then holds source
-            // lane 2 s1, .zw source lane 2 s1 + 1 (s1 = 0 for A, 1 for B)
-            swap16(A.x, A.z);
-            swap16(A.y, A.w);
-            swap16(B.x, B.z);
-            swap16(B.y, B.w);
-            o.q[2 * 0 + q] = make_uint2(A.x, A.y);
-            o.q[2 * 1 + q] = make_uint2(A.z, A.w);
-            o.q[2 * 2 + q] = make_uint2(B.x, B.y);
-            o.q[2 * 3 + q] = make_uint2(B.z, B.w);
+        for (int q = 0; q < 2; q++) { // planes 2q, 2q + 1: block parity q
+            uint2 r[4];
+            lane_regroup(c.v[2 * q], c.v[2 * q + 1], r);
+#pragma unroll
+            for (int j = 0; j < 4; j++) o.q[2 * j + q] = r[j];
         }
     };
     float accf[MT];
@@ -1397,7 +1420,7 @@ __global__ void __launch_bounds__(64 * NW) k_mm_q80(const uint8_t *__restrict__ 
         if (s % NSB == 0) {
             if (__builtin_expect(oany, 0)) correct((s - NSB) * 256); // (oany is false at s = 0)
             __syncthreads(); // the previous chunk's readers of LDS are done
-            mm_copy<KC, TR, 64 * NW>(lds, xg, t0, cols, s * 256, &oflag_s, ++seq);
+            mm_copy<KC, TR, 64 * NW, false>(lds, xg, t0, cols, s * 256, &oflag_s, ++seq);
             __syncthreads();
             oany = __builtin_amdgcn_readfirstlane(oflag_s) == seq;
         }
