@@ -921,11 +921,14 @@ def main():
                 res[f"gdn_block_n{n}_GB_s"] = round(nb / (ms * 1e-3) / 1e9, 1)
         elif args.only == "readprobe":
             nb = 14336 * ROW_BYTES[Q4K](4096)  # the headline's weight bytes
+            nq = 4096 * ROW_BYTES[Q8](4096)  # configs[0]'s Q8_0 weight bytes
             small = time_read_probe(g, nb, 16, MIN_TIMED // 2, 20)
+            q8 = time_read_probe(g, nq, 28, MIN_TIMED // 2, 20)
             big = time_read_probe(g, 512 << 20, 2, 20, 4)
             res = {"read_33MB_us": {f"{v}{k} {w}x{t}": round(ms * 1e3, 3) for (v, k, w, t), ms in small.items()},
+                   "read_19MB_us": {f"{v}{k} {w}x{t}": round(ms * 1e3, 3) for (v, k, w, t), ms in q8.items()},
                    "read_512MB_us": {f"{v}{k} {w}x{t}": round(ms * 1e3, 3) for (v, k, w, t), ms in big.items()},
-                   "bytes": [nb, 512 << 20],
+                   "bytes": [nb, nq, 512 << 20],
                    "key": "variant (gs: grid-stride, chunk: per-wavefront KiB stretches) and loads in flight, "
                           "workgroups per CU x threads"}
         else:
