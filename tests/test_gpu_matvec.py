@@ -205,7 +205,8 @@ def test_matmul_equals_single_matvecs(gpu, orc, dtype, rows, cols, n):
 @pytest.mark.parametrize("rows,cols,n", [(1000, 4096, 16), (384, 1536, 37), (136, 768, 20),
                                          (14336, 4096, 32), (14336, 4096, 64), (4096, 4096, 64),
                                          (4096, 14336, 32), (528, 1024, 256), (720, 1024, 200),
-                                         (1296, 1024, 96), (1424, 1024, 200), (14336, 4096, 128)])
+                                         (1296, 1024, 96), (1424, 1024, 200), (14336, 4096, 128),
+                                         (4100, 2048, 64), (14000, 4096, 64)])
 @pytest.mark.parametrize("dtype", [Q4K, Q8])
 def test_matmul_matrix_cores_match_cpu(gpu, orc, dtype, rows, cols, n):
     """From 16 vectors up, Q4_K and Q8_0 matmul run on the matrix cores
@@ -218,7 +219,12 @@ def test_matmul_matrix_cores_match_cpu(gpu, orc, dtype, rows, cols, n):
     at 32 tokens, (16, 4) at 64 (two column chunks) and at 128 (more
     workgroups than CUs: half the LDS each, four chunks), (8, 2) 4096 x 4096
     at 64, (8, 1) 4096 x 14336 at 32 (two chunks), and (16, 1), (4, 4),
-    (4, 2), (8, 4) the four 1024-column shapes."""
+    (4, 2), (8, 4) the four 1024-column shapes.  With x staged once per call
+    (k_mm_q80 / k_mm_q4k, whole 16-token rounds whose grid fills the GPU):
+    4096 and 14336 rows at 32 to 128 tokens, and partial last row blocks --
+    Q8_0 4100 x 2048 at 64 (4 rows in the last 64-row block, whose lanes read
+    zeros past the strip before the lane swaps regroup them), Q4_K 14000 x 4096
+    at 64 (112 rows in the last 224-row block)."""
     w = orc.synth(dtype, rows, cols, 7, n)
     xs = orc.normal(n * cols, 1.0, 8, n).reshape(n, cols)
     out = np.empty(n * rows, np.float32)
