@@ -480,8 +480,9 @@ __device__ int mf_scan_slots(const int32_t *__restrict__ sidx, int nslots, int e
 // FULL (dense products whose token count is a multiple of 4 MT): every round
 // holds 4 MT tokens, so the per-tile checks compile away and the A operand is
 // loaded by every lane (the zero-pad digit lanes read digit 2 and select 0).
-template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW, bool SCAN = false, bool FULL = false>
-__global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 : 4) : 1) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
+template <int NMAT, int MT, int LA, bool TILED = false, int NW = MF_NW, bool SCAN = false, bool FULL = false,
+          bool SPLIT = false>
+__global__ void __launch_bounds__(64 * NW, NW == 4 && MT <= 2 ? (NMAT == 2 ? 3 : 4) : 1) k_mfma_q4k(const uint8_t *const *__restrict__ tabA,
                                                   const uint8_t *const *__restrict__ tabB,
                                                   const uint8_t *__restrict__ W0, size_t stride, int rows, int cols,
                                                   const float *__restrict__ xs, int xdiv, const int *__restrict__ list,
@@ -612,6 +613,89 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
                     }
                 }
             };
+            // SPLIT: one v_mfma_i32_16x16x32_i8 per sub-block on the raw codes
+            // (0..15), the scale applied to its exact int32 sums by a 24-bit
+            // multiply-add: S = sum_sb sc_sb * D_sb, the same integer as
+            // Clo + 8 Chi, without the B operands' scale multiplies (for one
+            // token tile per super-block, the MoE experts' usual case).
+            auto superblock_split = [&](int sbl8, const MfSb &A_, const MfSb &B_) {
+                MfScale sc_[NMAT];
+                mf_scales(A_.h, sc_[0]);
+                if constexpr (NMAT == 2) mf_scales(B_.h, sc_[NMAT - 1]);
+                typedef long mf_i64;
+                int S[NMAT][MT][3];
+                float mins[NMAT][MT];
+#pragma unroll
+                for (int m = 0; m < NMAT; m++)
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        S[m][mt][0] = S[m][mt][1] = S[m][mt][2] = 0;
+                        mins[m][mt] = 0.0f;
+                    }
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    const int j0 = 2 * p, j1 = 2 * p + 1;
+                    mf_i64 bl[NMAT], bh[NMAT];
+                    int s0[NMAT], s1[NMAT];
+                    float m0[NMAT], m1[NMAT];
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        const uint2 q = m == 0 ? A_.q[p] : B_.q[p];
+                        const uint32_t lx = q.x & 0x0F0F0F0Fu, ly = q.y & 0x0F0F0F0Fu;
+                        const uint32_t hx = (q.x >> 4) & 0x0F0F0F0Fu, hy = (q.y >> 4) & 0x0F0F0F0Fu;
+                        bl[m] = (mf_i64)(((uint64_t)ly << 32) | lx);
+                        bh[m] = (mf_i64)(((uint64_t)hy << 32) | hx);
+                        s0[m] = mf_byte(sc_[m].sc4[j0 >> 2], j0 & 3);
+                        s1[m] = mf_byte(sc_[m].sc4[j1 >> 2], j1 & 3);
+                        m0[m] = (float)mf_byte(sc_[m].m4[j0 >> 2], j0 & 3);
+                        m1[m] = (float)mf_byte(sc_[m].m4[j1 >> 2], j1 & 3);
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++) {
+                        if (mt * 4 >= nt) break; // uniform
+                        const int ta = mt * 4 + a_tok;
+                        uint2 u0 = make_uint2(0u, 0u), u1 = u0;
+                        if constexpr (FULL) {
+                            const uint8_t *tp = lds + (size_t)ta * tb;
+                            u0 = *(const uint2 *)(tp + ((sbl8 + j0) * 3 + a_dg) * 32 + 8 * g);
+                            u1 = *(const uint2 *)(tp + ((sbl8 + j1) * 3 + a_dg) * 32 + 8 * g);
+                            if (a_dig == 3) u0 = u1 = make_uint2(0u, 0u);
+                        } else if (a_dig < 3 && ta < nt) {
+                            const uint8_t *tp = lds + (size_t)ta * tb;
+                            u0 = *(const uint2 *)(tp + ((sbl8 + j0) * 3 + a_dig) * 32 + 8 * g);
+                            u1 = *(const uint2 *)(tp + ((sbl8 + j1) * 3 + a_dig) * 32 + 8 * g);
+                        }
+                        const mf_i64 a0 = (mf_i64)(((uint64_t)u0.y << 32) | u0.x);
+                        const mf_i64 a1 = (mf_i64)(((uint64_t)u1.y << 32) | u1.x);
+                        const int to = mt * 4 + g;
+                        const float *xsum = (const float *)(lds + (size_t)(to < nt ? to : 0) * tb + (kc >> 5) * 96);
+                        const float xs0 = xsum[sbl8 + j0], xs1 = xsum[sbl8 + j1];
+#pragma unroll
+                        for (int m = 0; m < NMAT; m++) {
+                            const mf_v4i d0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bl[m], mf_v4i{0, 0, 0, 0}, 0, 0, 0);
+                            const mf_v4i d1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bh[m], mf_v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                            for (int d = 0; d < 3; d++)
+                                S[m][mt][d] = __mul24(s1[m], d1[d]) + (__mul24(s0[m], d0[d]) + S[m][mt][d]);
+                            mins[m][mt] = fmaf(m0[m], xs0, fmaf(m1[m], xs1, mins[m][mt]));
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) {
+                    if (mt * 4 >= nt) break;
+                    const int to = mt * 4 + g;
+                    const float P = *(const float *)(lds + (size_t)(to < nt ? to : 0) * tb + (kc >> 5) * 100 +
+                                                     4 * (sbl8 >> 3));
+#pragma unroll
+                    for (int m = 0; m < NMAT; m++) {
+                        const float t = fmaf((float)S[m][mt][2], 65536.0f,
+                                             fmaf((float)S[m][mt][1], 256.0f, (float)S[m][mt][0]));
+                        accf[m][mt] = fmaf(-sc_[m].dmin, mins[m][mt], fmaf(sc_[m].d * P, t, accf[m][mt]));
+                    }
+                }
+            };
             auto superblock = [&](int sbl8, const MfSb &A_, const MfSb &B_) {
                 // sbl8: first local sub-block of this super-block
                 MfScale sc_[NMAT];
@@ -713,7 +797,10 @@ __global__ void __launch_bounds__(64 * NW, NW == 4 && MT == 2 ? (NMAT == 2 ? 3 :
                 load_sb(rA, sb0 + i + LA, i + LA < nsb, pa[LA - 1]);
                 if constexpr (NMAT == 2) load_sb(rB, sb0 + i + LA, i + LA < nsb, pb[LA - 1]);
                 __builtin_amdgcn_sched_barrier(0);
-                superblock(8 * i, ca, cb);
+                if constexpr (SPLIT)
+                    superblock_split(8 * i, ca, cb);
+                else
+                    superblock(8 * i, ca, cb);
                 ca = pa[0];
                 if constexpr (NMAT == 2) cb = pb[0];
 #pragma unroll
@@ -1464,8 +1551,17 @@ static void mfma_moe_one(soso_hip *h, unsigned grid, size_t lds, const uint8_t *
                          const int *n_recs, int kc, float *out, const int32_t *sidx, int nslots)
 {
     constexpr int MT = 2, LA = NMAT == 2 ? MF_LA2 : MF_LA1, NW = NMAT == 2 ? MF_NW_GU : MF_NW_DN;
+    // The scanning launch (about two tokens per active expert): rounds of one
+    // 4-token tile, one MFMA per sub-block with the scales applied to the
+    // int32 sums (SPLIT).  Measured on MI355X, MoE batch 32 per layer: 92.3 us
+    // with rounds of 8 tokens and the scales folded into the B operands; 91.3-
+    // 91.7 with SPLIT for down; 90.4-90.7 with gate/up at 4 tokens and SPLIT
+    // too; 88.9-89.1 with down at 4 tokens as well.  Rejected: SPLIT for
+    // gate/up at 8 tokens (28 bytes per lane spilled, 97.9), gate/up at 4
+    // tokens without SPLIT (92.3-93.0), gate/up held to 128 VGPRs for four
+    // wavefronts per SIMD (91.4-91.9).
     if (sidx)
-        k_mfma_q4k<NMAT, MT, LA, TILED, NW, true><<<grid, 64 * NW, lds, h->stream>>>(
+        k_mfma_q4k<NMAT, 1, LA, TILED, NW, true, false, true><<<grid, 64 * NW, lds, h->stream>>>(
             A, B, nullptr, stride, rows, cols, xs, xdiv, list, recs, n_recs, 0, kc, out, sidx, nslots);
     else
         k_mfma_q4k<NMAT, MT, LA, TILED, NW><<<grid, 64 * NW, lds, h->stream>>>(
@@ -1479,7 +1575,7 @@ int launch_mfma_moe(soso_hip *h, int nmat, const uint8_t *const *A, const uint8_
     if (!mfma_shape_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols) || (tiled && !tiled_q4k_ok(SOSO_HIP_DTYPE_Q4_K, rows, cols)))
         return set_err(h, SOSO_HIP_DECLINED, "mfma: shape");
     if (sidx && nslots > (size_t)MF_SCAN_MAX) return set_err(h, SOSO_HIP_ERR_ARG, "mfma: too many slots to scan");
-    constexpr int MT = 2;
+    const int MT = sidx ? 1 : 2; // tiles per round (mfma_moe_one)
     const size_t scan_b = sidx ? (size_t)mf_scan_bytes((int)nslots) : 0;
     const int kc = mf_kc(h, cols, 4 * MT, h->max_lds - scan_b);
     const size_t mrows = (size_t)16 * (nmat == 2 ? MF_NW_GU : MF_NW_DN); // rows per workgroup
