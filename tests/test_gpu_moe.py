@@ -135,12 +135,12 @@ def test_router_ties_lowest_index_first(gpu, orc):
     (40, 256, 512, 1, 1, Q4K),     # one token, top-1
     (200, 512, 256, 5, 1, Q4K),    # one token, 200 experts (four logits per lane), top-5
     (12, 512, 256, 3, 1, Q8),      # one token with Q8_0 down projections: the general path
-    (16, 2048, 768, 8, 32, Q4K),   # batch 32: 16 tokens per expert, the matrix-core path
+    (16, 2048, 768, 8, 32, Q4K),   # batch 32: 16 tokens per expert (four rounds), the matrix-core path
     (128, 2048, 768, 8, 32, Q4K),  # configs[3] at batch 32: about 2.3 tokens per expert, tile-major copies
     (128, 2048, 768, 8, 64, Q4K),  # 512 ranked slots: the most the expert kernels find by scanning the ranking
     (64, 512, 256, 8, 65, Q4K),    # 520 slots: one past the scan, the route sorts the slots
     (12, 512, 256, 3, 7, Q8),      # Q8_0 down projections (soso's converted Q6_K experts)
-    (8, 512, 256, 4, 48, Q4K),     # 24 tokens per expert: three token rounds on the matrix cores
+    (8, 512, 256, 4, 48, Q4K),     # 24 tokens per expert: six 4-token rounds on the matrix cores
     (6, 512, 256, 3, 16, Q8),      # matrix-core gate/up, dot4 Q8_0 down
     (20, 512, 512, 6, 4, Q4K),     # 4 tokens, top-6: down and the weighted sum in one launch
     (10, 256, 1024, 2, 3, Q4K),    # 3 tokens, top-2, wide ffn: down + sum in one launch
