@@ -947,10 +947,13 @@ __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict_
 {
     // (SUMS false: the sub-block sums, which only Q4_K's min term reads, stay behind)
     constexpr int tb = mm_tok_bytes(KC), DW = KC * 3 / 16, SW = SUMS ? KC / 128 : 0, MW = KC / 128, PW = KC / 256;
-    // MB words per thread in flight: on MI355X, 64 tokens, 4 / 8 / 16: Q8_0
-    // 4096 x 4096 (256 threads) 37.0 / 34.7 / 43.1 us, Q4_K 14336 x 4096 (896
-    // threads) 47.1 / 46.9 / 46.9 us
-    constexpr int PT = DW + SW + MW, TOT = TR * PT, MB = 8;
+    // MB words per thread in flight: all of a thread's words (one round trip
+    // per chunk) up to 16, else batches of 8.  On MI355X, 64 tokens: Q8_0
+    // 4096 x 4096 (256 threads, 13 words each) 29.8-29.9 us with batches of
+    // 8 -> 28.6-28.7 with one batch; Q4_K 14336 x 4096 (896 threads, 4 words)
+    // 47.2-47.9 -> 47.0-47.5.  (With the pad plane still copied, 17 words per
+    // Q8_0 thread: batches of 4 / 8 / 16 37.0 / 34.7 / 43.1 us.)
+    constexpr int PT = DW + SW + MW, TOT = TR * PT, PER = (TOT + NT - 1) / NT, MB = PER <= 16 ? PER : 8;
     const int tbf = mm_tok_bytes(cols);
     const int dsrc = 4 * k0, ssrc = mm_sum_off(cols) + (k0 >> 3), psrc = mm_p_off(cols) + (k0 >> 6),
               msrc = mm_mask_off(cols) + (k0 >> 3);
