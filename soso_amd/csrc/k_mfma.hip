@@ -948,12 +948,13 @@ __device__ __forceinline__ void mm_copy(uint8_t *lds, const uint8_t *__restrict_
     // (SUMS false: the sub-block sums, which only Q4_K's min term reads, stay behind)
     constexpr int tb = mm_tok_bytes(KC), DW = KC * 3 / 16, SW = SUMS ? KC / 128 : 0, MW = KC / 128, PW = KC / 256;
     // MB words per thread in flight: all of a thread's words (one round trip
-    // per chunk) up to 16, else batches of 8.  On MI355X, 64 tokens: Q8_0
-    // 4096 x 4096 (256 threads, 13 words each) 29.8-29.9 us with batches of
-    // 8 -> 28.6-28.7 with one batch; Q4_K 14336 x 4096 (896 threads, 4 words)
-    // 47.2-47.9 -> 47.0-47.5.  (With the pad plane still copied, 17 words per
-    // Q8_0 thread: batches of 4 / 8 / 16 37.0 / 34.7 / 43.1 us.)
-    constexpr int PT = DW + SW + MW, TOT = TR * PT, PER = (TOT + NT - 1) / NT, MB = PER <= 16 ? PER : 8;
+    // per chunk) up to 32, else batches of 8.  On MI355X, 64 tokens: Q8_0
+    // 4096 x 4096 (256 threads, 13 words each per 1024 columns) 29.8-29.9 us
+    // with batches of 8 -> 28.6-28.7 with one batch; Q4_K 14336 x 4096 (896
+    // threads, 4 words) 47.2-47.9 -> 47.0-47.5.  (With the pad plane still
+    // copied, 17 words per Q8_0 thread: batches of 4 / 8 / 16 37.0 / 34.7 /
+    // 43.1 us.)
+    constexpr int PT = DW + SW + MW, TOT = TR * PT, PER = (TOT + NT - 1) / NT, MB = PER <= 32 ? PER : 8;
     const int tbf = mm_tok_bytes(cols);
     const int dsrc = 4 * k0, ssrc = mm_sum_off(cols) + (k0 >> 3), psrc = mm_p_off(cols) + (k0 >> 6),
               msrc = mm_mask_off(cols) + (k0 >> 3);
@@ -1713,16 +1714,28 @@ static int launch_mm_q4k(soso_hip *h, const Weight &w, const float *x, size_t n,
 }
 
 // Dense Q8_0 with x staged once: 4 wavefronts (64 rows), rounds of 16 tokens,
-// 1024-column chunks, where that grid fills the GPU.  Measured on MI355X,
-// 4096 x 4096 at 64 tokens (us): this shape 37.0; 512- / 2048-column chunks
-// 41.3 / 42.2; rounds of 8 tokens with 4 or 8 wavefronts 48.9 / 49.8;
-// k_mfma_q80 staging its own rounds 46.6.
-constexpr int MQ_NW = 4, MQ_MT = 4, MQ_KC = 1024;
+// 2048-column chunks where the width allows (else 1024), where that grid fills
+// the GPU.  Measured on MI355X, 4096 x 4096 at 64 tokens (us): 1024-column
+// chunks 28.71-28.74, 2048 28.08-28.15 (each chunk copied in one round trip;
+// with the chunk copies in batches of 8 words: 1024 37.0, 512 / 2048 41.3 /
+// 42.2); rounds of 8 tokens with 4 or 8 wavefronts 48.9 / 49.8; k_mfma_q80
+// staging its own rounds 46.6.
+constexpr int MQ_NW = 4, MQ_MT = 4, MQ_KC = 2048;
+
+template <int KC>
+static void mm_q80_launch(soso_hip *h, const Weight &w, size_t stride, const uint8_t *xg, const float *x, float *y,
+                          unsigned grid)
+{
+    const size_t lds = (size_t)4 * MQ_MT * mm_tok_bytes(KC);
+    k_mm_q80<MQ_NW, MQ_MT, KC><<<grid, 64 * MQ_NW, lds, h->stream>>>((const uint8_t *)w.dev, stride, (int)w.rows,
+                                                                    (int)weight_kcols(w), xg, x, y);
+}
 
 static int launch_mm_q80(soso_hip *h, const Weight &w, const float *x, size_t n, float *y)
 {
-    constexpr int NW = MQ_NW, MT = MQ_MT, KC = MQ_KC;
+    constexpr int NW = MQ_NW, MT = MQ_MT;
     const size_t cols = weight_kcols(w), nblk = (w.rows + 16 * NW - 1) / (16 * NW);
+    const int KC = cols % MQ_KC == 0 && (size_t)4 * MT * mm_tok_bytes(MQ_KC) <= h->max_lds ? MQ_KC : 1024;
     if (n % (size_t)(4 * MT) || cols % KC || (size_t)4 * MT * mm_tok_bytes(KC) > h->max_lds ||
         nblk * (n / (4 * MT)) * 5 < (size_t)h->num_cu * 4)
         return SOSO_HIP_DECLINED; // k_mfma_q80's launch takes it
@@ -1732,9 +1745,12 @@ static int launch_mm_q80(soso_hip *h, const Weight &w, const float *x, size_t n,
     k_mm_stage<<<(unsigned)((waves + 3) / 4), 256, 0, h->stream>>>(x, (int)n, (int)cols, xg);
     int rc = hip_check(h, hipGetLastError(), "mm stage launch");
     if (rc != SOSO_HIP_OK) return rc;
-    const size_t stride = packed_row_stride(w.dtype, cols), lds = (size_t)4 * MT * mm_tok_bytes(KC);
-    k_mm_q80<NW, MT, KC><<<(unsigned)(nblk * (n / (4 * (size_t)MT))), 64 * NW, lds, h->stream>>>(
-        (const uint8_t *)w.dev, stride, (int)w.rows, (int)cols, xg, x, y);
+    const size_t stride = packed_row_stride(w.dtype, cols);
+    const unsigned grid = (unsigned)(nblk * (n / (4 * (size_t)MT)));
+    if (KC == MQ_KC)
+        mm_q80_launch<MQ_KC>(h, w, stride, xg, x, y, grid);
+    else
+        mm_q80_launch<1024>(h, w, stride, xg, x, y, grid);
     return hip_check(h, hipGetLastError(), "mm q80 launch");
 }
 

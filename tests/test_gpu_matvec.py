@@ -206,7 +206,7 @@ def test_matmul_equals_single_matvecs(gpu, orc, dtype, rows, cols, n):
                                          (14336, 4096, 32), (14336, 4096, 64), (4096, 4096, 64),
                                          (4096, 14336, 32), (528, 1024, 256), (720, 1024, 200),
                                          (1296, 1024, 96), (1424, 1024, 200), (14336, 4096, 128),
-                                         (4100, 2048, 64), (14000, 4096, 64)])
+                                         (4100, 2048, 64), (14000, 4096, 64), (4096, 3072, 64)])
 @pytest.mark.parametrize("dtype", [Q4K, Q8])
 def test_matmul_matrix_cores_match_cpu(gpu, orc, dtype, rows, cols, n):
     """From 16 vectors up, Q4_K and Q8_0 matmul run on the matrix cores
@@ -224,7 +224,8 @@ def test_matmul_matrix_cores_match_cpu(gpu, orc, dtype, rows, cols, n):
     4096 and 14336 rows at 32 to 128 tokens, and partial last row blocks --
     Q8_0 4100 x 2048 at 64 (4 rows in the last 64-row block, whose lanes read
     zeros past the strip before the lane swaps regroup them), Q4_K 14000 x 4096
-    at 64 (112 rows in the last 224-row block)."""
+    at 64 (112 rows in the last 224-row block); and Q8_0 4096 x 3072, whose
+    width takes 1024-column chunks where a multiple of 2048 takes 2048."""
     w = orc.synth(dtype, rows, cols, 7, n)
     xs = orc.normal(n * cols, 1.0, 8, n).reshape(n, cols)
     out = np.empty(n * rows, np.float32)
